@@ -1,0 +1,504 @@
+/*
+ * CPU oracle for the fused-DAG execution path: TEST INFRASTRUCTURE ONLY.
+ * See chelis_oracle.h for who may load it and what pins each function.
+ *
+ * Build profile (oracle/Makefile): gcc -O2 -ffp-contract=off -fno-fast-math
+ * -fopenmp, the reference C lane's pinned profile
+ * (crates/chelis-backend-c/src/toolchain.rs:229-260). float and double
+ * arithmetic is IEEE binary32/binary64 with round-to-nearest-even and no
+ * contraction, so every expression below finalizes at its own dtype.
+ *
+ * Parallel loops only ever split independent output elements; no reduction
+ * is reassociated (the same rule as the reference's OpenMP loops,
+ * crates/chelis-backend-c/src/emit.rs:8113-8125).
+ */
+#include "chelis_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* CORE-MATH shims (crates/chelis-crmath/csrc/crmath_ffi.c), built into
+ * oracle/_ref/libcrmath_ref.so. The non-`raw` shims canonicalize NaN. */
+float chelis_crmath_ffi_expf(float);
+double chelis_crmath_ffi_exp(double);
+float chelis_crmath_ffi_logf(float);
+double chelis_crmath_ffi_log(double);
+float chelis_crmath_ffi_erfcf(float);
+double chelis_crmath_ffi_erfc(double);
+float chelis_crmath_ffi_tanhf(float);
+double chelis_crmath_ffi_tanh(double);
+
+/* ------------------------------------------------------------------ */
+/* [04-NUM-2] NaN finalization: crates/chelis-backend-c/src/fp_env.rs:46-52 */
+static inline float nan32(float v) {
+    if (isnan(v)) {
+        uint32_t b = 0x7fc00000u;
+        memcpy(&v, &b, 4);
+    }
+    return v;
+}
+static inline double nan64(double v) {
+    if (isnan(v)) {
+        uint64_t b = 0x7ff8000000000000ull;
+        memcpy(&v, &b, 8);
+    }
+    return v;
+}
+
+/* ------------------------------------------------------------------ */
+/* Keyed RNG: spec/05-risc-primitives.md [05-RNG-1] (splitmix64) and
+ * [05-RNG-2] (derive / word / unit); [05-OP-69..72] key derivations;
+ * crates/chelis-numeric-core/src/dtype_semantics.rs:4508-4540. */
+uint64_t orc_splitmix64(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+static inline uint64_t rotl64(uint64_t x, unsigned r) { return (x << r) | (x >> (64u - r)); }
+uint64_t orc_derive(uint64_t key, uint64_t j) { return orc_splitmix64(key ^ rotl64(orc_splitmix64(j), 29)); }
+uint64_t orc_word(uint64_t key, uint64_t index) { return orc_splitmix64(key ^ rotl64(orc_splitmix64(index), 41)); }
+double orc_unit(uint64_t key, uint64_t index) {
+    /* The high 53 bits over 2^53: exact in binary64. */
+    return (double)(orc_word(key, index) >> 11) * 0x1p-53;
+}
+void orc_split(uint64_t key, uint64_t out[2]) {
+    out[0] = orc_derive(key, 0);
+    out[1] = orc_derive(key, 1);
+}
+uint64_t orc_fold_in(uint64_t key, int64_t n) { return orc_derive(orc_derive(key, 2), (uint64_t)n); }
+void orc_split_n(uint64_t key, int64_t n, uint64_t *out) {
+    uint64_t base = orc_derive(key, 2);
+    for (int64_t j = 0; j < n; ++j) out[j] = orc_derive(base, (uint64_t)j);
+}
+/* [05-OP-8]: f32 is one fmaf(high - low, round_f32(u), low); f64 one fma. */
+void orc_uniform_like_f32(uint64_t key, float low, float high, float *out, int64_t n) {
+    float span = high - low;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) out[i] = nan32(fmaf(span, (float)orc_unit(key, (uint64_t)i), low));
+}
+void orc_uniform_like_f64(uint64_t key, double low, double high, double *out, int64_t n) {
+    double span = high - low;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) out[i] = nan64(fma(span, orc_unit(key, (uint64_t)i), low));
+}
+
+/* ------------------------------------------------------------------ */
+float orc_expf(float x) { return chelis_crmath_ffi_expf(x); }
+double orc_exp(double x) { return chelis_crmath_ffi_exp(x); }
+float orc_logf(float x) { return chelis_crmath_ffi_logf(x); }
+double orc_log(double x) { return chelis_crmath_ffi_log(x); }
+float orc_erfcf(float x) { return chelis_crmath_ffi_erfcf(x); }
+double orc_erfc(double x) { return chelis_crmath_ffi_erfc(x); }
+float orc_tanhf(float x) { return chelis_crmath_ffi_tanhf(x); }
+double orc_tanh(double x) { return chelis_crmath_ffi_tanh(x); }
+
+/* ------------------------------------------------------------------ */
+/* [05-OP-30] canonical adjacent-pair tree, streamed leaf by leaf.
+ * Restates the C lane's CarryTree (crates/chelis-backend-c/src/emit.rs:
+ * 272-283 struct, 8113-8215 push/total): a completed subtree of 2^d leaves
+ * waits in level[d]; leaf i first absorbs one waiting subtree per trailing
+ * one bit of i (the waiting, earlier subtree on the left); after the last
+ * leaf the waiting subtrees fold lowest level (rightmost) first. An empty
+ * slice is +0 with no addition; the stored total alone is NaN-finalized. */
+#define DEFINE_TREE_SUM(NAME, T, NANF)                                         \
+    T NAME(const T *x, int64_t n, int64_t stride) {                            \
+        T level[64];                                                           \
+        int64_t count = 0;                                                     \
+        for (int64_t i = 0; i < n; ++i) {                                      \
+            T carry = x[i * stride];                                           \
+            int depth = 0;                                                     \
+            for (int64_t pending = count++; pending & 1; pending >>= 1, ++depth) \
+                carry = level[depth] + carry;                                  \
+            level[depth] = carry;                                              \
+        }                                                                      \
+        T total = (T)0;                                                        \
+        int found = 0, depth = 0;                                              \
+        for (int64_t remaining = count; remaining; remaining >>= 1, ++depth) { \
+            if (remaining & 1) {                                               \
+                total = found ? level[depth] + total : level[depth];           \
+                found = 1;                                                     \
+            }                                                                  \
+        }                                                                      \
+        return NANF(total);                                                    \
+    }
+DEFINE_TREE_SUM(orc_tree_sum_f32, float, nan32)
+DEFINE_TREE_SUM(orc_tree_sum_f64, double, nan64)
+
+/* The same tree as spec/05-risc-primitives.md section 2.3 words it: one
+ * pass per level pairs adjacent values left to right and carries an odd
+ * final value unchanged. Kept as an independent restatement that pins the
+ * streamed form above. */
+#define DEFINE_LEVEL_SUM(NAME, T, NANF)                                        \
+    T NAME(const T *x, int64_t n) {                                            \
+        if (n == 0) return (T)0;                                               \
+        T *work = (T *)malloc((size_t)n * sizeof(T));                          \
+        memcpy(work, x, (size_t)n * sizeof(T));                                \
+        int64_t len = n;                                                       \
+        while (len > 1) {                                                      \
+            int64_t next = 0;                                                  \
+            for (int64_t i = 0; i + 1 < len; i += 2) work[next++] = work[i] + work[i + 1]; \
+            if (len & 1) work[next++] = work[len - 1];                         \
+            len = next;                                                        \
+        }                                                                      \
+        T total = work[0];                                                     \
+        free(work);                                                            \
+        return NANF(total);                                                    \
+    }
+DEFINE_LEVEL_SUM(orc_level_sum_f32, float, nan32)
+DEFINE_LEVEL_SUM(orc_level_sum_f64, double, nan64)
+
+/* [05-OP-12]: the first NaN in index order, with its stored bits; otherwise
+ * the maximum, keeping the first stored representation among equals (so
+ * -0 before +0 stays -0). n >= 1 (an empty axis traps before this). */
+#define DEFINE_MAX_REDUCE(NAME, T)                                             \
+    T NAME(const T *x, int64_t n, int64_t stride) {                            \
+        T best = x[0];                                                         \
+        if (isnan(best)) return best;                                          \
+        for (int64_t i = 1; i < n; ++i) {                                      \
+            T v = x[i * stride];                                               \
+            if (isnan(v)) return v;                                            \
+            if (v > best) best = v;                                            \
+        }                                                                      \
+        return best;                                                           \
+    }
+DEFINE_MAX_REDUCE(orc_max_reduce_f32, float)
+DEFINE_MAX_REDUCE(orc_max_reduce_f64, double)
+
+#define DEFINE_AXIS(NAME, T, LEAF)                                             \
+    void NAME(const T *x, int64_t outer, int64_t n, int64_t inner, T *out) {   \
+        _Pragma("omp parallel for collapse(2) schedule(static)")               \
+        for (int64_t o = 0; o < outer; ++o)                                    \
+            for (int64_t j = 0; j < inner; ++j)                                \
+                out[o * inner + j] = LEAF(x + o * n * inner + j, n, inner);    \
+    }
+DEFINE_AXIS(orc_sum_axis_f32, float, orc_tree_sum_f32)
+DEFINE_AXIS(orc_sum_axis_f64, double, orc_tree_sum_f64)
+DEFINE_AXIS(orc_max_axis_f32, float, orc_max_reduce_f32)
+DEFINE_AXIS(orc_max_axis_f64, double, orc_max_reduce_f64)
+
+/* [05-OP-29] count: Bool8 leaves are exact 0/1 i64 combined by the same
+ * tree with checked addition (an i64 count of at most 2^63-1 leaves cannot
+ * overflow, so the tree's value is the plain number of ones). A byte other
+ * than 0 or 1 is the reference device kernel's error code 1
+ * (crates/chelis-backend-hip/src/kernels.rs:375-557). */
+int32_t orc_count_axis(const uint8_t *x, int64_t outer, int64_t n, int64_t inner, int64_t *out) {
+    int32_t error = 0;
+    for (int64_t o = 0; o < outer; ++o)
+        for (int64_t j = 0; j < inner; ++j) {
+            int64_t c = 0;
+            for (int64_t i = 0; i < n; ++i) {
+                uint8_t b = x[(o * n + i) * inner + j];
+                if (b > 1) error = 1;
+                c += b & 1;
+            }
+            out[o * inner + j] = c;
+        }
+    return error;
+}
+
+/* ------------------------------------------------------------------ */
+/* Softmax rows: spec/05 section 4.2 and decompose_softmax
+ * (crates/chelis-dag-core/src/tier2.rs:1098-1178): max_reduce, sub
+ * (NaN-canonical), correctly rounded exp, canonical sum tree, div. Every
+ * primitive finalizes at the row dtype. */
+#define DEFINE_SOFTMAX(NAME, T, NANF, EXPF, MAXF, SUMF)                       \
+    void NAME(const T *x, T *y, int64_t rows, int64_t n) {                     \
+        _Pragma("omp parallel for schedule(static)")                           \
+        for (int64_t r = 0; r < rows; ++r) {                                   \
+            const T *xr = x + r * n;                                           \
+            T *yr = y + r * n;                                                 \
+            T m = MAXF(xr, n, 1);                                              \
+            for (int64_t i = 0; i < n; ++i) yr[i] = EXPF(NANF(xr[i] - m));     \
+            T s = SUMF(yr, n, 1);                                              \
+            for (int64_t i = 0; i < n; ++i) yr[i] = NANF(yr[i] / s);           \
+        }                                                                      \
+    }
+DEFINE_SOFTMAX(orc_softmax_rows_f32, float, nan32, orc_expf, orc_max_reduce_f32, orc_tree_sum_f32)
+DEFINE_SOFTMAX(orc_softmax_rows_f64, double, nan64, orc_exp, orc_max_reduce_f64, orc_tree_sum_f64)
+
+/* Layer norm over the last axis: spec/05 section 4.4, lower_layer_norm
+ * (tier2.rs:1248-1360) with mean = tree sum / extent ([05-OP-11],
+ * lower_mean tier2.rs:1183). */
+#define DEFINE_LAYER_NORM(NAME, T, NANF, SUMF, SQRTF)                         \
+    void NAME(const T *x, const T *gamma, const T *beta, T eps, T *y, int64_t rows, int64_t n) { \
+        T extent = (T)n;                                                       \
+        _Pragma("omp parallel for schedule(static)")                           \
+        for (int64_t r = 0; r < rows; ++r) {                                   \
+            const T *xr = x + r * n;                                           \
+            T *yr = y + r * n;                                                 \
+            T *c = (T *)malloc((size_t)n * sizeof(T));                         \
+            T *sq = (T *)malloc((size_t)n * sizeof(T));                        \
+            T mean = NANF(SUMF(xr, n, 1) / extent);                            \
+            for (int64_t i = 0; i < n; ++i) {                                  \
+                c[i] = NANF(xr[i] - mean);                                     \
+                sq[i] = NANF(c[i] * c[i]);                                     \
+            }                                                                  \
+            T var = NANF(SUMF(sq, n, 1) / extent);                             \
+            T denom = NANF(SQRTF(NANF(var + eps)));                            \
+            for (int64_t i = 0; i < n; ++i) {                                  \
+                T normed = NANF(c[i] / denom);                                 \
+                T scaled = NANF(normed * gamma[i]);                            \
+                yr[i] = NANF(scaled + beta[i]);                                \
+            }                                                                  \
+            free(c);                                                           \
+            free(sq);                                                          \
+        }                                                                      \
+    }
+DEFINE_LAYER_NORM(orc_layer_norm_rows_f32, float, nan32, orc_tree_sum_f32, sqrtf)
+DEFINE_LAYER_NORM(orc_layer_norm_rows_f64, double, nan64, orc_tree_sum_f64, sqrt)
+
+/* ------------------------------------------------------------------ */
+/* GELU = mul(m(x), Phi(x)) with spec/05 section 3.3's exact Phi graph and
+ * its constants (crates/chelis-numeric-core/src/activation.rs:25-56):
+ * c = 1/sqrt(2), cl = 1/sqrt(2) - c, k = 2/sqrt(pi) (each rounded to the
+ * dtype), Veltkamp splitter s, range bound L = 64. m(x) is the multiplicand
+ * guard where(cmplt(x, lowest), -0.0, x). Every primitive is NaN-final. */
+#define DEFINE_GELU(NAME, T, NANF, ERFCF, EXPF, FABS, C, CL, K, S, LOWEST)   \
+    static inline T NAME##_one(T x) {                                          \
+        const T c = C, cl = CL, k = K, s = S, L = (T)64, half = (T)0.5;        \
+        T e = ERFCF(NANF(NANF(-x) * c));                                       \
+        T z = (FABS(x) < L) ? x : (T)0;                                        \
+        T a = NANF(-z);                                                        \
+        T th = NANF(a * c);                                                    \
+        T ta = NANF(s * a);                                                    \
+        T ah = NANF(ta - NANF(ta - a));                                        \
+        T al = NANF(a - ah);                                                   \
+        T tc = NANF(s * c);                                                    \
+        T ch = NANF(tc - NANF(tc - c));                                        \
+        T cr = NANF(c - ch);                                                   \
+        T t0 = NANF(NANF(ah * ch) - th);                                       \
+        T t1 = NANF(t0 + NANF(ah * cr));                                       \
+        T t2 = NANF(t1 + NANF(al * ch));                                       \
+        T t3 = NANF(t2 + NANF(al * cr));                                       \
+        T tl = NANF(t3 + NANF(a * cl));                                        \
+        T g = EXPF(NANF(-NANF(th * th)));                                      \
+        T corr = NANF(NANF(k * g) * tl);                                       \
+        T phi = NANF(half * NANF(e - corr));                                   \
+        T m = (x < LOWEST) ? (T)-0.0 : x;                                      \
+        return NANF(m * phi);                                                  \
+    }                                                                          \
+    void NAME(const T *x, T *y, int64_t n) {                                   \
+        _Pragma("omp parallel for schedule(static)")                           \
+        for (int64_t i = 0; i < n; ++i) y[i] = NAME##_one(x[i]);               \
+    }
+DEFINE_GELU(orc_gelu_f32, float, nan32, orc_erfcf, orc_expf, fabsf, (float)0.70710678118654752440,
+            (float)1.2101617485882343e-8, (float)1.12837916709551257390, 4097.0f, -3.4028234663852886e38f)
+DEFINE_GELU(orc_gelu_f64, double, nan64, orc_erfc, orc_exp, fabs, 0.70710678118654752440,
+            -4.833646656726457e-17, 1.12837916709551257390, 134217729.0, -1.7976931348623157e308)
+
+/* [05-OP-43] relu = max_elem(x, +0) keeping lhs on ties and NaN bits:
+ * x < 0 ? +0 : x. Its adjoint is g where cmplt(0, x), else +0
+ * (crates/chelis-backend-hip/src/kernels.rs:1136-1196). */
+void orc_relu_f32(const float *x, float *y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = x[i] < 0.0f ? 0.0f : x[i];
+}
+void orc_relu_adjoint_f32(const float *x, const float *g, float *y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = 0.0f < x[i] ? g[i] : 0.0f;
+}
+
+/* [05-OP-37] keyed dropout at f32: the f32-rounded unit of word(key, i) is
+ * compared with the rate; a dropped element is +0, a kept one
+ * x / (1 - rate) (crates/chelis-backend-c/src/emit.rs:6139-6220). The
+ * replay adjoint reuses the same mask on the cotangent. */
+void orc_dropout_f32(uint64_t key, const float *x, float rate, float *y, int64_t n) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i)
+        y[i] = (float)orc_unit(key, (uint64_t)i) < rate ? 0.0f : nan32(x[i] / (1.0f - rate));
+}
+void orc_dropout_replay_f32(uint64_t key, const float *g, float rate, float *dx, int64_t n) {
+    orc_dropout_f32(key, g, rate, dx, n);
+}
+void orc_dropout_f64(uint64_t key, const double *x, double rate, double *y, int64_t n) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i)
+        y[i] = orc_unit(key, (uint64_t)i) < rate ? 0.0 : nan64(x[i] / (1.0 - rate));
+}
+
+/* ------------------------------------------------------------------ */
+/* Canonical-tree matmul: spec/05 section 4.1 (insert, mul, sum over k with
+ * [05-OP-30]'s tree), which the C lane emits as an inlined product
+ * (crates/chelis-backend-c/src/emit.rs:8431-8560). Each product finalizes at
+ * the dtype; the k leaves of every output enter its own carry tree.
+ *
+ * Lanes: VL consecutive output columns and RB rows share one leaf count, so
+ * their trees advance together; each lane still owns a private tree, so the
+ * bits equal the one-output-at-a-time tree. */
+#define DEFINE_MATMUL(NAME, T, NANF, VL)                                              \
+    typedef T NAME##_vec __attribute__((vector_size(VL * sizeof(T))));                \
+    void NAME(const T *A, int64_t sa0, int64_t sa1, const T *B, int64_t sb0,          \
+              int64_t sb1, T *C, int64_t M, int64_t N, int64_t K) {                   \
+        enum { RB = 4 };                                                              \
+        int64_t rblocks = (M + RB - 1) / RB, cblocks = (N + VL - 1) / VL;             \
+        _Pragma("omp parallel for collapse(2) schedule(dynamic, 4)")                  \
+        for (int64_t rb = 0; rb < rblocks; ++rb)                                      \
+            for (int64_t cb = 0; cb < cblocks; ++cb) {                                \
+                NAME##_vec level[RB][64];                                             \
+                int64_t i0 = rb * RB, j0 = cb * VL;                                   \
+                int rows = (int)(M - i0 < RB ? M - i0 : RB);                          \
+                int lanes = (int)(N - j0 < VL ? N - j0 : VL);                         \
+                for (int64_t k = 0; k < K; ++k) {                                     \
+                    NAME##_vec bv;                                                    \
+                    for (int l = 0; l < VL; ++l)                                      \
+                        bv[l] = l < lanes ? B[k * sb0 + (j0 + l) * sb1] : (T)0;       \
+                    int trailing = 0;                                                 \
+                    for (int64_t p = k; p & 1; p >>= 1) ++trailing;                   \
+                    for (int r = 0; r < rows; ++r) {                                  \
+                        NAME##_vec carry = A[(i0 + r) * sa0 + k * sa1] * bv;          \
+                        for (int d = 0; d < trailing; ++d) carry = level[r][d] + carry; \
+                        level[r][trailing] = carry;                                   \
+                    }                                                                 \
+                }                                                                     \
+                for (int r = 0; r < rows; ++r) {                                      \
+                    NAME##_vec total = {0};                                           \
+                    int found = 0, depth = 0;                                         \
+                    for (int64_t rem = K; rem; rem >>= 1, ++depth)                    \
+                        if (rem & 1) {                                                \
+                            total = found ? level[r][depth] + total : level[r][depth]; \
+                            found = 1;                                                \
+                        }                                                             \
+                    for (int l = 0; l < lanes; ++l)                                   \
+                        C[(i0 + r) * N + j0 + l] = NANF(total[l]);                    \
+                }                                                                     \
+            }                                                                         \
+    }
+DEFINE_MATMUL(orc_matmul_f32, float, nan32, 8)
+DEFINE_MATMUL(orc_matmul_f64, double, nan64, 4)
+
+/* ------------------------------------------------------------------ */
+/* Configuration 1, the linear-regression gradient step (linreg.ch form):
+ *   r = matmul(X, w) - y;  grad = matmul(X^T, r) / n;  loss = mean(r * r).
+ * Every matmul is the canonical tree, every mean a tree sum / extent. */
+void orc_linreg_step_f64(const double *X, const double *w, const double *y, double *grad,
+                         double *loss, int64_t n, int64_t d) {
+    double *r = (double *)malloc((size_t)n * sizeof(double));
+    double *sq = (double *)malloc((size_t)n * sizeof(double));
+    double *gs = (double *)malloc((size_t)d * sizeof(double));
+    orc_matmul_f64(X, d, 1, w, 1, 1, r, n, 1, d);
+    for (int64_t i = 0; i < n; ++i) {
+        r[i] = nan64(r[i] - y[i]);
+        sq[i] = nan64(r[i] * r[i]);
+    }
+    orc_matmul_f64(X, 1, d, r, 1, 1, gs, d, 1, n);
+    double extent = (double)n;
+    for (int64_t k = 0; k < d; ++k) grad[k] = nan64(gs[k] / extent);
+    *loss = nan64(orc_tree_sum_f64(sq, n, 1) / extent);
+    free(r);
+    free(sq);
+    free(gs);
+}
+
+/* ------------------------------------------------------------------ */
+static float *falloc(int64_t n) { return (float *)malloc((size_t)n * sizeof(float)); }
+
+/* y[rows, n] = matmul(x, W) + insert(b, 0, rows) */
+static void linear_f32(const float *x, const float *W, const float *b, float *y, int64_t rows,
+                       int64_t k, int64_t n) {
+    orc_matmul_f32(x, k, 1, W, n, 1, y, rows, n, k);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < rows; ++i)
+        for (int64_t j = 0; j < n; ++j) y[i * n + j] = nan32(y[i * n + j] + b[j]);
+}
+
+/* Configuration 4: one pre-LN transformer block, causal multi-head
+ * attention (spec/05 section 4.7) and a GELU FFN, all f32:
+ *   h = LN1(x); q,k,v = linear(h); per head: s = (q k^T) * scale,
+ *   masked = where(j <= i, s, -inf), p = softmax(masked), o = p v;
+ *   x1 = x + linear_o(o); y = x1 + linear_2(GELU(linear_1(LN2(x1)))).
+ * params: ln1_g ln1_b Wq bq Wk bk Wv bv Wo bo ln2_g ln2_b W1 b1 W2 b2. */
+void orc_transformer_block_f32(const float *x, const float *const *P, float *out, int64_t batch,
+                               int64_t seq, int64_t dm, int64_t heads, int64_t ffn) {
+    int64_t rows = batch * seq, dh = dm / heads;
+    const float eps = 1e-5f;
+    const float scale = 1.0f / sqrtf((float)dh);
+    float *h = falloc(rows * dm), *q = falloc(rows * dm), *k = falloc(rows * dm);
+    float *v = falloc(rows * dm), *o = falloc(rows * dm), *x1 = falloc(rows * dm);
+    float *f = falloc(rows * ffn), *sc = falloc(seq * seq);
+    orc_layer_norm_rows_f32(x, P[0], P[1], eps, h, rows, dm);
+    linear_f32(h, P[2], P[3], q, rows, dm, dm);
+    linear_f32(h, P[4], P[5], k, rows, dm, dm);
+    linear_f32(h, P[6], P[7], v, rows, dm, dm);
+    for (int64_t b = 0; b < batch; ++b)
+        for (int64_t hd = 0; hd < heads; ++hd) {
+            const float *qb = q + b * seq * dm + hd * dh;
+            const float *kb = k + b * seq * dm + hd * dh;
+            const float *vb = v + b * seq * dm + hd * dh;
+            orc_matmul_f32(qb, dm, 1, kb, 1, dm, sc, seq, seq, dh);
+            for (int64_t i = 0; i < seq; ++i)
+                for (int64_t j = 0; j < seq; ++j) {
+                    float s = nan32(sc[i * seq + j] * scale);
+                    sc[i * seq + j] = j <= i ? s : -INFINITY;
+                }
+            orc_softmax_rows_f32(sc, sc, seq, seq);
+            float *ob = falloc(seq * dh);
+            orc_matmul_f32(sc, seq, 1, vb, dm, 1, ob, seq, dh, seq);
+            for (int64_t i = 0; i < seq; ++i)
+                memcpy(o + (b * seq + i) * dm + hd * dh, ob + i * dh, (size_t)dh * sizeof(float));
+            free(ob);
+        }
+    linear_f32(o, P[8], P[9], q, rows, dm, dm); /* q reused as the attention output */
+    for (int64_t i = 0; i < rows * dm; ++i) x1[i] = nan32(x[i] + q[i]);
+    orc_layer_norm_rows_f32(x1, P[10], P[11], eps, h, rows, dm);
+    linear_f32(h, P[12], P[13], f, rows, dm, ffn);
+    orc_gelu_f32(f, f, rows * ffn);
+    linear_f32(f, P[14], P[15], q, rows, ffn, dm);
+    for (int64_t i = 0; i < rows * dm; ++i) out[i] = nan32(x1[i] + q[i]);
+    free(h); free(q); free(k); free(v); free(o); free(x1); free(f); free(sc);
+}
+
+/* Configuration 5: one MLP training step (mnist.ch form) with keyed dropout:
+ *   z1 = x W1 + b1; h = relu(z1); d = dropout(key, h, rate);
+ *   z2 = d W2 + b2; p = softmax(z2); loss = mean(-sum(log(p) * onehot, 1));
+ * reverse mode by the spec's adjoints (mean: g / extent; neg; sum: expand;
+ * mul; log: g / x; softmax: y * (g - sum(g * y)) as in
+ * crates/chelis-dag-core/src/grad.rs:2248; matmul: the transposed
+ * canonical-tree contractions; bias: tree sum over the batch; dropout
+ * replay; relu adjoint), then SGD w = w - lr * g in place. */
+void orc_mlp_train_step_f32(const float *x, const float *onehot, float *w1, float *b1, float *w2,
+                            float *b2, uint64_t key, float rate, float lr, float *loss,
+                            int64_t B, int64_t din, int64_t dh, int64_t dout) {
+    float *z1 = falloc(B * dh), *hd = falloc(B * dh), *d = falloc(B * dh);
+    float *z2 = falloc(B * dout), *p = falloc(B * dout), *t = falloc(B * dout);
+    float *nl = falloc(B), *gz2 = falloc(B * dout), *gd = falloc(B * dh);
+    float *gw2 = falloc(dh * dout), *gw1 = falloc(din * dh), *gb1 = falloc(dh), *gb2 = falloc(dout);
+    if (dout > 64) abort(); /* the per-row softmax-adjoint scratch below holds 64 classes */
+    linear_f32(x, w1, b1, z1, B, din, dh);
+    orc_relu_f32(z1, hd, B * dh);
+    orc_dropout_f32(key, hd, rate, d, B * dh);
+    linear_f32(d, w2, b2, z2, B, dh, dout);
+    orc_softmax_rows_f32(z2, p, B, dout);
+    for (int64_t b = 0; b < B; ++b) {
+        for (int64_t c = 0; c < dout; ++c) t[b * dout + c] = nan32(orc_logf(p[b * dout + c]) * onehot[b * dout + c]);
+        nl[b] = nan32(-orc_tree_sum_f32(t + b * dout, dout, 1));
+    }
+    *loss = nan32(orc_tree_sum_f32(nl, B, 1) / (float)B);
+    /* backward */
+    float g_nl = nan32(1.0f / (float)B);
+    float g_pr = nan32(-g_nl);
+    for (int64_t b = 0; b < B; ++b) {
+        for (int64_t c = 0; c < dout; ++c) {
+            float g_lp = nan32(g_pr * onehot[b * dout + c]);
+            float g_p = nan32(g_lp / p[b * dout + c]);
+            t[b * dout + c] = g_p;                    /* g */
+        }
+        float gy[64];
+        for (int64_t c = 0; c < dout; ++c) gy[c] = nan32(t[b * dout + c] * p[b * dout + c]);
+        float s = orc_tree_sum_f32(gy, dout, 1);
+        for (int64_t c = 0; c < dout; ++c)
+            gz2[b * dout + c] = nan32(p[b * dout + c] * nan32(t[b * dout + c] - s));
+    }
+    orc_sum_axis_f32(gz2, 1, B, dout, gb2);
+    orc_matmul_f32(d, 1, dh, gz2, dout, 1, gw2, dh, dout, B);   /* d^T gz2 */
+    orc_matmul_f32(gz2, dout, 1, w2, 1, dout, gd, B, dh, dout); /* gz2 W2^T */
+    orc_dropout_replay_f32(key, gd, rate, gd, B * dh);
+    orc_relu_adjoint_f32(z1, gd, gd, B * dh);
+    orc_sum_axis_f32(gd, 1, B, dh, gb1);
+    orc_matmul_f32(x, 1, din, gd, dh, 1, gw1, din, dh, B);      /* x^T gz1 */
+    for (int64_t i = 0; i < din * dh; ++i) w1[i] = nan32(w1[i] - nan32(lr * gw1[i]));
+    for (int64_t i = 0; i < dh; ++i) b1[i] = nan32(b1[i] - nan32(lr * gb1[i]));
+    for (int64_t i = 0; i < dh * dout; ++i) w2[i] = nan32(w2[i] - nan32(lr * gw2[i]));
+    for (int64_t i = 0; i < dout; ++i) b2[i] = nan32(b2[i] - nan32(lr * gb2[i]));
+    free(z1); free(hd); free(d); free(z2); free(p); free(t); free(nl); free(gz2); free(gd);
+    free(gw2); free(gw1); free(gb1); free(gb2);
+}

@@ -1,0 +1,279 @@
+"""ctypes view of the CPU oracle (liboracle.so): TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this module, and only as the checker or the timed CPU baseline. The product
+package (chelis_amd) never imports it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+_lib = None
+
+
+def build() -> None:
+    """Compile the oracle (and, where /root/reference exists, oracle/_ref)."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"oracle library missing: {LIB_PATH} (run `make -C oracle`)")
+        _lib = ctypes.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+c_i64, c_u64, c_f32, c_f64, c_p = ctypes.c_int64, ctypes.c_uint64, ctypes.c_float, ctypes.c_double, ctypes.c_void_p
+
+
+def _declare(L):
+    sig = {
+        "orc_splitmix64": (c_u64, [c_u64]),
+        "orc_derive": (c_u64, [c_u64, c_u64]),
+        "orc_word": (c_u64, [c_u64, c_u64]),
+        "orc_unit": (c_f64, [c_u64, c_u64]),
+        "orc_split": (None, [c_u64, c_p]),
+        "orc_fold_in": (c_u64, [c_u64, c_i64]),
+        "orc_split_n": (None, [c_u64, c_i64, c_p]),
+        "orc_uniform_like_f32": (None, [c_u64, c_f32, c_f32, c_p, c_i64]),
+        "orc_uniform_like_f64": (None, [c_u64, c_f64, c_f64, c_p, c_i64]),
+        "orc_expf": (c_f32, [c_f32]), "orc_exp": (c_f64, [c_f64]),
+        "orc_logf": (c_f32, [c_f32]), "orc_log": (c_f64, [c_f64]),
+        "orc_erfcf": (c_f32, [c_f32]), "orc_erfc": (c_f64, [c_f64]),
+        "orc_tanhf": (c_f32, [c_f32]), "orc_tanh": (c_f64, [c_f64]),
+        "orc_tree_sum_f32": (c_f32, [c_p, c_i64, c_i64]),
+        "orc_tree_sum_f64": (c_f64, [c_p, c_i64, c_i64]),
+        "orc_level_sum_f32": (c_f32, [c_p, c_i64]),
+        "orc_level_sum_f64": (c_f64, [c_p, c_i64]),
+        "orc_max_reduce_f32": (c_f32, [c_p, c_i64, c_i64]),
+        "orc_max_reduce_f64": (c_f64, [c_p, c_i64, c_i64]),
+        "orc_sum_axis_f32": (None, [c_p, c_i64, c_i64, c_i64, c_p]),
+        "orc_sum_axis_f64": (None, [c_p, c_i64, c_i64, c_i64, c_p]),
+        "orc_max_axis_f32": (None, [c_p, c_i64, c_i64, c_i64, c_p]),
+        "orc_max_axis_f64": (None, [c_p, c_i64, c_i64, c_i64, c_p]),
+        "orc_count_axis": (ctypes.c_int32, [c_p, c_i64, c_i64, c_i64, c_p]),
+        "orc_softmax_rows_f32": (None, [c_p, c_p, c_i64, c_i64]),
+        "orc_softmax_rows_f64": (None, [c_p, c_p, c_i64, c_i64]),
+        "orc_layer_norm_rows_f32": (None, [c_p, c_p, c_p, c_f32, c_p, c_i64, c_i64]),
+        "orc_layer_norm_rows_f64": (None, [c_p, c_p, c_p, c_f64, c_p, c_i64, c_i64]),
+        "orc_gelu_f32": (None, [c_p, c_p, c_i64]),
+        "orc_gelu_f64": (None, [c_p, c_p, c_i64]),
+        "orc_relu_f32": (None, [c_p, c_p, c_i64]),
+        "orc_relu_adjoint_f32": (None, [c_p, c_p, c_p, c_i64]),
+        "orc_dropout_f32": (None, [c_u64, c_p, c_f32, c_p, c_i64]),
+        "orc_dropout_replay_f32": (None, [c_u64, c_p, c_f32, c_p, c_i64]),
+        "orc_dropout_f64": (None, [c_u64, c_p, c_f64, c_p, c_i64]),
+        "orc_matmul_f32": (None, [c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_i64]),
+        "orc_matmul_f64": (None, [c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_i64]),
+        "orc_linreg_step_f64": (None, [c_p, c_p, c_p, c_p, c_p, c_i64, c_i64]),
+        "orc_transformer_block_f32": (None, [c_p, c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_i64]),
+        "orc_mlp_train_step_f32": (None, [c_p, c_p, c_p, c_p, c_p, c_p, c_u64, c_f32, c_f32, c_p,
+                                          c_i64, c_i64, c_i64, c_i64]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def _ptr(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data
+
+
+def _f(dtype):
+    return "f32" if np.dtype(dtype) == np.float32 else "f64"
+
+
+# ---- RNG ----
+def split(key: int) -> tuple[int, int]:
+    out = np.zeros(2, np.uint64)
+    lib().orc_split(key & (2**64 - 1), _ptr(out))
+    return int(out[0]), int(out[1])
+
+
+def fold_in(key: int, n: int) -> int:
+    return int(lib().orc_fold_in(key & (2**64 - 1), n))
+
+
+def split_n(key: int, n: int) -> list[int]:
+    out = np.zeros(max(n, 1), np.uint64)
+    lib().orc_split_n(key & (2**64 - 1), n, _ptr(out))
+    return [int(v) for v in out[:n]]
+
+
+def unit(key: int, index: int) -> float:
+    return float(lib().orc_unit(key & (2**64 - 1), index))
+
+
+def uniform_like(key: int, low, high, n: int, dtype=np.float32) -> np.ndarray:
+    out = np.empty(n, dtype)
+    getattr(lib(), f"orc_uniform_like_{_f(dtype)}")(key & (2**64 - 1), low, high, _ptr(out), n)
+    return out
+
+
+# ---- reductions ----
+def tree_sum(x: np.ndarray) -> np.floating:
+    x = np.ascontiguousarray(x)
+    return x.dtype.type(getattr(lib(), f"orc_tree_sum_{_f(x.dtype)}")(_ptr(x), x.size, 1))
+
+
+def level_sum(x: np.ndarray) -> np.floating:
+    x = np.ascontiguousarray(x)
+    return x.dtype.type(getattr(lib(), f"orc_level_sum_{_f(x.dtype)}")(_ptr(x), x.size))
+
+
+def _axis_view(x: np.ndarray, axis: int):
+    axis = axis % x.ndim
+    outer = int(np.prod(x.shape[:axis], dtype=np.int64))
+    inner = int(np.prod(x.shape[axis + 1:], dtype=np.int64))
+    return outer, x.shape[axis], inner, x.shape[:axis] + x.shape[axis + 1:]
+
+
+def sum_axis(x: np.ndarray, axis: int) -> np.ndarray:
+    x = np.ascontiguousarray(x)
+    outer, n, inner, shape = _axis_view(x, axis)
+    out = np.empty(shape, x.dtype)
+    getattr(lib(), f"orc_sum_axis_{_f(x.dtype)}")(_ptr(x), outer, n, inner, _ptr(out))
+    return out
+
+
+def max_axis(x: np.ndarray, axis: int) -> np.ndarray:
+    x = np.ascontiguousarray(x)
+    outer, n, inner, shape = _axis_view(x, axis)
+    out = np.empty(shape, x.dtype)
+    getattr(lib(), f"orc_max_axis_{_f(x.dtype)}")(_ptr(x), outer, n, inner, _ptr(out))
+    return out
+
+
+def count_axis(x: np.ndarray, axis: int):
+    x = np.ascontiguousarray(x, dtype=np.uint8)
+    outer, n, inner, shape = _axis_view(x, axis)
+    out = np.empty(shape, np.int64)
+    err = lib().orc_count_axis(_ptr(x), outer, n, inner, _ptr(out))
+    return out, int(err)
+
+
+# ---- row regions / elementwise ----
+def softmax_rows(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x)
+    y = np.empty_like(x)
+    n = x.shape[-1]
+    getattr(lib(), f"orc_softmax_rows_{_f(x.dtype)}")(_ptr(x), _ptr(y), x.size // max(n, 1), n)
+    return y
+
+
+def layer_norm_rows(x, gamma, beta, eps) -> np.ndarray:
+    x = np.ascontiguousarray(x)
+    g = np.ascontiguousarray(gamma, x.dtype)
+    b = np.ascontiguousarray(beta, x.dtype)
+    y = np.empty_like(x)
+    n = x.shape[-1]
+    getattr(lib(), f"orc_layer_norm_rows_{_f(x.dtype)}")(_ptr(x), _ptr(g), _ptr(b), eps, _ptr(y),
+                                                          x.size // n, n)
+    return y
+
+
+def gelu(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x)
+    y = np.empty_like(x)
+    getattr(lib(), f"orc_gelu_{_f(x.dtype)}")(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def relu(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().orc_relu_f32(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def relu_adjoint(x, g) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    g = np.ascontiguousarray(g, np.float32)
+    y = np.empty_like(x)
+    lib().orc_relu_adjoint_f32(_ptr(x), _ptr(g), _ptr(y), x.size)
+    return y
+
+
+def dropout(key: int, x: np.ndarray, rate) -> np.ndarray:
+    x = np.ascontiguousarray(x)
+    y = np.empty_like(x)
+    getattr(lib(), f"orc_dropout_{_f(x.dtype)}")(key & (2**64 - 1), _ptr(x), rate, _ptr(y), x.size)
+    return y
+
+
+def dropout_replay(key: int, g: np.ndarray, rate) -> np.ndarray:
+    g = np.ascontiguousarray(g, np.float32)
+    y = np.empty_like(g)
+    lib().orc_dropout_replay_f32(key & (2**64 - 1), _ptr(g), rate, _ptr(y), g.size)
+    return y
+
+
+def matmul(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Canonical-tree matmul of 2-D arrays (any strides, via element strides)."""
+    assert a.dtype == b.dtype and a.ndim == 2 and b.ndim == 2 and a.shape[1] == b.shape[0]
+    isz = a.dtype.itemsize
+    M, K = a.shape
+    N = b.shape[1]
+    c = np.empty((M, N), a.dtype)
+    getattr(lib(), f"orc_matmul_{_f(a.dtype)}")(
+        a.ctypes.data, a.strides[0] // isz, a.strides[1] // isz,
+        b.ctypes.data, b.strides[0] // isz, b.strides[1] // isz, _ptr(c), M, N, K)
+    return c
+
+
+def unary(name: str, x: np.ndarray) -> np.ndarray:
+    fn = getattr(lib(), f"orc_{name}{'f' if x.dtype == np.float32 else ''}")
+    return np.array([fn(v) for v in x.ravel()], x.dtype).reshape(x.shape)
+
+
+# ---- programs ----
+def linreg_step(X, w, y):
+    X = np.ascontiguousarray(X, np.float64)
+    w = np.ascontiguousarray(w, np.float64)
+    y = np.ascontiguousarray(y, np.float64)
+    n, d = X.shape
+    grad = np.empty(d, np.float64)
+    loss = np.empty(1, np.float64)
+    lib().orc_linreg_step_f64(_ptr(X), _ptr(w), _ptr(y), _ptr(grad), _ptr(loss), n, d)
+    return grad, loss[0]
+
+
+TRANSFORMER_PARAMS = ("ln1_g", "ln1_b", "wq", "bq", "wk", "bk", "wv", "bv", "wo", "bo",
+                      "ln2_g", "ln2_b", "w1", "b1", "w2", "b2")
+
+
+def transformer_block(x, params: dict, heads: int):
+    x = np.ascontiguousarray(x, np.float32)
+    batch, seq, dm = x.shape
+    ffn = params["w1"].shape[1]
+    arrs = [np.ascontiguousarray(params[k], np.float32) for k in TRANSFORMER_PARAMS]
+    ptrs = (ctypes.c_void_p * 16)(*[a.ctypes.data for a in arrs])
+    out = np.empty_like(x)
+    lib().orc_transformer_block_f32(_ptr(x), ctypes.cast(ptrs, ctypes.c_void_p), _ptr(out),
+                                    batch, seq, dm, heads, ffn)
+    return out
+
+
+def mlp_train_step(x, onehot, w1, b1, w2, b2, key, rate, lr):
+    """Returns (loss, w1', b1', w2', b2'); inputs are not modified."""
+    x = np.ascontiguousarray(x, np.float32)
+    onehot = np.ascontiguousarray(onehot, np.float32)
+    w1, b1, w2, b2 = (np.array(a, np.float32, copy=True) for a in (w1, b1, w2, b2))
+    loss = np.empty(1, np.float32)
+    B, din = x.shape
+    dh, dout = w2.shape
+    lib().orc_mlp_train_step_f32(_ptr(x), _ptr(onehot), _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2),
+                                 key & (2**64 - 1), rate, lr, _ptr(loss), B, din, dh, dout)
+    return loss[0], w1, b1, w2, b2

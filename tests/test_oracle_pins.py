@@ -1,0 +1,295 @@
+"""Pins of the CPU oracle against the reference's own golden vectors, an
+independent restatement or what the mathematics fixes. CPU only.
+
+What pins what:
+  RNG (splitmix64/derive/word/unit/split/fold_in/split_n): KAT hex values of
+      crates/chelis-numeric-core/tests/random_key_reference.rs:86-140.
+  keyed dropout + replay: crates/chelis-cli/tests/dropout_fixed_stream_cli.rs
+      (fixed-stream vectors [2,0,0,2] and [2,2,0,0]).
+  correctly rounded exp/log/erfc/tanh: CORE-MATH MPFR canary fixture
+      (crates/chelis-crmath/tests/fixtures/canary.txt), bit for bit.
+  canonical tree sum: the pass-by-pass restatement of spec/05 section 2.3 in
+      C and an independent numpy restatement, on inputs whose bits change
+      under any other association; the [05-OP-30] trace (((a+b)+(c+d))+e).
+  max_reduce: the first-NaN and first-representation rules of [05-OP-12].
+  matmul: crates/chelis-cli/tests/fixtures/inlined_product/matmul.expected;
+      lanes vs the scalar tree on random shapes.
+  softmax / layer norm / GELU: float64 closed forms within a few ulps plus
+      special values fixed by the spec (GELU(-inf) = -0, Phi graph limits).
+"""
+import json
+import math
+import os
+import struct
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def setup_module(_m):
+    O.build()
+
+
+def h(s):
+    return int(s, 16)
+
+
+# ---------------------------------------------------------------- RNG
+def test_rng_known_answers():
+    g = json.load(open(os.path.join(GOLD, "key_reference.json")))
+    k7 = 7
+    assert O.split(k7) == tuple(h(v) for v in g["key7_split"])
+    assert O.fold_in(k7, 3) == h(g["key7_fold_in_3"])
+    assert O.fold_in(k7, -1) == h(g["key7_fold_in_minus1"])
+    assert O.split_n(k7, 3) == [h(v) for v in g["key7_split_n_3"]]
+    assert int(O.lib().orc_derive(k7, 2)) == h(g["key7_derive_2"])
+    assert O.unit(k7, 0) == g["key7_units_1"][0]
+    c = g["chain"]
+    km3 = (-3) & (2**64 - 1)
+    assert km3 == h(c["key_minus3_bits"])
+    left, right = O.split(km3)
+    assert (left, right) == (h(c["split_left"]), h(c["split_right"]))
+    folded = O.fold_in(left, -5)
+    assert folded == h(c["left_fold_in_minus5"])
+    assert O.split_n(folded, 3) == [h(v) for v in c["folded_split_n_3"]]
+    assert O.fold_in(right, 9) == h(c["right_fold_in_9"])
+
+
+def test_dropout_fixed_stream():
+    g = json.load(open(os.path.join(GOLD, "key_reference.json")))["dropout_fixed_stream"]
+    left, right = O.split(g["seed"])
+    x = np.array(g["x"], np.float32)
+    assert O.dropout(right, x, np.float32(g["rate"])).tolist() == g["forward_right_key"]
+    # grad of sum(dropout(left, x)) wrt x is the replay of ones
+    assert O.dropout_replay(left, np.ones(4, np.float32), np.float32(g["rate"])).tolist() == g["grad_left_key"]
+
+
+def test_dropout_rate_zero_is_identity_and_mask_matches_units():
+    key = O.fold_in(44, 0)
+    x = np.random.default_rng(0).standard_normal(4096).astype(np.float32)
+    assert np.array_equal(O.dropout(key, x, np.float32(0.0)), x)
+    y = O.dropout(key, x, np.float32(0.1))
+    units = np.array([O.unit(key, i) for i in range(x.size)])
+    dropped = units.astype(np.float32) < np.float32(0.1)
+    assert np.array_equal(y == 0, dropped | (x == 0))
+    assert np.array_equal(y[~dropped], x[~dropped] / (np.float32(1) - np.float32(0.1)))
+    assert 0.08 < dropped.mean() < 0.12
+
+
+def test_uniform_like_is_the_fma_of_the_unit():
+    key = 12345
+    u = O.uniform_like(key, np.float64(0.0), np.float64(1.0), 64, np.float64)
+    assert [O.unit(key, i) for i in range(64)] == u.tolist()
+
+
+# ---------------------------------------------------------------- CORE-MATH
+def _canary_rows():
+    rows = []
+    for line in open(os.path.join(GOLD, "crmath_canary.txt")):
+        if line.startswith("#") or not line.strip():
+            continue
+        fn, width, xin, xout = line.split()[:4]
+        rows.append((fn, width, xin, xout))
+    return rows
+
+
+@pytest.mark.parametrize("fn", ["exp", "log", "erfc", "tanh"])
+def test_correctly_rounded_leaves_match_mpfr_canary(fn):
+    L = O.lib()
+    n = 0
+    for f, width, xin, xout in _canary_rows():
+        if f != fn:
+            continue
+        if width == "f32":
+            x = struct.unpack("<f", struct.pack("<I", h(xin)))[0]
+            got = struct.unpack("<I", struct.pack("<f", getattr(L, f"orc_{fn}f")(x)))[0]
+        else:
+            x = struct.unpack("<d", struct.pack("<Q", h(xin)))[0]
+            got = struct.unpack("<Q", struct.pack("<d", getattr(L, f"orc_{fn}")(x)))[0]
+        assert got == h(xout), (fn, width, xin)
+        n += 1
+    assert n > 30
+
+
+# ---------------------------------------------------------------- tree sum
+def _np_level_sum(x):
+    """Independent numpy restatement of spec/05 section 2.3's level passes."""
+    vals = list(x)
+    if not vals:
+        return x.dtype.type(0)
+    while len(vals) > 1:
+        nxt = [vals[i] + vals[i + 1] for i in range(0, len(vals) - 1, 2)]
+        if len(vals) % 2:
+            nxt.append(vals[-1])
+        vals = nxt
+    return vals[0]
+
+
+def _adversarial(n, dtype, seed):
+    rng = np.random.default_rng(seed)
+    mag = rng.choice([1e-8, 1.0, 1e8, 3e-3], size=n)
+    return (rng.standard_normal(n) * mag).astype(dtype)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_tree_sum_matches_level_passes(dtype):
+    ns = list(range(0, 70)) + [2**k + d for k in range(6, 13) for d in (-1, 0, 1)] + [1000, 4095]
+    for n in ns:
+        x = _adversarial(n, dtype, n)
+        t = O.tree_sum(x)
+        assert t.tobytes() == O.level_sum(x).tobytes(), n
+        if n <= 300:
+            assert t.tobytes() == dtype(_np_level_sum(x)).tobytes(), n
+
+
+def test_tree_sum_shape_is_the_canonical_trace():
+    # (((a+b)+(c+d))+e): with a=1e8, c=-1e8 the pairwise sums keep b,d exact
+    # only under this association.
+    x = np.array([1e8, 1.0, -1e8, 1.0, 0.5], np.float32)
+    a, b, c, d, e = (np.float32(v) for v in x)
+    assert O.tree_sum(x) == ((a + b) + (c + d)) + e
+    assert O.tree_sum(x) != (((a + b) + c) + d) + e   # a left fold differs
+
+
+def test_tree_sum_empty_and_signed_zero():
+    assert O.tree_sum(np.zeros(0, np.float32)).tobytes() == np.float32(0).tobytes()
+    assert O.tree_sum(np.array([-0.0], np.float32)).tobytes() == np.float32(-0.0).tobytes()
+    assert O.tree_sum(np.array([-0.0, -0.0, -0.0], np.float64)).tobytes() == np.float64(-0.0).tobytes()
+    nan = O.tree_sum(np.array([1.0, np.inf, -np.inf], np.float32))
+    assert nan.view(np.uint32) == 0x7FC00000
+
+
+def test_sum_axis_is_tree_per_slice():
+    x = _adversarial(5 * 37 * 3, np.float32, 1).reshape(5, 37, 3)
+    s = O.sum_axis(x, 1)
+    for o in range(5):
+        for j in range(3):
+            assert s[o, j] == O.tree_sum(x[o, :, j].copy())
+
+
+# ---------------------------------------------------------------- max / count
+def test_max_reduce_first_nan_and_first_representation():
+    nan_a = np.array([0x7FC00001], np.uint32).view(np.float32)[0]
+    nan_b = np.array([0xFFC00002], np.uint32).view(np.float32)[0]
+    x = np.array([1.0, nan_a, 5.0, nan_b], np.float32)
+    assert O.max_axis(x, 0).view(np.uint32) == 0x7FC00001
+    z = np.array([-0.0, 0.0, -1.0], np.float32)
+    assert O.max_axis(z, 0).tobytes() == np.float32(-0.0).tobytes()
+    r = np.random.default_rng(3).standard_normal((64, 33))
+    assert np.array_equal(O.max_axis(r, 1), r.max(1))
+
+
+def test_count_axis():
+    rng = np.random.default_rng(4)
+    b = (rng.random((7, 300)) < 0.3).astype(np.uint8)
+    c, err = O.count_axis(b, 1)
+    assert err == 0 and np.array_equal(c, b.sum(1))
+    b[3, 5] = 2
+    assert O.count_axis(b, 1)[1] == 1
+
+
+# ---------------------------------------------------------------- matmul
+def _decimal(v):
+    if np.isnan(v):
+        return "NaN"
+    if np.isinf(v):
+        return "inf" if v > 0 else "-inf"
+    r = repr(float(v)) if v.dtype == np.float64 else str(v)
+    return r.replace("e+", "e")
+
+
+def test_matmul_inlined_product_golden():
+    g = json.load(open(os.path.join(GOLD, "matmul_inlined_product.json")))
+    a = np.array(g["a32"], np.float32)
+    b = np.array(g["b32"], np.float32)
+    c = O.matmul(a, b).ravel()
+    assert [_decimal(v) for v in c] == g["f32"]
+    c64 = O.matmul(a.astype(np.float64), b.astype(np.float64)).ravel()
+    assert [_decimal(v) for v in c64] == g["f64_of_f32_inputs"]
+    cr = O.matmul(O.relu(a), b).ravel()
+    assert [_decimal(v) for v in cr] == g["relu_a32_f32"]
+    ir = O.matmul(np.array(g["inf_row"], np.float32), np.array(g["zero_col"], np.float32)).ravel()
+    assert [_decimal(v) for v in ir] == g["inf_row_times_zero_col"]
+    sq = O.matmul(a, a.T).ravel()    # strided view: the transpose is not copied
+    assert [_decimal(v) for v in sq] == g["square_a32_a32T"]
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_matmul_lanes_equal_scalar_tree(dtype):
+    rng = np.random.default_rng(5)
+    for M, N, K in [(1, 1, 1), (3, 9, 5), (7, 17, 33), (5, 3, 64), (9, 12, 100)]:
+        a = _adversarial(M * K, dtype, M).reshape(M, K)
+        b = _adversarial(K * N, dtype, N).reshape(K, N)
+        c = O.matmul(a, b)
+        for i in range(M):
+            for j in range(N):
+                assert c[i, j].tobytes() == O.tree_sum((a[i] * b[:, j]).astype(dtype)).tobytes()
+        ref = a.astype(np.float64) @ b.astype(np.float64)
+        assert np.allclose(c, ref, rtol=1e-3, atol=1e-3 * np.abs(ref).max())
+    del rng
+
+
+# ---------------------------------------------------------------- row regions
+@pytest.mark.parametrize("dtype,n", [(np.float32, 1024), (np.float32, 10), (np.float64, 777)])
+def test_softmax_rows_closed_form(dtype, n):
+    x = (np.random.default_rng(6).standard_normal((64, n)) * 2).astype(dtype)
+    y = O.softmax_rows(x)
+    x64 = x.astype(np.float64)
+    e = np.exp(x64 - x64.max(1, keepdims=True))
+    ref = e / e.sum(1, keepdims=True)
+    # the f32 subtraction x - max rounds at |x - max| * 2^-24 before exp
+    tol = 2e-6 if dtype == np.float32 else 1e-14
+    assert np.max(np.abs(y - ref) / ref) < tol
+
+
+def test_softmax_special_rows():
+    x = np.array([[0.0, -np.inf, 1.0, -np.inf], [-np.inf] * 4, [3.0, 3.0, 3.0, 3.0], [1.0, np.nan, 0, 0]],
+                 np.float32)
+    y = O.softmax_rows(x)
+    assert y[0, 1] == 0 and y[0, 3] == 0 and abs(y[0].sum() - 1) < 1e-6
+    assert (y[1].view(np.uint32) == 0x7FC00000).all()
+    assert (y[2] == 0.25).all()
+    assert (y[3].view(np.uint32) == 0x7FC00000).all()
+    assert O.softmax_rows(np.array([[5.0]], np.float32))[0, 0] == 1.0
+
+
+def test_layer_norm_closed_form():
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((32, 1024)).astype(np.float32)
+    g = rng.standard_normal(1024).astype(np.float32)
+    b = rng.standard_normal(1024).astype(np.float32)
+    y = O.layer_norm_rows(x, g, b, np.float32(1e-5))
+    x64 = x.astype(np.float64)
+    m = x64.mean(1, keepdims=True)
+    v = ((x64 - m) ** 2).mean(1, keepdims=True)
+    ref = (x64 - m) / np.sqrt(v + 1e-5) * g + b
+    assert np.max(np.abs(y - ref)) < 2e-5
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_gelu_closed_form_and_limits(dtype):
+    x = np.concatenate([np.linspace(-12, 12, 20001), np.random.default_rng(8).standard_normal(5000) * 3]).astype(dtype)
+    y = O.gelu(x)
+    ref = np.array([float(v) * 0.5 * math.erfc(-float(v) / math.sqrt(2)) for v in x])
+    big = np.abs(ref) > 1e-30
+    rel = np.abs(y[big] - ref[big]) / np.abs(ref[big])
+    # the float64 check rounds -x/sqrt(2) before erfc, an argument error the
+    # Phi graph corrects; at |x| ~ 12 that costs ~2 t^2 eps ~ 3e-14 relative
+    assert rel.max() < (6e-7 if dtype == np.float32 else 5e-14)
+    special = O.gelu(np.array([-np.inf, np.inf, 0.0, -0.0, np.nan, -100.0], dtype))
+    assert special[0] == 0 and np.signbit(special[0])
+    assert special[1] == np.inf and special[2] == 0 and special[3] == 0
+    assert np.isnan(special[4]) and special[5] == 0 and np.signbit(special[5])
+
+
+def test_relu_bit_rules():
+    nan_p = np.array([0x7FC01234], np.uint32).view(np.float32)[0]
+    x = np.array([-1.0, -0.0, 0.0, 2.0, nan_p], np.float32)
+    y = O.relu(x)
+    assert y.view(np.uint32).tolist() == [0, 0x80000000, 0, np.float32(2.0).view(np.uint32), 0x7FC01234]
+    g = np.full(5, 3.0, np.float32)
+    assert O.relu_adjoint(x, g).tolist() == [0, 0, 0, 3.0, 0]
