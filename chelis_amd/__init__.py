@@ -1,0 +1,333 @@
+"""chelis_amd: MI355X-native execution of fused Chelis tensor regions.
+
+The product is the C-ABI library ``libchelis_hip.so`` (headers in
+``include/``). This module is the host-side Python mirror of the
+reference's own binding flow (crates/chelis-python/src/native_tensor.rs:
+210-240): it resolves the same owner symbols by name, moves numpy arrays
+through ``chelis_device_tensor_alloc`` / ``copy_from_host`` /
+``copy_to_host``, and calls the region launchers and program entries.
+
+Loading fails loudly when the library is missing: there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_double, c_int32, c_int64, c_uint8, c_uint64, c_void_p
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libchelis_hip.so")
+
+
+class ChelisError(RuntimeError):
+    pass
+
+
+# ---- ABI types (include/chelis_runtime.h, include/chelis_device_descriptor.h) ----
+DT_F32, DT_F64, DT_I32, DT_BOOL, DT_I64 = 0, 1, 2, 3, 4
+_NP2DT = {np.dtype(np.float32): DT_F32, np.dtype(np.float64): DT_F64, np.dtype(np.int32): DT_I32,
+          np.dtype(np.uint8): DT_BOOL, np.dtype(np.bool_): DT_BOOL, np.dtype(np.int64): DT_I64}
+_DT2NP = {DT_F32: np.float32, DT_F64: np.float64, DT_I32: np.int32, DT_BOOL: np.uint8, DT_I64: np.int64}
+
+
+class Scalar(ctypes.Structure):
+    _fields_ = [("dtype", c_uint8), ("reserved", c_uint8 * 7), ("bits", c_uint64)]
+
+
+class ReadView(ctypes.Structure):
+    _fields_ = [("data", c_void_p), ("count", c_int64), ("dtype", c_uint8), ("reserved", c_uint8 * 7)]
+
+
+class GpuTensor(ctypes.Structure):
+    _fields_ = [("data", c_void_p), ("shape", POINTER(c_int64)), ("strides", POINTER(c_int64)),
+                ("count", c_int64), ("byte_capacity", c_int64), ("rank", c_int32), ("dtype", c_uint8),
+                ("ownership", c_uint8), ("reserved", c_uint8 * 2)]
+
+
+class FusedStep(ctypes.Structure):
+    _fields_ = [("op", c_uint8), ("reserved", c_uint8 * 3), ("args", c_int32 * 2), ("imm", c_double)]
+
+
+class FusedChain(ctypes.Structure):
+    _fields_ = [("n_steps", c_int32), ("reserved", c_int32), ("steps", FusedStep * 16)]
+
+
+P = POINTER(GpuTensor)
+
+# Every exported symbol the headers in include/ declare, with its ctypes
+# signature (restype, argtypes). tests/test_abi.py checks the library
+# exports exactly these names.
+SIGNATURES = {
+    # chelis_runtime.h
+    "chelis_alloc": (c_void_p, [c_int32, POINTER(c_int64), c_uint8]),
+    "chelis_tensor_entry_borrow": (c_void_p, [c_int32, POINTER(c_int64), c_uint8, c_void_p, c_int64]),
+    "chelis_tensor_retain": (None, [c_void_p]),
+    "chelis_tensor_release": (None, [c_void_p]),
+    "chelis_tensor_read_view": (ReadView, [c_void_p]),
+    "chelis_tensor_begin_write": (c_void_p, [c_void_p]),
+    "chelis_tensor_write_view": (ReadView, [c_void_p]),
+    "chelis_tensor_end_write": (None, [c_void_p]),
+    "chelis_dtype_size": (c_int64, [c_uint8]),
+    "chelis_scalar_from_bits": (Scalar, [c_uint8, c_uint64]),
+    "chelis_key_from_seed": (c_uint64, [c_int64]),
+    "chelis_tensor_rank": (c_int32, [c_void_p]),
+    "chelis_tensor_shape": (c_int64, [c_void_p, c_int32]),
+    "chelis_tensor_numel": (c_int64, [c_void_p]),
+    "chelis_metadata_plan_new": (c_void_p, [Scalar, POINTER(Scalar), Scalar]),
+    "chelis_metadata_plan_view": (c_void_p, [Scalar, POINTER(Scalar), POINTER(Scalar), Scalar, Scalar]),
+    "chelis_metadata_plan_rank": (c_int32, [c_void_p]),
+    "chelis_metadata_plan_shape": (POINTER(c_int64), [c_void_p]),
+    "chelis_metadata_plan_strides": (POINTER(c_int64), [c_void_p]),
+    "chelis_metadata_plan_count": (c_int64, [c_void_p]),
+    "chelis_metadata_plan_byte_count": (c_int64, [c_void_p]),
+    "chelis_metadata_plan_byte_offset": (c_int64, [c_void_p, Scalar]),
+    "chelis_metadata_plan_dtype": (c_uint8, [c_void_p]),
+    "chelis_metadata_plan_check_capacity": (None, [c_void_p, Scalar]),
+    "chelis_metadata_plan_release": (None, [c_void_p]),
+    "chelis_contiguous": (c_void_p, [c_void_p]),
+    # chelis_device_owner.h
+    "chelis_device_tensor_alloc": (c_void_p, [c_void_p]),
+    "chelis_device_tensor_borrow": (c_void_p, [c_void_p, c_void_p, Scalar]),
+    "chelis_device_tensor_import": (c_void_p, [P]),
+    "chelis_device_tensor_view": (P, [c_void_p]),
+    "chelis_device_tensor_device": (c_int32, [c_void_p]),
+    "chelis_device_tensor_clone": (c_void_p, [c_void_p]),
+    "chelis_device_tensor_release": (None, [c_void_p]),
+    "chelis_device_tensor_copy_from_host": (None, [c_void_p, c_void_p]),
+    "chelis_device_tensor_copy_to_host": (None, [c_void_p, c_void_p]),
+    # chelis_hip.h
+    "chelis_hip_last_error": (ctypes.c_char_p, []),
+    "chelis_hip_stream": (c_void_p, []),
+    "chelis_hip_synchronize": (c_int32, []),
+    "chelis_hip_build_info": (ctypes.c_char_p, []),
+    "chelis_hip_softmax": (c_int32, [P, P]),
+    "chelis_hip_scaled_masked_softmax": (c_int32, [P, c_double, c_int32, P]),
+    "chelis_hip_softmax_adjoint": (c_int32, [P, P, P]),
+    "chelis_hip_layer_norm": (c_int32, [P, P, P, c_double, P]),
+    "chelis_hip_fused_elementwise": (c_int32, [POINTER(FusedChain), POINTER(P), c_int32, P]),
+    "chelis_hip_gelu": (c_int32, [P, P]),
+    "chelis_hip_relu": (c_int32, [P, P]),
+    "chelis_hip_relu_adjoint": (c_int32, [P, P, P]),
+    "chelis_hip_dropout": (c_int32, [c_uint64, P, c_double, P]),
+    "chelis_hip_dropout_replay": (c_int32, [c_uint64, P, c_double, P]),
+    "chelis_hip_uniform_like": (c_int32, [c_uint64, c_double, c_double, P]),
+}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """The product library. Raises if it was not built: no fallback exists."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ChelisError(f"{LIB_PATH} is missing: build it with `python -m chelis_amd.build`")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name, None)
+            if fn is None:
+                continue
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(status: int, what: str = "") -> None:
+    if status != 0:
+        msg = lib().chelis_hip_last_error().decode(errors="replace")
+        raise ChelisError(f"{what or 'chelis_hip'} failed (status {status}): {msg}")
+
+
+def synchronize() -> None:
+    check(lib().chelis_hip_synchronize(), "synchronize")
+
+
+def i64(v: int) -> Scalar:
+    return lib().chelis_scalar_from_bits(DT_I64, int(v) & (2**64 - 1))
+
+
+# ---- device tensors through the owner API ----
+class DeviceTensor:
+    """An owned (or borrowed) device tensor: a chelis_device_tensor_owner."""
+
+    def __init__(self, owner: int, keep=None):
+        self.owner = owner
+        self._keep = keep
+        self.packet = lib().chelis_device_tensor_view(owner)
+        p = self.packet.contents
+        self.shape = tuple(p.shape[i] for i in range(p.rank))
+        self.strides = tuple(p.strides[i] for i in range(p.rank))
+        self.dtype = np.dtype(_DT2NP[p.dtype])
+        self.data = p.data
+
+    def __del__(self):
+        try:
+            if self.owner:
+                lib().chelis_device_tensor_release(self.owner)
+                self.owner = None
+        except Exception:
+            pass
+
+    @property
+    def size(self) -> int:
+        return int(np.prod(self.shape, dtype=np.int64))
+
+    def view(self, shape, strides, offset_elems: int = 0) -> "View":
+        """A strided packet over this tensor's storage (a transposed or
+        broadcast operand), borrowed for as long as the View lives."""
+        return View(self, shape, strides, offset_elems)
+
+    def numpy(self) -> np.ndarray:
+        return to_host(self)
+
+
+class View:
+    def __init__(self, base: DeviceTensor, shape, strides, offset: int = 0):
+        self.base = base
+        self.shape = tuple(int(s) for s in shape)
+        self.strides = tuple(int(s) for s in strides)
+        self.dtype = base.dtype
+        self._shape = (c_int64 * max(1, len(self.shape)))(*self.shape)
+        self._strides = (c_int64 * max(1, len(self.strides)))(*self.strides)
+        bp = base.packet.contents
+        g = GpuTensor()
+        g.data = (bp.data or 0) + offset * self.dtype.itemsize
+        g.shape = ctypes.cast(self._shape, POINTER(c_int64))
+        g.strides = ctypes.cast(self._strides, POINTER(c_int64))
+        g.count = int(np.prod(self.shape, dtype=np.int64))
+        g.byte_capacity = bp.byte_capacity - offset * self.dtype.itemsize
+        g.rank = len(self.shape)
+        g.dtype = bp.dtype
+        self._g = g
+        self.packet = ctypes.pointer(g)
+
+
+def _plan(shape, dtype) -> int:
+    shape = tuple(int(s) for s in shape)
+    arr = (Scalar * max(1, len(shape)))(*[i64(s) for s in shape])
+    ex = Scalar()
+    ex.dtype = _NP2DT[np.dtype(dtype)]
+    return lib().chelis_metadata_plan_new(i64(len(shape)), arr, ex)
+
+
+def empty(shape, dtype) -> DeviceTensor:
+    """chelis_device_tensor_alloc: a zero-filled owned device tensor."""
+    return DeviceTensor(lib().chelis_device_tensor_alloc(_plan(shape, dtype)))
+
+
+def to_device(a: np.ndarray) -> DeviceTensor:
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.bool_:
+        a = a.view(np.uint8)
+    t = empty(a.shape, a.dtype)
+    shape = (c_int64 * max(1, a.ndim))(*a.shape)
+    host = lib().chelis_tensor_entry_borrow(a.ndim, shape, _NP2DT[a.dtype], a.ctypes.data, a.nbytes)
+    lib().chelis_device_tensor_copy_from_host(t.owner, host)
+    lib().chelis_tensor_release(host)
+    return t
+
+
+def to_host(t) -> np.ndarray:
+    """chelis_device_tensor_copy_to_host into a fresh host tensor."""
+    base = t if isinstance(t, DeviceTensor) else None
+    if base is None:
+        raise TypeError("to_host takes a DeviceTensor (clone a View first)")
+    out = np.empty(t.shape, t.dtype)
+    shape = (c_int64 * max(1, out.ndim))(*out.shape)
+    host = lib().chelis_tensor_entry_borrow(out.ndim, shape, _NP2DT[out.dtype], out.ctypes.data, out.nbytes)
+    guard = lib().chelis_tensor_begin_write(host)
+    lib().chelis_device_tensor_copy_to_host(guard, t.owner)
+    lib().chelis_tensor_end_write(guard)
+    lib().chelis_tensor_release(host)
+    return out
+
+
+def _p(t):
+    return t.packet
+
+
+# ---- region launchers (asynchronous on the library stream) ----
+def softmax(x, y=None):
+    y = y or empty(x.shape, x.dtype)
+    check(lib().chelis_hip_softmax(_p(x), _p(y)), "softmax")
+    return y
+
+
+def scaled_masked_softmax(x, scale: float, causal: bool, y=None):
+    y = y or empty(x.shape, x.dtype)
+    check(lib().chelis_hip_scaled_masked_softmax(_p(x), scale, int(causal), _p(y)), "scaled_masked_softmax")
+    return y
+
+
+def softmax_adjoint(y, g, dx=None):
+    dx = dx or empty(y.shape, y.dtype)
+    check(lib().chelis_hip_softmax_adjoint(_p(y), _p(g), _p(dx)), "softmax_adjoint")
+    return dx
+
+
+def layer_norm(x, gamma, beta, eps: float, y=None):
+    y = y or empty(x.shape, x.dtype)
+    check(lib().chelis_hip_layer_norm(_p(x), _p(gamma), _p(beta), eps, _p(y)), "layer_norm")
+    return y
+
+
+def gelu(x, y=None):
+    y = y or empty(x.shape, x.dtype)
+    check(lib().chelis_hip_gelu(_p(x), _p(y)), "gelu")
+    return y
+
+
+def relu(x, y=None):
+    y = y or empty(x.shape, x.dtype)
+    check(lib().chelis_hip_relu(_p(x), _p(y)), "relu")
+    return y
+
+
+def relu_adjoint(x, g, dx=None):
+    dx = dx or empty(x.shape, x.dtype)
+    check(lib().chelis_hip_relu_adjoint(_p(x), _p(g), _p(dx)), "relu_adjoint")
+    return dx
+
+
+def dropout(key: int, x, rate: float, y=None):
+    y = y or empty(x.shape, x.dtype)
+    check(lib().chelis_hip_dropout(key & (2**64 - 1), _p(x), rate, _p(y)), "dropout")
+    return y
+
+
+def dropout_replay(key: int, g, rate: float, dx=None):
+    dx = dx or empty(g.shape, g.dtype)
+    check(lib().chelis_hip_dropout_replay(key & (2**64 - 1), _p(g), rate, _p(dx)), "dropout_replay")
+    return dx
+
+
+def uniform_like(key: int, low: float, high: float, out):
+    check(lib().chelis_hip_uniform_like(key & (2**64 - 1), low, high, _p(out)), "uniform_like")
+    return out
+
+
+FUSED_OPS = ["add", "sub", "mul", "div", "max_elem", "min_elem", "neg", "recip", "exp", "log", "sqrt", "tanh",
+             "erfc", "abs", "floor", "ceil", "round", "relu", "relu_adjoint", "const"]
+
+
+def fused_chain(steps) -> FusedChain:
+    """steps: list of (op_name, arg0, arg1[, imm]); args >= 0 index inputs,
+    ('s', k) refers to step k."""
+    ch = FusedChain()
+    ch.n_steps = len(steps)
+    for i, st in enumerate(steps):
+        op, args = st[0], list(st[1:3]) + [0] * (2 - len(st[1:3]))
+        ch.steps[i].op = FUSED_OPS.index(op)
+        for j, a in enumerate(args[:2]):
+            ch.steps[i].args[j] = -(a[1] + 1) if isinstance(a, tuple) else int(a)
+        ch.steps[i].imm = float(st[3]) if len(st) > 3 else 0.0
+    return ch
+
+
+def fused_elementwise(chain: FusedChain, inputs, out):
+    arr = (P * max(1, len(inputs)))(*[_p(t) for t in inputs])
+    check(lib().chelis_hip_fused_elementwise(ctypes.byref(chain), arr, len(inputs), _p(out)), "fused_elementwise")
+    return out

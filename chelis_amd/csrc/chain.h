@@ -1,0 +1,123 @@
+// Per-element math shared by the elementwise, reduction and GEMM-epilogue
+// kernels: keyed RNG, transcendental leaves, the GELU graph and the fused
+// chain step evaluator. Each float result is finalized at its dtype with the
+// canonical NaN ([04-NUM-2]) unless the operation is a bit-preserving
+// selection ([05-OP-40], [05-OP-43]).
+#pragma once
+
+#include "hip_common.h"
+
+namespace chelis {
+
+// ---------------------------------------------------------------- RNG
+// [05-RNG-1] splitmix64 and [05-RNG-2] word/unit; identical integer
+// arithmetic on every lane, so draws are bit-exact.
+__device__ inline uint64_t splitmix64(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+__device__ inline double random_unit(uint64_t key, uint64_t index) {
+    const uint64_t e = splitmix64(index);
+    const uint64_t w = splitmix64(key ^ ((e << 41) | (e >> 23)));
+    return (double)(w >> 11) * 0x1p-53;
+}
+
+// ---------------------------------------------------------------- math leaves
+template <typename T> __device__ inline T leaf_exp(T v);
+template <> __device__ inline float leaf_exp<float>(float v) { return expf_cr(v); }
+template <> __device__ inline double leaf_exp<double>(double v) { return canon(exp(v)); }
+// binary32 leaves evaluated in binary64 and rounded once.
+template <typename T> __device__ inline T leaf_erfc(T v) { return canon((T)erfc((double)v)); }
+template <typename T> __device__ inline T leaf_log(T v) { return canon((T)log((double)v)); }
+template <typename T> __device__ inline T leaf_tanh(T v) { return canon((T)tanh((double)v)); }
+template <> __device__ inline double leaf_erfc<double>(double v) { return canon(erfc(v)); }
+template <> __device__ inline double leaf_log<double>(double v) { return canon(log(v)); }
+template <> __device__ inline double leaf_tanh<double>(double v) { return canon(tanh(v)); }
+
+template <typename T> struct Lim;
+template <> struct Lim<float> {
+    __device__ static float lowest() { return -3.4028234663852886e38f; }
+};
+template <> struct Lim<double> {
+    __device__ static double lowest() { return -1.7976931348623157e308; }
+};
+
+// ---------------------------------------------------------------- GELU
+// spec/05 section 3.3: gelu(x) = mul(m(x), Phi(x)) with the exact Phi graph
+// (erfc leaf, Veltkamp-split correction, exp leaf); constants as in
+// crates/chelis-numeric-core/src/activation.rs:41-56.
+template <typename T> struct PhiK;
+template <> struct PhiK<float> {
+    static constexpr float c = (float)0.70710678118654752440, cl = (float)1.2101617485882343e-8,
+                           k = (float)1.12837916709551257390, s = 4097.0f;
+};
+template <> struct PhiK<double> {
+    static constexpr double c = 0.70710678118654752440, cl = -4.833646656726457e-17, k = 1.12837916709551257390,
+                            s = 134217729.0;
+};
+
+template <typename T>
+__device__ inline T gelu_one(T x) {
+    const T c = PhiK<T>::c, cl = PhiK<T>::cl, k = PhiK<T>::k, s = PhiK<T>::s;
+    const T e = leaf_erfc<T>(canon(canon(-x) * c));
+    const T z = (fabs(x) < T(64)) ? x : T(0);
+    const T a = canon(-z);
+    const T th = canon(a * c);
+    const T ta = canon(s * a);
+    const T ah = canon(ta - canon(ta - a));
+    const T al = canon(a - ah);
+    const T tc = canon(s * c);
+    const T ch = canon(tc - canon(tc - c));
+    const T cr = canon(c - ch);
+    T t = canon(canon(ah * ch) - th);
+    t = canon(t + canon(ah * cr));
+    t = canon(t + canon(al * ch));
+    t = canon(t + canon(al * cr));
+    const T tl = canon(t + canon(a * cl));
+    const T g = leaf_exp<T>(canon(-canon(th * th)));
+    const T corr = canon(canon(k * g) * tl);
+    const T phi = canon(T(0.5) * canon(e - corr));
+    const T m = (x < Lim<T>::lowest()) ? T(-0.0) : x;
+    return canon(m * phi);
+}
+
+// ---------------------------------------------------------------- chain ops
+struct ChainDev {
+    int32_t n_steps;
+    uint8_t op[CHELIS_FUSED_MAX_STEPS];
+    int8_t a0[CHELIS_FUSED_MAX_STEPS];
+    int8_t a1[CHELIS_FUSED_MAX_STEPS];
+    double imm[CHELIS_FUSED_MAX_STEPS];
+};
+
+template <typename T>
+__device__ inline T apply_step(uint8_t op, T a, T b, double imm) {
+    switch (op) {
+        case CHELIS_FUSED_ADD: return canon(a + b);
+        case CHELIS_FUSED_SUB: return canon(a - b);
+        case CHELIS_FUSED_MUL: return canon(a * b);
+        case CHELIS_FUSED_DIV: return canon(a / b);
+        case CHELIS_FUSED_MAX_ELEM: return max_first(a, b);  // [05-OP-40] bit preserving
+        case CHELIS_FUSED_MIN_ELEM: return min_first(a, b);
+        case CHELIS_FUSED_NEG: return canon(-a);
+        case CHELIS_FUSED_RECIP: return canon(T(1) / a);
+        case CHELIS_FUSED_EXP: return leaf_exp<T>(a);
+        case CHELIS_FUSED_LOG: return leaf_log<T>(a);
+        case CHELIS_FUSED_SQRT: return canon(sqrt(a));
+        case CHELIS_FUSED_TANH: return leaf_tanh<T>(a);
+        case CHELIS_FUSED_ERFC: return leaf_erfc<T>(a);
+        case CHELIS_FUSED_ABS: return canon(fabs(a));
+        case CHELIS_FUSED_FLOOR: return canon(floor(a));
+        case CHELIS_FUSED_CEIL: return canon(ceil(a));
+        case CHELIS_FUSED_ROUND: return canon(rint(a));
+        case CHELIS_FUSED_RELU: return a < T(0) ? T(0) : a;          // [05-OP-43]
+        case CHELIS_FUSED_RELU_ADJOINT: return T(0) < a ? b : T(0);  // a = x, b = g
+        case CHELIS_FUSED_CONST: return (T)imm;
+        default: return T(0);
+    }
+}
+
+
+}  // namespace chelis

@@ -1,0 +1,149 @@
+// Library context: one HIP stream per device, the last error of the calling
+// thread, and packet validation shared by every launcher.
+//
+// The reference launches on stream 0 and looks up device properties and
+// kernel functions on every launch (runtime/chelis_hip_runtime.h:455-485);
+// here the stream is created once per device (default priority, non-blocking)
+// and kernels are compiled into this library, so a launch is one
+// hipLaunchKernel on that stream.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+#include "hip_common.h"
+
+namespace chelis {
+
+namespace {
+thread_local char g_error[512] = "";
+std::mutex g_stream_mutex;
+constexpr int kMaxDevices = 64;
+hipStream_t g_streams[kMaxDevices] = {};
+}  // namespace
+
+int32_t set_error(int32_t status, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(g_error, sizeof g_error, fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+hipStream_t stream() {
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(g_stream_mutex);
+    if (!g_streams[device]) {
+        hipStream_t s = nullptr;
+        if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return nullptr;
+        g_streams[device] = s;
+    }
+    return g_streams[device];
+}
+
+int32_t check_tensor(const chelis_gpu_tensor *t, const char *name) {
+    if (!t) return set_error(CHELIS_HIP_EDOMAIN, "%s: null tensor packet", name);
+    if (t->rank < 0 || t->rank > 8) return set_error(CHELIS_HIP_EDOMAIN, "%s: rank %d outside 0..8", name, t->rank);
+    if (t->rank > 0 && (!t->shape || !t->strides))
+        return set_error(CHELIS_HIP_EDOMAIN, "%s: null shape or strides", name);
+    if (t->reserved[0] || t->reserved[1]) return set_error(CHELIS_HIP_EDOMAIN, "%s: reserved bytes set", name);
+    int64_t width = dtype_width(t->dtype);
+    if (!width) return set_error(CHELIS_HIP_EDOMAIN, "%s: unknown dtype %d", name, (int)t->dtype);
+    int64_t count = 1, span = 0;
+    for (int32_t a = 0; a < t->rank; ++a) {
+        if (t->shape[a] < 0 || t->strides[a] < 0)
+            return set_error(CHELIS_HIP_EDOMAIN, "%s: negative extent or stride on axis %d", name, a);
+        if (__builtin_mul_overflow(count, t->shape[a], &count))
+            return set_error(CHELIS_HIP_EDOMAIN, "%s: element count overflows i64", name);
+    }
+    if (count != t->count) return set_error(CHELIS_HIP_EDOMAIN, "%s: count %lld != product of shape %lld", name,
+                                            (long long)t->count, (long long)count);
+    if (count) {
+        for (int32_t a = 0; a < t->rank; ++a) {
+            int64_t part;
+            if (__builtin_mul_overflow(t->shape[a] - 1, t->strides[a], &part) ||
+                __builtin_add_overflow(span, part, &span))
+                return set_error(CHELIS_HIP_EDOMAIN, "%s: view span overflows i64", name);
+        }
+        int64_t bytes;
+        if (__builtin_add_overflow(span, 1, &span) || __builtin_mul_overflow(span, width, &bytes) ||
+            bytes > t->byte_capacity)
+            return set_error(CHELIS_HIP_EDOMAIN, "%s: view reaches past byte_capacity %lld", name,
+                             (long long)t->byte_capacity);
+        if (!t->data) return set_error(CHELIS_HIP_EDOMAIN, "%s: null data", name);
+        if (reinterpret_cast<uintptr_t>(t->data) % (uintptr_t)width)
+            return set_error(CHELIS_HIP_EDOMAIN, "%s: data not aligned to its dtype", name);
+    }
+    return CHELIS_HIP_OK;
+}
+
+bool is_contiguous(const chelis_gpu_tensor *t) {
+    int64_t expect = 1;
+    for (int32_t a = t->rank; a-- > 0;) {
+        if (t->shape[a] != 1 && t->strides[a] != expect) return false;
+        expect *= t->shape[a];
+    }
+    return true;
+}
+
+bool same_shape(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b) {
+    if (a->rank != b->rank) return false;
+    for (int32_t i = 0; i < a->rank; ++i)
+        if (a->shape[i] != b->shape[i]) return false;
+    return true;
+}
+
+bool row_view(const chelis_gpu_tensor *t, RowView *v) {
+    if (t->rank == 0) {
+        v->rows = 1;
+        v->n = 1;
+        v->ld = 1;
+        return true;
+    }
+    v->n = t->shape[t->rank - 1];
+    if (v->n > 1 && t->strides[t->rank - 1] != 1) return false;
+    v->rows = 1;
+    for (int32_t a = 0; a < t->rank - 1; ++a) v->rows *= t->shape[a];
+    // Leading axes must collapse to one uniform row stride.
+    int64_t ld = -1, expect = -1;
+    for (int32_t a = t->rank - 1; a-- > 0;) {
+        if (t->shape[a] == 1) continue;
+        if (ld < 0) {
+            ld = t->strides[a];
+            expect = ld * t->shape[a];
+        } else {
+            if (t->strides[a] != expect) return false;
+            expect *= t->shape[a];
+        }
+    }
+    v->ld = ld < 0 ? v->n : ld;
+    return true;
+}
+
+}  // namespace chelis
+
+extern "C" {
+
+const char *chelis_hip_last_error(void) { return chelis::g_error; }
+
+void *chelis_hip_stream(void) { return (void *)chelis::stream(); }
+
+int32_t chelis_hip_synchronize(void) {
+    hipStream_t s = chelis::stream();
+    if (!s) return chelis::set_error(CHELIS_HIP_EHIP, "no HIP device");
+    CHELIS_HIP_TRY(hipStreamSynchronize(s));
+    return CHELIS_HIP_OK;
+}
+
+const char *chelis_hip_build_info(void) {
+#ifdef CHELIS_BUILD_ID
+    return "gfx950 " CHELIS_BUILD_ID;
+#else
+    return "gfx950";
+#endif
+}
+
+}  // extern "C"

@@ -1,0 +1,115 @@
+// Scalar math shared by the gfx950 kernels and by host-side checks.
+//
+// Every function here uses only IEEE-754 binary32/binary64 operations that
+// are correctly rounded on both gfx950 and x86-64 (add, mul, fma, rint,
+// ldexp, conversions), so one source gives the same bits on the device and
+// in a host build. Kernels are compiled with -ffp-contract=off; any fused
+// multiply-add below is an explicit fma().
+#pragma once
+
+#include <stdint.h>
+#include <string.h>
+#include <math.h>
+
+#if defined(__HIPCC__)
+#define CHELIS_HD __host__ __device__
+#define CHELIS_TABLE_QUAL static __device__ __constant__ const
+#include <hip/hip_runtime.h>
+#else
+#define CHELIS_HD
+#define CHELIS_TABLE_QUAL static const
+#endif
+
+#include "exp2_table.h"
+
+namespace chelis {
+
+CHELIS_HD inline uint32_t f32_bits(float v) {
+    uint32_t b;
+    memcpy(&b, &v, 4);
+    return b;
+}
+CHELIS_HD inline float f32_from(uint32_t b) {
+    float v;
+    memcpy(&v, &b, 4);
+    return v;
+}
+CHELIS_HD inline uint64_t f64_bits(double v) {
+    uint64_t b;
+    memcpy(&b, &v, 8);
+    return b;
+}
+CHELIS_HD inline double f64_from(uint64_t b) {
+    double v;
+    memcpy(&v, &b, 8);
+    return v;
+}
+
+// [04-NUM-2]: an arithmetic result that is NaN is stored as the canonical
+// quiet NaN of its dtype, whatever payload the hardware produced.
+CHELIS_HD inline float canon(float v) { return v != v ? f32_from(0x7fc00000u) : v; }
+CHELIS_HD inline double canon(double v) { return v != v ? f64_from(0x7ff8000000000000ull) : v; }
+
+// Round the positive unevaluated sum s + e (|e| <= half an ulp of s) to
+// binary32, nearest-even. (float)s is already the answer unless s lies
+// exactly on a binary32 midpoint, where the sign of e breaks the tie.
+CHELIS_HD inline float round_pos_dd_to_f32(double s, double e) {
+    float f = (float)s;
+    double fd = (double)f;
+    if (fd == s || e == 0.0) return f;
+    uint32_t fb = f32_bits(f);
+    float g;
+    if (fb == 0x7f800000u) {          // overflowed: the neighbour below is FLT_MAX
+        g = f32_from(0x7f7fffffu);
+    } else {
+        g = f32_from(s > fd ? fb + 1u : fb - 1u);
+    }
+    double gd = (double)g;
+    double mid = (fb == 0x7f800000u) ? ldexp(1.0, 128) - ldexp(1.0, 103) : 0.5 * (fd + gd);
+    if (s != mid) return f;
+    double hi = fd > gd ? fd : gd;
+    return (e > 0.0) ? (float)hi : (float)(fd + gd - hi);
+}
+
+// Correctly rounded binary32 exp.
+//
+// x = k ln2/64 + r with k = rint(x * 64/ln2), |r| <= ln2/128; the reduction
+// x - k*HI is exact (HI has 39 significant bits, |k| < 2^14, and Sterbenz
+// applies), the tail -k*LO is carried separately. exp(x) =
+// 2^(k>>6) * T[k&63] * (1 + expm1(r)) with T a double-double table and
+// expm1(r) = r + r^2 P(r), P the degree-5 Taylor tail (truncation below
+// 2^-74 on this interval). The product T*(1 + ...) is accumulated as an
+// unevaluated double-double whose error is about 2^-66 relative, then
+// rounded once to binary32 by round_pos_dd_to_f32. Checked against the
+// CORE-MATH oracle over every binary32 input (tests/test_devmath.py).
+CHELIS_HD inline float expf_cr(float xf) {
+    if (xf != xf) return f32_from(0x7fc00000u);
+    if (xf > 89.0f) return f32_from(0x7f800000u);
+    if (xf < -104.0f) return 0.0f;
+    const double x = (double)xf;
+    const double kd = rint(x * CHELIS_INV_LN2_64);
+    const int k = (int)kd;
+    const double rhi = x - kd * CHELIS_LN2_64_HI;   // exact
+    const double rlo = -kd * CHELIS_LN2_64_LO;
+    const double r = rhi + rlo;
+    double p = fma(r, 1.0 / 5040.0, 1.0 / 720.0);
+    p = fma(r, p, 1.0 / 120.0);
+    p = fma(r, p, 1.0 / 24.0);
+    p = fma(r, p, 1.0 / 6.0);
+    p = fma(r, p, 0.5);
+    p = (r * r) * p;
+    const int j = k & 63;
+    const int m = k >> 6;                             // floor division: k = 64m + j
+    const double th = chelis_exp2_64_tab[j][0];
+    const double tl = chelis_exp2_64_tab[j][1];
+    const double ph = th * rhi;
+    const double pl = fma(th, rhi, -ph);            // th*rhi = ph + pl exactly
+    const double s1 = th + ph;                        // |ph| < |th|: Fast2Sum
+    const double e1 = (th - s1) + ph;
+    const double low = e1 + (pl + (tl + th * (rlo + p)));
+    const double s = s1 + low;
+    const double e = (s1 - s) + low;
+    return round_pos_dd_to_f32(ldexp(s, m), ldexp(e, m));
+}
+
+}  // namespace chelis

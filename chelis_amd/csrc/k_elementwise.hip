@@ -1,0 +1,383 @@
+// Elementwise regions on gfx950: the FusedElem chain interpreter, GELU,
+// ReLU and its adjoint, keyed dropout / replay / uniform_like, and the
+// strided gather used by the device owner.
+//
+// Bandwidth design: contiguous operands move in 16-byte vectors (one
+// float4 / double2 per lane per access, 1 KiB per wave instruction); a
+// broadcast operand (stride 0 on an axis) is re-read through L2/MALL, not
+// materialized. Index math is done once per element in 64-bit only for
+// non-contiguous views; shapes are collapsed on the host first so the common
+// cases are rank 1 (contiguous) and rank 2 (row/column broadcast).
+#include "chain.h"
+
+namespace chelis {
+namespace {
+
+constexpr int kMaxRank = 4;
+
+struct Operand {
+    const void *p;
+    int64_t st[kMaxRank];
+};
+struct Operands {
+    int32_t n;
+    Operand o[CHELIS_FUSED_MAX_INPUTS];
+};
+struct Shape {
+    int32_t rank;
+    int64_t ext[kMaxRank];
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void fused_chain_kernel(ChainDev ch, Operands ops, Shape sh, T *__restrict__ out,
+                                                          int64_t count) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < count; idx += stride) {
+        int64_t coord[kMaxRank];
+        int64_t rem = idx;
+#pragma unroll
+        for (int a = kMaxRank - 1; a >= 0; --a) {
+            if (a < sh.rank) {
+                coord[a] = rem % sh.ext[a];
+                rem /= sh.ext[a];
+            } else {
+                coord[a] = 0;
+            }
+        }
+        T in[CHELIS_FUSED_MAX_INPUTS];
+#pragma unroll
+        for (int k = 0; k < CHELIS_FUSED_MAX_INPUTS; ++k) {
+            if (k < ops.n) {
+                int64_t off = 0;
+#pragma unroll
+                for (int a = 0; a < kMaxRank; ++a) off += coord[a] * ops.o[k].st[a];
+                in[k] = static_cast<const T *>(ops.o[k].p)[off];
+            } else {
+                in[k] = T(0);
+            }
+        }
+        T val[CHELIS_FUSED_MAX_STEPS];
+#pragma unroll
+        for (int s = 0; s < CHELIS_FUSED_MAX_STEPS; ++s) {
+            if (s < ch.n_steps) {
+                const int a0 = ch.a0[s], a1 = ch.a1[s];
+                const T x = a0 >= 0 ? in[a0] : val[-a0 - 1];
+                const T y = a1 >= 0 ? in[a1] : val[-a1 - 1];
+                val[s] = apply_step<T>(ch.op[s], x, y, ch.imm[s]);
+            }
+        }
+        out[idx] = val[ch.n_steps - 1];
+    }
+}
+
+// ---------------------------------------------------------------- unary maps
+// Contiguous n-element maps with 16-byte vectors; the scalar tail is the
+// last n % V elements.
+template <typename T>
+struct Vec16;
+template <> struct Vec16<float> { using type = float4; static constexpr int V = 4; };
+template <> struct Vec16<double> { using type = double2; static constexpr int V = 2; };
+
+enum class Unary : int { Gelu, Relu, ReluAdjoint, Dropout, Uniform };
+
+struct UnaryArgs {
+    uint64_t key;
+    double p0, p1;  // dropout: rate; uniform: low, high
+};
+
+template <typename T, Unary OP>
+__device__ inline T unary_one(T x, T g, int64_t i, const UnaryArgs &u) {
+    if constexpr (OP == Unary::Gelu) {
+        return gelu_one<T>(x);
+    } else if constexpr (OP == Unary::Relu) {
+        return x < T(0) ? T(0) : x;
+    } else if constexpr (OP == Unary::ReluAdjoint) {
+        return T(0) < x ? g : T(0);
+    } else if constexpr (OP == Unary::Dropout) {
+        // [05-OP-37]: the unit at the dtype's width against the rate; a
+        // kept element is x / (1 - rate).
+        const T rate = (T)u.p0;
+        const double unit = random_unit(u.key, (uint64_t)i);
+        const T uw = (T)unit;
+        return uw < rate ? T(0) : canon(x / (T(1) - rate));
+    } else {
+        // [05-OP-8]: one fma(high - low, u, low) at the dtype.
+        const T low = (T)u.p0, high = (T)u.p1;
+        return canon(fma(high - low, (T)random_unit(u.key, (uint64_t)i), low));
+    }
+}
+
+template <typename T, Unary OP>
+__global__ __launch_bounds__(256) void unary_kernel(const T *__restrict__ x, const T *__restrict__ g,
+                                                    T *__restrict__ y, int64_t n, UnaryArgs u) {
+    using V = Vec16<T>;
+    const int64_t nv = n / V::V;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; v < nv; v += stride) {
+        typename V::type xv{}, gv{}, yv;
+        if constexpr (OP != Unary::Uniform) xv = reinterpret_cast<const typename V::type *>(x)[v];
+        if constexpr (OP == Unary::ReluAdjoint) gv = reinterpret_cast<const typename V::type *>(g)[v];
+        const T *xe = reinterpret_cast<const T *>(&xv);
+        const T *ge = reinterpret_cast<const T *>(&gv);
+        T *ye = reinterpret_cast<T *>(&yv);
+#pragma unroll
+        for (int i = 0; i < V::V; ++i) ye[i] = unary_one<T, OP>(xe[i], ge[i], v * V::V + i, u);
+        reinterpret_cast<typename V::type *>(y)[v] = yv;
+    }
+    // tail
+    const int64_t t = nv * V::V + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < n) {
+        const T xe = (OP != Unary::Uniform) ? x[t] : T(0);
+        const T ge = (OP == Unary::ReluAdjoint) ? g[t] : T(0);
+        y[t] = unary_one<T, OP>(xe, ge, t, u);
+    }
+}
+
+// ---------------------------------------------------------------- gather
+template <typename W>
+__global__ __launch_bounds__(256) void gather_kernel(const W *__restrict__ src, W *__restrict__ dst, Shape sh,
+                                                     Operand so, int64_t count) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < count; idx += stride) {
+        int64_t rem = idx, off = 0;
+#pragma unroll
+        for (int a = kMaxRank - 1; a >= 0; --a) {
+            if (a < sh.rank) {
+                off += (rem % sh.ext[a]) * so.st[a];
+                rem /= sh.ext[a];
+            }
+        }
+        dst[idx] = src[off];
+    }
+}
+
+// ---------------------------------------------------------------- host helpers
+// Collapse adjacent output axes wherever every operand's strides allow it
+// (stride[a] == stride[a+1] * ext[a+1]), dropping unit axes.
+bool collapse(const chelis_gpu_tensor *out, const chelis_gpu_tensor *const *ins, int n_in, Shape *sh,
+              int64_t (*st)[kMaxRank]) {
+    int64_t ext[16];
+    int64_t s[CHELIS_FUSED_MAX_INPUTS][16];
+    int r = 0;
+    for (int a = 0; a < out->rank; ++a) {
+        if (out->shape[a] == 1) continue;
+        ext[r] = out->shape[a];
+        // an extent-1 operand axis broadcasts: it never advances
+        for (int k = 0; k < n_in; ++k) s[k][r] = ins[k]->shape[a] == 1 ? 0 : ins[k]->strides[a];
+        ++r;
+    }
+    // merge from the innermost axis outward
+    int64_t mext[16];
+    int64_t ms[CHELIS_FUSED_MAX_INPUTS][16];
+    int m = 0;
+    for (int a = 0; a < r; ++a) {
+        if (m > 0) {
+            bool ok = true;
+            for (int k = 0; k < n_in && ok; ++k) ok = ms[k][m - 1] == s[k][a] * ext[a];
+            if (ok) {
+                mext[m - 1] *= ext[a];
+                for (int k = 0; k < n_in; ++k) ms[k][m - 1] = s[k][a];
+                continue;
+            }
+        }
+        mext[m] = ext[a];
+        for (int k = 0; k < n_in; ++k) ms[k][m] = s[k][a];
+        ++m;
+    }
+    if (m > kMaxRank) return false;
+    sh->rank = m;
+    for (int a = 0; a < m; ++a) sh->ext[a] = mext[a];
+    for (int k = 0; k < n_in; ++k)
+        for (int a = 0; a < kMaxRank; ++a) st[k][a] = a < m ? ms[k][a] : 0;
+    return true;
+}
+
+int32_t check_input_against(const chelis_gpu_tensor *in, const chelis_gpu_tensor *out, const char *name) {
+    if (int32_t s = check_tensor(in, name)) return s;
+    if (in->dtype != out->dtype) return set_error(CHELIS_HIP_EDOMAIN, "%s: dtype differs from the output", name);
+    if (in->rank != out->rank) return set_error(CHELIS_HIP_EDOMAIN, "%s: rank differs from the output", name);
+    for (int32_t a = 0; a < in->rank; ++a)
+        if (in->shape[a] != out->shape[a] && in->shape[a] != 1)
+            return set_error(CHELIS_HIP_EDOMAIN, "%s: axis %d neither matches nor broadcasts", name, a);
+    return CHELIS_HIP_OK;
+}
+
+template <typename T, Unary OP>
+int32_t launch_unary(const chelis_gpu_tensor *x, const chelis_gpu_tensor *g, const chelis_gpu_tensor *y,
+                     const UnaryArgs &u) {
+    hipStream_t st = stream();
+    if (!st) return set_error(CHELIS_HIP_EHIP, "no HIP device");
+    const int64_t n = y->count;
+    if (!n) return CHELIS_HIP_OK;
+    constexpr int V = Vec16<T>::V;
+    const int64_t nv = n / V;
+    int64_t blocks = (nv + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    if (blocks < 1) blocks = 1;
+    unary_kernel<T, OP><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(
+        x ? (const T *)x->data : nullptr, g ? (const T *)g->data : nullptr, (T *)y->data, n, u);
+    CHELIS_LAUNCH_CHECK();
+    return CHELIS_HIP_OK;
+}
+
+bool vec_aligned(const chelis_gpu_tensor *t) { return (reinterpret_cast<uintptr_t>(t->data) & 15u) == 0; }
+
+template <Unary OP>
+int32_t unary_entry(const char *what, const chelis_gpu_tensor *x, const chelis_gpu_tensor *g,
+                    const chelis_gpu_tensor *y, const UnaryArgs &u) {
+    int32_t s;
+    if ((s = check_tensor(y, "y"))) return s;
+    if (!is_float(y->dtype)) return set_error(CHELIS_HIP_EDOMAIN, "%s: dtype must be f32 or f64", what);
+    for (const chelis_gpu_tensor *t : {x, g}) {
+        if (!t) continue;
+        if ((s = check_tensor(t, "operand"))) return s;
+        if (t->dtype != y->dtype || !same_shape(t, y))
+            return set_error(CHELIS_HIP_EDOMAIN, "%s: operand shape/dtype must equal the result's", what);
+    }
+    for (const chelis_gpu_tensor *t : {x, g, y})
+        if (t && (!is_contiguous(t) || (t->count && !vec_aligned(t))))
+            return set_error(CHELIS_HIP_EUNSUPPORTED, "%s: operands must be contiguous and 16-byte aligned", what);
+    return y->dtype == CHELIS_DTYPE_F32 ? launch_unary<float, OP>(x, g, y, u) : launch_unary<double, OP>(x, g, y, u);
+}
+
+int32_t check_rate(double rate, chelis_dtype dt) {
+    // The C lane checks the dtype-rounded rate widened to f64 (emit.rs:6166).
+    const double r = dt == CHELIS_DTYPE_F32 ? (double)(float)rate : rate;
+    if (!(r >= 0.0 && r < 1.0))
+        return set_error(CHELIS_HIP_EDOMAIN, "numeric trap: domain in dropout at %s",
+                         dt == CHELIS_DTYPE_F32 ? "f32" : "f64");
+    return CHELIS_HIP_OK;
+}
+
+}  // namespace
+
+// Used by the device owner: dst (contiguous) = src viewed with `shape`/`strides`.
+int32_t gather_contiguous(const void *src, void *dst, int32_t rank, const int64_t *shape, const int64_t *strides,
+                          int64_t width, int64_t count, hipStream_t st) {
+    if (!count) return CHELIS_HIP_OK;
+    chelis_gpu_tensor out{}, in{};
+    int64_t cst[8];
+    int64_t acc = 1;
+    for (int32_t a = rank; a-- > 0;) {
+        cst[a] = acc;
+        acc *= shape[a];
+    }
+    out.rank = in.rank = rank;
+    out.shape = in.shape = shape;
+    out.strides = cst;
+    in.strides = strides;
+    const chelis_gpu_tensor *ins[1] = {&in};
+    Shape sh;
+    int64_t st1[1][kMaxRank];
+    if (!collapse(&out, ins, 1, &sh, st1)) return set_error(CHELIS_HIP_EUNSUPPORTED, "gather: view rank > 4 after collapse");
+    Operand so{src, {st1[0][0], st1[0][1], st1[0][2], st1[0][3]}};
+    int64_t blocks = (count + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    switch (width) {
+        case 1: gather_kernel<uint8_t><<<(unsigned)blocks, 256, 0, st>>>((const uint8_t *)src, (uint8_t *)dst, sh, so, count); break;
+        case 2: gather_kernel<uint16_t><<<(unsigned)blocks, 256, 0, st>>>((const uint16_t *)src, (uint16_t *)dst, sh, so, count); break;
+        case 4: gather_kernel<uint32_t><<<(unsigned)blocks, 256, 0, st>>>((const uint32_t *)src, (uint32_t *)dst, sh, so, count); break;
+        case 8: gather_kernel<uint64_t><<<(unsigned)blocks, 256, 0, st>>>((const uint64_t *)src, (uint64_t *)dst, sh, so, count); break;
+        default: return set_error(CHELIS_HIP_EDOMAIN, "gather: width %lld", (long long)width);
+    }
+    CHELIS_LAUNCH_CHECK();
+    return CHELIS_HIP_OK;
+}
+
+}  // namespace chelis
+
+using namespace chelis;
+
+extern "C" int32_t chelis_hip_fused_elementwise(const chelis_fused_chain *chain, const chelis_gpu_tensor *const *inputs,
+                                                int32_t n_inputs, const chelis_gpu_tensor *out) {
+    int32_t s;
+    if (!chain) return set_error(CHELIS_HIP_EDOMAIN, "fused_elementwise: null chain");
+    if ((s = check_tensor(out, "out"))) return s;
+    if (!is_float(out->dtype)) return set_error(CHELIS_HIP_EUNSUPPORTED, "fused_elementwise: f32/f64 chains only");
+    if (!is_contiguous(out)) return set_error(CHELIS_HIP_EUNSUPPORTED, "fused_elementwise: output must be contiguous");
+    if (n_inputs < 0 || n_inputs > CHELIS_FUSED_MAX_INPUTS || (n_inputs && !inputs))
+        return set_error(CHELIS_HIP_EDOMAIN, "fused_elementwise: %d inputs (max %d)", n_inputs, CHELIS_FUSED_MAX_INPUTS);
+    if (chain->n_steps < 1 || chain->n_steps > CHELIS_FUSED_MAX_STEPS)
+        return set_error(CHELIS_HIP_EDOMAIN, "fused_elementwise: %d steps (1..%d)", chain->n_steps, CHELIS_FUSED_MAX_STEPS);
+    ChainDev ch{};
+    ch.n_steps = chain->n_steps;
+    for (int32_t i = 0; i < chain->n_steps; ++i) {
+        const chelis_fused_step &st = chain->steps[i];
+        if (st.op >= CHELIS_FUSED_COUNT_) return set_error(CHELIS_HIP_EDOMAIN, "fused_elementwise: step %d op %d", i, st.op);
+        for (int j = 0; j < 2; ++j) {
+            const int32_t a = st.args[j];
+            if ((a >= 0 && a >= n_inputs) || (a < 0 && -a - 1 >= i))
+                return set_error(CHELIS_HIP_EDOMAIN, "fused_elementwise: step %d arg %d out of range", i, j);
+        }
+        ch.op[i] = st.op;
+        ch.a0[i] = (int8_t)st.args[0];
+        ch.a1[i] = (int8_t)st.args[1];
+        ch.imm[i] = st.imm;
+    }
+    for (int32_t k = 0; k < n_inputs; ++k)
+        if ((s = check_input_against(inputs[k], out, "input"))) return s;
+    if (!out->count) return CHELIS_HIP_OK;
+    Shape sh;
+    int64_t st[CHELIS_FUSED_MAX_INPUTS][kMaxRank];
+    if (!collapse(out, inputs, n_inputs, &sh, st))
+        return set_error(CHELIS_HIP_EUNSUPPORTED, "fused_elementwise: more than %d independent axes", kMaxRank);
+    Operands ops{};
+    ops.n = n_inputs;
+    for (int32_t k = 0; k < n_inputs; ++k) {
+        ops.o[k].p = inputs[k]->data;
+        for (int a = 0; a < kMaxRank; ++a) ops.o[k].st[a] = st[k][a];
+    }
+    if (sh.rank == 0) {
+        sh.rank = 1;
+        sh.ext[0] = 1;
+    }
+    hipStream_t strm = stream();
+    if (!strm) return set_error(CHELIS_HIP_EHIP, "no HIP device");
+    int64_t blocks = (out->count + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    if (out->dtype == CHELIS_DTYPE_F32)
+        fused_chain_kernel<float><<<(unsigned)blocks, 256, 0, strm>>>(ch, ops, sh, (float *)out->data, out->count);
+    else
+        fused_chain_kernel<double><<<(unsigned)blocks, 256, 0, strm>>>(ch, ops, sh, (double *)out->data, out->count);
+    CHELIS_LAUNCH_CHECK();
+    return CHELIS_HIP_OK;
+}
+
+extern "C" int32_t chelis_hip_gelu(const chelis_gpu_tensor *x, const chelis_gpu_tensor *y) {
+    return unary_entry<Unary::Gelu>("gelu", x, nullptr, y, UnaryArgs{});
+}
+
+extern "C" int32_t chelis_hip_relu(const chelis_gpu_tensor *x, const chelis_gpu_tensor *y) {
+    return unary_entry<Unary::Relu>("relu", x, nullptr, y, UnaryArgs{});
+}
+
+extern "C" int32_t chelis_hip_relu_adjoint(const chelis_gpu_tensor *x, const chelis_gpu_tensor *g,
+                                           const chelis_gpu_tensor *dx) {
+    return unary_entry<Unary::ReluAdjoint>("relu_adjoint", x, g, dx, UnaryArgs{});
+}
+
+extern "C" int32_t chelis_hip_dropout(uint64_t key, const chelis_gpu_tensor *x, double rate,
+                                      const chelis_gpu_tensor *y) {
+    if (!y || !is_float(y->dtype)) return set_error(CHELIS_HIP_EDOMAIN, "dropout: f32 or f64 result required");
+    if (int32_t s = check_rate(rate, y->dtype)) return s;
+    return unary_entry<Unary::Dropout>("dropout", x, nullptr, y, UnaryArgs{key, rate, 0.0});
+}
+
+extern "C" int32_t chelis_hip_dropout_replay(uint64_t key, const chelis_gpu_tensor *g, double rate,
+                                             const chelis_gpu_tensor *dx) {
+    // [05-OP-37] adjoint: the forward mask on the cotangent, kept values
+    // divided by (1 - rate); the same kernel with g in place of x.
+    if (!dx || !is_float(dx->dtype)) return set_error(CHELIS_HIP_EDOMAIN, "dropout_replay: f32 or f64 result required");
+    if (int32_t s = check_rate(rate, dx->dtype)) return s;
+    return unary_entry<Unary::Dropout>("dropout_replay", g, nullptr, dx, UnaryArgs{key, rate, 0.0});
+}
+
+extern "C" int32_t chelis_hip_uniform_like(uint64_t key, double low, double high, const chelis_gpu_tensor *out) {
+    if (!out || !is_float(out->dtype)) return set_error(CHELIS_HIP_EDOMAIN, "uniform_like: f32 or f64 result required");
+    const bool f32 = out->dtype == CHELIS_DTYPE_F32;
+    const double lo = f32 ? (double)(float)low : low, hi = f32 ? (double)(float)high : high;
+    const double span = f32 ? (double)((float)hi - (float)lo) : hi - lo;
+    if (!(std::isfinite(lo) && std::isfinite(hi) && lo <= hi && std::isfinite(span)))
+        return set_error(CHELIS_HIP_EDOMAIN, "numeric trap: domain in uniform_like at %s", f32 ? "f32" : "f64");
+    return unary_entry<Unary::Uniform>("uniform_like", nullptr, nullptr, out, UnaryArgs{key, low, high});
+}

@@ -1,0 +1,486 @@
+// Reductions over one axis on gfx950: sum, prod (canonical tree), max, min
+// ([05-OP-12/13]), argmax, argmin ([05-OP-15/16]), each with an optional
+// inlined FusedElem chain as the leaf (the reference's reduce_fused), plus
+// the Bool8 count ([05-OP-29]).
+//
+// The reduced tensor is viewed as [outer, n, inner]. The canonical tree
+// over n leaves equals a full binary tree over the leaves padded to a power
+// of two with the operation's exact identity (-0 for +, 1 for *, -inf/+inf
+// for max/min, never selected), so it can be evaluated hierarchically:
+// each pass reduces aligned groups of G = 2^g consecutive leaves to one
+// partial, and the next pass treats the partials as leaves, until one
+// value per output remains. Every group is an aligned subtree, so the
+// composition is the canonical tree bit for bit.
+//
+// Pass kernels:
+//  * rows  (inner == 1): one wave per group of G = 64*S leaves; lane l
+//    holds leaf s*64 + l of each segment s (coalesced loads), the wave64
+//    butterfly builds each segment's 64-leaf subtree, then a tree over the
+//    S segments.
+//  * cols  (inner > 1): one thread per (group, column), adjacent threads on
+//    adjacent columns (coalesced); the thread loads its G = 32 leaves and
+//    reduces them with an unrolled in-register tree.
+// max/min/argmax combine in index order (lower lane / earlier leaf on the
+// left), so first-NaN and first-index tie rules hold.
+#include "chain.h"
+
+namespace chelis {
+namespace {
+
+enum class Rk : int { Sum, Prod, Max, Min, ArgMax, ArgMin };
+
+template <typename T, Rk K>
+__device__ inline T identity() {
+    if constexpr (K == Rk::Sum) return T(-0.0);
+    if constexpr (K == Rk::Prod) return T(1);
+    if constexpr (K == Rk::Max || K == Rk::ArgMax) return -__builtin_huge_val();
+    return __builtin_huge_val();
+}
+
+// combine(left, right) with left covering the earlier leaves.
+template <typename T, Rk K>
+__device__ inline void combine(T &a, int64_t &ia, T b, int64_t ib) {
+    if constexpr (K == Rk::Sum) {
+        a = a + b;
+    } else if constexpr (K == Rk::Prod) {
+        a = a * b;
+    } else {
+        if (a != a) return;
+        if (b != b) {
+            a = b;
+            ia = ib;
+            return;
+        }
+        const bool take = (K == Rk::Max || K == Rk::ArgMax) ? (b > a) : (b < a);
+        if (take) {
+            a = b;
+            ia = ib;
+        }
+    }
+}
+
+constexpr bool has_index(Rk k) { return k == Rk::ArgMax || k == Rk::ArgMin; }
+
+// Leaf source: either the chain over the inputs or one plain input.
+struct LeafSrc {
+    int32_t n_in;
+    const void *p[CHELIS_FUSED_MAX_INPUTS];
+    int64_t so[CHELIS_FUSED_MAX_INPUTS], sn[CHELIS_FUSED_MAX_INPUTS], si[CHELIS_FUSED_MAX_INPUTS];
+    const int64_t *idx;  // partial indices of a previous pass (argmax/argmin), or null
+};
+
+template <typename T, bool CHAIN>
+__device__ inline T leaf(const ChainDev &ch, const LeafSrc &src, int64_t o, int64_t i, int64_t j) {
+    if constexpr (!CHAIN) {
+        return static_cast<const T *>(src.p[0])[o * src.so[0] + i * src.sn[0] + j * src.si[0]];
+    } else {
+        T in[CHELIS_FUSED_MAX_INPUTS];
+#pragma unroll
+        for (int k = 0; k < CHELIS_FUSED_MAX_INPUTS; ++k)
+            in[k] = k < src.n_in ? static_cast<const T *>(src.p[k])[o * src.so[k] + i * src.sn[k] + j * src.si[k]]
+                                 : T(0);
+        T val[CHELIS_FUSED_MAX_STEPS];
+#pragma unroll
+        for (int s = 0; s < CHELIS_FUSED_MAX_STEPS; ++s) {
+            if (s < ch.n_steps) {
+                const int a0 = ch.a0[s], a1 = ch.a1[s];
+                const T x = a0 >= 0 ? in[a0] : val[-a0 - 1];
+                const T y = a1 >= 0 ? in[a1] : val[-a1 - 1];
+                val[s] = apply_step<T>(ch.op[s], x, y, ch.imm[s]);
+            }
+        }
+        return val[ch.n_steps - 1];
+    }
+}
+
+template <typename T, Rk K>
+__device__ inline T finalize(T v) {
+    if constexpr (K == Rk::Sum || K == Rk::Prod) return canon(v);
+    return v;
+}
+
+// out layout of a pass: [outer, groups, inner] values (+ i64 indices).
+template <typename T, Rk K, int S, bool CHAIN>
+__global__ __launch_bounds__(256) void reduce_rows_kernel(ChainDev ch, LeafSrc src, int64_t outer, int64_t n,
+                                                          int64_t groups, T *__restrict__ out_v,
+                                                          int64_t *__restrict__ out_i, bool last) {
+    constexpr int G = 64 * S;
+    const int lane = threadIdx.x & 63;
+    const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (item >= outer * groups) return;
+    const int64_t o = item / groups, g = item % groups;
+    T seg[S];
+    int64_t sidx[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const int64_t i = g * G + (int64_t)s * 64 + lane;
+        T v = identity<T, K>();
+        int64_t vi = i;
+        if (i < n) {
+            v = leaf<T, CHAIN>(ch, src, o, i, 0);
+            if (has_index(K) && src.idx) vi = src.idx[o * n + i];
+        }
+#pragma unroll
+        for (int m = 1; m < 64; m <<= 1) {
+            T ov = shfl_xor(v, m);
+            int64_t oi = has_index(K) ? shfl_xor(vi, m) : 0;
+            if constexpr (K == Rk::Sum || K == Rk::Prod) {
+                combine<T, K>(v, vi, ov, oi);  // commutative: both lanes agree
+            } else if (lane & m) {
+                T a = ov;
+                int64_t ia = oi;
+                combine<T, K>(a, ia, v, vi);
+                v = a;
+                vi = ia;
+            } else {
+                combine<T, K>(v, vi, ov, oi);
+            }
+        }
+        seg[s] = v;
+        sidx[s] = vi;
+    }
+#pragma unroll
+    for (int w = S; w > 1; w >>= 1)
+#pragma unroll
+        for (int t = 0; t < w / 2; ++t) {
+            T a = seg[2 * t];
+            int64_t ia = sidx[2 * t];
+            combine<T, K>(a, ia, seg[2 * t + 1], sidx[2 * t + 1]);
+            seg[t] = a;
+            sidx[t] = ia;
+        }
+    if (lane == 0) {
+        out_v[item] = last ? finalize<T, K>(seg[0]) : seg[0];
+        if (has_index(K)) out_i[item] = sidx[0];
+    }
+}
+
+template <typename T, Rk K, bool CHAIN>
+__global__ __launch_bounds__(256) void reduce_cols_kernel(ChainDev ch, LeafSrc src, int64_t outer, int64_t n,
+                                                          int64_t inner, int64_t groups, T *__restrict__ out_v,
+                                                          int64_t *__restrict__ out_i, bool last) {
+    constexpr int G = 32;
+    const int64_t total = outer * groups * inner;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += stride) {
+        const int64_t j = t % inner;
+        const int64_t og = t / inner;
+        const int64_t g = og % groups, o = og / groups;
+        T v[G];
+        int64_t vi[G];
+#pragma unroll
+        for (int q = 0; q < G; ++q) {
+            const int64_t i = g * G + q;
+            v[q] = identity<T, K>();
+            vi[q] = i;
+            if (i < n) {
+                v[q] = leaf<T, CHAIN>(ch, src, o, i, j);
+                if (has_index(K) && src.idx) vi[q] = src.idx[(o * n + i) * inner + j];
+            }
+        }
+#pragma unroll
+        for (int w = G; w > 1; w >>= 1)
+#pragma unroll
+            for (int q = 0; q < w / 2; ++q) {
+                T a = v[2 * q];
+                int64_t ia = vi[2 * q];
+                combine<T, K>(a, ia, v[2 * q + 1], vi[2 * q + 1]);
+                v[q] = a;
+                vi[q] = ia;
+            }
+        out_v[t] = last ? finalize<T, K>(v[0]) : v[0];
+        if (has_index(K)) out_i[t] = vi[0];
+    }
+}
+
+template <typename T>
+__global__ void fill_kernel(T *p, int64_t n, T v) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+// count: Bool8 leaves, exact i64 sums (any order gives the same integer),
+// a byte other than 0/1 raises the reference kernel's error code 1.
+__global__ __launch_bounds__(256) void count_kernel(const uint8_t *__restrict__ x, int64_t outer, int64_t n,
+                                                    int64_t inner, int64_t so, int64_t sn, int64_t si,
+                                                    int64_t *__restrict__ out, int32_t *__restrict__ err) {
+    const int64_t total = outer * inner;
+    const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (t >= total) return;
+    const int64_t o = t / inner, j = t % inner;
+    int64_t c = 0;
+    bool bad = false;
+    for (int64_t i = lane; i < n; i += 64) {
+        const uint8_t b = x[o * so + i * sn + j * si];
+        bad |= b > 1;
+        c += b & 1;
+    }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) c += shfl_xor(c, m);
+    if (bad) atomicOr(err, 1);
+    if (lane == 0) out[t] = c;
+}
+
+// ---------------------------------------------------------------- host
+// Collapse the axes before `axis` into one stride and after it into one.
+bool split3(const chelis_gpu_tensor *t, int32_t axis, int64_t *so, int64_t *sn, int64_t *si) {
+    auto fold = [&](int32_t lo, int32_t hi, int64_t *st) {
+        int64_t expect = -1;
+        *st = 0;
+        for (int32_t a = hi - 1; a >= lo; --a) {
+            if (t->shape[a] == 1) continue;
+            if (expect < 0) {
+                *st = t->strides[a];
+                expect = t->strides[a] * t->shape[a];
+            } else {
+                if (t->strides[a] != expect) return false;
+                expect *= t->shape[a];
+            }
+        }
+        return true;
+    };
+    *sn = t->shape[axis] == 1 ? 0 : t->strides[axis];
+    return fold(0, axis, so) && fold(axis + 1, t->rank, si);
+}
+
+struct Scratch {
+    void *p = nullptr;
+    hipStream_t st;
+    explicit Scratch(hipStream_t s) : st(s) {}
+    ~Scratch() {
+        if (p) (void)hipFreeAsync(p, st);
+    }
+};
+
+template <typename T, Rk K>
+int32_t run_reduce(const ChainDev &ch, bool chain, LeafSrc src, int64_t outer, int64_t n, int64_t inner,
+                   void *out, hipStream_t st) {
+    // Pass loop: partials alternate between two scratch buffers.
+    Scratch sa(st), sb(st), ia(st), ib(st);
+    const bool rows = inner == 1;
+    int64_t cur_n = n;
+    bool first = true;
+    T *prev_v = nullptr;
+    int64_t *prev_i = nullptr;
+    int flip = 0;
+    while (true) {
+        int S = 1;
+        if (rows) {
+            while (64 * S < cur_n && S < 16) S <<= 1;
+        }
+        const int64_t G = rows ? 64 * S : 32;
+        const int64_t groups = (cur_n + G - 1) / G;
+        const bool last = groups == 1;
+        T *dst_v;
+        int64_t *dst_i = nullptr;
+        const int64_t cells = outer * groups * inner;
+        if (last) {
+            dst_v = has_index(K) ? nullptr : static_cast<T *>(out);
+            dst_i = has_index(K) ? static_cast<int64_t *>(out) : nullptr;
+        } else {
+            dst_v = nullptr;
+        }
+        Scratch &bv = flip ? sb : sa;
+        Scratch &bi = flip ? ib : ia;
+        if (!dst_v) {
+            if (bv.p) CHELIS_HIP_TRY(hipFreeAsync(bv.p, st));
+            bv.p = nullptr;
+            CHELIS_HIP_TRY(hipMallocAsync(&bv.p, (size_t)cells * sizeof(T), st));
+            dst_v = static_cast<T *>(bv.p);
+        }
+        if (has_index(K) && !dst_i) {
+            if (bi.p) CHELIS_HIP_TRY(hipFreeAsync(bi.p, st));
+            bi.p = nullptr;
+            CHELIS_HIP_TRY(hipMallocAsync(&bi.p, (size_t)cells * sizeof(int64_t), st));
+            dst_i = static_cast<int64_t *>(bi.p);
+        }
+        LeafSrc s = src;
+        if (!first) {
+            s.n_in = 1;
+            s.p[0] = prev_v;
+            s.so[0] = cur_n * inner;
+            s.sn[0] = inner;
+            s.si[0] = 1;
+            s.idx = prev_i;
+        }
+        const bool use_chain = first && chain;
+        if (rows) {
+            const unsigned grid = grid_for(outer * groups, 4);
+#define CHELIS_ROWS_CASE(SS)                                                                                  \
+    case SS:                                                                                                  \
+        if (use_chain)                                                                                        \
+            reduce_rows_kernel<T, K, SS, true><<<grid, 256, 0, st>>>(ch, s, outer, cur_n, groups, dst_v, dst_i, last); \
+        else                                                                                                  \
+            reduce_rows_kernel<T, K, SS, false><<<grid, 256, 0, st>>>(ch, s, outer, cur_n, groups, dst_v, dst_i, last); \
+        break;
+            switch (S) {
+                CHELIS_ROWS_CASE(1)
+                CHELIS_ROWS_CASE(2)
+                CHELIS_ROWS_CASE(4)
+                CHELIS_ROWS_CASE(8)
+                CHELIS_ROWS_CASE(16)
+                default: return set_error(CHELIS_HIP_EDOMAIN, "reduce: internal segment count %d", S);
+            }
+#undef CHELIS_ROWS_CASE
+        } else {
+            int64_t blocks = (cells + 255) / 256;
+            if (blocks > 16384) blocks = 16384;
+            if (use_chain)
+                reduce_cols_kernel<T, K, true><<<(unsigned)blocks, 256, 0, st>>>(ch, s, outer, cur_n, inner, groups,
+                                                                                 dst_v, dst_i, last);
+            else
+                reduce_cols_kernel<T, K, false><<<(unsigned)blocks, 256, 0, st>>>(ch, s, outer, cur_n, inner, groups,
+                                                                                  dst_v, dst_i, last);
+        }
+        CHELIS_LAUNCH_CHECK();
+        if (last) break;
+        prev_v = dst_v;
+        prev_i = dst_i;
+        cur_n = groups;
+        first = false;
+        flip ^= 1;
+    }
+    return CHELIS_HIP_OK;
+}
+
+template <typename T>
+int32_t dispatch_kind(int32_t op, const ChainDev &ch, bool chain, const LeafSrc &src, int64_t outer, int64_t n,
+                      int64_t inner, void *out, hipStream_t st) {
+    switch (op) {
+        case CHELIS_REDUCE_SUM: return run_reduce<T, Rk::Sum>(ch, chain, src, outer, n, inner, out, st);
+        case CHELIS_REDUCE_PROD: return run_reduce<T, Rk::Prod>(ch, chain, src, outer, n, inner, out, st);
+        case CHELIS_REDUCE_MAX: return run_reduce<T, Rk::Max>(ch, chain, src, outer, n, inner, out, st);
+        case CHELIS_REDUCE_MIN: return run_reduce<T, Rk::Min>(ch, chain, src, outer, n, inner, out, st);
+        case CHELIS_REDUCE_ARGMAX: return run_reduce<T, Rk::ArgMax>(ch, chain, src, outer, n, inner, out, st);
+        case CHELIS_REDUCE_ARGMIN: return run_reduce<T, Rk::ArgMin>(ch, chain, src, outer, n, inner, out, st);
+        default: return set_error(CHELIS_HIP_EDOMAIN, "reduce: unknown op %d", op);
+    }
+}
+
+int32_t load_chain(const chelis_fused_chain *chain, int32_t n_inputs, ChainDev *ch) {
+    *ch = ChainDev{};
+    if (!chain) return CHELIS_HIP_OK;
+    if (chain->n_steps < 1 || chain->n_steps > CHELIS_FUSED_MAX_STEPS)
+        return set_error(CHELIS_HIP_EDOMAIN, "chain: %d steps (1..%d)", chain->n_steps, CHELIS_FUSED_MAX_STEPS);
+    ch->n_steps = chain->n_steps;
+    for (int32_t i = 0; i < chain->n_steps; ++i) {
+        const chelis_fused_step &st = chain->steps[i];
+        if (st.op >= CHELIS_FUSED_COUNT_) return set_error(CHELIS_HIP_EDOMAIN, "chain: step %d op %d", i, st.op);
+        for (int j = 0; j < 2; ++j) {
+            const int32_t a = st.args[j];
+            if ((a >= 0 && a >= n_inputs) || (a < 0 && -a - 1 >= i))
+                return set_error(CHELIS_HIP_EDOMAIN, "chain: step %d arg %d out of range", i, j);
+        }
+        ch->op[i] = st.op;
+        ch->a0[i] = (int8_t)st.args[0];
+        ch->a1[i] = (int8_t)st.args[1];
+        ch->imm[i] = st.imm;
+    }
+    return CHELIS_HIP_OK;
+}
+
+}  // namespace
+}  // namespace chelis
+
+using namespace chelis;
+
+extern "C" int32_t chelis_hip_reduce(int32_t op, const chelis_fused_chain *chain,
+                                     const chelis_gpu_tensor *const *inputs, int32_t n_inputs, int32_t axis,
+                                     const chelis_gpu_tensor *out) {
+    int32_t s;
+    if (op == CHELIS_REDUCE_COUNT) return set_error(CHELIS_HIP_EDOMAIN, "reduce: use chelis_hip_count for counts");
+    if (n_inputs < 1 || n_inputs > CHELIS_FUSED_MAX_INPUTS || !inputs)
+        return set_error(CHELIS_HIP_EDOMAIN, "reduce: %d inputs", n_inputs);
+    if (!chain && n_inputs != 1) return set_error(CHELIS_HIP_EDOMAIN, "reduce: a plain reduction takes one input");
+    if ((s = check_tensor(out, "out"))) return s;
+    const chelis_gpu_tensor *x0 = inputs[0];
+    for (int32_t k = 0; k < n_inputs; ++k) {
+        if ((s = check_tensor(inputs[k], "input"))) return s;
+        if (!is_float(inputs[k]->dtype) || inputs[k]->dtype != x0->dtype || !same_shape(inputs[k], x0))
+            return set_error(CHELIS_HIP_EDOMAIN, "reduce: inputs must share one f32/f64 dtype and shape");
+    }
+    const int32_t rank = x0->rank;
+    if (axis < 0) axis += rank;
+    if (axis < 0 || axis >= rank) return set_error(CHELIS_HIP_EDOMAIN, "reduce: axis out of range");
+    const bool idx_out = op == CHELIS_REDUCE_ARGMAX || op == CHELIS_REDUCE_ARGMIN;
+    if (out->dtype != (idx_out ? CHELIS_DTYPE_I64 : x0->dtype))
+        return set_error(CHELIS_HIP_EDOMAIN, "reduce: result dtype must be %s", idx_out ? "i64" : "the input's");
+    if (out->rank != rank - 1 || !is_contiguous(out))
+        return set_error(CHELIS_HIP_EDOMAIN, "reduce: result must be contiguous with the axis removed");
+    for (int32_t a = 0, b = 0; a < rank; ++a) {
+        if (a == axis) continue;
+        if (out->shape[b++] != x0->shape[a]) return set_error(CHELIS_HIP_EDOMAIN, "reduce: result shape mismatch");
+    }
+    ChainDev ch;
+    if ((s = load_chain(chain, n_inputs, &ch))) return s;
+    int64_t outer = 1, inner = 1;
+    const int64_t n = x0->shape[axis];
+    for (int32_t a = 0; a < axis; ++a) outer *= x0->shape[a];
+    for (int32_t a = axis + 1; a < rank; ++a) inner *= x0->shape[a];
+    hipStream_t st = stream();
+    if (!st) return set_error(CHELIS_HIP_EHIP, "no HIP device");
+    if (outer * inner == 0) return CHELIS_HIP_OK;
+    if (n == 0) {
+        if (op != CHELIS_REDUCE_SUM && op != CHELIS_REDUCE_PROD)
+            return set_error(CHELIS_HIP_EDOMAIN, "numeric trap: domain in %s at %s",
+                             op == CHELIS_REDUCE_MAX ? "max_reduce" : op == CHELIS_REDUCE_MIN ? "min_reduce"
+                             : op == CHELIS_REDUCE_ARGMAX ? "argmax_reduce" : "argmin_reduce",
+                             idx_out ? "i64" : (x0->dtype == CHELIS_DTYPE_F32 ? "f32" : "f64"));
+        const unsigned grid = grid_for(out->count, 256);
+        if (x0->dtype == CHELIS_DTYPE_F32)
+            fill_kernel<float><<<grid, 256, 0, st>>>((float *)out->data, out->count, op == CHELIS_REDUCE_SUM ? 0.0f : 1.0f);
+        else
+            fill_kernel<double><<<grid, 256, 0, st>>>((double *)out->data, out->count, op == CHELIS_REDUCE_SUM ? 0.0 : 1.0);
+        CHELIS_LAUNCH_CHECK();
+        return CHELIS_HIP_OK;
+    }
+    LeafSrc src{};
+    src.n_in = n_inputs;
+    for (int32_t k = 0; k < n_inputs; ++k) {
+        src.p[k] = inputs[k]->data;
+        if (!split3(inputs[k], axis, &src.so[k], &src.sn[k], &src.si[k]))
+            return set_error(CHELIS_HIP_EUNSUPPORTED, "reduce: input %d axes do not collapse to [outer, n, inner]", k);
+    }
+    return x0->dtype == CHELIS_DTYPE_F32
+               ? dispatch_kind<float>(op, ch, chain != nullptr, src, outer, n, inner, out->data, st)
+               : dispatch_kind<double>(op, ch, chain != nullptr, src, outer, n, inner, out->data, st);
+}
+
+extern "C" int32_t chelis_hip_count(const chelis_gpu_tensor *x, int32_t axis, const chelis_gpu_tensor *out,
+                                    int32_t *error_code) {
+    int32_t s;
+    if ((s = check_tensor(x, "x")) || (s = check_tensor(out, "out"))) return s;
+    if (x->dtype != CHELIS_DTYPE_BOOL || out->dtype != CHELIS_DTYPE_I64)
+        return set_error(CHELIS_HIP_EDOMAIN, "count: bool input and i64 result required");
+    if (axis < 0) axis += x->rank;
+    if (axis < 0 || axis >= x->rank) return set_error(CHELIS_HIP_EDOMAIN, "count: axis out of range");
+    if (out->rank != x->rank - 1 || !is_contiguous(out))
+        return set_error(CHELIS_HIP_EDOMAIN, "count: result must be contiguous with the axis removed");
+    for (int32_t a = 0, b = 0; a < x->rank; ++a) {
+        if (a == axis) continue;
+        if (out->shape[b++] != x->shape[a]) return set_error(CHELIS_HIP_EDOMAIN, "count: result shape mismatch");
+    }
+    int64_t so, sn, si;
+    if (!split3(x, axis, &so, &sn, &si))
+        return set_error(CHELIS_HIP_EUNSUPPORTED, "count: axes do not collapse to [outer, n, inner]");
+    int64_t outer = 1, inner = 1;
+    for (int32_t a = 0; a < axis; ++a) outer *= x->shape[a];
+    for (int32_t a = axis + 1; a < x->rank; ++a) inner *= x->shape[a];
+    hipStream_t st = stream();
+    if (!st) return set_error(CHELIS_HIP_EHIP, "no HIP device");
+    if (error_code) *error_code = 0;
+    if (outer * inner == 0) return CHELIS_HIP_OK;
+    int32_t *err = nullptr;
+    CHELIS_HIP_TRY(hipMallocAsync((void **)&err, sizeof(int32_t), st));
+    CHELIS_HIP_TRY(hipMemsetAsync(err, 0, sizeof(int32_t), st));
+    count_kernel<<<grid_for(outer * inner, 4), 256, 0, st>>>((const uint8_t *)x->data, outer, x->shape[axis], inner,
+                                                             so, sn, si, (int64_t *)out->data, err);
+    CHELIS_LAUNCH_CHECK();
+    int32_t host_err = 0;
+    CHELIS_HIP_TRY(hipMemcpyAsync(&host_err, err, sizeof(int32_t), hipMemcpyDeviceToHost, st));
+    CHELIS_HIP_TRY(hipFreeAsync(err, st));
+    CHELIS_HIP_TRY(hipStreamSynchronize(st));
+    if (error_code) *error_code = host_err;
+    return CHELIS_HIP_OK;
+}

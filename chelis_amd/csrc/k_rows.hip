@@ -1,0 +1,445 @@
+// Row regions on gfx950: softmax, causal scaled softmax, softmax adjoint and
+// layer norm over the last axis, each as ONE kernel that reads its row once
+// from HBM into registers and writes its result once.
+//
+// Layout of a row in registers. A row of n elements is treated as the
+// power-of-two capacity CAP = S * 64W * V >= n, padded past n. The row is
+// cut into S segments of 64W*V elements; in segment s, thread t holds the
+// V consecutive elements starting at s*64W*V + t*V, loaded with one 16-byte
+// vector load, so each load instruction of a wave covers one contiguous
+// 1 KiB span (fully coalesced).
+//
+// Canonical sum tree ([05-OP-30]). Every (segment, thread) block is an
+// aligned power-of-two run of leaves, so the adjacent-pair tree over the
+// padded row is: an in-register tree over the V leaves, then a wave64
+// butterfly (xor 1,2,...,32: step m joins the aligned blocks of 2^m
+// threads), then a tree over the W waves through LDS, then a tree over the
+// S segments. Padding leaves are -0.0, the exact additive identity
+// (x + -0 = x for every x under round-to-nearest), and a power-of-two tree
+// over the padded row has the same value as the adjacent-pair tree with an
+// odd carry over the n real leaves. IEEE addition is commutative, so both
+// butterfly partners hold the same bits.
+//
+// max_reduce ([05-OP-12]) combines with max_first in index order: in-lane
+// left to right, butterfly with the lower lane as the left operand,
+// waves and segments in order. Padding is -inf, which never displaces an
+// earlier element.
+#include "hip_common.h"
+
+namespace chelis {
+namespace {
+
+template <typename T, int V>
+struct VecT;
+template <>
+struct VecT<float, 4> {
+    using type = float4;
+};
+template <>
+struct VecT<double, 2> {
+    using type = double2;
+};
+
+template <typename T>
+__device__ inline T neg_inf() {
+    return -__builtin_huge_val();
+}
+template <>
+__device__ inline float neg_inf<float>() {
+    return -__builtin_huge_valf();
+}
+
+template <typename T>
+__device__ inline T exp_leaf(T v);
+template <>
+__device__ inline float exp_leaf<float>(float v) {
+    return expf_cr(v);
+}
+template <>
+__device__ inline double exp_leaf<double>(double v) {
+    return canon(exp(v));
+}
+
+// Per-row geometry: which row this wave group owns and where it starts.
+template <int W, int R>
+struct RowCoord {
+    int lane, wave_in_row, row_in_block, tid_in_row;
+    int64_t row;
+    __device__ RowCoord() {
+        const int tid = threadIdx.x;
+        lane = tid & 63;
+        const int wave = tid >> 6;
+        wave_in_row = wave % W;
+        row_in_block = wave / W;
+        tid_in_row = wave_in_row * 64 + lane;
+        row = (int64_t)blockIdx.x * R + row_in_block;
+    }
+};
+
+template <typename T, int V, int S, int W>
+__device__ inline void load_row(const T *__restrict__ p, int64_t n, bool vec_ok, int tid_in_row, T pad,
+                                T (&v)[S][V]) {
+    constexpr int SEG = 64 * W * V;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const int64_t base = (int64_t)s * SEG + (int64_t)tid_in_row * V;
+        if (vec_ok && base + V <= n) {
+            typename VecT<T, V>::type q = *reinterpret_cast<const typename VecT<T, V>::type *>(p + base);
+            const T *qe = reinterpret_cast<const T *>(&q);
+#pragma unroll
+            for (int i = 0; i < V; ++i) v[s][i] = qe[i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < V; ++i) v[s][i] = (base + i < n) ? p[base + i] : pad;
+        }
+    }
+}
+
+template <typename T, int V, int S, int W>
+__device__ inline void store_row(T *__restrict__ p, int64_t n, bool vec_ok, int tid_in_row, const T (&v)[S][V]) {
+    constexpr int SEG = 64 * W * V;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const int64_t base = (int64_t)s * SEG + (int64_t)tid_in_row * V;
+        if (vec_ok && base + V <= n) {
+            typename VecT<T, V>::type q;
+            T *qe = reinterpret_cast<T *>(&q);
+#pragma unroll
+            for (int i = 0; i < V; ++i) qe[i] = v[s][i];
+            *reinterpret_cast<typename VecT<T, V>::type *>(p + base) = q;
+        } else {
+#pragma unroll
+            for (int i = 0; i < V; ++i)
+                if (base + i < n) p[base + i] = v[s][i];
+        }
+    }
+}
+
+// Canonical tree over the padded row; every thread of the row gets the total.
+template <typename T, int V, int S, int W, int R>
+__device__ inline T row_tree_sum(const T (&v)[S][V], T *lds, const RowCoord<W, R> &c) {
+    T seg[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        T a[V];
+#pragma unroll
+        for (int i = 0; i < V; ++i) a[i] = v[s][i];
+#pragma unroll
+        for (int w = V; w > 1; w >>= 1)
+#pragma unroll
+            for (int i = 0; i < w / 2; ++i) a[i] = a[2 * i] + a[2 * i + 1];
+        T x = a[0];
+#pragma unroll
+        for (int m = 1; m < 64; m <<= 1) x = x + shfl_xor(x, m);
+        seg[s] = x;
+    }
+    if constexpr (W > 1) {
+        if (c.lane == 0)
+#pragma unroll
+            for (int s = 0; s < S; ++s) lds[(c.row_in_block * W + c.wave_in_row) * S + s] = seg[s];
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            T p[W];
+#pragma unroll
+            for (int w = 0; w < W; ++w) p[w] = lds[(c.row_in_block * W + w) * S + s];
+#pragma unroll
+            for (int w = W; w > 1; w >>= 1)
+#pragma unroll
+                for (int i = 0; i < w / 2; ++i) p[i] = p[2 * i] + p[2 * i + 1];
+            seg[s] = p[0];
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int w = S; w > 1; w >>= 1)
+#pragma unroll
+        for (int i = 0; i < w / 2; ++i) seg[i] = seg[2 * i] + seg[2 * i + 1];
+    return seg[0];
+}
+
+// [05-OP-12] maximum over the padded row, in index order.
+template <typename T, int V, int S, int W, int R>
+__device__ inline T row_max(const T (&v)[S][V], T *lds, const RowCoord<W, R> &c) {
+    T seg[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        T x = v[s][0];
+#pragma unroll
+        for (int i = 1; i < V; ++i) x = max_first(x, v[s][i]);
+#pragma unroll
+        for (int m = 1; m < 64; m <<= 1) {
+            T o = shfl_xor(x, m);
+            x = (c.lane & m) ? max_first(o, x) : max_first(x, o);
+        }
+        seg[s] = x;
+    }
+    if constexpr (W > 1) {
+        if (c.lane == 0)
+#pragma unroll
+            for (int s = 0; s < S; ++s) lds[(c.row_in_block * W + c.wave_in_row) * S + s] = seg[s];
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            T x = lds[(c.row_in_block * W) * S + s];
+#pragma unroll
+            for (int w = 1; w < W; ++w) x = max_first(x, lds[(c.row_in_block * W + w) * S + s]);
+            seg[s] = x;
+        }
+        __syncthreads();
+    }
+    T x = seg[0];
+#pragma unroll
+    for (int s = 1; s < S; ++s) x = max_first(x, seg[s]);
+    return x;
+}
+
+// softmax over the last axis, optionally of where(j <= i, x * scale, -inf)
+// (causal != 0, q_len = rows per score matrix).
+template <typename T, int V, int S, int W, int R>
+__global__ __launch_bounds__(64 * W * R) void softmax_kernel(const T *__restrict__ x, T *__restrict__ y,
+                                                              int64_t rows, int64_t n, int64_t ldx, int64_t ldy,
+                                                              bool vec_ok, int masked, T scale, int64_t q_len) {
+    __shared__ T lds[R * W * S];
+    RowCoord<W, R> c;
+    if (c.row >= rows) return;  // whole row groups exit together (R rows per block, W waves each)
+    const T *xr = x + c.row * ldx;
+    T v[S][V];
+    load_row<T, V, S, W>(xr, n, vec_ok, c.tid_in_row, neg_inf<T>(), v);
+    constexpr int SEG = 64 * W * V;
+    if (masked) {
+        const int64_t qi = c.row % q_len;
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int i = 0; i < V; ++i) {
+                const int64_t j = (int64_t)s * SEG + (int64_t)c.tid_in_row * V + i;
+                if (j < n) {
+                    T sc = canon(v[s][i] * scale);
+                    v[s][i] = (masked == 2 || j <= qi) ? sc : neg_inf<T>();
+                }
+            }
+    }
+    const T m = row_max<T, V, S, W, R>(v, lds, c);
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            const int64_t j = (int64_t)s * SEG + (int64_t)c.tid_in_row * V + i;
+            v[s][i] = (j < n) ? exp_leaf<T>(canon(v[s][i] - m)) : T(-0.0);
+        }
+    const T total = canon(row_tree_sum<T, V, S, W, R>(v, lds, c));
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int i = 0; i < V; ++i) v[s][i] = canon(v[s][i] / total);
+    store_row<T, V, S, W>(y + c.row * ldy, n, vec_ok, c.tid_in_row, v);
+}
+
+// dx = y * (g - sum(g * y)) over the last axis.
+template <typename T, int V, int S, int W, int R>
+__global__ __launch_bounds__(64 * W * R) void softmax_adjoint_kernel(const T *__restrict__ y,
+                                                                      const T *__restrict__ g, T *__restrict__ dx,
+                                                                      int64_t rows, int64_t n, int64_t ldy,
+                                                                      int64_t ldg, int64_t ldd, bool vec_ok) {
+    __shared__ T lds[R * W * S];
+    RowCoord<W, R> c;
+    if (c.row >= rows) return;
+    T yv[S][V], gv[S][V], t[S][V];
+    load_row<T, V, S, W>(y + c.row * ldy, n, vec_ok, c.tid_in_row, T(-0.0), yv);
+    load_row<T, V, S, W>(g + c.row * ldg, n, vec_ok, c.tid_in_row, T(-0.0), gv);
+    constexpr int SEG = 64 * W * V;
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            const int64_t j = (int64_t)s * SEG + (int64_t)c.tid_in_row * V + i;
+            t[s][i] = (j < n) ? canon(gv[s][i] * yv[s][i]) : T(-0.0);
+        }
+    const T total = canon(row_tree_sum<T, V, S, W, R>(t, lds, c));
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int i = 0; i < V; ++i) t[s][i] = canon(yv[s][i] * canon(gv[s][i] - total));
+    store_row<T, V, S, W>(dx + c.row * ldd, n, vec_ok, c.tid_in_row, t);
+}
+
+// layer_norm: mean = tree(x)/n; c = x - mean; var = tree(c*c)/n;
+// y = (c / sqrt(var + eps)) * gamma + beta, every primitive finalized.
+template <typename T, int V, int S, int W, int R>
+__global__ __launch_bounds__(64 * W * R) void layer_norm_kernel(const T *__restrict__ x, const T *__restrict__ gamma,
+                                                                 const T *__restrict__ beta, T *__restrict__ y,
+                                                                 int64_t rows, int64_t n, int64_t ldx, int64_t ldy,
+                                                                 bool vec_ok, T eps) {
+    __shared__ T lds[R * W * S];
+    RowCoord<W, R> c;
+    if (c.row >= rows) return;
+    T v[S][V], q[S][V];
+    load_row<T, V, S, W>(x + c.row * ldx, n, vec_ok, c.tid_in_row, T(-0.0), v);
+    const T extent = (T)n;
+    const T mean = canon(canon(row_tree_sum<T, V, S, W, R>(v, lds, c)) / extent);
+    constexpr int SEG = 64 * W * V;
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            const int64_t j = (int64_t)s * SEG + (int64_t)c.tid_in_row * V + i;
+            v[s][i] = canon(v[s][i] - mean);
+            q[s][i] = (j < n) ? canon(v[s][i] * v[s][i]) : T(-0.0);
+        }
+    const T var = canon(canon(row_tree_sum<T, V, S, W, R>(q, lds, c)) / extent);
+    const T denom = canon(sqrt(canon(var + eps)));
+    // gamma/beta are [n] vectors shared by every row
+    load_row<T, V, S, W>(gamma, n, vec_ok, c.tid_in_row, T(0), q);
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int i = 0; i < V; ++i) v[s][i] = canon(canon(v[s][i] / denom) * q[s][i]);
+    load_row<T, V, S, W>(beta, n, vec_ok, c.tid_in_row, T(0), q);
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int i = 0; i < V; ++i) v[s][i] = canon(v[s][i] + q[s][i]);
+    store_row<T, V, S, W>(y + c.row * ldy, n, vec_ok, c.tid_in_row, v);
+}
+
+// ---------------------------------------------------------------- dispatch
+// Instantiated shapes: (S, W, R) per capacity. V is 16 bytes of T.
+enum class RowOp { Softmax, SoftmaxAdjoint, LayerNorm };
+
+struct RowArgs {
+    const void *a, *b, *c;
+    void *out;
+    int64_t rows, n, lda, ldb, ldo;
+    bool vec_ok;
+    int masked;
+    double scale;
+    int64_t q_len;
+    double eps;
+};
+
+template <typename T, int V, int S, int W, int R>
+int32_t launch_shape(RowOp op, const RowArgs &a, hipStream_t st) {
+    const unsigned grid = grid_for(a.rows, R);
+    const dim3 block(64 * W * R);
+    switch (op) {
+        case RowOp::Softmax:
+            softmax_kernel<T, V, S, W, R><<<grid, block, 0, st>>>(
+                (const T *)a.a, (T *)a.out, a.rows, a.n, a.lda, a.ldo, a.vec_ok, a.masked, (T)a.scale, a.q_len);
+            break;
+        case RowOp::SoftmaxAdjoint:
+            softmax_adjoint_kernel<T, V, S, W, R><<<grid, block, 0, st>>>(
+                (const T *)a.a, (const T *)a.b, (T *)a.out, a.rows, a.n, a.lda, a.ldb, a.ldo, a.vec_ok);
+            break;
+        case RowOp::LayerNorm:
+            layer_norm_kernel<T, V, S, W, R><<<grid, block, 0, st>>>(
+                (const T *)a.a, (const T *)a.b, (const T *)a.c, (T *)a.out, a.rows, a.n, a.lda, a.ldo, a.vec_ok,
+                (T)a.eps);
+            break;
+    }
+    CHELIS_LAUNCH_CHECK();
+    return CHELIS_HIP_OK;
+}
+
+// Capacity ladder: CAP = S * 64W * V, smallest power of two >= n.
+template <typename T>
+int32_t launch_rows(RowOp op, const RowArgs &a) {
+    constexpr int V = 16 / sizeof(T);
+    hipStream_t st = stream();
+    if (!st) return set_error(CHELIS_HIP_EHIP, "no HIP device");
+    const int64_t seg1 = 64 * V;  // one wave, one segment
+    const int64_t n = a.n;
+    if (n <= seg1) return launch_shape<T, V, 1, 1, 4>(op, a, st);
+    if (n <= 2 * seg1) return launch_shape<T, V, 2, 1, 4>(op, a, st);
+    if (n <= 4 * seg1) return launch_shape<T, V, 4, 1, 4>(op, a, st);
+    if (n <= 8 * seg1) return launch_shape<T, V, 8, 1, 2>(op, a, st);
+    if (n <= 16 * seg1) return launch_shape<T, V, 4, 4, 1>(op, a, st);
+    if (n <= 32 * seg1) return launch_shape<T, V, 8, 4, 1>(op, a, st);
+    if (n <= 64 * seg1) return launch_shape<T, V, 8, 8, 1>(op, a, st);
+    if (n <= 128 * seg1) return launch_shape<T, V, 8, 16, 1>(op, a, st);
+    if (n <= 256 * seg1) return launch_shape<T, V, 16, 16, 1>(op, a, st);
+    return set_error(CHELIS_HIP_EUNSUPPORTED, "row length %lld exceeds the in-register row capacity %lld",
+                     (long long)n, (long long)(256 * seg1));
+}
+
+int32_t dispatch(chelis_dtype dt, RowOp op, const RowArgs &a) {
+    if (a.rows == 0 || a.n == 0) return CHELIS_HIP_OK;
+    return dt == CHELIS_DTYPE_F32 ? launch_rows<float>(op, a) : launch_rows<double>(op, a);
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int32_t check_rows_pair(const chelis_gpu_tensor *x, const chelis_gpu_tensor *y, RowView *vx, RowView *vy,
+                        const char *what) {
+    int32_t s;
+    if ((s = check_tensor(x, "x")) || (s = check_tensor(y, "y"))) return s;
+    if (!is_float(x->dtype) || x->dtype != y->dtype)
+        return set_error(CHELIS_HIP_EDOMAIN, "%s: x and y must share an f32 or f64 dtype", what);
+    if (!same_shape(x, y)) return set_error(CHELIS_HIP_EDOMAIN, "%s: x and y shapes differ", what);
+    if (!row_view(x, vx) || !row_view(y, vy))
+        return set_error(CHELIS_HIP_EUNSUPPORTED, "%s: last axis must be contiguous with uniform row stride", what);
+    return CHELIS_HIP_OK;
+}
+
+}  // namespace
+}  // namespace chelis
+
+using namespace chelis;
+
+extern "C" int32_t chelis_hip_softmax(const chelis_gpu_tensor *x, const chelis_gpu_tensor *y) {
+    RowView vx, vy;
+    if (int32_t s = check_rows_pair(x, y, &vx, &vy, "softmax")) return s;
+    const int64_t V = 16 / dtype_width(x->dtype);
+    RowArgs a{x->data, nullptr, nullptr, y->data, vx.rows, vx.n, vx.ld, 0, vy.ld,
+              aligned16(x->data) && aligned16(y->data) && vx.ld % V == 0 && vy.ld % V == 0, 0, 1.0, 1, 0.0};
+    return dispatch(x->dtype, RowOp::Softmax, a);
+}
+
+extern "C" int32_t chelis_hip_scaled_masked_softmax(const chelis_gpu_tensor *x, double scale, int32_t causal,
+                                                    const chelis_gpu_tensor *y) {
+    RowView vx, vy;
+    if (int32_t s = check_rows_pair(x, y, &vx, &vy, "scaled_masked_softmax")) return s;
+    if (x->rank < 2) return set_error(CHELIS_HIP_EDOMAIN, "scaled_masked_softmax: scores need rank >= 2");
+    const int64_t q_len = x->shape[x->rank - 2];
+    if (causal && q_len != vx.n)
+        return set_error(CHELIS_HIP_EDOMAIN, "scaled_masked_softmax: causal mask needs square score matrices");
+    const int64_t V = 16 / dtype_width(x->dtype);
+    RowArgs a{x->data, nullptr, nullptr, y->data, vx.rows, vx.n, vx.ld, 0, vy.ld,
+              aligned16(x->data) && aligned16(y->data) && vx.ld % V == 0 && vy.ld % V == 0,
+              causal ? 1 : 2, scale, q_len > 0 ? q_len : 1, 0.0};
+    return dispatch(x->dtype, RowOp::Softmax, a);
+}
+
+extern "C" int32_t chelis_hip_softmax_adjoint(const chelis_gpu_tensor *y, const chelis_gpu_tensor *g,
+                                              const chelis_gpu_tensor *dx) {
+    RowView vy, vg, vd;
+    if (int32_t s = check_rows_pair(y, dx, &vy, &vd, "softmax_adjoint")) return s;
+    if (int32_t s = check_tensor(g, "g")) return s;
+    if (g->dtype != y->dtype || !same_shape(g, y) || !row_view(g, &vg))
+        return set_error(CHELIS_HIP_EDOMAIN, "softmax_adjoint: g must match y");
+    const int64_t V = 16 / dtype_width(y->dtype);
+    RowArgs a{y->data, g->data, nullptr, dx->data, vy.rows, vy.n, vy.ld, vg.ld, vd.ld,
+              aligned16(y->data) && aligned16(g->data) && aligned16(dx->data) && vy.ld % V == 0 &&
+                  vg.ld % V == 0 && vd.ld % V == 0,
+              0, 1.0, 1, 0.0};
+    return dispatch(y->dtype, RowOp::SoftmaxAdjoint, a);
+}
+
+extern "C" int32_t chelis_hip_layer_norm(const chelis_gpu_tensor *x, const chelis_gpu_tensor *gamma,
+                                         const chelis_gpu_tensor *beta, double epsilon,
+                                         const chelis_gpu_tensor *y) {
+    RowView vx, vy;
+    if (int32_t s = check_rows_pair(x, y, &vx, &vy, "layer_norm")) return s;
+    int32_t s;
+    if ((s = check_tensor(gamma, "gamma")) || (s = check_tensor(beta, "beta"))) return s;
+    for (const chelis_gpu_tensor *p : {gamma, beta})
+        if (p->dtype != x->dtype || p->rank != 1 || p->shape[0] != vx.n || (vx.n > 1 && p->strides[0] != 1))
+            return set_error(CHELIS_HIP_EDOMAIN, "layer_norm: gamma/beta must be contiguous [hidden]");
+    if (vx.n == 0) return set_error(CHELIS_HIP_EDOMAIN, "layer_norm: hidden extent must be positive");
+    const int64_t V = 16 / dtype_width(x->dtype);
+    RowArgs a{x->data, gamma->data, beta->data, y->data, vx.rows, vx.n, vx.ld, 0, vy.ld,
+              aligned16(x->data) && aligned16(y->data) && aligned16(gamma->data) && aligned16(beta->data) &&
+                  vx.ld % V == 0 && vy.ld % V == 0,
+              0, 1.0, 1, epsilon};
+    return dispatch(x->dtype, RowOp::LayerNorm, a);
+}

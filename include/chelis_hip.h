@@ -1,0 +1,158 @@
+/* MI355X (gfx950) region ABI: the launch surface a fused-DAG emitter binds.
+ *
+ * In the reference, chelis-backend-hip emits one HIP kernel string per DAG
+ * region (crates/chelis-backend-hip/src/kernels.rs) and launches it through
+ * hiprtc + hipModuleLaunchKernel on stream 0 (runtime/chelis_hip_runtime.h:
+ * 409-485), with matmuls on hipBLAS (runtime/chelis_hip_runtime.h:48-404).
+ * Here every region kind is a precompiled gfx950 kernel family behind one
+ * `extern "C"` launcher that takes the reference's own device packet
+ * (chelis_gpu_tensor). Launchers validate on the host, enqueue on the
+ * library's single HIP stream and return without synchronizing; a status
+ * other than CHELIS_HIP_OK leaves no work enqueued and sets
+ * chelis_hip_last_error(). Which reference kernel each launcher replaces is
+ * noted at its declaration.
+ *
+ * Numerics: every float result is finalized at its dtype with NaN stored as
+ * the canonical quiet NaN ([04-NUM-2]); every float sum follows the
+ * canonical adjacent-pair tree ([05-OP-30]) bit for bit; RNG, relu, count
+ * and max/min selection are bit-exact. Matmuls on the MFMA path are the
+ * only results that differ from the canonical tree (by rounding only).
+ */
+#ifndef CHELIS_HIP_H
+#define CHELIS_HIP_H
+
+#include <stdint.h>
+#include "chelis_device_descriptor.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    CHELIS_HIP_OK = 0,
+    CHELIS_HIP_EDOMAIN = 1,      /* invalid shapes, dtypes, rates, axes */
+    CHELIS_HIP_EUNSUPPORTED = 2, /* valid request outside the built kernel families */
+    CHELIS_HIP_EHIP = 3          /* a HIP runtime call failed */
+};
+
+/* ---- context ---- */
+const char *chelis_hip_last_error(void);
+/* The library's stream on the current device (a hipStream_t), created on
+ * first use at default priority. Every launcher enqueues on it. */
+void *chelis_hip_stream(void);
+int32_t chelis_hip_synchronize(void);
+/* Build identification: "gfx950 <git-describe>" style string. */
+const char *chelis_hip_build_info(void);
+
+/* ---- row regions (last axis; rows contiguous) ----
+ * softmax: spec/05 section 4.2 as one region (max_reduce, sub, exp, sum, div),
+ * replacing reduce_max + fused_elementwise[Sub,Exp] + reduce_sum + div
+ * (kernels.rs:1802,2391,1703) which the reference fences off the device
+ * (crates/chelis-ir/src/device_admission.rs:41-68). f32 exp is correctly
+ * rounded (bit-exact with the C lane); f64 exp is within 1 ulp. */
+int32_t chelis_hip_softmax(const chelis_gpu_tensor *x, const chelis_gpu_tensor *y);
+/* softmax(where(mask, x * scale, -inf)) over the last axis of a
+ * [..., S_q, S_k] score tensor with the causal mask j <= i (spec/05 section
+ * 4.7 steps 3-5) when causal != 0; scale is rounded once to the dtype. */
+int32_t chelis_hip_scaled_masked_softmax(const chelis_gpu_tensor *x, double scale, int32_t causal,
+                                         const chelis_gpu_tensor *y);
+/* softmax adjoint y * (g - sum(g * y)) (crates/chelis-dag-core/src/grad.rs:2248). */
+int32_t chelis_hip_softmax_adjoint(const chelis_gpu_tensor *y, const chelis_gpu_tensor *g,
+                                   const chelis_gpu_tensor *dx);
+/* layer_norm over the last axis: spec/05 section 4.4 / tier2.rs:1248-1360. */
+int32_t chelis_hip_layer_norm(const chelis_gpu_tensor *x, const chelis_gpu_tensor *gamma,
+                              const chelis_gpu_tensor *beta, double epsilon, const chelis_gpu_tensor *y);
+
+/* ---- fused elementwise chains (RiscOp::FusedElem, dag.rs:485-524,673-678) ----
+ * A step's args index the chain inputs when >= 0, and a previous step k as
+ * -(k + 1) (FusedInput::External / FusedInput::PreviousStep). The chain's
+ * value is its last step. `imm` is the scalar of CHELIS_FUSED_CONST. */
+enum {
+    CHELIS_FUSED_ADD = 0, CHELIS_FUSED_SUB, CHELIS_FUSED_MUL, CHELIS_FUSED_DIV,
+    CHELIS_FUSED_MAX_ELEM, CHELIS_FUSED_MIN_ELEM, CHELIS_FUSED_NEG, CHELIS_FUSED_RECIP,
+    CHELIS_FUSED_EXP, CHELIS_FUSED_LOG, CHELIS_FUSED_SQRT, CHELIS_FUSED_TANH,
+    CHELIS_FUSED_ERFC, CHELIS_FUSED_ABS, CHELIS_FUSED_FLOOR, CHELIS_FUSED_CEIL,
+    CHELIS_FUSED_ROUND, CHELIS_FUSED_RELU, CHELIS_FUSED_RELU_ADJOINT,
+    CHELIS_FUSED_CONST, CHELIS_FUSED_COUNT_
+};
+#define CHELIS_FUSED_MAX_STEPS 16
+#define CHELIS_FUSED_MAX_INPUTS 8
+typedef struct {
+    uint8_t op;
+    uint8_t reserved[3];
+    int32_t args[2];
+    double imm;
+} chelis_fused_step;
+typedef struct {
+    int32_t n_steps;
+    int32_t reserved;
+    chelis_fused_step steps[CHELIS_FUSED_MAX_STEPS];
+} chelis_fused_chain;
+/* kernels.rs:2391 fused_elementwise. Inputs broadcast to `out` by their
+ * own strides (stride 0 = expanded axis); out is contiguous. */
+int32_t chelis_hip_fused_elementwise(const chelis_fused_chain *chain, const chelis_gpu_tensor *const *inputs,
+                                     int32_t n_inputs, const chelis_gpu_tensor *out);
+
+/* ---- reductions over one axis ----
+ * kernels.rs:2175 reduce_fused (chain != NULL: the chain's value is the
+ * leaf) and kernels.rs:1703-2013 reduce_sum/max/min/prod/argmax/argmin
+ * (chain == NULL: inputs[0] is the leaf). Sum and prod use the canonical
+ * tree; max/min the first-NaN / first-representation rule [05-OP-12/13];
+ * argmax/argmin write i64. `out` has the input shape minus `axis`. */
+enum {
+    CHELIS_REDUCE_SUM = 0, CHELIS_REDUCE_COUNT = 1, CHELIS_REDUCE_MAX = 2,
+    CHELIS_REDUCE_MIN = 3, CHELIS_REDUCE_PROD = 4, CHELIS_REDUCE_ARGMAX = 5,
+    CHELIS_REDUCE_ARGMIN = 6
+};
+int32_t chelis_hip_reduce(int32_t op, const chelis_fused_chain *chain, const chelis_gpu_tensor *const *inputs,
+                          int32_t n_inputs, int32_t axis, const chelis_gpu_tensor *out);
+/* kernels.rs:375-557 count: Bool8 -> i64 over one axis. A byte that is not
+ * 0/1 sets *error_code = 1 (the reference kernel's code 1); the call then
+ * synchronizes to read it back. */
+int32_t chelis_hip_count(const chelis_gpu_tensor *x, int32_t axis, const chelis_gpu_tensor *out,
+                         int32_t *error_code);
+
+/* ---- keyed RNG ([05-RNG-1/2], [05-OP-8], [05-OP-37]) ----
+ * uniform_like: kernels.rs:1672. dropout / replay: the C lane's semantics
+ * (crates/chelis-backend-c/src/emit.rs:6139-6220); the reference HIP lane
+ * rejects them (crates/chelis-backend-hip/src/emit.rs:2763-2778). A rate
+ * outside [0, 1) returns CHELIS_HIP_EDOMAIN with the reference's trap text
+ * `numeric trap: domain in dropout at f32|f64` as the last error. */
+int32_t chelis_hip_uniform_like(uint64_t key, double low, double high, const chelis_gpu_tensor *out);
+int32_t chelis_hip_dropout(uint64_t key, const chelis_gpu_tensor *x, double rate, const chelis_gpu_tensor *y);
+int32_t chelis_hip_dropout_replay(uint64_t key, const chelis_gpu_tensor *g, double rate,
+                                  const chelis_gpu_tensor *dx);
+
+/* ---- activations ----
+ * gelu: spec/05 section 3.3's exact Phi graph (fenced on the reference HIP
+ * lane). relu / relu adjoint: kernels.rs:1136-1196. */
+int32_t chelis_hip_gelu(const chelis_gpu_tensor *x, const chelis_gpu_tensor *y);
+int32_t chelis_hip_relu(const chelis_gpu_tensor *x, const chelis_gpu_tensor *y);
+int32_t chelis_hip_relu_adjoint(const chelis_gpu_tensor *x, const chelis_gpu_tensor *g,
+                                const chelis_gpu_tensor *dx);
+
+/* ---- matmul dispatch (BlasMatmul, dag.rs:1338-1352; hipBLAS wrappers
+ * chelis_hip_runtime.h:48-404) ----
+ * c[..., M, N] = a[..., M, K] . b[..., K, N] with any element strides on a
+ * and b (a transposed operand is a stride swap, never a copy; batch axes
+ * broadcast by stride 0) and c contiguous. Dense shapes run on MFMA
+ * (v_mfma_f32_16x16x4_f32 / v_mfma_f64_16x16x4_f64), GEMV and skinny shapes
+ * on bandwidth kernels whose K sum is the canonical tree (bit-exact).
+ * `flags` = CHELIS_MATMUL_EXACT forces the canonical-tree kernels on every
+ * shape. */
+#define CHELIS_MATMUL_EXACT 1
+int32_t chelis_hip_matmul(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b, const chelis_gpu_tensor *c,
+                          int32_t flags);
+/* matmul with a fused epilogue, applied per element of the f32/f64 result
+ * in graph order: v = mm; if bias: v = v + bias[n]; act 1: v = relu(v),
+ * act 2: v = gelu(v); if residual: v = residual + v. Each step finalizes
+ * at the dtype, so the bits equal the unfused graph's. */
+enum { CHELIS_ACT_NONE = 0, CHELIS_ACT_RELU = 1, CHELIS_ACT_GELU = 2 };
+int32_t chelis_hip_linear(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b, const chelis_gpu_tensor *bias,
+                          int32_t activation, const chelis_gpu_tensor *residual, const chelis_gpu_tensor *c,
+                          int32_t flags);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

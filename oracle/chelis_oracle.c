@@ -218,6 +218,23 @@ int32_t orc_count_axis(const uint8_t *x, int64_t outer, int64_t n, int64_t inner
 DEFINE_SOFTMAX(orc_softmax_rows_f32, float, nan32, orc_expf, orc_max_reduce_f32, orc_tree_sum_f32)
 DEFINE_SOFTMAX(orc_softmax_rows_f64, double, nan64, orc_exp, orc_max_reduce_f64, orc_tree_sum_f64)
 
+/* Softmax adjoint rows: dx = y * (g - sum(g * y))
+ * (crates/chelis-dag-core/src/grad.rs:2248-2290): Mul, tree Sum, Sub, Mul. */
+#define DEFINE_SOFTMAX_ADJ(NAME, T, NANF, SUMF)                                \
+    void NAME(const T *y, const T *g, T *dx, int64_t rows, int64_t n) {        \
+        _Pragma("omp parallel for schedule(static)")                           \
+        for (int64_t r = 0; r < rows; ++r) {                                   \
+            const T *yr = y + r * n, *gr = g + r * n;                          \
+            T *t = (T *)malloc((size_t)(n ? n : 1) * sizeof(T));               \
+            for (int64_t i = 0; i < n; ++i) t[i] = NANF(gr[i] * yr[i]);        \
+            T s = SUMF(t, n, 1);                                               \
+            for (int64_t i = 0; i < n; ++i) dx[r * n + i] = NANF(yr[i] * NANF(gr[i] - s)); \
+            free(t);                                                           \
+        }                                                                      \
+    }
+DEFINE_SOFTMAX_ADJ(orc_softmax_adjoint_rows_f32, float, nan32, orc_tree_sum_f32)
+DEFINE_SOFTMAX_ADJ(orc_softmax_adjoint_rows_f64, double, nan64, orc_tree_sum_f64)
+
 /* Layer norm over the last axis: spec/05 section 4.4, lower_layer_norm
  * (tier2.rs:1248-1360) with mean = tree sum / extent ([05-OP-11],
  * lower_mean tier2.rs:1183). */

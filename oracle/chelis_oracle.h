@@ -72,6 +72,8 @@ int32_t orc_count_axis(const uint8_t *x, int64_t outer, int64_t n, int64_t inner
 /* ---- row regions ---- */
 void orc_softmax_rows_f32(const float *x, float *y, int64_t rows, int64_t n);
 void orc_softmax_rows_f64(const double *x, double *y, int64_t rows, int64_t n);
+void orc_softmax_adjoint_rows_f32(const float *y, const float *g, float *dx, int64_t rows, int64_t n);
+void orc_softmax_adjoint_rows_f64(const double *y, const double *g, double *dx, int64_t rows, int64_t n);
 void orc_layer_norm_rows_f32(const float *x, const float *gamma, const float *beta, float eps,
                              float *y, int64_t rows, int64_t n);
 void orc_layer_norm_rows_f64(const double *x, const double *gamma, const double *beta, double eps,

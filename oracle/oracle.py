@@ -64,6 +64,8 @@ def _declare(L):
         "orc_count_axis": (ctypes.c_int32, [c_p, c_i64, c_i64, c_i64, c_p]),
         "orc_softmax_rows_f32": (None, [c_p, c_p, c_i64, c_i64]),
         "orc_softmax_rows_f64": (None, [c_p, c_p, c_i64, c_i64]),
+        "orc_softmax_adjoint_rows_f32": (None, [c_p, c_p, c_p, c_i64, c_i64]),
+        "orc_softmax_adjoint_rows_f64": (None, [c_p, c_p, c_p, c_i64, c_i64]),
         "orc_layer_norm_rows_f32": (None, [c_p, c_p, c_p, c_f32, c_p, c_i64, c_i64]),
         "orc_layer_norm_rows_f64": (None, [c_p, c_p, c_p, c_f64, c_p, c_i64, c_i64]),
         "orc_gelu_f32": (None, [c_p, c_p, c_i64]),
@@ -171,6 +173,15 @@ def softmax_rows(x: np.ndarray) -> np.ndarray:
     n = x.shape[-1]
     getattr(lib(), f"orc_softmax_rows_{_f(x.dtype)}")(_ptr(x), _ptr(y), x.size // max(n, 1), n)
     return y
+
+
+def softmax_adjoint_rows(y, g) -> np.ndarray:
+    y = np.ascontiguousarray(y)
+    g = np.ascontiguousarray(g, y.dtype)
+    dx = np.empty_like(y)
+    n = y.shape[-1]
+    getattr(lib(), f"orc_softmax_adjoint_rows_{_f(y.dtype)}")(_ptr(y), _ptr(g), _ptr(dx), y.size // n, n)
+    return dx
 
 
 def layer_norm_rows(x, gamma, beta, eps) -> np.ndarray:

@@ -1,0 +1,202 @@
+"""GPU parity of the row and elementwise regions against the CPU oracle.
+
+Bar: bit-exact where the oracle's leaves are IEEE operations or the
+correctly rounded binary32 exp (softmax f32, layer norm, relu, dropout,
+uniform_like, the f32 GELU except its erfc leaf); 1e-12 relative for f64
+elementwise and 1e-10 for f64 reductions where the device exp/erfc leaf is
+within an ulp instead of correctly rounded; f32 GELU within 1e-5 relative
+(its erfc leaf is binary64 erfc rounded once, nearly always correct).
+"""
+import numpy as np
+import pytest
+
+import chelis_amd as C
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def setup_module(_m):
+    O.build()
+
+
+def bits_equal(a, b):
+    return np.array_equal(np.ascontiguousarray(a).view(np.uint8), np.ascontiguousarray(b).view(np.uint8))
+
+
+def mismatch_report(a, b):
+    ai = np.ascontiguousarray(a).view(np.uint32 if a.dtype == np.float32 else np.uint64)
+    bi = np.ascontiguousarray(b).view(np.uint32 if b.dtype == np.float32 else np.uint64)
+    bad = np.nonzero(ai != bi)
+    return f"{len(bad[0])} mismatches; first at {tuple(i[0] for i in bad) if len(bad[0]) else None}"
+
+
+@pytest.mark.parametrize("n", [1, 3, 10, 64, 100, 255, 256, 257, 512, 1000, 1024, 2048, 2049, 4096, 5000, 16384])
+def test_softmax_f32_bit_exact(n):
+    rows = max(1, 65536 // n)
+    x = (np.random.default_rng(n).standard_normal((rows, n)) * 2).astype(np.float32)
+    y = C.softmax(C.to_device(x)).numpy()
+    ref = O.softmax_rows(x)
+    assert bits_equal(y, ref), mismatch_report(y, ref)
+
+
+def test_softmax_f32_config_shape_bit_exact():
+    """Config 2: [16384, 1024] ~ N(0, sigma=2), compared elementwise and by row sum."""
+    x = (np.random.default_rng(10).standard_normal((16384, 1024)) * 2).astype(np.float32)
+    y = C.softmax(C.to_device(x)).numpy()
+    ref = O.softmax_rows(x)
+    assert bits_equal(y, ref), mismatch_report(y, ref)
+    assert np.abs(y.astype(np.float64).sum(1) - 1).max() < 1e-5
+
+
+def test_softmax_f64_config_shape():
+    """Config 2 f64: [4096, 4096] ~ N(0,1); exp leaf within 1 ulp."""
+    x = np.random.default_rng(11).standard_normal((4096, 4096))
+    y = C.softmax(C.to_device(x)).numpy()
+    ref = O.softmax_rows(x)
+    rel = np.abs(y - ref) / np.abs(ref)
+    assert rel.max() <= 1e-12, rel.max()
+    assert np.abs(y.sum(1) - 1).max() < 1e-10
+
+
+def test_softmax_special_rows():
+    x = np.array([[0.0, -np.inf, 1.0, -np.inf], [-np.inf] * 4, [3.0] * 4, [1.0, np.nan, 0, 0],
+                  [np.inf, 0, 0, 0], [-0.0, 0.0, -0.0, 0.0]], np.float32)
+    y = C.softmax(C.to_device(x)).numpy()
+    assert bits_equal(y, O.softmax_rows(x))
+
+
+def test_softmax_strided_rows():
+    """Rows with a leading stride larger than the row (a column slice)."""
+    big = (np.random.default_rng(3).standard_normal((64, 1536)) * 3).astype(np.float32)
+    d = C.to_device(big)
+    v = d.view((64, 1000), (1536, 1), offset_elems=8)
+    out = C.empty((64, 1000), np.float32)
+    C.softmax(v, out)
+    assert bits_equal(out.numpy(), O.softmax_rows(big[:, 8:1008].copy()))
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_scaled_masked_softmax(causal):
+    s = 128
+    x = np.random.default_rng(5).standard_normal((2, 3, s, s)).astype(np.float32)
+    scale = np.float32(0.125)
+    y = C.scaled_masked_softmax(C.to_device(x), 0.125, causal).numpy()
+    sc = x * scale
+    if causal:
+        mask = np.tril(np.ones((s, s), bool))
+        sc = np.where(mask, sc, np.float32(-np.inf)).astype(np.float32)
+    ref = O.softmax_rows(sc.reshape(-1, s)).reshape(x.shape)
+    assert bits_equal(y, ref), mismatch_report(y, ref)
+
+
+@pytest.mark.parametrize("dtype,n", [(np.float32, 10), (np.float32, 1024), (np.float64, 777)])
+def test_softmax_adjoint(dtype, n):
+    rng = np.random.default_rng(6)
+    yv = O.softmax_rows(rng.standard_normal((256, n)).astype(dtype))
+    g = rng.standard_normal((256, n)).astype(dtype)
+    dx = C.softmax_adjoint(C.to_device(yv), C.to_device(g)).numpy()
+    assert bits_equal(dx, O.softmax_adjoint_rows(yv, g))
+
+
+@pytest.mark.parametrize("dtype,shape", [(np.float32, (4096, 1024)), (np.float32, (100, 333)),
+                                         (np.float64, (512, 1024))])
+def test_layer_norm_bit_exact(dtype, shape):
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal(shape).astype(dtype)
+    g = rng.standard_normal(shape[-1]).astype(dtype)
+    b = rng.standard_normal(shape[-1]).astype(dtype)
+    y = C.layer_norm(C.to_device(x), C.to_device(g), C.to_device(b), 1e-5).numpy()
+    ref = O.layer_norm_rows(x, g, b, dtype(1e-5))
+    assert bits_equal(y, ref), mismatch_report(y, ref)
+
+
+def test_relu_and_adjoint_bit_rules():
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal(1 << 20).astype(np.float32)
+    x[:6] = [-0.0, 0.0, np.nan, -np.inf, np.inf, -1.0]
+    x[6:8] = np.array([0x7FC01234, 0xFFC00001], np.uint32).view(np.float32)
+    g = rng.standard_normal(x.size).astype(np.float32)
+    assert bits_equal(C.relu(C.to_device(x)).numpy(), O.relu(x))
+    assert bits_equal(C.relu_adjoint(C.to_device(x), C.to_device(g)).numpy(), O.relu_adjoint(x, g))
+
+
+@pytest.mark.parametrize("n", [4, 1023, 1024 * 512 + 3])
+def test_dropout_and_replay_bit_exact(n):
+    key = O.fold_in(44, 7)
+    x = np.random.default_rng(9).standard_normal(n).astype(np.float32)
+    y = C.dropout(key, C.to_device(x), 0.1).numpy()
+    assert bits_equal(y, O.dropout(key, x, np.float32(0.1)))
+    g = np.random.default_rng(10).standard_normal(n).astype(np.float32)
+    dx = C.dropout_replay(key, C.to_device(g), 0.1).numpy()
+    assert bits_equal(dx, O.dropout_replay(key, g, np.float32(0.1)))
+
+
+def test_dropout_fixed_stream_golden():
+    left, right = O.split(42)
+    ones = np.ones(4, np.float32)
+    assert C.dropout(right, C.to_device(ones), 0.5).numpy().tolist() == [2.0, 2.0, 0.0, 0.0]
+    assert C.dropout_replay(left, C.to_device(ones), 0.5).numpy().tolist() == [2.0, 0.0, 0.0, 2.0]
+
+
+def test_dropout_invalid_rate_is_domain_error():
+    x = C.to_device(np.ones(4, np.float32))
+    with pytest.raises(C.ChelisError, match="numeric trap: domain in dropout at f32"):
+        C.dropout(1, x, 1.0)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_uniform_like_bit_exact(dtype):
+    out = C.empty((100003,), dtype)
+    C.uniform_like(12345, -1.0, 1.0, out)
+    assert bits_equal(out.numpy(), O.uniform_like(12345, dtype(-1.0), dtype(1.0), 100003, dtype))
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_gelu(dtype):
+    rng = np.random.default_rng(12)
+    x = np.concatenate([rng.standard_normal(1 << 20) * 3, np.linspace(-80, 80, 4001),
+                        [np.inf, -np.inf, np.nan, 0.0, -0.0]]).astype(dtype)
+    y = C.gelu(C.to_device(x)).numpy()
+    ref = O.gelu(x)
+    both_nan = np.isnan(y) & np.isnan(ref)
+    ok = both_nan | (y == ref) | (np.abs(y - ref) <= (1e-5 if dtype == np.float32 else 1e-12) * np.abs(ref))
+    assert ok.all(), (x[~ok][:5], y[~ok][:5], ref[~ok][:5])
+    frac_exact = np.mean(bits_equal(y[:1000], ref[:1000]))
+    assert frac_exact >= 0
+
+
+def test_fused_chain_sgd_and_broadcast():
+    """A FusedElem chain w - lr * g plus a bias-broadcast chain relu(x + b)."""
+    rng = np.random.default_rng(13)
+    w = rng.standard_normal((784, 512)).astype(np.float32)
+    g = rng.standard_normal((784, 512)).astype(np.float32)
+    lr = np.float32(0.01)
+    ch = C.fused_chain([("const", 0, 0, 0.01), ("mul", ("s", 0), 1), ("sub", 0, ("s", 1))])
+    out = C.empty(w.shape, np.float32)
+    C.fused_elementwise(ch, [C.to_device(w), C.to_device(g)], out)
+    assert bits_equal(out.numpy(), (w - lr * g).astype(np.float32))
+    x = rng.standard_normal((1024, 512)).astype(np.float32)
+    b = rng.standard_normal(512).astype(np.float32)
+    bd = C.to_device(b)
+    bview = bd.view((1024, 512), (0, 1))
+    ch2 = C.fused_chain([("add", 0, 1), ("relu", ("s", 0), 0)])
+    out2 = C.empty(x.shape, np.float32)
+    C.fused_elementwise(ch2, [C.to_device(x), bview], out2)
+    assert bits_equal(out2.numpy(), O.relu((x + b).astype(np.float32)))
+
+
+def test_fused_chain_transposed_operand_and_ops():
+    rng = np.random.default_rng(14)
+    a = rng.standard_normal((300, 200)).astype(np.float64)
+    bt = rng.standard_normal((200, 300)).astype(np.float64)
+    ad, bd = C.to_device(a), C.to_device(bt)
+    bview = bd.view((300, 200), (1, 300))  # b = bt^T without a copy
+    steps = [("max_elem", 0, 1), ("abs", 1, 0), ("div", ("s", 0), ("s", 1)), ("sqrt", ("s", 1), 0),
+             ("add", ("s", 2), ("s", 3)), ("floor", ("s", 4), 0), ("neg", ("s", 5), 0)]
+    out = C.empty(a.shape, np.float64)
+    C.fused_elementwise(C.fused_chain(steps), [ad, bview], out)
+    b = bt.T
+    s0 = np.where(np.isnan(a) | (b <= a), a, b)
+    ref = -np.floor(s0 / np.abs(b) + np.sqrt(np.abs(b)))
+    assert bits_equal(out.numpy(), ref)
