@@ -73,6 +73,28 @@ def bench_softmax_f64(C, H, steps, warmup):
     return {"ms": ms, "bytes": nbytes, "gbps": nbytes / (ms * 1e-3) / 1e9}
 
 
+def bench_gemm(C, H, M, N, K, dtype, seeds, steps, warmup, reps=1):
+    """C = A.B with A, B ~ U(-1, 1); `reps` operand sets rotate when the
+    working set would otherwise sit in the 256 MB Infinity Cache."""
+    a = np.random.default_rng(seeds[0]).uniform(-1, 1, (M, K)).astype(dtype)
+    b = np.random.default_rng(seeds[1]).uniform(-1, 1, (K, N) if N > 1 else (K,)).astype(dtype)
+    sets = [(C.to_device(a), C.to_device(b)) for _ in range(reps)]
+    outs = [C.matmul(da, db) for da, db in sets]
+    ms = time_launches(C, H, lambda i: C.matmul(sets[i % reps][0], sets[i % reps][1], outs[i % reps]), steps, warmup)
+    isz = np.dtype(dtype).itemsize
+    nbytes = (M * K + K * N + M * N) * isz
+    flops = 2 * M * N * K
+    return {"ms": ms, "bytes": nbytes, "flops": flops, "gbps": nbytes / (ms * 1e-3) / 1e9,
+            "tflops": flops / (ms * 1e-3) / 1e12}
+
+
+def gemm_line(r, dt, bound):
+    line = {"ms": round(r["ms"], 5), "TFLOP/s": round(r["tflops"], 2), "GB/s": round(r["gbps"], 1),
+            "frac_mfma": round(r["tflops"] / PEAK_TFLOPS[dt], 4), "frac_hbm": round(r["gbps"] / HBM_PEAK_GBPS, 4),
+            "bound": bound}
+    return line
+
+
 def cpu_baseline_softmax(x: np.ndarray, budget_s: float = 10.0):
     from oracle import oracle as O
 
@@ -118,6 +140,15 @@ def main(argv=None) -> int:
         s64 = bench_softmax_f64(C, H, max(5, args.steps // 2), args.warmup)
         kernels["softmax_f64_4096x4096"] = {"ms": round(s64["ms"], 5), "GB/s": round(s64["gbps"], 1),
                                             "frac_hbm": round(s64["gbps"] / HBM_PEAK_GBPS, 4)}
+        gs = max(3, args.steps // 5)
+        kernels["gemm_f32_4096^3"] = gemm_line(bench_gemm(C, H, 4096, 4096, 4096, np.float32, (20, 21), gs, 2), "f32",
+                                               "mfma")
+        kernels["gemm_f64_4096^3"] = gemm_line(bench_gemm(C, H, 4096, 4096, 4096, np.float64, (22, 23), gs, 2), "f64",
+                                               "mfma")
+        kernels["skinny_f64_8192x64x4096"] = gemm_line(
+            bench_gemm(C, H, 8192, 64, 4096, np.float64, (24, 25), gs, 2, reps=2), "f64", "valu-tree")
+        kernels["gemv_f64_8192x8192"] = gemm_line(
+            bench_gemm(C, H, 8192, 1, 8192, np.float64, (26, 27), gs, 2, reps=2), "f64", "hbm")
     cpu = None if args.no_cpu else cpu_baseline_softmax(x)
     line = {
         "metric": METRIC,

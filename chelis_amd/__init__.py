@@ -113,6 +113,10 @@ SIGNATURES = {
     "chelis_hip_dropout": (c_int32, [c_uint64, P, c_double, P]),
     "chelis_hip_dropout_replay": (c_int32, [c_uint64, P, c_double, P]),
     "chelis_hip_uniform_like": (c_int32, [c_uint64, c_double, c_double, P]),
+    "chelis_hip_reduce": (c_int32, [c_int32, POINTER(FusedChain), POINTER(P), c_int32, c_int32, P]),
+    "chelis_hip_count": (c_int32, [P, c_int32, P, POINTER(c_int32)]),
+    "chelis_hip_matmul": (c_int32, [P, P, P, c_int32]),
+    "chelis_hip_linear": (c_int32, [P, P, P, c_int32, P, P, c_int32]),
 }
 
 _lib = None
@@ -331,3 +335,63 @@ def fused_elementwise(chain: FusedChain, inputs, out):
     arr = (P * max(1, len(inputs)))(*[_p(t) for t in inputs])
     check(lib().chelis_hip_fused_elementwise(ctypes.byref(chain), arr, len(inputs), _p(out)), "fused_elementwise")
     return out
+
+
+# ---- reductions ----
+REDUCE_OPS = {"sum": 0, "max": 2, "min": 3, "prod": 4, "argmax": 5, "argmin": 6}
+
+
+def reduce(op: str, inputs, axis: int, out=None, chain: FusedChain | None = None):
+    """chelis_hip_reduce over one axis; `chain` (with several inputs) is the
+    inlined FusedElem leaf, else inputs is one tensor."""
+    if not isinstance(inputs, (list, tuple)):
+        inputs = [inputs]
+    x0 = inputs[0]
+    ax = axis % len(x0.shape)
+    shape = x0.shape[:ax] + x0.shape[ax + 1:]
+    if out is None:
+        out = empty(shape, np.int64 if op in ("argmax", "argmin") else x0.dtype)
+    arr = (P * len(inputs))(*[_p(t) for t in inputs])
+    check(lib().chelis_hip_reduce(REDUCE_OPS[op], ctypes.byref(chain) if chain is not None else None, arr,
+                                  len(inputs), axis, _p(out)), f"reduce {op}")
+    return out
+
+
+def count(x, axis: int, out=None):
+    """chelis_hip_count: Bool8 -> i64; returns (out, error_code)."""
+    ax = axis % len(x.shape)
+    if out is None:
+        out = empty(x.shape[:ax] + x.shape[ax + 1:], np.int64)
+    err = c_int32(0)
+    check(lib().chelis_hip_count(_p(x), axis, _p(out), ctypes.byref(err)), "count")
+    return out, err.value
+
+
+# ---- matmul ----
+MATMUL_EXACT = 1
+ACT = {None: 0, "none": 0, "relu": 1, "gelu": 2}
+
+
+def _mm_shape(a, b):
+    lead_a, lead_b = a.shape[:-2], b.shape[:-2]
+    batch = tuple(np.broadcast_shapes(lead_a, lead_b)) if (lead_a or lead_b) else ()
+    m = (a.shape[-2],) if len(a.shape) > 1 else ()
+    n = (b.shape[-1],) if len(b.shape) > 1 else ()
+    return batch + m + n
+
+
+def matmul(a, b, c=None, exact: bool = False):
+    if c is None:
+        c = empty(_mm_shape(a, b), a.dtype)
+    check(lib().chelis_hip_matmul(_p(a), _p(b), _p(c), MATMUL_EXACT if exact else 0), "matmul")
+    return c
+
+
+def linear(a, b, bias=None, act=None, residual=None, c=None, exact: bool = False):
+    """c = act(a @ b + bias) + residual, fused in the matmul epilogue."""
+    if c is None:
+        c = empty(_mm_shape(a, b), a.dtype)
+    check(lib().chelis_hip_linear(_p(a), _p(b), _p(bias) if bias is not None else None, ACT[act],
+                                  _p(residual) if residual is not None else None, _p(c),
+                                  MATMUL_EXACT if exact else 0), "linear")
+    return c

@@ -71,7 +71,7 @@ CHELIS_HD inline float round_pos_dd_to_f32(double s, double e) {
     return (e > 0.0) ? (float)hi : (float)(fd + gd - hi);
 }
 
-// Correctly rounded binary32 exp.
+// Correctly rounded binary32 exp, double-double core (any input).
 //
 // x = k ln2/64 + r with k = rint(x * 64/ln2), |r| <= ln2/128; the reduction
 // x - k*HI is exact (HI has 39 significant bits, |k| < 2^14, and Sterbenz
@@ -82,7 +82,7 @@ CHELIS_HD inline float round_pos_dd_to_f32(double s, double e) {
 // unevaluated double-double whose error is about 2^-66 relative, then
 // rounded once to binary32 by round_pos_dd_to_f32. Checked against the
 // CORE-MATH oracle over every binary32 input (tests/test_devmath.py).
-CHELIS_HD inline float expf_cr(float xf) {
+CHELIS_HD inline float expf_cr_dd(float xf) {
     if (xf != xf) return f32_from(0x7fc00000u);
     if (xf > 89.0f) return f32_from(0x7f800000u);
     if (xf < -104.0f) return 0.0f;
@@ -110,6 +110,43 @@ CHELIS_HD inline float expf_cr(float xf) {
     const double s = s1 + low;
     const double e = (s1 - s) + low;
     return round_pos_dd_to_f32(ldexp(s, m), ldexp(e, m));
+}
+
+// Correctly rounded binary32 exp, fast path first.
+//
+// For -87 < x < 88 the result is a normal binary32. x = k ln2 + r with
+// k = rint(x / ln2), |r| <= ln2/2 + 2^-40 (two fma steps against a
+// double-double ln2), and exp(r) is the degree-11 Taylor polynomial in
+// Horner form: truncation below r^12/12! < 2^-47, rounding about 2^-51, so
+// y = 2^k p(r) is within 2^-46 relative, under 2^7 units in the last place
+// of the double y. (float)y is then the correctly rounded result unless the
+// exact value may lie on the other side of a binary32 rounding midpoint,
+// i.e. unless the 29 bits below binary32 precision in y are within 2^11
+// units of the midpoint pattern 1 << 28; those inputs (about one in 2^17),
+// the out-of-range ones and NaN take expf_cr_dd. Checked against the
+// CORE-MATH oracle over every binary32 input (tests/test_devmath.py).
+CHELIS_HD inline float expf_cr(float xf) {
+    if (!(xf > -87.0f && xf < 88.0f)) return expf_cr_dd(xf);
+    const double x = (double)xf;
+    const double kd = rint(x * 0x1.71547652b82fep+0);
+    double r = fma(-kd, 0x1.62e42fefa39efp-1, x);
+    r = fma(-kd, 0x1.abc9e3b39803fp-56, r);
+    double p = 0x1.ae64567f544e4p-26;
+    p = fma(p, r, 0x1.27e4fb7789f5cp-22);
+    p = fma(p, r, 0x1.71de3a556c734p-19);
+    p = fma(p, r, 0x1.a01a01a01a01ap-16);
+    p = fma(p, r, 0x1.a01a01a01a01ap-13);
+    p = fma(p, r, 0x1.6c16c16c16c17p-10);
+    p = fma(p, r, 0x1.1111111111111p-7);
+    p = fma(p, r, 0x1.5555555555555p-5);
+    p = fma(p, r, 0x1.5555555555555p-3);
+    p = fma(p, r, 0x1.0000000000000p-1);
+    p = fma(p, r, 1.0);
+    p = fma(p, r, 1.0);
+    const double y = ldexp(p, (int)kd);
+    const int64_t below = (int64_t)(f64_bits(y) & ((1ull << 29) - 1)) - (int64_t(1) << 28);
+    if (below > -2048 && below < 2048) return expf_cr_dd(xf);
+    return (float)y;
 }
 
 }  // namespace chelis

@@ -1,0 +1,46 @@
+// Internal interface between the matmul entry points (k_gemm.hip) and the
+// kernel families that serve them: the MFMA tile kernels (k_gemm.hip) and
+// the canonical-tree kernels (k_gemm_exact.hip).
+#pragma once
+
+#include "chain.h"
+
+namespace chelis {
+
+// One contraction c[z][m][n] = sum_k a[z][m][k] * b[z][k][n] over a batch of
+// up to two axes (z = z0 * nb1 + z1). Strides are in elements; every view
+// is already validated against its byte capacity on the host.
+struct GemmProblem {
+    const void *a, *b;
+    void *c;
+    int64_t M, N, K;
+    int64_t sam, sak, sbk, sbn, scm, scn;
+    int64_t nb0, nb1;                       // batch extents (1 when absent)
+    int64_t sa0, sa1, sb0, sb1, sc0, sc1;   // batch strides
+    // fused epilogue (graph order): v = mm; v = v + bias[n]; act; v = resid + v
+    const void *bias;
+    int64_t sbias;
+    int32_t act;
+    const void *resid;
+    int64_t srm, srn, sr0, sr1;
+};
+
+// Epilogue of one output element, each step finalized at the dtype so the
+// bits equal the unfused graph's (mm, add bias, relu/gelu, add residual).
+template <typename T>
+__device__ inline T gemm_epilogue(T acc, const GemmProblem &p, int64_t z0, int64_t z1, int64_t m, int64_t n) {
+    T v = canon(acc);
+    if (p.bias) v = canon(v + static_cast<const T *>(p.bias)[n * p.sbias]);
+    if (p.act == CHELIS_ACT_RELU) v = v < T(0) ? T(0) : v;
+    else if (p.act == CHELIS_ACT_GELU) v = gelu_one<T>(v);
+    if (p.resid) v = canon(static_cast<const T *>(p.resid)[z0 * p.sr0 + z1 * p.sr1 + m * p.srm + n * p.srn] + v);
+    return v;
+}
+
+int32_t gemm_mfma(chelis_dtype dt, const GemmProblem &p, hipStream_t st);
+// Canonical-tree kernels: bit-exact with the [05-OP-30] matmul.
+int32_t gemm_tree_wave(chelis_dtype dt, const GemmProblem &p, hipStream_t st);    // one wave per output
+int32_t gemm_tree_tiled(chelis_dtype dt, const GemmProblem &p, hipStream_t st);   // narrow N, long K
+int32_t gemm_tree_thread(chelis_dtype dt, const GemmProblem &p, hipStream_t st);  // short K
+
+}  // namespace chelis

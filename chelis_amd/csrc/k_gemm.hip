@@ -1,0 +1,302 @@
+// Dense matmul on the CDNA4 matrix cores, and the matmul / linear entry
+// points with their shape dispatch.
+//
+// MFMA tile kernel. A 256-thread workgroup (4 waves, 2 x 2) owns a 128 x 128
+// tile of C; each wave owns 64 x 64 = 4 x 4 blocks of 16 x 16, accumulated
+// by v_mfma_f32_16x16x4_f32 (f32) or v_mfma_f64_16x16x4_f64 (f64). K moves
+// in steps of BK (16 for f32, 8 for f64) through two LDS buffers: while the
+// matrix cores consume one buffer, the next A and B tiles are already in
+// flight from HBM into registers and land in the other buffer after the
+// step, so there is one barrier per K step.
+//
+// LDS holds both operands K-contiguous (As[m][k], Bs[n][k]) with the row
+// padded to 80 bytes. An MFMA of shape 16x16x4 takes A[i][q] from lane
+// q*16 + i and B[q][j] from lane q*16 + j, and returns C[i][j] in lane
+// q*16 + j, item r, with i = 4q + r for f32 and i = q + 4r for f64 (both
+// checked on gfx950 with a one-wave layout probe). Over the KV = BK/4 MFMAs of one
+// step, lane group q supplies k = q*KV + t for MFMA t, so both fragments of
+// a lane are KV consecutive k values: one 16-byte LDS read each, and the
+// 80-byte row pitch puts the 8 rows a read phase touches on 8 disjoint
+// 4-bank groups.
+//
+// Operands are strided views (a transposed operand is a stride swap):
+// each one is staged with 16-byte vector loads along whichever of its axes
+// is contiguous (K or the outer axis), or element by element when neither
+// is.
+//
+// Blocks are numbered so that each of the 8 XCDs (workgroups are dealt to
+// XCDs round-robin) receives one contiguous run of tiles, walked in groups
+// of 8 tile-rows, so the A row-panels and B column-panels a tile reads are
+// shared inside that XCD's L2.
+#include "gemm.h"
+
+namespace chelis {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+struct Mfma;
+template <>
+struct Mfma<float> {
+    using acc_t = f32x4;
+    static constexpr int BK = 16, LD = 20, V = 4;
+    // accumulator item r of lane group q holds row 4q + r of the 16x16 block
+    __device__ static int row(int q, int r) { return 4 * q + r; }
+    __device__ static acc_t step(float a, float b, acc_t c) {
+        return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+    }
+};
+template <>
+struct Mfma<double> {
+    using acc_t = f64x4;
+    static constexpr int BK = 8, LD = 10, V = 2;
+    // accumulator item r of lane group q holds row q + 4r of the 16x16 block
+    __device__ static int row(int q, int r) { return q + 4 * r; }
+    __device__ static acc_t step(double a, double b, acc_t c) {
+        return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+    }
+};
+
+constexpr int BM = 128, BN = 128, THREADS = 256;
+
+template <typename T>
+struct Vec16;
+template <>
+struct Vec16<float> {
+    using type = float4;
+};
+template <>
+struct Vec16<double> {
+    using type = double2;
+};
+
+// Layout of a staged operand: 0 = vectors along K, 1 = vectors along the
+// outer axis (M of A, N of B), 2 = element by element.
+template <typename T, int LAY, int ROWS>
+struct Stage {
+    static constexpr int BK = Mfma<T>::BK, V = Mfma<T>::V, LD = Mfma<T>::LD;
+    static constexpr int NE = ROWS * BK / THREADS;  // elements per thread
+    static constexpr int NV = NE / V;               // vectors per thread
+    T r[NE];
+
+    // element (row, k) lives at base[row * s_row + k * s_k]
+    __device__ void load(const T *__restrict__ base, int64_t s_row, int64_t s_k, int64_t row0, int64_t rows,
+                         int64_t k0, int64_t K, bool vec_ok) {
+        const int t = threadIdx.x;
+        if constexpr (LAY == 0) {
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const int idx = t + THREADS * j;
+                const int row = idx / (BK / V), kv = (idx % (BK / V)) * V;
+                const int64_t gr = row0 + row, gk = k0 + kv;
+                const T *p = base + gr * s_row + gk;
+                if (vec_ok && gr < rows && gk + V <= K) {
+                    typename Vec16<T>::type q = *reinterpret_cast<const typename Vec16<T>::type *>(p);
+                    const T *qe = reinterpret_cast<const T *>(&q);
+#pragma unroll
+                    for (int u = 0; u < V; ++u) r[j * V + u] = qe[u];
+                } else {
+#pragma unroll
+                    for (int u = 0; u < V; ++u) r[j * V + u] = (gr < rows && gk + u < K) ? p[u] : T(0);
+                }
+            }
+        } else if constexpr (LAY == 1) {
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const int idx = t + THREADS * j;
+                const int k = idx / (ROWS / V), rv = (idx % (ROWS / V)) * V;
+                const int64_t gr = row0 + rv, gk = k0 + k;
+                const T *p = base + gr + gk * s_k;
+                if (vec_ok && gk < K && gr + V <= rows) {
+                    typename Vec16<T>::type q = *reinterpret_cast<const typename Vec16<T>::type *>(p);
+                    const T *qe = reinterpret_cast<const T *>(&q);
+#pragma unroll
+                    for (int u = 0; u < V; ++u) r[j * V + u] = qe[u];
+                } else {
+#pragma unroll
+                    for (int u = 0; u < V; ++u) r[j * V + u] = (gk < K && gr + u < rows) ? p[u] : T(0);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < NE; ++j) {
+                const int idx = t + THREADS * j;
+                const int row = idx / BK, k = idx % BK;
+                const int64_t gr = row0 + row, gk = k0 + k;
+                r[j] = (gr < rows && gk < K) ? base[gr * s_row + gk * s_k] : T(0);
+            }
+        }
+    }
+
+    __device__ void store(T *__restrict__ s) const {
+        const int t = threadIdx.x;
+        if constexpr (LAY == 0) {
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const int idx = t + THREADS * j;
+                const int row = idx / (BK / V), kv = (idx % (BK / V)) * V;
+                typename Vec16<T>::type q;
+                T *qe = reinterpret_cast<T *>(&q);
+#pragma unroll
+                for (int u = 0; u < V; ++u) qe[u] = r[j * V + u];
+                *reinterpret_cast<typename Vec16<T>::type *>(s + row * LD + kv) = q;
+            }
+        } else if constexpr (LAY == 1) {
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const int idx = t + THREADS * j;
+                const int k = idx / (ROWS / V), rv = (idx % (ROWS / V)) * V;
+#pragma unroll
+                for (int u = 0; u < V; ++u) s[(rv + u) * LD + k] = r[j * V + u];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < NE; ++j) {
+                const int idx = t + THREADS * j;
+                s[(idx / BK) * LD + idx % BK] = r[j];
+            }
+        }
+    }
+};
+
+template <typename T, int ALAY, int BLAY>
+__global__ __launch_bounds__(THREADS) void gemm_mfma_kernel(GemmProblem p, int64_t tiles_m, int64_t tiles_n,
+                                                            bool a_vec, bool b_vec) {
+    using M = Mfma<T>;
+    using acc_t = typename M::acc_t;
+    constexpr int BK = M::BK, LD = M::LD, KV = BK / 4;
+    __shared__ __attribute__((aligned(16))) T As[2][BM * LD];
+    __shared__ __attribute__((aligned(16))) T Bs[2][BN * LD];
+
+    // XCD-aware tile order.
+    const int64_t tiles = tiles_m * tiles_n;
+    int64_t bid = blockIdx.x;
+    if (tiles % 8 == 0) bid = (bid % 8) * (tiles / 8) + bid / 8;
+    constexpr int64_t GM = 8;
+    const int64_t group = bid / (GM * tiles_n);
+    const int64_t first = group * GM;
+    const int64_t gsz = (tiles_m - first) < GM ? (tiles_m - first) : GM;
+    const int64_t in_group = bid % (GM * tiles_n);
+    const int64_t m0 = (first + in_group % gsz) * BM;
+    const int64_t n0 = (in_group / gsz) * BN;
+
+    const int64_t z = blockIdx.y;
+    const int64_t z0 = z / p.nb1, z1 = z % p.nb1;
+    const T *A = static_cast<const T *>(p.a) + z0 * p.sa0 + z1 * p.sa1;
+    const T *B = static_cast<const T *>(p.b) + z0 * p.sb0 + z1 * p.sb1;
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int fr = lane & 15, fq = lane >> 4;
+
+    acc_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = acc_t{};
+
+    Stage<T, ALAY, BM> sa;
+    Stage<T, BLAY, BN> sb;
+    const int64_t ksteps = (p.K + BK - 1) / BK;
+    sa.load(A, p.sam, p.sak, m0, p.M, 0, p.K, a_vec);
+    sb.load(B, p.sbn, p.sbk, n0, p.N, 0, p.K, b_vec);
+    sa.store(As[0]);
+    sb.store(Bs[0]);
+    __syncthreads();
+
+    for (int64_t ks = 0; ks < ksteps; ++ks) {
+        const int buf = ks & 1;
+        const bool more = ks + 1 < ksteps;
+        if (more) {
+            sa.load(A, p.sam, p.sak, m0, p.M, (ks + 1) * BK, p.K, a_vec);
+            sb.load(B, p.sbn, p.sbk, n0, p.N, (ks + 1) * BK, p.K, b_vec);
+        }
+        typename Vec16<T>::type af[4], bf[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            af[i] = *reinterpret_cast<const typename Vec16<T>::type *>(&As[buf][(wm * 64 + i * 16 + fr) * LD + fq * KV]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            bf[j] = *reinterpret_cast<const typename Vec16<T>::type *>(&Bs[buf][(wn * 64 + j * 16 + fr) * LD + fq * KV]);
+#pragma unroll
+        for (int t = 0; t < KV; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = M::step(reinterpret_cast<const T *>(&af[i])[t], reinterpret_cast<const T *>(&bf[j])[t],
+                                        acc[i][j]);
+        if (more) {
+            sa.store(As[buf ^ 1]);
+            sb.store(Bs[buf ^ 1]);
+        }
+        __syncthreads();
+    }
+
+    T *C = static_cast<T *>(p.c) + z0 * p.sc0 + z1 * p.sc1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t m = m0 + wm * 64 + i * 16 + M::row(fq, r);
+                const int64_t n = n0 + wn * 64 + j * 16 + fr;
+                if (m < p.M && n < p.N) C[m * p.scm + n * p.scn] = gemm_epilogue<T>(acc[i][j][r], p, z0, z1, m, n);
+            }
+}
+
+template <typename T>
+int lay_of(int64_t s_outer, int64_t s_k, const void *base, int64_t outer, int64_t K, bool *vec_ok) {
+    constexpr int V = Mfma<T>::V;
+    const bool al = (reinterpret_cast<uintptr_t>(base) & 15u) == 0;
+    if (s_k == 1 || K == 1) {
+        *vec_ok = al && (outer == 1 || s_outer % V == 0);
+        return 0;
+    }
+    if (s_outer == 1 || outer == 1) {
+        *vec_ok = al && s_k % V == 0;
+        return 1;
+    }
+    *vec_ok = false;
+    return 2;
+}
+
+template <typename T, int AL, int BL>
+void launch_mfma(const GemmProblem &p, dim3 grid, int64_t tm, int64_t tn, bool av, bool bv, hipStream_t st) {
+    gemm_mfma_kernel<T, AL, BL><<<grid, THREADS, 0, st>>>(p, tm, tn, av, bv);
+}
+
+template <typename T>
+int32_t run_mfma(const GemmProblem &p, hipStream_t st) {
+    bool av = false, bv = false;
+    const int al = lay_of<T>(p.sam, p.sak, p.a, p.M, p.K, &av);
+    const int bl = lay_of<T>(p.sbn, p.sbk, p.b, p.N, p.K, &bv);
+    const int64_t tm = (p.M + BM - 1) / BM, tn = (p.N + BN - 1) / BN;
+    const int64_t nz = p.nb0 * p.nb1;
+    if (tm * tn > 0x7fffffffLL || nz > 65535) return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: grid too large");
+    const dim3 grid((unsigned)(tm * tn), (unsigned)nz);
+    switch (al * 3 + bl) {
+        case 0: launch_mfma<T, 0, 0>(p, grid, tm, tn, av, bv, st); break;
+        case 1: launch_mfma<T, 0, 1>(p, grid, tm, tn, av, bv, st); break;
+        case 2: launch_mfma<T, 0, 2>(p, grid, tm, tn, av, bv, st); break;
+        case 3: launch_mfma<T, 1, 0>(p, grid, tm, tn, av, bv, st); break;
+        case 4: launch_mfma<T, 1, 1>(p, grid, tm, tn, av, bv, st); break;
+        case 5: launch_mfma<T, 1, 2>(p, grid, tm, tn, av, bv, st); break;
+        case 6: launch_mfma<T, 2, 0>(p, grid, tm, tn, av, bv, st); break;
+        case 7: launch_mfma<T, 2, 1>(p, grid, tm, tn, av, bv, st); break;
+        default: launch_mfma<T, 2, 2>(p, grid, tm, tn, av, bv, st); break;
+    }
+    CHELIS_LAUNCH_CHECK();
+    return CHELIS_HIP_OK;
+}
+
+}  // namespace
+
+int32_t gemm_mfma(chelis_dtype dt, const GemmProblem &p, hipStream_t st) {
+    return dt == CHELIS_DTYPE_F32 ? run_mfma<float>(p, st) : run_mfma<double>(p, st);
+}
+
+}  // namespace chelis

@@ -1,0 +1,177 @@
+// chelis_hip_matmul / chelis_hip_linear: validate the packets, reduce them
+// to one GemmProblem and pick the kernel family.
+//
+// Dispatch (the reference sends every BlasMatmul to hipBLAS,
+// crates/chelis-backend-hip/src/emit.rs:4718-4842):
+//   K <= 32                      -> tree_thread (short K, bit-exact)
+//   M == 1 or N == 1             -> tree_wave   (GEMV, HBM bound, bit-exact)
+//   CHELIS_MATMUL_EXACT          -> tree_tiled  (bit-exact, any shape)
+//   min(M, N) < 16, or f64 with min(M, N) <= 64
+//                                -> tree_tiled  (skinny, bit-exact)
+//   otherwise                    -> MFMA tiles  (dense; rounding differs
+//                                   from the canonical tree)
+#include "gemm.h"
+
+#include <algorithm>
+#include <atomic>
+
+#include "chelis_programs.h"
+
+namespace chelis {
+namespace {
+
+std::atomic<int32_t> g_exact{0};
+
+struct Mat {
+    int64_t rows, cols, srow, scol;  // the trailing 2-D view
+    int32_t nbatch;                  // leading axes (<= 2)
+    int64_t bext[2], bstr[2];
+};
+
+// View a packet as [batch..., rows, cols]; a rank-1 operand is a row
+// (as_row) or a column.
+bool as_mat(const chelis_gpu_tensor *t, bool as_row, Mat *m) {
+    *m = Mat{};
+    if (t->rank < 1) return false;
+    if (t->rank == 1) {
+        if (as_row) {
+            m->rows = 1, m->cols = t->shape[0], m->srow = 0, m->scol = t->strides[0];
+        } else {
+            m->rows = t->shape[0], m->cols = 1, m->srow = t->strides[0], m->scol = 0;
+        }
+        m->nbatch = 0;
+        return true;
+    }
+    const int32_t r = t->rank;
+    m->rows = t->shape[r - 2], m->cols = t->shape[r - 1];
+    m->srow = t->strides[r - 2], m->scol = t->strides[r - 1];
+    m->nbatch = r - 2;
+    if (m->nbatch > 2) return false;
+    for (int32_t i = 0; i < m->nbatch; ++i) m->bext[i] = t->shape[i], m->bstr[i] = t->strides[i];
+    return true;
+}
+
+// Distinct indices of a view must address distinct elements (no write races).
+bool non_overlapping(const chelis_gpu_tensor *t) {
+    int32_t idx[8];
+    int32_t n = 0;
+    for (int32_t a = 0; a < t->rank; ++a)
+        if (t->shape[a] > 1) idx[n++] = a;
+    std::sort(idx, idx + n, [&](int32_t x, int32_t y) { return t->strides[x] < t->strides[y]; });
+    int64_t span = 1;
+    for (int32_t i = 0; i < n; ++i) {
+        const int64_t s = t->strides[idx[i]];
+        if (s < span) return false;
+        span = s * t->shape[idx[i]];
+    }
+    return true;
+}
+
+int32_t build_problem(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b, const chelis_gpu_tensor *c,
+                      GemmProblem *p, const char *what) {
+    int32_t s;
+    if ((s = check_tensor(a, "a")) || (s = check_tensor(b, "b")) || (s = check_tensor(c, "c"))) return s;
+    if (!is_float(a->dtype) || a->dtype != b->dtype || a->dtype != c->dtype)
+        return set_error(CHELIS_HIP_EDOMAIN, "%s: a, b and c must share an f32 or f64 dtype", what);
+    Mat ma, mb, mc;
+    if (!as_mat(a, true, &ma) || !as_mat(b, false, &mb))
+        return set_error(CHELIS_HIP_EUNSUPPORTED, "%s: operands need rank 1..4", what);
+    if (ma.cols != mb.rows)
+        return set_error(CHELIS_HIP_EDOMAIN, "%s: contraction extents differ (%lld vs %lld)", what,
+                         (long long)ma.cols, (long long)mb.rows);
+    // expected result shape: broadcast batch, then [M] [N] (dropped for rank-1 operands)
+    const int32_t nb = std::max(ma.nbatch, mb.nbatch);
+    int64_t bext[2] = {1, 1}, sa[2] = {0, 0}, sb[2] = {0, 0};
+    for (int32_t i = 0; i < nb; ++i) {
+        const int32_t ia = i - (nb - ma.nbatch), ib = i - (nb - mb.nbatch);
+        const int64_t ea = ia >= 0 ? ma.bext[ia] : 1, eb = ib >= 0 ? mb.bext[ib] : 1;
+        if (ea != eb && ea != 1 && eb != 1) return set_error(CHELIS_HIP_EDOMAIN, "%s: batch axes do not broadcast", what);
+        bext[2 - nb + i] = std::max(ea, eb);
+        sa[2 - nb + i] = (ia >= 0 && ea != 1) ? ma.bstr[ia] : 0;
+        sb[2 - nb + i] = (ib >= 0 && eb != 1) ? mb.bstr[ib] : 0;
+    }
+    int64_t want[8];
+    int32_t wr = 0;
+    for (int32_t i = 0; i < nb; ++i) want[wr++] = bext[2 - nb + i];
+    if (a->rank > 1) want[wr++] = ma.rows;
+    if (b->rank > 1) want[wr++] = mb.cols;
+    if (c->rank != wr) return set_error(CHELIS_HIP_EDOMAIN, "%s: result rank %d, expected %d", what, c->rank, wr);
+    for (int32_t i = 0; i < wr; ++i)
+        if (c->shape[i] != want[i]) return set_error(CHELIS_HIP_EDOMAIN, "%s: result axis %d has the wrong extent", what, i);
+    if (!non_overlapping(c)) return set_error(CHELIS_HIP_EDOMAIN, "%s: result view overlaps itself", what);
+    // result strides per role
+    int64_t scm = 0, scn = 0, sc[2] = {0, 0};
+    {
+        int32_t ax = 0;
+        for (int32_t i = 0; i < nb; ++i) sc[2 - nb + i] = c->strides[ax++];
+        if (a->rank > 1) scm = c->strides[ax++];
+        if (b->rank > 1) scn = c->strides[ax++];
+    }
+    *p = GemmProblem{};
+    p->a = a->data, p->b = b->data, p->c = c->data;
+    p->M = ma.rows, p->N = mb.cols, p->K = ma.cols;
+    p->sam = ma.srow, p->sak = ma.scol, p->sbk = mb.srow, p->sbn = mb.scol, p->scm = scm, p->scn = scn;
+    p->nb0 = bext[0], p->nb1 = bext[1];
+    p->sa0 = sa[0], p->sa1 = sa[1], p->sb0 = sb[0], p->sb1 = sb[1], p->sc0 = sc[0], p->sc1 = sc[1];
+    // collapse one batch axis when strides allow (more blocks per launch row)
+    return CHELIS_HIP_OK;
+}
+
+int32_t dispatch(chelis_dtype dt, const GemmProblem &p, int32_t flags) {
+    hipStream_t st = stream();
+    if (!st) return set_error(CHELIS_HIP_EHIP, "no HIP device");
+    if (p.M == 0 || p.N == 0 || p.nb0 == 0 || p.nb1 == 0) return CHELIS_HIP_OK;
+    if (g_exact.load(std::memory_order_relaxed)) flags |= CHELIS_MATMUL_EXACT;
+    const bool f64 = dt == CHELIS_DTYPE_F64;
+    const int64_t narrow = std::min(p.M, p.N);
+    if (p.K <= 32) return gemm_tree_thread(dt, p, st);
+    if (p.M == 1 || p.N == 1) return gemm_tree_wave(dt, p, st);
+    if ((flags & CHELIS_MATMUL_EXACT) || narrow < 16 || (f64 && narrow <= 64)) return gemm_tree_tiled(dt, p, st);
+    return gemm_mfma(dt, p, st);
+}
+
+}  // namespace
+}  // namespace chelis
+
+using namespace chelis;
+
+extern "C" int32_t chelis_hip_set_exact_matmul(int32_t on) { return g_exact.exchange(on ? 1 : 0); }
+
+extern "C" int32_t chelis_hip_matmul(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b,
+                                     const chelis_gpu_tensor *c, int32_t flags) {
+    GemmProblem p;
+    if (int32_t s = build_problem(a, b, c, &p, "matmul")) return s;
+    if (flags & ~CHELIS_MATMUL_EXACT) return set_error(CHELIS_HIP_EDOMAIN, "matmul: unknown flags %d", flags);
+    return dispatch(a->dtype, p, flags);
+}
+
+extern "C" int32_t chelis_hip_linear(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b,
+                                     const chelis_gpu_tensor *bias, int32_t activation,
+                                     const chelis_gpu_tensor *residual, const chelis_gpu_tensor *c, int32_t flags) {
+    GemmProblem p;
+    if (int32_t s = build_problem(a, b, c, &p, "linear")) return s;
+    if (flags & ~CHELIS_MATMUL_EXACT) return set_error(CHELIS_HIP_EDOMAIN, "linear: unknown flags %d", flags);
+    if (activation < CHELIS_ACT_NONE || activation > CHELIS_ACT_GELU)
+        return set_error(CHELIS_HIP_EDOMAIN, "linear: unknown activation %d", activation);
+    if (a->rank < 2 || b->rank != 2) return set_error(CHELIS_HIP_EDOMAIN, "linear: a needs rank >= 2 and b rank 2");
+    p.act = activation;
+    if (bias) {
+        if (int32_t s = check_tensor(bias, "bias")) return s;
+        if (bias->dtype != a->dtype || bias->rank != 1 || bias->shape[0] != p.N)
+            return set_error(CHELIS_HIP_EDOMAIN, "linear: bias must be [N] of the operand dtype");
+        p.bias = bias->data;
+        p.sbias = bias->strides[0];
+    }
+    if (residual) {
+        if (int32_t s = check_tensor(residual, "residual")) return s;
+        if (residual->dtype != a->dtype || !same_shape(residual, c))
+            return set_error(CHELIS_HIP_EDOMAIN, "linear: residual must match the result");
+        const int32_t r = residual->rank;
+        p.resid = residual->data;
+        p.srm = residual->strides[r - 2];
+        p.srn = residual->strides[r - 1];
+        p.sr0 = r >= 4 ? residual->strides[r - 4] : 0;
+        p.sr1 = r >= 3 ? residual->strides[r - 3] : 0;
+    }
+    return dispatch(a->dtype, p, flags);
+}

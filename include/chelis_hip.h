@@ -134,10 +134,13 @@ int32_t chelis_hip_relu_adjoint(const chelis_gpu_tensor *x, const chelis_gpu_ten
 /* ---- matmul dispatch (BlasMatmul, dag.rs:1338-1352; hipBLAS wrappers
  * chelis_hip_runtime.h:48-404) ----
  * c[..., M, N] = a[..., M, K] . b[..., K, N] with any element strides on a
- * and b (a transposed operand is a stride swap, never a copy; batch axes
- * broadcast by stride 0) and c contiguous. Dense shapes run on MFMA
- * (v_mfma_f32_16x16x4_f32 / v_mfma_f64_16x16x4_f64), GEMV and skinny shapes
- * on bandwidth kernels whose K sum is the canonical tree (bit-exact).
+ * and b (a transposed operand is a stride swap, never a copy; up to two
+ * batch axes broadcast numpy-style, an extent-1 axis by stride 0; a rank-1
+ * a is a row [1, K] and a rank-1 b a column [K, 1], their axis dropped from
+ * c) and c any non-overlapping view. Dense shapes run on MFMA
+ * (v_mfma_f32_16x16x4_f32 / v_mfma_f64_16x16x4_f64); short K (<= 32), GEMV
+ * (M or N == 1) and skinny shapes (min(M, N) < 16, or <= 64 in f64) run on
+ * VALU kernels whose K sum is the canonical tree, bit-exact with the C lane.
  * `flags` = CHELIS_MATMUL_EXACT forces the canonical-tree kernels on every
  * shape. */
 #define CHELIS_MATMUL_EXACT 1

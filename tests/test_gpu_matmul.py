@@ -1,0 +1,210 @@
+"""GPU parity of the matmul dispatch against the C oracle's canonical-tree
+matmul (crates/chelis-backend-c/src/emit.rs:8431-8560).
+
+Bar: the canonical-tree kernels (short K, GEMV, skinny, and every shape
+under the exact flag) are bit-exact; the MFMA tile kernels differ from the
+tree by rounding only and must stay within the north star's tolerances:
+normwise ||c - ref||_inf / ||ref||_inf <= 1e-5 for f32 and <= 1e-10 for f64,
+and the same bound elementwise relative wherever |ref| >= rms(ref) (below
+that, cancellation makes the relative error of any summation order grow as
+rms/|ref|; the normwise bound covers those entries).
+"""
+import numpy as np
+import pytest
+
+import chelis_amd as C
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+TOL = {np.float32: 1e-5, np.float64: 1e-10}
+
+
+def setup_module(_m):
+    O.build()
+
+
+def bits_equal(a, b):
+    return np.array_equal(np.ascontiguousarray(a).view(np.uint8), np.ascontiguousarray(b).view(np.uint8))
+
+
+def first_diff(a, b):
+    bad = np.argwhere(~((a == b) | (np.isnan(a) & np.isnan(b))))
+    return f"{len(bad)} differ; first {bad[:3].tolist()}"
+
+
+def dev_view(host_full, rows, cols, transposed):
+    """(device tensor keeping storage alive, device view, numpy view) of a
+    rows x cols operand, stored transposed when asked."""
+    if transposed:
+        base = np.ascontiguousarray(host_full.T)
+        d = C.to_device(base)
+        return d, d.view((rows, cols), (1, rows)), base.T
+    d = C.to_device(np.ascontiguousarray(host_full))
+    return d, d, host_full
+
+
+def rand(rng, shape, dtype):
+    return rng.uniform(-1, 1, shape).astype(dtype)
+
+
+def check_close(c, ref, dtype):
+    tol = TOL[dtype]
+    scale = np.abs(ref).max()
+    assert np.abs(c - ref).max() <= tol * scale, ("normwise", np.abs(c - ref).max() / scale)
+    rms = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
+    big = np.abs(ref) >= rms
+    rel = np.abs(c - ref)[big] / np.abs(ref)[big]
+    assert rel.max() <= tol, ("elementwise", rel.max())
+
+
+TREE_CASES = [
+    # (M, N, K, a transposed, b transposed) - family chosen by the dispatch
+    (37, 50, 1, False, False),      # short K
+    (64, 33, 17, True, False),      # short K
+    (128, 512, 10, False, True),    # short K (the MLP's g_z2 . W2^T form)
+    (300, 1, 1000, False, False),   # GEMV
+    (300, 1, 1000, True, False),    # GEMV, transposed A (linreg X^T r form)
+    (1, 257, 4097, False, False),   # row vector times matrix
+    (100, 10, 3000, False, False),  # skinny (the MLP's d . W2 form)
+    (512, 10, 1024, True, False),   # skinny, transposed A (d^T . g_z2)
+    (50, 13, 513, False, True),     # skinny, transposed B
+]
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("case", TREE_CASES)
+def test_tree_kernels_bit_exact(case, dtype):
+    M, N, K, ta, tb = case
+    rng = np.random.default_rng(M * 7 + N * 3 + K)
+    a, b = rand(rng, (M, K), dtype), rand(rng, (K, N), dtype)
+    _da, va, na = dev_view(a, M, K, ta)
+    _db, vb, nb = dev_view(b, K, N, tb)
+    c = C.matmul(va, vb).numpy()
+    ref = O.matmul(na, nb)
+    assert bits_equal(c, ref), first_diff(c, ref)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_exact_flag_on_dense_shape(dtype):
+    rng = np.random.default_rng(21)
+    a, b = rand(rng, (200, 300), dtype), rand(rng, (300, 130), dtype)
+    c = C.matmul(C.to_device(a), C.to_device(b), exact=True).numpy()
+    assert bits_equal(c, O.matmul(a, b))
+
+
+def test_f64_skinny_band_is_exact():
+    """f64 with min(M, N) <= 64 stays on the canonical tree."""
+    rng = np.random.default_rng(22)
+    a, b = rand(rng, (700, 900), np.float64), rand(rng, (900, 64), np.float64)
+    c = C.matmul(C.to_device(a), C.to_device(b)).numpy()
+    assert bits_equal(c, O.matmul(a, b))
+
+
+def test_empty_contraction_is_positive_zero():
+    a = C.empty((5, 0), np.float32)
+    b = C.empty((0, 7), np.float32)
+    c = C.matmul(a, b).numpy()
+    assert c.shape == (5, 7) and bits_equal(c, np.zeros((5, 7), np.float32))
+
+
+def test_special_values_tree():
+    """Signed zeros, infinities, NaN and cancellation through the exact tree."""
+    a = np.array([[1e8, 1.0, -1e8, 1.0], [-0.0, -0.0, -0.0, -0.0], [np.inf, 1.0, -np.inf, 0.0],
+                  [np.nan, 0.0, 0.0, 0.0], [1e-38, 1e-38, -1e-38, 1e-45]], np.float32)
+    b = np.array([[1.0], [1.0], [1.0], [1.0]], np.float32)
+    c = C.matmul(C.to_device(a), C.to_device(b)).numpy()
+    ref = O.matmul(a, b)
+    assert bits_equal(c, ref), (c.ravel(), ref.ravel())
+
+
+def test_config_3d_gemv_bit_exact():
+    rng = np.random.default_rng(26)
+    A = rng.uniform(-1, 1, (8192, 8192))
+    x = np.random.default_rng(27).uniform(-1, 1, 8192)
+    y = C.matmul(C.to_device(A), C.to_device(x)).numpy()
+    ref = O.matmul(A, x.reshape(-1, 1)).ravel()
+    assert y.shape == (8192,) and bits_equal(y, ref)
+
+
+def test_config_3c_skinny_bit_exact():
+    A = np.random.default_rng(24).uniform(-1, 1, (8192, 4096))
+    B = np.random.default_rng(25).uniform(-1, 1, (4096, 64))
+    c = C.matmul(C.to_device(A), C.to_device(B)).numpy()
+    assert bits_equal(c, O.matmul(A, B))
+
+
+MFMA_CASES = [
+    (128, 128, 128, False, False),
+    (300, 260, 500, False, False),
+    (1000, 777, 999, True, False),
+    (257, 300, 129, False, True),
+    (256, 512, 64, True, True),
+]
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("case", MFMA_CASES)
+def test_mfma_within_tolerance(case, dtype):
+    M, N, K, ta, tb = case
+    if dtype == np.float64 and min(M, N) <= 64:
+        pytest.skip("f64 narrow shapes take the tree path")
+    rng = np.random.default_rng(M + N + K)
+    a, b = rand(rng, (M, K), dtype), rand(rng, (K, N), dtype)
+    _da, va, na = dev_view(a, M, K, ta)
+    _db, vb, nb = dev_view(b, K, N, tb)
+    c = C.matmul(va, vb).numpy()
+    check_close(c, O.matmul(na, nb), dtype)
+
+
+def test_batched_broadcast_attention_form():
+    """[2,3,S,d] . [2,3,d,S]^T-style batched products with a broadcast batch axis."""
+    rng = np.random.default_rng(31)
+    q = rand(rng, (2, 3, 96, 64), np.float32)
+    k = rand(rng, (2, 1, 96, 64), np.float32)
+    dq, dk = C.to_device(q), C.to_device(k)
+    kt = dk.view((2, 1, 64, 96), (96 * 64, 96 * 64, 1, 64))  # k^T without a copy
+    s = C.matmul(dq, kt).numpy()
+    assert s.shape == (2, 3, 96, 96)
+    for i in range(2):
+        for h in range(3):
+            check_close(s[i, h], O.matmul(q[i, h], np.ascontiguousarray(k[i, 0].T)), np.float32)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_config_3ab_4096_cube_sampled_rows(dtype):
+    seeds = (20, 21) if dtype == np.float32 else (22, 23)
+    A = np.random.default_rng(seeds[0]).uniform(-1, 1, (4096, 4096)).astype(dtype)
+    B = np.random.default_rng(seeds[1]).uniform(-1, 1, (4096, 4096)).astype(dtype)
+    c = C.matmul(C.to_device(A), C.to_device(B)).numpy()
+    rows = np.random.default_rng(0).choice(4096, 48, replace=False)
+    rows = np.concatenate([[0, 127, 128, 4095], rows])
+    check_close(c[rows], O.matmul(np.ascontiguousarray(A[rows]), B), dtype)
+
+
+@pytest.mark.parametrize("act", [None, "relu", "gelu"])
+def test_linear_epilogue_bit_exact_on_tree_path(act):
+    """bias, activation and residual fused after a skinny (tree) product equal
+    the unfused graph bit for bit."""
+    rng = np.random.default_rng(41)
+    x, w = rand(rng, (256, 512), np.float32), rand(rng, (512, 10), np.float32)
+    bias, res = rand(rng, (10,), np.float32), rand(rng, (256, 10), np.float32)
+    c = C.linear(C.to_device(x), C.to_device(w), C.to_device(bias), act, C.to_device(res)).numpy()
+    v = (O.matmul(x, w) + bias).astype(np.float32)
+    if act == "relu":
+        v = O.relu(v)
+    elif act == "gelu":
+        v = O.gelu(v)
+    v = (res + v).astype(np.float32)
+    if act == "gelu":
+        ok = np.abs(c - v) <= 1e-5 * np.abs(v) + 1e-30
+        assert ok.all()
+    else:
+        assert bits_equal(c, v)
+
+
+def test_linear_epilogue_on_mfma_path():
+    rng = np.random.default_rng(42)
+    x, w = rand(rng, (512, 256), np.float32), rand(rng, (256, 384), np.float32)
+    bias = rand(rng, (384,), np.float32)
+    c = C.linear(C.to_device(x), C.to_device(w), C.to_device(bias), "relu").numpy()
+    check_close(c, O.relu((O.matmul(x, w) + bias).astype(np.float32)), np.float32)

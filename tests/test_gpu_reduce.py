@@ -1,0 +1,83 @@
+"""GPU parity of the axis reductions (chelis_hip_reduce, chelis_hip_count)
+against the C oracle: sums are the canonical tree ([05-OP-30]) bit for bit,
+max/min keep the first NaN and the first stored representation ([05-OP-12]),
+argmax/argmin the first index, counts are exact with the reference kernel's
+error code 1 for a byte that is not 0 or 1
+(crates/chelis-backend-hip/src/kernels.rs:375-557)."""
+import numpy as np
+import pytest
+
+import chelis_amd as C
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def setup_module(_m):
+    O.build()
+
+
+def bits_equal(a, b):
+    return np.array_equal(np.ascontiguousarray(a).view(np.uint8), np.ascontiguousarray(b).view(np.uint8))
+
+
+SHAPES = [((1,), 0), ((7,), 0), ((64, 1000), 1), ((64, 1000), 0), ((3, 257, 5), 1), ((1024, 10), 1),
+          ((1024, 512), 0), ((2, 3, 4097), 2), ((4100, 3), 0), ((33, 65537), 1)]
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("shape,axis", SHAPES)
+def test_sum_and_max_bit_exact(shape, axis, dtype):
+    rng = np.random.default_rng(sum(shape) + axis)
+    x = (rng.standard_normal(shape) * 3).astype(dtype)
+    d = C.to_device(x)
+    assert bits_equal(C.reduce("sum", d, axis).numpy(), O.sum_axis(x, axis))
+    assert bits_equal(C.reduce("max", d, axis).numpy(), O.max_axis(x, axis))
+    assert bits_equal(C.reduce("min", d, axis).numpy(), -O.max_axis(-x, axis))
+    am = C.reduce("argmax", d, axis).numpy()
+    assert np.array_equal(am, np.argmax(x, axis))
+
+
+def test_max_first_nan_and_signed_zero():
+    x = np.array([[0.0, -0.0, 1.0, np.nan, 2.0], [-0.0, 0.0, -0.0, 0.0, -1.0], [1.0, 3.0, 3.0, -np.inf, 0.0]],
+                 np.float32)
+    x[0, 3] = np.array([0x7FC0BEEF], np.uint32).view(np.float32)[0]  # NaN with a payload
+    d = C.to_device(x)
+    mx = C.reduce("max", d, 1).numpy()
+    assert bits_equal(mx, O.max_axis(x, 1))
+    assert np.array_equal(C.reduce("argmax", d, 1).numpy(), [3, 0, 1])
+
+
+def test_sum_of_fused_chain_leaf():
+    """reduce_fused: sum over the axis of (x - m) * (x - m) with m broadcast."""
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((512, 1024)).astype(np.float32)
+    m = x.mean(1, dtype=np.float32)
+    dx, dm = C.to_device(x), C.to_device(m)
+    mv = dm.view((512, 1024), (1, 0))
+    ch = C.fused_chain([("sub", 0, 1), ("mul", ("s", 0), ("s", 0))])
+    out = C.reduce("sum", [dx, mv], 1, chain=ch).numpy()
+    leaf = ((x - m[:, None]) * (x - m[:, None])).astype(np.float32)
+    assert bits_equal(out, O.sum_axis(leaf, 1))
+
+
+def test_empty_axis():
+    d = C.empty((4, 0), np.float64)
+    assert bits_equal(C.reduce("sum", d, 1).numpy(), np.zeros(4))
+    with pytest.raises(C.ChelisError, match="numeric trap: domain in max_reduce at f64"):
+        C.reduce("max", d, 1)
+
+
+@pytest.mark.parametrize("shape,axis", [((1024, 512), 1), ((1024, 512), 0), ((7, 100003), 1)])
+def test_count_exact(shape, axis):
+    x = (np.random.default_rng(6).random(shape) < 0.3).astype(np.uint8)
+    out, err = C.count(C.to_device(x), axis)
+    ref, rerr = O.count_axis(x, axis)
+    assert err == 0 == rerr and np.array_equal(out.numpy(), ref)
+
+
+def test_count_rejects_non_bool_byte():
+    x = np.zeros((4, 64), np.uint8)
+    x[2, 17] = 2
+    out, err = C.count(C.to_device(x), 1)
+    assert err == 1 and O.count_axis(x, 1)[1] == 1
