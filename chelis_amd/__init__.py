@@ -26,10 +26,11 @@ class ChelisError(RuntimeError):
 
 
 # ---- ABI types (include/chelis_runtime.h, include/chelis_device_descriptor.h) ----
-DT_F32, DT_F64, DT_I32, DT_BOOL, DT_I64 = 0, 1, 2, 3, 4
+DT_F32, DT_F64, DT_I32, DT_BOOL, DT_I64, DT_KEY = 0, 1, 2, 3, 4, 9
 _NP2DT = {np.dtype(np.float32): DT_F32, np.dtype(np.float64): DT_F64, np.dtype(np.int32): DT_I32,
           np.dtype(np.uint8): DT_BOOL, np.dtype(np.bool_): DT_BOOL, np.dtype(np.int64): DT_I64}
-_DT2NP = {DT_F32: np.float32, DT_F64: np.float64, DT_I32: np.int32, DT_BOOL: np.uint8, DT_I64: np.int64}
+_DT2NP = {DT_F32: np.float32, DT_F64: np.float64, DT_I32: np.int32, DT_BOOL: np.uint8, DT_I64: np.int64,
+          DT_KEY: np.uint64}
 
 
 class Scalar(ctypes.Structure):
@@ -117,6 +118,14 @@ SIGNATURES = {
     "chelis_hip_count": (c_int32, [P, c_int32, P, POINTER(c_int32)]),
     "chelis_hip_matmul": (c_int32, [P, P, P, c_int32]),
     "chelis_hip_linear": (c_int32, [P, P, P, c_int32, P, P, c_int32]),
+    # chelis_programs.h
+    "chelis_prog_linreg_step": (c_int32, [POINTER(P), c_int32, POINTER(P), c_int32]),
+    "chelis_prog_transformer_block": (c_int32, [POINTER(P), c_int32, POINTER(P), c_int32]),
+    "chelis_prog_mlp_train_step": (c_int32, [POINTER(P), c_int32, POINTER(P), c_int32]),
+    "linreg_step_device": (None, [POINTER(c_void_p), c_int32, POINTER(c_void_p), c_int32]),
+    "transformer_block_device": (None, [POINTER(c_void_p), c_int32, POINTER(c_void_p), c_int32]),
+    "mlp_train_step_device": (None, [POINTER(c_void_p), c_int32, POINTER(c_void_p), c_int32]),
+    "chelis_hip_set_exact_matmul": (c_int32, [c_int32]),
 }
 
 _lib = None
@@ -209,11 +218,11 @@ class View:
         self.packet = ctypes.pointer(g)
 
 
-def _plan(shape, dtype) -> int:
+def _plan(shape, dtype, tag=None) -> int:
     shape = tuple(int(s) for s in shape)
     arr = (Scalar * max(1, len(shape)))(*[i64(s) for s in shape])
     ex = Scalar()
-    ex.dtype = _NP2DT[np.dtype(dtype)]
+    ex.dtype = _NP2DT[np.dtype(dtype)] if tag is None else tag
     return lib().chelis_metadata_plan_new(i64(len(shape)), arr, ex)
 
 
@@ -395,3 +404,34 @@ def linear(a, b, bias=None, act=None, residual=None, c=None, exact: bool = False
                                   _p(residual) if residual is not None else None, _p(c),
                                   MATMUL_EXACT if exact else 0), "linear")
     return c
+
+
+def key_tensor(key: int) -> DeviceTensor:
+    """A rank-0 KEY device tensor holding `key` (the RandomKey bits)."""
+    t = DeviceTensor(lib().chelis_device_tensor_alloc(_plan((), np.uint64, DT_KEY)))
+    host = np.array(key & (2**64 - 1), np.uint64)
+    h = lib().chelis_tensor_entry_borrow(0, None, DT_KEY, host.ctypes.data, 8)
+    lib().chelis_device_tensor_copy_from_host(t.owner, h)
+    lib().chelis_tensor_release(h)
+    return t
+
+
+# ---- program entries (include/chelis_programs.h) ----
+def program(name: str, inputs, outputs):
+    """chelis_prog_{name}: enqueue the whole program; outputs are caller-owned."""
+    ins = (P * len(inputs))(*[_p(t) for t in inputs])
+    outs = (P * len(outputs))(*[_p(t) for t in outputs])
+    check(getattr(lib(), f"chelis_prog_{name}")(ins, len(inputs), outs, len(outputs)), name)
+    return outputs
+
+
+def device_entry(name: str, inputs, n_out: int):
+    """{name}_device: the reference's generated-entry ABI; returns owned outputs."""
+    ins = (c_void_p * len(inputs))(*[t.owner for t in inputs])
+    outs = (c_void_p * n_out)()
+    getattr(lib(), f"{name}_device")(ins, len(inputs), outs, n_out)
+    return [DeviceTensor(o) for o in outs]
+
+
+def set_exact_matmul(on: bool) -> bool:
+    return bool(lib().chelis_hip_set_exact_matmul(1 if on else 0))

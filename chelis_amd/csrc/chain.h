@@ -92,6 +92,13 @@ struct ChainDev {
     double imm[CHELIS_FUSED_MAX_STEPS];
 };
 
+// Transcendental leaves of the chain interpreter stay out of line: every
+// unrolled step of every chain kernel would otherwise inline all of them.
+template <typename T> __device__ __noinline__ T chain_exp(T a) { return leaf_exp<T>(a); }
+template <typename T> __device__ __noinline__ T chain_log(T a) { return leaf_log<T>(a); }
+template <typename T> __device__ __noinline__ T chain_tanh(T a) { return leaf_tanh<T>(a); }
+template <typename T> __device__ __noinline__ T chain_erfc(T a) { return leaf_erfc<T>(a); }
+
 template <typename T>
 __device__ inline T apply_step(uint8_t op, T a, T b, double imm) {
     switch (op) {
@@ -103,11 +110,11 @@ __device__ inline T apply_step(uint8_t op, T a, T b, double imm) {
         case CHELIS_FUSED_MIN_ELEM: return min_first(a, b);
         case CHELIS_FUSED_NEG: return canon(-a);
         case CHELIS_FUSED_RECIP: return canon(T(1) / a);
-        case CHELIS_FUSED_EXP: return leaf_exp<T>(a);
-        case CHELIS_FUSED_LOG: return leaf_log<T>(a);
+        case CHELIS_FUSED_EXP: return chain_exp<T>(a);
+        case CHELIS_FUSED_LOG: return chain_log<T>(a);
         case CHELIS_FUSED_SQRT: return canon(sqrt(a));
-        case CHELIS_FUSED_TANH: return leaf_tanh<T>(a);
-        case CHELIS_FUSED_ERFC: return leaf_erfc<T>(a);
+        case CHELIS_FUSED_TANH: return chain_tanh<T>(a);
+        case CHELIS_FUSED_ERFC: return chain_erfc<T>(a);
         case CHELIS_FUSED_ABS: return canon(fabs(a));
         case CHELIS_FUSED_FLOOR: return canon(floor(a));
         case CHELIS_FUSED_CEIL: return canon(ceil(a));

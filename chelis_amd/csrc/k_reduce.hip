@@ -253,9 +253,15 @@ struct Scratch {
     }
 };
 
+// An inlined FusedElem leaf exists only for Sum and Max, the two
+// reductions fuse.rs folds a chain into (crates/chelis-dag-core/src/fuse.rs:463-487).
+template <Rk K>
+constexpr bool kChainable = K == Rk::Sum || K == Rk::Max;
+
 template <typename T, Rk K>
 int32_t run_reduce(const ChainDev &ch, bool chain, LeafSrc src, int64_t outer, int64_t n, int64_t inner,
                    void *out, hipStream_t st) {
+    if (chain && !kChainable<K>) return set_error(CHELIS_HIP_EUNSUPPORTED, "reduce: a fused leaf chain feeds sum or max only");
     // Pass loop: partials alternate between two scratch buffers.
     Scratch sa(st), sb(st), ia(st), ib(st);
     const bool rows = inner == 1;
@@ -309,10 +315,13 @@ int32_t run_reduce(const ChainDev &ch, bool chain, LeafSrc src, int64_t outer, i
             const unsigned grid = grid_for(outer * groups, 4);
 #define CHELIS_ROWS_CASE(SS)                                                                                  \
     case SS:                                                                                                  \
-        if (use_chain)                                                                                        \
-            reduce_rows_kernel<T, K, SS, true><<<grid, 256, 0, st>>>(ch, s, outer, cur_n, groups, dst_v, dst_i, last); \
-        else                                                                                                  \
-            reduce_rows_kernel<T, K, SS, false><<<grid, 256, 0, st>>>(ch, s, outer, cur_n, groups, dst_v, dst_i, last); \
+        if constexpr (kChainable<K>) {                                                                        \
+            if (use_chain) {                                                                                  \
+                reduce_rows_kernel<T, K, SS, true><<<grid, 256, 0, st>>>(ch, s, outer, cur_n, groups, dst_v, dst_i, last); \
+                break;                                                                                        \
+            }                                                                                                 \
+        }                                                                                                     \
+        reduce_rows_kernel<T, K, SS, false><<<grid, 256, 0, st>>>(ch, s, outer, cur_n, groups, dst_v, dst_i, last); \
         break;
             switch (S) {
                 CHELIS_ROWS_CASE(1)
@@ -326,10 +335,15 @@ int32_t run_reduce(const ChainDev &ch, bool chain, LeafSrc src, int64_t outer, i
         } else {
             int64_t blocks = (cells + 255) / 256;
             if (blocks > 16384) blocks = 16384;
-            if (use_chain)
-                reduce_cols_kernel<T, K, true><<<(unsigned)blocks, 256, 0, st>>>(ch, s, outer, cur_n, inner, groups,
-                                                                                 dst_v, dst_i, last);
-            else
+            bool done = false;
+            if constexpr (kChainable<K>) {
+                if (use_chain) {
+                    reduce_cols_kernel<T, K, true><<<(unsigned)blocks, 256, 0, st>>>(ch, s, outer, cur_n, inner, groups,
+                                                                                     dst_v, dst_i, last);
+                    done = true;
+                }
+            }
+            if (!done)
                 reduce_cols_kernel<T, K, false><<<(unsigned)blocks, 256, 0, st>>>(ch, s, outer, cur_n, inner, groups,
                                                                                   dst_v, dst_i, last);
         }
