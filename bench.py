@@ -2,25 +2,38 @@
 
 `python bench.py [--gpus 1] [--steps K] [--warmup W]` prints ONE JSON line.
 
-Headline workload (`value`): BASELINE config 2a, the fused row softmax over
-f32 [16384, 1024] logits ~ N(0, sigma=2): one step = one softmax region
-launch over the whole tensor, inputs resident in HBM. Five input/output
-buffer pairs (640 MiB) rotate so the 256 MB Infinity Cache cannot hold the
-working set. Algorithmic bytes per launch = 16384*1024*4 read + the same
-written = 134 217 728 B; `value` = those bytes / the average launch time,
-timed with HIP events on the library stream over exactly K launches.
+Headline workload (`value`): config 2a, the fused row softmax region over
+f32 [16384, 1024] logits ~ N(0, sigma=2); one step = one launch of the
+softmax region over the whole tensor, inputs resident in HBM. Five
+input/output buffer pairs (640 MiB) rotate so the 256 MB Infinity Cache
+cannot hold the working set. Algorithmic bytes per launch = 16384*1024*4
+read + the same written = 134 217 728 B; `value` = those bytes / the
+average launch time, timed with HIP events recorded on the library stream
+(the stream every launcher enqueues on) around exactly K launches.
 
-`kernels` reports the other configurations' regions the same way (GB/s for
-bandwidth kernels, TFLOP/s for GEMMs, ms for the transformer block).
-`cpu_baseline` times the C oracle (the restated reference C lane, OpenMP
-over all host cores) on the same workload on this host.
+`roofline.traffic` is the HBM bytes one softmax launch moves, from two
+rocprofv3 --pmc runs of this script (FETCH_SIZE, then WRITE_SIZE), each
+scaled by what the same counter reads for a plain 256 MiB relu map (a
+read-once, write-once elementwise kernel of known size).
+
+`kernels` reports every configuration the same way: GB/s against the 8 TB/s
+HBM peak for bandwidth kernels, TFLOP/s against the dtype's MFMA peak for
+GEMMs, ms / us end to end for the three programs. `cpu_baseline` times the C
+oracle (the restated reference C lane, gcc -O2 -ffp-contract=off -fopenmp)
+on the headline workload on this host; `kernels[*].cpu_ms` gives the same
+oracle's time on a bounded sample of the other configurations.
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import os
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
 
 import numpy as np
@@ -31,6 +44,8 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBPS = 8000.0
 PEAK_TFLOPS = {"f32": 157.3, "f64": 78.6}
 METRIC = "per-kernel GB/s & GFLOP/s (% roofline); transformer-block fwd ms at 1 GPU"
+SOFTMAX_ROWS, SOFTMAX_N = 16384, 1024
+COPY_ELEMS = 64 * 1024 * 1024  # f32 relu map used to calibrate the HBM counters
 
 
 def host_cores() -> int:
@@ -41,7 +56,8 @@ def host_cores() -> int:
 
 
 def time_launches(C, H, launch, steps: int, warmup: int) -> float:
-    """Average ms per launch of `launch(i)` over `steps` launches."""
+    """Average ms per launch of `launch(i)` over `steps` launches, HIP events
+    on the library stream."""
     stream = C.lib().chelis_hip_stream()
     for i in range(warmup):
         launch(i)
@@ -55,22 +71,24 @@ def time_launches(C, H, launch, steps: int, warmup: int) -> float:
     return start.elapsed_ms(end) / steps
 
 
+def softmax_inputs():
+    return (np.random.default_rng(10).standard_normal((SOFTMAX_ROWS, SOFTMAX_N)) * 2).astype(np.float32)
+
+
 def bench_softmax_f32(C, H, steps, warmup):
-    rows, n = 16384, 1024
-    nbytes = rows * n * 4 * 2
-    x = (np.random.default_rng(10).standard_normal((rows, n)) * 2).astype(np.float32)
-    pairs = [(C.to_device(x), C.empty((rows, n), np.float32)) for _ in range(5)]
+    nbytes = SOFTMAX_ROWS * SOFTMAX_N * 4 * 2
+    x = softmax_inputs()
+    pairs = [(C.to_device(x), C.empty(x.shape, np.float32)) for _ in range(5)]
     ms = time_launches(C, H, lambda i: C.softmax(pairs[i % 5][0], pairs[i % 5][1]), steps, warmup)
     return {"ms": ms, "bytes": nbytes, "gbps": nbytes / (ms * 1e-3) / 1e9}, x
 
 
 def bench_softmax_f64(C, H, steps, warmup):
-    rows = n = 4096
-    nbytes = rows * n * 8 * 2
-    x = np.random.default_rng(11).standard_normal((rows, n))
-    pairs = [(C.to_device(x), C.empty((rows, n), np.float64)) for _ in range(3)]
+    nbytes = 4096 * 4096 * 8 * 2
+    x = np.random.default_rng(11).standard_normal((4096, 4096))
+    pairs = [(C.to_device(x), C.empty(x.shape, np.float64)) for _ in range(3)]
     ms = time_launches(C, H, lambda i: C.softmax(pairs[i % 3][0], pairs[i % 3][1]), steps, warmup)
-    return {"ms": ms, "bytes": nbytes, "gbps": nbytes / (ms * 1e-3) / 1e9}
+    return {"ms": ms, "bytes": nbytes, "gbps": nbytes / (ms * 1e-3) / 1e9}, x
 
 
 def bench_gemm(C, H, M, N, K, dtype, seeds, steps, warmup, reps=1):
@@ -85,35 +103,203 @@ def bench_gemm(C, H, M, N, K, dtype, seeds, steps, warmup, reps=1):
     nbytes = (M * K + K * N + M * N) * isz
     flops = 2 * M * N * K
     return {"ms": ms, "bytes": nbytes, "flops": flops, "gbps": nbytes / (ms * 1e-3) / 1e9,
-            "tflops": flops / (ms * 1e-3) / 1e12}
+            "tflops": flops / (ms * 1e-3) / 1e12}, (a, b)
 
 
 def gemm_line(r, dt, bound):
-    line = {"ms": round(r["ms"], 5), "TFLOP/s": round(r["tflops"], 2), "GB/s": round(r["gbps"], 1),
+    return {"ms": round(r["ms"], 5), "TFLOP/s": round(r["tflops"], 2), "GB/s": round(r["gbps"], 1),
             "frac_mfma": round(r["tflops"] / PEAK_TFLOPS[dt], 4), "frac_hbm": round(r["gbps"] / HBM_PEAK_GBPS, 4),
             "bound": bound}
-    return line
 
 
-def cpu_baseline_softmax(x: np.ndarray, budget_s: float = 10.0):
+def linreg_data():
+    X = np.random.default_rng(1).standard_normal((8192, 32))
+    w = np.random.default_rng(2).standard_normal(32)
+    y = X @ w + np.random.default_rng(3).normal(0, 0.01, 8192)
+    return X, w, y
+
+
+def transformer_data(B=8, S=512, D=1024, F=4096):
+    x = np.random.default_rng(30).standard_normal((B, S, D)).astype(np.float32)
+    p = {}
+    seeds = iter(range(31, 37))
+    for name, shape in (("wq", (D, D)), ("wk", (D, D)), ("wv", (D, D)), ("wo", (D, D)), ("w1", (D, F)),
+                        ("w2", (F, D))):
+        p[name] = (np.random.default_rng(next(seeds)).standard_normal(shape) * 0.02).astype(np.float32)
+    for name, n in (("bq", D), ("bk", D), ("bv", D), ("bo", D), ("b1", F), ("b2", D), ("ln1_b", D), ("ln2_b", D)):
+        p[name] = np.zeros(n, np.float32)
+    p["ln1_g"] = np.ones(D, np.float32)
+    p["ln2_g"] = np.ones(D, np.float32)
+    return x, p
+
+
+PARAM_ORDER = ("ln1_g", "ln1_b", "wq", "bq", "wk", "bk", "wv", "bv", "wo", "bo", "ln2_g", "ln2_b", "w1", "b1", "w2",
+               "b2")
+
+
+def mlp_data(B=1024, I=784, Hd=512, O=10):
+    x = np.random.default_rng(40).uniform(0, 1, (B, I)).astype(np.float32)
+    labels = np.random.default_rng(41).integers(0, O, B)
+    onehot = np.eye(O, dtype=np.float32)[labels]
+    w1 = (np.random.default_rng(42).standard_normal((I, Hd)) * np.sqrt(2 / I)).astype(np.float32)
+    w2 = (np.random.default_rng(43).standard_normal((Hd, O)) * np.sqrt(2 / Hd)).astype(np.float32)
+    return x, onehot, w1, np.zeros(Hd, np.float32), w2, np.zeros(O, np.float32)
+
+
+TRANSFORMER_FLOPS = 111_669_149_696  # QKV + scores + PV + out + FFN, 2 flops per MAC
+MLP_FLOPS = 1_675_624_448
+LINREG_BYTES = 2_163_208
+
+
+def bench_programs(C, H, steps, warmup):
+    out = {}
+    X, w, y = linreg_data()
+    ins = [C.to_device(a) for a in (X, w, y)]
+    outs = [C.empty((32,), np.float64), C.empty((), np.float64)]
+    ms = time_launches(C, H, lambda i: C.program("linreg_step", ins, outs), steps, warmup)
+    out["linreg_step_f64_8192x32"] = {"us": round(ms * 1e3, 2), "GB/s": round(LINREG_BYTES / (ms * 1e-3) / 1e9, 1),
+                                      "frac_hbm": round(LINREG_BYTES / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                                      "bound": "launch latency (2 MB working set)"}
+    x, p = transformer_data()
+    tins = [C.to_device(x)] + [C.to_device(p[k]) for k in PARAM_ORDER]
+    ty = C.empty(x.shape, np.float32)
+    tsteps = max(3, steps // 5)
+    ms = time_launches(C, H, lambda i: C.program("transformer_block", tins, [ty]), tsteps, 2)
+    out["transformer_block_f32_b8_s512_d1024"] = {
+        "ms": round(ms, 4), "TFLOP/s": round(TRANSFORMER_FLOPS / (ms * 1e-3) / 1e12, 2),
+        "frac_mfma": round(TRANSFORMER_FLOPS / (ms * 1e-3) / 1e12 / PEAK_TFLOPS["f32"], 4)}
+    del tins, ty
+    args = mlp_data()
+    mins = [C.to_device(a) for a in args] + [C.key_tensor(44)]
+    mouts = [C.empty((), np.float32), C.empty(args[2].shape, np.float32), C.empty(args[3].shape, np.float32),
+             C.empty(args[4].shape, np.float32), C.empty(args[5].shape, np.float32)]
+    ms = time_launches(C, H, lambda i: C.program("mlp_train_step", mins, mouts), steps, warmup)
+    out["mlp_train_step_f32_1024x784x512x10"] = {
+        "us": round(ms * 1e3, 2), "TFLOP/s": round(MLP_FLOPS / (ms * 1e-3) / 1e12, 3),
+        "bound": "launch latency (21 small launches)"}
+    return out, (X, w, y), (x, p), args
+
+
+# ---------------------------------------------------------------- traffic
+def traffic_child():
+    """Runs under rocprofv3 --pmc: 10 headline softmax launches and 10
+    launches of the relu map used as the calibration copy."""
+    import chelis_amd as C
+
+    x = softmax_inputs()
+    pairs = [(C.to_device(x), C.empty(x.shape, np.float32)) for _ in range(5)]
+    src = C.to_device(np.abs(np.random.default_rng(5).standard_normal(COPY_ELEMS)).astype(np.float32))
+    dst = C.empty((COPY_ELEMS,), np.float32)
+    for i in range(10):
+        C.softmax(pairs[i % 5][0], pairs[i % 5][1])
+    for _ in range(10):
+        C.relu(src, dst)
+    C.synchronize()
+
+
+def _counter_rows(outdir):
+    files = glob.glob(os.path.join(outdir, "**", "*counter_collection*.csv"), recursive=True)
+    rows = []
+    for f in files:
+        with open(f, newline="") as fh:
+            rows.extend(csv.DictReader(fh))
+    return rows
+
+
+def measure_traffic(timeout_s=120):
+    """HBM bytes per softmax launch from FETCH_SIZE and WRITE_SIZE, each
+    scaled by the relu calibration map; None when rocprofv3 is unavailable."""
+    prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(prof):
+        return None, "rocprofv3 not found"
+    per = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        outdir = tempfile.mkdtemp(prefix="chelis_pmc_")
+        try:
+            cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", outdir, "-o", "pmc", "--",
+                   sys.executable, os.path.abspath(__file__), "--traffic-child"]
+            r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout_s)
+            rows = _counter_rows(outdir)
+            if not rows:
+                return None, f"rocprofv3 --pmc {counter} produced no counter rows (rc {r.returncode})"
+            vals = {"softmax": [], "relu": []}
+            for row in rows:
+                name = row.get("Kernel_Name", "")
+                if row.get("Counter_Name", counter) != counter:
+                    continue
+                v = float(row.get("Counter_Value", "nan"))
+                if "softmax_kernel" in name:
+                    vals["softmax"].append(v)
+                elif "unary_kernel" in name:
+                    vals["relu"].append(v)
+            if not vals["softmax"] or not vals["relu"]:
+                return None, f"{counter}: kernels not found in the counter rows"
+            per[counter] = {k: float(np.median(v)) for k, v in vals.items()}
+        finally:
+            shutil.rmtree(outdir, ignore_errors=True)
+    copy_bytes = COPY_ELEMS * 4
+    f_scale = copy_bytes / per["FETCH_SIZE"]["relu"]
+    w_scale = copy_bytes / per["WRITE_SIZE"]["relu"]
+    fetch = per["FETCH_SIZE"]["softmax"] * f_scale
+    write = per["WRITE_SIZE"]["softmax"] * w_scale
+    detail = {"fetch_bytes": round(fetch), "write_bytes": round(write),
+              "raw_kib": {"fetch_softmax": per["FETCH_SIZE"]["softmax"], "write_softmax": per["WRITE_SIZE"]["softmax"],
+                          "fetch_copy": per["FETCH_SIZE"]["relu"], "write_copy": per["WRITE_SIZE"]["relu"]},
+              "scale": {"fetch": round(f_scale, 3), "write": round(w_scale, 3)},
+              "calibration": f"relu map of {copy_bytes} B read + {copy_bytes} B written"}
+    return fetch + write, detail
+
+
+# ---------------------------------------------------------------- CPU baselines
+def _time_cpu(fn, budget_s, max_runs=20):
+    fn()
+    runs, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        runs += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or runs >= max_runs:
+            return el / runs, runs
+
+
+def cpu_baselines(x_softmax, kernels, linreg, transformer, mlp, gemm_inputs):
     from oracle import oracle as O
 
     O.build()
     cores = host_cores()
     os.environ.setdefault("OMP_NUM_THREADS", str(cores))
-    O.softmax_rows(x[:256])  # warm the library and thread pool
-    runs, t0 = 0, time.perf_counter()
-    while True:
-        O.softmax_rows(x)
-        runs += 1
-        el = time.perf_counter() - t0
-        if el > budget_s or runs >= 20:
-            break
-    per = el / runs
-    return {"value": x.nbytes * 2 / per / 1e9, "unit": "GB/s", "cores": int(os.environ["OMP_NUM_THREADS"]),
-            "kind": "port",
-            "sample": f"full config 2a tensor [16384,1024] f32, {runs} runs of the oracle softmax "
+    threads = int(os.environ["OMP_NUM_THREADS"])
+    per, runs = _time_cpu(lambda: O.softmax_rows(x_softmax), 10.0)
+    head = {"value": round(x_softmax.nbytes * 2 / per / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"the full config 2a tensor [16384,1024] f32, {runs} runs of the oracle softmax "
                       f"(gcc -O2 -ffp-contract=off -fopenmp, CORE-MATH expf), {per * 1e3:.1f} ms per run"}
+    X, w, y = linreg
+    t, _ = _time_cpu(lambda: O.linreg_step(X, w, y), 2.0)
+    kernels["linreg_step_f64_8192x32"]["cpu_ms"] = round(t * 1e3, 3)
+    a, b = gemm_inputs["f32"]
+    t, _ = _time_cpu(lambda: O.matmul(np.ascontiguousarray(a[:128]), b), 3.0, 3)
+    kernels["gemm_f32_4096^3"]["cpu_ms"] = round(t * 1e3 * 32, 1)
+    a, b = gemm_inputs["f64"]
+    t, _ = _time_cpu(lambda: O.matmul(np.ascontiguousarray(a[:128]), b), 3.0, 3)
+    kernels["gemm_f64_4096^3"]["cpu_ms"] = round(t * 1e3 * 32, 1)
+    a, b = gemm_inputs["skinny"]
+    t, _ = _time_cpu(lambda: O.matmul(np.ascontiguousarray(a[:1024]), b), 3.0, 5)
+    kernels["skinny_f64_8192x64x4096"]["cpu_ms"] = round(t * 1e3 * 8, 2)
+    a, b = gemm_inputs["gemv"]
+    t, _ = _time_cpu(lambda: O.matmul(a, b.reshape(-1, 1)), 3.0, 5)
+    kernels["gemv_f64_8192x8192"]["cpu_ms"] = round(t * 1e3, 2)
+    xs, p = transformer
+    t, _ = _time_cpu(lambda: O.transformer_block(np.ascontiguousarray(xs[:1]), p, 16), 5.0, 2)
+    kernels["transformer_block_f32_b8_s512_d1024"]["cpu_ms"] = round(t * 1e3 * 8, 1)
+    t, _ = _time_cpu(lambda: O.mlp_train_step(*mlp, 44, np.float32(0.1), np.float32(0.01)), 3.0, 5)
+    kernels["mlp_train_step_f32_1024x784x512x10"]["cpu_ms"] = round(t * 1e3, 2)
+    kernels["_cpu_note"] = (f"C oracle on {threads} host threads; GEMM 4096^3 timed on 128 rows x32, skinny on "
+                            f"1024 rows x8, transformer on batch 1 x8; others full size")
+    x64 = kernels.pop("_softmax_f64_input", None)
+    if x64 is not None:
+        t, _ = _time_cpu(lambda: O.softmax_rows(x64), 5.0, 5)
+        kernels["softmax_f64_4096x4096"]["cpu_ms"] = round(t * 1e3, 2)
+    return head
 
 
 def main(argv=None) -> int:
@@ -122,11 +308,16 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic runs")
     ap.add_argument("--only-headline", action="store_true")
+    ap.add_argument("--traffic-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args(argv)
+    if args.traffic_child:
+        traffic_child()
+        return 0
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "sharding is described in DESIGN.md, not run.", file=sys.stderr)
+              "how the path would shard is described in DESIGN.md, not run.", file=sys.stderr)
         return 2
 
     import chelis_amd as C
@@ -136,20 +327,40 @@ def main(argv=None) -> int:
     head, x = bench_softmax_f32(C, H, args.steps, args.warmup)
     kernels = {"softmax_f32_16384x1024": {"ms": round(head["ms"], 5), "GB/s": round(head["gbps"], 1),
                                           "frac_hbm": round(head["gbps"] / HBM_PEAK_GBPS, 4)}}
+    extra = None
     if not args.only_headline:
-        s64 = bench_softmax_f64(C, H, max(5, args.steps // 2), args.warmup)
+        s64, x64 = bench_softmax_f64(C, H, max(5, args.steps // 2), args.warmup)
         kernels["softmax_f64_4096x4096"] = {"ms": round(s64["ms"], 5), "GB/s": round(s64["gbps"], 1),
                                             "frac_hbm": round(s64["gbps"] / HBM_PEAK_GBPS, 4)}
         gs = max(3, args.steps // 5)
-        kernels["gemm_f32_4096^3"] = gemm_line(bench_gemm(C, H, 4096, 4096, 4096, np.float32, (20, 21), gs, 2), "f32",
-                                               "mfma")
-        kernels["gemm_f64_4096^3"] = gemm_line(bench_gemm(C, H, 4096, 4096, 4096, np.float64, (22, 23), gs, 2), "f64",
-                                               "mfma")
-        kernels["skinny_f64_8192x64x4096"] = gemm_line(
-            bench_gemm(C, H, 8192, 64, 4096, np.float64, (24, 25), gs, 2, reps=2), "f64", "valu-tree")
-        kernels["gemv_f64_8192x8192"] = gemm_line(
-            bench_gemm(C, H, 8192, 1, 8192, np.float64, (26, 27), gs, 2, reps=2), "f64", "hbm")
-    cpu = None if args.no_cpu else cpu_baseline_softmax(x)
+        gin = {}
+        r, gin["f32"] = bench_gemm(C, H, 4096, 4096, 4096, np.float32, (20, 21), gs, 2)
+        kernels["gemm_f32_4096^3"] = gemm_line(r, "f32", "mfma")
+        r, gin["f64"] = bench_gemm(C, H, 4096, 4096, 4096, np.float64, (22, 23), gs, 2)
+        kernels["gemm_f64_4096^3"] = gemm_line(r, "f64", "mfma")
+        r, gin["skinny"] = bench_gemm(C, H, 8192, 64, 4096, np.float64, (24, 25), gs, 2, reps=2)
+        kernels["skinny_f64_8192x64x4096"] = gemm_line(r, "f64", "valu canonical tree (bit-exact)")
+        r, gin["gemv"] = bench_gemm(C, H, 8192, 1, 8192, np.float64, (26, 27), gs, 2, reps=2)
+        kernels["gemv_f64_8192x8192"] = gemm_line(r, "f64", "hbm")
+        progs, lin, tr, mlp = bench_programs(C, H, max(5, args.steps // 2), args.warmup)
+        kernels.update(progs)
+        extra = (x64, lin, tr, mlp, gin)
+    traffic, tdetail = (None, "skipped") if args.no_traffic else measure_traffic()
+    cpu = None
+    if not args.no_cpu:
+        if extra is not None:
+            x64, lin, tr, mlp, gin = extra
+            kernels["_softmax_f64_input"] = x64
+            cpu = cpu_baselines(x, kernels, lin, tr, mlp, gin)
+        else:
+            from oracle import oracle as O
+
+            O.build()
+            os.environ.setdefault("OMP_NUM_THREADS", str(host_cores()))
+            per, runs = _time_cpu(lambda: O.softmax_rows(x), 10.0)
+            cpu = {"value": round(x.nbytes * 2 / per / 1e9, 3), "unit": "GB/s",
+                   "cores": int(os.environ["OMP_NUM_THREADS"]), "kind": "port",
+                   "sample": f"the full config 2a tensor, {runs} runs of the oracle softmax, {per * 1e3:.1f} ms/run"}
     line = {
         "metric": METRIC,
         "value": round(head["gbps"], 2),
@@ -164,9 +375,12 @@ def main(argv=None) -> int:
         "dtype": "f32",
         "data": "synthetic: N(0, sigma=2) logits from numpy seed 10, resident in HBM, 5 rotating buffer pairs",
         "config": {"workload": "config 2a: fused row softmax f32 [16384,1024] (max, sub, exp, tree sum, div)",
-                   "rows": 16384, "row_len": 1024, "parallelism": "single GPU"},
+                   "rows": SOFTMAX_ROWS, "row_len": SOFTMAX_N, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(head["gbps"], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(head["gbps"] / HBM_PEAK_GBPS, 4), "traffic": None},
+                     "frac": round(head["gbps"] / HBM_PEAK_GBPS, 4),
+                     "traffic": None if traffic is None else int(round(traffic)),
+                     "algorithmic_bytes": head["bytes"],
+                     "traffic_detail": tdetail},
         "cpu_baseline": cpu,
         "kernels": kernels,
     }

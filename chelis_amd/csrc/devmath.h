@@ -144,9 +144,18 @@ CHELIS_HD inline float expf_cr(float xf) {
     p = fma(p, r, 1.0);
     p = fma(p, r, 1.0);
     const double y = ldexp(p, (int)kd);
-    const int64_t below = (int64_t)(f64_bits(y) & ((1ull << 29) - 1)) - (int64_t(1) << 28);
-    if (below > -2048 && below < 2048) return expf_cr_dd(xf);
+    // 29 bits below binary32 precision, offset so the midpoint pattern is 2047
+    const uint32_t below = ((uint32_t)f64_bits(y) & 0x1fffffffu) - (0x10000000u - 2047u);
+    if (below < 4095u) return expf_cr_dd(xf);
     return (float)y;
 }
+
+// Correctly rounded binary32 v / t from a precomputed binary64 inv = 1 / t
+// (t >= 1 or NaN, as for a softmax row total): the binary64 product is
+// within 2^-52 relative of v / t, and the exact quotient of two binary32
+// values is never within 2^-49 relative of a binary32 rounding midpoint, so
+// one rounding to binary32 gives the correctly rounded quotient. Checked
+// against IEEE division on the host (tests/test_devmath.py).
+CHELIS_HD inline float quot_f32(float v, double inv) { return (float)((double)v * inv); }
 
 }  // namespace chelis

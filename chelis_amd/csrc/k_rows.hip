@@ -194,6 +194,57 @@ __device__ inline T row_max(const T (&v)[S][V], T *lds, const RowCoord<W, R> &c)
     return x;
 }
 
+// Plain IEEE maximum over the padded row (v_max: a NaN operand yields the
+// other one, and +0/-0 ties are unordered). Softmax uses it in place of
+// [05-OP-12]'s first-NaN / first-representation rule because the two give
+// identical softmax bits: a NaN anywhere in the row makes that element's
+// x - m NaN, hence the tree sum NaN and every output the canonical NaN under
+// either rule; and a zero maximum enters only through x - m, where
+// x - (+0) and x - (-0) differ at most in the sign of a zero, which exp maps
+// to the same 1.
+template <typename T>
+__device__ inline T vmax(T a, T b) {
+    if constexpr (sizeof(T) == 4) return __builtin_fmaxf(a, b);
+    else return __builtin_fmax(a, b);
+}
+template <typename T, int V, int S, int W, int R>
+__device__ inline T row_max_plain(const T (&v)[S][V], T *lds, const RowCoord<W, R> &c) {
+    T x = v[0][0];
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int i = 0; i < V; ++i) x = vmax(x, v[s][i]);
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) x = vmax(x, shfl_xor(x, m));
+    if constexpr (W > 1) {
+        if (c.lane == 0) lds[c.row_in_block * W + c.wave_in_row] = x;
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < W; ++w) x = vmax(x, lds[c.row_in_block * W + w]);
+        __syncthreads();
+    }
+    return x;
+}
+
+// v / total at the dtype. binary32: the quotient is formed as
+// (double)v * (1 / (double)total) and rounded once to binary32. That is the
+// correctly rounded v / total: the exact quotient of two binary32 values is
+// never closer than 2^-49 relative to a binary32 rounding midpoint (it is
+// X 2^a / (T 2^b) with 24-bit X, T against a midpoint M 2^c with 25-bit M,
+// and X 2^a - T M 2^(b+c) is a nonzero multiple of 2^min(a, b+c); the
+// subnormal range keeps an absolute gap of at least 2^-150 / T), while the
+// binary64 product is within 2^-52 relative of it.
+template <typename T>
+struct RowDiv {
+    T total;
+    double inv;
+    __device__ explicit RowDiv(T t) : total(t), inv(sizeof(T) == 4 ? 1.0 / (double)t : 0.0) {}
+    __device__ T operator()(T v) const {
+        if constexpr (sizeof(T) == 4) return canon(quot_f32(v, inv));
+        else return canon(v / total);
+    }
+};
+
 // softmax over the last axis, optionally of where(j <= i, x * scale, -inf)
 // (causal != 0, q_len = rows per score matrix).
 template <typename T, int V, int S, int W, int R>
@@ -220,19 +271,27 @@ __global__ __launch_bounds__(64 * W * R) void softmax_kernel(const T *__restrict
                 }
             }
     }
-    const T m = row_max<T, V, S, W, R>(v, lds, c);
+    const T m = row_max_plain<T, V, S, W, R>(v, lds, c);
+    // exp(x - m); x - m is NaN only where exp's leaf returns the canonical NaN
+    if (n == (int64_t)S * SEG) {
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int i = 0; i < V; ++i) v[s][i] = exp_leaf<T>(v[s][i] - m);
+    } else {
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int i = 0; i < V; ++i) {
+                const int64_t j = (int64_t)s * SEG + (int64_t)c.tid_in_row * V + i;
+                v[s][i] = (j < n) ? exp_leaf<T>(v[s][i] - m) : T(-0.0);
+            }
+    }
+    const RowDiv<T> div(canon(row_tree_sum<T, V, S, W, R>(v, lds, c)));
 #pragma unroll
     for (int s = 0; s < S; ++s)
 #pragma unroll
-        for (int i = 0; i < V; ++i) {
-            const int64_t j = (int64_t)s * SEG + (int64_t)c.tid_in_row * V + i;
-            v[s][i] = (j < n) ? exp_leaf<T>(canon(v[s][i] - m)) : T(-0.0);
-        }
-    const T total = canon(row_tree_sum<T, V, S, W, R>(v, lds, c));
-#pragma unroll
-    for (int s = 0; s < S; ++s)
-#pragma unroll
-        for (int i = 0; i < V; ++i) v[s][i] = canon(v[s][i] / total);
+        for (int i = 0; i < V; ++i) v[s][i] = div(v[s][i]);
     store_row<T, V, S, W>(y + c.row * ldy, n, vec_ok, c.tid_in_row, v);
 }
 

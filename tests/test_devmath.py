@@ -24,3 +24,15 @@ def test_expf_cr_matches_core_math_on_every_binary32(tmp_path):
     r = subprocess.run([str(exe), "1"], capture_output=True, text=True, timeout=600)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "checked 4294967296 mismatches 0" in r.stdout
+
+
+def test_quot_f32_matches_ieee_division(tmp_path):
+    """The softmax row division v / total through a binary64 reciprocal is
+    the correctly rounded binary32 quotient: every binary32 v in (0, 1]
+    against 16 totals, and 2^26 random pairs."""
+    exe = tmp_path / "div_check"
+    subprocess.run(["g++", "-O2", "-ffp-contract=off", "-fno-fast-math", "-fopenmp", "-std=c++17", "-o", str(exe),
+                    os.path.join(ROOT, "tests", "cpu", "div_check.cpp")], check=True)
+    r = subprocess.run([str(exe), "1"], capture_output=True, text=True, timeout=900)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "mismatches 0" in r.stdout
