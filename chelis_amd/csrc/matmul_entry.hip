@@ -73,7 +73,7 @@ int32_t build_problem(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b, co
     if ((s = check_tensor(a, "a")) || (s = check_tensor(b, "b")) || (s = check_tensor(c, "c"))) return s;
     if (!is_float(a->dtype) || a->dtype != b->dtype || a->dtype != c->dtype)
         return set_error(CHELIS_HIP_EDOMAIN, "%s: a, b and c must share an f32 or f64 dtype", what);
-    Mat ma, mb, mc;
+    Mat ma, mb;
     if (!as_mat(a, true, &ma) || !as_mat(b, false, &mb))
         return set_error(CHELIS_HIP_EUNSUPPORTED, "%s: operands need rank 1..4", what);
     if (ma.cols != mb.rows)
@@ -113,7 +113,6 @@ int32_t build_problem(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b, co
     p->sam = ma.srow, p->sak = ma.scol, p->sbk = mb.srow, p->sbn = mb.scol, p->scm = scm, p->scn = scn;
     p->nb0 = bext[0], p->nb1 = bext[1];
     p->sa0 = sa[0], p->sa1 = sa[1], p->sb0 = sb[0], p->sb1 = sb[1], p->sc0 = sc[0], p->sc1 = sc[1];
-    // collapse one batch axis when strides allow (more blocks per launch row)
     return CHELIS_HIP_OK;
 }
 
