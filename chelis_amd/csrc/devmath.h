@@ -112,42 +112,54 @@ CHELIS_HD inline float expf_cr_dd(float xf) {
     return round_pos_dd_to_f32(ldexp(s, m), ldexp(e, m));
 }
 
-// Correctly rounded binary32 exp, fast path first.
+// Binary32 exp, fast path, branch free. Returns (float)y and sets `slow`
+// when y is not known to be the correctly rounded result.
 //
-// For -87 < x < 88 the result is a normal binary32. x = k ln2 + r with
-// k = rint(x / ln2), |r| <= ln2/2 + 2^-40 (two fma steps against a
-// double-double ln2), and exp(r) is the degree-11 Taylor polynomial in
-// Horner form: truncation below r^12/12! < 2^-47, rounding about 2^-51, so
-// y = 2^k p(r) is within 2^-46 relative, under 2^7 units in the last place
-// of the double y. (float)y is then the correctly rounded result unless the
-// exact value may lie on the other side of a binary32 rounding midpoint,
-// i.e. unless the 29 bits below binary32 precision in y are within 2^11
-// units of the midpoint pattern 1 << 28; those inputs (about one in 2^17),
-// the out-of-range ones and NaN take expf_cr_dd. Checked against the
-// CORE-MATH oracle over every binary32 input (tests/test_devmath.py).
-CHELIS_HD inline float expf_cr(float xf) {
-    if (!(xf > -87.0f && xf < 88.0f)) return expf_cr_dd(xf);
-    const double x = (double)xf;
-    const double kd = rint(x * 0x1.71547652b82fep+0);
-    double r = fma(-kd, 0x1.62e42fefa39efp-1, x);
-    r = fma(-kd, 0x1.abc9e3b39803fp-56, r);
-    double p = 0x1.ae64567f544e4p-26;
-    p = fma(p, r, 0x1.27e4fb7789f5cp-22);
-    p = fma(p, r, 0x1.71de3a556c734p-19);
-    p = fma(p, r, 0x1.a01a01a01a01ap-16);
-    p = fma(p, r, 0x1.a01a01a01a01ap-13);
-    p = fma(p, r, 0x1.6c16c16c16c17p-10);
-    p = fma(p, r, 0x1.1111111111111p-7);
-    p = fma(p, r, 0x1.5555555555555p-5);
+// For -87 < x < 88 the result is a normal binary32: x = (64m + j) ln2/64 + r
+// with k = 64m + j = rint(64x/ln2), |r| <= ln2/128 + 2^-40 (two fma steps
+// against a split ln2/64), exp(r) the degree-5 Taylor polynomial (truncation
+// below r^6/720 < 2^-54), T[j] = 2^(j/64) rounded to binary64, and
+// y = 2^m T[j] p(r) within 2^-50 relative: under 2^3 units in the last place
+// of the double y. (float)y is the correctly rounded result unless the exact
+// value may lie across a binary32 rounding midpoint, i.e. unless the 29 bits
+// below binary32 precision in y are within 2^11 units of the midpoint
+// pattern 1 << 28 (about one input in 2^17). x <= -104 (with -inf) gives +0,
+// exp(x) being below half the least subnormal. NaN, [-104, -87] and [88, inf]
+// are left to the slow path. `tab(j)` supplies T[j]: a constant-memory
+// table, or (inside a full wave) the lane-held copy of it.
+template <class Tab>
+CHELIS_HD inline float expf_fast(float xf, const Tab &tab, bool &slow) {
+    const bool zero = xf <= -104.0f;
+    const bool fast = xf > -87.0f && xf < 88.0f;
+    slow = !fast && !zero;
+    const double x = fast ? (double)xf : 0.0;
+    const double kd = rint(x * CHELIS_INV_LN2_64);
+    const int k = (int)kd;
+    double r = fma(-kd, CHELIS_LN2_64_HI, x);
+    r = fma(-kd, CHELIS_LN2_64_LO, r);
+    double p = fma(r, 0x1.1111111111111p-7, 0x1.5555555555555p-5);
     p = fma(p, r, 0x1.5555555555555p-3);
-    p = fma(p, r, 0x1.0000000000000p-1);
+    p = fma(p, r, 0.5);
     p = fma(p, r, 1.0);
     p = fma(p, r, 1.0);
-    const double y = ldexp(p, (int)kd);
+    const double y = ldexp(tab(k & 63) * p, k >> 6);
     // 29 bits below binary32 precision, offset so the midpoint pattern is 2047
     const uint32_t below = ((uint32_t)f64_bits(y) & 0x1fffffffu) - (0x10000000u - 2047u);
-    if (below < 4095u) return expf_cr_dd(xf);
-    return (float)y;
+    slow = slow || (fast && below < 4095u);
+    return zero ? 0.0f : (float)y;
+}
+
+struct ExpTableConst {
+    CHELIS_HD double operator()(int j) const { return chelis_exp2_64_tab[j][0]; }
+};
+
+// Correctly rounded binary32 exp (any input): the fast path, else the
+// double-double core. Checked against the CORE-MATH oracle over every
+// binary32 input (tests/test_devmath.py).
+CHELIS_HD inline float expf_cr(float xf) {
+    bool slow;
+    const float y = expf_fast(xf, ExpTableConst{}, slow);
+    return slow ? expf_cr_dd(xf) : y;
 }
 
 // Correctly rounded binary32 v / t from a precomputed binary64 inv = 1 / t

@@ -60,6 +60,18 @@ __device__ inline double exp_leaf<double>(double v) {
     return canon(exp(v));
 }
 
+// 2^(j/64), j = 0..63, held one entry per lane (lane j holds T[j]); a
+// lookup is a wave64 shuffle, so every lane of the wave must be active.
+struct ExpTableLanes {
+    double t;
+    __device__ explicit ExpTableLanes(int lane) : t(chelis_exp2_64_tab[lane][0]) {}
+    __device__ double operator()(int j) const { return __shfl(t, j, 64); }
+};
+
+// The rare correctly rounded fallback stays out of line: inlined 16 times it
+// would dominate the kernel's code.
+__device__ __noinline__ float expf_slow(float x) { return expf_cr_dd(x); }
+
 // Per-row geometry: which row this wave group owns and where it starts.
 template <int W, int R>
 struct RowCoord {
@@ -272,26 +284,70 @@ __global__ __launch_bounds__(64 * W * R) void softmax_kernel(const T *__restrict
             }
     }
     const T m = row_max_plain<T, V, S, W, R>(v, lds, c);
-    // exp(x - m); x - m is NaN only where exp's leaf returns the canonical NaN
-    if (n == (int64_t)S * SEG) {
+    const bool full = n == (int64_t)S * SEG;
+    if constexpr (sizeof(T) == 4) {
+        // exp(x - m): the branch-free fast path for every element (2^(j/64)
+        // from the lane-held table), then one wave-uniform pass of the
+        // correctly rounded core over the few flagged elements.
+        const ExpTableLanes tab(c.lane);
+        T e[S][V];
+        uint32_t flags = 0;
 #pragma unroll
         for (int s = 0; s < S; ++s)
 #pragma unroll
-            for (int i = 0; i < V; ++i) v[s][i] = exp_leaf<T>(v[s][i] - m);
+            for (int i = 0; i < V; ++i) {
+                v[s][i] = v[s][i] - m;
+                bool slow;
+                e[s][i] = expf_fast(v[s][i], tab, slow);
+                flags |= (uint32_t)slow << (s * V + i);
+            }
+        if (__any(flags != 0)) {
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+#pragma unroll
+                for (int i = 0; i < V; ++i)
+                    if (flags & (1u << (s * V + i))) e[s][i] = expf_slow(v[s][i]);
+        }
+        if (!full) {
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+#pragma unroll
+                for (int i = 0; i < V; ++i) {
+                    const int64_t j = (int64_t)s * SEG + (int64_t)c.tid_in_row * V + i;
+                    if (j >= n) e[s][i] = T(-0.0);
+                }
+        }
+        const T total = row_tree_sum<T, V, S, W, R>(e, lds, c);
+        if (total != total) {
+            // a NaN total makes every quotient the canonical NaN
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+#pragma unroll
+                for (int i = 0; i < V; ++i) v[s][i] = canon(total);
+        } else {
+            // total >= 1 (the maximum contributes exp(0)) or +inf: finite
+            // e / total needs no NaN finalization
+            const double inv = 1.0 / (double)total;
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+#pragma unroll
+                for (int i = 0; i < V; ++i) v[s][i] = quot_f32(e[s][i], inv);
+        }
     } else {
+        // exp(x - m); x - m is NaN only where exp's leaf returns the canonical NaN
 #pragma unroll
         for (int s = 0; s < S; ++s)
 #pragma unroll
             for (int i = 0; i < V; ++i) {
                 const int64_t j = (int64_t)s * SEG + (int64_t)c.tid_in_row * V + i;
-                v[s][i] = (j < n) ? exp_leaf<T>(v[s][i] - m) : T(-0.0);
+                v[s][i] = (full || j < n) ? exp_leaf<T>(v[s][i] - m) : T(-0.0);
             }
+        const RowDiv<T> div(canon(row_tree_sum<T, V, S, W, R>(v, lds, c)));
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int i = 0; i < V; ++i) v[s][i] = div(v[s][i]);
     }
-    const RowDiv<T> div(canon(row_tree_sum<T, V, S, W, R>(v, lds, c)));
-#pragma unroll
-    for (int s = 0; s < S; ++s)
-#pragma unroll
-        for (int i = 0; i < V; ++i) v[s][i] = div(v[s][i]);
     store_row<T, V, S, W>(y + c.row * ldy, n, vec_ok, c.tid_in_row, v);
 }
 
