@@ -22,6 +22,7 @@ thread_local char g_error[512] = "";
 std::mutex g_stream_mutex;
 constexpr int kMaxDevices = 64;
 hipStream_t g_streams[kMaxDevices] = {};
+int g_cus[kMaxDevices] = {};
 }  // namespace
 
 int32_t set_error(int32_t status, const char *fmt, ...) {
@@ -42,6 +43,18 @@ hipStream_t stream() {
         g_streams[device] = s;
     }
     return g_streams[device];
+}
+
+int device_cus() {
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) return 0;
+    std::lock_guard<std::mutex> lock(g_stream_mutex);
+    if (!g_cus[device]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return 0;
+        g_cus[device] = n;
+    }
+    return g_cus[device];
 }
 
 int32_t check_tensor(const chelis_gpu_tensor *t, const char *name) {

@@ -16,6 +16,8 @@ namespace chelis {
 // ---- host side ---------------------------------------------------------
 int32_t set_error(int32_t status, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 hipStream_t stream();
+// Compute units of the current device (cached per device; 256 on MI355X).
+int device_cus();
 
 #define CHELIS_HIP_TRY(expr)                                                              \
     do {                                                                                  \

@@ -59,7 +59,7 @@ struct Mfma<double> {
     }
 };
 
-constexpr int BM = 128, BN = 128, THREADS = 256;
+constexpr int THREADS = 256;
 
 template <typename T>
 struct Vec16;
@@ -106,7 +106,7 @@ struct Stage {
 #pragma unroll
             for (int j = 0; j < NV; ++j) {
                 const int idx = t + THREADS * j;
-                const int k = idx / (ROWS / V), rv = (idx % (ROWS / V)) * V;
+                const int k = idx % BK, rv = (idx / BK) * V;
                 const int64_t gr = row0 + rv, gk = k0 + k;
                 const T *p = base + gr + gk * s_k;
                 if (vec_ok && gk < K && gr + V <= rows) {
@@ -144,10 +144,12 @@ struct Stage {
                 *reinterpret_cast<typename Vec16<T>::type *>(s + row * LD + kv) = q;
             }
         } else if constexpr (LAY == 1) {
+            // k fastest across lanes: each transposed store of a wave writes
+            // runs of consecutive k in a few rows instead of one k in 64 rows
 #pragma unroll
             for (int j = 0; j < NV; ++j) {
                 const int idx = t + THREADS * j;
-                const int k = idx / (ROWS / V), rv = (idx % (ROWS / V)) * V;
+                const int k = idx % BK, rv = (idx / BK) * V;
 #pragma unroll
                 for (int u = 0; u < V; ++u) s[(rv + u) * LD + k] = r[j * V + u];
             }
@@ -161,12 +163,22 @@ struct Stage {
     }
 };
 
-template <typename T, int ALAY, int BLAY>
-__global__ __launch_bounds__(THREADS) void gemm_mfma_kernel(GemmProblem p, int64_t tiles_m, int64_t tiles_n,
-                                                            bool a_vec, bool b_vec) {
+// f64 holds its 64x64 accumulators in 128 registers; capping the kernel at
+// 256 registers per lane keeps two waves per SIMD resident (measured 1.6x
+// over one wave at 4096^3). f32 is fastest with the compiler's own choice.
+template <typename T>
+constexpr int kMinWavesPerEu = sizeof(T) == 8 ? 2 : 1;
+
+// TM = 16x16 blocks per wave and dimension: 4 gives the 128 x 128 tile for
+// large products, 2 a 64 x 64 tile for products with few 128-tiles.
+template <typename T, int ALAY, int BLAY, int TM>
+__global__ __launch_bounds__(THREADS, kMinWavesPerEu<T>) void gemm_mfma_kernel(GemmProblem p, int64_t tiles_m,
+                                                                               int64_t tiles_n, bool a_vec,
+                                                                               bool b_vec) {
     using M = Mfma<T>;
     using acc_t = typename M::acc_t;
     constexpr int BK = M::BK, LD = M::LD, KV = BK / 4;
+    constexpr int BM = 32 * TM, BN = 32 * TM, WT = 16 * TM;
     __shared__ __attribute__((aligned(16))) T As[2][BM * LD];
     __shared__ __attribute__((aligned(16))) T Bs[2][BN * LD];
 
@@ -191,11 +203,11 @@ __global__ __launch_bounds__(THREADS) void gemm_mfma_kernel(GemmProblem p, int64
     const int wm = wave >> 1, wn = wave & 1;
     const int fr = lane & 15, fq = lane >> 4;
 
-    acc_t acc[4][4];
+    acc_t acc[TM][TM];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = acc_t{};
+        for (int j = 0; j < TM; ++j) acc[i][j] = acc_t{};
 
     Stage<T, ALAY, BM> sa;
     Stage<T, BLAY, BN> sb;
@@ -213,19 +225,19 @@ __global__ __launch_bounds__(THREADS) void gemm_mfma_kernel(GemmProblem p, int64
             sa.load(A, p.sam, p.sak, m0, p.M, (ks + 1) * BK, p.K, a_vec);
             sb.load(B, p.sbn, p.sbk, n0, p.N, (ks + 1) * BK, p.K, b_vec);
         }
-        typename Vec16<T>::type af[4], bf[4];
+        typename Vec16<T>::type af[TM], bf[TM];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            af[i] = *reinterpret_cast<const typename Vec16<T>::type *>(&As[buf][(wm * 64 + i * 16 + fr) * LD + fq * KV]);
+        for (int i = 0; i < TM; ++i)
+            af[i] = *reinterpret_cast<const typename Vec16<T>::type *>(&As[buf][(wm * WT + i * 16 + fr) * LD + fq * KV]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            bf[j] = *reinterpret_cast<const typename Vec16<T>::type *>(&Bs[buf][(wn * 64 + j * 16 + fr) * LD + fq * KV]);
+        for (int j = 0; j < TM; ++j)
+            bf[j] = *reinterpret_cast<const typename Vec16<T>::type *>(&Bs[buf][(wn * WT + j * 16 + fr) * LD + fq * KV]);
 #pragma unroll
         for (int t = 0; t < KV; ++t)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < TM; ++j)
                     acc[i][j] = M::step(reinterpret_cast<const T *>(&af[i])[t], reinterpret_cast<const T *>(&bf[j])[t],
                                         acc[i][j]);
         if (more) {
@@ -237,13 +249,13 @@ __global__ __launch_bounds__(THREADS) void gemm_mfma_kernel(GemmProblem p, int64
 
     T *C = static_cast<T *>(p.c) + z0 * p.sc0 + z1 * p.sc1;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < TM; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int64_t m = m0 + wm * 64 + i * 16 + M::row(fq, r);
-                const int64_t n = n0 + wn * 64 + j * 16 + fr;
+                const int64_t m = m0 + wm * WT + i * 16 + M::row(fq, r);
+                const int64_t n = n0 + wn * WT + j * 16 + fr;
                 if (m < p.M && n < p.N) C[m * p.scm + n * p.scn] = gemm_epilogue<T>(acc[i][j][r], p, z0, z1, m, n);
             }
 }
@@ -264,9 +276,31 @@ int lay_of(int64_t s_outer, int64_t s_k, const void *base, int64_t outer, int64_
     return 2;
 }
 
-template <typename T, int AL, int BL>
+template <typename T, int AL, int BL, int TM>
 void launch_mfma(const GemmProblem &p, dim3 grid, int64_t tm, int64_t tn, bool av, bool bv, hipStream_t st) {
-    gemm_mfma_kernel<T, AL, BL><<<grid, THREADS, 0, st>>>(p, tm, tn, av, bv);
+    gemm_mfma_kernel<T, AL, BL, TM><<<grid, THREADS, 0, st>>>(p, tm, tn, av, bv);
+}
+
+template <typename T, int TM>
+int32_t run_tiles(const GemmProblem &p, int al, int bl, bool av, bool bv, hipStream_t st) {
+    constexpr int64_t BT = 32 * TM;
+    const int64_t tm = (p.M + BT - 1) / BT, tn = (p.N + BT - 1) / BT;
+    const int64_t nz = p.nb0 * p.nb1;
+    if (tm * tn > 0x7fffffffLL || nz > 65535) return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: grid too large");
+    const dim3 grid((unsigned)(tm * tn), (unsigned)nz);
+    switch (al * 3 + bl) {
+        case 0: launch_mfma<T, 0, 0, TM>(p, grid, tm, tn, av, bv, st); break;
+        case 1: launch_mfma<T, 0, 1, TM>(p, grid, tm, tn, av, bv, st); break;
+        case 2: launch_mfma<T, 0, 2, TM>(p, grid, tm, tn, av, bv, st); break;
+        case 3: launch_mfma<T, 1, 0, TM>(p, grid, tm, tn, av, bv, st); break;
+        case 4: launch_mfma<T, 1, 1, TM>(p, grid, tm, tn, av, bv, st); break;
+        case 5: launch_mfma<T, 1, 2, TM>(p, grid, tm, tn, av, bv, st); break;
+        case 6: launch_mfma<T, 2, 0, TM>(p, grid, tm, tn, av, bv, st); break;
+        case 7: launch_mfma<T, 2, 1, TM>(p, grid, tm, tn, av, bv, st); break;
+        default: launch_mfma<T, 2, 2, TM>(p, grid, tm, tn, av, bv, st); break;
+    }
+    CHELIS_LAUNCH_CHECK();
+    return CHELIS_HIP_OK;
 }
 
 template <typename T>
@@ -274,23 +308,11 @@ int32_t run_mfma(const GemmProblem &p, hipStream_t st) {
     bool av = false, bv = false;
     const int al = lay_of<T>(p.sam, p.sak, p.a, p.M, p.K, &av);
     const int bl = lay_of<T>(p.sbn, p.sbk, p.b, p.N, p.K, &bv);
-    const int64_t tm = (p.M + BM - 1) / BM, tn = (p.N + BN - 1) / BN;
-    const int64_t nz = p.nb0 * p.nb1;
-    if (tm * tn > 0x7fffffffLL || nz > 65535) return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: grid too large");
-    const dim3 grid((unsigned)(tm * tn), (unsigned)nz);
-    switch (al * 3 + bl) {
-        case 0: launch_mfma<T, 0, 0>(p, grid, tm, tn, av, bv, st); break;
-        case 1: launch_mfma<T, 0, 1>(p, grid, tm, tn, av, bv, st); break;
-        case 2: launch_mfma<T, 0, 2>(p, grid, tm, tn, av, bv, st); break;
-        case 3: launch_mfma<T, 1, 0>(p, grid, tm, tn, av, bv, st); break;
-        case 4: launch_mfma<T, 1, 1>(p, grid, tm, tn, av, bv, st); break;
-        case 5: launch_mfma<T, 1, 2>(p, grid, tm, tn, av, bv, st); break;
-        case 6: launch_mfma<T, 2, 0>(p, grid, tm, tn, av, bv, st); break;
-        case 7: launch_mfma<T, 2, 1>(p, grid, tm, tn, av, bv, st); break;
-        default: launch_mfma<T, 2, 2>(p, grid, tm, tn, av, bv, st); break;
-    }
-    CHELIS_LAUNCH_CHECK();
-    return CHELIS_HIP_OK;
+    // 128-tiles when they give every CU two tiles and no dimension is at
+    // most half a tile; 64-tiles otherwise.
+    const int64_t big = ((p.M + 127) / 128) * ((p.N + 127) / 128) * p.nb0 * p.nb1;
+    const bool small = big < 2 * (int64_t)device_cus() || p.M <= 64 || p.N <= 64;
+    return small ? run_tiles<T, 2>(p, al, bl, av, bv, st) : run_tiles<T, 4>(p, al, bl, av, bv, st);
 }
 
 }  // namespace
