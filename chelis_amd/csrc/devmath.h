@@ -116,36 +116,42 @@ CHELIS_HD inline float expf_cr_dd(float xf) {
 // when y is not known to be the correctly rounded result.
 //
 // For -87 < x < 88 the result is a normal binary32: x = (64m + j) ln2/64 + r
-// with k = 64m + j = rint(64x/ln2), |r| <= ln2/128 + 2^-40 (two fma steps
-// against a split ln2/64), exp(r) the degree-5 Taylor polynomial (truncation
-// below r^6/720 < 2^-54), T[j] = 2^(j/64) rounded to binary64, and
-// y = 2^m T[j] p(r) within 2^-50 relative: under 2^3 units in the last place
-// of the double y. (float)y is the correctly rounded result unless the exact
-// value may lie across a binary32 rounding midpoint, i.e. unless the 29 bits
-// below binary32 precision in y are within 2^11 units of the midpoint
-// pattern 1 << 28 (about one input in 2^17). x <= -104 (with -inf) gives +0,
-// exp(x) being below half the least subnormal. NaN, [-104, -87] and [88, inf]
-// are left to the slow path. `tab(j)` supplies T[j]: a constant-memory
-// table, or (inside a full wave) the lane-held copy of it.
+// with k = 64m + j the integer nearest x * 64/ln2, |r| <= ln2/128 + 2^-40
+// (two fma steps against a split ln2/64), exp(r) the degree-4 Taylor
+// polynomial (truncation below r^5/120 < 2^-44.5), T[j] = 2^(j/64) rounded
+// to binary64, and y = 2^m T[j] p(r) within 2^-44.4 relative: under 2^8.7
+// units in the last place of the double y. (float)y is the correctly
+// rounded result unless the exact value may lie across a binary32 rounding
+// midpoint, i.e. unless the 29 bits below binary32 precision in y are
+// within 2^11 units of the midpoint pattern 1 << 28 (about one input in
+// 2^17). x <= -104 (with -inf) gives +0, exp(x) being below half the least
+// subnormal. NaN, [-104, -87] and [88, inf] are left to the slow path; for
+// them the arithmetic below runs on whatever the input is and its value is
+// discarded.
+//
+// k is read from the low word of x * 64/ln2 + 1.5 * 2^52, rounded once by
+// the fma: that sum's unit in the last place is 1, so its low 32 bits are k
+// in two's complement and subtracting the shift gives k exactly (|k| < 2^14
+// on the fast range). `tab(j)` supplies T[j]: a constant-memory table, or
+// (inside a full wave) the lane-held copy of it.
 template <class Tab>
 CHELIS_HD inline float expf_fast(float xf, const Tab &tab, bool &slow) {
     const bool zero = xf <= -104.0f;
     const bool fast = xf > -87.0f && xf < 88.0f;
-    slow = !fast && !zero;
-    const double x = fast ? (double)xf : 0.0;
-    const double kd = rint(x * CHELIS_INV_LN2_64);
-    const int k = (int)kd;
+    const double x = (double)xf;
+    const double shifted = fma(x, CHELIS_INV_LN2_64, 0x1.8p52);
+    const double kd = shifted - 0x1.8p52;
+    const int k = (int)(uint32_t)f64_bits(shifted);
     double r = fma(-kd, CHELIS_LN2_64_HI, x);
     r = fma(-kd, CHELIS_LN2_64_LO, r);
-    double p = fma(r, 0x1.1111111111111p-7, 0x1.5555555555555p-5);
-    p = fma(p, r, 0x1.5555555555555p-3);
+    double p = fma(r, 0x1.5555555555555p-5, 0x1.5555555555555p-3);
     p = fma(p, r, 0.5);
     p = fma(p, r, 1.0);
     p = fma(p, r, 1.0);
     const double y = ldexp(tab(k & 63) * p, k >> 6);
     // 29 bits below binary32 precision, offset so the midpoint pattern is 2047
     const uint32_t below = ((uint32_t)f64_bits(y) & 0x1fffffffu) - (0x10000000u - 2047u);
-    slow = slow || (fast && below < 4095u);
+    slow = (!fast && !zero) || (fast && below < 4095u);
     return zero ? 0.0f : (float)y;
 }
 

@@ -76,6 +76,67 @@ __device__ inline T shfl_xor(T v, int mask) {
     return __shfl_xor(v, mask, 64);
 }
 
+// ---- wave64 joins through DPP (VALU only, no LDS traffic) ----------------
+// Every lane of the wave must be active. A butterfly join of aligned lane
+// blocks: after level m every lane of an aligned 2^m-lane block holds the
+// same block value, so ANY lane of the sibling block is a valid partner.
+// Levels 1 and 2 use quad permutes (xor 1, xor 2), levels 3 and 4 the half
+// mirror (lane i <-> 7 - i in each 8) and mirror (i <-> 15 - i in each 16)
+// of a 16-lane DPP row, and the four row values are read into scalars and
+// joined as (r0 + r1) + (r2 + r3). For a sum this is exactly the canonical
+// adjacent-pair tree over the 64 lanes in lane order.
+enum : int { kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140 };
+
+template <int CTRL>
+__device__ inline float dpp_perm(float v) {
+    return __builtin_bit_cast(float,
+                              __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ inline double dpp_perm(double v) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, 0xF, 0xF, false);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+__device__ inline float read_lane(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+__device__ inline double read_lane(double v, int lane) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, lane);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), lane);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// Canonical tree sum of one value per lane (lane order = leaf order); every
+// lane gets the total. IEEE addition is commutative, so both partners of a
+// join compute the same bits.
+template <typename T>
+__device__ inline T wave_tree_sum(T x) {
+    x = x + dpp_perm<kDppXor1>(x);
+    x = x + dpp_perm<kDppXor2>(x);
+    x = x + dpp_perm<kDppHalfMirror>(x);
+    x = x + dpp_perm<kDppMirror>(x);
+    return (read_lane(x, 0) + read_lane(x, 16)) + (read_lane(x, 32) + read_lane(x, 48));
+}
+
+// Plain IEEE maximum (v_max: a NaN operand yields the other one) over the
+// wave; every lane gets it.
+template <typename T>
+__device__ inline T vmax(T a, T b) {
+    if constexpr (sizeof(T) == 4) return __builtin_fmaxf(a, b);
+    else return __builtin_fmax(a, b);
+}
+template <typename T>
+__device__ inline T wave_vmax(T x) {
+    x = vmax(x, dpp_perm<kDppXor1>(x));
+    x = vmax(x, dpp_perm<kDppXor2>(x));
+    x = vmax(x, dpp_perm<kDppHalfMirror>(x));
+    x = vmax(x, dpp_perm<kDppMirror>(x));
+    return vmax(vmax(read_lane(x, 0), read_lane(x, 16)), vmax(read_lane(x, 32), read_lane(x, 48)));
+}
+
 // [05-OP-12] combine of two adjacent partial maxima, `a` covering the
 // earlier indices: the first NaN wins with its bits, then the larger value,
 // and on equality the earlier stored representation.

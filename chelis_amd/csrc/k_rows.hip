@@ -29,16 +29,33 @@
 namespace chelis {
 namespace {
 
+// 16-byte native vectors (the nontemporal builtins take clang vector types).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef double f64x2 __attribute__((ext_vector_type(2)));
 template <typename T, int V>
 struct VecT;
 template <>
 struct VecT<float, 4> {
-    using type = float4;
+    using type = f32x4;
 };
 template <>
 struct VecT<double, 2> {
-    using type = double2;
+    using type = f64x2;
 };
+
+// Streaming rows are read once and written once: NT selects the
+// nontemporal (streaming) cache policy for them; vectors shared by every row
+// (layer norm's gamma and beta) use the default policy.
+template <bool NT, typename Q>
+__device__ inline Q vload(const Q *p) {
+    if constexpr (NT) return __builtin_nontemporal_load(p);
+    else return *p;
+}
+template <bool NT, typename Q>
+__device__ inline void vstore(Q v, Q *p) {
+    if constexpr (NT) __builtin_nontemporal_store(v, p);
+    else *p = v;
+}
 
 template <typename T>
 __device__ inline T neg_inf() {
@@ -88,7 +105,7 @@ struct RowCoord {
     }
 };
 
-template <typename T, int V, int S, int W>
+template <typename T, int V, int S, int W, bool NT = true>
 __device__ inline void load_row(const T *__restrict__ p, int64_t n, bool vec_ok, int tid_in_row, T pad,
                                 T (&v)[S][V]) {
     constexpr int SEG = 64 * W * V;
@@ -96,7 +113,7 @@ __device__ inline void load_row(const T *__restrict__ p, int64_t n, bool vec_ok,
     for (int s = 0; s < S; ++s) {
         const int64_t base = (int64_t)s * SEG + (int64_t)tid_in_row * V;
         if (vec_ok && base + V <= n) {
-            typename VecT<T, V>::type q = *reinterpret_cast<const typename VecT<T, V>::type *>(p + base);
+            typename VecT<T, V>::type q = vload<NT>(reinterpret_cast<const typename VecT<T, V>::type *>(p + base));
             const T *qe = reinterpret_cast<const T *>(&q);
 #pragma unroll
             for (int i = 0; i < V; ++i) v[s][i] = qe[i];
@@ -118,7 +135,7 @@ __device__ inline void store_row(T *__restrict__ p, int64_t n, bool vec_ok, int 
             T *qe = reinterpret_cast<T *>(&q);
 #pragma unroll
             for (int i = 0; i < V; ++i) qe[i] = v[s][i];
-            *reinterpret_cast<typename VecT<T, V>::type *>(p + base) = q;
+            vstore<true>(q, reinterpret_cast<typename VecT<T, V>::type *>(p + base));
         } else {
 #pragma unroll
             for (int i = 0; i < V; ++i)
@@ -140,10 +157,7 @@ __device__ inline T row_tree_sum(const T (&v)[S][V], T *lds, const RowCoord<W, R
         for (int w = V; w > 1; w >>= 1)
 #pragma unroll
             for (int i = 0; i < w / 2; ++i) a[i] = a[2 * i] + a[2 * i + 1];
-        T x = a[0];
-#pragma unroll
-        for (int m = 1; m < 64; m <<= 1) x = x + shfl_xor(x, m);
-        seg[s] = x;
+        seg[s] = wave_tree_sum(a[0]);
     }
     if constexpr (W > 1) {
         if (c.lane == 0)
@@ -170,42 +184,6 @@ __device__ inline T row_tree_sum(const T (&v)[S][V], T *lds, const RowCoord<W, R
     return seg[0];
 }
 
-// [05-OP-12] maximum over the padded row, in index order.
-template <typename T, int V, int S, int W, int R>
-__device__ inline T row_max(const T (&v)[S][V], T *lds, const RowCoord<W, R> &c) {
-    T seg[S];
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-        T x = v[s][0];
-#pragma unroll
-        for (int i = 1; i < V; ++i) x = max_first(x, v[s][i]);
-#pragma unroll
-        for (int m = 1; m < 64; m <<= 1) {
-            T o = shfl_xor(x, m);
-            x = (c.lane & m) ? max_first(o, x) : max_first(x, o);
-        }
-        seg[s] = x;
-    }
-    if constexpr (W > 1) {
-        if (c.lane == 0)
-#pragma unroll
-            for (int s = 0; s < S; ++s) lds[(c.row_in_block * W + c.wave_in_row) * S + s] = seg[s];
-        __syncthreads();
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-            T x = lds[(c.row_in_block * W) * S + s];
-#pragma unroll
-            for (int w = 1; w < W; ++w) x = max_first(x, lds[(c.row_in_block * W + w) * S + s]);
-            seg[s] = x;
-        }
-        __syncthreads();
-    }
-    T x = seg[0];
-#pragma unroll
-    for (int s = 1; s < S; ++s) x = max_first(x, seg[s]);
-    return x;
-}
-
 // Plain IEEE maximum over the padded row (v_max: a NaN operand yields the
 // other one, and +0/-0 ties are unordered). Softmax uses it in place of
 // [05-OP-12]'s first-NaN / first-representation rule because the two give
@@ -214,11 +192,6 @@ __device__ inline T row_max(const T (&v)[S][V], T *lds, const RowCoord<W, R> &c)
 // either rule; and a zero maximum enters only through x - m, where
 // x - (+0) and x - (-0) differ at most in the sign of a zero, which exp maps
 // to the same 1.
-template <typename T>
-__device__ inline T vmax(T a, T b) {
-    if constexpr (sizeof(T) == 4) return __builtin_fmaxf(a, b);
-    else return __builtin_fmax(a, b);
-}
 template <typename T, int V, int S, int W, int R>
 __device__ inline T row_max_plain(const T (&v)[S][V], T *lds, const RowCoord<W, R> &c) {
     T x = v[0][0];
@@ -226,8 +199,7 @@ __device__ inline T row_max_plain(const T (&v)[S][V], T *lds, const RowCoord<W, 
     for (int s = 0; s < S; ++s)
 #pragma unroll
         for (int i = 0; i < V; ++i) x = vmax(x, v[s][i]);
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) x = vmax(x, shfl_xor(x, m));
+    x = wave_vmax(x);
     if constexpr (W > 1) {
         if (c.lane == 0) lds[c.row_in_block * W + c.wave_in_row] = x;
         __syncthreads();
@@ -405,12 +377,12 @@ __global__ __launch_bounds__(64 * W * R) void layer_norm_kernel(const T *__restr
     const T var = canon(canon(row_tree_sum<T, V, S, W, R>(q, lds, c)) / extent);
     const T denom = canon(sqrt(canon(var + eps)));
     // gamma/beta are [n] vectors shared by every row
-    load_row<T, V, S, W>(gamma, n, vec_ok, c.tid_in_row, T(0), q);
+    load_row<T, V, S, W, false>(gamma, n, vec_ok, c.tid_in_row, T(0), q);
 #pragma unroll
     for (int s = 0; s < S; ++s)
 #pragma unroll
         for (int i = 0; i < V; ++i) v[s][i] = canon(canon(v[s][i] / denom) * q[s][i]);
-    load_row<T, V, S, W>(beta, n, vec_ok, c.tid_in_row, T(0), q);
+    load_row<T, V, S, W, false>(beta, n, vec_ok, c.tid_in_row, T(0), q);
 #pragma unroll
     for (int s = 0; s < S; ++s)
 #pragma unroll
@@ -466,7 +438,9 @@ int32_t launch_rows(RowOp op, const RowArgs &a) {
     const int64_t n = a.n;
     if (n <= seg1) return launch_shape<T, V, 1, 1, 4>(op, a, st);
     if (n <= 2 * seg1) return launch_shape<T, V, 2, 1, 4>(op, a, st);
-    if (n <= 4 * seg1) return launch_shape<T, V, 4, 1, 4>(op, a, st);
+    // one row per 64-lane block: blocks retire independently, so the waves
+    // of a CU drift apart and one wave's loads overlap another's arithmetic
+    if (n <= 4 * seg1) return launch_shape<T, V, 4, 1, 1>(op, a, st);
     if (n <= 8 * seg1) return launch_shape<T, V, 8, 1, 2>(op, a, st);
     if (n <= 16 * seg1) return launch_shape<T, V, 4, 4, 1>(op, a, st);
     if (n <= 32 * seg1) return launch_shape<T, V, 8, 4, 1>(op, a, st);
