@@ -133,11 +133,14 @@ CHELIS_HD inline float expf_cr_dd(float xf) {
 // the fma: that sum's unit in the last place is 1, so its low 32 bits are k
 // in two's complement and subtracting the shift gives k exactly (|k| < 2^14
 // on the fast range). `tab(j)` supplies T[j]: a constant-memory table, or
-// (inside a full wave) the lane-held copy of it.
-template <class Tab>
+// (inside a full wave) the lane-held copy of it. NONPOS instances serve
+// arguments known to be <= 0 or NaN (softmax's x - max): the upper range
+// test is dropped, and a positive argument would take the fast path
+// unchecked, so callers must not pass one.
+template <bool NONPOS = false, class Tab>
 CHELIS_HD inline float expf_fast(float xf, const Tab &tab, bool &slow) {
     const bool zero = xf <= -104.0f;
-    const bool fast = xf > -87.0f && xf < 88.0f;
+    const bool fast = NONPOS ? xf > -87.0f : (xf > -87.0f && xf < 88.0f);
     const double x = (double)xf;
     const double shifted = fma(x, CHELIS_INV_LN2_64, 0x1.8p52);
     const double kd = shifted - 0x1.8p52;
@@ -165,6 +168,15 @@ struct ExpTableConst {
 CHELIS_HD inline float expf_cr(float xf) {
     bool slow;
     const float y = expf_fast(xf, ExpTableConst{}, slow);
+    return slow ? expf_cr_dd(xf) : y;
+}
+
+// expf_cr restricted to arguments <= 0 or NaN, through the NONPOS fast
+// path. Checked against the CORE-MATH oracle over every binary32 input with
+// the sign bit set, +0 and every positive NaN (tests/test_devmath.py).
+CHELIS_HD inline float expf_cr_nonpos(float xf) {
+    bool slow;
+    const float y = expf_fast<true>(xf, ExpTableConst{}, slow);
     return slow ? expf_cr_dd(xf) : y;
 }
 

@@ -85,6 +85,31 @@ struct ExpTableLanes {
     __device__ double operator()(int j) const { return __shfl(t, j, 64); }
 };
 
+// Which of a lane's NE exp results need the correctly rounded fallback.
+// Up to 16 per lane: one wave-uniform lane mask per element (scalar
+// registers, set straight from the compare); beyond that: a per-lane bit set.
+template <int NE, bool UNIFORM = (NE <= 16)>
+struct SlowSet;
+template <int NE>
+struct SlowSet<NE, true> {
+    uint64_t lanes[NE];
+    uint64_t all = 0;
+    __device__ void set(int k, bool slow) {
+        lanes[k] = __ballot(slow);
+        all |= lanes[k];
+    }
+    __device__ bool any() const { return all != 0; }
+    __device__ bool has(int k, int lane) const { return (lanes[k] >> lane) & 1u; }
+};
+template <int NE>
+struct SlowSet<NE, false> {
+    static_assert(NE <= 64, "one bit per element");
+    uint64_t bits = 0;
+    __device__ void set(int k, bool slow) { bits |= (uint64_t)slow << k; }
+    __device__ bool any() const { return __any(bits != 0); }
+    __device__ bool has(int k, int) const { return (bits >> k) & 1u; }
+};
+
 // The rare correctly rounded fallback stays out of line: inlined 16 times it
 // would dominate the kernel's code.
 __device__ __noinline__ float expf_slow(float x) { return expf_cr_dd(x); }
@@ -229,56 +254,58 @@ struct RowDiv {
     }
 };
 
-// softmax over the last axis, optionally of where(j <= i, x * scale, -inf)
-// (causal != 0, q_len = rows per score matrix).
+// The value softmax takes x - max of: element j of a row, optionally
+// as where(j <= qi, x * scale, -inf) (masked 1: causal, masked 2: scale only).
+template <typename T>
+__device__ inline T softmax_arg(T raw, int64_t j, int64_t qi, int masked, T scale) {
+    if (!masked) return raw;
+    const T sc = canon(raw * scale);
+    return (masked == 2 || j <= qi) ? sc : neg_inf<T>();
+}
+
+// One row: v holds the raw row (padding -inf) on entry and the softmax on
+// exit; xr is the row in memory (re-read only by the rare exp fallback).
 template <typename T, int V, int S, int W, int R>
-__global__ __launch_bounds__(64 * W * R) void softmax_kernel(const T *__restrict__ x, T *__restrict__ y,
-                                                              int64_t rows, int64_t n, int64_t ldx, int64_t ldy,
-                                                              bool vec_ok, int masked, T scale, int64_t q_len) {
-    __shared__ T lds[R * W * S];
-    RowCoord<W, R> c;
-    if (c.row >= rows) return;  // whole row groups exit together (R rows per block, W waves each)
-    const T *xr = x + c.row * ldx;
-    T v[S][V];
-    load_row<T, V, S, W>(xr, n, vec_ok, c.tid_in_row, neg_inf<T>(), v);
+__device__ inline void softmax_row(T (&v)[S][V], const T *__restrict__ xr, int64_t row, int64_t n, int masked,
+                                   T scale, int64_t q_len, T *lds, const RowCoord<W, R> &c) {
     constexpr int SEG = 64 * W * V;
+    const int64_t qi = masked ? row % q_len : 0;
     if (masked) {
-        const int64_t qi = c.row % q_len;
 #pragma unroll
         for (int s = 0; s < S; ++s)
 #pragma unroll
             for (int i = 0; i < V; ++i) {
                 const int64_t j = (int64_t)s * SEG + (int64_t)c.tid_in_row * V + i;
-                if (j < n) {
-                    T sc = canon(v[s][i] * scale);
-                    v[s][i] = (masked == 2 || j <= qi) ? sc : neg_inf<T>();
-                }
+                if (j < n) v[s][i] = softmax_arg(v[s][i], j, qi, masked, scale);
             }
     }
     const T m = row_max_plain<T, V, S, W, R>(v, lds, c);
     const bool full = n == (int64_t)S * SEG;
     if constexpr (sizeof(T) == 4) {
-        // exp(x - m): the branch-free fast path for every element (2^(j/64)
-        // from the lane-held table), then one wave-uniform pass of the
-        // correctly rounded core over the few flagged elements.
+        // exp(x - m) in place: the branch-free fast path for every element
+        // (2^(j/64) from the lane-held table), then one wave-uniform pass of
+        // the correctly rounded core over the few flagged elements, whose
+        // argument is formed again from the row in memory. x - m is <= 0 or
+        // NaN (m is the row maximum), so the NONPOS path applies.
         const ExpTableLanes tab(c.lane);
-        T e[S][V];
-        uint32_t flags = 0;
+        SlowSet<S * V> flagged;
 #pragma unroll
         for (int s = 0; s < S; ++s)
 #pragma unroll
             for (int i = 0; i < V; ++i) {
-                v[s][i] = v[s][i] - m;
                 bool slow;
-                e[s][i] = expf_fast(v[s][i], tab, slow);
-                flags |= (uint32_t)slow << (s * V + i);
+                v[s][i] = expf_fast<true>(v[s][i] - m, tab, slow);
+                flagged.set(s * V + i, slow);
             }
-        if (__any(flags != 0)) {
+        if (flagged.any()) {
 #pragma unroll
             for (int s = 0; s < S; ++s)
 #pragma unroll
-                for (int i = 0; i < V; ++i)
-                    if (flags & (1u << (s * V + i))) e[s][i] = expf_slow(v[s][i]);
+                for (int i = 0; i < V; ++i) {
+                    const int64_t j = (int64_t)s * SEG + (int64_t)c.tid_in_row * V + i;
+                    if (flagged.has(s * V + i, c.lane) && (full || j < n))
+                        v[s][i] = expf_slow(softmax_arg(xr[j], j, qi, masked, scale) - m);
+                }
         }
         if (!full) {
 #pragma unroll
@@ -286,10 +313,10 @@ __global__ __launch_bounds__(64 * W * R) void softmax_kernel(const T *__restrict
 #pragma unroll
                 for (int i = 0; i < V; ++i) {
                     const int64_t j = (int64_t)s * SEG + (int64_t)c.tid_in_row * V + i;
-                    if (j >= n) e[s][i] = T(-0.0);
+                    if (j >= n) v[s][i] = T(-0.0);
                 }
         }
-        const T total = row_tree_sum<T, V, S, W, R>(e, lds, c);
+        const T total = row_tree_sum<T, V, S, W, R>(v, lds, c);
         if (total != total) {
             // a NaN total makes every quotient the canonical NaN
 #pragma unroll
@@ -303,7 +330,7 @@ __global__ __launch_bounds__(64 * W * R) void softmax_kernel(const T *__restrict
 #pragma unroll
             for (int s = 0; s < S; ++s)
 #pragma unroll
-                for (int i = 0; i < V; ++i) v[s][i] = quot_f32(e[s][i], inv);
+                for (int i = 0; i < V; ++i) v[s][i] = quot_f32(v[s][i], inv);
         }
     } else {
         // exp(x - m); x - m is NaN only where exp's leaf returns the canonical NaN
@@ -320,6 +347,28 @@ __global__ __launch_bounds__(64 * W * R) void softmax_kernel(const T *__restrict
 #pragma unroll
             for (int i = 0; i < V; ++i) v[s][i] = div(v[s][i]);
     }
+}
+
+// softmax over the last axis, optionally of where(j <= i, x * scale, -inf)
+// (causal != 0, q_len = rows per score matrix). DENSE instances serve the
+// common case (no mask, row length equal to the register capacity S*64W*V,
+// 16-byte aligned rows) with every bound test folded away.
+template <typename T, int V, int S, int W, int R, bool DENSE>
+__global__ __launch_bounds__(64 * W * R) void softmax_kernel(const T *__restrict__ x, T *__restrict__ y,
+                                                              int64_t rows, int64_t n_arg, int64_t ldx, int64_t ldy,
+                                                              bool vec_ok_arg, int masked_arg, T scale,
+                                                              int64_t q_len) {
+    __shared__ T lds[R * W * S];
+    constexpr int SEG = 64 * W * V;
+    const int64_t n = DENSE ? (int64_t)S * SEG : n_arg;
+    const bool vec_ok = DENSE || vec_ok_arg;
+    const int masked = DENSE ? 0 : masked_arg;
+    RowCoord<W, R> c;
+    if (c.row >= rows) return;  // whole row groups exit together (R rows per block, W waves each)
+    const T *xr = x + c.row * ldx;
+    T v[S][V];
+    load_row<T, V, S, W>(xr, n, vec_ok, c.tid_in_row, neg_inf<T>(), v);
+    softmax_row<T, V, S, W, R>(v, xr, c.row, n, masked, scale, q_len, lds, c);
     store_row<T, V, S, W>(y + c.row * ldy, n, vec_ok, c.tid_in_row, v);
 }
 
@@ -411,8 +460,12 @@ int32_t launch_shape(RowOp op, const RowArgs &a, hipStream_t st) {
     const dim3 block(64 * W * R);
     switch (op) {
         case RowOp::Softmax:
-            softmax_kernel<T, V, S, W, R><<<grid, block, 0, st>>>(
-                (const T *)a.a, (T *)a.out, a.rows, a.n, a.lda, a.ldo, a.vec_ok, a.masked, (T)a.scale, a.q_len);
+            if (!a.masked && a.vec_ok && a.n == (int64_t)S * 64 * W * V)
+                softmax_kernel<T, V, S, W, R, true><<<grid, block, 0, st>>>(
+                    (const T *)a.a, (T *)a.out, a.rows, a.n, a.lda, a.ldo, a.vec_ok, a.masked, (T)a.scale, a.q_len);
+            else
+                softmax_kernel<T, V, S, W, R, false><<<grid, block, 0, st>>>(
+                    (const T *)a.a, (T *)a.out, a.rows, a.n, a.lda, a.ldo, a.vec_ok, a.masked, (T)a.scale, a.q_len);
             break;
         case RowOp::SoftmaxAdjoint:
             softmax_adjoint_kernel<T, V, S, W, R><<<grid, block, 0, st>>>(

@@ -1,4 +1,5 @@
-// Host check of chelis::expf_cr against the CORE-MATH oracle (test only).
+// Host check of chelis::expf_cr and chelis::expf_cr_nonpos against the
+// CORE-MATH oracle (test only).
 // Usage: expf_check STRIDE  -> checks every STRIDE-th binary32 bit pattern,
 // prints the number of mismatching results and the first few inputs.
 #include <cstdio>
@@ -20,6 +21,14 @@ int main(int argc, char **argv) {
         if (got != want) {
             ++mismatches;
             if (mismatches < 8) std::printf("mismatch x=%08x got=%08x want=%08x\n", bits, got, want);
+        }
+        // the non-positive specialization: sign bit set, +0, positive NaNs
+        if ((bits >> 31) || bits == 0u || (bits & 0x7fffffffu) > 0x7f800000u) {
+            uint32_t got_np = chelis::f32_bits(chelis::expf_cr_nonpos(x));
+            if (got_np != want) {
+                ++mismatches;
+                if (mismatches < 8) std::printf("nonpos mismatch x=%08x got=%08x want=%08x\n", bits, got_np, want);
+            }
         }
     }
     std::printf("checked %lld mismatches %lld\n", count, mismatches);
