@@ -42,5 +42,6 @@ int32_t gemm_mfma(chelis_dtype dt, const GemmProblem &p, hipStream_t st);
 int32_t gemm_tree_wave(chelis_dtype dt, const GemmProblem &p, hipStream_t st);    // one wave per output
 int32_t gemm_tree_tiled(chelis_dtype dt, const GemmProblem &p, hipStream_t st);   // narrow N, long K
 int32_t gemm_tree_thread(chelis_dtype dt, const GemmProblem &p, hipStream_t st);  // short K
+int32_t gemm_tree_panel(chelis_dtype dt, const GemmProblem &p, hipStream_t st);   // min(M, N) <= 64
 
 }  // namespace chelis

@@ -24,6 +24,8 @@
 // free; the final NaN is canonicalized.
 #include "gemm.h"
 
+#include <algorithm>
+
 namespace chelis {
 namespace {
 
@@ -234,6 +236,256 @@ __global__ __launch_bounds__(64 * WAVES) void tree_tiled_kernel(GemmProblem p, b
     }
 }
 
+// ---------------------------------------------------------------- column panel
+// Narrow products (N <= 64, after swapping the operand roles when M is the
+// narrow side: c^T = b^T a^T has the same products in the same K order).
+// Lane l of every wave owns output column l and each wave owns RM rows, so
+// the A value of a product is the same for the whole wave. Per chunk of KC
+// leaves the workgroup stages, one chunk ahead (double buffered in LDS), the
+// A tile [RM*WAVES rows x KC] and the B panel [KC x 64 columns] with
+// coalesced loads; a wave then reads its A values as wave-uniform
+// (broadcast) LDS loads and B with one 64-lane load per pair of leaves,
+// shared by its RM products of each leaf. Operands of the next leaf pair are
+// read while the current pair computes.
+//
+// Each output streams its leaves in order through a static KC-leaf tree
+// (the unrolled leaf index fixes every join at compile time) and the chunk
+// totals through a carry stack of depth D whose branches are wave-uniform.
+// A workgroup covers one aligned power-of-two block of kpart leaves
+// (blockIdx.y); the canonical tree over K equals the full tree over K
+// padded with -0.0, which is the full tree over those block totals, so with
+// more than one block the totals go to a workspace and tree_combine_kernel
+// joins them in tree order.
+struct PanelView {
+    const void *a, *b;
+    int64_t M, N, K;
+    int64_t sam, sak, sbk, sbn;
+    int64_t sa0, sa1, sb0, sb1;
+    bool swapped;  // view (m, n) is output (n, m) of the problem
+};
+
+// Output element of view coordinates (z, m, n) through the problem's
+// epilogue.
+template <typename T>
+__device__ inline void panel_store(const GemmProblem &p, const PanelView &v, int64_t z0, int64_t z1, int64_t m,
+                                   int64_t n, T acc) {
+    const int64_t om = v.swapped ? n : m, on = v.swapped ? m : n;
+    T *C = static_cast<T *>(p.c) + z0 * p.sc0 + z1 * p.sc1;
+    C[om * p.scm + on * p.scn] = gemm_epilogue<T>(acc, p, z0, z1, om, on);
+}
+
+// Leaf i (compile-time after unrolling) of a static tree of 2^LV leaves; after
+// the last leaf the tree's total is in lv[LV - 1].
+template <typename T, int LV>
+__device__ inline void static_push(T (&lv)[LV], int i, T carry) {
+    bool done = false;
+#pragma unroll
+    for (int d = 0; d < LV; ++d) {
+        if (!done) {
+            if ((i >> d) & 1) {
+                carry = lv[d] + carry;
+            } else {
+                lv[d] = carry;
+                done = true;
+            }
+        }
+    }
+    if (!done) lv[LV - 1] = carry;
+}
+
+template <typename T>
+struct Pair;
+template <>
+struct Pair<float> {
+    typedef float type __attribute__((ext_vector_type(2)));
+};
+template <>
+struct Pair<double> {
+    typedef double type __attribute__((ext_vector_type(2)));
+};
+
+// One chunk of KC leaves for a wave's RM outputs: A from the wave-uniform
+// tile rows r0.., B from the lane's column. TAIL chunks end at `live`
+// leaves; the rest are -0.0. The operands of leaf pair i + 2 are read while
+// pair i computes, so the LDS latency overlaps the arithmetic.
+template <typename T, int RM, int KC, int LV, bool TAIL>
+__device__ __attribute__((always_inline)) inline void panel_chunk(T (&lv)[RM][LV], const T (&Bc)[KC][64],
+                                                                  const T (*Ac)[KC], int r0, int lane, int live) {
+    using P2 = typename Pair<T>::type;
+    T b[2], bn[2];
+    P2 a[RM], an[RM];
+    b[0] = Bc[0][lane], b[1] = Bc[1][lane];
+#pragma unroll
+    for (int r = 0; r < RM; ++r) a[r] = *reinterpret_cast<const P2 *>(&Ac[r0 + r][0]);
+#pragma unroll
+    for (int i = 0; i < KC; i += 2) {
+        if (i + 2 < KC) {
+            bn[0] = Bc[i + 2][lane], bn[1] = Bc[i + 3][lane];
+#pragma unroll
+            for (int r = 0; r < RM; ++r) an[r] = *reinterpret_cast<const P2 *>(&Ac[r0 + r][i + 2]);
+        }
+#pragma unroll
+        for (int r = 0; r < RM; ++r) {
+            T x0 = a[r][0] * b[0], x1 = a[r][1] * b[1];
+            if constexpr (TAIL) {
+                if (i >= live) x0 = T(-0.0);
+                if (i + 1 >= live) x1 = T(-0.0);
+            }
+            static_push<T, LV>(lv[r], i, x0);
+            static_push<T, LV>(lv[r], i + 1, x1);
+        }
+        if (i + 2 < KC) {
+            b[0] = bn[0], b[1] = bn[1];
+#pragma unroll
+            for (int r = 0; r < RM; ++r) a[r] = an[r];
+        }
+    }
+}
+
+template <typename T, int RM, int WAVES, int KC, int D, bool PARTIAL, bool AVEC>
+__global__ __launch_bounds__(64 * WAVES) void tree_panel_kernel(PanelView v, GemmProblem p, int64_t kpart,
+                                                                 T *__restrict__ part) {
+    constexpr int LV = __builtin_ctz(KC);
+    constexpr int ROWS = RM * WAVES;
+    constexpr int BPER = KC / WAVES;                // B elements staged per thread
+    constexpr int APER = ROWS * KC / (64 * WAVES);  // A elements staged per thread (a contiguous run)
+    static_assert((KC & (KC - 1)) == 0 && KC % WAVES == 0 && APER == 2, "chunk shape");
+    using P2 = typename Pair<T>::type;
+    __shared__ T Bs[2][KC][64];
+    __shared__ __attribute__((aligned(16))) T As[2][ROWS][KC];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t z = blockIdx.z, z0 = z / p.nb1, z1 = z % p.nb1;
+    const int64_t mg = (int64_t)blockIdx.x * ROWS;  // first row of the workgroup
+    const int64_t k_lo = (int64_t)blockIdx.y * kpart;
+    const int64_t k_hi = k_lo + kpart < v.K ? k_lo + kpart : v.K;
+    const int64_t nchunk = (k_hi - k_lo + KC - 1) / KC;
+    const T *A = static_cast<const T *>(v.a) + z0 * v.sa0 + z1 * v.sa1;
+    const T *B = static_cast<const T *>(v.b) + z0 * v.sb0 + z1 * v.sb1;
+    const bool col_ok = lane < v.N;
+    // this thread's A run: tile row ar, leaves ac, ac + 1
+    const int ar = tid / (KC / APER), ac = (tid % (KC / APER)) * APER;
+    const bool arow_ok = mg + ar < v.M;
+    const T *Arow = A + (arow_ok ? mg + ar : 0) * v.sam;
+
+    T sb[BPER], sa[APER];
+    auto fetch = [&](int64_t kc) {
+#pragma unroll
+        for (int j = 0; j < BPER; ++j) {
+            const int64_t k = kc + wave + WAVES * j;
+            sb[j] = (k < k_hi && col_ok) ? B[k * v.sbk + lane * v.sbn] : T(0);
+        }
+        const int64_t k = kc + ac;
+        if (AVEC && arow_ok && k + APER <= k_hi) {
+            const P2 q = *reinterpret_cast<const P2 *>(Arow + k);
+            sa[0] = q[0], sa[1] = q[1];
+        } else {
+#pragma unroll
+            for (int u = 0; u < APER; ++u) sa[u] = (arow_ok && k + u < k_hi) ? Arow[(k + u) * v.sak] : T(0);
+        }
+    };
+    auto put = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < BPER; ++j) Bs[buf][wave + WAVES * j][lane] = sb[j];
+        P2 q;
+        q[0] = sa[0], q[1] = sa[1];
+        *reinterpret_cast<P2 *>(&As[buf][ar][ac]) = q;
+    };
+    fetch(k_lo);
+    put(0);
+    __syncthreads();
+
+    T lvl[RM][D];
+    for (int64_t c = 0; c < nchunk; ++c) {
+        const int buf = (int)(c & 1);
+        const int64_t kc = k_lo + c * KC;
+        if (c + 1 < nchunk) fetch(kc + KC);
+        T lv[RM][LV];
+        if (kc + KC <= k_hi)
+            panel_chunk<T, RM, KC, LV, false>(lv, Bs[buf], As[buf], wave * RM, lane, 0);
+        else  // the last, partial chunk: leaves at k >= k_hi are -0.0
+            panel_chunk<T, RM, KC, LV, true>(lv, Bs[buf], As[buf], wave * RM, lane, (int)(k_hi - kc));
+        // chunk totals into the carry stacks: the chunk index is wave-uniform,
+        // so each level is one uniform branch for all RM outputs
+        const int t = __builtin_ctzll(~(unsigned long long)c);
+        T carry[RM];
+#pragma unroll
+        for (int r = 0; r < RM; ++r) carry[r] = lv[r][LV - 1];
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            if (d < t) {
+#pragma unroll
+                for (int r = 0; r < RM; ++r) carry[r] = lvl[r][d] + carry[r];
+            } else if (d == t) {
+#pragma unroll
+                for (int r = 0; r < RM; ++r) lvl[r][d] = carry[r];
+            }
+        }
+        // the other buffer was last read in chunk c - 1, before the barrier
+        // that closed it
+        if (c + 1 < nchunk) put(buf ^ 1);
+        __syncthreads();
+    }
+    if (!col_ok) return;
+#pragma unroll
+    for (int r = 0; r < RM; ++r) {
+        const int64_t m = mg + wave * RM + r;
+        if (m >= v.M) break;
+        T total = T(0);
+        bool found = false;
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+            if ((nchunk >> d) & 1) {
+                total = found ? lvl[r][d] + total : lvl[r][d];
+                found = true;
+            }
+        if constexpr (PARTIAL) {
+            part[(((int64_t)blockIdx.y * gridDim.z + z) * v.M + m) * 64 + lane] = total;
+        } else {
+            panel_store<T>(p, v, z0, z1, m, lane, total);
+        }
+    }
+}
+
+// Join the per-block totals of tree_panel_kernel: the canonical tree over
+// the nparts block totals (adjacent pairs, odd one carried), then the
+// epilogue. One thread per output.
+template <typename T>
+__global__ __launch_bounds__(256) void tree_combine_kernel(PanelView v, GemmProblem p, const T *__restrict__ part,
+                                                           int64_t nparts, int64_t nz) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t per_z = v.M * 64;
+    if (idx >= nz * per_z) return;
+    const int64_t n = idx % 64;
+    if (n >= v.N) return;
+    const int64_t z = idx / per_z, m = (idx / 64) % v.M;
+    T lvl[8];
+    for (int64_t j = 0; j < nparts; ++j) {
+        T carry = part[j * nz * per_z + idx];
+        bool done = false;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            if (!done) {
+                if ((j >> d) & 1) {
+                    carry = lvl[d] + carry;
+                } else {
+                    lvl[d] = carry;
+                    done = true;
+                }
+            }
+        }
+    }
+    T total = T(0);
+    bool found = false;
+#pragma unroll
+    for (int d = 0; d < 8; ++d)
+        if ((nparts >> d) & 1) {
+            total = found ? lvl[d] + total : lvl[d];
+            found = true;
+        }
+    panel_store<T>(p, v, z / p.nb1, z % p.nb1, m, n, total);
+}
+
 // ---------------------------------------------------------------- thread per output
 // Short K: one thread per output, leaves streamed straight into its carry
 // stack (depth 12, K <= 4096), n fastest so B and C accesses coalesce.
@@ -312,6 +564,58 @@ int32_t run_tiled(const GemmProblem &p, hipStream_t st) {
     return CHELIS_HIP_OK;
 }
 
+// Column-panel launch: RM = 4 rows per wave, 4 waves, KC = 32 leaves per
+// chunk, D = 5 carry levels (a block of up to 2^(D-1) = 16 chunks, 512
+// leaves, leaves its total in level D - 1). The K block size kpart shrinks
+// (powers of two, >= KC) until the grid holds about four workgroups per CU.
+template <typename T>
+int32_t run_panel(const GemmProblem &p, hipStream_t st) {
+    constexpr int RM = 4, WAVES = 4, KC = 32, D = 5;
+    PanelView v{};
+    v.swapped = p.N > 64;
+    if (!v.swapped) {
+        v.a = p.a, v.b = p.b, v.M = p.M, v.N = p.N, v.sam = p.sam, v.sak = p.sak, v.sbk = p.sbk, v.sbn = p.sbn;
+        v.sa0 = p.sa0, v.sa1 = p.sa1, v.sb0 = p.sb0, v.sb1 = p.sb1;
+    } else {
+        v.a = p.b, v.b = p.a, v.M = p.N, v.N = p.M, v.sam = p.sbn, v.sak = p.sbk, v.sbk = p.sak, v.sbn = p.sam;
+        v.sa0 = p.sb0, v.sa1 = p.sb1, v.sb0 = p.sa0, v.sb1 = p.sa1;
+    }
+    v.K = p.K;
+    if (v.N > 64) return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: panel kernel needs min(M, N) <= 64");
+    const int64_t nz = p.nb0 * p.nb1;
+    const int64_t gx = (v.M + RM * WAVES - 1) / (RM * WAVES);
+    int64_t p2 = KC;
+    while (p2 < v.K) p2 <<= 1;
+    int64_t kpart = std::min<int64_t>(p2, (int64_t)KC << (D - 1));
+    const int64_t want = 4 * (int64_t)std::max(device_cus(), 1);
+    while (kpart > KC && gx * nz * ((v.K + kpart - 1) / kpart) < want) kpart >>= 1;
+    const int64_t nparts = (v.K + kpart - 1) / kpart;
+    if (gx > 0x7fffffffLL || nparts > 255 || nz > 65535)
+        return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: panel grid too large");
+    const dim3 grid((unsigned)gx, (unsigned)nparts, (unsigned)nz);
+    // A runs load as one 2-element vector: unit K stride, aligned rows
+    const bool avec = v.sak == 1 && (reinterpret_cast<uintptr_t>(v.a) % (2 * sizeof(T))) == 0 && v.sam % 2 == 0 &&
+                      v.sa0 % 2 == 0 && v.sa1 % 2 == 0;
+    T *ws = nullptr;
+    if (nparts > 1)
+        CHELIS_HIP_TRY(hipMallocAsync(reinterpret_cast<void **>(&ws), (size_t)nparts * nz * v.M * 64 * sizeof(T), st));
+    if (nparts == 1) {
+        if (avec) tree_panel_kernel<T, RM, WAVES, KC, D, false, true><<<grid, 64 * WAVES, 0, st>>>(v, p, kpart, ws);
+        else tree_panel_kernel<T, RM, WAVES, KC, D, false, false><<<grid, 64 * WAVES, 0, st>>>(v, p, kpart, ws);
+    } else {
+        if (avec) tree_panel_kernel<T, RM, WAVES, KC, D, true, true><<<grid, 64 * WAVES, 0, st>>>(v, p, kpart, ws);
+        else tree_panel_kernel<T, RM, WAVES, KC, D, true, false><<<grid, 64 * WAVES, 0, st>>>(v, p, kpart, ws);
+    }
+    hipError_t le = hipGetLastError();
+    if (le == hipSuccess && nparts > 1) {
+        tree_combine_kernel<T><<<grid_for(nz * v.M * 64, 256), 256, 0, st>>>(v, p, ws, nparts, nz);
+        le = hipGetLastError();
+    }
+    if (ws) CHELIS_HIP_TRY(hipFreeAsync(ws, st));
+    if (le != hipSuccess) return set_error(CHELIS_HIP_EHIP, "kernel launch: %s", hipGetErrorString(le));
+    return CHELIS_HIP_OK;
+}
+
 template <typename T>
 int32_t run_thread(const GemmProblem &p, hipStream_t st) {
     if (p.K > (int64_t(1) << TD)) return set_error(CHELIS_HIP_EDOMAIN, "matmul: short-K kernel holds K <= %d", 1 << TD);
@@ -330,6 +634,9 @@ int32_t gemm_tree_wave(chelis_dtype dt, const GemmProblem &p, hipStream_t st) {
 }
 int32_t gemm_tree_tiled(chelis_dtype dt, const GemmProblem &p, hipStream_t st) {
     return dt == CHELIS_DTYPE_F32 ? run_tiled<float>(p, st) : run_tiled<double>(p, st);
+}
+int32_t gemm_tree_panel(chelis_dtype dt, const GemmProblem &p, hipStream_t st) {
+    return dt == CHELIS_DTYPE_F32 ? run_panel<float>(p, st) : run_panel<double>(p, st);
 }
 int32_t gemm_tree_thread(chelis_dtype dt, const GemmProblem &p, hipStream_t st) {
     return dt == CHELIS_DTYPE_F32 ? run_thread<float>(p, st) : run_thread<double>(p, st);

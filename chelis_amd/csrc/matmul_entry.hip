@@ -5,9 +5,10 @@
 // crates/chelis-backend-hip/src/emit.rs:4718-4842):
 //   K <= 32                      -> tree_thread (short K, bit-exact)
 //   M == 1 or N == 1             -> tree_wave   (GEMV, HBM bound, bit-exact)
-//   CHELIS_MATMUL_EXACT          -> tree_tiled  (bit-exact, any shape)
-//   min(M, N) < 16, or f64 with min(M, N) <= 64
-//                                -> tree_tiled  (skinny, bit-exact)
+//   min(M, N) <= 64 and (CHELIS_MATMUL_EXACT, min(M, N) < 16 or f64)
+//                                -> tree_panel  (narrow side on the lanes,
+//                                   bit-exact)
+//   CHELIS_MATMUL_EXACT          -> tree_tiled  (bit-exact, any other shape)
 //   otherwise                    -> MFMA tiles  (dense; rounding differs
 //                                   from the canonical tree)
 #include "gemm.h"
@@ -125,7 +126,9 @@ int32_t dispatch(chelis_dtype dt, const GemmProblem &p, int32_t flags) {
     const int64_t narrow = std::min(p.M, p.N);
     if (p.K <= 32) return gemm_tree_thread(dt, p, st);
     if (p.M == 1 || p.N == 1) return gemm_tree_wave(dt, p, st);
-    if ((flags & CHELIS_MATMUL_EXACT) || narrow < 16 || (f64 && narrow <= 64)) return gemm_tree_tiled(dt, p, st);
+    const bool exact = flags & CHELIS_MATMUL_EXACT;
+    if (narrow <= 64 && (exact || narrow < 16 || f64)) return gemm_tree_panel(dt, p, st);
+    if (exact) return gemm_tree_tiled(dt, p, st);
     return gemm_mfma(dt, p, st);
 }
 

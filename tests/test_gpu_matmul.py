@@ -68,6 +68,12 @@ TREE_CASES = [
     (100, 10, 3000, False, False),  # skinny (the MLP's d . W2 form)
     (512, 10, 1024, True, False),   # skinny, transposed A (d^T . g_z2)
     (50, 13, 513, False, True),     # skinny, transposed B
+    # column-panel kernel (narrow side <= 64 on the lanes)
+    (70, 64, 640, False, False),    # N = 64, ragged row groups, K a multiple of the 64-leaf chunk
+    (40, 300, 700, False, False),   # M is the narrow side: operand roles swapped
+    (33, 129, 777, True, True),     # swapped, both transposed
+    (900, 48, 5000, False, False),  # several aligned K blocks and a partial last chunk
+    (20, 5, 2049, False, True),     # tiny grid: many K blocks, last block one leaf
 ]
 
 
@@ -79,7 +85,10 @@ def test_tree_kernels_bit_exact(case, dtype):
     a, b = rand(rng, (M, K), dtype), rand(rng, (K, N), dtype)
     _da, va, na = dev_view(a, M, K, ta)
     _db, vb, nb = dev_view(b, K, N, tb)
-    c = C.matmul(va, vb).numpy()
+    # f32 with a narrow side of 16..64 is an MFMA shape; the exact flag keeps
+    # it on the canonical tree (the column-panel kernel)
+    exact = dtype == np.float32 and K > 32 and min(M, N) >= 16
+    c = C.matmul(va, vb, exact=exact).numpy()
     ref = O.matmul(na, nb)
     assert bits_equal(c, ref), first_diff(c, ref)
 
@@ -98,6 +107,18 @@ def test_f64_skinny_band_is_exact():
     a, b = rand(rng, (700, 900), np.float64), rand(rng, (900, 64), np.float64)
     c = C.matmul(C.to_device(a), C.to_device(b)).numpy()
     assert bits_equal(c, O.matmul(a, b))
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_exact_flag_narrow_f32_and_batched_panel(dtype):
+    """A batch of narrow products (the panel kernel over blockIdx.z), with a
+    broadcast batch operand, and the exact flag on a 16 <= N <= 64 shape."""
+    rng = np.random.default_rng(23)
+    a, b = rand(rng, (3, 150, 600), dtype), rand(rng, (600, 40), dtype)
+    c = C.matmul(C.to_device(a), C.to_device(b), exact=True).numpy()
+    assert c.shape == (3, 150, 40)
+    for i in range(3):
+        assert bits_equal(c[i], O.matmul(a[i], b)), i
 
 
 def test_empty_contraction_is_positive_zero():
@@ -200,6 +221,17 @@ def test_linear_epilogue_bit_exact_on_tree_path(act):
         assert ok.all()
     else:
         assert bits_equal(c, v)
+
+
+def test_linear_epilogue_on_swapped_panel_path():
+    """A narrow M (< 16) with N > 64 runs as c^T = w^T x^T; the bias and
+    residual must still follow the output's own axes."""
+    rng = np.random.default_rng(43)
+    x, w = rand(rng, (8, 300), np.float32), rand(rng, (300, 500), np.float32)
+    bias, res = rand(rng, (500,), np.float32), rand(rng, (8, 500), np.float32)
+    c = C.linear(C.to_device(x), C.to_device(w), C.to_device(bias), "relu", C.to_device(res)).numpy()
+    v = (res + O.relu((O.matmul(x, w) + bias).astype(np.float32))).astype(np.float32)
+    assert bits_equal(c, v), first_diff(c, v)
 
 
 def test_linear_epilogue_on_mfma_path():
