@@ -19,10 +19,16 @@ struct GemmProblem {
     int64_t sa0, sa1, sb0, sb1, sc0, sc1;   // batch strides
     // fused epilogue (graph order): v = mm; v = v + bias[n]; act; v = resid + v
     const void *bias;
-    int64_t sbias;
+    int64_t sbias, sbias0, sbias1;  // along n, batch axis 0, batch axis 1
     int32_t act;
     const void *resid;
     int64_t srm, srn, sr0, sr1;
+    // Causal attention structure (honoured by the MFMA tiles, ignored - so
+    // computed in full - elsewhere): 1 = only entries with n <= m are used
+    // downstream, tiles wholly above the diagonal are skipped and left as
+    // they were; 2 = a[m][k] is zero for k > m, the contraction of a row
+    // tile stops after its last row.
+    int32_t causal;
 };
 
 // Epilogue of one output element, each step finalized at the dtype so the
@@ -30,7 +36,7 @@ struct GemmProblem {
 template <typename T>
 __device__ inline T gemm_epilogue(T acc, const GemmProblem &p, int64_t z0, int64_t z1, int64_t m, int64_t n) {
     T v = canon(acc);
-    if (p.bias) v = canon(v + static_cast<const T *>(p.bias)[n * p.sbias]);
+    if (p.bias) v = canon(v + static_cast<const T *>(p.bias)[z0 * p.sbias0 + z1 * p.sbias1 + n * p.sbias]);
     if (p.act == CHELIS_ACT_RELU) v = v < T(0) ? T(0) : v;
     else if (p.act == CHELIS_ACT_GELU) v = gelu_one<T>(v);
     if (p.resid) v = canon(static_cast<const T *>(p.resid)[z0 * p.sr0 + z1 * p.sr1 + m * p.srm + n * p.srn] + v);
@@ -38,6 +44,9 @@ __device__ inline T gemm_epilogue(T acc, const GemmProblem &p, int64_t z0, int64
 }
 
 int32_t gemm_mfma(chelis_dtype dt, const GemmProblem &p, hipStream_t st);
+// c = a . b for attention with the causal mode above (programs only).
+int32_t matmul_causal(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b, const chelis_gpu_tensor *c,
+                      int32_t mode);
 // Canonical-tree kernels: bit-exact with the [05-OP-30] matmul.
 int32_t gemm_tree_wave(chelis_dtype dt, const GemmProblem &p, hipStream_t st);    // one wave per output
 int32_t gemm_tree_tiled(chelis_dtype dt, const GemmProblem &p, hipStream_t st);   // narrow N, long K

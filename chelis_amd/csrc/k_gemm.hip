@@ -193,6 +193,10 @@ __global__ __launch_bounds__(THREADS, kMinWavesPerEu<T>) void gemm_mfma_kernel(G
     const int64_t in_group = bid % (GM * tiles_n);
     const int64_t m0 = (first + in_group % gsz) * BM;
     const int64_t n0 = (in_group / gsz) * BN;
+    // causal 1: a tile wholly above the diagonal is never read (the whole
+    // workgroup leaves before any barrier); causal 2: a[m][k] = 0 for k > m
+    if (p.causal == 1 && n0 > m0 + BM - 1) return;
+    const int64_t K = (p.causal == 2 && m0 + BM < p.K) ? m0 + BM : p.K;
 
     const int64_t z = blockIdx.y;
     const int64_t z0 = z / p.nb1, z1 = z % p.nb1;
@@ -211,9 +215,9 @@ __global__ __launch_bounds__(THREADS, kMinWavesPerEu<T>) void gemm_mfma_kernel(G
 
     Stage<T, ALAY, BM> sa;
     Stage<T, BLAY, BN> sb;
-    const int64_t ksteps = (p.K + BK - 1) / BK;
-    sa.load(A, p.sam, p.sak, m0, p.M, 0, p.K, a_vec);
-    sb.load(B, p.sbn, p.sbk, n0, p.N, 0, p.K, b_vec);
+    const int64_t ksteps = (K + BK - 1) / BK;
+    sa.load(A, p.sam, p.sak, m0, p.M, 0, K, a_vec);
+    sb.load(B, p.sbn, p.sbk, n0, p.N, 0, K, b_vec);
     sa.store(As[0]);
     sb.store(Bs[0]);
     __syncthreads();
@@ -222,8 +226,8 @@ __global__ __launch_bounds__(THREADS, kMinWavesPerEu<T>) void gemm_mfma_kernel(G
         const int buf = ks & 1;
         const bool more = ks + 1 < ksteps;
         if (more) {
-            sa.load(A, p.sam, p.sak, m0, p.M, (ks + 1) * BK, p.K, a_vec);
-            sb.load(B, p.sbn, p.sbk, n0, p.N, (ks + 1) * BK, p.K, b_vec);
+            sa.load(A, p.sam, p.sak, m0, p.M, (ks + 1) * BK, K, a_vec);
+            sb.load(B, p.sbn, p.sbk, n0, p.N, (ks + 1) * BK, K, b_vec);
         }
         typename Vec16<T>::type af[TM], bf[TM];
 #pragma unroll

@@ -133,6 +133,15 @@ int32_t dispatch(chelis_dtype dt, const GemmProblem &p, int32_t flags) {
 }
 
 }  // namespace
+
+int32_t matmul_causal(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b, const chelis_gpu_tensor *c,
+                      int32_t mode) {
+    GemmProblem p;
+    if (int32_t s = build_problem(a, b, c, &p, "matmul")) return s;
+    p.causal = mode;
+    return dispatch(a->dtype, p, 0);
+}
+
 }  // namespace chelis
 
 using namespace chelis;
@@ -155,14 +164,26 @@ extern "C" int32_t chelis_hip_linear(const chelis_gpu_tensor *a, const chelis_gp
     if (flags & ~CHELIS_MATMUL_EXACT) return set_error(CHELIS_HIP_EDOMAIN, "linear: unknown flags %d", flags);
     if (activation < CHELIS_ACT_NONE || activation > CHELIS_ACT_GELU)
         return set_error(CHELIS_HIP_EDOMAIN, "linear: unknown activation %d", activation);
-    if (a->rank < 2 || b->rank != 2) return set_error(CHELIS_HIP_EDOMAIN, "linear: a needs rank >= 2 and b rank 2");
+    if (a->rank < 2 || b->rank < 2) return set_error(CHELIS_HIP_EDOMAIN, "linear: a and b need rank >= 2");
     p.act = activation;
     if (bias) {
         if (int32_t s = check_tensor(bias, "bias")) return s;
-        if (bias->dtype != a->dtype || bias->rank != 1 || bias->shape[0] != p.N)
-            return set_error(CHELIS_HIP_EDOMAIN, "linear: bias must be [N] of the operand dtype");
+        // [N], or [batch..., N] over the result's batch axes (c is [batch..., M, N])
+        const int32_t nbatch = c->rank - 2;
+        bool ok = bias->dtype == a->dtype && bias->rank >= 1 && bias->shape[bias->rank - 1] == p.N;
+        if (ok && bias->rank > 1) {
+            ok = bias->rank == nbatch + 1;
+            for (int32_t i = 0; ok && i < nbatch; ++i) ok = bias->shape[i] == c->shape[i];
+        }
+        if (!ok)
+            return set_error(CHELIS_HIP_EDOMAIN, "linear: bias must be [N] or [batch..., N] of the operand dtype");
         p.bias = bias->data;
-        p.sbias = bias->strides[0];
+        p.sbias = bias->strides[bias->rank - 1];
+        if (bias->rank > 1) {
+            // batch axes are right-aligned in the problem: one axis is z1, two are z0, z1
+            p.sbias1 = bias->strides[bias->rank - 2];
+            p.sbias0 = bias->rank > 2 ? bias->strides[bias->rank - 3] : 0;
+        }
     }
     if (residual) {
         if (int32_t s = check_tensor(residual, "residual")) return s;

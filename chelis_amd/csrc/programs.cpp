@@ -16,6 +16,7 @@
 #include <vector>
 
 #include "chelis_programs.h"
+#include "gemm.h"
 #include "hip_common.h"
 
 namespace chelis {
@@ -232,9 +233,12 @@ extern "C" int32_t chelis_prog_transformer_block(const chelis_gpu_tensor *const 
     TRY(chelis_hip_linear(&h, P[2], P[3], CHELIS_ACT_NONE, nullptr, &q, 0));
     TRY(chelis_hip_linear(&h, P[4], P[5], CHELIS_ACT_NONE, nullptr, &k, 0));
     TRY(chelis_hip_linear(&h, P[6], P[7], CHELIS_ACT_NONE, nullptr, &v, 0));
-    TRY(chelis_hip_matmul(&qh, &kt, &s, 0));
+    // causal: score tiles above the diagonal are masked to -inf by the
+    // softmax without being read, and P is exactly +0 there, so those tiles
+    // and contraction terms are skipped
+    TRY(matmul_causal(&qh, &kt, &s, 1));
     TRY(chelis_hip_scaled_masked_softmax(&s, 1.0 / 8.0, 1, &s));
-    TRY(chelis_hip_matmul(&s, &vh, &oh, 0));
+    TRY(matmul_causal(&s, &vh, &oh, 2));
     TRY(chelis_hip_linear(&o, P[8], P[9], CHELIS_ACT_NONE, &x2, &x1, 0));
     // feed-forward
     TRY(chelis_hip_layer_norm(&x1, P[10], P[11], 1e-5, &h));

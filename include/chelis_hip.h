@@ -149,7 +149,10 @@ int32_t chelis_hip_matmul(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b
 /* matmul with a fused epilogue, applied per element of the f32/f64 result
  * in graph order: v = mm; if bias: v = v + bias[n]; act 1: v = relu(v),
  * act 2: v = gelu(v); if residual: v = residual + v. Each step finalizes
- * at the dtype, so the bits equal the unfused graph's. */
+ * at the dtype, so the bits equal the unfused graph's. `bias` is [N], shared
+ * by every batch entry, or [batch..., N] with the result's batch axes (one
+ * bias row per batch entry, e.g. a stack of projections sharing one input).
+ * b may carry batch axes as in chelis_hip_matmul. */
 enum { CHELIS_ACT_NONE = 0, CHELIS_ACT_RELU = 1, CHELIS_ACT_GELU = 2 };
 int32_t chelis_hip_linear(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b, const chelis_gpu_tensor *bias,
                           int32_t activation, const chelis_gpu_tensor *residual, const chelis_gpu_tensor *c,

@@ -234,6 +234,25 @@ def test_linear_epilogue_on_swapped_panel_path():
     assert bits_equal(c, v), first_diff(c, v)
 
 
+def test_linear_per_batch_bias():
+    """A stack of projections: a broadcast over the batch, b and bias with one
+    entry per batch ([batch, K, N] and [batch, N]), bit-exact on the tree
+    path; and the same on an MFMA shape within tolerance."""
+    rng = np.random.default_rng(44)
+    x = rand(rng, (96, 200), np.float64)
+    w, bias = rand(rng, (3, 200, 40), np.float64), rand(rng, (3, 40), np.float64)
+    dx = C.to_device(x)
+    x3 = dx.view((3, 96, 200), (0, 200, 1))
+    c = C.linear(x3, C.to_device(w), C.to_device(bias)).numpy()
+    for j in range(3):
+        assert bits_equal(c[j], O.matmul(x, w[j]) + bias[j]), j
+    xf = rand(rng, (256, 128), np.float32)
+    wf, bf = rand(rng, (3, 128, 192), np.float32), rand(rng, (3, 192), np.float32)
+    cf = C.linear(C.to_device(xf).view((3, 256, 128), (0, 128, 1)), C.to_device(wf), C.to_device(bf)).numpy()
+    for j in range(3):
+        check_close(cf[j], (O.matmul(xf, wf[j]) + bf[j]).astype(np.float32), np.float32)
+
+
 def test_linear_epilogue_on_mfma_path():
     rng = np.random.default_rng(42)
     x, w = rand(rng, (512, 256), np.float32), rand(rng, (256, 384), np.float32)
