@@ -29,15 +29,16 @@
 namespace chelis {
 namespace {
 
-constexpr int MAXD = 24;  // carry-stack depth: up to 2^24 segments
+constexpr int MAXD = 24;  // carry-stack depth: up to 2^23 segments
 
-// Push one block total into a wave-uniform carry stack (count = index of
-// this block). Unrolled with static indices so the stack stays in VGPRs.
-template <typename T>
-__device__ inline void carry_push(T (&lvl)[MAXD], int64_t count, T carry) {
+// Push one block total into a wave-uniform carry stack of depth DEPTH (count
+// = index of this block, below 2^DEPTH). Unrolled with static indices so
+// the stack stays in VGPRs.
+template <typename T, int DEPTH>
+__device__ inline void carry_push(T (&lvl)[DEPTH], int64_t count, T carry) {
     bool done = false;
 #pragma unroll
-    for (int d = 0; d < MAXD; ++d) {
+    for (int d = 0; d < DEPTH; ++d) {
         if (!done) {
             if ((count >> d) & 1) {
                 carry = lvl[d] + carry;
@@ -49,12 +50,12 @@ __device__ inline void carry_push(T (&lvl)[MAXD], int64_t count, T carry) {
     }
 }
 
-template <typename T>
-__device__ inline T carry_total(const T (&lvl)[MAXD], int64_t count) {
+template <typename T, int DEPTH>
+__device__ inline T carry_total(const T (&lvl)[DEPTH], int64_t count) {
     T total = T(0);
     bool found = false;
 #pragma unroll
-    for (int d = 0; d < MAXD; ++d) {
+    for (int d = 0; d < DEPTH; ++d) {
         if ((count >> d) & 1) {
             total = found ? lvl[d] + total : lvl[d];
             found = true;
@@ -86,17 +87,19 @@ struct Vec16<double> {
 };
 
 // V elements at p[0], p[s], ..., zero where k >= K; vector loads when the
-// run is contiguous, aligned and complete.
-template <typename T, int V, bool CONTIG>
+// run is contiguous, aligned and complete (NT: streaming, read-once data).
+template <typename T, int V, bool CONTIG, bool NT = false>
 __device__ inline void load_run(const T *__restrict__ p, int64_t s, int64_t k, int64_t K, bool vec_ok, T (&x)[V]) {
     if (CONTIG && vec_ok && k + V <= K) {
         constexpr int W = Vec16<T>::W;
+        typedef T nv __attribute__((ext_vector_type(Vec16<T>::W)));
 #pragma unroll
         for (int q = 0; q < V / W; ++q) {
-            typename Vec16<T>::type v = reinterpret_cast<const typename Vec16<T>::type *>(p)[q];
-            const T *e = reinterpret_cast<const T *>(&v);
+            nv v;
+            if constexpr (NT) v = __builtin_nontemporal_load(reinterpret_cast<const nv *>(p) + q);
+            else v = reinterpret_cast<const nv *>(p)[q];
 #pragma unroll
-            for (int u = 0; u < W; ++u) x[q * W + u] = e[u];
+            for (int u = 0; u < W; ++u) x[q * W + u] = v[u];
         }
     } else {
 #pragma unroll
@@ -107,7 +110,7 @@ __device__ inline void load_run(const T *__restrict__ p, int64_t s, int64_t k, i
 // ---------------------------------------------------------------- wave per output
 // GEMV-class shapes: one wave streams one output's K products, 64*V leaves
 // per segment, fully coalesced when the operand is K-contiguous.
-template <typename T, int V, bool AK, bool BK>
+template <typename T, int V, bool AK, bool BK, int DEPTH>
 __global__ __launch_bounds__(256) void tree_wave_kernel(GemmProblem p, int64_t outputs, bool a_vec, bool b_vec) {
     const int lane = threadIdx.x & 63;
     const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -118,7 +121,7 @@ __global__ __launch_bounds__(256) void tree_wave_kernel(GemmProblem p, int64_t o
     const T *B = static_cast<const T *>(p.b) + z0 * p.sb0 + z1 * p.sb1 + n * p.sbn;
     constexpr int SEG = 64 * V;
     const int64_t nseg = (p.K + SEG - 1) / SEG;
-    T lvl[MAXD];
+    T lvl[DEPTH];
     for (int64_t s = 0; s < nseg; ++s) {
         const int64_t k = s * SEG + (int64_t)lane * V;
         T a[V], b[V];
@@ -126,14 +129,11 @@ __global__ __launch_bounds__(256) void tree_wave_kernel(GemmProblem p, int64_t o
         load_run<T, V, BK>(B + k * p.sbk, p.sbk, k, p.K, b_vec, b);
 #pragma unroll
         for (int u = 0; u < V; ++u) a[u] = (k + u < p.K) ? a[u] * b[u] : T(-0.0);
-        T x = tree_v<T, V>(a);
-#pragma unroll
-        for (int msk = 1; msk < 64; msk <<= 1) x = x + shfl_xor(x, msk);
-        carry_push<T>(lvl, s, x);
+        carry_push<T, DEPTH>(lvl, s, wave_tree_sum(tree_v<T, V>(a)));
     }
     if (lane == 0) {
         T *C = static_cast<T *>(p.c) + z0 * p.sc0 + z1 * p.sc1;
-        C[m * p.scm + n * p.scn] = gemm_epilogue<T>(carry_total<T>(lvl, nseg), p, z0, z1, m, n);
+        C[m * p.scm + n * p.scn] = gemm_epilogue<T>(carry_total<T, DEPTH>(lvl, nseg), p, z0, z1, m, n);
     }
 }
 
@@ -224,14 +224,14 @@ __global__ __launch_bounds__(64 * WAVES) void tree_tiled_kernel(GemmProblem p, b
         T x = part[0];
 #pragma unroll
         for (int msk = P; msk < 64; msk <<= 1) x = x + shfl_xor(x, msk);
-        carry_push<T>(lvl, s, x);
+        carry_push<T, MAXD>(lvl, s, x);
     }
     const int o = lane % P;
     if (lane < P) {
         const int64_t m = m_base + o / NJ, n = n0 + o % NJ;
         if (m < p.M && n < p.N) {
             T *C = static_cast<T *>(p.c) + z0 * p.sc0 + z1 * p.sc1;
-            C[m * p.scm + n * p.scn] = gemm_epilogue<T>(carry_total<T>(lvl, nseg), p, z0, z1, m, n);
+            C[m * p.scm + n * p.scn] = gemm_epilogue<T>(carry_total<T, MAXD>(lvl, nseg), p, z0, z1, m, n);
         }
     }
 }
@@ -538,10 +538,20 @@ int32_t run_wave(const GemmProblem &p, hipStream_t st) {
     const bool bv = bk && aligned16(p.b) && p.sbn % W == 0 && p.sb0 % W == 0 && p.sb1 % W == 0;
     const int64_t blocks = (outputs + 3) / 4;
     if (blocks > 0x7fffffffLL) return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: too many outputs");
-    if (ak && bk) tree_wave_kernel<T, V, true, true><<<(unsigned)blocks, 256, 0, st>>>(p, outputs, av, bv);
-    else if (ak) tree_wave_kernel<T, V, true, false><<<(unsigned)blocks, 256, 0, st>>>(p, outputs, av, bv);
-    else if (bk) tree_wave_kernel<T, V, false, true><<<(unsigned)blocks, 256, 0, st>>>(p, outputs, av, bv);
-    else tree_wave_kernel<T, V, false, false><<<(unsigned)blocks, 256, 0, st>>>(p, outputs, av, bv);
+    // carry depth: DEPTH levels hold up to 2^(DEPTH - 1) segments (the last
+    // push of 2^d segments lands in level d), so 9 levels cover K up to
+    // 256 * 64 * V
+    const bool shallow = (p.K + 64 * V - 1) / (64 * V) <= (int64_t(1) << 8);
+#define CHELIS_WAVE(A_, B_)                                                                                \
+    do {                                                                                                    \
+        if (shallow) tree_wave_kernel<T, V, A_, B_, 9><<<(unsigned)blocks, 256, 0, st>>>(p, outputs, av, bv);    \
+        else tree_wave_kernel<T, V, A_, B_, MAXD><<<(unsigned)blocks, 256, 0, st>>>(p, outputs, av, bv);         \
+    } while (0)
+    if (ak && bk) CHELIS_WAVE(true, true);
+    else if (ak) CHELIS_WAVE(true, false);
+    else if (bk) CHELIS_WAVE(false, true);
+    else CHELIS_WAVE(false, false);
+#undef CHELIS_WAVE
     CHELIS_LAUNCH_CHECK();
     return CHELIS_HIP_OK;
 }

@@ -65,6 +65,8 @@ TREE_CASES = [
     (300, 1, 1000, False, False),   # GEMV
     (300, 1, 1000, True, False),    # GEMV, transposed A (linreg X^T r form)
     (1, 257, 4097, False, False),   # row vector times matrix
+    (3, 1, 131072, False, False),   # GEMV: f64 exactly 256 segments (shallow carry stack)
+    (2, 1, 131073, False, False),   # one leaf more: the deep carry stack
     (100, 10, 3000, False, False),  # skinny (the MLP's d . W2 form)
     (512, 10, 1024, True, False),   # skinny, transposed A (d^T . g_z2)
     (50, 13, 513, False, True),     # skinny, transposed B
