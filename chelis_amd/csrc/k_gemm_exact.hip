@@ -576,29 +576,24 @@ int32_t run_tiled(const GemmProblem &p, hipStream_t st) {
 
 // Column-panel launch: RM = 4 rows per wave, 4 waves, KC = 32 leaves per
 // chunk, D = 5 carry levels (a block of up to 2^(D-1) = 16 chunks, 512
-// leaves, leaves its total in level D - 1). The K block size kpart shrinks
-// (powers of two, >= KC) until the grid holds about four workgroups per CU.
-template <typename T>
-int32_t run_panel(const GemmProblem &p, hipStream_t st) {
-    constexpr int RM = 4, WAVES = 4, KC = 32, D = 5;
-    PanelView v{};
-    v.swapped = p.N > 64;
-    if (!v.swapped) {
-        v.a = p.a, v.b = p.b, v.M = p.M, v.N = p.N, v.sam = p.sam, v.sak = p.sak, v.sbk = p.sbk, v.sbn = p.sbn;
-        v.sa0 = p.sa0, v.sa1 = p.sa1, v.sb0 = p.sb0, v.sb1 = p.sb1;
-    } else {
-        v.a = p.b, v.b = p.a, v.M = p.N, v.N = p.M, v.sam = p.sbn, v.sak = p.sbk, v.sbk = p.sak, v.sbn = p.sam;
-        v.sa0 = p.sb0, v.sa1 = p.sb1, v.sb0 = p.sa0, v.sb1 = p.sa1;
-    }
-    v.K = p.K;
-    if (v.N > 64) return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: panel kernel needs min(M, N) <= 64");
+// leaves, leaves its total in level D - 1). The K block size shrinks
+// (powers of two, >= KC) until the grid holds about four workgroups per CU;
+// the block totals are joined by tree_combine_kernel. Measured on the MLP's
+// narrow products: the extra workgroups outweigh the combine pass even for
+// products of a few million terms (one deep block per row group is slower).
+template <typename T, int D>
+int32_t launch_panel(const GemmProblem &p, const PanelView &v, bool cut, hipStream_t st) {
+    constexpr int RM = 4, WAVES = 4, KC = 32;
     const int64_t nz = p.nb0 * p.nb1;
     const int64_t gx = (v.M + RM * WAVES - 1) / (RM * WAVES);
     int64_t p2 = KC;
     while (p2 < v.K) p2 <<= 1;
     int64_t kpart = std::min<int64_t>(p2, (int64_t)KC << (D - 1));
     const int64_t want = 4 * (int64_t)std::max(device_cus(), 1);
-    while (kpart > KC && gx * nz * ((v.K + kpart - 1) / kpart) < want) kpart >>= 1;
+    // (the combine pass joins at most 255 block totals)
+    while (cut && kpart > KC && gx * nz * ((v.K + kpart - 1) / kpart) < want &&
+           (v.K + kpart / 2 - 1) / (kpart / 2) <= 255)
+        kpart >>= 1;
     const int64_t nparts = (v.K + kpart - 1) / kpart;
     if (gx > 0x7fffffffLL || nparts > 255 || nz > 65535)
         return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: panel grid too large");
@@ -624,6 +619,22 @@ int32_t run_panel(const GemmProblem &p, hipStream_t st) {
     if (ws) CHELIS_HIP_TRY(hipFreeAsync(ws, st));
     if (le != hipSuccess) return set_error(CHELIS_HIP_EHIP, "kernel launch: %s", hipGetErrorString(le));
     return CHELIS_HIP_OK;
+}
+
+template <typename T>
+int32_t run_panel(const GemmProblem &p, hipStream_t st) {
+    PanelView v{};
+    v.swapped = p.N > 64;
+    if (!v.swapped) {
+        v.a = p.a, v.b = p.b, v.M = p.M, v.N = p.N, v.sam = p.sam, v.sak = p.sak, v.sbk = p.sbk, v.sbn = p.sbn;
+        v.sa0 = p.sa0, v.sa1 = p.sa1, v.sb0 = p.sb0, v.sb1 = p.sb1;
+    } else {
+        v.a = p.b, v.b = p.a, v.M = p.N, v.N = p.M, v.sam = p.sbn, v.sak = p.sbk, v.sbk = p.sak, v.sbn = p.sam;
+        v.sa0 = p.sb0, v.sa1 = p.sb1, v.sb0 = p.sa0, v.sb1 = p.sa1;
+    }
+    v.K = p.K;
+    if (v.N > 64) return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: panel kernel needs min(M, N) <= 64");
+    return launch_panel<T, 5>(p, v, true, st);
 }
 
 template <typename T>

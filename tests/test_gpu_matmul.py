@@ -75,7 +75,8 @@ TREE_CASES = [
     (40, 300, 700, False, False),   # M is the narrow side: operand roles swapped
     (33, 129, 777, True, True),     # swapped, both transposed
     (900, 48, 5000, False, False),  # several aligned K blocks and a partial last chunk
-    (20, 5, 2049, False, True),     # tiny grid: many K blocks, last block one leaf
+    (20, 5, 2049, False, True),     # small product: one K block of 2049 leaves
+    (30, 7, 9000, True, False),     # small product, K past one deep block: three blocks and a combine
 ]
 
 
