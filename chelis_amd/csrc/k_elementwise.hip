@@ -82,7 +82,8 @@ enum class Unary : int { Gelu, Relu, ReluAdjoint, Dropout, Uniform };
 
 struct UnaryArgs {
     uint64_t key;
-    double p0, p1;  // dropout: rate; uniform: low, high
+    double p0, p1;            // dropout: rate; uniform: low, high
+    const uint64_t *key_dev;  // when set, the key is read from device memory (a KEY tensor)
 };
 
 template <typename T, Unary OP>
@@ -110,6 +111,8 @@ __device__ inline T unary_one(T x, T g, int64_t i, const UnaryArgs &u) {
 template <typename T, Unary OP>
 __global__ __launch_bounds__(256) void unary_kernel(const T *__restrict__ x, const T *__restrict__ g,
                                                     T *__restrict__ y, int64_t n, UnaryArgs u) {
+    if constexpr (OP == Unary::Dropout || OP == Unary::Uniform)
+        if (u.key_dev) u.key = *u.key_dev;
     using V = Vec16<T>;
     const int64_t nv = n / V::V;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -356,11 +359,21 @@ extern "C" int32_t chelis_hip_relu_adjoint(const chelis_gpu_tensor *x, const che
     return unary_entry<Unary::ReluAdjoint>("relu_adjoint", x, g, dx, UnaryArgs{});
 }
 
+namespace chelis {
+int32_t dropout_device_key(const uint64_t *key_dev, const chelis_gpu_tensor *x, double rate,
+                           const chelis_gpu_tensor *y) {
+    if (!key_dev) return set_error(CHELIS_HIP_EDOMAIN, "dropout: null key");
+    if (!y || !is_float(y->dtype)) return set_error(CHELIS_HIP_EDOMAIN, "dropout: f32 or f64 result required");
+    if (int32_t s = check_rate(rate, y->dtype)) return s;
+    return unary_entry<Unary::Dropout>("dropout", x, nullptr, y, UnaryArgs{0, rate, 0.0, key_dev});
+}
+}  // namespace chelis
+
 extern "C" int32_t chelis_hip_dropout(uint64_t key, const chelis_gpu_tensor *x, double rate,
                                       const chelis_gpu_tensor *y) {
     if (!y || !is_float(y->dtype)) return set_error(CHELIS_HIP_EDOMAIN, "dropout: f32 or f64 result required");
     if (int32_t s = check_rate(rate, y->dtype)) return s;
-    return unary_entry<Unary::Dropout>("dropout", x, nullptr, y, UnaryArgs{key, rate, 0.0});
+    return unary_entry<Unary::Dropout>("dropout", x, nullptr, y, UnaryArgs{key, rate, 0.0, nullptr});
 }
 
 extern "C" int32_t chelis_hip_dropout_replay(uint64_t key, const chelis_gpu_tensor *g, double rate,
@@ -369,7 +382,7 @@ extern "C" int32_t chelis_hip_dropout_replay(uint64_t key, const chelis_gpu_tens
     // divided by (1 - rate); the same kernel with g in place of x.
     if (!dx || !is_float(dx->dtype)) return set_error(CHELIS_HIP_EDOMAIN, "dropout_replay: f32 or f64 result required");
     if (int32_t s = check_rate(rate, dx->dtype)) return s;
-    return unary_entry<Unary::Dropout>("dropout_replay", g, nullptr, dx, UnaryArgs{key, rate, 0.0});
+    return unary_entry<Unary::Dropout>("dropout_replay", g, nullptr, dx, UnaryArgs{key, rate, 0.0, nullptr});
 }
 
 extern "C" int32_t chelis_hip_uniform_like(uint64_t key, double low, double high, const chelis_gpu_tensor *out) {
@@ -379,5 +392,5 @@ extern "C" int32_t chelis_hip_uniform_like(uint64_t key, double low, double high
     const double span = f32 ? (double)((float)hi - (float)lo) : hi - lo;
     if (!(std::isfinite(lo) && std::isfinite(hi) && lo <= hi && std::isfinite(span)))
         return set_error(CHELIS_HIP_EDOMAIN, "numeric trap: domain in uniform_like at %s", f32 ? "f32" : "f64");
-    return unary_entry<Unary::Uniform>("uniform_like", nullptr, nullptr, out, UnaryArgs{key, low, high});
+    return unary_entry<Unary::Uniform>("uniform_like", nullptr, nullptr, out, UnaryArgs{key, low, high, nullptr});
 }

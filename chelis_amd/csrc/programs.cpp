@@ -268,9 +268,8 @@ extern "C" int32_t chelis_prog_mlp_train_step(const chelis_gpu_tensor *const *in
     hipStream_t st = stream();
     if (!st) return set_error(CHELIS_HIP_EHIP, "no HIP device");
     const float rate = 0.1f, lr = 0.01f;
-    uint64_t k = 0;
-    CHELIS_HIP_TRY(hipMemcpyAsync(&k, key->data, sizeof k, hipMemcpyDeviceToHost, st));
-    CHELIS_HIP_TRY(hipStreamSynchronize(st));
+    // the dropout kernels read the key from its tensor on the device
+    const uint64_t *kdev = static_cast<const uint64_t *>(key->data);
     Workspace ws(st);
     const size_t o_hd = ws.reserve(Bt * Hd * 4), o_d = ws.reserve(Bt * Hd * 4), o_z2 = ws.reserve(Bt * O * 4),
                  o_p = ws.reserve(Bt * O * 4), o_nl = ws.reserve(Bt * 4), o_gp = ws.reserve(Bt * O * 4),
@@ -288,7 +287,7 @@ extern "C" int32_t chelis_prog_mlp_train_step(const chelis_gpu_tensor *const *in
     const Pkt xT(x->data, dt, {I, Bt}, {x->strides[1], x->strides[0]}, x->byte_capacity);
     // forward: hd = relu(x.w1 + b1); d = dropout(hd); z2 = d.w2 + b2; p = softmax(z2)
     TRY(chelis_hip_linear(x, w1, b1, CHELIS_ACT_RELU, nullptr, &hd, 0));
-    TRY(chelis_hip_dropout(k, &hd, rate, &d));
+    TRY(dropout_device_key(kdev, &hd, rate, &d));
     TRY(chelis_hip_linear(&d, w2, b2, CHELIS_ACT_NONE, nullptr, &z2, 0));
     TRY(chelis_hip_softmax(&z2, &p));
     // loss = mean(-sum(log(p) * onehot, 1))
@@ -313,7 +312,7 @@ extern "C" int32_t chelis_prog_mlp_train_step(const chelis_gpu_tensor *const *in
     TRY(chelis_hip_reduce(CHELIS_REDUCE_SUM, nullptr, g2, 1, 0, &gb2));
     TRY(chelis_hip_matmul(&dT, &gz2, &gw2, 0));
     TRY(chelis_hip_matmul(&gz2, &w2T, &gd, 0));
-    TRY(chelis_hip_dropout_replay(k, &gd, rate, &gd));
+    TRY(dropout_device_key(kdev, &gd, rate, &gd));
     TRY(chelis_hip_relu_adjoint(&hd, &gd, &gd));
     const chelis_gpu_tensor *g1[1] = {&gd};
     TRY(chelis_hip_reduce(CHELIS_REDUCE_SUM, nullptr, g1, 1, 0, &gb1));
