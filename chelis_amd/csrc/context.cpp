@@ -12,6 +12,7 @@
 #include <cstdio>
 #include <cstring>
 #include <mutex>
+#include <vector>
 
 #include "hip_common.h"
 
@@ -43,6 +44,53 @@ hipStream_t stream() {
         g_streams[device] = s;
     }
     return g_streams[device];
+}
+
+// ---- stream-ordered scratch ---------------------------------------------
+// Every launcher of a device enqueues on that device's one library stream,
+// so a block handed back by scratch_free() may be handed out again at once:
+// whoever gets it next enqueues its kernels on the same stream, after the
+// kernels that used the block before. Blocks are cached per device in
+// power-of-two size classes (at least 256 B) and kept until the process
+// ends; only a cache miss allocates (hipMalloc).
+namespace {
+std::mutex g_scratch_mutex;
+constexpr int kClasses = 48;
+std::vector<void *> g_free[kMaxDevices][kClasses];
+
+int size_class(size_t bytes) {
+    int c = 8;  // 256 B
+    while (c < kClasses - 1 && (size_t(1) << c) < bytes) ++c;
+    return c;
+}
+}  // namespace
+
+void *scratch_alloc(size_t bytes) {
+    if (!bytes) return nullptr;
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) return nullptr;
+    const int c = size_class(bytes);
+    if ((size_t(1) << c) < bytes) return nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mutex);
+        std::vector<void *> &fl = g_free[device][c];
+        if (!fl.empty()) {
+            void *p = fl.back();
+            fl.pop_back();
+            return p;
+        }
+    }
+    void *p = nullptr;
+    if (hipMalloc(&p, size_t(1) << c) != hipSuccess) return nullptr;
+    return p;
+}
+
+void scratch_free(void *p, size_t bytes) {
+    if (!p) return;
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) return;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    g_free[device][size_class(bytes)].push_back(p);
 }
 
 int device_cus() {

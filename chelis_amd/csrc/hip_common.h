@@ -18,6 +18,13 @@ int32_t set_error(int32_t status, const char *fmt, ...) __attribute__((format(pr
 hipStream_t stream();
 // Compute units of the current device (cached per device; 256 on MI355X).
 int device_cus();
+// Scratch device memory for work enqueued on the current device's library
+// stream: blocks are recycled in stream order (a freed block's earlier users
+// are already enqueued ahead of any later user) and cached for reuse, so
+// the hot path makes no allocation calls. scratch_free takes the size given
+// to scratch_alloc. Returns null when the device cannot allocate.
+void *scratch_alloc(size_t bytes);
+void scratch_free(void *p, size_t bytes);
 
 #define CHELIS_HIP_TRY(expr)                                                              \
     do {                                                                                  \

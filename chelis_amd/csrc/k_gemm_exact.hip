@@ -602,8 +602,9 @@ int32_t launch_panel(const GemmProblem &p, const PanelView &v, bool cut, hipStre
     const bool avec = v.sak == 1 && (reinterpret_cast<uintptr_t>(v.a) % (2 * sizeof(T))) == 0 && v.sam % 2 == 0 &&
                       v.sa0 % 2 == 0 && v.sa1 % 2 == 0;
     T *ws = nullptr;
-    if (nparts > 1)
-        CHELIS_HIP_TRY(hipMallocAsync(reinterpret_cast<void **>(&ws), (size_t)nparts * nz * v.M * 64 * sizeof(T), st));
+    const size_t ws_bytes = (size_t)nparts * nz * v.M * 64 * sizeof(T);
+    if (nparts > 1 && !(ws = static_cast<T *>(scratch_alloc(ws_bytes))))
+        return set_error(CHELIS_HIP_EHIP, "matmul: scratch allocation failed");
     if (nparts == 1) {
         if (avec) tree_panel_kernel<T, RM, WAVES, KC, D, false, true><<<grid, 64 * WAVES, 0, st>>>(v, p, kpart, ws);
         else tree_panel_kernel<T, RM, WAVES, KC, D, false, false><<<grid, 64 * WAVES, 0, st>>>(v, p, kpart, ws);
@@ -616,7 +617,7 @@ int32_t launch_panel(const GemmProblem &p, const PanelView &v, bool cut, hipStre
         tree_combine_kernel<T><<<grid_for(nz * v.M * 64, 256), 256, 0, st>>>(v, p, ws, nparts, nz);
         le = hipGetLastError();
     }
-    if (ws) CHELIS_HIP_TRY(hipFreeAsync(ws, st));
+    scratch_free(ws, ws_bytes);
     if (le != hipSuccess) return set_error(CHELIS_HIP_EHIP, "kernel launch: %s", hipGetErrorString(le));
     return CHELIS_HIP_OK;
 }

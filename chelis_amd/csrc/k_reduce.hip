@@ -244,12 +244,21 @@ bool split3(const chelis_gpu_tensor *t, int32_t axis, int64_t *so, int64_t *sn, 
     return fold(0, axis, so) && fold(axis + 1, t->rank, si);
 }
 
+// A pass's partials: library scratch, recycled in stream order.
 struct Scratch {
     void *p = nullptr;
-    hipStream_t st;
-    explicit Scratch(hipStream_t s) : st(s) {}
-    ~Scratch() {
-        if (p) (void)hipFreeAsync(p, st);
+    size_t bytes = 0;
+    explicit Scratch(hipStream_t) {}
+    ~Scratch() { release(); }
+    void release() {
+        scratch_free(p, bytes);
+        p = nullptr;
+    }
+    bool get(size_t n) {
+        release();
+        bytes = n;
+        p = scratch_alloc(n);
+        return p != nullptr;
     }
 };
 
@@ -290,15 +299,12 @@ int32_t run_reduce(const ChainDev &ch, bool chain, LeafSrc src, int64_t outer, i
         Scratch &bv = flip ? sb : sa;
         Scratch &bi = flip ? ib : ia;
         if (!dst_v) {
-            if (bv.p) CHELIS_HIP_TRY(hipFreeAsync(bv.p, st));
-            bv.p = nullptr;
-            CHELIS_HIP_TRY(hipMallocAsync(&bv.p, (size_t)cells * sizeof(T), st));
+            if (!bv.get((size_t)cells * sizeof(T))) return set_error(CHELIS_HIP_EHIP, "reduce: scratch allocation failed");
             dst_v = static_cast<T *>(bv.p);
         }
         if (has_index(K) && !dst_i) {
-            if (bi.p) CHELIS_HIP_TRY(hipFreeAsync(bi.p, st));
-            bi.p = nullptr;
-            CHELIS_HIP_TRY(hipMallocAsync(&bi.p, (size_t)cells * sizeof(int64_t), st));
+            if (!bi.get((size_t)cells * sizeof(int64_t)))
+                return set_error(CHELIS_HIP_EHIP, "reduce: scratch allocation failed");
             dst_i = static_cast<int64_t *>(bi.p);
         }
         LeafSrc s = src;

@@ -2,10 +2,10 @@
 // the HIP backend emits for the program's fused DAG, one region launcher
 // per fused region, on the library stream (include/chelis_programs.h).
 //
-// Intermediates live in one stream-ordered workspace per call
-// (hipMallocAsync / hipFreeAsync on the library stream, from a device pool
-// that keeps its memory between calls), in place of the reference's
-// per-call slot allocations (crates/chelis-backend-hip/src/emit.rs:3162).
+// Intermediates live in one stream-ordered workspace per call (the
+// library's cached scratch blocks, recycled in stream order on the library
+// stream), in place of the reference's per-call slot allocations
+// (crates/chelis-backend-hip/src/emit.rs:3162).
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -68,35 +68,24 @@ struct Pkt {
     const chelis_gpu_tensor *operator&() const { return &t; }
 };
 
-// One stream-ordered allocation carved into 256-byte aligned pieces.
+// One stream-ordered scratch block carved into 256-byte aligned pieces.
 class Workspace {
 public:
-    explicit Workspace(hipStream_t st) : st_(st) {}
-    ~Workspace() {
-        if (base_) (void)hipFreeAsync(base_, st_);
-    }
+    explicit Workspace(hipStream_t) {}
+    ~Workspace() { scratch_free(base_, size_); }
     size_t reserve(int64_t bytes) {
         const size_t off = size_;
         size_ += (static_cast<size_t>(bytes) + 255) & ~size_t(255);
         return off;
     }
     int32_t commit() {
-        static std::once_flag pool_once;
-        std::call_once(pool_once, [] {
-            int dev = 0;
-            hipMemPool_t pool;
-            if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
-                uint64_t keep = ~uint64_t(0);
-                (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
-            }
-        });
-        if (size_) CHELIS_HIP_TRY(hipMallocAsync(&base_, size_, st_));
+        if (size_ && !(base_ = scratch_alloc(size_)))
+            return set_error(CHELIS_HIP_EHIP, "workspace: cannot allocate %zu bytes", size_);
         return CHELIS_HIP_OK;
     }
     void *at(size_t off) const { return static_cast<char *>(base_) + off; }
 
 private:
-    hipStream_t st_;
     void *base_ = nullptr;
     size_t size_ = 0;
 };
