@@ -171,10 +171,14 @@ constexpr int kMinWavesPerEu = sizeof(T) == 8 ? 2 : 1;
 
 // TM = 16x16 blocks per wave and dimension: 4 gives the 128 x 128 tile for
 // large products, 2 a 64 x 64 tile for products with few 128-tiles.
+// Split K (kchunk > 0): grid.z slices K into runs of kchunk (a multiple of
+// BK) and each slice stores its raw sums to part[slice][z][m][n]; a combine
+// pass adds the slices in slice order and applies the epilogue.
 template <typename T, int ALAY, int BLAY, int TM>
 __global__ __launch_bounds__(THREADS, kMinWavesPerEu<T>) void gemm_mfma_kernel(GemmProblem p, int64_t tiles_m,
                                                                                int64_t tiles_n, bool a_vec,
-                                                                               bool b_vec) {
+                                                                               bool b_vec, T *part,
+                                                                               int64_t kchunk) {
     using M = Mfma<T>;
     using acc_t = typename M::acc_t;
     constexpr int BK = M::BK, LD = M::LD, KV = BK / 4;
@@ -196,12 +200,18 @@ __global__ __launch_bounds__(THREADS, kMinWavesPerEu<T>) void gemm_mfma_kernel(G
     // causal 1: a tile wholly above the diagonal is never read (the whole
     // workgroup leaves before any barrier); causal 2: a[m][k] = 0 for k > m
     if (p.causal == 1 && n0 > m0 + BM - 1) return;
-    const int64_t K = (p.causal == 2 && m0 + BM < p.K) ? m0 + BM : p.K;
+    int64_t K = (p.causal == 2 && m0 + BM < p.K) ? m0 + BM : p.K;
 
     const int64_t z = blockIdx.y;
     const int64_t z0 = z / p.nb1, z1 = z % p.nb1;
     const T *A = static_cast<const T *>(p.a) + z0 * p.sa0 + z1 * p.sa1;
     const T *B = static_cast<const T *>(p.b) + z0 * p.sb0 + z1 * p.sb1;
+    if (kchunk > 0) {
+        const int64_t kb = (int64_t)blockIdx.z * kchunk;
+        K = (K - kb < kchunk ? K - kb : kchunk);
+        A += kb * p.sak;
+        B += kb * p.sbk;
+    }
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
@@ -251,6 +261,20 @@ __global__ __launch_bounds__(THREADS, kMinWavesPerEu<T>) void gemm_mfma_kernel(G
         __syncthreads();
     }
 
+    if (kchunk > 0) {
+        T *P = part + ((int64_t)blockIdx.z * gridDim.y + z) * p.M * p.N;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t m = m0 + wm * WT + i * 16 + M::row(fq, r);
+                    const int64_t n = n0 + wn * WT + j * 16 + fr;
+                    if (m < p.M && n < p.N) P[m * p.N + n] = acc[i][j][r];
+                }
+        return;
+    }
     T *C = static_cast<T *>(p.c) + z0 * p.sc0 + z1 * p.sc1;
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -262,6 +286,20 @@ __global__ __launch_bounds__(THREADS, kMinWavesPerEu<T>) void gemm_mfma_kernel(G
                 const int64_t n = n0 + wn * WT + j * 16 + fr;
                 if (m < p.M && n < p.N) C[m * p.scm + n * p.scn] = gemm_epilogue<T>(acc[i][j][r], p, z0, z1, m, n);
             }
+}
+
+// c[z][m][n] = epilogue(sum over slices s, in order, of part[s][z][m][n]).
+template <typename T>
+__global__ __launch_bounds__(256) void splitk_combine_kernel(GemmProblem p, const T *part, int ks, int64_t nz) {
+    const int64_t mn = p.M * p.N, total = nz * mn;
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+        T v = part[e];
+        for (int s = 1; s < ks; ++s) v += part[s * total + e];
+        const int64_t z = e / mn, r = e - z * mn;
+        const int64_t m = r / p.N, n = r - m * p.N;
+        const int64_t z0 = z / p.nb1, z1 = z % p.nb1;
+        static_cast<T *>(p.c)[z0 * p.sc0 + z1 * p.sc1 + m * p.scm + n * p.scn] = gemm_epilogue<T>(v, p, z0, z1, m, n);
+    }
 }
 
 template <typename T>
@@ -281,8 +319,30 @@ int lay_of(int64_t s_outer, int64_t s_k, const void *base, int64_t outer, int64_
 }
 
 template <typename T, int AL, int BL, int TM>
-void launch_mfma(const GemmProblem &p, dim3 grid, int64_t tm, int64_t tn, bool av, bool bv, hipStream_t st) {
-    gemm_mfma_kernel<T, AL, BL, TM><<<grid, THREADS, 0, st>>>(p, tm, tn, av, bv);
+void launch_mfma(const GemmProblem &p, dim3 grid, int64_t tm, int64_t tn, bool av, bool bv, T *part, int64_t kchunk,
+                 hipStream_t st) {
+    gemm_mfma_kernel<T, AL, BL, TM><<<grid, THREADS, 0, st>>>(p, tm, tn, av, bv, part, kchunk);
+}
+
+// Slices of K for a product whose tiles cannot fill the chip: enough slices
+// to give every CU about two workgroups, each slice at least 256 deep (a
+// shorter run does not amortize a tile's first loads and its store), at most
+// 16. Returns 1 for no split.
+template <typename T>
+int64_t split_count(const GemmProblem &p, int64_t tiles, int64_t *kchunk) {
+    constexpr int64_t BK = Mfma<T>::BK;
+    const int64_t cus = device_cus();
+    if (p.causal != 0 || tiles >= cus || p.K < 512) return 1;
+    int64_t ks = (2 * cus + tiles - 1) / tiles;
+    if (ks > p.K / 256) ks = p.K / 256;
+    if (ks > 16) ks = 16;
+    if (ks < 2) return 1;
+    int64_t kc = (p.K + ks - 1) / ks;
+    kc = (kc + BK - 1) / BK * BK;
+    ks = (p.K + kc - 1) / kc;
+    if (ks < 2 || ks * p.nb0 * p.nb1 * p.M * p.N > (int64_t(64) << 20)) return 1;
+    *kchunk = kc;
+    return ks;
 }
 
 template <typename T, int TM>
@@ -291,17 +351,31 @@ int32_t run_tiles(const GemmProblem &p, int al, int bl, bool av, bool bv, hipStr
     const int64_t tm = (p.M + BT - 1) / BT, tn = (p.N + BT - 1) / BT;
     const int64_t nz = p.nb0 * p.nb1;
     if (tm * tn > 0x7fffffffLL || nz > 65535) return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: grid too large");
-    const dim3 grid((unsigned)(tm * tn), (unsigned)nz);
+    int64_t kchunk = 0;
+    const int64_t ks = split_count<T>(p, tm * tn * nz, &kchunk);
+    T *part = nullptr;
+    const size_t part_bytes = ks > 1 ? (size_t)(ks * nz * p.M * p.N) * sizeof(T) : 0;
+    if (ks > 1) {
+        part = static_cast<T *>(scratch_alloc(part_bytes));
+        if (!part) return set_error(CHELIS_HIP_EHIP, "matmul: split-K scratch of %zu bytes", part_bytes);
+    } else {
+        kchunk = 0;
+    }
+    const dim3 grid((unsigned)(tm * tn), (unsigned)nz, (unsigned)ks);
     switch (al * 3 + bl) {
-        case 0: launch_mfma<T, 0, 0, TM>(p, grid, tm, tn, av, bv, st); break;
-        case 1: launch_mfma<T, 0, 1, TM>(p, grid, tm, tn, av, bv, st); break;
-        case 2: launch_mfma<T, 0, 2, TM>(p, grid, tm, tn, av, bv, st); break;
-        case 3: launch_mfma<T, 1, 0, TM>(p, grid, tm, tn, av, bv, st); break;
-        case 4: launch_mfma<T, 1, 1, TM>(p, grid, tm, tn, av, bv, st); break;
-        case 5: launch_mfma<T, 1, 2, TM>(p, grid, tm, tn, av, bv, st); break;
-        case 6: launch_mfma<T, 2, 0, TM>(p, grid, tm, tn, av, bv, st); break;
-        case 7: launch_mfma<T, 2, 1, TM>(p, grid, tm, tn, av, bv, st); break;
-        default: launch_mfma<T, 2, 2, TM>(p, grid, tm, tn, av, bv, st); break;
+        case 0: launch_mfma<T, 0, 0, TM>(p, grid, tm, tn, av, bv, part, kchunk, st); break;
+        case 1: launch_mfma<T, 0, 1, TM>(p, grid, tm, tn, av, bv, part, kchunk, st); break;
+        case 2: launch_mfma<T, 0, 2, TM>(p, grid, tm, tn, av, bv, part, kchunk, st); break;
+        case 3: launch_mfma<T, 1, 0, TM>(p, grid, tm, tn, av, bv, part, kchunk, st); break;
+        case 4: launch_mfma<T, 1, 1, TM>(p, grid, tm, tn, av, bv, part, kchunk, st); break;
+        case 5: launch_mfma<T, 1, 2, TM>(p, grid, tm, tn, av, bv, part, kchunk, st); break;
+        case 6: launch_mfma<T, 2, 0, TM>(p, grid, tm, tn, av, bv, part, kchunk, st); break;
+        case 7: launch_mfma<T, 2, 1, TM>(p, grid, tm, tn, av, bv, part, kchunk, st); break;
+        default: launch_mfma<T, 2, 2, TM>(p, grid, tm, tn, av, bv, part, kchunk, st); break;
+    }
+    if (ks > 1) {
+        splitk_combine_kernel<T><<<grid_for(nz * p.M * p.N, 256), 256, 0, st>>>(p, part, (int)ks, nz);
+        scratch_free(part, part_bytes);
     }
     CHELIS_LAUNCH_CHECK();
     return CHELIS_HIP_OK;

@@ -460,17 +460,27 @@ __global__ __launch_bounds__(256) void tree_combine_kernel(PanelView v, GemmProb
     if (n >= v.N) return;
     const int64_t z = idx / per_z, m = (idx / 64) % v.M;
     T lvl[8];
-    for (int64_t j = 0; j < nparts; ++j) {
-        T carry = part[j * nz * per_z + idx];
-        bool done = false;
+    // eight block totals are read before any is pushed: one memory latency
+    // per eight parts
+    for (int64_t j0 = 0; j0 < nparts; j0 += 8) {
+        T q[8];
 #pragma unroll
-        for (int d = 0; d < 8; ++d) {
-            if (!done) {
-                if ((j >> d) & 1) {
-                    carry = lvl[d] + carry;
-                } else {
-                    lvl[d] = carry;
-                    done = true;
+        for (int u = 0; u < 8; ++u) q[u] = j0 + u < nparts ? part[(j0 + u) * nz * per_z + idx] : T(0);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int64_t j = j0 + u;
+            if (j >= nparts) break;
+            T carry = q[u];
+            bool done = false;
+#pragma unroll
+            for (int d = 0; d < 8; ++d) {
+                if (!done) {
+                    if ((j >> d) & 1) {
+                        carry = lvl[d] + carry;
+                    } else {
+                        lvl[d] = carry;
+                        done = true;
+                    }
                 }
             }
         }
@@ -487,41 +497,52 @@ __global__ __launch_bounds__(256) void tree_combine_kernel(PanelView v, GemmProb
 }
 
 // ---------------------------------------------------------------- thread per output
-// Short K: one thread per output, leaves streamed straight into its carry
-// stack (depth 12, K <= 4096), n fastest so B and C accesses coalesce.
-constexpr int TD = 12;
-template <typename T>
+// Short K (<= 32): one thread per output, n fastest so B and C accesses
+// coalesce. The K leaves are padded with -0.0 to P = 2^ceil(log2 K) and
+// summed as a complete register tree: x + (-0.0) = x for every x, so this is
+// the canonical tree over the K leaves. All loads are issued before the
+// first sum (one memory latency per output, not one per leaf); AV/BV read
+// a run along K with 16-byte vectors.
+template <typename T, int P, bool AV, bool BV>
 __global__ __launch_bounds__(256) void tree_thread_kernel(GemmProblem p, int64_t outputs) {
+    constexpr int W = (int)Vec16<T>::W;
     const int64_t w = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (w >= outputs) return;
     const int64_t n = w % p.N, mz = w / p.N, m = mz % p.M, z = mz / p.M;
     const int64_t z0 = z / p.nb1, z1 = z % p.nb1;
     const T *A = static_cast<const T *>(p.a) + z0 * p.sa0 + z1 * p.sa1 + m * p.sam;
     const T *B = static_cast<const T *>(p.b) + z0 * p.sb0 + z1 * p.sb1 + n * p.sbn;
-    T lvl[TD];
-    for (int64_t k = 0; k < p.K; ++k) {
-        T carry = A[k * p.sak] * B[k * p.sbk];
-        bool done = false;
+    const int K = (int)p.K;
+    T a[P], b[P];
 #pragma unroll
-        for (int d = 0; d < TD; ++d) {
-            if (!done) {
-                if ((k >> d) & 1) {
-                    carry = lvl[d] + carry;
-                } else {
-                    lvl[d] = carry;
-                    done = true;
-                }
-            }
+    for (int k0 = 0; k0 < P; k0 += W) {
+        if (AV && P >= W && k0 + W <= K) {
+            const typename Vec16<T>::type v = *reinterpret_cast<const typename Vec16<T>::type *>(A + k0);
+            const T *ve = reinterpret_cast<const T *>(&v);
+#pragma unroll
+            for (int u = 0; u < W && u < P; ++u) a[k0 + u] = ve[u];
+        } else {
+#pragma unroll
+            for (int u = 0; u < W && k0 + u < P; ++u) a[k0 + u] = k0 + u < K ? A[(k0 + u) * p.sak] : T(0);
+        }
+        if (BV && P >= W && k0 + W <= K) {
+            const typename Vec16<T>::type v = *reinterpret_cast<const typename Vec16<T>::type *>(B + k0);
+            const T *ve = reinterpret_cast<const T *>(&v);
+#pragma unroll
+            for (int u = 0; u < W && u < P; ++u) b[k0 + u] = ve[u];
+        } else {
+#pragma unroll
+            for (int u = 0; u < W && k0 + u < P; ++u) b[k0 + u] = k0 + u < K ? B[(k0 + u) * p.sbk] : T(0);
         }
     }
-    T total = T(0);
-    bool found = false;
 #pragma unroll
-    for (int d = 0; d < TD; ++d)
-        if ((p.K >> d) & 1) {
-            total = found ? lvl[d] + total : lvl[d];
-            found = true;
-        }
+    for (int k = 0; k < P; ++k) a[k] = k < K ? a[k] * b[k] : T(-0.0);
+#pragma unroll
+    for (int s = 1; s < P; s <<= 1)
+#pragma unroll
+        for (int i = 0; i + s < P; i += 2 * s) a[i] = a[i] + a[i + s];
+    // the empty contraction is +0
+    const T total = K == 0 ? T(0) : a[0];
     T *C = static_cast<T *>(p.c) + z0 * p.sc0 + z1 * p.sc1;
     C[m * p.scm + n * p.scn] = gemm_epilogue<T>(total, p, z0, z1, m, n);
 }
@@ -625,7 +646,9 @@ int32_t launch_panel(const GemmProblem &p, const PanelView &v, bool cut, hipStre
 template <typename T>
 int32_t run_panel(const GemmProblem &p, hipStream_t st) {
     PanelView v{};
-    v.swapped = p.N > 64;
+    // the narrow side goes on the lanes; a matrix-vector product (N = 1)
+    // puts its outputs there instead
+    v.swapped = p.N > 64 || (p.N == 1 && p.M > 1);
     if (!v.swapped) {
         v.a = p.a, v.b = p.b, v.M = p.M, v.N = p.N, v.sam = p.sam, v.sak = p.sak, v.sbk = p.sbk, v.sbn = p.sbn;
         v.sa0 = p.sa0, v.sa1 = p.sa1, v.sb0 = p.sb0, v.sb1 = p.sb1;
@@ -638,13 +661,31 @@ int32_t run_panel(const GemmProblem &p, hipStream_t st) {
     return launch_panel<T, 5>(p, v, true, st);
 }
 
+template <typename T, int P>
+void launch_thread(const GemmProblem &p, int64_t outputs, bool av, bool bv, hipStream_t st) {
+    const unsigned blocks = (unsigned)((outputs + 255) / 256);
+    if (av && bv) tree_thread_kernel<T, P, true, true><<<blocks, 256, 0, st>>>(p, outputs);
+    else if (av) tree_thread_kernel<T, P, true, false><<<blocks, 256, 0, st>>>(p, outputs);
+    else if (bv) tree_thread_kernel<T, P, false, true><<<blocks, 256, 0, st>>>(p, outputs);
+    else tree_thread_kernel<T, P, false, false><<<blocks, 256, 0, st>>>(p, outputs);
+}
+
 template <typename T>
 int32_t run_thread(const GemmProblem &p, hipStream_t st) {
-    if (p.K > (int64_t(1) << TD)) return set_error(CHELIS_HIP_EDOMAIN, "matmul: short-K kernel holds K <= %d", 1 << TD);
+    if (p.K > 32) return set_error(CHELIS_HIP_EDOMAIN, "matmul: short-K kernel holds K <= 32");
     const int64_t outputs = p.M * p.N * p.nb0 * p.nb1;
     const int64_t blocks = (outputs + 255) / 256;
     if (blocks > 0x7fffffffLL) return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: too many outputs");
-    tree_thread_kernel<T><<<(unsigned)blocks, 256, 0, st>>>(p, outputs);
+    constexpr int64_t W = Vec16<T>::W;
+    // a vector read of A (B) needs K contiguous and every row (column) start 16-byte aligned
+    const bool av = p.sak == 1 && aligned16(p.a) && (p.sam % W == 0 || p.M == 1) && p.sa0 % W == 0 && p.sa1 % W == 0;
+    const bool bv = p.sbk == 1 && aligned16(p.b) && (p.sbn % W == 0 || p.N == 1) && p.sb0 % W == 0 && p.sb1 % W == 0;
+    if (p.K <= 1) launch_thread<T, 1>(p, outputs, false, false, st);
+    else if (p.K <= 2) launch_thread<T, 2>(p, outputs, false, false, st);
+    else if (p.K <= 4) launch_thread<T, 4>(p, outputs, av, bv, st);
+    else if (p.K <= 8) launch_thread<T, 8>(p, outputs, av, bv, st);
+    else if (p.K <= 16) launch_thread<T, 16>(p, outputs, av, bv, st);
+    else launch_thread<T, 32>(p, outputs, av, bv, st);
     CHELIS_LAUNCH_CHECK();
     return CHELIS_HIP_OK;
 }

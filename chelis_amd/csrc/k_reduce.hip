@@ -120,6 +120,12 @@ __global__ __launch_bounds__(256) void reduce_rows_kernel(ChainDev ch, LeafSrc s
             v = leaf<T, CHAIN>(ch, src, o, i, 0);
             if (has_index(K) && src.idx) vi = src.idx[o * n + i];
         }
+        if constexpr (K == Rk::Sum) {
+            v = wave_tree_sum(v);
+            seg[s] = v;
+            sidx[s] = vi;
+            continue;
+        }
 #pragma unroll
         for (int m = 1; m < 64; m <<= 1) {
             T ov = shfl_xor(v, m);
@@ -280,9 +286,17 @@ int32_t run_reduce(const ChainDev &ch, bool chain, LeafSrc src, int64_t outer, i
     int64_t *prev_i = nullptr;
     int flip = 0;
     while (true) {
+        // rows: a row that fits one wave's 16 segments finishes in this pass;
+        // a longer one is cut into as many groups as keep >= 1024 waves busy
+        // (S = 16 only when there are rows enough), since a pass over few long
+        // groups runs on a handful of waves.
         int S = 1;
         if (rows) {
-            while (64 * S < cur_n && S < 16) S <<= 1;
+            if (cur_n <= 64 * 16) {
+                while (64 * S < cur_n) S <<= 1;
+            } else {
+                while (S < 16 && outer * ((cur_n + 128 * S - 1) / (128 * S)) >= 1024) S <<= 1;
+            }
         }
         const int64_t G = rows ? 64 * S : 32;
         const int64_t groups = (cur_n + G - 1) / G;

@@ -4,7 +4,9 @@
 // Dispatch (the reference sends every BlasMatmul to hipBLAS,
 // crates/chelis-backend-hip/src/emit.rs:4718-4842):
 //   K <= 32                      -> tree_thread (short K, bit-exact)
-//   M == 1 or N == 1             -> tree_wave   (GEMV, HBM bound, bit-exact)
+//   M == 1 or N == 1             -> tree_wave   (GEMV, HBM bound, bit-exact),
+//                                   or tree_panel when the matrix has at
+//                                   most 64 outputs and is stored along them
 //   min(M, N) <= 64 and (CHELIS_MATMUL_EXACT, min(M, N) < 16 or f64)
 //                                -> tree_panel  (narrow side on the lanes,
 //                                   bit-exact)
@@ -125,7 +127,13 @@ int32_t dispatch(chelis_dtype dt, const GemmProblem &p, int32_t flags) {
     const bool f64 = dt == CHELIS_DTYPE_F64;
     const int64_t narrow = std::min(p.M, p.N);
     if (p.K <= 32) return gemm_tree_thread(dt, p, st);
-    if (p.M == 1 || p.N == 1) return gemm_tree_wave(dt, p, st);
+    if (p.M == 1 || p.N == 1) {
+        // a matrix of at most 64 outputs stored along the output axis: the
+        // column panel puts the outputs on the lanes and reads whole rows
+        if (p.N == 1 && p.M > 1 && p.M <= 64 && p.sak != 1 && p.sam == 1) return gemm_tree_panel(dt, p, st);
+        if (p.M == 1 && p.N > 1 && p.N <= 64 && p.sbk != 1 && p.sbn == 1) return gemm_tree_panel(dt, p, st);
+        return gemm_tree_wave(dt, p, st);
+    }
     const bool exact = flags & CHELIS_MATMUL_EXACT;
     if (narrow <= 64 && (exact || narrow < 16 || f64)) return gemm_tree_panel(dt, p, st);
     if (exact) return gemm_tree_tiled(dt, p, st);

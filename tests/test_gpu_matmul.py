@@ -62,6 +62,9 @@ TREE_CASES = [
     (37, 50, 1, False, False),      # short K
     (64, 33, 17, True, False),      # short K
     (128, 512, 10, False, True),    # short K (the MLP's g_z2 . W2^T form)
+    (8192, 1, 32, False, False),    # short K, vector reads of A and B (the linreg X . w form)
+    (64, 20, 24, False, True),      # short K, vector runs and a zero-padded tail
+    (99, 2, 7, False, True),        # short K, odd row stride (scalar reads)
     (300, 1, 1000, False, False),   # GEMV
     (300, 1, 1000, True, False),    # GEMV, transposed A (linreg X^T r form)
     (1, 257, 4097, False, False),   # row vector times matrix
@@ -77,6 +80,10 @@ TREE_CASES = [
     (900, 48, 5000, False, False),  # several aligned K blocks and a partial last chunk
     (20, 5, 2049, False, True),     # small product: one K block of 2049 leaves
     (30, 7, 9000, True, False),     # small product, K past one deep block: three blocks and a combine
+    (32, 1, 8192, True, False),     # GEMV, A stored along the outputs (linreg X^T r): outputs on the lanes
+    (64, 1, 1000, True, False),     # the same with a full 64-lane panel
+    (1, 48, 5000, False, False),    # row vector times a row-major matrix: outputs on the lanes
+    (1, 64, 33, False, False),      # the same, one partial chunk
 ]
 
 
@@ -262,3 +269,39 @@ def test_linear_epilogue_on_mfma_path():
     bias = rand(rng, (384,), np.float32)
     c = C.linear(C.to_device(x), C.to_device(w), C.to_device(bias), "relu").numpy()
     check_close(c, O.relu((O.matmul(x, w) + bias).astype(np.float32)), np.float32)
+
+
+# Products whose tiles do not fill the chip and whose K runs long split K into
+# slices summed in slice order by a combine pass (still an MFMA-tolerance path).
+SPLIT_CASES = [
+    (784, 512, 1024, True, False),  # the MLP's x^T g
+    (100, 130, 3001, False, True),  # ragged last slice
+    (96, 200, 8192, True, True),    # 16 slices
+]
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("case", SPLIT_CASES)
+def test_split_k_within_tolerance(case, dtype):
+    M, N, K, ta, tb = case
+    rng = np.random.default_rng(M * 7 + N + K)
+    a, b = rand(rng, (M, K), dtype), rand(rng, (K, N), dtype)
+    _da, va, na = dev_view(a, M, K, ta)
+    _db, vb, nb = dev_view(b, K, N, tb)
+    c = C.matmul(va, vb).numpy()
+    check_close(c, O.matmul(na, nb), dtype)
+
+
+def test_split_k_batched_with_epilogue():
+    """Per-batch bias, GELU and residual applied once, after the slices are
+    summed; a broadcast batch operand."""
+    rng = np.random.default_rng(45)
+    x = rand(rng, (3, 96, 1500), np.float64)
+    w, bias = rand(rng, (1500, 100), np.float64), rand(rng, (3, 100), np.float64)
+    res = rand(rng, (3, 96, 100), np.float64)
+    dw = C.to_device(w)
+    c = C.linear(C.to_device(x), dw.view((3, 1500, 100), (0, 100, 1)), C.to_device(bias), "gelu",
+                 C.to_device(res)).numpy()
+    for j in range(3):
+        v = res[j] + O.gelu(O.matmul(x[j], w) + bias[j])
+        check_close(c[j], v, np.float64)
