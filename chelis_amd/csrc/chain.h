@@ -28,13 +28,39 @@ __device__ inline double random_unit(uint64_t key, uint64_t index) {
 template <typename T> __device__ inline T leaf_exp(T v);
 template <> __device__ inline float leaf_exp<float>(float v) { return expf_cr(v); }
 template <> __device__ inline double leaf_exp<double>(double v) { return canon(exp(v)); }
-// binary32 leaves evaluated in binary64 and rounded once.
-template <typename T> __device__ inline T leaf_erfc(T v) { return canon((T)erfc((double)v)); }
-template <typename T> __device__ inline T leaf_log(T v) { return canon((T)log((double)v)); }
-template <typename T> __device__ inline T leaf_tanh(T v) { return canon((T)tanh((double)v)); }
+template <typename T> __device__ inline T leaf_erfc(T v);
+template <typename T> __device__ inline T leaf_log(T v);
+template <typename T> __device__ inline T leaf_tanh(T v);
 template <> __device__ inline double leaf_erfc<double>(double v) { return canon(erfc(v)); }
 template <> __device__ inline double leaf_log<double>(double v) { return canon(log(v)); }
 template <> __device__ inline double leaf_tanh<double>(double v) { return canon(tanh(v)); }
+
+// Binary32 log, erfc and tanh: the binary64 device function rounded once to
+// binary32 is the correctly rounded result (the same bits as CORE-MATH, the
+// C backend's libm) on every binary32 input except the six below, where the
+// binary64 value sits within its own error of a rounding midpoint. The
+// inputs come from comparing all 2^32 inputs on the device; the results are
+// the correctly rounded values (80-digit decimal arithmetic). tanh has no
+// exception. A change of the device math library is caught by the
+// exhaustive comparison, which runs over every input again.
+__device__ inline float cr_exception(float y, uint32_t xb, uint32_t in, uint32_t out) {
+    return xb == in ? f32_from(out) : y;
+}
+template <> __device__ inline float leaf_log<float>(float v) {
+    const uint32_t b = f32_bits(v);
+    float y = (float)log((double)v);
+    y = cr_exception(y, b, 0x3c413d3au, 0xc08e158fu);
+    y = cr_exception(y, b, 0x41178febu, 0x400fe5e7u);
+    y = cr_exception(y, b, 0x4c5d65a5u, 0x418f034bu);
+    y = cr_exception(y, b, 0x65d890d3u, 0x4254d1f9u);
+    y = cr_exception(y, b, 0x6f31a8ecu, 0x42845a89u);
+    return canon(y);
+}
+template <> __device__ inline float leaf_erfc<float>(float v) {
+    const float y = cr_exception((float)erfc((double)v), f32_bits(v), 0xb76c9f62u, 0x3f800085u);
+    return canon(y);
+}
+template <> __device__ inline float leaf_tanh<float>(float v) { return canon((float)tanh((double)v)); }
 
 template <typename T> struct Lim;
 template <> struct Lim<float> {

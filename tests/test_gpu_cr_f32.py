@@ -1,0 +1,71 @@
+"""Exhaustive device check of the binary32 transcendental leaves against
+CORE-MATH (the C backend's libm, crates/chelis-crmath/csrc/crmath_ffi.c,
+with the wrapper's NaN canonicalization): every one of the 2^32 binary32
+inputs, bit for bit. exp is the correctly rounded expf_cr of devmath.h;
+log, erfc and tanh are the binary64 device evaluation rounded once, with
+the inputs near a rounding midpoint resolved through the exception tables
+of cr_exceptions.h.
+
+Each function takes 16 runs of 2^28 inputs: the device evaluates a run
+through a one-step fused chain, the host evaluates CORE-MATH over the same
+bit patterns with OpenMP threads and compares.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import chelis_amd as C
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+RUN = 1 << 28
+OPS = {"exp": 0, "log": 1, "erfc": 2, "tanh": 3}
+
+
+@pytest.fixture(scope="module")
+def cr(tmp_path_factory):
+    O.build()
+    so = tmp_path_factory.mktemp("cr") / "libcr_array.so"
+    ref = os.path.join(ROOT, "oracle", "_ref")
+    subprocess.run(["gcc", "-O2", "-fopenmp", "-fPIC", "-shared", "-o", str(so),
+                    os.path.join(ROOT, "tests", "cpu", "cr_array.c"), f"-L{ref}", "-lcrmath_ref",
+                    f"-Wl,-rpath,{ref}"], check=True)
+    lib = ctypes.CDLL(str(so))
+    lib.cr_check_run.restype = ctypes.c_long
+    lib.cr_check_run.argtypes = [ctypes.c_int, ctypes.c_uint32, ctypes.c_long, ctypes.c_void_p, ctypes.c_void_p,
+                                 ctypes.c_long]
+    return lib
+
+
+def device_run(op, first, n):
+    x = (np.arange(n, dtype=np.uint32) + np.uint32(first)).view(np.float32)
+    dx = C.to_device(x)
+    out = C.empty(x.shape, np.float32)
+    C.fused_elementwise(C.fused_chain([(op, 0)]), [dx], out)
+    return np.ascontiguousarray(out.numpy()).view(np.uint32)
+
+
+def mismatches(cr, op, cap=64):
+    """(count, [(input, expected, device) bits]) over all 2^32 inputs."""
+    total, bad = 0, []
+    buf = np.zeros(3 * cap, np.uint32)
+    for r in range((1 << 32) // RUN):
+        first = r * RUN
+        got = device_run(op, first, RUN)
+        n = cr.cr_check_run(OPS[op], first, RUN, got.ctypes.data, buf.ctypes.data, cap)
+        if n:
+            k = min(n, cap)
+            bad += [tuple(int(v) for v in buf[3 * i:3 * i + 3]) for i in range(k)]
+        total += n
+        print(f"{op}: run {r} done, {n} mismatches", flush=True)
+    return total, sorted(bad)
+
+
+@pytest.mark.parametrize("op", ["exp", "log", "erfc", "tanh"])
+def test_binary32_leaf_is_correctly_rounded_on_every_input(cr, op):
+    n, bad = mismatches(cr, op)
+    assert n == 0, f"{n} inputs differ; first {[tuple(hex(v) for v in b) for b in bad[:8]]}"
