@@ -84,27 +84,35 @@ template <> struct PhiK<double> {
                             s = 134217729.0;
 };
 
+//
+// Every primitive of the graph rounds at T; only the final product is
+// NaN-finalized. That gives the same bits as finalizing each primitive: for
+// a non-NaN x no intermediate is NaN (z is finite with |z| < 64, so the
+// split, the products and the exp argument are finite; erfc and exp of
+// finite or infinite arguments are not NaN; m * phi is +-inf * 1 or
+// -0 * 0 at the infinities), and a NaN x makes the product NaN, which the
+// final step canonicalizes.
 template <typename T>
 __device__ inline T gelu_one(T x) {
     const T c = PhiK<T>::c, cl = PhiK<T>::cl, k = PhiK<T>::k, s = PhiK<T>::s;
-    const T e = leaf_erfc<T>(canon(canon(-x) * c));
+    const T e = leaf_erfc<T>(-x * c);
     const T z = (fabs(x) < T(64)) ? x : T(0);
-    const T a = canon(-z);
-    const T th = canon(a * c);
-    const T ta = canon(s * a);
-    const T ah = canon(ta - canon(ta - a));
-    const T al = canon(a - ah);
-    const T tc = canon(s * c);
-    const T ch = canon(tc - canon(tc - c));
-    const T cr = canon(c - ch);
-    T t = canon(canon(ah * ch) - th);
-    t = canon(t + canon(ah * cr));
-    t = canon(t + canon(al * ch));
-    t = canon(t + canon(al * cr));
-    const T tl = canon(t + canon(a * cl));
-    const T g = leaf_exp<T>(canon(-canon(th * th)));
-    const T corr = canon(canon(k * g) * tl);
-    const T phi = canon(T(0.5) * canon(e - corr));
+    const T a = -z;
+    const T th = a * c;
+    const T ta = s * a;
+    const T ah = ta - (ta - a);
+    const T al = a - ah;
+    const T tc = s * c;
+    const T ch = tc - (tc - c);
+    const T cr = c - ch;
+    T t = ah * ch - th;
+    t = t + ah * cr;
+    t = t + al * ch;
+    t = t + al * cr;
+    const T tl = t + a * cl;
+    const T g = leaf_exp<T>(-(th * th));
+    const T corr = (k * g) * tl;
+    const T phi = T(0.5) * (e - corr);
     const T m = (x < Lim<T>::lowest()) ? T(-0.0) : x;
     return canon(m * phi);
 }

@@ -76,6 +76,15 @@ int32_t gather_contiguous(const void *src, void *dst, int32_t rank, const int64_
 int32_t dropout_device_key(const uint64_t *key_dev, const chelis_gpu_tensor *x, double rate,
                            const chelis_gpu_tensor *y);
 
+// One FusedElem chain over n_groups independent (inputs, output) groups in
+// as few launches as possible: inputs holds n_groups runs of n_inputs
+// packets. Groups whose operands all stream with their output (or are one
+// broadcast element) share a launch, four at a time; any other group runs
+// through chelis_hip_fused_elementwise. Same bits as one call per group.
+int32_t fused_elementwise_groups(const chelis_fused_chain *chain, int32_t n_inputs,
+                                 const chelis_gpu_tensor *const *inputs, const chelis_gpu_tensor *const *outs,
+                                 int32_t n_groups);
+
 inline unsigned grid_for(int64_t work, int per_block) {
     int64_t g = (work + per_block - 1) / per_block;
     return (unsigned)(g < 1 ? 1 : g);

@@ -2,12 +2,15 @@
 // ReLU and its adjoint, keyed dropout / replay / uniform_like, and the
 // strided gather used by the device owner.
 //
-// Bandwidth design: contiguous operands move in 16-byte vectors (one
-// float4 / double2 per lane per access, 1 KiB per wave instruction); a
-// broadcast operand (stride 0 on an axis) is re-read through L2/MALL, not
-// materialized. Index math is done once per element in 64-bit only for
-// non-contiguous views; shapes are collapsed on the host first so the common
-// cases are rank 1 (contiguous) and rank 2 (row/column broadcast).
+// Bandwidth design: the unary maps (GELU, ReLU, dropout, uniform) move
+// contiguous operands in 16-byte vectors (one float4 / double2 per lane per
+// access, 1 KiB per wave instruction). The chain interpreter reads one
+// element per lane (coalesced) and keeps its code small; shapes are
+// collapsed on the host first, so the common case is a flat map (every
+// operand contiguous with the output or a broadcast scalar) with no index
+// arithmetic, and only genuinely strided views (row/column broadcast,
+// permuted axes) pay for coordinates. A broadcast operand (stride 0) is
+// re-read through L2/MALL, not materialized.
 #include "chain.h"
 
 namespace chelis {
@@ -28,9 +31,37 @@ struct Shape {
     int64_t ext[kMaxRank];
 };
 
+// The chain interpreter: one thread per element, the element's inputs and
+// step results in a row of LDS slots (inputs first, then steps), the steps
+// run by a loop over the chain rather than unrolled. A launch is mostly a
+// handful of small tensors, so the kernel is kept small: its code is
+// fetched by every CU once per launch. The slot row stride is odd, so the
+// lanes of a wave hit distinct LDS banks.
+constexpr int kSlots = CHELIS_FUSED_MAX_INPUTS + CHELIS_FUSED_MAX_STEPS;
+constexpr int kSlotStride = kSlots + 1;
+
+template <typename T>
+__device__ inline T run_chain(const ChainDev &ch, T *slot) {
+    T v = T(0);
+#pragma unroll 1
+    for (int s = 0; s < ch.n_steps; ++s) {
+        const int a0 = ch.a0[s], a1 = ch.a1[s];
+        const T x = slot[a0 >= 0 ? a0 : CHELIS_FUSED_MAX_INPUTS - a0 - 1];
+        const T y = slot[a1 >= 0 ? a1 : CHELIS_FUSED_MAX_INPUTS - a1 - 1];
+        v = apply_step<T>(ch.op[s], x, y, ch.imm[s]);
+        slot[CHELIS_FUSED_MAX_INPUTS + s] = v;
+    }
+    return v;
+}
+
+// Strided operands (any of the up-to-4 collapsed axes, broadcast by stride
+// 0): the element's coordinates from its flat index, then one offset per
+// operand.
 template <typename T>
 __global__ __launch_bounds__(256) void fused_chain_kernel(ChainDev ch, Operands ops, Shape sh, T *__restrict__ out,
                                                           int64_t count) {
+    __shared__ T slots[256 * kSlotStride];
+    T *slot = slots + threadIdx.x * kSlotStride;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < count; idx += stride) {
         int64_t coord[kMaxRank];
@@ -52,22 +83,53 @@ __global__ __launch_bounds__(256) void fused_chain_kernel(ChainDev ch, Operands 
 #pragma unroll
                 for (int a = 0; a < kMaxRank; ++a) off += coord[a] * ops.o[k].st[a];
                 in[k] = static_cast<const T *>(ops.o[k].p)[off];
-            } else {
-                in[k] = T(0);
             }
         }
-        T val[CHELIS_FUSED_MAX_STEPS];
 #pragma unroll
-        for (int s = 0; s < CHELIS_FUSED_MAX_STEPS; ++s) {
-            if (s < ch.n_steps) {
-                const int a0 = ch.a0[s], a1 = ch.a1[s];
-                const T x = a0 >= 0 ? in[a0] : val[-a0 - 1];
-                const T y = a1 >= 0 ? in[a1] : val[-a1 - 1];
-                val[s] = apply_step<T>(ch.op[s], x, y, ch.imm[s]);
-            }
-        }
-        out[idx] = val[ch.n_steps - 1];
+        for (int k = 0; k < CHELIS_FUSED_MAX_INPUTS; ++k)
+            if (k < ops.n) slot[k] = in[k];
+        out[idx] = run_chain<T>(ch, slot);
     }
+}
+
+// ---------------------------------------------------------------- flat maps
+// Every operand either runs with the output (stride 1) or is one element
+// broadcast to all (stride 0): no index arithmetic. One launch serves up to
+// kMaxGroups independent (inputs, output) groups under the same chain (a
+// program's parameter updates); block ranges select the group.
+constexpr int kMaxGroups = 4;
+struct FlatGroup {
+    const void *in[CHELIS_FUSED_MAX_INPUTS];
+    uint32_t bcast;  // bit k: input k is a single element broadcast to all
+    void *out;
+    int64_t count;
+    int64_t first_block;  // the group's first block in the grid
+};
+struct FlatGroups {
+    int32_t n, n_in;
+    FlatGroup g[kMaxGroups];
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void fused_flat_kernel(ChainDev ch, FlatGroups fg) {
+    __shared__ T slots[256 * kSlotStride];
+    int gi = 0;
+#pragma unroll
+    for (int k = 1; k < kMaxGroups; ++k)
+        if (k < fg.n && (int64_t)blockIdx.x >= fg.g[k].first_block) gi = k;
+    const FlatGroup &G = fg.g[gi];
+    const int64_t i = ((int64_t)blockIdx.x - G.first_block) * 256 + threadIdx.x;
+    if (i >= G.count) return;
+    T *slot = slots + threadIdx.x * kSlotStride;
+    // every load issued before the first slot store: one memory latency
+    T in[CHELIS_FUSED_MAX_INPUTS];
+#pragma unroll
+    for (int k = 0; k < CHELIS_FUSED_MAX_INPUTS; ++k)
+        if (k < fg.n_in) in[k] = static_cast<const T *>(G.in[k])[((G.bcast >> k) & 1u) ? 0 : i];
+#pragma unroll
+    for (int k = 0; k < CHELIS_FUSED_MAX_INPUTS; ++k)
+        if (k < fg.n_in) slot[k] = in[k];
+    static_cast<T *>(G.out)[i] = run_chain<T>(ch, slot);
 }
 
 // ---------------------------------------------------------------- unary maps
@@ -291,19 +353,17 @@ int32_t gather_contiguous(const void *src, void *dst, int32_t rank, const int64_
 
 using namespace chelis;
 
-extern "C" int32_t chelis_hip_fused_elementwise(const chelis_fused_chain *chain, const chelis_gpu_tensor *const *inputs,
-                                                int32_t n_inputs, const chelis_gpu_tensor *out) {
-    int32_t s;
+namespace chelis {
+namespace {
+
+int32_t load_chain_steps(const chelis_fused_chain *chain, int32_t n_inputs, ChainDev *ch) {
     if (!chain) return set_error(CHELIS_HIP_EDOMAIN, "fused_elementwise: null chain");
-    if ((s = check_tensor(out, "out"))) return s;
-    if (!is_float(out->dtype)) return set_error(CHELIS_HIP_EUNSUPPORTED, "fused_elementwise: f32/f64 chains only");
-    if (!is_contiguous(out)) return set_error(CHELIS_HIP_EUNSUPPORTED, "fused_elementwise: output must be contiguous");
-    if (n_inputs < 0 || n_inputs > CHELIS_FUSED_MAX_INPUTS || (n_inputs && !inputs))
+    if (n_inputs < 0 || n_inputs > CHELIS_FUSED_MAX_INPUTS)
         return set_error(CHELIS_HIP_EDOMAIN, "fused_elementwise: %d inputs (max %d)", n_inputs, CHELIS_FUSED_MAX_INPUTS);
     if (chain->n_steps < 1 || chain->n_steps > CHELIS_FUSED_MAX_STEPS)
         return set_error(CHELIS_HIP_EDOMAIN, "fused_elementwise: %d steps (1..%d)", chain->n_steps, CHELIS_FUSED_MAX_STEPS);
-    ChainDev ch{};
-    ch.n_steps = chain->n_steps;
+    *ch = ChainDev{};
+    ch->n_steps = chain->n_steps;
     for (int32_t i = 0; i < chain->n_steps; ++i) {
         const chelis_fused_step &st = chain->steps[i];
         if (st.op >= CHELIS_FUSED_COUNT_) return set_error(CHELIS_HIP_EDOMAIN, "fused_elementwise: step %d op %d", i, st.op);
@@ -312,30 +372,121 @@ extern "C" int32_t chelis_hip_fused_elementwise(const chelis_fused_chain *chain,
             if ((a >= 0 && a >= n_inputs) || (a < 0 && -a - 1 >= i))
                 return set_error(CHELIS_HIP_EDOMAIN, "fused_elementwise: step %d arg %d out of range", i, j);
         }
-        ch.op[i] = st.op;
-        ch.a0[i] = (int8_t)st.args[0];
-        ch.a1[i] = (int8_t)st.args[1];
-        ch.imm[i] = st.imm;
+        ch->op[i] = st.op;
+        ch->a0[i] = (int8_t)st.args[0];
+        ch->a1[i] = (int8_t)st.args[1];
+        ch->imm[i] = st.imm;
     }
+    return CHELIS_HIP_OK;
+}
+
+// One (inputs, output) group checked and collapsed; *flat when every
+// operand streams with the output or is a single broadcast element.
+int32_t prepare_group(const chelis_gpu_tensor *const *inputs, int32_t n_inputs, const chelis_gpu_tensor *out,
+                      Shape *sh, int64_t (*st)[kMaxRank], bool *flat) {
+    int32_t s;
+    if ((s = check_tensor(out, "out"))) return s;
+    if (!is_float(out->dtype)) return set_error(CHELIS_HIP_EUNSUPPORTED, "fused_elementwise: f32/f64 chains only");
+    if (!is_contiguous(out)) return set_error(CHELIS_HIP_EUNSUPPORTED, "fused_elementwise: output must be contiguous");
+    if (n_inputs && !inputs) return set_error(CHELIS_HIP_EDOMAIN, "fused_elementwise: null input array");
     for (int32_t k = 0; k < n_inputs; ++k)
         if ((s = check_input_against(inputs[k], out, "input"))) return s;
-    if (!out->count) return CHELIS_HIP_OK;
+    if (!collapse(out, inputs, n_inputs, sh, st))
+        return set_error(CHELIS_HIP_EUNSUPPORTED, "fused_elementwise: more than %d independent axes", kMaxRank);
+    *flat = sh->rank <= 1;
+    for (int32_t k = 0; k < n_inputs && *flat; ++k) *flat = st[k][0] == 0 || st[k][0] == 1;
+    return CHELIS_HIP_OK;
+}
+
+template <typename T>
+int32_t launch_flat(const ChainDev &ch, FlatGroups &fg, hipStream_t strm) {
+    int64_t blocks = 0;
+    for (int32_t i = 0; i < fg.n; ++i) {
+        fg.g[i].first_block = blocks;
+        blocks += (fg.g[i].count + 255) / 256;
+    }
+    if (blocks == 0) return CHELIS_HIP_OK;
+    if (blocks > 0x7fffffffLL) return set_error(CHELIS_HIP_EUNSUPPORTED, "fused_elementwise: too many elements");
+    fused_flat_kernel<T><<<(unsigned)blocks, 256, 0, strm>>>(ch, fg);
+    CHELIS_LAUNCH_CHECK();
+    return CHELIS_HIP_OK;
+}
+
+void add_group(FlatGroups &fg, const chelis_gpu_tensor *const *inputs, int32_t n_inputs, const chelis_gpu_tensor *out,
+               const int64_t (*st)[kMaxRank]) {
+    FlatGroup &g = fg.g[fg.n++];
+    g = FlatGroup{};
+    for (int32_t k = 0; k < n_inputs; ++k) {
+        g.in[k] = inputs[k]->data;
+        if (st[k][0] == 0) g.bcast |= 1u << k;
+    }
+    g.out = out->data;
+    g.count = out->count;
+}
+
+}  // namespace
+
+int32_t fused_elementwise_groups(const chelis_fused_chain *chain, int32_t n_inputs,
+                                 const chelis_gpu_tensor *const *inputs, const chelis_gpu_tensor *const *outs,
+                                 int32_t n_groups) {
+    ChainDev ch;
+    if (int32_t s = load_chain_steps(chain, n_inputs, &ch)) return s;
+    if (n_groups < 1 || !outs) return set_error(CHELIS_HIP_EDOMAIN, "fused_elementwise: no groups");
+    hipStream_t strm = stream();
+    if (!strm) return set_error(CHELIS_HIP_EHIP, "no HIP device");
+    const chelis_dtype dt = outs[0] ? outs[0]->dtype : CHELIS_DTYPE_F32;
+    FlatGroups fg{};
+    fg.n_in = n_inputs;
+    for (int32_t i = 0; i < n_groups; ++i) {
+        const chelis_gpu_tensor *const *in = inputs + (size_t)i * n_inputs;
+        Shape sh;
+        int64_t st[CHELIS_FUSED_MAX_INPUTS][kMaxRank];
+        bool flat = false;
+        if (int32_t s = prepare_group(in, n_inputs, outs[i], &sh, st, &flat)) return s;
+        if (outs[i]->dtype != dt) return set_error(CHELIS_HIP_EDOMAIN, "fused_elementwise: groups differ in dtype");
+        if (!flat) {
+            // a strided group runs on its own
+            if (int32_t s = chelis_hip_fused_elementwise(chain, in, n_inputs, outs[i])) return s;
+            continue;
+        }
+        if (fg.n == kMaxGroups) {
+            if (int32_t s = dt == CHELIS_DTYPE_F32 ? launch_flat<float>(ch, fg, strm) : launch_flat<double>(ch, fg, strm))
+                return s;
+            fg.n = 0;
+        }
+        add_group(fg, in, n_inputs, outs[i], st);
+    }
+    if (fg.n == 0) return CHELIS_HIP_OK;
+    return dt == CHELIS_DTYPE_F32 ? launch_flat<float>(ch, fg, strm) : launch_flat<double>(ch, fg, strm);
+}
+
+}  // namespace chelis
+
+using namespace chelis;
+
+extern "C" int32_t chelis_hip_fused_elementwise(const chelis_fused_chain *chain, const chelis_gpu_tensor *const *inputs,
+                                                int32_t n_inputs, const chelis_gpu_tensor *out) {
+    ChainDev ch;
+    if (int32_t s = load_chain_steps(chain, n_inputs, &ch)) return s;
     Shape sh;
     int64_t st[CHELIS_FUSED_MAX_INPUTS][kMaxRank];
-    if (!collapse(out, inputs, n_inputs, &sh, st))
-        return set_error(CHELIS_HIP_EUNSUPPORTED, "fused_elementwise: more than %d independent axes", kMaxRank);
+    bool flat = false;
+    if (int32_t s = prepare_group(inputs, n_inputs, out, &sh, st, &flat)) return s;
+    if (!out->count) return CHELIS_HIP_OK;
+    hipStream_t strm = stream();
+    if (!strm) return set_error(CHELIS_HIP_EHIP, "no HIP device");
+    if (flat) {
+        FlatGroups fg{};
+        fg.n_in = n_inputs;
+        add_group(fg, inputs, n_inputs, out, st);
+        return out->dtype == CHELIS_DTYPE_F32 ? launch_flat<float>(ch, fg, strm) : launch_flat<double>(ch, fg, strm);
+    }
     Operands ops{};
     ops.n = n_inputs;
     for (int32_t k = 0; k < n_inputs; ++k) {
         ops.o[k].p = inputs[k]->data;
         for (int a = 0; a < kMaxRank; ++a) ops.o[k].st[a] = st[k][a];
     }
-    if (sh.rank == 0) {
-        sh.rank = 1;
-        sh.ext[0] = 1;
-    }
-    hipStream_t strm = stream();
-    if (!strm) return set_error(CHELIS_HIP_EHIP, "no HIP device");
     int64_t blocks = (out->count + 255) / 256;
     if (blocks > 8192) blocks = 8192;
     if (out->dtype == CHELIS_DTYPE_F32)

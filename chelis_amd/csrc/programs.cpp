@@ -310,11 +310,9 @@ extern "C" int32_t chelis_prog_mlp_train_step(const chelis_gpu_tensor *const *in
     const chelis_fused_chain sgd =
         chain({step(CHELIS_FUSED_CONST, 0, 0, (double)lr), step(CHELIS_FUSED_MUL, prev(0), 1),
                step(CHELIS_FUSED_SUB, 0, prev(1))});
-    const chelis_gpu_tensor *pw1[2] = {w1, &gw1}, *pb1[2] = {b1, &gb1}, *pw2[2] = {w2, &gw2}, *pb2[2] = {b2, &gb2};
-    TRY(chelis_hip_fused_elementwise(&sgd, pw1, 2, out[1]));
-    TRY(chelis_hip_fused_elementwise(&sgd, pb1, 2, out[2]));
-    TRY(chelis_hip_fused_elementwise(&sgd, pw2, 2, out[3]));
-    TRY(chelis_hip_fused_elementwise(&sgd, pb2, 2, out[4]));
+    // the four parameter updates in one launch
+    const chelis_gpu_tensor *pin[8] = {w1, &gw1, b1, &gb1, w2, &gw2, b2, &gb2};
+    TRY(fused_elementwise_groups(&sgd, 2, pin, out + 1, 4));
     return CHELIS_HIP_OK;
 }
 

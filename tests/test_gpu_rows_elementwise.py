@@ -187,6 +187,33 @@ def test_f32_transcendental_chain_leaves_bit_exact(op):
     assert bits_equal(y, ref), mismatch_report(y, ref)
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_fused_chain_flat_paths(dtype):
+    """Flat maps: 16-byte vectors with a ragged tail, a scalar broadcast
+    operand, and an input one element off 16-byte alignment (scalar path)."""
+    rng = np.random.default_rng(15)
+    n = 4099
+    a, b = rng.standard_normal(n + 1).astype(dtype), rng.standard_normal(n).astype(dtype)
+    s = np.array(rng.standard_normal(), dtype)
+    da, db, ds = C.to_device(a), C.to_device(b), C.to_device(s)
+    ch = C.fused_chain([("mul", 0, 2), ("sub", ("s", 0), 1), ("exp", ("s", 1))])
+    out = C.empty((n,), dtype)
+    C.fused_elementwise(ch, [da.view((n,), (1,)), db, ds.view((n,), (0,))], out)
+    exp = (lambda v: np.array([O.lib().orc_expf(e) for e in v], np.float32)) if dtype == np.float32 else None
+    t = (a[:n] * s - b).astype(dtype)
+    if exp:
+        assert bits_equal(out.numpy(), exp(t)), mismatch_report(out.numpy(), exp(t))
+    else:
+        assert np.allclose(out.numpy(), np.exp(t), rtol=1e-12, atol=0)
+    out2 = C.empty((n,), dtype)
+    C.fused_elementwise(ch, [da.view((n,), (1,), 1), db, ds.view((n,), (0,))], out2)
+    t2 = (a[1:] * s - b).astype(dtype)
+    if exp:
+        assert bits_equal(out2.numpy(), exp(t2)), mismatch_report(out2.numpy(), exp(t2))
+    else:
+        assert np.allclose(out2.numpy(), np.exp(t2), rtol=1e-12, atol=0)
+
+
 def test_fused_chain_sgd_and_broadcast():
     """A FusedElem chain w - lr * g plus a bias-broadcast chain relu(x + b)."""
     rng = np.random.default_rng(13)
