@@ -174,7 +174,7 @@ constexpr int kMinWavesPerEu = sizeof(T) == 8 ? 2 : 1;
 // Split K (kchunk > 0): grid.z slices K into runs of kchunk (a multiple of
 // BK) and each slice stores its raw sums to part[slice][z][m][n]; a combine
 // pass adds the slices in slice order and applies the epilogue.
-template <typename T, int ALAY, int BLAY, int TM>
+template <typename T, int ALAY, int BLAY, int TM, bool GELU>
 __global__ __launch_bounds__(THREADS, kMinWavesPerEu<T>) void gemm_mfma_kernel(GemmProblem p, int64_t tiles_m,
                                                                                int64_t tiles_n, bool a_vec,
                                                                                bool b_vec, T *part,
@@ -284,7 +284,8 @@ __global__ __launch_bounds__(THREADS, kMinWavesPerEu<T>) void gemm_mfma_kernel(G
             for (int r = 0; r < 4; ++r) {
                 const int64_t m = m0 + wm * WT + i * 16 + M::row(fq, r);
                 const int64_t n = n0 + wn * WT + j * 16 + fr;
-                if (m < p.M && n < p.N) C[m * p.scm + n * p.scn] = gemm_epilogue<T>(acc[i][j][r], p, z0, z1, m, n);
+                if (m < p.M && n < p.N)
+                    C[m * p.scm + n * p.scn] = gemm_epilogue<T, GELU>(acc[i][j][r], p, z0, z1, m, n);
             }
 }
 
@@ -318,10 +319,30 @@ int lay_of(int64_t s_outer, int64_t s_k, const void *base, int64_t outer, int64_
     return 2;
 }
 
+// Occupancy of the f32 128-tile kernel without the GELU epilogue: its
+// registers allow three workgroups per CU, but a grid of T tiles then runs in
+// ceil(T / 3C) rounds of three; two per CU (ceil(T / 2C) rounds of two) is
+// chosen when that is fewer workgroup-slots in all, e.g. 1024 tiles on 256
+// CUs run as two full rounds of two rather than a round of three and a third
+// of one (measured 1.42 ms against 1.54 ms at 4096^3), while 768 tiles run
+// as one round of three (344 us against 407 us at 4096 x 3072 x 1024).
+// Dynamic LDS beyond a third of the CU's 160 KiB pins two.
+constexpr size_t kPinTwoLds = 16384;
+
 template <typename T, int AL, int BL, int TM>
 void launch_mfma(const GemmProblem &p, dim3 grid, int64_t tm, int64_t tn, bool av, bool bv, T *part, int64_t kchunk,
                  hipStream_t st) {
-    gemm_mfma_kernel<T, AL, BL, TM><<<grid, THREADS, 0, st>>>(p, tm, tn, av, bv, part, kchunk);
+    // split-K slices store raw sums: the combine pass applies the epilogue
+    if (p.act == CHELIS_ACT_GELU && kchunk == 0) {
+        gemm_mfma_kernel<T, AL, BL, TM, true><<<grid, THREADS, 0, st>>>(p, tm, tn, av, bv, part, kchunk);
+        return;
+    }
+    size_t dyn = 0;
+    if (sizeof(T) == 4 && TM == 4) {
+        const int64_t C = device_cus(), t = (int64_t)grid.x * grid.y * grid.z;
+        if (((t + 2 * C - 1) / (2 * C)) * 2 <= ((t + 3 * C - 1) / (3 * C)) * 3) dyn = kPinTwoLds;
+    }
+    gemm_mfma_kernel<T, AL, BL, TM, false><<<grid, THREADS, dyn, st>>>(p, tm, tn, av, bv, part, kchunk);
 }
 
 // Slices of K for a product whose tiles cannot fill the chip: enough slices
@@ -386,13 +407,14 @@ int32_t run_mfma(const GemmProblem &p, hipStream_t st) {
     bool av = false, bv = false;
     const int al = lay_of<T>(p.sam, p.sak, p.a, p.M, p.K, &av);
     const int bl = lay_of<T>(p.sbn, p.sbk, p.b, p.N, p.K, &bv);
-    // 128-tiles when they give every CU two tiles, no dimension is at most
-    // half a tile and K runs long enough (> 128) to amortize a tile's first
-    // loads and its epilogue; 64-tiles, four times as many workgroups that
-    // overlap those phases, otherwise (measured: the 128 x (512 x 512 x 64)
-    // attention scores take 80 us on 64-tiles against 132 us on 128-tiles).
+    // 128-tiles when they give every CU a tile, no dimension is at most half
+    // a tile and K runs long enough (> 128) to amortize a tile's first loads
+    // and its epilogue (measured: 4096 x 1024 x 1024 takes 115 us on 256
+    // 128-tiles against 120 us on 1024 64-tiles); 64-tiles, four times as
+    // many workgroups that overlap those phases, otherwise (the 128 x (512 x
+    // 512 x 64) attention scores take 80 us on 64-tiles against 132 us).
     const int64_t big = ((p.M + 127) / 128) * ((p.N + 127) / 128) * p.nb0 * p.nb1;
-    const bool small = big < 2 * (int64_t)device_cus() || p.M <= 64 || p.N <= 64 || p.K <= 128;
+    const bool small = big < (int64_t)device_cus() || p.M <= 64 || p.N <= 64 || p.K <= 128;
     return small ? run_tiles<T, 2>(p, al, bl, av, bv, st) : run_tiles<T, 4>(p, al, bl, av, bv, st);
 }
 
