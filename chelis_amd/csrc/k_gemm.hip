@@ -30,6 +30,8 @@
 // shared inside that XCD's L2.
 #include "gemm.h"
 
+#include <type_traits>
+
 namespace chelis {
 namespace {
 
@@ -81,11 +83,32 @@ struct Stage {
     static constexpr int NV = NE / V;               // vectors per thread
     T r[NE];
 
-    // element (row, k) lives at base[row * s_row + k * s_k]
+    // element (row, k) lives at base[row * s_row + k * s_k]. CHECK = false:
+    // the caller guarantees aligned vectors inside the operand (LAY 0 or 1),
+    // so every load is an unconditional 16-byte vector load; straight-line
+    // loads let the compiler wait for exactly the older ones.
+    template <bool CHECK = true>
     __device__ void load(const T *__restrict__ base, int64_t s_row, int64_t s_k, int64_t row0, int64_t rows,
                          int64_t k0, int64_t K, bool vec_ok) {
         const int t = threadIdx.x;
-        if constexpr (LAY == 0) {
+        if constexpr (!CHECK && LAY != 2) {
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const int idx = t + THREADS * j;
+                const T *p;
+                if constexpr (LAY == 0) {
+                    const int row = idx / (BK / V), kv = (idx % (BK / V)) * V;
+                    p = base + (row0 + row) * s_row + (k0 + kv);
+                } else {
+                    const int k = idx % BK, rv = (idx / BK) * V;
+                    p = base + (row0 + rv) + (k0 + k) * s_k;
+                }
+                typename Vec16<T>::type q = *reinterpret_cast<const typename Vec16<T>::type *>(p);
+                const T *qe = reinterpret_cast<const T *>(&q);
+#pragma unroll
+                for (int u = 0; u < V; ++u) r[j * V + u] = qe[u];
+            }
+        } else if constexpr (LAY == 0) {
 #pragma unroll
             for (int j = 0; j < NV; ++j) {
                 const int idx = t + THREADS * j;
@@ -223,22 +246,35 @@ __global__ __launch_bounds__(THREADS, kMinWavesPerEu<T>) void gemm_mfma_kernel(G
 #pragma unroll
         for (int j = 0; j < TM; ++j) acc[i][j] = acc_t{};
 
-    Stage<T, ALAY, BM> sa;
-    Stage<T, BLAY, BN> sb;
+    // Two register staging sets: the global loads of step s + 3 are issued
+    // right after step s + 1 leaves its set for LDS, so each load has two
+    // whole k-steps to arrive before its own store.
+    Stage<T, ALAY, BM> sa0, sa1;
+    Stage<T, BLAY, BN> sb0, sb1;
     const int64_t ksteps = (K + BK - 1) / BK;
-    sa.load(A, p.sam, p.sak, m0, p.M, 0, K, a_vec);
-    sb.load(B, p.sbn, p.sbk, n0, p.N, 0, K, b_vec);
-    sa.store(As[0]);
-    sb.store(Bs[0]);
-    __syncthreads();
+    // an interior tile of aligned operands and whole K steps loads without checks
+    const bool inside = a_vec && b_vec && ALAY != 2 && BLAY != 2 && m0 + BM <= p.M && n0 + BN <= p.N && K % BK == 0;
 
-    for (int64_t ks = 0; ks < ksteps; ++ks) {
+    // step ks computes from LDS buffer ks % 2; (sa_n, sb_n) hold step ks + 1
+    // The body has no branches around its loads and stores: a step past the
+    // last is clamped to the last, so the extra loads read valid memory and
+    // the extra store fills the LDS buffer no later step reads. Straight-line
+    // memory operations let the compiler wait for exactly the older loads.
+    auto run = [&](auto check) {
+    constexpr bool CK = decltype(check)::value;
+    const int64_t last = ksteps - 1;
+    auto kstep = [&](int64_t s) { return (s < last ? s : last) * BK; };
+    sa0.template load<CK>(A, p.sam, p.sak, m0, p.M, 0, K, a_vec);
+    sb0.template load<CK>(B, p.sbn, p.sbk, n0, p.N, 0, K, b_vec);
+    sa1.template load<CK>(A, p.sam, p.sak, m0, p.M, kstep(1), K, a_vec);
+    sb1.template load<CK>(B, p.sbn, p.sbk, n0, p.N, kstep(1), K, b_vec);
+    sa0.store(As[0]);
+    sb0.store(Bs[0]);
+    sa0.template load<CK>(A, p.sam, p.sak, m0, p.M, kstep(2), K, a_vec);
+    sb0.template load<CK>(B, p.sbn, p.sbk, n0, p.N, kstep(2), K, b_vec);
+    __syncthreads();
+    auto step = [&](int64_t ks, Stage<T, ALAY, BM> &sa_n, Stage<T, BLAY, BN> &sb_n) {
         const int buf = ks & 1;
-        const bool more = ks + 1 < ksteps;
-        if (more) {
-            sa.load(A, p.sam, p.sak, m0, p.M, (ks + 1) * BK, K, a_vec);
-            sb.load(B, p.sbn, p.sbk, n0, p.N, (ks + 1) * BK, K, b_vec);
-        }
         typename Vec16<T>::type af[TM], bf[TM];
 #pragma unroll
         for (int i = 0; i < TM; ++i)
@@ -254,12 +290,21 @@ __global__ __launch_bounds__(THREADS, kMinWavesPerEu<T>) void gemm_mfma_kernel(G
                 for (int j = 0; j < TM; ++j)
                     acc[i][j] = M::step(reinterpret_cast<const T *>(&af[i])[t], reinterpret_cast<const T *>(&bf[j])[t],
                                         acc[i][j]);
-        if (more) {
-            sa.store(As[buf ^ 1]);
-            sb.store(Bs[buf ^ 1]);
-        }
+        sa_n.store(As[buf ^ 1]);
+        sb_n.store(Bs[buf ^ 1]);
+        sa_n.template load<CK>(A, p.sam, p.sak, m0, p.M, kstep(ks + 3), K, a_vec);
+        sb_n.template load<CK>(B, p.sbn, p.sbk, n0, p.N, kstep(ks + 3), K, b_vec);
         __syncthreads();
+    };
+    int64_t ks = 0;
+    for (; ks + 1 < ksteps; ks += 2) {
+        step(ks, sa1, sb1);
+        step(ks + 1, sa0, sb0);
     }
+    if (ks < ksteps) step(ks, sa1, sb1);
+    };
+    if (inside) run(std::false_type{});
+    else run(std::true_type{});
 
     if (kchunk > 0) {
         T *P = part + ((int64_t)blockIdx.z * gridDim.y + z) * p.M * p.N;
