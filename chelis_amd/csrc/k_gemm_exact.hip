@@ -122,7 +122,38 @@ __global__ __launch_bounds__(256) void tree_wave_kernel(GemmProblem p, int64_t o
     constexpr int SEG = 64 * V;
     const int64_t nseg = (p.K + SEG - 1) / SEG;
     T lvl[DEPTH];
-    for (int64_t s = 0; s < nseg; ++s) {
+    int64_t s = 0;
+    if (AK && BK && a_vec && b_vec) {
+        // whole segments of contiguous, aligned runs: branch-free vector
+        // loads, the next segment's loads in flight while this one is summed
+        // (the last prefetch is clamped to the last whole segment)
+        const int64_t nfull = p.K / SEG;
+        T a0[V], b0[V], a1[V], b1[V];
+        auto fetch = [&](int64_t seg, T(&a)[V], T(&b)[V]) {
+            const int64_t k = (seg < nfull ? seg : nfull - 1) * SEG + (int64_t)lane * V;
+            load_run<T, V, true>(A + k, 1, 0, SEG, true, a);
+            load_run<T, V, true>(B + k, 1, 0, SEG, true, b);
+        };
+        auto sum = [&](int64_t seg, T(&a)[V], const T(&b)[V]) {
+#pragma unroll
+            for (int u = 0; u < V; ++u) a[u] = a[u] * b[u];
+            carry_push<T, DEPTH>(lvl, seg, wave_tree_sum(tree_v<T, V>(a)));
+        };
+        // unrolled by two so the two register sets swap roles without copies
+        // (a copy of a prefetched set would wait for its loads at once)
+        if (nfull > 0) fetch(0, a0, b0);
+        for (; s + 1 < nfull; s += 2) {
+            fetch(s + 1, a1, b1);
+            sum(s, a0, b0);
+            fetch(s + 2, a0, b0);
+            sum(s + 1, a1, b1);
+        }
+        if (s < nfull) {
+            sum(s, a0, b0);
+            ++s;
+        }
+    }
+    for (; s < nseg; ++s) {
         const int64_t k = s * SEG + (int64_t)lane * V;
         T a[V], b[V];
         load_run<T, V, AK>(A + k * p.sak, p.sak, k, p.K, a_vec, a);
