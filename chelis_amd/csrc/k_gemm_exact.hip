@@ -127,25 +127,47 @@ __global__ __launch_bounds__(256) void tree_wave_kernel(GemmProblem p, int64_t o
         // whole segments of contiguous, aligned runs: branch-free vector
         // loads, the next segment's loads in flight while this one is summed
         // (the last prefetch is clamped to the last whole segment)
+        // Layout: vector q of lane l holds the W leaves at 64W q + W l, so
+        // each load instruction of the wave reads one contiguous 1 KiB run
+        // (nontemporal: the matrix is read once). Quarter q of the segment,
+        // [64W q, 64W (q + 1)), is an aligned subtree: W-leaf trees in the
+        // lanes, joined across the wave, then the quarters in order.
+        constexpr int W = Vec16<T>::W, NQ = V / W;
+        typedef T nv __attribute__((ext_vector_type(W)));
         const int64_t nfull = p.K / SEG;
         T a0[V], b0[V], a1[V], b1[V];
         auto fetch = [&](int64_t seg, T(&a)[V], T(&b)[V]) {
-            const int64_t k = (seg < nfull ? seg : nfull - 1) * SEG + (int64_t)lane * V;
-            load_run<T, V, true>(A + k, 1, 0, SEG, true, a);
-            load_run<T, V, true>(B + k, 1, 0, SEG, true, b);
+            const int64_t k = (seg < nfull ? seg : nfull - 1) * SEG + (int64_t)lane * W;
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                const nv va = __builtin_nontemporal_load(reinterpret_cast<const nv *>(A + k + q * 64 * W));
+                const nv vb = *reinterpret_cast<const nv *>(B + k + q * 64 * W);
+#pragma unroll
+                for (int u = 0; u < W; ++u) a[q * W + u] = va[u], b[q * W + u] = vb[u];
+            }
         };
         auto sum = [&](int64_t seg, T(&a)[V], const T(&b)[V]) {
+            T quarter[NQ];
 #pragma unroll
-            for (int u = 0; u < V; ++u) a[u] = a[u] * b[u];
-            carry_push<T, DEPTH>(lvl, seg, wave_tree_sum(tree_v<T, V>(a)));
+            for (int q = 0; q < NQ; ++q) {
+                T x[W];
+#pragma unroll
+                for (int u = 0; u < W; ++u) x[u] = a[q * W + u] * b[q * W + u];
+                quarter[q] = wave_tree_sum(tree_v<T, W>(x));
+            }
+            carry_push<T, DEPTH>(lvl, seg, tree_v<T, NQ>(quarter));
         };
         // unrolled by two so the two register sets swap roles without copies
         // (a copy of a prefetched set would wait for its loads at once)
+        // (the scheduling barriers keep each prefetch ahead of the sum that
+        // follows it: sunk below, its loads would be waited for at once)
         if (nfull > 0) fetch(0, a0, b0);
         for (; s + 1 < nfull; s += 2) {
             fetch(s + 1, a1, b1);
+            __builtin_amdgcn_sched_barrier(0);
             sum(s, a0, b0);
             fetch(s + 2, a0, b0);
+            __builtin_amdgcn_sched_barrier(0);
             sum(s + 1, a1, b1);
         }
         if (s < nfull) {
