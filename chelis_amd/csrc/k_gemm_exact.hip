@@ -549,6 +549,30 @@ __global__ __launch_bounds__(256) void tree_combine_kernel(PanelView v, GemmProb
     panel_store<T>(p, v, z / p.nb1, z % p.nb1, m, n, total);
 }
 
+// The same join for few outputs with many block totals: one wave per
+// output, total j in lane j % 64 of segment j / 64 (-0.0 past nparts, at
+// most four segments), each segment joined by the wave tree, then the
+// segments in order. That is the full tree over the totals padded to 256
+// with -0.0, i.e. their canonical tree: the same bits as the thread form.
+template <typename T>
+__global__ __launch_bounds__(256) void tree_combine_wave_kernel(PanelView v, GemmProblem p,
+                                                                const T *__restrict__ part, int64_t nparts,
+                                                                int64_t nz) {
+    const int lane = threadIdx.x & 63;
+    const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (w >= nz * v.M * v.N) return;  // whole waves leave together
+    const int64_t n = w % v.N, zm = w / v.N, m = zm % v.M, z = zm / v.M;
+    const int64_t per_z = v.M * 64, idx = (z * v.M + m) * 64 + n;
+    T seg[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const int64_t j = s * 64 + lane;
+        seg[s] = wave_tree_sum(j < nparts ? part[j * nz * per_z + idx] : T(-0.0));
+    }
+    const T total = (seg[0] + seg[1]) + (seg[2] + seg[3]);
+    if (lane == 0) panel_store<T>(p, v, z / p.nb1, z % p.nb1, m, n, total);
+}
+
 // ---------------------------------------------------------------- thread per output
 // Short K (<= 32): one thread per output, n fastest so B and C accesses
 // coalesce. The K leaves are padded with -0.0 to P = 2^ceil(log2 K) and
@@ -688,7 +712,13 @@ int32_t launch_panel(const GemmProblem &p, const PanelView &v, bool cut, hipStre
     }
     hipError_t le = hipGetLastError();
     if (le == hipSuccess && nparts > 1) {
-        tree_combine_kernel<T><<<grid_for(nz * v.M * 64, 256), 256, 0, st>>>(v, p, ws, nparts, nz);
+        // many totals for few outputs: lanes over the totals (a thread per
+        // output would read its totals one batch after another)
+        const int64_t outputs = nz * v.M * v.N;
+        if (nparts >= 32 && outputs <= 65536)
+            tree_combine_wave_kernel<T><<<grid_for(outputs, 4), 256, 0, st>>>(v, p, ws, nparts, nz);
+        else
+            tree_combine_kernel<T><<<grid_for(nz * v.M * 64, 256), 256, 0, st>>>(v, p, ws, nparts, nz);
         le = hipGetLastError();
     }
     scratch_free(ws, ws_bytes);
