@@ -27,7 +27,15 @@ __device__ inline double random_unit(uint64_t key, uint64_t index) {
 // ---------------------------------------------------------------- math leaves
 template <typename T> __device__ inline T leaf_exp(T v);
 template <> __device__ inline float leaf_exp<float>(float v) { return expf_cr(v); }
-template <> __device__ inline double leaf_exp<double>(double v) { return canon(exp(v)); }
+// Binary64 exp: the branch-free fast path, and for the rare flagged input
+// (about one in 2^19, plus NaN and the saturated and subnormal ranges) the
+// 128-bit fixed-point path out of line.
+__device__ __noinline__ inline double exp_slow64(double v) { return exp_cr_slow(v); }
+template <> __device__ inline double leaf_exp<double>(double v) {
+    bool slow;
+    const double y = exp_fast(v, Exp2TableConst{}, slow);
+    return slow ? exp_slow64(v) : y;
+}
 template <typename T> __device__ inline T leaf_erfc(T v);
 template <typename T> __device__ inline T leaf_log(T v);
 template <typename T> __device__ inline T leaf_tanh(T v);

@@ -188,4 +188,251 @@ CHELIS_HD inline float expf_cr_nonpos(float xf) {
 // against IEEE division on the host (tests/test_devmath.py).
 CHELIS_HD inline float quot_f32(float v, double inv) { return (float)((double)v * inv); }
 
+// ------------------------------------------------------------ binary64 exp
+//
+// Correctly rounded binary64 exp in two stages, both on the reduction
+// x = k ln2/64 + r, k the integer nearest x * 64/ln2 (|k| < 2^17 on the
+// finite range), exp(x) = 2^m * 2^(j/64) * exp(r), k = 64m + j, |r| <= ln2/128
+// (plus 2^-30 relative for the rounding of x * 64/ln2).
+//
+// exp_fast: binary64 and double-double arithmetic to an error below 2^-73.7
+// (bound derived at the function), then Ziv's rounding test: the
+// result is returned when both ends of the error interval round to the same
+// binary64 number (all but about one input in 2^19).
+//
+// exp_cr_fx: 128-bit fixed-point arithmetic to an error below 2^-124.4
+// relative, rounded at the binary64 (or subnormal) grid of the result. The
+// inputs whose exp lies closest to a binary64 rounding midpoint need about
+// 2^-113 (Lefevre and Muller's worst cases for exp over the binary64
+// domain), so this rounding is the correct one; the sampled worst cases of
+// tests/golden/exp_worst_cases.txt and CORE-MATH on random inputs are
+// checked on the host and on the device.
+
+struct U128 {
+    uint64_t hi, lo;
+};
+
+// 64 x 64 -> 128-bit product from 32-bit halves (the same integer result on
+// host and device).
+CHELIS_HD inline uint64_t mul64_wide(uint64_t a, uint64_t b, uint64_t *lo) {
+    const uint64_t a0 = (uint32_t)a, a1 = a >> 32, b0 = (uint32_t)b, b1 = b >> 32;
+    const uint64_t p00 = a0 * b0, p01 = a0 * b1, p10 = a1 * b0, p11 = a1 * b1;
+    const uint64_t mid = (p00 >> 32) + (uint32_t)p01 + (uint32_t)p10;
+    *lo = (mid << 32) | (uint32_t)p00;
+    return p11 + (p01 >> 32) + (p10 >> 32) + (mid >> 32);
+}
+
+// floor(a * b / 2^128), exactly.
+CHELIS_HD inline U128 mulhi128(U128 a, U128 b) {
+    uint64_t l00, l01, l10, l11;
+    const uint64_t h00 = mul64_wide(a.lo, b.lo, &l00);
+    const uint64_t h01 = mul64_wide(a.lo, b.hi, &l01);
+    const uint64_t h10 = mul64_wide(a.hi, b.lo, &l10);
+    const uint64_t h11 = mul64_wide(a.hi, b.hi, &l11);
+    uint64_t w1 = h00 + l01;
+    uint64_t c1 = w1 < l01;
+    w1 += l10;
+    c1 += w1 < l10;
+    uint64_t w2 = h01 + h10;
+    uint64_t c2 = w2 < h10;
+    w2 += l11;
+    c2 += w2 < l11;
+    w2 += c1;
+    c2 += w2 < c1;
+    return {h11 + c2, w2};
+}
+
+CHELIS_HD inline U128 add128(U128 a, U128 b) {
+    U128 r;
+    r.lo = a.lo + b.lo;
+    r.hi = a.hi + b.hi + (r.lo < a.lo);
+    return r;
+}
+CHELIS_HD inline U128 sub128(U128 a, U128 b) {
+    U128 r;
+    r.lo = a.lo - b.lo;
+    r.hi = a.hi - b.hi - (a.lo < b.lo);
+    return r;
+}
+CHELIS_HD inline U128 shr128(U128 a, int s) {  // 0 <= s
+    if (s >= 128) return {0, 0};
+    if (s >= 64) return {0, a.hi >> (s - 64)};
+    if (s == 0) return a;
+    return {a.hi >> s, (a.lo >> s) | (a.hi << (64 - s))};
+}
+CHELIS_HD inline U128 shl128(U128 a, int s) {  // 0 <= s < 128
+    if (s >= 64) return {a.lo << (s - 64), 0};
+    if (s == 0) return a;
+    return {(a.hi << s) | (a.lo >> (64 - s)), a.lo << s};
+}
+CHELIS_HD inline bool less128(U128 a, U128 b) { return a.hi < b.hi || (a.hi == b.hi && a.lo < b.lo); }
+CHELIS_HD inline U128 table128(const unsigned long long (&w)[2]) { return {w[0], w[1]}; }
+
+// d * 2^s truncated toward zero, as a two's complement 128-bit integer;
+// |d| 2^s < 2^127.
+CHELIS_HD inline U128 fixed_scaled(double d, int s) {
+    const uint64_t b = f64_bits(d);
+    const int be = (int)((b >> 52) & 0x7ff);
+    if (be == 0) return {0, 0};  // zero or subnormal: far below the 2^-s resolution here
+    const U128 m = {0, (b & 0xfffffffffffffull) | (1ull << 52)};
+    const int sh = be - 1075 + s;  // d = m * 2^(be - 1075)
+    const U128 mag = sh >= 0 ? shl128(m, sh) : shr128(m, -sh);
+    return (b >> 63) ? sub128(U128{0, 0}, mag) : mag;
+}
+
+// exp(x) = Y 2^(m - 126) for -745.2 <= x <= 709.79, Y within 5.9 units of
+// the exact value, 2^-124.4 relative (Y >= 0.99 * 2^126).
+//
+// r = x - k (HI + LO + LO2): x - k HI is exact (HI has 36 significant bits),
+// k LO and k LO2 are split exactly into double-double products, and the
+// five terms are summed in fixed point at 2^-134 (truncation error below
+// 4 * 2^-134; c - HI - LO - LO2 is below 2^-152, times |k| < 2^17).
+// exp(r) by Horner over 1/n!, n = 0..13, at 2^-127 (the omitted terms are
+// below 2^-141; each step's truncation adds at most 1.03 units of 2^-127 and
+// earlier errors shrink by |r| < 2^-7.5, so the sum is within 1.7 units).
+// Y = T[j] exp(r) at 2^-126 with T[j] within half a unit of 2^-127: within
+// 0.5 + 2 * 1.7 + 2 = 5.9 units of 2^-127 of the exact product.
+CHELIS_HD inline U128 exp_fx(double x, int &m) {
+    const double kd = rint(x * CHELIS_INV_LN2_64);
+    const int k = (int)kd;
+    const double rhi = fma(-kd, CHELIS_LN2_64_HI36, x);  // exact
+    const double t = kd * CHELIS_LN2_64_LO36;
+    const double tl = fma(kd, CHELIS_LN2_64_LO36, -t);
+    const double u = kd * CHELIS_LN2_64_LO36B;
+    const double ul = fma(kd, CHELIS_LN2_64_LO36B, -u);
+    U128 r = fixed_scaled(rhi, 134);
+    r = sub128(r, fixed_scaled(t, 134));
+    r = sub128(r, fixed_scaled(tl, 134));
+    r = sub128(r, fixed_scaled(u, 134));
+    r = sub128(r, fixed_scaled(ul, 134));
+    const bool neg = (int64_t)r.hi < 0;
+    const U128 ra = neg ? sub128(U128{0, 0}, r) : r;
+    U128 p = table128(chelis_inv_fact_fx[13]);
+    for (int n = 12; n >= 0; --n) {
+        const U128 term = shr128(mulhi128(ra, p), 6);  // |r| p at 2^-127
+        const U128 c = table128(chelis_inv_fact_fx[n]);
+        p = neg ? sub128(c, term) : add128(c, term);
+    }
+    const int j = k & 63;
+    m = (k - j) / 64;
+    return mulhi128(table128(chelis_exp2_64_fx[j]), p);
+}
+
+// Correctly rounded exp for -745.2 <= x <= 709.79: Y of exp_fx rounded to
+// nearest at the cut where the result keeps 53 bits, or at 2^-1074 in the
+// subnormal range.
+CHELIS_HD inline double exp_cr_fx(double x) {
+    int m;
+    const U128 y = exp_fx(x, m);
+    const int lead = y.hi >> 63 ? 127 : (y.hi >> 62 ? 126 : 125);
+    int cut = lead - 52;
+    if (-948 - m > cut) cut = -948 - m;  // below 2^-1022: the subnormal grid 2^-1074
+    if (cut > 128) return 0.0;           // below half the least subnormal
+    const U128 kept = shr128(y, cut);
+    const U128 rem = cut >= 128 ? y : sub128(y, shl128(kept, cut));
+    const U128 half = shl128(U128{0, 1}, cut - 1);
+    uint64_t q = kept.lo;
+    if (less128(half, rem) || (!less128(rem, half) && (q & 1))) ++q;
+    return ldexp((double)q, cut + m - 126);
+}
+
+// Binary64 exp, fast path, branch free: exp_dd evaluates exp(x) as
+// (yh + yl) 2^m, exp_fast returns the rounded result and sets `slow` when it
+// is not known to be the correctly rounded one (and for NaN, x <= -708 and,
+// unless NONPOS, x >= 709; NONPOS instances serve arguments known to be <= 0
+// or NaN, and a positive argument would take the fast path unchecked).
+// `tab(j, hi, lo)` supplies 2^(j/64) as a double-double: a constant-memory
+// table, or (inside a full wave) the lane-held copy of it.
+//
+// Error budget on -708 < x < 709 (|k| < 2^16, results normal, no overflow),
+// absolute on y = T[j] exp(r) < 2.02:
+// - r = rh + rl: x - k HI exact, k LO split exactly as t + tl; rh = rhi - t
+//   with its rounding error recovered exactly when |rhi| >= |t| and to 2^-81
+//   otherwise (then |r| < 2^-28); the omitted k (c - HI - LO) is below
+//   2^16 * 2^-99 = 2^-83;
+// - exp(r) - 1 = rh + rh^2/2 + rh^3 C(rh) + rl (1 + qh) with C the Taylor
+//   coefficients 1/3! .. 1/8! (omitted degree 9: 2^-86.2; rl^2 and
+//   rl rh^3/6: below 2^-86): rh^2 exact as sh + sl, qh + e1 = rh + sh/2
+//   exactly (Fast2Sum); the cubic part P carries at most 4.2 roundings of
+//   2^-53 relative on |P| < 2^-25.16 (2^-76.1) and is added, with the low
+//   terms, into ql (|ql| < 2^-25; two roundings below 2^-78.2 each);
+// - T[j] = th + tl within 2^-107; th qh split exactly (ph + pl), yh + e2 =
+//   th + ph exactly (Fast2Sum); yl sums e2, pl, th ql and tl (1 + qh), of
+//   magnitude below 2^-24, with three roundings below 2^-77.2 each; the
+//   omitted tl ql is below 2^-78.
+// Total below 2^-73.7 (2 * 2^-76.1 + 5 * 2^-77.2 + 2^-78 + smaller terms,
+// times T[j] < 2 where the terms are relative to exp(r)); the host check
+// measures the largest error over 2 * 10^7 inputs against the fixed-point
+// value and requires it below that bound. The rounding test uses eps =
+// 2^-72.
+struct ExpDD {
+    double yh, yl;
+    int m;
+};
+template <class Tab2>
+CHELIS_HD inline ExpDD exp_dd(double x, const Tab2 &tab) {
+    const double shifted = fma(x, CHELIS_INV_LN2_64, 0x1.8p52);
+    const double kd = shifted - 0x1.8p52;
+    const int k = (int)(uint32_t)f64_bits(shifted);
+    const double rhi = fma(-kd, CHELIS_LN2_64_HI36, x);  // exact on the fast range
+    const double t = kd * CHELIS_LN2_64_LO36;
+    const double tl = fma(kd, CHELIS_LN2_64_LO36, -t);
+    const double rh = rhi - t;  // Fast2Sum when |rhi| >= |t|; else |r| < 2^-28
+    const double rl = ((rhi - rh) - t) - tl;
+    const double sh = rh * rh;
+    const double sl = fma(rh, rh, -sh);
+    double c = fma(rh, 0x1.a01a01a01a01ap-16, 0x1.a01a01a01a01ap-13);  // 1/8!, 1/7!
+    c = fma(rh, c, 0x1.6c16c16c16c17p-10);                              // 1/6!
+    c = fma(rh, c, 0x1.1111111111111p-7);                               // 1/5!
+    c = fma(rh, c, 0x1.5555555555555p-5);                               // 1/4!
+    c = fma(rh, c, 0x1.5555555555555p-3);                               // 1/3!
+    const double P = (sh * rh) * c;
+    const double half = 0.5 * sh;
+    const double qh = rh + half;  // Fast2Sum: |rh| >= rh^2/2
+    const double e1 = half - (qh - rh);
+    const double ql = e1 + (P + (rl + fma(qh, rl, 0.5 * sl)));
+    double th, tlo;
+    tab(k & 63, th, tlo);
+    const double ph = th * qh;
+    const double pl = fma(th, qh, -ph);
+    const double yh = th + ph;  // Fast2Sum: th >= 1 > |ph|
+    const double e2 = ph - (yh - th);
+    const double yl = e2 + (pl + fma(th, ql, fma(tlo, qh, tlo)));
+    return {yh, yl, (k - (k & 63)) / 64};
+}
+
+template <bool NONPOS = false, class Tab2>
+CHELIS_HD inline double exp_fast(double x, const Tab2 &tab, bool &slow) {
+    const bool fast = NONPOS ? x > -708.0 : (x > -708.0 && x < 709.0);
+    const ExpDD d = exp_dd(x, tab);
+    constexpr double eps = 0x1p-72;
+    const double a = d.yh + (d.yl - eps);
+    const double b = d.yh + (d.yl + eps);
+    slow = !fast || a != b;
+    return ldexp(a, d.m);
+}
+
+struct Exp2TableConst {
+    CHELIS_HD void operator()(int j, double &hi, double &lo) const {
+        hi = chelis_exp2_64_tab[j][0];
+        lo = chelis_exp2_64_tab[j][1];
+    }
+};
+
+// The binary64 exp's slow path with its special cases: NaN -> the canonical
+// NaN; above 709.79 (with +inf) -> +inf; below -745.2 (with -inf) -> +0.
+CHELIS_HD inline double exp_cr_slow(double x) {
+    if (x != x) return f64_from(0x7ff8000000000000ull);
+    if (x > 709.79) return f64_from(0x7ff0000000000000ull);
+    if (x < -745.2) return 0.0;
+    return exp_cr_fx(x);
+}
+
+// Correctly rounded binary64 exp (any input).
+CHELIS_HD inline double exp_cr(double x) {
+    bool slow;
+    const double y = exp_fast(x, Exp2TableConst{}, slow);
+    return slow ? exp_cr_slow(x) : y;
+}
+
 }  // namespace chelis

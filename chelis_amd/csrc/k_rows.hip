@@ -24,7 +24,7 @@
 // left to right, butterfly with the lower lane as the left operand,
 // waves and segments in order. Padding is -inf, which never displaces an
 // earlier element.
-#include "hip_common.h"
+#include "chain.h"
 
 namespace chelis {
 namespace {
@@ -74,7 +74,7 @@ __device__ inline float exp_leaf<float>(float v) {
 }
 template <>
 __device__ inline double exp_leaf<double>(double v) {
-    return canon(exp(v));
+    return leaf_exp<double>(v);
 }
 
 // 2^(j/64), j = 0..63, held one entry per lane (lane j holds T[j]); a
@@ -83,6 +83,30 @@ struct ExpTableLanes {
     double t;
     __device__ explicit ExpTableLanes(int lane) : t(chelis_exp2_64_tab[lane][0]) {}
     __device__ double operator()(int j) const { return __shfl(t, j, 64); }
+};
+
+// 2^(j/64) as a double-double, held one entry per lane like ExpTableLanes.
+struct Exp2TableLanes {
+    double hi, lo;
+    __device__ explicit Exp2TableLanes(int lane)
+        : hi(chelis_exp2_64_tab[lane][0]), lo(chelis_exp2_64_tab[lane][1]) {}
+    __device__ void operator()(int j, double &h, double &l) const {
+        h = __shfl(hi, j, 64);
+        l = __shfl(lo, j, 64);
+    }
+};
+
+// The lane-held exp table of each dtype. Kernels build it before their row
+// loads, so waiting for it never waits for a row.
+template <typename T>
+struct RowExpTab;
+template <>
+struct RowExpTab<float> {
+    using type = ExpTableLanes;
+};
+template <>
+struct RowExpTab<double> {
+    using type = Exp2TableLanes;
 };
 
 // Which of a lane's NE exp results need the correctly rounded fallback.
@@ -267,7 +291,8 @@ __device__ inline T softmax_arg(T raw, int64_t j, int64_t qi, int masked, T scal
 // exit; xr is the row in memory (re-read only by the rare exp fallback).
 template <typename T, int V, int S, int W, int R>
 __device__ inline void softmax_row(T (&v)[S][V], const T *__restrict__ xr, int64_t row, int64_t n, int masked,
-                                   T scale, int64_t q_len, T *lds, const RowCoord<W, R> &c) {
+                                   T scale, int64_t q_len, T *lds, const RowCoord<W, R> &c,
+                                   const typename RowExpTab<T>::type &tab) {
     constexpr int SEG = 64 * W * V;
     const int64_t qi = masked ? row % q_len : 0;
     if (masked) {
@@ -287,7 +312,6 @@ __device__ inline void softmax_row(T (&v)[S][V], const T *__restrict__ xr, int64
         // the correctly rounded core over the few flagged elements, whose
         // argument is formed again from the row in memory. x - m is <= 0 or
         // NaN (m is the row maximum), so the NONPOS path applies.
-        const ExpTableLanes tab(c.lane);
         SlowSet<S * V> flagged;
 #pragma unroll
         for (int s = 0; s < S; ++s)
@@ -333,14 +357,38 @@ __device__ inline void softmax_row(T (&v)[S][V], const T *__restrict__ xr, int64
                 for (int i = 0; i < V; ++i) v[s][i] = quot_f32(v[s][i], inv);
         }
     } else {
-        // exp(x - m); x - m is NaN only where exp's leaf returns the canonical NaN
+        // exp(x - m) in place, as for binary32: the binary64 fast path for
+        // every element (2^(j/64) as a double-double from the lane-held
+        // table), then one wave-uniform pass of the fixed-point path over the
+        // flagged elements (about one in 2^19, and NaN arguments).
+        SlowSet<S * V> flagged;
 #pragma unroll
         for (int s = 0; s < S; ++s)
 #pragma unroll
             for (int i = 0; i < V; ++i) {
-                const int64_t j = (int64_t)s * SEG + (int64_t)c.tid_in_row * V + i;
-                v[s][i] = (full || j < n) ? exp_leaf<T>(v[s][i] - m) : T(-0.0);
+                bool slow;
+                v[s][i] = exp_fast<true>(v[s][i] - m, tab, slow);
+                flagged.set(s * V + i, slow);
             }
+        if (flagged.any()) {
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+#pragma unroll
+                for (int i = 0; i < V; ++i) {
+                    const int64_t j = (int64_t)s * SEG + (int64_t)c.tid_in_row * V + i;
+                    if (flagged.has(s * V + i, c.lane) && (full || j < n))
+                        v[s][i] = exp_slow64(softmax_arg(xr[j], j, qi, masked, scale) - m);
+                }
+        }
+        if (!full) {
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+#pragma unroll
+                for (int i = 0; i < V; ++i) {
+                    const int64_t j = (int64_t)s * SEG + (int64_t)c.tid_in_row * V + i;
+                    if (j >= n) v[s][i] = T(-0.0);
+                }
+        }
         const RowDiv<T> div(canon(row_tree_sum<T, V, S, W, R>(v, lds, c)));
 #pragma unroll
         for (int s = 0; s < S; ++s)
@@ -366,9 +414,10 @@ __global__ __launch_bounds__(64 * W * R) void softmax_kernel(const T *__restrict
     RowCoord<W, R> c;
     if (c.row >= rows) return;  // whole row groups exit together (R rows per block, W waves each)
     const T *xr = x + c.row * ldx;
+    const typename RowExpTab<T>::type tab(c.lane);
     T v[S][V];
     load_row<T, V, S, W>(xr, n, vec_ok, c.tid_in_row, neg_inf<T>(), v);
-    softmax_row<T, V, S, W, R>(v, xr, c.row, n, masked, scale, q_len, lds, c);
+    softmax_row<T, V, S, W, R>(v, xr, c.row, n, masked, scale, q_len, lds, c, tab);
     store_row<T, V, S, W>(y + c.row * ldy, n, vec_ok, c.tid_in_row, v);
 }
 

@@ -45,3 +45,32 @@ long cr_check_run(int op, uint32_t first, long n, const uint32_t *got, uint32_t 
     }
     return count;
 }
+
+/* Binary64: CORE-MATH exp over explicit input bit patterns in[i], compared
+ * with the device results got[i]; the first `cap` mismatches are stored as
+ * (input bits, expected bits, device bits). */
+double chelis_crmath_ffi_exp(double);
+
+long cr_check64(int op, const uint64_t *in, long n, const uint64_t *got, uint64_t *bad, long cap) {
+    long count = 0;
+    (void)op; /* 0 exp: the only binary64 leaf held to correct rounding */
+#pragma omp parallel for schedule(static, 65536)
+    for (long i = 0; i < n; ++i) {
+        double x;
+        memcpy(&x, &in[i], 8);
+        const double w = chelis_crmath_ffi_exp(x);
+        uint64_t wb;
+        memcpy(&wb, &w, 8);
+        if (wb != got[i]) {
+            long slot;
+#pragma omp atomic capture
+            slot = count++;
+            if (slot < cap) {
+                bad[3 * slot] = in[i];
+                bad[3 * slot + 1] = wb;
+                bad[3 * slot + 2] = got[i];
+            }
+        }
+    }
+    return count;
+}

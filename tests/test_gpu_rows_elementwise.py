@@ -1,11 +1,11 @@
 """GPU parity of the row and elementwise regions against the CPU oracle.
 
 Bar: bit-exact where the oracle's leaves are IEEE operations or correctly
-rounded binary32 transcendentals (softmax f32, layer norm, relu, dropout,
-uniform_like, GELU f32 and the f32 exp/log/erfc/tanh chain leaves, whose
-device results equal CORE-MATH on every binary32 input); 1e-12 relative for
-f64 elementwise and 1e-10 for f64 reductions where the device exp/erfc leaf
-is within an ulp instead of correctly rounded.
+rounded transcendentals (softmax f32 and f64, layer norm, relu, dropout,
+uniform_like, GELU f32, the f32 exp/log/erfc/tanh chain leaves, whose device
+results equal CORE-MATH on every binary32 input, and the f64 exp leaf, a
+correctly rounded binary64 exp); 1e-12 relative for f64 GELU, whose device
+erfc leaf is within an ulp instead of correctly rounded.
 """
 import numpy as np
 import pytest
@@ -50,13 +50,29 @@ def test_softmax_f32_config_shape_bit_exact():
 
 
 def test_softmax_f64_config_shape():
-    """Config 2 f64: [4096, 4096] ~ N(0,1); exp leaf within 1 ulp."""
+    """Config 2 f64: [4096, 4096] ~ N(0,1), bit-exact (correctly rounded
+    binary64 exp), and by row sum."""
     x = np.random.default_rng(11).standard_normal((4096, 4096))
     y = C.softmax(C.to_device(x)).numpy()
     ref = O.softmax_rows(x)
-    rel = np.abs(y - ref) / np.abs(ref)
-    assert rel.max() <= 1e-12, rel.max()
+    assert bits_equal(y, ref), mismatch_report(y, ref)
     assert np.abs(y.sum(1) - 1).max() < 1e-10
+
+
+@pytest.mark.parametrize("n", [1, 5, 100, 256, 1000, 1025, 4096, 5000])
+def test_softmax_f64_bit_exact(n):
+    rows = max(1, 65536 // n)
+    x = np.random.default_rng(100 + n).standard_normal((rows, n)) * 3
+    y = C.softmax(C.to_device(x)).numpy()
+    ref = O.softmax_rows(x)
+    assert bits_equal(y, ref), mismatch_report(y, ref)
+
+
+def test_softmax_f64_special_rows():
+    x = np.array([[0.0, -np.inf, 1.0, -np.inf], [-np.inf] * 4, [3.0] * 4, [1.0, np.nan, 0, 0],
+                  [np.inf, 0, 0, 0], [-0.0, 0.0, -0.0, 0.0], [0.0, -745.0, -708.5, -1e-300]])
+    y = C.softmax(C.to_device(x)).numpy()
+    assert bits_equal(y, O.softmax_rows(x))
 
 
 def test_softmax_special_rows():
@@ -199,19 +215,14 @@ def test_fused_chain_flat_paths(dtype):
     ch = C.fused_chain([("mul", 0, 2), ("sub", ("s", 0), 1), ("exp", ("s", 1))])
     out = C.empty((n,), dtype)
     C.fused_elementwise(ch, [da.view((n,), (1,)), db, ds.view((n,), (0,))], out)
-    exp = (lambda v: np.array([O.lib().orc_expf(e) for e in v], np.float32)) if dtype == np.float32 else None
+    fn = O.lib().orc_expf if dtype == np.float32 else O.lib().orc_exp
+    exp = lambda v: np.array([fn(e) for e in v], dtype)  # noqa: E731
     t = (a[:n] * s - b).astype(dtype)
-    if exp:
-        assert bits_equal(out.numpy(), exp(t)), mismatch_report(out.numpy(), exp(t))
-    else:
-        assert np.allclose(out.numpy(), np.exp(t), rtol=1e-12, atol=0)
+    assert bits_equal(out.numpy(), exp(t)), mismatch_report(out.numpy(), exp(t))
     out2 = C.empty((n,), dtype)
     C.fused_elementwise(ch, [da.view((n,), (1,), 1), db, ds.view((n,), (0,))], out2)
     t2 = (a[1:] * s - b).astype(dtype)
-    if exp:
-        assert bits_equal(out2.numpy(), exp(t2)), mismatch_report(out2.numpy(), exp(t2))
-    else:
-        assert np.allclose(out2.numpy(), np.exp(t2), rtol=1e-12, atol=0)
+    assert bits_equal(out2.numpy(), exp(t2)), mismatch_report(out2.numpy(), exp(t2))
 
 
 def test_fused_chain_sgd_and_broadcast():
