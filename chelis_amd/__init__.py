@@ -26,11 +26,13 @@ class ChelisError(RuntimeError):
 
 
 # ---- ABI types (include/chelis_runtime.h, include/chelis_device_descriptor.h) ----
-DT_F32, DT_F64, DT_I32, DT_BOOL, DT_I64, DT_KEY = 0, 1, 2, 3, 4, 9
+DT_F32, DT_F64, DT_I32, DT_BOOL, DT_I64, DT_BF16, DT_F16, DT_KEY = 0, 1, 2, 3, 4, 5, 6, 9
+# bfloat16 has no numpy dtype: bf16 tensors travel as np.uint16 bit patterns
 _NP2DT = {np.dtype(np.float32): DT_F32, np.dtype(np.float64): DT_F64, np.dtype(np.int32): DT_I32,
-          np.dtype(np.uint8): DT_BOOL, np.dtype(np.bool_): DT_BOOL, np.dtype(np.int64): DT_I64}
+          np.dtype(np.uint8): DT_BOOL, np.dtype(np.bool_): DT_BOOL, np.dtype(np.int64): DT_I64,
+          np.dtype(np.uint16): DT_BF16, np.dtype(np.float16): DT_F16}
 _DT2NP = {DT_F32: np.float32, DT_F64: np.float64, DT_I32: np.int32, DT_BOOL: np.uint8, DT_I64: np.int64,
-          DT_KEY: np.uint64}
+          DT_BF16: np.uint16, DT_F16: np.float16, DT_KEY: np.uint64}
 
 
 class Scalar(ctypes.Structure):

@@ -47,6 +47,14 @@ __device__ inline T gemm_epilogue(T acc, const GemmProblem &p, int64_t z0, int64
 }
 
 int32_t gemm_mfma(chelis_dtype dt, const GemmProblem &p, hipStream_t st);
+// bf16 / f16 operands and result, binary32 accumulation (k_gemm16.hip).
+int32_t gemm_mfma16(chelis_dtype dt, const GemmProblem &p, hipStream_t st);
+// 16-bit [nz0][nz1][rows][cols] view <-> contiguous binary32 (the exact
+// 16-bit matmul runs the binary32 canonical tree between them).
+int32_t widen16(chelis_dtype dt, const void *src, float *dst, int64_t nz0, int64_t nz1, int64_t rows, int64_t cols,
+                int64_t s0, int64_t s1, int64_t sr, int64_t sc, hipStream_t st);
+int32_t narrow16(chelis_dtype dt, const float *src, void *dst, int64_t nz0, int64_t nz1, int64_t rows, int64_t cols,
+                 int64_t s0, int64_t s1, int64_t sr, int64_t sc, hipStream_t st);
 // c = a . b for attention with the causal mode above (programs only).
 int32_t matmul_causal(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b, const chelis_gpu_tensor *c,
                       int32_t mode);

@@ -43,6 +43,8 @@ void scratch_free(void *p, size_t bytes);
     } while (0)
 
 inline bool is_float(chelis_dtype d) { return d == CHELIS_DTYPE_F32 || d == CHELIS_DTYPE_F64; }
+// bfloat16 / binary16: 16-bit storage computed at binary32 (narrow.h).
+inline bool is_narrow16(chelis_dtype d) { return d == CHELIS_DTYPE_BF16 || d == CHELIS_DTYPE_F16; }
 inline int64_t dtype_width(chelis_dtype d) {
     switch (d) {
         case CHELIS_DTYPE_F32: case CHELIS_DTYPE_I32: return 4;

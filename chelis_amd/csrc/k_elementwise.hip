@@ -12,6 +12,7 @@
 // permuted axes) pay for coordinates. A broadcast operand (stride 0) is
 // re-read through L2/MALL, not materialized.
 #include "chain.h"
+#include "narrow.h"
 
 namespace chelis {
 namespace {
@@ -90,6 +91,85 @@ __global__ __launch_bounds__(256) void fused_chain_kernel(ChainDev ch, Operands 
             if (k < ops.n) slot[k] = in[k];
         out[idx] = run_chain<T>(ch, slot);
     }
+}
+
+// ---------------------------------------------------------------- narrow floats
+// bf16 / f16 chains of sub, max_elem and min_elem, the steps the reference
+// admits for 16-bit storage (crates/chelis-backend-hip/src/emit.rs:2292-2319,
+// kernels.rs:2274-2310): each step reads 16-bit operands, works at binary32
+// and stores 16 bits (narrow.h). Slots hold stored bits; the operands are
+// gathered as in fused_chain_kernel.
+template <Narrow K>
+__device__ inline uint16_t run_narrow_chain(const ChainDev &ch, uint16_t *slot) {
+    uint16_t v = 0;
+#pragma unroll 1
+    for (int s = 0; s < ch.n_steps; ++s) {
+        const int a0 = ch.a0[s], a1 = ch.a1[s];
+        const uint16_t x = slot[a0 >= 0 ? a0 : CHELIS_FUSED_MAX_INPUTS - a0 - 1];
+        const uint16_t y = slot[a1 >= 0 ? a1 : CHELIS_FUSED_MAX_INPUTS - a1 - 1];
+        const uint8_t op = ch.op[s];
+        v = op == CHELIS_FUSED_SUB ? narrow_sub<K>(x, y)
+                                   : (op == CHELIS_FUSED_MAX_ELEM ? narrow_max<K>(x, y) : narrow_min<K>(x, y));
+        slot[CHELIS_FUSED_MAX_INPUTS + s] = v;
+    }
+    return v;
+}
+
+template <Narrow K>
+__global__ __launch_bounds__(256) void narrow_chain_kernel(ChainDev ch, Operands ops, Shape sh,
+                                                           uint16_t *__restrict__ out, int64_t count) {
+    __shared__ uint16_t slots[256 * kSlotStride];
+    uint16_t *slot = slots + threadIdx.x * kSlotStride;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < count; idx += stride) {
+        int64_t coord[kMaxRank];
+        int64_t rem = idx;
+#pragma unroll
+        for (int a = kMaxRank - 1; a >= 0; --a) {
+            if (a < sh.rank) {
+                coord[a] = rem % sh.ext[a];
+                rem /= sh.ext[a];
+            } else {
+                coord[a] = 0;
+            }
+        }
+        uint16_t in[CHELIS_FUSED_MAX_INPUTS];
+#pragma unroll
+        for (int k = 0; k < CHELIS_FUSED_MAX_INPUTS; ++k) {
+            if (k < ops.n) {
+                int64_t off = 0;
+#pragma unroll
+                for (int a = 0; a < kMaxRank; ++a) off += coord[a] * ops.o[k].st[a];
+                in[k] = static_cast<const uint16_t *>(ops.o[k].p)[off];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < CHELIS_FUSED_MAX_INPUTS; ++k)
+            if (k < ops.n) slot[k] = in[k];
+        out[idx] = run_narrow_chain<K>(ch, slot);
+    }
+}
+
+// bf16 / f16 relu (ADJ = false) and its adjoint on contiguous operands,
+// eight 16-bit values per 16-byte access (kernels.rs:1196-1260).
+template <Narrow K, bool ADJ>
+__global__ __launch_bounds__(256) void narrow_relu_kernel(const uint16_t *__restrict__ x,
+                                                          const uint16_t *__restrict__ g, uint16_t *__restrict__ y,
+                                                          int64_t n) {
+    const int64_t nv = n / 8;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; v < nv; v += stride) {
+        uint4 xv = reinterpret_cast<const uint4 *>(x)[v], gv{}, yv;
+        if constexpr (ADJ) gv = reinterpret_cast<const uint4 *>(g)[v];
+        const uint16_t *xe = reinterpret_cast<const uint16_t *>(&xv);
+        const uint16_t *ge = reinterpret_cast<const uint16_t *>(&gv);
+        uint16_t *ye = reinterpret_cast<uint16_t *>(&yv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ye[i] = ADJ ? narrow_relu_adjoint<K>(xe[i], ge[i]) : narrow_relu<K>(xe[i]);
+        reinterpret_cast<uint4 *>(y)[v] = yv;
+    }
+    const int64_t t = nv * 8 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < n) y[t] = ADJ ? narrow_relu_adjoint<K>(x[t], g[t]) : narrow_relu<K>(x[t]);
 }
 
 // ---------------------------------------------------------------- flat maps
@@ -287,12 +367,35 @@ int32_t launch_unary(const chelis_gpu_tensor *x, const chelis_gpu_tensor *g, con
 
 bool vec_aligned(const chelis_gpu_tensor *t) { return (reinterpret_cast<uintptr_t>(t->data) & 15u) == 0; }
 
+template <bool ADJ>
+int32_t launch_narrow_relu(const chelis_gpu_tensor *x, const chelis_gpu_tensor *g, const chelis_gpu_tensor *y) {
+    hipStream_t st = stream();
+    if (!st) return set_error(CHELIS_HIP_EHIP, "no HIP device");
+    const int64_t n = y->count;
+    if (!n) return CHELIS_HIP_OK;
+    int64_t blocks = (n / 8 + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    if (blocks < 1) blocks = 1;
+    const uint16_t *xp = (const uint16_t *)x->data, *gp = g ? (const uint16_t *)g->data : nullptr;
+    uint16_t *yp = (uint16_t *)y->data;
+    if (y->dtype == CHELIS_DTYPE_BF16)
+        narrow_relu_kernel<Narrow::Bf16, ADJ><<<(unsigned)blocks, 256, 0, st>>>(xp, gp, yp, n);
+    else
+        narrow_relu_kernel<Narrow::F16, ADJ><<<(unsigned)blocks, 256, 0, st>>>(xp, gp, yp, n);
+    CHELIS_LAUNCH_CHECK();
+    return CHELIS_HIP_OK;
+}
+
 template <Unary OP>
 int32_t unary_entry(const char *what, const chelis_gpu_tensor *x, const chelis_gpu_tensor *g,
                     const chelis_gpu_tensor *y, const UnaryArgs &u) {
     int32_t s;
     if ((s = check_tensor(y, "y"))) return s;
-    if (!is_float(y->dtype)) return set_error(CHELIS_HIP_EDOMAIN, "%s: dtype must be f32 or f64", what);
+    const bool narrow = is_narrow16(y->dtype);
+    if (narrow && OP != Unary::Relu && OP != Unary::ReluAdjoint)
+        return set_error(CHELIS_HIP_EUNSUPPORTED, "%s: bf16/f16 operands are admitted for relu and its adjoint only",
+                         what);
+    if (!narrow && !is_float(y->dtype)) return set_error(CHELIS_HIP_EDOMAIN, "%s: dtype must be f32 or f64", what);
     for (const chelis_gpu_tensor *t : {x, g}) {
         if (!t) continue;
         if ((s = check_tensor(t, "operand"))) return s;
@@ -302,6 +405,10 @@ int32_t unary_entry(const char *what, const chelis_gpu_tensor *x, const chelis_g
     for (const chelis_gpu_tensor *t : {x, g, y})
         if (t && (!is_contiguous(t) || (t->count && !vec_aligned(t))))
             return set_error(CHELIS_HIP_EUNSUPPORTED, "%s: operands must be contiguous and 16-byte aligned", what);
+    if (narrow) {
+        if constexpr (OP == Unary::Relu || OP == Unary::ReluAdjoint)
+            return launch_narrow_relu<OP == Unary::ReluAdjoint>(x, g, y);
+    }
     return y->dtype == CHELIS_DTYPE_F32 ? launch_unary<float, OP>(x, g, y, u) : launch_unary<double, OP>(x, g, y, u);
 }
 
@@ -383,10 +490,11 @@ int32_t load_chain_steps(const chelis_fused_chain *chain, int32_t n_inputs, Chai
 // One (inputs, output) group checked and collapsed; *flat when every
 // operand streams with the output or is a single broadcast element.
 int32_t prepare_group(const chelis_gpu_tensor *const *inputs, int32_t n_inputs, const chelis_gpu_tensor *out,
-                      Shape *sh, int64_t (*st)[kMaxRank], bool *flat) {
+                      Shape *sh, int64_t (*st)[kMaxRank], bool *flat, bool allow_narrow = false) {
     int32_t s;
     if ((s = check_tensor(out, "out"))) return s;
-    if (!is_float(out->dtype)) return set_error(CHELIS_HIP_EUNSUPPORTED, "fused_elementwise: f32/f64 chains only");
+    if (!is_float(out->dtype) && !(allow_narrow && is_narrow16(out->dtype)))
+        return set_error(CHELIS_HIP_EUNSUPPORTED, "fused_elementwise: f32/f64 chains only");
     if (!is_contiguous(out)) return set_error(CHELIS_HIP_EUNSUPPORTED, "fused_elementwise: output must be contiguous");
     if (n_inputs && !inputs) return set_error(CHELIS_HIP_EDOMAIN, "fused_elementwise: null input array");
     for (int32_t k = 0; k < n_inputs; ++k)
@@ -468,13 +576,39 @@ extern "C" int32_t chelis_hip_fused_elementwise(const chelis_fused_chain *chain,
                                                 int32_t n_inputs, const chelis_gpu_tensor *out) {
     ChainDev ch;
     if (int32_t s = load_chain_steps(chain, n_inputs, &ch)) return s;
+    const bool narrow = out && is_narrow16(out->dtype);
+    if (narrow) {
+        // 16-bit chains: sub / max_elem / min_elem steps only (emit.rs:2292-2319)
+        for (int32_t i = 0; i < ch.n_steps; ++i)
+            if (ch.op[i] != CHELIS_FUSED_SUB && ch.op[i] != CHELIS_FUSED_MAX_ELEM && ch.op[i] != CHELIS_FUSED_MIN_ELEM)
+                return set_error(CHELIS_HIP_EUNSUPPORTED,
+                                 "fused_elementwise: bf16/f16 chain step %d is outside sub/max_elem/min_elem", i);
+    }
     Shape sh;
     int64_t st[CHELIS_FUSED_MAX_INPUTS][kMaxRank];
     bool flat = false;
-    if (int32_t s = prepare_group(inputs, n_inputs, out, &sh, st, &flat)) return s;
+    if (int32_t s = prepare_group(inputs, n_inputs, out, &sh, st, &flat, true)) return s;
     if (!out->count) return CHELIS_HIP_OK;
     hipStream_t strm = stream();
     if (!strm) return set_error(CHELIS_HIP_EHIP, "no HIP device");
+    if (narrow) {
+        Operands ops{};
+        ops.n = n_inputs;
+        for (int32_t k = 0; k < n_inputs; ++k) {
+            ops.o[k].p = inputs[k]->data;
+            for (int a = 0; a < kMaxRank; ++a) ops.o[k].st[a] = st[k][a];
+        }
+        int64_t blocks = (out->count + 255) / 256;
+        if (blocks > 8192) blocks = 8192;
+        if (out->dtype == CHELIS_DTYPE_BF16)
+            narrow_chain_kernel<Narrow::Bf16><<<(unsigned)blocks, 256, 0, strm>>>(ch, ops, sh, (uint16_t *)out->data,
+                                                                                 out->count);
+        else
+            narrow_chain_kernel<Narrow::F16><<<(unsigned)blocks, 256, 0, strm>>>(ch, ops, sh, (uint16_t *)out->data,
+                                                                                out->count);
+        CHELIS_LAUNCH_CHECK();
+        return CHELIS_HIP_OK;
+    }
     if (flat) {
         FlatGroups fg{};
         fg.n_in = n_inputs;

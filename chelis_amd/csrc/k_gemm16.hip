@@ -1,0 +1,286 @@
+// bf16 / f16 matmul on the CDNA4 matrix cores, and the 16-bit <-> binary32
+// conversions of the exact matmul path.
+//
+// spec/04 section 5.7.1 gives a 16-bit matmul a binary32 accumulator; the
+// reference runs it on hipblasGemmEx with HIPBLAS_COMPUTE_32F and a 16-bit
+// result (crates/chelis-backend-hip/runtime/chelis_hip_runtime.h:92-170).
+// Here v_mfma_f32_16x16x32_bf16 / _f16 accumulate in binary32 and the
+// epilogue encodes each result once (narrow.h: nearest even, canonical NaN).
+//
+// Tile: a 256-thread workgroup (4 waves, 2 x 2) owns 128 x 128 of C; each
+// wave 64 x 64 = 4 x 4 blocks of 16 x 16. K moves in steps of 32 through two
+// LDS buffers holding both operands K-contiguous (As[m][k], Bs[n][k]) with
+// an 80-byte row pitch. An MFMA of shape 16x16x32 takes from lane q*16 + i
+// the 8 values of row i (A) or column i (B) at k = 8q .. 8q + 7, one 16-byte
+// LDS read, and pairs A and B entries of the same lane group and item, so
+// both operands share one k map; it returns C[4q + r][j] in lane q*16 + j,
+// item r (the 16x16 binary32 output layout of the 16x16x4 f32 MFMA, which
+// the f32 kernel uses). The next step's global loads are in flight in
+// registers while the matrix cores run the current one.
+#include "gemm.h"
+#include "narrow.h"
+
+namespace chelis {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+template <Narrow K>
+__device__ inline f32x4 mfma16(uint4 a, uint4 b, f32x4 c) {
+    if constexpr (K == Narrow::Bf16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                       c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                      0, 0, 0);
+}
+
+constexpr int THREADS = 256, BM = 128, BN = 128, BK = 32, LD = 40;
+
+// One operand tile [ROWS][BK] staged in registers, 8 values per 16-byte
+// vector: LAY 0 = vectors along K, 1 = vectors along the outer axis (M of
+// A, N of B; transposed into LDS by the store), 2 = element by element.
+template <int LAY, int ROWS>
+struct Stage16 {
+    static constexpr int NV = ROWS * BK / 8 / THREADS;
+    uint4 r[NV];
+
+    // element (row, k) at base[row * s_row + k * s_k]; CHECK = false: the
+    // whole tile is inside the operand and the vectors are aligned.
+    template <bool CHECK>
+    __device__ void load(const uint16_t *__restrict__ base, int64_t s_row, int64_t s_k, int64_t row0, int64_t rows,
+                         int64_t k0, int64_t K) {
+        const int t = threadIdx.x;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int idx = t + THREADS * j;
+            if constexpr (LAY == 0 || LAY == 2) {
+                const int row = idx / (BK / 8), kv = (idx % (BK / 8)) * 8;
+                const int64_t gr = row0 + row, gk = k0 + kv;
+                const uint16_t *p = base + gr * s_row + gk * s_k;
+                if (LAY == 0 && (!CHECK || (gr < rows && gk + 8 <= K))) {
+                    r[j] = *reinterpret_cast<const uint4 *>(p);
+                } else {
+                    uint16_t e[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) e[u] = (gr < rows && gk + u < K) ? p[u * s_k] : (uint16_t)0;
+                    r[j] = __builtin_bit_cast(uint4, e);
+                }
+            } else {
+                const int k = idx % BK, rv = (idx / BK) * 8;
+                const int64_t gr = row0 + rv, gk = k0 + k;
+                const uint16_t *p = base + gr * s_row + gk * s_k;
+                if (!CHECK || (gk < K && gr + 8 <= rows)) {
+                    r[j] = *reinterpret_cast<const uint4 *>(p);
+                } else {
+                    uint16_t e[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) e[u] = (gk < K && gr + u < rows) ? p[u * s_row] : (uint16_t)0;
+                    r[j] = __builtin_bit_cast(uint4, e);
+                }
+            }
+        }
+    }
+
+    __device__ void store(uint16_t *lds) const {
+        const int t = threadIdx.x;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int idx = t + THREADS * j;
+            if constexpr (LAY == 0 || LAY == 2) {
+                const int row = idx / (BK / 8), kv = (idx % (BK / 8)) * 8;
+                *reinterpret_cast<uint4 *>(lds + row * LD + kv) = r[j];
+            } else {
+                const int k = idx % BK, rv = (idx / BK) * 8;
+                const uint16_t *e = reinterpret_cast<const uint16_t *>(&r[j]);
+#pragma unroll
+                for (int u = 0; u < 8; ++u) lds[(rv + u) * LD + k] = e[u];
+            }
+        }
+    }
+};
+
+template <Narrow KIND, int ALAY, int BLAY>
+__global__ __launch_bounds__(THREADS) void gemm16_kernel(GemmProblem p, int64_t tiles_m, int64_t tiles_n) {
+    __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * LD];
+    __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * LD];
+
+    // XCD-aware tile order: each XCD (workgroups are dealt round-robin) gets
+    // one contiguous run of tiles, walked in groups of 8 tile-rows.
+    const int64_t tiles = tiles_m * tiles_n;
+    int64_t bid = blockIdx.x;
+    if (tiles % 8 == 0) bid = (bid % 8) * (tiles / 8) + bid / 8;
+    constexpr int64_t GM = 8;
+    const int64_t group = bid / (GM * tiles_n);
+    const int64_t first = group * GM;
+    const int64_t gsz = (tiles_m - first) < GM ? (tiles_m - first) : GM;
+    const int64_t in_group = bid % (GM * tiles_n);
+    const int64_t m0 = (first + in_group % gsz) * BM;
+    const int64_t n0 = (in_group / gsz) * BN;
+
+    const int64_t z = blockIdx.y;
+    const int64_t z0 = z / p.nb1, z1 = z % p.nb1;
+    const uint16_t *A = static_cast<const uint16_t *>(p.a) + z0 * p.sa0 + z1 * p.sa1;
+    const uint16_t *B = static_cast<const uint16_t *>(p.b) + z0 * p.sb0 + z1 * p.sb1;
+    const int64_t K = p.K;
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int fr = lane & 15, fq = lane >> 4;
+
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{};
+
+    Stage16<ALAY, BM> sa;
+    Stage16<BLAY, BN> sb;
+    const int64_t ksteps = (K + BK - 1) / BK;
+    const bool inside = ALAY != 2 && BLAY != 2 && m0 + BM <= p.M && n0 + BN <= p.N && K >= BK && K % BK == 0;
+    auto run = [&](auto check) {
+        constexpr bool CK = decltype(check)::value;
+        const int64_t last = ksteps - 1;
+        sa.template load<CK>(A, p.sam, p.sak, m0, p.M, 0, K);
+        sb.template load<CK>(B, p.sbn, p.sbk, n0, p.N, 0, K);
+        sa.store(As[0]);
+        sb.store(Bs[0]);
+        __syncthreads();
+        for (int64_t ks = 0; ks < ksteps; ++ks) {
+            const int buf = (int)(ks & 1);
+            // the next step's loads (the last step reloads itself: branch free)
+            const int64_t kn = (ks < last ? ks + 1 : last) * BK;
+            sa.template load<CK>(A, p.sam, p.sak, m0, p.M, kn, K);
+            sb.template load<CK>(B, p.sbn, p.sbk, n0, p.N, kn, K);
+            const uint16_t *as = As[buf] + (wm * 64 + fr) * LD + fq * 8;
+            const uint16_t *bs = Bs[buf] + (wn * 64 + fr) * LD + fq * 8;
+            uint4 af[4], bf[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const uint4 *>(as + i * 16 * LD);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bf[j] = *reinterpret_cast<const uint4 *>(bs + j * 16 * LD);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<KIND>(af[i], bf[j], acc[i][j]);
+            sa.store(As[buf ^ 1]);
+            sb.store(Bs[buf ^ 1]);
+            __syncthreads();
+        }
+    };
+    if (inside) run(std::false_type{});
+    else run(std::true_type{});
+
+    uint16_t *C = static_cast<uint16_t *>(p.c) + z0 * p.sc0 + z1 * p.sc1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t m = m0 + wm * 64 + i * 16 + 4 * fq + r;
+                const int64_t n = n0 + wn * 64 + j * 16 + fr;
+                if (m < p.M && n < p.N) C[m * p.scm + n * p.scn] = f32_to_narrow<KIND>(acc[i][j][r]);
+            }
+}
+
+// Staging layout of an operand: vectors along K (0) or along its outer
+// axis (1) when that axis has unit stride, the other stride and every batch
+// offset keep 16-byte alignment, and the base is aligned; else 2.
+int lay_of(const void *base, int64_t s_outer, int64_t s_k, int64_t s0, int64_t s1) {
+    const bool aligned = (reinterpret_cast<uintptr_t>(base) & 15u) == 0 && s0 % 8 == 0 && s1 % 8 == 0;
+    if (aligned && s_k == 1 && s_outer % 8 == 0) return 0;
+    if (aligned && s_outer == 1 && s_k % 8 == 0) return 1;
+    return 2;
+}
+
+template <Narrow KIND, int ALAY, int BLAY>
+void launch16(const GemmProblem &p, dim3 grid, int64_t tm, int64_t tn, hipStream_t st) {
+    gemm16_kernel<KIND, ALAY, BLAY><<<grid, THREADS, 0, st>>>(p, tm, tn);
+}
+
+template <Narrow KIND>
+int32_t gemm16_kind(const GemmProblem &p, hipStream_t st) {
+    const int64_t tm = (p.M + BM - 1) / BM, tn = (p.N + BN - 1) / BN;
+    const int64_t nz = p.nb0 * p.nb1;
+    if (tm * tn > 0x7fffffffLL || nz > 65535) return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: grid too large");
+    const dim3 grid((unsigned)(tm * tn), (unsigned)nz);
+    const int la = lay_of(p.a, p.sam, p.sak, p.sa0, p.sa1), lb = lay_of(p.b, p.sbn, p.sbk, p.sb0, p.sb1);
+    // instantiated layouts: both K-contiguous, A K-contiguous with B along N
+    // (row-major operands), and the element-by-element fallback
+    if (la == 0 && lb == 0) launch16<KIND, 0, 0>(p, grid, tm, tn, st);
+    else if (la == 0 && lb == 1) launch16<KIND, 0, 1>(p, grid, tm, tn, st);
+    else if (la == 1 && lb == 0) launch16<KIND, 1, 0>(p, grid, tm, tn, st);
+    else if (la == 1 && lb == 1) launch16<KIND, 1, 1>(p, grid, tm, tn, st);
+    else launch16<KIND, 2, 2>(p, grid, tm, tn, st);
+    CHELIS_LAUNCH_CHECK();
+    return CHELIS_HIP_OK;
+}
+
+// dst[z][r][c] = src[z0 * s0 + z1 * s1 + r * sr + c * sc] widened to binary32
+// (z = z0 * nz1 + z1; dst contiguous).
+template <Narrow KIND>
+__global__ __launch_bounds__(256) void widen_kernel(const uint16_t *__restrict__ src, float *__restrict__ dst,
+                                                    int64_t nz1, int64_t rows, int64_t cols, int64_t s0, int64_t s1,
+                                                    int64_t sr, int64_t sc, int64_t count) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+        const int64_t c = i % cols, r = (i / cols) % rows, z = i / (cols * rows);
+        dst[i] = narrow_to_f32<KIND>(src[(z / nz1) * s0 + (z % nz1) * s1 + r * sr + c * sc]);
+    }
+}
+
+// dst[z0 * s0 + z1 * s1 + r * sr + c * sc] = src[z][r][c] encoded to 16 bits.
+template <Narrow KIND>
+__global__ __launch_bounds__(256) void narrow_kernel(const float *__restrict__ src, uint16_t *__restrict__ dst,
+                                                     int64_t nz1, int64_t rows, int64_t cols, int64_t s0, int64_t s1,
+                                                     int64_t sr, int64_t sc, int64_t count) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+        const int64_t c = i % cols, r = (i / cols) % rows, z = i / (cols * rows);
+        dst[(z / nz1) * s0 + (z % nz1) * s1 + r * sr + c * sc] = f32_to_narrow<KIND>(src[i]);
+    }
+}
+
+unsigned blocks_for(int64_t n) {
+    int64_t b = (n + 255) / 256;
+    return (unsigned)(b < 1 ? 1 : (b > 16384 ? 16384 : b));
+}
+
+}  // namespace
+
+int32_t gemm_mfma16(chelis_dtype dt, const GemmProblem &p, hipStream_t st) {
+    return dt == CHELIS_DTYPE_BF16 ? gemm16_kind<Narrow::Bf16>(p, st) : gemm16_kind<Narrow::F16>(p, st);
+}
+
+int32_t widen16(chelis_dtype dt, const void *src, float *dst, int64_t nz0, int64_t nz1, int64_t rows, int64_t cols,
+                int64_t s0, int64_t s1, int64_t sr, int64_t sc, hipStream_t st) {
+    const int64_t n = nz0 * nz1 * rows * cols;
+    if (!n) return CHELIS_HIP_OK;
+    if (dt == CHELIS_DTYPE_BF16)
+        widen_kernel<Narrow::Bf16><<<blocks_for(n), 256, 0, st>>>((const uint16_t *)src, dst, nz1, rows, cols, s0, s1,
+                                                                  sr, sc, n);
+    else
+        widen_kernel<Narrow::F16><<<blocks_for(n), 256, 0, st>>>((const uint16_t *)src, dst, nz1, rows, cols, s0, s1,
+                                                                 sr, sc, n);
+    CHELIS_LAUNCH_CHECK();
+    return CHELIS_HIP_OK;
+}
+
+int32_t narrow16(chelis_dtype dt, const float *src, void *dst, int64_t nz0, int64_t nz1, int64_t rows, int64_t cols,
+                 int64_t s0, int64_t s1, int64_t sr, int64_t sc, hipStream_t st) {
+    const int64_t n = nz0 * nz1 * rows * cols;
+    if (!n) return CHELIS_HIP_OK;
+    if (dt == CHELIS_DTYPE_BF16)
+        narrow_kernel<Narrow::Bf16><<<blocks_for(n), 256, 0, st>>>(src, (uint16_t *)dst, nz1, rows, cols, s0, s1, sr,
+                                                                   sc, n);
+    else
+        narrow_kernel<Narrow::F16><<<blocks_for(n), 256, 0, st>>>(src, (uint16_t *)dst, nz1, rows, cols, s0, s1, sr,
+                                                                  sc, n);
+    CHELIS_LAUNCH_CHECK();
+    return CHELIS_HIP_OK;
+}
+
+}  // namespace chelis

@@ -13,6 +13,10 @@
 //   CHELIS_MATMUL_EXACT          -> tree_tiled  (bit-exact, any other shape)
 //   otherwise                    -> MFMA tiles  (dense; rounding differs
 //                                   from the canonical tree)
+// bf16 / f16 (every shape): MFMA 16x16x32 tiles with a binary32
+// accumulator; with CHELIS_MATMUL_EXACT (or K == 0) the operands are
+// widened to binary32, the binary32 dispatch above runs exact, and the
+// result is encoded once - the C lane's decode / tree / encode, bit-exact.
 #include "gemm.h"
 
 #include <algorithm>
@@ -74,8 +78,8 @@ int32_t build_problem(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b, co
                       GemmProblem *p, const char *what) {
     int32_t s;
     if ((s = check_tensor(a, "a")) || (s = check_tensor(b, "b")) || (s = check_tensor(c, "c"))) return s;
-    if (!is_float(a->dtype) || a->dtype != b->dtype || a->dtype != c->dtype)
-        return set_error(CHELIS_HIP_EDOMAIN, "%s: a, b and c must share an f32 or f64 dtype", what);
+    if (!(is_float(a->dtype) || is_narrow16(a->dtype)) || a->dtype != b->dtype || a->dtype != c->dtype)
+        return set_error(CHELIS_HIP_EDOMAIN, "%s: a, b and c must share an f32, f64, bf16 or f16 dtype", what);
     Mat ma, mb;
     if (!as_mat(a, true, &ma) || !as_mat(b, false, &mb))
         return set_error(CHELIS_HIP_EUNSUPPORTED, "%s: operands need rank 1..4", what);
@@ -119,11 +123,47 @@ int32_t build_problem(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b, co
     return CHELIS_HIP_OK;
 }
 
+int32_t dispatch(chelis_dtype dt, const GemmProblem &p, int32_t flags);
+
+// The exact 16-bit matmul: widen both operands to contiguous binary32,
+// run the binary32 canonical-tree dispatch, encode the result into c.
+int32_t dispatch_narrow_exact(chelis_dtype dt, const GemmProblem &p, hipStream_t st) {
+    const int64_t nz0 = p.nb0, nz1 = p.nb1, M = p.M, N = p.N, K = p.K;
+    const size_t ab = sizeof(float) * (size_t)(nz0 * nz1 * M * K) + 16,
+                 bb = sizeof(float) * (size_t)(nz0 * nz1 * K * N) + 16,
+                 cb = sizeof(float) * (size_t)(nz0 * nz1 * M * N) + 16;
+    float *a32 = static_cast<float *>(scratch_alloc(ab));
+    float *b32 = static_cast<float *>(scratch_alloc(bb));
+    float *c32 = static_cast<float *>(scratch_alloc(cb));
+    int32_t s = CHELIS_HIP_OK;
+    if (!a32 || !b32 || !c32) s = set_error(CHELIS_HIP_EHIP, "matmul: scratch allocation failed");
+    if (!s) s = widen16(dt, p.a, a32, nz0, nz1, M, K, p.sa0, p.sa1, p.sam, p.sak, st);
+    if (!s) s = widen16(dt, p.b, b32, nz0, nz1, K, N, p.sb0, p.sb1, p.sbk, p.sbn, st);
+    if (!s) {
+        GemmProblem q{};
+        q.a = a32, q.b = b32, q.c = c32;
+        q.M = M, q.N = N, q.K = K;
+        q.sam = K, q.sak = 1, q.sbk = N, q.sbn = 1, q.scm = N, q.scn = 1;
+        q.nb0 = nz0, q.nb1 = nz1;
+        q.sa0 = nz1 * M * K, q.sa1 = M * K, q.sb0 = nz1 * K * N, q.sb1 = K * N, q.sc0 = nz1 * M * N, q.sc1 = M * N;
+        s = dispatch(CHELIS_DTYPE_F32, q, CHELIS_MATMUL_EXACT);
+    }
+    if (!s) s = narrow16(dt, c32, p.c, nz0, nz1, M, N, p.sc0, p.sc1, p.scm, p.scn, st);
+    if (a32) scratch_free(a32, ab);
+    if (b32) scratch_free(b32, bb);
+    if (c32) scratch_free(c32, cb);
+    return s;
+}
+
 int32_t dispatch(chelis_dtype dt, const GemmProblem &p, int32_t flags) {
     hipStream_t st = stream();
     if (!st) return set_error(CHELIS_HIP_EHIP, "no HIP device");
     if (p.M == 0 || p.N == 0 || p.nb0 == 0 || p.nb1 == 0) return CHELIS_HIP_OK;
     if (g_exact.load(std::memory_order_relaxed)) flags |= CHELIS_MATMUL_EXACT;
+    if (is_narrow16(dt)) {
+        if ((flags & CHELIS_MATMUL_EXACT) || p.K == 0) return dispatch_narrow_exact(dt, p, st);
+        return gemm_mfma16(dt, p, st);
+    }
     const bool f64 = dt == CHELIS_DTYPE_F64;
     const int64_t narrow = std::min(p.M, p.N);
     if (p.K <= 32) return gemm_tree_thread(dt, p, st);
@@ -173,6 +213,8 @@ extern "C" int32_t chelis_hip_linear(const chelis_gpu_tensor *a, const chelis_gp
     if (activation < CHELIS_ACT_NONE || activation > CHELIS_ACT_GELU)
         return set_error(CHELIS_HIP_EDOMAIN, "linear: unknown activation %d", activation);
     if (a->rank < 2 || b->rank < 2) return set_error(CHELIS_HIP_EDOMAIN, "linear: a and b need rank >= 2");
+    if (is_narrow16(a->dtype))
+        return set_error(CHELIS_HIP_EUNSUPPORTED, "linear: bf16/f16 matmuls take no fused epilogue (use matmul)");
     p.act = activation;
     if (bias) {
         if (int32_t s = check_tensor(bias, "bias")) return s;

@@ -315,6 +315,141 @@ void orc_relu_adjoint_f32(const float *x, const float *g, float *y, int64_t n) {
     for (int64_t i = 0; i < n; ++i) y[i] = 0.0f < x[i] ? g[i] : 0.0f;
 }
 
+/* bfloat16 and IEEE binary16 storage ([04-NUM-8]): widening is exact,
+ * narrowing rounds to nearest even (overflow to infinity, binary16
+ * subnormals kept) and stores NaN as the format's canonical quiet NaN
+ * (crates/chelis-runtime/include/chelis_runtime.h:664-760: bf16 to f32 by a
+ * 16-bit shift, f32 to bf16 by the round-half-even bias on the low half,
+ * f16 through its field decomposition). */
+static float orc_dec16(int kind, uint16_t h) {
+    uint32_t bits;
+    if (kind == 0) {
+        bits = (uint32_t)h << 16;
+    } else {
+        const uint32_t sign = (uint32_t)(h >> 15) << 31;
+        const int e = (h >> 10) & 31;
+        const uint32_t m = h & 1023u;
+        if (e == 31) {
+            bits = sign | 0x7f800000u | (m << 13);
+        } else if (e > 0) {
+            bits = sign | ((uint32_t)(e - 15 + 127) << 23) | (m << 13);
+        } else {
+            float mag = ldexpf((float)m, -24);
+            memcpy(&bits, &mag, 4);
+            bits |= sign;
+        }
+    }
+    float v;
+    memcpy(&v, &bits, 4);
+    return v;
+}
+static uint16_t orc_enc16(int kind, float v) {
+    uint32_t b;
+    memcpy(&b, &v, 4);
+    const int nan = (b & 0x7fffffffu) > 0x7f800000u;
+    if (kind == 0) {
+        if (nan) return 0x7fc0u;
+        const uint32_t low = b & 0xffffu, up = b >> 16;
+        /* round half to even on the discarded half word */
+        const uint32_t r = (low > 0x8000u || (low == 0x8000u && (up & 1u))) ? up + 1u : up;
+        return (uint16_t)r;
+    }
+    if (nan) return 0x7e00u;
+    const uint16_t sign = (uint16_t)((b >> 31) << 15);
+    const int be = (int)((b >> 23) & 0xffu);
+    if (be == 0xff) return (uint16_t)(sign | 0x7c00u);
+    /* |v| = sig * 2^(ex) with a 24-bit integer significand */
+    const uint32_t sig = be ? ((b & 0x7fffffu) | 0x800000u) : (b & 0x7fffffu);
+    const int ex = (be ? be : 1) - 150;
+    /* binary16 quantum at |v|: 2^-24 below 2^-14, else 2^(e - 10) */
+    int q = -24;
+    if (sig) {
+        int top = ex + 23; /* exponent of the leading bit */
+        while (top > ex && !((sig >> (top - ex)) & 1u)) --top;
+        if (top - 10 > q) q = top - 10;
+    }
+    uint64_t kept;
+    if (q <= ex) {
+        kept = (uint64_t)sig << (ex - q);
+    } else {
+        const int sh = q - ex;
+        if (sh > 40) {
+            kept = 0;
+        } else {
+            kept = (uint64_t)sig >> sh;
+            const uint64_t dropped = (uint64_t)sig & ((1ull << sh) - 1ull), half = 1ull << (sh - 1);
+            if (dropped > half || (dropped == half && (kept & 1u))) ++kept;
+        }
+    }
+    /* kept * 2^q with q >= -24: encode (a carry past 11 bits bumps q) */
+    if (kept >= 2048u) {
+        kept >>= 1;
+        ++q;
+    }
+    if (kept < 1024u) return (uint16_t)(sign | kept); /* subnormal (q = -24) */
+    const int e16 = q + 10 + 15;
+    if (e16 >= 31) return (uint16_t)(sign | 0x7c00u);
+    return (uint16_t)(sign | ((uint32_t)e16 << 10) | (kept & 1023u));
+}
+void orc_narrow_decode(int kind, const uint16_t *x, float *y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = orc_dec16(kind, x[i]);
+}
+void orc_narrow_encode(int kind, const float *x, uint16_t *y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = orc_enc16(kind, x[i]);
+}
+void orc_narrow_sub(int kind, const uint16_t *a, const uint16_t *b, uint16_t *y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = orc_enc16(kind, orc_dec16(kind, a[i]) - orc_dec16(kind, b[i]));
+}
+/* [05-OP-40] selections keep the chosen operand's stored bits: the left one
+ * when it is NaN, or when the right is not NaN and left >= right (max) /
+ * left <= right (min) (crates/chelis-backend-hip/src/kernels.rs:2291-2305). */
+void orc_narrow_max(int kind, const uint16_t *a, const uint16_t *b, uint16_t *y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float l = orc_dec16(kind, a[i]), r = orc_dec16(kind, b[i]);
+        y[i] = (isnan(l) || (!isnan(r) && l >= r)) ? a[i] : b[i];
+    }
+}
+void orc_narrow_min(int kind, const uint16_t *a, const uint16_t *b, uint16_t *y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float l = orc_dec16(kind, a[i]), r = orc_dec16(kind, b[i]);
+        y[i] = (isnan(l) || (!isnan(r) && l <= r)) ? a[i] : b[i];
+    }
+}
+/* [05-OP-43] on stored bits: a negative, nonzero, non-NaN x gives +0, any
+ * other x itself; the adjoint keeps g where x is positive, nonzero and not
+ * NaN (crates/chelis-backend-hip/src/kernels.rs:1196-1260). */
+void orc_narrow_relu(int kind, const uint16_t *x, uint16_t *y, int64_t n) {
+    const uint16_t em = kind == 0 ? 0x7f80u : 0x7c00u, fm = kind == 0 ? 0x007fu : 0x03ffu;
+    for (int64_t i = 0; i < n; ++i) {
+        const uint16_t v = x[i];
+        const int is_nan = (v & em) == em && (v & fm);
+        y[i] = ((v & 0x8000u) && (v & 0x7fffu) && !is_nan) ? 0 : v;
+    }
+}
+void orc_narrow_relu_adjoint(int kind, const uint16_t *x, const uint16_t *g, uint16_t *y, int64_t n) {
+    const uint16_t em = kind == 0 ? 0x7f80u : 0x7c00u, fm = kind == 0 ? 0x007fu : 0x03ffu;
+    for (int64_t i = 0; i < n; ++i) {
+        const uint16_t v = x[i];
+        const int is_nan = (v & em) == em && (v & fm);
+        y[i] = (!(v & 0x8000u) && (v & 0x7fffu) && !is_nan) ? g[i] : 0;
+    }
+}
+/* spec/04 section 5.7.1: a bf16/f16 matmul accumulates at binary32; the C
+ * lane decodes, runs the binary32 canonical-tree product (each product of
+ * two 16-bit values is exact in binary32) and encodes the result. */
+void orc_matmul_narrow(int kind, const uint16_t *A, const uint16_t *B, uint16_t *C, int64_t M, int64_t N,
+                       int64_t K) {
+    float *a = malloc(sizeof(float) * (size_t)(M * K + 1)), *b = malloc(sizeof(float) * (size_t)(K * N + 1));
+    float *c = malloc(sizeof(float) * (size_t)(M * N + 1));
+    orc_narrow_decode(kind, A, a, M * K);
+    orc_narrow_decode(kind, B, b, K * N);
+    orc_matmul_f32(a, K, 1, b, N, 1, c, M, N, K);
+    orc_narrow_encode(kind, c, C, M * N);
+    free(a);
+    free(b);
+    free(c);
+}
+
 /* [05-OP-37] keyed dropout at f32: the f32-rounded unit of word(key, i) is
  * compared with the rate; a dropped element is +0, a kept one
  * x / (1 - rate) (crates/chelis-backend-c/src/emit.rs:6139-6220). The

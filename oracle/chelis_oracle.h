@@ -88,6 +88,21 @@ void orc_dropout_f32(uint64_t key, const float *x, float rate, float *y, int64_t
 void orc_dropout_replay_f32(uint64_t key, const float *g, float rate, float *dx, int64_t n);
 void orc_dropout_f64(uint64_t key, const double *x, double rate, double *y, int64_t n);
 
+/* ---- bfloat16 / binary16 storage (kind 0 = bf16, 1 = f16) ----
+ * [04-NUM-8]: stored as 16 bits, computed at binary32, finalized once per
+ * op (crates/chelis-runtime/include/chelis_runtime.h:664-760). */
+void orc_narrow_decode(int kind, const uint16_t *x, float *y, int64_t n);
+void orc_narrow_encode(int kind, const float *x, uint16_t *y, int64_t n);
+void orc_narrow_sub(int kind, const uint16_t *a, const uint16_t *b, uint16_t *y, int64_t n);
+void orc_narrow_max(int kind, const uint16_t *a, const uint16_t *b, uint16_t *y, int64_t n);
+void orc_narrow_min(int kind, const uint16_t *a, const uint16_t *b, uint16_t *y, int64_t n);
+void orc_narrow_relu(int kind, const uint16_t *x, uint16_t *y, int64_t n);
+void orc_narrow_relu_adjoint(int kind, const uint16_t *x, const uint16_t *g, uint16_t *y, int64_t n);
+/* C = encode(tree_k(decode(A) * decode(B))) with the binary32 accumulator
+ * (spec/04 section 5.7.1); row-major contiguous A [M,K], B [K,N], C [M,N]. */
+void orc_matmul_narrow(int kind, const uint16_t *A, const uint16_t *B, uint16_t *C, int64_t M, int64_t N,
+                       int64_t K);
+
 /* ---- canonical-tree matmul (inlined product, emit.rs:8431-8560) ----
  * C[i,j] = tree_k(A[i*sa0 + k*sa1] * B[k*sb0 + j*sb1]); strides in elements. */
 void orc_matmul_f32(const float *A, int64_t sa0, int64_t sa1, const float *B, int64_t sb0,

@@ -78,6 +78,14 @@ def _declare(L):
         "orc_matmul_f32": (None, [c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_i64]),
         "orc_matmul_f64": (None, [c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_i64]),
         "orc_linreg_step_f64": (None, [c_p, c_p, c_p, c_p, c_p, c_i64, c_i64]),
+        "orc_narrow_decode": (None, [ctypes.c_int, c_p, c_p, c_i64]),
+        "orc_narrow_encode": (None, [ctypes.c_int, c_p, c_p, c_i64]),
+        "orc_narrow_sub": (None, [ctypes.c_int, c_p, c_p, c_p, c_i64]),
+        "orc_narrow_max": (None, [ctypes.c_int, c_p, c_p, c_p, c_i64]),
+        "orc_narrow_min": (None, [ctypes.c_int, c_p, c_p, c_p, c_i64]),
+        "orc_narrow_relu": (None, [ctypes.c_int, c_p, c_p, c_i64]),
+        "orc_narrow_relu_adjoint": (None, [ctypes.c_int, c_p, c_p, c_p, c_i64]),
+        "orc_matmul_narrow": (None, [ctypes.c_int, c_p, c_p, c_p, c_i64, c_i64, c_i64]),
         "orc_transformer_block_f32": (None, [c_p, c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_i64]),
         "orc_mlp_train_step_f32": (None, [c_p, c_p, c_p, c_p, c_p, c_p, c_u64, c_f32, c_f32, c_p,
                                           c_i64, c_i64, c_i64, c_i64]),
@@ -250,6 +258,57 @@ def unary(name: str, x: np.ndarray) -> np.ndarray:
 
 
 # ---- programs ----
+# ---- bfloat16 / binary16 storage (16-bit carriers as np.uint16 bit patterns) ----
+NARROW = {"bf16": 0, "f16": 1}
+
+
+def narrow_decode(kind: str, x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.uint16)
+    y = np.empty(x.shape, np.float32)
+    lib().orc_narrow_decode(NARROW[kind], _ptr(x), _ptr(y), x.size)
+    return y
+
+
+def narrow_encode(kind: str, x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(x.shape, np.uint16)
+    lib().orc_narrow_encode(NARROW[kind], _ptr(x), _ptr(y), x.size)
+    return y
+
+
+def narrow_binary(op: str, kind: str, a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, np.uint16)
+    b = np.ascontiguousarray(b, np.uint16)
+    y = np.empty(a.shape, np.uint16)
+    getattr(lib(), f"orc_narrow_{op}")(NARROW[kind], _ptr(a), _ptr(b), _ptr(y), a.size)
+    return y
+
+
+def narrow_relu(kind: str, x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.uint16)
+    y = np.empty(x.shape, np.uint16)
+    lib().orc_narrow_relu(NARROW[kind], _ptr(x), _ptr(y), x.size)
+    return y
+
+
+def narrow_relu_adjoint(kind: str, x: np.ndarray, g: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.uint16)
+    g = np.ascontiguousarray(g, np.uint16)
+    y = np.empty(x.shape, np.uint16)
+    lib().orc_narrow_relu_adjoint(NARROW[kind], _ptr(x), _ptr(g), _ptr(y), x.size)
+    return y
+
+
+def narrow_matmul(kind: str, a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, np.uint16)
+    b = np.ascontiguousarray(b, np.uint16)
+    M, K = a.shape
+    N = b.shape[1]
+    c = np.empty((M, N), np.uint16)
+    lib().orc_matmul_narrow(NARROW[kind], _ptr(a), _ptr(b), _ptr(c), M, N, K)
+    return c
+
+
 def linreg_step(X, w, y):
     X = np.ascontiguousarray(X, np.float64)
     w = np.ascontiguousarray(w, np.float64)

@@ -293,3 +293,120 @@ def test_relu_bit_rules():
     assert y.view(np.uint32).tolist() == [0, 0x80000000, 0, np.float32(2.0).view(np.uint32), 0x7FC01234]
     g = np.full(5, 3.0, np.float32)
     assert O.relu_adjoint(x, g).tolist() == [0, 0, 0, 3.0, 0]
+
+
+# ---- bfloat16 / binary16 storage ----
+def _f32_edge_patterns(rng, n):
+    """Random binary32 bit patterns plus every binary16 value's rounding
+    midpoint (as binary32) and its two binary32 neighbours."""
+    r = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)
+    h = np.arange(0x7c00, dtype=np.uint16)
+    lo = h.view(np.float16).astype(np.float64)
+    hi = (h + 1).view(np.float16).astype(np.float64)
+    mids = ((lo + hi) / 2).astype(np.float32).view(np.uint32)  # exact: 12 significant bits
+    both = np.concatenate([mids, mids - 1, mids + 1])
+    return np.concatenate([r, both, both | np.uint32(0x80000000)])
+
+
+def test_f16_decode_every_pattern_is_ieee():
+    h = np.arange(2**16, dtype=np.uint16)
+    got = O.narrow_decode("f16", h)
+    want = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_f16_encode_is_ieee_round_to_nearest_even():
+    """Against numpy's binary32 -> binary16 conversion (IEEE round to
+    nearest even, gradual underflow, overflow to infinity), including every
+    binary16 midpoint; NaN is the canonical 0x7e00."""
+    x = _f32_edge_patterns(np.random.default_rng(21), 1 << 21).view(np.float32)
+    got = O.narrow_encode("f16", x)
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    nan = np.isnan(x)
+    assert np.all(got[nan] == 0x7E00)
+    bad = np.nonzero(got[~nan] != want[~nan])[0]
+    assert bad.size == 0, [(hex(int(x[~nan].view(np.uint32)[i])), hex(int(got[~nan][i])), hex(int(want[~nan][i])))
+                           for i in bad[:5]]
+
+
+def test_bf16_encode_is_nearest_even_by_distance():
+    """bf16 rounding from its definition: of the two bf16 values around x
+    (truncation and the next one away from zero, 2^128 standing for the
+    overflow), the nearer by exact binary64 distance, ties to the even
+    pattern; NaN is the canonical 0x7fc0."""
+    x = np.random.default_rng(22).integers(0, 2**32, 1 << 21, dtype=np.uint64).astype(np.uint32)
+    half_ulps = np.arange(0, 2**16, dtype=np.uint32) << 16 | np.uint32(0x8000)  # every exact tie
+    x = np.concatenate([x, half_ulps, half_ulps + 1, half_ulps - 1]).view(np.float32)
+    got = O.narrow_encode("bf16", x)
+    fin = np.isfinite(x)
+    assert np.all(got[np.isnan(x)] == 0x7FC0)
+    inf = np.isinf(x)
+    assert np.array_equal(got[inf], (x[inf].view(np.uint32) >> 16).astype(np.uint16))
+    xb = x[fin].view(np.uint32)
+    v = x[fin].astype(np.float64)
+    lo = (xb & np.uint32(0xFFFF0000)).view(np.float32).astype(np.float64)
+    hib = (xb & np.uint32(0xFFFF0000)) + np.uint32(0x10000)
+    hi = hib.view(np.float32).astype(np.float64)
+    hi = np.where(np.isinf(hi), np.sign(v) * 2.0**128, hi)
+    dl, dh = np.abs(v - lo), np.abs(hi - v)
+    lo_bits = (xb >> 16).astype(np.uint16)
+    want = np.where(dl < dh, lo_bits, lo_bits + 1)
+    tie = dl == dh
+    want = np.where(tie, np.where(lo_bits & 1, lo_bits + 1, lo_bits), want).astype(np.uint16)
+    assert np.array_equal(got[fin], want)
+
+
+@pytest.mark.parametrize("kind", ["bf16", "f16"])
+def test_narrow_sub_is_binary32_then_one_rounding(kind):
+    rng = np.random.default_rng(23)
+    a = O.narrow_encode(kind, (rng.standard_normal(100000) * 8).astype(np.float32))
+    b = O.narrow_encode(kind, (rng.standard_normal(100000) * 8).astype(np.float32))
+    got = O.narrow_binary("sub", kind, a, b)
+    diff = (O.narrow_decode(kind, a) - O.narrow_decode(kind, b)).astype(np.float32)
+    if kind == "f16":
+        want = diff.astype(np.float16).view(np.uint16)  # IEEE narrowing, independent of the oracle's
+    else:
+        want = O.narrow_encode(kind, diff)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("kind", ["bf16", "f16"])
+def test_narrow_selection_special_cases(kind):
+    nan1, nan2 = (0x7FC1, 0xFFC3) if kind == "bf16" else (0x7E01, 0xFE03)
+    one = 0x3F80 if kind == "bf16" else 0x3C00
+    two = 0x4000 if kind == "bf16" else 0x4000
+    a = np.array([nan1, one, 0x0000, 0x8000, one, nan1, two], np.uint16)
+    b = np.array([one, nan2, 0x8000, 0x0000, two, nan2, one], np.uint16)
+    mx = O.narrow_binary("max", kind, a, b)
+    mn = O.narrow_binary("min", kind, a, b)
+    # NaN on the left wins with its own bits; NaN on the right wins when the
+    # left is a number; ties (+0 / -0) keep the left operand
+    assert list(mx) == [nan1, nan2, 0x0000, 0x8000, two, nan1, two]
+    assert list(mn) == [nan1, nan2, 0x0000, 0x8000, one, nan1, one]
+
+
+@pytest.mark.parametrize("kind", ["bf16", "f16"])
+def test_narrow_relu_bit_rules(kind):
+    nan = 0x7FC1 if kind == "bf16" else 0x7E01
+    x = np.array([0x3F80, 0xBF80, 0x0000, 0x8000, nan, nan | 0x8000, 0x0001, 0x8001], np.uint16)
+    g = np.full(x.shape, 0x1234, np.uint16)
+    assert list(O.narrow_relu(kind, x)) == [0x3F80, 0, 0, 0x8000, nan, nan | 0x8000, 0x0001, 0]
+    assert list(O.narrow_relu_adjoint(kind, x, g)) == [0x1234, 0, 0, 0, 0, 0, 0x1234, 0]
+
+
+@pytest.mark.parametrize("kind", ["bf16", "f16"])
+def test_narrow_matmul_against_float64(kind):
+    """decode, binary32 tree product, encode: within one 16-bit rounding of
+    the float64 product of the decoded operands; exact on an identity."""
+    rng = np.random.default_rng(24)
+    a = O.narrow_encode(kind, rng.standard_normal((37, 70)).astype(np.float32))
+    b = O.narrow_encode(kind, rng.standard_normal((70, 29)).astype(np.float32))
+    c = O.narrow_decode(kind, O.narrow_matmul(kind, a, b)).astype(np.float64)
+    ref = O.narrow_decode(kind, a).astype(np.float64) @ O.narrow_decode(kind, b).astype(np.float64)
+    ulp = 2.0**-8 if kind == "bf16" else 2.0**-11
+    assert np.all(np.abs(c - ref) <= ulp * np.abs(ref) + 1e-5 * np.abs(ref).max())
+    eye = O.narrow_encode(kind, np.eye(70, dtype=np.float32))
+    assert np.array_equal(O.narrow_matmul(kind, a, eye), a)
