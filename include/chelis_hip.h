@@ -48,8 +48,8 @@ const char *chelis_hip_build_info(void);
  * softmax: spec/05 section 4.2 as one region (max_reduce, sub, exp, sum, div),
  * replacing reduce_max + fused_elementwise[Sub,Exp] + reduce_sum + div
  * (kernels.rs:1802,2391,1703) which the reference fences off the device
- * (crates/chelis-ir/src/device_admission.rs:41-68). f32 exp is correctly
- * rounded (bit-exact with the C lane); f64 exp is within 1 ulp. */
+ * (crates/chelis-ir/src/device_admission.rs:41-68). exp is correctly
+ * rounded at f32 and f64, so both are bit-exact with the C lane. */
 int32_t chelis_hip_softmax(const chelis_gpu_tensor *x, const chelis_gpu_tensor *y);
 /* softmax(where(mask, x * scale, -inf)) over the last axis of a
  * [..., S_q, S_k] score tensor with the causal mask j <= i (spec/05 section
@@ -89,7 +89,11 @@ typedef struct {
     chelis_fused_step steps[CHELIS_FUSED_MAX_STEPS];
 } chelis_fused_chain;
 /* kernels.rs:2391 fused_elementwise. Inputs broadcast to `out` by their
- * own strides (stride 0 = expanded axis); out is contiguous. */
+ * own strides (stride 0 = expanded axis); out is contiguous. bf16 / f16
+ * chains (CHELIS_DTYPE_BF16 / F16) may hold only SUB, MAX_ELEM and MIN_ELEM
+ * steps, each computed at binary32 and stored at 16 bits, as the reference
+ * admits them (emit.rs:2292-2319, kernels.rs:2274-2373); any other step
+ * returns CHELIS_HIP_EUNSUPPORTED. */
 int32_t chelis_hip_fused_elementwise(const chelis_fused_chain *chain, const chelis_gpu_tensor *const *inputs,
                                      int32_t n_inputs, const chelis_gpu_tensor *out);
 
@@ -125,7 +129,8 @@ int32_t chelis_hip_dropout_replay(uint64_t key, const chelis_gpu_tensor *g, doub
 
 /* ---- activations ----
  * gelu: spec/05 section 3.3's exact Phi graph (fenced on the reference HIP
- * lane). relu / relu adjoint: kernels.rs:1136-1196. */
+ * lane). relu / relu adjoint: kernels.rs:1136-1196, and for bf16 / f16
+ * operands kernels.rs:1196-1260 (stored bits selected). */
 int32_t chelis_hip_gelu(const chelis_gpu_tensor *x, const chelis_gpu_tensor *y);
 int32_t chelis_hip_relu(const chelis_gpu_tensor *x, const chelis_gpu_tensor *y);
 int32_t chelis_hip_relu_adjoint(const chelis_gpu_tensor *x, const chelis_gpu_tensor *g,
@@ -142,7 +147,12 @@ int32_t chelis_hip_relu_adjoint(const chelis_gpu_tensor *x, const chelis_gpu_ten
  * (M or N == 1) and skinny shapes (min(M, N) < 16, or <= 64 in f64) run on
  * VALU kernels whose K sum is the canonical tree, bit-exact with the C lane.
  * `flags` = CHELIS_MATMUL_EXACT forces the canonical-tree kernels on every
- * shape. */
+ * shape. bf16 / f16 operands (all three of one dtype) run on
+ * v_mfma_f32_16x16x32_bf16 / _f16 with a binary32 accumulator and a 16-bit
+ * result (the reference's hipblasGemmEx with HIPBLAS_COMPUTE_32F,
+ * runtime/chelis_hip_runtime.h:92-170); with CHELIS_MATMUL_EXACT they are
+ * widened, run through the binary32 canonical tree and encoded once,
+ * bit-exact with the C lane. */
 #define CHELIS_MATMUL_EXACT 1
 int32_t chelis_hip_matmul(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b, const chelis_gpu_tensor *c,
                           int32_t flags);
@@ -152,7 +162,8 @@ int32_t chelis_hip_matmul(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b
  * at the dtype, so the bits equal the unfused graph's. `bias` is [N], shared
  * by every batch entry, or [batch..., N] with the result's batch axes (one
  * bias row per batch entry, e.g. a stack of projections sharing one input).
- * b may carry batch axes as in chelis_hip_matmul. */
+ * b may carry batch axes as in chelis_hip_matmul. f32 / f64 only: the
+ * reference gives 16-bit matmuls no epilogue (CHELIS_HIP_EUNSUPPORTED). */
 enum { CHELIS_ACT_NONE = 0, CHELIS_ACT_RELU = 1, CHELIS_ACT_GELU = 2 };
 int32_t chelis_hip_linear(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b, const chelis_gpu_tensor *bias,
                           int32_t activation, const chelis_gpu_tensor *residual, const chelis_gpu_tensor *c,
