@@ -42,7 +42,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0
-PEAK_TFLOPS = {"f32": 157.3, "f64": 78.6}
+PEAK_TFLOPS = {"f32": 157.3, "f64": 78.6, "bf16": 2500.0}
 METRIC = "per-kernel GB/s & GFLOP/s (% roofline); transformer-block fwd ms at 1 GPU"
 SOFTMAX_ROWS, SOFTMAX_N = 16384, 1024
 COPY_ELEMS = 64 * 1024 * 1024  # f32 relu map used to calibrate the HBM counters
@@ -94,8 +94,13 @@ def bench_softmax_f64(C, H, steps, warmup):
 def bench_gemm(C, H, M, N, K, dtype, seeds, steps, warmup, reps=1):
     """C = A.B with A, B ~ U(-1, 1); `reps` operand sets rotate when the
     working set would otherwise sit in the 256 MB Infinity Cache."""
-    a = np.random.default_rng(seeds[0]).uniform(-1, 1, (M, K)).astype(dtype)
-    b = np.random.default_rng(seeds[1]).uniform(-1, 1, (K, N) if N > 1 else (K,)).astype(dtype)
+    a = np.random.default_rng(seeds[0]).uniform(-1, 1, (M, K)).astype(np.float32 if dtype == "bf16" else dtype)
+    b = np.random.default_rng(seeds[1]).uniform(-1, 1, (K, N) if N > 1 else (K,)).astype(a.dtype)
+    if dtype == "bf16":
+        # bf16 operands as bit patterns: the upper halves, rounded to nearest even
+        a, b = [((x.view(np.uint32) + 0x7FFF + ((x.view(np.uint32) >> 16) & 1)) >> 16).astype(np.uint16)
+                for x in (a, b)]
+        dtype = np.uint16
     sets = [(C.to_device(a), C.to_device(b)) for _ in range(reps)]
     outs = [C.matmul(da, db) for da, db in sets]
     ms = time_launches(C, H, lambda i: C.matmul(sets[i % reps][0], sets[i % reps][1], outs[i % reps]), steps, warmup)
@@ -345,6 +350,9 @@ def main(argv=None) -> int:
         kernels["skinny_f64_8192x64x4096"] = gemm_line(r, "f64", "valu canonical tree (bit-exact)")
         r, gin["gemv"] = bench_gemm(C, H, 8192, 1, 8192, np.float64, (26, 27), gs, gw, reps=2)
         kernels["gemv_f64_8192x8192"] = gemm_line(r, "f64", "hbm")
+        # bf16 (np.uint16 bit patterns) with the binary32 accumulator
+        r, _ = bench_gemm(C, H, 4096, 4096, 4096, "bf16", (28, 29), gs, gw)
+        kernels["gemm_bf16_4096^3"] = gemm_line(r, "bf16", "mfma")
         progs, lin, tr, mlp = bench_programs(C, H, max(5, args.steps // 2), args.warmup)
         kernels.update(progs)
         extra = (x64, lin, tr, mlp, gin)
