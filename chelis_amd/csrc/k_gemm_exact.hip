@@ -500,6 +500,131 @@ __global__ __launch_bounds__(64 * WAVES) void tree_panel_kernel(PanelView v, Gem
     }
 }
 
+// Column panel with the A leaves in scalar registers. A wave's RM rows are
+// wave-uniform, so with K-contiguous A their leaves are read through the
+// scalar cache (constant address space loads: A is read-only here) and
+// enter the multiplies as SGPR operands; only B, one value per lane, is
+// staged in LDS. Staged in LDS, every A value was a 64-lane broadcast read
+// and the LDS return path, not the arithmetic, bounded the panel. The
+// leaf order, padding and carry stack are tree_panel_kernel's.
+template <typename T, int RM, int KC, int LV, bool TAIL, typename CT>
+__device__ __attribute__((always_inline)) inline void panel_chunk_s(T (&lv)[RM][LV], const T (&Bc)[KC][64],
+                                                                    CT *const (&arow)[RM], int64_t kc, int lane,
+                                                                    int live) {
+    T b[2], bn[2];
+    b[0] = Bc[0][lane], b[1] = Bc[1][lane];
+#pragma unroll
+    for (int i = 0; i < KC; i += 2) {
+        if (i + 2 < KC) bn[0] = Bc[i + 2][lane], bn[1] = Bc[i + 3][lane];
+#pragma unroll
+        for (int r = 0; r < RM; ++r) {
+            // a leaf past the live ones reads leaf kc (in range) and is replaced by -0.0
+            const int64_t k0 = kc + ((TAIL && i >= live) ? 0 : i);
+            const int64_t k1 = kc + ((TAIL && i + 1 >= live) ? 0 : i + 1);
+            T x0 = arow[r][k0] * b[0], x1 = arow[r][k1] * b[1];
+            if constexpr (TAIL) {
+                if (i >= live) x0 = T(-0.0);
+                if (i + 1 >= live) x1 = T(-0.0);
+            }
+            static_push<T, LV>(lv[r], i, x0);
+            static_push<T, LV>(lv[r], i + 1, x1);
+        }
+        if (i + 2 < KC) b[0] = bn[0], b[1] = bn[1];
+    }
+}
+
+template <typename T, int RM, int WAVES, int KC, int D, bool PARTIAL>
+__global__ __launch_bounds__(64 * WAVES) void tree_panel_s_kernel(PanelView v, GemmProblem p, int64_t kpart,
+                                                                   T *__restrict__ part) {
+    typedef __attribute__((address_space(4))) const T CT;
+    constexpr int LV = __builtin_ctz(KC);
+    constexpr int ROWS = RM * WAVES;
+    constexpr int BPER = KC / WAVES;  // B elements staged per thread
+    static_assert((KC & (KC - 1)) == 0 && KC % WAVES == 0, "chunk shape");
+    __shared__ T Bs[2][KC][64];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t z = blockIdx.z, z0 = z / p.nb1, z1 = z % p.nb1;
+    const int64_t mg = (int64_t)blockIdx.x * ROWS;  // first row of the workgroup
+    const int64_t k_lo = (int64_t)blockIdx.y * kpart;
+    const int64_t k_hi = k_lo + kpart < v.K ? k_lo + kpart : v.K;
+    const int64_t nchunk = (k_hi - k_lo + KC - 1) / KC;
+    const T *A = static_cast<const T *>(v.a) + z0 * v.sa0 + z1 * v.sa1;
+    const T *B = static_cast<const T *>(v.b) + z0 * v.sb0 + z1 * v.sb1;
+    const bool col_ok = lane < v.N;
+    // the wave's rows; a row past M reads row M - 1 and stores nothing
+    CT *arow[RM];
+#pragma unroll
+    for (int r = 0; r < RM; ++r) {
+        const int64_t m = mg + wave * RM + r;
+        // a global address is also its constant address space address
+        arow[r] = (CT *)(uintptr_t)(A + (m < v.M ? m : v.M - 1) * v.sam);
+    }
+
+    T sb[BPER];
+    auto fetch = [&](int64_t kc) {
+#pragma unroll
+        for (int j = 0; j < BPER; ++j) {
+            const int64_t k = kc + wave + WAVES * j;
+            sb[j] = (k < k_hi && col_ok) ? B[k * v.sbk + lane * v.sbn] : T(0);
+        }
+    };
+    auto put = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < BPER; ++j) Bs[buf][wave + WAVES * j][lane] = sb[j];
+    };
+    fetch(k_lo);
+    put(0);
+    __syncthreads();
+
+    T lvl[RM][D];
+    for (int64_t c = 0; c < nchunk; ++c) {
+        const int buf = (int)(c & 1);
+        const int64_t kc = k_lo + c * KC;
+        if (c + 1 < nchunk) fetch(kc + KC);
+        T lv[RM][LV];
+        if (kc + KC <= k_hi)
+            panel_chunk_s<T, RM, KC, LV, false>(lv, Bs[buf], arow, kc, lane, KC);
+        else  // the last, partial chunk: leaves at k >= k_hi are -0.0
+            panel_chunk_s<T, RM, KC, LV, true>(lv, Bs[buf], arow, kc, lane, (int)(k_hi - kc));
+        const int t = __builtin_ctzll(~(unsigned long long)c);
+        T carry[RM];
+#pragma unroll
+        for (int r = 0; r < RM; ++r) carry[r] = lv[r][LV - 1];
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            if (d < t) {
+#pragma unroll
+                for (int r = 0; r < RM; ++r) carry[r] = lvl[r][d] + carry[r];
+            } else if (d == t) {
+#pragma unroll
+                for (int r = 0; r < RM; ++r) lvl[r][d] = carry[r];
+            }
+        }
+        if (c + 1 < nchunk) put(buf ^ 1);
+        __syncthreads();
+    }
+    if (!col_ok) return;
+#pragma unroll
+    for (int r = 0; r < RM; ++r) {
+        const int64_t m = mg + wave * RM + r;
+        if (m >= v.M) break;
+        T total = T(0);
+        bool found = false;
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+            if ((nchunk >> d) & 1) {
+                total = found ? lvl[r][d] + total : lvl[r][d];
+                found = true;
+            }
+        if constexpr (PARTIAL) {
+            part[(((int64_t)blockIdx.y * gridDim.z + z) * v.M + m) * 64 + lane] = total;
+        } else {
+            panel_store<T>(p, v, z0, z1, m, lane, total);
+        }
+    }
+}
+
 // Join the per-block totals of tree_panel_kernel: the canonical tree over
 // the nparts block totals (adjacent pairs, odd one carried), then the
 // epilogue. One thread per output.
@@ -703,11 +828,15 @@ int32_t launch_panel(const GemmProblem &p, const PanelView &v, bool cut, hipStre
     const size_t ws_bytes = (size_t)nparts * nz * v.M * 64 * sizeof(T);
     if (nparts > 1 && !(ws = static_cast<T *>(scratch_alloc(ws_bytes))))
         return set_error(CHELIS_HIP_EHIP, "matmul: scratch allocation failed");
+    // K-contiguous A: its leaves through the scalar cache
+    const bool ascalar = v.sak == 1;
     if (nparts == 1) {
-        if (avec) tree_panel_kernel<T, RM, WAVES, KC, D, false, true><<<grid, 64 * WAVES, 0, st>>>(v, p, kpart, ws);
+        if (ascalar) tree_panel_s_kernel<T, RM, WAVES, KC, D, false><<<grid, 64 * WAVES, 0, st>>>(v, p, kpart, ws);
+        else if (avec) tree_panel_kernel<T, RM, WAVES, KC, D, false, true><<<grid, 64 * WAVES, 0, st>>>(v, p, kpart, ws);
         else tree_panel_kernel<T, RM, WAVES, KC, D, false, false><<<grid, 64 * WAVES, 0, st>>>(v, p, kpart, ws);
     } else {
-        if (avec) tree_panel_kernel<T, RM, WAVES, KC, D, true, true><<<grid, 64 * WAVES, 0, st>>>(v, p, kpart, ws);
+        if (ascalar) tree_panel_s_kernel<T, RM, WAVES, KC, D, true><<<grid, 64 * WAVES, 0, st>>>(v, p, kpart, ws);
+        else if (avec) tree_panel_kernel<T, RM, WAVES, KC, D, true, true><<<grid, 64 * WAVES, 0, st>>>(v, p, kpart, ws);
         else tree_panel_kernel<T, RM, WAVES, KC, D, true, false><<<grid, 64 * WAVES, 0, st>>>(v, p, kpart, ws);
     }
     hipError_t le = hipGetLastError();
