@@ -271,10 +271,38 @@ template <typename T>
 struct RowDiv {
     T total;
     double inv;
-    __device__ explicit RowDiv(T t) : total(t), inv(sizeof(T) == 4 ? 1.0 / (double)t : 0.0) {}
-    __device__ T operator()(T v) const {
-        if constexpr (sizeof(T) == 4) return canon(quot_f32(v, inv));
-        else return canon(v / total);
+    __device__ explicit RowDiv(T t) : total(t), inv(1.0 / (double)t) {}
+    __device__ T operator()(T v) const { return canon(quot_f32(v, inv)); }
+};
+
+__device__ __noinline__ double div_full(double v, double t) { return v / t; }
+
+// binary64: the steps of the device's IEEE division (v_div_scale_f64 of
+// both operands, v_rcp_f64 with two Newton steps, product, residual, fma,
+// v_div_fixup_f64), with the reciprocal - which depends only on the
+// divisor - formed once per row. The steps are taken as they are where the
+// scale steps are the identity: a divisor in [1, 2^20] (the row totals)
+// and a dividend that is 0 or at least 2^-960 (v_div_scale_f64 scales a
+// dividend whose biased exponent is at most 53, or whose quotient would be
+// subnormal); any other element takes the full division.
+template <>
+struct RowDiv<double> {
+    double total, rcp;
+    bool fast;
+    __device__ explicit RowDiv(double t) : total(t), fast(t >= 1.0 && t <= 0x1p20) {
+        double r = __builtin_amdgcn_rcp(t);
+        double e = fma(-t, r, 1.0);
+        r = fma(r, e, r);
+        e = fma(-t, r, 1.0);
+        rcp = fma(r, e, r);
+    }
+    __device__ double operator()(double v) const {
+        if (fast && (v == 0.0 || v >= 0x1p-960)) {
+            const double q = v * rcp;
+            const double r = fma(-total, q, v);
+            return canon(__builtin_amdgcn_div_fixup(fma(r, rcp, q), total, v));
+        }
+        return canon(div_full(v, total));
     }
 };
 

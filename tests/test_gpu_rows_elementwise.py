@@ -68,6 +68,18 @@ def test_softmax_f64_bit_exact(n):
     assert bits_equal(y, ref), mismatch_report(y, ref)
 
 
+def test_softmax_f64_tiny_and_subnormal_quotients():
+    """Elements whose exp is below 2^-960 or subnormal take the full division;
+    the rest divide by the row reciprocal's steps: both bit-exact."""
+    rng = np.random.default_rng(99)
+    x = rng.uniform(-745.0, 0.0, (256, 4096))
+    x[:, 0] = 0.0
+    x[::2, 1:64] = rng.uniform(-3.0, 0.0, (128, 63))
+    y = C.softmax(C.to_device(x)).numpy()
+    ref = O.softmax_rows(x)
+    assert bits_equal(y, ref), mismatch_report(y, ref)
+
+
 def test_softmax_f64_special_rows():
     x = np.array([[0.0, -np.inf, 1.0, -np.inf], [-np.inf] * 4, [3.0] * 4, [1.0, np.nan, 0, 0],
                   [np.inf, 0, 0, 0], [-0.0, 0.0, -0.0, 0.0], [0.0, -745.0, -708.5, -1e-300]])
