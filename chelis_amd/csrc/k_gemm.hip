@@ -456,14 +456,16 @@ int32_t run_mfma(const GemmProblem &p, hipStream_t st) {
     bool av = false, bv = false;
     const int al = lay_of<T>(p.sam, p.sak, p.a, p.M, p.K, &av);
     const int bl = lay_of<T>(p.sbn, p.sbk, p.b, p.N, p.K, &bv);
-    // 128-tiles when they give every CU a tile, no dimension is at most half
-    // a tile and K runs long enough (> 128) to amortize a tile's first loads
-    // and its epilogue (measured: 4096 x 1024 x 1024 takes 115 us on 256
-    // 128-tiles against 120 us on 1024 64-tiles); 64-tiles, four times as
-    // many workgroups that overlap those phases, otherwise (the 128 x (512 x
-    // 512 x 64) attention scores take 80 us on 64-tiles against 132 us).
+    // 128-tiles when they give every CU two tiles (the two workgroups a CU
+    // holds), no dimension is at most half a tile and K runs long enough
+    // (> 128) to amortize a tile's first loads and its epilogue; 64-tiles,
+    // four times as many workgroups that overlap those phases, otherwise.
+    // Measured: the transformer block's projections and FFN2 (256 128-tiles
+    // each, with bias and residual epilogues) run the block in 1.25 ms on
+    // 64-tiles against 1.32 ms on 128-tiles; the 128 x (512 x 512 x 64)
+    // attention scores take 80 us on 64-tiles against 132 us.
     const int64_t big = ((p.M + 127) / 128) * ((p.N + 127) / 128) * p.nb0 * p.nb1;
-    const bool small = big < (int64_t)device_cus() || p.M <= 64 || p.N <= 64 || p.K <= 128;
+    const bool small = big < 2 * (int64_t)device_cus() || p.M <= 64 || p.N <= 64 || p.K <= 128;
     return small ? run_tiles<T, 2>(p, al, bl, av, bv, st) : run_tiles<T, 4>(p, al, bl, av, bv, st);
 }
 
