@@ -64,9 +64,16 @@ template <> __device__ inline float leaf_log<float>(float v) {
     y = cr_exception(y, b, 0x6f31a8ecu, 0x42845a89u);
     return canon(y);
 }
-template <> __device__ inline float leaf_erfc<float>(float v) {
+__device__ __noinline__ inline float erfc_slow32(float v) {
     const float y = cr_exception((float)erfc((double)v), f32_bits(v), 0xb76c9f62u, 0x3f800085u);
     return canon(y);
+}
+// the branch-free fast path (devmath.h erfcf_fast), else the binary64
+// device erfc rounded once with its exception (out of line)
+template <> __device__ inline float leaf_erfc<float>(float v) {
+    bool slow;
+    const float y = erfcf_fast(v, slow);
+    return slow ? erfc_slow32(v) : y;
 }
 template <> __device__ inline float leaf_tanh<float>(float v) { return canon((float)tanh((double)v)); }
 

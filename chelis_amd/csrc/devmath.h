@@ -21,6 +21,7 @@
 #endif
 
 #include "exp2_table.h"
+#include "erfc_table.h"
 
 namespace chelis {
 
@@ -187,6 +188,59 @@ CHELIS_HD inline float expf_cr_nonpos(float xf) {
 // one rounding to binary32 gives the correctly rounded quotient. Checked
 // against IEEE division on the host (tests/test_devmath.py).
 CHELIS_HD inline float quot_f32(float v, double inv) { return (float)((double)v * inv); }
+
+// Binary32 erfc, fast path, branch free. Returns (float)y and sets `slow`
+// when y is not known to be the correctly rounded result (and for NaN and
+// 9.1 <= x < 10.1, left to the caller's fallback).
+//
+// For -4.5 < x < 9.1, y is erfc(x) in binary64 to about 2^-47 relative:
+// for |x| < 1/2, 1 - x P(x^2) with P a degree-7 fit of erf(x)/x (2^-49);
+// otherwise exp(-x^2) erfcx(|x|) with erfcx a degree-9 fit on intervals of
+// 1/4 (2^-48; x^2 is exact, exp(-x^2) is reduced as in expf_fast with a
+// degree-5 Taylor polynomial, truncation below 2^-54), and erfc(x) =
+// 2 - erfc(-x) for x < 0. The coefficients are erfc_table.h's
+// (gen_erfc_table.py). Every such result is a normal binary32 (erfc(9.1) >
+// 2^-126), so (float)y is the correctly rounded result unless the 29 bits
+// below binary32 precision in y lie within 2^9 units of the midpoint
+// pattern 1 << 28: the error is below 2^6 units there. x <= -4.5 gives 2
+// (erfc(-4.5) lies above 2 - 2^-24, the midpoint below 2), x >= 10.1 gives
+// +0 (erfc(10.1) is below 2^-150, half the least subnormal), and +inf and
+// -inf fall in those ranges. Checked against CORE-MATH over every binary32
+// input (tests/test_devmath.py).
+CHELIS_HD inline float erfcf_fast(float xf, bool &slow) {
+    const double x = (double)xf;
+    const double ax = fabs(x);
+    const double s = x * x;  // exact
+    const double ta = fma(8.0, s, -1.0);
+    double pa = chelis_erf_a[7];
+#pragma unroll
+    for (int d = 6; d >= 0; --d) pa = fma(pa, ta, chelis_erf_a[d]);
+    const double ya = fma(-x, pa, 1.0);
+    int i = (int)((ax - 0.5) * 4.0);
+    i = i < 0 ? 0 : (i > 34 ? 34 : i);
+    const double tb = (ax - (0.5 + 0.25 * i)) * 8.0 - 1.0;  // exact
+    double g = chelis_erfcx_b[i][9];
+#pragma unroll
+    for (int d = 8; d >= 0; --d) g = fma(g, tb, chelis_erfcx_b[i][d]);
+    // exp(-s), -s = k ln2/64 + r, |k| < 2^11
+    const double shifted = fma(-s, CHELIS_INV_LN2_64, 0x1.8p52);
+    const double kd = shifted - 0x1.8p52;
+    const int k = (int)(uint32_t)f64_bits(shifted);
+    double r = fma(-kd, CHELIS_LN2_64_HI, -s);
+    r = fma(-kd, CHELIS_LN2_64_LO, r);
+    double p = fma(r, 0x1.1111111111111p-7, 0x1.5555555555555p-5);  // 1/5!, 1/4!
+    p = fma(p, r, 0x1.5555555555555p-3);
+    p = fma(p, r, 0.5);
+    p = fma(p, r, 1.0);
+    p = fma(p, r, 1.0);
+    const double e = ldexp(chelis_exp2_64_tab[k & 63][0] * p, (k - (k & 63)) / 64);
+    const double yb = e * g;
+    double y = ax < 0.5 ? ya : (x > 0.0 ? yb : 2.0 - yb);
+    y = x <= -4.5 ? 2.0 : (x >= 10.1 ? 0.0 : y);
+    const uint32_t below = ((uint32_t)f64_bits(y) & 0x1fffffffu) - (0x10000000u - 512u);
+    slow = (x != x) || (x >= 9.1 && x < 10.1) || below < 1024u;
+    return (float)y;
+}
 
 // ------------------------------------------------------------ binary64 exp
 //

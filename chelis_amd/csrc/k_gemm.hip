@@ -325,6 +325,41 @@ __global__ __launch_bounds__(THREADS, kMinWavesPerEu<T>) void gemm_mfma_kernel(G
         return;
     }
     T *C = static_cast<T *>(p.c) + z0 * p.sc0 + z1 * p.sc1;
+    if constexpr (GELU && sizeof(T) == 4) {
+        // The GELU graph once, not once per held output: the tile goes
+        // through LDS in quarters of BM/4 rows; the two waves owning a
+        // quarter write their accumulators, then every thread runs the
+        // epilogue over the quarter in a loop that is not unrolled, with
+        // consecutive threads on consecutive columns (coalesced stores).
+        // Inline per output, the graph took the kernel to one wave per SIMD
+        // with spills.
+        constexpr int QR = BM / 4, LDT = BN + 8;
+        static_assert(QR * LDT <= 2 * BM * LD, "quarter tile fits in As");
+        T *tile = &As[0][0];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            __syncthreads();  // As: the main loop's (or the last quarter's) reads are done
+            if (wm == q / 2) {
+#pragma unroll
+                for (int ii = 0; ii < TM / 2; ++ii)
+#pragma unroll
+                    for (int j = 0; j < TM; ++j)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            tile[(ii * 16 + M::row(fq, r)) * LDT + wn * WT + j * 16 + fr] =
+                                acc[(q % 2) * (TM / 2) + ii][j][r];
+            }
+            __syncthreads();
+#pragma unroll 1
+            for (int e = threadIdx.x; e < QR * BN; e += THREADS) {
+                const int row = e / BN, col = e % BN;
+                const int64_t m = m0 + q * QR + row, n = n0 + col;
+                if (m < p.M && n < p.N)
+                    C[m * p.scm + n * p.scn] = gemm_epilogue<T, true>(tile[row * LDT + col], p, z0, z1, m, n);
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll

@@ -50,6 +50,21 @@ def test_exp_f64_matches_core_math(tmp_path):
     assert err <= -73.7, r.stdout
 
 
+def test_erfcf_fast_path_matches_core_math_on_every_binary32(tmp_path):
+    """The binary32 erfc fast path: every input it does not flag gives
+    CORE-MATH's bits (the flagged ones take the fallback, which the device
+    test checks over every input)."""
+    O.build()
+    exe = tmp_path / "erfcf_check"
+    ref = os.path.join(ROOT, "oracle", "_ref")
+    subprocess.run(["g++", "-O2", "-ffp-contract=off", "-fno-fast-math", "-fopenmp", "-std=c++17", "-o", str(exe),
+                    os.path.join(ROOT, "tests", "cpu", "erfcf_check.cpp"), f"-L{ref}", "-lcrmath_ref",
+                    f"-Wl,-rpath,{ref}"], check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=900)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "mismatches 0" in r.stdout
+
+
 def test_quot_f32_matches_ieee_division(tmp_path):
     """The softmax row division v / total through a binary64 reciprocal is
     the correctly rounded binary32 quotient: every binary32 v in (0, 1]
