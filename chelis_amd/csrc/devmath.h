@@ -140,6 +140,30 @@ CHELIS_HD inline float expf_cr_dd(float xf) {
 // unchecked, so callers must not pass one.
 template <bool NONPOS = false, class Tab>
 CHELIS_HD inline float expf_fast(float xf, const Tab &tab, bool &slow) {
+    if constexpr (NONPOS) {
+        // x <= 0 or NaN: arguments below -104.5 are raised to it (their exp,
+        // like exp(-104.5) < 2^-150, rounds to +0 at any of the fast path's
+        // errors), (-104, -87] (subnormal results) and NaN are flagged
+        // (every comparison with NaN is false), and the midpoint test runs
+        // on every other result; a flag on a raised argument only costs the
+        // slow path.
+        const float xc = xf > -104.5f ? xf : -104.5f;
+        const double x = (double)xc;
+        const double shifted = fma(x, CHELIS_INV_LN2_64, 0x1.8p52);
+        const double kd = shifted - 0x1.8p52;
+        const int k = (int)(uint32_t)f64_bits(shifted);
+        double r = fma(-kd, CHELIS_LN2_64_HI, x);
+        r = fma(-kd, CHELIS_LN2_64_LO, r);
+        double p = fma(r, 0x1.5555555555555p-5, 0x1.5555555555555p-3);
+        p = fma(p, r, 0.5);
+        p = fma(p, r, 1.0);
+        p = fma(p, r, 1.0);
+        const double y = ldexp(tab(k & 63) * p, k >> 6);
+        const uint32_t below = ((uint32_t)f64_bits(y) & 0x1fffffffu) - (0x10000000u - 2047u);
+        slow = !(xf > -87.0f) && !(xf <= -104.0f);
+        slow = slow || below < 4095u;
+        return (float)y;
+    }
     const bool zero = xf <= -104.0f;
     const bool fast = NONPOS ? xf > -87.0f : (xf > -87.0f && xf < 88.0f);
     const double x = (double)xf;
