@@ -176,4 +176,28 @@ __device__ inline T apply_step(uint8_t op, T a, T b, double imm) {
 }
 
 
+// ---------------------------------------------------------------- chain interpreter
+// One element's inputs and step results live in a row of LDS slots (inputs
+// first, then steps) and the steps run as a loop over the chain: a private
+// array indexed by the run-time step arguments would live in scratch
+// memory. The slot row stride is odd, so the lanes of a wave hit distinct
+// LDS banks.
+constexpr int kSlots = CHELIS_FUSED_MAX_INPUTS + CHELIS_FUSED_MAX_STEPS;
+constexpr int kSlotStride = kSlots + 1;
+
+template <typename T>
+__device__ inline T run_chain(const ChainDev &ch, T *slot) {
+    T v = T(0);
+#pragma unroll 1
+    for (int s = 0; s < ch.n_steps; ++s) {
+        const int a0 = ch.a0[s], a1 = ch.a1[s];
+        const T x = slot[a0 >= 0 ? a0 : CHELIS_FUSED_MAX_INPUTS - a0 - 1];
+        const T y = slot[a1 >= 0 ? a1 : CHELIS_FUSED_MAX_INPUTS - a1 - 1];
+        v = apply_step<T>(ch.op[s], x, y, ch.imm[s]);
+        slot[CHELIS_FUSED_MAX_INPUTS + s] = v;
+    }
+    return v;
+}
+
+
 }  // namespace chelis

@@ -32,28 +32,10 @@ struct Shape {
     int64_t ext[kMaxRank];
 };
 
-// The chain interpreter: one thread per element, the element's inputs and
-// step results in a row of LDS slots (inputs first, then steps), the steps
-// run by a loop over the chain rather than unrolled. A launch is mostly a
-// handful of small tensors, so the kernel is kept small: its code is
-// fetched by every CU once per launch. The slot row stride is odd, so the
-// lanes of a wave hit distinct LDS banks.
-constexpr int kSlots = CHELIS_FUSED_MAX_INPUTS + CHELIS_FUSED_MAX_STEPS;
-constexpr int kSlotStride = kSlots + 1;
-
-template <typename T>
-__device__ inline T run_chain(const ChainDev &ch, T *slot) {
-    T v = T(0);
-#pragma unroll 1
-    for (int s = 0; s < ch.n_steps; ++s) {
-        const int a0 = ch.a0[s], a1 = ch.a1[s];
-        const T x = slot[a0 >= 0 ? a0 : CHELIS_FUSED_MAX_INPUTS - a0 - 1];
-        const T y = slot[a1 >= 0 ? a1 : CHELIS_FUSED_MAX_INPUTS - a1 - 1];
-        v = apply_step<T>(ch.op[s], x, y, ch.imm[s]);
-        slot[CHELIS_FUSED_MAX_INPUTS + s] = v;
-    }
-    return v;
-}
+// The chain interpreter (run_chain, chain.h): one thread per element, the
+// element's inputs and step results in a row of LDS slots. A launch is
+// mostly a handful of small tensors, so the kernel is kept small: its code
+// is fetched by every CU once per launch.
 
 // Strided operands (any of the up-to-4 collapsed axes, broadcast by stride
 // 0): the element's coordinates from its flat index, then one offset per

@@ -17,6 +17,11 @@
 //    holds leaf s*64 + l of each segment s (coalesced loads), the wave64
 //    butterfly builds each segment's 64-leaf subtree, then a tree over the
 //    S segments.
+//  * rows, contiguous (every input's leaves at stride 1, rows 16-byte
+//    aligned): one wave per group of G = 64*V*S leaves, V = 16/sizeof(T);
+//    lane l holds the V consecutive leaves 64V*s + V*l .. of segment s,
+//    read with one 16-byte load per input. The in-lane tree over them is an
+//    aligned V-leaf subtree; the butterfly joins 64 of those.
 //  * cols  (inner > 1): one thread per (group, column), adjacent threads on
 //    adjacent columns (coalesced); the thread loads its G = 32 leaves and
 //    reduces them with an unrolled in-register tree.
@@ -69,28 +74,63 @@ struct LeafSrc {
     const int64_t *idx;  // partial indices of a previous pass (argmax/argmin), or null
 };
 
+// A chain leaf runs on the element's row of LDS slots (run_chain).
 template <typename T, bool CHAIN>
-__device__ inline T leaf(const ChainDev &ch, const LeafSrc &src, int64_t o, int64_t i, int64_t j) {
+__device__ inline T leaf(const ChainDev &ch, const LeafSrc &src, T *slot, int64_t o, int64_t i, int64_t j) {
     if constexpr (!CHAIN) {
         return static_cast<const T *>(src.p[0])[o * src.so[0] + i * src.sn[0] + j * src.si[0]];
     } else {
         T in[CHELIS_FUSED_MAX_INPUTS];
 #pragma unroll
         for (int k = 0; k < CHELIS_FUSED_MAX_INPUTS; ++k)
-            in[k] = k < src.n_in ? static_cast<const T *>(src.p[k])[o * src.so[k] + i * src.sn[k] + j * src.si[k]]
-                                 : T(0);
-        T val[CHELIS_FUSED_MAX_STEPS];
+            if (k < src.n_in) in[k] = static_cast<const T *>(src.p[k])[o * src.so[k] + i * src.sn[k] + j * src.si[k]];
 #pragma unroll
-        for (int s = 0; s < CHELIS_FUSED_MAX_STEPS; ++s) {
-            if (s < ch.n_steps) {
-                const int a0 = ch.a0[s], a1 = ch.a1[s];
-                const T x = a0 >= 0 ? in[a0] : val[-a0 - 1];
-                const T y = a1 >= 0 ? in[a1] : val[-a1 - 1];
-                val[s] = apply_step<T>(ch.op[s], x, y, ch.imm[s]);
-            }
-        }
-        return val[ch.n_steps - 1];
+        for (int k = 0; k < CHELIS_FUSED_MAX_INPUTS; ++k)
+            if (k < src.n_in) slot[k] = in[k];
+        return run_chain<T>(ch, slot);
     }
+}
+
+// Wave64 butterfly over one value (and index) per lane: lane l ends with the
+// combination of the 64 lanes' values in lane order (the lower lane is
+// always the left operand, so first-NaN and first-index rules hold).
+template <typename T, Rk K>
+__device__ inline void wave_join(T &v, int64_t &vi, int lane) {
+    if constexpr (K == Rk::Sum) {
+        v = wave_tree_sum(v);
+        return;
+    }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        T ov = shfl_xor(v, m);
+        int64_t oi = has_index(K) ? shfl_xor(vi, m) : 0;
+        if constexpr (K == Rk::Prod) {
+            combine<T, K>(v, vi, ov, oi);  // commutative: both lanes agree
+        } else if (lane & m) {
+            T a = ov;
+            int64_t ia = oi;
+            combine<T, K>(a, ia, v, vi);
+            v = a;
+            vi = ia;
+        } else {
+            combine<T, K>(v, vi, ov, oi);
+        }
+    }
+}
+
+// Tree over n (a power of two) values with their indices, in order.
+template <typename T, Rk K, int N>
+__device__ inline void ordered_tree(T (&v)[N], int64_t (&vi)[N]) {
+#pragma unroll
+    for (int w = N; w > 1; w >>= 1)
+#pragma unroll
+        for (int t = 0; t < w / 2; ++t) {
+            T a = v[2 * t];
+            int64_t ia = vi[2 * t];
+            combine<T, K>(a, ia, v[2 * t + 1], vi[2 * t + 1]);
+            v[t] = a;
+            vi[t] = ia;
+        }
 }
 
 template <typename T, Rk K>
@@ -105,6 +145,8 @@ __global__ __launch_bounds__(256) void reduce_rows_kernel(ChainDev ch, LeafSrc s
                                                           int64_t groups, T *__restrict__ out_v,
                                                           int64_t *__restrict__ out_i, bool last) {
     constexpr int G = 64 * S;
+    __shared__ T slots[CHAIN ? 256 * kSlotStride : 1];
+    T *slot = slots + (CHAIN ? threadIdx.x * kSlotStride : 0);
     const int lane = threadIdx.x & 63;
     const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (item >= outer * groups) return;
@@ -117,44 +159,102 @@ __global__ __launch_bounds__(256) void reduce_rows_kernel(ChainDev ch, LeafSrc s
         T v = identity<T, K>();
         int64_t vi = i;
         if (i < n) {
-            v = leaf<T, CHAIN>(ch, src, o, i, 0);
+            v = leaf<T, CHAIN>(ch, src, slot, o, i, 0);
             if (has_index(K) && src.idx) vi = src.idx[o * n + i];
         }
-        if constexpr (K == Rk::Sum) {
-            v = wave_tree_sum(v);
-            seg[s] = v;
-            sidx[s] = vi;
-            continue;
-        }
-#pragma unroll
-        for (int m = 1; m < 64; m <<= 1) {
-            T ov = shfl_xor(v, m);
-            int64_t oi = has_index(K) ? shfl_xor(vi, m) : 0;
-            if constexpr (K == Rk::Sum || K == Rk::Prod) {
-                combine<T, K>(v, vi, ov, oi);  // commutative: both lanes agree
-            } else if (lane & m) {
-                T a = ov;
-                int64_t ia = oi;
-                combine<T, K>(a, ia, v, vi);
-                v = a;
-                vi = ia;
-            } else {
-                combine<T, K>(v, vi, ov, oi);
-            }
-        }
+        wave_join<T, K>(v, vi, lane);
         seg[s] = v;
         sidx[s] = vi;
     }
+    ordered_tree<T, K, S>(seg, sidx);
+    if (lane == 0) {
+        out_v[item] = last ? finalize<T, K>(seg[0]) : seg[0];
+        if (has_index(K)) out_i[item] = sidx[0];
+    }
+}
+
+// Contiguous rows: leaf i of row o of input k at p[k] + o*so[k] + i, each
+// row start 16-byte aligned. Leaf indices are positions (a first pass, or a
+// later pass of a value-only reduction).
+template <typename T>
+struct Vec16Of;
+template <>
+struct Vec16Of<float> {
+    using type = float4;
+};
+template <>
+struct Vec16Of<double> {
+    using type = double2;
+};
+
+template <typename T, Rk K, int S, bool CHAIN>
+__global__ __launch_bounds__(256) void reduce_rows_vec_kernel(ChainDev ch, LeafSrc src, int64_t outer, int64_t n,
+                                                              int64_t groups, T *__restrict__ out_v,
+                                                              int64_t *__restrict__ out_i, bool last) {
+    constexpr int V = 16 / sizeof(T);
+    constexpr int G = 64 * V * S;
+    using Q = typename Vec16Of<T>::type;
+    __shared__ T slots[CHAIN ? 256 * kSlotStride : 1];
+    T *slot = slots + (CHAIN ? threadIdx.x * kSlotStride : 0);
+    const int lane = threadIdx.x & 63;
+    const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (item >= outer * groups) return;
+    const int64_t o = item / groups, g = item % groups;
+    T v[CHAIN ? 1 : S][V];
+    if constexpr (!CHAIN) {
+        // every load issued before the first combine
+        const T *row = static_cast<const T *>(src.p[0]) + o * src.so[0];
 #pragma unroll
-    for (int w = S; w > 1; w >>= 1)
+        for (int s = 0; s < S; ++s) {
+            const int64_t i0 = g * G + (int64_t)s * 64 * V + (int64_t)lane * V;
+            if (i0 + V <= n) {
+                const Q q = *reinterpret_cast<const Q *>(row + i0);
+                const T *qe = reinterpret_cast<const T *>(&q);
 #pragma unroll
-        for (int t = 0; t < w / 2; ++t) {
-            T a = seg[2 * t];
-            int64_t ia = sidx[2 * t];
-            combine<T, K>(a, ia, seg[2 * t + 1], sidx[2 * t + 1]);
-            seg[t] = a;
-            sidx[t] = ia;
+                for (int e = 0; e < V; ++e) v[s][e] = qe[e];
+            } else {
+#pragma unroll
+                for (int e = 0; e < V; ++e) v[s][e] = i0 + e < n ? row[i0 + e] : identity<T, K>();
+            }
         }
+    }
+    T seg[S];
+    int64_t sidx[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const int64_t i0 = g * G + (int64_t)s * 64 * V + (int64_t)lane * V;
+        T(&cur)[V] = v[CHAIN ? 0 : s];
+        if constexpr (CHAIN) {
+            if (i0 + V <= n) {
+                Q in[CHELIS_FUSED_MAX_INPUTS];
+#pragma unroll
+                for (int k = 0; k < CHELIS_FUSED_MAX_INPUTS; ++k)
+                    if (k < src.n_in)
+                        in[k] = *reinterpret_cast<const Q *>(static_cast<const T *>(src.p[k]) + o * src.so[k] + i0);
+#pragma unroll
+                for (int e = 0; e < V; ++e) {
+#pragma unroll
+                    for (int k = 0; k < CHELIS_FUSED_MAX_INPUTS; ++k)
+                        if (k < src.n_in) slot[k] = reinterpret_cast<const T *>(&in[k])[e];
+                    cur[e] = run_chain<T>(ch, slot);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < V; ++e)
+                    cur[e] = i0 + e < n ? leaf<T, true>(ch, src, slot, o, i0 + e, 0) : identity<T, K>();
+            }
+        }
+        int64_t vi[V];
+#pragma unroll
+        for (int e = 0; e < V; ++e) vi[e] = i0 + e;
+        ordered_tree<T, K, V>(cur, vi);
+        T x = cur[0];
+        int64_t xi = vi[0];
+        wave_join<T, K>(x, xi, lane);
+        seg[s] = x;
+        sidx[s] = xi;
+    }
+    ordered_tree<T, K, S>(seg, sidx);
     if (lane == 0) {
         out_v[item] = last ? finalize<T, K>(seg[0]) : seg[0];
         if (has_index(K)) out_i[item] = sidx[0];
@@ -166,6 +266,8 @@ __global__ __launch_bounds__(256) void reduce_cols_kernel(ChainDev ch, LeafSrc s
                                                           int64_t inner, int64_t groups, T *__restrict__ out_v,
                                                           int64_t *__restrict__ out_i, bool last) {
     constexpr int G = 32;
+    __shared__ T slots[CHAIN ? 256 * kSlotStride : 1];
+    T *slot = slots + (CHAIN ? threadIdx.x * kSlotStride : 0);
     const int64_t total = outer * groups * inner;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += stride) {
@@ -180,20 +282,11 @@ __global__ __launch_bounds__(256) void reduce_cols_kernel(ChainDev ch, LeafSrc s
             v[q] = identity<T, K>();
             vi[q] = i;
             if (i < n) {
-                v[q] = leaf<T, CHAIN>(ch, src, o, i, j);
+                v[q] = leaf<T, CHAIN>(ch, src, slot, o, i, j);
                 if (has_index(K) && src.idx) vi[q] = src.idx[(o * n + i) * inner + j];
             }
         }
-#pragma unroll
-        for (int w = G; w > 1; w >>= 1)
-#pragma unroll
-            for (int q = 0; q < w / 2; ++q) {
-                T a = v[2 * q];
-                int64_t ia = vi[2 * q];
-                combine<T, K>(a, ia, v[2 * q + 1], vi[2 * q + 1]);
-                v[q] = a;
-                vi[q] = ia;
-            }
+        ordered_tree<T, K, G>(v, vi);
         out_v[t] = last ? finalize<T, K>(v[0]) : v[0];
         if (has_index(K)) out_i[t] = vi[0];
     }
@@ -220,6 +313,37 @@ __global__ __launch_bounds__(256) void count_kernel(const uint8_t *__restrict__ 
     for (int64_t i = lane; i < n; i += 64) {
         const uint8_t b = x[o * so + i * sn + j * si];
         bad |= b > 1;
+        c += b & 1;
+    }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) c += shfl_xor(c, m);
+    if (bad) atomicOr(err, 1);
+    if (lane == 0) out[t] = c;
+}
+
+// count over contiguous rows (16-byte aligned starts): each lane reads 16
+// bytes per access; a byte's low bit is its count and any higher bit marks
+// a byte other than 0/1.
+__global__ __launch_bounds__(256) void count_rows_vec_kernel(const uint8_t *__restrict__ x, int64_t rows,
+                                                             int64_t n, int64_t so, int64_t *__restrict__ out,
+                                                             int32_t *__restrict__ err) {
+    const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (t >= rows) return;
+    const uint8_t *r = x + t * so;
+    const int64_t nv = n / 16;
+    int64_t c = 0;
+    uint32_t bad = 0;
+#pragma unroll 4
+    for (int64_t v = lane; v < nv; v += 64) {
+        const uint4 w = reinterpret_cast<const uint4 *>(r)[v];
+        bad |= (w.x | w.y | w.z | w.w) & 0xFEFEFEFEu;
+        c += __popc(w.x & 0x01010101u) + __popc(w.y & 0x01010101u) + __popc(w.z & 0x01010101u) +
+             __popc(w.w & 0x01010101u);
+    }
+    for (int64_t i = nv * 16 + lane; i < n; i += 64) {
+        const uint8_t b = r[i];
+        bad |= b & 0xFEu;
         c += b & 1;
     }
 #pragma unroll
@@ -290,15 +414,35 @@ int32_t run_reduce(const ChainDev &ch, bool chain, LeafSrc src, int64_t outer, i
         // a longer one is cut into as many groups as keep >= 1024 waves busy
         // (S = 16 only when there are rows enough), since a pass over few long
         // groups runs on a handful of waves.
+        LeafSrc s = src;
+        if (!first) {
+            s.n_in = 1;
+            s.p[0] = prev_v;
+            s.so[0] = cur_n * inner;
+            s.sn[0] = inner;
+            s.si[0] = 1;
+            s.idx = prev_i;
+        }
+        const bool use_chain = first && chain;
+        // contiguous rows take 16-byte loads: leaves at stride 1, row
+        // starts aligned, and leaf indices that are positions
+        bool vec = rows && !(has_index(K) && !first);
+        for (int32_t k = 0; vec && k < s.n_in; ++k)
+            vec = s.sn[k] == 1 && (reinterpret_cast<uintptr_t>(s.p[k]) & 15u) == 0 &&
+                  (s.so[k] * (int64_t)sizeof(T)) % 16 == 0;
+        const int64_t unit = vec ? 64 * (16 / (int64_t)sizeof(T)) : 64;
+        // a contiguous chain leaf runs one segment per wave: the interpreter
+        // is inlined once per element a lane holds
+        const int smax = vec && use_chain ? 1 : 16;
         int S = 1;
         if (rows) {
-            if (cur_n <= 64 * 16) {
-                while (64 * S < cur_n) S <<= 1;
+            if (cur_n <= unit * smax) {
+                while (unit * S < cur_n) S <<= 1;
             } else {
-                while (S < 16 && outer * ((cur_n + 128 * S - 1) / (128 * S)) >= 1024) S <<= 1;
+                while (S < smax && outer * ((cur_n + 2 * unit * S - 1) / (2 * unit * S)) >= 1024) S <<= 1;
             }
         }
-        const int64_t G = rows ? 64 * S : 32;
+        const int64_t G = rows ? unit * S : 32;
         const int64_t groups = (cur_n + G - 1) / G;
         const bool last = groups == 1;
         T *dst_v;
@@ -321,28 +465,23 @@ int32_t run_reduce(const ChainDev &ch, bool chain, LeafSrc src, int64_t outer, i
                 return set_error(CHELIS_HIP_EHIP, "reduce: scratch allocation failed");
             dst_i = static_cast<int64_t *>(bi.p);
         }
-        LeafSrc s = src;
-        if (!first) {
-            s.n_in = 1;
-            s.p[0] = prev_v;
-            s.so[0] = cur_n * inner;
-            s.sn[0] = inner;
-            s.si[0] = 1;
-            s.idx = prev_i;
-        }
-        const bool use_chain = first && chain;
         if (rows) {
             const unsigned grid = grid_for(outer * groups, 4);
+#define CHELIS_ROWS_LAUNCH(KERNEL, SS, CHAIN_OK)                                                             \
+    if constexpr (kChainable<K> && (CHAIN_OK)) {                                                              \
+        if (use_chain) {                                                                                      \
+            KERNEL<T, K, SS, true><<<grid, 256, 0, st>>>(ch, s, outer, cur_n, groups, dst_v, dst_i, last);    \
+            break;                                                                                            \
+        }                                                                                                     \
+    }                                                                                                         \
+    KERNEL<T, K, SS, false><<<grid, 256, 0, st>>>(ch, s, outer, cur_n, groups, dst_v, dst_i, last);           \
+    break;
 #define CHELIS_ROWS_CASE(SS)                                                                                  \
     case SS:                                                                                                  \
-        if constexpr (kChainable<K>) {                                                                        \
-            if (use_chain) {                                                                                  \
-                reduce_rows_kernel<T, K, SS, true><<<grid, 256, 0, st>>>(ch, s, outer, cur_n, groups, dst_v, dst_i, last); \
-                break;                                                                                        \
-            }                                                                                                 \
+        if (vec) {                                                                                            \
+            CHELIS_ROWS_LAUNCH(reduce_rows_vec_kernel, SS, SS == 1)                                           \
         }                                                                                                     \
-        reduce_rows_kernel<T, K, SS, false><<<grid, 256, 0, st>>>(ch, s, outer, cur_n, groups, dst_v, dst_i, last); \
-        break;
+        CHELIS_ROWS_LAUNCH(reduce_rows_kernel, SS, true)
             switch (S) {
                 CHELIS_ROWS_CASE(1)
                 CHELIS_ROWS_CASE(2)
@@ -352,6 +491,7 @@ int32_t run_reduce(const ChainDev &ch, bool chain, LeafSrc src, int64_t outer, i
                 default: return set_error(CHELIS_HIP_EDOMAIN, "reduce: internal segment count %d", S);
             }
 #undef CHELIS_ROWS_CASE
+#undef CHELIS_ROWS_LAUNCH
         } else {
             int64_t blocks = (cells + 255) / 256;
             if (blocks > 16384) blocks = 16384;
@@ -508,8 +648,12 @@ extern "C" int32_t chelis_hip_count(const chelis_gpu_tensor *x, int32_t axis, co
     int32_t *err = nullptr;
     CHELIS_HIP_TRY(hipMallocAsync((void **)&err, sizeof(int32_t), st));
     CHELIS_HIP_TRY(hipMemsetAsync(err, 0, sizeof(int32_t), st));
-    count_kernel<<<grid_for(outer * inner, 4), 256, 0, st>>>((const uint8_t *)x->data, outer, x->shape[axis], inner,
-                                                             so, sn, si, (int64_t *)out->data, err);
+    if (inner == 1 && sn == 1 && so % 16 == 0 && (reinterpret_cast<uintptr_t>(x->data) & 15u) == 0)
+        count_rows_vec_kernel<<<grid_for(outer, 4), 256, 0, st>>>((const uint8_t *)x->data, outer, x->shape[axis], so,
+                                                                  (int64_t *)out->data, err);
+    else
+        count_kernel<<<grid_for(outer * inner, 4), 256, 0, st>>>((const uint8_t *)x->data, outer, x->shape[axis],
+                                                                 inner, so, sn, si, (int64_t *)out->data, err);
     CHELIS_LAUNCH_CHECK();
     int32_t host_err = 0;
     CHELIS_HIP_TRY(hipMemcpyAsync(&host_err, err, sizeof(int32_t), hipMemcpyDeviceToHost, st));

@@ -81,3 +81,78 @@ def test_count_rejects_non_bool_byte():
     x[2, 17] = 2
     out, err = C.count(C.to_device(x), 1)
     assert err == 1 and O.count_axis(x, 1)[1] == 1
+
+
+# Contiguous rows take the 16-byte path (reduce_rows_vec_kernel): row starts
+# aligned to 16 bytes, leaves at stride 1. The views below keep the rows
+# aligned while the row length leaves a partial vector at the end, and the
+# long rows take several passes (the later argmax passes use the scalar
+# kernel, which carries the partial indices).
+VEC_CASES = [((64, 1024), 1001), ((5, 8), 7), ((40, 4104), 4100), ((3, 300000), 300000), ((2, 70000), 69999)]
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("alloc,n", VEC_CASES)
+def test_contiguous_rows_partial_vector_and_passes(alloc, n, dtype):
+    rng = np.random.default_rng(alloc[1] + n)
+    buf = (rng.standard_normal(alloc) * 3).astype(dtype)
+    x = np.ascontiguousarray(buf[:, :n])
+    d = C.to_device(buf).view((alloc[0], n), (alloc[1], 1))
+    assert bits_equal(C.reduce("sum", d, 1).numpy(), O.sum_axis(x, 1))
+    assert bits_equal(C.reduce("max", d, 1).numpy(), O.max_axis(x, 1))
+    assert bits_equal(C.reduce("min", d, 1).numpy(), -O.max_axis(-x, 1))
+    assert np.array_equal(C.reduce("argmax", d, 1).numpy(), np.argmax(x, 1))
+    assert np.array_equal(C.reduce("argmin", d, 1).numpy(), np.argmin(x, 1))
+
+
+def test_contiguous_rows_nan_and_ties_in_vectors():
+    """First NaN / first index inside one lane's vector and across lanes."""
+    x = np.zeros((4, 1024), np.float32)
+    x[0, [5, 6, 700]] = [np.nan, 3.0, np.nan]
+    x[0, 5] = np.array([0x7FC0BEEF], np.uint32).view(np.float32)[0]
+    x[1, [2, 3, 900]] = 7.0
+    x[2, :] = -0.0
+    x[2, 513] = 0.0
+    x[3, 1023] = -np.inf
+    d = C.to_device(x)
+    assert bits_equal(C.reduce("max", d, 1).numpy(), O.max_axis(x, 1))
+    assert bits_equal(C.reduce("min", d, 1).numpy(), -O.max_axis(-x, 1))
+    assert np.array_equal(C.reduce("argmax", d, 1).numpy()[1:], np.argmax(x, 1)[1:])
+    assert C.reduce("argmax", d, 1).numpy()[0] == 5
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("alloc,n", [((256, 1000), 1000), ((64, 1024), 1001), ((4, 20000), 20000)])
+def test_sum_of_contiguous_chain_leaf(alloc, n, dtype):
+    """reduce_fused with every input contiguous: sum((x - g) * (x - g))."""
+    rng = np.random.default_rng(n)
+    xb = rng.standard_normal(alloc).astype(dtype)
+    gb = rng.standard_normal(alloc).astype(dtype)
+    x, g = xb[:, :n], gb[:, :n]
+    dx = C.to_device(xb).view((alloc[0], n), (alloc[1], 1))
+    dg = C.to_device(gb).view((alloc[0], n), (alloc[1], 1))
+    ch = C.fused_chain([("sub", 0, 1), ("mul", ("s", 0), ("s", 0))])
+    leaf = ((x - g) * (x - g)).astype(dtype)
+    assert bits_equal(C.reduce("sum", [dx, dg], 1, chain=ch).numpy(), O.sum_axis(np.ascontiguousarray(leaf), 1))
+    ch2 = C.fused_chain([("sub", 0, 1), ("exp", ("s", 0), 0)])
+    leaf2 = O.unary("exp", np.ascontiguousarray((x - g).astype(dtype)))
+    assert bits_equal(C.reduce("max", [dx, dg], 1, chain=ch2).numpy(), O.max_axis(leaf2, 1))
+
+
+@pytest.mark.parametrize("alloc,n", [((6, 4112), 4112), ((6, 4112), 4100), ((3, 16), 5)])
+def test_count_contiguous_rows(alloc, n):
+    buf = (np.random.default_rng(n).random(alloc) < 0.6).astype(np.uint8)
+    x = np.ascontiguousarray(buf[:, :n])
+    out, err = C.count(C.to_device(buf).view((alloc[0], n), (alloc[1], 1)), 1)
+    ref, rerr = O.count_axis(x, 1)
+    assert err == 0 == rerr and np.array_equal(out.numpy(), ref)
+
+
+@pytest.mark.parametrize("col", [17, 4099])
+def test_count_contiguous_rows_rejects_non_bool_byte(col):
+    """A byte other than 0/1 in the 16-byte body (col 17) or the scalar tail."""
+    buf = np.ones((4, 4112), np.uint8)
+    buf[2, col] = 0x81
+    x = np.ascontiguousarray(buf[:, :4100])
+    out, err = C.count(C.to_device(buf).view((4, 4100), (4112, 1)), 1)
+    assert err == 1 and O.count_axis(x, 1)[1] == 1
