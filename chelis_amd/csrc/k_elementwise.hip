@@ -208,6 +208,7 @@ struct UnaryArgs {
     uint64_t key;
     double p0, p1;            // dropout: rate; uniform: low, high
     const uint64_t *key_dev;  // when set, the key is read from device memory (a KEY tensor)
+    double inv_keep;          // dropout, binary32: 1 / (double)(1 - (float)rate), set by the kernel
 };
 
 template <typename T, Unary OP>
@@ -220,11 +221,14 @@ __device__ inline T unary_one(T x, T g, int64_t i, const UnaryArgs &u) {
         return T(0) < x ? g : T(0);
     } else if constexpr (OP == Unary::Dropout) {
         // [05-OP-37]: the unit at the dtype's width against the rate; a
-        // kept element is x / (1 - rate).
+        // kept element is x / (1 - rate) (binary32: through the binary64
+        // reciprocal of the divisor, quot_f32, which rounds to the IEEE
+        // quotient).
         const T rate = (T)u.p0;
         const double unit = random_unit(u.key, (uint64_t)i);
         const T uw = (T)unit;
-        return uw < rate ? T(0) : canon(x / (T(1) - rate));
+        if constexpr (sizeof(T) == 4) return uw < rate ? T(0) : canon(quot_f32(x, u.inv_keep));
+        else return uw < rate ? T(0) : canon(x / (T(1) - rate));
     } else {
         // [05-OP-8]: one fma(high - low, u, low) at the dtype.
         const T low = (T)u.p0, high = (T)u.p1;
@@ -237,6 +241,7 @@ __global__ __launch_bounds__(256) void unary_kernel(const T *__restrict__ x, con
                                                     T *__restrict__ y, int64_t n, UnaryArgs u) {
     if constexpr (OP == Unary::Dropout || OP == Unary::Uniform)
         if (u.key_dev) u.key = *u.key_dev;
+    if constexpr (OP == Unary::Dropout) u.inv_keep = 1.0 / (double)(T(1) - (T)u.p0);
     using V = Vec16<T>;
     const int64_t nv = n / V::V;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -338,8 +343,11 @@ int32_t launch_unary(const chelis_gpu_tensor *x, const chelis_gpu_tensor *g, con
     if (!n) return CHELIS_HIP_OK;
     constexpr int V = Vec16<T>::V;
     const int64_t nv = n / V;
+    // one 16-byte vector per thread up to 2^16 blocks (16 Mi vectors):
+    // enough waves that one's loads overlap another's arithmetic (the RNG
+    // maps are VALU-heavy), grid-stride beyond
     int64_t blocks = (nv + 255) / 256;
-    if (blocks > 4096) blocks = 4096;
+    if (blocks > 65536) blocks = 65536;
     if (blocks < 1) blocks = 1;
     unary_kernel<T, OP><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(
         x ? (const T *)x->data : nullptr, g ? (const T *)g->data : nullptr, (T *)y->data, n, u);

@@ -160,6 +160,26 @@ def test_dropout_and_replay_bit_exact(n):
     assert bits_equal(dx, O.dropout_replay(key, g, np.float32(0.1)))
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("rate", [0.1, 0.3, 0.7, 0.0])
+def test_dropout_quotient_special_values(rate, dtype):
+    """The kept quotient x / (1 - rate) at the edges of the format: binary32
+    subnormals (inputs and results), values that overflow to inf once
+    divided, inf, NaN (canonical on output) and signed zeros; a random bulk
+    sets the rounding of ordinary quotients."""
+    fi = np.finfo(dtype)
+    special = np.array([fi.tiny, fi.tiny / 3, -fi.tiny / 7, fi.smallest_subnormal, fi.max, -fi.max, fi.max * 0.8,
+                        np.inf, -np.inf, np.nan, 0.0, -0.0, 1.0, 3.0, -7.5], dtype)
+    rng = np.random.default_rng(17)
+    bulk = (rng.standard_normal(40000) * np.exp2(rng.integers(-140, 120, 40000).astype(np.float64))).astype(dtype)
+    x = np.concatenate([np.tile(special, 64), bulk])
+    key = 0x1234_5678_9ABC_DEF0
+    with np.errstate(all="ignore"):
+        y = C.dropout(key, C.to_device(x), rate).numpy()
+        ref = O.dropout(key, x, dtype(rate))
+    assert bits_equal(y, ref)
+
+
 def test_dropout_fixed_stream_golden():
     left, right = O.split(42)
     ones = np.ones(4, np.float32)
