@@ -194,6 +194,126 @@ __global__ __launch_bounds__(256) void fused_flat_kernel(ChainDev ch, FlatGroups
     static_cast<T *>(G.out)[i] = run_chain<T>(ch, slot);
 }
 
+// Flat maps over 16-byte vectors: each thread carries V = 16/sizeof(T)
+// consecutive elements, so a wave has V times the bytes of the scalar form
+// in flight, and each step's operation is chosen once for all V. The slots
+// are slot-major in dynamic LDS ([n_in + n_steps][256] vectors: adjacent
+// lanes read adjacent 16-byte words) and sized to the chain. Every
+// non-broadcast input and the output start 16-byte aligned; a group's last
+// partial vector is read and written element by element.
+template <typename T>
+struct Vec16F;
+template <>
+struct Vec16F<float> {
+    using type = float4;
+};
+template <>
+struct Vec16F<double> {
+    using type = double2;
+};
+
+template <typename T, int V>
+__device__ inline void apply_step_vec(uint8_t op, const T (&x)[V], const T (&y)[V], double imm, T (&r)[V]) {
+    switch (op) {
+#define CHELIS_STEP_CASE(OPC)                                                  \
+    case OPC:                                                                  \
+        _Pragma("unroll") for (int e = 0; e < V; ++e) r[e] = apply_step<T>(OPC, x[e], y[e], imm); \
+        break;
+        CHELIS_STEP_CASE(CHELIS_FUSED_ADD)
+        CHELIS_STEP_CASE(CHELIS_FUSED_SUB)
+        CHELIS_STEP_CASE(CHELIS_FUSED_MUL)
+        CHELIS_STEP_CASE(CHELIS_FUSED_DIV)
+        CHELIS_STEP_CASE(CHELIS_FUSED_MAX_ELEM)
+        CHELIS_STEP_CASE(CHELIS_FUSED_MIN_ELEM)
+        CHELIS_STEP_CASE(CHELIS_FUSED_NEG)
+        CHELIS_STEP_CASE(CHELIS_FUSED_RECIP)
+        CHELIS_STEP_CASE(CHELIS_FUSED_EXP)
+        CHELIS_STEP_CASE(CHELIS_FUSED_LOG)
+        CHELIS_STEP_CASE(CHELIS_FUSED_SQRT)
+        CHELIS_STEP_CASE(CHELIS_FUSED_TANH)
+        CHELIS_STEP_CASE(CHELIS_FUSED_ERFC)
+        CHELIS_STEP_CASE(CHELIS_FUSED_ABS)
+        CHELIS_STEP_CASE(CHELIS_FUSED_FLOOR)
+        CHELIS_STEP_CASE(CHELIS_FUSED_CEIL)
+        CHELIS_STEP_CASE(CHELIS_FUSED_ROUND)
+        CHELIS_STEP_CASE(CHELIS_FUSED_RELU)
+        CHELIS_STEP_CASE(CHELIS_FUSED_RELU_ADJOINT)
+        CHELIS_STEP_CASE(CHELIS_FUSED_CONST)
+#undef CHELIS_STEP_CASE
+        default:
+#pragma unroll
+            for (int e = 0; e < V; ++e) r[e] = T(0);
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void fused_flat_vec_kernel(ChainDev ch, FlatGroups fg) {
+    constexpr int V = 16 / sizeof(T);
+    using Q = typename Vec16F<T>::type;
+    extern __shared__ __align__(16) unsigned char flat_lds[];
+    Q *slots = reinterpret_cast<Q *>(flat_lds);
+    int gi = 0;
+#pragma unroll
+    for (int k = 1; k < kMaxGroups; ++k)
+        if (k < fg.n && (int64_t)blockIdx.x >= fg.g[k].first_block) gi = k;
+    const FlatGroup &G = fg.g[gi];
+    const int64_t i0 = (((int64_t)blockIdx.x - G.first_block) * 256 + threadIdx.x) * V;
+    if (i0 >= G.count) return;
+    const bool full = i0 + V <= G.count;
+    const int n_in = fg.n_in;
+    // every load issued before the first slot store: one memory latency
+    Q in[CHELIS_FUSED_MAX_INPUTS];
+#pragma unroll
+    for (int k = 0; k < CHELIS_FUSED_MAX_INPUTS; ++k) {
+        if (k < n_in) {
+            const T *p = static_cast<const T *>(G.in[k]);
+            T *e = reinterpret_cast<T *>(&in[k]);
+            if ((G.bcast >> k) & 1u) {
+                const T b = p[0];
+#pragma unroll
+                for (int j = 0; j < V; ++j) e[j] = b;
+            } else if (full) {
+                in[k] = *reinterpret_cast<const Q *>(p + i0);
+            } else {
+#pragma unroll
+                for (int j = 0; j < V; ++j) e[j] = i0 + j < G.count ? p[i0 + j] : T(0);
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < CHELIS_FUSED_MAX_INPUTS; ++k)
+        if (k < n_in) slots[k * 256 + threadIdx.x] = in[k];
+    T r[V];
+#pragma unroll 1
+    for (int st = 0; st < ch.n_steps; ++st) {
+        const int a0 = ch.a0[st], a1 = ch.a1[st];
+        const Q xq = slots[(a0 >= 0 ? a0 : n_in - a0 - 1) * 256 + threadIdx.x];
+        const Q yq = slots[(a1 >= 0 ? a1 : n_in - a1 - 1) * 256 + threadIdx.x];
+        T x[V], y[V];
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            x[j] = reinterpret_cast<const T *>(&xq)[j];
+            y[j] = reinterpret_cast<const T *>(&yq)[j];
+        }
+        apply_step_vec<T, V>(ch.op[st], x, y, ch.imm[st], r);
+        Q rq;
+#pragma unroll
+        for (int j = 0; j < V; ++j) reinterpret_cast<T *>(&rq)[j] = r[j];
+        slots[(n_in + st) * 256 + threadIdx.x] = rq;
+    }
+    T *out = static_cast<T *>(G.out);
+    if (full) {
+        Q rq;
+#pragma unroll
+        for (int j = 0; j < V; ++j) reinterpret_cast<T *>(&rq)[j] = r[j];
+        *reinterpret_cast<Q *>(out + i0) = rq;
+    } else {
+#pragma unroll
+        for (int j = 0; j < V; ++j)
+            if (i0 + j < G.count) out[i0 + j] = r[j];
+    }
+}
+
 // ---------------------------------------------------------------- unary maps
 // Contiguous n-element maps with 16-byte vectors; the scalar tail is the
 // last n % V elements.
@@ -496,8 +616,30 @@ int32_t prepare_group(const chelis_gpu_tensor *const *inputs, int32_t n_inputs, 
     return CHELIS_HIP_OK;
 }
 
+// The vector form when every streamed pointer is 16-byte aligned and the
+// chain's slots fit 64 KiB of LDS; the scalar interpreter otherwise.
 template <typename T>
 int32_t launch_flat(const ChainDev &ch, FlatGroups &fg, hipStream_t strm) {
+    constexpr int64_t V = 16 / sizeof(T);
+    const size_t lds = (size_t)(fg.n_in + ch.n_steps) * 256 * 16;
+    bool vec = lds <= 65536;
+    for (int32_t i = 0; vec && i < fg.n; ++i) {
+        vec = (reinterpret_cast<uintptr_t>(fg.g[i].out) & 15u) == 0;
+        for (int32_t k = 0; vec && k < fg.n_in; ++k)
+            vec = ((fg.g[i].bcast >> k) & 1u) || (reinterpret_cast<uintptr_t>(fg.g[i].in[k]) & 15u) == 0;
+    }
+    if (vec) {
+        int64_t blocks = 0;
+        for (int32_t i = 0; i < fg.n; ++i) {
+            fg.g[i].first_block = blocks;
+            blocks += (fg.g[i].count + 256 * V - 1) / (256 * V);
+        }
+        if (blocks == 0) return CHELIS_HIP_OK;
+        if (blocks > 0x7fffffffLL) return set_error(CHELIS_HIP_EUNSUPPORTED, "fused_elementwise: too many elements");
+        fused_flat_vec_kernel<T><<<(unsigned)blocks, 256, lds, strm>>>(ch, fg);
+        CHELIS_LAUNCH_CHECK();
+        return CHELIS_HIP_OK;
+    }
     int64_t blocks = 0;
     for (int32_t i = 0; i < fg.n; ++i) {
         fg.g[i].first_block = blocks;

@@ -291,3 +291,40 @@ def test_fused_chain_transposed_operand_and_ops():
     s0 = np.where(np.isnan(a) | (b <= a), a, b)
     ref = -np.floor(s0 / np.abs(b) + np.sqrt(np.abs(b)))
     assert bits_equal(out.numpy(), ref)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("n_extra_inputs", [0, 5])
+def test_fused_chain_every_op_vector_and_scalar_interpreters(dtype, n_extra_inputs):
+    """A chain over every arithmetic op: 3 inputs + 13 steps (16 slots, the
+    vector interpreter's 64 KiB LDS budget) and 8 inputs + 16 steps (24
+    slots: the scalar interpreter)."""
+    rng = np.random.default_rng(21)
+    n = 10003
+    a = rng.uniform(0.5, 2.0, n).astype(dtype)
+    b = rng.uniform(0.5, 2.0, n).astype(dtype)
+    c = np.array(1.75, dtype)
+    steps = [("add", 0, 1), ("mul", ("s", 0), 2), ("div", ("s", 1), 1), ("recip", ("s", 2)), ("sqrt", ("s", 3)),
+             ("min_elem", ("s", 4), 0), ("ceil", ("s", 0)), ("round", ("s", 1)), ("relu_adjoint", ("s", 5), ("s", 7)),
+             ("sub", ("s", 8), ("s", 6)), ("const", 0, 0, 0.25), ("mul", ("s", 9), ("s", 10)), ("neg", ("s", 11))]
+    if n_extra_inputs:
+        steps += [("abs", ("s", 12)), ("max_elem", ("s", 13), 3), ("floor", ("s", 14))]
+    extra = [rng.uniform(-1, 1, n).astype(dtype) for _ in range(n_extra_inputs)]
+    ins = [C.to_device(a), C.to_device(b), C.to_device(c).view((n,), (0,))] + [C.to_device(e) for e in extra]
+    out = C.empty((n,), dtype)
+    C.fused_elementwise(C.fused_chain(steps), ins, out)
+    s0 = a + b
+    s1 = s0 * c
+    s2 = s1 / b
+    s3 = dtype(1) / s2
+    s4 = np.sqrt(s3)
+    s5 = np.where(a < s4, a, s4)
+    s6, s7 = np.ceil(s0), np.rint(s1)
+    s8 = np.where(dtype(0) < s5, s7, dtype(0))
+    s12 = -((s8 - s6) * dtype(0.25))
+    ref = s12
+    if n_extra_inputs:
+        s13 = np.abs(s12)
+        s14 = np.where(extra[0] > s13, extra[0], s13)
+        ref = np.floor(s14)
+    assert bits_equal(out.numpy(), ref.astype(dtype))
