@@ -202,51 +202,6 @@ __global__ __launch_bounds__(256) void fused_flat_kernel(ChainDev ch, FlatGroups
 // non-broadcast input and the output start 16-byte aligned; a group's last
 // partial vector is read and written element by element.
 template <typename T>
-struct Vec16F;
-template <>
-struct Vec16F<float> {
-    using type = float4;
-};
-template <>
-struct Vec16F<double> {
-    using type = double2;
-};
-
-template <typename T, int V>
-__device__ inline void apply_step_vec(uint8_t op, const T (&x)[V], const T (&y)[V], double imm, T (&r)[V]) {
-    switch (op) {
-#define CHELIS_STEP_CASE(OPC)                                                  \
-    case OPC:                                                                  \
-        _Pragma("unroll") for (int e = 0; e < V; ++e) r[e] = apply_step<T>(OPC, x[e], y[e], imm); \
-        break;
-        CHELIS_STEP_CASE(CHELIS_FUSED_ADD)
-        CHELIS_STEP_CASE(CHELIS_FUSED_SUB)
-        CHELIS_STEP_CASE(CHELIS_FUSED_MUL)
-        CHELIS_STEP_CASE(CHELIS_FUSED_DIV)
-        CHELIS_STEP_CASE(CHELIS_FUSED_MAX_ELEM)
-        CHELIS_STEP_CASE(CHELIS_FUSED_MIN_ELEM)
-        CHELIS_STEP_CASE(CHELIS_FUSED_NEG)
-        CHELIS_STEP_CASE(CHELIS_FUSED_RECIP)
-        CHELIS_STEP_CASE(CHELIS_FUSED_EXP)
-        CHELIS_STEP_CASE(CHELIS_FUSED_LOG)
-        CHELIS_STEP_CASE(CHELIS_FUSED_SQRT)
-        CHELIS_STEP_CASE(CHELIS_FUSED_TANH)
-        CHELIS_STEP_CASE(CHELIS_FUSED_ERFC)
-        CHELIS_STEP_CASE(CHELIS_FUSED_ABS)
-        CHELIS_STEP_CASE(CHELIS_FUSED_FLOOR)
-        CHELIS_STEP_CASE(CHELIS_FUSED_CEIL)
-        CHELIS_STEP_CASE(CHELIS_FUSED_ROUND)
-        CHELIS_STEP_CASE(CHELIS_FUSED_RELU)
-        CHELIS_STEP_CASE(CHELIS_FUSED_RELU_ADJOINT)
-        CHELIS_STEP_CASE(CHELIS_FUSED_CONST)
-#undef CHELIS_STEP_CASE
-        default:
-#pragma unroll
-            for (int e = 0; e < V; ++e) r[e] = T(0);
-    }
-}
-
-template <typename T>
 __global__ __launch_bounds__(256) void fused_flat_vec_kernel(ChainDev ch, FlatGroups fg) {
     constexpr int V = 16 / sizeof(T);
     using Q = typename Vec16F<T>::type;
@@ -284,23 +239,7 @@ __global__ __launch_bounds__(256) void fused_flat_vec_kernel(ChainDev ch, FlatGr
     for (int k = 0; k < CHELIS_FUSED_MAX_INPUTS; ++k)
         if (k < n_in) slots[k * 256 + threadIdx.x] = in[k];
     T r[V];
-#pragma unroll 1
-    for (int st = 0; st < ch.n_steps; ++st) {
-        const int a0 = ch.a0[st], a1 = ch.a1[st];
-        const Q xq = slots[(a0 >= 0 ? a0 : n_in - a0 - 1) * 256 + threadIdx.x];
-        const Q yq = slots[(a1 >= 0 ? a1 : n_in - a1 - 1) * 256 + threadIdx.x];
-        T x[V], y[V];
-#pragma unroll
-        for (int j = 0; j < V; ++j) {
-            x[j] = reinterpret_cast<const T *>(&xq)[j];
-            y[j] = reinterpret_cast<const T *>(&yq)[j];
-        }
-        apply_step_vec<T, V>(ch.op[st], x, y, ch.imm[st], r);
-        Q rq;
-#pragma unroll
-        for (int j = 0; j < V; ++j) reinterpret_cast<T *>(&rq)[j] = r[j];
-        slots[(n_in + st) * 256 + threadIdx.x] = rq;
-    }
+    run_chain_vec<T, V>(ch, slots, n_in, threadIdx.x, r);
     T *out = static_cast<T *>(G.out);
     if (full) {
         Q rq;

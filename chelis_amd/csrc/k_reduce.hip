@@ -176,26 +176,17 @@ __global__ __launch_bounds__(256) void reduce_rows_kernel(ChainDev ch, LeafSrc s
 // Contiguous rows: leaf i of row o of input k at p[k] + o*so[k] + i, each
 // row start 16-byte aligned. Leaf indices are positions (a first pass, or a
 // later pass of a value-only reduction).
-template <typename T>
-struct Vec16Of;
-template <>
-struct Vec16Of<float> {
-    using type = float4;
-};
-template <>
-struct Vec16Of<double> {
-    using type = double2;
-};
-
 template <typename T, Rk K, int S, bool CHAIN>
 __global__ __launch_bounds__(256) void reduce_rows_vec_kernel(ChainDev ch, LeafSrc src, int64_t outer, int64_t n,
                                                               int64_t groups, T *__restrict__ out_v,
                                                               int64_t *__restrict__ out_i, bool last) {
     constexpr int V = 16 / sizeof(T);
     constexpr int G = 64 * V * S;
-    using Q = typename Vec16Of<T>::type;
-    __shared__ T slots[CHAIN ? 256 * kSlotStride : 1];
-    T *slot = slots + (CHAIN ? threadIdx.x * kSlotStride : 0);
+    using Q = typename Vec16F<T>::type;
+    // a chain leaf runs on the vector interpreter (run_chain_vec): its
+    // slots are this launch's dynamic LDS
+    extern __shared__ __align__(16) unsigned char red_lds[];
+    Q *qs = reinterpret_cast<Q *>(red_lds);
     const int lane = threadIdx.x & 63;
     const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (item >= outer * groups) return;
@@ -225,24 +216,26 @@ __global__ __launch_bounds__(256) void reduce_rows_vec_kernel(ChainDev ch, LeafS
         const int64_t i0 = g * G + (int64_t)s * 64 * V + (int64_t)lane * V;
         T(&cur)[V] = v[CHAIN ? 0 : s];
         if constexpr (CHAIN) {
-            if (i0 + V <= n) {
-                Q in[CHELIS_FUSED_MAX_INPUTS];
+            Q in[CHELIS_FUSED_MAX_INPUTS];
 #pragma unroll
-                for (int k = 0; k < CHELIS_FUSED_MAX_INPUTS; ++k)
-                    if (k < src.n_in)
-                        in[k] = *reinterpret_cast<const Q *>(static_cast<const T *>(src.p[k]) + o * src.so[k] + i0);
+            for (int k = 0; k < CHELIS_FUSED_MAX_INPUTS; ++k) {
+                if (k < src.n_in) {
+                    const T *p = static_cast<const T *>(src.p[k]) + o * src.so[k];
+                    if (i0 + V <= n) {
+                        in[k] = *reinterpret_cast<const Q *>(p + i0);
+                    } else {
 #pragma unroll
-                for (int e = 0; e < V; ++e) {
-#pragma unroll
-                    for (int k = 0; k < CHELIS_FUSED_MAX_INPUTS; ++k)
-                        if (k < src.n_in) slot[k] = reinterpret_cast<const T *>(&in[k])[e];
-                    cur[e] = run_chain<T>(ch, slot);
+                        for (int e = 0; e < V; ++e) reinterpret_cast<T *>(&in[k])[e] = i0 + e < n ? p[i0 + e] : T(0);
+                    }
                 }
-            } else {
-#pragma unroll
-                for (int e = 0; e < V; ++e)
-                    cur[e] = i0 + e < n ? leaf<T, true>(ch, src, slot, o, i0 + e, 0) : identity<T, K>();
             }
+#pragma unroll
+            for (int k = 0; k < CHELIS_FUSED_MAX_INPUTS; ++k)
+                if (k < src.n_in) qs[k * 256 + threadIdx.x] = in[k];
+            T r[V];
+            run_chain_vec<T, V>(ch, qs, src.n_in, threadIdx.x, r);
+#pragma unroll
+            for (int e = 0; e < V; ++e) cur[e] = i0 + e < n ? r[e] : identity<T, K>();
         }
         int64_t vi[V];
 #pragma unroll
@@ -430,6 +423,8 @@ int32_t run_reduce(const ChainDev &ch, bool chain, LeafSrc src, int64_t outer, i
         for (int32_t k = 0; vec && k < s.n_in; ++k)
             vec = s.sn[k] == 1 && (reinterpret_cast<uintptr_t>(s.p[k]) & 15u) == 0 &&
                   (s.so[k] * (int64_t)sizeof(T)) % 16 == 0;
+        const size_t chain_lds = (size_t)(s.n_in + ch.n_steps) * 256 * 16;
+        if (use_chain && chain_lds > 65536) vec = false;
         const int64_t unit = vec ? 64 * (16 / (int64_t)sizeof(T)) : 64;
         // a contiguous chain leaf runs one segment per wave: the interpreter
         // is inlined once per element a lane holds
@@ -467,10 +462,10 @@ int32_t run_reduce(const ChainDev &ch, bool chain, LeafSrc src, int64_t outer, i
         }
         if (rows) {
             const unsigned grid = grid_for(outer * groups, 4);
-#define CHELIS_ROWS_LAUNCH(KERNEL, SS, CHAIN_OK)                                                             \
+#define CHELIS_ROWS_LAUNCH(KERNEL, SS, CHAIN_OK, LDS)                                                        \
     if constexpr (kChainable<K> && (CHAIN_OK)) {                                                              \
         if (use_chain) {                                                                                      \
-            KERNEL<T, K, SS, true><<<grid, 256, 0, st>>>(ch, s, outer, cur_n, groups, dst_v, dst_i, last);    \
+            KERNEL<T, K, SS, true><<<grid, 256, LDS, st>>>(ch, s, outer, cur_n, groups, dst_v, dst_i, last);  \
             break;                                                                                            \
         }                                                                                                     \
     }                                                                                                         \
@@ -479,9 +474,9 @@ int32_t run_reduce(const ChainDev &ch, bool chain, LeafSrc src, int64_t outer, i
 #define CHELIS_ROWS_CASE(SS)                                                                                  \
     case SS:                                                                                                  \
         if (vec) {                                                                                            \
-            CHELIS_ROWS_LAUNCH(reduce_rows_vec_kernel, SS, SS == 1)                                           \
+            CHELIS_ROWS_LAUNCH(reduce_rows_vec_kernel, SS, SS == 1, chain_lds)                                \
         }                                                                                                     \
-        CHELIS_ROWS_LAUNCH(reduce_rows_kernel, SS, true)
+        CHELIS_ROWS_LAUNCH(reduce_rows_kernel, SS, true, 0)
             switch (S) {
                 CHELIS_ROWS_CASE(1)
                 CHELIS_ROWS_CASE(2)
