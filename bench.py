@@ -185,6 +185,63 @@ def bench_programs(C, H, steps, warmup):
     return out, (X, w, y), (x, p), args
 
 
+# ---------------------------------------------------------------- bandwidth families
+def bench_bandwidth(C, H, steps, warmup):
+    """The memory-bound region families at HBM-sized shapes (the config
+    programs hold them only at launch-bound sizes): GB/s of algorithmic bytes
+    (every operand read once, every result written once) against the 8 TB/s
+    peak. Three buffer sets of 256 MiB rotate, so the 256 MB Infinity Cache
+    cannot hold the working set."""
+    out = {}
+    rng = np.random.default_rng(50)
+    R, N = 16384, 4096
+    x = rng.standard_normal((R, N)).astype(np.float32)
+    nb = x.nbytes
+    X = [C.to_device(x) for _ in range(3)]
+    G = [C.to_device(x) for _ in range(3)]
+    Y = [C.empty(x.shape, np.float32) for _ in range(3)]
+
+    def line(name, launch, nbytes, bound="hbm"):
+        ms = time_launches(C, H, launch, steps, warmup)
+        gbps = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"us": round(ms * 1e3, 2), "GB/s": round(gbps, 1), "frac_hbm": round(gbps / HBM_PEAK_GBPS, 4),
+                     "bytes": nbytes, "bound": bound}
+
+    line("relu_f32_16384x4096", lambda i: C.relu(X[i % 3], Y[i % 3]), 2 * nb)
+    line("relu_adjoint_f32_16384x4096", lambda i: C.relu_adjoint(X[i % 3], G[i % 3], Y[i % 3]), 3 * nb)
+    line("dropout_f32_16384x4096", lambda i: C.dropout(44, X[i % 3], 0.1, Y[i % 3]), 2 * nb,
+         "VALU (splitmix64 64-bit multiplies per element)")
+    line("gelu_f32_16384x4096", lambda i: C.gelu(X[i % 3], Y[i % 3]), 2 * nb,
+         "VALU (correctly rounded exp and erfc leaves)")
+    sq = C.fused_chain([("sub", 0, 1), ("mul", ("s", 0), ("s", 0))])
+    line("fused_chain_sqdiff_f32_16384x4096", lambda i: C.fused_elementwise(sq, [X[i % 3], G[i % 3]], Y[i % 3]),
+         3 * nb)
+    S1 = [C.empty((R,), np.float32) for _ in range(3)]
+    line("reduce_sum_rows_f32_16384x4096", lambda i: C.reduce("sum", X[i % 3], 1, S1[i % 3]), nb + R * 4)
+    line("reduce_max_rows_f32_16384x4096", lambda i: C.reduce("max", X[i % 3], 1, S1[i % 3]), nb + R * 4)
+    line("reduce_sum_sqdiff_rows_f32_16384x4096",
+         lambda i: C.reduce("sum", [X[i % 3], G[i % 3]], 1, S1[i % 3], chain=sq), 2 * nb + R * 4)
+    S0 = [C.empty((N,), np.float32) for _ in range(3)]
+    line("reduce_sum_cols_f32_16384x4096", lambda i: C.reduce("sum", X[i % 3], 0, S0[i % 3]), nb + N * 4)
+    del X, G, Y
+    b = rng.random((R, N)) < 0.9
+    B = [C.to_device(b) for _ in range(3)]
+    I1 = [C.empty((R,), np.int64) for _ in range(3)]
+    line("count_bool_rows_16384x4096", lambda i: C.count(B[i % 3], 1, I1[i % 3]), b.nbytes + R * 8,
+         "host round trip (the call returns the error code synchronously)")
+    del B
+    xs = rng.standard_normal((65536, 1024)).astype(np.float32)
+    XS = [C.to_device(xs) for _ in range(3)]
+    YS = [C.empty(xs.shape, np.float32) for _ in range(3)]
+    gam, bet = C.to_device(np.ones(1024, np.float32)), C.to_device(np.zeros(1024, np.float32))
+    line("layer_norm_f32_65536x1024", lambda i: C.layer_norm(XS[i % 3], gam, bet, 1e-5, YS[i % 3]), 2 * xs.nbytes)
+    line("softmax_f32_65536x1024", lambda i: C.softmax(XS[i % 3], YS[i % 3]), 2 * xs.nbytes)
+    sm = C.softmax(XS[0])
+    line("softmax_adjoint_f32_65536x1024", lambda i: C.softmax_adjoint(sm, XS[(i + 1) % 3], YS[i % 3]),
+         3 * xs.nbytes)
+    return out
+
+
 # ---------------------------------------------------------------- traffic
 def traffic_child():
     """Runs under rocprofv3 --pmc: 10 headline softmax launches and 10
@@ -355,6 +412,7 @@ def main(argv=None) -> int:
         kernels["gemm_bf16_4096^3"] = gemm_line(r, "bf16", "mfma")
         progs, lin, tr, mlp = bench_programs(C, H, max(5, args.steps // 2), args.warmup)
         kernels.update(progs)
+        kernels.update(bench_bandwidth(C, H, max(5, args.steps // 2), args.warmup))
         extra = (x64, lin, tr, mlp, gin)
     traffic, tdetail = (None, "skipped") if args.no_traffic else measure_traffic()
     cpu = None

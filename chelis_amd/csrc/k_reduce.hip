@@ -209,6 +209,27 @@ __global__ __launch_bounds__(256) void reduce_rows_vec_kernel(ChainDev ch, LeafS
             }
         }
     }
+    if constexpr (!CHAIN && (K == Rk::Max || K == Rk::Min)) {
+        // Plain v_max (of the negated leaves for min) gives the [05-OP-12]
+        // bits whenever the group holds no NaN and its extremum is not a
+        // zero: a nonzero non-NaN value has one representation. Otherwise
+        // the ordered combine below runs on the same registers.
+        constexpr T sgn = K == Rk::Max ? T(1) : T(-1);
+        T m = sgn * v[0][0];
+        bool nan = false;
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+                m = vmax(m, sgn * v[s][e]);
+                nan |= v[s][e] != v[s][e];
+            }
+        m = wave_vmax(m);
+        if (!__any(nan) && m != T(0)) {
+            if (lane == 0) out_v[item] = sgn * m;
+            return;
+        }
+    }
     T seg[S];
     int64_t sidx[S];
 #pragma unroll
