@@ -306,6 +306,58 @@ __global__ __launch_bounds__(256) void reduce_cols_kernel(ChainDev ch, LeafSrc s
     }
 }
 
+// Columns with inner >= 64, four waves per block on the same 64 columns:
+// wave w reduces leaf group 4*gb + w (32 leaves, as reduce_cols_kernel
+// does) and the four group totals join in LDS in order, so one block writes
+// the total of an aligned 128-leaf group: fewer passes and partials.
+template <typename T, Rk K, bool CHAIN>
+__global__ __launch_bounds__(256) void reduce_cols4_kernel(ChainDev ch, LeafSrc src, int64_t outer, int64_t n,
+                                                           int64_t inner, int64_t groups, T *__restrict__ out_v,
+                                                           int64_t *__restrict__ out_i, bool last) {
+    constexpr int G = 32;
+    __shared__ T pv[4][64];
+    __shared__ int64_t pi[has_index(K) ? 4 : 1][64];
+    __shared__ T slots[CHAIN ? 256 * kSlotStride : 1];
+    T *slot = slots + (CHAIN ? threadIdx.x * kSlotStride : 0);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t jblocks = (inner + 63) / 64;
+    int64_t b = blockIdx.x;
+    const int64_t jb = b % jblocks;
+    b /= jblocks;
+    const int64_t gb = b % groups, o = b / groups;
+    const int64_t j = jb * 64 + lane;
+    const bool jok = j < inner;
+    T v[G];
+    int64_t vi[G];
+#pragma unroll
+    for (int q = 0; q < G; ++q) {
+        const int64_t i = (gb * 4 + w) * G + q;
+        v[q] = identity<T, K>();
+        vi[q] = i;
+        if (jok && i < n) {
+            v[q] = leaf<T, CHAIN>(ch, src, slot, o, i, j);
+            if (has_index(K) && src.idx) vi[q] = src.idx[(o * n + i) * inner + j];
+        }
+    }
+    ordered_tree<T, K, G>(v, vi);
+    pv[w][lane] = v[0];
+    if constexpr (has_index(K)) pi[w][lane] = vi[0];
+    __syncthreads();
+    if (w == 0 && jok) {
+        T a[4];
+        int64_t ia[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            a[k] = pv[k][lane];
+            ia[k] = has_index(K) ? pi[k][lane] : 0;
+        }
+        ordered_tree<T, K, 4>(a, ia);
+        const int64_t t = (o * groups + gb) * inner + j;
+        out_v[t] = last ? finalize<T, K>(a[0]) : a[0];
+        if (has_index(K)) out_i[t] = ia[0];
+    }
+}
+
 template <typename T>
 __global__ void fill_kernel(T *p, int64_t n, T v) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -458,7 +510,10 @@ int32_t run_reduce(const ChainDev &ch, bool chain, LeafSrc src, int64_t outer, i
                 while (S < smax && outer * ((cur_n + 2 * unit * S - 1) / (2 * unit * S)) >= 1024) S <<= 1;
             }
         }
-        const int64_t G = rows ? unit * S : 32;
+        // columns: 128-leaf groups per block when 64 columns fill a wave
+        const bool cols4 = !rows && inner >= 64 &&
+                           outer * ((cur_n + 127) / 128) * ((inner + 63) / 64) <= 0x7fffffffLL;
+        const int64_t G = rows ? unit * S : (cols4 ? 128 : 32);
         const int64_t groups = (cur_n + G - 1) / G;
         const bool last = groups == 1;
         T *dst_v;
@@ -508,6 +563,19 @@ int32_t run_reduce(const ChainDev &ch, bool chain, LeafSrc src, int64_t outer, i
             }
 #undef CHELIS_ROWS_CASE
 #undef CHELIS_ROWS_LAUNCH
+        } else if (cols4) {
+            const unsigned grid = (unsigned)(outer * groups * ((inner + 63) / 64));
+            bool done = false;
+            if constexpr (kChainable<K>) {
+                if (use_chain) {
+                    reduce_cols4_kernel<T, K, true><<<grid, 256, 0, st>>>(ch, s, outer, cur_n, inner, groups, dst_v,
+                                                                          dst_i, last);
+                    done = true;
+                }
+            }
+            if (!done)
+                reduce_cols4_kernel<T, K, false><<<grid, 256, 0, st>>>(ch, s, outer, cur_n, inner, groups, dst_v, dst_i,
+                                                                       last);
         } else {
             int64_t blocks = (cells + 255) / 256;
             if (blocks > 16384) blocks = 16384;

@@ -156,3 +156,30 @@ def test_count_contiguous_rows_rejects_non_bool_byte(col):
     x = np.ascontiguousarray(buf[:, :4100])
     out, err = C.count(C.to_device(buf).view((4, 4100), (4112, 1)), 1)
     assert err == 1 and O.count_axis(x, 1)[1] == 1
+
+
+# Columns with at least 64 of them take reduce_cols4_kernel: 128-leaf groups
+# per block (four 32-leaf wave groups joined in order). Column counts that
+# leave a partial 64-column block, several passes, indices carried through
+# the passes.
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("shape,axis", [((20000, 100), 0), ((3, 300, 70), 1), ((129, 64), 0), ((5, 4096), 0)])
+def test_column_blocks_bit_exact(shape, axis, dtype):
+    rng = np.random.default_rng(sum(shape))
+    x = (rng.standard_normal(shape) * 3).astype(dtype)
+    x.flat[::97] = x.flat[1::97]  # repeated values: first-index ties
+    d = C.to_device(x)
+    assert bits_equal(C.reduce("sum", d, axis).numpy(), O.sum_axis(x, axis))
+    assert bits_equal(C.reduce("max", d, axis).numpy(), O.max_axis(x, axis))
+    assert bits_equal(C.reduce("min", d, axis).numpy(), -O.max_axis(-x, axis))
+    assert np.array_equal(C.reduce("argmax", d, axis).numpy(), np.argmax(x, axis))
+    assert np.array_equal(C.reduce("argmin", d, axis).numpy(), np.argmin(x, axis))
+
+
+def test_column_blocks_chain_leaf():
+    rng = np.random.default_rng(31)
+    x = rng.standard_normal((1000, 96)).astype(np.float32)
+    g = rng.standard_normal((1000, 96)).astype(np.float32)
+    ch = C.fused_chain([("sub", 0, 1), ("mul", ("s", 0), ("s", 0))])
+    out = C.reduce("sum", [C.to_device(x), C.to_device(g)], 0, chain=ch).numpy()
+    assert bits_equal(out, O.sum_axis(((x - g) * (x - g)).astype(np.float32), 0))
