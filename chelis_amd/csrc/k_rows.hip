@@ -444,7 +444,10 @@ __global__ __launch_bounds__(64 * W * R) void softmax_kernel(const T *__restrict
     const T *xr = x + c.row * ldx;
     const typename RowExpTab<T>::type tab(c.lane);
     T v[S][V];
-    load_row<T, V, S, W>(xr, n, vec_ok, c.tid_in_row, neg_inf<T>(), v);
+    // causal rows read only j <= qi: the mask turns every later element into
+    // -inf whatever it holds, which is the padding value
+    const int64_t n_load = masked == 1 ? (c.row % q_len + 1 < n ? c.row % q_len + 1 : n) : n;
+    load_row<T, V, S, W>(xr, n_load, vec_ok, c.tid_in_row, neg_inf<T>(), v);
     softmax_row<T, V, S, W, R>(v, xr, c.row, n, masked, scale, q_len, lds, c, tab);
     store_row<T, V, S, W>(y + c.row * ldy, n, vec_ok, c.tid_in_row, v);
 }

@@ -118,6 +118,21 @@ def test_scaled_masked_softmax(causal):
     assert bits_equal(y, ref), mismatch_report(y, ref)
 
 
+@pytest.mark.parametrize("dtype,s", [(np.float32, 512), (np.float64, 512), (np.float32, 100), (np.float64, 37)])
+def test_causal_softmax_ignores_the_masked_triangle(dtype, s):
+    """Causal rows read only j <= i: NaN and inf planted above the diagonal
+    (where the scores product leaves memory unwritten) change nothing."""
+    rng = np.random.default_rng(s)
+    x = rng.standard_normal((2, 2, s, s)).astype(dtype)
+    upper = np.triu(np.ones((s, s), bool), 1)
+    junk = x.copy()
+    junk[..., upper] = np.where(rng.random(upper.sum()) < 0.5, np.nan, np.inf).astype(dtype)
+    y = C.scaled_masked_softmax(C.to_device(junk), 0.125, True).numpy()
+    sc = np.where(~upper, x * dtype(0.125), dtype(-np.inf)).astype(dtype)
+    ref = O.softmax_rows(sc.reshape(-1, s)).reshape(x.shape)
+    assert bits_equal(y, ref), mismatch_report(y, ref)
+
+
 @pytest.mark.parametrize("dtype,n", [(np.float32, 10), (np.float32, 1024), (np.float64, 777)])
 def test_softmax_adjoint(dtype, n):
     rng = np.random.default_rng(6)
