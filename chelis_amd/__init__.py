@@ -200,24 +200,67 @@ class DeviceTensor:
 
 
 class View:
+    """A strided view of a device tensor's storage, made the way the
+    reference's Python loader hands a foreign tensor to a compiled entry
+    (crates/chelis-python/src/native_tensor.rs:210-240): a borrowed packet
+    imported through chelis_device_tensor_import. The view's owner borrows
+    the base storage and is released with the View."""
+
     def __init__(self, base: DeviceTensor, shape, strides, offset: int = 0):
         self.base = base
         self.shape = tuple(int(s) for s in shape)
         self.strides = tuple(int(s) for s in strides)
         self.dtype = base.dtype
-        self._shape = (c_int64 * max(1, len(self.shape)))(*self.shape)
-        self._strides = (c_int64 * max(1, len(self.strides)))(*self.strides)
         bp = base.packet.contents
-        g = GpuTensor()
-        g.data = (bp.data or 0) + offset * self.dtype.itemsize
-        g.shape = ctypes.cast(self._shape, POINTER(c_int64))
-        g.strides = ctypes.cast(self._strides, POINTER(c_int64))
-        g.count = int(np.prod(self.shape, dtype=np.int64))
-        g.byte_capacity = bp.byte_capacity - offset * self.dtype.itemsize
-        g.rank = len(self.shape)
-        g.dtype = bp.dtype
-        self._g = g
-        self.packet = ctypes.pointer(g)
+        self.owner = import_packet(self.shape, self.strides, (bp.data or 0) + offset * self.dtype.itemsize,
+                                   bp.byte_capacity - offset * self.dtype.itemsize, bp.dtype)
+        self.packet = lib().chelis_device_tensor_view(self.owner)
+
+    def numpy(self) -> np.ndarray:
+        return to_host(self)
+
+    def __del__(self):
+        try:
+            if self.owner:
+                lib().chelis_device_tensor_release(self.owner)
+                self.owner = None
+        except Exception:
+            pass
+
+
+def make_packet(shape, strides, data: int, byte_capacity: int, dtype_tag: int, ownership: int = 0):
+    """A chelis_gpu_tensor over caller memory; returns (packet, keep-alive)."""
+    shape = tuple(int(s) for s in shape)
+    sh = (c_int64 * max(1, len(shape)))(*shape)
+    st = (c_int64 * max(1, len(strides)))(*[int(s) for s in strides])
+    g = GpuTensor()
+    g.data = data or None
+    g.shape = ctypes.cast(sh, POINTER(c_int64))
+    g.strides = ctypes.cast(st, POINTER(c_int64))
+    g.count = int(np.prod(shape, dtype=np.int64))
+    g.byte_capacity = int(byte_capacity)
+    g.rank = len(shape)
+    g.dtype = dtype_tag
+    g.ownership = ownership
+    return g, (sh, st)
+
+
+def import_packet(shape, strides, data: int, byte_capacity: int, dtype_tag: int) -> int:
+    """chelis_device_tensor_import of a borrowed packet: a new owner handle."""
+    g, keep = make_packet(shape, strides, data, byte_capacity, dtype_tag)
+    owner = lib().chelis_device_tensor_import(ctypes.byref(g))
+    del keep
+    return owner
+
+
+def borrow(shape, dtype, data: int, byte_capacity: int) -> "DeviceTensor":
+    """chelis_device_tensor_borrow: a row-major owner over caller storage."""
+    return DeviceTensor(lib().chelis_device_tensor_borrow(_plan(shape, dtype), data, i64(byte_capacity)))
+
+
+def clone(t) -> "DeviceTensor":
+    """chelis_device_tensor_clone: an owned dense copy of a tensor or view."""
+    return DeviceTensor(lib().chelis_device_tensor_clone(t.owner))
 
 
 def _plan(shape, dtype, tag=None) -> int:
@@ -246,10 +289,8 @@ def to_device(a: np.ndarray) -> DeviceTensor:
 
 
 def to_host(t) -> np.ndarray:
-    """chelis_device_tensor_copy_to_host into a fresh host tensor."""
-    base = t if isinstance(t, DeviceTensor) else None
-    if base is None:
-        raise TypeError("to_host takes a DeviceTensor (clone a View first)")
+    """chelis_device_tensor_copy_to_host of a DeviceTensor or a View (a
+    strided view is gathered on the device first) into a fresh array."""
     out = np.empty(t.shape, t.dtype)
     shape = (c_int64 * max(1, out.ndim))(*out.shape)
     host = lib().chelis_tensor_entry_borrow(out.ndim, shape, _NP2DT[out.dtype], out.ctypes.data, out.nbytes)

@@ -161,7 +161,7 @@ __device__ inline T apply_step(uint8_t op, T a, T b, double imm) {
         case CHELIS_FUSED_RECIP: return canon(T(1) / a);
         case CHELIS_FUSED_EXP: return chain_exp<T>(a);
         case CHELIS_FUSED_LOG: return chain_log<T>(a);
-        case CHELIS_FUSED_SQRT: return canon(sqrt(a));
+        case CHELIS_FUSED_SQRT: return canon_bits(sqrt(a));
         case CHELIS_FUSED_TANH: return chain_tanh<T>(a);
         case CHELIS_FUSED_ERFC: return chain_erfc<T>(a);
         case CHELIS_FUSED_ABS: return canon(fabs(a));

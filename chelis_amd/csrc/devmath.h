@@ -50,6 +50,16 @@ CHELIS_HD inline double f64_from(uint64_t b) {
 // quiet NaN of its dtype, whatever payload the hardware produced.
 CHELIS_HD inline float canon(float v) { return v != v ? f32_from(0x7fc00000u) : v; }
 CHELIS_HD inline double canon(double v) { return v != v ? f64_from(0x7ff8000000000000ull) : v; }
+// The same rule decided on the stored bits, for results the compiler treats
+// as never NaN: after the device sqrt it folds `v != v` to false, so canon()
+// would let the hardware's NaN (sign set, or the operand's payload) through.
+// An integer test on the bits cannot be folded that way.
+CHELIS_HD inline float canon_bits(float v) {
+    return (f32_bits(v) & 0x7fffffffu) > 0x7f800000u ? f32_from(0x7fc00000u) : v;
+}
+CHELIS_HD inline double canon_bits(double v) {
+    return (f64_bits(v) & 0x7fffffffffffffffull) > 0x7ff0000000000000ull ? f64_from(0x7ff8000000000000ull) : v;
+}
 
 // Round the positive unevaluated sum s + e (|e| <= half an ulp of s) to
 // binary32, nearest-even. (float)s is already the answer unless s lies

@@ -68,11 +68,6 @@ struct RowView {
 };
 bool row_view(const chelis_gpu_tensor *t, RowView *v);
 
-// dst (contiguous, count elements of `width` bytes) = src viewed through
-// shape/strides; enqueued on `st`.
-int32_t gather_contiguous(const void *src, void *dst, int32_t rank, const int64_t *shape, const int64_t *strides,
-                          int64_t width, int64_t count, hipStream_t st);
-
 // Keyed dropout (and, applied to a cotangent, its replay) with the key read
 // on the device from key_dev, the storage of a KEY tensor: no host round trip.
 int32_t dropout_device_key(const uint64_t *key_dev, const chelis_gpu_tensor *x, double rate,

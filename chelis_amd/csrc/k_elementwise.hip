@@ -1,6 +1,5 @@
 // Elementwise regions on gfx950: the FusedElem chain interpreter, GELU,
-// ReLU and its adjoint, keyed dropout / replay / uniform_like, and the
-// strided gather used by the device owner.
+// ReLU and its adjoint, keyed dropout / replay / uniform_like.
 //
 // Bandwidth design: the unary maps (GELU, ReLU, dropout, uniform) move
 // contiguous operands in 16-byte vectors (one float4 / double2 per lane per
@@ -324,24 +323,6 @@ __global__ __launch_bounds__(256) void unary_kernel(const T *__restrict__ x, con
     }
 }
 
-// ---------------------------------------------------------------- gather
-template <typename W>
-__global__ __launch_bounds__(256) void gather_kernel(const W *__restrict__ src, W *__restrict__ dst, Shape sh,
-                                                     Operand so, int64_t count) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < count; idx += stride) {
-        int64_t rem = idx, off = 0;
-#pragma unroll
-        for (int a = kMaxRank - 1; a >= 0; --a) {
-            if (a < sh.rank) {
-                off += (rem % sh.ext[a]) * so.st[a];
-                rem /= sh.ext[a];
-            }
-        }
-        dst[idx] = src[off];
-    }
-}
-
 // ---------------------------------------------------------------- host helpers
 // Collapse adjacent output axes wherever every operand's strides allow it
 // (stride[a] == stride[a+1] * ext[a+1]), dropping unit axes.
@@ -471,39 +452,6 @@ int32_t check_rate(double rate, chelis_dtype dt) {
 }
 
 }  // namespace
-
-// Used by the device owner: dst (contiguous) = src viewed with `shape`/`strides`.
-int32_t gather_contiguous(const void *src, void *dst, int32_t rank, const int64_t *shape, const int64_t *strides,
-                          int64_t width, int64_t count, hipStream_t st) {
-    if (!count) return CHELIS_HIP_OK;
-    chelis_gpu_tensor out{}, in{};
-    int64_t cst[8];
-    int64_t acc = 1;
-    for (int32_t a = rank; a-- > 0;) {
-        cst[a] = acc;
-        acc *= shape[a];
-    }
-    out.rank = in.rank = rank;
-    out.shape = in.shape = shape;
-    out.strides = cst;
-    in.strides = strides;
-    const chelis_gpu_tensor *ins[1] = {&in};
-    Shape sh;
-    int64_t st1[1][kMaxRank];
-    if (!collapse(&out, ins, 1, &sh, st1)) return set_error(CHELIS_HIP_EUNSUPPORTED, "gather: view rank > 4 after collapse");
-    Operand so{src, {st1[0][0], st1[0][1], st1[0][2], st1[0][3]}};
-    int64_t blocks = (count + 255) / 256;
-    if (blocks > 8192) blocks = 8192;
-    switch (width) {
-        case 1: gather_kernel<uint8_t><<<(unsigned)blocks, 256, 0, st>>>((const uint8_t *)src, (uint8_t *)dst, sh, so, count); break;
-        case 2: gather_kernel<uint16_t><<<(unsigned)blocks, 256, 0, st>>>((const uint16_t *)src, (uint16_t *)dst, sh, so, count); break;
-        case 4: gather_kernel<uint32_t><<<(unsigned)blocks, 256, 0, st>>>((const uint32_t *)src, (uint32_t *)dst, sh, so, count); break;
-        case 8: gather_kernel<uint64_t><<<(unsigned)blocks, 256, 0, st>>>((const uint64_t *)src, (uint64_t *)dst, sh, so, count); break;
-        default: return set_error(CHELIS_HIP_EDOMAIN, "gather: width %lld", (long long)width);
-    }
-    CHELIS_LAUNCH_CHECK();
-    return CHELIS_HIP_OK;
-}
 
 }  // namespace chelis
 

@@ -1,12 +1,13 @@
-// Reductions over one axis on gfx950: sum, prod (canonical tree), max, min
-// ([05-OP-12/13]), argmax, argmin ([05-OP-15/16]), each with an optional
-// inlined FusedElem chain as the leaf (the reference's reduce_fused), plus
-// the Bool8 count ([05-OP-29]).
+// Reductions over one axis on gfx950: sum (canonical tree), max, min
+// ([05-OP-12/13]), argmax, argmin ([05-OP-15/16]), sum and max with an
+// optional inlined FusedElem chain as the leaf (the reference's
+// reduce_fused), prod (the C lane's left fold), plus the Bool8 count
+// ([05-OP-29]).
 //
 // The reduced tensor is viewed as [outer, n, inner]. The canonical tree
 // over n leaves equals a full binary tree over the leaves padded to a power
-// of two with the operation's exact identity (-0 for +, 1 for *, -inf/+inf
-// for max/min, never selected), so it can be evaluated hierarchically:
+// of two with the operation's exact identity (-0 for +, -inf/+inf for
+// max/min, never selected), so it can be evaluated hierarchically:
 // each pass reduces aligned groups of G = 2^g consecutive leaves to one
 // partial, and the next pass treats the partials as leaves, until one
 // value per output remains. Every group is an aligned subtree, so the
@@ -32,12 +33,11 @@
 namespace chelis {
 namespace {
 
-enum class Rk : int { Sum, Prod, Max, Min, ArgMax, ArgMin };
+enum class Rk : int { Sum, Max, Min, ArgMax, ArgMin };
 
 template <typename T, Rk K>
 __device__ inline T identity() {
     if constexpr (K == Rk::Sum) return T(-0.0);
-    if constexpr (K == Rk::Prod) return T(1);
     if constexpr (K == Rk::Max || K == Rk::ArgMax) return -__builtin_huge_val();
     return __builtin_huge_val();
 }
@@ -47,8 +47,6 @@ template <typename T, Rk K>
 __device__ inline void combine(T &a, int64_t &ia, T b, int64_t ib) {
     if constexpr (K == Rk::Sum) {
         a = a + b;
-    } else if constexpr (K == Rk::Prod) {
-        a = a * b;
     } else {
         if (a != a) return;
         if (b != b) {
@@ -104,9 +102,7 @@ __device__ inline void wave_join(T &v, int64_t &vi, int lane) {
     for (int m = 1; m < 64; m <<= 1) {
         T ov = shfl_xor(v, m);
         int64_t oi = has_index(K) ? shfl_xor(vi, m) : 0;
-        if constexpr (K == Rk::Prod) {
-            combine<T, K>(v, vi, ov, oi);  // commutative: both lanes agree
-        } else if (lane & m) {
+        if (lane & m) {
             T a = ov;
             int64_t ia = oi;
             combine<T, K>(a, ia, v, vi);
@@ -135,7 +131,7 @@ __device__ inline void ordered_tree(T (&v)[N], int64_t (&vi)[N]) {
 
 template <typename T, Rk K>
 __device__ inline T finalize(T v) {
-    if constexpr (K == Rk::Sum || K == Rk::Prod) return canon(v);
+    if constexpr (K == Rk::Sum) return canon(v);
     return v;
 }
 
@@ -362,6 +358,38 @@ template <typename T>
 __global__ void fill_kernel(T *p, int64_t n, T v) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = v;
+}
+
+// ProdReduce as the C lane computes it (crates/chelis-backend-c/src/emit.rs:
+// 2551-2561 -> emit_reduce_simple, 8817-8912): `acc = 1; acc *= x[k]` over
+// the axis in index order, a left fold rounded at the dtype after every
+// multiply, the stored value NaN-finalized. The fold is sequential by
+// definition (products do not reassociate bit for bit), so a thread owns one
+// output; adjacent threads take adjacent columns (inner > 1) or adjacent rows.
+// The reference HIP lane's reduce_prod folds the same way at f32 and f64
+// (crates/chelis-backend-hip/src/kernels.rs:1888-1925).
+template <typename T>
+__global__ __launch_bounds__(256) void prod_fold_kernel(const T *__restrict__ x, int64_t outer, int64_t n,
+                                                        int64_t inner, int64_t so, int64_t sn, int64_t si,
+                                                        T *__restrict__ out) {
+    const int64_t total = outer * inner;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += stride) {
+        const int64_t o = t / inner, j = t % inner;
+        const T *p = x + o * so + j * si;
+        T acc = T(1);
+        int64_t k = 0;
+        // four loads in flight ahead of the dependent multiplies
+        for (; k + 4 <= n; k += 4) {
+            const T a0 = p[k * sn], a1 = p[(k + 1) * sn], a2 = p[(k + 2) * sn], a3 = p[(k + 3) * sn];
+            acc = acc * a0;
+            acc = acc * a1;
+            acc = acc * a2;
+            acc = acc * a3;
+        }
+        for (; k < n; ++k) acc = acc * p[k * sn];
+        out[t] = canon(acc);
+    }
 }
 
 // count: Bool8 leaves, exact i64 sums (any order gives the same integer),
@@ -607,7 +635,6 @@ int32_t dispatch_kind(int32_t op, const ChainDev &ch, bool chain, const LeafSrc 
                       int64_t inner, void *out, hipStream_t st) {
     switch (op) {
         case CHELIS_REDUCE_SUM: return run_reduce<T, Rk::Sum>(ch, chain, src, outer, n, inner, out, st);
-        case CHELIS_REDUCE_PROD: return run_reduce<T, Rk::Prod>(ch, chain, src, outer, n, inner, out, st);
         case CHELIS_REDUCE_MAX: return run_reduce<T, Rk::Max>(ch, chain, src, outer, n, inner, out, st);
         case CHELIS_REDUCE_MIN: return run_reduce<T, Rk::Min>(ch, chain, src, outer, n, inner, out, st);
         case CHELIS_REDUCE_ARGMAX: return run_reduce<T, Rk::ArgMax>(ch, chain, src, outer, n, inner, out, st);
@@ -699,6 +726,21 @@ extern "C" int32_t chelis_hip_reduce(int32_t op, const chelis_fused_chain *chain
         src.p[k] = inputs[k]->data;
         if (!split3(inputs[k], axis, &src.so[k], &src.sn[k], &src.si[k]))
             return set_error(CHELIS_HIP_EUNSUPPORTED, "reduce: input %d axes do not collapse to [outer, n, inner]", k);
+    }
+    if (op == CHELIS_REDUCE_PROD) {
+        if (chain) return set_error(CHELIS_HIP_EUNSUPPORTED, "reduce: a fused leaf chain feeds sum or max only");
+        int64_t blocks = (outer * inner + 255) / 256;
+        if (blocks > 65536) blocks = 65536;
+        if (x0->dtype == CHELIS_DTYPE_F32)
+            prod_fold_kernel<float><<<(unsigned)blocks, 256, 0, st>>>((const float *)src.p[0], outer, n, inner,
+                                                                       src.so[0], src.sn[0], src.si[0],
+                                                                       (float *)out->data);
+        else
+            prod_fold_kernel<double><<<(unsigned)blocks, 256, 0, st>>>((const double *)src.p[0], outer, n, inner,
+                                                                        src.so[0], src.sn[0], src.si[0],
+                                                                        (double *)out->data);
+        CHELIS_LAUNCH_CHECK();
+        return CHELIS_HIP_OK;
     }
     return x0->dtype == CHELIS_DTYPE_F32
                ? dispatch_kind<float>(op, ch, chain != nullptr, src, outer, n, inner, out->data, st)

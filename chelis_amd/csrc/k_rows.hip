@@ -504,7 +504,7 @@ __global__ __launch_bounds__(64 * W * R) void layer_norm_kernel(const T *__restr
             q[s][i] = (j < n) ? canon(v[s][i] * v[s][i]) : T(-0.0);
         }
     const T var = canon(canon(row_tree_sum<T, V, S, W, R>(q, lds, c)) / extent);
-    const T denom = canon(sqrt(canon(var + eps)));
+    const T denom = canon_bits(sqrt(canon(var + eps)));
     // gamma/beta are [n] vectors shared by every row
     load_row<T, V, S, W, false>(gamma, n, vec_ok, c.tid_in_row, T(0), q);
 #pragma unroll

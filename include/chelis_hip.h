@@ -99,10 +99,13 @@ int32_t chelis_hip_fused_elementwise(const chelis_fused_chain *chain, const chel
 
 /* ---- reductions over one axis ----
  * kernels.rs:2175 reduce_fused (chain != NULL: the chain's value is the
- * leaf) and kernels.rs:1703-2013 reduce_sum/max/min/prod/argmax/argmin
- * (chain == NULL: inputs[0] is the leaf). Sum and prod use the canonical
- * tree; max/min the first-NaN / first-representation rule [05-OP-12/13];
- * argmax/argmin write i64. `out` has the input shape minus `axis`. */
+ * leaf; sum and max only, the reductions fuse.rs:463-487 inlines a chain
+ * into) and kernels.rs:1703-2013 reduce_sum/max/min/prod/argmax/argmin
+ * (chain == NULL: inputs[0] is the leaf). Sum uses the canonical tree;
+ * prod is the C lane's left fold from 1 (crates/chelis-backend-c/src/
+ * emit.rs:2551-2561, 8817-8912), NaN-finalized; max/min follow the
+ * first-NaN / first-representation rule [05-OP-12/13]; argmax/argmin write
+ * i64. `out` has the input shape minus `axis`. */
 enum {
     CHELIS_REDUCE_SUM = 0, CHELIS_REDUCE_COUNT = 1, CHELIS_REDUCE_MAX = 2,
     CHELIS_REDUCE_MIN = 3, CHELIS_REDUCE_PROD = 4, CHELIS_REDUCE_ARGMAX = 5,

@@ -450,6 +450,22 @@ void orc_matmul_narrow(int kind, const uint16_t *A, const uint16_t *B, uint16_t 
     free(c);
 }
 
+/* ProdReduce: `float acc = 1.0f; acc *= x[...]` per output in axis order,
+ * then the stored value NaN-finalized (crates/chelis-backend-c/src/emit.rs:
+ * 2551-2561 -> emit_reduce_simple 8817-8912). */
+#define DEFINE_PROD_AXIS(NAME, T, NANF)                                          \
+    void NAME(const T *x, int64_t outer, int64_t n, int64_t inner, T *out) {     \
+        _Pragma("omp parallel for collapse(2) schedule(static)")                  \
+        for (int64_t o = 0; o < outer; ++o)                                      \
+            for (int64_t j = 0; j < inner; ++j) {                                \
+                T acc = (T)1;                                                    \
+                for (int64_t k = 0; k < n; ++k) acc *= x[(o * n + k) * inner + j]; \
+                out[o * inner + j] = NANF(acc);                                  \
+            }                                                                    \
+    }
+DEFINE_PROD_AXIS(orc_prod_axis_f32, float, nan32)
+DEFINE_PROD_AXIS(orc_prod_axis_f64, double, nan64)
+
 /* [05-OP-37] keyed dropout at f32: the f32-rounded unit of word(key, i) is
  * compared with the rate; a dropped element is +0, a kept one
  * x / (1 - rate) (crates/chelis-backend-c/src/emit.rs:6139-6220). The

@@ -65,6 +65,13 @@ void orc_sum_axis_f32(const float *x, int64_t outer, int64_t n, int64_t inner, f
 void orc_sum_axis_f64(const double *x, int64_t outer, int64_t n, int64_t inner, double *out);
 void orc_max_axis_f32(const float *x, int64_t outer, int64_t n, int64_t inner, float *out);
 void orc_max_axis_f64(const double *x, int64_t outer, int64_t n, int64_t inner, double *out);
+/* ProdReduce over [outer, n, inner]: the C lane's left fold from 1
+ * (crates/chelis-backend-c/src/emit.rs:2551-2561, 8817-8912), NaN-finalized.
+ * The C lane admits f32 only (emit.rs:8838-8855); the f64 form is the same
+ * fold at binary64, as the reference HIP lane's reduce_prod computes it
+ * (crates/chelis-backend-hip/src/kernels.rs:1888-1925). */
+void orc_prod_axis_f32(const float *x, int64_t outer, int64_t n, int64_t inner, float *out);
+void orc_prod_axis_f64(const double *x, int64_t outer, int64_t n, int64_t inner, double *out);
 /* Bool8 count over [outer, n, inner]; returns 0 or the reference error
  * code 1 (a byte that is not 0 or 1). */
 int32_t orc_count_axis(const uint8_t *x, int64_t outer, int64_t n, int64_t inner, int64_t *out);

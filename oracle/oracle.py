@@ -61,6 +61,8 @@ def _declare(L):
         "orc_sum_axis_f64": (None, [c_p, c_i64, c_i64, c_i64, c_p]),
         "orc_max_axis_f32": (None, [c_p, c_i64, c_i64, c_i64, c_p]),
         "orc_max_axis_f64": (None, [c_p, c_i64, c_i64, c_i64, c_p]),
+        "orc_prod_axis_f32": (None, [c_p, c_i64, c_i64, c_i64, c_p]),
+        "orc_prod_axis_f64": (None, [c_p, c_i64, c_i64, c_i64, c_p]),
         "orc_count_axis": (ctypes.c_int32, [c_p, c_i64, c_i64, c_i64, c_p]),
         "orc_softmax_rows_f32": (None, [c_p, c_p, c_i64, c_i64]),
         "orc_softmax_rows_f64": (None, [c_p, c_p, c_i64, c_i64]),
@@ -163,6 +165,15 @@ def max_axis(x: np.ndarray, axis: int) -> np.ndarray:
     outer, n, inner, shape = _axis_view(x, axis)
     out = np.empty(shape, x.dtype)
     getattr(lib(), f"orc_max_axis_{_f(x.dtype)}")(_ptr(x), outer, n, inner, _ptr(out))
+    return out
+
+
+def prod_axis(x: np.ndarray, axis: int) -> np.ndarray:
+    """ProdReduce: the C lane's left fold from 1 over `axis`."""
+    x = np.ascontiguousarray(x)
+    outer, n, inner, shape = _axis_view(x, axis)
+    out = np.empty(shape, x.dtype)
+    getattr(lib(), f"orc_prod_axis_{_f(x.dtype)}")(_ptr(x), outer, n, inner, _ptr(out))
     return out
 
 

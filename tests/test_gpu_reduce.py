@@ -183,3 +183,34 @@ def test_column_blocks_chain_leaf():
     ch = C.fused_chain([("sub", 0, 1), ("mul", ("s", 0), ("s", 0))])
     out = C.reduce("sum", [C.to_device(x), C.to_device(g)], 0, chain=ch).numpy()
     assert bits_equal(out, O.sum_axis(((x - g) * (x - g)).astype(np.float32), 0))
+
+
+PROD_SHAPES = [((1,), 0), ((7,), 0), ((64, 1000), 1), ((64, 1000), 0), ((3, 257, 5), 1), ((2, 3, 4097), 2),
+               ((4100, 3), 0), ((5, 0), 1)]
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("shape,axis", PROD_SHAPES)
+def test_prod_is_the_left_fold_bit_exact(shape, axis, dtype):
+    """ProdReduce: the C lane's left fold from 1 (oracle prod_axis), with
+    values near 1 so long folds stay finite, plus planted zeros, infinities,
+    NaN payloads and subnormals whose order decides the result."""
+    rng = np.random.default_rng(sum(shape) + 3 * axis)
+    x = rng.uniform(0.97, 1.03, shape).astype(dtype)
+    flat = x.reshape(-1)
+    if flat.size > 40:
+        tiny = np.finfo(dtype).smallest_subnormal
+        big = np.finfo(dtype).max
+        flat[[3, 11, 17, 29, 31]] = [0.0, np.inf, tiny, big, -0.0]
+        flat[37] = np.array([0x7FC0BEEF], np.uint32).view(np.float32)[0] if dtype == np.float32 else \
+            np.array([0x7FF800000000BEEF], np.uint64).view(np.float64)[0]
+    d = C.to_device(x)
+    got = C.reduce("prod", d, axis).numpy()
+    assert bits_equal(got, O.prod_axis(x, axis))
+
+
+def test_prod_refuses_a_chain_leaf():
+    x = C.to_device(np.ones((4, 8), np.float32))
+    ch = C.fused_chain([("mul", 0, 0)])
+    with pytest.raises(C.ChelisError, match="status 2"):
+        C.reduce("prod", [x], 1, chain=ch)

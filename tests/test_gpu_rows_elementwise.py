@@ -343,3 +343,106 @@ def test_fused_chain_every_op_vector_and_scalar_interpreters(dtype, n_extra_inpu
         s14 = np.where(extra[0] > s13, extra[0], s13)
         ref = np.floor(s14)
     assert bits_equal(out.numpy(), ref.astype(dtype))
+
+
+def _specials(dtype):
+    if dtype == np.float32:
+        bits = [0x7FC0BEEF, 0xFFC00001, 0x7F800000, 0xFF800000, 0x00000000, 0x80000000, 0x00000001, 0x80000003,
+                0x3F800000, 0xBF800000, 0x7F7FFFFF, 0x3F000000, 0x40490FDB, 0xC2B00000]
+        return np.array(bits, np.uint32).view(np.float32)
+    bits = [0x7FF800000000BEEF, 0xFFF8000000000001, 0x7FF0000000000000, 0xFFF0000000000000, 0, 0x8000000000000000,
+            1, 0x8000000000000003, 0x3FF0000000000000, 0xBFF0000000000000, 0x7FEFFFFFFFFFFFFF, 0x3FE0000000000000,
+            0x400921FB54442D18, 0xC086000000000000]
+    return np.array(bits, np.uint64).view(np.float64)
+
+
+def _canon(v):
+    v = np.array(v)
+    out = v.copy()
+    nan = np.isnan(v)
+    out[nan] = np.array([0x7FC00000], np.uint32).view(np.float32)[0] if v.dtype == np.float32 else \
+        np.array([0x7FF8000000000000], np.uint64).view(np.float64)[0]
+    return out
+
+
+def _ref_step(op, a, b, imm, dtype):
+    """One FusedElem step as the C lane evaluates it (crates/chelis-backend-c/
+    src/emit.rs:6744-6895, NaN finalization per fp_env.rs:214-241): every op
+    stores the canonical NaN except max_elem / min_elem, which keep the
+    selected operand's bits; relu / relu_adjoint select stored bits
+    ([05-OP-43]); transcendental leaves are the oracle's CORE-MATH values."""
+    L = O.lib()
+    leaf = {"exp": (L.orc_expf, L.orc_exp), "log": (L.orc_logf, L.orc_log), "tanh": (L.orc_tanhf, L.orc_tanh),
+            "erfc": (L.orc_erfcf, L.orc_erfc)}
+    with np.errstate(all="ignore"):
+        if op in leaf:
+            fn = leaf[op][0 if dtype == np.float32 else 1]
+            return np.array([fn(v) for v in a], dtype)
+        if op == "max_elem":
+            return np.where(np.isnan(a) | (~np.isnan(b) & (a >= b)), a, b)
+        if op == "min_elem":
+            return np.where(np.isnan(a) | (~np.isnan(b) & (a <= b)), a, b)
+        if op == "relu":
+            return np.where(a < 0, dtype(0), a)
+        if op == "relu_adjoint":
+            return np.where(dtype(0) < a, b, dtype(0))
+        if op == "const":
+            return np.full(a.shape, dtype(imm))
+        f = {"add": lambda: a + b, "sub": lambda: a - b, "mul": lambda: a * b, "div": lambda: a / b,
+             "neg": lambda: -a, "recip": lambda: dtype(1) / a, "sqrt": lambda: np.sqrt(a), "abs": lambda: np.abs(a),
+             "floor": lambda: np.floor(a), "ceil": lambda: np.ceil(a), "round": lambda: np.rint(a)}[op]
+        return _canon(f().astype(dtype))
+
+
+SPECIAL_CHAINS = [
+    [("add", 0, 1), ("sub", 0, 1), ("mul", 0, 1), ("div", 0, 1), ("max_elem", 0, 1), ("min_elem", 1, 0),
+     ("neg", 0), ("recip", 1), ("sqrt", 0), ("abs", 1), ("floor", 0), ("ceil", 1), ("round", 0),
+     ("relu", 1), ("relu_adjoint", 0, 1), ("max_elem", ("s", 4), ("s", 14))],
+    [("exp", 0), ("log", 1), ("tanh", 0), ("erfc", 1), ("min_elem", ("s", 0), ("s", 1)),
+     ("max_elem", ("s", 2), ("s", 3)), ("const", 0, 0, -0.0), ("add", ("s", 6), ("s", 4)),
+     ("mul", ("s", 7), ("s", 5)), ("relu", ("s", 8))],
+]
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("chain_id", [0, 1])
+@pytest.mark.parametrize("last_step", list(range(16)))
+@pytest.mark.parametrize("n_inputs", [2, 8])
+def test_fused_chain_special_values_both_interpreters(dtype, chain_id, last_step, n_inputs):
+    """NaN payloads (quiet, negative), +-inf, +-0, subnormals, the largest
+    finite value and ordinary values, every ordered pair of them, through
+    every step kind, with a ragged tail (n % (16 / itemsize) != 0). Two
+    inputs take the 16-byte vector interpreter; eight inputs (six unused)
+    take the one-element LDS-slot interpreter. Each chain is cut after every
+    step in turn, so each step's result is observed directly."""
+    steps = SPECIAL_CHAINS[chain_id]
+    if last_step >= len(steps):
+        pytest.skip("chain shorter than the cut")
+    steps = steps[:last_step + 1]
+    sp = _specials(dtype)
+    a = np.repeat(sp, sp.size)
+    b = np.tile(sp, sp.size)
+    rng = np.random.default_rng(31)
+    pad = 7
+    a = np.concatenate([a, (rng.standard_normal(pad) * 3).astype(dtype)])
+    b = np.concatenate([b, (rng.standard_normal(pad) * 3).astype(dtype)])
+    n = a.size
+    ins = [C.to_device(a), C.to_device(b)] + [C.to_device(np.zeros(n, dtype)) for _ in range(n_inputs - 2)]
+    out = C.empty((n,), dtype)
+    C.fused_elementwise(C.fused_chain(steps), ins, out)
+    vals = []
+    for st in steps:
+        op = st[0]
+        args = [st[1] if len(st) > 1 else 0, st[2] if len(st) > 2 else 0]
+        av = [vals[x[1]] if isinstance(x, tuple) else (a, b)[x] if x < 2 else np.zeros(n, dtype) for x in args]
+        vals.append(_ref_step(op, av[0], av[1], st[3] if len(st) > 3 else 0.0, dtype))
+    ref = vals[-1].astype(dtype)
+    y = out.numpy()
+    if dtype == np.float64 and any(st[0] in ("log", "tanh", "erfc") for st in steps):
+        # binary64 log / tanh / erfc leaves are the device library's (within
+        # 1 ulp, the 1e-12 relative contract); specials keep exact bits
+        finite = np.isfinite(ref) & (ref != 0)
+        assert bits_equal(y[~finite], ref[~finite]), mismatch_report(y[~finite], ref[~finite])
+        assert np.all(np.abs(y[finite] - ref[finite]) <= 1e-12 * np.abs(ref[finite]))
+    else:
+        assert bits_equal(y, ref), mismatch_report(y, ref)

@@ -19,6 +19,7 @@ What pins what:
 """
 import json
 import math
+from fractions import Fraction
 import os
 import struct
 
@@ -84,6 +85,124 @@ def test_uniform_like_is_the_fma_of_the_unit():
     key = 12345
     u = O.uniform_like(key, np.float64(0.0), np.float64(1.0), 64, np.float64)
     assert [O.unit(key, i) for i in range(64)] == u.tolist()
+
+
+def _round_f32(q: Fraction) -> np.float32:
+    """The binary32 value nearest the exact rational q, ties to even (finite
+    range only): one rounding, independent of numpy's float arithmetic."""
+    c = np.float32(float(q))  # within one binary32 ulp of q
+    best = None
+    for cand in (np.nextafter(c, np.float32(-np.inf)), c, np.nextafter(c, np.float32(np.inf))):
+        d = abs(Fraction(float(cand)) - q)
+        key = (d, int(np.array(cand).view(np.uint32)) & 1)
+        if best is None or key < best[0]:
+            best = (key, cand)
+    return best[1]
+
+
+def test_uniform_like_f32_is_one_rounding_of_the_exact_affine_map():
+    """[05-OP-8] at f32: fmaf(high - low, (float)unit, low). Against the exact
+    rational span * u32 + low rounded once; a multiply-then-add (two
+    roundings) differs on many of these elements, so the check has teeth."""
+    key, n = O.fold_in(77, 5), 4096
+    low, high = np.float32(-1.5), np.float32(2.25)
+    span = high - low  # 3.75, exact
+    got = O.uniform_like(key, low, high, n, np.float32)
+    two_roundings = 0
+    for i in range(n):
+        u32 = np.float32(O.unit(key, i))
+        exact = Fraction(float(span)) * Fraction(float(u32)) + Fraction(float(low))
+        want = _round_f32(exact)
+        assert got[i].view(np.uint32) == np.array(want).view(np.uint32), i
+        two_roundings += (span * u32 + low) != want
+    assert two_roundings > 50
+
+
+def test_uniform_like_f64_is_one_rounding_of_the_exact_affine_map():
+    """[05-OP-8] at f64: fma(high - low, unit, low), against the exact rational
+    rounded once (Python's int / int division is correctly rounded)."""
+    key, n = O.fold_in(78, 1), 4096
+    low, high = -0.7, 2.9  # span 3.5999999999999996: products round
+    span = np.float64(high) - np.float64(low)
+    got = O.uniform_like(key, np.float64(low), np.float64(high), n, np.float64)
+    two_roundings = 0
+    for i in range(n):
+        u = O.unit(key, i)
+        exact = Fraction(float(span)) * Fraction(u) + Fraction(low)
+        want = float(exact)
+        assert got[i] == want and np.signbit(got[i]) == np.signbit(want), i
+        two_roundings += float(span) * u + low != want
+    assert two_roundings > 50
+
+
+def test_dropout_f64_mask_is_the_binary64_unit_and_kept_values_are_one_division():
+    """[05-OP-37] at f64 (crates/chelis-backend-c/src/emit.rs:6179-6189): the
+    binary64 unit is compared with the binary64 rate (no binary32 rounding of
+    the unit), a kept element is x / (1 - rate) rounded once. Element 7's
+    rate is placed between its unit and that unit's binary32 rounding, so a
+    binary32 comparison would keep an element the binary64 rule drops."""
+    key, n = O.fold_in(91, 3), 2048
+    x = np.random.default_rng(5).standard_normal(n) * 10.0 ** np.random.default_rng(6).integers(-30, 30, n)
+    u7 = O.unit(key, 7)
+    f7 = float(np.float32(u7))
+    if f7 < u7:  # make the binary32 rounding of u7 lie above it
+        u7 = O.unit(key, 8)
+        f7 = float(np.float32(u7))
+    assert f7 > u7
+    rate = float(Fraction(u7) + (Fraction(f7) - Fraction(u7)) / 2)
+    assert u7 < rate < f7
+    y = O.dropout(key, x, rate)
+    denom = 1.0 - rate
+    dropped = 0
+    for i in range(n):
+        u = O.unit(key, i)
+        if u < rate:
+            assert y[i] == 0.0 and not np.signbit(y[i]), i
+            dropped += 1
+        else:
+            assert y[i] == float(Fraction(float(x[i])) / Fraction(denom)), i
+    kept32 = [i for i in range(n) if not (np.float32(O.unit(key, i)) < np.float32(rate))]
+    assert y[[i for i in kept32 if O.unit(key, i) < rate]].tolist() != []
+    assert 0 < dropped < n
+
+
+# ---------------------------------------------------------------- prod
+def test_prod_axis_is_the_left_fold_of_the_c_lane():
+    """ProdReduce = ((1 * x0) * x1) * x2 ... at the dtype
+    (crates/chelis-backend-c/src/emit.rs:2551-2561). Hand-derived answers
+    that any other association or a dropped factor changes:
+      [1e-30, 1e-30, 1e30, 1e30] f32: 1e-60 underflows to +0, so the fold is
+        +0; pairwise (1e-60 -> 0) * (1e60 -> inf) is NaN.
+      [2^100, 2^100, 2^-100, 2^-100] f32: the fold overflows to inf at the
+        second factor and stays inf; pairwise it is exactly 1.
+      [3, 5, 7, 11] and powers of two: exact products.
+      a NaN anywhere: the canonical quiet NaN.
+      an empty axis: 1 (the identity, no multiply)."""
+    f = np.float32
+    def run(v, dt=np.float32):
+        return O.prod_axis(np.array([v], dt), 1)[0]
+    assert run([1e-30, 1e-30, 1e30, 1e30]) == 0.0
+    assert run([2.0 ** 100, 2.0 ** 100, 2.0 ** -100, 2.0 ** -100]) == np.inf
+    assert run([3, 5, 7, 11]) == f(1155)
+    assert run([0.5, -4, 0.25, 2]) == f(-1)
+    nan = run([1, float("nan"), 2])
+    assert np.array(nan).view(np.uint32) == 0x7FC00000
+    assert O.prod_axis(np.zeros((3, 0), np.float32), 1).tolist() == [1.0, 1.0, 1.0]
+    # binary64: 1e-200 * 1e-200 underflows to +0 before the 1e200 factors
+    assert run([1e-200, 1e-200, 1e200, 1e200], np.float64) == 0.0
+    # left-to-right rounding: for these three binary32 values (bits below)
+    # ((1 * a) * b) * c rounds to 0x4057ed10 while a * (b * c) rounds to
+    # 0x4057ed0f (each product taken exactly as a rational and rounded once
+    # with _round_f32)
+    a, b, c = np.array([0x3FC1835F, 0x3FF9A8CB, 0x3F9273D2], np.uint32).view(np.float32)
+    F = lambda v: Fraction(float(v))
+    left = _round_f32(F(_round_f32(F(a) * F(b))) * F(c))
+    right = _round_f32(F(a) * F(_round_f32(F(b) * F(c))))
+    assert np.array(left).view(np.uint32) == 0x4057ED10 and np.array(right).view(np.uint32) == 0x4057ED0F
+    assert np.array(run([a, b, c])).view(np.uint32) == 0x4057ED10
+    # axis 0 of a [n, m] matrix folds each column top to bottom
+    m = np.array([[2, 3], [5, 7], [11, 13]], np.float32)
+    assert O.prod_axis(m, 0).tolist() == [110.0, 273.0]
 
 
 # ---------------------------------------------------------------- CORE-MATH
