@@ -117,6 +117,7 @@ SIGNATURES = {
     "chelis_hip_dropout_replay": (c_int32, [c_uint64, P, c_double, P]),
     "chelis_hip_uniform_like": (c_int32, [c_uint64, c_double, c_double, P]),
     "chelis_hip_reduce": (c_int32, [c_int32, POINTER(FusedChain), POINTER(P), c_int32, c_int32, P]),
+    "chelis_hip_reduce_static": (c_int32, [c_int32, POINTER(FusedChain), POINTER(P), c_int32, c_int32, P]),
     "chelis_hip_count": (c_int32, [P, c_int32, P, POINTER(c_int32)]),
     "chelis_hip_matmul": (c_int32, [P, P, P, c_int32]),
     "chelis_hip_linear": (c_int32, [P, P, P, c_int32, P, P, c_int32]),
@@ -393,9 +394,10 @@ def fused_elementwise(chain: FusedChain, inputs, out):
 REDUCE_OPS = {"sum": 0, "max": 2, "min": 3, "prod": 4, "argmax": 5, "argmin": 6}
 
 
-def reduce(op: str, inputs, axis: int, out=None, chain: FusedChain | None = None):
+def reduce(op: str, inputs, axis: int, out=None, chain: FusedChain | None = None, static: bool = False):
     """chelis_hip_reduce over one axis; `chain` (with several inputs) is the
-    inlined FusedElem leaf, else inputs is one tensor."""
+    inlined FusedElem leaf, else inputs is one tensor. static=True calls the
+    allocation-free chelis_hip_reduce_static."""
     if not isinstance(inputs, (list, tuple)):
         inputs = [inputs]
     x0 = inputs[0]
@@ -404,8 +406,9 @@ def reduce(op: str, inputs, axis: int, out=None, chain: FusedChain | None = None
     if out is None:
         out = empty(shape, np.int64 if op in ("argmax", "argmin") else x0.dtype)
     arr = (P * len(inputs))(*[_p(t) for t in inputs])
-    check(lib().chelis_hip_reduce(REDUCE_OPS[op], ctypes.byref(chain) if chain is not None else None, arr,
-                                  len(inputs), axis, _p(out)), f"reduce {op}")
+    fn = lib().chelis_hip_reduce_static if static else lib().chelis_hip_reduce
+    check(fn(REDUCE_OPS[op], ctypes.byref(chain) if chain is not None else None, arr, len(inputs), axis, _p(out)),
+          f"reduce {op}")
     return out
 
 

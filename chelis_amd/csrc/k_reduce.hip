@@ -28,6 +28,9 @@
 //    reduces them with an unrolled in-register tree.
 // max/min/argmax combine in index order (lower lane / earlier leaf on the
 // left), so first-NaN and first-index tie rules hold.
+#include <algorithm>
+#include <mutex>
+
 #include "chain.h"
 
 namespace chelis {
@@ -468,67 +471,52 @@ bool split3(const chelis_gpu_tensor *t, int32_t axis, int64_t *so, int64_t *sn, 
     return fold(0, axis, so) && fold(axis + 1, t->rank, si);
 }
 
-// A pass's partials: library scratch, recycled in stream order.
-struct Scratch {
-    void *p = nullptr;
-    size_t bytes = 0;
-    explicit Scratch(hipStream_t) {}
-    ~Scratch() { release(); }
-    void release() {
-        scratch_free(p, bytes);
-        p = nullptr;
-    }
-    bool get(size_t n) {
-        release();
-        bytes = n;
-        p = scratch_alloc(n);
-        return p != nullptr;
-    }
-};
-
 // An inlined FusedElem leaf exists only for Sum and Max, the two
 // reductions fuse.rs folds a chain into (crates/chelis-dag-core/src/fuse.rs:463-487).
 template <Rk K>
 constexpr bool kChainable = K == Rk::Sum || K == Rk::Max;
 
+// One pass of a reduction, planned on the host before anything is enqueued.
+struct Pass {
+    bool vec;       // contiguous rows with 16-byte loads
+    int S;          // rows: segments per wave
+    bool cols4;     // columns: four waves per 128-leaf group
+    int64_t n;      // leaves per output this pass
+    int64_t groups; // partials per output it writes
+};
+constexpr int kMaxPasses = 16;
+
+// The pass sequence: partials of pass i are the leaves of pass i + 1 and
+// live in a buffer 256-byte aligned, so their row alignment depends only
+// on the row length. Returns the number of passes.
 template <typename T, Rk K>
-int32_t run_reduce(const ChainDev &ch, bool chain, LeafSrc src, int64_t outer, int64_t n, int64_t inner,
-                   void *out, hipStream_t st) {
-    if (chain && !kChainable<K>) return set_error(CHELIS_HIP_EUNSUPPORTED, "reduce: a fused leaf chain feeds sum or max only");
-    // Pass loop: partials alternate between two scratch buffers.
-    Scratch sa(st), sb(st), ia(st), ib(st);
+int plan_passes(const ChainDev &ch, bool chain, const LeafSrc &src, int64_t outer, int64_t n, int64_t inner,
+                Pass (&passes)[kMaxPasses]) {
     const bool rows = inner == 1;
     int64_t cur_n = n;
-    bool first = true;
-    T *prev_v = nullptr;
-    int64_t *prev_i = nullptr;
-    int flip = 0;
-    while (true) {
-        // rows: a row that fits one wave's 16 segments finishes in this pass;
-        // a longer one is cut into as many groups as keep >= 1024 waves busy
-        // (S = 16 only when there are rows enough), since a pass over few long
-        // groups runs on a handful of waves.
-        LeafSrc s = src;
-        if (!first) {
-            s.n_in = 1;
-            s.p[0] = prev_v;
-            s.so[0] = cur_n * inner;
-            s.sn[0] = inner;
-            s.si[0] = 1;
-            s.idx = prev_i;
-        }
+    for (int i = 0; i < kMaxPasses; ++i) {
+        const bool first = i == 0;
         const bool use_chain = first && chain;
         // contiguous rows take 16-byte loads: leaves at stride 1, row
         // starts aligned, and leaf indices that are positions
         bool vec = rows && !(has_index(K) && !first);
-        for (int32_t k = 0; vec && k < s.n_in; ++k)
-            vec = s.sn[k] == 1 && (reinterpret_cast<uintptr_t>(s.p[k]) & 15u) == 0 &&
-                  (s.so[k] * (int64_t)sizeof(T)) % 16 == 0;
-        const size_t chain_lds = (size_t)(s.n_in + ch.n_steps) * 256 * 16;
+        if (first) {
+            for (int32_t k = 0; vec && k < src.n_in; ++k)
+                vec = src.sn[k] == 1 && (reinterpret_cast<uintptr_t>(src.p[k]) & 15u) == 0 &&
+                      (src.so[k] * (int64_t)sizeof(T)) % 16 == 0;
+        } else {
+            vec = vec && (cur_n * (int64_t)sizeof(T)) % 16 == 0;
+        }
+        const int n_in = first ? src.n_in : 1;
+        const size_t chain_lds = (size_t)(n_in + ch.n_steps) * 256 * 16;
         if (use_chain && chain_lds > 65536) vec = false;
         const int64_t unit = vec ? 64 * (16 / (int64_t)sizeof(T)) : 64;
-        // a contiguous chain leaf runs one segment per wave: the interpreter
-        // is inlined once per element a lane holds
+        // rows: a row that fits one wave's 16 segments finishes in this pass;
+        // a longer one is cut into as many groups as keep >= 1024 waves busy
+        // (S = 16 only when there are rows enough), since a pass over few long
+        // groups runs on a handful of waves. A contiguous chain leaf runs one
+        // segment per wave: the interpreter is inlined once per element a
+        // lane holds.
         const int smax = vec && use_chain ? 1 : 16;
         int S = 1;
         if (rows) {
@@ -543,27 +531,110 @@ int32_t run_reduce(const ChainDev &ch, bool chain, LeafSrc src, int64_t outer, i
                            outer * ((cur_n + 127) / 128) * ((inner + 63) / 64) <= 0x7fffffffLL;
         const int64_t G = rows ? unit * S : (cols4 ? 128 : 32);
         const int64_t groups = (cur_n + G - 1) / G;
-        const bool last = groups == 1;
+        passes[i] = Pass{vec, S, cols4, cur_n, groups};
+        if (groups == 1) return i + 1;
+        cur_n = groups;
+    }
+    return kMaxPasses;  // unreachable: each pass divides the leaves by >= 32
+}
+
+// Bytes of partials a plan needs: passes alternate between two value
+// buffers (and two index buffers for argmax / argmin), each sized by the
+// largest pass that writes it. Fills the four sizes when sizes != null.
+template <typename T, Rk K>
+size_t partial_bytes(const Pass *passes, int np, int64_t outer, int64_t inner, size_t *sizes = nullptr) {
+    size_t need[4] = {0, 0, 0, 0};  // values A, values B, indices A, indices B
+    for (int i = 0; i < np; ++i) {
+        const bool last = i + 1 == np;
+        const size_t cells = (size_t)(outer * passes[i].groups * inner);
+        const int b = i & 1;
+        // the last pass writes the result, except the values of argmax /
+        // argmin, whose result is the index
+        if (!last || has_index(K)) need[b] = std::max(need[b], ((cells * sizeof(T)) + 255) & ~size_t(255));
+        if (has_index(K) && !last)
+            need[2 + b] = std::max(need[2 + b], ((cells * sizeof(int64_t)) + 255) & ~size_t(255));
+    }
+    if (sizes)
+        for (int k = 0; k < 4; ++k) sizes[k] = need[k];
+    return need[0] + need[1] + need[2] + need[3];
+}
+
+// Where pass partials live: the library's stream-ordered cached scratch
+// (region == null), or a caller-fixed device region carved in order.
+struct PartialStore {
+    char *region = nullptr;
+    size_t region_bytes = 0;
+};
+
+// Cached-scratch blocks held for one reduction, returned in stream order.
+struct HeldScratch {
+    void *p[4] = {nullptr, nullptr, nullptr, nullptr};
+    size_t bytes[4] = {0, 0, 0, 0};
+    ~HeldScratch() {
+        for (int k = 0; k < 4; ++k) scratch_free(p[k], bytes[k]);
+    }
+};
+
+template <typename T, Rk K>
+int32_t run_reduce(const ChainDev &ch, bool chain, LeafSrc src, int64_t outer, int64_t n, int64_t inner,
+                   void *out, hipStream_t st, const PartialStore &store) {
+    if (chain && !kChainable<K>) return set_error(CHELIS_HIP_EUNSUPPORTED, "reduce: a fused leaf chain feeds sum or max only");
+    Pass passes[kMaxPasses];
+    const int np = plan_passes<T, K>(ch, chain, src, outer, n, inner, passes);
+    size_t sizes[4];
+    const size_t total = partial_bytes<T, K>(passes, np, outer, inner, sizes);
+    void *buf[4] = {nullptr, nullptr, nullptr, nullptr};
+    HeldScratch held;
+    if (store.region) {
+        if (total > store.region_bytes)
+            return set_error(CHELIS_HIP_EDOMAIN, "reduce: the passes need %zu bytes of partials, the static scratch holds %zu",
+                             total, store.region_bytes);
+        size_t off = 0;
+        for (int k = 0; k < 4; ++k) {
+            buf[k] = sizes[k] ? store.region + off : nullptr;
+            off += sizes[k];
+        }
+    } else {
+        for (int k = 0; k < 4; ++k) {
+            if (!sizes[k]) continue;
+            held.bytes[k] = sizes[k];
+            if (!(held.p[k] = buf[k] = scratch_alloc(sizes[k])))
+                return set_error(CHELIS_HIP_EHIP, "reduce: scratch allocation failed");
+        }
+    }
+    const bool rows = inner == 1;
+    T *prev_v = nullptr;
+    int64_t *prev_i = nullptr;
+    for (int pi = 0; pi < np; ++pi) {
+        const Pass &ps = passes[pi];
+        const bool first = pi == 0;
+        const int64_t cur_n = ps.n, groups = ps.groups;
+        const bool vec = ps.vec, cols4 = ps.cols4;
+        const int S = ps.S;
+        LeafSrc s = src;
+        if (!first) {
+            s.n_in = 1;
+            s.p[0] = prev_v;
+            s.so[0] = cur_n * inner;
+            s.sn[0] = inner;
+            s.si[0] = 1;
+            s.idx = prev_i;
+        }
+        const bool use_chain = first && chain;
+        const size_t chain_lds = (size_t)(s.n_in + ch.n_steps) * 256 * 16;
+        const bool last = pi + 1 == np;
+        const int64_t cells = outer * groups * inner;
         T *dst_v;
         int64_t *dst_i = nullptr;
-        const int64_t cells = outer * groups * inner;
         if (last) {
             dst_v = has_index(K) ? nullptr : static_cast<T *>(out);
             dst_i = has_index(K) ? static_cast<int64_t *>(out) : nullptr;
         } else {
-            dst_v = nullptr;
+            dst_v = static_cast<T *>(buf[pi & 1]);
+            dst_i = static_cast<int64_t *>(buf[2 + (pi & 1)]);
         }
-        Scratch &bv = flip ? sb : sa;
-        Scratch &bi = flip ? ib : ia;
-        if (!dst_v) {
-            if (!bv.get((size_t)cells * sizeof(T))) return set_error(CHELIS_HIP_EHIP, "reduce: scratch allocation failed");
-            dst_v = static_cast<T *>(bv.p);
-        }
-        if (has_index(K) && !dst_i) {
-            if (!bi.get((size_t)cells * sizeof(int64_t)))
-                return set_error(CHELIS_HIP_EHIP, "reduce: scratch allocation failed");
-            dst_i = static_cast<int64_t *>(bi.p);
-        }
+        // the index-only result of argmax / argmin still needs value partials
+        if (!dst_v) dst_v = static_cast<T *>(buf[pi & 1]);
         if (rows) {
             const unsigned grid = grid_for(outer * groups, 4);
 #define CHELIS_ROWS_LAUNCH(KERNEL, SS, CHAIN_OK, LDS)                                                        \
@@ -620,25 +691,21 @@ int32_t run_reduce(const ChainDev &ch, bool chain, LeafSrc src, int64_t outer, i
                                                                                   dst_v, dst_i, last);
         }
         CHELIS_LAUNCH_CHECK();
-        if (last) break;
         prev_v = dst_v;
         prev_i = dst_i;
-        cur_n = groups;
-        first = false;
-        flip ^= 1;
     }
     return CHELIS_HIP_OK;
 }
 
 template <typename T>
 int32_t dispatch_kind(int32_t op, const ChainDev &ch, bool chain, const LeafSrc &src, int64_t outer, int64_t n,
-                      int64_t inner, void *out, hipStream_t st) {
+                      int64_t inner, void *out, hipStream_t st, const PartialStore &store) {
     switch (op) {
-        case CHELIS_REDUCE_SUM: return run_reduce<T, Rk::Sum>(ch, chain, src, outer, n, inner, out, st);
-        case CHELIS_REDUCE_MAX: return run_reduce<T, Rk::Max>(ch, chain, src, outer, n, inner, out, st);
-        case CHELIS_REDUCE_MIN: return run_reduce<T, Rk::Min>(ch, chain, src, outer, n, inner, out, st);
-        case CHELIS_REDUCE_ARGMAX: return run_reduce<T, Rk::ArgMax>(ch, chain, src, outer, n, inner, out, st);
-        case CHELIS_REDUCE_ARGMIN: return run_reduce<T, Rk::ArgMin>(ch, chain, src, outer, n, inner, out, st);
+        case CHELIS_REDUCE_SUM: return run_reduce<T, Rk::Sum>(ch, chain, src, outer, n, inner, out, st, store);
+        case CHELIS_REDUCE_MAX: return run_reduce<T, Rk::Max>(ch, chain, src, outer, n, inner, out, st, store);
+        case CHELIS_REDUCE_MIN: return run_reduce<T, Rk::Min>(ch, chain, src, outer, n, inner, out, st, store);
+        case CHELIS_REDUCE_ARGMAX: return run_reduce<T, Rk::ArgMax>(ch, chain, src, outer, n, inner, out, st, store);
+        case CHELIS_REDUCE_ARGMIN: return run_reduce<T, Rk::ArgMin>(ch, chain, src, outer, n, inner, out, st, store);
         default: return set_error(CHELIS_HIP_EDOMAIN, "reduce: unknown op %d", op);
     }
 }
@@ -670,9 +737,11 @@ int32_t load_chain(const chelis_fused_chain *chain, int32_t n_inputs, ChainDev *
 
 using namespace chelis;
 
-extern "C" int32_t chelis_hip_reduce(int32_t op, const chelis_fused_chain *chain,
-                                     const chelis_gpu_tensor *const *inputs, int32_t n_inputs, int32_t axis,
-                                     const chelis_gpu_tensor *out) {
+namespace chelis {
+namespace {
+
+int32_t reduce_entry(int32_t op, const chelis_fused_chain *chain, const chelis_gpu_tensor *const *inputs,
+                     int32_t n_inputs, int32_t axis, const chelis_gpu_tensor *out, const PartialStore &store) {
     int32_t s;
     if (op == CHELIS_REDUCE_COUNT) return set_error(CHELIS_HIP_EDOMAIN, "reduce: use chelis_hip_count for counts");
     if (n_inputs < 1 || n_inputs > CHELIS_FUSED_MAX_INPUTS || !inputs)
@@ -743,8 +812,57 @@ extern "C" int32_t chelis_hip_reduce(int32_t op, const chelis_fused_chain *chain
         return CHELIS_HIP_OK;
     }
     return x0->dtype == CHELIS_DTYPE_F32
-               ? dispatch_kind<float>(op, ch, chain != nullptr, src, outer, n, inner, out->data, st)
-               : dispatch_kind<double>(op, ch, chain != nullptr, src, outer, n, inner, out->data, st);
+               ? dispatch_kind<float>(op, ch, chain != nullptr, src, outer, n, inner, out->data, st, store)
+               : dispatch_kind<double>(op, ch, chain != nullptr, src, outer, n, inner, out->data, st, store);
+}
+
+}  // namespace
+}  // namespace chelis
+
+// The allocation-free reduce entry's pass partials: one fixed array per
+// device, reached through its device address (the host-side name is only a
+// stand-in). The address is looked up once per device, with that device
+// current, and kept.
+static __device__ __align__(256) unsigned char scratch[CHELIS_HIP_STATIC_SCRATCH_BYTES];
+
+namespace {
+std::mutex g_scratch_addr_mutex;
+constexpr int kMaxScratchDevices = 64;
+void *g_scratch_addr[kMaxScratchDevices] = {};
+
+int32_t static_scratch_address(void **addr) {
+    int device = -1;
+    CHELIS_HIP_TRY(hipGetDevice(&device));
+    if (device < 0 || device >= kMaxScratchDevices)
+        return set_error(CHELIS_HIP_EHIP, "static scratch: device %d outside 0..%d", device, kMaxScratchDevices - 1);
+    std::lock_guard<std::mutex> lock(g_scratch_addr_mutex);
+    if (!g_scratch_addr[device]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return set_error(CHELIS_HIP_EHIP, "static scratch: hipGetSymbolAddress: %s", hipGetErrorString(e));
+        g_scratch_addr[device] = p;
+    }
+    *addr = g_scratch_addr[device];
+    return CHELIS_HIP_OK;
+}
+}  // namespace
+
+extern "C" int32_t chelis_hip_reduce(int32_t op, const chelis_fused_chain *chain,
+                                     const chelis_gpu_tensor *const *inputs, int32_t n_inputs, int32_t axis,
+                                     const chelis_gpu_tensor *out) {
+    return reduce_entry(op, chain, inputs, n_inputs, axis, out, PartialStore{});
+}
+
+extern "C" int32_t chelis_hip_reduce_static(int32_t op, const chelis_fused_chain *chain,
+                                            const chelis_gpu_tensor *const *inputs, int32_t n_inputs, int32_t axis,
+                                            const chelis_gpu_tensor *out) {
+    void *addr = nullptr;
+    if (int32_t s = static_scratch_address(&addr)) return s;
+    PartialStore store;
+    store.region = static_cast<char *>(addr);
+    store.region_bytes = CHELIS_HIP_STATIC_SCRATCH_BYTES;
+    return reduce_entry(op, chain, inputs, n_inputs, axis, out, store);
 }
 
 extern "C" int32_t chelis_hip_count(const chelis_gpu_tensor *x, int32_t axis, const chelis_gpu_tensor *out,

@@ -113,6 +113,22 @@ enum {
 };
 int32_t chelis_hip_reduce(int32_t op, const chelis_fused_chain *chain, const chelis_gpu_tensor *const *inputs,
                           int32_t n_inputs, int32_t axis, const chelis_gpu_tensor *out);
+/* Allocation-free reduction. No counterpart in the reference: for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). Same arguments, results
+ * and statuses as chelis_hip_reduce; the pass partials live in one fixed
+ * per-device array of CHELIS_HIP_STATIC_SCRATCH_BYTES (held until the
+ * process ends) instead of the library's cached scratch, and the call makes
+ * no allocation. A reduction whose partials need more than the array
+ * returns CHELIS_HIP_EDOMAIN before enqueueing anything. Every pass writes
+ * the partials it later reads, so nothing needs clearing between calls.
+ * All calls on a device share its array: calls whose work overlaps in time
+ * on one GPU (work on different streams, e.g. a captured graph replayed on
+ * another stream beside a direct call) race on it; calls enqueued on the
+ * library stream run in order. */
+#define CHELIS_HIP_STATIC_SCRATCH_BYTES (8u * 1024u * 1024u)
+int32_t chelis_hip_reduce_static(int32_t op, const chelis_fused_chain *chain, const chelis_gpu_tensor *const *inputs,
+                                 int32_t n_inputs, int32_t axis, const chelis_gpu_tensor *out);
 /* kernels.rs:375-557 count: Bool8 -> i64 over one axis. A byte that is not
  * 0/1 sets *error_code = 1 (the reference kernel's code 1); the call then
  * synchronizes to read it back. */
