@@ -129,6 +129,30 @@ SIGNATURES = {
     "transformer_block_device": (None, [POINTER(c_void_p), c_int32, POINTER(c_void_p), c_int32]),
     "mlp_train_step_device": (None, [POINTER(c_void_p), c_int32, POINTER(c_void_p), c_int32]),
     "chelis_hip_set_exact_matmul": (c_int32, [c_int32]),
+    # chelis_dag.h
+    "chelis_dag_compile": (c_void_p, [ctypes.c_char_p, c_int64]),
+    "chelis_dag_release": (None, [c_void_p]),
+    "chelis_dag_run": (c_int32, [c_void_p, POINTER(P), c_int32, POINTER(P), c_int32]),
+    "chelis_dag_input_count": (c_int32, [c_void_p]),
+    "chelis_dag_output_count": (c_int32, [c_void_p]),
+    "chelis_dag_label": (ctypes.c_char_p, [c_void_p, c_int32, c_int32]),
+    "chelis_dag_type": (c_int32, [c_void_p, c_int32, c_int32, POINTER(c_int32), POINTER(c_int64), c_int32,
+                                  POINTER(c_int32)]),
+    "chelis_dag_peak_device_bytes": (c_int64, [c_void_p]),
+    "chelis_dag_launch_count": (c_int64, [c_void_p]),
+    "chelis_dag_describe": (ctypes.c_char_p, [c_void_p]),
+    "chelis_dag_fuse": (ctypes.c_char_p, [ctypes.c_char_p, c_int64]),
+    "chelis_codegen_hip": (c_void_p, [ctypes.c_char_p, c_int64, ctypes.c_char_p]),
+    "chelis_codegen_release": (None, [c_void_p]),
+    "chelis_codegen_c_source": (ctypes.c_char_p, [c_void_p]),
+    "chelis_codegen_h_header": (ctypes.c_char_p, [c_void_p]),
+    "chelis_codegen_list_count": (c_int32, [c_void_p, c_int32]),
+    "chelis_codegen_list_item": (ctypes.c_char_p, [c_void_p, c_int32, c_int32]),
+    "chelis_codegen_peak_device_bytes_formula": (ctypes.c_char_p, [c_void_p]),
+    "chelis_codegen_peak_device_bytes_estimate": (c_int64, [c_void_p]),
+    "linreg_step": (None, [POINTER(c_void_p), ctypes.c_int, POINTER(c_void_p), ctypes.c_int]),
+    "transformer_block": (None, [POINTER(c_void_p), ctypes.c_int, POINTER(c_void_p), ctypes.c_int]),
+    "mlp_train_step": (None, [POINTER(c_void_p), ctypes.c_int, POINTER(c_void_p), ctypes.c_int]),
 }
 
 _lib = None
@@ -479,5 +503,123 @@ def device_entry(name: str, inputs, n_out: int):
     return [DeviceTensor(o) for o in outs]
 
 
+def host_entry(name: str, arrays, n_out: int):
+    """{name}(chelis_tensor **, int, chelis_tensor **, int): the reference's
+    host-tensor entry. numpy arrays in (borrowed as host tensors; a KEY input
+    is passed as ("key", bits)), numpy arrays out (copied from the returned
+    host tensors, which are then released)."""
+    keep, hosts = [], []
+    for a in arrays:
+        if isinstance(a, tuple) and a[0] == "key":
+            arr, tag = np.array(a[1] & (2**64 - 1), np.uint64), DT_KEY
+        else:
+            arr = np.ascontiguousarray(a)
+            arr, tag = (arr.view(np.uint8), DT_BOOL) if arr.dtype == np.bool_ else (arr, _NP2DT[arr.dtype])
+        shape = (c_int64 * max(1, arr.ndim))(*arr.shape)
+        keep.append((arr, shape))
+        hosts.append(lib().chelis_tensor_entry_borrow(arr.ndim, shape, tag, arr.ctypes.data, arr.nbytes))
+    ins = (c_void_p * len(hosts))(*hosts)
+    outs = (c_void_p * n_out)()
+    getattr(lib(), name)(ins, len(hosts), outs, n_out)
+    result = []
+    for o in outs:
+        rank = lib().chelis_tensor_rank(o)
+        shape = tuple(lib().chelis_tensor_shape(o, a) for a in range(rank))
+        v = lib().chelis_tensor_read_view(o)
+        dt = np.dtype(_DT2NP[v.dtype])
+        result.append(np.ctypeslib.as_array(ctypes.cast(v.data, POINTER(ctypes.c_uint8)), (v.count * dt.itemsize,))
+                      .view(dt).reshape(shape).copy() if v.count else np.zeros(shape, dt))
+        lib().chelis_tensor_release(o)
+    for h in hosts:
+        lib().chelis_tensor_release(h)
+    return result
+
+
 def set_exact_matmul(on: bool) -> bool:
     return bool(lib().chelis_hip_set_exact_matmul(1 if on else 0))
+
+
+# ---- the DAG front end (include/chelis_dag.h) ----
+class DagProgram:
+    """chelis_dag_compile / chelis_dag_run over a serde-form Chelis DAG."""
+
+    def __init__(self, json_text: str):
+        data = json_text.encode()
+        self.handle = lib().chelis_dag_compile(data, len(data))
+        if not self.handle:
+            raise ChelisError("dag compile failed: " + lib().chelis_hip_last_error().decode(errors="replace"))
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib().chelis_dag_release(self.handle)
+                self.handle = None
+        except Exception:
+            pass
+
+    def _slot(self, output: int, i: int):
+        rank, dt = c_int32(), c_int32()
+        shape = (c_int64 * 16)()
+        check(lib().chelis_dag_type(self.handle, output, i, ctypes.byref(rank), shape, 16, ctypes.byref(dt)), "dag type")
+        return tuple(shape[k] for k in range(rank.value)), dt.value
+
+    @property
+    def inputs(self):
+        n = lib().chelis_dag_input_count(self.handle)
+        return [(lib().chelis_dag_label(self.handle, 0, i).decode(),) + self._slot(0, i) for i in range(n)]
+
+    @property
+    def outputs(self):
+        n = lib().chelis_dag_output_count(self.handle)
+        return [(lib().chelis_dag_label(self.handle, 1, i).decode(),) + self._slot(1, i) for i in range(n)]
+
+    def describe(self) -> str:
+        return lib().chelis_dag_describe(self.handle).decode()
+
+    @property
+    def launches(self) -> int:
+        return lib().chelis_dag_launch_count(self.handle)
+
+    @property
+    def peak_device_bytes(self) -> int:
+        return lib().chelis_dag_peak_device_bytes(self.handle)
+
+    def empty_outputs(self):
+        return [DeviceTensor(lib().chelis_device_tensor_alloc(_plan(shape, None, dt))) for _, shape, dt in self.outputs]
+
+    def run(self, inputs, outputs=None):
+        """Enqueue on the library stream; returns the output tensors."""
+        outputs = outputs if outputs is not None else self.empty_outputs()
+        ins = (P * max(1, len(inputs)))(*[_p(t) for t in inputs])
+        outs = (P * max(1, len(outputs)))(*[_p(t) for t in outputs])
+        check(lib().chelis_dag_run(self.handle, ins, len(inputs), outs, len(outputs)), "dag run")
+        return outputs
+
+
+def dag_fuse(json_text: str) -> str:
+    """fuse.rs alone: the DAG after greedy chain fusion, in the wire form."""
+    data = json_text.encode()
+    out = lib().chelis_dag_fuse(data, len(data))
+    if out is None:
+        raise ChelisError(lib().chelis_hip_last_error().decode(errors="replace"))
+    return out.decode()
+
+
+class CodegenResult:
+    """chelis_codegen_hip: the HipCodegenResult fields."""
+
+    def __init__(self, json_text: str, func_name: str):
+        data = json_text.encode()
+        h = lib().chelis_codegen_hip(data, len(data), func_name.encode())
+        if not h:
+            raise ChelisError("codegen_hip failed: " + lib().chelis_hip_last_error().decode(errors="replace"))
+        L = lib()
+        lists = [[L.chelis_codegen_list_item(h, w, i).decode() for i in range(L.chelis_codegen_list_count(h, w))]
+                 for w in range(5)]
+        self.c_source = L.chelis_codegen_c_source(h).decode()
+        self.h_header = L.chelis_codegen_h_header(h).decode()
+        self.compile_flags, self.link_flags, self.input_labels, self.output_labels, self.symbolic_dims = lists
+        self.peak_device_bytes_formula = L.chelis_codegen_peak_device_bytes_formula(h).decode()
+        est = L.chelis_codegen_peak_device_bytes_estimate(h)
+        self.peak_device_bytes_estimate = None if est < 0 else est
+        L.chelis_codegen_release(h)

@@ -1,0 +1,201 @@
+// The DAG front end: reads a lowered or fused Chelis RISC DAG in the
+// reference's serde JSON shape, forms launch regions, plans their memory and
+// runs them through this library's region launchers (include/chelis_dag.h).
+//
+// Pipeline (each stage in its own file):
+//   dag_json.cpp    JSON text <-> Json values
+//   dag_read.cpp    Json -> Graph (the reference's Dag / DagNode / RiscOp
+//                   wire form, crates/chelis-dag-core/src/dag.rs:835-1352,
+//                   2364-2400, 2913-2919) and Graph -> JSON
+//   dag_fuse.cpp    fuse.rs's greedy single-consumer chains and the
+//                   reduction-inlined chain set (crates/chelis-dag-core/src/
+//                   fuse.rs:32-487), plus the inverse (a FusedElem back to
+//                   its primitive nodes) so patterns see one form
+//   dag_plan.cpp    region formation (matmul + epilogue, softmax, masked
+//                   softmax, softmax adjoint, layer norm, GELU, dropout,
+//                   reductions, chains), output layouts and the slot plan
+//   dag_exec.cpp    packets at run time and the launches; the C ABI
+//   dag_codegen.cpp host source for `{f}` / `{f}_device` over the same plan
+#pragma once
+
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "chelis_hip.h"
+
+namespace chelis {
+namespace dag {
+
+// ---------------------------------------------------------------- JSON
+struct Json {
+    enum Kind { Null, Bool, Number, String, Array, Object } kind = Null;
+    bool boolean = false;
+    std::string text;  // number spelling or string value
+    std::vector<Json> items;
+    std::vector<std::pair<std::string, Json>> fields;
+
+    const Json *get(const char *key) const;
+    bool is_int() const;
+    int64_t as_int() const;  // caller checks is_int()
+    double as_double() const;
+};
+// Parses `n` bytes; on failure returns false and describes the position.
+bool parse_json(const char *s, size_t n, Json *out, std::string *error);
+void write_json(const Json &v, std::string *out);
+std::string json_quote(const std::string &s);
+
+// ---------------------------------------------------------------- IR
+enum class Prim : uint8_t { F32, F64, F16, Bf16, Int8, Int16, Int32, Int64, Bool, Key, Other };
+const char *prim_name(Prim p);
+int64_t prim_width(Prim p);
+chelis_dtype prim_dtype(Prim p);
+bool prim_is_float(Prim p);
+
+enum class Op : uint8_t {
+    // leaves
+    Load, Const, Iota,
+    // elementwise ops fuse.rs folds into chains (fused_step_op, fuse.rs:98-127)
+    Add, Sub, Mul, Div, Pow, FloorDiv, TruncDiv, MaxElem, MinElem, Neg, Recip, Exp, Log, Sin, Sqrt, Cos, Tan,
+    Atan, Tanh, Erf, Erfc, Abs, Floor, Ceil, Round,
+    // elementwise ops that stay their own node
+    Relu, ReluAdjoint, Where, Compare, Dropout, DropoutReplay, Cast,
+    // reductions over one axis
+    Sum, MaxReduce, MinReduce, ProdReduce, Argmax, Argmin, Count, Softmax,
+    // movement
+    Expand, Permute, Reshape, Realize, Copy,
+    // fused and specialized forms
+    FusedElem, BlasMatmul,
+    // anything else the reader does not interpret
+    Other
+};
+const char *op_name(Op op);
+bool op_is_chain_step(Op op);  // fuse.rs's fusible elementwise table
+
+// One step of a FusedElem: its op and its inputs, each an external input
+// (>= 0) or a previous step k (encoded -(k + 1)), as FusedInput::External /
+// FusedInput::PreviousStep.
+struct Step {
+    Op op = Op::Other;
+    std::vector<int> args;
+};
+
+struct Node {
+    int64_t id = 0;
+    Op op = Op::Other;
+    std::string variant;  // the op's variant name on the wire
+    std::vector<int64_t> inputs, shape_deps, claim_deps;
+    std::vector<int64_t> dims;  // extents (-1: known only at run time)
+    Prim prec = Prim::Other;
+    int64_t reusable = -1;
+    bool has_span = false;
+    std::string span;
+    std::vector<std::string> merged_spans;
+    int64_t owner_decl = 0, owner_activation = -1;
+    // op fields
+    int64_t axis = 0;               // Sum / MaxReduce / ... / Expand / Softmax
+    std::vector<int64_t> axes;      // Permute / Count
+    Prim accumulator = Prim::Other; // Sum
+    int64_t size = -1;              // Expand (literal size, -1 otherwise)
+    std::vector<int64_t> new_shape; // Reshape (literal extents, -1 otherwise)
+    std::string name;               // Load
+    std::string compare;            // Compare kind (snake_case wire name)
+    Prim const_prec = Prim::Other;  // Const
+    uint64_t const_bits = 0;        // float bits, or the integer / bool value
+    std::vector<Step> steps;        // FusedElem
+    Prim cast_to = Prim::Other;     // Cast
+    std::string raw_op;             // the op as read (written back verbatim)
+
+    int64_t count() const;  // elements (-1 if any extent is unknown)
+    double const_value() const;
+};
+
+struct Graph {
+    std::vector<Node> nodes;  // ids are positions, inputs precede users
+    std::vector<int64_t> roots;
+    std::string declarations = "[]";  // JSON text, carried through
+};
+
+// Reads the reference's serde Dag; returns false with a message naming the
+// offending node on any structural problem.
+bool read_graph(const char *json, size_t n, Graph *g, std::string *error);
+std::string write_graph(const Graph &g);
+
+// ---------------------------------------------------------------- fusion
+// fuse.rs:36-121: consumer counts (roots count as consumers), maximal chains
+// of fusible float elementwise nodes where each link is its producer's only
+// consumer and shares its owner, chains of length >= 2 rebuilt as FusedElem
+// nodes. old_to_new maps every old node to its node in the result.
+Graph fuse(const Graph &g, std::vector<int64_t> *old_to_new);
+// fuse.rs:463-487: FusedElem nodes whose only consumer is a Sum or
+// MaxReduce (they become that reduction's leaf).
+std::vector<bool> reduction_inlined(const Graph &g);
+// A FusedElem written back as its primitive nodes (inverse of fuse).
+Graph unfuse(const Graph &g);
+std::vector<int64_t> consumer_counts(const Graph &g);
+
+// ---------------------------------------------------------------- plan
+// A region is one launch. Its inputs are values (node ids); a value is
+// either a caller input, a constant, a view of another value, or a
+// materialized region output.
+enum class RegionKind : uint8_t {
+    Chain, Reduce, Count, Softmax, MaskedSoftmax, SoftmaxAdjoint, LayerNorm, Gelu, Relu, ReluAdjoint, Dropout,
+    Matmul, Copy
+};
+const char *region_kind_name(RegionKind k);
+
+struct Region {
+    RegionKind kind = RegionKind::Chain;
+    int64_t out = -1;                 // the node whose value the launch produces
+    std::vector<int64_t> in;          // value nodes read
+    std::vector<int64_t> covers;      // every node the region computes
+    chelis_fused_chain chain{};       // Chain / Reduce leaf
+    bool has_chain = false;
+    int32_t reduce_op = CHELIS_REDUCE_SUM;
+    int64_t axis = 0;
+    double scale = 1.0, epsilon = 0.0, rate = 0.0;
+    int32_t causal = 0;
+    bool replay = false;
+    // matmul: in = {a, b[, bias][, residual]}
+    bool has_bias = false, has_residual = false;
+    int32_t activation = CHELIS_ACT_NONE;
+    int32_t causal_mode = 0;  // 1: skip tiles above the diagonal, 2: clip the contraction
+};
+
+// How a value's storage is found at run time.
+enum class Storage : uint8_t { Input, Const, View, Slot, Output, Inlined };
+struct ValueInfo {
+    Storage storage = Storage::Inlined;
+    int64_t input = -1, output = -1;  // caller slot indices
+    int64_t base = -1;                // View: the value it views
+    int64_t slot = -1;                // Slot: workspace slot
+    int64_t const_index = -1;         // Const: constant pool entry
+    // physical order of a materialized value: perm[i] = the logical axis
+    // stored i-th (outermost first); empty = row-major
+    std::vector<int64_t> layout;
+};
+
+struct Slot {
+    int64_t offset = 0, bytes = 0;
+};
+
+struct Plan {
+    Graph graph;  // the unfused graph the regions refer to
+    std::vector<Region> regions;
+    std::vector<ValueInfo> values;  // per node
+    std::vector<int64_t> input_nodes, output_nodes;
+    std::vector<std::string> input_labels, output_labels;
+    std::vector<Slot> slots;
+    int64_t workspace_bytes = 0;
+    std::vector<uint64_t> const_bits;  // one element per constant, stored at its dtype width
+    std::vector<Prim> const_prec;
+    int64_t peak_device_bytes = 0;     // workspace + constants + outputs
+};
+
+bool build_plan(const Graph &input, Plan *plan, std::string *error);
+std::string describe_plan(const Plan &plan);
+
+}  // namespace dag
+}  // namespace chelis

@@ -1,0 +1,441 @@
+// Running a planned DAG (include/chelis_dag.h): every value's packet is
+// derived at run time (inputs are the caller's packets with their own
+// strides; movement ops become views of them), intermediates are carved
+// from one stream-ordered workspace, and each region is one call of this
+// library's launchers on the library stream.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+
+#include "chelis_dag.h"
+#include "dag.h"
+#include "gemm.h"
+#include "hip_common.h"
+
+struct chelis_dag_program {
+    chelis::dag::Plan plan;
+    std::string description;
+    std::mutex mutex;
+    void *constants[64] = {};  // the constant pool on each device, uploaded on first use
+    ~chelis_dag_program() {
+        int here = -1;
+        if (hipGetDevice(&here) != hipSuccess) return;
+        for (int d = 0; d < 64; ++d) {
+            if (!constants[d]) continue;
+            if (hipSetDevice(d) == hipSuccess) (void)hipFree(constants[d]);
+        }
+        (void)hipSetDevice(here);
+    }
+};
+
+namespace chelis {
+namespace dag {
+namespace {
+
+struct Packet {
+    std::vector<int64_t> shape, strides;
+    chelis_gpu_tensor t{};
+    bool live = false;
+    void seal() {
+        t.shape = shape.data();
+        t.strides = strides.data();
+        t.rank = (int32_t)shape.size();
+        int64_t c = 1;
+        for (int64_t e : shape) c *= e;
+        t.count = c;
+    }
+};
+
+int64_t span_elements(const Packet &p) {
+    int64_t s = 0;
+    for (size_t a = 0; a < p.shape.size(); ++a) {
+        if (p.shape[a] == 0) return 0;
+        s += (p.shape[a] - 1) * p.strides[a];
+    }
+    return s + 1;
+}
+
+// A view of `in` with `shape`, if one exists without moving data.
+bool reshape_view(const Packet &in, const std::vector<int64_t> &shape, std::vector<int64_t> *strides) {
+    strides->assign(shape.size(), 0);
+    int64_t count = 1;
+    for (int64_t e : shape) count *= e;
+    if (count == 0 || count == 1) {
+        int64_t acc = 1;
+        for (size_t a = shape.size(); a-- > 0;) {
+            (*strides)[a] = acc;
+            acc *= std::max<int64_t>(shape[a], 1);
+        }
+        return true;
+    }
+    std::vector<int64_t> os, ost;
+    for (size_t a = 0; a < in.shape.size(); ++a)
+        if (in.shape[a] != 1) {
+            os.push_back(in.shape[a]);
+            ost.push_back(in.strides[a]);
+        }
+    size_t oi = 0, ni = 0;
+    while (ni < shape.size() && oi < os.size()) {
+        int64_t np = shape[ni], op = os[oi];
+        size_t nj = ni + 1, oj = oi + 1;
+        while (np != op) {
+            if (np < op) {
+                if (nj >= shape.size()) return false;
+                np *= shape[nj++];
+            } else {
+                if (oj >= os.size()) return false;
+                op *= os[oj++];
+            }
+        }
+        for (size_t k = oi; k + 1 < oj; ++k)
+            if (ost[k] != ost[k + 1] * os[k + 1]) return false;
+        (*strides)[nj - 1] = ost[oj - 1];
+        for (size_t k = nj - 1; k > ni; --k) (*strides)[k - 1] = (*strides)[k] * shape[k];
+        ni = nj;
+        oi = oj;
+    }
+    for (; ni < shape.size(); ++ni) (*strides)[ni] = 1;  // trailing extent-1 axes
+    return oi == os.size();
+}
+
+bool type_matches(const Node &n, const chelis_gpu_tensor *t) {
+    if (!t || t->rank != (int32_t)n.dims.size() || t->dtype != prim_dtype(n.prec)) return false;
+    for (size_t a = 0; a < n.dims.size(); ++a)
+        if (n.dims[a] >= 0 && t->shape[a] != n.dims[a]) return false;
+    return true;
+}
+
+int32_t constant_pool(chelis_dag_program *prog, void **pool) {
+    int device = 0;
+    CHELIS_HIP_TRY(hipGetDevice(&device));
+    if (device < 0 || device >= 64) return set_error(CHELIS_HIP_EHIP, "dag: device %d outside 0..63", device);
+    std::lock_guard<std::mutex> lock(prog->mutex);
+    const Plan &P = prog->plan;
+    if (!prog->constants[device] && !P.const_bits.empty()) {
+        std::vector<uint64_t> cells(P.const_bits.size());
+        for (size_t k = 0; k < cells.size(); ++k) {
+            const int64_t w = prim_width(P.const_prec[k]);
+            uint64_t v = P.const_bits[k];
+            cells[k] = w >= 8 ? v : (v & ((uint64_t(1) << (8 * w)) - 1));  // little-endian: low bytes first
+        }
+        void *p = nullptr;
+        CHELIS_HIP_TRY(hipMalloc(&p, cells.size() * 8));
+        const hipError_t e = hipMemcpy(p, cells.data(), cells.size() * 8, hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            (void)hipFree(p);
+            return set_error(CHELIS_HIP_EHIP, "dag: constant upload: %s", hipGetErrorString(e));
+        }
+        prog->constants[device] = p;
+    }
+    *pool = prog->constants[device];
+    return CHELIS_HIP_OK;
+}
+
+const chelis_fused_chain &identity_chain() {
+    // max_elem(a, a) selects a's stored bits (NaN payloads and -0 included)
+    static const chelis_fused_chain c = [] {
+        chelis_fused_chain x{};
+        x.n_steps = 1;
+        x.steps[0].op = CHELIS_FUSED_MAX_ELEM;
+        return x;
+    }();
+    return c;
+}
+
+int32_t run_plan(chelis_dag_program *prog, const chelis_gpu_tensor *const *inputs, int32_t n_in,
+                 const chelis_gpu_tensor *const *outputs, int32_t n_out) {
+    const Plan &P = prog->plan;
+    const Graph &g = P.graph;
+    if (n_in != (int32_t)P.input_nodes.size() || n_out != (int32_t)P.output_nodes.size())
+        return set_error(CHELIS_HIP_EDOMAIN, "dag: expected %zu inputs and %zu outputs, got %d and %d",
+                         P.input_nodes.size(), P.output_nodes.size(), n_in, n_out);
+    if ((n_in && !inputs) || (n_out && !outputs)) return set_error(CHELIS_HIP_EDOMAIN, "dag: null packet array");
+    for (int32_t i = 0; i < n_in; ++i) {
+        if (int32_t s = check_tensor(inputs[i], "dag input")) return s;
+        if (!type_matches(g.nodes[P.input_nodes[i]], inputs[i]))
+            return set_error(CHELIS_HIP_EDOMAIN, "dag: input %d (%s) does not have the program's shape and dtype", i,
+                             P.input_labels[i].c_str());
+    }
+    for (int32_t o = 0; o < n_out; ++o) {
+        if (int32_t s = check_tensor(outputs[o], "dag output")) return s;
+        if (!type_matches(g.nodes[P.output_nodes[o]], outputs[o]))
+            return set_error(CHELIS_HIP_EDOMAIN, "dag: output %d (%s) does not have the program's shape and dtype", o,
+                             P.output_labels[o].c_str());
+    }
+    hipStream_t st = stream();
+    if (!st) return set_error(CHELIS_HIP_EHIP, "no HIP device");
+    void *pool = nullptr;
+    if (int32_t s = constant_pool(prog, &pool)) return s;
+    char *ws = nullptr;
+    if (P.workspace_bytes) {
+        ws = static_cast<char *>(scratch_alloc((size_t)P.workspace_bytes));
+        if (!ws) return set_error(CHELIS_HIP_EHIP, "dag: cannot allocate a %lld-byte workspace",
+                                  (long long)P.workspace_bytes);
+    }
+    struct Release {
+        char *p;
+        size_t n;
+        ~Release() { scratch_free(p, n); }
+    } release{ws, (size_t)P.workspace_bytes};
+    // ---- packets
+    std::vector<Packet> pk(g.nodes.size());
+    auto from = [](Packet &p, const chelis_gpu_tensor *t) {
+        p.shape.assign(t->shape, t->shape + t->rank);
+        p.strides.assign(t->strides, t->strides + t->rank);
+        p.t = *t;
+        p.t.ownership = 0;
+        p.live = true;
+        p.seal();
+    };
+    for (const Node &n : g.nodes) {
+        const ValueInfo &v = P.values[n.id];
+        Packet &p = pk[n.id];
+        switch (v.storage) {
+            case Storage::Input: from(p, inputs[v.input]); break;
+            case Storage::Const:
+                p.shape = n.dims;
+                p.strides.assign(n.dims.size(), 0);
+                p.t.data = static_cast<char *>(pool) + 8 * v.const_index;
+                p.t.byte_capacity = 8;
+                p.t.dtype = prim_dtype(n.prec);
+                p.live = true;
+                p.seal();
+                break;
+            case Storage::Slot: {
+                const Slot &s = P.slots[v.slot];
+                p.shape = n.dims;
+                p.strides.assign(n.dims.size(), 0);
+                // dense in the stored order: layout[i] is the axis stored i-th
+                int64_t acc = 1;
+                if (v.layout.empty()) {
+                    for (size_t a = n.dims.size(); a-- > 0;) {
+                        p.strides[a] = acc;
+                        acc *= std::max<int64_t>(n.dims[a], 1);
+                    }
+                } else {
+                    for (size_t i = v.layout.size(); i-- > 0;) {
+                        p.strides[v.layout[i]] = acc;
+                        acc *= std::max<int64_t>(n.dims[v.layout[i]], 1);
+                    }
+                }
+                p.t.data = ws + s.offset;
+                p.t.byte_capacity = s.bytes;
+                p.t.dtype = prim_dtype(n.prec);
+                p.live = true;
+                p.seal();
+                break;
+            }
+            case Storage::Output: {
+                Packet out;
+                from(out, outputs[v.output]);
+                if (v.base == n.id) {
+                    p = out;
+                    p.seal();
+                } else {
+                    p.t = out.t;
+                    p.shape = n.dims;
+                    if (!reshape_view(out, n.dims, &p.strides))
+                        return set_error(CHELIS_HIP_EUNSUPPORTED, "dag: output %lld is too strided to take node %lld",
+                                         (long long)v.output, (long long)n.id);
+                    p.live = true;
+                    p.seal();
+                }
+                break;
+            }
+            case Storage::View: {
+                const Packet &b = pk[v.base];
+                if (!b.live) return set_error(CHELIS_HIP_EUNSUPPORTED, "dag: node %lld views a value with no storage",
+                                              (long long)n.id);
+                p.t = b.t;
+                p.shape = n.dims;
+                switch (n.op) {
+                    case Op::Expand:
+                        p.strides = b.strides;
+                        p.strides.insert(p.strides.begin() + n.axis, 0);
+                        break;
+                    case Op::Permute:
+                        p.strides.resize(n.axes.size());
+                        for (size_t a = 0; a < n.axes.size(); ++a) p.strides[a] = b.strides[n.axes[a]];
+                        break;
+                    case Op::Reshape:
+                        if (!reshape_view(b, n.dims, &p.strides))
+                            return set_error(CHELIS_HIP_EUNSUPPORTED,
+                                             "dag: node %lld reshapes a view that is not one run of memory",
+                                             (long long)n.id);
+                        break;
+                    default:  // Realize / Copy: the same bytes
+                        p.strides = b.strides;
+                        break;
+                }
+                p.live = true;
+                p.seal();
+                break;
+            }
+            default: break;
+        }
+        if (p.live && span_elements(p) * prim_width(n.prec) > p.t.byte_capacity && p.t.count)
+            return set_error(CHELIS_HIP_EUNSUPPORTED, "dag: node %lld's view reaches past its storage", (long long)n.id);
+    }
+    // ---- launches
+    for (const Region &r : P.regions) {
+        std::vector<const chelis_gpu_tensor *> in;
+        for (int64_t id : r.in) in.push_back(&pk[id].t);
+        const chelis_gpu_tensor *out = &pk[r.out].t;
+        int32_t s = CHELIS_HIP_OK;
+        switch (r.kind) {
+            case RegionKind::Chain:
+                s = chelis_hip_fused_elementwise(&r.chain, in.data(), (int32_t)in.size(), out);
+                break;
+            case RegionKind::Reduce:
+                s = chelis_hip_reduce(r.reduce_op, r.has_chain ? &r.chain : nullptr, in.data(), (int32_t)in.size(),
+                                      (int32_t)r.axis, out);
+                break;
+            case RegionKind::Count: {
+                int32_t code = 0;
+                s = chelis_hip_count(in[0], (int32_t)r.axis, out, &code);
+                if (!s && code) s = set_error(CHELIS_HIP_EDOMAIN, "dag: count read a byte that is not 0 or 1");
+                break;
+            }
+            case RegionKind::Softmax: s = chelis_hip_softmax(in[0], out); break;
+            case RegionKind::MaskedSoftmax:
+                s = chelis_hip_scaled_masked_softmax(in[0], r.scale, r.causal, out);
+                break;
+            case RegionKind::SoftmaxAdjoint: s = chelis_hip_softmax_adjoint(in[0], in[1], out); break;
+            case RegionKind::LayerNorm: s = chelis_hip_layer_norm(in[0], in[1], in[2], r.epsilon, out); break;
+            case RegionKind::Gelu: s = chelis_hip_gelu(in[0], out); break;
+            case RegionKind::Relu: s = chelis_hip_relu(in[0], out); break;
+            case RegionKind::ReluAdjoint: s = chelis_hip_relu_adjoint(in[0], in[1], out); break;
+            case RegionKind::Dropout:
+                s = dropout_device_key(static_cast<const uint64_t *>(in[1]->data), in[0], r.rate, out);
+                break;
+            case RegionKind::Matmul: {
+                const chelis_gpu_tensor *bias = r.has_bias ? in[2] : nullptr;
+                const chelis_gpu_tensor *res = r.has_residual ? in[r.has_bias ? 3 : 2] : nullptr;
+                if (r.causal_mode && !bias && !res && r.activation == CHELIS_ACT_NONE)
+                    s = matmul_causal(in[0], in[1], out, r.causal_mode);
+                else if (bias || res || r.activation != CHELIS_ACT_NONE)
+                    s = chelis_hip_linear(in[0], in[1], bias, r.activation, res, out, 0);
+                else
+                    s = chelis_hip_matmul(in[0], in[1], out, 0);
+                break;
+            }
+            case RegionKind::Copy: {
+                const chelis_gpu_tensor *dst = outputs[r.axis];
+                s = chelis_hip_fused_elementwise(&identity_chain(), in.data(), 1, dst);
+                break;
+            }
+        }
+        if (s) return s;
+    }
+    return CHELIS_HIP_OK;
+}
+
+}  // namespace
+}  // namespace dag
+}  // namespace chelis
+
+using namespace chelis;
+using namespace chelis::dag;
+
+namespace {
+thread_local std::string g_text;
+}
+
+extern "C" chelis_dag_program *chelis_dag_compile(const char *json, int64_t length) {
+    if (!json || length < 0) {
+        set_error(CHELIS_HIP_EDOMAIN, "dag: null or negative-length text");
+        return nullptr;
+    }
+    try {
+        Graph g;
+        std::string error;
+        if (!read_graph(json, (size_t)length, &g, &error)) {
+            set_error(CHELIS_HIP_EDOMAIN, "dag: %s", error.c_str());
+            return nullptr;
+        }
+        auto *prog = new chelis_dag_program();
+        if (!build_plan(g, &prog->plan, &error)) {
+            delete prog;
+            set_error(CHELIS_HIP_EUNSUPPORTED, "dag: %s", error.c_str());
+            return nullptr;
+        }
+        prog->description = describe_plan(prog->plan);
+        return prog;
+    } catch (const std::exception &e) {
+        set_error(CHELIS_HIP_EHIP, "dag: %s", e.what());
+        return nullptr;
+    }
+}
+
+extern "C" void chelis_dag_release(chelis_dag_program *program) { delete program; }
+
+extern "C" int32_t chelis_dag_run(chelis_dag_program *program, const chelis_gpu_tensor *const *inputs, int32_t n_in,
+                                  const chelis_gpu_tensor *const *outputs, int32_t n_out) {
+    if (!program) return set_error(CHELIS_HIP_EDOMAIN, "dag: null program");
+    try {
+        return run_plan(program, inputs, n_in, outputs, n_out);
+    } catch (const std::exception &e) {
+        return set_error(CHELIS_HIP_EHIP, "dag: %s", e.what());
+    }
+}
+
+extern "C" int32_t chelis_dag_input_count(const chelis_dag_program *p) {
+    return p ? (int32_t)p->plan.input_nodes.size() : -1;
+}
+extern "C" int32_t chelis_dag_output_count(const chelis_dag_program *p) {
+    return p ? (int32_t)p->plan.output_nodes.size() : -1;
+}
+
+namespace {
+const Node *slot_node(const chelis_dag_program *p, int32_t output, int32_t index) {
+    if (!p) return nullptr;
+    const auto &ids = output ? p->plan.output_nodes : p->plan.input_nodes;
+    if (index < 0 || index >= (int32_t)ids.size()) return nullptr;
+    return &p->plan.graph.nodes[ids[index]];
+}
+}  // namespace
+
+extern "C" const char *chelis_dag_label(const chelis_dag_program *p, int32_t output, int32_t index) {
+    if (!slot_node(p, output, index)) return nullptr;
+    return (output ? p->plan.output_labels : p->plan.input_labels)[index].c_str();
+}
+
+extern "C" int32_t chelis_dag_type(const chelis_dag_program *p, int32_t output, int32_t index, int32_t *rank,
+                                   int64_t *shape, int32_t shape_capacity, int32_t *dtype) {
+    const Node *n = slot_node(p, output, index);
+    if (!n) return set_error(CHELIS_HIP_EDOMAIN, "dag: no such slot");
+    if (rank) *rank = (int32_t)n->dims.size();
+    if (shape)
+        for (int32_t a = 0; a < (int32_t)n->dims.size() && a < shape_capacity; ++a) shape[a] = n->dims[a];
+    if (dtype) *dtype = prim_dtype(n->prec);
+    return CHELIS_HIP_OK;
+}
+
+extern "C" int64_t chelis_dag_peak_device_bytes(const chelis_dag_program *p) {
+    return p ? p->plan.peak_device_bytes : -1;
+}
+
+extern "C" int64_t chelis_dag_launch_count(const chelis_dag_program *p) {
+    return p ? (int64_t)p->plan.regions.size() : -1;
+}
+
+extern "C" const char *chelis_dag_describe(const chelis_dag_program *p) { return p ? p->description.c_str() : ""; }
+
+extern "C" const char *chelis_dag_fuse(const char *json, int64_t length) {
+    if (!json || length < 0) {
+        set_error(CHELIS_HIP_EDOMAIN, "dag: null or negative-length text");
+        return nullptr;
+    }
+    Graph g;
+    std::string error;
+    if (!read_graph(json, (size_t)length, &g, &error)) {
+        set_error(CHELIS_HIP_EDOMAIN, "dag: %s", error.c_str());
+        return nullptr;
+    }
+    g_text = write_graph(fuse(g, nullptr));
+    return g_text.c_str();
+}

@@ -1,0 +1,978 @@
+// Region formation and memory planning for a lowered Chelis DAG.
+//
+// The reference's HIP emitter launches one kernel per fused node
+// (crates/chelis-backend-hip/src/emit.rs:2472-3048) after fuse.rs's linear
+// chains, so a softmax is four launches and a layer norm eight. Here the
+// lowered forms the compiler writes are recognized whole and given to this
+// library's region kernels:
+//   matmul      Sum{L+1}(Mul(Expand{L+2}(a), Expand{L}(b))) (tier2.rs:706-857,
+//               blas.rs:25-104) or BlasMatmul, with a following bias add,
+//               relu or GELU graph and residual add folded into its epilogue
+//   softmax     decompose_softmax (tier2.rs:1098-1178) over the last axis
+//   masked      softmax(where(causal mask, s * scale, -inf)) (spec/05 4.7)
+//   adjoint     y * (g - sum(g * y)) (grad.rs:2248)
+//   layer norm  lower_layer_norm (tier2.rs:1248-1360)
+//   gelu        activation.rs:145-149,183-276
+// A pattern is taken only when every node it covers, other than its result,
+// is read by nothing outside it (so nothing is computed twice); constants
+// and inputs are shared freely. Everything else runs as fuse.rs would group
+// it: maximal single-consumer chains of float elementwise ops (one
+// FusedElem launch each), a chain or single elementwise node read only by a
+// Sum / MaxReduce becomes that reduction's leaf (fuse.rs:463-487), and the
+// remaining ops one launch each. Movement ops are views.
+//
+// The slot plan gives every materialized intermediate a 256-byte aligned
+// range of one workspace, reusing a range once its last reader has been
+// enqueued (the greedy non-overlapping reuse of spec/08-backends.md:285-297,
+// crates/chelis-backend-hip/src/memory.rs:32-182).
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <set>
+
+#include "dag.h"
+
+namespace chelis {
+namespace dag {
+
+const char *region_kind_name(RegionKind k) {
+    switch (k) {
+        case RegionKind::Chain: return "chain";
+        case RegionKind::Reduce: return "reduce";
+        case RegionKind::Count: return "count";
+        case RegionKind::Softmax: return "softmax";
+        case RegionKind::MaskedSoftmax: return "masked_softmax";
+        case RegionKind::SoftmaxAdjoint: return "softmax_adjoint";
+        case RegionKind::LayerNorm: return "layer_norm";
+        case RegionKind::Gelu: return "gelu";
+        case RegionKind::Relu: return "relu";
+        case RegionKind::ReluAdjoint: return "relu_adjoint";
+        case RegionKind::Dropout: return "dropout";
+        case RegionKind::Matmul: return "matmul";
+        case RegionKind::Copy: return "copy";
+    }
+    return "?";
+}
+
+namespace {
+
+// ---------------------------------------------------------------- templates
+// A template is a small graph in the shape a lowering writes, with numbered
+// placeholders for the values it reads. match() maps it onto the DAG node
+// for node (a template node may map to a node another template node also
+// maps to, since the compiler may share equal constants).
+struct TNode {
+    Op op = Op::Other;
+    int placeholder = -1;
+    bool any_const = false;  // a Const of this type whatever its value
+    std::vector<int> in;
+    std::vector<int64_t> dims;
+    Prim prec = Prim::Other;
+    int64_t axis = 0, size = -1;
+    std::vector<int64_t> axes;
+    std::string compare;
+    uint64_t bits = 0;
+};
+
+struct Template {
+    std::vector<TNode> t;
+    int add(TNode n) {
+        t.push_back(std::move(n));
+        return (int)t.size() - 1;
+    }
+    int ph(int k, std::vector<int64_t> dims, Prim p) {
+        TNode n;
+        n.placeholder = k;
+        n.dims = std::move(dims);
+        n.prec = p;
+        return add(n);
+    }
+    int op(Op o, std::vector<int> in, std::vector<int64_t> dims, Prim p) {
+        TNode n;
+        n.op = o;
+        n.in = std::move(in);
+        n.dims = std::move(dims);
+        n.prec = p;
+        return add(n);
+    }
+    const TNode &at(int k) const { return t[k]; }
+    int bin(Op o, int a, int b) { return op(o, {a, b}, t[a].dims, t[a].prec); }
+    int un(Op o, int a) { return op(o, {a}, t[a].dims, t[a].prec); }
+    int cnst(double v, std::vector<int64_t> dims, Prim p) {
+        TNode n;
+        n.op = Op::Const;
+        n.dims = std::move(dims);
+        n.prec = p;
+        if (p == Prim::F32) {
+            const float f = (float)v;
+            uint32_t b;
+            std::memcpy(&b, &f, 4);
+            n.bits = b;
+        } else if (p == Prim::F64) {
+            std::memcpy(&n.bits, &v, 8);
+        } else {
+            n.bits = (uint64_t)(int64_t)v;
+        }
+        return add(n);
+    }
+    int any_const(std::vector<int64_t> dims, Prim p) {
+        TNode n;
+        n.op = Op::Const;
+        n.any_const = true;
+        n.dims = std::move(dims);
+        n.prec = p;
+        return add(n);
+    }
+    int expand(int x, int64_t axis, int64_t size) {
+        std::vector<int64_t> d = t[x].dims;
+        d.insert(d.begin() + axis, size);
+        TNode n;
+        n.op = Op::Expand;
+        n.in = {x};
+        n.dims = d;
+        n.prec = t[x].prec;
+        n.axis = axis;
+        n.size = size;
+        return add(n);
+    }
+    // tier2.rs:629-680: insert axes at 0 until the rank matches
+    int expand_to(int x, const std::vector<int64_t> &target) {
+        while (t[x].dims.size() < target.size()) {
+            const size_t missing = target.size() - t[x].dims.size();
+            x = expand(x, 0, target[missing - 1]);
+        }
+        return x;
+    }
+    int reduce(Op o, int x, int64_t axis) {
+        std::vector<int64_t> d = t[x].dims;
+        d.erase(d.begin() + axis);
+        TNode n;
+        n.op = o;
+        n.in = {x};
+        n.dims = d;
+        n.prec = t[x].prec;
+        n.axis = axis;
+        return add(n);
+    }
+    int mean(int x, int64_t axis) {
+        const int s = reduce(Op::Sum, x, axis);
+        const int c = cnst((double)t[x].dims[axis], t[s].dims, t[x].prec);
+        return bin(Op::Div, s, c);
+    }
+    int softmax(int x, int64_t axis) {
+        const int64_t n = t[x].dims[axis];
+        const int m = reduce(Op::MaxReduce, x, axis);
+        const int e = un(Op::Exp, bin(Op::Sub, x, expand(m, axis, n)));
+        const int s = reduce(Op::Sum, e, axis);
+        return bin(Op::Div, e, expand(s, axis, n));
+    }
+};
+
+struct Binding {
+    std::vector<int64_t> map, ph;
+};
+
+bool match_node(const Template &T, int ti, const Graph &g, int64_t d, Binding &b) {
+    if (b.map[ti] >= 0) return b.map[ti] == d;
+    const TNode &t = T.at(ti);
+    const Node &n = g.nodes[d];
+    if (t.placeholder >= 0) {
+        if (b.ph[t.placeholder] >= 0 && b.ph[t.placeholder] != d) return false;
+        if (!t.dims.empty() && n.dims != t.dims) return false;
+        if (t.prec != Prim::Other && n.prec != t.prec) return false;
+        b.ph[t.placeholder] = d;
+        b.map[ti] = d;
+        return true;
+    }
+    if (n.op != t.op || n.inputs.size() != t.in.size() || n.dims != t.dims || n.prec != t.prec) return false;
+    switch (t.op) {
+        case Op::Sum: case Op::MaxReduce: if (n.axis != t.axis) return false; break;
+        case Op::Expand: if (n.axis != t.axis || n.size != t.size) return false; break;
+        case Op::Permute: if (n.axes != t.axes) return false; break;
+        case Op::Compare: if (n.compare != t.compare) return false; break;
+        case Op::Const: if (!t.any_const && (n.const_prec != t.prec || n.const_bits != t.bits)) return false; break;
+        default: break;
+    }
+    b.map[ti] = d;
+    for (size_t k = 0; k < t.in.size(); ++k)
+        if (!match_node(T, t.in[k], g, n.inputs[k], b)) return false;
+    return true;
+}
+
+bool match(const Template &T, int root, const Graph &g, int64_t d, int n_ph, Binding *b) {
+    b->map.assign(T.t.size(), -1);
+    b->ph.assign((size_t)n_ph, -1);
+    return match_node(T, root, g, d, *b);
+}
+
+// ---------------------------------------------------------------- planner state
+struct Planner {
+    const Graph &g;
+    std::vector<int64_t> counts;
+    std::vector<std::vector<int64_t>> users;  // data consumers (inputs), each once, in node order
+    std::vector<bool> is_root;
+    std::vector<int> claimed;                 // region index, -1 free
+    std::vector<Region> regions;
+    std::string error;
+
+    explicit Planner(const Graph &graph) : g(graph) {
+        counts = consumer_counts(g);
+        users.resize(g.nodes.size());
+        is_root.assign(g.nodes.size(), false);
+        for (int64_t r : g.roots) is_root[r] = true;
+        for (const Node &n : g.nodes)
+            for (int64_t i : n.inputs)
+                if (users[i].empty() || users[i].back() != n.id) users[i].push_back(n.id);
+        claimed.assign(g.nodes.size(), -1);
+    }
+    const Node &N(int64_t id) const { return g.nodes[id]; }
+    bool free_leaf(int64_t id) const { return N(id).op == Op::Load || N(id).op == Op::Const; }
+
+    // Every node of `cover` other than `out` and the free leaves is read
+    // only inside `cover`, is no root, and is not yet in a region.
+    bool closed(const std::set<int64_t> &cover, int64_t out) const {
+        for (int64_t id : cover) {
+            if (claimed[id] >= 0) return false;
+            if (id == out || free_leaf(id)) continue;
+            if (is_root[id]) return false;
+            for (int64_t u : users[id])
+                if (!cover.count(u)) return false;
+        }
+        return true;
+    }
+    static std::set<int64_t> image(const Binding &b, const Template &T) {
+        std::set<int64_t> s;
+        for (size_t k = 0; k < T.t.size(); ++k)
+            if (T.t[k].placeholder < 0 && b.map[k] >= 0) s.insert(b.map[k]);
+        return s;
+    }
+    int claim(Region r) {
+        const int idx = (int)regions.size();
+        for (int64_t id : r.covers)
+            if (!free_leaf(id)) claimed[id] = idx;
+        claimed[r.out] = idx;
+        regions.push_back(std::move(r));
+        return idx;
+    }
+    bool fail(const std::string &what) {
+        if (error.empty()) error = what;
+        return false;
+    }
+    // The value of a Const, or of an Expand chain over one.
+    bool const_of(int64_t id, double *v, Prim *p) const {
+        while (N(id).op == Op::Expand || N(id).op == Op::Reshape) id = N(id).inputs[0];
+        if (N(id).op != Op::Const) return false;
+        *v = N(id).const_value();
+        *p = N(id).const_prec;
+        return true;
+    }
+
+    // ------------------------------------------------------------ patterns
+    bool try_softmax(int64_t d) {
+        const Node &n = N(d);
+        if (n.op != Op::Div || n.dims.empty() || !prim_is_float(n.prec)) return false;
+        const int64_t axis = (int64_t)n.dims.size() - 1;
+        // softmax(where(causal mask, s * scale, -inf)) (spec/05 section 4.7 steps 3-5)
+        const int64_t sq = n.dims.size() >= 2 ? n.dims[n.dims.size() - 2] : -1, sk = n.dims.back();
+        for (const char *kind : {"gte", "lte"}) {
+            if (sq != sk) break;
+            Template T;
+            const int s = T.ph(0, n.dims, n.prec);
+            const int scale = T.expand_to(T.any_const({}, n.prec), n.dims);
+            const int scaled = T.bin(Op::Mul, s, scale);
+            const int ninf = T.expand_to(T.any_const({}, n.prec), n.dims);
+            const int lo = T.any_const({}, Prim::Int64), hi = T.any_const({}, Prim::Int64);
+            const int iota = T.op(Op::Iota, {lo, hi}, {sq}, Prim::Int64);
+            const int rows = T.expand(iota, 1, sq), cols = T.expand(iota, 0, sq);
+            TNode cmp;
+            cmp.op = Op::Compare;
+            cmp.compare = kind;
+            cmp.in = std::string(kind) == "gte" ? std::vector<int>{rows, cols} : std::vector<int>{cols, rows};
+            cmp.dims = {sq, sq};
+            cmp.prec = Prim::Bool;
+            const int mask = T.expand_to(T.add(cmp), n.dims);
+            const int masked = T.op(Op::Where, {mask, scaled, ninf}, n.dims, n.prec);
+            const int root = T.softmax(masked, axis);
+            Binding b;
+            if (!match(T, root, g, d, 1, &b)) continue;
+            double sv, nv, lov, hiv;
+            Prim sp, np_, lp, hp;
+            if (!const_of(b.map[scale], &sv, &sp) || !const_of(b.map[ninf], &nv, &np_) ||
+                !const_of(b.map[lo], &lov, &lp) || !const_of(b.map[hi], &hiv, &hp))
+                continue;
+            if (!(std::isinf(nv) && nv < 0) || lov != 0.0 || hiv != (double)sq) continue;
+            std::set<int64_t> cover = image(b, T);
+            if (!closed(cover, d)) continue;
+            Region r;
+            r.kind = RegionKind::MaskedSoftmax;
+            r.out = d;
+            r.in = {b.ph[0]};
+            r.scale = sv;
+            r.causal = 1;
+            r.covers.assign(cover.begin(), cover.end());
+            claim(r);
+            return true;
+        }
+        // plain softmax over a placeholder
+        {
+            Template T;
+            const int x = T.ph(0, n.dims, n.prec);
+            const int root = T.softmax(x, axis);
+            Binding b;
+            if (match(T, root, g, d, 1, &b)) {
+                std::set<int64_t> cover = image(b, T);
+                if (closed(cover, d)) {
+                    Region r;
+                    r.kind = RegionKind::Softmax;
+                    r.out = d;
+                    r.in = {b.ph[0]};
+                    r.covers.assign(cover.begin(), cover.end());
+                    claim(r);
+                    return true;
+                }
+            }
+        }
+        return false;
+    }
+
+    bool try_softmax_adjoint(int64_t d) {
+        const Node &n = N(d);
+        if (n.op != Op::Mul || n.dims.empty() || !prim_is_float(n.prec)) return false;
+        const int64_t axis = (int64_t)n.dims.size() - 1;
+        Template T;
+        const int y = T.ph(0, n.dims, n.prec), gr = T.ph(1, n.dims, n.prec);
+        const int s = T.reduce(Op::Sum, T.bin(Op::Mul, gr, y), axis);
+        const int root = T.bin(Op::Mul, y, T.bin(Op::Sub, gr, T.expand(s, axis, n.dims[axis])));
+        Binding b;
+        if (!match(T, root, g, d, 2, &b)) return false;
+        std::set<int64_t> cover = image(b, T);
+        if (!closed(cover, d)) return false;
+        Region r;
+        r.kind = RegionKind::SoftmaxAdjoint;
+        r.out = d;
+        r.in = {b.ph[0], b.ph[1]};
+        r.covers.assign(cover.begin(), cover.end());
+        claim(r);
+        return true;
+    }
+
+    bool try_layer_norm(int64_t d) {
+        const Node &n = N(d);
+        if (n.op != Op::Add || n.dims.empty() || !prim_is_float(n.prec)) return false;
+        const std::vector<int64_t> &dims = n.dims;
+        const int64_t axis = (int64_t)dims.size() - 1, h = dims[axis];
+        Template T;
+        const int x = T.ph(0, dims, n.prec), gamma = T.ph(1, {h}, n.prec), beta = T.ph(2, {h}, n.prec),
+                  eps = T.ph(3, {}, n.prec);
+        const int mean = T.mean(x, axis);
+        const int centered = T.bin(Op::Sub, x, T.expand(mean, axis, h));
+        const int var = T.mean(T.bin(Op::Mul, centered, centered), axis);
+        const int denom = T.un(Op::Sqrt, T.bin(Op::Add, T.expand(var, axis, h), T.expand_to(eps, dims)));
+        const int normed = T.bin(Op::Div, centered, denom);
+        const int root =
+            T.bin(Op::Add, T.bin(Op::Mul, normed, T.expand_to(gamma, dims)), T.expand_to(beta, dims));
+        Binding b;
+        if (!match(T, root, g, d, 4, &b)) return false;
+        double ev;
+        Prim ep;
+        if (!const_of(b.ph[3], &ev, &ep)) return false;
+        std::set<int64_t> cover = image(b, T);
+        if (!closed(cover, d)) return false;
+        Region r;
+        r.kind = RegionKind::LayerNorm;
+        r.out = d;
+        r.in = {b.ph[0], b.ph[1], b.ph[2]};
+        r.epsilon = ev;
+        r.covers.assign(cover.begin(), cover.end());
+        claim(r);
+        return true;
+    }
+
+    // activation.rs:145-149,183-276 at the operand's dtype
+    static int gelu_template(Template &T, const std::vector<int64_t> &dims, Prim p) {
+        struct K {
+            double c, cl, k, s, lowest;
+        };
+        const K k = p == Prim::F32
+                        ? K{(double)(float)0.70710678118654752440, 1.2101617485882343e-8,
+                            (double)(float)1.12837916709551257390, 4097.0, -3.4028234663852886e38}
+                        : K{0.70710678118654752440, -4.833646656726457e-17, 1.12837916709551257390, 134217729.0,
+                            -1.7976931348623157e308};
+        const int x = T.ph(0, dims, p);
+        const int lowest = T.cnst(k.lowest, dims, p);
+        TNode below;
+        below.op = Op::Compare;
+        below.compare = "cmp_lt";
+        below.in = {x, lowest};
+        below.dims = dims;
+        below.prec = Prim::Bool;
+        const int bl = T.add(below);
+        const int nzero = T.un(Op::Neg, T.cnst(0.0, dims, p));
+        const int m = T.op(Op::Where, {bl, nzero, x}, dims, p);
+        const int c = T.cnst(k.c, dims, p), cl = T.cnst(k.cl, dims, p), kk = T.cnst(k.k, dims, p),
+                  s = T.cnst(k.s, dims, p);
+        const int e = T.un(Op::Erfc, T.bin(Op::Mul, T.un(Op::Neg, x), c));
+        TNode inside;
+        inside.op = Op::Compare;
+        inside.compare = "cmp_lt";
+        inside.in = {T.un(Op::Abs, x), T.cnst(64.0, dims, p)};
+        inside.dims = dims;
+        inside.prec = Prim::Bool;
+        const int in_ = T.add(inside);
+        const int z = T.op(Op::Where, {in_, x, T.cnst(0.0, dims, p)}, dims, p);
+        const int a = T.un(Op::Neg, z);
+        const int th = T.bin(Op::Mul, a, c);
+        const int ta = T.bin(Op::Mul, s, a);
+        const int ah = T.bin(Op::Sub, ta, T.bin(Op::Sub, ta, a));
+        const int al = T.bin(Op::Sub, a, ah);
+        const int tc = T.bin(Op::Mul, s, c);
+        const int ch = T.bin(Op::Sub, tc, T.bin(Op::Sub, tc, c));
+        const int cr = T.bin(Op::Sub, c, ch);
+        int err = T.bin(Op::Sub, T.bin(Op::Mul, ah, ch), th);
+        err = T.bin(Op::Add, err, T.bin(Op::Mul, ah, cr));
+        err = T.bin(Op::Add, err, T.bin(Op::Mul, al, ch));
+        err = T.bin(Op::Add, err, T.bin(Op::Mul, al, cr));
+        const int tl = T.bin(Op::Add, err, T.bin(Op::Mul, a, cl));
+        const int dens = T.un(Op::Exp, T.un(Op::Neg, T.bin(Op::Mul, th, th)));
+        const int corr = T.bin(Op::Mul, T.bin(Op::Mul, kk, dens), tl);
+        const int phi = T.bin(Op::Mul, T.cnst(0.5, dims, p), T.bin(Op::Sub, e, corr));
+        return T.bin(Op::Mul, m, phi);
+    }
+
+    // The GELU graph rooted at `d`; returns its input value or -1.
+    int64_t gelu_at(int64_t d, std::set<int64_t> *cover) {
+        const Node &n = N(d);
+        if (n.op != Op::Mul || (n.prec != Prim::F32 && n.prec != Prim::F64)) return -1;
+        Template T;
+        const int root = gelu_template(T, n.dims, n.prec);
+        Binding b;
+        if (!match(T, root, g, d, 1, &b)) return -1;
+        *cover = image(b, T);
+        return b.ph[0];
+    }
+
+    bool try_gelu(int64_t d) {
+        std::set<int64_t> cover;
+        const int64_t x = gelu_at(d, &cover);
+        if (x < 0 || !closed(cover, d)) return false;
+        Region r;
+        r.kind = RegionKind::Gelu;
+        r.out = d;
+        r.in = {x};
+        r.covers.assign(cover.begin(), cover.end());
+        claim(r);
+        return true;
+    }
+
+    // matmul: Sum{L+1}(Mul(Expand{L+2, k}(a), Expand{L, i}(b))) or BlasMatmul
+    bool try_matmul(int64_t d) {
+        const Node &n = N(d);
+        int64_t a = -1, b = -1;
+        std::set<int64_t> cover{d};
+        if (n.op == Op::BlasMatmul && n.inputs.size() == 2) {
+            a = n.inputs[0];
+            b = n.inputs[1];
+        } else if (n.op == Op::Sum && n.inputs.size() == 1 && prim_is_float(n.prec)) {
+            const Node &mul = N(n.inputs[0]);
+            if (mul.op != Op::Mul || mul.inputs.size() != 2) return false;
+            const Node &ea = N(mul.inputs[0]), &eb = N(mul.inputs[1]);
+            if (ea.op != Op::Expand || eb.op != Op::Expand || ea.inputs.size() != 1 || eb.inputs.size() != 1)
+                return false;
+            const int64_t rank = (int64_t)mul.dims.size();  // [..., i, j, k]
+            if (rank < 3) return false;
+            const int64_t L = rank - 3;
+            if (n.axis != L + 1 || ea.axis != L + 2 || eb.axis != L) return false;
+            a = ea.inputs[0];
+            b = eb.inputs[0];
+            const Node &A = N(a), &B = N(b);
+            if (A.dims.size() != (size_t)L + 2 || B.dims.size() != (size_t)L + 2) return false;
+            if (A.dims[L + 1] != B.dims[L] || ea.size != B.dims[L + 1] || eb.size != A.dims[L]) return false;
+            cover.insert({n.inputs[0], mul.inputs[0], mul.inputs[1]});
+        } else {
+            return false;
+        }
+        if (!closed(cover, d)) return false;
+        Region r;
+        r.kind = RegionKind::Matmul;
+        r.in = {a, b};
+        int64_t v = d;
+        // epilogue: bias, then relu or GELU, then a residual add, each taken
+        // only when it is the value's one reader
+        auto sole_user = [&](int64_t id) -> int64_t {
+            if (is_root[id] || users[id].size() != 1) return -1;
+            return users[id][0];
+        };
+        int64_t bias = -1, residual = -1;
+        int32_t act = CHELIS_ACT_NONE;
+        int64_t u = sole_user(v);
+        if (u >= 0 && N(u).op == Op::Add && N(u).inputs.size() == 2 && N(u).inputs[0] == v && claimed[u] < 0) {
+            // the bias operand: expand_to_match of an [N] vector
+            int64_t e = N(u).inputs[1];
+            std::set<int64_t> chain{u};
+            while (N(e).op == Op::Expand && N(e).axis == 0 && users[e].size() == 1 && !is_root[e]) {
+                chain.insert(e);
+                e = N(e).inputs[0];
+            }
+            if (N(e).dims.size() == 1 && N(e).dims[0] == N(v).dims.back() && N(e).prec == N(v).prec &&
+                chain.size() == N(v).dims.size()) {
+                bias = e;
+                cover.insert(chain.begin(), chain.end());
+                v = u;
+            }
+        }
+        u = sole_user(v);
+        if (u >= 0 && N(u).op == Op::Relu && claimed[u] < 0) {
+            act = CHELIS_ACT_RELU;
+            cover.insert(u);
+            v = u;
+        } else if (!is_root[v]) {
+            // the GELU graph reads its input at several nodes; its result is
+            // the Mul of the guard's Where
+            for (int64_t w : users[v]) {
+                if (N(w).op != Op::Where || N(w).inputs.size() != 3 || N(w).inputs[2] != v) continue;
+                for (int64_t f : users[w]) {
+                    std::set<int64_t> gc;
+                    if (gelu_at(f, &gc) != v) continue;
+                    std::set<int64_t> all = cover;
+                    all.insert(gc.begin(), gc.end());
+                    all.insert(v);
+                    if (!closed(all, f)) continue;
+                    cover = all;
+                    act = CHELIS_ACT_GELU;
+                    v = f;
+                    break;
+                }
+                if (act == CHELIS_ACT_GELU) break;
+            }
+        }
+        u = sole_user(v);
+        if (u >= 0 && N(u).op == Op::Add && N(u).inputs.size() == 2 && claimed[u] < 0) {
+            const int64_t other = N(u).inputs[0] == v ? N(u).inputs[1] : N(u).inputs[0];
+            if (other != v && N(other).dims == N(v).dims && N(other).prec == N(v).prec) {
+                residual = other;
+                cover.insert(u);
+                v = u;
+            }
+        }
+        r.out = v;
+        if (bias >= 0) {
+            r.in.push_back(bias);
+            r.has_bias = true;
+        }
+        if (residual >= 0) {
+            r.in.push_back(residual);
+            r.has_residual = true;
+        }
+        r.activation = act;
+        cover.insert(v);
+        r.covers.assign(cover.begin(), cover.end());
+        claim(r);
+        return true;
+    }
+
+    // ------------------------------------------------------------ generic regions
+    static int chain_op(Op op) {
+        switch (op) {
+            case Op::Add: return CHELIS_FUSED_ADD;
+            case Op::Sub: return CHELIS_FUSED_SUB;
+            case Op::Mul: return CHELIS_FUSED_MUL;
+            case Op::Div: return CHELIS_FUSED_DIV;
+            case Op::MaxElem: return CHELIS_FUSED_MAX_ELEM;
+            case Op::MinElem: return CHELIS_FUSED_MIN_ELEM;
+            case Op::Neg: return CHELIS_FUSED_NEG;
+            case Op::Recip: return CHELIS_FUSED_RECIP;
+            case Op::Exp: return CHELIS_FUSED_EXP;
+            case Op::Log: return CHELIS_FUSED_LOG;
+            case Op::Sqrt: return CHELIS_FUSED_SQRT;
+            case Op::Tanh: return CHELIS_FUSED_TANH;
+            case Op::Erfc: return CHELIS_FUSED_ERFC;
+            case Op::Abs: return CHELIS_FUSED_ABS;
+            case Op::Floor: return CHELIS_FUSED_FLOOR;
+            case Op::Ceil: return CHELIS_FUSED_CEIL;
+            case Op::Round: return CHELIS_FUSED_ROUND;
+            default: return -1;
+        }
+    }
+    bool fusible(int64_t id) const {
+        const Node &n = N(id);
+        return claimed[id] < 0 && op_is_chain_step(n.op) && prim_is_float(n.prec);
+    }
+
+    // Build chelis_fused_chain launches from a run of chain nodes; nodes
+    // beyond 16 steps or 8 external inputs start a new launch whose result
+    // feeds the next. Returns the regions' indices.
+    bool emit_chain(const std::vector<int64_t> &nodes, int64_t reduce_node) {
+        size_t start = 0;
+        while (start < nodes.size()) {
+            Region r;
+            r.kind = RegionKind::Chain;
+            r.has_chain = true;
+            std::vector<int64_t> ext;
+            std::vector<int64_t> steps;
+            size_t k = start;
+            for (; k < nodes.size(); ++k) {
+                const Node &n = N(nodes[k]);
+                std::vector<int64_t> need;
+                for (int64_t in : n.inputs)
+                    if (std::find(steps.begin(), steps.end(), in) == steps.end() &&
+                        std::find(ext.begin(), ext.end(), in) == ext.end() &&
+                        std::find(need.begin(), need.end(), in) == need.end())
+                        need.push_back(in);
+                if (steps.size() + 1 > CHELIS_FUSED_MAX_STEPS || ext.size() + need.size() > CHELIS_FUSED_MAX_INPUTS)
+                    break;
+                const int cop = chain_op(n.op);
+                if (cop < 0) return fail(std::string("node ") + std::to_string(n.id) + ": " + op_name(n.op) +
+                                         " has no device chain step in this build");
+                ext.insert(ext.end(), need.begin(), need.end());
+                chelis_fused_step &s = r.chain.steps[steps.size()];
+                s.op = (uint8_t)cop;
+                for (size_t a = 0; a < 2; ++a) {
+                    const int64_t in = n.inputs[a < n.inputs.size() ? a : 0];
+                    auto sp = std::find(steps.begin(), steps.end(), in);
+                    s.args[a] = sp != steps.end() ? -(int32_t)(sp - steps.begin()) - 1
+                                                  : (int32_t)(std::find(ext.begin(), ext.end(), in) - ext.begin());
+                }
+                steps.push_back(n.id);
+            }
+            if (k == start) return fail("a chain step needs more than 8 inputs");
+            r.chain.n_steps = (int32_t)steps.size();
+            r.in = ext;
+            r.covers = steps;
+            r.out = steps.back();
+            const bool last = k == nodes.size();
+            if (last && reduce_node >= 0) {
+                const Node &red = N(reduce_node);
+                r.kind = RegionKind::Reduce;
+                r.reduce_op = red.op == Op::Sum ? CHELIS_REDUCE_SUM : CHELIS_REDUCE_MAX;
+                r.axis = red.axis;
+                r.covers.push_back(reduce_node);
+                r.out = reduce_node;
+            }
+            claim(r);
+            start = k;
+        }
+        return true;
+    }
+
+    bool generic() {
+        for (const Node &n : g.nodes) {
+            if (claimed[n.id] >= 0) continue;
+            if (fusible(n.id)) {
+                // fuse.rs:136-191: extend through single-consumer fusible links
+                std::vector<int64_t> chain{n.id};
+                int64_t cur = n.id;
+                while (counts[cur] == 1 && users[cur].size() == 1) {
+                    const int64_t c = users[cur][0];
+                    if (!fusible(c) || N(c).owner_decl != n.owner_decl ||
+                        N(c).owner_activation != n.owner_activation ||
+                        std::find(chain.begin(), chain.end(), c) != chain.end())
+                        break;
+                    chain.push_back(c);
+                    cur = c;
+                }
+                // a chain whose one reader is a Sum or MaxReduce is its leaf
+                int64_t red = -1;
+                if (counts[cur] == 1 && users[cur].size() == 1) {
+                    const int64_t c = users[cur][0];
+                    if (claimed[c] < 0 && (N(c).op == Op::Sum || N(c).op == Op::MaxReduce) && N(c).inputs[0] == cur)
+                        red = c;
+                }
+                if (!emit_chain(chain, red)) return false;
+                continue;
+            }
+            switch (n.op) {
+                case Op::Load: case Op::Const: case Op::Expand: case Op::Permute: case Op::Reshape:
+                case Op::Realize: case Op::Copy:
+                    continue;  // inputs, constants and views
+                case Op::Sum: case Op::MaxReduce: case Op::MinReduce: case Op::ProdReduce: case Op::Argmax:
+                case Op::Argmin: {
+                    Region r;
+                    r.kind = RegionKind::Reduce;
+                    r.reduce_op = n.op == Op::Sum ? CHELIS_REDUCE_SUM : n.op == Op::MaxReduce ? CHELIS_REDUCE_MAX
+                                  : n.op == Op::MinReduce ? CHELIS_REDUCE_MIN : n.op == Op::ProdReduce ? CHELIS_REDUCE_PROD
+                                  : n.op == Op::Argmax ? CHELIS_REDUCE_ARGMAX : CHELIS_REDUCE_ARGMIN;
+                    r.axis = n.axis;
+                    r.in = {n.inputs[0]};
+                    r.out = n.id;
+                    r.covers = {n.id};
+                    claim(r);
+                    continue;
+                }
+                case Op::Count: {
+                    if (n.axes.size() != 1)
+                        return fail("node " + std::to_string(n.id) + ": Count over several axes is not built");
+                    Region r;
+                    r.kind = RegionKind::Count;
+                    r.axis = n.axes[0];
+                    r.in = {n.inputs[0]};
+                    r.out = n.id;
+                    r.covers = {n.id};
+                    claim(r);
+                    continue;
+                }
+                case Op::Softmax: {
+                    if (n.axis != (int64_t)n.dims.size() - 1)
+                        return fail("node " + std::to_string(n.id) + ": softmax over a leading axis is not built");
+                    Region r;
+                    r.kind = RegionKind::Softmax;
+                    r.in = {n.inputs[0]};
+                    r.out = n.id;
+                    r.covers = {n.id};
+                    claim(r);
+                    continue;
+                }
+                case Op::Relu: case Op::ReluAdjoint: {
+                    Region r;
+                    r.kind = n.op == Op::Relu ? RegionKind::Relu : RegionKind::ReluAdjoint;
+                    r.in = n.inputs;
+                    r.out = n.id;
+                    r.covers = {n.id};
+                    claim(r);
+                    continue;
+                }
+                case Op::Dropout: case Op::DropoutReplay: {
+                    double rate;
+                    Prim rp;
+                    if (n.inputs.size() != 3 || !const_of(n.inputs[1], &rate, &rp))
+                        return fail("node " + std::to_string(n.id) + ": dropout needs a constant rate and a key");
+                    if (N(n.inputs[2]).prec != Prim::Key || !N(n.inputs[2]).dims.empty())
+                        return fail("node " + std::to_string(n.id) + ": dropout's key must be one rank-0 key");
+                    Region r;
+                    r.kind = RegionKind::Dropout;
+                    r.replay = n.op == Op::DropoutReplay;
+                    r.rate = rate;
+                    r.in = {n.inputs[0], n.inputs[2]};
+                    r.out = n.id;
+                    r.covers = {n.id};
+                    claim(r);
+                    continue;
+                }
+                default:
+                    return fail("node " + std::to_string(n.id) + ": " + n.variant +
+                                " is outside the region kinds this build runs");
+            }
+        }
+        return true;
+    }
+
+    bool form() {
+        for (const Node &n : g.nodes) {
+            if (claimed[n.id] >= 0) continue;
+            if (try_matmul(n.id)) continue;
+            if (try_layer_norm(n.id)) continue;
+            if (try_softmax(n.id)) continue;
+            if (try_softmax_adjoint(n.id)) continue;
+            if (try_gelu(n.id)) continue;
+        }
+        if (!generic()) return false;
+        // keep launches in dependency order: by their result node
+        std::vector<int> order(regions.size());
+        for (size_t k = 0; k < order.size(); ++k) order[k] = (int)k;
+        std::stable_sort(order.begin(), order.end(),
+                         [&](int x, int y) { return regions[x].out < regions[y].out; });
+        std::vector<Region> sorted;
+        for (int k : order) sorted.push_back(regions[k]);
+        regions.swap(sorted);
+        for (size_t k = 0; k < regions.size(); ++k)
+            for (int64_t id : regions[k].covers)
+                if (!free_leaf(id)) claimed[id] = (int)k;
+        return true;
+    }
+};
+
+bool is_view_op(Op op) {
+    return op == Op::Expand || op == Op::Permute || op == Op::Reshape || op == Op::Realize || op == Op::Copy;
+}
+
+}  // namespace
+
+bool build_plan(const Graph &input, Plan *plan, std::string *error) {
+    *plan = Plan{};
+    plan->graph = unfuse(input);
+    const Graph &g = plan->graph;
+    Planner P(g);
+    if (!P.form()) {
+        *error = P.error;
+        return false;
+    }
+    // causal matmul modes: the scores product of a causal softmax skips the
+    // tiles above the diagonal; the product reading the probabilities stops
+    // each row tile's contraction at its last row
+    for (Region &r : P.regions) {
+        if (r.kind != RegionKind::MaskedSoftmax || !r.causal) continue;
+        int64_t s = r.in[0];
+        for (Region &m : P.regions)
+            if (m.kind == RegionKind::Matmul && m.out == s && !m.has_bias && !m.has_residual &&
+                m.activation == CHELIS_ACT_NONE && P.users[s].size() == 1 && !P.is_root[s])
+                m.causal_mode = 1;
+        for (Region &m : P.regions)
+            if (m.kind == RegionKind::Matmul && m.in[0] == r.out && !m.has_bias && !m.has_residual &&
+                m.activation == CHELIS_ACT_NONE && P.users[r.out].size() == 1 && !P.is_root[r.out])
+                m.causal_mode = 2;
+    }
+    plan->regions = P.regions;
+    const size_t n = g.nodes.size();
+    plan->values.assign(n, ValueInfo{});
+    std::vector<bool> produced(n, false);
+    for (const Region &r : plan->regions) produced[r.out] = true;
+    for (const Node &nd : g.nodes) {
+        ValueInfo &v = plan->values[nd.id];
+        if (nd.op == Op::Load) {
+            v.storage = Storage::Input;
+            v.input = (int64_t)plan->input_nodes.size();
+            plan->input_nodes.push_back(nd.id);
+            plan->input_labels.push_back(nd.name);
+        } else if (nd.op == Op::Const) {
+            v.storage = Storage::Const;
+            v.const_index = (int64_t)plan->const_bits.size();
+            plan->const_bits.push_back(nd.const_bits);
+            plan->const_prec.push_back(nd.const_prec);
+        } else if (produced[nd.id]) {
+            v.storage = Storage::Slot;
+        } else if (is_view_op(nd.op) && P.claimed[nd.id] < 0) {
+            v.storage = Storage::View;
+            v.base = nd.inputs[0];
+        } else {
+            v.storage = Storage::Inlined;
+        }
+    }
+    // every region input must have storage
+    for (const Region &r : plan->regions)
+        for (int64_t in : r.in)
+            if (plan->values[in].storage == Storage::Inlined) {
+                *error = "node " + std::to_string(in) + " is read by a launch but computed inside another";
+                return false;
+            }
+    // outputs: a region result is written straight into the caller's
+    // output (through a reshape when the root is one); anything else is
+    // copied there by a last launch
+    std::vector<int64_t> copies;
+    for (size_t o = 0; o < g.roots.size(); ++o) {
+        const int64_t root = g.roots[o];
+        plan->output_nodes.push_back(root);
+        plan->output_labels.push_back(g.nodes[root].has_span ? g.nodes[root].span : "out" + std::to_string(o));
+        int64_t v = root;
+        while (plan->values[v].storage == Storage::View && g.nodes[v].op == Op::Reshape && P.users[v].size() <= 1 &&
+               P.users[plan->values[v].base].size() == 1 && !P.is_root[plan->values[v].base])
+            v = plan->values[v].base;
+        ValueInfo &vi = plan->values[v];
+        if (vi.storage == Storage::Slot && vi.output < 0 && (v == root || P.users[v].size() == 1)) {
+            vi.storage = Storage::Output;
+            vi.output = (int64_t)o;
+            vi.base = root;  // the packet is the output's, viewed with this node's shape
+        } else {
+            Region c;
+            c.kind = RegionKind::Copy;
+            c.in = {root};
+            c.out = root;
+            c.axis = (int64_t)o;  // the output slot
+            copies.push_back((int64_t)plan->regions.size());
+            plan->regions.push_back(c);
+        }
+    }
+    // a materialized value read only through one Permute is stored in the
+    // permuted order, so the permuted view is dense (a later Reshape of it
+    // is then a view too); matmul results only, the one launcher that
+    // writes any strided layout
+    for (const Region &r : plan->regions) {
+        if (r.kind != RegionKind::Matmul) continue;
+        ValueInfo &vi = plan->values[r.out];
+        if (vi.storage != Storage::Slot || P.users[r.out].size() != 1) continue;
+        const Node &u = g.nodes[P.users[r.out][0]];
+        if (u.op == Op::Permute && u.axes.size() == g.nodes[r.out].dims.size()) vi.layout = u.axes;
+    }
+    // slot plan: lifetimes in launch order, views charged to their base
+    std::vector<int64_t> def(n, -1), last(n, -1);
+    for (size_t k = 0; k < plan->regions.size(); ++k) {
+        const Region &r = plan->regions[k];
+        if (r.kind != RegionKind::Copy && def[r.out] < 0) def[r.out] = (int64_t)k;
+        for (int64_t in : r.in) {
+            int64_t b = in;
+            while (plan->values[b].storage == Storage::View) b = plan->values[b].base;
+            last[b] = std::max(last[b], (int64_t)k);
+        }
+    }
+    std::vector<int64_t> slot_size;
+    std::vector<bool> busy;
+    std::vector<std::vector<int64_t>> release_at(plan->regions.size());
+    for (size_t k = 0; k < plan->regions.size(); ++k) {
+        const Region &r = plan->regions[k];
+        if (r.kind != RegionKind::Copy) {
+            ValueInfo &vi = plan->values[r.out];
+            if (vi.storage == Storage::Slot) {
+                const Node &nd = g.nodes[r.out];
+                const int64_t width = r.kind == RegionKind::Reduce && (r.reduce_op == CHELIS_REDUCE_ARGMAX ||
+                                                                       r.reduce_op == CHELIS_REDUCE_ARGMIN)
+                                          ? 8
+                                          : (r.kind == RegionKind::Count ? 8 : prim_width(nd.prec));
+                const int64_t cnt = nd.count();
+                if (cnt < 0) {
+                    *error = "node " + std::to_string(nd.id) + ": an extent known only at run time";
+                    return false;
+                }
+                const int64_t need = ((cnt * width) + 255) & ~int64_t(255);
+                int64_t best = -1;
+                for (size_t s = 0; s < slot_size.size(); ++s)
+                    if (!busy[s] && slot_size[s] >= need && (best < 0 || slot_size[s] < slot_size[best])) best = (int64_t)s;
+                if (best < 0)
+                    for (size_t s = 0; s < slot_size.size(); ++s)
+                        if (!busy[s] && (best < 0 || slot_size[s] > slot_size[best])) best = (int64_t)s;
+                if (best < 0) {
+                    best = (int64_t)slot_size.size();
+                    slot_size.push_back(0);
+                    busy.push_back(false);
+                }
+                slot_size[best] = std::max(slot_size[best], need);
+                busy[best] = true;
+                vi.slot = best;
+                const int64_t end = std::max(last[r.out], (int64_t)k);
+                release_at[end].push_back(best);
+            }
+        }
+        for (int64_t s : release_at[k]) busy[s] = false;
+    }
+    int64_t off = 0;
+    for (int64_t s : slot_size) {
+        plan->slots.push_back(Slot{off, s});
+        off += s;
+    }
+    plan->workspace_bytes = off;
+    // the constant pool holds one 8-byte cell per constant
+    plan->peak_device_bytes = plan->workspace_bytes + 8 * (int64_t)plan->const_bits.size();
+    (void)copies;
+    return true;
+}
+
+std::string describe_plan(const Plan &plan) {
+    std::string s;
+    for (size_t k = 0; k < plan.regions.size(); ++k) {
+        const Region &r = plan.regions[k];
+        s += std::to_string(k) + " " + region_kind_name(r.kind) + " out=" + std::to_string(r.out) + " in=[";
+        for (size_t i = 0; i < r.in.size(); ++i) s += (i ? "," : "") + std::to_string(r.in[i]);
+        s += "]";
+        if (r.kind == RegionKind::Chain || (r.kind == RegionKind::Reduce && r.has_chain))
+            s += " steps=" + std::to_string(r.chain.n_steps);
+        if (r.kind == RegionKind::Reduce) s += " op=" + std::to_string(r.reduce_op) + " axis=" + std::to_string(r.axis);
+        if (r.kind == RegionKind::Matmul) {
+            if (r.has_bias) s += " bias";
+            if (r.activation == CHELIS_ACT_RELU) s += " relu";
+            if (r.activation == CHELIS_ACT_GELU) s += " gelu";
+            if (r.has_residual) s += " residual";
+            if (r.causal_mode) s += " causal=" + std::to_string(r.causal_mode);
+            if (!plan.values[r.out].layout.empty()) s += " permuted";
+        }
+        if (r.kind == RegionKind::MaskedSoftmax) s += " causal";
+        const ValueInfo &v = plan.values[r.out];
+        if (r.kind != RegionKind::Copy) {
+            if (v.storage == Storage::Output) s += " -> output " + std::to_string(v.output);
+            else if (v.storage == Storage::Slot) s += " -> slot " + std::to_string(v.slot);
+        } else {
+            s += " -> output " + std::to_string(r.axis);
+        }
+        s += "\n";
+    }
+    return s;
+}
+
+}  // namespace dag
+}  // namespace chelis

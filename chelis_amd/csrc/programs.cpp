@@ -394,3 +394,65 @@ extern "C" void mlp_train_step_device(const chelis_device_tensor_owner *const *i
                {dims(inputs[4]), CHELIS_DTYPE_F32},
                {dims(inputs[5]), CHELIS_DTYPE_F32}});
 }
+
+// ------------------------------------------------------------------ host-tensor entry form
+// The generated `{f}(chelis_tensor **inputs, int n_in, chelis_tensor
+// **outputs, int n_out)` (crates/chelis-backend-hip/src/emit.rs:667-808):
+// a wrong count prints `{f}: expected N inputs, got M` and aborts; each
+// host input is copied into a fresh device tensor (the PCIe crossing of a
+// Load); the program runs as its `{f}_device` entry; each result comes back
+// as a new host tensor from chelis_alloc, written under its write lease;
+// the device is synchronized and every device tensor released before the
+// call returns. Inputs stay owned by the caller.
+namespace {
+
+using DeviceEntry = void (*)(const chelis_device_tensor_owner *const *, chelis_device_rank,
+                             chelis_device_tensor_owner **, chelis_device_rank);
+
+void run_host_entry(const char *name, DeviceEntry entry, int expected_in, int expected_out, chelis_tensor **inputs,
+                    int n_in, chelis_tensor **outputs, int n_out) {
+    if (n_in != expected_in) {
+        std::fprintf(stderr, "%s: expected %d inputs, got %d\n", name, expected_in, n_in);
+        std::abort();
+    }
+    if (n_out != expected_out) {
+        std::fprintf(stderr, "%s: expected %d outputs, got %d\n", name, expected_out, n_out);
+        std::abort();
+    }
+    if (!inputs || !outputs) entry_trap(name);
+    std::vector<chelis_device_tensor_owner *> device_in(n_in, nullptr);
+    for (int i = 0; i < n_in; ++i) {
+        const chelis_tensor *t = inputs[i];
+        const int32_t rank = chelis_tensor_rank(t);
+        std::vector<int64_t> shape(rank);
+        for (int32_t a = 0; a < rank; ++a) shape[a] = chelis_tensor_shape(t, a);
+        device_in[i] = alloc_like(shape, chelis_tensor_read_view(t).dtype);
+        chelis_device_tensor_copy_from_host(device_in[i], t);
+    }
+    std::vector<chelis_device_tensor_owner *> device_out(n_out, nullptr);
+    entry(device_in.data(), n_in, device_out.data(), n_out);
+    for (int o = 0; o < n_out; ++o) {
+        const chelis_gpu_tensor *v = chelis_device_tensor_view(device_out[o]);
+        outputs[o] = chelis_alloc(v->rank, v->rank ? v->shape : nullptr, v->dtype);
+        chelis_tensor_write *lease = chelis_tensor_begin_write(outputs[o]);
+        chelis_device_tensor_copy_to_host(lease, device_out[o]);
+        chelis_tensor_end_write(lease);
+    }
+    if (hipDeviceSynchronize() != hipSuccess) entry_trap(name);
+    for (chelis_device_tensor_owner *t : device_out) chelis_device_tensor_release(t);
+    for (chelis_device_tensor_owner *t : device_in) chelis_device_tensor_release(t);
+}
+
+}  // namespace
+
+extern "C" void linreg_step(chelis_tensor **inputs, int n_in, chelis_tensor **outputs, int n_out) {
+    run_host_entry("linreg_step", linreg_step_device, 3, 2, inputs, n_in, outputs, n_out);
+}
+
+extern "C" void transformer_block(chelis_tensor **inputs, int n_in, chelis_tensor **outputs, int n_out) {
+    run_host_entry("transformer_block", transformer_block_device, 17, 1, inputs, n_in, outputs, n_out);
+}
+
+extern "C" void mlp_train_step(chelis_tensor **inputs, int n_in, chelis_tensor **outputs, int n_out) {
+    run_host_entry("mlp_train_step", mlp_train_step_device, 7, 5, inputs, n_in, outputs, n_out);
+}

@@ -1,0 +1,85 @@
+/* The DAG front end: a lowered or fused Chelis RISC DAG, in the reference's
+ * serde JSON wire form, run on gfx950 through this library's region
+ * launchers.
+ *
+ * In the reference, `chelis build --target hip` fuses the DAG
+ * (crates/chelis-dag-core/src/fuse.rs:32), lowers it to HIP source with one
+ * kernel string per fused node (codegen_hip, crates/chelis-backend-hip/src/
+ * lib.rs:104-167; HipEmitter::emit_dag, emit.rs:488-964) and compiles that.
+ * Here the same DAG is read as JSON (the form serde_json::to_string(&dag)
+ * writes, crates/chelis-dag-core/src/dag.rs:2364-2400,2913-2919), its
+ * lowered patterns become single region launches (a matmul with its bias /
+ * activation / residual epilogue, softmax, causal masked softmax, softmax
+ * adjoint, layer norm, GELU), the rest is grouped by fuse.rs's chain rules,
+ * and intermediates share one planned workspace.
+ *
+ * Errors: a NULL result or a status other than CHELIS_HIP_OK, with
+ * chelis_hip_last_error() describing it (the node and op a plan cannot run
+ * are named, as the reference's Unsupported diagnostics do). */
+#ifndef CHELIS_DAG_H
+#define CHELIS_DAG_H
+
+#include <stdint.h>
+#include "chelis_device_descriptor.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct chelis_dag_program chelis_dag_program;
+
+/* Reads and plans a DAG; host work only (constants reach a device on the
+ * first run there). The inputs are the DAG's Load nodes in node order, the
+ * outputs its roots in order. */
+chelis_dag_program *chelis_dag_compile(const char *json, int64_t length);
+void chelis_dag_release(chelis_dag_program *program);
+/* Enqueues the program on the library stream (chelis_hip_stream()) over
+ * caller-owned device packets; returns without synchronizing. Input packets
+ * may be any strided views of the declared shapes and dtypes. */
+int32_t chelis_dag_run(chelis_dag_program *program, const chelis_gpu_tensor *const *inputs, int32_t n_in,
+                       const chelis_gpu_tensor *const *outputs, int32_t n_out);
+
+int32_t chelis_dag_input_count(const chelis_dag_program *program);
+int32_t chelis_dag_output_count(const chelis_dag_program *program);
+/* output == 0: input slot `index` (its Load's name); 1: output slot (the
+ * root's span name, else "out<index>"). */
+const char *chelis_dag_label(const chelis_dag_program *program, int32_t output, int32_t index);
+int32_t chelis_dag_type(const chelis_dag_program *program, int32_t output, int32_t index, int32_t *rank,
+                        int64_t *shape, int32_t shape_capacity, int32_t *dtype);
+/* Workspace plus constant pool bytes one run needs on a device (the
+ * reference's peak_device_bytes_estimate, memory.rs:130-155). */
+int64_t chelis_dag_peak_device_bytes(const chelis_dag_program *program);
+int64_t chelis_dag_launch_count(const chelis_dag_program *program);
+/* One line per launch: index, region kind, result node, input nodes. */
+const char *chelis_dag_describe(const chelis_dag_program *program);
+
+/* fuse.rs on its own: the DAG after greedy chain fusion, as JSON in the same
+ * wire form (a thread-local string, valid until the next call). */
+const char *chelis_dag_fuse(const char *json, int64_t length);
+
+/* ---- codegen surface: the reference's HipCodegenResult
+ * (crates/chelis-backend-hip/src/lib.rs:32-53) ----
+ * codegen_hip(dag, func_name) writes host C++ defining
+ *   void {f}(chelis_tensor **, int, chelis_tensor **, int);
+ *   void {f}_device(const chelis_device_tensor_owner *const *, chelis_device_rank,
+ *                   chelis_device_tensor_owner **, chelis_device_rank);
+ * with the reference's entry contracts (emit.rs:667-808, 838-964), built by
+ * compiling it with compile_flags and linking link_flags (this library in
+ * place of -lhiprtc -lhipblas). */
+typedef struct chelis_hip_codegen_result chelis_hip_codegen_result;
+chelis_hip_codegen_result *chelis_codegen_hip(const char *json, int64_t length, const char *func_name);
+void chelis_codegen_release(chelis_hip_codegen_result *result);
+const char *chelis_codegen_c_source(const chelis_hip_codegen_result *result);
+const char *chelis_codegen_h_header(const chelis_hip_codegen_result *result);
+/* which: 0 compile flags, 1 link flags, 2 input labels, 3 output labels,
+ * 4 symbolic dims */
+int32_t chelis_codegen_list_count(const chelis_hip_codegen_result *result, int32_t which);
+const char *chelis_codegen_list_item(const chelis_hip_codegen_result *result, int32_t which, int32_t index);
+const char *chelis_codegen_peak_device_bytes_formula(const chelis_hip_codegen_result *result);
+/* -1 when an extent is known only at run time */
+int64_t chelis_codegen_peak_device_bytes_estimate(const chelis_hip_codegen_result *result);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

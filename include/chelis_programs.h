@@ -44,6 +44,16 @@ void transformer_block_device(const chelis_device_tensor_owner *const *inputs, c
 void mlp_train_step_device(const chelis_device_tensor_owner *const *inputs, chelis_device_rank n_in,
                            chelis_device_tensor_owner **outputs, chelis_device_rank n_out);
 
+/* The generated host-tensor entries `{f}` (emit.rs:667-808, header
+ * lib.rs:116-118): host tensors in, new host tensors out (chelis_alloc,
+ * written under a write lease, released by the caller with
+ * chelis_tensor_release); a wrong input or output count prints
+ * "{f}: expected N inputs, got M" and aborts; the device is synchronized
+ * before the call returns. */
+void linreg_step(chelis_tensor **inputs, int n_in, chelis_tensor **outputs, int n_out);
+void transformer_block(chelis_tensor **inputs, int n_in, chelis_tensor **outputs, int n_out);
+void mlp_train_step(chelis_tensor **inputs, int n_in, chelis_tensor **outputs, int n_out);
+
 int32_t chelis_prog_linreg_step(const chelis_gpu_tensor *const *inputs, int32_t n_in,
                                 const chelis_gpu_tensor *const *outputs, int32_t n_out);
 int32_t chelis_prog_transformer_block(const chelis_gpu_tensor *const *inputs, int32_t n_in,

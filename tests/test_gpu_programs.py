@@ -147,3 +147,36 @@ def test_transformer_block_device_entry():
     ins = [C.to_device(x)] + [C.to_device(p[k]) for k in O.TRANSFORMER_PARAMS]
     (y,) = C.device_entry("transformer_block", ins, 1)
     assert y.shape == x.shape and normwise(y.numpy(), ref) <= 1e-5
+
+
+def test_host_entries_match_the_oracle():
+    """The generated host-tensor entries {f}(chelis_tensor **, ...): host
+    arrays in, fresh host tensors out, the same results as the device form."""
+    X, w, y = linreg_inputs(2000, 16)
+    grad_ref, loss_ref = O.linreg_step(X, w, y)
+    grad, loss = C.host_entry("linreg_step", [X, w, y], 2)
+    assert grad.shape == (16,) and loss.shape == ()
+    assert bits_equal(grad, grad_ref) and bits_equal(loss, np.float64(loss_ref))
+    args = mlp_inputs(256, 784, 128, 10)
+    ref = O.mlp_train_step(*args, 44, np.float32(0.1), np.float32(0.01))
+    prev = C.set_exact_matmul(True)
+    try:
+        got = C.host_entry("mlp_train_step", list(args) + [("key", 44)], 5)
+    finally:
+        C.set_exact_matmul(prev)
+    for g, r in zip(got, ref):
+        assert bits_equal(np.asarray(g, np.float32), np.asarray(r, np.float32))
+    x, p = transformer_inputs(B=1, S=64, D=128, F=256)
+    (yt,) = C.host_entry("transformer_block", [x] + [p[k] for k in O.TRANSFORMER_PARAMS], 1)
+    assert yt.shape == x.shape and normwise(yt, O.transformer_block(x, p, 2)) <= 1e-5
+
+
+def test_host_entry_count_mismatch_aborts():
+    import subprocess
+    import sys
+    import os
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    code = (f"import sys; sys.path.insert(0, {root!r}); import numpy as np, chelis_amd as C; "
+            "C.host_entry('linreg_step', [np.zeros((4, 2)), np.zeros(2)], 2)")
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode != 0 and "linreg_step: expected 3 inputs, got 2" in r.stderr
