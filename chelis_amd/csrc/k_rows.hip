@@ -85,28 +85,33 @@ struct ExpTableLanes {
     __device__ double operator()(int j) const { return __shfl(t, j, 64); }
 };
 
-// 2^(j/64) as a double-double, held one entry per lane like ExpTableLanes.
-struct Exp2TableLanes {
-    double hi, lo;
-    __device__ explicit Exp2TableLanes(int lane)
-        : hi(chelis_exp2_64_tab[lane][0]), lo(chelis_exp2_64_tab[lane][1]) {}
+// 2^(j/64) as a double-double, read from the block's LDS copy: one 16-byte
+// LDS read per lookup where a lane-held copy took four lane shuffles and
+// four registers (the f64 softmax row: 58 against 64-68 us for [4096, 4096]
+// on one box, bit-identical).
+struct Exp2TableLds {
+    const double2 *t;
     __device__ void operator()(int j, double &h, double &l) const {
-        h = __shfl(hi, j, 64);
-        l = __shfl(lo, j, 64);
+        const double2 e = t[j];
+        h = e.x;
+        l = e.y;
     }
 };
 
-// The lane-held exp table of each dtype. Kernels build it before their row
-// loads, so waiting for it never waits for a row.
+// The exp table of each dtype, built before the row loads so waiting for it
+// never waits for a row: binary32 holds it one entry per lane, binary64 in
+// LDS (filled by the kernel's first wave).
 template <typename T>
 struct RowExpTab;
 template <>
 struct RowExpTab<float> {
     using type = ExpTableLanes;
+    __device__ static type make(int lane, const double2 *) { return type(lane); }
 };
 template <>
 struct RowExpTab<double> {
-    using type = Exp2TableLanes;
+    using type = Exp2TableLds;
+    __device__ static type make(int, const double2 *lds) { return type{lds}; }
 };
 
 // Which of a lane's NE exp results need the correctly rounded fallback.
@@ -439,10 +444,15 @@ __global__ __launch_bounds__(64 * W * R) void softmax_kernel(const T *__restrict
     const int64_t n = DENSE ? (int64_t)S * SEG : n_arg;
     const bool vec_ok = DENSE || vec_ok_arg;
     const int masked = DENSE ? 0 : masked_arg;
+    __shared__ double2 exp_tab[sizeof(T) == 8 ? 64 : 1];
+    if constexpr (sizeof(T) == 8) {
+        if (threadIdx.x < 64) exp_tab[threadIdx.x] = double2{chelis_exp2_64_tab[threadIdx.x][0], chelis_exp2_64_tab[threadIdx.x][1]};
+        __syncthreads();
+    }
     RowCoord<W, R> c;
     if (c.row >= rows) return;  // whole row groups exit together (R rows per block, W waves each)
     const T *xr = x + c.row * ldx;
-    const typename RowExpTab<T>::type tab(c.lane);
+    const typename RowExpTab<T>::type tab = RowExpTab<T>::make(c.lane, exp_tab);
     T v[S][V];
     // causal rows read only j <= qi: the mask turns every later element into
     // -inf whatever it holds, which is the padding value
@@ -571,9 +581,16 @@ int32_t launch_rows(RowOp op, const RowArgs &a) {
     const int64_t n = a.n;
     if (n <= seg1) return launch_shape<T, V, 1, 1, 4>(op, a, st);
     if (n <= 2 * seg1) return launch_shape<T, V, 2, 1, 4>(op, a, st);
-    // one row per 64-lane block: blocks retire independently, so the waves
-    // of a CU drift apart and one wave's loads overlap another's arithmetic
-    if (n <= 4 * seg1) return launch_shape<T, V, 4, 1, 1>(op, a, st);
+    // binary32 rows of 513-1024: two waves per row, two segments each
+    // (23.4 against 24.2 us for [16384, 1024] with one wave of four
+    // segments, same box: the shorter per-wave dependency chain keeps more
+    // stores in flight); other rows of this bucket: one row per 64-lane
+    // block, so blocks retire independently and the waves of a CU drift
+    // apart, one wave's loads overlapping another's arithmetic
+    if (n <= 4 * seg1) {
+        if constexpr (sizeof(T) == 4) return launch_shape<T, V, 2, 2, 1>(op, a, st);
+        return launch_shape<T, V, 4, 1, 1>(op, a, st);
+    }
     if (n <= 8 * seg1) return launch_shape<T, V, 8, 1, 2>(op, a, st);
     if (n <= 16 * seg1) return launch_shape<T, V, 4, 4, 1>(op, a, st);
     if (n <= 32 * seg1) return launch_shape<T, V, 8, 4, 1>(op, a, st);

@@ -95,9 +95,9 @@ def test_tree_kernels_bit_exact(case, dtype):
     a, b = rand(rng, (M, K), dtype), rand(rng, (K, N), dtype)
     _da, va, na = dev_view(a, M, K, ta)
     _db, vb, nb = dev_view(b, K, N, tb)
-    # f32 with a narrow side of 16..64 is an MFMA shape; the exact flag keeps
-    # it on the canonical tree (the column-panel kernel)
-    exact = dtype == np.float32 and K > 32 and min(M, N) >= 16
+    # a narrow side of 16..64 is an MFMA shape; the exact flag keeps it on
+    # the canonical tree (the column-panel kernel)
+    exact = K > 32 and min(M, N) >= 16
     c = C.matmul(va, vb, exact=exact).numpy()
     ref = O.matmul(na, nb)
     assert bits_equal(c, ref), first_diff(c, ref)
@@ -111,12 +111,15 @@ def test_exact_flag_on_dense_shape(dtype):
     assert bits_equal(c, O.matmul(a, b))
 
 
-def test_f64_skinny_band_is_exact():
-    """f64 with min(M, N) <= 64 stays on the canonical tree."""
+def test_f64_skinny_band_tolerance_and_exact_flag():
+    """f64 with 16 <= min(M, N) <= 64 runs on the MFMA tiles within the 1e-10
+    GEMM tolerance; the exact flag keeps it on the canonical tree."""
     rng = np.random.default_rng(22)
     a, b = rand(rng, (700, 900), np.float64), rand(rng, (900, 64), np.float64)
+    ref = O.matmul(a, b)
     c = C.matmul(C.to_device(a), C.to_device(b)).numpy()
-    assert bits_equal(c, O.matmul(a, b))
+    check_close(c, ref, np.float64)
+    assert bits_equal(C.matmul(C.to_device(a), C.to_device(b), exact=True).numpy(), ref)
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
@@ -157,11 +160,15 @@ def test_config_3d_gemv_bit_exact():
     assert y.shape == (8192,) and bits_equal(y, ref)
 
 
-def test_config_3c_skinny_bit_exact():
+def test_config_3c_skinny():
+    """Config 3c at full size: the default (MFMA, split-K) result within the
+    1e-10 f64 GEMM tolerance, the exact flag's bit-exact."""
     A = np.random.default_rng(24).uniform(-1, 1, (8192, 4096))
     B = np.random.default_rng(25).uniform(-1, 1, (4096, 64))
-    c = C.matmul(C.to_device(A), C.to_device(B)).numpy()
-    assert bits_equal(c, O.matmul(A, B))
+    ref = O.matmul(A, B)
+    dA, dB = C.to_device(A), C.to_device(B)
+    check_close(C.matmul(dA, dB).numpy(), ref, np.float64)
+    assert bits_equal(C.matmul(dA, dB, exact=True).numpy(), ref)
 
 
 MFMA_CASES = [
@@ -177,8 +184,6 @@ MFMA_CASES = [
 @pytest.mark.parametrize("case", MFMA_CASES)
 def test_mfma_within_tolerance(case, dtype):
     M, N, K, ta, tb = case
-    if dtype == np.float64 and min(M, N) <= 64:
-        pytest.skip("f64 narrow shapes take the tree path")
     rng = np.random.default_rng(M + N + K)
     a, b = rand(rng, (M, K), dtype), rand(rng, (K, N), dtype)
     _da, va, na = dev_view(a, M, K, ta)
@@ -243,13 +248,14 @@ def test_linear_epilogue_on_swapped_panel_path():
 def test_linear_per_batch_bias():
     """A stack of projections: a broadcast over the batch, b and bias with one
     entry per batch ([batch, K, N] and [batch, N]), bit-exact on the tree
-    path; and the same on an MFMA shape within tolerance."""
+    path (the exact flag: an f64 narrow side of 40 is an MFMA shape by
+    default); and the same on an MFMA shape within tolerance."""
     rng = np.random.default_rng(44)
     x = rand(rng, (96, 200), np.float64)
     w, bias = rand(rng, (3, 200, 40), np.float64), rand(rng, (3, 40), np.float64)
     dx = C.to_device(x)
     x3 = dx.view((3, 96, 200), (0, 200, 1))
-    c = C.linear(x3, C.to_device(w), C.to_device(bias)).numpy()
+    c = C.linear(x3, C.to_device(w), C.to_device(bias), exact=True).numpy()
     for j in range(3):
         assert bits_equal(c[j], O.matmul(x, w[j]) + bias[j]), j
     xf = rand(rng, (256, 128), np.float32)
