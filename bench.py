@@ -12,16 +12,22 @@ average launch time, timed with HIP events recorded on the library stream
 (the stream every launcher enqueues on) around exactly K launches.
 
 `roofline.traffic` is the HBM bytes one softmax launch moves, from two
-rocprofv3 --pmc runs of this script (FETCH_SIZE, then WRITE_SIZE), each
-scaled by what the same counter reads for a plain 256 MiB relu map (a
-read-once, write-once elementwise kernel of known size).
+rocprofv3 --pmc passes over a child run of this script (FETCH_SIZE, then
+WRITE_SIZE), each scaled by what the same counter reads for a plain 256 MiB
+relu map (a read-once, write-once elementwise kernel of known size). The
+same passes give every bandwidth kernel in `kernels` its measured traffic
+(`hbm_traffic_bytes`, `traffic_ratio` against the algorithmic bytes,
+`frac_hbm_counter`), and a third and fourth pass (SQ_VALU_MFMA_BUSY_CYCLES,
+GRBM_GUI_ACTIVE, the MFMA op counts) give the GEMMs their MFMA busy share.
 
 `kernels` reports every configuration the same way: GB/s against the 8 TB/s
 HBM peak for bandwidth kernels, TFLOP/s against the dtype's MFMA peak for
 GEMMs, ms / us end to end for the three programs. `cpu_baseline` times the C
 oracle (the restated reference C lane, gcc -O2 -ffp-contract=off -fopenmp)
-on the headline workload on this host; `kernels[*].cpu_ms` gives the same
-oracle's time on a bounded sample of the other configurations.
+on the headline workload on this host with every core (5 warm-ups, median
+of 50 calls) and once on one thread; `kernels[*].cpu` gives the same
+oracle's median on the other configurations, on the stated sample where the
+full size would take minutes (never scaled up).
 """
 from __future__ import annotations
 
@@ -45,7 +51,6 @@ HBM_PEAK_GBPS = 8000.0
 PEAK_TFLOPS = {"f32": 157.3, "f64": 78.6, "bf16": 2500.0}
 METRIC = "per-kernel GB/s & GFLOP/s (% roofline); transformer-block fwd ms at 1 GPU"
 SOFTMAX_ROWS, SOFTMAX_N = 16384, 1024
-COPY_ELEMS = 64 * 1024 * 1024  # f32 relu map used to calibrate the HBM counters
 
 
 def host_cores() -> int:
@@ -242,125 +247,308 @@ def bench_bandwidth(C, H, steps, warmup):
     return out
 
 
-# ---------------------------------------------------------------- traffic
-def traffic_child():
-    """Runs under rocprofv3 --pmc: 10 headline softmax launches and 10
-    launches of the relu map used as the calibration copy."""
+# ---------------------------------------------------------------- counters
+# Kernels whose HBM traffic (FETCH_SIZE then WRITE_SIZE, one rocprofv3 --pmc
+# pass each) is read per dispatch, each with the algorithmic bytes one
+# launch moves and the kernel-name pattern of its dispatches. The relu map
+# is also the calibration: FETCH_SIZE / WRITE_SIZE read in units whose size
+# the relu's known bytes fix.
+CAUSAL_READ = 8 * 16 * (512 * 513 // 2) * 4  # causal score rows read only j <= i
+BW_SET = [
+    ("softmax_f32_16384x1024", r"softmax_kernel<float,.*true>", 2 * 16384 * 1024 * 4),
+    ("softmax_f64_4096x4096", r"softmax_kernel<double", 2 * 4096 * 4096 * 8),
+    ("gemv_f64_8192x8192", r"tree_wave_kernel<double", 8192 * 8192 * 8 + 2 * 8192 * 8),
+    ("layer_norm_f32_65536x1024", r"layer_norm_kernel<float", 2 * 65536 * 1024 * 4),
+    ("relu_f32_16384x4096", r"unary_kernel<float", 2 * 16384 * 4096 * 4),
+    ("fused_chain_sqdiff_f32_16384x4096", r"fused_flat_vec_kernel<float", 3 * 16384 * 4096 * 4),
+    ("reduce_sum_rows_f32_16384x4096", r"reduce_rows_vec_kernel<float", 16384 * 4096 * 4 + 16384 * 4),
+    ("softmax_adjoint_f32_65536x1024", r"softmax_adjoint_kernel<float", 3 * 65536 * 1024 * 4),
+    ("causal_softmax_f32_8x16x512x512", r"softmax_kernel<float,.*false>", CAUSAL_READ + 8 * 16 * 512 * 512 * 4),
+]
+CALIBRATION = "relu_f32_16384x4096"
+# GEMMs whose MFMA activity is read (SQ_VALU_MFMA_BUSY_CYCLES per SIMD over
+# the dispatch's GRBM_GUI_ACTIVE cycles, and the MFMA math ops).
+MFMA_SET = [
+    ("gemm_f32_4096^3", r"gemm_mfma_kernel<float"),
+    ("gemm_f64_4096^3", r"gemm_mfma_kernel<double, \d, \d, 4,"),
+    ("skinny_f64_8192x64x4096", r"gemm_mfma_kernel<double, \d, \d, 2,"),
+]
+TRANSFORMER_SET = [("transformer_block_f32_b8_s512_d1024", r"gemm_mfma_kernel<float")]
+SIMDS = 1024  # 256 CUs x 4 SIMDs
+PROFILE_LAUNCHES = 3
+
+
+def profile_child(kind: str):
+    """Runs under rocprofv3: a few launches of every kernel of one set."""
     import chelis_amd as C
 
-    x = softmax_inputs()
-    pairs = [(C.to_device(x), C.empty(x.shape, np.float32)) for _ in range(5)]
-    src = C.to_device(np.abs(np.random.default_rng(5).standard_normal(COPY_ELEMS)).astype(np.float32))
-    dst = C.empty((COPY_ELEMS,), np.float32)
-    for i in range(10):
-        C.softmax(pairs[i % 5][0], pairs[i % 5][1])
-    for _ in range(10):
-        C.relu(src, dst)
+    rng = np.random.default_rng(5)
+    n = PROFILE_LAUNCHES
+    if kind == "bandwidth":
+        x = softmax_inputs()
+        pairs = [(C.to_device(x), C.empty(x.shape, np.float32)) for _ in range(5)]
+        for i in range(n):
+            C.softmax(pairs[i % 5][0], pairs[i % 5][1])
+        x64 = np.random.default_rng(11).standard_normal((4096, 4096))
+        p64 = [(C.to_device(x64), C.empty(x64.shape, np.float64)) for _ in range(2)]
+        for i in range(n):
+            C.softmax(p64[i % 2][0], p64[i % 2][1])
+        del pairs, p64
+        A = C.to_device(rng.uniform(-1, 1, (8192, 8192)))
+        v = C.to_device(rng.uniform(-1, 1, 8192))
+        out = C.empty((8192,), np.float64)
+        for _ in range(n):
+            C.matmul(A, v, out)
+        del A
+        xs = rng.standard_normal((65536, 1024)).astype(np.float32)
+        XS = [C.to_device(xs) for _ in range(2)]
+        YS = C.empty(xs.shape, np.float32)
+        gam, bet = C.to_device(np.ones(1024, np.float32)), C.to_device(np.zeros(1024, np.float32))
+        for i in range(n):
+            C.layer_norm(XS[i % 2], gam, bet, 1e-5, YS)
+        for i in range(n):
+            C.softmax_adjoint(XS[i % 2], XS[(i + 1) % 2], YS)
+        del XS, YS
+        xb = rng.standard_normal((16384, 4096)).astype(np.float32)
+        X, G, Y = C.to_device(xb), C.to_device(xb), C.empty(xb.shape, np.float32)
+        for _ in range(n):
+            C.relu(X, Y)
+        sq = C.fused_chain([("sub", 0, 1), ("mul", ("s", 0), ("s", 0))])
+        for _ in range(n):
+            C.fused_elementwise(sq, [X, G], Y)
+        S1 = C.empty((16384,), np.float32)
+        for _ in range(n):
+            C.reduce("sum", X, 1, S1)
+        del X, G, Y
+        s = C.to_device(rng.standard_normal((8, 16, 512, 512)).astype(np.float32))
+        so = C.empty((8, 16, 512, 512), np.float32)
+        for _ in range(n):
+            C.scaled_masked_softmax(s, 0.125, True, so)
+    elif kind == "mfma":
+        for (M, N, K, dt, seeds) in ((4096, 4096, 4096, np.float32, (20, 21)), (4096, 4096, 4096, np.float64, (22, 23)),
+                                     (8192, 64, 4096, np.float64, (24, 25))):
+            a = C.to_device(np.random.default_rng(seeds[0]).uniform(-1, 1, (M, K)).astype(dt))
+            b = C.to_device(np.random.default_rng(seeds[1]).uniform(-1, 1, (K, N)).astype(dt))
+            c = C.matmul(a, b)
+            for _ in range(n):
+                C.matmul(a, b, c)
+    elif kind == "transformer":
+        x, prm = transformer_data()
+        ins = [C.to_device(x)] + [C.to_device(prm[k]) for k in PARAM_ORDER]
+        y = C.empty(x.shape, np.float32)
+        C.program("transformer_block", ins, [y])
     C.synchronize()
 
 
 def _counter_rows(outdir):
-    files = glob.glob(os.path.join(outdir, "**", "*counter_collection*.csv"), recursive=True)
     rows = []
-    for f in files:
+    for f in glob.glob(os.path.join(outdir, "**", "*counter_collection*.csv"), recursive=True):
         with open(f, newline="") as fh:
             rows.extend(csv.DictReader(fh))
     return rows
 
 
-def measure_traffic(timeout_s=120):
-    """HBM bytes per softmax launch from FETCH_SIZE and WRITE_SIZE, each
-    scaled by the relu calibration map; None when rocprofv3 is unavailable."""
+def _pmc_pass(counters, kind, keep_dir=None, timeout_s=240):
+    """One rocprofv3 --pmc pass over a profile child; returns a list of
+    (kernel name, {counter: value}) per dispatch, and the command run."""
     prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
     if not os.path.exists(prof):
-        return None, "rocprofv3 not found"
-    per = {}
-    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
-        outdir = tempfile.mkdtemp(prefix="chelis_pmc_")
-        try:
-            cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", outdir, "-o", "pmc", "--",
-                   sys.executable, os.path.abspath(__file__), "--traffic-child"]
-            r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout_s)
-            rows = _counter_rows(outdir)
-            if not rows:
-                return None, f"rocprofv3 --pmc {counter} produced no counter rows (rc {r.returncode})"
-            vals = {"softmax": [], "relu": []}
-            for row in rows:
-                name = row.get("Kernel_Name", "")
-                if row.get("Counter_Name", counter) != counter:
-                    continue
-                v = float(row.get("Counter_Value", "nan"))
-                if "softmax_kernel" in name:
-                    vals["softmax"].append(v)
-                elif "unary_kernel" in name:
-                    vals["relu"].append(v)
-            if not vals["softmax"] or not vals["relu"]:
-                return None, f"{counter}: kernels not found in the counter rows"
-            per[counter] = {k: float(np.median(v)) for k, v in vals.items()}
-        finally:
+        raise RuntimeError("rocprofv3 not found")
+    outdir = keep_dir or tempfile.mkdtemp(prefix="chelis_pmc_")
+    cmd = [prof, "--pmc", *counters, "--output-format", "csv", "-d", outdir, "-o", "pmc", "--",
+           sys.executable, os.path.abspath(__file__), "--profile-child", kind]
+    try:
+        subprocess.run(cmd, capture_output=True, text=True, timeout=timeout_s)
+        per = {}
+        for row in _counter_rows(outdir):
+            did = row.get("Dispatch_Id") or row.get("Correlation_Id") or str(len(per))
+            ent = per.setdefault(did, (row.get("Kernel_Name", ""), {}))
+            ent[1][row.get("Counter_Name", "")] = float(row.get("Counter_Value", "nan"))
+            try:
+                ent[1]["_dur_ns"] = float(row["End_Timestamp"]) - float(row["Start_Timestamp"])
+            except (KeyError, ValueError):
+                pass
+    finally:
+        if keep_dir is None:
             shutil.rmtree(outdir, ignore_errors=True)
-    copy_bytes = COPY_ELEMS * 4
-    f_scale = copy_bytes / per["FETCH_SIZE"]["relu"]
-    w_scale = copy_bytes / per["WRITE_SIZE"]["relu"]
-    fetch = per["FETCH_SIZE"]["softmax"] * f_scale
-    write = per["WRITE_SIZE"]["softmax"] * w_scale
-    detail = {"fetch_bytes": round(fetch), "write_bytes": round(write),
-              "raw_kib": {"fetch_softmax": per["FETCH_SIZE"]["softmax"], "write_softmax": per["WRITE_SIZE"]["softmax"],
-                          "fetch_copy": per["FETCH_SIZE"]["relu"], "write_copy": per["WRITE_SIZE"]["relu"]},
-              "scale": {"fetch": round(f_scale, 3), "write": round(w_scale, 3)},
-              "calibration": f"relu map of {copy_bytes} B read + {copy_bytes} B written"}
-    return fetch + write, detail
+    shown = " ".join(["rocprofv3", "--pmc", *counters, "--output-format", "csv", "-d", "<dir>", "-o", "pmc", "--",
+                      "python3", "bench.py", "--profile-child", kind])
+    return list(per.values()), shown
+
+
+def _median_of(dispatches, pattern, counter):
+    import re
+
+    vals = [c[counter] for name, c in dispatches if re.search(pattern, name) and counter in c]
+    return (float(np.median(vals)), len(vals)) if vals else (None, 0)
+
+
+def measure_counters(kernels, keep_root=None):
+    """HBM bytes per dispatch of every BW_SET kernel and MFMA utilization of
+    every MFMA_SET / TRANSFORMER_SET kernel, attached to `kernels`; returns
+    the headline's roofline traffic figures and a summary of the passes."""
+    keep = (lambda name: os.path.join(keep_root, name)) if keep_root else (lambda name: None)
+    fetch, cmd_f = _pmc_pass(["FETCH_SIZE"], "bandwidth", keep("fetch"))
+    write, cmd_w = _pmc_pass(["WRITE_SIZE"], "bandwidth", keep("write"))
+    calib = dict((k, (pat, b)) for k, pat, b in BW_SET)[CALIBRATION]
+    f_unit, _ = _median_of(fetch, calib[0], "FETCH_SIZE")
+    w_unit, _ = _median_of(write, calib[0], "WRITE_SIZE")
+    if not f_unit or not w_unit:
+        raise RuntimeError("calibration kernel missing from the counter rows")
+    f_scale, w_scale = (calib[1] / 2) / f_unit, (calib[1] / 2) / w_unit
+    summary = {"commands": [cmd_f, cmd_w],
+               "calibration": f"{CALIBRATION}: {calib[1] // 2} B read and written; FETCH_SIZE unit "
+                              f"{f_scale:.1f} B, WRITE_SIZE unit {w_scale:.1f} B",
+               "bandwidth": {}, "mfma": {}}
+    for key, pat, alg in BW_SET:
+        fv, nf = _median_of(fetch, pat, "FETCH_SIZE")
+        wv, nw = _median_of(write, pat, "WRITE_SIZE")
+        if fv is None or wv is None:
+            continue
+        traffic = fv * f_scale + wv * w_scale
+        rec = {"fetch_bytes": round(fv * f_scale), "write_bytes": round(wv * w_scale),
+               "traffic_bytes": round(traffic), "algorithmic_bytes": alg, "traffic_ratio": round(traffic / alg, 4),
+               "dispatches": min(nf, nw)}
+        summary["bandwidth"][key] = rec
+        if key in kernels:
+            k = kernels[key]
+            k["hbm_traffic_bytes"] = rec["traffic_bytes"]
+            k["traffic_ratio"] = rec["traffic_ratio"]
+            t_s = (k["ms"] * 1e-3) if "ms" in k else (k["us"] * 1e-6 if "us" in k else None)
+            if t_s:
+                k["frac_hbm_counter"] = round(traffic / t_s / 1e9 / HBM_PEAK_GBPS, 4)
+    counters = ["SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE", "SQ_INSTS_VALU_MFMA_MOPS_F32",
+                "SQ_INSTS_VALU_MFMA_MOPS_F64"]
+    for kind, entries in (("mfma", MFMA_SET), ("transformer", TRANSFORMER_SET)):
+        disp, cmd = _pmc_pass(counters, kind, keep("mfma_" + kind))
+        summary["commands"].append(cmd)
+        import re
+
+        for key, pat in entries:
+            sel = [c for name, c in disp if re.search(pat, name) and "GRBM_GUI_ACTIVE" in c]
+            if not sel:
+                continue
+            busy = sum(c.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) for c in sel)
+            active = sum(c["GRBM_GUI_ACTIVE"] for c in sel)
+            mops = sum(c.get("SQ_INSTS_VALU_MFMA_MOPS_F32", 0.0) + c.get("SQ_INSTS_VALU_MFMA_MOPS_F64", 0.0)
+                       for c in sel)
+            dur = sum(c.get("_dur_ns", 0.0) for c in sel)
+            # GRBM_GUI_ACTIVE counts GPU clock cycles; where it is summed
+            # over the 8 XCDs its rate per ns reads 8x the ~2.4 GHz clock
+            per_xcd = 8 if dur > 0 and active / dur > 4.0 else 1
+            rec = {"mfma_busy_pct": round(100.0 * busy / (active / per_xcd * SIMDS), 2), "dispatches": len(sel),
+                   "mfma_flop_per_dispatch": round(mops * 512 / len(sel)),
+                   "busy_cycles": busy, "gui_active_cycles": active, "gui_active_xcd_sum": per_xcd == 8,
+                   "clock_ghz": round(active / per_xcd / dur, 3) if dur > 0 else None}
+            summary["mfma"][key] = rec
+            if key in kernels:
+                kernels[key]["mfma_busy_pct_counter"] = rec["mfma_busy_pct"]
+    head = summary["bandwidth"].get("softmax_f32_16384x1024")
+    return head, summary
+
+
+def counters_markdown(summary) -> str:
+    lines = ["# HBM traffic and MFMA activity per kernel (rocprofv3 counters)", "",
+             "Commands (each a pass of its own; `bench.py` runs them with `--counters`):", ""]
+    lines += [f"    cd /tmp && export TMPDIR=/tmp && {c}" for c in summary["commands"]]
+    lines += ["", summary["calibration"], "",
+              "| kernel | FETCH bytes | WRITE bytes | traffic | algorithmic | traffic / algorithmic |",
+              "|---|---|---|---|---|---|"]
+    for k, r in summary["bandwidth"].items():
+        lines.append(f"| {k} | {r['fetch_bytes']} | {r['write_bytes']} | {r['traffic_bytes']} | "
+                     f"{r['algorithmic_bytes']} | {r['traffic_ratio']} |")
+    lines += ["", "MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 1024 SIMDs); the clock is "
+                  "GRBM_GUI_ACTIVE over the dispatch's duration.", "",
+              "| GEMM | MFMA busy (% of SIMD cycles) | MFMA flop per dispatch | clock GHz | dispatches |",
+              "|---|---|---|---|---|"]
+    for k, r in summary["mfma"].items():
+        lines.append(f"| {k} | {r['mfma_busy_pct']} | {r['mfma_flop_per_dispatch']} | {r['clock_ghz']} | "
+                     f"{r['dispatches']} |")
+    return "\n".join(lines) + "\n"
 
 
 # ---------------------------------------------------------------- CPU baselines
-def _time_cpu(fn, budget_s, max_runs=20):
-    fn()
-    runs, t0 = 0, time.perf_counter()
-    while True:
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _time_cpu(fn, warmup, runs, budget_s=None):
+    """`warmup` untimed calls, then the median of
+    `runs` timed calls of the entry alone; with `budget_s`, warm-up stops
+    after a third of it and timing after all of it (at least one of each)."""
+    t_all = time.perf_counter()
+    for i in range(warmup):
         fn()
-        runs += 1
-        el = time.perf_counter() - t0
-        if el > budget_s or runs >= max_runs:
-            return el / runs, runs
+        if budget_s is not None and time.perf_counter() - t_all > budget_s / 3:
+            break
+    times = []
+    t_all = time.perf_counter()
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if budget_s is not None and time.perf_counter() - t_all > budget_s:
+            break
+    return float(np.median(times)), len(times)
 
 
-def cpu_baselines(x_softmax, kernels, linreg, transformer, mlp, gemm_inputs):
+def cpu_baselines(x_softmax, x64, kernels, linreg, transformer, mlp, gemm_inputs):
+    """The C oracle on this host with every core, timed per BASELINE.md
+    section 3 (5 warm-ups, the median of 50 timed calls; the 4096^3 GEMMs on
+    a stated slice of their rows, whose rate is reported, not scaled up),
+    plus one single-thread run of the headline."""
     from oracle import oracle as O
 
     O.build()
-    cores = host_cores()
-    os.environ.setdefault("OMP_NUM_THREADS", str(cores))
-    threads = int(os.environ["OMP_NUM_THREADS"])
-    per, runs = _time_cpu(lambda: O.softmax_rows(x_softmax), 10.0)
+    threads = host_cores()
+    O.lib().orc_set_threads(threads)
+    per, runs = _time_cpu(lambda: O.softmax_rows(x_softmax), 5, 50)
+    O.lib().orc_set_threads(1)
+    single, _ = _time_cpu(lambda: O.softmax_rows(x_softmax), 1, 1)
+    O.lib().orc_set_threads(threads)
     head = {"value": round(x_softmax.nbytes * 2 / per / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"the full config 2a tensor [16384,1024] f32, {runs} runs of the oracle softmax "
-                      f"(gcc -O2 -ffp-contract=off -fopenmp, CORE-MATH expf), {per * 1e3:.1f} ms per run"}
+            "sample": f"the full config 2a tensor [16384,1024] f32: median of {runs} oracle softmax calls after 5 "
+                      f"warm-ups ({per * 1e3:.2f} ms each), gcc -O2 -ffp-contract=off -fopenmp, CORE-MATH expf",
+            "single_thread": {"value": round(x_softmax.nbytes * 2 / single / 1e9, 3), "unit": "GB/s",
+                              "ms": round(single * 1e3, 2)},
+            "cpu_model": cpu_model()}
+
+    def put(key, t, n, sample=None, rate=None):
+        ent = {"ms": round(t * 1e3, 3), "median_of": n}
+        if sample:
+            ent["sample"] = sample
+        if rate:
+            ent.update(rate)
+        kernels[key]["cpu"] = ent
+
     X, w, y = linreg
-    t, _ = _time_cpu(lambda: O.linreg_step(X, w, y), 2.0)
-    kernels["linreg_step_f64_8192x32"]["cpu_ms"] = round(t * 1e3, 3)
-    a, b = gemm_inputs["f32"]
-    t, _ = _time_cpu(lambda: O.matmul(np.ascontiguousarray(a[:128]), b), 3.0, 3)
-    kernels["gemm_f32_4096^3"]["cpu_ms"] = round(t * 1e3 * 32, 1)
-    a, b = gemm_inputs["f64"]
-    t, _ = _time_cpu(lambda: O.matmul(np.ascontiguousarray(a[:128]), b), 3.0, 3)
-    kernels["gemm_f64_4096^3"]["cpu_ms"] = round(t * 1e3 * 32, 1)
-    a, b = gemm_inputs["skinny"]
-    t, _ = _time_cpu(lambda: O.matmul(np.ascontiguousarray(a[:1024]), b), 3.0, 5)
-    kernels["skinny_f64_8192x64x4096"]["cpu_ms"] = round(t * 1e3 * 8, 2)
+    put("linreg_step_f64_8192x32", *_time_cpu(lambda: O.linreg_step(X, w, y), 5, 50))
+    put("softmax_f64_4096x4096", *_time_cpu(lambda: O.softmax_rows(x64), 5, 50, budget_s=15))
+    for key, (a, b), rows in (("gemm_f32_4096^3", gemm_inputs["f32"], 64), ("gemm_f64_4096^3", gemm_inputs["f64"], 64),
+                              ("skinny_f64_8192x64x4096", gemm_inputs["skinny"], 1024)):
+        sub = np.ascontiguousarray(a[:rows])
+        t, n = _time_cpu(lambda: O.matmul(sub, b), 5, 10, budget_s=15)
+        flops = 2 * rows * b.shape[0] * b.shape[1]
+        put(key, t, n, f"the first {rows} of {a.shape[0]} rows of A (the same contraction per output)",
+            {"GFLOP/s": round(flops / t / 1e9, 2)})
     a, b = gemm_inputs["gemv"]
-    t, _ = _time_cpu(lambda: O.matmul(a, b.reshape(-1, 1)), 3.0, 5)
-    kernels["gemv_f64_8192x8192"]["cpu_ms"] = round(t * 1e3, 2)
+    put("gemv_f64_8192x8192", *_time_cpu(lambda: O.matmul(a, b.reshape(-1, 1)), 5, 50, budget_s=15))
     xs, p = transformer
-    t, _ = _time_cpu(lambda: O.transformer_block(np.ascontiguousarray(xs[:1]), p, 16), 5.0, 2)
-    kernels["transformer_block_f32_b8_s512_d1024"]["cpu_ms"] = round(t * 1e3 * 8, 1)
-    t, _ = _time_cpu(lambda: O.mlp_train_step(*mlp, 44, np.float32(0.1), np.float32(0.01)), 3.0, 5)
-    kernels["mlp_train_step_f32_1024x784x512x10"]["cpu_ms"] = round(t * 1e3, 2)
-    kernels["_cpu_note"] = (f"C oracle on {threads} host threads; GEMM 4096^3 timed on 128 rows x32, skinny on "
-                            f"1024 rows x8, transformer on batch 1 x8; others full size")
-    x64 = kernels.pop("_softmax_f64_input", None)
-    if x64 is not None:
-        t, _ = _time_cpu(lambda: O.softmax_rows(x64), 5.0, 5)
-        kernels["softmax_f64_4096x4096"]["cpu_ms"] = round(t * 1e3, 2)
+    one = np.ascontiguousarray(xs[:1])
+    t, n = _time_cpu(lambda: O.transformer_block(one, p, 16), 1, 3, budget_s=20)
+    put("transformer_block_f32_b8_s512_d1024", t, n, "batch 1 of 8 (one 512-token sequence)",
+        {"tokens/s": round(512 / t, 1)})
+    put("mlp_train_step_f32_1024x784x512x10",
+        *_time_cpu(lambda: O.mlp_train_step(*mlp, 44, np.float32(0.1), np.float32(0.01)), 5, 50, budget_s=15))
+    kernels["_cpu_note"] = (f"C oracle on {threads} threads of a {cpu_model()}; medians after 5 warm-ups; samples as "
+                            f"stated per entry (no extrapolation)")
     return head
 
 
@@ -370,12 +558,14 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic runs")
+    ap.add_argument("--no-counters", action="store_true", help="skip the rocprofv3 --pmc counter passes")
+    ap.add_argument("--counters-dir", default=None, help="keep the raw counter output here")
+    ap.add_argument("--counters-md", default=None, help="write the counter summary as markdown here")
     ap.add_argument("--only-headline", action="store_true")
-    ap.add_argument("--traffic-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--profile-child", choices=("bandwidth", "mfma", "transformer"), help=argparse.SUPPRESS)
     args = ap.parse_args(argv)
-    if args.traffic_child:
-        traffic_child()
+    if args.profile_child:
+        profile_child(args.profile_child)
         return 0
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -404,7 +594,7 @@ def main(argv=None) -> int:
         r, gin["f64"] = bench_gemm(C, H, 4096, 4096, 4096, np.float64, (22, 23), gs, gw)
         kernels["gemm_f64_4096^3"] = gemm_line(r, "f64", "mfma")
         r, gin["skinny"] = bench_gemm(C, H, 8192, 64, 4096, np.float64, (24, 25), gs, gw, reps=2)
-        kernels["skinny_f64_8192x64x4096"] = gemm_line(r, "f64", "valu canonical tree (bit-exact)")
+        kernels["skinny_f64_8192x64x4096"] = gemm_line(r, "f64", "mfma (64-tiles, split-K)")
         r, gin["gemv"] = bench_gemm(C, H, 8192, 1, 8192, np.float64, (26, 27), gs, gw, reps=2)
         kernels["gemv_f64_8192x8192"] = gemm_line(r, "f64", "hbm")
         # bf16 (np.uint16 bit patterns) with the binary32 accumulator
@@ -414,22 +604,34 @@ def main(argv=None) -> int:
         kernels.update(progs)
         kernels.update(bench_bandwidth(C, H, max(5, args.steps // 2), args.warmup))
         extra = (x64, lin, tr, mlp, gin)
-    traffic, tdetail = (None, "skipped") if args.no_traffic else measure_traffic()
+    traffic, tdetail = None, "skipped (--no-counters)"
+    if not args.no_counters:
+        try:
+            hrec, summary = measure_counters(kernels, args.counters_dir)
+            if hrec is not None:
+                traffic = hrec["traffic_bytes"]
+                tdetail = (f"FETCH {hrec['fetch_bytes']} B + WRITE {hrec['write_bytes']} B per launch, median of "
+                           f"{hrec['dispatches']} dispatches; {summary['calibration']}")
+            if args.counters_md:
+                with open(args.counters_md, "w") as fh:
+                    fh.write(counters_markdown(summary))
+        except Exception as e:  # the counters are evidence beside the timing, not the timing
+            tdetail = f"counter passes failed: {e}"
     cpu = None
     if not args.no_cpu:
         if extra is not None:
             x64, lin, tr, mlp, gin = extra
-            kernels["_softmax_f64_input"] = x64
-            cpu = cpu_baselines(x, kernels, lin, tr, mlp, gin)
+            cpu = cpu_baselines(x, x64, kernels, lin, tr, mlp, gin)
         else:
             from oracle import oracle as O
 
             O.build()
-            os.environ.setdefault("OMP_NUM_THREADS", str(host_cores()))
-            per, runs = _time_cpu(lambda: O.softmax_rows(x), 10.0)
-            cpu = {"value": round(x.nbytes * 2 / per / 1e9, 3), "unit": "GB/s",
-                   "cores": int(os.environ["OMP_NUM_THREADS"]), "kind": "port",
-                   "sample": f"the full config 2a tensor, {runs} runs of the oracle softmax, {per * 1e3:.1f} ms/run"}
+            O.lib().orc_set_threads(host_cores())
+            per, runs = _time_cpu(lambda: O.softmax_rows(x), 5, 50)
+            cpu = {"value": round(x.nbytes * 2 / per / 1e9, 3), "unit": "GB/s", "cores": host_cores(),
+                   "kind": "port", "cpu_model": cpu_model(),
+                   "sample": f"the full config 2a tensor: median of {runs} oracle softmax calls, "
+                             f"{per * 1e3:.2f} ms each"}
     line = {
         "metric": METRIC,
         "value": round(head["gbps"], 2),

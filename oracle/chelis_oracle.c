@@ -15,6 +15,7 @@
 #include "chelis_oracle.h"
 
 #include <math.h>
+#include <omp.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -28,6 +29,14 @@ float chelis_crmath_ffi_erfcf(float);
 double chelis_crmath_ffi_erfc(double);
 float chelis_crmath_ffi_tanhf(float);
 double chelis_crmath_ffi_tanh(double);
+
+/* Threads of the oracle's parallel loops (the CPU baseline's single-thread
+ * run); returns the previous setting. */
+int orc_set_threads(int n) {
+    const int prev = omp_get_max_threads();
+    omp_set_num_threads(n);
+    return prev;
+}
 
 /* ------------------------------------------------------------------ */
 /* [04-NUM-2] NaN finalization: crates/chelis-backend-c/src/fp_env.rs:46-52 */

@@ -52,6 +52,9 @@ double orc_erfc(double x);
 float orc_tanhf(float x);
 double orc_tanh(double x);
 
+/* OpenMP threads of the parallel loops; returns the previous setting. */
+int orc_set_threads(int n);
+
 /* ---- canonical reductions ([05-OP-30], [05-OP-12], [05-OP-29]) ---- */
 float orc_tree_sum_f32(const float *x, int64_t n, int64_t stride);
 double orc_tree_sum_f64(const double *x, int64_t n, int64_t stride);

@@ -38,6 +38,7 @@ c_i64, c_u64, c_f32, c_f64, c_p = ctypes.c_int64, ctypes.c_uint64, ctypes.c_floa
 
 def _declare(L):
     sig = {
+        "orc_set_threads": (ctypes.c_int, [ctypes.c_int]),
         "orc_splitmix64": (c_u64, [c_u64]),
         "orc_derive": (c_u64, [c_u64, c_u64]),
         "orc_word": (c_u64, [c_u64, c_u64]),
