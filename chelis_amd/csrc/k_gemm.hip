@@ -3,21 +3,23 @@
 //
 // MFMA tile kernel. A 256-thread workgroup (4 waves, 2 x 2) owns a 128 x 128
 // tile of C; each wave owns 64 x 64 = 4 x 4 blocks of 16 x 16, accumulated
-// by v_mfma_f32_16x16x4_f32 (f32) or v_mfma_f64_16x16x4_f64 (f64). K moves
-// in steps of BK (16 for f32, 8 for f64) through two LDS buffers: while the
+// by v_mfma_f32_16x16x4_f32 (f32) or v_mfma_f64_16x16x4_f64 (f64); a 64 x 64
+// tile (32 x 32 per wave) serves products with few 128-tiles. K moves in
+// steps of BK (16 for f32, 8 for f64; twice that for the 64-tile) through
+// two LDS buffers: while the
 // matrix cores consume one buffer, the next A and B tiles are already in
 // flight from HBM into registers and land in the other buffer after the
 // step, so there is one barrier per K step.
 //
 // LDS holds both operands K-contiguous (As[m][k], Bs[n][k]) with the row
-// padded to 80 bytes. An MFMA of shape 16x16x4 takes A[i][q] from lane
+// padded by 16 bytes (80 or 144 bytes). An MFMA of shape 16x16x4 takes A[i][q] from lane
 // q*16 + i and B[q][j] from lane q*16 + j, and returns C[i][j] in lane
 // q*16 + j, item r, with i = 4q + r for f32 and i = q + 4r for f64 (both
 // checked on gfx950 with a one-wave layout probe). Over the KV = BK/4 MFMAs of one
 // step, lane group q supplies k = q*KV + t for MFMA t, so both fragments of
-// a lane are KV consecutive k values: one 16-byte LDS read each, and the
-// 80-byte row pitch puts the 8 rows a read phase touches on 8 disjoint
-// 4-bank groups.
+// a lane are KV consecutive k values: one or two 16-byte LDS reads each,
+// and the padded row pitch puts the 8 rows a read phase touches on 8
+// disjoint 4-bank groups.
 //
 // Operands are strided views (a transposed operand is a stride swap):
 // each one is staged with 16-byte vector loads along whichever of its axes
@@ -43,7 +45,7 @@ struct Mfma;
 template <>
 struct Mfma<float> {
     using acc_t = f32x4;
-    static constexpr int BK = 16, LD = 20, V = 4;
+    static constexpr int V = 4;
     // accumulator item r of lane group q holds row 4q + r of the 16x16 block
     __device__ static int row(int q, int r) { return 4 * q + r; }
     __device__ static acc_t step(float a, float b, acc_t c) {
@@ -53,7 +55,7 @@ struct Mfma<float> {
 template <>
 struct Mfma<double> {
     using acc_t = f64x4;
-    static constexpr int BK = 8, LD = 10, V = 2;
+    static constexpr int V = 2;
     // accumulator item r of lane group q holds row q + 4r of the 16x16 block
     __device__ static int row(int q, int r) { return q + 4 * r; }
     __device__ static acc_t step(double a, double b, acc_t c) {
@@ -62,6 +64,20 @@ struct Mfma<double> {
 };
 
 constexpr int THREADS = 256;
+
+// K depth of one step. The 128-tile takes 16 (f32) / 8 (f64): four MFMA
+// chains of 4 x 4 blocks per wave between barriers. The 64-tile has a
+// quarter of those blocks per wave, so it takes twice the depth, keeping
+// the matrix work between barriers (and the lead the two register staging
+// sets give each global load, two steps) at half the 128-tile's rather than
+// a quarter. The LDS row pitch is BK plus 16 bytes: 80 or 144 bytes, so
+// the 8 rows one 16-byte read phase touches fall on 8 disjoint 4-bank groups.
+template <typename T, int TM>
+struct Depth {
+    static constexpr int BK = (sizeof(T) == 8 ? 8 : 16) * (TM == 2 ? 2 : 1);
+    static constexpr int LD = BK + 16 / (int)sizeof(T);
+    static constexpr int KV = BK / 4;  // consecutive k per lane and MFMA chain
+};
 
 template <typename T>
 struct Vec16;
@@ -76,9 +92,9 @@ struct Vec16<double> {
 
 // Layout of a staged operand: 0 = vectors along K, 1 = vectors along the
 // outer axis (M of A, N of B), 2 = element by element.
-template <typename T, int LAY, int ROWS>
+template <typename T, int LAY, int ROWS, int BK_, int LD_>
 struct Stage {
-    static constexpr int BK = Mfma<T>::BK, V = Mfma<T>::V, LD = Mfma<T>::LD;
+    static constexpr int BK = BK_, V = Mfma<T>::V, LD = LD_;
     static constexpr int NE = ROWS * BK / THREADS;  // elements per thread
     static constexpr int NV = NE / V;               // vectors per thread
     T r[NE];
@@ -204,7 +220,8 @@ __global__ __launch_bounds__(THREADS, kMinWavesPerEu<T>) void gemm_mfma_kernel(G
                                                                                int64_t kchunk) {
     using M = Mfma<T>;
     using acc_t = typename M::acc_t;
-    constexpr int BK = M::BK, LD = M::LD, KV = BK / 4;
+    using D = Depth<T, TM>;
+    constexpr int BK = D::BK, LD = D::LD, KV = D::KV, V = M::V, NVF = KV / V;
     constexpr int BM = 32 * TM, BN = 32 * TM, WT = 16 * TM;
     __shared__ __attribute__((aligned(16))) T As[2][BM * LD];
     __shared__ __attribute__((aligned(16))) T Bs[2][BN * LD];
@@ -246,13 +263,10 @@ __global__ __launch_bounds__(THREADS, kMinWavesPerEu<T>) void gemm_mfma_kernel(G
 #pragma unroll
         for (int j = 0; j < TM; ++j) acc[i][j] = acc_t{};
 
-    // Two register staging sets: the global loads of step s + 3 are issued
-    // right after step s + 1 leaves its set for LDS, so each load has two
-    // whole k-steps to arrive before its own store (measured: f32 4096^3
-    // 1.42 -> 1.17 ms, f64 2.44 -> 2.31 ms; a third set gained nothing, and
-    // two MFMA chunks per step with its 74 KB of LDS lost 10 %).
-    Stage<T, ALAY, BM> sa0, sa1;
-    Stage<T, BLAY, BN> sb0, sb1;
+    // Two register staging sets (measured: f32 4096^3 1.42 -> 1.17 ms, f64
+    // 2.44 -> 2.31 ms over one; a third set gained nothing).
+    Stage<T, ALAY, BM, BK, LD> sa0, sa1;
+    Stage<T, BLAY, BN, BK, LD> sb0, sb1;
     const int64_t ksteps = (K + BK - 1) / BK;
     // an interior tile of aligned operands and whole K steps loads without checks
     const bool inside = a_vec && b_vec && ALAY != 2 && BLAY != 2 && m0 + BM <= p.M && n0 + BN <= p.N && K % BK == 0;
@@ -262,50 +276,113 @@ __global__ __launch_bounds__(THREADS, kMinWavesPerEu<T>) void gemm_mfma_kernel(G
     // last is clamped to the last, so the extra loads read valid memory and
     // the extra store fills the LDS buffer no later step reads. Straight-line
     // memory operations let the compiler wait for exactly the older loads.
+    // a lane's fragments of one step: KV consecutive k, in NVF 16-byte LDS reads
+    struct Frags {
+        typename Vec16<T>::type a[TM][NVF], b[TM][NVF];
+    };
+    auto read_frags = [&](Frags &f, int buf) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int h = 0; h < NVF; ++h)
+                f.a[i][h] = *reinterpret_cast<const typename Vec16<T>::type *>(
+                    &As[buf][(wm * WT + i * 16 + fr) * LD + fq * KV + h * V]);
+#pragma unroll
+        for (int j = 0; j < TM; ++j)
+#pragma unroll
+            for (int h = 0; h < NVF; ++h)
+                f.b[j][h] = *reinterpret_cast<const typename Vec16<T>::type *>(
+                    &Bs[buf][(wn * WT + j * 16 + fr) * LD + fq * KV + h * V]);
+    };
+    auto mfmas = [&](const Frags &f) {
+#pragma unroll
+        for (int t = 0; t < KV; ++t)
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TM; ++j)
+                    acc[i][j] = M::step(reinterpret_cast<const T *>(f.a[i])[t],
+                                        reinterpret_cast<const T *>(f.b[j])[t], acc[i][j]);
+    };
+
+    // 128-tiles: both LDS buffers hold a step. At the top of step s, buffer
+    // s % 2 holds step s (already in this lane's registers as fragments)
+    // and buffer (s + 1) % 2 step s + 1. Step s reads the fragments of step
+    // s + 1 while its matrix work runs, then overwrites buffer s % 2 with
+    // step s + 2 from a register staging set and refills that set from
+    // memory with step s + 4; one barrier ends the step. The matrix cores
+    // never wait for an LDS read after the barrier (measured: f32 4096^3
+    // 1.13 -> 1.09 ms, f64 2.22 -> 2.03 ms).
+    // 64-tiles (measured faster this way: 4096 x 1024 x 1024 f32 in 90
+    // against 98 us): step s reads step s from buffer s % 2, runs its matrix
+    // work, stores step s + 1 into the other buffer and refills that set
+    // with step s + 3.
+    // Either way each global load has two whole steps to arrive before its
+    // LDS store, and the body has no branches around its loads and stores:
+    // a step past the last is clamped to the last, so the extra loads read
+    // valid memory and the extra LDS traffic touches buffers no later step
+    // reads. Straight-line memory operations let the compiler wait for
+    // exactly the older loads.
     auto run = [&](auto check) {
         constexpr bool CK = decltype(check)::value;
         const int64_t last = ksteps - 1;
         auto kstep = [&](int64_t s) { return (s < last ? s : last) * BK; };
-        sa0.template load<CK>(A, p.sam, p.sak, m0, p.M, 0, K, a_vec);
-        sb0.template load<CK>(B, p.sbn, p.sbk, n0, p.N, 0, K, b_vec);
-        sa1.template load<CK>(A, p.sam, p.sak, m0, p.M, kstep(1), K, a_vec);
-        sb1.template load<CK>(B, p.sbn, p.sbk, n0, p.N, kstep(1), K, b_vec);
-        sa0.store(As[0]);
-        sb0.store(Bs[0]);
-        sa0.template load<CK>(A, p.sam, p.sak, m0, p.M, kstep(2), K, a_vec);
-        sb0.template load<CK>(B, p.sbn, p.sbk, n0, p.N, kstep(2), K, b_vec);
-        __syncthreads();
-        auto step = [&](int64_t ks, Stage<T, ALAY, BM> &sa_n, Stage<T, BLAY, BN> &sb_n) {
-            const int buf = ks & 1;
-            typename Vec16<T>::type af[TM], bf[TM];
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-                af[i] = *reinterpret_cast<const typename Vec16<T>::type *>(
-                    &As[buf][(wm * WT + i * 16 + fr) * LD + fq * KV]);
-#pragma unroll
-            for (int j = 0; j < TM; ++j)
-                bf[j] = *reinterpret_cast<const typename Vec16<T>::type *>(
-                    &Bs[buf][(wn * WT + j * 16 + fr) * LD + fq * KV]);
-#pragma unroll
-            for (int t = 0; t < KV; ++t)
-#pragma unroll
-                for (int i = 0; i < TM; ++i)
-#pragma unroll
-                    for (int j = 0; j < TM; ++j)
-                        acc[i][j] = M::step(reinterpret_cast<const T *>(&af[i])[t],
-                                            reinterpret_cast<const T *>(&bf[j])[t], acc[i][j]);
-            sa_n.store(As[buf ^ 1]);
-            sb_n.store(Bs[buf ^ 1]);
-            sa_n.template load<CK>(A, p.sam, p.sak, m0, p.M, kstep(ks + 3), K, a_vec);
-            sb_n.template load<CK>(B, p.sbn, p.sbk, n0, p.N, kstep(ks + 3), K, b_vec);
-            __syncthreads();
+        auto load = [&](Stage<T, ALAY, BM, BK, LD> &sa, Stage<T, BLAY, BN, BK, LD> &sb, int64_t s) {
+            sa.template load<CK>(A, p.sam, p.sak, m0, p.M, kstep(s), K, a_vec);
+            sb.template load<CK>(B, p.sbn, p.sbk, n0, p.N, kstep(s), K, b_vec);
         };
-        int64_t ks = 0;
-        for (; ks + 1 < ksteps; ks += 2) {
-            step(ks, sa1, sb1);
-            step(ks + 1, sa0, sb0);
+        auto store = [&](const Stage<T, ALAY, BM, BK, LD> &sa, const Stage<T, BLAY, BN, BK, LD> &sb, int buf) {
+            sa.store(As[buf]);
+            sb.store(Bs[buf]);
+        };
+        if constexpr (TM == 2) {
+            load(sa0, sb0, 0);
+            load(sa1, sb1, 1);
+            store(sa0, sb0, 0);
+            load(sa0, sb0, 2);
+            __syncthreads();
+            auto step = [&](int64_t s, Stage<T, ALAY, BM, BK, LD> &sa_n, Stage<T, BLAY, BN, BK, LD> &sb_n) {
+                const int buf = s & 1;
+                Frags f;
+                read_frags(f, buf);
+                mfmas(f);
+                store(sa_n, sb_n, buf ^ 1);
+                load(sa_n, sb_n, s + 3);
+                __syncthreads();
+            };
+            int64_t ks = 0;
+            for (; ks + 1 < ksteps; ks += 2) {
+                step(ks, sa1, sb1);
+                step(ks + 1, sa0, sb0);
+            }
+            if (ks < ksteps) step(ks, sa1, sb1);
+        } else {
+            load(sa0, sb0, 0);
+            load(sa1, sb1, 1);
+            store(sa0, sb0, 0);
+            store(sa1, sb1, 1);
+            load(sa0, sb0, 2);
+            load(sa1, sb1, 3);
+            __syncthreads();
+            Frags f0, f1;
+            read_frags(f0, 0);
+            __syncthreads();  // every lane has step 0 before step 0 overwrites buffer 0
+            auto step = [&](int64_t s, Frags &cur, Frags &next, Stage<T, ALAY, BM, BK, LD> &sa_n,
+                            Stage<T, BLAY, BN, BK, LD> &sb_n) {
+                const int buf = s & 1;
+                read_frags(next, buf ^ 1);
+                mfmas(cur);
+                store(sa_n, sb_n, buf);
+                load(sa_n, sb_n, s + 4);
+                __syncthreads();
+            };
+            int64_t ks = 0;
+            for (; ks + 1 < ksteps; ks += 2) {
+                step(ks, f0, f1, sa0, sb0);
+                step(ks + 1, f1, f0, sa1, sb1);
+            }
+            if (ks < ksteps) step(ks, f0, f1, sa0, sb0);
         }
-        if (ks < ksteps) step(ks, sa1, sb1);
     };
     if (inside) run(std::false_type{});
     else run(std::true_type{});
@@ -430,15 +507,16 @@ void launch_mfma(const GemmProblem &p, dim3 grid, int64_t tm, int64_t tn, bool a
 }
 
 // Slices of K for a product whose tiles cannot fill the chip: enough slices
-// to give every CU about two workgroups, each slice at least 256 deep (a
+// to give every CU about three workgroups, each slice at least 256 deep (a
 // shorter run does not amortize a tile's first loads and its store), at most
-// 16. Returns 1 for no split.
-template <typename T>
+// 16. Returns 1 for no split. (Measured on the skinny f64 8192 x 64 x 4096,
+// 128 64-tiles: 4 slices 109.5 us, 6 slices 102.5 us, 8 slices 113.5 us.)
+template <typename T, int TM>
 int64_t split_count(const GemmProblem &p, int64_t tiles, int64_t *kchunk) {
-    constexpr int64_t BK = Mfma<T>::BK;
+    constexpr int64_t BK = Depth<T, TM>::BK;
     const int64_t cus = device_cus();
     if (p.causal != 0 || tiles >= cus || p.K < 512) return 1;
-    int64_t ks = (2 * cus + tiles - 1) / tiles;
+    int64_t ks = (3 * cus + tiles - 1) / tiles;
     if (ks > p.K / 256) ks = p.K / 256;
     if (ks > 16) ks = 16;
     if (ks < 2) return 1;
@@ -457,7 +535,7 @@ int32_t run_tiles(const GemmProblem &p, int al, int bl, bool av, bool bv, hipStr
     const int64_t nz = p.nb0 * p.nb1;
     if (tm * tn > 0x7fffffffLL || nz > 65535) return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: grid too large");
     int64_t kchunk = 0;
-    const int64_t ks = split_count<T>(p, tm * tn * nz, &kchunk);
+    const int64_t ks = split_count<T, TM>(p, tm * tn * nz, &kchunk);
     T *part = nullptr;
     const size_t part_bytes = ks > 1 ? (size_t)(ks * nz * p.M * p.N) * sizeof(T) : 0;
     if (ks > 1) {

@@ -175,11 +175,10 @@ int32_t dispatch(chelis_dtype dt, const GemmProblem &p, int32_t flags) {
         return gemm_tree_wave(dt, p, st);
     }
     const bool exact = flags & CHELIS_MATMUL_EXACT;
-    // f64 with a narrow side of 16..64 (the skinny 8192x64x4096 of config
-    // 3c) runs on the f64 MFMA tiles (split across K when the tiles cannot
-    // fill the chip): within the 1e-10 GEMM tolerance, where the tree panel
-    // is bit-exact but bound by its separate multiply and add (329 us
-    // against a 55 us f64 FMA floor); the exact flag keeps the tree
+    // A narrow side of 16..64 (the skinny 8192x64x4096 of config 3c) runs
+    // on the matrix cores within the GEMM tolerance, where the tree panel is
+    // bit-exact but bound by its separate multiply and add (329 us against a
+    // 55 us f64 FMA floor); the exact flag keeps the tree
     if (narrow <= 64 && (exact || narrow < 16)) return gemm_tree_panel(dt, p, st);
     if (exact) return gemm_tree_tiled(dt, p, st);
     return gemm_mfma(dt, p, st);

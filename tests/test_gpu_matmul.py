@@ -307,3 +307,72 @@ def test_split_k_batched_with_epilogue():
     for j in range(3):
         v = res[j] + O.gelu(O.matmul(x[j], w) + bias[j])
         check_close(c[j], v, np.float64)
+
+
+# A narrow side of 16..64 on the MFMA tiles (the 64-tile, K split over
+# workgroups when the tiles cannot fill the chip): ragged edges, strided and
+# misaligned operands, batches and epilogues.
+SKINNY_CASES = [
+    # (M, N, K, b transposed, a row offset in elements)
+    (8192, 64, 4096, False, 0),  # config 3c's shape (two K slices)
+    (1000, 33, 1001, False, 0),  # ragged rows, columns and K (a partial last chunk)
+    (37, 16, 5000, True, 0),     # few rows: many K slices; B stored along K
+    (512, 48, 70, False, 0),     # K of 4.4 chunks: waves with 2 and 1 chunks
+    (300, 64, 640, False, 1),    # A rows start off the 16-byte grid: element loads
+    (64, 20, 33, False, 0),      # K of 3 chunks, most waves idle
+]
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("case", SKINNY_CASES)
+def test_skinny_within_tolerance(case, dtype):
+    M, N, K, tb, off = case
+    rng = np.random.default_rng(M + 3 * N + K)
+    a, b = rand(rng, (M, K), dtype), rand(rng, (K, N), dtype)
+    if off:
+        # rows of K + 1 elements starting at element `off`: a strided view
+        # whose rows are not 16-byte aligned
+        buf = np.zeros(M * (K + 1) + off, dtype)
+        buf[off:].reshape(M, K + 1)[:, :K] = a
+        d = C.to_device(buf)
+        va = d.view((M, K), (K + 1, 1), off)
+    else:
+        _d, va, _n = dev_view(a, M, K, False)
+    _db, vb, nb = dev_view(b, K, N, tb)
+    c = C.matmul(va, vb).numpy()
+    check_close(c, O.matmul(a, nb), dtype)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("act", [None, "relu", "gelu"])
+def test_skinny_batched_epilogue(dtype, act):
+    """A broadcast batch (B shared), per-batch bias, activation and residual
+    on a narrow product: applied in the tile kernel (one slice) or in the
+    split-K combine pass."""
+    rng = np.random.default_rng(46)
+    for M, K in ((2048, 256), (96, 3000)):
+        x = rand(rng, (2, M, K), dtype)
+        w, bias = rand(rng, (K, 40), dtype), rand(rng, (2, 40), dtype)
+        res = rand(rng, (2, M, 40), dtype)
+        dw = C.to_device(w)
+        c = C.linear(C.to_device(x), dw.view((2, K, 40), (0, 40, 1)), C.to_device(bias), act,
+                     C.to_device(res)).numpy()
+        for j in range(2):
+            v = (O.matmul(x[j], w) + bias[j]).astype(dtype)
+            if act == "relu":
+                # the oracle's relu is binary32 only; max(v, +0) is exact
+                v = O.relu(v) if dtype == np.float32 else np.where(v < 0, 0.0, v)
+            elif act == "gelu":
+                v = O.gelu(v)
+            check_close(c[j], (res[j] + v).astype(dtype), dtype)
+
+
+def test_skinny_repeatable():
+    """The same inputs give the same bits on every call (fixed tile and
+    slice order)."""
+    rng = np.random.default_rng(47)
+    a, b = rand(rng, (4000, 3000), np.float64), rand(rng, (3000, 64), np.float64)
+    da, db = C.to_device(a), C.to_device(b)
+    c0 = C.matmul(da, db).numpy()
+    for _ in range(3):
+        assert bits_equal(C.matmul(da, db).numpy(), c0)
