@@ -506,18 +506,22 @@ void launch_mfma(const GemmProblem &p, dim3 grid, int64_t tm, int64_t tn, bool a
     gemm_mfma_kernel<T, AL, BL, TM, false><<<grid, THREADS, dyn, st>>>(p, tm, tn, av, bv, part, kchunk);
 }
 
-// Slices of K for a product whose tiles cannot fill the chip: enough slices
-// to give every CU about three workgroups, each slice at least 256 deep (a
-// shorter run does not amortize a tile's first loads and its store), at most
-// 16. Returns 1 for no split. (Measured on the skinny f64 8192 x 64 x 4096,
-// 128 64-tiles: 4 slices 109.5 us, 6 slices 102.5 us, 8 slices 113.5 us.)
+// Slices of K for a product whose tiles cannot fill the chip. 64-tiles:
+// enough slices to give every CU about three workgroups, each slice at least
+// 256 deep (a shorter run does not amortize a tile's first loads and its
+// store). (Measured on the skinny f64 8192 x 64 x 4096, 128 64-tiles: 4
+// slices 109.5 us, 6 slices 102.5 us, 8 slices 113.5 us.) 128-tiles (chosen
+// for fewer than two per CU only when K is long, see run_mfma): two
+// workgroups per CU, each slice at least 1024 deep. At most 16 slices;
+// returns 1 for no split.
 template <typename T, int TM>
 int64_t split_count(const GemmProblem &p, int64_t tiles, int64_t *kchunk) {
     constexpr int64_t BK = Depth<T, TM>::BK;
     const int64_t cus = device_cus();
-    if (p.causal != 0 || tiles >= cus || p.K < 512) return 1;
-    int64_t ks = (3 * cus + tiles - 1) / tiles;
-    if (ks > p.K / 256) ks = p.K / 256;
+    const int64_t per_cu = TM == 2 ? 3 : 2, min_depth = TM == 2 ? 256 : 1024;
+    if (p.causal != 0 || tiles >= (TM == 2 ? cus : 2 * cus) || p.K < 2 * min_depth) return 1;
+    int64_t ks = (per_cu * cus + tiles - 1) / tiles;
+    if (ks > p.K / min_depth) ks = p.K / min_depth;
     if (ks > 16) ks = 16;
     if (ks < 2) return 1;
     int64_t kc = (p.K + ks - 1) / ks;
@@ -573,12 +577,17 @@ int32_t run_mfma(const GemmProblem &p, hipStream_t st) {
     // holds), no dimension is at most half a tile and K runs long enough
     // (> 128) to amortize a tile's first loads and its epilogue; 64-tiles,
     // four times as many workgroups that overlap those phases, otherwise.
-    // Measured: the transformer block's projections and FFN2 (256 128-tiles
-    // each, with bias and residual epilogues) run the block in 1.25 ms on
-    // 64-tiles against 1.32 ms on 128-tiles; the 128 x (512 x 512 x 64)
-    // attention scores take 80 us on 64-tiles against 132 us.
+    // Measured: the transformer block's projections (256 128-tiles each,
+    // K = 1024) take 87 us on 64-tiles against 94 us on 128-tiles; the 128 x
+    // (512 x 512 x 64) attention scores 80 us against 132 us. With K of at
+    // least 2048, 128-tiles split across K win instead: FFN2 (4096 x 1024 x
+    // 4096, 256 128-tiles) takes 279 us as 2 slices of 128-tiles against
+    // 305 us on 64-tiles.
+    const int64_t cus = device_cus();
     const int64_t big = ((p.M + 127) / 128) * ((p.N + 127) / 128) * p.nb0 * p.nb1;
-    const bool small = big < 2 * (int64_t)device_cus() || p.M <= 64 || p.N <= 64 || p.K <= 128;
+    const int64_t kslices = p.K / 1024 < 16 ? p.K / 1024 : 16;
+    const bool few = big < 2 * cus && !(p.causal == 0 && p.K >= 2048 && big * kslices >= 2 * cus && big >= cus / 2);
+    const bool small = few || p.M <= 64 || p.N <= 64 || p.K <= 128;
     return small ? run_tiles<T, 2>(p, al, bl, av, bv, st) : run_tiles<T, 4>(p, al, bl, av, bv, st);
 }
 

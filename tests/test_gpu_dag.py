@@ -98,8 +98,11 @@ def transformer_inputs(B, S, D, F):
 
 @pytest.mark.parametrize("dims", [(2, 128, 256, 1024), (8, 512, 1024, 4096)])
 def test_transformer_config4_from_dag(dims):
-    """Eleven launches, the hand-wired program's sequence: bit-identical to
-    chelis_prog_transformer_block, and within 1e-5 normwise of the oracle."""
+    """Eleven launches, the hand-wired program's sequence, within 1e-5
+    normwise of the oracle. The hand-wired chelis_prog_transformer_block
+    runs the Q, K and V projections as one batched product (its tiles sum in
+    another order), so the two agree to the same tolerance, not bit for
+    bit."""
     B, S, D, F = dims
     text = fixture("transformer_block_b8_s512_d1024") if dims == (8, 512, 1024, 4096) else \
         DB.transformer_program(B, S, D, F).json()
@@ -110,7 +113,7 @@ def test_transformer_config4_from_dag(dims):
     (y,) = prog.run(ins)
     hand = C.empty(x.shape, np.float32)
     C.program("transformer_block", ins, [hand])
-    assert bits_equal(y.numpy(), hand.numpy())
+    assert normwise(y.numpy(), hand.numpy()) <= 1e-5
     ref = O.transformer_block(x, p, D // 64)
     assert normwise(y.numpy(), ref) <= 1e-5
 
