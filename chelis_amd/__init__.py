@@ -107,6 +107,7 @@ SIGNATURES = {
     "chelis_hip_build_info": (ctypes.c_char_p, []),
     "chelis_hip_softmax": (c_int32, [P, P]),
     "chelis_hip_scaled_masked_softmax": (c_int32, [P, c_double, c_int32, P]),
+    "chelis_hip_causal_attention": (c_int32, [P, P, P, c_double, P]),
     "chelis_hip_softmax_adjoint": (c_int32, [P, P, P]),
     "chelis_hip_layer_norm": (c_int32, [P, P, P, c_double, P]),
     "chelis_hip_fused_elementwise": (c_int32, [POINTER(FusedChain), POINTER(P), c_int32, P]),
@@ -341,6 +342,14 @@ def scaled_masked_softmax(x, scale: float, causal: bool, y=None):
     y = y or empty(x.shape, x.dtype)
     check(lib().chelis_hip_scaled_masked_softmax(_p(x), scale, int(causal), _p(y)), "scaled_masked_softmax")
     return y
+
+
+def causal_attention(q, k, v, scale: float, o=None):
+    """softmax(where(key <= row, q.k^T * scale, -inf)).v in one launch over
+    f32 [batch, heads, seq, 64] views."""
+    o = o or empty(q.shape, q.dtype)
+    check(lib().chelis_hip_causal_attention(_p(q), _p(k), _p(v), scale, _p(o)), "causal_attention")
+    return o
 
 
 def softmax_adjoint(y, g, dx=None):

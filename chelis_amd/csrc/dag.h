@@ -142,7 +142,7 @@ std::vector<int64_t> consumer_counts(const Graph &g);
 // materialized region output.
 enum class RegionKind : uint8_t {
     Chain, Reduce, Count, Softmax, MaskedSoftmax, SoftmaxAdjoint, LayerNorm, Gelu, Relu, ReluAdjoint, Dropout,
-    Matmul, Copy
+    Matmul, Copy, Attention
 };
 const char *region_kind_name(RegionKind k);
 
@@ -162,6 +162,7 @@ struct Region {
     bool has_bias = false, has_residual = false;
     int32_t activation = CHELIS_ACT_NONE;
     int32_t causal_mode = 0;  // 1: skip tiles above the diagonal, 2: clip the contraction
+    // attention: in = {q [.., S, 64], k^T [.., 64, S], v [.., S, 64]}, scale
 };
 
 // How a value's storage is found at run time.

@@ -323,6 +323,44 @@ int32_t run_plan(chelis_dag_program *prog, const chelis_gpu_tensor *const *input
                     s = chelis_hip_matmul(in[0], in[1], out, 0);
                 break;
             }
+            case RegionKind::Attention: {
+                // k arrives as the k^T view the scores product read
+                chelis_gpu_tensor kh = *in[1];
+                int64_t shape[8], strides[8];
+                for (int32_t a = 0; a < kh.rank; ++a) shape[a] = kh.shape[a], strides[a] = kh.strides[a];
+                std::swap(shape[kh.rank - 1], shape[kh.rank - 2]);
+                std::swap(strides[kh.rank - 1], strides[kh.rank - 2]);
+                kh.shape = shape;
+                kh.strides = strides;
+                // collapse leading axes to [batch, heads] for the kernel's rank-4 form
+                chelis_gpu_tensor t4[4];
+                int64_t sh4[4][4], st4[4][4];
+                const chelis_gpu_tensor *src[4] = {in[0], &kh, in[2], out};
+                bool flat = true;
+                for (int u = 0; u < 4; ++u) {
+                    const chelis_gpu_tensor *t = src[u];
+                    const int32_t rk = t->rank;
+                    if (rk < 3 || rk > 4) { flat = false; break; }
+                    t4[u] = *t;
+                    if (rk == 3) {
+                        sh4[u][0] = 1, st4[u][0] = t->shape[0] * t->strides[0];
+                        for (int a = 0; a < 3; ++a) sh4[u][a + 1] = t->shape[a], st4[u][a + 1] = t->strides[a];
+                    } else {
+                        for (int a = 0; a < 4; ++a) sh4[u][a] = t->shape[a], st4[u][a] = t->strides[a];
+                    }
+                    t4[u].rank = 4;
+                    t4[u].shape = sh4[u];
+                    t4[u].strides = st4[u];
+                }
+                if (!flat || !attention_causal_fits(&t4[0], &t4[1], &t4[2], &t4[3])) {
+                    s = set_error(CHELIS_HIP_EUNSUPPORTED,
+                                  "dag: node %lld: attention operands are not [.., S, 64] views with a contiguous "
+                                  "head axis", (long long)r.out);
+                    break;
+                }
+                s = attention_causal(&t4[0], &t4[1], &t4[2], r.scale, &t4[3]);
+                break;
+            }
             case RegionKind::Copy: {
                 const chelis_gpu_tensor *dst = outputs[r.axis];
                 s = chelis_hip_fused_elementwise(&identity_chain(), in.data(), 1, dst);

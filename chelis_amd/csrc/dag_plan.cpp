@@ -50,6 +50,7 @@ const char *region_kind_name(RegionKind k) {
         case RegionKind::Dropout: return "dropout";
         case RegionKind::Matmul: return "matmul";
         case RegionKind::Copy: return "copy";
+        case RegionKind::Attention: return "attention";
     }
     return "?";
 }
@@ -810,6 +811,47 @@ bool build_plan(const Graph &input, Plan *plan, std::string *error) {
                 m.activation == CHELIS_ACT_NONE && P.users[r.out].size() == 1 && !P.is_root[r.out])
                 m.causal_mode = 2;
     }
+    // causal attention: the scores product, the causal softmax over them and
+    // the product reading the probabilities become one fused region when
+    // the operands are binary32 [.., S, 64] with S a multiple of 64 (known
+    // from the static extents); the scores and probabilities then never
+    // reach memory
+    for (size_t i = 0; i < P.regions.size(); ++i) {
+        const Region &r = P.regions[i];
+        if (r.kind != RegionKind::MaskedSoftmax || !r.causal) continue;
+        int64_t m1 = -1, m2 = -1;
+        for (size_t j = 0; j < P.regions.size(); ++j) {
+            const Region &m = P.regions[j];
+            if (m.kind == RegionKind::Matmul && m.causal_mode == 1 && m.out == r.in[0]) m1 = (int64_t)j;
+            if (m.kind == RegionKind::Matmul && m.causal_mode == 2 && m.in[0] == r.out) m2 = (int64_t)j;
+        }
+        if (m1 < 0 || m2 < 0) continue;
+        const Region &a = P.regions[m1], &b = P.regions[m2];
+        const std::vector<int64_t> &qd = g.nodes[a.in[0]].dims, &kd = g.nodes[a.in[1]].dims,
+                                   &vd = g.nodes[b.in[1]].dims, &od = g.nodes[b.out].dims;
+        const size_t rk = qd.size();
+        bool ok = rk >= 3 && kd.size() == rk && vd.size() == rk && od.size() == rk &&
+                  g.nodes[a.in[0]].prec == Prim::F32 && g.nodes[a.in[1]].prec == Prim::F32 &&
+                  g.nodes[b.in[1]].prec == Prim::F32 && g.nodes[b.out].prec == Prim::F32;
+        for (size_t d = 0; ok && d < rk; ++d)
+            ok = qd[d] > 0 && qd[d] == vd[d] && qd[d] == od[d] && (d + 2 < rk ? kd[d] == qd[d] : true);
+        ok = ok && qd[rk - 1] == 64 && kd[rk - 2] == 64 && kd[rk - 1] == qd[rk - 2] && qd[rk - 2] % 64 == 0;
+        if (!ok) continue;
+        Region f;
+        f.kind = RegionKind::Attention;
+        f.out = b.out;
+        f.in = {a.in[0], a.in[1], b.in[1]};
+        f.scale = r.scale;
+        for (const Region *part : {&a, &r, &b}) f.covers.insert(f.covers.end(), part->covers.begin(), part->covers.end());
+        const size_t keep = (size_t)m2;
+        std::vector<Region> next;
+        for (size_t j = 0; j < P.regions.size(); ++j) {
+            if (j == keep) next.push_back(f);
+            else if (j != (size_t)m1 && j != i) next.push_back(P.regions[j]);
+        }
+        P.regions.swap(next);
+        i = (size_t)-1;  // rescan from the start: indices moved
+    }
     plan->regions = P.regions;
     const size_t n = g.nodes.size();
     plan->values.assign(n, ValueInfo{});
@@ -872,14 +914,18 @@ bool build_plan(const Graph &input, Plan *plan, std::string *error) {
     }
     // a materialized value read only through one Permute is stored in the
     // permuted order, so the permuted view is dense (a later Reshape of it
-    // is then a view too); matmul results only, the one launcher that
-    // writes any strided layout
+    // is then a view too); matmul results (their launcher writes any strided
+    // layout) and attention results whose permutation keeps the head axis
+    // innermost (the fused kernel writes rows of 64 contiguous values)
     for (const Region &r : plan->regions) {
-        if (r.kind != RegionKind::Matmul) continue;
+        if (r.kind != RegionKind::Matmul && r.kind != RegionKind::Attention) continue;
         ValueInfo &vi = plan->values[r.out];
         if (vi.storage != Storage::Slot || P.users[r.out].size() != 1) continue;
         const Node &u = g.nodes[P.users[r.out][0]];
-        if (u.op == Op::Permute && u.axes.size() == g.nodes[r.out].dims.size()) vi.layout = u.axes;
+        const size_t rk = g.nodes[r.out].dims.size();
+        if (u.op != Op::Permute || u.axes.size() != rk) continue;
+        if (r.kind == RegionKind::Attention && u.axes[rk - 1] != (int64_t)rk - 1) continue;
+        vi.layout = u.axes;
     }
     // slot plan: lifetimes in launch order, views charged to their base
     std::vector<int64_t> def(n, -1), last(n, -1);
@@ -961,7 +1007,8 @@ std::string describe_plan(const Plan &plan) {
             if (r.causal_mode) s += " causal=" + std::to_string(r.causal_mode);
             if (!plan.values[r.out].layout.empty()) s += " permuted";
         }
-        if (r.kind == RegionKind::MaskedSoftmax) s += " causal";
+        if (r.kind == RegionKind::MaskedSoftmax || r.kind == RegionKind::Attention) s += " causal";
+        if (r.kind == RegionKind::Attention && !plan.values[r.out].layout.empty()) s += " permuted";
         const ValueInfo &v = plan.values[r.out];
         if (r.kind != RegionKind::Copy) {
             if (v.storage == Storage::Output) s += " -> output " + std::to_string(v.output);

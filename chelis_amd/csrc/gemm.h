@@ -55,6 +55,13 @@ int32_t widen16(chelis_dtype dt, const void *src, float *dst, int64_t nz0, int64
                 int64_t s0, int64_t s1, int64_t sr, int64_t sc, hipStream_t st);
 int32_t narrow16(chelis_dtype dt, const float *src, void *dst, int64_t nz0, int64_t nz1, int64_t rows, int64_t cols,
                  int64_t s0, int64_t s1, int64_t sr, int64_t sc, hipStream_t st);
+// Causal attention fused in one launch (k_attention.hip): o = softmax(
+// where(key <= row, q.k^T * scale, -inf)).v over f32 [batch, heads, seq, 64]
+// views, seq a multiple of 64; o must not overlap q, k or v.
+bool attention_causal_fits(const chelis_gpu_tensor *q, const chelis_gpu_tensor *k, const chelis_gpu_tensor *v,
+                           const chelis_gpu_tensor *o);
+int32_t attention_causal(const chelis_gpu_tensor *q, const chelis_gpu_tensor *k, const chelis_gpu_tensor *v,
+                         double scale, const chelis_gpu_tensor *o);
 // c = a . b for attention with the causal mode above (programs only).
 int32_t matmul_causal(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b, const chelis_gpu_tensor *c,
                       int32_t mode);

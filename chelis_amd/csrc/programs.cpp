@@ -206,8 +206,12 @@ extern "C" int32_t chelis_prog_transformer_block(const chelis_gpu_tensor *const 
     // the batch of three on 128-tiles against 3 x 90 us).
     const bool pack = is_contiguous(P[2]) && is_contiguous(P[4]) && is_contiguous(P[6]) && is_contiguous(P[3]) &&
                       is_contiguous(P[5]) && is_contiguous(P[7]);
+    // attention as one fused launch where it applies (binary32, seq a
+    // multiple of 64), else scores, causal softmax and P.V
+    const bool fused = dt == CHELIS_DTYPE_F32 && S % 64 == 0;
     Workspace ws(st);
-    const size_t o_h = ws.reserve(R * D * w), o_qkv = ws.reserve(3 * R * D * w), o_s = ws.reserve(B * H * S * S * w),
+    const size_t o_h = ws.reserve(R * D * w), o_qkv = ws.reserve(3 * R * D * w),
+                 o_s = ws.reserve(fused ? 0 : B * H * S * S * w),
                  o_o = ws.reserve(R * D * w), o_x1 = ws.reserve(R * D * w), o_f = ws.reserve(R * F * w),
                  o_w = ws.reserve(pack ? 3 * D * D * w : 0), o_b = ws.reserve(pack ? 3 * D * w : 0);
     TRY(ws.commit());
@@ -242,12 +246,18 @@ extern "C" int32_t chelis_prog_transformer_block(const chelis_gpu_tensor *const 
         TRY(chelis_hip_linear(&h, P[4], P[5], CHELIS_ACT_NONE, nullptr, &k, 0));
         TRY(chelis_hip_linear(&h, P[6], P[7], CHELIS_ACT_NONE, nullptr, &v, 0));
     }
-    // causal: score tiles above the diagonal are masked to -inf by the
-    // softmax without being read, and P is exactly +0 there, so those tiles
-    // and contraction terms are skipped
-    TRY(matmul_causal(&qh, &kt, &s, 1));
-    TRY(chelis_hip_scaled_masked_softmax(&s, 1.0 / 8.0, 1, &s));
-    TRY(matmul_causal(&s, &vh, &oh, 2));
+    const Pkt kh(k.t.data, dt, {B, H, S, DH}, {S * D, DH, D, 1}, cap);
+    if (fused && attention_causal_fits(&qh.t, &kh.t, &vh.t, &oh.t)) {
+        TRY(attention_causal(&qh.t, &kh.t, &vh.t, 1.0 / 8.0, &oh.t));
+    } else {
+        // causal: score tiles above the diagonal are masked to -inf by the
+        // softmax without being read, and P is exactly +0 there, so those
+        // tiles and contraction terms are skipped
+        if (fused) return set_error(CHELIS_HIP_EUNSUPPORTED, "transformer_block: attention operands misaligned");
+        TRY(matmul_causal(&qh, &kt, &s, 1));
+        TRY(chelis_hip_scaled_masked_softmax(&s, 1.0 / 8.0, 1, &s));
+        TRY(matmul_causal(&s, &vh, &oh, 2));
+    }
     TRY(chelis_hip_linear(&o, P[8], P[9], CHELIS_ACT_NONE, &x2, &x1, 0));
     // feed-forward
     TRY(chelis_hip_layer_norm(&x1, P[10], P[11], 1e-5, &h));

@@ -56,6 +56,17 @@ int32_t chelis_hip_softmax(const chelis_gpu_tensor *x, const chelis_gpu_tensor *
  * 4.7 steps 3-5) when causal != 0; scale is rounded once to the dtype. */
 int32_t chelis_hip_scaled_masked_softmax(const chelis_gpu_tensor *x, double scale, int32_t causal,
                                          const chelis_gpu_tensor *y);
+
+/* Causal self-attention in one launch: o = softmax(where(key <= row,
+ * (q . k^T) * scale, -inf)) . v over f32 [batch, heads, seq, 64] views, seq
+ * a multiple of 64, the head axis contiguous and rows 16-byte aligned; o
+ * must not overlap q, k or v. No single counterpart in the reference's C
+ * ABI: the fused form of the attention graph of spec/05 section 4.7 (scores
+ * matmul, causal where, softmax, P.V) for plans that run the three as one
+ * region. Within the binary32 tolerance of the unfused graph, not
+ * bit-identical to it. */
+int32_t chelis_hip_causal_attention(const chelis_gpu_tensor *q, const chelis_gpu_tensor *k, const chelis_gpu_tensor *v,
+                                    double scale, const chelis_gpu_tensor *o);
 /* softmax adjoint y * (g - sum(g * y)) (crates/chelis-dag-core/src/grad.rs:2248). */
 int32_t chelis_hip_softmax_adjoint(const chelis_gpu_tensor *y, const chelis_gpu_tensor *g,
                                    const chelis_gpu_tensor *dx);

@@ -446,3 +446,48 @@ def test_fused_chain_special_values_both_interpreters(dtype, chain_id, last_step
         assert np.all(np.abs(y[finite] - ref[finite]) <= 1e-12 * np.abs(ref[finite]))
     else:
         assert bits_equal(y, ref), mismatch_report(y, ref)
+
+
+def _attention_ref(q, k, v, scale):
+    """float64 reference of softmax(where(j <= i, q.k^T * scale, -inf)).v."""
+    s = np.einsum("bhid,bhjd->bhij", q.astype(np.float64), k.astype(np.float64)) * scale
+    n = s.shape[-1]
+    s = np.where(np.tril(np.ones((n, n), bool)), s, -np.inf)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    return np.einsum("bhij,bhjd->bhid", p, v.astype(np.float64))
+
+
+@pytest.mark.parametrize("B,H,S", [(1, 1, 64), (2, 3, 192), (2, 16, 512)])
+def test_causal_attention_fused(B, H, S):
+    """The fused attention kernel against a float64 reference of the graph,
+    within the binary32 tolerance (normwise 1e-5)."""
+    rng = np.random.default_rng(B * 100 + H * 10 + S)
+    q, k, v = (rng.standard_normal((B, H, S, 64)).astype(np.float32) for _ in range(3))
+    o = C.causal_attention(C.to_device(q), C.to_device(k), C.to_device(v), 0.125).numpy()
+    ref = _attention_ref(q, k, v, 0.125)
+    assert np.abs(o - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+def test_causal_attention_head_interleaved_views():
+    """q, k, v and o as [B, H, S, 64] views of [B, S, H*64] storage (the
+    transformer block's projections), large logits (scale 1) so the running
+    maxima move."""
+    B, S, H = 2, 256, 4
+    rng = np.random.default_rng(9)
+    raw = [rng.standard_normal((B, S, H * 64)).astype(np.float32) * 2 for _ in range(3)]
+    dev = [C.to_device(x) for x in raw]
+    views = [d.view((B, H, S, 64), (S * H * 64, 64, H * 64, 1)) for d in dev]
+    out = C.empty((B, S, H * 64), np.float32)
+    ov = out.view((B, H, S, 64), (S * H * 64, 64, H * 64, 1))
+    C.causal_attention(views[0], views[1], views[2], 1.0, ov)
+    q, k, v = (x.reshape(B, S, H, 64).transpose(0, 2, 1, 3) for x in raw)
+    ref = _attention_ref(q, k, v, 1.0).transpose(0, 2, 1, 3).reshape(B, S, H * 64)
+    o = out.numpy()
+    assert np.abs(o - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+def test_causal_attention_rejects_unsupported_shapes():
+    q = C.to_device(np.zeros((1, 1, 96, 64), np.float32))
+    with pytest.raises(C.ChelisError):
+        C.causal_attention(q, q, q, 0.125, C.empty((1, 1, 96, 64), np.float32))
