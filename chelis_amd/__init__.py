@@ -120,6 +120,7 @@ SIGNATURES = {
     "chelis_hip_reduce": (c_int32, [c_int32, POINTER(FusedChain), POINTER(P), c_int32, c_int32, P]),
     "chelis_hip_reduce_static": (c_int32, [c_int32, POINTER(FusedChain), POINTER(P), c_int32, c_int32, P]),
     "chelis_hip_count": (c_int32, [P, c_int32, P, POINTER(c_int32)]),
+    "chelis_hip_trap_status": (c_int32, [POINTER(c_int32)]),
     "chelis_hip_matmul": (c_int32, [P, P, P, c_int32]),
     "chelis_hip_linear": (c_int32, [P, P, P, c_int32, P, P, c_int32]),
     # chelis_programs.h
@@ -445,14 +446,27 @@ def reduce(op: str, inputs, axis: int, out=None, chain: FusedChain | None = None
     return out
 
 
-def count(x, axis: int, out=None):
-    """chelis_hip_count: Bool8 -> i64; returns (out, error_code)."""
+def count(x, axis: int, out=None, deferred: bool = False):
+    """chelis_hip_count: Bool8 -> i64; returns (out, error_code). With
+    deferred=True the call does not wait and the code goes to the trap
+    channel (trap_status); error_code is then None."""
     ax = axis % len(x.shape)
     if out is None:
         out = empty(x.shape[:ax] + x.shape[ax + 1:], np.int64)
+    if deferred:
+        check(lib().chelis_hip_count(_p(x), axis, _p(out), None), "count")
+        return out, None
     err = c_int32(0)
     check(lib().chelis_hip_count(_p(x), axis, _p(out), ctypes.byref(err)), "count")
     return out, err.value
+
+
+def trap_status() -> int:
+    """chelis_hip_trap_status: waits for the library stream, returns and
+    clears the codes deferred launches recorded (0: none)."""
+    code = c_int32(0)
+    check(lib().chelis_hip_trap_status(ctypes.byref(code)), "trap status")
+    return code.value
 
 
 # ---- matmul ----
@@ -557,6 +571,7 @@ class DagProgram:
         self.handle = lib().chelis_dag_compile(data, len(data))
         if not self.handle:
             raise ChelisError("dag compile failed: " + lib().chelis_hip_last_error().decode(errors="replace"))
+        self.has_count = any(line.split()[1:2] == ["count"] for line in self.describe().splitlines())
 
     def __del__(self):
         try:
@@ -602,6 +617,10 @@ class DagProgram:
         ins = (P * max(1, len(inputs)))(*[_p(t) for t in inputs])
         outs = (P * max(1, len(outputs)))(*[_p(t) for t in outputs])
         check(lib().chelis_dag_run(self.handle, ins, len(inputs), outs, len(outputs)), "dag run")
+        if self.has_count:
+            # the trap channel, read once after the run (a synchronization)
+            if trap_status():
+                raise ChelisError("numeric trap: domain in count at bool")
         return outputs
 
 

@@ -93,6 +93,37 @@ void scratch_free(void *p, size_t bytes) {
     g_free[device][size_class(bytes)].push_back(p);
 }
 
+// ---- status words ---------------------------------------------------------
+// Two int32 words per device, allocated and cleared once, kept until the
+// process ends: word 0 carries the error code of a launcher that returns it
+// synchronously, word 1 is the trap channel that launchers enqueued without
+// waiting record into (OR of codes) until chelis_hip_trap_status reads and
+// clears it. The host side of both reads is one pinned word per device.
+namespace {
+std::mutex g_status_mutex;
+int32_t *g_status[kMaxDevices] = {};
+int32_t *g_status_host[kMaxDevices] = {};
+}  // namespace
+
+int32_t *status_words(int32_t **host) {
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(g_status_mutex);
+    if (!g_status[device]) {
+        int32_t *d = nullptr, *h = nullptr;
+        if (hipMalloc(&d, 256) != hipSuccess) return nullptr;
+        if (hipMemset(d, 0, 256) != hipSuccess || hipDeviceSynchronize() != hipSuccess ||
+            hipHostMalloc(&h, sizeof(int32_t), hipHostMallocDefault) != hipSuccess) {
+            (void)hipFree(d);
+            return nullptr;
+        }
+        g_status[device] = d;
+        g_status_host[device] = h;
+    }
+    if (host) *host = g_status_host[device];
+    return g_status[device];
+}
+
 int device_cus() {
     int device = 0;
     if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) return 0;

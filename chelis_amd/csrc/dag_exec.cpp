@@ -294,12 +294,11 @@ int32_t run_plan(chelis_dag_program *prog, const chelis_gpu_tensor *const *input
                 s = chelis_hip_reduce(r.reduce_op, r.has_chain ? &r.chain : nullptr, in.data(), (int32_t)in.size(),
                                       (int32_t)r.axis, out);
                 break;
-            case RegionKind::Count: {
-                int32_t code = 0;
-                s = chelis_hip_count(in[0], (int32_t)r.axis, out, &code);
-                if (!s && code) s = set_error(CHELIS_HIP_EDOMAIN, "dag: count read a byte that is not 0 or 1");
+            case RegionKind::Count:
+                // a byte other than 0 / 1 goes to the trap channel, read once
+                // by whoever waits for the run (chelis_hip_trap_status)
+                s = chelis_hip_count(in[0], (int32_t)r.axis, out, nullptr);
                 break;
-            }
             case RegionKind::Softmax: s = chelis_hip_softmax(in[0], out); break;
             case RegionKind::MaskedSoftmax:
                 s = chelis_hip_scaled_masked_softmax(in[0], r.scale, r.causal, out);

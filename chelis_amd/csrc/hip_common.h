@@ -18,6 +18,10 @@ int32_t set_error(int32_t status, const char *fmt, ...) __attribute__((format(pr
 hipStream_t stream();
 // Compute units of the current device (cached per device; 256 on MI355X).
 int device_cus();
+// The current device's two status words (device memory; *host, when given,
+// receives a pinned host word for reading one back): [0] synchronous error
+// codes, [1] the deferred trap channel. Null when the device has none.
+int32_t *status_words(int32_t **host);
 // Scratch device memory for work enqueued on the current device's library
 // stream: blocks are recycled in stream order (a freed block's earlier users
 // are already enqueued ahead of any later user) and cached for reuse, so

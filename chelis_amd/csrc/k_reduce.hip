@@ -889,9 +889,13 @@ extern "C" int32_t chelis_hip_count(const chelis_gpu_tensor *x, int32_t axis, co
     if (!st) return set_error(CHELIS_HIP_EHIP, "no HIP device");
     if (error_code) *error_code = 0;
     if (outer * inner == 0) return CHELIS_HIP_OK;
-    int32_t *err = nullptr;
-    CHELIS_HIP_TRY(hipMallocAsync((void **)&err, sizeof(int32_t), st));
-    CHELIS_HIP_TRY(hipMemsetAsync(err, 0, sizeof(int32_t), st));
+    int32_t *host = nullptr;
+    int32_t *words = status_words(&host);
+    if (!words) return set_error(CHELIS_HIP_EHIP, "count: no status word on this device");
+    // with error_code: this call's own word, read back before returning;
+    // without: the trap channel, read at the caller's entry end
+    int32_t *err = error_code ? words : words + 1;
+    if (error_code) CHELIS_HIP_TRY(hipMemsetAsync(err, 0, sizeof(int32_t), st));
     if (inner == 1 && sn == 1 && so % 16 == 0 && (reinterpret_cast<uintptr_t>(x->data) & 15u) == 0)
         count_rows_vec_kernel<<<grid_for(outer, 4), 256, 0, st>>>((const uint8_t *)x->data, outer, x->shape[axis], so,
                                                                   (int64_t *)out->data, err);
@@ -899,10 +903,26 @@ extern "C" int32_t chelis_hip_count(const chelis_gpu_tensor *x, int32_t axis, co
         count_kernel<<<grid_for(outer * inner, 4), 256, 0, st>>>((const uint8_t *)x->data, outer, x->shape[axis],
                                                                  inner, so, sn, si, (int64_t *)out->data, err);
     CHELIS_LAUNCH_CHECK();
-    int32_t host_err = 0;
-    CHELIS_HIP_TRY(hipMemcpyAsync(&host_err, err, sizeof(int32_t), hipMemcpyDeviceToHost, st));
-    CHELIS_HIP_TRY(hipFreeAsync(err, st));
+    if (!error_code) return CHELIS_HIP_OK;
+    CHELIS_HIP_TRY(hipMemcpyAsync(host, err, sizeof(int32_t), hipMemcpyDeviceToHost, st));
     CHELIS_HIP_TRY(hipStreamSynchronize(st));
-    if (error_code) *error_code = host_err;
+    *error_code = *host;
+    return CHELIS_HIP_OK;
+}
+
+extern "C" int32_t chelis_hip_trap_status(int32_t *code) {
+    hipStream_t st = chelis::stream();
+    if (!st) return chelis::set_error(CHELIS_HIP_EHIP, "no HIP device");
+    int32_t *host = nullptr;
+    int32_t *words = chelis::status_words(&host);
+    if (!words) return chelis::set_error(CHELIS_HIP_EHIP, "trap status: no status word on this device");
+    CHELIS_HIP_TRY(hipMemcpyAsync(host, words + 1, sizeof(int32_t), hipMemcpyDeviceToHost, st));
+    CHELIS_HIP_TRY(hipStreamSynchronize(st));
+    const int32_t v = *host;
+    if (v) {
+        CHELIS_HIP_TRY(hipMemsetAsync(words + 1, 0, sizeof(int32_t), st));
+        CHELIS_HIP_TRY(hipStreamSynchronize(st));
+    }
+    if (code) *code = v;
     return CHELIS_HIP_OK;
 }

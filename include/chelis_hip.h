@@ -141,10 +141,19 @@ int32_t chelis_hip_reduce(int32_t op, const chelis_fused_chain *chain, const che
 int32_t chelis_hip_reduce_static(int32_t op, const chelis_fused_chain *chain, const chelis_gpu_tensor *const *inputs,
                                  int32_t n_inputs, int32_t axis, const chelis_gpu_tensor *out);
 /* kernels.rs:375-557 count: Bool8 -> i64 over one axis. A byte that is not
- * 0/1 sets *error_code = 1 (the reference kernel's code 1); the call then
- * synchronizes to read it back. */
+ * 0/1 raises the reference kernel's error code 1. With error_code, the call
+ * synchronizes and stores the code there, as the reference's launch does
+ * (emit.rs:4520-4620, one status word per call). With error_code == NULL it
+ * returns at once and the code goes to the device's trap channel, to be read
+ * once at the end of the caller's entry with chelis_hip_trap_status. */
 int32_t chelis_hip_count(const chelis_gpu_tensor *x, int32_t axis, const chelis_gpu_tensor *out,
                          int32_t *error_code);
+/* The current device's trap channel: synchronizes the library stream, stores
+ * the OR of the codes recorded since the last read (0: none) and clears it.
+ * The reference reads its numeric-failure flag after every trapping launch
+ * (kernels.rs:21-32, emit.rs:5185-5240); this channel lets an entry read it
+ * once, after its last launch. */
+int32_t chelis_hip_trap_status(int32_t *code);
 
 /* ---- keyed RNG ([05-RNG-1/2], [05-OP-8], [05-OP-37]) ----
  * uniform_like: kernels.rs:1672. dropout / replay: the C lane's semantics

@@ -204,3 +204,23 @@ def test_generic_regions_every_op_kind():
     assert bits_equal(outs[6], O.relu_adjoint(xv, -xv))
     assert bits_equal(outs[7], O.dropout(77, xv, np.float32(0.25)))
     assert bits_equal(outs[8], O.dropout_replay(77, xv, np.float32(0.25)))
+
+
+def test_count_region_reports_through_the_trap_channel():
+    """A Count region runs without waiting; a byte other than 0 / 1 is read
+    from the trap channel once after the run and raised there; the channel
+    is clear for the next run."""
+    g = DB.Dag("count")
+    b = g.load("b", [64, 300], "bool")
+    c = g.node({"Count": {"axes": [1]}}, [b], [64], "i64")
+    g.roots = [c]
+    prog = C.DagProgram(g.json())
+    bits = (np.random.default_rng(3).random((64, 300)) < 0.3).astype(np.uint8)
+    (y,) = prog.run([C.to_device(bits)])
+    assert np.array_equal(y.numpy(), bits.sum(1))
+    bad = bits.copy()
+    bad[5, 7] = 2
+    with pytest.raises(C.ChelisError, match="domain in count at bool"):
+        prog.run([C.to_device(bad)])
+    (y,) = prog.run([C.to_device(bits)])
+    assert np.array_equal(y.numpy(), bits.sum(1))

@@ -214,3 +214,24 @@ def test_prod_refuses_a_chain_leaf():
     ch = C.fused_chain([("mul", 0, 0)])
     with pytest.raises(C.ChelisError, match="status 2"):
         C.reduce("prod", [x], 1, chain=ch)
+
+
+def test_count_deferred_trap_channel():
+    """Deferred counts do not wait: their codes accumulate in the device's
+    trap channel until chelis_hip_trap_status reads and clears it."""
+    rng = np.random.default_rng(12)
+    good = (rng.random((256, 1000)) < 0.5).astype(np.uint8)
+    bad = good.copy()
+    bad[100, 999] = 7
+    assert C.trap_status() == 0
+    out, err = C.count(C.to_device(good), 1, deferred=True)
+    assert err is None and C.trap_status() == 0
+    assert np.array_equal(out.numpy(), good.sum(1))
+    C.count(C.to_device(bad), 1, deferred=True)
+    C.count(C.to_device(good), 1, deferred=True)
+    assert C.trap_status() == 1
+    assert C.trap_status() == 0
+    # a synchronous count neither reads nor clears the channel
+    C.count(C.to_device(bad), 0, deferred=True)
+    _, e = C.count(C.to_device(good), 1)
+    assert e == 0 and C.trap_status() == 1
