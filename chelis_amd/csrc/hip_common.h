@@ -10,6 +10,7 @@
 
 #include "chelis_hip.h"
 #include "devmath.h"
+#include "launch_limits.h"
 
 namespace chelis {
 
@@ -86,10 +87,7 @@ int32_t fused_elementwise_groups(const chelis_fused_chain *chain, int32_t n_inpu
                                  const chelis_gpu_tensor *const *inputs, const chelis_gpu_tensor *const *outs,
                                  int32_t n_groups);
 
-inline unsigned grid_for(int64_t work, int per_block) {
-    int64_t g = (work + per_block - 1) / per_block;
-    return (unsigned)(g < 1 ? 1 : g);
-}
+// grid_for / grid_fits: launch_limits.h
 
 // ---- device side -------------------------------------------------------
 // Wave64 butterfly exchange.

@@ -231,7 +231,7 @@ int32_t attention_causal(const chelis_gpu_tensor *q, const chelis_gpu_tensor *k,
     a.o0 = o->strides[0], a.o1 = o->strides[1], a.os = o->strides[2];
     a.scale = (float)scale;
     const int64_t blocks = a.pairs * a.qtiles;
-    if (blocks > 0x7fffffffLL) return set_error(CHELIS_HIP_EUNSUPPORTED, "attention: grid too large");
+    if (!grid_fits(blocks, kThreads)) return set_error(CHELIS_HIP_EUNSUPPORTED, "attention: grid too large");
     attention_causal_kernel<<<(unsigned)blocks, kThreads, 0, st>>>(a);
     CHELIS_LAUNCH_CHECK();
     return CHELIS_HIP_OK;

@@ -522,7 +522,7 @@ int32_t launch_flat(const ChainDev &ch, FlatGroups &fg, hipStream_t strm) {
             blocks += (fg.g[i].count + 256 * V - 1) / (256 * V);
         }
         if (blocks == 0) return CHELIS_HIP_OK;
-        if (blocks > 0x7fffffffLL) return set_error(CHELIS_HIP_EUNSUPPORTED, "fused_elementwise: too many elements");
+        if (!grid_fits(blocks, 256)) return set_error(CHELIS_HIP_EUNSUPPORTED, "fused_elementwise: too many elements");
         fused_flat_vec_kernel<T><<<(unsigned)blocks, 256, lds, strm>>>(ch, fg);
         CHELIS_LAUNCH_CHECK();
         return CHELIS_HIP_OK;
@@ -533,7 +533,7 @@ int32_t launch_flat(const ChainDev &ch, FlatGroups &fg, hipStream_t strm) {
         blocks += (fg.g[i].count + 255) / 256;
     }
     if (blocks == 0) return CHELIS_HIP_OK;
-    if (blocks > 0x7fffffffLL) return set_error(CHELIS_HIP_EUNSUPPORTED, "fused_elementwise: too many elements");
+    if (!grid_fits(blocks, 256)) return set_error(CHELIS_HIP_EUNSUPPORTED, "fused_elementwise: too many elements");
     fused_flat_kernel<T><<<(unsigned)blocks, 256, 0, strm>>>(ch, fg);
     CHELIS_LAUNCH_CHECK();
     return CHELIS_HIP_OK;

@@ -537,7 +537,7 @@ int32_t run_tiles(const GemmProblem &p, int al, int bl, bool av, bool bv, hipStr
     constexpr int64_t BT = 32 * TM;
     const int64_t tm = (p.M + BT - 1) / BT, tn = (p.N + BT - 1) / BT;
     const int64_t nz = p.nb0 * p.nb1;
-    if (tm * tn > 0x7fffffffLL || nz > 65535) return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: grid too large");
+    if (!grid_fits(tm * tn, THREADS) || nz > 65535) return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: grid too large");
     int64_t kchunk = 0;
     const int64_t ks = split_count<T, TM>(p, tm * tn * nz, &kchunk);
     T *part = nullptr;
@@ -561,7 +561,9 @@ int32_t run_tiles(const GemmProblem &p, int al, int bl, bool av, bool bv, hipStr
         default: launch_mfma<T, 2, 2, TM>(p, grid, tm, tn, av, bv, part, kchunk, st); break;
     }
     if (ks > 1) {
-        splitk_combine_kernel<T><<<grid_for(nz * p.M * p.N, 256), 256, 0, st>>>(p, part, (int)ks, nz);
+        unsigned g = grid_for(nz * p.M * p.N, 256);
+        if (g > 65536u) g = 65536u;  // the combine loops over the rest
+        splitk_combine_kernel<T><<<g, 256, 0, st>>>(p, part, (int)ks, nz);
         scratch_free(part, part_bytes);
     }
     CHELIS_LAUNCH_CHECK();

@@ -212,7 +212,7 @@ template <Narrow KIND>
 int32_t gemm16_kind(const GemmProblem &p, hipStream_t st) {
     const int64_t tm = (p.M + BM - 1) / BM, tn = (p.N + BN - 1) / BN;
     const int64_t nz = p.nb0 * p.nb1;
-    if (tm * tn > 0x7fffffffLL || nz > 65535) return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: grid too large");
+    if (!grid_fits(tm * tn, 256) || nz > 65535) return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: grid too large");
     const dim3 grid((unsigned)(tm * tn), (unsigned)nz);
     const int la = lay_of(p.a, p.sam, p.sak, p.sa0, p.sa1), lb = lay_of(p.b, p.sbn, p.sbk, p.sb0, p.sb1);
     // instantiated layouts: both K-contiguous, A K-contiguous with B along N

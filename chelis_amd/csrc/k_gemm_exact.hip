@@ -760,7 +760,7 @@ int32_t run_wave(const GemmProblem &p, hipStream_t st) {
     const bool av = ak && aligned16(p.a) && p.sam % W == 0 && p.sa0 % W == 0 && p.sa1 % W == 0;
     const bool bv = bk && aligned16(p.b) && p.sbn % W == 0 && p.sb0 % W == 0 && p.sb1 % W == 0;
     const int64_t blocks = (outputs + 3) / 4;
-    if (blocks > 0x7fffffffLL) return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: too many outputs");
+    if (!grid_fits(blocks, 256)) return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: too many outputs");
     // carry depth: DEPTH levels hold up to 2^(DEPTH - 1) segments (the last
     // push of 2^d segments lands in level d), so 9 levels cover K up to
     // 256 * 64 * V
@@ -787,7 +787,8 @@ int32_t run_tiled(const GemmProblem &p, hipStream_t st) {
     const bool av = ak && aligned16(p.a) && p.sam % W == 0 && p.sa0 % W == 0 && p.sa1 % W == 0;
     const bool kfast = p.sbk == 1 || (p.sbn != 1 && p.sbk < p.sbn);
     const int64_t gx = (p.M + WAVES * R - 1) / (WAVES * R), gy = (p.N + NJ - 1) / NJ, gz = p.nb0 * p.nb1;
-    if (gx > 0x7fffffffLL || gy > 65535 || gz > 65535) return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: grid too large");
+    if (!grid_fits(gx, 64 * WAVES) || gy > 65535 || gz > 65535)
+        return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: grid too large");
     const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)gz);
     if (ak && kfast) tree_tiled_kernel<T, V, R, NJ, WAVES, true, true><<<grid, 64 * WAVES, 0, st>>>(p, av);
     else if (ak) tree_tiled_kernel<T, V, R, NJ, WAVES, true, false><<<grid, 64 * WAVES, 0, st>>>(p, av);
@@ -818,7 +819,7 @@ int32_t launch_panel(const GemmProblem &p, const PanelView &v, bool cut, hipStre
            (v.K + kpart / 2 - 1) / (kpart / 2) <= 255)
         kpart >>= 1;
     const int64_t nparts = (v.K + kpart - 1) / kpart;
-    if (gx > 0x7fffffffLL || nparts > 255 || nz > 65535)
+    if (!grid_fits(gx, 64 * WAVES) || nparts > 255 || nz > 65535 || !grid_fits(grid_for(nz * v.M * 64, 256), 256))
         return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: panel grid too large");
     const dim3 grid((unsigned)gx, (unsigned)nparts, (unsigned)nz);
     // A runs load as one 2-element vector: unit K stride, aligned rows
@@ -887,7 +888,7 @@ int32_t run_thread(const GemmProblem &p, hipStream_t st) {
     if (p.K > 32) return set_error(CHELIS_HIP_EDOMAIN, "matmul: short-K kernel holds K <= 32");
     const int64_t outputs = p.M * p.N * p.nb0 * p.nb1;
     const int64_t blocks = (outputs + 255) / 256;
-    if (blocks > 0x7fffffffLL) return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: too many outputs");
+    if (!grid_fits(blocks, 256)) return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: too many outputs");
     constexpr int64_t W = Vec16<T>::W;
     // a vector read of A (B) needs K contiguous and every row (column) start 16-byte aligned
     const bool av = p.sak == 1 && aligned16(p.a) && (p.sam % W == 0 || p.M == 1) && p.sa0 % W == 0 && p.sa1 % W == 0;

@@ -527,8 +527,7 @@ int plan_passes(const ChainDev &ch, bool chain, const LeafSrc &src, int64_t oute
             }
         }
         // columns: 128-leaf groups per block when 64 columns fill a wave
-        const bool cols4 = !rows && inner >= 64 &&
-                           outer * ((cur_n + 127) / 128) * ((inner + 63) / 64) <= 0x7fffffffLL;
+        const bool cols4 = !rows && inner >= 64 && grid_fits(outer * ((cur_n + 127) / 128) * ((inner + 63) / 64), 256);
         const int64_t G = rows ? unit * S : (cols4 ? 128 : 32);
         const int64_t groups = (cur_n + G - 1) / G;
         passes[i] = Pass{vec, S, cols4, cur_n, groups};
@@ -637,6 +636,7 @@ int32_t run_reduce(const ChainDev &ch, bool chain, LeafSrc src, int64_t outer, i
         if (!dst_v) dst_v = static_cast<T *>(buf[pi & 1]);
         if (rows) {
             const unsigned grid = grid_for(outer * groups, 4);
+            if (!grid_fits(grid, 256)) return set_error(CHELIS_HIP_EUNSUPPORTED, "reduce: too many row groups");
 #define CHELIS_ROWS_LAUNCH(KERNEL, SS, CHAIN_OK, LDS)                                                        \
     if constexpr (kChainable<K> && (CHAIN_OK)) {                                                              \
         if (use_chain) {                                                                                      \
@@ -782,6 +782,7 @@ int32_t reduce_entry(int32_t op, const chelis_fused_chain *chain, const chelis_g
                              : op == CHELIS_REDUCE_ARGMAX ? "argmax_reduce" : "argmin_reduce",
                              idx_out ? "i64" : (x0->dtype == CHELIS_DTYPE_F32 ? "f32" : "f64"));
         const unsigned grid = grid_for(out->count, 256);
+        if (!grid_fits(grid, 256)) return set_error(CHELIS_HIP_EUNSUPPORTED, "reduce: too many results");
         if (x0->dtype == CHELIS_DTYPE_F32)
             fill_kernel<float><<<grid, 256, 0, st>>>((float *)out->data, out->count, op == CHELIS_REDUCE_SUM ? 0.0f : 1.0f);
         else
@@ -896,6 +897,7 @@ extern "C" int32_t chelis_hip_count(const chelis_gpu_tensor *x, int32_t axis, co
     // without: the trap channel, read at the caller's entry end
     int32_t *err = error_code ? words : words + 1;
     if (error_code) CHELIS_HIP_TRY(hipMemsetAsync(err, 0, sizeof(int32_t), st));
+    if (!grid_fits(grid_for(outer * inner, 4), 256)) return set_error(CHELIS_HIP_EUNSUPPORTED, "count: too many results");
     if (inner == 1 && sn == 1 && so % 16 == 0 && (reinterpret_cast<uintptr_t>(x->data) & 15u) == 0)
         count_rows_vec_kernel<<<grid_for(outer, 4), 256, 0, st>>>((const uint8_t *)x->data, outer, x->shape[axis], so,
                                                                   (int64_t *)out->data, err);

@@ -26,6 +26,8 @@
 // earlier element.
 #include "chain.h"
 
+#include <initializer_list>
+
 namespace chelis {
 namespace {
 
@@ -547,6 +549,8 @@ struct RowArgs {
 template <typename T, int V, int S, int W, int R>
 int32_t launch_shape(RowOp op, const RowArgs &a, hipStream_t st) {
     const unsigned grid = grid_for(a.rows, R);
+    if (!grid_fits(grid, 64 * W * R)) return set_error(CHELIS_HIP_EUNSUPPORTED, "rows: %lld rows exceed one launch",
+                                                       (long long)a.rows);
     const dim3 block(64 * W * R);
     switch (op) {
         case RowOp::Softmax:
@@ -620,6 +624,142 @@ int32_t check_rows_pair(const chelis_gpu_tensor *x, const chelis_gpu_tensor *y, 
     return CHELIS_HIP_OK;
 }
 
+// ---------------------------------------------------------------- long rows
+// Rows longer than the register capacity (64 * 256 * 16 / sizeof(T): 65 536
+// binary32 or 32 768 binary64 values) run as the graph the region stands
+// for, one launch per reduction and per elementwise pass, in the same
+// primitive order as the row kernels: the reductions take the canonical
+// tree over the whole row (aligned segment totals joined pass by pass), the
+// chains finalize every primitive, so the results are bit-identical to what
+// the row kernels would give (and to the C lane's).
+constexpr int64_t kRowCapacityBytes = 64 * 256 * 16;
+
+struct Rows2 {
+    int64_t shape[2], strides[2];
+    chelis_gpu_tensor t{};
+    Rows2(void *data, chelis_dtype dt, int64_t rows, int64_t n, int64_t s_row, int64_t s_col, int64_t cap) {
+        shape[0] = rows, shape[1] = n, strides[0] = s_row, strides[1] = s_col;
+        t.data = data;
+        t.dtype = dt;
+        t.rank = 2;
+        t.shape = shape;
+        t.strides = strides;
+        t.count = rows * n;
+        t.byte_capacity = cap;
+    }
+};
+struct Vec1 {
+    int64_t shape[1], strides[1];
+    chelis_gpu_tensor t{};
+    Vec1(void *data, chelis_dtype dt, int64_t n) {
+        shape[0] = n, strides[0] = 1;
+        t.data = data;
+        t.dtype = dt;
+        t.rank = 1;
+        t.shape = shape;
+        t.strides = strides;
+        t.count = n;
+        t.byte_capacity = n * dtype_width(dt);
+    }
+};
+
+chelis_fused_step fstep(int op, int32_t a0, int32_t a1 = 0, double imm = 0.0) {
+    chelis_fused_step st{};
+    st.op = (uint8_t)op;
+    st.args[0] = a0;
+    st.args[1] = a1;
+    st.imm = imm;
+    return st;
+}
+constexpr int32_t prv(int32_t k) { return -(k + 1); }
+chelis_fused_chain fchain(std::initializer_list<chelis_fused_step> steps) {
+    chelis_fused_chain c{};
+    for (const chelis_fused_step &st : steps) c.steps[c.n_steps++] = st;
+    return c;
+}
+
+// Per-row scratch vectors, released (stream-ordered) at scope exit.
+struct RowScratch {
+    void *p = nullptr;
+    size_t bytes = 0;
+    explicit RowScratch(size_t b) : p(scratch_alloc(b)), bytes(b) {}
+    ~RowScratch() { scratch_free(p, bytes); }
+};
+
+int32_t long_softmax(const chelis_gpu_tensor *x, const chelis_gpu_tensor *y, const RowView &vx, const RowView &vy) {
+    const chelis_dtype dt = x->dtype;
+    const int64_t w = dtype_width(dt), R = vx.rows, n = vx.n;
+    RowScratch m(R * w), sum(R * w);
+    if (!m.p || !sum.p) return set_error(CHELIS_HIP_EHIP, "softmax: row scratch of %lld bytes", (long long)(2 * R * w));
+    const Rows2 X(x->data, dt, R, n, vx.ld, 1, x->byte_capacity), Y(y->data, dt, R, n, vy.ld, 1, y->byte_capacity);
+    const Vec1 M(m.p, dt, R), S(sum.p, dt, R);
+    const Rows2 Mb(m.p, dt, R, n, 1, 0, R * w), Sb(sum.p, dt, R, n, 1, 0, R * w);
+    // m = max over the row; s = tree(exp(x - m)); y = exp(x - m) / s
+    const chelis_gpu_tensor *in1[1] = {&X.t};
+    if (int32_t st = chelis_hip_reduce(CHELIS_REDUCE_MAX, nullptr, in1, 1, 1, &M.t)) return st;
+    const chelis_fused_chain e = fchain({fstep(CHELIS_FUSED_SUB, 0, 1), fstep(CHELIS_FUSED_EXP, prv(0))});
+    const chelis_gpu_tensor *in2[2] = {&X.t, &Mb.t};
+    if (int32_t st = chelis_hip_reduce(CHELIS_REDUCE_SUM, &e, in2, 2, 1, &S.t)) return st;
+    const chelis_fused_chain q = fchain(
+        {fstep(CHELIS_FUSED_SUB, 0, 1), fstep(CHELIS_FUSED_EXP, prv(0)), fstep(CHELIS_FUSED_DIV, prv(1), 2)});
+    const chelis_gpu_tensor *in3[3] = {&X.t, &Mb.t, &Sb.t};
+    return chelis_hip_fused_elementwise(&q, in3, 3, &Y.t);
+}
+
+int32_t long_softmax_adjoint(const chelis_gpu_tensor *y, const chelis_gpu_tensor *g, const chelis_gpu_tensor *dx,
+                             const RowView &vy, const RowView &vg, const RowView &vd) {
+    const chelis_dtype dt = y->dtype;
+    const int64_t w = dtype_width(dt), R = vy.rows, n = vy.n;
+    RowScratch tot(R * w);
+    if (!tot.p) return set_error(CHELIS_HIP_EHIP, "softmax_adjoint: row scratch of %lld bytes", (long long)(R * w));
+    const Rows2 Yv(y->data, dt, R, n, vy.ld, 1, y->byte_capacity), G(g->data, dt, R, n, vg.ld, 1, g->byte_capacity),
+        D(dx->data, dt, R, n, vd.ld, 1, dx->byte_capacity);
+    const Vec1 T(tot.p, dt, R);
+    const Rows2 Tb(tot.p, dt, R, n, 1, 0, R * w);
+    // t = tree(g * y); dx = y * (g - t)
+    const chelis_fused_chain gy = fchain({fstep(CHELIS_FUSED_MUL, 0, 1)});
+    const chelis_gpu_tensor *in2[2] = {&G.t, &Yv.t};
+    if (int32_t st = chelis_hip_reduce(CHELIS_REDUCE_SUM, &gy, in2, 2, 1, &T.t)) return st;
+    const chelis_fused_chain d = fchain({fstep(CHELIS_FUSED_SUB, 1, 2), fstep(CHELIS_FUSED_MUL, 0, prv(0))});
+    const chelis_gpu_tensor *in3[3] = {&Yv.t, &G.t, &Tb.t};
+    return chelis_hip_fused_elementwise(&d, in3, 3, &D.t);
+}
+
+int32_t long_layer_norm(const chelis_gpu_tensor *x, const chelis_gpu_tensor *gamma, const chelis_gpu_tensor *beta,
+                        double eps, const chelis_gpu_tensor *y, const RowView &vx, const RowView &vy) {
+    const chelis_dtype dt = x->dtype;
+    const int64_t w = dtype_width(dt), R = vx.rows, n = vx.n;
+    RowScratch tmp(R * w), mean(R * w), den(R * w);
+    if (!tmp.p || !mean.p || !den.p)
+        return set_error(CHELIS_HIP_EHIP, "layer_norm: row scratch of %lld bytes", (long long)(3 * R * w));
+    const Rows2 X(x->data, dt, R, n, vx.ld, 1, x->byte_capacity), Y(y->data, dt, R, n, vy.ld, 1, y->byte_capacity);
+    const Vec1 Tv(tmp.p, dt, R), Mv(mean.p, dt, R), Dv(den.p, dt, R);
+    const Rows2 Mb(mean.p, dt, R, n, 1, 0, R * w), Db(den.p, dt, R, n, 1, 0, R * w);
+    const Rows2 Gb(gamma->data, dt, R, n, 0, 1, gamma->byte_capacity), Bb(beta->data, dt, R, n, 0, 1, beta->byte_capacity);
+    const double extent = (double)n;
+    // mean = tree(x) / n
+    const chelis_gpu_tensor *in1[1] = {&X.t};
+    if (int32_t st = chelis_hip_reduce(CHELIS_REDUCE_SUM, nullptr, in1, 1, 1, &Tv.t)) return st;
+    const chelis_fused_chain by_n = fchain({fstep(CHELIS_FUSED_CONST, 0, 0, extent), fstep(CHELIS_FUSED_DIV, 0, prv(0))});
+    const chelis_gpu_tensor *t1[1] = {&Tv.t};
+    if (int32_t st = chelis_hip_fused_elementwise(&by_n, t1, 1, &Mv.t)) return st;
+    // var = tree((x - mean)^2) / n; denom = sqrt(var + eps)
+    const chelis_fused_chain sq = fchain({fstep(CHELIS_FUSED_SUB, 0, 1), fstep(CHELIS_FUSED_MUL, prv(0), prv(0))});
+    const chelis_gpu_tensor *in2[2] = {&X.t, &Mb.t};
+    if (int32_t st = chelis_hip_reduce(CHELIS_REDUCE_SUM, &sq, in2, 2, 1, &Tv.t)) return st;
+    const chelis_fused_chain dn = fchain({fstep(CHELIS_FUSED_CONST, 0, 0, extent), fstep(CHELIS_FUSED_DIV, 0, prv(0)),
+                                          fstep(CHELIS_FUSED_CONST, 0, 0, eps), fstep(CHELIS_FUSED_ADD, prv(1), prv(2)),
+                                          fstep(CHELIS_FUSED_SQRT, prv(3))});
+    if (int32_t st = chelis_hip_fused_elementwise(&dn, t1, 1, &Dv.t)) return st;
+    // y = ((x - mean) / denom) * gamma + beta
+    const chelis_fused_chain out = fchain({fstep(CHELIS_FUSED_SUB, 0, 1), fstep(CHELIS_FUSED_DIV, prv(0), 2),
+                                           fstep(CHELIS_FUSED_MUL, prv(1), 3), fstep(CHELIS_FUSED_ADD, prv(2), 4)});
+    const chelis_gpu_tensor *in5[5] = {&X.t, &Mb.t, &Db.t, &Gb.t, &Bb.t};
+    return chelis_hip_fused_elementwise(&out, in5, 5, &Y.t);
+}
+
+bool long_rows(chelis_dtype dt, int64_t n) { return n > kRowCapacityBytes / dtype_width(dt); }
+
 }  // namespace
 }  // namespace chelis
 
@@ -628,6 +768,7 @@ using namespace chelis;
 extern "C" int32_t chelis_hip_softmax(const chelis_gpu_tensor *x, const chelis_gpu_tensor *y) {
     RowView vx, vy;
     if (int32_t s = check_rows_pair(x, y, &vx, &vy, "softmax")) return s;
+    if (vx.rows && long_rows(x->dtype, vx.n)) return long_softmax(x, y, vx, vy);
     const int64_t V = 16 / dtype_width(x->dtype);
     RowArgs a{x->data, nullptr, nullptr, y->data, vx.rows, vx.n, vx.ld, 0, vy.ld,
               aligned16(x->data) && aligned16(y->data) && vx.ld % V == 0 && vy.ld % V == 0, 0, 1.0, 1, 0.0};
@@ -656,6 +797,7 @@ extern "C" int32_t chelis_hip_softmax_adjoint(const chelis_gpu_tensor *y, const 
     if (int32_t s = check_tensor(g, "g")) return s;
     if (g->dtype != y->dtype || !same_shape(g, y) || !row_view(g, &vg))
         return set_error(CHELIS_HIP_EDOMAIN, "softmax_adjoint: g must match y");
+    if (vy.rows && long_rows(y->dtype, vy.n)) return long_softmax_adjoint(y, g, dx, vy, vg, vd);
     const int64_t V = 16 / dtype_width(y->dtype);
     RowArgs a{y->data, g->data, nullptr, dx->data, vy.rows, vy.n, vy.ld, vg.ld, vd.ld,
               aligned16(y->data) && aligned16(g->data) && aligned16(dx->data) && vy.ld % V == 0 &&
@@ -675,6 +817,7 @@ extern "C" int32_t chelis_hip_layer_norm(const chelis_gpu_tensor *x, const cheli
         if (p->dtype != x->dtype || p->rank != 1 || p->shape[0] != vx.n || (vx.n > 1 && p->strides[0] != 1))
             return set_error(CHELIS_HIP_EDOMAIN, "layer_norm: gamma/beta must be contiguous [hidden]");
     if (vx.n == 0) return set_error(CHELIS_HIP_EDOMAIN, "layer_norm: hidden extent must be positive");
+    if (vx.rows && long_rows(x->dtype, vx.n)) return long_layer_norm(x, gamma, beta, epsilon, y, vx, vy);
     const int64_t V = 16 / dtype_width(x->dtype);
     RowArgs a{x->data, gamma->data, beta->data, y->data, vx.rows, vx.n, vx.ld, 0, vy.ld,
               aligned16(x->data) && aligned16(y->data) && aligned16(gamma->data) && aligned16(beta->data) &&

@@ -491,3 +491,31 @@ def test_causal_attention_rejects_unsupported_shapes():
     q = C.to_device(np.zeros((1, 1, 96, 64), np.float32))
     with pytest.raises(C.ChelisError):
         C.causal_attention(q, q, q, 0.125, C.empty((1, 1, 96, 64), np.float32))
+
+
+LONG_ROWS = [(np.float32, 3, 65537), (np.float32, 2, 200_003), (np.float64, 3, 32769), (np.float64, 2, 100_001)]
+
+
+@pytest.mark.parametrize("dtype,rows,n", LONG_ROWS)
+def test_long_rows_bit_exact(dtype, rows, n):
+    """Rows past the register capacity (65 536 f32 / 32 768 f64 values) run
+    as reductions and chains in the row kernels' primitive order: softmax,
+    its adjoint and layer norm stay bit-exact against the oracle; strided
+    rows included."""
+    rng = np.random.default_rng(n + rows)
+    x = (rng.standard_normal((rows, n)) * 3).astype(dtype)
+    g = rng.standard_normal((rows, n)).astype(dtype)
+    gamma = (1 + 0.1 * rng.standard_normal(n)).astype(dtype)
+    beta = (0.1 * rng.standard_normal(n)).astype(dtype)
+    # x as a strided view: rows padded by 5 elements
+    buf = np.zeros((rows, n + 5), dtype)
+    buf[:, :n] = x
+    dbuf = C.to_device(buf)
+    xv = dbuf.view((rows, n), (n + 5, 1))
+    y = C.softmax(xv).numpy()
+    ref = O.softmax_rows(x)
+    assert bits_equal(y, ref)
+    dx = C.softmax_adjoint(C.to_device(ref), C.to_device(g)).numpy()
+    assert bits_equal(dx, O.softmax_adjoint_rows(ref, g))
+    ln = C.layer_norm(xv, C.to_device(gamma), C.to_device(beta), 1e-5).numpy()
+    assert bits_equal(ln, O.layer_norm_rows(x, gamma, beta, 1e-5))
