@@ -62,6 +62,12 @@ bool attention_causal_fits(const chelis_gpu_tensor *q, const chelis_gpu_tensor *
                            const chelis_gpu_tensor *o);
 int32_t attention_causal(const chelis_gpu_tensor *q, const chelis_gpu_tensor *k, const chelis_gpu_tensor *v,
                          double scale, const chelis_gpu_tensor *o);
+// The linear-regression step r = X.w - y, grad = X^T.r / n, loss =
+// tree(r * r) / n in two launches, bit-identical to the unfused graph
+// (k_linreg.hip); linreg_fused_fits: d <= 32 and rows of X contiguous.
+bool linreg_fused_fits(const chelis_gpu_tensor *X, const chelis_gpu_tensor *w);
+int32_t linreg_fused(const chelis_gpu_tensor *X, const chelis_gpu_tensor *w, const chelis_gpu_tensor *y,
+                     const chelis_gpu_tensor *grad, const chelis_gpu_tensor *loss, hipStream_t st);
 // c = a . b for attention with the causal mode above (programs only).
 int32_t matmul_causal(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b, const chelis_gpu_tensor *c,
                       int32_t mode);

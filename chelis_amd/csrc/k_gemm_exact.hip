@@ -309,6 +309,12 @@ __global__ __launch_bounds__(64 * WAVES) void tree_tiled_kernel(GemmProblem p, b
 // padded with -0.0, which is the full tree over those block totals, so with
 // more than one block the totals go to a workspace and tree_combine_kernel
 // joins them in tree order.
+// Carry-stack depth of the block-total join: up to 2^16 - 1 totals, i.e.
+// K up to 2^16 - 1 blocks of 512 leaves (the totals run along grid y,
+// whose limit is the same 65535).
+constexpr int kCombineLevels = 16;
+constexpr int64_t kMaxParts = (int64_t(1) << kCombineLevels) - 1;
+
 struct PanelView {
     const void *a, *b;
     int64_t M, N, K;
@@ -626,8 +632,9 @@ __global__ __launch_bounds__(64 * WAVES) void tree_panel_s_kernel(PanelView v, G
 }
 
 // Join the per-block totals of tree_panel_kernel: the canonical tree over
-// the nparts block totals (adjacent pairs, odd one carried), then the
-// epilogue. One thread per output.
+// the nparts block totals (adjacent pairs, odd one carried; a carry stack
+// of kCombineLevels levels holds up to 2^kCombineLevels - 1 totals), then
+// the epilogue. One thread per output.
 template <typename T>
 __global__ __launch_bounds__(256) void tree_combine_kernel(PanelView v, GemmProblem p, const T *__restrict__ part,
                                                            int64_t nparts, int64_t nz) {
@@ -637,7 +644,7 @@ __global__ __launch_bounds__(256) void tree_combine_kernel(PanelView v, GemmProb
     const int64_t n = idx % 64;
     if (n >= v.N) return;
     const int64_t z = idx / per_z, m = (idx / 64) % v.M;
-    T lvl[8];
+    T lvl[kCombineLevels];
     // eight block totals are read before any is pushed: one memory latency
     // per eight parts
     for (int64_t j0 = 0; j0 < nparts; j0 += 8) {
@@ -651,7 +658,7 @@ __global__ __launch_bounds__(256) void tree_combine_kernel(PanelView v, GemmProb
             T carry = q[u];
             bool done = false;
 #pragma unroll
-            for (int d = 0; d < 8; ++d) {
+            for (int d = 0; d < kCombineLevels; ++d) {
                 if (!done) {
                     if ((j >> d) & 1) {
                         carry = lvl[d] + carry;
@@ -666,7 +673,7 @@ __global__ __launch_bounds__(256) void tree_combine_kernel(PanelView v, GemmProb
     T total = T(0);
     bool found = false;
 #pragma unroll
-    for (int d = 0; d < 8; ++d)
+    for (int d = 0; d < kCombineLevels; ++d)
         if ((nparts >> d) & 1) {
             total = found ? lvl[d] + total : lvl[d];
             found = true;
@@ -814,12 +821,14 @@ int32_t launch_panel(const GemmProblem &p, const PanelView &v, bool cut, hipStre
     while (p2 < v.K) p2 <<= 1;
     int64_t kpart = std::min<int64_t>(p2, (int64_t)KC << (D - 1));
     const int64_t want = 4 * (int64_t)std::max(device_cus(), 1);
-    // (the combine pass joins at most 255 block totals)
+    // (cutting stops at 255 block totals; a long K keeps the full block
+    // and may leave up to kMaxParts)
     while (cut && kpart > KC && gx * nz * ((v.K + kpart - 1) / kpart) < want &&
            (v.K + kpart / 2 - 1) / (kpart / 2) <= 255)
         kpart >>= 1;
     const int64_t nparts = (v.K + kpart - 1) / kpart;
-    if (!grid_fits(gx, 64 * WAVES) || nparts > 255 || nz > 65535 || !grid_fits(grid_for(nz * v.M * 64, 256), 256))
+    if (!grid_fits(gx, 64 * WAVES) || nparts > kMaxParts || nz > 65535 ||
+        !grid_fits(grid_for(nz * v.M * 64, 256), 256))
         return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: panel grid too large");
     const dim3 grid((unsigned)gx, (unsigned)nparts, (unsigned)nz);
     // A runs load as one 2-element vector: unit K stride, aligned rows
@@ -845,7 +854,7 @@ int32_t launch_panel(const GemmProblem &p, const PanelView &v, bool cut, hipStre
         // many totals for few outputs: lanes over the totals (a thread per
         // output would read its totals one batch after another)
         const int64_t outputs = nz * v.M * v.N;
-        if (nparts >= 32 && outputs <= 65536)
+        if (nparts >= 32 && nparts <= 256 && outputs <= 65536)
             tree_combine_wave_kernel<T><<<grid_for(outputs, 4), 256, 0, st>>>(v, p, ws, nparts, nz);
         else
             tree_combine_kernel<T><<<grid_for(nz * v.M * 64, 256), 256, 0, st>>>(v, p, ws, nparts, nz);

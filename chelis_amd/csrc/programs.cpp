@@ -153,6 +153,9 @@ extern "C" int32_t chelis_prog_linreg_step(const chelis_gpu_tensor *const *in, i
         return set_error(CHELIS_HIP_EDOMAIN, "linreg_step: shapes/dtypes must be X[n,d], w[d], y[n] -> grad[d], loss[]");
     hipStream_t st = stream();
     if (!st) return set_error(CHELIS_HIP_EHIP, "no HIP device");
+    // two launches (row blocks, then the joins) where d <= 32; the same bits
+    // as the launch-per-region form below
+    if (linreg_fused_fits(X, w)) return linreg_fused(X, w, y, out[0], out[1], st);
     Workspace ws(st);
     const size_t o_r = ws.reserve(n * dtype_width(dt)), o_g = ws.reserve(d * dtype_width(dt));
     TRY(ws.commit());

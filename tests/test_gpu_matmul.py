@@ -84,6 +84,8 @@ TREE_CASES = [
     (64, 1, 1000, True, False),     # the same with a full 64-lane panel
     (1, 48, 5000, False, False),    # row vector times a row-major matrix: outputs on the lanes
     (1, 64, 33, False, False),      # the same, one partial chunk
+    (4, 1, 262145, True, False),    # linreg X^T r form, K past 255 blocks of 512: the deep block-total join
+    (3, 5, 300000, False, False),   # panel, 586 block totals
 ]
 
 

@@ -50,6 +50,20 @@ def test_linreg_step_config1_bit_exact():
     assert bits_equal(loss.numpy(), np.float64(loss_ref))
 
 
+@pytest.mark.parametrize("n,d", [(1, 1), (63, 2), (65, 3), (8193, 32), (4096 * 64, 8), (4096 * 64 + 1, 4), (300, 33)])
+def test_linreg_step_shapes_bit_exact(n, d):
+    """Ragged row blocks, every register-tree width, the largest row count
+    the two-launch step takes (4096 blocks of 64 rows) and the first past it,
+    and d = 33 (past the short contraction): all bit-exact."""
+    X, w, y = linreg_inputs(n, d)
+    grad_ref, loss_ref = O.linreg_step(X, w, y)
+    ins = [C.to_device(a) for a in (X, w, y)]
+    grad, loss = C.empty((d,), np.float64), C.empty((), np.float64)
+    C.program("linreg_step", ins, [grad, loss])
+    assert bits_equal(grad.numpy(), grad_ref)
+    assert bits_equal(loss.numpy(), np.float64(loss_ref))
+
+
 def test_linreg_step_device_entry_allocates_outputs():
     X, w, y = linreg_inputs(1000, 7)
     grad_ref, loss_ref = O.linreg_step(X, w, y)
