@@ -47,6 +47,16 @@ __device__ inline T gemm_epilogue(T acc, const GemmProblem &p, int64_t z0, int64
 }
 
 int32_t gemm_mfma(chelis_dtype dt, const GemmProblem &p, hipStream_t st);
+// The MFMA tiles' raw sums as K slices, part[slice][z][m][n] (no epilogue,
+// no combine; one slice when the product is not split), and their count.
+int64_t gemm_mfma_slice_count(chelis_dtype dt, const GemmProblem &p);
+int32_t gemm_mfma_slices(chelis_dtype dt, const GemmProblem &p, void *part, hipStream_t st);
+// c = a . b of two matrices as raw K slices for a consumer that sums them
+// in slice order itself (then finalizes: canon, epilogue): part holds
+// matmul_slice_count(a, b) contiguous [M, N] slices. Whatever the dispatch
+// routes elsewhere (tree kernels, the exact flag) is one finished slice.
+int64_t matmul_slice_count(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b);
+int32_t matmul_slices(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b, void *part, int64_t slices);
 // bf16 / f16 operands and result, binary32 accumulation (k_gemm16.hip).
 int32_t gemm_mfma16(chelis_dtype dt, const GemmProblem &p, hipStream_t st);
 // 16-bit [nz0][nz1][rows][cols] view <-> contiguous binary32 (the exact
@@ -68,6 +78,30 @@ int32_t attention_causal(const chelis_gpu_tensor *q, const chelis_gpu_tensor *k,
 bool linreg_fused_fits(const chelis_gpu_tensor *X, const chelis_gpu_tensor *w);
 int32_t linreg_fused(const chelis_gpu_tensor *X, const chelis_gpu_tensor *w, const chelis_gpu_tensor *y,
                      const chelis_gpu_tensor *grad, const chelis_gpu_tensor *loss, hipStream_t st);
+// The MLP step between and after its two wide products (k_mlp.hip),
+// bit-identical to the unfused launches. mlp_head_tail: from x.W1's raw K
+// slices (z1, [z1_slices][B][H]) to d, g_z2, nl, g_d (the input of the
+// x^T.g_d product) and the tail's row-block totals in part
+// (mlp_part_bytes). mlp_finish, after x^T.g_d (gw1, [gw1_slices][I][H]):
+// the W1, W2, b1, b2 updates and the loss. All pointers are contiguous f32
+// device arrays ([B,H] d, gd; [H,O] W2; [B,O] onehot, gz2; [B] nl); key is
+// the KEY tensor's storage.
+struct MlpNarrow {
+    int64_t B, I, H, O;
+    const float *z1;
+    int64_t z1_slices;
+    const float *gw1;
+    int64_t gw1_slices;
+    const float *w1, *w2, *b2, *onehot, *b1;
+    const uint64_t *key;
+    float *d, *gz2, *nl, *gd, *part;
+    float *w1_out, *w2_out, *b1_out, *b2_out, *loss;
+    float rate, lr;
+};
+bool mlp_narrow_fits(int64_t B, int64_t I, int64_t H, int64_t O);
+size_t mlp_part_bytes(int64_t B, int64_t H);
+int32_t mlp_head_tail(const MlpNarrow &m, hipStream_t st);
+int32_t mlp_finish(const MlpNarrow &m, hipStream_t st);
 // c = a . b for attention with the causal mode above (programs only).
 int32_t matmul_causal(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b, const chelis_gpu_tensor *c,
                       int32_t mode);

@@ -532,17 +532,31 @@ int64_t split_count(const GemmProblem &p, int64_t tiles, int64_t *kchunk) {
     return ks;
 }
 
+// K slices the tiles of this size take for p (1: no split) and their depth.
 template <typename T, int TM>
-int32_t run_tiles(const GemmProblem &p, int al, int bl, bool av, bool bv, hipStream_t st) {
+int64_t tile_slices(const GemmProblem &p, int64_t *kchunk) {
+    constexpr int64_t BT = 32 * TM;
+    const int64_t tm = (p.M + BT - 1) / BT, tn = (p.N + BT - 1) / BT;
+    *kchunk = 0;
+    return split_count<T, TM>(p, tm * tn * p.nb0 * p.nb1, kchunk);
+}
+
+// ext_part: the caller's [slices][z][m][n] buffer; the slices' raw sums go
+// there (one slice when the product is not split) and no combine runs.
+template <typename T, int TM>
+int32_t run_tiles(const GemmProblem &p, int al, int bl, bool av, bool bv, hipStream_t st, T *ext_part = nullptr) {
     constexpr int64_t BT = 32 * TM;
     const int64_t tm = (p.M + BT - 1) / BT, tn = (p.N + BT - 1) / BT;
     const int64_t nz = p.nb0 * p.nb1;
     if (!grid_fits(tm * tn, THREADS) || nz > 65535) return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: grid too large");
     int64_t kchunk = 0;
-    const int64_t ks = split_count<T, TM>(p, tm * tn * nz, &kchunk);
-    T *part = nullptr;
-    const size_t part_bytes = ks > 1 ? (size_t)(ks * nz * p.M * p.N) * sizeof(T) : 0;
-    if (ks > 1) {
+    const int64_t ks = tile_slices<T, TM>(p, &kchunk);
+    T *part = ext_part;
+    const size_t part_bytes = ks > 1 && !ext_part ? (size_t)(ks * nz * p.M * p.N) * sizeof(T) : 0;
+    if (ext_part) {
+        // one slice spanning K when unsplit (a multiple of the tile depth)
+        if (ks == 1) kchunk = (p.K + Depth<T, TM>::BK - 1) / Depth<T, TM>::BK * Depth<T, TM>::BK;
+    } else if (ks > 1) {
         part = static_cast<T *>(scratch_alloc(part_bytes));
         if (!part) return set_error(CHELIS_HIP_EHIP, "matmul: split-K scratch of %zu bytes", part_bytes);
     } else {
@@ -560,7 +574,7 @@ int32_t run_tiles(const GemmProblem &p, int al, int bl, bool av, bool bv, hipStr
         case 7: launch_mfma<T, 2, 1, TM>(p, grid, tm, tn, av, bv, part, kchunk, st); break;
         default: launch_mfma<T, 2, 2, TM>(p, grid, tm, tn, av, bv, part, kchunk, st); break;
     }
-    if (ks > 1) {
+    if (ks > 1 && !ext_part) {
         unsigned g = grid_for(nz * p.M * p.N, 256);
         if (g > 65536u) g = 65536u;  // the combine loops over the rest
         splitk_combine_kernel<T><<<g, 256, 0, st>>>(p, part, (int)ks, nz);
@@ -570,11 +584,9 @@ int32_t run_tiles(const GemmProblem &p, int al, int bl, bool av, bool bv, hipStr
     return CHELIS_HIP_OK;
 }
 
+// Tile size for p: 128-tiles (true) or 64-tiles.
 template <typename T>
-int32_t run_mfma(const GemmProblem &p, hipStream_t st) {
-    bool av = false, bv = false;
-    const int al = lay_of<T>(p.sam, p.sak, p.a, p.M, p.K, &av);
-    const int bl = lay_of<T>(p.sbn, p.sbk, p.b, p.N, p.K, &bv);
+bool big_tiles(const GemmProblem &p) {
     // 128-tiles when they give every CU two tiles (the two workgroups a CU
     // holds), no dimension is at most half a tile and K runs long enough
     // (> 128) to amortize a tile's first loads and its epilogue; 64-tiles,
@@ -590,13 +602,37 @@ int32_t run_mfma(const GemmProblem &p, hipStream_t st) {
     const int64_t kslices = p.K / 1024 < 16 ? p.K / 1024 : 16;
     const bool few = big < 2 * cus && !(p.causal == 0 && p.K >= 2048 && big * kslices >= 2 * cus && big >= cus / 2);
     const bool small = few || p.M <= 64 || p.N <= 64 || p.K <= 128;
-    return small ? run_tiles<T, 2>(p, al, bl, av, bv, st) : run_tiles<T, 4>(p, al, bl, av, bv, st);
+    return !small;
+}
+
+template <typename T>
+int32_t run_mfma(const GemmProblem &p, hipStream_t st, T *ext_part = nullptr) {
+    bool av = false, bv = false;
+    const int al = lay_of<T>(p.sam, p.sak, p.a, p.M, p.K, &av);
+    const int bl = lay_of<T>(p.sbn, p.sbk, p.b, p.N, p.K, &bv);
+    return big_tiles<T>(p) ? run_tiles<T, 4>(p, al, bl, av, bv, st, ext_part)
+                           : run_tiles<T, 2>(p, al, bl, av, bv, st, ext_part);
+}
+
+template <typename T>
+int64_t mfma_slices(const GemmProblem &p) {
+    int64_t kchunk = 0;
+    return big_tiles<T>(p) ? tile_slices<T, 4>(p, &kchunk) : tile_slices<T, 2>(p, &kchunk);
 }
 
 }  // namespace
 
 int32_t gemm_mfma(chelis_dtype dt, const GemmProblem &p, hipStream_t st) {
     return dt == CHELIS_DTYPE_F32 ? run_mfma<float>(p, st) : run_mfma<double>(p, st);
+}
+
+int64_t gemm_mfma_slice_count(chelis_dtype dt, const GemmProblem &p) {
+    return dt == CHELIS_DTYPE_F32 ? mfma_slices<float>(p) : mfma_slices<double>(p);
+}
+
+int32_t gemm_mfma_slices(chelis_dtype dt, const GemmProblem &p, void *part, hipStream_t st) {
+    return dt == CHELIS_DTYPE_F32 ? run_mfma<float>(p, st, static_cast<float *>(part))
+                                  : run_mfma<double>(p, st, static_cast<double *>(part));
 }
 
 }  // namespace chelis

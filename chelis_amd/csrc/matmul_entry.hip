@@ -184,7 +184,60 @@ int32_t dispatch(chelis_dtype dt, const GemmProblem &p, int32_t flags) {
     return gemm_mfma(dt, p, st);
 }
 
+// True when dispatch sends p to the MFMA tiles.
+bool takes_mfma(chelis_dtype dt, const GemmProblem &p) {
+    if (is_narrow16(dt) || (dt != CHELIS_DTYPE_F32 && dt != CHELIS_DTYPE_F64)) return false;
+    if (g_exact.load(std::memory_order_relaxed) || p.K <= 32 || p.M == 1 || p.N == 1) return false;
+    return std::min(p.M, p.N) >= 16 && p.M > 0 && p.N > 0 && p.nb0 > 0 && p.nb1 > 0;
+}
+
+// A [M, N] contiguous view of part's first slice, for build_problem (the
+// packet points into this object, which is not copied).
+struct SliceView {
+    int64_t shape[2], strides[2];
+    chelis_gpu_tensor t{};
+    SliceView(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b, void *part) {
+        shape[0] = a->shape[a->rank - 2];
+        shape[1] = b->shape[b->rank - 1];
+        strides[0] = shape[1];
+        strides[1] = 1;
+        t.data = part;
+        t.dtype = a->dtype;
+        t.rank = 2;
+        t.shape = shape;
+        t.strides = strides;
+        t.count = shape[0] * shape[1];
+        t.byte_capacity = t.count * dtype_width(a->dtype);
+    }
+    SliceView(const SliceView &) = delete;
+};
+
 }  // namespace
+
+int64_t matmul_slice_count(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b) {
+    if (!a || !b || a->rank != 2 || b->rank != 2) return 1;
+    // a stand-in address: only the problem's shape is read
+    static int64_t dummy[1];
+    const SliceView c(a, b, dummy);
+    GemmProblem p;
+    if (build_problem(a, b, &c.t, &p, "matmul")) return 1;
+    return takes_mfma(a->dtype, p) ? gemm_mfma_slice_count(a->dtype, p) : 1;
+}
+
+int32_t matmul_slices(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b, void *part, int64_t slices) {
+    if (!a || !b || a->rank != 2 || b->rank != 2)
+        return set_error(CHELIS_HIP_EDOMAIN, "matmul slices: two matrices required");
+    const SliceView c(a, b, part);
+    GemmProblem p;
+    if (int32_t s = build_problem(a, b, &c.t, &p, "matmul")) return s;
+    const int64_t ks = takes_mfma(a->dtype, p) ? gemm_mfma_slice_count(a->dtype, p) : 1;
+    if (ks != slices) return set_error(CHELIS_HIP_EDOMAIN, "matmul slices: %lld slices, not %lld", (long long)ks,
+                                       (long long)slices);
+    if (ks == 1 && !takes_mfma(a->dtype, p)) return dispatch(a->dtype, p, 0);
+    hipStream_t st = stream();
+    if (!st) return set_error(CHELIS_HIP_EHIP, "no HIP device");
+    return gemm_mfma_slices(a->dtype, p, part, st);
+}
 
 int32_t matmul_causal(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b, const chelis_gpu_tensor *c,
                       int32_t mode) {

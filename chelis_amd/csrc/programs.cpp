@@ -270,6 +270,48 @@ extern "C" int32_t chelis_prog_transformer_block(const chelis_gpu_tensor *const 
 }
 
 // ------------------------------------------------------------------ MLP train step
+namespace {
+
+// The step in five launches: x.W1 as raw K slices, the head and the tail
+// of the narrow part (k_mlp.hip), x^T.g_d as raw K slices, and the finish
+// (W1 update from the slices, the tail's join, the other updates, the loss).
+int32_t mlp_fused(const chelis_gpu_tensor *x, const chelis_gpu_tensor *oh, const chelis_gpu_tensor *w1,
+                  const chelis_gpu_tensor *b1, const chelis_gpu_tensor *w2, const chelis_gpu_tensor *b2,
+                  const uint64_t *kdev, const chelis_gpu_tensor *const *out, int64_t Bt, int64_t I, int64_t Hd,
+                  int64_t O, float rate, float lr, hipStream_t st) {
+    const chelis_dtype dt = CHELIS_DTYPE_F32;
+    const Pkt xT(x->data, dt, {I, Bt}, {x->strides[1], x->strides[0]}, x->byte_capacity);
+    Workspace ws(st);
+    const size_t o_d = ws.reserve(Bt * Hd * 4), o_gd = ws.reserve(Bt * Hd * 4), o_gz2 = ws.reserve(Bt * O * 4),
+                 o_nl = ws.reserve(Bt * 4), o_part = ws.reserve(mlp_part_bytes(Bt, Hd));
+    // the slice count reads only shapes: any non-null address stands in for g_d
+    const Pkt gd_probe(x->data, dt, {Bt, Hd});
+    const int64_t ks1 = matmul_slice_count(x, w1), ks2 = matmul_slice_count(&xT.t, &gd_probe.t);
+    const size_t o_z1 = ws.reserve(ks1 * Bt * Hd * 4), o_gw1 = ws.reserve(ks2 * I * Hd * 4);
+    TRY(ws.commit());
+    const Pkt gd(ws.at(o_gd), dt, {Bt, Hd});
+    MlpNarrow m{};
+    m.B = Bt, m.I = I, m.H = Hd, m.O = O;
+    m.z1 = static_cast<const float *>(ws.at(o_z1)), m.z1_slices = ks1;
+    m.gw1 = static_cast<const float *>(ws.at(o_gw1)), m.gw1_slices = ks2;
+    m.w1 = static_cast<const float *>(w1->data), m.w2 = static_cast<const float *>(w2->data);
+    m.b2 = static_cast<const float *>(b2->data), m.onehot = static_cast<const float *>(oh->data);
+    m.b1 = static_cast<const float *>(b1->data), m.key = kdev;
+    m.d = static_cast<float *>(ws.at(o_d)), m.gz2 = static_cast<float *>(ws.at(o_gz2));
+    m.nl = static_cast<float *>(ws.at(o_nl)), m.gd = static_cast<float *>(gd.t.data);
+    m.part = static_cast<float *>(ws.at(o_part));
+    m.w1_out = static_cast<float *>(out[1]->data), m.b1_out = static_cast<float *>(out[2]->data);
+    m.w2_out = static_cast<float *>(out[3]->data), m.b2_out = static_cast<float *>(out[4]->data);
+    m.loss = static_cast<float *>(out[0]->data);
+    m.rate = rate, m.lr = lr;
+    TRY(matmul_slices(x, w1, ws.at(o_z1), ks1));
+    TRY(mlp_head_tail(m, st));
+    TRY(matmul_slices(&xT.t, &gd.t, ws.at(o_gw1), ks2));
+    return mlp_finish(m, st);
+}
+
+}  // namespace
+
 extern "C" int32_t chelis_prog_mlp_train_step(const chelis_gpu_tensor *const *in, int32_t n_in,
                                               const chelis_gpu_tensor *const *out, int32_t n_out) {
     if (n_in != 7 || n_out != 5) return set_error(CHELIS_HIP_EDOMAIN, "mlp_train_step: 7 inputs, 5 outputs");
@@ -292,6 +334,9 @@ extern "C" int32_t chelis_prog_mlp_train_step(const chelis_gpu_tensor *const *in
     const float rate = 0.1f, lr = 0.01f;
     // the dropout kernels read the key from its tensor on the device
     const uint64_t *kdev = static_cast<const uint64_t *>(key->data);
+    if (mlp_narrow_fits(Bt, I, Hd, O) && is_contiguous(oh) && is_contiguous(w1) && is_contiguous(w2) &&
+        is_contiguous(b1) && is_contiguous(b2))
+        return mlp_fused(x, oh, w1, b1, w2, b2, kdev, out, Bt, I, Hd, O, rate, lr, st);
     Workspace ws(st);
     const size_t o_hd = ws.reserve(Bt * Hd * 4), o_d = ws.reserve(Bt * Hd * 4), o_z2 = ws.reserve(Bt * O * 4),
                  o_p = ws.reserve(Bt * O * 4), o_nl = ws.reserve(Bt * 4), o_gp = ws.reserve(Bt * O * 4),
