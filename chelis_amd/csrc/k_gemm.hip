@@ -507,9 +507,9 @@ void launch_mfma(const GemmProblem &p, dim3 grid, int64_t tm, int64_t tn, bool a
 }
 
 // Slices of K for a product whose tiles cannot fill the chip. 64-tiles:
-// enough slices to give every CU about three workgroups, each slice at least
-// 256 deep (a shorter run does not amortize a tile's first loads and its
-// store). (Measured on the skinny f64 8192 x 64 x 4096, 128 64-tiles: 4
+// enough slices to give every CU about three workgroups (binary64; two for
+// binary32), each slice at least 256 deep (128 for binary32; a shorter run
+// does not amortize a tile's first loads and its store). (Measured on the skinny f64 8192 x 64 x 4096, 128 64-tiles: 4
 // slices 109.5 us, 6 slices 102.5 us, 8 slices 113.5 us.) 128-tiles (chosen
 // for fewer than two per CU only when K is long, see run_mfma): two
 // workgroups per CU, each slice at least 1024 deep. At most 16 slices;
@@ -518,7 +518,11 @@ template <typename T, int TM>
 int64_t split_count(const GemmProblem &p, int64_t tiles, int64_t *kchunk) {
     constexpr int64_t BK = Depth<T, TM>::BK;
     const int64_t cus = device_cus();
-    const int64_t per_cu = TM == 2 ? 3 : 2, min_depth = TM == 2 ? 256 : 1024;
+    // 64-tiles, binary32: two workgroups per CU and slices down to 128 deep
+    // (the MLP's 1024 x 512 x 784 product: 4 slices 15.7 us, 3 slices 18.8
+    // us, 6 slices 18.5 us)
+    const int64_t per_cu = TM == 2 ? (sizeof(T) == 4 ? 2 : 3) : 2;
+    const int64_t min_depth = TM == 2 ? (sizeof(T) == 4 ? 128 : 256) : 1024;
     if (p.causal != 0 || tiles >= (TM == 2 ? cus : 2 * cus) || p.K < 2 * min_depth) return 1;
     int64_t ks = (per_cu * cus + tiles - 1) / tiles;
     if (ks > p.K / min_depth) ks = p.K / min_depth;

@@ -100,39 +100,57 @@ __device__ __noinline__ float unit32(uint64_t key, uint64_t index) { return (flo
 __device__ __noinline__ float exp_class(float x) { return expf_cr_nonpos(x); }
 __device__ __noinline__ float log_class(float x) { return leaf_log<float>(x); }
 
-// hd for row b, this lane's run: the slices of x.W1 added in slice order,
-// then the linear epilogue (canon, + b1, relu) as the split-K combine
-// applies it.
+// Raw x.W1 sums for row b, this lane's run, slice by slice: NS > 0 slices
+// read together (every load issued before the first is used); NS = 0, any
+// count, one slice after another into raw[0].
+template <int L, int NS>
+struct RawRun {
+    float v[NS > 0 ? NS : 1][L];
+};
+
 template <int L>
-__device__ inline void hidden_run(const MlpArgs &a, int64_t b, int64_t k0, bool vec, const float (&b1v)[L],
-                                  float (&hv)[L]) {
-    const int64_t H = a.H, slice = a.B * H;
-    const float *row = a.z1 + b * H + k0;
+__device__ inline void load_slice(const MlpArgs &a, const float *row, int64_t k0, bool vec, float (&v)[L]) {
     if (vec) {
 #pragma unroll
         for (int i = 0; i < L; i += 4) {
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (k0 + i < H) v = *reinterpret_cast<const float4 *>(row + i);
-            hv[i] = v.x, hv[i + 1] = v.y, hv[i + 2] = v.z, hv[i + 3] = v.w;
-        }
-        for (int64_t s = 1; s < a.z1_slices; ++s) {
-#pragma unroll
-            for (int i = 0; i < L; i += 4) {
-                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (k0 + i < H) v = *reinterpret_cast<const float4 *>(row + s * slice + i);
-                hv[i] += v.x, hv[i + 1] += v.y, hv[i + 2] += v.z, hv[i + 3] += v.w;
-            }
+            float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (k0 + i < a.H) q = *reinterpret_cast<const float4 *>(row + i);
+            v[i] = q.x, v[i + 1] = q.y, v[i + 2] = q.z, v[i + 3] = q.w;
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < L; ++i) hv[i] = k0 + i < H ? row[i] : 0.f;
-        for (int64_t s = 1; s < a.z1_slices; ++s)
-#pragma unroll
-            for (int i = 0; i < L; ++i) hv[i] += k0 + i < H ? row[s * slice + i] : 0.f;
+        for (int i = 0; i < L; ++i) v[i] = k0 + i < a.H ? row[i] : 0.f;
     }
+}
+
+template <int L, int NS>
+__device__ inline void load_raw(const MlpArgs &a, int64_t b, int64_t k0, bool vec, RawRun<L, NS> &r) {
+    const float *row = a.z1 + b * a.H + k0;
+    const int64_t slice = a.B * a.H;
+    if constexpr (NS > 0) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) load_slice<L>(a, row + s * slice, k0, vec, r.v[s]);
+    } else {
+        load_slice<L>(a, row, k0, vec, r.v[0]);
+        for (int64_t s = 1; s < a.z1_slices; ++s) {
+            float t[L];
+            load_slice<L>(a, row + s * slice, k0, vec, t);
+#pragma unroll
+            for (int i = 0; i < L; ++i) r.v[0][i] += t[i];
+        }
+    }
+}
+
+// hd: the slices added in slice order, then the linear epilogue (canon,
+// + b1, relu) as the split-K combine applies it.
+template <int L, int NS>
+__device__ inline void hidden_run(const RawRun<L, NS> &r, const float (&b1v)[L], float (&hv)[L]) {
 #pragma unroll
     for (int i = 0; i < L; ++i) {
-        const float v = canon(canon(hv[i]) + b1v[i]);
+        float acc = r.v[0][i];
+#pragma unroll
+        for (int s = 1; s < NS; ++s) acc += r.v[s][i];
+        const float v = canon(canon(acc) + b1v[i]);
         hv[i] = v < 0.f ? 0.f : v;
     }
 }
@@ -153,7 +171,7 @@ __device__ inline void store_run(float *row, int64_t H, int64_t k0, bool vec, co
 // One wave per batch row; lane l holds hidden units [l L, l L + L). The
 // per-class steps (exp, log, the quotients) run once per class: class c in
 // lane c of each 16-lane row, its row sums by row16_tree_sum.
-template <int L>
+template <int L, int NS>
 __global__ __launch_bounds__(256) void mlp_head_kernel(MlpArgs a) {
     // W2 transposed as [class][i][lane]: hidden unit l L + i of class c at
     // c 64 L + i 64 + l, so a wave's reads of one (c, i) are 64 consecutive
@@ -167,8 +185,13 @@ __global__ __launch_bounds__(256) void mlp_head_kernel(MlpArgs a) {
     const int64_t k0 = (int64_t)lane * L;
     const bool vec = a.vec && L >= 4;
     int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    // set-up loads together: b1 for this lane's run, the key, this thread's
-    // W2 values, b2
+    // set-up loads together: the first row's slices and one-hot entry (a
+    // clamped row: no branch), b1 for this lane's run, the key, this
+    // thread's W2 values, b2
+    RawRun<L, NS> raw;
+    const int64_t b_first = b < a.B ? b : a.B - 1;
+    load_raw<L, NS>(a, b_first, k0, vec, raw);
+    float ohv = a.oh[b_first * O + (cl < O ? cl : 0)];
     const BufRead b1b(a.b1, H * 4), w2b(a.w2, H * O * 4), b2b(a.b2, O * 4);
     float b1v[L];
 #pragma unroll
@@ -198,9 +221,8 @@ __global__ __launch_bounds__(256) void mlp_head_kernel(MlpArgs a) {
     __syncthreads();
 #pragma unroll 1
     for (; b < a.B; b += (int64_t)gridDim.x * 4) {
-        const float ohv = a.oh[b * O + (cl < O ? cl : 0)];
         float hv[L];
-        hidden_run<L>(a, b, k0, vec, b1v, hv);
+        hidden_run<L, NS>(raw, b1v, hv);
         const float ohc = cl < O ? ohv : 0.f;
         // dropout: mask and d for this lane's run
         float dv[L];
@@ -268,6 +290,11 @@ __global__ __launch_bounds__(256) void mlp_head_kernel(MlpArgs a) {
             gv[i] = 0.f < hv[i] ? r : 0.f;
         }
         store_run<L>(a.gd + b * H, H, k0, vec, gv);
+        const int64_t bn = b + (int64_t)gridDim.x * 4;
+        if (bn < a.B) {
+            load_raw<L, NS>(a, bn, k0, vec, raw);
+            ohv = a.oh[bn * O + (cl < O ? cl : 0)];
+        }
     }
 }
 
@@ -275,7 +302,8 @@ __global__ __launch_bounds__(256) void mlp_head_kernel(MlpArgs a) {
 // Groups 0 .. G-2 hold hidden units [64 g, 64 g + 64) on the lanes with
 // O + 1 outputs each (d^T.g_z2 per class, then sum g_d), the waves taking
 // every fourth output; group G-1 holds sum g_z2 (lane c < O) and sum nl
-// (lane O). Block totals go to part[g][output][lane][rb].
+// (lane O). Block totals go to part[g][rb][output][lane] (a wave's stores
+// and the join's loads run along the lanes).
 __global__ __launch_bounds__(256) void mlp_tail_kernel(MlpArgs a) {
     __shared__ float gzs[64][kOuts];
     __shared__ float tile[2][64][64];  // d and g_d rows of this block, this group's columns
@@ -347,7 +375,7 @@ __global__ __launch_bounds__(256) void mlp_tail_kernel(MlpArgs a) {
             }
             q[h] = reg_tree<16>(t);
         }
-        part[((int64_t)j * 64 + lane) * blocks + rb] = (q[0] + q[1]) + (q[2] + q[3]);
+        part[(rb * kOuts + j) * 64 + lane] = (q[0] + q[1]) + (q[2] + q[3]);
     }
 }
 
@@ -391,6 +419,7 @@ __device__ inline float stack_total(const float (&lv)[LV], int64_t n) {
 // complete tree, the runs joined by a carry stack) and apply SGD to W2, b1,
 // b2 and write the loss; the rest update W1 from the slices of x^T.g_d,
 // four elements per thread.
+template <int NS>
 __global__ __launch_bounds__(256) void mlp_finish_kernel(MlpArgs a, int groups) {
     const int O = a.O;
     if ((int)blockIdx.x >= groups) {
@@ -398,10 +427,21 @@ __global__ __launch_bounds__(256) void mlp_finish_kernel(MlpArgs a, int groups) 
         const int64_t e0 = ((int64_t)(blockIdx.x - groups) * 256 + threadIdx.x) * 4;
         if (e0 >= n) return;
         if (e0 + 4 <= n && a.vec) {
-            float4 g = *reinterpret_cast<const float4 *>(a.gw1 + e0);
-            for (int64_t s = 1; s < a.gw1_slices; ++s) {
-                const float4 v = *reinterpret_cast<const float4 *>(a.gw1 + s * slice + e0);
-                g.x += v.x, g.y += v.y, g.z += v.z, g.w += v.w;
+            // NS > 0: the slices read together, then added in slice order
+            float4 g;
+            if constexpr (NS > 0) {
+                float4 v[NS];
+#pragma unroll
+                for (int s = 0; s < NS; ++s) v[s] = *reinterpret_cast<const float4 *>(a.gw1 + s * slice + e0);
+                g = v[0];
+#pragma unroll
+                for (int s = 1; s < NS; ++s) g.x += v[s].x, g.y += v[s].y, g.z += v[s].z, g.w += v[s].w;
+            } else {
+                g = *reinterpret_cast<const float4 *>(a.gw1 + e0);
+                for (int64_t s = 1; s < a.gw1_slices; ++s) {
+                    const float4 v = *reinterpret_cast<const float4 *>(a.gw1 + s * slice + e0);
+                    g.x += v.x, g.y += v.y, g.z += v.z, g.w += v.w;
+                }
             }
             const float4 w = *reinterpret_cast<const float4 *>(a.w1 + e0);
             float4 o;
@@ -424,7 +464,7 @@ __global__ __launch_bounds__(256) void mlp_finish_kernel(MlpArgs a, int groups) 
     const int outs = extra ? 1 : O + 1;
     const int64_t blocks = a.blocks;
     const float *part = a.part + (int64_t)g * kOuts * 64 * blocks;
-    const BufRead w2b(a.w2, a.H * O * 4), b1b(a.b1, a.H * 4), b2b(a.b2, O * 4), pb(part, outs * 64 * blocks * 4);
+    const BufRead w2b(a.w2, a.H * O * 4), b1b(a.b1, a.H * 4), b2b(a.b2, O * 4), pb(part, kOuts * 64 * blocks * 4);
     float prm[5];
 #pragma unroll
     for (int u = 0; u < 5; ++u) {
@@ -444,7 +484,7 @@ __global__ __launch_bounds__(256) void mlp_finish_kernel(MlpArgs a, int groups) 
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const bool ok = e < outs * 64 && q0 + i < blocks;
-                const float x = pb[ok ? (int64_t)e * blocks + q0 + i : 0];
+                const float x = pb[ok ? (q0 + i) * kOuts * 64 + e : 0];
                 v[u][i] = ok ? x : -0.0f;
             }
         }
@@ -472,7 +512,13 @@ __global__ __launch_bounds__(256) void mlp_finish_kernel(MlpArgs a, int groups) 
 template <int L>
 void launch_head(const MlpArgs &a, hipStream_t st) {
     const int64_t blocks = std::min<int64_t>((a.B + 3) / 4, 4 * (int64_t)std::max(device_cus(), 1));
-    mlp_head_kernel<L><<<(unsigned)blocks, 256, 0, st>>>(a);
+    switch (a.z1_slices) {
+        case 1: mlp_head_kernel<L, 1><<<(unsigned)blocks, 256, 0, st>>>(a); break;
+        case 2: mlp_head_kernel<L, 2><<<(unsigned)blocks, 256, 0, st>>>(a); break;
+        case 3: mlp_head_kernel<L, 3><<<(unsigned)blocks, 256, 0, st>>>(a); break;
+        case 4: mlp_head_kernel<L, 4><<<(unsigned)blocks, 256, 0, st>>>(a); break;
+        default: mlp_head_kernel<L, 0><<<(unsigned)blocks, 256, 0, st>>>(a); break;
+    }
 }
 
 // Hidden units per lane in the head: the power of two that covers H with
@@ -540,7 +586,16 @@ int32_t mlp_finish(const MlpNarrow &m, hipStream_t st) {
     const MlpArgs a = make_args(m);
     const int groups = (int)((m.H + 63) / 64 + 1);
     const int64_t w1_blocks = (m.I * m.H + 1023) / 1024;
-    mlp_finish_kernel<<<(unsigned)(groups + w1_blocks), 256, 0, st>>>(a, groups);
+    const unsigned grid = (unsigned)(groups + w1_blocks);
+    switch (m.gw1_slices) {
+        case 1: mlp_finish_kernel<1><<<grid, 256, 0, st>>>(a, groups); break;
+        case 2: mlp_finish_kernel<2><<<grid, 256, 0, st>>>(a, groups); break;
+        case 3: mlp_finish_kernel<3><<<grid, 256, 0, st>>>(a, groups); break;
+        case 4: mlp_finish_kernel<4><<<grid, 256, 0, st>>>(a, groups); break;
+        case 5: mlp_finish_kernel<5><<<grid, 256, 0, st>>>(a, groups); break;
+        case 6: mlp_finish_kernel<6><<<grid, 256, 0, st>>>(a, groups); break;
+        default: mlp_finish_kernel<0><<<grid, 256, 0, st>>>(a, groups); break;
+    }
     CHELIS_LAUNCH_CHECK();
     return CHELIS_HIP_OK;
 }

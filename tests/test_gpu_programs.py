@@ -113,6 +113,33 @@ def test_mlp_train_step_config5(exact):
         assert err <= 1e-5, (name, err)
 
 
+@pytest.mark.parametrize("B,I,H,O_", [
+    (1, 8, 5, 1),         # one row, one class, a partial lane run
+    (100, 50, 70, 3),     # ragged row blocks, H past one 64-unit group, scalar rows (H % 4 != 0)
+    (65, 33, 1024, 16),   # the widest fused head (16 units per lane, 16 classes)
+    (130, 40, 96, 7),     # three row blocks
+    (64, 16, 1100, 4),    # H past the fused head: the unfused launches
+    (64, 16, 64, 17),     # 17 classes: the unfused launches
+])
+def test_mlp_train_step_shapes_bit_exact(B, I, H, O_):
+    """Under the exact flag every launch of the step is a canonical-tree or
+    correctly rounded primitive, so each output is bit-identical to the C
+    oracle; biases are nonzero here so the bias steps are checked too."""
+    x, onehot, w1, b1, w2, b2 = mlp_inputs(B, I, H, O_)
+    b1 = np.random.default_rng(44).standard_normal(H).astype(np.float32) * 0.1
+    b2 = np.random.default_rng(45).standard_normal(O_).astype(np.float32) * 0.1
+    args = (x, onehot, w1, b1, w2, b2)
+    ref = O.mlp_train_step(*args, 7, np.float32(0.1), np.float32(0.01))
+    prev = C.set_exact_matmul(True)
+    try:
+        got = run_mlp(args, 7)
+    finally:
+        C.set_exact_matmul(prev)
+    for g, r, name in zip(got, ref, ("loss", "w1", "b1", "w2", "b2")):
+        assert np.array_equal(np.asarray(g, np.float32).view(np.uint32),
+                              np.asarray(r, np.float32).view(np.uint32)), (name, normwise(g, r))
+
+
 def test_mlp_train_step_updates_match_in_exact_mode():
     """The parameter deltas w' - w (lr * gradient) agree to 1e-5 relative
     normwise on every parameter, a much tighter check than on w' itself."""
