@@ -186,7 +186,8 @@ def bench_programs(C, H, steps, warmup):
     ms = time_launches(C, H, lambda i: C.program("mlp_train_step", mins, mouts), steps, warmup)
     out["mlp_train_step_f32_1024x784x512x10"] = {
         "us": round(ms * 1e3, 2), "TFLOP/s": round(MLP_FLOPS / (ms * 1e-3) / 1e12, 3),
-        "bound": "launch latency (21 small launches)"}
+        "frac_mfma": round(MLP_FLOPS / (ms * 1e-3) / 1e12 / PEAK_TFLOPS["f32"], 4),
+        "bound": "launch latency (5 launches: two split-K products, head, tail, finish)"}
     return out, (X, w, y), (x, p), args
 
 

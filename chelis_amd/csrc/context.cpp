@@ -124,35 +124,6 @@ int32_t *status_words(int32_t **host) {
     return g_status[device];
 }
 
-// ---- arrival counters -----------------------------------------------------
-// kArrivalCounters uint32 words per device, allocated and cleared once, kept
-// until the process ends. A kernel whose workgroups finish with "the last
-// one to arrive joins the partial results" counts arrivals in them; the last
-// arrival sets its counter back to zero, so every launch finds them clear.
-// Launches on the library stream run one after another, so they share the
-// words.
-namespace {
-std::mutex g_arrival_mutex;
-uint32_t *g_arrival[kMaxDevices] = {};
-}  // namespace
-
-uint32_t *arrival_counters() {
-    int device = 0;
-    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) return nullptr;
-    std::lock_guard<std::mutex> lock(g_arrival_mutex);
-    if (!g_arrival[device]) {
-        uint32_t *d = nullptr;
-        const size_t bytes = kArrivalCounters * sizeof(uint32_t);
-        if (hipMalloc(&d, bytes) != hipSuccess) return nullptr;
-        if (hipMemset(d, 0, bytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
-            (void)hipFree(d);
-            return nullptr;
-        }
-        g_arrival[device] = d;
-    }
-    return g_arrival[device];
-}
-
 int device_cus() {
     int device = 0;
     if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) return 0;

@@ -23,11 +23,6 @@ int device_cus();
 // receives a pinned host word for reading one back): [0] synchronous error
 // codes, [1] the deferred trap channel. Null when the device has none.
 int32_t *status_words(int32_t **host);
-// The current device's arrival counters (kArrivalCounters zeroed uint32
-// words in device memory, each returned to zero by the kernel that uses it;
-// last_arrival below). Null when the device has none.
-constexpr int64_t kArrivalCounters = 16384;
-uint32_t *arrival_counters();
 // Scratch device memory for work enqueued on the current device's library
 // stream: blocks are recycled in stream order (a freed block's earlier users
 // are already enqueued ahead of any later user) and cached for reuse, so
@@ -132,28 +127,6 @@ __device__ inline double read_lane(double v, int lane) {
     const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, lane);
     const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), lane);
     return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
-}
-
-// True in every thread of the workgroup that is the last of `expected`
-// workgroups to call it with this counter. Each thread's earlier global
-// writes are released (agent-scope fence) before its workgroup counts
-// itself, and the last workgroup acquires before it returns, so it reads
-// every other workgroup's results; it also sets the counter back to zero
-// for the next launch. Every thread of the workgroup must call it; no
-// workgroup waits on another.
-__device__ inline bool last_arrival(uint32_t *counter, uint32_t expected) {
-    __shared__ uint32_t arrived;
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t prev = atomicAdd(counter, 1u);
-        if (prev == expected - 1) atomicExch(counter, 0u);
-        arrived = prev;
-    }
-    __syncthreads();
-    const bool last = arrived == expected - 1;
-    if (last) __threadfence();
-    return last;
 }
 
 // Canonical tree sum of one value per lane (lane order = leaf order); every
