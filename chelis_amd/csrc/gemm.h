@@ -7,6 +7,8 @@
 
 namespace chelis {
 
+constexpr int kMaxBatchPtrs = 4;
+
 // One contraction c[z][m][n] = sum_k a[z][m][k] * b[z][k][n] over a batch of
 // up to two axes (z = z0 * nb1 + z1). Strides are in elements; every view
 // is already validated against its byte capacity on the host.
@@ -29,6 +31,13 @@ struct GemmProblem {
     // they were; 2 = a[m][k] is zero for k > m, the contraction of a row
     // tile stops after its last row.
     int32_t causal;
+    // Batches whose B operand and bias sit at unrelated addresses (the Q, K
+    // and V weights): nbz > 0 makes batch z read B at bz[z] and its bias at
+    // biasz[z] (each with batch 0's strides). Only the MFMA tiles take such
+    // a problem (linear_multi_b).
+    int32_t nbz;
+    const void *bz[kMaxBatchPtrs];
+    const void *biasz[kMaxBatchPtrs];
 };
 
 // Epilogue of one output element, each step finalized at the dtype so the
@@ -39,7 +48,8 @@ struct GemmProblem {
 template <typename T, bool GELU = true>
 __device__ inline T gemm_epilogue(T acc, const GemmProblem &p, int64_t z0, int64_t z1, int64_t m, int64_t n) {
     T v = canon(acc);
-    if (p.bias) v = canon(v + static_cast<const T *>(p.bias)[z0 * p.sbias0 + z1 * p.sbias1 + n * p.sbias]);
+    const T *bias = static_cast<const T *>(p.nbz ? p.biasz[z0 * p.nb1 + z1] : p.bias);
+    if (bias) v = canon(v + bias[(p.nbz ? 0 : z0 * p.sbias0 + z1 * p.sbias1) + n * p.sbias]);
     if (p.act == CHELIS_ACT_RELU) v = v < T(0) ? T(0) : v;
     else if (GELU && p.act == CHELIS_ACT_GELU) v = gelu_one<T>(v);
     if (p.resid) v = canon(static_cast<const T *>(p.resid)[z0 * p.sr0 + z1 * p.sr1 + m * p.srm + n * p.srn] + v);
@@ -51,6 +61,12 @@ int32_t gemm_mfma(chelis_dtype dt, const GemmProblem &p, hipStream_t st);
 // no combine; one slice when the product is not split), and their count.
 int64_t gemm_mfma_slice_count(chelis_dtype dt, const GemmProblem &p);
 int32_t gemm_mfma_slices(chelis_dtype dt, const GemmProblem &p, void *part, hipStream_t st);
+// c[i] = a . b[i] + bias[i] (i < n <= kMaxBatchPtrs; the b[i] alike in
+// shape and strides, c a [n, M, N] block): one batched MFMA launch over the
+// n weights where they sit, or n linear launches where the dispatch takes
+// another kernel.
+int32_t linear_multi_b(const chelis_gpu_tensor *a, const chelis_gpu_tensor *const *b,
+                       const chelis_gpu_tensor *const *bias, int32_t n, const chelis_gpu_tensor *c);
 // c = a . b of two matrices as raw K slices for a consumer that sums them
 // in slice order itself (then finalizes: canon, epilogue): part holds
 // matmul_slice_count(a, b) contiguous [M, N] slices. Whatever the dispatch

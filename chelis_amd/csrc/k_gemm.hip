@@ -245,7 +245,7 @@ __global__ __launch_bounds__(THREADS, kMinWavesPerEu<T>) void gemm_mfma_kernel(G
     const int64_t z = blockIdx.y;
     const int64_t z0 = z / p.nb1, z1 = z % p.nb1;
     const T *A = static_cast<const T *>(p.a) + z0 * p.sa0 + z1 * p.sa1;
-    const T *B = static_cast<const T *>(p.b) + z0 * p.sb0 + z1 * p.sb1;
+    const T *B = p.nbz ? static_cast<const T *>(p.bz[z]) : static_cast<const T *>(p.b) + z0 * p.sb0 + z1 * p.sb1;
     if (kchunk > 0) {
         const int64_t kb = (int64_t)blockIdx.z * kchunk;
         K = (K - kb < kchunk ? K - kb : kchunk);

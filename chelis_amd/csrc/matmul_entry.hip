@@ -214,6 +214,51 @@ struct SliceView {
 
 }  // namespace
 
+int32_t linear_multi_b(const chelis_gpu_tensor *a, const chelis_gpu_tensor *const *b,
+                       const chelis_gpu_tensor *const *bias, int32_t n, const chelis_gpu_tensor *c) {
+    if (n < 1 || n > kMaxBatchPtrs || !a || !b || !bias || !c || a->rank != 2 || c->rank != 3 || c->shape[0] != n)
+        return set_error(CHELIS_HIP_EDOMAIN, "linear_multi_b: a [M,K], n <= %d weights, c [n,M,N]", kMaxBatchPtrs);
+    bool same = true;
+    for (int32_t i = 0; i < n; ++i) {
+        if (int32_t s = check_tensor(b[i], "b")) return s;
+        if (int32_t s = check_tensor(bias[i], "bias")) return s;
+        same = same && b[i]->rank == 2 && same_shape(b[i], b[0]) && b[i]->strides[0] == b[0]->strides[0] &&
+               b[i]->strides[1] == b[0]->strides[1] && b[i]->dtype == a->dtype && bias[i]->rank == 1 &&
+               bias[i]->dtype == a->dtype && bias[i]->shape[0] == b[0]->shape[1] &&
+               bias[i]->strides[0] == bias[0]->strides[0] &&
+               (reinterpret_cast<uintptr_t>(b[i]->data) & 15) == (reinterpret_cast<uintptr_t>(b[0]->data) & 15);
+    }
+    if (!same) return set_error(CHELIS_HIP_EDOMAIN, "linear_multi_b: weights and biases must match in shape and strides");
+    // the batch view of a (stride 0) and of the first weight; the problem
+    // then reads weight and bias i at their own addresses
+    const int64_t a_sh[3] = {n, a->shape[0], a->shape[1]}, a_st[3] = {0, a->strides[0], a->strides[1]};
+    const int64_t b_sh[3] = {n, b[0]->shape[0], b[0]->shape[1]}, b_st[3] = {0, b[0]->strides[0], b[0]->strides[1]};
+    chelis_gpu_tensor a3 = *a, b3 = *b[0];
+    a3.rank = 3, a3.shape = a_sh, a3.strides = a_st, a3.count = n * a->count;
+    b3.rank = 3, b3.shape = b_sh, b3.strides = b_st, b3.count = n * b[0]->count;
+    GemmProblem p;
+    if (int32_t s = build_problem(&a3, &b3, c, &p, "linear")) return s;
+    if (!takes_mfma(a->dtype, p)) {
+        // one launch per weight, each into its slice of c
+        for (int32_t i = 0; i < n; ++i) {
+            const int64_t sh[2] = {c->shape[1], c->shape[2]}, st[2] = {c->strides[1], c->strides[2]};
+            chelis_gpu_tensor ci = *c;
+            ci.data = static_cast<char *>(c->data) + i * c->strides[0] * dtype_width(c->dtype);
+            ci.rank = 2, ci.shape = sh, ci.strides = st, ci.count = sh[0] * sh[1];
+            ci.byte_capacity = c->byte_capacity - i * c->strides[0] * dtype_width(c->dtype);
+            if (int32_t s = chelis_hip_linear(a, b[i], bias[i], CHELIS_ACT_NONE, nullptr, &ci, 0)) return s;
+        }
+        return CHELIS_HIP_OK;
+    }
+    p.nbz = n;
+    for (int32_t i = 0; i < n; ++i) p.bz[i] = b[i]->data, p.biasz[i] = bias[i]->data;
+    p.bias = bias[0]->data;
+    p.sbias = bias[0]->strides[0];
+    hipStream_t st = stream();
+    if (!st) return set_error(CHELIS_HIP_EHIP, "no HIP device");
+    return gemm_mfma(a->dtype, p, st);
+}
+
 int64_t matmul_slice_count(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b) {
     if (!a || !b || a->rank != 2 || b->rank != 2) return 1;
     // a stand-in address: only the problem's shape is read

@@ -202,21 +202,17 @@ extern "C" int32_t chelis_prog_transformer_block(const chelis_gpu_tensor *const 
     hipStream_t st = stream();
     if (!st) return set_error(CHELIS_HIP_EHIP, "no HIP device");
     const int64_t w = dtype_width(dt);
-    // The Q, K and V projections run as one batch of three products: their
-    // weights and biases are packed side by side (12 MB at d_model 1024) so
-    // the batch has constant strides, and the three results land in one
-    // [3, B*S, D] block (measured at [4096,1024] x [1024,1024]: 255 us for
-    // the batch of three on 128-tiles against 3 x 90 us).
-    const bool pack = is_contiguous(P[2]) && is_contiguous(P[4]) && is_contiguous(P[6]) && is_contiguous(P[3]) &&
-                      is_contiguous(P[5]) && is_contiguous(P[7]);
+    // The Q, K and V projections run as one batch of three products that
+    // reads each weight and bias where it sits, the three results landing
+    // in one [3, B*S, D] block (measured at [4096,1024] x [1024,1024]: 255
+    // us for the batch of three on 128-tiles against 3 x 90 us).
     // attention as one fused launch where it applies (binary32, seq a
     // multiple of 64), else scores, causal softmax and P.V
     const bool fused = dt == CHELIS_DTYPE_F32 && S % 64 == 0;
     Workspace ws(st);
     const size_t o_h = ws.reserve(R * D * w), o_qkv = ws.reserve(3 * R * D * w),
                  o_s = ws.reserve(fused ? 0 : B * H * S * S * w),
-                 o_o = ws.reserve(R * D * w), o_x1 = ws.reserve(R * D * w), o_f = ws.reserve(R * F * w),
-                 o_w = ws.reserve(pack ? 3 * D * D * w : 0), o_b = ws.reserve(pack ? 3 * D * w : 0);
+                 o_o = ws.reserve(R * D * w), o_x1 = ws.reserve(R * D * w), o_f = ws.reserve(R * F * w);
     TRY(ws.commit());
     const Pkt x2(x->data, dt, {R, D}, {x->strides[1], x->strides[2]}, x->byte_capacity);
     char *qkv = static_cast<char *>(ws.at(o_qkv));
@@ -235,19 +231,10 @@ extern "C" int32_t chelis_prog_transformer_block(const chelis_gpu_tensor *const 
         return set_error(CHELIS_HIP_EUNSUPPORTED, "transformer_block: batch and seq axes of x/y must collapse");
     // attention
     TRY(chelis_hip_layer_norm(&x2, P[0], P[1], 1e-5, &h));
-    if (pack) {
-        char *wp = static_cast<char *>(ws.at(o_w)), *bp = static_cast<char *>(ws.at(o_b));
-        for (int j = 0; j < 3; ++j) {
-            CHELIS_HIP_TRY(hipMemcpyAsync(wp + j * D * D * w, P[2 + 2 * j]->data, D * D * w, hipMemcpyDeviceToDevice, st));
-            CHELIS_HIP_TRY(hipMemcpyAsync(bp + j * D * w, P[3 + 2 * j]->data, D * w, hipMemcpyDeviceToDevice, st));
-        }
-        const Pkt h3(h.t.data, dt, {3, R, D}, {0, D, 1}, R * D * w);
-        const Pkt w3(wp, dt, {3, D, D}), b3(bp, dt, {3, D}), qkv3(qkv, dt, {3, R, D});
-        TRY(chelis_hip_linear(&h3, &w3, &b3, CHELIS_ACT_NONE, nullptr, &qkv3, 0));
-    } else {
-        TRY(chelis_hip_linear(&h, P[2], P[3], CHELIS_ACT_NONE, nullptr, &q, 0));
-        TRY(chelis_hip_linear(&h, P[4], P[5], CHELIS_ACT_NONE, nullptr, &k, 0));
-        TRY(chelis_hip_linear(&h, P[6], P[7], CHELIS_ACT_NONE, nullptr, &v, 0));
+    {
+        const chelis_gpu_tensor *wqkv[3] = {P[2], P[4], P[6]}, *bqkv[3] = {P[3], P[5], P[7]};
+        const Pkt qkv3(qkv, dt, {3, R, D});
+        TRY(linear_multi_b(&h.t, wqkv, bqkv, 3, &qkv3.t));
     }
     const Pkt kh(k.t.data, dt, {B, H, S, DH}, {S * D, DH, D, 1}, cap);
     if (fused && attention_causal_fits(&qh.t, &kh.t, &vh.t, &oh.t)) {
