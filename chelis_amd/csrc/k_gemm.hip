@@ -451,17 +451,40 @@ __global__ __launch_bounds__(THREADS, kMinWavesPerEu<T>) void gemm_mfma_kernel(G
 }
 
 // c[z][m][n] = epilogue(sum over slices s, in order, of part[s][z][m][n]).
+// Four consecutive columns per thread; tpr (a power of two, at most 256)
+// threads per row cover its first 4 tpr columns, 256 / tpr rows per
+// workgroup, and grid y steps over further runs of 1024 columns. The slices
+// are read as vectors when N is a multiple of four (each slice row then
+// starts aligned), and no thread divides per element.
 template <typename T>
-__global__ __launch_bounds__(256) void splitk_combine_kernel(GemmProblem p, const T *part, int ks, int64_t nz) {
-    const int64_t mn = p.M * p.N, total = nz * mn;
-    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
-        T v = part[e];
-        for (int s = 1; s < ks; ++s) v += part[s * total + e];
-        const int64_t z = e / mn, r = e - z * mn;
-        const int64_t m = r / p.N, n = r - m * p.N;
-        const int64_t z0 = z / p.nb1, z1 = z % p.nb1;
-        static_cast<T *>(p.c)[z0 * p.sc0 + z1 * p.sc1 + m * p.scm + n * p.scn] = gemm_epilogue<T>(v, p, z0, z1, m, n);
+__global__ __launch_bounds__(256) void splitk_combine_kernel(GemmProblem p, const T *part, int ks, int64_t nz,
+                                                             int tpr) {
+    const int64_t row = (int64_t)blockIdx.x * (256 / tpr) + threadIdx.x / tpr;
+    const int64_t n0 = (int64_t)blockIdx.y * 1024 + (threadIdx.x % tpr) * 4;
+    if (row >= nz * p.M || n0 >= p.N) return;
+    const int64_t z = row / p.M, m = row - z * p.M, total = nz * p.M * p.N;
+    const int64_t z0 = z / p.nb1, z1 = z % p.nb1;
+    const T *src = part + row * p.N + n0;
+    T v[4];
+    if (p.N % 4 == 0) {
+        using V4 = typename std::conditional<sizeof(T) == 4, float4, double4>::type;
+        V4 q = *reinterpret_cast<const V4 *>(src);
+        v[0] = q.x, v[1] = q.y, v[2] = q.z, v[3] = q.w;
+        for (int s = 1; s < ks; ++s) {
+            q = *reinterpret_cast<const V4 *>(src + s * total);
+            v[0] += q.x, v[1] += q.y, v[2] += q.z, v[3] += q.w;
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = n0 + u < p.N ? src[u] : T(0);
+        for (int s = 1; s < ks; ++s)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] += n0 + u < p.N ? src[s * total + u] : T(0);
     }
+    T *C = static_cast<T *>(p.c) + z0 * p.sc0 + z1 * p.sc1 + m * p.scm;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+        if (n0 + u < p.N) C[(n0 + u) * p.scn] = gemm_epilogue<T>(v[u], p, z0, z1, m, n0 + u);
 }
 
 template <typename T>
@@ -579,9 +602,14 @@ int32_t run_tiles(const GemmProblem &p, int al, int bl, bool av, bool bv, hipStr
         default: launch_mfma<T, 2, 2, TM>(p, grid, tm, tn, av, bv, part, kchunk, st); break;
     }
     if (ks > 1 && !ext_part) {
-        unsigned g = grid_for(nz * p.M * p.N, 256);
-        if (g > 65536u) g = 65536u;  // the combine loops over the rest
-        splitk_combine_kernel<T><<<g, 256, 0, st>>>(p, part, (int)ks, nz);
+        int tpr = 1;
+        while (tpr < 256 && 4 * tpr < p.N) tpr <<= 1;
+        const int64_t rows = nz * p.M, blocks = (rows + 256 / tpr - 1) / (256 / tpr), cols = (p.N + 1023) / 1024;
+        if (!grid_fits(blocks, 256) || cols > 65535) {
+            scratch_free(part, part_bytes);
+            return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: split-K combine grid too large");
+        }
+        splitk_combine_kernel<T><<<dim3((unsigned)blocks, (unsigned)cols), 256, 0, st>>>(p, part, (int)ks, nz, tpr);
         scratch_free(part, part_bytes);
     }
     CHELIS_LAUNCH_CHECK();
