@@ -64,6 +64,8 @@ template <> __device__ inline float leaf_log<float>(float v) {
     y = cr_exception(y, b, 0x6f31a8ecu, 0x42845a89u);
     return canon(y);
 }
+// expf_cr's correctly rounded core for the arguments its fast path flags.
+__device__ __noinline__ inline float expf_slow_cr(float v) { return expf_cr_dd(v); }
 __device__ __noinline__ inline float erfc_slow32(float v) {
     const float y = cr_exception((float)erfc((double)v), f32_bits(v), 0xb76c9f62u, 0x3f800085u);
     return canon(y);
@@ -107,10 +109,20 @@ template <> struct PhiK<double> {
 // finite or infinite arguments are not NaN; m * phi is +-inf * 1 or
 // -0 * 0 at the infinities), and a NaN x makes the product NaN, which the
 // final step canonicalizes.
-template <typename T>
-__device__ inline T gelu_one(T x) {
+//
+// gelu_one_t reads the binary32 erfc and exp tables through `tb`
+// (ErfcTablesConst or ErfcTablesLds, same bits); binary64 uses none.
+template <typename T, class Tabs>
+__device__ inline T gelu_one_t(T x, const Tabs &tb) {
     const T c = PhiK<T>::c, cl = PhiK<T>::cl, k = PhiK<T>::k, s = PhiK<T>::s;
-    const T e = leaf_erfc<T>(-x * c);
+    T e;
+    if constexpr (sizeof(T) == 4) {
+        bool slow;
+        e = erfcf_fast_t(-x * c, slow, tb);
+        if (slow) e = erfc_slow32(-x * c);
+    } else {
+        e = leaf_erfc<T>(-x * c);
+    }
     const T z = (fabs(x) < T(64)) ? x : T(0);
     const T a = -z;
     const T th = a * c;
@@ -125,12 +137,36 @@ __device__ inline T gelu_one(T x) {
     t = t + al * ch;
     t = t + al * cr;
     const T tl = t + a * cl;
-    const T g = leaf_exp<T>(-(th * th));
+    T g;
+    if constexpr (sizeof(T) == 4) {
+        bool slow;
+        g = expf_fast(-(th * th), tb, slow);
+        if (slow) g = expf_slow_cr(-(th * th));
+    } else {
+        g = leaf_exp<T>(-(th * th));
+    }
     const T corr = (k * g) * tl;
     const T phi = T(0.5) * (e - corr);
     const T m = (x < Lim<T>::lowest()) ? T(-0.0) : x;
     return canon(m * phi);
 }
+
+template <typename T>
+__device__ inline T gelu_one(T x) {
+    return gelu_one_t<T>(x, ErfcTablesConst{});
+}
+
+// A workgroup's copy of the binary32 erfc and exp tables in LDS; every
+// thread calls it, and the caller's next barrier publishes the copy.
+struct ErfcLdsStore {
+    double bt[35][10];
+    double et[64];
+    __device__ void fill() {
+        for (int i = threadIdx.x; i < 35 * 10; i += blockDim.x) bt[i / 10][i % 10] = chelis_erfcx_b[i / 10][i % 10];
+        for (int i = threadIdx.x; i < 64; i += blockDim.x) et[i] = chelis_exp2_64_tab[i][0];
+    }
+    __device__ ErfcTablesLds tabs() const { return ErfcTablesLds{bt, et}; }
+};
 
 // ---------------------------------------------------------------- chain ops
 struct ChainDev {

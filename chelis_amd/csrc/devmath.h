@@ -241,7 +241,14 @@ CHELIS_HD inline float quot_f32(float v, double inv) { return (float)((double)v 
 // +0 (erfc(10.1) is below 2^-150, half the least subnormal), and +inf and
 // -inf fall in those ranges. Checked against CORE-MATH over every binary32
 // input (tests/test_devmath.py).
-CHELIS_HD inline float erfcf_fast(float xf, bool &slow) {
+// erfcf_fast_t reads the erfcx coefficients B[i][d] and 2^(j/64) through
+// `tb`: ErfcTablesConst (below) reads the constant-memory tables; a kernel
+// that evaluates many erfc per lane stages the same values in LDS and passes
+// an accessor reading them there (a per-lane index into constant memory is a
+// vector memory load per coefficient: GELU over 16.7M binary32 values 82-85
+// us from constant memory, 65-72 us from LDS, same bits).
+template <class Tabs>
+CHELIS_HD inline float erfcf_fast_t(float xf, bool &slow, const Tabs &tb) {
     const double x = (double)xf;
     const double ax = fabs(x);
     const double s = x * x;  // exact
@@ -252,10 +259,10 @@ CHELIS_HD inline float erfcf_fast(float xf, bool &slow) {
     const double ya = fma(-x, pa, 1.0);
     int i = (int)((ax - 0.5) * 4.0);
     i = i < 0 ? 0 : (i > 34 ? 34 : i);
-    const double tb = (ax - (0.5 + 0.25 * i)) * 8.0 - 1.0;  // exact
-    double g = chelis_erfcx_b[i][9];
+    const double tv = (ax - (0.5 + 0.25 * i)) * 8.0 - 1.0;  // exact
+    double g = tb.b(i, 9);
 #pragma unroll
-    for (int d = 8; d >= 0; --d) g = fma(g, tb, chelis_erfcx_b[i][d]);
+    for (int d = 8; d >= 0; --d) g = fma(g, tv, tb.b(i, d));
     // exp(-s), -s = k ln2/64 + r, |k| < 2^11
     const double shifted = fma(-s, CHELIS_INV_LN2_64, 0x1.8p52);
     const double kd = shifted - 0x1.8p52;
@@ -267,7 +274,7 @@ CHELIS_HD inline float erfcf_fast(float xf, bool &slow) {
     p = fma(p, r, 0.5);
     p = fma(p, r, 1.0);
     p = fma(p, r, 1.0);
-    const double e = ldexp(chelis_exp2_64_tab[k & 63][0] * p, (k - (k & 63)) / 64);
+    const double e = ldexp(tb.e(k & 63) * p, (k - (k & 63)) / 64);
     const double yb = e * g;
     double y = ax < 0.5 ? ya : (x > 0.0 ? yb : 2.0 - yb);
     y = x <= -4.5 ? 2.0 : (x >= 10.1 ? 0.0 : y);
@@ -275,6 +282,24 @@ CHELIS_HD inline float erfcf_fast(float xf, bool &slow) {
     slow = (x != x) || (x >= 9.1 && x < 10.1) || below < 1024u;
     return (float)y;
 }
+
+// The constant-memory tables (also the 2^(j/64) accessor of expf_fast).
+struct ErfcTablesConst {
+    CHELIS_HD double b(int i, int d) const { return chelis_erfcx_b[i][d]; }
+    CHELIS_HD double e(int j) const { return chelis_exp2_64_tab[j][0]; }
+    CHELIS_HD double operator()(int j) const { return chelis_exp2_64_tab[j][0]; }
+};
+
+// The same values staged in LDS (stage_erfc_tables).
+struct ErfcTablesLds {
+    const double (*bt)[10];
+    const double *et;
+    CHELIS_HD double b(int i, int d) const { return bt[i][d]; }
+    CHELIS_HD double e(int j) const { return et[j]; }
+    CHELIS_HD double operator()(int j) const { return et[j]; }
+};
+
+CHELIS_HD inline float erfcf_fast(float xf, bool &slow) { return erfcf_fast_t(xf, slow, ErfcTablesConst{}); }
 
 // ------------------------------------------------------------ binary64 exp
 //

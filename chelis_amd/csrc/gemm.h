@@ -45,13 +45,14 @@ struct GemmProblem {
 // GELU = false instances serve launches whose activation is not GELU: a
 // kernel that holds many outputs per lane would otherwise carry the GELU
 // graph's registers (and code) through its whole main loop.
-template <typename T, bool GELU = true>
-__device__ inline T gemm_epilogue(T acc, const GemmProblem &p, int64_t z0, int64_t z1, int64_t m, int64_t n) {
+template <typename T, bool GELU = true, class Tabs = ErfcTablesConst>
+__device__ inline T gemm_epilogue(T acc, const GemmProblem &p, int64_t z0, int64_t z1, int64_t m, int64_t n,
+                                  const Tabs &tb = Tabs{}) {
     T v = canon(acc);
     const T *bias = static_cast<const T *>(p.nbz ? p.biasz[z0 * p.nb1 + z1] : p.bias);
     if (bias) v = canon(v + bias[(p.nbz ? 0 : z0 * p.sbias0 + z1 * p.sbias1) + n * p.sbias]);
     if (p.act == CHELIS_ACT_RELU) v = v < T(0) ? T(0) : v;
-    else if (GELU && p.act == CHELIS_ACT_GELU) v = gelu_one<T>(v);
+    else if (GELU && p.act == CHELIS_ACT_GELU) v = gelu_one_t<T>(v, tb);
     if (p.resid) v = canon(static_cast<const T *>(p.resid)[z0 * p.sr0 + z1 * p.sr1 + m * p.srm + n * p.srn] + v);
     return v;
 }

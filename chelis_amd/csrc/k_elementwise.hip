@@ -269,10 +269,10 @@ struct UnaryArgs {
     double inv_keep;          // dropout, binary32: 1 / (double)(1 - (float)rate), set by the kernel
 };
 
-template <typename T, Unary OP>
-__device__ inline T unary_one(T x, T g, int64_t i, const UnaryArgs &u) {
+template <typename T, Unary OP, class Tabs = ErfcTablesConst>
+__device__ inline T unary_one(T x, T g, int64_t i, const UnaryArgs &u, const Tabs &tb = Tabs{}) {
     if constexpr (OP == Unary::Gelu) {
-        return gelu_one<T>(x);
+        return gelu_one_t<T>(x, tb);
     } else if constexpr (OP == Unary::Relu) {
         return x < T(0) ? T(0) : x;
     } else if constexpr (OP == Unary::ReluAdjoint) {
@@ -300,26 +300,37 @@ __global__ __launch_bounds__(256) void unary_kernel(const T *__restrict__ x, con
     if constexpr (OP == Unary::Dropout || OP == Unary::Uniform)
         if (u.key_dev) u.key = *u.key_dev;
     if constexpr (OP == Unary::Dropout) u.inv_keep = 1.0 / (double)(T(1) - (T)u.p0);
-    using V = Vec16<T>;
-    const int64_t nv = n / V::V;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; v < nv; v += stride) {
-        typename V::type xv{}, gv{}, yv;
-        if constexpr (OP != Unary::Uniform) xv = reinterpret_cast<const typename V::type *>(x)[v];
-        if constexpr (OP == Unary::ReluAdjoint) gv = reinterpret_cast<const typename V::type *>(g)[v];
-        const T *xe = reinterpret_cast<const T *>(&xv);
-        const T *ge = reinterpret_cast<const T *>(&gv);
-        T *ye = reinterpret_cast<T *>(&yv);
+    // binary32 GELU reads its erfc and exp tables from LDS
+    auto run = [&](const auto &tb) {
+        using V = Vec16<T>;
+        const int64_t nv = n / V::V;
+        const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+        for (int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; v < nv; v += stride) {
+            typename V::type xv{}, gv{}, yv;
+            if constexpr (OP != Unary::Uniform) xv = reinterpret_cast<const typename V::type *>(x)[v];
+            if constexpr (OP == Unary::ReluAdjoint) gv = reinterpret_cast<const typename V::type *>(g)[v];
+            const T *xe = reinterpret_cast<const T *>(&xv);
+            const T *ge = reinterpret_cast<const T *>(&gv);
+            T *ye = reinterpret_cast<T *>(&yv);
 #pragma unroll
-        for (int i = 0; i < V::V; ++i) ye[i] = unary_one<T, OP>(xe[i], ge[i], v * V::V + i, u);
-        reinterpret_cast<typename V::type *>(y)[v] = yv;
-    }
-    // tail
-    const int64_t t = nv * V::V + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t < n) {
-        const T xe = (OP != Unary::Uniform) ? x[t] : T(0);
-        const T ge = (OP == Unary::ReluAdjoint) ? g[t] : T(0);
-        y[t] = unary_one<T, OP>(xe, ge, t, u);
+            for (int i = 0; i < V::V; ++i) ye[i] = unary_one<T, OP>(xe[i], ge[i], v * V::V + i, u, tb);
+            reinterpret_cast<typename V::type *>(y)[v] = yv;
+        }
+        // tail
+        const int64_t t = nv * V::V + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+        if (t < n) {
+            const T xe = (OP != Unary::Uniform) ? x[t] : T(0);
+            const T ge = (OP == Unary::ReluAdjoint) ? g[t] : T(0);
+            y[t] = unary_one<T, OP>(xe, ge, t, u, tb);
+        }
+    };
+    if constexpr (OP == Unary::Gelu && sizeof(T) == 4) {
+        __shared__ ErfcLdsStore gtab;
+        gtab.fill();
+        __syncthreads();
+        run(gtab.tabs());
+    } else {
+        run(ErfcTablesConst{});
     }
 }
 

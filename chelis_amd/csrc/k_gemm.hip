@@ -413,6 +413,11 @@ __global__ __launch_bounds__(THREADS, kMinWavesPerEu<T>) void gemm_mfma_kernel(G
         constexpr int QR = BM / 4, LDT = BN + 8;
         static_assert(QR * LDT <= 2 * BM * LD, "quarter tile fits in As");
         T *tile = &As[0][0];
+        // the erfc and exp tables in LDS for the epilogue's GELU (published
+        // by the first quarter's barrier)
+        __shared__ ErfcLdsStore gtab;
+        gtab.fill();
+        const ErfcTablesLds tb = gtab.tabs();
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             __syncthreads();  // As: the main loop's (or the last quarter's) reads are done
@@ -432,7 +437,7 @@ __global__ __launch_bounds__(THREADS, kMinWavesPerEu<T>) void gemm_mfma_kernel(G
                 const int row = e / BN, col = e % BN;
                 const int64_t m = m0 + q * QR + row, n = n0 + col;
                 if (m < p.M && n < p.N)
-                    C[m * p.scm + n * p.scn] = gemm_epilogue<T, true>(tile[row * LDT + col], p, z0, z1, m, n);
+                    C[m * p.scm + n * p.scn] = gemm_epilogue<T, true>(tile[row * LDT + col], p, z0, z1, m, n, tb);
             }
         }
         return;
