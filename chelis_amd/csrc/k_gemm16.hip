@@ -43,13 +43,22 @@ __device__ inline f32x4 mfma16(uint4 a, uint4 b, f32x4 c) {
 
 constexpr int THREADS = 256, BM = 128, BN = 128, BK = 64, LD = 72;
 
-// One operand tile [ROWS][BK] staged in registers, 8 values per 16-byte
-// vector: LAY 0 = vectors along K, 1 = vectors along the outer axis (M of
-// A, N of B; transposed into LDS by the store), 2 = element by element.
+// One operand tile [ROWS][BK] staged in registers: LAY 0 = vectors along K,
+// 8 values per 16-byte vector, stored as they are; 2 = element by element.
+// LAY 1 = vectors along the outer axis (M of A, N of B), which LDS wants
+// K-contiguous: thread t owns the 4 x 8 block of outer rows 4 nb + e (e < 4)
+// and k = 8 kb + u (u < 8), nb = t % 4 + 4 (t / 32), kb = (t / 4) % 8. It
+// reads one 8-byte vector of 4 rows per k, transposes the block in
+// registers (one byte permute per output word) and writes one 16-byte
+// vector of 8 k per row: with the 144-byte row pitch, 16 consecutive lanes
+// write 16 distinct 4-bank groups (rows 4 nb + e, columns 8 kb), where the
+// former element-by-element 2-byte stores took 32 LDS writes per thread.
 template <int LAY, int ROWS>
 struct Stage16 {
     static constexpr int NV = ROWS * BK / 8 / THREADS;
-    uint4 r[NV];
+    static_assert(LAY != 1 || ROWS * BK == 32 * THREADS, "one 4 x 8 block per thread");
+    uint4 r[LAY == 1 ? 1 : NV];
+    uint2 q[LAY == 1 ? 8 : 1];
 
     // element (row, k) at base[row * s_row + k * s_k]; CHECK = false: the
     // whole tile is inside the operand and the vectors are aligned.
@@ -57,51 +66,65 @@ struct Stage16 {
     __device__ void load(const uint16_t *__restrict__ base, int64_t s_row, int64_t s_k, int64_t row0, int64_t rows,
                          int64_t k0, int64_t K) {
         const int t = threadIdx.x;
+        if constexpr (LAY == 1) {
+            const int nb = t % 4 + 4 * (t / 32), kb = (t / 4) % 8;
+            const int64_t gr = row0 + 4 * nb;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int64_t gk = k0 + 8 * kb + u;
+                const uint16_t *p = base + gr + gk * s_k;
+                if (!CHECK || (gk < K && gr + 4 <= rows)) {
+                    q[u] = *reinterpret_cast<const uint2 *>(p);
+                } else {
+                    uint16_t e[4];
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) e[w] = (gk < K && gr + w < rows) ? p[w * s_row] : (uint16_t)0;
+                    q[u] = __builtin_bit_cast(uint2, e);
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             const int idx = t + THREADS * j;
-            if constexpr (LAY == 0 || LAY == 2) {
-                const int row = idx / (BK / 8), kv = (idx % (BK / 8)) * 8;
-                const int64_t gr = row0 + row, gk = k0 + kv;
-                const uint16_t *p = base + gr * s_row + gk * s_k;
-                if (LAY == 0 && (!CHECK || (gr < rows && gk + 8 <= K))) {
-                    r[j] = *reinterpret_cast<const uint4 *>(p);
-                } else {
-                    uint16_t e[8];
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) e[u] = (gr < rows && gk + u < K) ? p[u * s_k] : (uint16_t)0;
-                    r[j] = __builtin_bit_cast(uint4, e);
-                }
+            const int row = idx / (BK / 8), kv = (idx % (BK / 8)) * 8;
+            const int64_t gr = row0 + row, gk = k0 + kv;
+            const uint16_t *p = base + gr * s_row + gk * s_k;
+            if (LAY == 0 && (!CHECK || (gr < rows && gk + 8 <= K))) {
+                r[j] = *reinterpret_cast<const uint4 *>(p);
             } else {
-                const int k = idx % BK, rv = (idx / BK) * 8;
-                const int64_t gr = row0 + rv, gk = k0 + k;
-                const uint16_t *p = base + gr * s_row + gk * s_k;
-                if (!CHECK || (gk < K && gr + 8 <= rows)) {
-                    r[j] = *reinterpret_cast<const uint4 *>(p);
-                } else {
-                    uint16_t e[8];
+                uint16_t e[8];
 #pragma unroll
-                    for (int u = 0; u < 8; ++u) e[u] = (gk < K && gr + u < rows) ? p[u * s_row] : (uint16_t)0;
-                    r[j] = __builtin_bit_cast(uint4, e);
-                }
+                for (int u = 0; u < 8; ++u) e[u] = (gr < rows && gk + u < K) ? p[u * s_k] : (uint16_t)0;
+                r[j] = __builtin_bit_cast(uint4, e);
             }
         }
     }
 
     __device__ void store(uint16_t *lds) const {
         const int t = threadIdx.x;
+        if constexpr (LAY == 1) {
+            const int nb = t % 4 + 4 * (t / 32), kb = (t / 4) % 8;
+            // output row e, word w: k = 2w in the low half, 2w + 1 in the high
+            uint32_t w[4][4];
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const uint32_t a0 = q[2 * h].x, a1 = q[2 * h].y, b0 = q[2 * h + 1].x, b1 = q[2 * h + 1].y;
+                w[0][h] = (a0 & 0xffffu) | (b0 << 16);
+                w[1][h] = (a0 >> 16) | (b0 & 0xffff0000u);
+                w[2][h] = (a1 & 0xffffu) | (b1 << 16);
+                w[3][h] = (a1 >> 16) | (b1 & 0xffff0000u);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                *reinterpret_cast<uint4 *>(lds + (4 * nb + e) * LD + 8 * kb) = uint4{w[e][0], w[e][1], w[e][2], w[e][3]};
+            return;
+        }
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             const int idx = t + THREADS * j;
-            if constexpr (LAY == 0 || LAY == 2) {
-                const int row = idx / (BK / 8), kv = (idx % (BK / 8)) * 8;
-                *reinterpret_cast<uint4 *>(lds + row * LD + kv) = r[j];
-            } else {
-                const int k = idx % BK, rv = (idx / BK) * 8;
-                const uint16_t *e = reinterpret_cast<const uint16_t *>(&r[j]);
-#pragma unroll
-                for (int u = 0; u < 8; ++u) lds[(rv + u) * LD + k] = e[u];
-            }
+            const int row = idx / (BK / 8), kv = (idx % (BK / 8)) * 8;
+            *reinterpret_cast<uint4 *>(lds + row * LD + kv) = r[j];
         }
     }
 };
