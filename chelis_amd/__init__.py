@@ -131,6 +131,7 @@ SIGNATURES = {
     "transformer_block_device": (None, [POINTER(c_void_p), c_int32, POINTER(c_void_p), c_int32]),
     "mlp_train_step_device": (None, [POINTER(c_void_p), c_int32, POINTER(c_void_p), c_int32]),
     "chelis_hip_set_exact_matmul": (c_int32, [c_int32]),
+    "chelis_hip_set_exact": (c_int32, [c_int32]),
     # chelis_dag.h
     "chelis_dag_compile": (c_void_p, [ctypes.c_char_p, c_int64]),
     "chelis_dag_release": (None, [c_void_p]),
@@ -558,7 +559,15 @@ def host_entry(name: str, arrays, n_out: int):
     return result
 
 
+def set_exact(on: bool) -> bool:
+    """The library-wide exact mode (chelis_hip_set_exact): matmuls on the
+    canonical-tree kernels and binary64 softmax rows with the correctly
+    rounded exp, bit-identical to the C lane. Returns the previous mode."""
+    return bool(lib().chelis_hip_set_exact(1 if on else 0))
+
+
 def set_exact_matmul(on: bool) -> bool:
+    """The same switch under its first name (chelis_hip_set_exact_matmul)."""
     return bool(lib().chelis_hip_set_exact_matmul(1 if on else 0))
 
 

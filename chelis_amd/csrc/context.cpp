@@ -8,6 +8,7 @@
 // hipLaunchKernel on that stream.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -215,11 +216,21 @@ bool row_view(const chelis_gpu_tensor *t, RowView *v) {
     return true;
 }
 
+namespace {
+std::atomic<int32_t> g_exact_mode{0};
+}  // namespace
+
+bool exact_mode() { return g_exact_mode.load(std::memory_order_relaxed) != 0; }
+
 }  // namespace chelis
 
 extern "C" {
 
 const char *chelis_hip_last_error(void) { return chelis::g_error; }
+
+int32_t chelis_hip_set_exact(int32_t on) { return chelis::g_exact_mode.exchange(on ? 1 : 0); }
+
+int32_t chelis_hip_set_exact_matmul(int32_t on) { return chelis_hip_set_exact(on); }
 
 void *chelis_hip_stream(void) { return (void *)chelis::stream(); }
 

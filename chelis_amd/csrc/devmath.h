@@ -548,4 +548,34 @@ CHELIS_HD inline double exp_cr(double x) {
     return slow ? exp_cr_slow(x) : y;
 }
 
+// Binary64 exp of an argument <= 0 or NaN, faithful rather than correctly
+// rounded, for the default binary64 softmax row. One binary64 evaluation,
+// branch free:
+//   exp(x) = 2^m T[j] exp(r),  x = (64m + j) ln2/64 + r,  |r| <= ln2/128,
+// r reduced with the two-part ln2/64 as in expf_fast; expm1(r) as its
+// degree-5 Taylor polynomial r c(r) (omitted r^6/6!: below 2^-54.6);
+// y = fma(T_hi, r c, T_hi), T_hi the binary64 rounding of 2^(j/64). On the
+// normal range the error is below 0.5 ulp (the final rounding) plus
+// 1.4 * 2^-53 relative (T_hi, the truncation, the Horner roundings), so
+// under 2 ulp; below 2^-1022 ldexp rounds once into the subnormal grid.
+// x < -746 (-inf included) is raised to -746, whose exp rounds to +0; a NaN
+// fails the comparison and propagates (k & 63 stays in range).
+// `tab(j)` supplies T_hi[j]. Checked against CORE-MATH on the host
+// (tests/test_devmath.py).
+template <class Tab1>
+CHELIS_HD inline double exp_nonpos_faithful(double x, const Tab1 &tab) {
+    const double xc = x < -746.0 ? -746.0 : x;
+    const double shifted = fma(xc, CHELIS_INV_LN2_64, 0x1.8p52);
+    const double kd = shifted - 0x1.8p52;
+    const int k = (int)(uint32_t)f64_bits(shifted);
+    double r = fma(-kd, CHELIS_LN2_64_HI, xc);
+    r = fma(-kd, CHELIS_LN2_64_LO, r);
+    double c = fma(r, 0x1.1111111111111p-7, 0x1.5555555555555p-5);  // 1/5!, 1/4!
+    c = fma(r, c, 0x1.5555555555555p-3);                               // 1/3!
+    c = fma(r, c, 0.5);
+    c = fma(r, c, 1.0);
+    const double th = tab(k & 63);
+    return ldexp(fma(th, r * c, th), k >> 6);
+}
+
 }  // namespace chelis

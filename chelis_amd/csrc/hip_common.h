@@ -17,6 +17,13 @@ namespace chelis {
 // ---- host side ---------------------------------------------------------
 int32_t set_error(int32_t status, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 hipStream_t stream();
+// The library-wide exact mode (chelis_hip_set_exact): when set, every
+// launcher that has the C lane's primitive for its result uses it (matmuls
+// on the canonical-tree kernels, binary64 softmax rows with the correctly
+// rounded exp and the IEEE division), so results are bit-identical to the
+// C lane's; when clear, the default MFMA products and faithful binary64
+// softmax rows, within the stated tolerances.
+bool exact_mode();
 // Compute units of the current device (cached per device; 256 on MI355X).
 int device_cus();
 // The current device's two status words (device memory; *host, when given,

@@ -98,6 +98,8 @@ struct Exp2TableLds {
         h = e.x;
         l = e.y;
     }
+    // the high part alone (the faithful exp)
+    __device__ double operator()(int j) const { return t[j].x; }
 };
 
 // The exp table of each dtype, built before the row loads so waiting for it
@@ -324,7 +326,9 @@ __device__ inline T softmax_arg(T raw, int64_t j, int64_t qi, int masked, T scal
 
 // One row: v holds the raw row (padding -inf) on entry and the softmax on
 // exit; xr is the row in memory (re-read only by the rare exp fallback).
-template <typename T, int V, int S, int W, int R>
+// FAITHFUL (binary64 only): the faithful exp and one reciprocal per row in
+// place of the correctly rounded exp and the IEEE division.
+template <typename T, int V, int S, int W, int R, bool FAITHFUL = false>
 __device__ inline void softmax_row(T (&v)[S][V], const T *__restrict__ xr, int64_t row, int64_t n, int masked,
                                    T scale, int64_t q_len, T *lds, const RowCoord<W, R> &c,
                                    const typename RowExpTab<T>::type &tab) {
@@ -391,6 +395,39 @@ __device__ inline void softmax_row(T (&v)[S][V], const T *__restrict__ xr, int64
 #pragma unroll
                 for (int i = 0; i < V; ++i) v[s][i] = quot_f32(v[s][i], inv);
         }
+    } else if constexpr (FAITHFUL) {
+        // the default binary64 row: exp(x - m) faithful (within 1 ulp, no
+        // fallback pass), the canonical tree total, then e * (1 / total):
+        // within a few ulps of the correctly rounded quotients. A NaN
+        // argument yields a NaN exp, hence a NaN total and every output the
+        // canonical NaN, as in the exact row.
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int i = 0; i < V; ++i) v[s][i] = exp_nonpos_faithful(v[s][i] - m, tab);
+        if (!full) {
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+#pragma unroll
+                for (int i = 0; i < V; ++i) {
+                    const int64_t j = (int64_t)s * SEG + (int64_t)c.tid_in_row * V + i;
+                    if (j >= n) v[s][i] = T(-0.0);
+                }
+        }
+        const T total = row_tree_sum<T, V, S, W, R>(v, lds, c);
+        if (total != total) {
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+#pragma unroll
+                for (int i = 0; i < V; ++i) v[s][i] = canon(total);
+        } else {
+            // 1 <= total <= n: every product is finite
+            const T inv = T(1) / total;
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+#pragma unroll
+                for (int i = 0; i < V; ++i) v[s][i] = v[s][i] * inv;
+        }
     } else {
         // exp(x - m) in place, as for binary32: the binary64 fast path for
         // every element (2^(j/64) as a double-double from the lane-held
@@ -435,8 +472,9 @@ __device__ inline void softmax_row(T (&v)[S][V], const T *__restrict__ xr, int64
 // softmax over the last axis, optionally of where(j <= i, x * scale, -inf)
 // (causal != 0, q_len = rows per score matrix). DENSE instances serve the
 // common case (no mask, row length equal to the register capacity S*64W*V,
-// 16-byte aligned rows) with every bound test folded away.
-template <typename T, int V, int S, int W, int R, bool DENSE>
+// 16-byte aligned rows) with every bound test folded away. FAITHFUL as for
+// softmax_row.
+template <typename T, int V, int S, int W, int R, bool DENSE, bool FAITHFUL = false>
 __global__ __launch_bounds__(64 * W * R) void softmax_kernel(const T *__restrict__ x, T *__restrict__ y,
                                                               int64_t rows, int64_t n_arg, int64_t ldx, int64_t ldy,
                                                               bool vec_ok_arg, int masked_arg, T scale,
@@ -460,7 +498,7 @@ __global__ __launch_bounds__(64 * W * R) void softmax_kernel(const T *__restrict
     // -inf whatever it holds, which is the padding value
     const int64_t n_load = masked == 1 ? (c.row % q_len + 1 < n ? c.row % q_len + 1 : n) : n;
     load_row<T, V, S, W>(xr, n_load, vec_ok, c.tid_in_row, neg_inf<T>(), v);
-    softmax_row<T, V, S, W, R>(v, xr, c.row, n, masked, scale, q_len, lds, c, tab);
+    softmax_row<T, V, S, W, R, FAITHFUL>(v, xr, c.row, n, masked, scale, q_len, lds, c, tab);
     store_row<T, V, S, W>(y + c.row * ldy, n, vec_ok, c.tid_in_row, v);
 }
 
@@ -553,14 +591,31 @@ int32_t launch_shape(RowOp op, const RowArgs &a, hipStream_t st) {
                                                        (long long)a.rows);
     const dim3 block(64 * W * R);
     switch (op) {
-        case RowOp::Softmax:
-            if (!a.masked && a.vec_ok && a.n == (int64_t)S * 64 * W * V)
+        case RowOp::Softmax: {
+            const bool dense = !a.masked && a.vec_ok && a.n == (int64_t)S * 64 * W * V;
+            // binary64 outside the exact mode: the faithful row
+            if constexpr (sizeof(T) == 8) {
+                if (!exact_mode()) {
+                    if (dense)
+                        softmax_kernel<T, V, S, W, R, true, true><<<grid, block, 0, st>>>(
+                            (const T *)a.a, (T *)a.out, a.rows, a.n, a.lda, a.ldo, a.vec_ok, a.masked, (T)a.scale,
+                            a.q_len);
+                    else
+                        softmax_kernel<T, V, S, W, R, false, true><<<grid, block, 0, st>>>(
+                            (const T *)a.a, (T *)a.out, a.rows, a.n, a.lda, a.ldo, a.vec_ok, a.masked, (T)a.scale,
+                            a.q_len);
+                    break;
+                }
+            }
+            if (dense) {
                 softmax_kernel<T, V, S, W, R, true><<<grid, block, 0, st>>>(
                     (const T *)a.a, (T *)a.out, a.rows, a.n, a.lda, a.ldo, a.vec_ok, a.masked, (T)a.scale, a.q_len);
-            else
+            } else {
                 softmax_kernel<T, V, S, W, R, false><<<grid, block, 0, st>>>(
                     (const T *)a.a, (T *)a.out, a.rows, a.n, a.lda, a.ldo, a.vec_ok, a.masked, (T)a.scale, a.q_len);
+            }
             break;
+        }
         case RowOp::SoftmaxAdjoint:
             softmax_adjoint_kernel<T, V, S, W, R><<<grid, block, 0, st>>>(
                 (const T *)a.a, (const T *)a.b, (T *)a.out, a.rows, a.n, a.lda, a.ldb, a.ldo, a.vec_ok);

@@ -20,14 +20,9 @@
 #include "gemm.h"
 
 #include <algorithm>
-#include <atomic>
-
-#include "chelis_programs.h"
 
 namespace chelis {
 namespace {
-
-std::atomic<int32_t> g_exact{0};
 
 struct Mat {
     int64_t rows, cols, srow, scol;  // the trailing 2-D view
@@ -159,7 +154,7 @@ int32_t dispatch(chelis_dtype dt, const GemmProblem &p, int32_t flags) {
     hipStream_t st = stream();
     if (!st) return set_error(CHELIS_HIP_EHIP, "no HIP device");
     if (p.M == 0 || p.N == 0 || p.nb0 == 0 || p.nb1 == 0) return CHELIS_HIP_OK;
-    if (g_exact.load(std::memory_order_relaxed)) flags |= CHELIS_MATMUL_EXACT;
+    if (exact_mode()) flags |= CHELIS_MATMUL_EXACT;
     if (is_narrow16(dt)) {
         if ((flags & CHELIS_MATMUL_EXACT) || p.K == 0) return dispatch_narrow_exact(dt, p, st);
         return gemm_mfma16(dt, p, st);
@@ -187,7 +182,7 @@ int32_t dispatch(chelis_dtype dt, const GemmProblem &p, int32_t flags) {
 // True when dispatch sends p to the MFMA tiles.
 bool takes_mfma(chelis_dtype dt, const GemmProblem &p) {
     if (is_narrow16(dt) || (dt != CHELIS_DTYPE_F32 && dt != CHELIS_DTYPE_F64)) return false;
-    if (g_exact.load(std::memory_order_relaxed) || p.K <= 32 || p.M == 1 || p.N == 1) return false;
+    if (exact_mode() || p.K <= 32 || p.M == 1 || p.N == 1) return false;
     return std::min(p.M, p.N) >= 16 && p.M > 0 && p.N > 0 && p.nb0 > 0 && p.nb1 > 0;
 }
 
@@ -296,7 +291,6 @@ int32_t matmul_causal(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b, co
 
 using namespace chelis;
 
-extern "C" int32_t chelis_hip_set_exact_matmul(int32_t on) { return g_exact.exchange(on ? 1 : 0); }
 
 extern "C" int32_t chelis_hip_matmul(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b,
                                      const chelis_gpu_tensor *c, int32_t flags) {

@@ -43,6 +43,17 @@ void *chelis_hip_stream(void);
 int32_t chelis_hip_synchronize(void);
 /* Build identification: "gfx950 <git-describe>" style string. */
 const char *chelis_hip_build_info(void);
+/* Library-wide exact mode (no reference counterpart: the reference has one
+ * numeric contract per lane). Non-zero: every result whose primitive the C
+ * lane defines bit for bit is computed that way - matmuls (programs
+ * included) on the canonical-tree kernels, binary64 softmax rows with the
+ * correctly rounded exp and the IEEE division - so results are
+ * bit-identical to the C lane (crates/chelis-backend-c). Zero (default):
+ * MFMA products and binary64 softmax rows with a faithful exp (within
+ * 1 ulp) and one reciprocal per row, within the stated tolerances, as the
+ * reference HIP lane's device exp and division are. Affects launches
+ * enqueued after the call; returns the previous mode. */
+int32_t chelis_hip_set_exact(int32_t on);
 
 /* ---- row regions (last axis; rows contiguous) ----
  * softmax: spec/05 section 4.2 as one region (max_reduce, sub, exp, sum, div),

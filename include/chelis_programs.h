@@ -61,10 +61,11 @@ int32_t chelis_prog_transformer_block(const chelis_gpu_tensor *const *inputs, in
 int32_t chelis_prog_mlp_train_step(const chelis_gpu_tensor *const *inputs, int32_t n_in,
                                    const chelis_gpu_tensor *const *outputs, int32_t n_out);
 
-/* Library-wide matmul mode: non-zero routes every matmul (programs
- * included) through the canonical-tree kernels, so whole programs are
- * bit-exact with the C lane except for leaves that are not correctly
- * rounded on the device (f64 exp, log, erfc). Returns the previous mode. */
+/* The exact mode of chelis_hip_set_exact (chelis_hip.h) under its first
+ * name: non-zero routes every matmul (programs included) through the
+ * canonical-tree kernels, so whole programs are bit-exact with the C lane
+ * except for leaves that are not correctly rounded on the device (binary64
+ * log, erfc, tanh). Returns the previous mode. */
 int32_t chelis_hip_set_exact_matmul(int32_t on);
 
 #ifdef __cplusplus

@@ -50,6 +50,24 @@ def test_exp_f64_matches_core_math(tmp_path):
     assert err <= -73.7, r.stdout
 
 
+def test_exp_f64_nonpos_faithful_within_one_ulp(tmp_path):
+    """The default binary64 softmax row's exp (exp_nonpos_faithful): over
+    2 * 10^7 seeded arguments <= 0 it stays within 1 ulp of CORE-MATH's
+    correctly rounded result (1 unit of the least subnormal below 2^-1022),
+    and 0, -inf, -746 and NaN give 1, +0, +0 and NaN."""
+    O.build()
+    exe = tmp_path / "exp64_faithful_check"
+    ref = os.path.join(ROOT, "oracle", "_ref")
+    subprocess.run(["g++", "-O2", "-ffp-contract=off", "-fno-fast-math", "-fopenmp", "-std=c++17", "-o", str(exe),
+                    os.path.join(ROOT, "tests", "cpu", "exp64_faithful_check.cpp"), f"-L{ref}", "-lcrmath_ref",
+                    f"-Wl,-rpath,{ref}"], check=True)
+    r = subprocess.run([str(exe), "20000000", "11"], capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stdout + r.stderr
+    ulp = float(r.stdout.split("max-ulp ")[1].split()[0])
+    sub = float(r.stdout.split("max-subnormal-units ")[1].split()[0])
+    assert ulp <= 1.0 and sub <= 1.0, r.stdout
+
+
 def test_erfcf_fast_path_matches_core_math_on_every_binary32(tmp_path):
     """The binary32 erfc fast path: every input it does not flag gives
     CORE-MATH's bits (the flagged ones take the fallback, which the device
