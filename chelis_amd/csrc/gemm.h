@@ -45,16 +45,26 @@ struct GemmProblem {
 // GELU = false instances serve launches whose activation is not GELU: a
 // kernel that holds many outputs per lane would otherwise carry the GELU
 // graph's registers (and code) through its whole main loop.
+// The epilogue's arithmetic on values already loaded (b: the bias element,
+// r: the residual element, each used only when the problem has it).
+template <typename T, bool GELU = true, class Tabs = ErfcTablesConst>
+__device__ inline T epilogue_values(T acc, const GemmProblem &p, bool has_bias, T b, T r,
+                                    const Tabs &tb = Tabs{}) {
+    T v = canon(acc);
+    if (has_bias) v = canon(v + b);
+    if (p.act == CHELIS_ACT_RELU) v = v < T(0) ? T(0) : v;
+    else if (GELU && p.act == CHELIS_ACT_GELU) v = gelu_one_t<T>(v, tb);
+    if (p.resid) v = canon(r + v);
+    return v;
+}
+
 template <typename T, bool GELU = true, class Tabs = ErfcTablesConst>
 __device__ inline T gemm_epilogue(T acc, const GemmProblem &p, int64_t z0, int64_t z1, int64_t m, int64_t n,
                                   const Tabs &tb = Tabs{}) {
-    T v = canon(acc);
     const T *bias = static_cast<const T *>(p.nbz ? p.biasz[z0 * p.nb1 + z1] : p.bias);
-    if (bias) v = canon(v + bias[(p.nbz ? 0 : z0 * p.sbias0 + z1 * p.sbias1) + n * p.sbias]);
-    if (p.act == CHELIS_ACT_RELU) v = v < T(0) ? T(0) : v;
-    else if (GELU && p.act == CHELIS_ACT_GELU) v = gelu_one_t<T>(v, tb);
-    if (p.resid) v = canon(static_cast<const T *>(p.resid)[z0 * p.sr0 + z1 * p.sr1 + m * p.srm + n * p.srn] + v);
-    return v;
+    const T b = bias ? bias[(p.nbz ? 0 : z0 * p.sbias0 + z1 * p.sbias1) + n * p.sbias] : T(0);
+    const T r = p.resid ? static_cast<const T *>(p.resid)[z0 * p.sr0 + z1 * p.sr1 + m * p.srm + n * p.srn] : T(0);
+    return epilogue_values<T, GELU>(acc, p, bias != nullptr, b, r, tb);
 }
 
 int32_t gemm_mfma(chelis_dtype dt, const GemmProblem &p, hipStream_t st);

@@ -460,8 +460,11 @@ __global__ __launch_bounds__(THREADS, kMinWavesPerEu<T>) void gemm_mfma_kernel(G
 // threads per row cover its first 4 tpr columns, 256 / tpr rows per
 // workgroup, and grid y steps over further runs of 1024 columns. The slices
 // are read as vectors when N is a multiple of four (each slice row then
-// starts aligned), and no thread divides per element.
-template <typename T>
+// starts aligned), and no thread divides per element. VEC (N a multiple of
+// four; output, residual and an unbatched-pointer bias contiguous along n
+// and 16-byte aligned at every row): the bias, residual and output as
+// vectors too.
+template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void splitk_combine_kernel(GemmProblem p, const T *part, int ks, int64_t nz,
                                                              int tpr) {
     const int64_t row = (int64_t)blockIdx.x * (256 / tpr) + threadIdx.x / tpr;
@@ -487,9 +490,41 @@ __global__ __launch_bounds__(256) void splitk_combine_kernel(GemmProblem p, cons
             for (int u = 0; u < 4; ++u) v[u] += n0 + u < p.N ? src[s * total + u] : T(0);
     }
     T *C = static_cast<T *>(p.c) + z0 * p.sc0 + z1 * p.sc1 + m * p.scm;
+    if constexpr (VEC) {
+        using V4 = typename std::conditional<sizeof(T) == 4, float4, double4>::type;
+        const T *bias = static_cast<const T *>(p.bias);
+        V4 b{}, r{};
+        if (bias) b = *reinterpret_cast<const V4 *>(bias + z0 * p.sbias0 + z1 * p.sbias1 + n0);
+        if (p.resid)
+            r = *reinterpret_cast<const V4 *>(static_cast<const T *>(p.resid) + z0 * p.sr0 + z1 * p.sr1 + m * p.srm + n0);
+        const bool hb = bias != nullptr;
+        V4 o;
+        o.x = epilogue_values<T>(v[0], p, hb, b.x, r.x);
+        o.y = epilogue_values<T>(v[1], p, hb, b.y, r.y);
+        o.z = epilogue_values<T>(v[2], p, hb, b.z, r.z);
+        o.w = epilogue_values<T>(v[3], p, hb, b.w, r.w);
+        *reinterpret_cast<V4 *>(C + n0) = o;
+    } else {
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-        if (n0 + u < p.N) C[(n0 + u) * p.scn] = gemm_epilogue<T>(v[u], p, z0, z1, m, n0 + u);
+        for (int u = 0; u < 4; ++u)
+            if (n0 + u < p.N) C[(n0 + u) * p.scn] = gemm_epilogue<T>(v[u], p, z0, z1, m, n0 + u);
+    }
+}
+
+// The vector form of splitk_combine_kernel applies: every row of the output,
+// the residual and the bias starts 16-byte aligned and runs along n.
+template <typename T>
+bool combine_vec_ok(const GemmProblem &p, int64_t nz) {
+    auto al = [](const void *q, int64_t elems) {
+        return (reinterpret_cast<uintptr_t>(q) % 16) == 0 && (elems * (int64_t)sizeof(T)) % 16 == 0;
+    };
+    if (p.N % 4 || p.scn != 1 || !al(p.c, p.scm) || (nz > 1 && (!al(p.c, p.sc0) || !al(p.c, p.sc1)))) return false;
+    if (p.resid && (p.srn != 1 || !al(p.resid, p.srm) || (nz > 1 && (!al(p.resid, p.sr0) || !al(p.resid, p.sr1)))))
+        return false;
+    if (p.nbz) return false;
+    if (p.bias && (p.sbias != 1 || !al(p.bias, 0) || (nz > 1 && (!al(p.bias, p.sbias0) || !al(p.bias, p.sbias1)))))
+        return false;
+    return true;
 }
 
 template <typename T>
@@ -614,7 +649,12 @@ int32_t run_tiles(const GemmProblem &p, int al, int bl, bool av, bool bv, hipStr
             scratch_free(part, part_bytes);
             return set_error(CHELIS_HIP_EUNSUPPORTED, "matmul: split-K combine grid too large");
         }
-        splitk_combine_kernel<T><<<dim3((unsigned)blocks, (unsigned)cols), 256, 0, st>>>(p, part, (int)ks, nz, tpr);
+        if (combine_vec_ok<T>(p, nz))
+            splitk_combine_kernel<T, true><<<dim3((unsigned)blocks, (unsigned)cols), 256, 0, st>>>(p, part, (int)ks,
+                                                                                                   nz, tpr);
+        else
+            splitk_combine_kernel<T, false><<<dim3((unsigned)blocks, (unsigned)cols), 256, 0, st>>>(p, part, (int)ks,
+                                                                                                    nz, tpr);
         scratch_free(part, part_bytes);
     }
     CHELIS_LAUNCH_CHECK();
