@@ -41,6 +41,7 @@ constexpr int kD = 64;       // head dimension
 constexpr int kT = 64;       // query rows per workgroup, keys per tile
 constexpr int kPitch = 68;   // LDS row pitch in floats
 constexpr int kThreads = 256;
+constexpr int kMaxOrder = 32;  // q-tiles the round table covers
 
 struct AttnArgs {
     const float *q, *k, *v;
@@ -49,6 +50,10 @@ struct AttnArgs {
     // element strides of [batch][head][seq] (the last axis is contiguous)
     int64_t q0, q1, qs, k0, k1, ks, v0, v1, vs, o0, o1, os;
     float scale;
+    // round r (workgroups r * pairs ..) takes q-tile order[r] when
+    // use_order, else the heaviest-first qtiles - 1 - r
+    int32_t use_order;
+    int8_t order[kMaxOrder];
 };
 
 __device__ inline f32x4 mma(float a, float b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
@@ -67,8 +72,8 @@ __global__ __launch_bounds__(kThreads, 2) void attention_causal_kernel(AttnArgs 
     __shared__ __attribute__((aligned(16))) float Ks[kT][kPitch];  // [key][d]
     __shared__ __attribute__((aligned(16))) float Vt[kD][kPitch];  // [d][key]
 
-    // heaviest row tiles first: the first `pairs` workgroups take the last tile
-    const int64_t qt = a.qtiles - 1 - (int64_t)blockIdx.x / a.pairs;
+    const int64_t round = (int64_t)blockIdx.x / a.pairs;
+    const int64_t qt = a.use_order ? a.order[round] : a.qtiles - 1 - round;
     const int64_t z = (int64_t)blockIdx.x % a.pairs;
     const int64_t zb = z / a.heads, zh = z % a.heads;
     const float *Q = a.q + zb * a.q0 + zh * a.q1;
@@ -196,6 +201,37 @@ bool view4(const chelis_gpu_tensor *t, int64_t B, int64_t H, int64_t S) {
            t->strides[2] % 4 == 0;
 }
 
+// The q-tile of each round of `pairs` workgroups. Workgroup b runs on CU
+// b mod C when the whole grid is resident (the dispatcher deals workgroups
+// round-robin over the XCDs and their CUs; four fit per CU), so when C is a
+// multiple of pairs the rounds fall into g = C / pairs groups that share
+// their CUs (round r in group r mod g). A q-tile t costs t + 1 key tiles:
+// the tiles go heaviest first to the group with the least work so far, and
+// each group takes its tiles heaviest first. B8 H16 S512 on 256 CUs: 18 key
+// tiles on every CU, against 20 and 16 for heaviest-first rounds. Other
+// geometries keep heaviest-first rounds.
+void plan_rounds(AttnArgs &a, int64_t blocks, int cus) {
+    a.use_order = 0;
+    if (a.qtiles > kMaxOrder || a.pairs >= cus || cus % a.pairs != 0 || blocks > 4 * (int64_t)cus) return;
+    const int g = (int)(cus / a.pairs);
+    int64_t load[kMaxOrder] = {};
+    int tiles[kMaxOrder][kMaxOrder], count[kMaxOrder] = {};
+    for (int t = (int)a.qtiles - 1; t >= 0; --t) {
+        int best = 0;
+        for (int k = 1; k < g && k < kMaxOrder; ++k)
+            if (load[k] < load[best]) best = k;
+        load[best] += t + 1;
+        tiles[best][count[best]++] = t;
+    }
+    int used[kMaxOrder] = {};
+    for (int64_t r = 0; r < a.qtiles; ++r) {
+        const int k = (int)(r % g);
+        if (k >= kMaxOrder || used[k] >= count[k]) return;  // a group short of tiles: keep heaviest-first
+        a.order[r] = (int8_t)tiles[k][used[k]++];
+    }
+    a.use_order = 1;
+}
+
 }  // namespace
 
 bool attention_causal_fits(const chelis_gpu_tensor *q, const chelis_gpu_tensor *k, const chelis_gpu_tensor *v,
@@ -232,6 +268,7 @@ int32_t attention_causal(const chelis_gpu_tensor *q, const chelis_gpu_tensor *k,
     a.scale = (float)scale;
     const int64_t blocks = a.pairs * a.qtiles;
     if (!grid_fits(blocks, kThreads)) return set_error(CHELIS_HIP_EUNSUPPORTED, "attention: grid too large");
+    plan_rounds(a, blocks, device_cus());
     attention_causal_kernel<<<(unsigned)blocks, kThreads, 0, st>>>(a);
     CHELIS_LAUNCH_CHECK();
     return CHELIS_HIP_OK;

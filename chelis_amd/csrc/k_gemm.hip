@@ -432,12 +432,22 @@ __global__ __launch_bounds__(THREADS, kMinWavesPerEu<T>) void gemm_mfma_kernel(G
                                 acc[(q % 2) * (TM / 2) + ii][j][r];
             }
             __syncthreads();
+            // THREADS is a multiple of BN: each thread keeps one column, so
+            // its bias element is read once, ahead of the loop
+            static_assert(THREADS % BN == 0, "one column per thread");
+            const int col = threadIdx.x % BN;
+            const int64_t n = n0 + col;
+            const T *bias = static_cast<const T *>(p.nbz ? p.biasz[z0 * p.nb1 + z1] : p.bias);
+            const bool nin = n < p.N, hb = bias != nullptr;
+            const T b = hb && nin ? bias[(p.nbz ? 0 : z0 * p.sbias0 + z1 * p.sbias1) + n * p.sbias] : T(0);
+            const T *resid = static_cast<const T *>(p.resid);
 #pragma unroll 1
-            for (int e = threadIdx.x; e < QR * BN; e += THREADS) {
-                const int row = e / BN, col = e % BN;
-                const int64_t m = m0 + q * QR + row, n = n0 + col;
-                if (m < p.M && n < p.N)
-                    C[m * p.scm + n * p.scn] = gemm_epilogue<T, true>(tile[row * LDT + col], p, z0, z1, m, n, tb);
+            for (int row = threadIdx.x / BN; row < QR; row += THREADS / BN) {
+                const int64_t m = m0 + q * QR + row;
+                if (m < p.M && nin) {
+                    const T r = resid ? resid[z0 * p.sr0 + z1 * p.sr1 + m * p.srm + n * p.srn] : T(0);
+                    C[m * p.scm + n * p.scn] = epilogue_values<T, true>(tile[row * LDT + col], p, hb, b, r, tb);
+                }
             }
         }
         return;
