@@ -97,38 +97,59 @@ __global__ __launch_bounds__(kThreads, 2) void attention_causal_kernel(AttnArgs 
     }
 
     // staging: thread t moves 4-float runs e = 4t + 1024i (i = 0..3) of the
-    // 64 x 64 K and V tiles: key e / 64, d e % 64
-    float4 kr[4], vr[4];
-    auto load_tile = [&](int64_t kt) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int e = 4 * tid + 1024 * i, key = e >> 6, d = e & 63;
-            kr[i] = *reinterpret_cast<const float4 *>(K + (kt * kT + key) * a.ks + d);
-            vr[i] = *reinterpret_cast<const float4 *>(V + (kt * kT + key) * a.vs + d);
-        }
-    };
-    auto store_tile = [&]() {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int e = 4 * tid + 1024 * i, key = e >> 6, d = e & 63;
-            *reinterpret_cast<float4 *>(&Ks[key][d]) = kr[i];
-            Vt[d][key] = vr[i].x;
-            Vt[d + 1][key] = vr[i].y;
-            Vt[d + 2][key] = vr[i].z;
-            Vt[d + 3][key] = vr[i].w;
-        }
-    };
+    // 64 x 64 K and V tiles: key e / 64 = t / 16 + 16i, d e % 64 = 4 (t % 16).
+    // The staging registers are written and read only in straight-line code
+    // (through a lambda capturing them, the compiler kept the K half in
+    // scratch memory and waited for the next tile's loads right after
+    // issuing them, to store them there).
+    const int skey = tid >> 4, sd = (tid & 15) * 4;
+    const float *kbase = K + skey * a.ks + sd, *vbase = V + skey * a.vs + sd;
+    const int64_t kstep = 16 * a.ks, vstep = 16 * a.vs;
+    f32x4 kr0, kr1, kr2, kr3, vr0, vr1, vr2, vr3;
+#define CHELIS_ATT_LOAD(kt)                                                                      \
+    do {                                                                                         \
+        const float *kp = kbase + (kt) * kT * a.ks, *vp = vbase + (kt) * kT * a.vs;              \
+        kr0 = *reinterpret_cast<const f32x4 *>(kp);                                              \
+        kr1 = *reinterpret_cast<const f32x4 *>(kp + kstep);                                      \
+        kr2 = *reinterpret_cast<const f32x4 *>(kp + 2 * kstep);                                  \
+        kr3 = *reinterpret_cast<const f32x4 *>(kp + 3 * kstep);                                  \
+        vr0 = *reinterpret_cast<const f32x4 *>(vp);                                              \
+        vr1 = *reinterpret_cast<const f32x4 *>(vp + vstep);                                      \
+        vr2 = *reinterpret_cast<const f32x4 *>(vp + 2 * vstep);                                  \
+        vr3 = *reinterpret_cast<const f32x4 *>(vp + 3 * vstep);                                  \
+    } while (0)
+#define CHELIS_ATT_STORE1(i, kr, vr)                                                             \
+    do {                                                                                         \
+        *reinterpret_cast<f32x4 *>(&Ks[skey + 16 * (i)][sd]) = kr;                               \
+        Vt[sd][skey + 16 * (i)] = vr[0];                                                         \
+        Vt[sd + 1][skey + 16 * (i)] = vr[1];                                                     \
+        Vt[sd + 2][skey + 16 * (i)] = vr[2];                                                     \
+        Vt[sd + 3][skey + 16 * (i)] = vr[3];                                                     \
+    } while (0)
+#define CHELIS_ATT_STORE()                                                                       \
+    do {                                                                                         \
+        CHELIS_ATT_STORE1(0, kr0, vr0);                                                          \
+        CHELIS_ATT_STORE1(1, kr1, vr1);                                                          \
+        CHELIS_ATT_STORE1(2, kr2, vr2);                                                          \
+        CHELIS_ATT_STORE1(3, kr3, vr3);                                                          \
+    } while (0)
 
     f32x4 acc_o[4];
 #pragma unroll
     for (int bd = 0; bd < 4; ++bd) acc_o[bd] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_run = 0.f;
 
-    load_tile(0);
-    store_tile();
+    CHELIS_ATT_LOAD(0);
+    CHELIS_ATT_STORE();
     __syncthreads();
+    // Every load issued so far (the query row included) completes here, so
+    // the loop header has nothing older to wait for: otherwise the wait the
+    // compiler places there for the query row (its first use) also waits
+    // for the next tile's loads on every iteration, and the prefetch never
+    // overlaps the tile's arithmetic.
+    __builtin_amdgcn_s_waitcnt(0);
     for (int64_t kt = 0; kt <= qt; ++kt) {
-        if (kt < qt) load_tile(kt + 1);
+        if (kt < qt) CHELIS_ATT_LOAD(kt + 1);
         // S^T = K Q^T for the tile's four key blocks
         f32x4 s[4];
 #pragma unroll
@@ -182,10 +203,13 @@ __global__ __launch_bounds__(kThreads, 2) void attention_causal_kernel(AttnArgs 
             }
         if (kt < qt) {
             __syncthreads();  // every wave is done with this tile
-            store_tile();
+            CHELIS_ATT_STORE();
             __syncthreads();
         }
     }
+#undef CHELIS_ATT_STORE
+#undef CHELIS_ATT_STORE1
+#undef CHELIS_ATT_LOAD
     const float inv = 1.f / l_run;
 #pragma unroll
     for (int bd = 0; bd < 4; ++bd) {
