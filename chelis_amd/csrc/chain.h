@@ -116,9 +116,10 @@ template <typename T, class Tabs>
 __device__ inline T gelu_one_t(T x, const Tabs &tb) {
     const T c = PhiK<T>::c, cl = PhiK<T>::cl, k = PhiK<T>::k, s = PhiK<T>::s;
     T e;
+    double e_neg_sq = 0.0;  // binary32: exp(-(x c)^2) in binary64 from the erfc fast path
     if constexpr (sizeof(T) == 4) {
         bool slow;
-        e = erfcf_fast_t(-x * c, slow, tb);
+        e = erfcf_fast_t(-x * c, slow, tb, &e_neg_sq);
         if (slow) e = erfc_slow32(-x * c);
     } else {
         e = leaf_erfc<T>(-x * c);
@@ -139,9 +140,13 @@ __device__ inline T gelu_one_t(T x, const Tabs &tb) {
     const T tl = t + a * cl;
     T g;
     if constexpr (sizeof(T) == 4) {
+        // |x| < 64: th is the erfc argument -x c itself, so exp(-fl(th^2))
+        // comes from the erfc path's exp(-th^2); otherwise th = -0, g = 1
+        const bool near = fabs(x) < T(64);
         bool slow;
-        g = expf_fast(-(th * th), tb, slow);
-        if (slow) g = expf_slow_cr(-(th * th));
+        const float gf = expf_neg_square_from(th, e_neg_sq, slow);
+        g = near ? gf : T(1);
+        if (near && slow) g = expf_slow_cr(-(th * th));
     } else {
         g = leaf_exp<T>(-(th * th));
     }

@@ -247,8 +247,12 @@ CHELIS_HD inline float quot_f32(float v, double inv) { return (float)((double)v 
 // an accessor reading them there (a per-lane index into constant memory is a
 // vector memory load per coefficient: GELU over 16.7M binary32 values 82-85
 // us from constant memory, 65-72 us from LDS, same bits).
+// exp_neg_sq, when given, receives the binary64 exp(-x^2) of the exact
+// square that the x >= 1/2 branch uses (computed for every x; within
+// 2^-51.2 relative while x^2 < 104: truncation 2^-54.5, the Horner
+// polynomial's last rounding 1.1 * 2^-53, T[j] and the product 2^-53 each).
 template <class Tabs>
-CHELIS_HD inline float erfcf_fast_t(float xf, bool &slow, const Tabs &tb) {
+CHELIS_HD inline float erfcf_fast_t(float xf, bool &slow, const Tabs &tb, double *exp_neg_sq = nullptr) {
     const double x = (double)xf;
     const double ax = fabs(x);
     const double s = x * x;  // exact
@@ -275,12 +279,34 @@ CHELIS_HD inline float erfcf_fast_t(float xf, bool &slow, const Tabs &tb) {
     p = fma(p, r, 1.0);
     p = fma(p, r, 1.0);
     const double e = ldexp(tb.e(k & 63) * p, (k - (k & 63)) / 64);
+    if (exp_neg_sq) *exp_neg_sq = e;
     const double yb = e * g;
     double y = ax < 0.5 ? ya : (x > 0.0 ? yb : 2.0 - yb);
     y = x <= -4.5 ? 2.0 : (x >= 10.1 ? 0.0 : y);
     const uint32_t below = ((uint32_t)f64_bits(y) & 0x1fffffffu) - (0x10000000u - 512u);
     slow = (x != x) || (x >= 9.1 && x < 10.1) || below < 1024u;
     return (float)y;
+}
+
+// Correctly rounded binary32 exp(-fl(t * t)) for a binary32 t, derived from
+// E = exp(-t^2) in binary64 for the exact square (erfcf_fast_t's exp_neg_sq
+// for x = t, within 2^-51.2 relative), so GELU's correction term needs no
+// exp evaluation of its own. d = t^2 - fl(t^2) is exact in binary64 and
+// |d| <= 2^-18 wherever the result is not +0 (fl(t^2) < 104), so
+// exp(-fl(t^2)) = E exp(d) = E (1 + d + d^2/2) to 2^-56.6; with the two
+// fma and the product, y is within 2^-50.5 relative: under 6 units of the
+// rounding test's 2^-29 binary32-ulp grid, whose window is 2047 units (the
+// test and the ranges are expf_fast's: arguments at or below -104 give +0,
+// (-104, -87] - subnormal results - are flagged). t must be finite.
+CHELIS_HD inline float expf_neg_square_from(float t, double E, bool &slow) {
+    const float s32 = t * t;
+    const double d = (double)t * (double)t - (double)s32;
+    const double y = E * fma(d, fma(d, 0.5, 1.0), 1.0);
+    const float xf = -s32;
+    const bool zero = xf <= -104.0f;
+    const uint32_t below = ((uint32_t)f64_bits(y) & 0x1fffffffu) - (0x10000000u - 2047u);
+    slow = !zero && (!(xf > -87.0f) || below < 4095u);
+    return zero ? 0.0f : (float)y;
 }
 
 // The constant-memory tables (also the 2^(j/64) accessor of expf_fast).

@@ -1,5 +1,5 @@
 """Exhaustive device check of the binary32 transcendental leaves against
-CORE-MATH (the C backend's libm, crates/chelis-crmath/csrc/crmath_ffi.c,
+CORE-MATH, and of the binary32 GELU graph against the C oracle (the C backend's libm, crates/chelis-crmath/csrc/crmath_ffi.c,
 with the wrapper's NaN canonicalization): every one of the 2^32 binary32
 inputs, bit for bit. exp is the correctly rounded expf_cr of devmath.h;
 log, erfc and tanh are the binary64 device evaluation rounded once, with
@@ -69,3 +69,22 @@ def mismatches(cr, op, cap=64):
 def test_binary32_leaf_is_correctly_rounded_on_every_input(cr, op):
     n, bad = mismatches(cr, op)
     assert n == 0, f"{n} inputs differ; first {[tuple(hex(v) for v in b) for b in bad[:8]]}"
+
+
+def test_gelu_f32_matches_the_oracle_on_every_input():
+    """GELU over all 2^32 binary32 inputs through the unary kernel (whose
+    GELU is the one the GEMM epilogue and the chain interpreter inline),
+    bit for bit against the C oracle's restated Phi graph with CORE-MATH's
+    erfc and exp leaves: pins the erfc fast path, the exp(-th^2) the
+    correction derives from it, their rounding tests and fallbacks."""
+    O.build()
+    total, bad = 0, []
+    for r in range((1 << 32) // RUN):
+        x = (np.arange(RUN, dtype=np.uint32) + np.uint32(r * RUN)).view(np.float32)
+        got = np.ascontiguousarray(C.gelu(C.to_device(x)).numpy()).view(np.uint32)
+        ref = np.ascontiguousarray(O.gelu(x)).view(np.uint32)
+        diff = np.nonzero(got != ref)[0]
+        total += len(diff)
+        bad += [(hex(int(x.view(np.uint32)[i])), hex(int(ref[i])), hex(int(got[i]))) for i in diff[:8]]
+        print(f"gelu: run {r} done, {len(diff)} mismatches", flush=True)
+    assert total == 0, f"{total} inputs differ; first {bad[:8]}"
