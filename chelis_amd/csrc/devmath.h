@@ -278,7 +278,7 @@ CHELIS_HD inline float erfcf_fast_t(float xf, bool &slow, const Tabs &tb, double
     p = fma(p, r, 0.5);
     p = fma(p, r, 1.0);
     p = fma(p, r, 1.0);
-    const double e = ldexp(tb.e(k & 63) * p, (k - (k & 63)) / 64);
+    const double e = ldexp(tb.e(k & 63) * p, k >> 6);  // k = 64 (k >> 6) + (k & 63)
     if (exp_neg_sq) *exp_neg_sq = e;
     const double yb = e * g;
     double y = ax < 0.5 ? ya : (x > 0.0 ? yb : 2.0 - yb);
@@ -537,7 +537,7 @@ CHELIS_HD inline ExpDD exp_dd(double x, const Tab2 &tab) {
     const double yh = th + ph;  // Fast2Sum: th >= 1 > |ph|
     const double e2 = ph - (yh - th);
     const double yl = e2 + (pl + fma(th, ql, fma(tlo, qh, tlo)));
-    return {yh, yl, (k - (k & 63)) / 64};
+    return {yh, yl, k >> 6};  // k = 64 (k >> 6) + (k & 63)
 }
 
 template <bool NONPOS = false, class Tab2>
