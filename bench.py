@@ -259,15 +259,16 @@ def bench_bandwidth(C, H, steps, warmup):
 # the relu's known bytes fix.
 CAUSAL_READ = 8 * 16 * (512 * 513 // 2) * 4  # causal score rows read only j <= i
 BW_SET = [
-    ("softmax_f32_16384x1024", r"softmax_kernel<float,.*true>", 2 * 16384 * 1024 * 4),
-    ("softmax_f64_4096x4096", r"softmax_kernel<double", 2 * 4096 * 4096 * 8),
+    ("softmax_f32_16384x1024", r"softmax_kernel<float,[^>]*, true, false>", 2 * 16384 * 1024 * 4),
+    ("softmax_f64_4096x4096", r"softmax_kernel<double,[^>]*, true, true>", 2 * 4096 * 4096 * 8),
     ("gemv_f64_8192x8192", r"tree_wave_kernel<double", 8192 * 8192 * 8 + 2 * 8192 * 8),
     ("layer_norm_f32_65536x1024", r"layer_norm_kernel<float", 2 * 65536 * 1024 * 4),
     ("relu_f32_16384x4096", r"unary_kernel<float", 2 * 16384 * 4096 * 4),
     ("fused_chain_sqdiff_f32_16384x4096", r"fused_flat_vec_kernel<float", 3 * 16384 * 4096 * 4),
     ("reduce_sum_rows_f32_16384x4096", r"reduce_rows_vec_kernel<float", 16384 * 4096 * 4 + 16384 * 4),
     ("softmax_adjoint_f32_65536x1024", r"softmax_adjoint_kernel<float", 3 * 65536 * 1024 * 4),
-    ("causal_softmax_f32_8x16x512x512", r"softmax_kernel<float,.*false>", CAUSAL_READ + 8 * 16 * 512 * 512 * 4),
+    ("causal_softmax_f32_8x16x512x512", r"softmax_kernel<float,[^>]*, false, false>",
+     CAUSAL_READ + 8 * 16 * 512 * 512 * 4),
 ]
 CALIBRATION = "relu_f32_16384x4096"
 # GEMMs whose MFMA activity is read (SQ_VALU_MFMA_BUSY_CYCLES per SIMD over

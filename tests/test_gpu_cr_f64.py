@@ -11,7 +11,8 @@ canonicalization), bit for bit:
   (tests/golden/binary64_worst_cases.txt, MPFR-derived) and of the canary
   file (specials, NaN payloads, the overflow and underflow thresholds);
 - softmax rows built so that x - max equals a negative worst-case input,
-  which the softmax kernel's wave-uniform slow pass must round correctly.
+  which the softmax kernel's wave-uniform slow pass must round correctly
+  (the exact mode's row; the default row is held to 1e-13).
 """
 import ctypes
 import os
@@ -110,6 +111,13 @@ def test_softmax_f64_worst_case_arguments(n):
     for r in range(rows):
         x[r] = rng.choice(w, n)
         x[r, rng.integers(0, n)] = 0.0
-    y = C.softmax(C.to_device(x)).numpy()
     ref = O.softmax_rows(x)
+    prev = C.set_exact(True)  # the correctly rounded row (the default row's exp is faithful)
+    try:
+        y = C.softmax(C.to_device(x)).numpy()
+    finally:
+        C.set_exact(prev)
     assert np.array_equal(y.view(np.uint64), ref.view(np.uint64))
+    # the default row on the same arguments: within 1e-13 per element
+    y = C.softmax(C.to_device(x)).numpy()
+    assert (np.abs(y - ref) <= 1e-13 * np.abs(ref) + 4 * 2.0 ** -1074).all()
