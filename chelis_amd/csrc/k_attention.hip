@@ -150,11 +150,16 @@ __global__ __launch_bounds__(kThreads, 2) void attention_causal_kernel(AttnArgs 
     __builtin_amdgcn_s_waitcnt(0);
     for (int64_t kt = 0; kt <= qt; ++kt) {
         if (kt < qt) CHELIS_ATT_LOAD(kt + 1);
+        // On the diagonal tile, key block kb > wave lies wholly above this
+        // wave's rows: its scores are masked to -inf below and its P.V terms
+        // are skipped, as the tiles above the diagonal are.
+        const bool diag = kt == qt;
         // S^T = K Q^T for the tile's four key blocks
         f32x4 s[4];
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
             s[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (diag && kb > wave) continue;
 #pragma unroll
             for (int h = 0; h < 4; ++h) {
                 const float4 kf = *reinterpret_cast<const float4 *>(&Ks[16 * kb + j][16 * q + 4 * h]);
@@ -192,7 +197,8 @@ __global__ __launch_bounds__(kThreads, 2) void attention_causal_kernel(AttnArgs 
         for (int bd = 0; bd < 4; ++bd) acc_o[bd] *= alpha;
         // O^T += V^T P^T
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
+        for (int kb = 0; kb < 4; ++kb) {
+            if (diag && kb > wave) continue;
 #pragma unroll
             for (int bd = 0; bd < 4; ++bd) {
                 const float4 vf = *reinterpret_cast<const float4 *>(&Vt[16 * bd + j][16 * kb + 4 * q]);
@@ -201,6 +207,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_causal_kernel(AttnArgs 
                 acc_o[bd] = mma(vf.z, s[kb][2], acc_o[bd]);
                 acc_o[bd] = mma(vf.w, s[kb][3], acc_o[bd]);
             }
+        }
         if (kt < qt) {
             __syncthreads();  // every wave is done with this tile
             CHELIS_ATT_STORE();
