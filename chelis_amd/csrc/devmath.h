@@ -228,11 +228,13 @@ CHELIS_HD inline float quot_f32(float v, double inv) { return (float)((double)v 
 // 9.1 <= x < 10.1, left to the caller's fallback).
 //
 // For -4.5 < x < 9.1, y is erfc(x) in binary64 to about 2^-47 relative:
-// for |x| < 1/2, 1 - x P(x^2) with P a degree-7 fit of erf(x)/x (2^-49);
-// otherwise exp(-x^2) erfcx(|x|) with erfcx a degree-9 fit on intervals of
-// 1/4 (2^-48; x^2 is exact, exp(-x^2) is reduced as in expf_fast with a
-// degree-5 Taylor polynomial, truncation below 2^-54), and erfc(x) =
-// 2 - erfc(-x) for x < 0. The coefficients are erfc_table.h's
+// exp(-x^2) erfcx(|x|) with erfcx a degree-9 fit on the intervals
+// [i/4, (i + 1)/4) (2^-48; x^2 is exact, exp(-x^2) is reduced as in
+// expf_fast with a degree-5 Taylor polynomial, truncation below 2^-54), and
+// erfc(x) = 2 - erfc(-x) for x < 0 (a result in (1, 2], no cancellation).
+// One branch-free evaluation serves every x: the interval 0 fit starts at
+// x = 0, where a separate fit of erf(x)/x for |x| < 1/2 was evaluated for
+// every argument beside the interval one and then mostly discarded. The coefficients are erfc_table.h's
 // (gen_erfc_table.py). Every such result is a normal binary32 (erfc(9.1) >
 // 2^-126), so (float)y is the correctly rounded result unless the 29 bits
 // below binary32 precision in y lie within 2^9 units of the midpoint
@@ -248,22 +250,19 @@ CHELIS_HD inline float quot_f32(float v, double inv) { return (float)((double)v 
 // vector memory load per coefficient: GELU over 16.7M binary32 values 82-85
 // us from constant memory, 65-72 us from LDS, same bits).
 // exp_neg_sq, when given, receives the binary64 exp(-x^2) of the exact
-// square that the x >= 1/2 branch uses (computed for every x; within
-// 2^-51.2 relative while x^2 < 104: truncation 2^-54.5, the Horner
-// polynomial's last rounding 1.1 * 2^-53, T[j] and the product 2^-53 each).
+// square that the evaluation uses (within 2^-51.2 relative while x^2 < 104:
+// truncation 2^-54.5, the Horner polynomial's last rounding 1.1 * 2^-53,
+// T[j] and the product 2^-53 each).
 template <class Tabs>
 CHELIS_HD inline float erfcf_fast_t(float xf, bool &slow, const Tabs &tb, double *exp_neg_sq = nullptr) {
     const double x = (double)xf;
     const double ax = fabs(x);
     const double s = x * x;  // exact
-    const double ta = fma(8.0, s, -1.0);
-    double pa = chelis_erf_a[7];
-#pragma unroll
-    for (int d = 6; d >= 0; --d) pa = fma(pa, ta, chelis_erf_a[d]);
-    const double ya = fma(-x, pa, 1.0);
-    int i = (int)((ax - 0.5) * 4.0);
-    i = i < 0 ? 0 : (i > 34 ? 34 : i);
-    const double tv = (ax - (0.5 + 0.25 * i)) * 8.0 - 1.0;  // exact
+    // the interval, clamped before the conversion (NaN and the infinities
+    // take the last one; their results are flagged or replaced below)
+    const double q = ax * 4.0;
+    const int i = q < 36.0 ? (int)q : 36;
+    const double tv = (ax - 0.25 * i) * 8.0 - 1.0;  // exact
     double g = tb.b(i, 9);
 #pragma unroll
     for (int d = 8; d >= 0; --d) g = fma(g, tv, tb.b(i, d));
@@ -281,7 +280,7 @@ CHELIS_HD inline float erfcf_fast_t(float xf, bool &slow, const Tabs &tb, double
     const double e = ldexp(tb.e(k & 63) * p, k >> 6);  // k = 64 (k >> 6) + (k & 63)
     if (exp_neg_sq) *exp_neg_sq = e;
     const double yb = e * g;
-    double y = ax < 0.5 ? ya : (x > 0.0 ? yb : 2.0 - yb);
+    double y = x > 0.0 ? yb : 2.0 - yb;
     y = x <= -4.5 ? 2.0 : (x >= 10.1 ? 0.0 : y);
     const uint32_t below = ((uint32_t)f64_bits(y) & 0x1fffffffu) - (0x10000000u - 512u);
     slow = (x != x) || (x >= 9.1 && x < 10.1) || below < 1024u;
