@@ -127,6 +127,38 @@ def test_narrow_matmul_mfma_within_bound(kind, shape):
 
 
 @pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("b_along_k", [False, True])
+@pytest.mark.parametrize("shape", [(128, 256, 192), (256, 128, 64), (384, 256, 320)])
+def test_narrow_matmul_whole_tiles(kind, b_along_k, shape):
+    """Whole 128 x 128 tiles and whole 64-deep K steps (the two-staging-set
+    kernel), B along N (row-major) or along K (a transposed view), odd and
+    even step counts: within the same bound as every other product."""
+    M, N, K = shape
+    a, b = finite_bits(kind, (M, K), 20), finite_bits(kind, (K, N), 21)
+    da = C.to_device(carrier(kind, a))
+    if b_along_k:
+        dbt = C.to_device(carrier(kind, np.ascontiguousarray(b.T)))
+        db = dbt.view((K, N), (1, K))
+    else:
+        db = C.to_device(carrier(kind, b))
+    c = C.matmul(da, db)
+    got = O.narrow_decode(kind, bits_of(c.numpy())).astype(np.float64)
+    ref, bound = _mm_bound(kind, a, b)
+    bad = np.abs(got - ref) > bound
+    assert not bad.any(), (np.argwhere(bad)[:5], got[bad][:5], ref[bad][:5])
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_narrow_matmul_whole_tiles_batched(kind):
+    """A batch of whole-tile products against one broadcast B (batch stride 0)."""
+    a, b = finite_bits(kind, (3, 128, 256), 22), finite_bits(kind, (256, 128), 23)
+    c = C.matmul(C.to_device(carrier(kind, a)), C.to_device(carrier(kind, b)))
+    got = O.narrow_decode(kind, bits_of(c.numpy())).astype(np.float64)
+    ref, bound = _mm_bound(kind, a, b)
+    assert np.all(np.abs(got - ref) <= bound)
+
+
+@pytest.mark.parametrize("kind", KINDS)
 def test_narrow_matmul_transposed_and_batched(kind):
     """Transposed operands (stride swaps), a broadcast batch axis, and the
     element-by-element staging of a misaligned view."""
