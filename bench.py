@@ -485,7 +485,7 @@ def cpu_model() -> str:
 
 
 def _time_cpu(fn, warmup, runs, budget_s=None):
-    """`warmup` untimed calls, then the median of
+    """The CPU timing protocol: `warmup` untimed calls, then the median of
     `runs` timed calls of the entry alone; with `budget_s`, warm-up stops
     after a third of it and timing after all of it (at least one of each)."""
     t_all = time.perf_counter()
@@ -505,8 +505,8 @@ def _time_cpu(fn, warmup, runs, budget_s=None):
 
 
 def cpu_baselines(x_softmax, x64, kernels, linreg, transformer, mlp, gemm_inputs):
-    """The C oracle on this host with every core, timed per BASELINE.md
-    section 3 (5 warm-ups, the median of 50 timed calls; the 4096^3 GEMMs on
+    """The C oracle on this host with every core (5 warm-ups, the median of
+    50 timed calls; the 4096^3 GEMMs on
     a stated slice of their rows, whose rate is reported, not scaled up),
     plus one single-thread run of the headline."""
     from oracle import oracle as O
@@ -574,7 +574,7 @@ def main(argv=None) -> int:
         return 0
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "how the path would shard is described in DESIGN.md, not run.", file=sys.stderr)
+              "sharding across GPUs is a design note of this build, not a measured path.", file=sys.stderr)
         return 2
 
     import chelis_amd as C
