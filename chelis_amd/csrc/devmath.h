@@ -157,13 +157,15 @@ CHELIS_HD inline float expf_fast(float xf, const Tab &tab, bool &slow) {
         // (every comparison with NaN is false), and the midpoint test runs
         // on every other result; a flag on a raised argument only costs the
         // slow path.
+        // Here |k| <= 9660, so one fma against ln2/64 rounded to binary64
+        // (within 2^-60 of it) reduces x to within 2^-46.7 absolute: the
+        // two-part constant of the general case is not needed.
         const float xc = xf > -104.5f ? xf : -104.5f;
         const double x = (double)xc;
         const double shifted = fma(x, CHELIS_INV_LN2_64, 0x1.8p52);
         const double kd = shifted - 0x1.8p52;
         const int k = (int)(uint32_t)f64_bits(shifted);
-        double r = fma(-kd, CHELIS_LN2_64_HI, x);
-        r = fma(-kd, CHELIS_LN2_64_LO, r);
+        const double r = fma(-kd, 0x1.62e42fefa39efp-7, x);  // ln2/64
         double p = fma(r, 0x1.5555555555555p-5, 0x1.5555555555555p-3);
         p = fma(p, r, 0.5);
         p = fma(p, r, 1.0);
