@@ -17,8 +17,10 @@ WRITE_SIZE), each scaled by what the same counter reads for a plain 256 MiB
 relu map (a read-once, write-once elementwise kernel of known size). The
 same passes give every bandwidth kernel in `kernels` its measured traffic
 (`hbm_traffic_bytes`, `traffic_ratio` against the algorithmic bytes,
-`frac_hbm_counter`), and a third and fourth pass (SQ_VALU_MFMA_BUSY_CYCLES,
-GRBM_GUI_ACTIVE, the MFMA op counts) give the GEMMs their MFMA busy share.
+`frac_hbm_counter`), a third and fourth pass (SQ_VALU_MFMA_BUSY_CYCLES,
+GRBM_GUI_ACTIVE, the MFMA op counts) give the GEMMs their MFMA busy share, and
+a fifth (SQ_INSTS_VALU, SQ_WAVES, GRBM_GUI_ACTIVE) the kernels labelled
+VALU-bound their VALU issue share (`valu_issue_pct_counter`).
 
 `kernels` reports every configuration the same way: GB/s against the 8 TB/s
 HBM peak for bandwidth kernels, TFLOP/s against the dtype's MFMA peak for
@@ -279,6 +281,18 @@ MFMA_SET = [
     ("skinny_f64_8192x64x4096", r"gemm_mfma_kernel<double, \d, \d, 2,"),
 ]
 TRANSFORMER_SET = [("transformer_block_f32_b8_s512_d1024", r"gemm_mfma_kernel<float")]
+# Kernels labelled VALU-bound (and the headline for comparison), with their
+# VALU issue read per dispatch: SQ_INSTS_VALU counts wave instructions, each
+# of which holds its SIMD for 4 cycles (64 lanes over 16; the binary64 FMA is
+# full rate on this part), so 4 * SQ_INSTS_VALU / (GRBM_GUI_ACTIVE x SIMDs)
+# is the share of the SIMDs' VALU issue capacity the dispatch used.
+VALU_SET = [
+    ("softmax_f32_16384x1024", r"softmax_kernel<float,[^>]*, true, false>"),
+    ("softmax_f64_4096x4096", r"softmax_kernel<double,[^>]*, true, true>"),
+    ("softmax_f64_4096x4096_exact", r"softmax_kernel<double,[^>]*, true, false>"),
+    ("gelu_f32_16384x4096", r"unary_kernel<float, \(.*Unary\)0>"),
+    ("dropout_f32_16384x4096", r"unary_kernel<float, \(.*Unary\)3>"),
+]
 SIMDS = 1024  # 256 CUs x 4 SIMDs
 PROFILE_LAUNCHES = 3
 
@@ -337,6 +351,28 @@ def profile_child(kind: str):
             c = C.matmul(a, b)
             for _ in range(n):
                 C.matmul(a, b, c)
+    elif kind == "valu":
+        x = softmax_inputs()
+        pairs = [(C.to_device(x), C.empty(x.shape, np.float32)) for _ in range(5)]
+        for i in range(n):
+            C.softmax(pairs[i % 5][0], pairs[i % 5][1])
+        del pairs
+        x64 = np.random.default_rng(11).standard_normal((4096, 4096))
+        p64 = [(C.to_device(x64), C.empty(x64.shape, np.float64)) for _ in range(2)]
+        for exact in (False, True):
+            prev = C.set_exact(exact)
+            try:
+                for i in range(n):
+                    C.softmax(p64[i % 2][0], p64[i % 2][1])
+            finally:
+                C.set_exact(prev)
+        del p64
+        xb = rng.standard_normal((16384, 4096)).astype(np.float32)
+        X, Y = C.to_device(xb), C.empty(xb.shape, np.float32)
+        for _ in range(n):
+            C.gelu(X, Y)
+        for _ in range(n):
+            C.dropout(44, X, 0.1, Y)
     elif kind == "transformer":
         x, prm = transformer_data()
         ins = [C.to_device(x)] + [C.to_device(prm[k]) for k in PARAM_ORDER]
@@ -448,12 +484,33 @@ def measure_counters(kernels, keep_root=None):
             summary["mfma"][key] = rec
             if key in kernels:
                 kernels[key]["mfma_busy_pct_counter"] = rec["mfma_busy_pct"]
+    disp, cmd = _pmc_pass(["SQ_INSTS_VALU", "SQ_ACTIVE_INST_VALU", "SQ_WAVES", "GRBM_GUI_ACTIVE"], "valu",
+                          keep("valu"))
+    summary["commands"].append(cmd)
+    summary["valu"] = {}
+    import re
+
+    for key, pat in VALU_SET:
+        sel = [c for name, c in disp if re.search(pat, name) and "GRBM_GUI_ACTIVE" in c and "SQ_INSTS_VALU" in c]
+        if not sel:
+            continue
+        insts = sum(c["SQ_INSTS_VALU"] for c in sel)
+        waves = sum(c.get("SQ_WAVES", 0.0) for c in sel)
+        active = sum(c["GRBM_GUI_ACTIVE"] for c in sel)
+        dur = sum(c.get("_dur_ns", 0.0) for c in sel)
+        per_xcd = 8 if dur > 0 and active / dur > 4.0 else 1
+        rec = {"valu_issue_pct": round(100.0 * 4 * insts / (active / per_xcd * SIMDS), 1),
+               "valu_insts_per_wave": round(insts / waves, 1) if waves else None, "dispatches": len(sel),
+               "clock_ghz": round(active / per_xcd / dur, 3) if dur > 0 else None}
+        summary["valu"][key] = rec
+        if key in kernels:
+            kernels[key]["valu_issue_pct_counter"] = rec["valu_issue_pct"]
     head = summary["bandwidth"].get("softmax_f32_16384x1024")
     return head, summary
 
 
 def counters_markdown(summary) -> str:
-    lines = ["# HBM traffic and MFMA activity per kernel (rocprofv3 counters)", "",
+    lines = ["# HBM traffic, MFMA activity and VALU issue per kernel (rocprofv3 counters)", "",
              "Commands (each a pass of its own; `bench.py` runs them with `--counters`):", ""]
     lines += [f"    cd /tmp && export TMPDIR=/tmp && {c}" for c in summary["commands"]]
     lines += ["", summary["calibration"], "",
@@ -469,6 +526,14 @@ def counters_markdown(summary) -> str:
     for k, r in summary["mfma"].items():
         lines.append(f"| {k} | {r['mfma_busy_pct']} | {r['mfma_flop_per_dispatch']} | {r['clock_ghz']} | "
                      f"{r['dispatches']} |")
+    if summary.get("valu"):
+        lines += ["", "VALU issue = 4 x SQ_INSTS_VALU / (GRBM_GUI_ACTIVE x 1024 SIMDs): each wave instruction holds "
+                      "its SIMD for 4 cycles (64 lanes over 16).", "",
+                  "| kernel | VALU issue (% of SIMD cycles) | VALU instructions per wave | clock GHz | dispatches |",
+                  "|---|---|---|---|---|"]
+        for k, r in summary["valu"].items():
+            lines.append(f"| {k} | {r['valu_issue_pct']} | {r['valu_insts_per_wave']} | {r['clock_ghz']} | "
+                         f"{r['dispatches']} |")
     return "\n".join(lines) + "\n"
 
 
@@ -567,7 +632,7 @@ def main(argv=None) -> int:
     ap.add_argument("--counters-dir", default=None, help="keep the raw counter output here")
     ap.add_argument("--counters-md", default=None, help="write the counter summary as markdown here")
     ap.add_argument("--only-headline", action="store_true")
-    ap.add_argument("--profile-child", choices=("bandwidth", "mfma", "transformer"), help=argparse.SUPPRESS)
+    ap.add_argument("--profile-child", choices=("bandwidth", "mfma", "transformer", "valu"), help=argparse.SUPPRESS)
     args = ap.parse_args(argv)
     if args.profile_child:
         profile_child(args.profile_child)
