@@ -174,11 +174,15 @@ struct ErfcLdsStore {
 };
 
 // ---------------------------------------------------------------- chain ops
+// The step fields are 32-bit words: the interpreter reads them at a
+// run-time step index, and gfx950's scalar loads move whole dwords, so a
+// byte field would be read with a vector load (a full memory round trip per
+// step, queued behind the kernel's streaming loads).
 struct ChainDev {
     int32_t n_steps;
-    uint8_t op[CHELIS_FUSED_MAX_STEPS];
-    int8_t a0[CHELIS_FUSED_MAX_STEPS];
-    int8_t a1[CHELIS_FUSED_MAX_STEPS];
+    int32_t op[CHELIS_FUSED_MAX_STEPS];
+    int32_t a0[CHELIS_FUSED_MAX_STEPS];
+    int32_t a1[CHELIS_FUSED_MAX_STEPS];
     double imm[CHELIS_FUSED_MAX_STEPS];
 };
 

@@ -174,16 +174,22 @@ __global__ __launch_bounds__(256) void reduce_rows_kernel(ChainDev ch, LeafSrc s
 
 // Contiguous rows: leaf i of row o of input k at p[k] + o*so[k] + i, each
 // row start 16-byte aligned. Leaf indices are positions (a first pass, or a
-// later pass of a value-only reduction).
-template <typename T, Rk K, int S, bool CHAIN>
+// later pass of a value-only reduction). A chain leaf with NIN > 0 inputs
+// (the count fixed at compile time) issues the 16-byte loads of all S
+// segments before the first segment's interpreter run, so a wave holds
+// S * NIN * 1 KiB in flight; NIN = 0 takes the input count at run time with
+// one segment per wave.
+template <typename T, Rk K, int S, bool CHAIN, int NIN = 0>
 __global__ __launch_bounds__(256) void reduce_rows_vec_kernel(ChainDev ch, LeafSrc src, int64_t outer, int64_t n,
                                                               int64_t groups, T *__restrict__ out_v,
                                                               int64_t *__restrict__ out_i, bool last) {
     constexpr int V = 16 / sizeof(T);
     constexpr int G = 64 * V * S;
+    constexpr int NI = NIN > 0 ? NIN : CHELIS_FUSED_MAX_INPUTS;
+    static_assert(!CHAIN || NIN > 0 || S == 1, "a run-time input count takes one segment per wave");
     using Q = typename Vec16F<T>::type;
     // a chain leaf runs on the vector interpreter (run_chain_vec): its
-    // slots are this launch's dynamic LDS
+    // slots are this launch's dynamic LDS, each thread's own
     extern __shared__ __align__(16) unsigned char red_lds[];
     Q *qs = reinterpret_cast<Q *>(red_lds);
     const int lane = threadIdx.x & 63;
@@ -191,6 +197,27 @@ __global__ __launch_bounds__(256) void reduce_rows_vec_kernel(ChainDev ch, LeafS
     if (item >= outer * groups) return;
     const int64_t o = item / groups, g = item % groups;
     T v[CHAIN ? 1 : S][V];
+    Q in[CHAIN ? S : 1][CHAIN ? NI : 1];
+    if constexpr (CHAIN) {
+        // every segment's loads issued before the first interpreter run
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const int64_t i0 = g * G + (int64_t)s * 64 * V + (int64_t)lane * V;
+#pragma unroll
+            for (int k = 0; k < NI; ++k) {
+                if (NIN > 0 || k < src.n_in) {
+                    const T *p = static_cast<const T *>(src.p[k]) + o * src.so[k];
+                    if (i0 + V <= n) {
+                        in[s][k] = *reinterpret_cast<const Q *>(p + i0);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < V; ++e)
+                            reinterpret_cast<T *>(&in[s][k])[e] = i0 + e < n ? p[i0 + e] : T(0);
+                    }
+                }
+            }
+        }
+    }
     if constexpr (!CHAIN) {
         // every load issued before the first combine
         const T *row = static_cast<const T *>(src.p[0]) + o * src.so[0];
@@ -236,24 +263,11 @@ __global__ __launch_bounds__(256) void reduce_rows_vec_kernel(ChainDev ch, LeafS
         const int64_t i0 = g * G + (int64_t)s * 64 * V + (int64_t)lane * V;
         T(&cur)[V] = v[CHAIN ? 0 : s];
         if constexpr (CHAIN) {
-            Q in[CHELIS_FUSED_MAX_INPUTS];
 #pragma unroll
-            for (int k = 0; k < CHELIS_FUSED_MAX_INPUTS; ++k) {
-                if (k < src.n_in) {
-                    const T *p = static_cast<const T *>(src.p[k]) + o * src.so[k];
-                    if (i0 + V <= n) {
-                        in[k] = *reinterpret_cast<const Q *>(p + i0);
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < V; ++e) reinterpret_cast<T *>(&in[k])[e] = i0 + e < n ? p[i0 + e] : T(0);
-                    }
-                }
-            }
-#pragma unroll
-            for (int k = 0; k < CHELIS_FUSED_MAX_INPUTS; ++k)
-                if (k < src.n_in) qs[k * 256 + threadIdx.x] = in[k];
+            for (int k = 0; k < NI; ++k)
+                if (NIN > 0 || k < src.n_in) qs[k * 256 + threadIdx.x] = in[s][k];
             T r[V];
-            run_chain_vec<T, V>(ch, qs, src.n_in, threadIdx.x, r);
+            run_chain_vec<T, V>(ch, qs, NIN > 0 ? NIN : src.n_in, threadIdx.x, r);
 #pragma unroll
             for (int e = 0; e < V; ++e) cur[e] = i0 + e < n ? r[e] : identity<T, K>();
         }
@@ -485,6 +499,11 @@ struct Pass {
     int64_t groups; // partials per output it writes
 };
 constexpr int kMaxPasses = 16;
+// Contiguous chain leaves: the input counts with a compile-time instance
+// whose loads for up to kChainSegments segments per wave are all issued
+// before the interpreter runs.
+constexpr int kChainPreloadInputs = 3;
+constexpr int kChainSegments = 4;
 
 // The pass sequence: partials of pass i are the leaves of pass i + 1 and
 // live in a buffer 256-byte aligned, so their row alignment depends only
@@ -514,10 +533,11 @@ int plan_passes(const ChainDev &ch, bool chain, const LeafSrc &src, int64_t oute
         // rows: a row that fits one wave's 16 segments finishes in this pass;
         // a longer one is cut into as many groups as keep >= 1024 waves busy
         // (S = 16 only when there are rows enough), since a pass over few long
-        // groups runs on a handful of waves. A contiguous chain leaf runs one
-        // segment per wave: the interpreter is inlined once per element a
-        // lane holds.
-        const int smax = vec && use_chain ? 1 : 16;
+        // groups runs on a handful of waves. A contiguous chain leaf over up
+        // to kChainPreloadInputs inputs takes up to kChainSegments segments
+        // per wave (the interpreter is inlined once per segment), over more
+        // inputs one.
+        const int smax = vec && use_chain ? (src.n_in <= kChainPreloadInputs ? kChainSegments : 1) : 16;
         int S = 1;
         if (rows) {
             if (cur_n <= unit * smax) {
@@ -649,6 +669,23 @@ int32_t run_reduce(const ChainDev &ch, bool chain, LeafSrc src, int64_t outer, i
 #define CHELIS_ROWS_CASE(SS)                                                                                  \
     case SS:                                                                                                  \
         if (vec) {                                                                                            \
+            if constexpr (kChainable<K> && SS > 1 && SS <= kChainSegments) {                                 \
+                if (use_chain) {                                                                              \
+                    if (s.n_in == 1)                                                                          \
+                        reduce_rows_vec_kernel<T, K, SS, true, 1>                                             \
+                            <<<grid, 256, chain_lds, st>>>(ch, s, outer, cur_n, groups, dst_v, dst_i, last);  \
+                    else if (s.n_in == 2)                                                                     \
+                        reduce_rows_vec_kernel<T, K, SS, true, 2>                                             \
+                            <<<grid, 256, chain_lds, st>>>(ch, s, outer, cur_n, groups, dst_v, dst_i, last);  \
+                    else if (s.n_in == 3)                                                                     \
+                        reduce_rows_vec_kernel<T, K, SS, true, 3>                                             \
+                            <<<grid, 256, chain_lds, st>>>(ch, s, outer, cur_n, groups, dst_v, dst_i, last);  \
+                    else                                                                                      \
+                        return set_error(CHELIS_HIP_EDOMAIN, "reduce: internal chain plan, %d inputs over %d segments", \
+                                         s.n_in, SS);                                                         \
+                    break;                                                                                    \
+                }                                                                                             \
+            }                                                                                                 \
             CHELIS_ROWS_LAUNCH(reduce_rows_vec_kernel, SS, SS == 1, chain_lds)                                \
         }                                                                                                     \
         CHELIS_ROWS_LAUNCH(reduce_rows_kernel, SS, true, 0)

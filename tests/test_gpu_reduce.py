@@ -139,6 +139,34 @@ def test_sum_of_contiguous_chain_leaf(alloc, n, dtype):
     assert bits_equal(C.reduce("max", [dx, dg], 1, chain=ch2).numpy(), O.max_axis(leaf2, 1))
 
 
+CHAINS_BY_INPUTS = {
+    1: ([("mul", 0, 0)], lambda a: a[0] * a[0]),
+    3: ([("sub", 0, 1), ("mul", ("s", 0), 2)], lambda a: (a[0] - a[1]) * a[2]),
+    4: ([("sub", 0, 1), ("sub", 2, 3), ("mul", ("s", 0), ("s", 1))], lambda a: (a[0] - a[1]) * (a[2] - a[3])),
+}
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("n_in", [1, 3, 4])
+@pytest.mark.parametrize("rows,n", [(2048, 4096), (300, 1000), (64, 1001), (8, 2500)])
+def test_contiguous_chain_leaf_by_input_count(n_in, rows, n, dtype):
+    """Chain leaves over 1, 3 and 4 contiguous inputs at row counts and
+    lengths that put 1, 2 or 4 segments on a wave (ragged tails included):
+    sum and max bit-identical to the oracle's tree over the same leaves, the
+    max with NaN leaves in some rows."""
+    rng = np.random.default_rng(rows * 7 + n_in)
+    width = (n + 3) // 4 * 4
+    bufs = [rng.standard_normal((rows, width)).astype(dtype) for _ in range(n_in)]
+    bufs[0][1::5, n // 3] = np.nan
+    arrs = [b[:, :n] for b in bufs]
+    devs = [C.to_device(b).view((rows, n), (width, 1)) for b in bufs]
+    steps, ref = CHAINS_BY_INPUTS[n_in]
+    ch = C.fused_chain(steps)
+    leaf = np.ascontiguousarray(ref(arrs).astype(dtype))
+    assert bits_equal(C.reduce("sum", devs, 1, chain=ch).numpy(), O.sum_axis(leaf, 1))
+    assert bits_equal(C.reduce("max", devs, 1, chain=ch).numpy(), O.max_axis(leaf, 1))
+
+
 @pytest.mark.parametrize("alloc,n", [((6, 4112), 4112), ((6, 4112), 4100), ((3, 16), 5)])
 def test_count_contiguous_rows(alloc, n):
     buf = (np.random.default_rng(n).random(alloc) < 0.6).astype(np.uint8)
