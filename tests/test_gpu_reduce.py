@@ -139,6 +139,28 @@ def test_sum_of_contiguous_chain_leaf(alloc, n, dtype):
     assert bits_equal(C.reduce("max", [dx, dg], 1, chain=ch2).numpy(), O.max_axis(leaf2, 1))
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("shape,axis", [((3, 1000, 256), 1), ((20000, 512), 0), ((130, 4100), 0), ((64, 1030), 0),
+                                        ((16384, 64), 0)])
+def test_column_reductions_with_special_values(shape, axis, dtype):
+    """Column reductions (inner >= 64: four waves per 128-leaf group, one or
+    more partial passes, widths that are and are not multiples of four):
+    sum, max and min bit-identical to the oracle, with NaN, signed zeros and
+    infinities placed in some columns."""
+    rng = np.random.default_rng(sum(shape))
+    x = rng.standard_normal(shape).astype(dtype)
+    flat = x.reshape(-1, shape[-1])
+    flat[5::97, 7] = np.nan
+    flat[:, 9] = -0.0
+    flat[3::11, 9] = 0.0
+    flat[:, 11] = 0.0
+    flat[::13, 13] = -np.inf
+    d = C.to_device(x)
+    assert bits_equal(C.reduce("sum", d, axis).numpy(), O.sum_axis(x, axis))
+    assert bits_equal(C.reduce("max", d, axis).numpy(), O.max_axis(x, axis))
+    assert bits_equal(C.reduce("min", d, axis).numpy(), -O.max_axis(-x, axis))
+
+
 CHAINS_BY_INPUTS = {
     1: ([("mul", 0, 0)], lambda a: a[0] * a[0]),
     3: ([("sub", 0, 1), ("mul", ("s", 0), 2)], lambda a: (a[0] - a[1]) * a[2]),
