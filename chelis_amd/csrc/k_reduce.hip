@@ -73,6 +73,7 @@ struct LeafSrc {
     const void *p[CHELIS_FUSED_MAX_INPUTS];
     int64_t so[CHELIS_FUSED_MAX_INPUTS], sn[CHELIS_FUSED_MAX_INPUTS], si[CHELIS_FUSED_MAX_INPUTS];
     const int64_t *idx;  // partial indices of a previous pass (argmax/argmin), or null
+    int32_t join;        // rows: groups per row (2 or 4) joined inside the workgroup, or 0
 };
 
 // A chain leaf runs on the element's row of LDS slots (run_chain).
@@ -282,6 +283,30 @@ __global__ __launch_bounds__(256) void reduce_rows_vec_kernel(ChainDev ch, LeafS
         sidx[s] = xi;
     }
     ordered_tree<T, K, S>(seg, sidx);
+    if constexpr (CHAIN && NIN > 0 && !has_index(K)) {
+        if (src.join) {
+            // The row's join groups are this workgroup's consecutive waves
+            // (every item in range): their totals are the leaves of the
+            // row's top subtree, joined in order and stored as the result.
+            __shared__ T jv[4];
+            if (lane == 0) jv[threadIdx.x >> 6] = seg[0];
+            __syncthreads();
+            const int w = threadIdx.x >> 6;
+            if (lane == 0 && w % src.join == 0) {
+                T a[4] = {jv[w], jv[w + 1], identity<T, K>(), identity<T, K>()};
+                int64_t ia[4] = {0, 0, 0, 0};
+                if (src.join == 4) {
+                    a[2] = jv[2];
+                    a[3] = jv[3];
+                    ordered_tree<T, K, 4>(a, ia);
+                } else {
+                    combine<T, K>(a[0], ia[0], a[1], ia[1]);
+                }
+                out_v[item / src.join] = finalize<T, K>(a[0]);
+            }
+            return;
+        }
+    }
     if (lane == 0) {
         out_v[item] = last ? finalize<T, K>(seg[0]) : seg[0];
         if (has_index(K)) out_i[item] = sidx[0];
@@ -497,6 +522,7 @@ struct Pass {
     bool cols4;     // columns: four waves per 128-leaf group
     int64_t n;      // leaves per output this pass
     int64_t groups; // partials per output it writes
+    int join = 0;   // rows, chain leaves: 2 or 4 groups joined in the workgroup, the pass writing the result
 };
 constexpr int kMaxPasses = 16;
 // Contiguous chain leaves: the input counts with a compile-time instance
@@ -552,6 +578,14 @@ int plan_passes(const ChainDev &ch, bool chain, const LeafSrc &src, int64_t oute
         const int64_t groups = (cur_n + G - 1) / G;
         passes[i] = Pass{vec, S, cols4, cur_n, groups};
         if (groups == 1) return i + 1;
+        // a contiguous chain leaf over 2 or 4 groups per row, rows filling
+        // whole workgroups: the workgroup joins each row's groups itself
+        // (no second launch)
+        if (rows && vec && use_chain && !has_index(K) && S == kChainSegments && src.n_in <= kChainPreloadInputs &&
+            (groups == 2 || groups == 4) && (outer * groups) % 4 == 0) {
+            passes[i].join = (int)groups;
+            return i + 1;
+        }
         cur_n = groups;
     }
     return kMaxPasses;  // unreachable: each pass divides the leaves by >= 32
@@ -631,6 +665,7 @@ int32_t run_reduce(const ChainDev &ch, bool chain, LeafSrc src, int64_t outer, i
         const bool vec = ps.vec, cols4 = ps.cols4;
         const int S = ps.S;
         LeafSrc s = src;
+        s.join = ps.join;
         if (!first) {
             s.n_in = 1;
             s.p[0] = prev_v;
