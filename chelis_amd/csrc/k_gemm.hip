@@ -553,13 +553,15 @@ int lay_of(int64_t s_outer, int64_t s_k, const void *base, int64_t outer, int64_
     return 2;
 }
 
-// Occupancy of the f32 128-tile kernel without the GELU epilogue: its
-// registers allow three workgroups per CU, but a grid of T tiles then runs in
-// ceil(T / 3C) rounds of three; two per CU (ceil(T / 2C) rounds of two) is
-// chosen when that is fewer workgroup-slots in all, e.g. 1024 tiles on 256
-// CUs run as two full rounds of two rather than a round of three and a third
-// of one (measured 1.42 ms against 1.54 ms at 4096^3), while 768 tiles run
-// as one round of three (344 us against 407 us at 4096 x 3072 x 1024).
+// Occupancy of the f32 128-tile kernel without the GELU epilogue: its 40 KiB
+// of LDS allow three workgroups per CU. Its registers decide first: the
+// current build holds 224 per lane (116 vector + 108 accumulation), two
+// waves per SIMD, so two workgroups per CU. Were the count to drop to 168 or
+// fewer, a grid of T tiles would run in ceil(T / 3C) rounds of three; two
+// per CU (ceil(T / 2C) rounds of two) is then kept when that is fewer
+// workgroup-slots in all, e.g. 1024 tiles on 256 CUs as two full rounds of
+// two rather than a round of three and a third of one (measured 1.42 ms
+// against 1.54 ms at 4096^3 with an earlier build that fitted three).
 // Dynamic LDS beyond a third of the CU's 160 KiB pins two.
 constexpr size_t kPinTwoLds = 16384;
 
