@@ -170,15 +170,16 @@ CHAINS_BY_INPUTS = {
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 @pytest.mark.parametrize("n_in", [1, 3, 4])
-@pytest.mark.parametrize("rows,n", [(2048, 4096), (512, 2000), (513, 2000), (300, 1000), (64, 1001), (8, 2500)])
+@pytest.mark.parametrize("rows,n", [(2048, 4096), (256, 8000), (512, 2000), (513, 2000), (300, 1000), (64, 1001),
+                                    (8, 2500)])
 def test_contiguous_chain_leaf_by_input_count(n_in, rows, n, dtype):
     """Chain leaves over 1, 3 and 4 contiguous inputs at row counts and
     lengths that put 1, 2 or 4 segments on a wave (ragged tails included),
     with the row's 2 or 4 groups joined inside the workgroup ([2048,4096]
-    and [512,2000] f32, [512,2000] f64) or by a second pass ([513,2000]:
-    the rows do not fill whole workgroups): sum and max bit-identical to the
-    oracle's tree over the same leaves, the max with NaN leaves in some
-    rows."""
+    and [512,2000] f32, [512,2000] f64) or by further passes ([513,2000]:
+    the rows do not fill whole workgroups; [256,8000]: more than four
+    groups): sum and max bit-identical to the oracle's tree over the same
+    leaves, the max with NaN leaves in some rows."""
     rng = np.random.default_rng(rows * 7 + n_in)
     width = (n + 3) // 4 * 4
     bufs = [rng.standard_normal((rows, width)).astype(dtype) for _ in range(n_in)]
