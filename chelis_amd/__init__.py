@@ -12,6 +12,7 @@ Loading fails loudly when the library is missing: there is no CPU fallback.
 from __future__ import annotations
 
 import ctypes
+import subprocess
 import os
 from ctypes import POINTER, c_double, c_int32, c_int64, c_uint8, c_uint64, c_void_p
 
@@ -142,6 +143,11 @@ SIGNATURES = {
     "chelis_dag_type": (c_int32, [c_void_p, c_int32, c_int32, POINTER(c_int32), POINTER(c_int64), c_int32,
                                   POINTER(c_int32)]),
     "chelis_dag_peak_device_bytes": (c_int64, [c_void_p]),
+    "chelis_dag_peak_device_bytes_at": (c_int64, [c_void_p, POINTER(c_int64), c_int32]),
+    "chelis_dag_symbol_count": (c_int32, [c_void_p]),
+    "chelis_dag_symbol_name": (ctypes.c_char_p, [c_void_p, c_int32]),
+    "chelis_dag_output_shape": (c_int32, [c_void_p, POINTER(P), c_int32, c_int32, POINTER(c_int32),
+                                          POINTER(c_int64), c_int32]),
     "chelis_dag_launch_count": (c_int64, [c_void_p]),
     "chelis_dag_describe": (ctypes.c_char_p, [c_void_p]),
     "chelis_dag_fuse": (ctypes.c_char_p, [ctypes.c_char_p, c_int64]),
@@ -519,15 +525,17 @@ def program(name: str, inputs, outputs):
     return outputs
 
 
-def device_entry(name: str, inputs, n_out: int):
-    """{name}_device: the reference's generated-entry ABI; returns owned outputs."""
-    ins = (c_void_p * len(inputs))(*[t.owner for t in inputs])
-    outs = (c_void_p * n_out)()
-    getattr(lib(), f"{name}_device")(ins, len(inputs), outs, n_out)
-    return [DeviceTensor(o) for o in outs]
+def device_entry(name: str, inputs, n_out: int, library=None):
+    """{name}_device: the reference's generated-entry ABI; returns owned
+    outputs. `library` is the ctypes library defining it (this one by
+    default)."""
+    ins = (c_void_p * max(1, len(inputs)))(*[t.owner for t in inputs])
+    outs = (c_void_p * max(1, n_out))()
+    getattr(library or lib(), f"{name}_device")(ins, len(inputs), outs, n_out)
+    return [DeviceTensor(outs[k]) for k in range(n_out)]
 
 
-def host_entry(name: str, arrays, n_out: int):
+def host_entry(name: str, arrays, n_out: int, library=None):
     """{name}(chelis_tensor **, int, chelis_tensor **, int): the reference's
     host-tensor entry. numpy arrays in (borrowed as host tensors; a KEY input
     is passed as ("key", bits)), numpy arrays out (copied from the returned
@@ -542,11 +550,11 @@ def host_entry(name: str, arrays, n_out: int):
         shape = (c_int64 * max(1, arr.ndim))(*arr.shape)
         keep.append((arr, shape))
         hosts.append(lib().chelis_tensor_entry_borrow(arr.ndim, shape, tag, arr.ctypes.data, arr.nbytes))
-    ins = (c_void_p * len(hosts))(*hosts)
-    outs = (c_void_p * n_out)()
-    getattr(lib(), name)(ins, len(hosts), outs, n_out)
+    ins = (c_void_p * max(1, len(hosts)))(*hosts)
+    outs = (c_void_p * max(1, n_out))()
+    getattr(library or lib(), name)(ins, len(hosts), outs, n_out)
     result = []
-    for o in outs:
+    for o in outs[:n_out]:
         rank = lib().chelis_tensor_rank(o)
         shape = tuple(lib().chelis_tensor_shape(o, a) for a in range(rank))
         v = lib().chelis_tensor_read_view(o)
@@ -615,14 +623,45 @@ class DagProgram:
 
     @property
     def peak_device_bytes(self) -> int:
+        """Bytes one run needs; -1 when a run-time extent sizes them."""
         return lib().chelis_dag_peak_device_bytes(self.handle)
 
-    def empty_outputs(self):
-        return [DeviceTensor(lib().chelis_device_tensor_alloc(_plan(shape, None, dt))) for _, shape, dt in self.outputs]
+    @property
+    def symbolic_dims(self):
+        """The run-time extents, in binding order."""
+        L = lib()
+        return [L.chelis_dag_symbol_name(self.handle, k).decode() for k in range(L.chelis_dag_symbol_count(self.handle))]
+
+    def peak_device_bytes_at(self, **extents) -> int:
+        names = self.symbolic_dims
+        vals = (c_int64 * max(1, len(names)))(*[int(extents[n]) for n in names])
+        v = lib().chelis_dag_peak_device_bytes_at(self.handle, vals, len(names))
+        if v < 0:
+            raise ChelisError(lib().chelis_hip_last_error().decode(errors="replace"))
+        return v
+
+    def output_shapes(self, inputs):
+        """Each output's shape for these inputs (run-time extents bound)."""
+        ins = (P * max(1, len(inputs)))(*[_p(t) for t in inputs])
+        shapes = []
+        for o in range(lib().chelis_dag_output_count(self.handle)):
+            rank = c_int32()
+            shape = (c_int64 * 16)()
+            check(lib().chelis_dag_output_shape(self.handle, ins, len(inputs), o, ctypes.byref(rank), shape, 16),
+                  "dag output shape")
+            shapes.append(tuple(shape[k] for k in range(rank.value)))
+        return shapes
+
+    def empty_outputs(self, inputs=None):
+        if inputs is None:
+            return [DeviceTensor(lib().chelis_device_tensor_alloc(_plan(shape, None, dt)))
+                    for _, shape, dt in self.outputs]
+        return [DeviceTensor(lib().chelis_device_tensor_alloc(_plan(shape, None, dt)))
+                for shape, (_, _, dt) in zip(self.output_shapes(inputs), self.outputs)]
 
     def run(self, inputs, outputs=None):
         """Enqueue on the library stream; returns the output tensors."""
-        outputs = outputs if outputs is not None else self.empty_outputs()
+        outputs = outputs if outputs is not None else self.empty_outputs(inputs)
         ins = (P * max(1, len(inputs)))(*[_p(t) for t in inputs])
         outs = (P * max(1, len(outputs)))(*[_p(t) for t in outputs])
         check(lib().chelis_dag_run(self.handle, ins, len(inputs), outs, len(outputs)), "dag run")
@@ -660,3 +699,34 @@ class CodegenResult:
         est = L.chelis_codegen_peak_device_bytes_estimate(h)
         self.peak_device_bytes_estimate = None if est < 0 else est
         L.chelis_codegen_release(h)
+
+
+class GeneratedProgram:
+    """chelis_codegen_hip's source compiled with its own compile and link
+    flags into `directory` and loaded: the generated {f}_device and {f}
+    entries, as the reference's Python binding loads a built module
+    (crates/chelis-python/src/lib.rs:406-441)."""
+
+    def __init__(self, json_text: str, func_name: str, directory: str, compiler: str = "g++"):
+        self.result = CodegenResult(json_text, func_name)
+        self.name = func_name
+        src = os.path.join(directory, func_name + ".cpp")
+        with open(src, "w") as fh:
+            fh.write(self.result.c_source)
+        self.path = os.path.join(directory, "lib" + func_name + ".so")
+        cmd = [compiler, "-shared", "-fPIC", *self.result.compile_flags, src, "-o", self.path,
+               *self.result.link_flags]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise ChelisError("generated source failed to build:\n" + r.stderr[-4000:])
+        lib()  # the library the generated code links is loaded first, from this tree
+        self.library = ctypes.CDLL(self.path)
+        self.n_out = len(self.result.output_labels)
+
+    def device(self, inputs):
+        """{f}_device over owned device tensors; returns the owned outputs."""
+        return device_entry(self.name, inputs, self.n_out, self.library)
+
+    def host(self, arrays):
+        """{f} over numpy arrays (host tensors in and out)."""
+        return host_entry(self.name, arrays, self.n_out, self.library)

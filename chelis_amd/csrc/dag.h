@@ -68,6 +68,8 @@ enum class Op : uint8_t {
     Expand, Permute, Reshape, Realize, Copy,
     // fused and specialized forms
     FusedElem, BlasMatmul,
+    // outputs by name, and the extent obligations fusion must not cross
+    Store, ExtentWitness, NamedCast,
     // anything else the reader does not interpret
     Other
 };
@@ -82,12 +84,27 @@ struct Step {
     std::vector<int> args;
 };
 
+// An extent is a literal (>= 0) or the run-time extent of a symbol, coded
+// as -2 - symbol. -1 marks an extent this build cannot bind (a bound read
+// from a node value, or the to-the-end sentinel); Node::extent_error says
+// which, and the planner refuses it.
+constexpr int64_t kUnboundExtent = -1;
+inline bool extent_is_symbol(int64_t e) { return e <= -2; }
+inline int64_t symbol_extent(int64_t symbol) { return -2 - symbol; }
+inline int64_t extent_symbol(int64_t e) { return -2 - e; }
+
+// The ExtentWitness sites whose owner no rewrite may merge away
+// (crates/chelis-dag-core/src/axis_sources.rs:3736-3753).
+enum class WitnessSite : uint8_t { None, LiteralResultClaim, ResultClaim, LocalAscriptionClaim, Other };
+
 struct Node {
     int64_t id = 0;
     Op op = Op::Other;
     std::string variant;  // the op's variant name on the wire
     std::vector<int64_t> inputs, shape_deps, claim_deps;
-    std::vector<int64_t> dims;  // extents (-1: known only at run time)
+    std::vector<int64_t> dims;  // extents (literal or symbol codes, above)
+    std::vector<std::string> dims_raw;  // each DimInfo as read, written back verbatim
+    std::string extent_error;           // why an extent is unbound, if one is
     Prim prec = Prim::Other;
     int64_t reusable = -1;
     bool has_span = false;
@@ -98,9 +115,12 @@ struct Node {
     int64_t axis = 0;               // Sum / MaxReduce / ... / Expand / Softmax
     std::vector<int64_t> axes;      // Permute / Count
     Prim accumulator = Prim::Other; // Sum
-    int64_t size = -1;              // Expand (literal size, -1 otherwise)
-    std::vector<int64_t> new_shape; // Reshape (literal extents, -1 otherwise)
-    std::string name;               // Load
+    int64_t size = -1;              // Expand (extent code)
+    std::vector<int64_t> new_shape; // Reshape (extent codes)
+    std::string name;               // Load / Store; ExtentWitness: the parameter it reads
+    WitnessSite site = WitnessSite::None;  // ExtentWitness
+    std::vector<int64_t> requirements;     // ExtentWitness: literal extents its axis must equal
+    int64_t named_claims = 0;              // ExtentWitness: claims against other witnesses
     std::string compare;            // Compare kind (snake_case wire name)
     Prim const_prec = Prim::Other;  // Const
     uint64_t const_bits = 0;        // float bits, or the integer / bool value
@@ -108,14 +128,21 @@ struct Node {
     Prim cast_to = Prim::Other;     // Cast
     std::string raw_op;             // the op as read (written back verbatim)
 
-    int64_t count() const;  // elements (-1 if any extent is unknown)
+    int64_t count() const;  // elements (-1 if any extent is not a literal)
     double const_value() const;
+    // The inputs whose payload the op reads: an Expand or Reshape reads only
+    // inputs[0] (later inputs are the tensors an InputAxis extent is read
+    // from); a Store reads its one value.
+    size_t payload_inputs() const { return (op == Op::Expand || op == Op::Reshape) ? 1 : inputs.size(); }
 };
 
 struct Graph {
     std::vector<Node> nodes;  // ids are positions, inputs precede users
     std::vector<int64_t> roots;
     std::string declarations = "[]";  // JSON text, carried through
+    std::vector<std::string> symbols;  // run-time extent names, by symbol index
+
+    int64_t symbol(const std::string &name);  // interned index
 };
 
 // Reads the reference's serde Dag; returns false with a message naming the
@@ -127,8 +154,17 @@ std::string write_graph(const Graph &g);
 // fuse.rs:36-121: consumer counts (roots count as consumers), maximal chains
 // of fusible float elementwise nodes where each link is its producer's only
 // consumer and shares its owner, chains of length >= 2 rebuilt as FusedElem
-// nodes. old_to_new maps every old node to its node in the result.
+// nodes; a node that owns a result claim (or a Copy / Cast / NamedCast
+// such a node reads, transitively) neither starts nor joins a chain.
+// old_to_new maps every old node to its node in the result.
 Graph fuse(const Graph &g, std::vector<int64_t> *old_to_new);
+// axis_sources.rs:3693-3753: the nodes whose shape or claim dependencies
+// name a ResultClaim / LiteralResultClaim / LocalAscriptionClaim witness,
+// closed over the first input of Copy, Cast and NamedCast.
+std::vector<bool> claimed_producers(const Graph &g);
+// fuse.rs:76-96 with the activation gate (dag.rs:2864-2880): whether the
+// node may be a chain link at all.
+bool chain_fusible(const Node &n);
 // fuse.rs:463-487: FusedElem nodes whose only consumer is a Sum or
 // MaxReduce (they become that reduction's leaf).
 std::vector<bool> reduction_inlined(const Graph &g);
@@ -178,8 +214,30 @@ struct ValueInfo {
     std::vector<int64_t> layout;
 };
 
+// A workspace range: a literal byte count, or `coef` times the product of
+// the run-time extents `symbols` (symbol indices, repeated for powers)
+// rounded up to 256 bytes. Ranges are laid out back to back in slot order;
+// with run-time extents the offsets are taken per run.
 struct Slot {
-    int64_t offset = 0, bytes = 0;
+    int64_t offset = 0, bytes = 0;  // literal slots
+    int64_t coef = 0;               // run-time slots
+    std::vector<int64_t> symbols;
+    bool symbolic() const { return !symbols.empty(); }
+};
+
+// Where a run-time extent is read: the caller input slot and axis of the
+// first Load declaring it (the reference's canonical binding source,
+// emit.rs:1141-1150); every other Load axis naming it must agree.
+struct SymbolRead {
+    int64_t symbol = -1, input = -1, axis = -1;
+};
+
+// An ExtentWitness requirement checked before a run: the extent of the
+// caller input's axis must equal `required` (spec/04 section 4.7 entry
+// checks; a LiteralResultClaim witness checks nothing there, dag.rs:2582).
+struct ExtentCheck {
+    int64_t input = -1, axis = -1, required = 0;
+    std::string parameter;
 };
 
 struct Plan {
@@ -189,14 +247,39 @@ struct Plan {
     std::vector<int64_t> input_nodes, output_nodes;
     std::vector<std::string> input_labels, output_labels;
     std::vector<Slot> slots;
-    int64_t workspace_bytes = 0;
+    int64_t workspace_bytes = 0;       // -1 when a slot is sized at run time
     std::vector<uint64_t> const_bits;  // one element per constant, stored at its dtype width
     std::vector<Prim> const_prec;
-    int64_t peak_device_bytes = 0;     // workspace + constants + outputs
+    int64_t peak_device_bytes = 0;     // workspace + constants; -1 when sized at run time
+    // run-time extents: symbolic_dims lists the graph's symbols in binding
+    // order (their names); binds[k] reads symbolic_dims[k]; checks are the
+    // other Load axes that must agree with a bound symbol
+    std::vector<int64_t> symbolic_dims;
+    std::vector<SymbolRead> binds, checks;
+    std::vector<ExtentCheck> extent_checks;
 };
 
 bool build_plan(const Graph &input, Plan *plan, std::string *error);
 std::string describe_plan(const Plan &plan);
+
+// Run-time extents. values[s] is the extent of graph symbol s.
+inline int64_t resolve_extent(int64_t e, const std::vector<int64_t> &values) {
+    return extent_is_symbol(e) ? values[(size_t)extent_symbol(e)] : e;
+}
+std::vector<int64_t> resolve_dims(const std::vector<int64_t> &dims, const std::vector<int64_t> &values);
+// Reads every symbol from the input shapes (rank-checked by the caller) and
+// checks the agreeing axes; false with a message naming the input, axis
+// and symbol on a mismatch or a negative extent.
+bool bind_symbols(const Plan &plan, const int64_t *const *input_shapes, const int32_t *input_ranks,
+                  std::vector<int64_t> *values, std::string *error);
+// Lays the slots out for these extents: offsets[k], and the workspace size.
+// False when a size overflows.
+bool layout_slots(const Plan &plan, const std::vector<int64_t> &values, std::vector<int64_t> *offsets,
+                  int64_t *workspace);
+// The peak formula's text: one term per slot (a literal, or coef * names
+// with a round_up(.., 256) where the coefficient is not a multiple of 256),
+// then the constant pool; "0" when empty.
+std::string peak_formula(const Plan &plan);
 
 }  // namespace dag
 }  // namespace chelis

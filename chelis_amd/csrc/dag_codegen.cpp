@@ -1,18 +1,24 @@
 // The codegen surface (include/chelis_dag.h): what codegen_hip returns in
 // the reference (HipCodegenResult, crates/chelis-backend-hip/src/lib.rs:
 // 32-53,104-167), for this library. The generated host C++ embeds the DAG
-// and its launch plan, and defines the two generated entries with the
-// reference's contracts:
+// and defines the two generated entries with the reference's contracts and
+// diagnostics:
 //   {f}         host tensors in and out (emit.rs:667-808): count checks that
-//               print "{f}: expected N inputs, got M" and abort, inputs
-//               copied to fresh device tensors, outputs from chelis_alloc
-//               under a write lease, device synchronized before return;
+//               print "{f}: expected N inputs, got M" and abort, the input
+//               shape preamble (emit.rs:1081-1200), inputs copied to fresh
+//               device tensors, outputs from chelis_alloc under a write
+//               lease, device synchronized before return;
 //   {f}_device  device owners in, owned contiguous outputs
-//               (emit.rs:838-964, spec/11-ffi.md:144-156): null arrays, a
-//               wrong count or an input on another device trap `domain`.
-// The program is planned once per process, on first call.
+//               (emit.rs:838-964, spec/11-ffi.md:144-156): count checks,
+//               null arrays trap "domain in entry", an input on another
+//               device traps "domain in device_entry", then the device
+//               shape preamble (emit.rs:1309-1395).
+// Run-time extents are read from the inputs that declare them (the
+// preamble's `chelis_device_metadata <name>` bindings) and size the outputs;
+// the program is planned once per process, on first call.
 #include <dlfcn.h>
 
+#include <algorithm>
 #include <string>
 #include <vector>
 
@@ -57,94 +63,290 @@ std::string c_string_lines(const std::string &text) {
     return out;
 }
 
-std::string dims_text(const Node &n) {
-    std::string s = "{";
-    for (size_t a = 0; a < n.dims.size(); ++a) s += (a ? ", " : "") + std::to_string(n.dims[a]);
-    return s + "}";
+// C source text of a string literal's contents, with '%' doubled so it can
+// sit inside a printf format (the reference's sanitize_for_format_string).
+std::string fmt_text(const std::string &s) {
+    std::string q = json_quote(s);
+    q = q.substr(1, q.size() - 2);
+    std::string out;
+    for (char c : q) {
+        if (c == '%') out += "%%";
+        else out += c;
+    }
+    return out;
+}
+
+const char *dtype_macro(Prim p) {
+    switch (p) {
+        case Prim::F32: return "CHELIS_DTYPE_F32";
+        case Prim::F64: return "CHELIS_DTYPE_F64";
+        case Prim::Int32: return "CHELIS_DTYPE_I32";
+        case Prim::Bool: return "CHELIS_DTYPE_BOOL";
+        case Prim::Int64: return "CHELIS_DTYPE_I64";
+        case Prim::Bf16: return "CHELIS_DTYPE_BF16";
+        case Prim::F16: return "CHELIS_DTYPE_F16";
+        case Prim::Int8: return "CHELIS_DTYPE_I8";
+        case Prim::Int16: return "CHELIS_DTYPE_I16";
+        case Prim::Key: return "CHELIS_DTYPE_KEY";
+        default: return "255";
+    }
+}
+
+// The C variable a run-time extent is bound to: its own name when that is
+// an identifier (as the reference emits it), else a numbered stand-in.
+std::string symbol_var(const Graph &g, int64_t sym) {
+    const std::string &name = g.symbols[(size_t)sym];
+    return identifier(name) && name.rfind("chelis_", 0) != 0 ? name : "chelis_sym_" + std::to_string(sym);
+}
+
+struct Lines {
+    std::string text;
+    int indent = 1;
+    void line(const std::string &l) { text += (l.empty() ? std::string() : std::string(4 * indent, ' ') + l) + "\n"; }
+};
+
+// The input shape preamble of either entry (emit.rs:1081-1200 host,
+// :1309-1395 device): the host entry reads the runtime tensors, the device
+// entry the owners' packets; then the symbol bindings, the witness
+// requirements and the output shapes.
+void shape_preamble(Lines &e, const Plan &plan, const std::string &f, bool device) {
+    const Graph &g = plan.graph;
+    std::vector<size_t> order(plan.input_labels.size());
+    for (size_t k = 0; k < order.size(); ++k) order[k] = k;
+    std::sort(order.begin(), order.end(),
+              [&](size_t x, size_t y) { return plan.input_labels[x] < plan.input_labels[y]; });
+    const std::string fn = fmt_text(f) + (device ? "_device" : "");
+    for (size_t slot : order) {
+        const Node &ld = g.nodes[plan.input_nodes[slot]];
+        const std::string s = std::to_string(slot), label = fmt_text(plan.input_labels[slot]);
+        e.line("if (inputs[" + s + "] == NULL) {");
+        e.line("    fprintf(stderr, \"" + fn + ": input `" + label + "` at slot " + s + " is NULL\\n\");");
+        e.line("    abort();");
+        e.line("}");
+        std::string dtype, rank, shape;
+        if (device) {
+            e.line("const chelis_gpu_tensor *input_view_" + s + " = chelis_device_tensor_view(inputs[" + s + "]);");
+            dtype = "input_view_" + s + "->dtype";
+            rank = "input_view_" + s + "->rank";
+            shape = "input_view_" + s + "->shape[";
+        } else {
+            dtype = "chelis_tensor_read_view(inputs[" + s + "]).dtype";
+            rank = "chelis_tensor_rank(inputs[" + s + "])";
+            shape = "chelis_tensor_shape(inputs[" + s + "], ";
+        }
+        const std::string close = device ? "]" : ")";
+        e.line("if (" + dtype + " != " + dtype_macro(ld.prec) +
+               ") chelis_numeric_trap(\"numeric trap: domain in load at i64\");");
+        const std::string r = std::to_string(ld.dims.size());
+        e.line("if (" + rank + " != " + r + ") {");
+        e.line("    fprintf(stderr, \"" + fn + ": input `" + label + "` expected rank " + r + ", got %d\\n\", " + rank +
+               ");");
+        e.line("    abort();");
+        e.line("}");
+        for (size_t a = 0; a < ld.dims.size(); ++a) {
+            if (extent_is_symbol(ld.dims[a])) continue;
+            const std::string ax = std::to_string(a), want = std::to_string(ld.dims[a]);
+            e.line("if (" + shape + ax + close + " != " + want + ") {");
+            e.line("    fprintf(stderr, \"" + fn + ": input `" + label + "` axis " + ax + " expected " + want +
+                   ", got %lld\\n\", (long long)" + shape + ax + close + ");");
+            e.line("    abort();");
+            e.line("}");
+        }
+    }
+    for (const SymbolRead &b : plan.binds) {
+        const std::string var = symbol_var(g, b.symbol), name = fmt_text(g.symbols[(size_t)b.symbol]);
+        auto read = [&](const SymbolRead &r) {
+            return device ? "input_view_" + std::to_string(r.input) + "->shape[" + std::to_string(r.axis) + "]"
+                          : "chelis_tensor_shape(inputs[" + std::to_string(r.input) + "], " + std::to_string(r.axis) +
+                                ")";
+        };
+        e.line("chelis_device_metadata " + var + " = " + read(b) + ";");
+        for (const SymbolRead &c : plan.checks) {
+            if (c.symbol != b.symbol) continue;
+            e.line("if (" + read(c) + " != " + var + ") {");
+            e.line("    fprintf(stderr, \"" + fn + ": symbolic dim `" + name + "` mismatch: " +
+                   fmt_text(plan.input_labels[c.input]) + "[" + std::to_string(c.axis) + "]=%lld but " + name +
+                   "=%lld\\n\", (long long)" + read(c) + ", (long long)" + var + ");");
+            e.line("    abort();");
+            e.line("}");
+        }
+    }
+    for (const ExtentCheck &c : plan.extent_checks) {
+        const std::string rd = device ? "input_view_" + std::to_string(c.input) + "->shape[" + std::to_string(c.axis) + "]"
+                                      : "chelis_tensor_shape(inputs[" + std::to_string(c.input) + "], " +
+                                            std::to_string(c.axis) + ")";
+        e.line("if (" + rd + " != " + std::to_string(c.required) + ") {");
+        e.line("    fprintf(stderr, \"extent `" + fmt_text(c.parameter) + "`: claimed = %lld, " +
+               fmt_text(c.parameter) + " axis " + std::to_string(c.axis) + " = %lld\\n\", (long long)" +
+               std::to_string(c.required) + ", (long long)" + rd + ");");
+        e.line("    chelis_numeric_trap(\"numeric trap: domain in load at i64\");");
+        e.line("}");
+    }
+    // output shapes from the literal extents and the bound symbols
+    for (size_t o = 0; o < plan.output_nodes.size(); ++o) {
+        const Node &nd = g.nodes[plan.output_nodes[o]];
+        std::string dims;
+        for (size_t a = 0; a < nd.dims.size(); ++a)
+            dims += (a ? ", " : "") +
+                    (extent_is_symbol(nd.dims[a]) ? symbol_var(g, extent_symbol(nd.dims[a])) : std::to_string(nd.dims[a]));
+        e.line("chelis_device_metadata chelis_output_shape_" + std::to_string(o) + "[" +
+               std::to_string(std::max<size_t>(nd.dims.size(), 1)) + "] = { " + (dims.empty() ? "1" : dims) + " };");
+    }
 }
 
 std::string emit_source(const Plan &plan, const Graph &fused, const std::string &f) {
     const Graph &g = plan.graph;
     std::string s;
     s += "// Generated by chelis_codegen_hip for `" + f + "` (gfx950): " + std::to_string(plan.regions.size()) +
-         " launches, workspace " + std::to_string(plan.workspace_bytes) + " bytes.\n";
+         " launches; peak device bytes " + peak_formula(plan) + ".\n";
     s += "// Launch plan (index, region kind, result node, input nodes):\n";
     const std::string d = describe_plan(plan);
     size_t start = 0;
     while (start < d.size()) {
         const size_t end = d.find('\n', start);
+        if (end == start) break;
         s += "//   " + d.substr(start, end - start) + "\n";
         if (end == std::string::npos) break;
         start = end + 1;
     }
-    s += "#include <hip/hip_runtime_api.h>\n\n#include <cstdio>\n#include <cstdlib>\n#include <mutex>\n"
-         "#include <vector>\n\n#include \"chelis_dag.h\"\n#include \"chelis_device_owner.h\"\n#include \"chelis_hip.h\"\n\n";
+    s += "#include <hip/hip_runtime_api.h>\n\n#include <cstdio>\n#include <cstdlib>\n#include <mutex>\n\n"
+         "#include \"chelis_dag.h\"\n#include \"chelis_device_owner.h\"\n#include \"chelis_hip.h\"\n"
+         "#include \"chelis_runtime.h\"\n\n";
     s += "namespace {\n\n";
     s += "// the fused DAG this program was planned from (crates/chelis-dag-core wire form)\n";
     s += "const char kDag[] =\n" + c_string_lines(write_graph(fused)) + "    ;\n\n";
     const size_t n_in = plan.input_nodes.size(), n_out = plan.output_nodes.size();
-    s += "constexpr int kInputs = " + std::to_string(n_in) + ", kOutputs = " + std::to_string(n_out) + ";\n";
-    s += "const std::vector<std::vector<int64_t>> kOutputShapes = {";
-    for (size_t o = 0; o < n_out; ++o) s += (o ? ", " : "") + dims_text(g.nodes[plan.output_nodes[o]]);
-    s += "};\nconst chelis_dtype kOutputDtypes[] = {";
-    for (size_t o = 0; o < n_out; ++o) s += (o ? ", " : "") + std::to_string((int)prim_dtype(g.nodes[plan.output_nodes[o]].prec));
+    s += "const chelis_dtype kOutputDtypes[] = {";
+    for (size_t o = 0; o < n_out; ++o) s += (o ? ", " : "") + std::string(dtype_macro(g.nodes[plan.output_nodes[o]].prec));
+    if (!n_out) s += "0";
     s += "};\n\n";
-    s += "[[noreturn]] void trap_domain(const char *what) {\n"
-         "    std::fprintf(stderr, \"numeric trap: domain in " + f + " at device entry: %s\\n\", what);\n"
-         "    std::fflush(stdout);\n    std::fflush(stderr);\n    std::exit(1);\n}\n\n";
     s += "chelis_dag_program *program() {\n"
          "    static std::once_flag once;\n    static chelis_dag_program *p = nullptr;\n"
          "    std::call_once(once, [] { p = chelis_dag_compile(kDag, (int64_t)(sizeof kDag - 1)); });\n"
-         "    if (!p) {\n        std::fprintf(stderr, \"" + f + ": %s\\n\", chelis_hip_last_error());\n"
-         "        std::abort();\n    }\n    return p;\n}\n\n";
-    s += "chelis_device_tensor_owner *device_tensor(const std::vector<int64_t> &shape, chelis_dtype dtype) {\n"
-         "    std::vector<chelis_scalar> dims;\n"
-         "    for (int64_t e : shape) dims.push_back(chelis_scalar_from_bits(CHELIS_DTYPE_I64, (uint64_t)e));\n"
+         "    if (!p) {\n        fprintf(stderr, \"" + fmt_text(f) + ": %s\\n\", chelis_hip_last_error());\n"
+         "        abort();\n    }\n    return p;\n}\n\n";
+    s += "void hip_check(hipError_t e) {\n    if (e != hipSuccess) {\n"
+         "        fprintf(stderr, \"HIP error: %s\\n\", hipGetErrorString(e));\n        abort();\n    }\n}\n\n";
+    s += "chelis_device_tensor_owner *device_tensor(const chelis_device_metadata *shape, int32_t rank, "
+         "chelis_dtype dtype) {\n"
+         "    chelis_scalar dims[16];\n"
+         "    for (int32_t a = 0; a < rank; ++a) dims[a] = chelis_scalar_from_bits(CHELIS_DTYPE_I64, (uint64_t)shape[a]);\n"
          "    chelis_scalar exemplar{};\n    exemplar.dtype = dtype;\n"
          "    return chelis_device_tensor_alloc(chelis_metadata_plan_new(\n"
-         "        chelis_scalar_from_bits(CHELIS_DTYPE_I64, (uint64_t)shape.size()), dims.empty() ? nullptr : dims.data(),\n"
-         "        exemplar));\n}\n\n}  // namespace\n\n";
+         "        chelis_scalar_from_bits(CHELIS_DTYPE_I64, (uint64_t)rank), rank ? dims : nullptr, exemplar));\n}\n\n";
+    // the run after the preamble: outputs allocated, the plan enqueued,
+    // failures reported as the reference reports them
+    auto run_tail = [&](Lines &e, bool device) {
+        e.line("const chelis_gpu_tensor *chelis_in[" + std::to_string(std::max<size_t>(n_in, 1)) + "];");
+        e.line("const chelis_gpu_tensor *chelis_out[" + std::to_string(std::max<size_t>(n_out, 1)) + "];");
+        if (device) {
+            for (size_t i = 0; i < n_in; ++i)
+                e.line("chelis_in[" + std::to_string(i) + "] = input_view_" + std::to_string(i) + ";");
+        } else {
+            for (size_t i = 0; i < n_in; ++i) {
+                const std::string k = std::to_string(i);
+                e.line("chelis_device_metadata host_shape_" + k + "[16];");
+                e.line("for (int32_t a = 0; a < chelis_tensor_rank(inputs[" + k + "]); ++a) host_shape_" + k +
+                       "[a] = chelis_tensor_shape(inputs[" + k + "], a);");
+                e.line("chelis_device_tensor_owner *din_" + k + " = device_tensor(host_shape_" + k +
+                       ", chelis_tensor_rank(inputs[" + k + "]), chelis_tensor_read_view(inputs[" + k + "]).dtype);");
+                e.line("chelis_device_tensor_copy_from_host(din_" + k + ", inputs[" + k + "]);");
+                e.line("chelis_in[" + k + "] = chelis_device_tensor_view(din_" + k + ");");
+            }
+        }
+        for (size_t o = 0; o < n_out; ++o) {
+            const std::string k = std::to_string(o);
+            const Node &nd = g.nodes[plan.output_nodes[o]];
+            const std::string owner = device ? "outputs[" + k + "]" : "dout_" + k;
+            e.line(std::string(device ? "" : "chelis_device_tensor_owner *") + owner + " = device_tensor(chelis_output_shape_" +
+                   k + ", " + std::to_string(nd.dims.size()) + ", kOutputDtypes[" + k + "]);");
+            e.line("chelis_out[" + k + "] = chelis_device_tensor_view(" + owner + ");");
+        }
+        e.line("const int32_t status = chelis_dag_run(program(), chelis_in, " + std::to_string(n_in) + ", chelis_out, " +
+               std::to_string(n_out) + ");");
+        e.line("if (status == CHELIS_HIP_EDOMAIN) {");
+        e.line("    fprintf(stderr, \"%s\\n\", chelis_hip_last_error());");
+        e.line("    chelis_numeric_trap(\"numeric trap: domain in launch at i64\");");
+        e.line("}");
+        e.line("if (status != CHELIS_HIP_OK) {");
+        e.line("    fprintf(stderr, \"" + fmt_text(f) + ": %s\\n\", chelis_hip_last_error());");
+        e.line("    abort();");
+        e.line("}");
+        e.line("int32_t chelis_count_error = 0;");
+        e.line("if (chelis_hip_trap_status(&chelis_count_error) != CHELIS_HIP_OK) abort();");
+        e.line("if (chelis_count_error) {");
+        e.line("    fprintf(stderr, \"numeric trap: domain in count at bool\");");
+        e.line("    fprintf(stderr, \"\\n\");");
+        e.line("    abort();");
+        e.line("}");
+        if (!device) {
+            for (size_t o = 0; o < n_out; ++o) {
+                const std::string k = std::to_string(o);
+                const Node &nd = g.nodes[plan.output_nodes[o]];
+                e.line("outputs[" + k + "] = chelis_alloc(" + std::to_string(nd.dims.size()) + ", chelis_output_shape_" +
+                       k + ", kOutputDtypes[" + k + "]);");
+                e.line("{");
+                e.line("    chelis_tensor_write *lease = chelis_tensor_begin_write(outputs[" + k + "]);");
+                e.line("    chelis_device_tensor_copy_to_host(lease, dout_" + k + ");");
+                e.line("    chelis_tensor_end_write(lease);");
+                e.line("}");
+            }
+        }
+        e.line("hip_check(hipDeviceSynchronize());");
+        if (!device) {
+            for (size_t o = 0; o < n_out; ++o) e.line("chelis_device_tensor_release(dout_" + std::to_string(o) + ");");
+            for (size_t i = 0; i < n_in; ++i) e.line("chelis_device_tensor_release(din_" + std::to_string(i) + ");");
+        }
+    };
+    s += "}  // namespace\n\n";
+    const std::string fn = fmt_text(f);
     // {f}_device
-    s += "extern \"C\" void " + f + "_device(const chelis_device_tensor_owner *const *inputs, chelis_device_rank n_in,\n"
-         "        chelis_device_tensor_owner **outputs, chelis_device_rank n_out) {\n"
-         "    if (!inputs || !outputs || n_in != kInputs || n_out != kOutputs) trap_domain(\"arity\");\n"
-         "    int device = -1;\n    if (hipGetDevice(&device) != hipSuccess) std::abort();\n"
-         "    std::vector<const chelis_gpu_tensor *> in(kInputs), out(kOutputs);\n"
-         "    for (int i = 0; i < kInputs; ++i) {\n"
-         "        if (!inputs[i] || chelis_device_tensor_device(inputs[i]) != device) trap_domain(\"input device\");\n"
-         "        in[i] = chelis_device_tensor_view(inputs[i]);\n    }\n"
-         "    for (int o = 0; o < kOutputs; ++o) {\n"
-         "        outputs[o] = device_tensor(kOutputShapes[o], kOutputDtypes[o]);\n"
-         "        out[o] = chelis_device_tensor_view(outputs[o]);\n    }\n"
-         "    if (chelis_dag_run(program(), in.data(), kInputs, out.data(), kOutputs) != CHELIS_HIP_OK)\n"
-         "        trap_domain(chelis_hip_last_error());\n"
-         "    int32_t trap = 0;\n"
-         "    if (chelis_hip_trap_status(&trap) != CHELIS_HIP_OK) std::abort();\n"
-         "    if (trap) {\n        std::fprintf(stderr, \"numeric trap: domain in count at bool\\n\");\n"
-         "        std::abort();\n    }\n"
-         "    if (hipDeviceSynchronize() != hipSuccess) std::abort();\n}\n\n";
+    {
+        Lines e;
+        e.line("if (n_in != " + std::to_string(n_in) + ") {");
+        e.line("    fprintf(stderr, \"" + fn + "_device: expected %d inputs, got %d\\n\", " + std::to_string(n_in) +
+               ", n_in);");
+        e.line("    abort();");
+        e.line("}");
+        e.line("if (n_out != " + std::to_string(n_out) + ") {");
+        e.line("    fprintf(stderr, \"" + fn + "_device: expected %d outputs, got %d\\n\", " + std::to_string(n_out) +
+               ", n_out);");
+        e.line("    abort();");
+        e.line("}");
+        e.line("");
+        e.line("if ((n_in > 0 && inputs == NULL) || (n_out > 0 && outputs == NULL)) chelis_numeric_trap(\"numeric trap: "
+               "domain in entry at i64\");");
+        e.line("int current_device = 0;");
+        e.line("hip_check(hipGetDevice(&current_device));");
+        e.line("for (chelis_device_rank slot = 0; slot < n_in; ++slot) if (chelis_device_tensor_device(inputs[slot]) != "
+               "current_device) chelis_numeric_trap(\"numeric trap: domain in device_entry at i64\");");
+        shape_preamble(e, plan, f, true);
+        e.line("");
+        run_tail(e, true);
+        s += "extern \"C\" void " + f + "_device(const chelis_device_tensor_owner *const *inputs, chelis_device_rank n_in, "
+             "chelis_device_tensor_owner **outputs, chelis_device_rank n_out) {\n" + e.text + "}\n\n";
+    }
     // {f}
-    s += "extern \"C\" void " + f + "(chelis_tensor **inputs, int n_in, chelis_tensor **outputs, int n_out) {\n"
-         "    if (n_in != kInputs) {\n        std::fprintf(stderr, \"" + f +
-         ": expected %d inputs, got %d\\n\", kInputs, n_in);\n        std::abort();\n    }\n"
-         "    if (n_out != kOutputs) {\n        std::fprintf(stderr, \"" + f +
-         ": expected %d outputs, got %d\\n\", kOutputs, n_out);\n        std::abort();\n    }\n"
-         "    std::vector<chelis_device_tensor_owner *> din(kInputs), dout(kOutputs);\n"
-         "    for (int i = 0; i < kInputs; ++i) {\n"
-         "        std::vector<int64_t> shape(chelis_tensor_rank(inputs[i]));\n"
-         "        for (size_t a = 0; a < shape.size(); ++a) shape[a] = chelis_tensor_shape(inputs[i], (int32_t)a);\n"
-         "        din[i] = device_tensor(shape, chelis_tensor_read_view(inputs[i]).dtype);\n"
-         "        chelis_device_tensor_copy_from_host(din[i], inputs[i]);\n    }\n"
-         "    " + f + "_device(din.data(), kInputs, dout.data(), kOutputs);\n"
-         "    for (int o = 0; o < kOutputs; ++o) {\n"
-         "        const std::vector<int64_t> &shape = kOutputShapes[o];\n"
-         "        outputs[o] = chelis_alloc((int32_t)shape.size(), shape.empty() ? nullptr : shape.data(), kOutputDtypes[o]);\n"
-         "        chelis_tensor_write *lease = chelis_tensor_begin_write(outputs[o]);\n"
-         "        chelis_device_tensor_copy_to_host(lease, dout[o]);\n"
-         "        chelis_tensor_end_write(lease);\n    }\n"
-         "    if (hipDeviceSynchronize() != hipSuccess) std::abort();\n"
-         "    for (auto *t : dout) chelis_device_tensor_release(t);\n"
-         "    for (auto *t : din) chelis_device_tensor_release(t);\n}\n";
+    {
+        Lines e;
+        e.line("if (n_in != " + std::to_string(n_in) + ") {");
+        e.line("    fprintf(stderr, \"" + fn + ": expected %d inputs, got %d\\n\", " + std::to_string(n_in) + ", n_in);");
+        e.line("    abort();");
+        e.line("}");
+        e.line("if (n_out != " + std::to_string(n_out) + ") {");
+        e.line("    fprintf(stderr, \"" + fn + ": expected %d outputs, got %d\\n\", " + std::to_string(n_out) +
+               ", n_out);");
+        e.line("    abort();");
+        e.line("}");
+        e.line("");
+        e.line("if ((n_in > 0 && inputs == NULL) || (n_out > 0 && outputs == NULL)) chelis_numeric_trap(\"numeric trap: "
+               "domain in entry at i64\");");
+        shape_preamble(e, plan, f, false);
+        e.line("");
+        run_tail(e, false);
+        s += "extern \"C\" void " + f + "(chelis_tensor **inputs, int n_in, chelis_tensor **outputs, int n_out) {\n" +
+             e.text + "}\n";
+    }
     return s;
 }
 
@@ -185,12 +387,8 @@ extern "C" chelis_hip_codegen_result *chelis_codegen_hip(const char *json, int64
         r->lists[1] = {"-L" + lib, "-lchelis_hip", "-Wl,-rpath," + lib, "-L/opt/rocm/lib", "-lamdhip64"};
         r->lists[2] = plan.input_labels;
         r->lists[3] = plan.output_labels;
-        // every extent of these programs is a literal: nothing is bound at run time
-        std::string formula;
-        for (const Slot &s : plan.slots) formula += (formula.empty() ? "" : " + ") + std::to_string(s.bytes);
-        if (!plan.const_bits.empty())
-            formula += (formula.empty() ? "" : " + ") + std::to_string(8 * plan.const_bits.size());
-        r->formula = formula.empty() ? "0" : formula;
+        for (int64_t sym : plan.symbolic_dims) r->lists[4].push_back(plan.graph.symbols[(size_t)sym]);
+        r->formula = peak_formula(plan);
         r->estimate = plan.peak_device_bytes;
         return r;
     } catch (const std::exception &e) {

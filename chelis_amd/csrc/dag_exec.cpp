@@ -102,11 +102,48 @@ bool reshape_view(const Packet &in, const std::vector<int64_t> &shape, std::vect
     return oi == os.size();
 }
 
-bool type_matches(const Node &n, const chelis_gpu_tensor *t) {
-    if (!t || t->rank != (int32_t)n.dims.size() || t->dtype != prim_dtype(n.prec)) return false;
+bool rank_and_dtype_match(const Node &n, const chelis_gpu_tensor *t) {
+    return t && t->rank == (int32_t)n.dims.size() && t->dtype == prim_dtype(n.prec);
+}
+
+bool type_matches(const Node &n, const chelis_gpu_tensor *t, const std::vector<int64_t> &values) {
+    if (!rank_and_dtype_match(n, t)) return false;
     for (size_t a = 0; a < n.dims.size(); ++a)
-        if (n.dims[a] >= 0 && t->shape[a] != n.dims[a]) return false;
+        if (t->shape[a] != resolve_extent(n.dims[a], values)) return false;
     return true;
+}
+
+// Checks the inputs' ranks and dtypes and reads the run-time extents.
+int32_t bind_inputs(const Plan &P, const chelis_gpu_tensor *const *inputs, int32_t n_in,
+                    std::vector<int64_t> *values) {
+    const Graph &g = P.graph;
+    if (n_in != (int32_t)P.input_nodes.size())
+        return set_error(CHELIS_HIP_EDOMAIN, "dag: expected %zu inputs, got %d", P.input_nodes.size(), n_in);
+    if (n_in && !inputs) return set_error(CHELIS_HIP_EDOMAIN, "dag: null packet array");
+    std::vector<const int64_t *> shapes((size_t)n_in);
+    std::vector<int32_t> ranks((size_t)n_in);
+    for (int32_t i = 0; i < n_in; ++i) {
+        if (int32_t s = check_tensor(inputs[i], "dag input")) return s;
+        if (!rank_and_dtype_match(g.nodes[P.input_nodes[i]], inputs[i]))
+            return set_error(CHELIS_HIP_EDOMAIN, "dag: input %d (%s) does not have the program's rank and dtype", i,
+                             P.input_labels[i].c_str());
+        shapes[i] = inputs[i]->shape;
+        ranks[i] = inputs[i]->rank;
+    }
+    std::string why;
+    if (!bind_symbols(P, shapes.data(), ranks.data(), values, &why))
+        return set_error(CHELIS_HIP_EDOMAIN, "dag: %s", why.c_str());
+    for (int32_t i = 0; i < n_in; ++i)
+        if (!type_matches(g.nodes[P.input_nodes[i]], inputs[i], *values))
+            return set_error(CHELIS_HIP_EDOMAIN, "dag: input %d (%s) does not have the program's shape", i,
+                             P.input_labels[i].c_str());
+    for (const ExtentCheck &c : P.extent_checks) {
+        const int64_t got = inputs[c.input]->shape[c.axis];
+        if (got != c.required)
+            return set_error(CHELIS_HIP_EDOMAIN, "dag: extent `%s` axis %lld: claimed = %lld, got %lld",
+                             c.parameter.c_str(), (long long)c.axis, (long long)c.required, (long long)got);
+    }
+    return CHELIS_HIP_OK;
 }
 
 int32_t constant_pool(chelis_dag_program *prog, void **pool) {
@@ -150,37 +187,35 @@ int32_t run_plan(chelis_dag_program *prog, const chelis_gpu_tensor *const *input
                  const chelis_gpu_tensor *const *outputs, int32_t n_out) {
     const Plan &P = prog->plan;
     const Graph &g = P.graph;
-    if (n_in != (int32_t)P.input_nodes.size() || n_out != (int32_t)P.output_nodes.size())
-        return set_error(CHELIS_HIP_EDOMAIN, "dag: expected %zu inputs and %zu outputs, got %d and %d",
-                         P.input_nodes.size(), P.output_nodes.size(), n_in, n_out);
-    if ((n_in && !inputs) || (n_out && !outputs)) return set_error(CHELIS_HIP_EDOMAIN, "dag: null packet array");
-    for (int32_t i = 0; i < n_in; ++i) {
-        if (int32_t s = check_tensor(inputs[i], "dag input")) return s;
-        if (!type_matches(g.nodes[P.input_nodes[i]], inputs[i]))
-            return set_error(CHELIS_HIP_EDOMAIN, "dag: input %d (%s) does not have the program's shape and dtype", i,
-                             P.input_labels[i].c_str());
-    }
+    if (n_out != (int32_t)P.output_nodes.size())
+        return set_error(CHELIS_HIP_EDOMAIN, "dag: expected %zu outputs, got %d", P.output_nodes.size(), n_out);
+    if (n_out && !outputs) return set_error(CHELIS_HIP_EDOMAIN, "dag: null packet array");
+    std::vector<int64_t> values;
+    if (int32_t s = bind_inputs(P, inputs, n_in, &values)) return s;
     for (int32_t o = 0; o < n_out; ++o) {
         if (int32_t s = check_tensor(outputs[o], "dag output")) return s;
-        if (!type_matches(g.nodes[P.output_nodes[o]], outputs[o]))
+        if (!type_matches(g.nodes[P.output_nodes[o]], outputs[o], values))
             return set_error(CHELIS_HIP_EDOMAIN, "dag: output %d (%s) does not have the program's shape and dtype", o,
                              P.output_labels[o].c_str());
     }
+    std::vector<int64_t> offsets;
+    int64_t workspace = 0;
+    if (!layout_slots(P, values, &offsets, &workspace))
+        return set_error(CHELIS_HIP_EDOMAIN, "dag: the workspace for these extents overflows");
     hipStream_t st = stream();
     if (!st) return set_error(CHELIS_HIP_EHIP, "no HIP device");
     void *pool = nullptr;
     if (int32_t s = constant_pool(prog, &pool)) return s;
     char *ws = nullptr;
-    if (P.workspace_bytes) {
-        ws = static_cast<char *>(scratch_alloc((size_t)P.workspace_bytes));
-        if (!ws) return set_error(CHELIS_HIP_EHIP, "dag: cannot allocate a %lld-byte workspace",
-                                  (long long)P.workspace_bytes);
+    if (workspace) {
+        ws = static_cast<char *>(scratch_alloc((size_t)workspace));
+        if (!ws) return set_error(CHELIS_HIP_EHIP, "dag: cannot allocate a %lld-byte workspace", (long long)workspace);
     }
     struct Release {
         char *p;
         size_t n;
         ~Release() { scratch_free(p, n); }
-    } release{ws, (size_t)P.workspace_bytes};
+    } release{ws, (size_t)workspace};
     // ---- packets
     std::vector<Packet> pk(g.nodes.size());
     auto from = [](Packet &p, const chelis_gpu_tensor *t) {
@@ -194,11 +229,12 @@ int32_t run_plan(chelis_dag_program *prog, const chelis_gpu_tensor *const *input
     for (const Node &n : g.nodes) {
         const ValueInfo &v = P.values[n.id];
         Packet &p = pk[n.id];
+        const std::vector<int64_t> dims = resolve_dims(n.dims, values);
         switch (v.storage) {
             case Storage::Input: from(p, inputs[v.input]); break;
             case Storage::Const:
-                p.shape = n.dims;
-                p.strides.assign(n.dims.size(), 0);
+                p.shape = dims;
+                p.strides.assign(dims.size(), 0);
                 p.t.data = static_cast<char *>(pool) + 8 * v.const_index;
                 p.t.byte_capacity = 8;
                 p.t.dtype = prim_dtype(n.prec);
@@ -206,24 +242,24 @@ int32_t run_plan(chelis_dag_program *prog, const chelis_gpu_tensor *const *input
                 p.seal();
                 break;
             case Storage::Slot: {
-                const Slot &s = P.slots[v.slot];
-                p.shape = n.dims;
-                p.strides.assign(n.dims.size(), 0);
+                p.shape = dims;
+                p.strides.assign(dims.size(), 0);
                 // dense in the stored order: layout[i] is the axis stored i-th
                 int64_t acc = 1;
                 if (v.layout.empty()) {
-                    for (size_t a = n.dims.size(); a-- > 0;) {
+                    for (size_t a = dims.size(); a-- > 0;) {
                         p.strides[a] = acc;
-                        acc *= std::max<int64_t>(n.dims[a], 1);
+                        acc *= std::max<int64_t>(dims[a], 1);
                     }
                 } else {
                     for (size_t i = v.layout.size(); i-- > 0;) {
                         p.strides[v.layout[i]] = acc;
-                        acc *= std::max<int64_t>(n.dims[v.layout[i]], 1);
+                        acc *= std::max<int64_t>(dims[v.layout[i]], 1);
                     }
                 }
-                p.t.data = ws + s.offset;
-                p.t.byte_capacity = s.bytes;
+                const size_t k = (size_t)v.slot;
+                p.t.data = ws + offsets[k];
+                p.t.byte_capacity = (k + 1 < offsets.size() ? offsets[k + 1] : workspace) - offsets[k];
                 p.t.dtype = prim_dtype(n.prec);
                 p.live = true;
                 p.seal();
@@ -237,8 +273,8 @@ int32_t run_plan(chelis_dag_program *prog, const chelis_gpu_tensor *const *input
                     p.seal();
                 } else {
                     p.t = out.t;
-                    p.shape = n.dims;
-                    if (!reshape_view(out, n.dims, &p.strides))
+                    p.shape = dims;
+                    if (!reshape_view(out, dims, &p.strides))
                         return set_error(CHELIS_HIP_EUNSUPPORTED, "dag: output %lld is too strided to take node %lld",
                                          (long long)v.output, (long long)n.id);
                     p.live = true;
@@ -251,7 +287,7 @@ int32_t run_plan(chelis_dag_program *prog, const chelis_gpu_tensor *const *input
                 if (!b.live) return set_error(CHELIS_HIP_EUNSUPPORTED, "dag: node %lld views a value with no storage",
                                               (long long)n.id);
                 p.t = b.t;
-                p.shape = n.dims;
+                p.shape = dims;
                 switch (n.op) {
                     case Op::Expand:
                         p.strides = b.strides;
@@ -262,12 +298,12 @@ int32_t run_plan(chelis_dag_program *prog, const chelis_gpu_tensor *const *input
                         for (size_t a = 0; a < n.axes.size(); ++a) p.strides[a] = b.strides[n.axes[a]];
                         break;
                     case Op::Reshape:
-                        if (!reshape_view(b, n.dims, &p.strides))
+                        if (!reshape_view(b, dims, &p.strides))
                             return set_error(CHELIS_HIP_EUNSUPPORTED,
                                              "dag: node %lld reshapes a view that is not one run of memory",
                                              (long long)n.id);
                         break;
-                    default:  // Realize / Copy: the same bytes
+                    default:  // Realize / Copy / Store: the same bytes
                         p.strides = b.strides;
                         break;
                 }
@@ -447,13 +483,67 @@ extern "C" int32_t chelis_dag_type(const chelis_dag_program *p, int32_t output, 
     if (!n) return set_error(CHELIS_HIP_EDOMAIN, "dag: no such slot");
     if (rank) *rank = (int32_t)n->dims.size();
     if (shape)
-        for (int32_t a = 0; a < (int32_t)n->dims.size() && a < shape_capacity; ++a) shape[a] = n->dims[a];
+        for (int32_t a = 0; a < (int32_t)n->dims.size() && a < shape_capacity; ++a)
+            shape[a] = extent_is_symbol(n->dims[a]) ? -1 : n->dims[a];
     if (dtype) *dtype = prim_dtype(n->prec);
     return CHELIS_HIP_OK;
 }
 
 extern "C" int64_t chelis_dag_peak_device_bytes(const chelis_dag_program *p) {
     return p ? p->plan.peak_device_bytes : -1;
+}
+
+extern "C" int32_t chelis_dag_symbol_count(const chelis_dag_program *p) {
+    return p ? (int32_t)p->plan.symbolic_dims.size() : -1;
+}
+
+extern "C" const char *chelis_dag_symbol_name(const chelis_dag_program *p, int32_t index) {
+    if (!p || index < 0 || index >= (int32_t)p->plan.symbolic_dims.size()) return nullptr;
+    return p->plan.graph.symbols[(size_t)p->plan.symbolic_dims[(size_t)index]].c_str();
+}
+
+extern "C" int64_t chelis_dag_peak_device_bytes_at(const chelis_dag_program *p, const int64_t *values, int32_t n) {
+    if (!p) return -1;
+    const Plan &P = p->plan;
+    if (n != (int32_t)P.symbolic_dims.size() || (n && !values)) {
+        set_error(CHELIS_HIP_EDOMAIN, "dag: %zu run-time extents expected, got %d", P.symbolic_dims.size(), n);
+        return -1;
+    }
+    std::vector<int64_t> v(P.graph.symbols.size(), 0);
+    for (int32_t k = 0; k < n; ++k) {
+        if (values[k] < 0) {
+            set_error(CHELIS_HIP_EDOMAIN, "dag: a negative extent");
+            return -1;
+        }
+        v[(size_t)P.symbolic_dims[(size_t)k]] = values[k];
+    }
+    std::vector<int64_t> offsets;
+    int64_t ws = 0;
+    if (!layout_slots(P, v, &offsets, &ws)) {
+        set_error(CHELIS_HIP_EDOMAIN, "dag: the workspace for these extents overflows");
+        return -1;
+    }
+    return ws + 8 * (int64_t)P.const_bits.size();
+}
+
+extern "C" int32_t chelis_dag_output_shape(const chelis_dag_program *p, const chelis_gpu_tensor *const *inputs,
+                                           int32_t n_in, int32_t index, int32_t *rank, int64_t *shape,
+                                           int32_t shape_capacity) {
+    const Node *n = slot_node(p, 1, index);
+    if (!n) return set_error(CHELIS_HIP_EDOMAIN, "dag: no such output");
+    try {
+        std::vector<int64_t> values;
+        if (int32_t s = bind_inputs(p->plan, inputs, n_in, &values)) return s;
+        if (rank) *rank = (int32_t)n->dims.size();
+        if ((int32_t)n->dims.size() > shape_capacity && shape)
+            return set_error(CHELIS_HIP_EDOMAIN, "dag: output rank %zu exceeds the capacity %d", n->dims.size(),
+                             shape_capacity);
+        if (shape)
+            for (size_t a = 0; a < n->dims.size(); ++a) shape[a] = resolve_extent(n->dims[a], values);
+        return CHELIS_HIP_OK;
+    } catch (const std::exception &e) {
+        return set_error(CHELIS_HIP_EHIP, "dag: %s", e.what());
+    }
 }
 
 extern "C" int64_t chelis_dag_launch_count(const chelis_dag_program *p) {

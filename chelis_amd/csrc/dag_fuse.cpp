@@ -32,18 +32,68 @@ bool is_integer(Prim p) {
     return p == Prim::Int8 || p == Prim::Int16 || p == Prim::Int32 || p == Prim::Int64;
 }
 
+// DagView::is_activation_gated (crates/chelis-dag-core/src/dag.rs:2864-2880)
+// over the chain ops: under an activation, an op whose run-time check may
+// fail keeps its own kernel - integer add / sub / mul / neg / abs / floor
+// and truncating division (operand values, dag.rs:2548-2551) and every
+// division (an integer operand check, or a lowered mean's divisor,
+// dag.rs:2555-2556).
+bool activation_gated(const Node &n) {
+    if (n.owner_activation < 0) return false;
+    if (n.op == Op::Div) return true;
+    if (!is_integer(n.prec)) return false;
+    switch (n.op) {
+        case Op::Add: case Op::Sub: case Op::Mul: case Op::Neg: case Op::Abs: case Op::FloorDiv:
+        case Op::TruncDiv:
+            return true;
+        default:
+            return false;
+    }
+}
+
 // fuse.rs:76-96: fused_step_op's table, minus the integer forms that stay
-// materialized (abs / sub / max / min), and an integer op under an
-// activation (it checks its operands there, so it keeps its own kernel).
+// materialized (abs / sub / max / min) and the activation-gated ops.
 bool fusible(const Node &n) {
     if (!op_is_chain_step(n.op)) return false;
-    if (is_integer(n.prec) &&
-        (n.op == Op::Abs || n.op == Op::Sub || n.op == Op::MaxElem || n.op == Op::MinElem || n.owner_activation >= 0))
+    if (is_integer(n.prec) && (n.op == Op::Abs || n.op == Op::Sub || n.op == Op::MaxElem || n.op == Op::MinElem))
         return false;
-    return true;
+    return !activation_gated(n);
+}
+
+bool owns_result_claim(const Graph &g, const Node &n) {
+    auto claim = [&](int64_t dep) {
+        const Node &w = g.nodes[(size_t)dep];
+        return w.op == Op::ExtentWitness &&
+               (w.site == WitnessSite::LiteralResultClaim || w.site == WitnessSite::ResultClaim ||
+                w.site == WitnessSite::LocalAscriptionClaim);
+    };
+    for (int64_t d : n.shape_deps)
+        if (claim(d)) return true;
+    for (int64_t d : n.claim_deps)
+        if (claim(d)) return true;
+    return false;
 }
 
 }  // namespace
+
+bool chain_fusible(const Node &n) { return fusible(n); }
+
+std::vector<bool> claimed_producers(const Graph &g) {
+    std::vector<bool> owned(g.nodes.size(), false);
+    std::vector<int64_t> pending;
+    for (const Node &n : g.nodes)
+        if (owns_result_claim(g, n)) pending.push_back(n.id);
+    while (!pending.empty()) {
+        const int64_t cur = pending.back();
+        pending.pop_back();
+        if (owned[(size_t)cur]) continue;
+        owned[(size_t)cur] = true;
+        const Node &n = g.nodes[(size_t)cur];
+        if ((n.op == Op::Copy || n.op == Op::Cast || n.op == Op::NamedCast) && !n.inputs.empty())
+            pending.push_back(n.inputs[0]);
+    }
+    return owned;
+}
 
 Graph fuse(const Graph &g, std::vector<int64_t> *old_to_new) {
     const std::vector<int64_t> counts = consumer_counts(g);
@@ -57,8 +107,10 @@ Graph fuse(const Graph &g, std::vector<int64_t> *old_to_new) {
     std::vector<int64_t> chain_of(n, -1);
     std::vector<std::vector<int64_t>> chains;
     std::vector<bool> in_chain(n, false);
+    // fuse.rs:147-161,183: a claimed producer is a barrier
+    const std::vector<bool> barrier = claimed_producers(g);
     for (const Node &nd : g.nodes) {
-        if (in_chain[nd.id] || !fusible(nd)) continue;
+        if (in_chain[nd.id] || !fusible(nd) || barrier[nd.id]) continue;
         std::vector<int64_t> chain{nd.id};
         in_chain[nd.id] = true;
         int64_t cur = nd.id;
@@ -71,7 +123,9 @@ Graph fuse(const Graph &g, std::vector<int64_t> *old_to_new) {
                 }
             if (next < 0) break;
             const Node &c = g.nodes[next];
-            if (!fusible(c) || c.owner_decl != nd.owner_decl || c.owner_activation != nd.owner_activation) break;
+            if (!fusible(c) || barrier[next] || c.owner_decl != nd.owner_decl ||
+                c.owner_activation != nd.owner_activation)
+                break;
             chain.push_back(next);
             in_chain[next] = true;
             cur = next;
@@ -86,6 +140,7 @@ Graph fuse(const Graph &g, std::vector<int64_t> *old_to_new) {
     // fuse.rs:206-332: rebuild, a chain becoming one FusedElem at its last node
     Graph out;
     out.declarations = g.declarations;
+    out.symbols = g.symbols;
     std::vector<int64_t> map(n, -1);
     auto add = [&](Node node) {
         node.id = (int64_t)out.nodes.size();
@@ -133,6 +188,7 @@ Graph fuse(const Graph &g, std::vector<int64_t> *old_to_new) {
         for (int64_t e : ext) f.inputs.push_back(map[e]);
         const Node &last = g.nodes[chain.back()], &first = g.nodes[chain.front()];
         f.dims = last.dims;
+        f.dims_raw = last.dims_raw;
         f.prec = last.prec;
         f.owner_decl = last.owner_decl;
         f.owner_activation = last.owner_activation >= 0 ? map[last.owner_activation] : -1;
@@ -192,6 +248,7 @@ std::vector<bool> reduction_inlined(const Graph &g) {
 Graph unfuse(const Graph &g) {
     Graph out;
     out.declarations = g.declarations;
+    out.symbols = g.symbols;
     std::vector<int64_t> map(g.nodes.size(), -1);
     for (const Node &nd : g.nodes) {
         if (nd.op != Op::FusedElem) {
@@ -215,6 +272,7 @@ Graph unfuse(const Graph &g) {
             p.raw_op = json_quote(p.variant);
             for (int a : st.args) p.inputs.push_back(a >= 0 ? map[nd.inputs[a]] : step_ids[-a - 1]);
             p.dims = nd.dims;
+            p.dims_raw = nd.dims_raw;
             p.prec = nd.prec;
             p.owner_decl = nd.owner_decl;
             p.owner_activation = nd.owner_activation >= 0 ? map[nd.owner_activation] : -1;

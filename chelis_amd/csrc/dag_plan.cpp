@@ -28,6 +28,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <map>
 #include <set>
 
 #include "dag.h"
@@ -185,7 +186,7 @@ bool match_node(const Template &T, int ti, const Graph &g, int64_t d, Binding &b
         b.map[ti] = d;
         return true;
     }
-    if (n.op != t.op || n.inputs.size() != t.in.size() || n.dims != t.dims || n.prec != t.prec) return false;
+    if (n.op != t.op || n.payload_inputs() != t.in.size() || n.dims != t.dims || n.prec != t.prec) return false;
     switch (t.op) {
         case Op::Sum: case Op::MaxReduce: if (n.axis != t.axis) return false; break;
         case Op::Expand: if (n.axis != t.axis || n.size != t.size) return false; break;
@@ -213,18 +214,24 @@ struct Planner {
     std::vector<std::vector<int64_t>> users;  // data consumers (inputs), each once, in node order
     std::vector<bool> is_root;
     std::vector<int> claimed;                 // region index, -1 free
+    std::vector<bool> barrier;                // claimed producers (fuse.rs:147-161)
     std::vector<Region> regions;
     std::string error;
 
-    explicit Planner(const Graph &graph) : g(graph) {
+    explicit Planner(const Graph &graph, const std::vector<int64_t> &outputs) : g(graph) {
         counts = consumer_counts(g);
         users.resize(g.nodes.size());
         is_root.assign(g.nodes.size(), false);
-        for (int64_t r : g.roots) is_root[r] = true;
+        for (int64_t r : outputs) is_root[r] = true;
+        // data readers only: the tensor an InputAxis extent is read from is
+        // not read by the Expand / Reshape that names it
         for (const Node &n : g.nodes)
-            for (int64_t i : n.inputs)
+            for (size_t k = 0; k < n.payload_inputs(); ++k) {
+                const int64_t i = n.inputs[k];
                 if (users[i].empty() || users[i].back() != n.id) users[i].push_back(n.id);
+            }
         claimed.assign(g.nodes.size(), -1);
+        barrier = claimed_producers(g);
     }
     const Node &N(int64_t id) const { return g.nodes[id]; }
     bool free_leaf(int64_t id) const { return N(id).op == Op::Load || N(id).op == Op::Const; }
@@ -596,7 +603,8 @@ struct Planner {
     }
     bool fusible(int64_t id) const {
         const Node &n = N(id);
-        return claimed[id] < 0 && op_is_chain_step(n.op) && prim_is_float(n.prec);
+        return claimed[id] < 0 && op_is_chain_step(n.op) && prim_is_float(n.prec) && chain_fusible(n) &&
+               !barrier[id];
     }
 
     // Build chelis_fused_chain launches from a run of chain nodes; nodes
@@ -683,8 +691,17 @@ struct Planner {
             }
             switch (n.op) {
                 case Op::Load: case Op::Const: case Op::Expand: case Op::Permute: case Op::Reshape:
-                case Op::Realize: case Op::Copy:
+                case Op::Realize: case Op::Copy: case Op::Store:
                     continue;  // inputs, constants and views
+                case Op::ExtentWitness:
+                    // checked on the host before the launches (build_plan);
+                    // its value itself is read by nothing this build runs
+                    if (!users[n.id].empty())
+                        return fail("node " + std::to_string(n.id) + ": an ExtentWitness value read by a launch");
+                    if (n.named_claims)
+                        return fail("node " + std::to_string(n.id) +
+                                    ": an ExtentWitness with named claims is not checked by this build");
+                    continue;
                 case Op::Sum: case Op::MaxReduce: case Op::MinReduce: case Op::ProdReduce: case Op::Argmax:
                 case Op::Argmin: {
                     Region r;
@@ -782,7 +799,55 @@ struct Planner {
 };
 
 bool is_view_op(Op op) {
-    return op == Op::Expand || op == Op::Permute || op == Op::Reshape || op == Op::Realize || op == Op::Copy;
+    return op == Op::Expand || op == Op::Permute || op == Op::Reshape || op == Op::Realize || op == Op::Copy ||
+           op == Op::Store;
+}
+
+// The reference's output specs (emit.rs:5901-5933): Store nodes in node
+// order under their names, then the roots (the last node when there are
+// none) as "root<index>", each node once.
+void output_specs(const Graph &g, std::vector<int64_t> *nodes, std::vector<std::string> *labels) {
+    std::set<int64_t> seen;
+    for (const Node &n : g.nodes)
+        if (n.op == Op::Store && seen.insert(n.id).second) {
+            nodes->push_back(n.id);
+            labels->push_back(n.name);
+        }
+    std::vector<int64_t> roots = g.roots;
+    if (roots.empty() && !g.nodes.empty()) roots.push_back(g.nodes.back().id);
+    for (size_t k = 0; k < roots.size(); ++k)
+        if (seen.insert(roots[k]).second) {
+            nodes->push_back(roots[k]);
+            labels->push_back("root" + std::to_string(k));
+        }
+}
+
+// The first extent this build cannot bind, as an error, or "".
+std::string unbound_extent(const Node &n) {
+    bool bad = false;
+    for (int64_t d : n.dims) bad |= d == kUnboundExtent;
+    if (n.op == Op::Expand) bad |= n.size == kUnboundExtent;
+    if (n.op == Op::Reshape)
+        for (int64_t d : n.new_shape) bad |= d == kUnboundExtent;
+    if (!bad) return "";
+    return "node " + std::to_string(n.id) + ": " + (n.extent_error.empty() ? "an unbound extent" : n.extent_error) +
+           " is a run-time extent this build cannot bind";
+}
+
+// A materialized value's bytes: a literal, or coef * prod(symbols).
+struct Size {
+    int64_t coef = 0;
+    std::vector<int64_t> symbols;
+};
+Size value_size(const Node &nd, int64_t width) {
+    Size z;
+    z.coef = width;
+    for (int64_t d : nd.dims) {
+        if (extent_is_symbol(d)) z.symbols.push_back(extent_symbol(d));
+        else z.coef *= d;
+    }
+    std::sort(z.symbols.begin(), z.symbols.end());
+    return z;
 }
 
 }  // namespace
@@ -791,7 +856,15 @@ bool build_plan(const Graph &input, Plan *plan, std::string *error) {
     *plan = Plan{};
     plan->graph = unfuse(input);
     const Graph &g = plan->graph;
-    Planner P(g);
+    for (const Node &nd : g.nodes) {
+        const std::string why = unbound_extent(nd);
+        if (!why.empty()) {
+            *error = why;
+            return false;
+        }
+    }
+    output_specs(g, &plan->output_nodes, &plan->output_labels);
+    Planner P(g, plan->output_nodes);
     if (!P.form()) {
         *error = P.error;
         return false;
@@ -857,13 +930,28 @@ bool build_plan(const Graph &input, Plan *plan, std::string *error) {
     plan->values.assign(n, ValueInfo{});
     std::vector<bool> produced(n, false);
     for (const Region &r : plan->regions) produced[r.out] = true;
+    // caller inputs: one slot per Load name (a repeated Load aliases it,
+    // emit.rs:5881-5892), in first-appearance order
+    std::map<std::string, int64_t> input_slot;
     for (const Node &nd : g.nodes) {
         ValueInfo &v = plan->values[nd.id];
         if (nd.op == Op::Load) {
             v.storage = Storage::Input;
-            v.input = (int64_t)plan->input_nodes.size();
-            plan->input_nodes.push_back(nd.id);
-            plan->input_labels.push_back(nd.name);
+            auto it = input_slot.find(nd.name);
+            if (it == input_slot.end()) {
+                v.input = (int64_t)plan->input_nodes.size();
+                input_slot[nd.name] = v.input;
+                plan->input_nodes.push_back(nd.id);
+                plan->input_labels.push_back(nd.name);
+            } else {
+                const Node &first = g.nodes[plan->input_nodes[it->second]];
+                if (first.dims != nd.dims || first.prec != nd.prec) {
+                    *error = "node " + std::to_string(nd.id) + ": Load `" + nd.name +
+                             "` repeats an input name with another type";
+                    return false;
+                }
+                v.input = it->second;
+            }
         } else if (nd.op == Op::Const) {
             v.storage = Storage::Const;
             v.const_index = (int64_t)plan->const_bits.size();
@@ -878,6 +966,49 @@ bool build_plan(const Graph &input, Plan *plan, std::string *error) {
             v.storage = Storage::Inlined;
         }
     }
+    // run-time extents: each symbol is read from the first input axis that
+    // declares it (inputs in slot order, axes in order); later declaring
+    // axes must agree (emit.rs:1141-1168)
+    std::vector<bool> bound(g.symbols.size(), false);
+    for (size_t slot = 0; slot < plan->input_nodes.size(); ++slot) {
+        const Node &ld = g.nodes[plan->input_nodes[slot]];
+        for (size_t a = 0; a < ld.dims.size(); ++a) {
+            if (!extent_is_symbol(ld.dims[a])) continue;
+            const int64_t sym = extent_symbol(ld.dims[a]);
+            SymbolRead r{sym, (int64_t)slot, (int64_t)a};
+            if (bound[sym]) {
+                plan->checks.push_back(r);
+            } else {
+                bound[sym] = true;
+                plan->binds.push_back(r);
+                plan->symbolic_dims.push_back(sym);
+            }
+        }
+    }
+    for (const Node &nd : g.nodes) {
+        std::vector<int64_t> ext = nd.dims;
+        if (nd.op == Op::Expand) ext.push_back(nd.size);
+        if (nd.op == Op::Reshape) ext.insert(ext.end(), nd.new_shape.begin(), nd.new_shape.end());
+        for (int64_t e : ext)
+            if (extent_is_symbol(e) && !bound[extent_symbol(e)]) {
+                *error = "node " + std::to_string(nd.id) + ": run-time extent `" + g.symbols[extent_symbol(e)] +
+                         "` is not declared by any input";
+                return false;
+            }
+    }
+    // ExtentWitness requirements, checked on the host before the launches
+    for (const Node &nd : g.nodes) {
+        if (nd.op != Op::ExtentWitness || nd.site == WitnessSite::LiteralResultClaim || nd.requirements.empty())
+            continue;
+        auto it = input_slot.find(nd.name);
+        const Node *ld = it == input_slot.end() ? nullptr : &g.nodes[plan->input_nodes[it->second]];
+        if (!ld || nd.axis < 0 || nd.axis >= (int64_t)ld->dims.size()) {
+            *error = "node " + std::to_string(nd.id) + ": ExtentWitness reads `" + nd.name +
+                     "`, which is no input axis of this program";
+            return false;
+        }
+        for (int64_t req : nd.requirements) plan->extent_checks.push_back({it->second, nd.axis, req, nd.name});
+    }
     // every region input must have storage
     for (const Region &r : plan->regions)
         for (int64_t in : r.in)
@@ -886,15 +1017,13 @@ bool build_plan(const Graph &input, Plan *plan, std::string *error) {
                 return false;
             }
     // outputs: a region result is written straight into the caller's
-    // output (through a reshape when the root is one); anything else is
-    // copied there by a last launch
-    std::vector<int64_t> copies;
-    for (size_t o = 0; o < g.roots.size(); ++o) {
-        const int64_t root = g.roots[o];
-        plan->output_nodes.push_back(root);
-        plan->output_labels.push_back(g.nodes[root].has_span ? g.nodes[root].span : "out" + std::to_string(o));
+    // output (through a reshape or store view when the output is one);
+    // anything else is copied there by a last launch
+    for (size_t o = 0; o < plan->output_nodes.size(); ++o) {
+        const int64_t root = plan->output_nodes[o];
         int64_t v = root;
-        while (plan->values[v].storage == Storage::View && g.nodes[v].op == Op::Reshape && P.users[v].size() <= 1 &&
+        while (plan->values[v].storage == Storage::View &&
+               (g.nodes[v].op == Op::Reshape || g.nodes[v].op == Op::Store) && P.users[v].size() <= 1 &&
                P.users[plan->values[v].base].size() == 1 && !P.is_root[plan->values[v].base])
             v = plan->values[v].base;
         ValueInfo &vi = plan->values[v];
@@ -908,7 +1037,6 @@ bool build_plan(const Graph &input, Plan *plan, std::string *error) {
             c.in = {root};
             c.out = root;
             c.axis = (int64_t)o;  // the output slot
-            copies.push_back((int64_t)plan->regions.size());
             plan->regions.push_back(c);
         }
     }
@@ -927,66 +1055,156 @@ bool build_plan(const Graph &input, Plan *plan, std::string *error) {
         if (r.kind == RegionKind::Attention && u.axes[rk - 1] != (int64_t)rk - 1) continue;
         vi.layout = u.axes;
     }
-    // slot plan: lifetimes in launch order, views charged to their base
-    std::vector<int64_t> def(n, -1), last(n, -1);
+    // slot plan: lifetimes in launch order, views charged to their base.
+    // A literal value takes the free literal range that fits it best (or
+    // grows the largest); a value sized by run-time extents reuses a free
+    // range only of the same size expression (the reference's exact-capacity
+    // reuse, memory.rs:32-182), so every range has one formula.
+    std::vector<int64_t> last(n, -1);
     for (size_t k = 0; k < plan->regions.size(); ++k) {
-        const Region &r = plan->regions[k];
-        if (r.kind != RegionKind::Copy && def[r.out] < 0) def[r.out] = (int64_t)k;
-        for (int64_t in : r.in) {
+        for (int64_t in : plan->regions[k].in) {
             int64_t b = in;
             while (plan->values[b].storage == Storage::View) b = plan->values[b].base;
             last[b] = std::max(last[b], (int64_t)k);
         }
     }
-    std::vector<int64_t> slot_size;
+    std::vector<Slot> slots;
     std::vector<bool> busy;
     std::vector<std::vector<int64_t>> release_at(plan->regions.size());
     for (size_t k = 0; k < plan->regions.size(); ++k) {
         const Region &r = plan->regions[k];
-        if (r.kind != RegionKind::Copy) {
+        if (r.kind != RegionKind::Copy && plan->values[r.out].storage == Storage::Slot) {
             ValueInfo &vi = plan->values[r.out];
-            if (vi.storage == Storage::Slot) {
-                const Node &nd = g.nodes[r.out];
-                const int64_t width = r.kind == RegionKind::Reduce && (r.reduce_op == CHELIS_REDUCE_ARGMAX ||
-                                                                       r.reduce_op == CHELIS_REDUCE_ARGMIN)
-                                          ? 8
-                                          : (r.kind == RegionKind::Count ? 8 : prim_width(nd.prec));
-                const int64_t cnt = nd.count();
-                if (cnt < 0) {
-                    *error = "node " + std::to_string(nd.id) + ": an extent known only at run time";
-                    return false;
-                }
-                const int64_t need = ((cnt * width) + 255) & ~int64_t(255);
-                int64_t best = -1;
-                for (size_t s = 0; s < slot_size.size(); ++s)
-                    if (!busy[s] && slot_size[s] >= need && (best < 0 || slot_size[s] < slot_size[best])) best = (int64_t)s;
+            const Node &nd = g.nodes[r.out];
+            const int64_t width = r.kind == RegionKind::Reduce && (r.reduce_op == CHELIS_REDUCE_ARGMAX ||
+                                                                   r.reduce_op == CHELIS_REDUCE_ARGMIN)
+                                      ? 8
+                                      : (r.kind == RegionKind::Count ? 8 : prim_width(nd.prec));
+            const Size z = value_size(nd, width);
+            int64_t best = -1;
+            if (z.symbols.empty()) {
+                const int64_t need = (z.coef + 255) & ~int64_t(255);
+                for (size_t s = 0; s < slots.size(); ++s)
+                    if (!busy[s] && !slots[s].symbolic() && slots[s].bytes >= need &&
+                        (best < 0 || slots[s].bytes < slots[best].bytes))
+                        best = (int64_t)s;
                 if (best < 0)
-                    for (size_t s = 0; s < slot_size.size(); ++s)
-                        if (!busy[s] && (best < 0 || slot_size[s] > slot_size[best])) best = (int64_t)s;
+                    for (size_t s = 0; s < slots.size(); ++s)
+                        if (!busy[s] && !slots[s].symbolic() && (best < 0 || slots[s].bytes > slots[best].bytes))
+                            best = (int64_t)s;
                 if (best < 0) {
-                    best = (int64_t)slot_size.size();
-                    slot_size.push_back(0);
+                    best = (int64_t)slots.size();
+                    slots.push_back(Slot{});
                     busy.push_back(false);
                 }
-                slot_size[best] = std::max(slot_size[best], need);
-                busy[best] = true;
-                vi.slot = best;
-                const int64_t end = std::max(last[r.out], (int64_t)k);
-                release_at[end].push_back(best);
+                slots[best].bytes = std::max(slots[best].bytes, need);
+            } else {
+                for (size_t s = 0; s < slots.size() && best < 0; ++s)
+                    if (!busy[s] && slots[s].symbolic() && slots[s].coef == z.coef && slots[s].symbols == z.symbols)
+                        best = (int64_t)s;
+                if (best < 0) {
+                    best = (int64_t)slots.size();
+                    Slot sl;
+                    sl.coef = z.coef;
+                    sl.symbols = z.symbols;
+                    slots.push_back(sl);
+                    busy.push_back(false);
+                }
             }
+            busy[best] = true;
+            vi.slot = best;
+            release_at[std::max(last[r.out], (int64_t)k)].push_back(best);
         }
         for (int64_t s : release_at[k]) busy[s] = false;
     }
+    bool symbolic = false;
     int64_t off = 0;
-    for (int64_t s : slot_size) {
-        plan->slots.push_back(Slot{off, s});
-        off += s;
+    for (Slot &sl : slots) {
+        symbolic |= sl.symbolic();
+        sl.offset = off;
+        off += sl.bytes;
+        plan->slots.push_back(sl);
     }
-    plan->workspace_bytes = off;
     // the constant pool holds one 8-byte cell per constant
-    plan->peak_device_bytes = plan->workspace_bytes + 8 * (int64_t)plan->const_bits.size();
-    (void)copies;
+    plan->workspace_bytes = symbolic ? -1 : off;
+    plan->peak_device_bytes = symbolic ? -1 : plan->workspace_bytes + 8 * (int64_t)plan->const_bits.size();
     return true;
+}
+
+std::vector<int64_t> resolve_dims(const std::vector<int64_t> &dims, const std::vector<int64_t> &values) {
+    std::vector<int64_t> out(dims.size());
+    for (size_t a = 0; a < dims.size(); ++a) out[a] = resolve_extent(dims[a], values);
+    return out;
+}
+
+bool bind_symbols(const Plan &plan, const int64_t *const *input_shapes, const int32_t *input_ranks,
+                  std::vector<int64_t> *values, std::string *error) {
+    const Graph &g = plan.graph;
+    values->assign(g.symbols.size(), 0);
+    for (const SymbolRead &r : plan.binds) {
+        if (r.axis >= input_ranks[r.input]) {
+            *error = "input `" + plan.input_labels[r.input] + "` has no axis " + std::to_string(r.axis);
+            return false;
+        }
+        const int64_t e = input_shapes[r.input][r.axis];
+        if (e < 0) {
+            *error = "input `" + plan.input_labels[r.input] + "` axis " + std::to_string(r.axis) +
+                     " is negative";
+            return false;
+        }
+        (*values)[r.symbol] = e;
+    }
+    for (const SymbolRead &r : plan.checks) {
+        const int64_t e = r.axis < input_ranks[r.input] ? input_shapes[r.input][r.axis] : -1;
+        if (e != (*values)[r.symbol]) {
+            *error = "symbolic dim `" + g.symbols[r.symbol] + "` mismatch: " + plan.input_labels[r.input] + "[" +
+                     std::to_string(r.axis) + "]=" + std::to_string(e) + " but " + g.symbols[r.symbol] + "=" +
+                     std::to_string((*values)[r.symbol]);
+            return false;
+        }
+    }
+    return true;
+}
+
+bool layout_slots(const Plan &plan, const std::vector<int64_t> &values, std::vector<int64_t> *offsets,
+                  int64_t *workspace) {
+    offsets->assign(plan.slots.size(), 0);
+    int64_t off = 0;
+    const int64_t limit = int64_t(1) << 62;
+    for (size_t k = 0; k < plan.slots.size(); ++k) {
+        const Slot &sl = plan.slots[k];
+        int64_t bytes = sl.bytes;
+        if (sl.symbolic()) {
+            bytes = sl.coef;
+            for (int64_t s : sl.symbols) {
+                const int64_t v = values[(size_t)s];
+                if (v != 0 && bytes > limit / v) return false;
+                bytes *= v;
+            }
+            bytes = (bytes + 255) & ~int64_t(255);
+        }
+        (*offsets)[k] = off;
+        if (off > limit - bytes) return false;
+        off += bytes;
+    }
+    *workspace = off;
+    return true;
+}
+
+std::string peak_formula(const Plan &plan) {
+    std::string f;
+    auto term = [&](const std::string &t) { f += (f.empty() ? "" : " + ") + t; };
+    for (const Slot &sl : plan.slots) {
+        if (!sl.symbolic()) {
+            term(std::to_string(sl.bytes));
+            continue;
+        }
+        std::string t = std::to_string(sl.coef);
+        for (int64_t s : sl.symbols) t += "*" + plan.graph.symbols[(size_t)s];
+        term(sl.coef % 256 == 0 ? t : "round_up(" + t + ", 256)");
+    }
+    if (!plan.const_bits.empty()) term(std::to_string(8 * plan.const_bits.size()));
+    return f.empty() ? "0" : f;
 }
 
 std::string describe_plan(const Plan &plan) {

@@ -2,10 +2,18 @@
 // back. Shapes follow serde's externally tagged enums over the types of
 // crates/chelis-dag-core/src/dag.rs: a unit RiscOp is its variant name, any
 // other is {"Variant": payload}; DimInfo is {"Lit": n} or {"Named": [name,
-// n | null]}; RtDim is {"Lit": n} (other forms are run-time extents); a
-// scalar is {"dtype": "f32", "bits": "<hex>"} or {"dtype": "int64",
+// n | null]}; RtDim is {"Lit": n}, {"Sym": name}, {"InputAxis": {"tensor": t,
+// "axis": {"Lit": a}}}, {"Node": i} or "ToEnd"; a scalar is {"dtype": "f32", "bits": "<hex>"} or {"dtype": "int64",
 // "value": n} (crates/chelis-numeric-core/src/dtype_semantics/wire_codec.rs:
 // 488-512). Golden strings: crates/chelis-dag-core/tests/wire_behavior.rs:48,121.
+//
+// Extents (dag.rs:221-290): a literal; a run-time extent named by a symbol -
+// DimInfo::Named(name, None) or RtDim::Sym(name) - bound from the input that
+// declares it when the program runs; RtDim::InputAxis{tensor, axis}, the
+// extent of that axis of the node's inputs[tensor] (literal or symbol);
+// DimInfo::Named(name, Some(n)) is n. Bounds read from a node value
+// (RtDim::Node), the to-the-end sentinel and DimExpr products or quotients
+// are kept for the write-back and refused by the planner.
 #include <cmath>
 #include <cstring>
 
@@ -33,6 +41,7 @@ const OpName kOps[] = {
     {"Argmax", Op::Argmax}, {"Argmin", Op::Argmin}, {"Count", Op::Count}, {"Softmax", Op::Softmax},
     {"Expand", Op::Expand}, {"Permute", Op::Permute}, {"Reshape", Op::Reshape}, {"Realize", Op::Realize},
     {"Copy", Op::Copy}, {"FusedElem", Op::FusedElem}, {"BlasMatmul", Op::BlasMatmul},
+    {"Store", Op::Store}, {"ExtentWitness", Op::ExtentWitness}, {"NamedCast", Op::NamedCast},
 };
 
 struct PrimName {
@@ -82,16 +91,58 @@ bool ids_of(const Json *j, std::vector<int64_t> *out) {
     return true;
 }
 
-// RtDim / DimInfo / DimExpr: the literal extent, or -1 for a run-time one.
-int64_t extent_of(const Json &j) {
-    if (j.kind == Json::Object && j.fields.size() == 1) {
-        const auto &f = j.fields[0];
-        if ((f.first == "Lit" || f.first == "Concrete") && f.second.is_int()) return f.second.as_int();
-        if (f.first == "Named" && f.second.kind == Json::Array && f.second.items.size() == 2 &&
-            f.second.items[1].is_int())
-            return f.second.items[1].as_int();
+// RtDim / DimInfo / DimExpr (dag.rs:221-290) as an extent code of `n`,
+// whose inputs are already read. Unbindable forms give kUnboundExtent and
+// set n->extent_error; malformed ones return false.
+bool extent_of(const Json &j, Graph *g, Node *n, int64_t *code) {
+    auto unbound = [&](const char *why) {
+        if (n->extent_error.empty()) n->extent_error = why;
+        *code = kUnboundExtent;
+        return true;
+    };
+    if (j.kind == Json::String) {
+        if (j.text == "ToEnd") return unbound("the to-the-end bound of a shrink");
+        return false;
     }
-    return -1;
+    if (j.kind != Json::Object || j.fields.size() != 1) return false;
+    const std::string &tag = j.fields[0].first;
+    const Json &v = j.fields[0].second;
+    if (tag == "Lit" || tag == "Concrete") {
+        if (!v.is_int() || v.as_int() < 0) return false;
+        *code = v.as_int();
+        return true;
+    }
+    if (tag == "Named") {
+        if (v.kind != Json::Array || v.items.size() != 2 || v.items[0].kind != Json::String) return false;
+        if (v.items[1].is_int() && v.items[1].as_int() >= 0) {
+            *code = v.items[1].as_int();
+            return true;
+        }
+        if (v.items[1].kind != Json::Null) return false;
+        *code = symbol_extent(g->symbol(v.items[0].text));
+        return true;
+    }
+    if (tag == "Sym") {
+        if (v.kind != Json::String) return false;
+        *code = symbol_extent(g->symbol(v.text));
+        return true;
+    }
+    if (tag == "InputAxis") {
+        const Json *t = v.get("tensor"), *ax = v.get("axis");
+        if (!t || !t->is_int() || !ax || ax->kind != Json::Object || ax->fields.size() != 1 ||
+            ax->fields[0].first != "Lit" || !ax->fields[0].second.is_int())
+            return false;
+        const int64_t ti = t->as_int(), a = ax->fields[0].second.as_int();
+        if (ti < 0 || ti >= (int64_t)n->inputs.size()) return false;
+        const Node &src = g->nodes[(size_t)n->inputs[(size_t)ti]];
+        if (a < 0 || a >= (int64_t)src.dims.size()) return false;
+        *code = src.dims[(size_t)a];
+        if (*code == kUnboundExtent) return unbound("an extent read from an unbound axis");
+        return true;
+    }
+    if (tag == "Node") return unbound("a bound read from a node value");
+    if (tag == "Mul" || tag == "Div") return unbound("a product or quotient of run-time extents");
+    return false;
 }
 
 uint64_t hex_bits(const std::string &t, bool *ok) {
@@ -148,7 +199,7 @@ bool step_op_of(const Json &j, Step *s) {
     return true;
 }
 
-bool read_op(const Json &op, Node *n, std::string *why) {
+bool read_op(const Json &op, Graph *g, Node *n, std::string *why) {
     std::string raw;
     write_json(op, &raw);
     n->raw_op = raw;
@@ -166,10 +217,35 @@ bool read_op(const Json &op, Node *n, std::string *why) {
     n->variant = var;
     n->op = op_of(var);
     switch (n->op) {
-        case Op::Load: {
+        case Op::Load:
+        case Op::Store: {
             const Json *name = p.get("name");
-            if (!name || name->kind != Json::String) return (*why = "Load without a name", false);
+            if (!name || name->kind != Json::String) return (*why = var + " without a name", false);
             n->name = name->text;
+            return true;
+        }
+        case Op::ExtentWitness: {
+            const Json *site = p.get("site"), *param = p.get("parameter"), *axis = p.get("axis"),
+                       *reqs = p.get("requirements"), *claims = p.get("claims");
+            if (!param || param->kind != Json::String || !axis || axis->kind != Json::Object ||
+                axis->fields.size() != 1 || !axis->fields[0].second.is_int() || !reqs || reqs->kind != Json::Array)
+                return (*why = "ExtentWitness needs parameter, axis and requirements", false);
+            n->name = param->text;
+            n->axis = axis->fields[0].second.as_int();
+            for (const Json &r : reqs->items) {
+                Node tmp;
+                if (!scalar_of(&r, &tmp) || prim_is_float(tmp.const_prec))
+                    return (*why = "ExtentWitness requirement is not an integer scalar", false);
+                n->requirements.push_back((int64_t)tmp.const_bits);
+            }
+            n->named_claims = (claims && claims->kind == Json::Array) ? (int64_t)claims->items.size() : 0;
+            n->site = WitnessSite::Other;
+            if (site && site->kind == Json::String && site->text == "LiteralResultClaim")
+                n->site = WitnessSite::LiteralResultClaim;
+            else if (site && site->kind == Json::Object && site->fields.size() == 1) {
+                if (site->fields[0].first == "ResultClaim") n->site = WitnessSite::ResultClaim;
+                if (site->fields[0].first == "LocalAscriptionClaim") n->site = WitnessSite::LocalAscriptionClaim;
+            }
             return true;
         }
         case Op::Const:
@@ -190,13 +266,17 @@ bool read_op(const Json &op, Node *n, std::string *why) {
         case Op::Expand: {
             const Json *size = p.get("size");
             if (!int_of(p.get("axis"), &n->axis) || !size) return (*why = "Expand needs axis and size", false);
-            n->size = extent_of(*size);
+            if (!extent_of(*size, g, n, &n->size)) return (*why = "Expand size is not an extent", false);
             return true;
         }
         case Op::Reshape: {
             const Json *shape = p.get("new_shape");
             if (!shape || shape->kind != Json::Array) return (*why = "Reshape needs new_shape", false);
-            for (const Json &d : shape->items) n->new_shape.push_back(extent_of(d));
+            for (const Json &d : shape->items) {
+                int64_t e;
+                if (!extent_of(d, g, n, &e)) return (*why = "Reshape new_shape holds a non-extent", false);
+                n->new_shape.push_back(e);
+            }
             return true;
         }
         case Op::Compare:
@@ -205,6 +285,8 @@ bool read_op(const Json &op, Node *n, std::string *why) {
             return true;
         case Op::Cast:
             if (!prim_of(p.get("new_precision"), &n->cast_to)) return (*why = "Cast needs new_precision", false);
+            return true;
+        case Op::NamedCast:
             return true;
         case Op::FusedElem: {
             const Json *ops = p.get("ops");
@@ -274,6 +356,13 @@ int64_t Node::count() const {
     return c;
 }
 
+int64_t Graph::symbol(const std::string &name) {
+    for (size_t s = 0; s < symbols.size(); ++s)
+        if (symbols[s] == name) return (int64_t)s;
+    symbols.push_back(name);
+    return (int64_t)symbols.size() - 1;
+}
+
 double Node::const_value() const {
     switch (const_prec) {
         case Prim::F32: {
@@ -313,11 +402,11 @@ bool read_graph(const char *text, size_t n, Graph *g, std::string *error) {
             return false;
         };
         if (!int_of(j.get("id"), &nd.id) || nd.id != (int64_t)k) return bad("id must equal its position");
-        const Json *op = j.get("op");
-        if (!op || !read_op(*op, &nd, &why)) return bad(why.empty() ? "missing op" : why);
         if (!ids_of(j.get("inputs"), &nd.inputs) || !j.get("inputs")) return bad("inputs must be node ids");
         for (int64_t in : nd.inputs)
             if (in < 0 || in >= nd.id) return bad("input " + std::to_string(in) + " does not precede the node");
+        const Json *op = j.get("op");
+        if (!op || !read_op(*op, g, &nd, &why)) return bad(why.empty() ? "missing op" : why);
         if (!ids_of(j.get("shape_deps"), &nd.shape_deps) || !ids_of(j.get("result_claim_deps"), &nd.claim_deps))
             return bad("shape_deps / result_claim_deps must be node ids");
         for (int64_t d : nd.shape_deps)
@@ -327,7 +416,16 @@ bool read_graph(const char *text, size_t n, Graph *g, std::string *error) {
         const Json *ty = j.get("output_type");
         if (!ty || !ty->get("dims") || ty->get("dims")->kind != Json::Array || !prim_of(ty->get("precision"), &nd.prec))
             return bad("output_type needs dims and precision");
-        for (const Json &d : ty->get("dims")->items) nd.dims.push_back(extent_of(d));
+        for (const Json &d : ty->get("dims")->items) {
+            int64_t e;
+            if (d.kind != Json::Object || d.fields.size() != 1 ||
+                (d.fields[0].first != "Lit" && d.fields[0].first != "Named") || !extent_of(d, g, &nd, &e))
+                return bad("output_type dims must be DimInfo values");
+            nd.dims.push_back(e);
+            std::string raw;
+            write_json(d, &raw);
+            nd.dims_raw.push_back(raw);
+        }
         const Json *reuse = j.get("reusable_input");
         if (reuse && reuse->kind != Json::Null && !int_of(reuse, &nd.reusable)) return bad("bad reusable_input");
         if (const Json *span = j.get("span_id")) {
@@ -406,7 +504,10 @@ std::string write_graph(const Graph &g) {
         o += ",\"output_type\":{\"dims\":[";
         for (size_t d = 0; d < n.dims.size(); ++d) {
             if (d) o += ",";
-            o += "{\"Lit\":" + std::to_string(n.dims[d]) + "}";
+            if (d < n.dims_raw.size()) o += n.dims_raw[d];
+            else if (extent_is_symbol(n.dims[d]))
+                o += "{\"Named\":[" + json_quote(g.symbols[(size_t)extent_symbol(n.dims[d])]) + ",null]}";
+            else o += "{\"Lit\":" + std::to_string(n.dims[d]) + "}";
         }
         o += "],\"precision\":" + json_quote(prim_name(n.prec)) + "}";
         o += ",\"reusable_input\":" + (n.reusable >= 0 ? std::to_string(n.reusable) : std::string("null"));

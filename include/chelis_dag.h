@@ -29,26 +29,45 @@ extern "C" {
 typedef struct chelis_dag_program chelis_dag_program;
 
 /* Reads and plans a DAG; host work only (constants reach a device on the
- * first run there). The inputs are the DAG's Load nodes in node order, the
- * outputs its roots in order. */
+ * first run there). The inputs are the DAG's Load names in first-appearance
+ * order (a repeated name is one input); the outputs its Store nodes, then
+ * its roots, each node once (the reference's output specs,
+ * crates/chelis-backend-hip/src/emit.rs:5881-5933).
+ *
+ * Run-time extents: a dimension declared as Named(name, None), or an
+ * RtDim Sym / InputAxis extent, is a symbol bound when the program runs
+ * from the first input axis that declares it; every other declaring axis
+ * must agree. One compiled program runs at any binding. */
 chelis_dag_program *chelis_dag_compile(const char *json, int64_t length);
 void chelis_dag_release(chelis_dag_program *program);
 /* Enqueues the program on the library stream (chelis_hip_stream()) over
  * caller-owned device packets; returns without synchronizing. Input packets
- * may be any strided views of the declared shapes and dtypes. */
+ * may be any strided views of the declared shapes and dtypes; outputs have
+ * the shapes chelis_dag_output_shape reports for these inputs. */
 int32_t chelis_dag_run(chelis_dag_program *program, const chelis_gpu_tensor *const *inputs, int32_t n_in,
                        const chelis_gpu_tensor *const *outputs, int32_t n_out);
 
 int32_t chelis_dag_input_count(const chelis_dag_program *program);
 int32_t chelis_dag_output_count(const chelis_dag_program *program);
-/* output == 0: input slot `index` (its Load's name); 1: output slot (the
- * root's span name, else "out<index>"). */
+/* output == 0: input slot `index` (its Load's name); 1: output slot (a
+ * Store's name, else "root<index>" with the root's position). */
 const char *chelis_dag_label(const chelis_dag_program *program, int32_t output, int32_t index);
+/* The declared type; a run-time extent is reported as -1. */
 int32_t chelis_dag_type(const chelis_dag_program *program, int32_t output, int32_t index, int32_t *rank,
                         int64_t *shape, int32_t shape_capacity, int32_t *dtype);
+/* Output `index`'s shape for these inputs (their run-time extents bound as
+ * chelis_dag_run binds them); host work only. */
+int32_t chelis_dag_output_shape(const chelis_dag_program *program, const chelis_gpu_tensor *const *inputs,
+                                int32_t n_in, int32_t index, int32_t *rank, int64_t *shape, int32_t shape_capacity);
+/* The run-time extents, in binding order (the reference's symbolic_dims). */
+int32_t chelis_dag_symbol_count(const chelis_dag_program *program);
+const char *chelis_dag_symbol_name(const chelis_dag_program *program, int32_t index);
 /* Workspace plus constant pool bytes one run needs on a device (the
- * reference's peak_device_bytes_estimate, memory.rs:130-155). */
+ * reference's peak_device_bytes_estimate, memory.rs:130-155); -1 when a
+ * run-time extent sizes it. _at evaluates it for extents given in binding
+ * order (HipCodegenResult::peak_device_bytes_at, lib.rs:67-77). */
 int64_t chelis_dag_peak_device_bytes(const chelis_dag_program *program);
+int64_t chelis_dag_peak_device_bytes_at(const chelis_dag_program *program, const int64_t *values, int32_t n);
 int64_t chelis_dag_launch_count(const chelis_dag_program *program);
 /* One line per launch: index, region kind, result node, input nodes. */
 const char *chelis_dag_describe(const chelis_dag_program *program);

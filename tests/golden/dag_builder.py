@@ -3,7 +3,8 @@ for the DAG front end (chelis_amd/csrc/dag_*.cpp).
 
 The wire shape is the reference's `serde_json::to_string(&dag)`:
   Dag      {"nodes": [DagNode...], "roots": [id...], "declarations": [{"name", "value"}]}
-  DagNode  {"id", "op", "inputs", "output_type": {"dims": [{"Lit": n}], "precision": "F32"},
+  DagNode  {"id", "op", "inputs", "output_type": {"dims": [{"Lit": n} | {"Named": [name, null]}],
+            "precision": "F32"},
             "reusable_input", "span_id", "merged_spans", "shape_deps", "result_claim_deps",
             "owner": {"decl": 0, "activation": null}}
   op       a unit variant as a string ("Add") or {"Variant": {fields}}
@@ -45,6 +46,12 @@ def _f64_bits(v: float) -> str:
     return "%016x" % struct.unpack("<Q", struct.pack("<d", v))[0]
 
 
+def _dim(d):
+    """DimInfo: a literal, or a string naming an extent known only at run
+    time (DimInfo::Named(name, None), crates/chelis-dag-core/src/dag.rs:276-281)."""
+    return {"Named": [d, None]} if isinstance(d, str) else {"Lit": int(d)}
+
+
 class Dag:
     def __init__(self, name: str = "entry"):
         self.nodes: list[dict] = []
@@ -57,7 +64,7 @@ class Dag:
         nid = len(self.nodes)
         self.nodes.append({
             "id": nid, "op": op, "inputs": list(inputs),
-            "output_type": {"dims": [{"Lit": int(d)} for d in dims], "precision": PREC[prec]},
+            "output_type": {"dims": [_dim(d) for d in dims], "precision": PREC[prec]},
             "reusable_input": None, "span_id": span, "merged_spans": [], "shape_deps": list(shape_deps),
             "result_claim_deps": [], "owner": {"decl": 0, "activation": None},
         })
@@ -121,9 +128,16 @@ class Dag:
         return self.node("DropoutReplay" if replay else "Dropout", [x, rate, key], self.dims(x), self.prec(x))
 
     # ---- movement ----
-    def expand(self, x, axis, size):
+    def expand(self, x, axis, size, source=None):
+        """A literal size, or (size a run-time extent's name) the extent of
+        `source`'s axis `axis`, read as RtDim::InputAxis{tensor: 1} with
+        `source` as the second input (tier2.rs:1106-1141)."""
         d = list(self.dims(x))
         d.insert(axis, size)
+        if isinstance(size, str):
+            assert source is not None and self.dims(source)[axis] == size
+            rt = {"InputAxis": {"tensor": 1, "axis": {"Lit": axis}}}
+            return self.node({"Expand": {"axis": axis, "size": rt}}, [x, source], d, self.prec(x))
         return self.node({"Expand": {"axis": axis, "size": {"Lit": int(size)}}}, [x], d, self.prec(x))
 
     def permute(self, x, axes):
@@ -166,11 +180,11 @@ class Dag:
     def softmax(self, x, axis):
         n = self.dims(x)[axis]
         m = self.max_reduce(x, axis)
-        me = self.expand(m, axis, n)
+        me = self.expand(m, axis, n, source=x)
         shifted = self.sub(x, me)
         e = self.exp(shifted)
         s = self.sum(e, axis)
-        se = self.expand(s, axis, n)
+        se = self.expand(s, axis, n, source=x)
         return self.div(e, se)
 
     def matmul(self, a, b):
@@ -383,6 +397,10 @@ def mlp_program(Bt, I, Hd, O, rate=0.1, lr=0.01):
 FIXTURES = {
     "softmax_f32_16384x1024": lambda: softmax_program(16384, 1024, "f32"),
     "softmax_f64_4096x4096": lambda: softmax_program(4096, 4096, "f64"),
+    # run-time extents: the row count, and both extents (the softmax axis
+    # then reaches its expands as InputAxis reads of x, tier2.rs:1106-1114)
+    "softmax_f32_rows_x1024": lambda: softmax_program("rows", 1024, "f32"),
+    "softmax_f32_rows_x_cols": lambda: softmax_program("rows", "cols", "f32"),
     "gemm_f32_4096": lambda: matmul_program(4096, 4096, 4096, "f32"),
     "gemm_f64_4096": lambda: matmul_program(4096, 4096, 4096, "f64"),
     "skinny_f64_8192x64x4096": lambda: matmul_program(8192, 64, 4096, "f64"),

@@ -2,6 +2,7 @@
 and written back byte for byte, fuse.rs's chain rules, the region plans of
 the configuration programs, unsupported ops named, and the codegen surface
 (its source compiles against the library's headers)."""
+import ctypes
 import json
 import os
 import subprocess
@@ -142,7 +143,9 @@ def test_plans_of_the_configuration_programs():
     k = kinds(m)
     assert k.count("matmul") == 5 and k.count("softmax") == 1 and k.count("softmax_adjoint") == 1
     assert k.count("dropout") == 2 and k.count("relu") == 1 and k.count("relu_adjoint") == 1
-    assert [o[0] for o in m.outputs] == ["out0", "out1", "out2", "out3", "out4"]
+    # output labels are the reference's output specs: "root<index>"
+    # (crates/chelis-backend-hip/src/emit.rs:5923-5930)
+    assert [o[0] for o in m.outputs] == ["root0", "root1", "root2", "root3", "root4"]
     assert [i[0] for i in m.inputs] == ["x", "onehot", "w1", "b1", "w2", "b2", "key"]
 
 
@@ -168,7 +171,7 @@ def test_unsupported_ops_are_named():
 def test_codegen_surface_and_its_source_compiles():
     text = open(os.path.join(DAGS, "linreg_step_8192x32.json")).read()
     r = C.CodegenResult(text, "linreg_step_dag")
-    assert r.input_labels == ["X", "w", "y"] and r.output_labels == ["out0", "out1"]
+    assert r.input_labels == ["X", "w", "y"] and r.output_labels == ["root0", "root1"]
     assert r.symbolic_dims == [] and r.peak_device_bytes_estimate == plan("linreg_step_8192x32").peak_device_bytes
     assert "-lchelis_hip" in r.link_flags
     assert "extern \"C\" void linreg_step_dag_device(" in r.c_source
@@ -185,3 +188,264 @@ def test_codegen_surface_and_its_source_compiles():
         assert out.returncode == 0, out.stderr[-3000:]
         syms = subprocess.run(["nm", "-D", "--defined-only", lib], capture_output=True, text=True).stdout
         assert " linreg_step_dag_device" in syms and " linreg_step_dag\n" in syms
+
+
+# ---------------------------------------------------------------- run-time extents
+def node(nid, op, inputs, dims, prec="F32", claims=(), span=None):
+    """One DagNode in the wire form; dims are DimInfo values."""
+    return {"id": nid, "op": op, "inputs": list(inputs), "output_type": {"dims": list(dims), "precision": prec},
+            "reusable_input": None, "span_id": span, "merged_spans": [], "shape_deps": [],
+            "result_claim_deps": list(claims), "owner": {"decl": 0, "activation": None}}
+
+
+def dag(nodes, roots):
+    return json.dumps({"nodes": nodes, "roots": roots, "declarations": [{"name": "t", "value": False}]},
+                      separators=(",", ":"))
+
+
+LIT = lambda n: {"Lit": n}  # noqa: E731
+NAMED = lambda s, n=None: {"Named": [s, n]}  # noqa: E731
+
+
+def fake_packet(shape, dtype=0, width=4):
+    """A packet with a dummy device address: the binding and shape queries
+    read only metadata, so no device is touched."""
+    n = len(shape)
+    sh = (ctypes.c_int64 * max(1, n))(*shape)
+    st = (ctypes.c_int64 * max(1, n))()
+    acc = 1
+    for a in reversed(range(n)):
+        st[a] = acc
+        acc *= max(1, shape[a])
+    t = C.GpuTensor()
+    t.data, t.shape, t.strides, t.rank, t.dtype = 0x10000, sh, st, n, dtype
+    t.count = 1
+    for e in shape:
+        t.count *= e
+    t.byte_capacity = max(1, t.count) * width
+    t._keep = (sh, st)
+    return t
+
+
+class Fake:
+    def __init__(self, shape, dtype=0, width=4):
+        self.t = fake_packet(shape, dtype, width)
+        self.packet = ctypes.pointer(self.t)
+
+
+def test_named_extents_round_trip_byte_for_byte():
+    """DimInfo::Named with and without a value, an RtDim::Sym reshape target
+    and an InputAxis expand are written back exactly as read."""
+    text = dag([node(0, {"Load": {"name": "x"}}, [], [NAMED("rows"), NAMED("n", 4)], span="x"),
+                node(1, {"MaxReduce": {"axis": 1}}, [0], [NAMED("rows")]),
+                node(2, {"Expand": {"axis": 1, "size": {"InputAxis": {"tensor": 1, "axis": {"Lit": 1}}}}}, [1, 0],
+                     [NAMED("rows"), NAMED("n", 4)]),
+                node(3, {"Reshape": {"new_shape": [{"Sym": "rows"}, {"Lit": 4}]}}, [2], [NAMED("rows"), LIT(4)])],
+               [3])
+    assert C.dag_fuse(text) == text
+    # the fused form keeps a chain's run-time extents too
+    sm = open(os.path.join(DAGS, "softmax_f32_rows_x_cols.json")).read().strip()
+    fe = [n for n in json.loads(C.dag_fuse(sm))["nodes"] if isinstance(n["op"], dict) and "FusedElem" in n["op"]]
+    assert fe and fe[0]["output_type"]["dims"] == [NAMED("rows"), NAMED("cols")]
+    assert "Lit\":-1" not in C.dag_fuse(sm)
+
+
+def test_softmax_with_run_time_extents_binds_them_from_its_input():
+    """tier2.rs:2964 softmax_accepts_symbolic_axis_extent: the expands read
+    the softmax axis from x; the plan is still the one softmax region and
+    binds both extents from the input packet at each call."""
+    p = C.DagProgram(open(os.path.join(DAGS, "softmax_f32_rows_x_cols.json")).read())
+    assert kinds(p) == ["softmax"]
+    assert p.symbolic_dims == ["rows", "cols"]
+    assert p.inputs == [("x", (-1, -1), 0)] and p.outputs == [("root0", (-1, -1), 0)]
+    for shape in [(3, 5), (4096, 1024)]:
+        assert p.output_shapes([Fake(shape)]) == [shape]
+    with pytest.raises(C.ChelisError, match="rank"):
+        p.output_shapes([Fake((3, 5, 1))])
+    r = C.CodegenResult(open(os.path.join(DAGS, "softmax_f32_rows_x_cols.json")).read(), "softmax_rows")
+    assert r.symbolic_dims == ["rows", "cols"]
+    assert "chelis_device_metadata rows = input_view_0->shape[0];" in r.c_source
+    assert "chelis_output_shape_0[2] = { rows, cols };" in r.c_source
+
+
+def test_a_slot_sized_by_a_run_time_extent_has_a_symbolic_peak():
+    g = DB.Dag("sym")
+    x = g.load("x", ["rows", 1024], "f32")
+    sm = g.softmax(x, 1)
+    g.roots = [g.add(sm, sm)]
+    p = plan(g.json())
+    assert kinds(p) == ["softmax", "chain"]
+    assert p.peak_device_bytes == -1
+    assert p.peak_device_bytes_at(rows=3) == 3 * 4096
+    assert p.peak_device_bytes_at(rows=5) == 5 * 4096
+    r = C.CodegenResult(g.json(), "sym")
+    assert r.peak_device_bytes_formula == "4096*rows" and r.peak_device_bytes_estimate is None
+    # a size expression whose coefficient is not a multiple of 256 is rounded
+    g2 = DB.Dag("odd")
+    y = g2.load("y", ["n", 3], "f32")
+    s2 = g2.softmax(y, 1)
+    g2.roots = [g2.add(s2, s2)]
+    p2 = plan(g2.json())
+    assert C.CodegenResult(g2.json(), "odd").peak_device_bytes_formula == "round_up(12*n, 256)"
+    assert p2.peak_device_bytes_at(n=1) == 256 and p2.peak_device_bytes_at(n=22) == 512
+
+
+def test_agreeing_declarations_of_one_extent_are_checked():
+    g = DB.Dag("two")
+    x, y = g.load("x", ["n", 4], "f32"), g.load("y", ["n", 4], "f32")
+    g.roots = [g.add(g.exp(x), y)]
+    p = plan(g.json())
+    assert p.symbolic_dims == ["n"]
+    assert p.output_shapes([Fake((3, 4)), Fake((3, 4))]) == [(3, 4)]
+    with pytest.raises(C.ChelisError, match=r"symbolic dim `n` mismatch: y\[0\]=5 but n=3"):
+        p.output_shapes([Fake((3, 4)), Fake((5, 4))])
+    r = C.CodegenResult(g.json(), "two")
+    assert "symbolic dim `n` mismatch: y[0]=%lld but n=%lld" in r.c_source
+
+
+def test_extents_this_build_cannot_bind_are_refused_never_written_as_literals():
+    read_from_node = dag([node(0, {"Load": {"name": "x"}}, [], [LIT(4)], span="x"),
+                          node(1, {"Load": {"name": "k"}}, [], [], prec="Int64"),
+                          node(2, {"Expand": {"axis": 0, "size": {"Node": 1}}}, [0, 1], [NAMED("m"), LIT(4)])],
+                         [2])
+    assert C.dag_fuse(read_from_node) == read_from_node
+    with pytest.raises(C.ChelisError, match="a bound read from a node value is a run-time extent"):
+        plan(read_from_node)
+    with pytest.raises(C.ChelisError, match="run-time extent"):
+        C.CodegenResult(read_from_node, "f")
+    undeclared = dag([node(0, {"Load": {"name": "x"}}, [], [LIT(4)], span="x"),
+                      node(1, {"Reshape": {"new_shape": [{"Sym": "k"}, {"Lit": 2}]}}, [0], [NAMED("k"), LIT(2)])],
+                     [1])
+    with pytest.raises(C.ChelisError, match="run-time extent `k` is not declared by any input"):
+        plan(undeclared)
+
+
+def test_output_specs_follow_the_reference():
+    """emit.rs:5881-5933: one input slot per Load name, Store nodes first
+    under their names, then each root once as root<index>."""
+    text = dag([node(0, {"Load": {"name": "x"}}, [], [LIT(4)], span="x"),
+                node(1, {"Load": {"name": "x"}}, [], [LIT(4)], span="x"),
+                node(2, "Neg", [0], [LIT(4)]),
+                node(3, "Exp", [1], [LIT(4)]),
+                node(4, {"Store": {"name": "grads.1"}}, [3], [LIT(4)])],
+               [2, 2, 3])
+    p = plan(text)
+    assert [i[0] for i in p.inputs] == ["x"]
+    assert [o[0] for o in p.outputs] == ["grads.1", "root0", "root2"]
+
+
+def test_extent_witness_requirements_are_checked_before_a_run():
+    witness = {"ExtentWitness": {"site": "Caller", "parameter": "x", "axis": {"Lit": 0},
+                                 "requirements": [{"dtype": "int64", "value": 4}], "claims": []}}
+    text = dag([node(0, {"Load": {"name": "x"}}, [], [NAMED("n"), LIT(2)], span="x"),
+                node(1, witness, [], [], prec="Int64"),
+                node(2, "Neg", [0], [NAMED("n"), LIT(2)])],
+               [2])
+    p = plan(text)
+    assert p.output_shapes([Fake((4, 2))]) == [(4, 2)]
+    with pytest.raises(C.ChelisError, match="extent `x` axis 0: claimed = 4, got 5"):
+        p.output_shapes([Fake((5, 2))])
+
+
+# ---------------------------------------------------------------- fuse's claim barrier
+LITERAL_CLAIM = {"ExtentWitness": {"site": "LiteralResultClaim", "parameter": "", "axis": {"Lit": 0},
+                                   "requirements": [{"dtype": "int64", "value": 4}], "claims": []}}
+
+
+def test_a_claimed_producer_neither_starts_nor_joins_a_chain():
+    """fuse.rs:147-161,183 with axis_sources.rs:3693-3753. Without the
+    barrier Neg -> Exp is one two-step chain; with a result claim on Neg it
+    cannot start one, and Exp alone is not a chain, so the DAG is unchanged."""
+    free = dag([node(0, {"Load": {"name": "x"}}, [], [LIT(4)], span="x"),
+                node(1, LITERAL_CLAIM, [], [], prec="Int64"),
+                node(2, "Neg", [0], [LIT(4)]),
+                node(3, "Exp", [2], [LIT(4)])], [3])
+    assert ops(json.loads(C.dag_fuse(free))) == ["Load", "ExtentWitness", "FusedElem"]
+    claimed = json.loads(free)
+    claimed["nodes"][2]["result_claim_deps"] = [1]
+    text = json.dumps(claimed, separators=(",", ":"))
+    assert C.dag_fuse(text) == text
+    # the claim on the chain's end stops the extension into it
+    end = json.loads(free)
+    end["nodes"][3]["result_claim_deps"] = [1]
+    text = json.dumps(end, separators=(",", ":"))
+    assert C.dag_fuse(text) == text
+
+
+def test_the_claim_barrier_follows_copies_and_casts():
+    """A Copy that owns a claim protects its input (the transitive walk,
+    axis_sources.rs:3713-3731): Exp cannot join Neg's chain."""
+    d = {"nodes": [node(0, {"Load": {"name": "x"}}, [], [LIT(4)], span="x"),
+                   node(1, LITERAL_CLAIM, [], [], prec="Int64"),
+                   node(2, "Neg", [0], [LIT(4)]),
+                   node(3, "Exp", [2], [LIT(4)]),
+                   node(4, "Copy", [3], [LIT(4)], claims=[1])],
+         "roots": [4], "declarations": []}
+    text = json.dumps(d, separators=(",", ":"))
+    assert C.dag_fuse(text) == text
+    d["nodes"][4]["result_claim_deps"] = []  # no claim: Neg -> Exp fuse
+    assert ops(json.loads(C.dag_fuse(json.dumps(d)))) == ["Load", "ExtentWitness", "FusedElem", "Copy"]
+
+
+def test_a_division_under_an_activation_keeps_its_own_kernel():
+    """dag.rs:2555-2556,2864-2880: every Div may fail its check, so under an
+    activation it is not fused; Exp -> Log under the same activation is."""
+    d = {"nodes": [node(0, {"Load": {"name": "on"}}, [], [], prec="Bool", span="on"),
+                   node(1, {"Load": {"name": "x"}}, [], [LIT(4)], span="x"),
+                   node(2, "Exp", [1], [LIT(4)]),
+                   node(3, "Div", [2, 2], [LIT(4)]),
+                   node(4, "Log", [3], [LIT(4)]),
+                   node(5, "Sqrt", [4], [LIT(4)])],
+         "roots": [5], "declarations": []}
+    for n in d["nodes"][2:]:
+        n["owner"]["activation"] = 0
+    assert ops(json.loads(C.dag_fuse(json.dumps(d)))) == ["Load", "Load", "Exp", "Div", "FusedElem"]
+
+
+# ---------------------------------------------------------------- generated entry traps
+def _generated(tmp, name="linreg_step_8192x32", func="gen"):
+    r = C.CodegenResult(open(os.path.join(DAGS, name + ".json")).read(), func)
+    src = os.path.join(tmp, "gen.cpp")
+    with open(src, "w") as fh:
+        fh.write(r.c_source)
+    lib = os.path.join(tmp, "libgen.so")
+    out = subprocess.run(["g++", "-shared", "-fPIC", *r.compile_flags, src, "-o", lib, *r.link_flags],
+                         capture_output=True, text=True)
+    assert out.returncode == 0, out.stderr[-3000:]
+    return lib
+
+
+CHILD = r"""
+import ctypes, sys
+lib = ctypes.CDLL(sys.argv[1])
+case = sys.argv[2]
+arr = (ctypes.c_void_p * 4)()
+if case == "device_arity":
+    lib.gen_device(arr, 2, arr, 2)
+elif case == "device_outputs":
+    lib.gen_device(arr, 3, arr, 5)
+elif case == "device_null":
+    lib.gen_device(None, 3, arr, 2)
+elif case == "host_arity":
+    lib.gen(arr, 1, arr, 2)
+elif case == "host_null":
+    lib.gen(arr, 3, None, 2)
+"""
+
+
+@pytest.mark.parametrize("case,status,text", [
+    ("device_arity", -6, "gen_device: expected 3 inputs, got 2"),
+    ("device_outputs", -6, "gen_device: expected 2 outputs, got 5"),
+    ("device_null", 1, "numeric trap: domain in entry at i64"),
+    ("host_arity", -6, "gen: expected 3 inputs, got 1"),
+    ("host_null", 1, "numeric trap: domain in entry at i64"),
+])
+def test_generated_entries_trap_as_the_reference_does(case, status, text):
+    """emit.rs:676-695,857-876: a count mismatch prints and aborts; null
+    arrays are a `domain` numeric trap (exit status 1). Both are checked
+    before any HIP call, so they run without a device."""
+    with tempfile.TemporaryDirectory() as tmp:
+        lib = _generated(tmp)
+        r = subprocess.run([sys.executable, "-c", CHILD, lib, case], capture_output=True, text=True, timeout=120)
+    assert r.returncode == status, (r.returncode, r.stderr[-2000:])
+    assert text in r.stderr
