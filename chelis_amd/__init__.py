@@ -152,6 +152,15 @@ SIGNATURES = {
     "chelis_dag_describe": (ctypes.c_char_p, [c_void_p]),
     "chelis_dag_fuse": (ctypes.c_char_p, [ctypes.c_char_p, c_int64]),
     "chelis_codegen_hip": (c_void_p, [ctypes.c_char_p, c_int64, ctypes.c_char_p]),
+    "chelis_prepare_dag_for_codegen": (ctypes.c_char_p, [ctypes.c_char_p, c_int64]),
+    "chelis_hip_tensor_capable_prims": (c_int32, [POINTER(POINTER(c_uint8))]),
+    "chelis_hip_runtime_dir": (ctypes.c_char_p, []),
+    "chelis_codegen_hip_host_program": (c_void_p, [c_int32, POINTER(ctypes.c_char_p), POINTER(ctypes.c_char_p),
+                                                   POINTER(c_int64)]),
+    "chelis_host_program_release": (None, [c_void_p]),
+    "chelis_host_program_helper_count": (c_int32, [c_void_p]),
+    "chelis_host_program_helper_name": (ctypes.c_char_p, [c_void_p, c_int32]),
+    "chelis_host_program_helper": (c_void_p, [c_void_p, c_int32]),
     "chelis_codegen_release": (None, [c_void_p]),
     "chelis_codegen_c_source": (ctypes.c_char_p, [c_void_p]),
     "chelis_codegen_h_header": (ctypes.c_char_p, [c_void_p]),
@@ -681,14 +690,64 @@ def dag_fuse(json_text: str) -> str:
     return out.decode()
 
 
+def prepare_dag_for_codegen(json_text: str) -> str:
+    """The BLAS selection before codegen (lowered matmuls as BlasMatmul)."""
+    data = json_text.encode()
+    out = lib().chelis_prepare_dag_for_codegen(data, len(data))
+    if out is None:
+        raise ChelisError(lib().chelis_hip_last_error().decode(errors="replace"))
+    return out.decode()
+
+
+def tensor_capable_prims():
+    """TENSOR_CAPABLE_PRIMS as dtype ids."""
+    arr = POINTER(c_uint8)()
+    n = lib().chelis_hip_tensor_capable_prims(ctypes.byref(arr))
+    return [arr[k] for k in range(n)]
+
+
+def runtime_dir() -> str:
+    return lib().chelis_hip_runtime_dir().decode()
+
+
+def codegen_hip_host_program(helpers):
+    """[(name, dag_json)] -> [(name, CodegenResult)] for the Count-bearing helpers."""
+    names = (ctypes.c_char_p * max(1, len(helpers)))(*[n.encode() for n, _ in helpers])
+    texts = [t.encode() for _, t in helpers]
+    dags = (ctypes.c_char_p * max(1, len(helpers)))(*texts)
+    lens = (c_int64 * max(1, len(helpers)))(*[len(t) for t in texts])
+    L = lib()
+    h = L.chelis_codegen_hip_host_program(len(helpers), names, dags, lens)
+    if not h:
+        raise ChelisError("codegen_hip_host_program failed: " + L.chelis_hip_last_error().decode(errors="replace"))
+    try:
+        return [(L.chelis_host_program_helper_name(h, k).decode(),
+                 CodegenResult._from_handle(L.chelis_host_program_helper(h, k)))
+                for k in range(L.chelis_host_program_helper_count(h))]
+    finally:
+        L.chelis_host_program_release(h)
+
+
 class CodegenResult:
     """chelis_codegen_hip: the HipCodegenResult fields."""
+
+    @classmethod
+    def _from_handle(cls, h):
+        self = cls.__new__(cls)
+        self._read(h)
+        return self
 
     def __init__(self, json_text: str, func_name: str):
         data = json_text.encode()
         h = lib().chelis_codegen_hip(data, len(data), func_name.encode())
         if not h:
             raise ChelisError("codegen_hip failed: " + lib().chelis_hip_last_error().decode(errors="replace"))
+        try:
+            self._read(h)
+        finally:
+            lib().chelis_codegen_release(h)
+
+    def _read(self, h):
         L = lib()
         lists = [[L.chelis_codegen_list_item(h, w, i).decode() for i in range(L.chelis_codegen_list_count(h, w))]
                  for w in range(5)]
@@ -698,7 +757,6 @@ class CodegenResult:
         self.peak_device_bytes_formula = L.chelis_codegen_peak_device_bytes_formula(h).decode()
         est = L.chelis_codegen_peak_device_bytes_estimate(h)
         self.peak_device_bytes_estimate = None if est < 0 else est
-        L.chelis_codegen_release(h)
 
 
 class GeneratedProgram:

@@ -165,6 +165,10 @@ std::vector<bool> claimed_producers(const Graph &g);
 // fuse.rs:76-96 with the activation gate (dag.rs:2864-2880): whether the
 // node may be a chain link at all.
 bool chain_fusible(const Node &n);
+// prepare_dag_for_codegen's BLAS selection (lib.rs:173-227, specialize.rs:
+// 150-226): lowered matmuls as BlasMatmul nodes over strided operands (no
+// Realize copies); idempotent.
+Graph prepare_for_codegen(const Graph &g);
 // fuse.rs:463-487: FusedElem nodes whose only consumer is a Sum or
 // MaxReduce (they become that reduction's leaf).
 std::vector<bool> reduction_inlined(const Graph &g);

@@ -17,6 +17,8 @@
 // preamble's `chelis_device_metadata <name>` bindings) and size the outputs;
 // the program is planned once per process, on first call.
 #include <dlfcn.h>
+#include <limits.h>
+#include <stdlib.h>
 
 #include <algorithm>
 #include <string>
@@ -357,6 +359,48 @@ std::string emit_source(const Plan &plan, const Graph &fused, const std::string 
 using namespace chelis;
 using namespace chelis::dag;
 
+namespace {
+thread_local std::string g_prepared;
+}
+
+extern "C" const char *chelis_prepare_dag_for_codegen(const char *json, int64_t length) {
+    if (!json || length < 0) {
+        set_error(CHELIS_HIP_EDOMAIN, "prepare_dag_for_codegen: null or negative-length text");
+        return nullptr;
+    }
+    try {
+        Graph g;
+        std::string error;
+        if (!read_graph(json, (size_t)length, &g, &error)) {
+            set_error(CHELIS_HIP_EDOMAIN, "prepare_dag_for_codegen: %s", error.c_str());
+            return nullptr;
+        }
+        g_prepared = write_graph(prepare_for_codegen(g));
+        return g_prepared.c_str();
+    } catch (const std::exception &e) {
+        set_error(CHELIS_HIP_EHIP, "prepare_dag_for_codegen: %s", e.what());
+        return nullptr;
+    }
+}
+
+extern "C" int32_t chelis_hip_tensor_capable_prims(const chelis_dtype **prims) {
+    // lib.rs:10-18, in its order: F32, F64, Bool, Bf16, F16, Int32, Int64
+    static const chelis_dtype kPrims[] = {CHELIS_DTYPE_F32, CHELIS_DTYPE_F64, CHELIS_DTYPE_BOOL, CHELIS_DTYPE_BF16,
+                                          CHELIS_DTYPE_F16, CHELIS_DTYPE_I32, CHELIS_DTYPE_I64};
+    if (prims) *prims = kPrims;
+    return (int32_t)(sizeof kPrims / sizeof kPrims[0]);
+}
+
+extern "C" const char *chelis_hip_runtime_dir(void) {
+    static const std::string dir = [] {
+        std::string d = library_dir() + "/../include";
+        char buf[4096];
+        if (realpath(d.c_str(), buf)) d = buf;
+        return d;
+    }();
+    return dir.c_str();
+}
+
 extern "C" chelis_hip_codegen_result *chelis_codegen_hip(const char *json, int64_t length, const char *func_name) {
     if (!json || length < 0 || !func_name || !identifier(func_name)) {
         set_error(CHELIS_HIP_EDOMAIN, "codegen_hip: a DAG and a C identifier for the function name are required");
@@ -412,4 +456,66 @@ extern "C" const char *chelis_codegen_peak_device_bytes_formula(const chelis_hip
 }
 extern "C" int64_t chelis_codegen_peak_device_bytes_estimate(const chelis_hip_codegen_result *r) {
     return r ? r->estimate : -1;
+}
+
+struct chelis_hip_host_program_result {
+    std::vector<std::string> names;
+    std::vector<chelis_hip_codegen_result *> helpers;
+    ~chelis_hip_host_program_result() {
+        for (auto *h : helpers) delete h;
+    }
+};
+
+extern "C" chelis_hip_host_program_result *chelis_codegen_hip_host_program(int32_t n_helpers,
+                                                                           const char *const *names,
+                                                                           const char *const *dags,
+                                                                           const int64_t *lengths) {
+    if (n_helpers < 0 || (n_helpers && (!names || !dags || !lengths))) {
+        set_error(CHELIS_HIP_EDOMAIN, "codegen_hip_host_program: a helper manifest is required");
+        return nullptr;
+    }
+    auto *r = new chelis_hip_host_program_result();
+    try {
+        for (int32_t h = 0; h < n_helpers; ++h) {
+            Graph g;
+            std::string error;
+            if (!names[h] || !dags[h] || lengths[h] < 0 || !read_graph(dags[h], (size_t)lengths[h], &g, &error)) {
+                set_error(CHELIS_HIP_EDOMAIN, "codegen_hip_host_program: helper %d: %s", h,
+                          error.empty() ? "a name and a DAG are required" : error.c_str());
+                delete r;
+                return nullptr;
+            }
+            // lib.rs:245-256: the one selection predicate - a helper whose
+            // DAG holds a Count runs on the device; there is no C fallback
+            bool count = false;
+            for (const Node &nd : g.nodes) count = count || nd.op == Op::Count;
+            if (!count) continue;
+            const std::string prepared = write_graph(prepare_for_codegen(g));
+            chelis_hip_codegen_result *c =
+                chelis_codegen_hip(prepared.c_str(), (int64_t)prepared.size(), names[h]);
+            if (!c) {
+                delete r;
+                return nullptr;  // chelis_codegen_hip set the error, naming the helper's node
+            }
+            r->names.push_back(names[h]);
+            r->helpers.push_back(c);
+        }
+        return r;
+    } catch (const std::exception &e) {
+        delete r;
+        set_error(CHELIS_HIP_EHIP, "codegen_hip_host_program: %s", e.what());
+        return nullptr;
+    }
+}
+
+extern "C" void chelis_host_program_release(chelis_hip_host_program_result *r) { delete r; }
+extern "C" int32_t chelis_host_program_helper_count(const chelis_hip_host_program_result *r) {
+    return r ? (int32_t)r->helpers.size() : -1;
+}
+extern "C" const char *chelis_host_program_helper_name(const chelis_hip_host_program_result *r, int32_t i) {
+    return (r && i >= 0 && i < (int32_t)r->names.size()) ? r->names[(size_t)i].c_str() : nullptr;
+}
+extern "C" const chelis_hip_codegen_result *chelis_host_program_helper(const chelis_hip_host_program_result *r,
+                                                                       int32_t i) {
+    return (r && i >= 0 && i < (int32_t)r->helpers.size()) ? r->helpers[(size_t)i] : nullptr;
 }

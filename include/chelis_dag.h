@@ -98,6 +98,39 @@ const char *chelis_codegen_peak_device_bytes_formula(const chelis_hip_codegen_re
 /* -1 when an extent is known only at run time */
 int64_t chelis_codegen_peak_device_bytes_estimate(const chelis_hip_codegen_result *result);
 
+/* ---- the rest of the reference's build-side surface ----
+ * prepare_dag_for_codegen (crates/chelis-backend-hip/src/lib.rs:173-227):
+ * the BLAS selection before codegen - each lowered matmul
+ * [Cast](Sum(Mul(Expand(a), Expand(b)))) the reference's recognizer takes
+ * (crates/chelis-ir-core/src/specialize.rs:150-226,623-793) becomes one
+ * BlasMatmul node - written back in the wire form (a thread-local string,
+ * valid until the next call). No Realize copies are inserted: this
+ * library's matmul reads strided operands. Idempotent. */
+const char *chelis_prepare_dag_for_codegen(const char *json, int64_t length);
+/* TENSOR_CAPABLE_PRIMS (lib.rs:10-18): the dtype ids of the primitive types
+ * the tensor path realizes; returns their count. */
+int32_t chelis_hip_tensor_capable_prims(const chelis_dtype **prims);
+/* runtime_dir() (lib.rs:81-83): the directory of the headers generated
+ * code includes (this library's include/), as an absolute path. */
+const char *chelis_hip_runtime_dir(void);
+
+/* codegen_hip_host_program (lib.rs:229-300): of a host program's tensor
+ * helpers (name and DAG each, the wrapper's helper manifest), every helper
+ * whose DAG holds a Count becomes its own HIP translation unit through
+ * chelis_codegen_hip under its own name; the others keep their C-host
+ * disposition and are not listed. The scalar / container host wrapper
+ * itself is the C backend's output, which this library does not produce;
+ * it declares each listed helper as an external symbol. */
+typedef struct chelis_hip_host_program_result chelis_hip_host_program_result;
+chelis_hip_host_program_result *chelis_codegen_hip_host_program(int32_t n_helpers, const char *const *names,
+                                                                const char *const *dags, const int64_t *lengths);
+void chelis_host_program_release(chelis_hip_host_program_result *result);
+int32_t chelis_host_program_helper_count(const chelis_hip_host_program_result *result);
+const char *chelis_host_program_helper_name(const chelis_hip_host_program_result *result, int32_t index);
+/* owned by `result` */
+const chelis_hip_codegen_result *chelis_host_program_helper(const chelis_hip_host_program_result *result,
+                                                            int32_t index);
+
 #ifdef __cplusplus
 }
 #endif

@@ -128,15 +128,17 @@ class Dag:
         return self.node("DropoutReplay" if replay else "Dropout", [x, rate, key], self.dims(x), self.prec(x))
 
     # ---- movement ----
-    def expand(self, x, axis, size, source=None):
+    def expand(self, x, axis, size, source=None, source_axis=None):
         """A literal size, or (size a run-time extent's name) the extent of
-        `source`'s axis `axis`, read as RtDim::InputAxis{tensor: 1} with
-        `source` as the second input (tier2.rs:1106-1141)."""
+        `source`'s axis `source_axis` (default `axis`), read as
+        RtDim::InputAxis{tensor: 1} with `source` as the second input
+        (tier2.rs:1106-1141)."""
         d = list(self.dims(x))
         d.insert(axis, size)
         if isinstance(size, str):
-            assert source is not None and self.dims(source)[axis] == size
-            rt = {"InputAxis": {"tensor": 1, "axis": {"Lit": axis}}}
+            source_axis = axis if source_axis is None else source_axis
+            assert source is not None and self.dims(source)[source_axis] == size
+            rt = {"InputAxis": {"tensor": 1, "axis": {"Lit": source_axis}}}
             return self.node({"Expand": {"axis": axis, "size": rt}}, [x, source], d, self.prec(x))
         return self.node({"Expand": {"axis": axis, "size": {"Lit": int(size)}}}, [x], d, self.prec(x))
 
@@ -194,8 +196,8 @@ class Dag:
         L = len(lead)
         i, j, k = da[-2], da[-1], db[-1]
         assert db[-2] == j
-        ae = self.expand(a, L + 2, k)
-        be = self.expand(b, L, i)
+        ae = self.expand(a, L + 2, k, source=b, source_axis=L + 1)
+        be = self.expand(b, L, i, source=a, source_axis=L)
         prod = self.mul(ae, be)
         return self.sum(prod, L + 1)
 

@@ -449,3 +449,73 @@ def test_generated_entries_trap_as_the_reference_does(case, status, text):
         r = subprocess.run([sys.executable, "-c", CHILD, lib, case], capture_output=True, text=True, timeout=120)
     assert r.returncode == status, (r.returncode, r.stderr[-2000:])
     assert text in r.stderr
+
+
+# ---------------------------------------------------------------- build-side surface
+def blas_nodes(text):
+    return [n for n in json.loads(text)["nodes"] if isinstance(n["op"], dict) and "BlasMatmul" in n["op"]]
+
+
+def test_prepare_selects_blas_matmul_and_is_idempotent():
+    """lib.rs:173-227 over specialize.rs:150-226: a lowered matmul becomes one
+    BlasMatmul node (its Mul and Expands dropped); applying it again changes
+    nothing; the plan is the same launches."""
+    text = DB.matmul_program(64, 48, 32, "f32").json()
+    p = C.prepare_dag_for_codegen(text)
+    assert ops(json.loads(p)) == ["Load", "Load", "BlasMatmul"]
+    (bm,) = blas_nodes(p)
+    assert bm["op"]["BlasMatmul"] == {"batch_dims": [], "m": {"Concrete": 64}, "n": {"Concrete": 48},
+                                      "k": {"Concrete": 32}, "accumulator": "F32"}
+    assert bm["inputs"] == [0, 1]
+    assert C.prepare_dag_for_codegen(p) == p
+    assert kinds(plan(p)) == kinds(plan(text)) == ["matmul"]
+
+
+def test_prepare_leaves_transposed_operands_and_claimed_regions():
+    """specialize.rs:795-900: an operand read through a Permute has no
+    contiguous matrix slices, so the MLP's gradient products stay lowered
+    while its two forward products are selected; a matched region that owns
+    a result claim is not rewritten."""
+    mlp = open(os.path.join(DAGS, "mlp_train_step_1024x784x512x10.json")).read()
+    p = C.prepare_dag_for_codegen(mlp)
+    assert [(b["op"]["BlasMatmul"]["m"], b["op"]["BlasMatmul"]["n"], b["op"]["BlasMatmul"]["k"])
+            for b in blas_nodes(p)] == [({"Concrete": 1024}, {"Concrete": 512}, {"Concrete": 784}),
+                                        ({"Concrete": 1024}, {"Concrete": 10}, {"Concrete": 512})]
+    assert kinds(plan(p)) == kinds(plan(mlp))
+    d = json.loads(DB.matmul_program(8, 4, 2, "f64").json())
+    d["nodes"].append(node(len(d["nodes"]), LITERAL_CLAIM, [], [], prec="Int64"))
+    d["nodes"][-2]["result_claim_deps"] = [len(d["nodes"]) - 1]
+    d["nodes"][-1], d["nodes"][-2] = d["nodes"][-2], d["nodes"][-1]  # the witness precedes its owner
+    d["nodes"][-2]["id"], d["nodes"][-1]["id"] = len(d["nodes"]) - 2, len(d["nodes"]) - 1
+    d["nodes"][-1]["result_claim_deps"] = [len(d["nodes"]) - 2]
+    d["roots"] = [len(d["nodes"]) - 1]
+    text = json.dumps(d, separators=(",", ":"))
+    assert blas_nodes(C.prepare_dag_for_codegen(text)) == []
+
+
+def test_prepare_keeps_run_time_extents_as_symbols():
+    g = DB.Dag("sym")
+    a, b = g.load("a", ["m", 16], "f32"), g.load("b", [16, 8], "f32")
+    g.roots = [g.matmul(a, b)]
+    (bm,) = blas_nodes(C.prepare_dag_for_codegen(g.json()))
+    assert bm["op"]["BlasMatmul"]["m"] == {"Sym": "m"} and bm["output_type"]["dims"][0] == NAMED("m")
+
+
+def test_tensor_capable_prims_and_runtime_dir():
+    # lib.rs:10-18: F32, F64, Bool, Bf16, F16, Int32, Int64 as runtime dtype ids
+    assert C.tensor_capable_prims() == [0, 1, 3, 5, 6, 2, 4]
+    d = C.runtime_dir()
+    assert os.path.isabs(d) and os.path.exists(os.path.join(d, "chelis_device_owner.h"))
+
+
+def test_host_program_lowers_only_its_count_helpers():
+    """lib.rs:229-300: the Count-bearing helper becomes a HIP translation
+    unit under its own name; the softmax helper keeps its C-host disposition."""
+    g = DB.Dag("count")
+    b = g.load("b", [64, 300], "bool")
+    g.roots = [g.node({"Count": {"axes": [1]}}, [b], [64], "i64")]
+    helpers = [("row_counts", g.json()), ("probs", DB.softmax_program(4, 8, "f32").json())]
+    out = C.codegen_hip_host_program(helpers)
+    assert [n for n, _ in out] == ["row_counts"]
+    r = out[0][1]
+    assert "extern \"C\" void row_counts_device(" in r.c_source and r.input_labels == ["b"]

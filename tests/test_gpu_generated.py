@@ -174,3 +174,20 @@ def test_a_run_time_sized_workspace_slot_at_two_sizes():
         s = O.softmax_rows(xv)
         (y,) = p.run([C.to_device(xv)])
         assert bits_equal(y.numpy(), (s + s).astype(np.float32))
+
+
+@pytest.mark.parametrize("name", ["linreg_step_8192x32", "mlp_train_step_1024x784x512x10", "gemm_f64_4096"])
+def test_prepared_dag_runs_the_same_bits(name):
+    """prepare_dag_for_codegen's BlasMatmul nodes plan to the same launches
+    as the lowered matmuls they replace: identical results."""
+    text = fixture(name)
+    a, b = C.DagProgram(text), C.DagProgram(C.prepare_dag_for_codegen(text))
+    if name.startswith("linreg"):
+        ins = [C.to_device(v) for v in linreg_inputs()]
+    elif name.startswith("mlp"):
+        ins = [C.to_device(v) for v in mlp_inputs()] + [C.key_tensor(44)]
+    else:
+        rng = np.random.default_rng(5)
+        ins = [C.to_device(rng.uniform(-1, 1, (4096, 4096))) for _ in range(2)]
+    for x, y in zip(a.run(ins), b.run(ins)):
+        assert bits_equal(x.numpy(), y.numpy())
