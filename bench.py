@@ -24,7 +24,10 @@ VALU-bound their VALU issue share (`valu_issue_pct_counter`).
 
 `kernels` reports every configuration the same way: GB/s against the 8 TB/s
 HBM peak for bandwidth kernels, TFLOP/s against the dtype's MFMA peak for
-GEMMs, ms / us end to end for the three programs. `cpu_baseline` times the C
+GEMMs, ms / us end to end for the three programs. `dag_path` times the
+drop-in path on configurations 1, 2a, 2b, 4 and 5: the configuration DAGs
+run by chelis_dag_run (events, as the programs) and by the generated
+{f}_device entry (a synchronous call, wall clock). `cpu_baseline` times the C
 oracle (the restated reference C lane, gcc -O2 -ffp-contract=off -fopenmp)
 on the headline workload on this host with every core (5 warm-ups, median
 of 50 calls) and once on one thread; `kernels[*].cpu` gives the same
@@ -191,6 +194,71 @@ def bench_programs(C, H, steps, warmup):
         "frac_mfma": round(MLP_FLOPS / (ms * 1e-3) / 1e12 / PEAK_TFLOPS["f32"], 4),
         "bound": "launch latency (5 launches: two split-K products, head, tail, finish)"}
     return out, (X, w, y), (x, p), args
+
+
+# ---------------------------------------------------------------- the DAG path
+DAGS = os.path.join(ROOT, "tests", "golden", "dags")
+
+
+def _wall_us(fn, warmup=2, runs=7):
+    """Median wall-clock microseconds of a synchronous call."""
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)) * 1e6
+
+
+def _us(rec):
+    return rec["us"] if "us" in rec else rec["ms"] * 1e3
+
+
+def bench_dag_path(C, H, steps, warmup, progs, lin, tr, mlp, x_softmax, x64):
+    """The drop-in path beside the hand-wired programs: the configuration
+    DAGs (the reference's wire form, tests/golden/dags/) compiled by
+    chelis_dag_compile and enqueued by chelis_dag_run over resident inputs
+    and outputs (HIP events on the library stream, as the programs), and
+    the generated {f}_device entry compiled from chelis_codegen_hip's source
+    (a synchronous call: output allocation, the run, a device
+    synchronization; wall clock, median of 7)."""
+    out = {}
+    tmp = tempfile.TemporaryDirectory()
+    X, w, y = lin
+    x, p = tr
+    cases = [
+        ("config1_linreg_step_f64_8192x32", "linreg_step_8192x32", [C.to_device(a) for a in (X, w, y)],
+         _us(progs["linreg_step_f64_8192x32"])),
+        ("config2a_softmax_f32_16384x1024", "softmax_f32_16384x1024", [C.to_device(x_softmax)],
+         _us(progs["softmax_f32_16384x1024"])),
+        ("config2b_softmax_f64_4096x4096", "softmax_f64_4096x4096", [C.to_device(x64)],
+         _us(progs["softmax_f64_4096x4096"])),
+        ("config4_transformer_block_f32_b8_s512_d1024", "transformer_block_b8_s512_d1024",
+         [C.to_device(x)] + [C.to_device(p[k]) for k in PARAM_ORDER],
+         _us(progs["transformer_block_f32_b8_s512_d1024"])),
+        ("config5_mlp_train_step_f32_1024x784x512x10", "mlp_train_step_1024x784x512x10",
+         [C.to_device(a) for a in mlp] + [C.key_tensor(44)], _us(progs["mlp_train_step_f32_1024x784x512x10"])),
+    ]
+    for key, fixture, ins, hand_us in cases:
+        with open(os.path.join(DAGS, fixture + ".json")) as fh:
+            text = fh.read()
+        prog = C.DagProgram(text)
+        outs = prog.empty_outputs(ins)
+        big = key.startswith("config4")
+        ms = time_launches(C, H, lambda i: prog.run(ins, outs), max(3, steps // 5) if big else steps,
+                           2 if big else warmup)
+        gen = C.GeneratedProgram(text, "bench_" + fixture, tmp.name)
+        entry_us = _wall_us(lambda: gen.device(ins), runs=5 if big else 7)
+        rec = {"regions": prog.launches, "dag_run_us": round(ms * 1e3, 2),
+               "generated_device_entry_us": round(entry_us, 2)}
+        rec["hand_wired_us"] = round(hand_us, 2)
+        rec["dag_run_over_hand_wired"] = round(ms * 1e3 / hand_us, 3)
+        out[key] = rec
+        del prog, outs, gen
+    tmp.cleanup()
+    return out
 
 
 # ---------------------------------------------------------------- bandwidth families
@@ -650,6 +718,7 @@ def main(argv=None) -> int:
     kernels = {"softmax_f32_16384x1024": {"ms": round(head["ms"], 5), "GB/s": round(head["gbps"], 1),
                                           "frac_hbm": round(head["gbps"] / HBM_PEAK_GBPS, 4)}}
     extra = None
+    dag_path = None
     if not args.only_headline:
         s64, x64 = bench_softmax_f64(C, H, max(5, args.steps // 2), args.warmup)
         kernels["softmax_f64_4096x4096"] = {"ms": round(s64["ms"], 5), "GB/s": round(s64["gbps"], 1),
@@ -684,6 +753,7 @@ def main(argv=None) -> int:
         kernels["gemm_bf16_4096^3"] = gemm_line(r, "bf16", "mfma")
         progs, lin, tr, mlp = bench_programs(C, H, max(5, args.steps // 2), args.warmup)
         kernels.update(progs)
+        dag_path = bench_dag_path(C, H, max(5, args.steps // 2), args.warmup, kernels, lin, tr, mlp, x, x64)
         kernels.update(bench_bandwidth(C, H, max(5, args.steps // 2), args.warmup))
         extra = (x64, lin, tr, mlp, gin)
     traffic, tdetail = None, "skipped (--no-counters)"
@@ -736,6 +806,7 @@ def main(argv=None) -> int:
                      "traffic_detail": tdetail},
         "cpu_baseline": cpu,
         "kernels": kernels,
+        "dag_path": dag_path,
     }
     print(json.dumps(line))
     return 0

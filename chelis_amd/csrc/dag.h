@@ -182,13 +182,20 @@ std::vector<int64_t> consumer_counts(const Graph &g);
 // materialized region output.
 enum class RegionKind : uint8_t {
     Chain, Reduce, Count, Softmax, MaskedSoftmax, SoftmaxAdjoint, LayerNorm, Gelu, Relu, ReluAdjoint, Dropout,
-    Matmul, Copy, Attention
+    Matmul, Copy, Attention,
+    // several products sharing their left operand, run as one batch
+    MatmulGroup,
+    // whole lowered programs recognized as one region (their results in
+    // `out` and `more_out`): the linear-regression step and the MLP
+    // training step, run as this library's fused programs
+    LinregStep, MlpStep
 };
 const char *region_kind_name(RegionKind k);
 
 struct Region {
     RegionKind kind = RegionKind::Chain;
     int64_t out = -1;                 // the node whose value the launch produces
+    std::vector<int64_t> more_out;    // further results of a multi-result region
     std::vector<int64_t> in;          // value nodes read
     std::vector<int64_t> covers;      // every node the region computes
     chelis_fused_chain chain{};       // Chain / Reduce leaf
@@ -203,6 +210,17 @@ struct Region {
     int32_t activation = CHELIS_ACT_NONE;
     int32_t causal_mode = 0;  // 1: skip tiles above the diagonal, 2: clip the contraction
     // attention: in = {q [.., S, 64], k^T [.., 64, S], v [.., S, 64]}, scale
+    // matmul group: in = {a, b_0, bias_0, b_1, bias_1, ...}, results out,
+    // more_out in one workspace range, back to back
+    // linreg step: in = {X, w, y}, out = grad, more_out = {loss}
+    // mlp step: in = {x, onehot, w1, b1, w2, b2, key}, out = loss,
+    // more_out = {w1', b1', w2', b2'}, rate, lr (below)
+    double lr = 0.0;
+    std::vector<int64_t> outputs() const {
+        std::vector<int64_t> o{out};
+        o.insert(o.end(), more_out.begin(), more_out.end());
+        return o;
+    }
 };
 
 // How a value's storage is found at run time.
@@ -212,6 +230,7 @@ struct ValueInfo {
     int64_t input = -1, output = -1;  // caller slot indices
     int64_t base = -1;                // View: the value it views
     int64_t slot = -1;                // Slot: workspace slot
+    int64_t slot_offset = 0;          // Slot: bytes into the slot (a matmul group's later results)
     int64_t const_index = -1;         // Const: constant pool entry
     // physical order of a materialized value: perm[i] = the logical axis
     // stored i-th (outermost first); empty = row-major

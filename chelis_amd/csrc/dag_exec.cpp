@@ -12,6 +12,7 @@
 #include <mutex>
 
 #include "chelis_dag.h"
+#include "chelis_programs.h"
 #include "dag.h"
 #include "gemm.h"
 #include "hip_common.h"
@@ -258,8 +259,8 @@ int32_t run_plan(chelis_dag_program *prog, const chelis_gpu_tensor *const *input
                     }
                 }
                 const size_t k = (size_t)v.slot;
-                p.t.data = ws + offsets[k];
-                p.t.byte_capacity = (k + 1 < offsets.size() ? offsets[k + 1] : workspace) - offsets[k];
+                p.t.data = ws + offsets[k] + v.slot_offset;
+                p.t.byte_capacity = (k + 1 < offsets.size() ? offsets[k + 1] : workspace) - offsets[k] - v.slot_offset;
                 p.t.dtype = prim_dtype(n.prec);
                 p.live = true;
                 p.seal();
@@ -399,6 +400,37 @@ int32_t run_plan(chelis_dag_program *prog, const chelis_gpu_tensor *const *input
             case RegionKind::Copy: {
                 const chelis_gpu_tensor *dst = outputs[r.axis];
                 s = chelis_hip_fused_elementwise(&identity_chain(), in.data(), 1, dst);
+                break;
+            }
+            case RegionKind::MatmulGroup: {
+                // the results lie back to back in one range: one [n, M, N] block
+                const int32_t nb = (int32_t)r.more_out.size() + 1;
+                const chelis_gpu_tensor *w[8], *b[8];
+                for (int32_t k = 0; k < nb; ++k) w[k] = in[1 + 2 * k], b[k] = in[2 + 2 * k];
+                const int64_t M = out->shape[0], N = out->shape[1];
+                const int64_t sh[3] = {nb, M, N}, stv[3] = {M * N, N, 1};
+                chelis_gpu_tensor c3 = *out;
+                c3.rank = 3, c3.shape = sh, c3.strides = stv, c3.count = nb * M * N;
+                c3.byte_capacity = nb * M * N * dtype_width(out->dtype);
+                s = linear_multi_b(in[0], w, b, nb, &c3);
+                break;
+            }
+            case RegionKind::LinregStep: {
+                const chelis_gpu_tensor *res[2] = {out, &pk[r.more_out[0]].t};
+                s = chelis_prog_linreg_step(in.data(), 3, res, 2);
+                break;
+            }
+            case RegionKind::MlpStep: {
+                // the program writes dense results (as a chain region does)
+                const std::vector<int64_t> outs = r.outputs();
+                const chelis_gpu_tensor *res[5];
+                for (size_t k = 0; k < outs.size(); ++k) {
+                    res[k] = &pk[outs[k]].t;
+                    if (!is_contiguous(res[k]) && !s)
+                        s = set_error(CHELIS_HIP_EUNSUPPORTED, "dag: the MLP step writes dense results; node %lld is "
+                                      "a strided view", (long long)outs[k]);
+                }
+                if (!s) s = mlp_train_step_run(in.data(), 7, res, 5, (float)r.rate, (float)r.lr);
                 break;
             }
         }

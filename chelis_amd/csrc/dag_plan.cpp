@@ -36,6 +36,10 @@
 namespace chelis {
 namespace dag {
 
+// the most products one batched launch takes (the problem's per-batch
+// weight and bias addresses, gemm.h kMaxBatchPtrs)
+constexpr int kMaxGroup = 4;
+
 const char *region_kind_name(RegionKind k) {
     switch (k) {
         case RegionKind::Chain: return "chain";
@@ -52,6 +56,9 @@ const char *region_kind_name(RegionKind k) {
         case RegionKind::Matmul: return "matmul";
         case RegionKind::Copy: return "copy";
         case RegionKind::Attention: return "attention";
+        case RegionKind::MatmulGroup: return "matmul_group";
+        case RegionKind::LinregStep: return "linreg_step";
+        case RegionKind::MlpStep: return "mlp_step";
     }
     return "?";
 }
@@ -168,11 +175,54 @@ struct Template {
         const int s = reduce(Op::Sum, e, axis);
         return bin(Op::Div, e, expand(s, axis, n));
     }
+    int permute(int x, std::vector<int64_t> axes) {
+        std::vector<int64_t> d;
+        for (int64_t a : axes) d.push_back(t[x].dims[a]);
+        TNode n;
+        n.op = Op::Permute;
+        n.in = {x};
+        n.dims = d;
+        n.prec = t[x].prec;
+        n.axes = std::move(axes);
+        return add(n);
+    }
+    int reshape(int x, std::vector<int64_t> shape) { return op(Op::Reshape, {x}, std::move(shape), t[x].prec); }
+    // a matmul in either form: BlasMatmul(a, b), or the lowered
+    // Sum{L+1}(Mul(Expand{L+2}(a), Expand{L}(b))) (tier2.rs:706-857)
+    int matmul(int a, int b) {
+        std::vector<int64_t> d = t[a].dims;
+        d.back() = t[b].dims.back();
+        return op(Op::BlasMatmul, {a, b}, d, t[a].prec);
+    }
+    int linear(int x, int w, int b) {
+        const int mm = matmul(x, w);
+        return bin(Op::Add, mm, expand_to(b, t[mm].dims));
+    }
 };
 
 struct Binding {
     std::vector<int64_t> map, ph;
+    std::vector<int64_t> lowered;  // the Mul / Expand nodes of matched lowered matmuls
 };
+
+// The lowered matmul at graph node d: its operands, and the nodes between.
+bool lowered_matmul(const Graph &g, int64_t d, int64_t *a, int64_t *b, int64_t inner[3]) {
+    const Node &n = g.nodes[d];
+    if (n.op != Op::Sum || n.inputs.size() != 1 || n.dims.size() < 2) return false;
+    const Node &mul = g.nodes[n.inputs[0]];
+    if (mul.op != Op::Mul || mul.inputs.size() != 2) return false;
+    const Node &ea = g.nodes[mul.inputs[0]], &eb = g.nodes[mul.inputs[1]];
+    const int64_t L = (int64_t)n.dims.size() - 2;
+    if (ea.op != Op::Expand || eb.op != Op::Expand || n.axis != L + 1 || ea.axis != L + 2 || eb.axis != L)
+        return false;
+    const Node &A = g.nodes[ea.inputs[0]], &B = g.nodes[eb.inputs[0]];
+    if (A.dims.size() != (size_t)L + 2 || B.dims.size() != (size_t)L + 2) return false;
+    if (A.dims[L + 1] != B.dims[L] || ea.size != B.dims[L + 1] || eb.size != A.dims[L]) return false;
+    *a = ea.inputs[0];
+    *b = eb.inputs[0];
+    inner[0] = n.inputs[0], inner[1] = mul.inputs[0], inner[2] = mul.inputs[1];
+    return true;
+}
 
 bool match_node(const Template &T, int ti, const Graph &g, int64_t d, Binding &b) {
     if (b.map[ti] >= 0) return b.map[ti] == d;
@@ -185,6 +235,13 @@ bool match_node(const Template &T, int ti, const Graph &g, int64_t d, Binding &b
         b.ph[t.placeholder] = d;
         b.map[ti] = d;
         return true;
+    }
+    if (t.op == Op::BlasMatmul && n.op == Op::Sum) {
+        int64_t a, bb, inner[3];
+        if (!lowered_matmul(g, d, &a, &bb, inner) || n.dims != t.dims || n.prec != t.prec) return false;
+        b.map[ti] = d;
+        b.lowered.insert(b.lowered.end(), inner, inner + 3);
+        return match_node(T, t.in[0], g, a, b) && match_node(T, t.in[1], g, bb, b);
     }
     if (n.op != t.op || n.payload_inputs() != t.in.size() || n.dims != t.dims || n.prec != t.prec) return false;
     switch (t.op) {
@@ -204,7 +261,20 @@ bool match_node(const Template &T, int ti, const Graph &g, int64_t d, Binding &b
 bool match(const Template &T, int root, const Graph &g, int64_t d, int n_ph, Binding *b) {
     b->map.assign(T.t.size(), -1);
     b->ph.assign((size_t)n_ph, -1);
+    b->lowered.clear();
     return match_node(T, root, g, d, *b);
+}
+
+// Several template roots onto several graph nodes under one binding.
+bool match_all(const Template &T, const std::vector<int> &roots, const Graph &g, const std::vector<int64_t> &nodes,
+               int n_ph, Binding *b) {
+    b->map.assign(T.t.size(), -1);
+    b->ph.assign((size_t)n_ph, -1);
+    b->lowered.clear();
+    if (roots.size() != nodes.size()) return false;
+    for (size_t k = 0; k < roots.size(); ++k)
+        if (!match_node(T, roots[k], g, nodes[k], *b)) return false;
+    return true;
 }
 
 // ---------------------------------------------------------------- planner state
@@ -249,16 +319,28 @@ struct Planner {
         return true;
     }
     static std::set<int64_t> image(const Binding &b, const Template &T) {
-        std::set<int64_t> s;
+        std::set<int64_t> s(b.lowered.begin(), b.lowered.end());
         for (size_t k = 0; k < T.t.size(); ++k)
             if (T.t[k].placeholder < 0 && b.map[k] >= 0) s.insert(b.map[k]);
         return s;
+    }
+    // closed() for a region with several results
+    bool closed_all(const std::set<int64_t> &cover, const std::vector<int64_t> &outs) const {
+        for (int64_t id : cover) {
+            if (claimed[id] >= 0 || barrier[id]) return false;
+            const bool result = std::find(outs.begin(), outs.end(), id) != outs.end();
+            if (result || free_leaf(id)) continue;
+            if (is_root[id]) return false;
+            for (int64_t u : users[id])
+                if (!cover.count(u)) return false;
+        }
+        return true;
     }
     int claim(Region r) {
         const int idx = (int)regions.size();
         for (int64_t id : r.covers)
             if (!free_leaf(id)) claimed[id] = idx;
-        claimed[r.out] = idx;
+        for (int64_t o : r.outputs()) claimed[o] = idx;
         regions.push_back(std::move(r));
         return idx;
     }
@@ -470,6 +552,112 @@ struct Planner {
         r.covers.assign(cover.begin(), cover.end());
         claim(r);
         return true;
+    }
+
+    // ------------------------------------------------------------ whole programs
+    // The linear-regression step as the compiler lowers it: r = X.w - y,
+    // grad = X^T.r / n, loss = mean(r * r) (tier2.rs:706-857 for the
+    // products, :1183-1245 for the mean), the roots [grad, loss]; run as
+    // this library's linreg step (two launches where d <= 32), the same bits
+    // as its unfused regions.
+    bool try_linreg(const std::vector<int64_t> &outs) {
+        if (outs.size() != 2) return false;
+        const Node &grad = N(outs[0]), &loss = N(outs[1]);
+        const Prim p = grad.prec;
+        if ((p != Prim::F32 && p != Prim::F64) || grad.dims.size() != 1 || !loss.dims.empty() || loss.prec != p)
+            return false;
+        const int64_t d = grad.dims[0];
+        for (const Node &ld : g.nodes) {
+            if (ld.op != Op::Load || ld.dims.size() != 2 || ld.dims[1] != d || ld.prec != p) continue;
+            const int64_t n = ld.dims[0];
+            if (n < 0 || d < 0) continue;
+            Template T;
+            const int X = T.ph(0, {n, d}, p), w = T.ph(1, {d}, p), y = T.ph(2, {n}, p);
+            const int r = T.bin(Op::Sub, T.reshape(T.matmul(X, T.reshape(w, {d, 1})), {n}), y);
+            const int gs = T.matmul(T.permute(X, {1, 0}), T.reshape(r, {n, 1}));
+            const int gt = T.bin(Op::Div, T.reshape(gs, {d}), T.cnst((double)n, {d}, p));
+            const int lt = T.mean(T.bin(Op::Mul, r, r), 0);
+            Binding b;
+            if (!match_all(T, {gt, lt}, g, outs, 3, &b)) continue;
+            std::set<int64_t> cover = image(b, T);
+            if (!closed_all(cover, outs)) continue;
+            Region rg;
+            rg.kind = RegionKind::LinregStep;
+            rg.out = outs[0];
+            rg.more_out = {outs[1]};
+            rg.in = {b.ph[0], b.ph[1], b.ph[2]};
+            rg.covers.assign(cover.begin(), cover.end());
+            claim(rg);
+            return true;
+        }
+        return false;
+    }
+
+    // The MLP training step as the compiler lowers it (mnist.ch form):
+    // forward relu(x.W1 + b1) -> dropout(key) -> softmax(. W2 + b2), loss
+    // the mean cross-entropy against one-hot labels, its reverse pass
+    // (mean, neg, sum, log and softmax adjoints, grad.rs:2248; transposed
+    // products; dropout replay; relu adjoint) and SGD, the roots [loss, w1',
+    // b1', w2', b2']; run as this library's MLP step (five launches where it
+    // fits), the same bits as its unfused regions.
+    bool try_mlp(const std::vector<int64_t> &outs) {
+        if (outs.size() != 5) return false;
+        const Node &w1n = N(outs[1]), &w2n = N(outs[3]);
+        const Prim p = Prim::F32;
+        if (w1n.prec != p || w1n.dims.size() != 2 || w2n.dims.size() != 2 || w2n.dims[0] != w1n.dims[1]) return false;
+        const int64_t I = w1n.dims[0], Hd = w1n.dims[1], O = w2n.dims[1];
+        for (const Node &ld : g.nodes) {
+            if (ld.op != Op::Load || ld.dims.size() != 2 || ld.dims[1] != I || ld.prec != p || ld.dims[0] < 0) continue;
+            const int64_t Bt = ld.dims[0];
+            if (I < 0 || Hd < 0 || O < 0) continue;
+            Template T;
+            const int x = T.ph(0, {Bt, I}, p), oh = T.ph(1, {Bt, O}, p), w1 = T.ph(2, {I, Hd}, p),
+                      b1 = T.ph(3, {Hd}, p), w2 = T.ph(4, {Hd, O}, p), b2 = T.ph(5, {O}, p),
+                      key = T.ph(6, {}, Prim::Key);
+            const int rate = T.any_const({}, p);
+            const int z1 = T.linear(x, w1, b1);
+            const int hd = T.un(Op::Relu, z1);
+            const int d = T.op(Op::Dropout, {hd, rate, key}, {Bt, Hd}, p);
+            const int pr = T.softmax(T.linear(d, w2, b2), 1);
+            const int nl = T.un(Op::Neg, T.reduce(Op::Sum, T.bin(Op::Mul, T.un(Op::Log, pr), oh), 1));
+            const int loss = T.mean(nl, 0);
+            const int gsum = T.bin(Op::Div, T.cnst(1.0, {}, p), T.cnst((double)Bt, {}, p));
+            const int gt = T.expand(T.un(Op::Neg, T.expand(gsum, 0, Bt)), 1, O);
+            const int gp = T.bin(Op::Div, T.bin(Op::Mul, gt, oh), pr);
+            const int gy = T.bin(Op::Mul, gp, pr);
+            const int gz2 = T.bin(Op::Mul, pr, T.bin(Op::Sub, gp, T.expand(T.reduce(Op::Sum, gy, 1), 1, O)));
+            const int gb2 = T.reduce(Op::Sum, gz2, 0);
+            const int gw2 = T.matmul(T.permute(d, {1, 0}), gz2);
+            const int gd = T.matmul(gz2, T.permute(w2, {1, 0}));
+            const int gh = T.op(Op::DropoutReplay, {gd, rate, key}, {Bt, Hd}, p);
+            const int gz1 = T.op(Op::ReluAdjoint, {z1, gh}, {Bt, Hd}, p);
+            const int gb1 = T.reduce(Op::Sum, gz1, 0);
+            const int gw1 = T.matmul(T.permute(x, {1, 0}), gz1);
+            const int lr = T.any_const({}, p);
+            auto sgd = [&](int w, int gw) {
+                return T.bin(Op::Sub, w, T.bin(Op::Mul, T.expand_to(lr, T.at(w).dims), gw));
+            };
+            const std::vector<int> roots = {loss, sgd(w1, gw1), sgd(b1, gb1), sgd(w2, gw2), sgd(b2, gb2)};
+            Binding b;
+            if (!match_all(T, roots, g, outs, 7, &b)) continue;
+            double rv, lv;
+            Prim rp, lp;
+            if (!const_of(b.map[rate], &rv, &rp) || !const_of(b.map[lr], &lv, &lp) || rp != p || lp != p) continue;
+            if (!(rv >= 0.0 && rv < 1.0)) continue;
+            std::set<int64_t> cover = image(b, T);
+            if (!closed_all(cover, outs)) continue;
+            Region rg;
+            rg.kind = RegionKind::MlpStep;
+            rg.out = outs[0];
+            rg.more_out.assign(outs.begin() + 1, outs.end());
+            rg.in.assign(b.ph.begin(), b.ph.end());
+            rg.rate = rv;
+            rg.lr = lv;
+            rg.covers.assign(cover.begin(), cover.end());
+            claim(rg);
+            return true;
+        }
+        return false;
     }
 
     // matmul: Sum{L+1}(Mul(Expand{L+2, k}(a), Expand{L, i}(b))) or BlasMatmul
@@ -773,7 +961,8 @@ struct Planner {
         return true;
     }
 
-    bool form() {
+    bool form(const std::vector<int64_t> &outputs) {
+        if (!try_linreg(outputs)) try_mlp(outputs);
         for (const Node &n : g.nodes) {
             if (claimed[n.id] >= 0) continue;
             if (try_matmul(n.id)) continue;
@@ -791,9 +980,11 @@ struct Planner {
         std::vector<Region> sorted;
         for (int k : order) sorted.push_back(regions[k]);
         regions.swap(sorted);
-        for (size_t k = 0; k < regions.size(); ++k)
+        for (size_t k = 0; k < regions.size(); ++k) {
             for (int64_t id : regions[k].covers)
                 if (!free_leaf(id)) claimed[id] = (int)k;
+            for (int64_t o : regions[k].outputs()) claimed[o] = (int)k;
+        }
         return true;
     }
 };
@@ -865,7 +1056,7 @@ bool build_plan(const Graph &input, Plan *plan, std::string *error) {
     }
     output_specs(g, &plan->output_nodes, &plan->output_labels);
     Planner P(g, plan->output_nodes);
-    if (!P.form()) {
+    if (!P.form(plan->output_nodes)) {
         *error = P.error;
         return false;
     }
@@ -925,11 +1116,64 @@ bool build_plan(const Graph &input, Plan *plan, std::string *error) {
         P.regions.swap(next);
         i = (size_t)-1;  // rescan from the start: indices moved
     }
+    // products sharing their left operand, each with a bias and nothing
+    // else after it, of one shape, whose weights and biases are available
+    // where the first of them runs: one batched launch writing the results
+    // back to back (the transformer's Q, K and V projections)
+    {
+        std::vector<bool> produced_before(g.nodes.size(), false);
+        std::vector<Region> next;
+        std::vector<bool> taken(P.regions.size(), false);
+        auto plain = [&](const Region &r) {
+            return r.kind == RegionKind::Matmul && r.has_bias && !r.has_residual && r.activation == CHELIS_ACT_NONE &&
+                   !r.causal_mode && r.in.size() == 3 && !P.is_root[r.out] && g.nodes[r.out].count() > 0 &&
+                   g.nodes[r.out].dims.size() == 2 && g.nodes[r.in[1]].dims.size() == 2;
+        };
+        for (size_t i = 0; i < P.regions.size(); ++i) {
+            if (taken[i]) continue;
+            const Region &r = P.regions[i];
+            std::vector<size_t> members{i};
+            if (plain(r)) {
+                for (size_t j = i + 1; j < P.regions.size() && members.size() < (size_t)kMaxGroup; ++j) {
+                    const Region &q = P.regions[j];
+                    if (taken[j] || !plain(q) || q.in[0] != r.in[0] || g.nodes[q.out].dims != g.nodes[r.out].dims ||
+                        g.nodes[q.out].prec != g.nodes[r.out].prec || g.nodes[q.in[1]].dims != g.nodes[r.in[1]].dims ||
+                        g.nodes[q.in[2]].dims != g.nodes[r.in[2]].dims)
+                        continue;
+                    // its weight and bias exist before the group runs
+                    bool ready = true;
+                    for (size_t k = i; k < j && ready; ++k)
+                        for (int64_t o : P.regions[k].outputs())
+                            ready = ready && o != q.in[1] && o != q.in[2];
+                    if (ready) members.push_back(j);
+                }
+            }
+            if (members.size() < 2) {
+                next.push_back(r);
+                continue;
+            }
+            Region grp;
+            grp.kind = RegionKind::MatmulGroup;
+            grp.out = r.out;
+            grp.in = {r.in[0]};
+            for (size_t m : members) {
+                taken[m] = true;
+                const Region &q = P.regions[m];
+                if (m != i) grp.more_out.push_back(q.out);
+                grp.in.push_back(q.in[1]);
+                grp.in.push_back(q.in[2]);
+                grp.covers.insert(grp.covers.end(), q.covers.begin(), q.covers.end());
+            }
+            next.push_back(grp);
+        }
+        P.regions.swap(next);
+    }
     plan->regions = P.regions;
     const size_t n = g.nodes.size();
     plan->values.assign(n, ValueInfo{});
     std::vector<bool> produced(n, false);
-    for (const Region &r : plan->regions) produced[r.out] = true;
+    for (const Region &r : plan->regions)
+        for (int64_t o : r.outputs()) produced[o] = true;
     // caller inputs: one slot per Load name (a repeated Load aliases it,
     // emit.rs:5881-5892), in first-appearance order
     std::map<std::string, int64_t> input_slot;
@@ -1019,6 +1263,10 @@ bool build_plan(const Graph &input, Plan *plan, std::string *error) {
     // outputs: a region result is written straight into the caller's
     // output (through a reshape or store view when the output is one);
     // anything else is copied there by a last launch
+    std::vector<bool> grouped(n, false);
+    for (const Region &r : plan->regions)
+        if (r.kind == RegionKind::MatmulGroup)
+            for (int64_t o : r.outputs()) grouped[o] = true;
     for (size_t o = 0; o < plan->output_nodes.size(); ++o) {
         const int64_t root = plan->output_nodes[o];
         int64_t v = root;
@@ -1027,7 +1275,7 @@ bool build_plan(const Graph &input, Plan *plan, std::string *error) {
                P.users[plan->values[v].base].size() == 1 && !P.is_root[plan->values[v].base])
             v = plan->values[v].base;
         ValueInfo &vi = plan->values[v];
-        if (vi.storage == Storage::Slot && vi.output < 0 && (v == root || P.users[v].size() == 1)) {
+        if (vi.storage == Storage::Slot && vi.output < 0 && !grouped[v] && (v == root || P.users[v].size() == 1)) {
             vi.storage = Storage::Output;
             vi.output = (int64_t)o;
             vi.base = root;  // the packet is the output's, viewed with this node's shape
@@ -1073,14 +1321,28 @@ bool build_plan(const Graph &input, Plan *plan, std::string *error) {
     std::vector<std::vector<int64_t>> release_at(plan->regions.size());
     for (size_t k = 0; k < plan->regions.size(); ++k) {
         const Region &r = plan->regions[k];
-        if (r.kind != RegionKind::Copy && plan->values[r.out].storage == Storage::Slot) {
-            ValueInfo &vi = plan->values[r.out];
-            const Node &nd = g.nodes[r.out];
+        // a matmul group's results share one range, back to back
+        const bool group = r.kind == RegionKind::MatmulGroup;
+        const std::vector<int64_t> results = r.kind == RegionKind::Copy ? std::vector<int64_t>{} : r.outputs();
+        for (size_t ri = 0; ri < results.size() && (!group || ri == 0); ++ri) {
+            const int64_t out = results[ri];
+            if (plan->values[out].storage != Storage::Slot) continue;
+            ValueInfo &vi = plan->values[out];
+            const Node &nd = g.nodes[out];
             const int64_t width = r.kind == RegionKind::Reduce && (r.reduce_op == CHELIS_REDUCE_ARGMAX ||
                                                                    r.reduce_op == CHELIS_REDUCE_ARGMIN)
                                       ? 8
                                       : (r.kind == RegionKind::Count ? 8 : prim_width(nd.prec));
-            const Size z = value_size(nd, width);
+            Size z = value_size(nd, width);
+            int64_t end = std::max(last[out], (int64_t)k);
+            if (group) {
+                for (size_t m = 0; m < results.size(); ++m) {
+                    ValueInfo &mv = plan->values[results[m]];
+                    mv.slot_offset = (int64_t)m * z.coef;  // literal extents (a group requires them)
+                    end = std::max(end, last[results[m]]);
+                }
+                z.coef *= (int64_t)results.size();
+            }
             int64_t best = -1;
             if (z.symbols.empty()) {
                 const int64_t need = (z.coef + 255) & ~int64_t(255);
@@ -1113,7 +1375,9 @@ bool build_plan(const Graph &input, Plan *plan, std::string *error) {
             }
             busy[best] = true;
             vi.slot = best;
-            release_at[std::max(last[r.out], (int64_t)k)].push_back(best);
+            if (group)
+                for (int64_t o : results) plan->values[o].slot = best;
+            release_at[end].push_back(best);
         }
         for (int64_t s : release_at[k]) busy[s] = false;
     }
@@ -1211,7 +1475,13 @@ std::string describe_plan(const Plan &plan) {
     std::string s;
     for (size_t k = 0; k < plan.regions.size(); ++k) {
         const Region &r = plan.regions[k];
-        s += std::to_string(k) + " " + region_kind_name(r.kind) + " out=" + std::to_string(r.out) + " in=[";
+        s += std::to_string(k) + " " + region_kind_name(r.kind) + " out=" + std::to_string(r.out);
+        if (!r.more_out.empty()) {
+            s += "+[";
+            for (size_t i = 0; i < r.more_out.size(); ++i) s += (i ? "," : "") + std::to_string(r.more_out[i]);
+            s += "]";
+        }
+        s += " in=[";
         for (size_t i = 0; i < r.in.size(); ++i) s += (i ? "," : "") + std::to_string(r.in[i]);
         s += "]";
         if (r.kind == RegionKind::Chain || (r.kind == RegionKind::Reduce && r.has_chain))

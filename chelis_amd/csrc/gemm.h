@@ -129,6 +129,11 @@ bool mlp_narrow_fits(int64_t B, int64_t I, int64_t H, int64_t O);
 size_t mlp_part_bytes(int64_t B, int64_t H);
 int32_t mlp_head_tail(const MlpNarrow &m, hipStream_t st);
 int32_t mlp_finish(const MlpNarrow &m, hipStream_t st);
+// The MLP training step (chelis_prog_mlp_train_step) at a given dropout
+// rate and learning rate: five launches where mlp_narrow_fits, else the
+// launch-per-region form; the same bits either way.
+int32_t mlp_train_step_run(const chelis_gpu_tensor *const *in, int32_t n_in, const chelis_gpu_tensor *const *out,
+                           int32_t n_out, float rate, float lr);
 // c = a . b for attention with the causal mode above (programs only).
 int32_t matmul_causal(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b, const chelis_gpu_tensor *c,
                       int32_t mode);

@@ -301,6 +301,12 @@ int32_t mlp_fused(const chelis_gpu_tensor *x, const chelis_gpu_tensor *oh, const
 
 extern "C" int32_t chelis_prog_mlp_train_step(const chelis_gpu_tensor *const *in, int32_t n_in,
                                               const chelis_gpu_tensor *const *out, int32_t n_out) {
+    // the configuration's dropout rate and learning rate (mnist.ch form)
+    return chelis::mlp_train_step_run(in, n_in, out, n_out, 0.1f, 0.01f);
+}
+
+int32_t chelis::mlp_train_step_run(const chelis_gpu_tensor *const *in, int32_t n_in,
+                                   const chelis_gpu_tensor *const *out, int32_t n_out, float rate, float lr) {
     if (n_in != 7 || n_out != 5) return set_error(CHELIS_HIP_EDOMAIN, "mlp_train_step: 7 inputs, 5 outputs");
     TRY(check_all(in, 7, "mlp_train_step input"));
     TRY(check_all(out, 5, "mlp_train_step output"));
@@ -316,9 +322,9 @@ extern "C" int32_t chelis_prog_mlp_train_step(const chelis_gpu_tensor *const *in
     if (!ok) return set_error(CHELIS_HIP_EDOMAIN, "mlp_train_step: shapes/dtypes do not match the program");
     for (int32_t i = 1; i < 5; ++i)
         if (!is_contiguous(out[i])) return set_error(CHELIS_HIP_EUNSUPPORTED, "mlp_train_step: outputs must be contiguous");
+    if (!(rate >= 0.0f && rate < 1.0f)) return set_error(CHELIS_HIP_EDOMAIN, "mlp_train_step: rate outside [0, 1)");
     hipStream_t st = stream();
     if (!st) return set_error(CHELIS_HIP_EHIP, "no HIP device");
-    const float rate = 0.1f, lr = 0.01f;
     // the dropout kernels read the key from its tensor on the device
     const uint64_t *kdev = static_cast<const uint64_t *>(key->data);
     if (mlp_narrow_fits(Bt, I, Hd, O) && is_contiguous(oh) && is_contiguous(w1) && is_contiguous(w2) &&

@@ -123,29 +123,43 @@ def kinds(p):
     return [line.split()[1] for line in p.describe().strip().splitlines()]
 
 
+def with_roots_reversed(name):
+    """The fixture with its roots in reverse order: the same values, but not
+    the lowered program the whole-program regions recognize."""
+    d = json.load(open(os.path.join(DAGS, name + ".json")))
+    d["roots"] = d["roots"][::-1]
+    return json.dumps(d, separators=(",", ":"))
+
+
 def test_plans_of_the_configuration_programs():
     assert kinds(plan("softmax_f32_16384x1024")) == ["softmax"]
     assert kinds(plan("gemm_f32_4096")) == ["matmul"]
-    assert kinds(plan("linreg_step_8192x32")) == ["matmul", "chain", "matmul", "chain", "reduce", "chain"]
+    # the whole linear-regression step: the fused program (two launches)
+    assert kinds(plan("linreg_step_8192x32")) == ["linreg_step"]
+    assert kinds(plan(with_roots_reversed("linreg_step_8192x32"))) == ["matmul", "chain", "matmul", "chain", "reduce",
+                                                                        "chain"]
     t = plan("transformer_block_b8_s512_d1024")
-    # the scores product, causal softmax and P.V fold into one attention region
-    assert kinds(t) == ["layer_norm", "matmul", "matmul", "matmul", "attention", "matmul", "layer_norm", "matmul",
-                        "matmul"]
+    # Q, K and V as one batched product; the scores product, causal softmax
+    # and P.V fold into one attention region
+    assert kinds(t) == ["layer_norm", "matmul_group", "attention", "matmul", "layer_norm", "matmul", "matmul"]
     desc = t.describe().splitlines()
-    assert "causal" in desc[4] and "permuted" in desc[4]
-    assert "bias gelu" in desc[7] and "bias residual" in desc[8] and "-> output 0" in desc[8]
-    # the slot plan reuses ranges: four slots, three of [4096, 1024] f32 and
-    # one holding the [4096, 4096] FFN hidden layer; no score tensor
+    assert "causal" in desc[2] and "permuted" in desc[2]
+    assert "bias gelu" in desc[5] and "bias residual" in desc[6] and "-> output 0" in desc[6]
+    # the slot plan reuses ranges: [4096, 1024] f32 for the layer norms and
+    # attention, the Q/K/V block (three of them back to back) then the
+    # output projection, and the [4096, 4096] FFN hidden layer; no scores
     n_const = sum(1 for n in json.load(open(os.path.join(DAGS, "transformer_block_b8_s512_d1024.json")))["nodes"]
                   if isinstance(n["op"], dict) and "Const" in n["op"])
-    assert t.peak_device_bytes == 3 * 8 * 512 * 1024 * 4 + 8 * 512 * 4096 * 4 + 8 * n_const
-    m = plan("mlp_train_step_1024x784x512x10")
+    assert t.peak_device_bytes == 4 * 8 * 512 * 1024 * 4 + 8 * 512 * 4096 * 4 + 8 * n_const
+    assert kinds(plan("mlp_train_step_1024x784x512x10")) == ["mlp_step"]
+    m = plan(with_roots_reversed("mlp_train_step_1024x784x512x10"))
     k = kinds(m)
     assert k.count("matmul") == 5 and k.count("softmax") == 1 and k.count("softmax_adjoint") == 1
     assert k.count("dropout") == 2 and k.count("relu") == 1 and k.count("relu_adjoint") == 1
     # output labels are the reference's output specs: "root<index>"
     # (crates/chelis-backend-hip/src/emit.rs:5923-5930)
     assert [o[0] for o in m.outputs] == ["root0", "root1", "root2", "root3", "root4"]
+    assert [o[1] for o in m.outputs] == [(10,), (512, 10), (512,), (784, 512), ()]
     assert [i[0] for i in m.inputs] == ["x", "onehot", "w1", "b1", "w2", "b2", "key"]
 
 
