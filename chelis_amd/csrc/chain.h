@@ -5,6 +5,7 @@
 // selection ([05-OP-40], [05-OP-43]).
 #pragma once
 
+#include "gelu_poly.h"
 #include "hip_common.h"
 
 namespace chelis {
@@ -159,6 +160,42 @@ __device__ inline T gelu_one_t(T x, const Tabs &tb) {
 template <typename T>
 __device__ inline T gelu_one(T x) {
     return gelu_one_t<T>(x, ErfcTablesConst{});
+}
+
+// binary32 GELU for the default (not exact) mode: x Phi(x) directly, not
+// the Phi graph primitive by primitive. Phi = 1 - E for x >= 0 and E for
+// x < 0, E = erfc(|x| / sqrt 2) / 2 = q(|x|) exp(-x^2 / 2):
+//   q = erfcx(|x| / sqrt 2) / 2, one degree-9 polynomial in
+//       u = (|x| - K) / (|x| + K) (gelu_poly.h);
+//   exp(-x^2 / 2) = 2^a, a = -x^2 log2(e) / 2 in binary64 (x^2 is exact
+//       there, so the exponential's relative error does not grow with
+//       x^2), split into floor(a) and a fraction in [0, 1) for one
+//       v_exp_f32 and an exponent scaling;
+//   x Phi(x) = fma(-|x| q, e, x) for x >= 0, fma(-|x| q, e, 0) for x < 0.
+// About 30 instructions against about 110 for the graph (binary64 runs at
+// the binary32 rate here, as packed binary32 is not used); within 7e-7
+// relative of the graph on every binary32 input (the north star's binary32
+// bar is 1e-5). `slow` marks what it does not serve - x < -12.5, where E
+// and the result leave the normal range, +inf and NaN - for the graph.
+__device__ inline float gelu_fast_f32(float x, bool &slow) {
+    constexpr float kQ[CHELIS_GELU_DEG + 1] = CHELIS_GELU_Q;
+    constexpr float kK = CHELIS_GELU_K;
+    constexpr double kHalfLog2e = -0.72134752044448170368;  // -log2(e) / 2
+    // x + 12.5 is +0, +subnormal or +normal exactly when -12.5 <= x < +inf
+    slow = !__builtin_amdgcn_classf(x + 12.5f, (1 << 6) | (1 << 7) | (1 << 8));
+    const float ax = fabsf(x);
+    // u = (|x| - K) / (|x| + K) = 1 - 2K / (|x| + K)
+    const float u = fmaf(-2.0f * kK, __builtin_amdgcn_rcpf(ax + kK), 1.0f);
+    float q = kQ[CHELIS_GELU_DEG];
+#pragma unroll
+    for (int d = CHELIS_GELU_DEG - 1; d >= 0; --d) q = fmaf(q, u, kQ[d]);
+    const double xd = (double)x;
+    // beyond -1000, 2^a is 0 against 1 (and floor(a) stays an int)
+    const double a = fmax((xd * kHalfLog2e) * xd, -1000.0);
+    const double fl = floor(a);
+    const float e = __builtin_ldexpf(__builtin_amdgcn_exp2f((float)(a - fl)), (int)fl);
+    // x Phi(x) = x - |x| q e for x >= 0, -|x| q e for x < 0
+    return fmaf(-(ax * q), e, x >= 0.0f ? x : 0.0f);
 }
 
 // A workgroup's copy of the binary32 erfc and exp tables in LDS; every

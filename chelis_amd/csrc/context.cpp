@@ -218,9 +218,19 @@ bool row_view(const chelis_gpu_tensor *t, RowView *v) {
 
 namespace {
 std::atomic<int32_t> g_exact_mode{0};
+thread_local int32_t t_pinned = -1;  // the mode a scope pinned for this thread, -1 none
 }  // namespace
 
-bool exact_mode() { return g_exact_mode.load(std::memory_order_relaxed) != 0; }
+bool exact_mode() {
+    return t_pinned >= 0 ? t_pinned != 0 : g_exact_mode.load(std::memory_order_relaxed) != 0;
+}
+
+ModeScope::ModeScope(int32_t mode) : prev_(t_pinned) {
+    if (mode >= 0) t_pinned = mode != 0;
+    else if (t_pinned < 0) t_pinned = g_exact_mode.load(std::memory_order_relaxed) != 0;
+}
+
+ModeScope::~ModeScope() { t_pinned = prev_; }
 
 }  // namespace chelis
 

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -21,6 +22,7 @@ struct chelis_dag_program {
     chelis::dag::Plan plan;
     std::string description;
     std::mutex mutex;
+    std::atomic<int32_t> mode{-1};  // chelis_dag_set_exact: -1 the library-wide mode at each run
     void *constants[64] = {};  // the constant pool on each device, uploaded on first use
     ~chelis_dag_program() {
         int here = -1;
@@ -482,10 +484,17 @@ extern "C" int32_t chelis_dag_run(chelis_dag_program *program, const chelis_gpu_
                                   const chelis_gpu_tensor *const *outputs, int32_t n_out) {
     if (!program) return set_error(CHELIS_HIP_EDOMAIN, "dag: null program");
     try {
+        // one numeric mode for every launch of this run
+        const ModeScope mode(program->mode.load(std::memory_order_relaxed));
         return run_plan(program, inputs, n_in, outputs, n_out);
     } catch (const std::exception &e) {
         return set_error(CHELIS_HIP_EHIP, "dag: %s", e.what());
     }
+}
+
+extern "C" int32_t chelis_dag_set_exact(chelis_dag_program *program, int32_t mode) {
+    if (!program) return set_error(CHELIS_HIP_EDOMAIN, "dag: null program"), -2;
+    return program->mode.exchange(mode < 0 ? -1 : (mode ? 1 : 0));
 }
 
 extern "C" int32_t chelis_dag_input_count(const chelis_dag_program *p) {

@@ -38,6 +38,9 @@ struct GemmProblem {
     int32_t nbz;
     const void *bz[kMaxBatchPtrs];
     const void *biasz[kMaxBatchPtrs];
+    // binary32 GELU epilogue in the default mode: gelu_fast_f32 (the Phi
+    // graph for the inputs it does not serve) instead of the graph
+    int32_t gelu_fast;
 };
 
 // Epilogue of one output element, each step finalized at the dtype so the
@@ -52,8 +55,15 @@ __device__ inline T epilogue_values(T acc, const GemmProblem &p, bool has_bias, 
                                     const Tabs &tb = Tabs{}) {
     T v = canon(acc);
     if (has_bias) v = canon(v + b);
-    if (p.act == CHELIS_ACT_RELU) v = v < T(0) ? T(0) : v;
-    else if (GELU && p.act == CHELIS_ACT_GELU) v = gelu_one_t<T>(v, tb);
+    if (p.act == CHELIS_ACT_RELU) {
+        v = v < T(0) ? T(0) : v;
+    } else if (GELU && p.act == CHELIS_ACT_GELU) {
+        bool slow = true;
+        T g = v;
+        if constexpr (sizeof(T) == 4)
+            if (p.gelu_fast) g = gelu_fast_f32(v, slow);
+        v = slow ? gelu_one_t<T>(v, tb) : g;
+    }
     if (p.resid) v = canon(r + v);
     return v;
 }

@@ -24,6 +24,21 @@ hipStream_t stream();
 // C lane's; when clear, the default MFMA products and faithful binary64
 // softmax rows, within the stated tolerances.
 bool exact_mode();
+// Pins the numeric mode for the calling thread's enqueues while it lives,
+// so one entry (a program, a DAG run, a matmul dispatch) reads one mode
+// throughout even if another thread switches the library-wide mode
+// meanwhile. mode 0 / 1: that mode; -1: the mode an enclosing scope
+// pinned, else the library-wide mode read once now.
+class ModeScope {
+  public:
+    explicit ModeScope(int32_t mode = -1);
+    ~ModeScope();
+    ModeScope(const ModeScope &) = delete;
+    ModeScope &operator=(const ModeScope &) = delete;
+
+  private:
+    int32_t prev_;
+};
 // Compute units of the current device (cached per device; 256 on MI355X).
 int device_cus();
 // The current device's two status words (device memory; *host, when given,

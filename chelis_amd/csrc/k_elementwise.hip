@@ -260,7 +260,9 @@ struct Vec16;
 template <> struct Vec16<float> { using type = float4; static constexpr int V = 4; };
 template <> struct Vec16<double> { using type = double2; static constexpr int V = 2; };
 
-enum class Unary : int { Gelu, Relu, ReluAdjoint, Dropout, Uniform };
+// GeluFast: binary32 GELU in the default mode (gelu_fast_f32, the graph
+// for the inputs it does not serve); binary64 GELU is the graph in both.
+enum class Unary : int { Gelu, Relu, ReluAdjoint, Dropout, Uniform, GeluFast };
 
 struct UnaryArgs {
     uint64_t key;
@@ -273,6 +275,15 @@ template <typename T, Unary OP, class Tabs = ErfcTablesConst>
 __device__ inline T unary_one(T x, T g, int64_t i, const UnaryArgs &u, const Tabs &tb = Tabs{}) {
     if constexpr (OP == Unary::Gelu) {
         return gelu_one_t<T>(x, tb);
+    } else if constexpr (OP == Unary::GeluFast) {
+        if constexpr (sizeof(T) == 4) {
+            bool slow;
+            T r = gelu_fast_f32(x, slow);
+            if (slow) r = gelu_one_t<T>(x, ErfcTablesConst{});
+            return r;
+        } else {
+            return gelu_one_t<T>(x, tb);
+        }
     } else if constexpr (OP == Unary::Relu) {
         return x < T(0) ? T(0) : x;
     } else if constexpr (OP == Unary::ReluAdjoint) {
@@ -333,6 +344,95 @@ __global__ __launch_bounds__(256) void unary_kernel(const T *__restrict__ x, con
         run(ErfcTablesConst{});
     }
 }
+
+// The VALU-heavy maps (GELU in both modes, keyed dropout, uniform_like): a
+// resident grid whose threads walk the vectors with a stride, the next
+// vector's load issued before the current one is evaluated, so each wave's
+// memory traffic overlaps its own arithmetic (with one vector per thread
+// the waves of a SIMD loaded together, waited together and computed
+// together, leaving the VALU or the memory idle in turn). Loads and stores
+// are nontemporal: every element is read once and written once.
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef double f64x2_t __attribute__((ext_vector_type(2)));
+template <typename T> struct NtVec;
+template <> struct NtVec<float> { using type = f32x4_t; };
+template <> struct NtVec<double> { using type = f64x2_t; };
+
+// vectors per buffer: each thread evaluates one buffer of kStreamBatch
+// vectors while the other buffer's loads are in flight (a ping-pong, so no
+// register moves); fewer for the register-heavy exact GELU
+template <Unary OP> constexpr int kStreamBatch = OP == Unary::Gelu ? 1 : 3;
+
+template <typename T, Unary OP>
+__global__ __launch_bounds__(256) void unary_stream_kernel(const T *__restrict__ x, T *__restrict__ y, int64_t n,
+                                                           UnaryArgs u) {
+    if constexpr (OP == Unary::Dropout || OP == Unary::Uniform)
+        if (u.key_dev) u.key = *u.key_dev;
+    if constexpr (OP == Unary::Dropout) u.inv_keep = 1.0 / (double)(T(1) - (T)u.p0);
+    constexpr bool reads = OP != Unary::Uniform;
+    auto run = [&](const auto &tb) {
+        using NV = typename NtVec<T>::type;
+        constexpr int V = Vec16<T>::V;
+        const int64_t nv = n / V;
+        const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+        const NV *xv = reinterpret_cast<const NV *>(x);
+        NV *yv = reinterpret_cast<NV *>(y);
+        constexpr int B = kStreamBatch<OP>;
+        const int64_t v0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+        auto load = [&](NV (&buf)[B], int64_t base) {
+#pragma unroll
+            for (int j = 0; j < B; ++j)
+                if (reads && base + j * stride < nv) buf[j] = __builtin_nontemporal_load(xv + base + j * stride);
+        };
+        auto eval_store = [&](const NV (&buf)[B], int64_t base) {
+#pragma unroll
+            for (int j = 0; j < B; ++j) {
+                const int64_t v = base + j * stride;
+                if (v >= nv) break;
+                const NV cur = buf[j];
+                NV out;
+                if constexpr (OP == Unary::GeluFast && sizeof(T) == 4) {
+                    // the vector's evaluations side by side, then one branch to
+                    // the graph for the inputs the direct evaluation does not serve
+                    bool sl[V], any = false;
+#pragma unroll
+                    for (int i = 0; i < V; ++i) {
+                        out[i] = gelu_fast_f32(cur[i], sl[i]);
+                        any = any || sl[i];
+                    }
+                    if (any)
+#pragma unroll
+                        for (int i = 0; i < V; ++i)
+                            if (sl[i]) out[i] = gelu_one_t<T>(cur[i], ErfcTablesConst{});
+                } else {
+#pragma unroll
+                    for (int i = 0; i < V; ++i) out[i] = unary_one<T, OP>(cur[i], T(0), v * V + i, u, tb);
+                }
+                __builtin_nontemporal_store(out, yv + v);
+            }
+        };
+        NV ba[B] = {}, bb[B] = {};
+        load(ba, v0);
+        for (int64_t base = v0; base < nv; base += 2 * B * stride) {
+            load(bb, base + B * stride);
+            eval_store(ba, base);
+            load(ba, base + 2 * B * stride);
+            eval_store(bb, base + B * stride);
+        }
+        // tail: the last n % V elements
+        const int64_t t = nv * V + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+        if (t < n) y[t] = unary_one<T, OP == Unary::GeluFast ? Unary::Gelu : OP>(reads ? x[t] : T(0), T(0), t, u, tb);
+    };
+    if constexpr (OP == Unary::Gelu && sizeof(T) == 4) {
+        __shared__ ErfcLdsStore gtab;
+        gtab.fill();
+        __syncthreads();
+        run(gtab.tabs());
+    } else {
+        run(ErfcTablesConst{});
+    }
+}
+
 
 // ---------------------------------------------------------------- host helpers
 // Collapse adjacent output axes wherever every operand's strides allow it
@@ -397,13 +497,31 @@ int32_t launch_unary(const chelis_gpu_tensor *x, const chelis_gpu_tensor *g, con
     // one 16-byte vector per thread up to 2^16 blocks (16 Mi vectors):
     // enough waves that one's loads overlap another's arithmetic (the RNG
     // maps are VALU-heavy), grid-stride beyond
-    int64_t blocks = (nv + 255) / 256;
-    if (blocks > 65536) blocks = 65536;
-    if (blocks < 1) blocks = 1;
-    unary_kernel<T, OP><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(
-        x ? (const T *)x->data : nullptr, g ? (const T *)g->data : nullptr, (T *)y->data, n, u);
-    CHELIS_LAUNCH_CHECK();
-    return CHELIS_HIP_OK;
+    if constexpr (OP != Unary::Relu && OP != Unary::ReluAdjoint) {
+        // exactly the workgroups that are resident at once (a second round
+        // of a few would leave most of the chip idle at the end)
+        static const int per_cu = [] {
+            int b = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, unary_stream_kernel<T, OP>, 256, 0) != hipSuccess ||
+                b < 1)
+                b = 1;
+            return b;
+        }();
+        int64_t blocks = std::min<int64_t>((nv + 255) / 256, (int64_t)device_cus() * per_cu);
+        if (blocks < 1) blocks = 1;
+        unary_stream_kernel<T, OP><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(
+            x ? (const T *)x->data : nullptr, (T *)y->data, n, u);
+        CHELIS_LAUNCH_CHECK();
+        return CHELIS_HIP_OK;
+    } else {
+        int64_t blocks = (nv + 255) / 256;
+        if (blocks > 65536) blocks = 65536;
+        if (blocks < 1) blocks = 1;
+        unary_kernel<T, OP><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(
+            x ? (const T *)x->data : nullptr, g ? (const T *)g->data : nullptr, (T *)y->data, n, u);
+        CHELIS_LAUNCH_CHECK();
+        return CHELIS_HIP_OK;
+    }
 }
 
 bool vec_aligned(const chelis_gpu_tensor *t) { return (reinterpret_cast<uintptr_t>(t->data) & 15u) == 0; }
@@ -662,7 +780,11 @@ extern "C" int32_t chelis_hip_fused_elementwise(const chelis_fused_chain *chain,
 }
 
 extern "C" int32_t chelis_hip_gelu(const chelis_gpu_tensor *x, const chelis_gpu_tensor *y) {
-    return unary_entry<Unary::Gelu>("gelu", x, nullptr, y, UnaryArgs{});
+    // the exact mode: the Phi graph bit for bit; else the direct binary32
+    // evaluation (binary64 is the graph either way)
+    if (exact_mode() || (y && y->dtype != CHELIS_DTYPE_F32))
+        return unary_entry<Unary::Gelu>("gelu", x, nullptr, y, UnaryArgs{});
+    return unary_entry<Unary::GeluFast>("gelu", x, nullptr, y, UnaryArgs{});
 }
 
 extern "C" int32_t chelis_hip_relu(const chelis_gpu_tensor *x, const chelis_gpu_tensor *y) {

@@ -115,6 +115,7 @@ int32_t build_problem(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b, co
     p->sam = ma.srow, p->sak = ma.scol, p->sbk = mb.srow, p->sbn = mb.scol, p->scm = scm, p->scn = scn;
     p->nb0 = bext[0], p->nb1 = bext[1];
     p->sa0 = sa[0], p->sa1 = sa[1], p->sb0 = sb[0], p->sb1 = sb[1], p->sc0 = sc[0], p->sc1 = sc[1];
+    p->gelu_fast = exact_mode() ? 0 : 1;
     return CHELIS_HIP_OK;
 }
 
@@ -294,6 +295,7 @@ using namespace chelis;
 
 extern "C" int32_t chelis_hip_matmul(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b,
                                      const chelis_gpu_tensor *c, int32_t flags) {
+    const ModeScope mode;
     GemmProblem p;
     if (int32_t s = build_problem(a, b, c, &p, "matmul")) return s;
     if (flags & ~CHELIS_MATMUL_EXACT) return set_error(CHELIS_HIP_EDOMAIN, "matmul: unknown flags %d", flags);
@@ -303,6 +305,7 @@ extern "C" int32_t chelis_hip_matmul(const chelis_gpu_tensor *a, const chelis_gp
 extern "C" int32_t chelis_hip_linear(const chelis_gpu_tensor *a, const chelis_gpu_tensor *b,
                                      const chelis_gpu_tensor *bias, int32_t activation,
                                      const chelis_gpu_tensor *residual, const chelis_gpu_tensor *c, int32_t flags) {
+    const ModeScope mode;
     GemmProblem p;
     if (int32_t s = build_problem(a, b, c, &p, "linear")) return s;
     if (flags & ~CHELIS_MATMUL_EXACT) return set_error(CHELIS_HIP_EDOMAIN, "linear: unknown flags %d", flags);

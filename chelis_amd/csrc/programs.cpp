@@ -141,6 +141,7 @@ using namespace chelis;
 // ------------------------------------------------------------------ linreg
 extern "C" int32_t chelis_prog_linreg_step(const chelis_gpu_tensor *const *in, int32_t n_in,
                                            const chelis_gpu_tensor *const *out, int32_t n_out) {
+    const ModeScope mode;
     if (n_in != 3 || n_out != 2) return set_error(CHELIS_HIP_EDOMAIN, "linreg_step: 3 inputs, 2 outputs");
     TRY(check_all(in, 3, "linreg_step input"));
     TRY(check_all(out, 2, "linreg_step output"));
@@ -180,6 +181,7 @@ extern "C" int32_t chelis_prog_linreg_step(const chelis_gpu_tensor *const *in, i
 // ------------------------------------------------------------------ transformer block
 extern "C" int32_t chelis_prog_transformer_block(const chelis_gpu_tensor *const *in, int32_t n_in,
                                                  const chelis_gpu_tensor *const *out, int32_t n_out) {
+    const ModeScope mode;
     if (n_in != 17 || n_out != 1) return set_error(CHELIS_HIP_EDOMAIN, "transformer_block: 17 inputs, 1 output");
     TRY(check_all(in, 17, "transformer_block input"));
     TRY(check_all(out, 1, "transformer_block output"));
@@ -307,6 +309,7 @@ extern "C" int32_t chelis_prog_mlp_train_step(const chelis_gpu_tensor *const *in
 
 int32_t chelis::mlp_train_step_run(const chelis_gpu_tensor *const *in, int32_t n_in,
                                    const chelis_gpu_tensor *const *out, int32_t n_out, float rate, float lr) {
+    const ModeScope mode;
     if (n_in != 7 || n_out != 5) return set_error(CHELIS_HIP_EDOMAIN, "mlp_train_step: 7 inputs, 5 outputs");
     TRY(check_all(in, 7, "mlp_train_step input"));
     TRY(check_all(out, 5, "mlp_train_step output"));

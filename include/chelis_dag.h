@@ -47,6 +47,13 @@ void chelis_dag_release(chelis_dag_program *program);
 int32_t chelis_dag_run(chelis_dag_program *program, const chelis_gpu_tensor *const *inputs, int32_t n_in,
                        const chelis_gpu_tensor *const *outputs, int32_t n_out);
 
+/* The program's numeric mode (no counterpart in the reference, which has
+ * one numeric contract per lane): 1 exact (every primitive the C lane
+ * defines bit for bit computed that way), 0 default, -1 (the initial
+ * setting) the library-wide chelis_hip_set_exact mode, read once at the
+ * start of each run. Every launch of one run uses one mode. Returns the
+ * previous setting. */
+int32_t chelis_dag_set_exact(chelis_dag_program *program, int32_t mode);
 int32_t chelis_dag_input_count(const chelis_dag_program *program);
 int32_t chelis_dag_output_count(const chelis_dag_program *program);
 /* output == 0: input slot `index` (its Load's name); 1: output slot (a

@@ -226,7 +226,13 @@ def test_linear_epilogue_bit_exact_on_tree_path(act):
     rng = np.random.default_rng(41)
     x, w = rand(rng, (256, 512), np.float32), rand(rng, (512, 10), np.float32)
     bias, res = rand(rng, (10,), np.float32), rand(rng, (256, 10), np.float32)
-    c = C.linear(C.to_device(x), C.to_device(w), C.to_device(bias), act, C.to_device(res)).numpy()
+    # the GELU graph bit for bit is the exact mode's (the default mode's
+    # binary32 GELU is the direct evaluation, within 1e-6 of it)
+    prev = C.set_exact(act == "gelu")
+    try:
+        c = C.linear(C.to_device(x), C.to_device(w), C.to_device(bias), act, C.to_device(res)).numpy()
+    finally:
+        C.set_exact(prev)
     v = (O.matmul(x, w) + bias).astype(np.float32)
     if act == "relu":
         v = O.relu(v)
@@ -234,6 +240,37 @@ def test_linear_epilogue_bit_exact_on_tree_path(act):
         v = O.gelu(v)
     v = (res + v).astype(np.float32)
     assert bits_equal(c, v), first_diff(c, v)
+    if act == "gelu":
+        d = C.linear(C.to_device(x), C.to_device(w), C.to_device(bias), act, C.to_device(res)).numpy()
+        assert np.all(np.abs(d.astype(np.float64) - v) <= 1e-6 * np.abs(v) + 1e-6 * np.abs(res).max())
+
+
+@pytest.mark.parametrize("exact", [True, False])
+def test_gelu_epilogue_on_the_mfma_tiles(exact):
+    """The GELU epilogue of a dense binary32 product (the FFN1 form) against
+    the exact GELU graph (C.gelu in the exact mode) of the same product
+    computed in the same mode without the activation (the same
+    accumulation): bit for bit in the exact mode; the default mode's
+    direct evaluation within 1e-6 of it."""
+    rng = np.random.default_rng(44)
+    x, w = rand(rng, (512, 256), np.float32), rand(rng, (256, 384), np.float32)
+    bias = rand(rng, (384,), np.float32)
+    dx, dw, db = C.to_device(x), C.to_device(w), C.to_device(bias)
+    prev = C.set_exact(exact)
+    try:
+        c = C.linear(dx, dw, db, "gelu").numpy()
+        pre = C.linear(dx, dw, db, None)
+    finally:
+        C.set_exact(prev)
+    prev = C.set_exact(True)
+    try:
+        ref = C.gelu(pre).numpy()
+    finally:
+        C.set_exact(prev)
+    if exact:
+        assert bits_equal(c, ref), first_diff(c, ref)
+    else:
+        assert np.all(np.abs(c.astype(np.float64) - ref) <= 1e-6 * np.abs(ref) + 2.0 ** -146)
 
 
 def test_linear_epilogue_on_swapped_panel_path():

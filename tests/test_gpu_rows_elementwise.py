@@ -271,16 +271,37 @@ def test_uniform_like_bit_exact(dtype):
     assert bits_equal(out.numpy(), O.uniform_like(12345, dtype(-1.0), dtype(1.0), 100003, dtype))
 
 
+def gelu_f32_close(y, ref, x):
+    """The binary32 default-mode GELU bar: within 1e-6 relative of the Phi
+    graph (ten times inside the north star's 1e-5), with an absolute floor
+    of 2^-146 for subnormal results; NaN, the infinities, the signed zeros
+    and the inputs below -12.5 (the graph's own path) bit for bit."""
+    y64, r64 = y.astype(np.float64), ref.astype(np.float64)
+    close = np.abs(y64 - r64) <= 1e-6 * np.abs(r64) + 2.0 ** -146
+    exact = np.isnan(x) | np.isinf(x) | (x == 0) | (x < -12.5)
+    same = y.view(np.uint32) == ref.view(np.uint32)
+    return (same | (close & ~exact)).all(), float(np.nanmax(np.abs(y64 - r64) / np.maximum(np.abs(r64), 1e-300)))
+
+
+@pytest.mark.parametrize("exact", [True, False])
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
-def test_gelu(dtype):
+def test_gelu(dtype, exact):
     rng = np.random.default_rng(12)
     x = np.concatenate([rng.standard_normal(1 << 20) * 3, np.linspace(-80, 80, 4001),
-                        [np.inf, -np.inf, np.nan, 0.0, -0.0]]).astype(dtype)
-    y = C.gelu(C.to_device(x)).numpy()
+                        [np.inf, -np.inf, np.nan, 0.0, -0.0, -12.5, -12.499999, 1e-40, -1e-40, 14.0, 15.0]]).astype(dtype)
+    prev = C.set_exact(exact)
+    try:
+        y = C.gelu(C.to_device(x)).numpy()
+    finally:
+        C.set_exact(prev)
     ref = O.gelu(x)
     if dtype == np.float32:
-        # every leaf correctly rounded: the whole Phi graph matches bit for bit
-        assert bits_equal(y, ref), mismatch_report(y, ref)
+        if exact:
+            # every leaf correctly rounded: the whole Phi graph matches bit for bit
+            assert bits_equal(y, ref), mismatch_report(y, ref)
+        else:
+            ok, worst = gelu_f32_close(y, ref, x)
+            assert ok, worst
         return
     both_nan = np.isnan(y) & np.isnan(ref)
     ok = both_nan | (y == ref) | (np.abs(y - ref) <= 1e-12 * np.abs(ref))
