@@ -19,10 +19,12 @@ __device__ inline uint64_t splitmix64(uint64_t x) {
     x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
     return x ^ (x >> 31);
 }
-__device__ inline double random_unit(uint64_t key, uint64_t index) {
+__device__ inline uint64_t random_word(uint64_t key, uint64_t index) {
     const uint64_t e = splitmix64(index);
-    const uint64_t w = splitmix64(key ^ ((e << 41) | (e >> 23)));
-    return (double)(w >> 11) * 0x1p-53;
+    return splitmix64(key ^ ((e << 41) | (e >> 23)));
+}
+__device__ inline double random_unit(uint64_t key, uint64_t index) {
+    return (double)(random_word(key, index) >> 11) * 0x1p-53;
 }
 
 // ---------------------------------------------------------------- math leaves

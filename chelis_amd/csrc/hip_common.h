@@ -97,6 +97,9 @@ bool row_view(const chelis_gpu_tensor *t, RowView *v);
 
 // Keyed dropout (and, applied to a cotangent, its replay) with the key read
 // on the device from key_dev, the storage of a KEY tensor: no host round trip.
+// [05-OP-37]'s drop test unit < rate at the dtype, as an integer cut-off:
+// an element is dropped exactly when its word >> 11 is below the result.
+uint64_t dropout_cut(double rate, chelis_dtype dt);
 int32_t dropout_device_key(const uint64_t *key_dev, const chelis_gpu_tensor *x, double rate,
                            const chelis_gpu_tensor *y);
 

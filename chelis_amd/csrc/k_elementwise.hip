@@ -269,6 +269,7 @@ struct UnaryArgs {
     double p0, p1;            // dropout: rate; uniform: low, high
     const uint64_t *key_dev;  // when set, the key is read from device memory (a KEY tensor)
     double inv_keep;          // dropout, binary32: 1 / (double)(1 - (float)rate), set by the kernel
+    uint64_t cut;             // dropout: an element whose word >> 11 is below it is dropped (dropout_cut)
 };
 
 template <typename T, Unary OP, class Tabs = ErfcTablesConst>
@@ -289,15 +290,14 @@ __device__ inline T unary_one(T x, T g, int64_t i, const UnaryArgs &u, const Tab
     } else if constexpr (OP == Unary::ReluAdjoint) {
         return T(0) < x ? g : T(0);
     } else if constexpr (OP == Unary::Dropout) {
-        // [05-OP-37]: the unit at the dtype's width against the rate; a
-        // kept element is x / (1 - rate) (binary32: through the binary64
+        // [05-OP-37]: the unit at the dtype's width against the rate, as the
+        // integer comparison it is equivalent to (dropout_cut); a kept
+        // element is x / (1 - rate) (binary32: through the binary64
         // reciprocal of the divisor, quot_f32, which rounds to the IEEE
         // quotient).
-        const T rate = (T)u.p0;
-        const double unit = random_unit(u.key, (uint64_t)i);
-        const T uw = (T)unit;
-        if constexpr (sizeof(T) == 4) return uw < rate ? T(0) : canon(quot_f32(x, u.inv_keep));
-        else return uw < rate ? T(0) : canon(x / (T(1) - rate));
+        const bool drop = (random_word(u.key, (uint64_t)i) >> 11) < u.cut;
+        if constexpr (sizeof(T) == 4) return drop ? T(0) : canon(quot_f32(x, u.inv_keep));
+        else return drop ? T(0) : canon(x / (T(1) - (T)u.p0));
     } else {
         // [05-OP-8]: one fma(high - low, u, low) at the dtype.
         const T low = (T)u.p0, high = (T)u.p1;
@@ -797,20 +797,52 @@ extern "C" int32_t chelis_hip_relu_adjoint(const chelis_gpu_tensor *x, const che
 }
 
 namespace chelis {
+uint64_t dropout_cut(double rate, chelis_dtype dt) {
+    // The unit of a word is m * 2^-53 (m = word >> 11, exact in binary64),
+    // taken to the dtype (binary32: rounded to nearest, a monotone map) and
+    // compared with the dtype's rate: unit < rate holds exactly for m in a
+    // prefix [0, cut). cut is the least m whose unit is not below the rate,
+    // found by bisection over [0, 2^53].
+    const bool f32 = dt == CHELIS_DTYPE_F32;
+    auto below = [&](uint64_t m) {
+        const double v = (double)m * 0x1p-53;
+        return f32 ? (float)v < (float)rate : v < rate;
+    };
+    uint64_t lo = 0, hi = uint64_t(1) << 53;  // below(hi) is false: units are < 1 <= any rate tested here
+    if (!below(hi - 1)) {
+        while (lo < hi) {
+            const uint64_t mid = lo + (hi - lo) / 2;
+            if (below(mid)) lo = mid + 1;
+            else hi = mid;
+        }
+    } else {
+        lo = hi;
+    }
+    return lo;
+}
+
 int32_t dropout_device_key(const uint64_t *key_dev, const chelis_gpu_tensor *x, double rate,
                            const chelis_gpu_tensor *y) {
     if (!key_dev) return set_error(CHELIS_HIP_EDOMAIN, "dropout: null key");
     if (!y || !is_float(y->dtype)) return set_error(CHELIS_HIP_EDOMAIN, "dropout: f32 or f64 result required");
     if (int32_t s = check_rate(rate, y->dtype)) return s;
-    return unary_entry<Unary::Dropout>("dropout", x, nullptr, y, UnaryArgs{0, rate, 0.0, key_dev});
+    UnaryArgs u{0, rate, 0.0, key_dev};
+    u.cut = dropout_cut(rate, y->dtype);
+    return unary_entry<Unary::Dropout>("dropout", x, nullptr, y, u);
 }
 }  // namespace chelis
+
+extern "C" uint64_t chelis_hip_dropout_cut(double rate, int32_t dtype) {
+    return chelis::dropout_cut(rate, (chelis_dtype)dtype);
+}
 
 extern "C" int32_t chelis_hip_dropout(uint64_t key, const chelis_gpu_tensor *x, double rate,
                                       const chelis_gpu_tensor *y) {
     if (!y || !is_float(y->dtype)) return set_error(CHELIS_HIP_EDOMAIN, "dropout: f32 or f64 result required");
     if (int32_t s = check_rate(rate, y->dtype)) return s;
-    return unary_entry<Unary::Dropout>("dropout", x, nullptr, y, UnaryArgs{key, rate, 0.0, nullptr});
+    UnaryArgs u{key, rate, 0.0, nullptr};
+    u.cut = dropout_cut(rate, y->dtype);
+    return unary_entry<Unary::Dropout>("dropout", x, nullptr, y, u);
 }
 
 extern "C" int32_t chelis_hip_dropout_replay(uint64_t key, const chelis_gpu_tensor *g, double rate,
@@ -819,7 +851,9 @@ extern "C" int32_t chelis_hip_dropout_replay(uint64_t key, const chelis_gpu_tens
     // divided by (1 - rate); the same kernel with g in place of x.
     if (!dx || !is_float(dx->dtype)) return set_error(CHELIS_HIP_EDOMAIN, "dropout_replay: f32 or f64 result required");
     if (int32_t s = check_rate(rate, dx->dtype)) return s;
-    return unary_entry<Unary::Dropout>("dropout_replay", g, nullptr, dx, UnaryArgs{key, rate, 0.0, nullptr});
+    UnaryArgs u{key, rate, 0.0, nullptr};
+    u.cut = dropout_cut(rate, dx->dtype);
+    return unary_entry<Unary::Dropout>("dropout_replay", g, nullptr, dx, u);
 }
 
 extern "C" int32_t chelis_hip_uniform_like(uint64_t key, double low, double high, const chelis_gpu_tensor *out) {

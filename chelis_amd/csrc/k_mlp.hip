@@ -49,6 +49,7 @@ struct MlpArgs {
     int O;
     bool vec;  // z1 slices, d and g_d rows load and store as float4
     float rate, g_pr, lr;
+    uint64_t cut;  // dropout: keep when word >> 11 is at least this (dropout_cut)
     double inv_keep, inv_batch;
 };
 
@@ -95,7 +96,8 @@ __device__ inline float lane_value(float v, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
 
-__device__ __noinline__ float unit32(uint64_t key, uint64_t index) { return (float)random_unit(key, index); }
+// the word's top 53 bits, compared with the dropout cut-off (dropout_cut)
+__device__ __noinline__ uint64_t word53(uint64_t key, uint64_t index) { return random_word(key, index) >> 11; }
 // exp of x - max (<= 0 or NaN), correctly rounded
 __device__ __noinline__ float exp_class(float x) { return expf_cr_nonpos(x); }
 __device__ __noinline__ float log_class(float x) { return leaf_log<float>(x); }
@@ -229,7 +231,7 @@ __global__ __launch_bounds__(256) void mlp_head_kernel(MlpArgs a) {
         uint32_t keep = 0;
 #pragma unroll
         for (int i = 0; i < L; ++i) {
-            const bool kp = !(unit32(key, (uint64_t)(b * H + k0 + i)) < a.rate);
+            const bool kp = word53(key, (uint64_t)(b * H + k0 + i)) >= a.cut;
             keep |= (uint32_t)kp << i;
             dv[i] = kp ? canon(quot_f32(hv[i], a.inv_keep)) : 0.f;
         }
@@ -545,6 +547,7 @@ MlpArgs make_args(const MlpNarrow &m) {
     // -(1 / B): finite and not NaN for B >= 1
     a.g_pr = -(1.0f / (float)m.B);
     a.inv_keep = 1.0 / (double)(1.0f - m.rate);
+    a.cut = dropout_cut((double)m.rate, CHELIS_DTYPE_F32);
     a.inv_batch = 1.0 / (double)(float)m.B;
     return a;
 }

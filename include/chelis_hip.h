@@ -176,11 +176,20 @@ int32_t chelis_hip_uniform_like(uint64_t key, double low, double high, const che
 int32_t chelis_hip_dropout(uint64_t key, const chelis_gpu_tensor *x, double rate, const chelis_gpu_tensor *y);
 int32_t chelis_hip_dropout_replay(uint64_t key, const chelis_gpu_tensor *g, double rate,
                                   const chelis_gpu_tensor *dx);
+/* The drop test unit(key, i) < rate at the dtype (the unit (word >> 11) *
+ * 2^-53 taken to the dtype, rounded to nearest for f32) as the integer test
+ * (word >> 11) < cut the kernels run: the least m in [0, 2^53] whose unit
+ * is not below the rate. No counterpart in the reference (its C lane
+ * compares the units); exported so the equivalence can be checked. */
+uint64_t chelis_hip_dropout_cut(double rate, int32_t dtype);
 
 /* ---- activations ----
- * gelu: spec/05 section 3.3's exact Phi graph (fenced on the reference HIP
- * lane). relu / relu adjoint: kernels.rs:1136-1196, and for bf16 / f16
- * operands kernels.rs:1196-1260 (stored bits selected). */
+ * gelu: spec/05 section 3.3's Phi graph (fenced on the reference HIP
+ * lane): bit for bit in the exact mode (chelis_hip_set_exact); in the
+ * default mode binary32 is evaluated directly as x Phi(x), within 1e-6
+ * relative of the graph (binary64 is the graph in both). relu / relu
+ * adjoint: kernels.rs:1136-1196, and for bf16 / f16 operands
+ * kernels.rs:1196-1260 (stored bits selected). */
 int32_t chelis_hip_gelu(const chelis_gpu_tensor *x, const chelis_gpu_tensor *y);
 int32_t chelis_hip_relu(const chelis_gpu_tensor *x, const chelis_gpu_tensor *y);
 int32_t chelis_hip_relu_adjoint(const chelis_gpu_tensor *x, const chelis_gpu_tensor *g,

@@ -115,3 +115,40 @@ def test_metadata_plan_traps_like_the_reference(case):
     assert r.returncode == 1, (r.returncode, r.stdout, r.stderr)
     kind = "overflow" if case == "overflow" else "domain"
     assert f"numeric trap: {kind} in metadata_plan at i64" in r.stderr
+
+
+def _cut_closed_form(rate, f32):
+    """The least m in [0, 2^53] whose unit m * 2^-53, taken to the dtype, is
+    not below the dtype's rate, from exact rationals: binary64 compares the
+    unit itself; binary32 rounds it to nearest even, so the unit is not below
+    r exactly above the midpoint between r and its predecessor (at the
+    midpoint when r's significand is even)."""
+    from fractions import Fraction
+    if not f32:
+        q = Fraction(rate) * 2 ** 53
+        return int(q) if q.denominator == 1 else int(q) + 1
+    r = np.float32(rate)
+    if r == 0:
+        return 0
+    p = np.nextafter(r, np.float32(0))
+    mid = (Fraction(float(p)) + Fraction(float(r))) / 2 * 2 ** 53
+    r_even = (int(r.view(np.uint32)) & 1) == 0
+    if mid.denominator == 1:
+        return int(mid) if r_even else int(mid) + 1
+    return int(mid) + 1
+
+
+@pytest.mark.parametrize("rate", [0.0, 0.1, 0.5, 0.25, 1e-30, 1e-45, 0.9999999, 0.3333333333333333,
+                                  float(np.nextafter(np.float32(0.5), np.float32(1))),
+                                  2.0 ** -53, 1 - 2.0 ** -53, 0.7])
+@pytest.mark.parametrize("dtype", [0, 1])
+def test_dropout_cut_is_the_drop_test(rate, dtype):
+    """chelis_hip_dropout_cut, the integer form of [05-OP-37]'s unit < rate
+    the dropout kernels run, against its closed form."""
+    f32 = dtype == 0
+    if f32 and float(np.float32(rate)) >= 1.0:
+        pytest.skip("the binary32 rate rounds to 1")
+    L = C.lib()
+    L.chelis_hip_dropout_cut.restype = ctypes.c_uint64
+    L.chelis_hip_dropout_cut.argtypes = [ctypes.c_double, ctypes.c_int32]
+    assert L.chelis_hip_dropout_cut(rate, dtype) == _cut_closed_form(rate, f32)
