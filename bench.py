@@ -288,7 +288,7 @@ def bench_bandwidth(C, H, steps, warmup):
     line("dropout_f32_16384x4096", lambda i: C.dropout(44, X[i % 3], 0.1, Y[i % 3]), 2 * nb,
          "VALU (splitmix64 64-bit multiplies per element)")
     line("gelu_f32_16384x4096", lambda i: C.gelu(X[i % 3], Y[i % 3]), 2 * nb,
-         "VALU (correctly rounded exp and erfc leaves)")
+         "VALU (binary32 x Phi(x): an erfcx polynomial times exp2 of a binary64 argument)")
     sq = C.fused_chain([("sub", 0, 1), ("mul", ("s", 0), ("s", 0))])
     line("fused_chain_sqdiff_f32_16384x4096", lambda i: C.fused_elementwise(sq, [X[i % 3], G[i % 3]], Y[i % 3]),
          3 * nb)
@@ -335,7 +335,13 @@ BW_SET = [
     ("layer_norm_f32_65536x1024", r"layer_norm_kernel<float", 2 * 65536 * 1024 * 4),
     ("relu_f32_16384x4096", r"unary_kernel<float", 2 * 16384 * 4096 * 4),
     ("fused_chain_sqdiff_f32_16384x4096", r"fused_flat_vec_kernel<float", 3 * 16384 * 4096 * 4),
-    ("reduce_sum_rows_f32_16384x4096", r"reduce_rows_vec_kernel<float", 16384 * 4096 * 4 + 16384 * 4),
+    ("reduce_sum_rows_f32_16384x4096", r"reduce_rows_vec_kernel<float, \(Rk\)0, \d+, false",
+     16384 * 4096 * 4 + 16384 * 4),
+    ("reduce_sum_sqdiff_rows_f32_16384x4096", r"reduce_rows_vec_kernel<float, \(Rk\)0, \d+, true",
+     2 * 16384 * 4096 * 4 + 16384 * 4),
+    # two launches per column sum (the 128-leaf groups, then their join):
+    # the traffic is their sum
+    ("reduce_sum_cols_f32_16384x4096", r"reduce_cols4_kernel<float", 16384 * 4096 * 4 + 4096 * 4, 2),
     ("softmax_adjoint_f32_65536x1024", r"softmax_adjoint_kernel<float", 3 * 65536 * 1024 * 4),
     ("causal_softmax_f32_8x16x512x512", r"softmax_kernel<float,[^>]*, false, false>",
      CAUSAL_READ + 8 * 16 * 512 * 512 * 4),
@@ -406,6 +412,11 @@ def profile_child(kind: str):
         S1 = C.empty((16384,), np.float32)
         for _ in range(n):
             C.reduce("sum", X, 1, S1)
+        for _ in range(n):
+            C.reduce("sum", [X, G], 1, S1, chain=sq)
+        S0 = C.empty((4096,), np.float32)
+        for _ in range(n):
+            C.reduce("sum", X, 0, S0)
         del X, G, Y
         s = C.to_device(rng.standard_normal((8, 16, 512, 512)).astype(np.float32))
         so = C.empty((8, 16, 512, 512), np.float32)
@@ -485,11 +496,22 @@ def _pmc_pass(counters, kind, keep_dir=None, timeout_s=240):
     return list(per.values()), shown
 
 
-def _median_of(dispatches, pattern, counter):
+def _median_of(dispatches, pattern, counter, launches=1):
+    """The counter per call of an op: the median over its dispatches, or,
+    for an op of `launches` > 1 dispatches, their mean times that count."""
     import re
 
     vals = [c[counter] for name, c in dispatches if re.search(pattern, name) and counter in c]
-    return (float(np.median(vals)), len(vals)) if vals else (None, 0)
+    if not vals:
+        return None, 0
+    if launches > 1:
+        return float(np.mean(vals)) * launches, len(vals) // launches
+    return float(np.median(vals)), len(vals)
+
+
+def _bw_entries():
+    """BW_SET rows as (key, pattern, algorithmic bytes, launches per call)."""
+    return [(e[0], e[1], e[2], e[3] if len(e) > 3 else 1) for e in BW_SET]
 
 
 def measure_counters(kernels, keep_root=None):
@@ -499,7 +521,7 @@ def measure_counters(kernels, keep_root=None):
     keep = (lambda name: os.path.join(keep_root, name)) if keep_root else (lambda name: None)
     fetch, cmd_f = _pmc_pass(["FETCH_SIZE"], "bandwidth", keep("fetch"))
     write, cmd_w = _pmc_pass(["WRITE_SIZE"], "bandwidth", keep("write"))
-    calib = dict((k, (pat, b)) for k, pat, b in BW_SET)[CALIBRATION]
+    calib = dict((k, (pat, b)) for k, pat, b, _ in _bw_entries())[CALIBRATION]
     f_unit, _ = _median_of(fetch, calib[0], "FETCH_SIZE")
     w_unit, _ = _median_of(write, calib[0], "WRITE_SIZE")
     if not f_unit or not w_unit:
@@ -509,9 +531,9 @@ def measure_counters(kernels, keep_root=None):
                "calibration": f"{CALIBRATION}: {calib[1] // 2} B read and written; FETCH_SIZE unit "
                               f"{f_scale:.1f} B, WRITE_SIZE unit {w_scale:.1f} B",
                "bandwidth": {}, "mfma": {}}
-    for key, pat, alg in BW_SET:
-        fv, nf = _median_of(fetch, pat, "FETCH_SIZE")
-        wv, nw = _median_of(write, pat, "WRITE_SIZE")
+    for key, pat, alg, launches in _bw_entries():
+        fv, nf = _median_of(fetch, pat, "FETCH_SIZE", launches)
+        wv, nw = _median_of(write, pat, "WRITE_SIZE", launches)
         if fv is None or wv is None:
             continue
         traffic = fv * f_scale + wv * w_scale

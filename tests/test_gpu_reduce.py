@@ -289,3 +289,36 @@ def test_count_deferred_trap_channel():
     C.count(C.to_device(bad), 0, deferred=True)
     _, e = C.count(C.to_device(good), 1)
     assert e == 0 and C.trap_status() == 1
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("shape,axis", [((16384, 4096), 0), ((128, 4), 0), ((256, 1026), 0), ((3, 1024, 520), 1),
+                                        ((32768, 1000), 0), ((384, 4100), 0), ((1280, 300), 0),
+                                        ((32896, 64), 0), ((2, 128, 8), 1)])
+def test_column_sums_at_many_shapes(shape, axis, dtype):
+    """Column sums whose leaf counts are and are not multiples of the
+    128-leaf groups, whose partial counts are and are not powers of two, and
+    whose column counts are narrower and wider than a workgroup's 64 columns:
+    the canonical tree bit for bit, with NaN, signed zeros and infinities in
+    some columns, twice in a row."""
+    rng = np.random.default_rng(sum(shape) + 3)
+    x = rng.standard_normal(shape).astype(dtype)
+    flat = np.moveaxis(x, axis, 0).reshape(shape[axis], -1)
+    flat[5::97, 1] = np.nan
+    flat[:, 2] = -0.0
+    flat[3::11, 2] = 0.0
+    flat[::13, 3] = -np.inf
+    d = C.to_device(x)
+    ref = O.sum_axis(x, axis)
+    for _ in range(2):
+        assert bits_equal(C.reduce("sum", d, axis).numpy(), ref)
+
+
+def test_column_sum_of_a_strided_view():
+    """A column sum over rows whose stride is not a whole number of 16-byte
+    vectors: the same values, the same bits as over the dense copy."""
+    rng = np.random.default_rng(77)
+    big = rng.standard_normal((1024, 1031)).astype(np.float32)
+    d = C.to_device(big)
+    view = d.view((1024, 1024), (1031, 1))
+    assert bits_equal(C.reduce("sum", view, 0).numpy(), O.sum_axis(np.ascontiguousarray(big[:, :1024]), 0))
