@@ -27,13 +27,14 @@ class ChelisError(RuntimeError):
 
 
 # ---- ABI types (include/chelis_runtime.h, include/chelis_device_descriptor.h) ----
-DT_F32, DT_F64, DT_I32, DT_BOOL, DT_I64, DT_BF16, DT_F16, DT_KEY = 0, 1, 2, 3, 4, 5, 6, 9
+DT_F32, DT_F64, DT_I32, DT_BOOL, DT_I64, DT_BF16, DT_F16, DT_I8, DT_I16, DT_KEY = 0, 1, 2, 3, 4, 5, 6, 7, 8, 9
 # bfloat16 has no numpy dtype: bf16 tensors travel as np.uint16 bit patterns
 _NP2DT = {np.dtype(np.float32): DT_F32, np.dtype(np.float64): DT_F64, np.dtype(np.int32): DT_I32,
           np.dtype(np.uint8): DT_BOOL, np.dtype(np.bool_): DT_BOOL, np.dtype(np.int64): DT_I64,
-          np.dtype(np.uint16): DT_BF16, np.dtype(np.float16): DT_F16}
+          np.dtype(np.uint16): DT_BF16, np.dtype(np.float16): DT_F16, np.dtype(np.int8): DT_I8,
+          np.dtype(np.int16): DT_I16}
 _DT2NP = {DT_F32: np.float32, DT_F64: np.float64, DT_I32: np.int32, DT_BOOL: np.uint8, DT_I64: np.int64,
-          DT_BF16: np.uint16, DT_F16: np.float16, DT_KEY: np.uint64}
+          DT_BF16: np.uint16, DT_F16: np.float16, DT_I8: np.int8, DT_I16: np.int16, DT_KEY: np.uint64}
 
 
 class Scalar(ctypes.Structure):
@@ -48,6 +49,10 @@ class GpuTensor(ctypes.Structure):
     _fields_ = [("data", c_void_p), ("shape", POINTER(c_int64)), ("strides", POINTER(c_int64)),
                 ("count", c_int64), ("byte_capacity", c_int64), ("rank", c_int32), ("dtype", c_uint8),
                 ("ownership", c_uint8), ("reserved", c_uint8 * 2)]
+
+
+class NumericFailure(ctypes.Structure):
+    _fields_ = [("index", c_int64), ("kind", c_int32), ("reserved", c_int32), ("message", ctypes.c_char * 96)]
 
 
 class FusedStep(ctypes.Structure):
@@ -131,6 +136,13 @@ SIGNATURES = {
     "linreg_step_device": (None, [POINTER(c_void_p), c_int32, POINTER(c_void_p), c_int32]),
     "transformer_block_device": (None, [POINTER(c_void_p), c_int32, POINTER(c_void_p), c_int32]),
     "mlp_train_step_device": (None, [POINTER(c_void_p), c_int32, POINTER(c_void_p), c_int32]),
+    "chelis_hip_compare": (c_int32, [c_int32, P, P, P]),
+    "chelis_hip_logical": (c_int32, [c_int32, P, P, P]),
+    "chelis_hip_where": (c_int32, [P, P, P, P]),
+    "chelis_hip_cast": (c_int32, [P, P, POINTER(NumericFailure)]),
+    "chelis_hip_integer_elementwise": (c_int32, [c_int32, P, P, P, POINTER(NumericFailure)]),
+    "chelis_hip_gather": (c_int32, [P, P, c_int32, c_int32, P, POINTER(NumericFailure)]),
+    "chelis_hip_take_numeric_failure": (c_int32, [POINTER(NumericFailure)]),
     "chelis_hip_set_exact_matmul": (c_int32, [c_int32]),
     "chelis_hip_set_exact": (c_int32, [c_int32]),
     # chelis_dag.h
@@ -485,6 +497,81 @@ def trap_status() -> int:
     return code.value
 
 
+# ---- comparison, logical, where, checked casts / integer arithmetic, gather ----
+COMPARE_KINDS = {"cmp_lt": 0, "lt": 1, "eq": 2, "neq": 3, "gt": 4, "gte": 5, "lte": 6}
+LOGICAL_KINDS = {"and": 0, "or": 1, "not": 2}
+INT_OPS = {"add": 0, "sub": 1, "mul": 2, "floor_div": 3, "trunc_div": 4, "mod": 5, "max_elem": 6, "min_elem": 7,
+           "neg": 8, "abs": 9}
+
+
+def _bshape(*ts):
+    return tuple(np.broadcast_shapes(*[t.shape for t in ts]))
+
+
+def _failure(f: NumericFailure):
+    """(index, kind, trap line) of a failure record, None when it holds none."""
+    return None if f.kind == 0 else (f.index, f.kind, f.message.decode())
+
+
+def compare(kind: str, a, b, out=None):
+    """chelis_hip_compare: Bool8 (np.uint8) result; operands of one rank
+    broadcast by their extent-1 axes."""
+    out = out or empty(_bshape(a, b), np.uint8)
+    check(lib().chelis_hip_compare(COMPARE_KINDS[kind], _p(a), _p(b), _p(out)), "compare")
+    return out
+
+
+def logical(kind: str, a, b=None, out=None):
+    out = out or empty(_bshape(a, b) if b is not None else a.shape, np.uint8)
+    check(lib().chelis_hip_logical(LOGICAL_KINDS[kind], _p(a), _p(b) if b is not None else None, _p(out)),
+          "logical")
+    return out
+
+
+def where(cond, a, b, out=None):
+    out = out or empty(_bshape(cond, a, b), a.dtype)
+    check(lib().chelis_hip_where(_p(cond), _p(a), _p(b), _p(out)), "where")
+    return out
+
+
+def cast(x, dtype, out=None, deferred: bool = False):
+    """chelis_hip_cast to `dtype` (np.uint16 for bf16, np.float16 for f16,
+    np.uint8 for bool); returns (out, failure) with failure None when no
+    element failed (and always None with deferred=True: the record goes to
+    take_numeric_failure)."""
+    out = out or empty(x.shape, dtype)
+    f = NumericFailure()
+    check(lib().chelis_hip_cast(_p(x), _p(out), None if deferred else ctypes.byref(f)), "cast")
+    return out, None if deferred else _failure(f)
+
+
+def integer_op(op: str, a, b=None, out=None, deferred: bool = False):
+    """chelis_hip_integer_elementwise; returns (out, failure) as cast does."""
+    out = out or empty(_bshape(a, b) if b is not None else a.shape, a.dtype)
+    f = NumericFailure()
+    check(lib().chelis_hip_integer_elementwise(INT_OPS[op], _p(a), _p(b) if b is not None else None, _p(out),
+                                               None if deferred else ctypes.byref(f)), "integer_elementwise")
+    return out, None if deferred else _failure(f)
+
+
+def gather(values, indices, axis: int, batch_rank: int = 0, out=None, deferred: bool = False):
+    """chelis_hip_gather; returns (out, failure) as cast does."""
+    shape = tuple(values.shape[:axis]) + tuple(indices.shape[batch_rank:]) + tuple(values.shape[axis + 1:])
+    out = out or empty(shape, values.dtype)
+    f = NumericFailure()
+    check(lib().chelis_hip_gather(_p(values), _p(indices), axis, batch_rank, _p(out),
+                                  None if deferred else ctypes.byref(f)), "gather")
+    return out, None if deferred else _failure(f)
+
+
+def take_numeric_failure():
+    """chelis_hip_take_numeric_failure: the earliest deferred failure since
+    the last read as (index, kind, trap line), or None; clears the record."""
+    f = NumericFailure()
+    check(lib().chelis_hip_take_numeric_failure(ctypes.byref(f)), "take_numeric_failure")
+    return _failure(f)
+
+
 # ---- matmul ----
 MATMUL_EXACT = 1
 ACT = {None: 0, "none": 0, "relu": 1, "gelu": 2}
@@ -597,7 +684,10 @@ class DagProgram:
         self.handle = lib().chelis_dag_compile(data, len(data))
         if not self.handle:
             raise ChelisError("dag compile failed: " + lib().chelis_hip_last_error().decode(errors="replace"))
-        self.has_count = any(line.split()[1:2] == ["count"] for line in self.describe().splitlines())
+        kinds = [line.split()[1] for line in self.describe().splitlines() if len(line.split()) > 1]
+        self.has_count = "count" in kinds
+        # launches that record into the deferred failure record
+        self.has_traps = any(k in ("cast", "integer", "gather") for k in kinds)
 
     def __del__(self):
         try:
@@ -674,6 +764,12 @@ class DagProgram:
         ins = (P * max(1, len(inputs)))(*[_p(t) for t in inputs])
         outs = (P * max(1, len(outputs)))(*[_p(t) for t in outputs])
         check(lib().chelis_dag_run(self.handle, ins, len(inputs), outs, len(outputs)), "dag run")
+        if self.has_traps:
+            # the earliest failing launch's lowest failing element, read once
+            # after the run (a synchronization)
+            failure = take_numeric_failure()
+            if failure:
+                raise ChelisError(failure[2])
         if self.has_count:
             # the trap channel, read once after the run (a synchronization)
             if trap_status():

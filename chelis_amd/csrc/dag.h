@@ -53,6 +53,7 @@ const char *prim_name(Prim p);
 int64_t prim_width(Prim p);
 chelis_dtype prim_dtype(Prim p);
 bool prim_is_float(Prim p);
+bool is_integer(Prim p);  // i8, i16, i32, i64
 
 enum class Op : uint8_t {
     // leaves
@@ -61,7 +62,9 @@ enum class Op : uint8_t {
     Add, Sub, Mul, Div, Pow, FloorDiv, TruncDiv, MaxElem, MinElem, Neg, Recip, Exp, Log, Sin, Sqrt, Cos, Tan,
     Atan, Tanh, Erf, Erfc, Abs, Floor, Ceil, Round,
     // elementwise ops that stay their own node
-    Relu, ReluAdjoint, Where, Compare, Dropout, DropoutReplay, Cast,
+    Relu, ReluAdjoint, Where, Compare, Dropout, DropoutReplay, Cast, Logical, Mod,
+    // sparse selection along one axis
+    Gather,
     // reductions over one axis
     Sum, MaxReduce, MinReduce, ProdReduce, Argmax, Argmin, Count, Softmax,
     // movement
@@ -121,7 +124,8 @@ struct Node {
     WitnessSite site = WitnessSite::None;  // ExtentWitness
     std::vector<int64_t> requirements;     // ExtentWitness: literal extents its axis must equal
     int64_t named_claims = 0;              // ExtentWitness: claims against other witnesses
-    std::string compare;            // Compare kind (snake_case wire name)
+    std::string compare;            // Compare / Logical kind (snake_case wire name)
+    int64_t batch_rank = 0;         // Gather (its axis in `axis`)
     Prim const_prec = Prim::Other;  // Const
     uint64_t const_bits = 0;        // float bits, or the integer / bool value
     std::vector<Step> steps;        // FusedElem
@@ -188,7 +192,10 @@ enum class RegionKind : uint8_t {
     // whole lowered programs recognized as one region (their results in
     // `out` and `more_out`): the linear-regression step and the MLP
     // training step, run as this library's fused programs
-    LinregStep, MlpStep
+    LinregStep, MlpStep,
+    // one node each: comparison, logical, where, checked cast, checked
+    // integer arithmetic (code = the op), gather (axis, batch_rank)
+    Compare, Logical, Where, Cast, Integer, Gather
 };
 const char *region_kind_name(RegionKind k);
 
@@ -216,6 +223,10 @@ struct Region {
     // mlp step: in = {x, onehot, w1, b1, w2, b2, key}, out = loss,
     // more_out = {w1', b1', w2', b2'}, rate, lr (below)
     double lr = 0.0;
+    // compare / logical: the kind; integer: the CHELIS_INT_* op; gather's
+    // batch rank (its axis in `axis`)
+    int32_t code = 0;
+    int64_t batch_rank = 0;
     std::vector<int64_t> outputs() const {
         std::vector<int64_t> o{out};
         o.insert(o.end(), more_out.begin(), more_out.end());

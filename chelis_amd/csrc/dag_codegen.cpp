@@ -211,7 +211,7 @@ std::string emit_source(const Plan &plan, const Graph &fused, const std::string 
         if (end == std::string::npos) break;
         start = end + 1;
     }
-    s += "#include <hip/hip_runtime_api.h>\n\n#include <cstdio>\n#include <cstdlib>\n#include <mutex>\n\n"
+    s += "#include <hip/hip_runtime_api.h>\n\n#include <cstdio>\n#include <cstdlib>\n#include <cstring>\n#include <mutex>\n\n"
          "#include \"chelis_dag.h\"\n#include \"chelis_device_owner.h\"\n#include \"chelis_hip.h\"\n"
          "#include \"chelis_runtime.h\"\n\n";
     s += "namespace {\n\n";
@@ -266,14 +266,30 @@ std::string emit_source(const Plan &plan, const Graph &fused, const std::string 
         }
         e.line("const int32_t status = chelis_dag_run(program(), chelis_in, " + std::to_string(n_in) + ", chelis_out, " +
                std::to_string(n_out) + ");");
+        // a launcher's own trap line (a gather's paired batch extents) is the
+        // trap; any other domain error is the launch's
         e.line("if (status == CHELIS_HIP_EDOMAIN) {");
-        e.line("    fprintf(stderr, \"%s\\n\", chelis_hip_last_error());");
+        e.line("    const char *why = chelis_hip_last_error();");
+        e.line("    if (strncmp(why, \"numeric trap: \", 14) == 0) chelis_numeric_trap(why);");
+        e.line("    fprintf(stderr, \"%s\\n\", why);");
         e.line("    chelis_numeric_trap(\"numeric trap: domain in launch at i64\");");
         e.line("}");
         e.line("if (status != CHELIS_HIP_OK) {");
         e.line("    fprintf(stderr, \"" + fmt_text(f) + ": %s\\n\", chelis_hip_last_error());");
         e.line("    abort();");
         e.line("}");
+        bool traps = false;
+        for (const Region &r : plan.regions)
+            traps = traps || r.kind == RegionKind::Cast || r.kind == RegionKind::Integer || r.kind == RegionKind::Gather;
+        if (traps) {
+            // the earliest failing launch's lowest failing element
+            // ([04-NUM-15]), read once after the run
+            e.line("{");
+            e.line("    chelis_hip_numeric_failure chelis_failure;");
+            e.line("    if (chelis_hip_take_numeric_failure(&chelis_failure) != CHELIS_HIP_OK) abort();");
+            e.line("    if (chelis_failure.kind != 0) chelis_numeric_trap(chelis_failure.message);");
+            e.line("}");
+        }
         e.line("int32_t chelis_count_error = 0;");
         e.line("if (chelis_hip_trap_status(&chelis_count_error) != CHELIS_HIP_OK) abort();");
         e.line("if (chelis_count_error) {");

@@ -399,6 +399,21 @@ int32_t run_plan(chelis_dag_program *prog, const chelis_gpu_tensor *const *input
                 s = attention_causal(&t4[0], &t4[1], &t4[2], r.scale, &t4[3]);
                 break;
             }
+            // trapping launches record into the device's deferred failure
+            // record, read once by whoever waits for the run
+            // (chelis_hip_take_numeric_failure)
+            case RegionKind::Compare: s = chelis_hip_compare(r.code, in[0], in[1], out); break;
+            case RegionKind::Logical:
+                s = chelis_hip_logical(r.code, in[0], in.size() > 1 ? in[1] : nullptr, out);
+                break;
+            case RegionKind::Where: s = chelis_hip_where(in[0], in[1], in[2], out); break;
+            case RegionKind::Cast: s = chelis_hip_cast(in[0], out, nullptr); break;
+            case RegionKind::Integer:
+                s = chelis_hip_integer_elementwise(r.code, in[0], in.size() > 1 ? in[1] : nullptr, out, nullptr);
+                break;
+            case RegionKind::Gather:
+                s = chelis_hip_gather(in[0], in[1], (int32_t)r.axis, (int32_t)r.batch_rank, out, nullptr);
+                break;
             case RegionKind::Copy: {
                 const chelis_gpu_tensor *dst = outputs[r.axis];
                 s = chelis_hip_fused_elementwise(&identity_chain(), in.data(), 1, dst);

@@ -26,11 +26,11 @@ std::vector<int64_t> consumer_counts(const Graph &g) {
     return c;
 }
 
-namespace {
-
 bool is_integer(Prim p) {
     return p == Prim::Int8 || p == Prim::Int16 || p == Prim::Int32 || p == Prim::Int64;
 }
+
+namespace {
 
 // DagView::is_activation_gated (crates/chelis-dag-core/src/dag.rs:2864-2880)
 // over the chain ops: under an activation, an op whose run-time check may

@@ -59,6 +59,12 @@ const char *region_kind_name(RegionKind k) {
         case RegionKind::MatmulGroup: return "matmul_group";
         case RegionKind::LinregStep: return "linreg_step";
         case RegionKind::MlpStep: return "mlp_step";
+        case RegionKind::Compare: return "compare";
+        case RegionKind::Logical: return "logical";
+        case RegionKind::Where: return "where";
+        case RegionKind::Cast: return "cast";
+        case RegionKind::Integer: return "integer";
+        case RegionKind::Gather: return "gather";
     }
     return "?";
 }
@@ -851,9 +857,72 @@ struct Planner {
         return true;
     }
 
+    // fuse.rs would join an integer node and its one reader into a FusedElem
+    // chain (its fusibility table holds integer add, mul, neg, floor_div and
+    // trunc_div); both reference lanes refuse integer chains.
+    bool int_fusible(int64_t id) const {
+        const Node &n = N(id);
+        return claimed[id] < 0 && op_is_chain_step(n.op) && is_integer(n.prec) && chain_fusible(n) && !barrier[id];
+    }
+    bool in_integer_chain(int64_t id) const {
+        if (!int_fusible(id)) return false;
+        auto link = [&](int64_t p) {
+            if (counts[p] != 1 || users[p].size() != 1) return false;
+            const int64_t c = users[p][0];
+            return int_fusible(p) && int_fusible(c) && N(c).owner_decl == N(p).owner_decl &&
+                   N(c).owner_activation == N(p).owner_activation;
+        };
+        if (link(id)) return true;
+        for (int64_t in : N(id).inputs)
+            if (link(in) && users[in][0] == id) return true;
+        return false;
+    }
+    static int int_code(Op op) {
+        switch (op) {
+            case Op::Add: return CHELIS_INT_ADD;
+            case Op::Sub: return CHELIS_INT_SUB;
+            case Op::Mul: return CHELIS_INT_MUL;
+            case Op::FloorDiv: return CHELIS_INT_FLOOR_DIV;
+            case Op::TruncDiv: return CHELIS_INT_TRUNC_DIV;
+            case Op::Mod: return CHELIS_INT_MOD;
+            case Op::MaxElem: return CHELIS_INT_MAX_ELEM;
+            case Op::MinElem: return CHELIS_INT_MIN_ELEM;
+            case Op::Neg: return CHELIS_INT_NEG;
+            case Op::Abs: return CHELIS_INT_ABS;
+            default: return -1;
+        }
+    }
+    static int compare_code(const std::string &k) {
+        static const char *names[] = {"cmp_lt", "lt", "eq", "neq", "gt", "gte", "lte"};
+        for (int i = 0; i < 7; ++i)
+            if (k == names[i]) return i;
+        return -1;
+    }
+    bool single(const Node &n, RegionKind kind, int32_t code = 0) {
+        Region r;
+        r.kind = kind;
+        r.code = code;
+        r.in = n.inputs;
+        r.out = n.id;
+        r.covers = {n.id};
+        claim(r);
+        return true;
+    }
+
     bool generic() {
         for (const Node &n : g.nodes) {
             if (claimed[n.id] >= 0) continue;
+            if (is_integer(n.prec) && in_integer_chain(n.id))
+                return fail("node " + std::to_string(n.id) + ": " + n.variant +
+                            " would join an integer fused elementwise chain, which neither reference lane runs "
+                            "(crates/chelis-backend-c/src/emit.rs:6933-6945)");
+            if (is_integer(n.prec) && int_code(n.op) >= 0 && n.owner_activation < 0) {
+                const size_t want = (n.op == Op::Neg || n.op == Op::Abs) ? 1 : 2;
+                if (n.inputs.size() != want)
+                    return fail("node " + std::to_string(n.id) + ": " + n.variant + " with the wrong arity");
+                single(n, RegionKind::Integer, int_code(n.op));
+                continue;
+            }
             if (fusible(n.id)) {
                 // fuse.rs:136-191: extend through single-consumer fusible links
                 std::vector<int64_t> chain{n.id};
@@ -930,6 +999,45 @@ struct Planner {
                 case Op::Relu: case Op::ReluAdjoint: {
                     Region r;
                     r.kind = n.op == Op::Relu ? RegionKind::Relu : RegionKind::ReluAdjoint;
+                    r.in = n.inputs;
+                    r.out = n.id;
+                    r.covers = {n.id};
+                    claim(r);
+                    continue;
+                }
+                case Op::Compare: {
+                    const int code = compare_code(n.compare);
+                    if (code < 0 || n.inputs.size() != 2)
+                        return fail("node " + std::to_string(n.id) + ": Compare `" + n.compare + "` is not built");
+                    single(n, RegionKind::Compare, code);
+                    continue;
+                }
+                case Op::Logical: {
+                    const int code = n.compare == "and" ? CHELIS_LOGICAL_AND : n.compare == "or" ? CHELIS_LOGICAL_OR
+                                     : n.compare == "not" ? CHELIS_LOGICAL_NOT : -1;
+                    if (code < 0 || n.inputs.size() != (code == CHELIS_LOGICAL_NOT ? 1u : 2u))
+                        return fail("node " + std::to_string(n.id) + ": Logical `" + n.compare + "` is not built");
+                    single(n, RegionKind::Logical, code);
+                    continue;
+                }
+                case Op::Where:
+                    if (n.inputs.size() != 3)
+                        return fail("node " + std::to_string(n.id) + ": Where needs a condition and two branches");
+                    single(n, RegionKind::Where);
+                    continue;
+                case Op::Cast:
+                    if (n.inputs.size() != 1 || prim_width(n.cast_to) == 0 || n.cast_to == Prim::Key ||
+                        N(n.inputs[0]).prec == Prim::Key)
+                        return fail("node " + std::to_string(n.id) + ": a Cast this build has no conversion for");
+                    single(n, RegionKind::Cast);
+                    continue;
+                case Op::Gather: {
+                    if (n.inputs.size() != 2)
+                        return fail("node " + std::to_string(n.id) + ": Gather needs values and indices");
+                    Region r;
+                    r.kind = RegionKind::Gather;
+                    r.axis = n.axis;
+                    r.batch_rank = n.batch_rank;
                     r.in = n.inputs;
                     r.out = n.id;
                     r.covers = {n.id};

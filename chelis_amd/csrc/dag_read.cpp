@@ -42,6 +42,7 @@ const OpName kOps[] = {
     {"Expand", Op::Expand}, {"Permute", Op::Permute}, {"Reshape", Op::Reshape}, {"Realize", Op::Realize},
     {"Copy", Op::Copy}, {"FusedElem", Op::FusedElem}, {"BlasMatmul", Op::BlasMatmul},
     {"Store", Op::Store}, {"ExtentWitness", Op::ExtentWitness}, {"NamedCast", Op::NamedCast},
+    {"Logical", Op::Logical}, {"Mod", Op::Mod}, {"Gather", Op::Gather},
 };
 
 struct PrimName {
@@ -279,9 +280,13 @@ bool read_op(const Json &op, Graph *g, Node *n, std::string *why) {
             }
             return true;
         }
-        case Op::Compare:
-            if (p.kind != Json::String) return (*why = "Compare needs its kind", false);
+        case Op::Compare: case Op::Logical:
+            if (p.kind != Json::String) return (*why = var + " needs its kind", false);
             n->compare = p.text;
+            return true;
+        case Op::Gather:
+            if (!int_of(p.get("axis"), &n->axis) || !int_of(p.get("batch_rank"), &n->batch_rank))
+                return (*why = "Gather needs axis and batch_rank", false);
             return true;
         case Op::Cast:
             if (!prim_of(p.get("new_precision"), &n->cast_to)) return (*why = "Cast needs new_precision", false);

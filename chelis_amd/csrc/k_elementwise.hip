@@ -12,11 +12,10 @@
 // re-read through L2/MALL, not materialized.
 #include "chain.h"
 #include "narrow.h"
+#include "strided.h"
 
 namespace chelis {
 namespace {
-
-constexpr int kMaxRank = 4;
 
 struct Operand {
     const void *p;
@@ -25,10 +24,6 @@ struct Operand {
 struct Operands {
     int32_t n;
     Operand o[CHELIS_FUSED_MAX_INPUTS];
-};
-struct Shape {
-    int32_t rank;
-    int64_t ext[kMaxRank];
 };
 
 // The chain interpreter (run_chain, chain.h): one thread per element, the
@@ -435,46 +430,6 @@ __global__ __launch_bounds__(256) void unary_stream_kernel(const T *__restrict__
 
 
 // ---------------------------------------------------------------- host helpers
-// Collapse adjacent output axes wherever every operand's strides allow it
-// (stride[a] == stride[a+1] * ext[a+1]), dropping unit axes.
-bool collapse(const chelis_gpu_tensor *out, const chelis_gpu_tensor *const *ins, int n_in, Shape *sh,
-              int64_t (*st)[kMaxRank]) {
-    int64_t ext[16];
-    int64_t s[CHELIS_FUSED_MAX_INPUTS][16];
-    int r = 0;
-    for (int a = 0; a < out->rank; ++a) {
-        if (out->shape[a] == 1) continue;
-        ext[r] = out->shape[a];
-        // an extent-1 operand axis broadcasts: it never advances
-        for (int k = 0; k < n_in; ++k) s[k][r] = ins[k]->shape[a] == 1 ? 0 : ins[k]->strides[a];
-        ++r;
-    }
-    // merge from the innermost axis outward
-    int64_t mext[16];
-    int64_t ms[CHELIS_FUSED_MAX_INPUTS][16];
-    int m = 0;
-    for (int a = 0; a < r; ++a) {
-        if (m > 0) {
-            bool ok = true;
-            for (int k = 0; k < n_in && ok; ++k) ok = ms[k][m - 1] == s[k][a] * ext[a];
-            if (ok) {
-                mext[m - 1] *= ext[a];
-                for (int k = 0; k < n_in; ++k) ms[k][m - 1] = s[k][a];
-                continue;
-            }
-        }
-        mext[m] = ext[a];
-        for (int k = 0; k < n_in; ++k) ms[k][m] = s[k][a];
-        ++m;
-    }
-    if (m > kMaxRank) return false;
-    sh->rank = m;
-    for (int a = 0; a < m; ++a) sh->ext[a] = mext[a];
-    for (int k = 0; k < n_in; ++k)
-        for (int a = 0; a < kMaxRank; ++a) st[k][a] = a < m ? ms[k][a] : 0;
-    return true;
-}
-
 int32_t check_input_against(const chelis_gpu_tensor *in, const chelis_gpu_tensor *out, const char *name) {
     if (int32_t s = check_tensor(in, name)) return s;
     if (in->dtype != out->dtype) return set_error(CHELIS_HIP_EDOMAIN, "%s: dtype differs from the output", name);

@@ -1,0 +1,822 @@
+// Comparison, logical, where, checked casts, checked integer arithmetic and
+// gather on gfx950: the node kinds the reference HIP lane launches one
+// kernel each for beside its float chains (crates/chelis-backend-hip/src/
+// kernels.rs:1270-1346 comparison / logical / where, :1382 and
+// emit.rs:2413 casts, kernels.rs:769-866 and :1434 the trapping integer
+// kernels, :2557-2597 gather). Where the two reference lanes differ the C
+// lane's semantics hold: integer add and mul are checked as sub and abs are
+// (crates/chelis-numeric-core/src/dtype_semantics.rs:930-1030), and a cast
+// is [04-NUM-14]'s checked cast with the C lane's single roundings
+// (crates/chelis-backend-c/src/host_emit.rs:1700-2120).
+//
+// Every map is a grid-stride loop over the output's elements, one per lane
+// per step (coalesced), over operands collapsed to at most four strided
+// axes (stride 0 broadcasts). A failing element ([04-NUM-9]) stores zero
+// and contributes a record key: bits 63..42 the launch's sequence number,
+// 41..2 the element's row-major index, 1..0 the kind. The wave joins its
+// keys and one lane merges them into the device's record word with an
+// atomic max of the complement, so the word keeps the lowest key - the
+// earliest launch's lowest-index offender, [04-NUM-15] - and 0 means none.
+#include <algorithm>
+#include <limits>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "hip_common.h"
+#include "narrow.h"
+#include "strided.h"
+
+namespace chelis {
+namespace {
+
+enum : int { kOverflow = 1, kDomain = 2, kDivZero = 3 };
+
+// ---------------------------------------------------------------- element types
+template <int DT> struct Dt;
+template <> struct Dt<CHELIS_DTYPE_F32> { using S = float; static constexpr bool kFloat = true; };
+template <> struct Dt<CHELIS_DTYPE_F64> { using S = double; static constexpr bool kFloat = true; };
+template <> struct Dt<CHELIS_DTYPE_BF16> { using S = uint16_t; static constexpr bool kFloat = true; };
+template <> struct Dt<CHELIS_DTYPE_F16> { using S = uint16_t; static constexpr bool kFloat = true; };
+template <> struct Dt<CHELIS_DTYPE_I8> { using S = int8_t; static constexpr bool kFloat = false; };
+template <> struct Dt<CHELIS_DTYPE_I16> { using S = int16_t; static constexpr bool kFloat = false; };
+template <> struct Dt<CHELIS_DTYPE_I32> { using S = int32_t; static constexpr bool kFloat = false; };
+template <> struct Dt<CHELIS_DTYPE_I64> { using S = int64_t; static constexpr bool kFloat = false; };
+template <> struct Dt<CHELIS_DTYPE_BOOL> { using S = uint8_t; static constexpr bool kFloat = false; };
+
+// The value a comparison sees: bf16 / f16 decoded to binary32 (exact),
+// every other dtype its stored value (kernels.rs:1266-1268).
+template <int DT>
+__device__ inline auto semantic(typename Dt<DT>::S v) {
+    if constexpr (DT == CHELIS_DTYPE_BF16) return bf16_to_f32(v);
+    else if constexpr (DT == CHELIS_DTYPE_F16) return f16_to_f32(v);
+    else return v;
+}
+// A float element's exact value in binary64.
+template <int DT>
+__device__ inline double widen(typename Dt<DT>::S v) {
+    return (double)semantic<DT>(v);
+}
+
+// ---------------------------------------------------------------- operands
+struct Ops {
+    const void *p[3];
+    int64_t st[3][kMaxRank];
+};
+
+template <int N>
+__device__ inline void offsets(const Ops &o, const Shape &sh, int64_t idx, int64_t (&off)[N]) {
+    if (sh.rank <= 1) {
+#pragma unroll
+        for (int k = 0; k < N; ++k) off[k] = idx * o.st[k][0];
+        return;
+    }
+    int64_t coord[kMaxRank];
+    int64_t rem = idx;
+#pragma unroll
+    for (int a = kMaxRank - 1; a >= 0; --a) {
+        if (a < sh.rank) {
+            coord[a] = rem % sh.ext[a];
+            rem /= sh.ext[a];
+        } else {
+            coord[a] = 0;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        int64_t s = 0;
+#pragma unroll
+        for (int a = 0; a < kMaxRank; ++a) s += coord[a] * o.st[k][a];
+        off[k] = s;
+    }
+}
+
+__device__ inline unsigned long long fail_key(uint64_t seq, int64_t i, int kind) {
+    return ~(seq | ((uint64_t)i << 2) | (uint64_t)kind);
+}
+
+// Joins the wave's failure keys (0: none) and merges the largest into the
+// record word from one lane. Every lane of the wave calls it in the same
+// loop step (the loop bound is uniform).
+__device__ inline void merge_failures(unsigned long long k, unsigned long long *rec) {
+    if (!__any(k != 0ull)) return;
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        const unsigned long long o = __shfl_xor(k, m);
+        k = o > k ? o : k;
+    }
+    if ((threadIdx.x & 63) == 0) atomicMax(rec, k);
+}
+
+// One element per lane per step; the block's steps start at a uniform base
+// so a wave's lanes are always in the same step (lanes past the end take no
+// element and report no failure).
+template <class F>
+__global__ __launch_bounds__(256) void map_kernel(F f, Ops o, Shape sh, int64_t count, unsigned long long *rec) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t base = (int64_t)blockIdx.x * blockDim.x; base < count; base += stride) {
+        const int64_t i = base + threadIdx.x;
+        unsigned long long k = 0ull;
+        if (i < count) {
+            int64_t off[F::N];
+            offsets(o, sh, i, off);
+            k = f(i, o, off);
+        }
+        if constexpr (F::kTraps) merge_failures(k, rec);
+    }
+}
+
+// ---------------------------------------------------------------- comparison, logical, where
+template <typename V>
+__device__ inline bool compare_values(int kind, V x, V y) {
+    switch (kind) {
+        case CHELIS_CMP_CMPLT: case CHELIS_CMP_LT: return x < y;
+        case CHELIS_CMP_EQ: return x == y;
+        case CHELIS_CMP_NEQ: return x != y;
+        case CHELIS_CMP_GT: return x > y;
+        case CHELIS_CMP_GTE: return x >= y;
+        default: return x <= y;
+    }
+}
+
+template <int DT>
+struct CompareOp {
+    static constexpr int N = 2;
+    static constexpr bool kTraps = false;
+    int32_t kind;
+    uint8_t *out;
+    __device__ unsigned long long operator()(int64_t i, const Ops &o, const int64_t (&off)[2]) const {
+        using S = typename Dt<DT>::S;
+        const auto x = semantic<DT>(static_cast<const S *>(o.p[0])[off[0]]);
+        const auto y = semantic<DT>(static_cast<const S *>(o.p[1])[off[1]]);
+        out[i] = (uint8_t)compare_values(kind, x, y);
+        return 0ull;
+    }
+};
+
+// A Bool8 byte is true when nonzero (kernels.rs:1305-1335).
+struct LogicalOp {
+    static constexpr int N = 2;
+    static constexpr bool kTraps = false;
+    int32_t kind;
+    uint8_t *out;
+    __device__ unsigned long long operator()(int64_t i, const Ops &o, const int64_t (&off)[2]) const {
+        const uint8_t a = static_cast<const uint8_t *>(o.p[0])[off[0]];
+        const uint8_t b = static_cast<const uint8_t *>(o.p[1])[off[1]];
+        out[i] = (uint8_t)(kind == CHELIS_LOGICAL_AND ? (a != 0 && b != 0)
+                           : kind == CHELIS_LOGICAL_OR ? (a != 0 || b != 0) : a == 0);
+        return 0ull;
+    }
+};
+
+// [05-OP-53]: the selected operand's stored bits; the other is not read.
+template <typename U>
+struct WhereOp {
+    static constexpr int N = 3;
+    static constexpr bool kTraps = false;
+    U *out;
+    __device__ unsigned long long operator()(int64_t i, const Ops &o, const int64_t (&off)[3]) const {
+        const bool c = static_cast<const uint8_t *>(o.p[0])[off[0]] != 0;
+        out[i] = c ? static_cast<const U *>(o.p[1])[off[1]] : static_cast<const U *>(o.p[2])[off[2]];
+        return 0ull;
+    }
+};
+
+// ---------------------------------------------------------------- checked cast
+// Round-half-even right shift of a magnitude.
+__device__ inline uint64_t rshift_even(uint64_t v, int s) {
+    if (s <= 0) return v;
+    if (s >= 64) return 0;
+    const uint64_t q = v >> s, r = v & ((1ull << s) - 1ull), h = 1ull << (s - 1);
+    return (r > h || (r == h && (q & 1ull))) ? q + 1 : q;
+}
+// Sign, unbiased exponent of the leading bit and an (M+1)-bit rounded
+// significand packed into an IEEE layout with E exponent bits; a round-up
+// past M+1 bits carries into the exponent, overflow gives infinity.
+template <int E, int M, typename U>
+__device__ inline U pack_ieee(U sign, int e, uint64_t rounded) {
+    constexpr int bias = (1 << (E - 1)) - 1;
+    if (rounded == (1ull << (M + 1))) {
+        rounded >>= 1;
+        ++e;
+    }
+    if (e > bias) return (U)(sign | ((U)((1 << E) - 1) << M));
+    return (U)(sign | ((U)(e + bias) << M) | (U)(rounded & ((1ull << M) - 1ull)));
+}
+// An exact integer to an IEEE format with one rounding to nearest even.
+template <int E, int M, typename U>
+__device__ inline U int_to_ieee(int64_t v) {
+    const U sign = v < 0 ? (U)((U)1 << (E + M)) : (U)0;
+    const uint64_t mag = v < 0 ? (uint64_t)(-(v + 1)) + 1ull : (uint64_t)v;
+    if (!mag) return sign;
+    const int e = 63 - __builtin_clzll(mag);
+    constexpr int bias = (1 << (E - 1)) - 1;
+    if (e > bias) return (U)(sign | ((U)((1 << E) - 1) << M));
+    const uint64_t r = e > M ? rshift_even(mag, e - M) : mag << (M - e);
+    return pack_ieee<E, M, U>(sign, e, r);
+}
+// binary64 to a 16-bit IEEE format with one rounding to nearest even; NaN
+// to the format's canonical quiet NaN (host_emit.rs:1715-1755).
+template <int E, int M>
+__device__ inline uint16_t f64_to_ieee16(double v) {
+    const uint64_t bits = __builtin_bit_cast(uint64_t, v);
+    const uint16_t sign = (uint16_t)((bits >> 48) & 0x8000u);
+    const int se = (int)((bits >> 52) & 0x7ff);
+    const uint64_t man = bits & 0xfffffffffffffull;
+    constexpr int bias = (1 << (E - 1)) - 1;
+    constexpr uint16_t inf = (uint16_t)(((1 << E) - 1) << M);
+    if (se == 0x7ff) return man ? (uint16_t)(inf | (1u << (M - 1))) : (uint16_t)(sign | inf);
+    if (se == 0 && man == 0) return sign;
+    const int e = se ? se - 1023 : -1022;
+    const uint64_t sig = se ? (man | (1ull << 52)) : man;
+    if (se && e > bias) return (uint16_t)(sign | inf);
+    if (se && e >= 1 - bias) return pack_ieee<E, M, uint16_t>(sign, e, rshift_even(sig, 52 - M));
+    // below the normal range: quantum 2^(1 - bias - M); a carry into the
+    // leading position is the smallest normal's encoding
+    return (uint16_t)(sign | (uint16_t)rshift_even(sig, (52 - M) + ((1 - bias) - e)));
+}
+
+template <int DT> constexpr int64_t int_min() {
+    return DT == CHELIS_DTYPE_I8 ? -128 : DT == CHELIS_DTYPE_I16 ? -32768 : DT == CHELIS_DTYPE_I32 ? -2147483648LL
+                                                                          : (-9223372036854775807LL - 1);
+}
+template <int DT> constexpr int64_t int_max() {
+    return DT == CHELIS_DTYPE_I8 ? 127 : DT == CHELIS_DTYPE_I16 ? 32767 : DT == CHELIS_DTYPE_I32 ? 2147483647LL
+                                                                        : 9223372036854775807LL;
+}
+
+// [04-NUM-14] for one element: the failure kind, or 0 with *r set.
+template <int SRC, int DST>
+__device__ inline int cast_one(typename Dt<SRC>::S v, typename Dt<DST>::S *r) {
+    using D = typename Dt<DST>::S;
+    if constexpr (SRC == DST) {
+        *r = v;  // identity keeps the stored bits
+    } else if constexpr (Dt<SRC>::kFloat) {
+        const double x = widen<SRC>(v);
+        if constexpr (DST == CHELIS_DTYPE_F64) {
+            *r = x != x ? __builtin_bit_cast(double, 0x7ff8000000000000ull) : x;
+        } else if constexpr (DST == CHELIS_DTYPE_F32) {
+            const float f = (float)x;
+            *r = f != f ? __builtin_bit_cast(float, 0x7fc00000u) : f;
+        } else if constexpr (DST == CHELIS_DTYPE_BF16) {
+            *r = f64_to_ieee16<8, 7>(x);
+        } else if constexpr (DST == CHELIS_DTYPE_F16) {
+            *r = f64_to_ieee16<5, 10>(x);
+        } else if constexpr (DST == CHELIS_DTYPE_BOOL) {
+            if (!__builtin_isfinite(x) || (x != 0.0 && x != 1.0)) return kDomain;
+            *r = (D)(x == 1.0);
+        } else {
+            if (!__builtin_isfinite(x) || __builtin_trunc(x) != x) return kDomain;
+            if (DST == CHELIS_DTYPE_I64 ? (x < -9223372036854775808.0 || x >= 9223372036854775808.0)
+                                        : (x < (double)int_min<DST>() || x > (double)int_max<DST>()))
+                return kOverflow;
+            *r = (D)(int64_t)x;
+        }
+    } else {
+        const int64_t x = (int64_t)v;
+        if constexpr (DST == CHELIS_DTYPE_F64) {
+            *r = __builtin_bit_cast(double, int_to_ieee<11, 52, uint64_t>(x));
+        } else if constexpr (DST == CHELIS_DTYPE_F32) {
+            *r = __builtin_bit_cast(float, int_to_ieee<8, 23, uint32_t>(x));
+        } else if constexpr (DST == CHELIS_DTYPE_BF16) {
+            *r = int_to_ieee<8, 7, uint16_t>(x);
+        } else if constexpr (DST == CHELIS_DTYPE_F16) {
+            *r = int_to_ieee<5, 10, uint16_t>(x);
+        } else if constexpr (DST == CHELIS_DTYPE_BOOL) {
+            if (x != 0 && x != 1) return kDomain;
+            *r = (D)(x == 1);
+        } else {
+            if (x < int_min<DST>() || x > int_max<DST>()) return kOverflow;
+            *r = (D)x;
+        }
+    }
+    return 0;
+}
+
+template <int SRC, int DST>
+struct CastOp {
+    static constexpr int N = 1;
+    static constexpr bool kTraps = true;
+    typename Dt<DST>::S *out;
+    uint64_t seq;
+    __device__ unsigned long long operator()(int64_t i, const Ops &o, const int64_t (&off)[1]) const {
+        using S = typename Dt<SRC>::S;
+        using D = typename Dt<DST>::S;
+        D r{};
+        const int kind = cast_one<SRC, DST>(static_cast<const S *>(o.p[0])[off[0]], &r);
+        out[i] = kind ? D{} : r;
+        return kind ? fail_key(seq, i, kind) : 0ull;
+    }
+};
+
+// ---------------------------------------------------------------- checked integer arithmetic
+template <typename T>
+__device__ inline int int_binary(int op, T x, T z, T *r) {
+    constexpr T lo = std::numeric_limits<T>::min();
+    switch (op) {
+        case CHELIS_INT_ADD: return __builtin_add_overflow(x, z, r) ? kOverflow : 0;
+        case CHELIS_INT_SUB: return __builtin_sub_overflow(x, z, r) ? kOverflow : 0;
+        case CHELIS_INT_MUL: return __builtin_mul_overflow(x, z, r) ? kOverflow : 0;
+        case CHELIS_INT_FLOOR_DIV: case CHELIS_INT_TRUNC_DIV: case CHELIS_INT_MOD: {
+            if (z == 0) return kDivZero;
+            if (op == CHELIS_INT_MOD) {
+                *r = z == (T)-1 ? (T)0 : (T)(x % z);
+                return 0;
+            }
+            if (x == lo && z == (T)-1) return kOverflow;
+            T q = (T)(x / z);
+            const T m = (T)(x % z);
+            if (op == CHELIS_INT_FLOOR_DIV && m != 0 && ((m < 0) != (z < 0))) q = (T)(q - 1);
+            *r = q;
+            return 0;
+        }
+        case CHELIS_INT_MAX_ELEM: *r = x > z ? x : z; return 0;
+        default: *r = x < z ? x : z; return 0;
+    }
+}
+
+template <typename T>
+struct IntBinaryOp {
+    static constexpr int N = 2;
+    static constexpr bool kTraps = true;
+    int32_t op;
+    T *out;
+    uint64_t seq;
+    __device__ unsigned long long operator()(int64_t i, const Ops &o, const int64_t (&off)[2]) const {
+        T r = 0;
+        const int kind = int_binary<T>(op, static_cast<const T *>(o.p[0])[off[0]],
+                                       static_cast<const T *>(o.p[1])[off[1]], &r);
+        out[i] = kind ? (T)0 : r;
+        return kind ? fail_key(seq, i, kind) : 0ull;
+    }
+};
+
+template <typename T>
+struct IntUnaryOp {
+    static constexpr int N = 1;
+    static constexpr bool kTraps = true;
+    int32_t op;
+    T *out;
+    uint64_t seq;
+    __device__ unsigned long long operator()(int64_t i, const Ops &o, const int64_t (&off)[1]) const {
+        constexpr T lo = std::numeric_limits<T>::min();
+        const T x = static_cast<const T *>(o.p[0])[off[0]];
+        if (x == lo) {
+            out[i] = 0;
+            return fail_key(seq, i, kOverflow);
+        }
+        out[i] = (op == CHELIS_INT_NEG || x < 0) ? (T)-x : x;
+        return 0ull;
+    }
+};
+
+// ---------------------------------------------------------------- gather
+// A view's element at a row-major logical index (chelis_logical_offset).
+struct View8 {
+    int32_t rank;
+    int32_t dense;
+    int64_t shape[8], strides[8];
+};
+__device__ inline int64_t logical_offset(const View8 &v, int64_t i) {
+    if (v.dense) return i;
+    int64_t off = 0;
+#pragma unroll
+    for (int a = 7; a >= 0; --a) {
+        if (a < v.rank) {
+            off += (i % v.shape[a]) * v.strides[a];
+            i /= v.shape[a];
+        }
+    }
+    return off;
+}
+struct GatherGeom {
+    int64_t axis_size, after, index_count, outer_per_batch, total;
+};
+// emit.rs:3807-3842 / kernels.rs:2557-2597: result element (b, j, d) of
+// [before, index_count, after] reads values (b, g, d), g the index at
+// (batch of b, j); an index outside [0, axis_size) fails (domain).
+template <typename U, typename I>
+__global__ __launch_bounds__(256) void gather_kernel(const U *__restrict__ values, View8 vv,
+                                                     const I *__restrict__ idx, View8 iv, U *__restrict__ out,
+                                                     GatherGeom g, uint64_t seq, unsigned long long *rec) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t base = (int64_t)blockIdx.x * blockDim.x; base < g.total; base += stride) {
+        const int64_t i = base + threadIdx.x;
+        unsigned long long k = 0ull;
+        if (i < g.total) {
+            const int64_t d = i % g.after, t = i / g.after;
+            const int64_t j = t % g.index_count, b = t / g.index_count;
+            const int64_t pos = (b / g.outer_per_batch) * g.index_count + j;
+            const int64_t x = (int64_t)idx[logical_offset(iv, pos)];
+            if (x < 0 || x >= g.axis_size) {
+                out[i] = U{};
+                k = fail_key(seq, i, kDomain);
+            } else {
+                out[i] = values[logical_offset(vv, (b * g.axis_size + x) * g.after + d)];
+            }
+        }
+        merge_failures(k, rec);
+    }
+}
+
+// ---------------------------------------------------------------- host: the failure channel
+// Per device: word [2..3] of the status words is the deferred record, [4..5]
+// the record of a call that waits for its own result. A deferred launch's
+// sequence number indexes the label ("add at i64") its message names.
+constexpr int kMaxDevices = 64;
+constexpr int kSeqShift = 42;
+constexpr uint64_t kSeqMax = (1ull << (64 - kSeqShift)) - 1;
+std::mutex g_fail_mutex;
+std::vector<std::string> g_labels[kMaxDevices];
+
+struct Sink {
+    unsigned long long *rec = nullptr;
+    uint64_t seq = 0;
+    bool wait = false;
+};
+
+const char *dtype_name(chelis_dtype d) {
+    switch (d) {
+        case CHELIS_DTYPE_F32: return "f32";
+        case CHELIS_DTYPE_F64: return "f64";
+        case CHELIS_DTYPE_I32: return "i32";
+        case CHELIS_DTYPE_BOOL: return "bool";
+        case CHELIS_DTYPE_I64: return "i64";
+        case CHELIS_DTYPE_BF16: return "bf16";
+        case CHELIS_DTYPE_F16: return "f16";
+        case CHELIS_DTYPE_I8: return "i8";
+        case CHELIS_DTYPE_I16: return "i16";
+        default: return "key";
+    }
+}
+const char *kind_text(int kind) {
+    return kind == kOverflow ? "overflow" : kind == kDomain ? "domain" : "division by zero";
+}
+
+// The sink a trapping launch records into: its own word when the caller
+// waits for the result (failure != NULL), else the deferred word under the
+// next sequence number, labelled "<op> at <prim>".
+int32_t open_sink(bool wait, const std::string &label, Sink *s) {
+    int32_t *words = status_words(nullptr);
+    if (!words) return set_error(CHELIS_HIP_EHIP, "no HIP device status words");
+    s->wait = wait;
+    if (wait) {
+        s->rec = reinterpret_cast<unsigned long long *>(words + 4);
+        s->seq = 0;
+        return CHELIS_HIP_OK;
+    }
+    int device = 0;
+    CHELIS_HIP_TRY(hipGetDevice(&device));
+    std::lock_guard<std::mutex> lock(g_fail_mutex);
+    std::vector<std::string> &labels = g_labels[device];
+    const uint64_t seq = std::min<uint64_t>(labels.size(), kSeqMax);
+    if (labels.size() <= kSeqMax) labels.push_back(label);
+    s->rec = reinterpret_cast<unsigned long long *>(words + 2);
+    s->seq = seq << kSeqShift;
+    return CHELIS_HIP_OK;
+}
+
+void fill_failure(chelis_hip_numeric_failure *f, unsigned long long word, const std::string &label) {
+    f->index = -1;
+    f->kind = 0;
+    f->reserved = 0;
+    f->message[0] = 0;
+    if (!word) return;
+    const uint64_t key = ~word;
+    f->kind = (int32_t)(key & 3u);
+    f->index = (int64_t)((key >> 2) & ((1ull << (kSeqShift - 2)) - 1));
+    snprintf(f->message, sizeof f->message, "numeric trap: %s in %s", kind_text(f->kind), label.c_str());
+}
+
+// Reads and clears a record word (the stream is idle).
+int32_t take_word(unsigned long long *rec, unsigned long long *word) {
+    CHELIS_HIP_TRY(hipMemcpy(word, rec, sizeof *word, hipMemcpyDeviceToHost));
+    if (*word) {
+        const unsigned long long zero = 0ull;
+        CHELIS_HIP_TRY(hipMemcpy(rec, &zero, sizeof zero, hipMemcpyHostToDevice));
+    }
+    return CHELIS_HIP_OK;
+}
+
+// After the launch of a waiting call: its record, read and cleared.
+int32_t close_sink(const Sink &s, const std::string &label, chelis_hip_numeric_failure *f) {
+    if (!s.wait) return CHELIS_HIP_OK;
+    CHELIS_HIP_TRY(hipStreamSynchronize(stream()));
+    unsigned long long word = 0ull;
+    if (int32_t st = take_word(s.rec, &word)) return st;
+    fill_failure(f, word, label);
+    return CHELIS_HIP_OK;
+}
+
+// ---------------------------------------------------------------- host: checks and launches
+int32_t check_broadcast(const chelis_gpu_tensor *in, const chelis_gpu_tensor *out, const char *what,
+                        const char *name) {
+    if (int32_t s = check_tensor(in, name)) return s;
+    if (in->rank != out->rank) return set_error(CHELIS_HIP_EDOMAIN, "%s: %s rank differs from the output", what, name);
+    for (int32_t a = 0; a < in->rank; ++a)
+        if (in->shape[a] != out->shape[a] && in->shape[a] != 1)
+            return set_error(CHELIS_HIP_EDOMAIN, "%s: %s axis %d neither matches nor broadcasts", what, name, a);
+    return CHELIS_HIP_OK;
+}
+
+int32_t check_out(const chelis_gpu_tensor *out, const char *what) {
+    if (int32_t s = check_tensor(out, "out")) return s;
+    if (!is_contiguous(out)) return set_error(CHELIS_HIP_EUNSUPPORTED, "%s: the output must be contiguous", what);
+    return CHELIS_HIP_OK;
+}
+
+int64_t map_blocks(int64_t count) { return std::max<int64_t>(1, std::min<int64_t>((count + 255) / 256, 65536)); }
+
+template <class F>
+int32_t launch_map(const F &f, const chelis_gpu_tensor *const *ins, int n, const chelis_gpu_tensor *out,
+                   unsigned long long *rec, const char *what) {
+    hipStream_t st = stream();
+    if (!st) return set_error(CHELIS_HIP_EHIP, "no HIP device");
+    if (!out->count) return CHELIS_HIP_OK;
+    Shape sh;
+    int64_t s[CHELIS_FUSED_MAX_INPUTS][kMaxRank] = {};
+    if (!collapse(out, ins, n, &sh, s))
+        return set_error(CHELIS_HIP_EUNSUPPORTED, "%s: more than %d independent axes", what, kMaxRank);
+    Ops o{};
+    for (int k = 0; k < n; ++k) {
+        o.p[k] = ins[k]->data;
+        for (int a = 0; a < kMaxRank; ++a) o.st[k][a] = s[k][a];
+    }
+    map_kernel<F><<<dim3((unsigned)map_blocks(out->count)), dim3(256), 0, st>>>(f, o, sh, out->count, rec);
+    CHELIS_LAUNCH_CHECK();
+    return CHELIS_HIP_OK;
+}
+
+template <int DT>
+int32_t launch_compare(int32_t kind, const chelis_gpu_tensor *a, const chelis_gpu_tensor *b,
+                       const chelis_gpu_tensor *out) {
+    const chelis_gpu_tensor *ins[2] = {a, b};
+    return launch_map(CompareOp<DT>{kind, static_cast<uint8_t *>(out->data)}, ins, 2, out, nullptr, "compare");
+}
+
+template <int SRC, int DST>
+int32_t launch_cast(const chelis_gpu_tensor *x, const chelis_gpu_tensor *out, const Sink &s) {
+    const chelis_gpu_tensor *ins[1] = {x};
+    return launch_map(CastOp<SRC, DST>{static_cast<typename Dt<DST>::S *>(out->data), s.seq}, ins, 1, out, s.rec,
+                      "cast");
+}
+
+template <int SRC>
+int32_t cast_to(chelis_dtype dst, const chelis_gpu_tensor *x, const chelis_gpu_tensor *out, const Sink &s) {
+    switch (dst) {
+        case CHELIS_DTYPE_F32: return launch_cast<SRC, CHELIS_DTYPE_F32>(x, out, s);
+        case CHELIS_DTYPE_F64: return launch_cast<SRC, CHELIS_DTYPE_F64>(x, out, s);
+        case CHELIS_DTYPE_BF16: return launch_cast<SRC, CHELIS_DTYPE_BF16>(x, out, s);
+        case CHELIS_DTYPE_F16: return launch_cast<SRC, CHELIS_DTYPE_F16>(x, out, s);
+        case CHELIS_DTYPE_I8: return launch_cast<SRC, CHELIS_DTYPE_I8>(x, out, s);
+        case CHELIS_DTYPE_I16: return launch_cast<SRC, CHELIS_DTYPE_I16>(x, out, s);
+        case CHELIS_DTYPE_I32: return launch_cast<SRC, CHELIS_DTYPE_I32>(x, out, s);
+        case CHELIS_DTYPE_I64: return launch_cast<SRC, CHELIS_DTYPE_I64>(x, out, s);
+        case CHELIS_DTYPE_BOOL: return launch_cast<SRC, CHELIS_DTYPE_BOOL>(x, out, s);
+        default: return set_error(CHELIS_HIP_EUNSUPPORTED, "cast: no target dtype %d", (int)dst);
+    }
+}
+
+bool is_int(chelis_dtype d) {
+    return d == CHELIS_DTYPE_I8 || d == CHELIS_DTYPE_I16 || d == CHELIS_DTYPE_I32 || d == CHELIS_DTYPE_I64;
+}
+bool is_castable(chelis_dtype d) { return is_int(d) || is_float(d) || is_narrow16(d) || d == CHELIS_DTYPE_BOOL; }
+
+template <typename T>
+int32_t launch_int(int32_t op, const chelis_gpu_tensor *a, const chelis_gpu_tensor *b, const chelis_gpu_tensor *out,
+                   const Sink &s) {
+    T *o = static_cast<T *>(out->data);
+    if (op == CHELIS_INT_NEG || op == CHELIS_INT_ABS) {
+        const chelis_gpu_tensor *ins[1] = {a};
+        return launch_map(IntUnaryOp<T>{op, o, s.seq}, ins, 1, out, s.rec, "integer_elementwise");
+    }
+    const chelis_gpu_tensor *ins[2] = {a, b};
+    return launch_map(IntBinaryOp<T>{op, o, s.seq}, ins, 2, out, s.rec, "integer_elementwise");
+}
+
+const char *int_op_name(int32_t op) {
+    static const char *names[] = {"add", "sub", "mul", "floor_div", "trunc_div", "mod",
+                                  "max_elem", "min_elem", "neg", "abs"};
+    return op >= 0 && op <= CHELIS_INT_ABS ? names[op] : "?";
+}
+
+View8 view_of(const chelis_gpu_tensor *t) {
+    View8 v{};
+    v.rank = t->rank;
+    v.dense = is_contiguous(t) ? 1 : 0;
+    for (int32_t a = 0; a < t->rank; ++a) {
+        v.shape[a] = t->shape[a];
+        v.strides[a] = t->strides[a];
+    }
+    return v;
+}
+
+template <typename U>
+int32_t launch_gather(const chelis_gpu_tensor *values, const chelis_gpu_tensor *indices, const chelis_gpu_tensor *out,
+                      const GatherGeom &g, const Sink &s) {
+    hipStream_t st = stream();
+    if (!st) return set_error(CHELIS_HIP_EHIP, "no HIP device");
+    if (!g.total) return CHELIS_HIP_OK;
+    const unsigned blocks = (unsigned)map_blocks(g.total);
+    if (indices->dtype == CHELIS_DTYPE_I32)
+        gather_kernel<U, int32_t><<<dim3(blocks), dim3(256), 0, st>>>(
+            static_cast<const U *>(values->data), view_of(values), static_cast<const int32_t *>(indices->data),
+            view_of(indices), static_cast<U *>(out->data), g, s.seq, s.rec);
+    else
+        gather_kernel<U, int64_t><<<dim3(blocks), dim3(256), 0, st>>>(
+            static_cast<const U *>(values->data), view_of(values), static_cast<const int64_t *>(indices->data),
+            view_of(indices), static_cast<U *>(out->data), g, s.seq, s.rec);
+    CHELIS_LAUNCH_CHECK();
+    return CHELIS_HIP_OK;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- C ABI
+extern "C" int32_t chelis_hip_compare(int32_t kind, const chelis_gpu_tensor *a, const chelis_gpu_tensor *b,
+                                      const chelis_gpu_tensor *out) {
+    if (int32_t s = check_out(out, "compare")) return s;
+    if (out->dtype != CHELIS_DTYPE_BOOL) return set_error(CHELIS_HIP_EDOMAIN, "compare: the output must be bool");
+    if (kind < CHELIS_CMP_CMPLT || kind > CHELIS_CMP_LTE)
+        return set_error(CHELIS_HIP_EDOMAIN, "compare: unknown kind %d", kind);
+    if (int32_t s = check_broadcast(a, out, "compare", "a")) return s;
+    if (int32_t s = check_broadcast(b, out, "compare", "b")) return s;
+    if (a->dtype != b->dtype) return set_error(CHELIS_HIP_EDOMAIN, "compare: operand dtypes differ");
+    switch (a->dtype) {
+        case CHELIS_DTYPE_F32: return launch_compare<CHELIS_DTYPE_F32>(kind, a, b, out);
+        case CHELIS_DTYPE_F64: return launch_compare<CHELIS_DTYPE_F64>(kind, a, b, out);
+        case CHELIS_DTYPE_BF16: return launch_compare<CHELIS_DTYPE_BF16>(kind, a, b, out);
+        case CHELIS_DTYPE_F16: return launch_compare<CHELIS_DTYPE_F16>(kind, a, b, out);
+        case CHELIS_DTYPE_I8: return launch_compare<CHELIS_DTYPE_I8>(kind, a, b, out);
+        case CHELIS_DTYPE_I16: return launch_compare<CHELIS_DTYPE_I16>(kind, a, b, out);
+        case CHELIS_DTYPE_I32: return launch_compare<CHELIS_DTYPE_I32>(kind, a, b, out);
+        case CHELIS_DTYPE_I64: return launch_compare<CHELIS_DTYPE_I64>(kind, a, b, out);
+        case CHELIS_DTYPE_BOOL:
+            if (kind != CHELIS_CMP_EQ && kind != CHELIS_CMP_NEQ)
+                return set_error(CHELIS_HIP_EDOMAIN, "compare: bool admits eq and neq only");
+            return launch_compare<CHELIS_DTYPE_BOOL>(kind, a, b, out);
+        default: return set_error(CHELIS_HIP_EUNSUPPORTED, "compare: no dtype %d", (int)a->dtype);
+    }
+}
+
+extern "C" int32_t chelis_hip_logical(int32_t kind, const chelis_gpu_tensor *a, const chelis_gpu_tensor *b,
+                                      const chelis_gpu_tensor *out) {
+    if (int32_t s = check_out(out, "logical")) return s;
+    if (kind < CHELIS_LOGICAL_AND || kind > CHELIS_LOGICAL_NOT)
+        return set_error(CHELIS_HIP_EDOMAIN, "logical: unknown kind %d", kind);
+    if (kind == CHELIS_LOGICAL_NOT) b = a;
+    if (int32_t s = check_broadcast(a, out, "logical", "a")) return s;
+    if (int32_t s = check_broadcast(b, out, "logical", "b")) return s;
+    if (a->dtype != CHELIS_DTYPE_BOOL || b->dtype != CHELIS_DTYPE_BOOL || out->dtype != CHELIS_DTYPE_BOOL)
+        return set_error(CHELIS_HIP_EDOMAIN, "logical: operands and output must be bool");
+    const chelis_gpu_tensor *ins[2] = {a, b};
+    return launch_map(LogicalOp{kind, static_cast<uint8_t *>(out->data)}, ins, 2, out, nullptr, "logical");
+}
+
+extern "C" int32_t chelis_hip_where(const chelis_gpu_tensor *cond, const chelis_gpu_tensor *a,
+                                    const chelis_gpu_tensor *b, const chelis_gpu_tensor *out) {
+    if (int32_t s = check_out(out, "where")) return s;
+    if (int32_t s = check_broadcast(cond, out, "where", "cond")) return s;
+    if (int32_t s = check_broadcast(a, out, "where", "a")) return s;
+    if (int32_t s = check_broadcast(b, out, "where", "b")) return s;
+    if (cond->dtype != CHELIS_DTYPE_BOOL) return set_error(CHELIS_HIP_EDOMAIN, "where: the condition must be bool");
+    if (a->dtype != out->dtype || b->dtype != out->dtype)
+        return set_error(CHELIS_HIP_EDOMAIN, "where: branch dtypes differ from the output");
+    const chelis_gpu_tensor *ins[3] = {cond, a, b};
+    switch (dtype_width(out->dtype)) {
+        case 1: return launch_map(WhereOp<uint8_t>{static_cast<uint8_t *>(out->data)}, ins, 3, out, nullptr, "where");
+        case 2: return launch_map(WhereOp<uint16_t>{static_cast<uint16_t *>(out->data)}, ins, 3, out, nullptr, "where");
+        case 4: return launch_map(WhereOp<uint32_t>{static_cast<uint32_t *>(out->data)}, ins, 3, out, nullptr, "where");
+        default:
+            return launch_map(WhereOp<uint64_t>{static_cast<uint64_t *>(out->data)}, ins, 3, out, nullptr, "where");
+    }
+}
+
+extern "C" int32_t chelis_hip_cast(const chelis_gpu_tensor *x, const chelis_gpu_tensor *out,
+                                   chelis_hip_numeric_failure *failure) {
+    if (int32_t s = check_out(out, "cast")) return s;
+    if (int32_t s = check_broadcast(x, out, "cast", "x")) return s;
+    if (!is_castable(x->dtype) || !is_castable(out->dtype))
+        return set_error(CHELIS_HIP_EUNSUPPORTED, "cast: no cast from dtype %d to %d", (int)x->dtype,
+                         (int)out->dtype);
+    const std::string label = std::string("cast at ") + dtype_name(out->dtype);
+    Sink sink;
+    if (int32_t s = open_sink(failure != nullptr, label, &sink)) return s;
+    int32_t st;
+    switch (x->dtype) {
+        case CHELIS_DTYPE_F32: st = cast_to<CHELIS_DTYPE_F32>(out->dtype, x, out, sink); break;
+        case CHELIS_DTYPE_F64: st = cast_to<CHELIS_DTYPE_F64>(out->dtype, x, out, sink); break;
+        case CHELIS_DTYPE_BF16: st = cast_to<CHELIS_DTYPE_BF16>(out->dtype, x, out, sink); break;
+        case CHELIS_DTYPE_F16: st = cast_to<CHELIS_DTYPE_F16>(out->dtype, x, out, sink); break;
+        case CHELIS_DTYPE_I8: st = cast_to<CHELIS_DTYPE_I8>(out->dtype, x, out, sink); break;
+        case CHELIS_DTYPE_I16: st = cast_to<CHELIS_DTYPE_I16>(out->dtype, x, out, sink); break;
+        case CHELIS_DTYPE_I32: st = cast_to<CHELIS_DTYPE_I32>(out->dtype, x, out, sink); break;
+        case CHELIS_DTYPE_I64: st = cast_to<CHELIS_DTYPE_I64>(out->dtype, x, out, sink); break;
+        default: st = cast_to<CHELIS_DTYPE_BOOL>(out->dtype, x, out, sink); break;
+    }
+    if (st) return st;
+    return close_sink(sink, label, failure);
+}
+
+extern "C" int32_t chelis_hip_integer_elementwise(int32_t op, const chelis_gpu_tensor *a, const chelis_gpu_tensor *b,
+                                                  const chelis_gpu_tensor *out, chelis_hip_numeric_failure *failure) {
+    if (op < CHELIS_INT_ADD || op > CHELIS_INT_ABS)
+        return set_error(CHELIS_HIP_EDOMAIN, "integer_elementwise: unknown op %d", op);
+    const bool unary = op == CHELIS_INT_NEG || op == CHELIS_INT_ABS;
+    if (int32_t s = check_out(out, "integer_elementwise")) return s;
+    if (int32_t s = check_broadcast(a, out, "integer_elementwise", "a")) return s;
+    if (!unary) {
+        if (int32_t s = check_broadcast(b, out, "integer_elementwise", "b")) return s;
+        if (b->dtype != out->dtype) return set_error(CHELIS_HIP_EDOMAIN, "integer_elementwise: b's dtype differs");
+    }
+    if (a->dtype != out->dtype) return set_error(CHELIS_HIP_EDOMAIN, "integer_elementwise: a's dtype differs");
+    if (!is_int(out->dtype))
+        return set_error(CHELIS_HIP_EDOMAIN, "integer_elementwise: i8, i16, i32 or i64 operands only");
+    const std::string label = std::string(int_op_name(op)) + " at " + dtype_name(out->dtype);
+    Sink sink;
+    if (int32_t s = open_sink(failure != nullptr, label, &sink)) return s;
+    int32_t st;
+    switch (out->dtype) {
+        case CHELIS_DTYPE_I8: st = launch_int<int8_t>(op, a, b, out, sink); break;
+        case CHELIS_DTYPE_I16: st = launch_int<int16_t>(op, a, b, out, sink); break;
+        case CHELIS_DTYPE_I32: st = launch_int<int32_t>(op, a, b, out, sink); break;
+        default: st = launch_int<int64_t>(op, a, b, out, sink); break;
+    }
+    if (st) return st;
+    return close_sink(sink, label, failure);
+}
+
+extern "C" int32_t chelis_hip_gather(const chelis_gpu_tensor *values, const chelis_gpu_tensor *indices, int32_t axis,
+                                     int32_t batch_rank, const chelis_gpu_tensor *out,
+                                     chelis_hip_numeric_failure *failure) {
+    if (int32_t s = check_tensor(values, "values")) return s;
+    if (int32_t s = check_tensor(indices, "indices")) return s;
+    if (int32_t s = check_out(out, "gather")) return s;
+    if (indices->dtype != CHELIS_DTYPE_I32 && indices->dtype != CHELIS_DTYPE_I64)
+        return set_error(CHELIS_HIP_EDOMAIN, "gather: indices must be i32 or i64");
+    if (out->dtype != values->dtype) return set_error(CHELIS_HIP_EDOMAIN, "gather: output dtype differs from values");
+    if (axis < 0 || axis >= values->rank || batch_rank < 0 || batch_rank > axis || batch_rank > indices->rank)
+        return set_error(CHELIS_HIP_EDOMAIN, "gather: axis %d / batch_rank %d outside the operands", axis, batch_rank);
+    // the result is values[..axis] ++ indices[batch_rank..] ++ values[axis+1..]
+    const int32_t want_rank = values->rank - 1 + indices->rank - batch_rank;
+    bool shape_ok = out->rank == want_rank;
+    for (int32_t a = 0, k = 0; shape_ok && a < values->rank; ++a) {
+        if (a == axis) {
+            for (int32_t q = batch_rank; q < indices->rank && shape_ok; ++q) shape_ok = out->shape[k++] == indices->shape[q];
+        } else {
+            shape_ok = out->shape[k++] == values->shape[a];
+        }
+    }
+    if (!shape_ok) return set_error(CHELIS_HIP_EDOMAIN, "gather: output shape is not the gathered shape");
+    // emit.rs:3829-3841: paired batch axes must agree (a domain trap)
+    int64_t batch = 1, before = 1, after = 1;
+    for (int32_t a = 0; a < batch_rank; ++a) {
+        if (values->shape[a] != indices->shape[a])
+            return set_error(CHELIS_HIP_EDOMAIN, "numeric trap: domain in gather at i64");
+        batch *= values->shape[a];
+    }
+    for (int32_t a = 0; a < axis; ++a) before *= values->shape[a];
+    for (int32_t a = axis + 1; a < values->rank; ++a) after *= values->shape[a];
+    GatherGeom g{};
+    g.axis_size = values->shape[axis];
+    g.after = after;
+    g.index_count = batch == 0 ? 0 : indices->count / batch;
+    g.outer_per_batch = (batch == 0 || before == 0) ? 1 : before / batch;
+    g.total = out->count;
+    if (g.total && (g.after == 0 || g.index_count == 0)) g.total = 0;  // no element to read
+    const std::string label = "gather at i64";
+    Sink sink;
+    if (int32_t s = open_sink(failure != nullptr, label, &sink)) return s;
+    int32_t st;
+    switch (dtype_width(values->dtype)) {
+        case 1: st = launch_gather<uint8_t>(values, indices, out, g, sink); break;
+        case 2: st = launch_gather<uint16_t>(values, indices, out, g, sink); break;
+        case 4: st = launch_gather<uint32_t>(values, indices, out, g, sink); break;
+        default: st = launch_gather<uint64_t>(values, indices, out, g, sink); break;
+    }
+    if (st) return st;
+    return close_sink(sink, label, failure);
+}
+
+extern "C" int32_t chelis_hip_take_numeric_failure(chelis_hip_numeric_failure *failure) {
+    if (!failure) return set_error(CHELIS_HIP_EDOMAIN, "take_numeric_failure: null record");
+    int32_t *words = status_words(nullptr);
+    if (!words) return set_error(CHELIS_HIP_EHIP, "no HIP device status words");
+    CHELIS_HIP_TRY(hipStreamSynchronize(stream()));
+    unsigned long long word = 0ull;
+    if (int32_t s = take_word(reinterpret_cast<unsigned long long *>(words + 2), &word)) return s;
+    int device = 0;
+    CHELIS_HIP_TRY(hipGetDevice(&device));
+    std::string label;
+    {
+        std::lock_guard<std::mutex> lock(g_fail_mutex);
+        std::vector<std::string> &labels = g_labels[device];
+        const uint64_t seq = word ? (~word) >> kSeqShift : 0;
+        if (word && seq < labels.size()) label = labels[seq];
+        labels.clear();
+    }
+    fill_failure(failure, word, label);
+    return CHELIS_HIP_OK;
+}
+
+}  // namespace chelis

@@ -166,6 +166,89 @@ int32_t chelis_hip_count(const chelis_gpu_tensor *x, int32_t axis, const chelis_
  * once, after its last launch. */
 int32_t chelis_hip_trap_status(int32_t *code);
 
+/* ---- comparison, logical, where ----
+ * One launch per node, as the reference HIP lane's kernels: comparison
+ * (kernels.rs:1266-1300) of two operands of one dtype to Bool8 - IEEE
+ * comparison of the semantic values for f32 / f64 / bf16 / f16 (any NaN
+ * false, neq true; signed zeros equal), exact order for i8..i64, eq / neq
+ * only for bool ([05-OP-36]); logical and / or / not on Bool8 bytes, a byte
+ * true when nonzero (kernels.rs:1303-1336; b is ignored for not); where
+ * (kernels.rs:1338-1380): the selected branch's stored bits, any dtype.
+ * Operands broadcast to `out` by their own strides (stride 0 = expanded
+ * axis); out is contiguous. No failure is possible. */
+enum {
+    CHELIS_CMP_CMPLT = 0, CHELIS_CMP_LT = 1, CHELIS_CMP_EQ = 2, CHELIS_CMP_NEQ = 3,
+    CHELIS_CMP_GT = 4, CHELIS_CMP_GTE = 5, CHELIS_CMP_LTE = 6
+};
+int32_t chelis_hip_compare(int32_t kind, const chelis_gpu_tensor *a, const chelis_gpu_tensor *b,
+                           const chelis_gpu_tensor *out);
+enum { CHELIS_LOGICAL_AND = 0, CHELIS_LOGICAL_OR = 1, CHELIS_LOGICAL_NOT = 2 };
+int32_t chelis_hip_logical(int32_t kind, const chelis_gpu_tensor *a, const chelis_gpu_tensor *b,
+                           const chelis_gpu_tensor *out);
+int32_t chelis_hip_where(const chelis_gpu_tensor *cond, const chelis_gpu_tensor *a, const chelis_gpu_tensor *b,
+                         const chelis_gpu_tensor *out);
+
+/* ---- checked casts, checked integer arithmetic, gather ----
+ * Failures follow [04-NUM-9]: a failing element stores zero and the launch
+ * reports the lowest-index failing element ([04-NUM-15]) with its kind and
+ * the rendered trap line. With `failure` non-NULL the call waits for its
+ * own result and fills *failure (kind 0: none), as the reference reads its
+ * numeric-failure record after a trapping launch (emit.rs:5185-5240). With
+ * `failure` NULL it returns at once and records into the device's deferred
+ * record, which chelis_hip_take_numeric_failure reads once after a run of
+ * launches: the earliest launch that failed, at its lowest failing index.
+ *
+ * cast: [04-NUM-14]'s checked cast between f32, f64, bf16, f16, i8, i16,
+ * i32, i64 and bool, with the C lane's conversions
+ * (crates/chelis-backend-c/src/host_emit.rs:1700-2120; the reference HIP
+ * lane's cast kernels are kernels.rs:1382, 2489, 2521): equal dtypes keep the
+ * stored bits; a float to an integer fails `domain` unless finite and
+ * integral, then `overflow` outside the range; an integer or bool to an
+ * integer fails `overflow` outside the range; to bool anything but 0 / 1
+ * fails `domain`; to a float, one rounding to nearest even from the exact
+ * source value, NaN to the canonical quiet NaN. Trap line
+ * `numeric trap: <kind> in cast at <target>`.
+ *
+ * integer_elementwise: i8 / i16 / i32 / i64 at the operand width
+ * (crates/chelis-numeric-core/src/dtype_semantics.rs:930-1030): add, sub,
+ * mul, neg and abs fail `overflow` outside the range; floor_div, trunc_div
+ * and mod fail `division by zero` on a zero divisor, floor_div and
+ * trunc_div `overflow` on MIN / -1; max_elem / min_elem never fail. The
+ * reference HIP lane checks sub and abs only (kernels.rs:769-810, 1434) and
+ * has no mod (emit.rs:2574); this build checks every op as the C lane does.
+ * b is ignored for neg and abs. Trap line `numeric trap: <kind> in <op> at
+ * <dtype>`.
+ *
+ * gather: RiscOp::Gather{axis, batch_rank} (crates/chelis-dag-core/src/
+ * dag.rs:1349-1356) with the reference's geometry (emit.rs:3807-3900,
+ * kernels.rs:2557-2597): out = values[..axis] ++ indices[batch_rank..] ++
+ * values[axis+1..], the first batch_rank axes of values and indices paired;
+ * element (b, j, d) reads values at index indices[batch of b, j] on `axis`.
+ * Any dtype of values (the reference admits f32 / f64), i32 or i64 indices,
+ * strided views of either. An index outside [0, extent) fails `domain`
+ * (`numeric trap: domain in gather at i64`); paired batch extents that
+ * differ return CHELIS_HIP_EDOMAIN with that line before any launch. */
+typedef struct {
+    int64_t index;     /* row-major index of the first failing element, -1 when none */
+    int32_t kind;      /* 0 none, 1 overflow, 2 domain, 3 division by zero */
+    int32_t reserved;
+    char message[96];  /* the trap line, e.g. "numeric trap: overflow in add at i64"; "" when none */
+} chelis_hip_numeric_failure;
+int32_t chelis_hip_cast(const chelis_gpu_tensor *x, const chelis_gpu_tensor *out,
+                        chelis_hip_numeric_failure *failure);
+enum {
+    CHELIS_INT_ADD = 0, CHELIS_INT_SUB = 1, CHELIS_INT_MUL = 2, CHELIS_INT_FLOOR_DIV = 3,
+    CHELIS_INT_TRUNC_DIV = 4, CHELIS_INT_MOD = 5, CHELIS_INT_MAX_ELEM = 6, CHELIS_INT_MIN_ELEM = 7,
+    CHELIS_INT_NEG = 8, CHELIS_INT_ABS = 9
+};
+int32_t chelis_hip_integer_elementwise(int32_t op, const chelis_gpu_tensor *a, const chelis_gpu_tensor *b,
+                                       const chelis_gpu_tensor *out, chelis_hip_numeric_failure *failure);
+int32_t chelis_hip_gather(const chelis_gpu_tensor *values, const chelis_gpu_tensor *indices, int32_t axis,
+                          int32_t batch_rank, const chelis_gpu_tensor *out, chelis_hip_numeric_failure *failure);
+/* Waits for the library stream, then reads and clears the current device's
+ * deferred failure record (kind 0: none). */
+int32_t chelis_hip_take_numeric_failure(chelis_hip_numeric_failure *failure);
+
 /* ---- keyed RNG ([05-RNG-1/2], [05-OP-8], [05-OP-37]) ----
  * uniform_like: kernels.rs:1672. dropout / replay: the C lane's semantics
  * (crates/chelis-backend-c/src/emit.rs:6139-6220); the reference HIP lane

@@ -679,3 +679,328 @@ void orc_mlp_train_step_f32(const float *x, const float *onehot, float *w1, floa
     free(z1); free(hd); free(d); free(z2); free(p); free(t); free(nl); free(gz2); free(gd);
     free(gw2); free(gw1); free(gb1); free(gb2);
 }
+
+/* ------------------------------------------------------------------ */
+/* Comparison, logical, where, checked cast, checked integer arithmetic
+ * and gather: the region kinds of the reference HIP lane around the float
+ * path (crates/chelis-backend-hip/src/kernels.rs:1270-1346 comparison /
+ * logical / where, :1382 and emit.rs:2413 casts, :769-866 and :1434 the
+ * trapping integer kernels, :2557-2600 gather), restated with the C lane's
+ * and the numeric core's semantics where the two lanes differ (the C lane
+ * checks add and mul; the HIP lane's add and mul kernels do not).
+ *
+ * Dtype ids are the device packet's (chelis_runtime_dtype.h): F32 0, F64 1,
+ * I32 2, BOOL 3, I64 4, BF16 5, F16 6, I8 7, I16 8. A trapping function
+ * returns the row-major index of its first failing element ([04-NUM-15]),
+ * or -1, and stores the failure kind of [04-NUM-9] in *kind (1 overflow,
+ * 2 domain, 3 division by zero); a failing element's output is zero. */
+enum { ODT_F32 = 0, ODT_F64 = 1, ODT_I32 = 2, ODT_BOOL = 3, ODT_I64 = 4, ODT_BF16 = 5, ODT_F16 = 6, ODT_I8 = 7,
+       ODT_I16 = 8 };
+enum { OFAIL_OVERFLOW = 1, OFAIL_DOMAIN = 2, OFAIL_DIVZERO = 3 };
+
+static int odt_is_float(int dt) { return dt == ODT_F32 || dt == ODT_F64 || dt == ODT_BF16 || dt == ODT_F16; }
+static int odt_width(int dt) {
+    switch (dt) {
+        case ODT_F64: case ODT_I64: return 8;
+        case ODT_F32: case ODT_I32: return 4;
+        case ODT_BF16: case ODT_F16: case ODT_I16: return 2;
+        default: return 1;
+    }
+}
+static int odt_bits(int dt) { return 8 * odt_width(dt); }
+static void odt_limits(int dt, int64_t *lo, int64_t *hi) {
+    const int b = odt_bits(dt);
+    *hi = b == 64 ? INT64_MAX : (int64_t)((1ull << (b - 1)) - 1ull);
+    *lo = -*hi - 1;
+}
+
+/* Element i of a float buffer widened exactly to binary64. */
+static double odt_float_at(int dt, const void *p, int64_t i) {
+    switch (dt) {
+        case ODT_F32: return (double)((const float *)p)[i];
+        case ODT_F64: return ((const double *)p)[i];
+        case ODT_BF16: return (double)orc_dec16(0, ((const uint16_t *)p)[i]);
+        default: return (double)orc_dec16(1, ((const uint16_t *)p)[i]);
+    }
+}
+/* Element i of an integer or bool buffer as its exact value. */
+static int64_t odt_int_at(int dt, const void *p, int64_t i) {
+    switch (dt) {
+        case ODT_I8: return ((const int8_t *)p)[i];
+        case ODT_I16: return ((const int16_t *)p)[i];
+        case ODT_I32: return ((const int32_t *)p)[i];
+        case ODT_I64: return ((const int64_t *)p)[i];
+        default: return ((const uint8_t *)p)[i];
+    }
+}
+static void odt_int_store(int dt, void *p, int64_t i, int64_t v) {
+    switch (dt) {
+        case ODT_I8: ((int8_t *)p)[i] = (int8_t)v; break;
+        case ODT_I16: ((int16_t *)p)[i] = (int16_t)v; break;
+        case ODT_I32: ((int32_t *)p)[i] = (int32_t)v; break;
+        case ODT_I64: ((int64_t *)p)[i] = v; break;
+        default: ((uint8_t *)p)[i] = (uint8_t)v; break;
+    }
+}
+
+/* [05-OP-36]: IEEE comparison of the semantic values (bf16 / f16 widened,
+ * signed zeros equal, any NaN false except for neq); integers by exact
+ * order; bool equality on the stored byte. kind: 0 cmplt, 1 lt, 2 eq,
+ * 3 neq, 4 gt, 5 gte, 6 lte (ComparisonKind's order,
+ * crates/chelis-dag-core/src/dag.rs:528-536). */
+void orc_compare(int kind, int dt, const void *a, const void *b, uint8_t *out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        int r;
+        if (odt_is_float(dt)) {
+            const double x = odt_float_at(dt, a, i), y = odt_float_at(dt, b, i);
+            switch (kind) {
+                case 0: case 1: r = x < y; break;
+                case 2: r = x == y; break;
+                case 3: r = x != y; break;
+                case 4: r = x > y; break;
+                case 5: r = x >= y; break;
+                default: r = x <= y; break;
+            }
+        } else {
+            const int64_t x = odt_int_at(dt, a, i), y = odt_int_at(dt, b, i);
+            switch (kind) {
+                case 0: case 1: r = x < y; break;
+                case 2: r = x == y; break;
+                case 3: r = x != y; break;
+                case 4: r = x > y; break;
+                case 5: r = x >= y; break;
+                default: r = x <= y; break;
+            }
+        }
+        out[i] = (uint8_t)r;
+    }
+}
+
+/* [05-OP-26..28] on Bool8 bytes as the HIP lane reads them (a byte is true
+ * when nonzero, kernels.rs:1305-1335). kind: 0 and, 1 or, 2 not. */
+void orc_logical(int kind, const uint8_t *a, const uint8_t *b, uint8_t *out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i)
+        out[i] = (uint8_t)(kind == 0 ? (a[i] != 0 && b[i] != 0) : kind == 1 ? (a[i] != 0 || b[i] != 0) : a[i] == 0);
+}
+
+/* [05-OP-53] where: the selected operand's stored bytes (NaN payloads and
+ * signed zeros kept), kernels.rs:1338-1346. */
+void orc_where(const uint8_t *cond, const void *a, const void *b, void *out, int64_t width, int64_t n) {
+    for (int64_t i = 0; i < n; ++i)
+        memcpy((char *)out + i * width, (const char *)(cond[i] ? a : b) + i * width, (size_t)width);
+}
+
+/* Round-half-even right shift of a magnitude (the C lane's
+ * chelis_host_round_shift_even_u64, crates/chelis-backend-c/src/
+ * host_emit.rs:1705-1713). */
+static uint64_t orc_rshift_even(uint64_t v, int s) {
+    if (s <= 0) return v;
+    if (s >= 64) return 0;
+    const uint64_t q = v >> s, r = v & ((1ull << s) - 1ull), h = 1ull << (s - 1);
+    return (r > h || (r == h && (q & 1ull))) ? q + 1 : q;
+}
+/* Pack sign, unbiased exponent of the leading bit and an (M+1)-bit rounded
+ * significand into a 16-bit IEEE layout, carrying a round-up past M+1 bits
+ * into the exponent and overflowing to infinity. */
+static uint16_t orc_pack16(uint16_t sign, int e, uint64_t rounded, int E, int M) {
+    const int bias = (1 << (E - 1)) - 1, emax = bias;
+    if (rounded == (1ull << (M + 1))) {
+        rounded >>= 1;
+        ++e;
+    }
+    if (e > emax) return (uint16_t)(sign | ((uint32_t)((1 << E) - 1) << M));
+    return (uint16_t)(sign | ((uint32_t)(e + bias) << M) | (uint32_t)(rounded & ((1ull << M) - 1ull)));
+}
+/* binary64 -> 16-bit IEEE (E exponent bits, M fraction bits) with one
+ * rounding to nearest even; NaN to the canonical quiet NaN
+ * (host_emit.rs:1715-1755). */
+static uint16_t orc_f64_to_ieee16(double v, int E, int M) {
+    uint64_t bits;
+    memcpy(&bits, &v, 8);
+    const uint16_t sign = (uint16_t)((bits >> 48) & 0x8000u);
+    const int se = (int)((bits >> 52) & 0x7ff);
+    const uint64_t man = bits & 0xfffffffffffffull;
+    const int bias = (1 << (E - 1)) - 1;
+    if (se == 0x7ff)
+        return man ? (uint16_t)(((uint32_t)((1 << E) - 1) << M) | (1u << (M - 1)))
+                   : (uint16_t)(sign | ((uint32_t)((1 << E) - 1) << M));
+    if (se == 0 && man == 0) return sign;
+    const int e = se ? se - 1023 : -1022;
+    const uint64_t sig = se ? (man | (1ull << 52)) : man;
+    if (se && e > bias) return (uint16_t)(sign | ((uint32_t)((1 << E) - 1) << M));
+    if (se && e >= 1 - bias) return orc_pack16(sign, e, orc_rshift_even(sig, 52 - M), E, M);
+    /* below the normal range: quantum 2^(1 - bias - M); a carry into the
+     * leading bit position lands on the smallest normal's encoding */
+    const int shift = (52 - M) + ((1 - bias) - e);
+    return (uint16_t)(sign | (uint16_t)orc_rshift_even(sig, shift));
+}
+/* exact integer -> 16-bit IEEE with one rounding (host_emit.rs:1757-1776). */
+static uint16_t orc_i64_to_ieee16(int64_t v, int E, int M) {
+    const uint16_t sign = v < 0 ? 0x8000u : 0u;
+    const uint64_t mag = v < 0 ? (uint64_t)(-(v + 1)) + 1ull : (uint64_t)v;
+    if (!mag) return sign;
+    int e = 63 - __builtin_clzll(mag);
+    const int bias = (1 << (E - 1)) - 1;
+    if (e > bias) return (uint16_t)(sign | ((uint32_t)((1 << E) - 1) << M));
+    const uint64_t r = e > M ? orc_rshift_even(mag, e - M) : mag << (M - e);
+    return orc_pack16(sign, e, r, E, M);
+}
+
+/* [04-NUM-14] checked cast, as the C lane's plan kinds
+ * (crates/chelis-backend-c/src/host_emit.rs:1959-2120) and the runtime's
+ * checks (crates/chelis-runtime/include/chelis_runtime.h:209-273):
+ * identity for equal dtypes (stored bits kept); a float source to an
+ * integer target traps domain unless finite and integral, then overflow
+ * outside the target range; an integer or bool source to an integer target
+ * traps overflow outside it; to bool, anything but 0 / 1 traps domain; to a
+ * float target, one rounding to nearest even (NaN canonical). */
+int64_t orc_cast(int src, int dst, const void *x, void *y, int64_t n, int32_t *kind) {
+    int64_t first = -1;
+    *kind = 0;
+    const int ws = odt_width(src), wd = odt_width(dst);
+    for (int64_t i = 0; i < n; ++i) {
+        int fail = 0;
+        if (src == dst) {
+            memcpy((char *)y + i * wd, (const char *)x + i * ws, (size_t)wd);
+            continue;
+        }
+        if (odt_is_float(src)) {
+            const double v = odt_float_at(src, x, i);
+            if (odt_is_float(dst)) {
+                if (dst == ODT_F64) {
+                    ((double *)y)[i] = nan64(v);
+                } else if (dst == ODT_F32) {
+                    ((float *)y)[i] = nan32((float)v);
+                } else {
+                    ((uint16_t *)y)[i] = dst == ODT_BF16 ? orc_f64_to_ieee16(v, 8, 7) : orc_f64_to_ieee16(v, 5, 10);
+                }
+            } else if (dst == ODT_BOOL) {
+                if (!isfinite(v) || (v != 0.0 && v != 1.0)) fail = OFAIL_DOMAIN;
+                ((uint8_t *)y)[i] = fail ? 0 : (uint8_t)(v == 1.0);
+            } else {
+                int64_t lo, hi;
+                odt_limits(dst, &lo, &hi);
+                if (!isfinite(v) || trunc(v) != v) fail = OFAIL_DOMAIN;
+                else if (dst == ODT_I64 ? (v < -9223372036854775808.0 || v >= 9223372036854775808.0)
+                                        : (v < (double)lo || v > (double)hi))
+                    fail = OFAIL_OVERFLOW;
+                odt_int_store(dst, y, i, fail ? 0 : (int64_t)v);
+            }
+        } else {
+            const int64_t v = odt_int_at(src, x, i);
+            if (dst == ODT_F64) {
+                ((double *)y)[i] = (double)v;
+            } else if (dst == ODT_F32) {
+                ((float *)y)[i] = (float)v;
+            } else if (dst == ODT_BF16 || dst == ODT_F16) {
+                ((uint16_t *)y)[i] = dst == ODT_BF16 ? orc_i64_to_ieee16(v, 8, 7) : orc_i64_to_ieee16(v, 5, 10);
+            } else if (dst == ODT_BOOL) {
+                if (v != 0 && v != 1) fail = OFAIL_DOMAIN;
+                ((uint8_t *)y)[i] = fail ? 0 : (uint8_t)(v == 1);
+            } else {
+                int64_t lo, hi;
+                odt_limits(dst, &lo, &hi);
+                if (v < lo || v > hi) fail = OFAIL_OVERFLOW;
+                odt_int_store(dst, y, i, fail ? 0 : v);
+            }
+        }
+        if (fail && first < 0) {
+            first = i;
+            *kind = fail;
+        }
+    }
+    return first;
+}
+
+/* Checked signed-integer arithmetic at the operand width
+ * (crates/chelis-numeric-core/src/dtype_semantics.rs:930-985 binary,
+ * :1015-1030 unary): add, sub, mul overflow outside the width's range;
+ * floor_div / trunc_div / mod trap division by zero on a zero divisor,
+ * floor_div and trunc_div overflow on MIN / -1 (mod of -1 is 0); floor_div
+ * rounds the truncated quotient down when the remainder's sign differs from
+ * the divisor's; max_elem / min_elem never trap. op: 0 add, 1 sub, 2 mul,
+ * 3 floor_div, 4 trunc_div, 5 mod, 6 max_elem, 7 min_elem. */
+int64_t orc_int_binary(int op, int dt, const void *a, const void *b, void *y, int64_t n, int32_t *kind) {
+    int64_t first = -1, lo, hi;
+    *kind = 0;
+    odt_limits(dt, &lo, &hi);
+    for (int64_t i = 0; i < n; ++i) {
+        const int64_t x = odt_int_at(dt, a, i), z = odt_int_at(dt, b, i);
+        int64_t r = 0;
+        int fail = 0;
+        switch (op) {
+            case 0: fail = (__builtin_add_overflow(x, z, &r) || r < lo || r > hi) ? OFAIL_OVERFLOW : 0; break;
+            case 1: fail = (__builtin_sub_overflow(x, z, &r) || r < lo || r > hi) ? OFAIL_OVERFLOW : 0; break;
+            case 2: fail = (__builtin_mul_overflow(x, z, &r) || r < lo || r > hi) ? OFAIL_OVERFLOW : 0; break;
+            case 3: case 4: case 5:
+                if (z == 0) {
+                    fail = OFAIL_DIVZERO;
+                } else if (op == 5) {
+                    r = z == -1 ? 0 : x % z;
+                } else if (x == lo && z == -1) {
+                    fail = OFAIL_OVERFLOW;
+                } else {
+                    r = x / z;
+                    if (op == 3 && x % z != 0 && ((x % z < 0) != (z < 0))) r -= 1;
+                }
+                break;
+            case 6: r = x > z ? x : z; break;
+            default: r = x < z ? x : z; break;
+        }
+        odt_int_store(dt, y, i, fail ? 0 : r);
+        if (fail && first < 0) {
+            first = i;
+            *kind = fail;
+        }
+    }
+    return first;
+}
+/* op: 0 neg, 1 abs; both overflow on the width's minimum. */
+int64_t orc_int_unary(int op, int dt, const void *x, void *y, int64_t n, int32_t *kind) {
+    int64_t first = -1, lo, hi;
+    *kind = 0;
+    odt_limits(dt, &lo, &hi);
+    for (int64_t i = 0; i < n; ++i) {
+        const int64_t v = odt_int_at(dt, x, i);
+        const int fail = v == lo ? OFAIL_OVERFLOW : 0;
+        odt_int_store(dt, y, i, fail ? 0 : (op == 0 || v < 0) ? -v : v);
+        if (fail && first < 0) {
+            first = i;
+            *kind = fail;
+        }
+    }
+    return first;
+}
+
+/* Gather (RiscOp::Gather{axis, batch_rank}, crates/chelis-dag-core/src/
+ * dag.rs:1349-1356) with the HIP lane's geometry (emit.rs:3807-3842,
+ * kernels.rs:2557-2597): values viewed as [before, axis_size, after], the
+ * result as [before, index_count, after] where index_count counts the
+ * indices past their batch_rank leading axes, which pair with the values'
+ * leading axes; result element (b, j, d) reads values (b, g, d) with g the
+ * index at (batch of b, j). An index outside [0, axis_size) traps domain;
+ * its element is zero. Values elements are `width` bytes; indices i32
+ * (idx_dt 2) or i64 (idx_dt 4), contiguous. */
+int64_t orc_gather(const void *values, int64_t width, int64_t before, int64_t axis_size, int64_t after,
+                   const void *idx, int idx_dt, int64_t index_count, int64_t batch_count, void *out, int32_t *kind) {
+    int64_t first = -1;
+    *kind = 0;
+    const int64_t outer_per_batch = (batch_count == 0 || before == 0) ? 1 : before / batch_count;
+    const int64_t total = before * index_count * after;
+    for (int64_t i = 0; i < total; ++i) {
+        const int64_t d = i % after, t = i / after, j = t % index_count, b = t / index_count;
+        const int64_t pos = (b / outer_per_batch) * index_count + j;
+        const int64_t g = odt_int_at(idx_dt, idx, pos);
+        char *dst = (char *)out + i * width;
+        if (g < 0 || g >= axis_size) {
+            memset(dst, 0, (size_t)width);
+            if (first < 0) {
+                first = i;
+                *kind = OFAIL_DOMAIN;
+            }
+            continue;
+        }
+        memcpy(dst, (const char *)values + ((b * axis_size + g) * after + d) * width, (size_t)width);
+    }
+    return first;
+}

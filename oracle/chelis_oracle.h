@@ -129,6 +129,19 @@ void orc_mlp_train_step_f32(const float *x, const float *onehot, float *w1, floa
                             float *b2, uint64_t key, float rate, float lr, float *loss,
                             int64_t batch, int64_t din, int64_t dhid, int64_t dout);
 
+/* ---- comparison, logical, where, checked cast and integer arithmetic,
+ * gather (flat, equal-length operands; dtype ids of the device packet).
+ * Trapping functions return the first failing index or -1 and set *kind
+ * (1 overflow, 2 domain, 3 division by zero). ---- */
+void orc_compare(int kind, int dt, const void *a, const void *b, uint8_t *out, int64_t n);
+void orc_logical(int kind, const uint8_t *a, const uint8_t *b, uint8_t *out, int64_t n);
+void orc_where(const uint8_t *cond, const void *a, const void *b, void *out, int64_t width, int64_t n);
+int64_t orc_cast(int src, int dst, const void *x, void *y, int64_t n, int32_t *kind);
+int64_t orc_int_binary(int op, int dt, const void *a, const void *b, void *y, int64_t n, int32_t *kind);
+int64_t orc_int_unary(int op, int dt, const void *x, void *y, int64_t n, int32_t *kind);
+int64_t orc_gather(const void *values, int64_t width, int64_t before, int64_t axis_size, int64_t after,
+                   const void *idx, int idx_dt, int64_t index_count, int64_t batch_count, void *out, int32_t *kind);
+
 #ifdef __cplusplus
 }
 #endif

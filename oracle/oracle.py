@@ -93,6 +93,15 @@ def _declare(L):
         "orc_mlp_train_step_f32": (None, [c_p, c_p, c_p, c_p, c_p, c_p, c_u64, c_f32, c_f32, c_p,
                                           c_i64, c_i64, c_i64, c_i64]),
     }
+    sig.update({
+        "orc_compare": (None, [ctypes.c_int, ctypes.c_int, c_p, c_p, c_p, c_i64]),
+        "orc_logical": (None, [ctypes.c_int, c_p, c_p, c_p, c_i64]),
+        "orc_where": (None, [c_p, c_p, c_p, c_p, c_i64, c_i64]),
+        "orc_cast": (c_i64, [ctypes.c_int, ctypes.c_int, c_p, c_p, c_i64, c_p]),
+        "orc_int_binary": (c_i64, [ctypes.c_int, ctypes.c_int, c_p, c_p, c_p, c_i64, c_p]),
+        "orc_int_unary": (c_i64, [ctypes.c_int, ctypes.c_int, c_p, c_p, c_i64, c_p]),
+        "orc_gather": (c_i64, [c_p, c_i64, c_i64, c_i64, c_i64, c_p, ctypes.c_int, c_i64, c_i64, c_p, c_p]),
+    })
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
         fn.restype = res
@@ -359,3 +368,112 @@ def mlp_train_step(x, onehot, w1, b1, w2, b2, key, rate, lr):
     lib().orc_mlp_train_step_f32(_ptr(x), _ptr(onehot), _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2),
                                  key & (2**64 - 1), rate, lr, _ptr(loss), B, din, dh, dout)
     return loss[0], w1, b1, w2, b2
+
+
+# ---- comparison, logical, where, checked cast / integer arithmetic, gather ----
+# Dtype names and the device packet's ids; bf16 / f16 travel as np.uint16
+# bit patterns, bool as one byte per element.
+DTYPE_IDS = {"f32": 0, "f64": 1, "i32": 2, "bool": 3, "i64": 4, "bf16": 5, "f16": 6, "i8": 7, "i16": 8}
+CARRIERS = {"f32": np.float32, "f64": np.float64, "i32": np.int32, "bool": np.uint8, "i64": np.int64,
+            "bf16": np.uint16, "f16": np.uint16, "i8": np.int8, "i16": np.int16}
+COMPARE_KINDS = {"cmp_lt": 0, "lt": 1, "eq": 2, "neq": 3, "gt": 4, "gte": 5, "lte": 6}
+LOGICAL_KINDS = {"and": 0, "or": 1, "not": 2}
+INT_BINARY = {"add": 0, "sub": 1, "mul": 2, "floor_div": 3, "trunc_div": 4, "mod": 5, "max_elem": 6, "min_elem": 7}
+INT_UNARY = {"neg": 0, "abs": 1}
+FAILURE_KINDS = {1: "overflow", 2: "domain", 3: "division by zero"}
+
+
+def _carrier(dt: str, a) -> np.ndarray:
+    a = np.asarray(a)
+    if dt == "f16" and a.dtype == np.float16:
+        a = a.view(np.uint16)
+    return np.ascontiguousarray(a, CARRIERS[dt])
+
+
+def _broadcast(*arrays):
+    shape = np.broadcast_shapes(*[a.shape for a in arrays])
+    return shape, [np.ascontiguousarray(np.broadcast_to(a, shape)) for a in arrays]
+
+
+def trap_text(kind: int, op: str, dt: str) -> str:
+    """[04-NUM-9]'s rendering of a failure (spec/04-type-system.md:3896-3898)."""
+    return f"numeric trap: {FAILURE_KINDS[kind]} in {op} at {dt}"
+
+
+def compare(kind: str, dt: str, a, b) -> np.ndarray:
+    """Bool8 result of one comparison; operands broadcast (numpy rules)."""
+    shape, (a, b) = _broadcast(_carrier(dt, a), _carrier(dt, b))
+    out = np.empty(shape, np.uint8)
+    lib().orc_compare(COMPARE_KINDS[kind], DTYPE_IDS[dt], _ptr(a), _ptr(b), _ptr(out), out.size)
+    return out
+
+
+def logical(kind: str, a, b=None) -> np.ndarray:
+    a = _carrier("bool", a)
+    if b is None:
+        b = a
+    shape, (a, b) = _broadcast(a, _carrier("bool", b))
+    out = np.empty(shape, np.uint8)
+    lib().orc_logical(LOGICAL_KINDS[kind], _ptr(a), _ptr(b), _ptr(out), out.size)
+    return out
+
+
+def where(cond, a, b) -> np.ndarray:
+    """The selected operand's stored bytes; a and b share one numpy dtype."""
+    a, b = np.asarray(a), np.asarray(b)
+    shape, (c, a, b) = _broadcast(_carrier("bool", cond), a, b.astype(a.dtype, copy=False))
+    out = np.empty(shape, a.dtype)
+    lib().orc_where(_ptr(c), _ptr(a), _ptr(b), _ptr(out), a.dtype.itemsize, out.size)
+    return out
+
+
+def cast(src: str, dst: str, x):
+    """(result, first failing index or -1, failure kind)."""
+    x = _carrier(src, x)
+    y = np.empty(x.shape, CARRIERS[dst])
+    kind = ctypes.c_int32(0)
+    first = lib().orc_cast(DTYPE_IDS[src], DTYPE_IDS[dst], _ptr(x), _ptr(y), x.size, ctypes.byref(kind))
+    return y, first, kind.value
+
+
+def int_binary(op: str, dt: str, a, b):
+    """(result, first failing index or -1, failure kind); operands broadcast."""
+    shape, (a, b) = _broadcast(_carrier(dt, a), _carrier(dt, b))
+    y = np.empty(shape, CARRIERS[dt])
+    kind = ctypes.c_int32(0)
+    first = lib().orc_int_binary(INT_BINARY[op], DTYPE_IDS[dt], _ptr(a), _ptr(b), _ptr(y), y.size,
+                                 ctypes.byref(kind))
+    return y, first, kind.value
+
+
+def int_unary(op: str, dt: str, x):
+    x = _carrier(dt, x)
+    y = np.empty(x.shape, CARRIERS[dt])
+    kind = ctypes.c_int32(0)
+    first = lib().orc_int_unary(INT_UNARY[op], DTYPE_IDS[dt], _ptr(x), _ptr(y), x.size, ctypes.byref(kind))
+    return y, first, kind.value
+
+
+def gather_shape(vshape, ishape, axis: int, batch_rank: int):
+    return tuple(vshape[:axis]) + tuple(ishape[batch_rank:]) + tuple(vshape[axis + 1:])
+
+
+def gather(values: np.ndarray, indices: np.ndarray, axis: int, batch_rank: int = 0):
+    """(result, first failing index or -1, failure kind): RiscOp::Gather with
+    the reference HIP lane's geometry. The leading batch_rank axes of values
+    and indices must match (the host-side domain check)."""
+    values = np.ascontiguousarray(values)
+    indices = np.ascontiguousarray(indices)
+    assert indices.dtype in (np.int32, np.int64)
+    assert tuple(values.shape[:batch_rank]) == tuple(indices.shape[:batch_rank])
+    axis_size = values.shape[axis]
+    after = int(np.prod(values.shape[axis + 1:], dtype=np.int64))
+    before = int(np.prod(values.shape[:axis], dtype=np.int64))
+    batch = int(np.prod(values.shape[:batch_rank], dtype=np.int64))
+    index_count = 0 if batch == 0 else indices.size // batch
+    out = np.empty(gather_shape(values.shape, indices.shape, axis, batch_rank), values.dtype)
+    kind = ctypes.c_int32(0)
+    first = lib().orc_gather(_ptr(values), values.dtype.itemsize, before, axis_size, after, _ptr(indices),
+                             2 if indices.dtype == np.int32 else 4, index_count, batch, _ptr(out),
+                             ctypes.byref(kind))
+    return out, first, kind.value

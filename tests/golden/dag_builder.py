@@ -34,7 +34,9 @@ import json
 import os
 import struct
 
-PREC = {"f32": "F32", "f64": "F64", "bool": "Bool", "i64": "Int64", "key": "Key"}
+PREC = {"f32": "F32", "f64": "F64", "bool": "Bool", "i64": "Int64", "key": "Key", "i32": "Int32", "i16": "Int16",
+        "i8": "Int8", "bf16": "Bf16", "f16": "F16"}
+INT_TAGS = {"i64": "int64", "i32": "int32", "i16": "int16", "i8": "int8"}
 F32_LOWEST = -3.4028234663852886e38
 
 
@@ -90,8 +92,8 @@ class Dag:
             v = {"dtype": "f32", "bits": _f32_bits(value)}
         elif prec == "f64":
             v = {"dtype": "f64", "bits": _f64_bits(value)}
-        elif prec == "i64":
-            v = {"dtype": "int64", "value": int(value)}
+        elif prec in INT_TAGS:
+            v = {"dtype": INT_TAGS[prec], "value": int(value)}
         else:
             raise ValueError(prec)
         return self.node({"Const": {"value": v}}, [], dims, prec, shape_deps=shape_deps)
@@ -123,6 +125,20 @@ class Dag:
 
     def where(self, c, a, b):
         return self.node("Where", [c, a, b], self.dims(a), self.prec(a))
+
+    def logical(self, kind, a, b=None):
+        """RiscOp::Logical(LogicalKind), snake_case kinds (dag.rs:553-559)."""
+        return self.node({"Logical": kind}, [a] if b is None else [a, b], self.dims(a), "bool")
+
+    def cast(self, x, prec):
+        return self.node({"Cast": {"new_precision": PREC[prec]}}, [x], self.dims(x), prec)
+
+    def gather(self, values, indices, axis, batch_rank=0):
+        """RiscOp::Gather{axis, batch_rank} (dag.rs:1349-1356): the result is
+        values[..axis] ++ indices[batch_rank..] ++ values[axis+1..]."""
+        dims = self.dims(values)[:axis] + self.dims(indices)[batch_rank:] + self.dims(values)[axis + 1:]
+        return self.node({"Gather": {"axis": axis, "batch_rank": batch_rank}}, [values, indices], dims,
+                         self.prec(values))
 
     def dropout(self, x, rate, key, replay=False):
         return self.node("DropoutReplay" if replay else "Dropout", [x, rate, key], self.dims(x), self.prec(x))
@@ -396,6 +412,55 @@ def mlp_program(Bt, I, Hd, O, rate=0.1, lr=0.01):
     return g
 
 
+def select_program(R, N):
+    """Comparison, logical and where over f32 rows: keep x where it exceeds
+    the row threshold t and y is not negative, else y."""
+    g = Dag("select_rows")
+    x = g.load("x", [R, N], "f32")
+    y = g.load("y", [R, N], "f32")
+    t = g.load("t", [N], "f32")
+    above = g.compare("gt", x, g.expand(t, 0, R))
+    negative = g.compare("lt", y, g.const(0.0, [R, N], "f32"))
+    keep = g.logical("and", above, g.logical("not", negative))
+    w = g.where(keep, x, y)
+    g.roots = [w, keep, g.compare("eq", w, x)]
+    return g
+
+
+def cast_program(n):
+    """Checked casts of an f64 vector: rounded to i32, and narrowed to f32
+    and bf16."""
+    g = Dag("casts")
+    x = g.load("x", [n], "f64")
+    g.roots = [g.cast(g.unary("Round", x), "i32"), g.cast(x, "f32"), g.cast(x, "bf16")]
+    return g
+
+
+def integer_program(n, prec="i64"):
+    """Checked integer arithmetic: floor and truncating division, the
+    remainder, max_elem and sub, none of them in a fused chain."""
+    g = Dag("integer_ops")
+    a = g.load("a", [n], prec)
+    b = g.load("b", [n], prec)
+    q = g.binary("FloorDiv", a, b)
+    r = g.binary("Mod", a, b)
+    m = g.binary("MaxElem", q, r)
+    g.roots = [q, r, g.binary("Sub", a, m), g.binary("TruncDiv", a, b)]
+    return g
+
+
+def gather_program(V, D, B, T):
+    """Row gather (an embedding lookup) and a batched gather of one column
+    per row (a label's logit)."""
+    g = Dag("gathers")
+    table = g.load("table", [V, D], "f32")
+    ids = g.load("ids", [B], "i64")
+    logits = g.load("logits", [B, T], "f32")
+    labels = g.load("labels", [B, 1], "i64")
+    g.roots = [g.gather(table, ids, 0), g.gather(logits, labels, 1, batch_rank=1)]
+    return g
+
+
 FIXTURES = {
     "softmax_f32_16384x1024": lambda: softmax_program(16384, 1024, "f32"),
     "softmax_f64_4096x4096": lambda: softmax_program(4096, 4096, "f64"),
@@ -410,6 +475,10 @@ FIXTURES = {
     "linreg_step_8192x32": lambda: linreg_program(8192, 32),
     "transformer_block_b8_s512_d1024": lambda: transformer_program(8, 512, 1024, 4096),
     "mlp_train_step_1024x784x512x10": lambda: mlp_program(1024, 784, 512, 10),
+    "select_rows_f32_4096x1024": lambda: select_program(4096, 1024),
+    "casts_f64_65536": lambda: cast_program(65536),
+    "integer_ops_i64_65536": lambda: integer_program(65536),
+    "gathers_50000x64_4096x10": lambda: gather_program(50000, 64, 4096, 10),
 }
 
 OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "dags")

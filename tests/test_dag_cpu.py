@@ -533,3 +533,63 @@ def test_host_program_lowers_only_its_count_helpers():
     assert [n for n, _ in out] == ["row_counts"]
     r = out[0][1]
     assert "extern \"C\" void row_counts_device(" in r.c_source and r.input_labels == ["b"]
+
+
+# ---------------------------------------------------------------- comparison, cast, integer, gather regions
+def region_kinds(prog):
+    return [line.split()[1] for line in prog.describe().splitlines()]
+
+
+def test_select_cast_integer_and_gather_regions_plan_one_launch_per_node():
+    """Compare / Logical / Where / Cast / integer arithmetic / Gather stay
+    their own node (fuse.rs:76-96 fuses none of them, and excludes integer
+    sub, abs, max_elem and min_elem), one launch each, as the reference HIP
+    lane emits them (kernels.rs:1270-1346, 1382, 769-866, 2557-2597)."""
+    def load(name):
+        return C.DagProgram(open(os.path.join(DAGS, name + ".json")).read())
+    assert region_kinds(load("select_rows_f32_4096x1024")) == ["compare", "compare", "logical", "logical", "where",
+                                                               "compare"]
+    assert region_kinds(load("casts_f64_65536")) == ["chain", "cast", "cast", "cast"]
+    assert region_kinds(load("integer_ops_i64_65536")) == ["integer"] * 5
+    p = load("gathers_50000x64_4096x10")
+    assert region_kinds(p) == ["gather", "gather"]
+    assert [o[1] for o in p.outputs] == [(4096, 64), (4096, 1)]
+
+
+def test_new_ops_read_and_write_back_verbatim():
+    """Logical, Gather and Mod payloads survive the reader and the fuse pass's
+    writer unchanged (the serde forms of dag.rs:553-559, 1349-1356)."""
+    g = DB.Dag("ops")
+    a = g.load("a", [4, 6], "f32")
+    i = g.load("i", [3], "i64")
+    x = g.load("x", [3], "i64")
+    c = g.compare("lt", a, a)
+    g.roots = [g.logical("not", c), g.gather(a, i, 1), g.binary("Mod", x, x), g.logical("or", c, c)]
+    out = json.loads(C.dag_fuse(g.json()))
+    assert [n["op"] for n in out["nodes"]][3:] == [{"Compare": "lt"}, {"Logical": "not"},
+                                                    {"Gather": {"axis": 1, "batch_rank": 0}}, "Mod",
+                                                    {"Logical": "or"}]
+
+
+def test_an_integer_fused_chain_is_refused_as_both_reference_lanes_refuse_it():
+    """fuse.rs joins integer add and mul into a FusedElem; the C lane rejects
+    integer chains (crates/chelis-backend-c/src/emit.rs:6933-6945) and the HIP
+    lane has no integer chain kernel, so the planner refuses them too. The
+    same ops apart (a fan-out between them) plan as integer launches."""
+    g = DB.Dag("int_chain")
+    a, b, c = (g.load(n, [16], "i64") for n in "abc")
+    g.roots = [g.add(g.mul(a, b), c)]
+    with pytest.raises(C.ChelisError, match="integer fused elementwise chain"):
+        C.DagProgram(g.json())
+    g = DB.Dag("int_apart")
+    a, b = (g.load(n, [16], "i64") for n in "ab")
+    m = g.mul(a, b)
+    g.roots = [m, g.add(m, b)]
+    assert region_kinds(C.DagProgram(g.json())) == ["integer", "integer"]
+
+
+def test_generated_entries_read_the_failure_record_only_when_a_launch_traps():
+    src = C.CodegenResult(open(os.path.join(DAGS, "integer_ops_i64_65536.json")).read(), "f").c_source
+    assert "chelis_hip_take_numeric_failure" in src and "chelis_numeric_trap(chelis_failure.message)" in src
+    src = C.CodegenResult(open(os.path.join(DAGS, "select_rows_f32_4096x1024.json")).read(), "f").c_source
+    assert "chelis_hip_take_numeric_failure" not in src

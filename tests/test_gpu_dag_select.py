@@ -1,0 +1,225 @@
+"""The comparison / logical / where, checked-cast, checked-integer and gather
+region kinds through the DAG path (chelis_dag_run) and the generated entries
+({f}_device and {f}), against the C oracle bit for bit. A failing element
+reaches the caller as the reference's trap line: a ChelisError from the
+DAG run, and from a generated entry the line on stderr with exit status 1
+([04-NUM-10]'s boundary; crates/chelis-runtime/include/chelis_runtime.h:
+73-82), for the earliest failing launch at its lowest failing element."""
+import os
+import subprocess
+import sys
+import tempfile
+
+import numpy as np
+import pytest
+
+import chelis_amd as C
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+DAGS = os.path.join(HERE, "golden", "dags")
+_TMP = tempfile.TemporaryDirectory()
+_BUILT = {}
+
+
+def setup_module(_m):
+    O.build()
+
+
+def fixture(name):
+    with open(os.path.join(DAGS, name + ".json")) as fh:
+        return fh.read()
+
+
+def generated(name):
+    if name not in _BUILT:
+        _BUILT[name] = C.GeneratedProgram(fixture(name), "gen_" + name.split("_")[0], _TMP.name)
+    return _BUILT[name]
+
+
+def bits(a):
+    return np.ascontiguousarray(a).view(np.uint8).tobytes()
+
+
+def run_dag(name, arrays):
+    prog = C.DagProgram(fixture(name))
+    return [t.numpy() for t in prog.run([C.to_device(a) for a in arrays])]
+
+
+def run_all(name, arrays):
+    """The outputs through the DAG run, the device entry and the host entry."""
+    g = generated(name)
+    return {"dag": run_dag(name, arrays),
+            "device": [t.numpy() for t in g.device([C.to_device(a) for a in arrays])],
+            "host": g.host(arrays)}
+
+
+# ---------------------------------------------------------------- select rows
+def select_inputs(R=4096, N=1024):
+    rng = np.random.default_rng(60)
+    x = rng.standard_normal((R, N)).astype(np.float32)
+    y = rng.standard_normal((R, N)).astype(np.float32)
+    t = (rng.standard_normal(N) * 0.5).astype(np.float32)
+    x[0, :8] = [np.nan, -0.0, 0.0, np.inf, -np.inf, 1.0, t[6], 2.0]
+    y[0, :8] = [1.0, 0.0, -0.0, np.nan, -1.0, -0.0, np.nan, -np.inf]
+    return x, y, t
+
+
+def select_oracle(x, y, t):
+    R, N = x.shape
+    above = O.compare("gt", "f32", x, np.broadcast_to(t, (R, N)))
+    negative = O.compare("lt", "f32", y, np.zeros((R, N), np.float32))
+    keep = O.logical("and", above, O.logical("not", negative))
+    w = O.where(keep, x, y)
+    return [w, keep, O.compare("eq", "f32", w, x)]
+
+
+@pytest.mark.parametrize("path", ["dag", "device", "host"])
+def test_select_rows_bit_exact(path):
+    x, y, t = select_inputs()
+    got = run_all("select_rows_f32_4096x1024", [x, y, t])[path]
+    for g, w in zip(got, select_oracle(x, y, t)):
+        assert bits(g) == bits(w)
+
+
+# ---------------------------------------------------------------- casts
+def cast_inputs(n=65536, bad=None):
+    rng = np.random.default_rng(61)
+    x = rng.standard_normal(n) * 10.0 ** rng.integers(-5, 9, n)
+    x[:12] = [0.5, 1.5, 2.5, -0.5, -2.5, 1e-320, -0.0, 1.5e9 + 0.5, 1.0 + 2.0 ** -8 + 2.0 ** -40,
+              65519.99, 2147483647.4, -2147483648.49]
+    if bad is not None:
+        x[bad] = np.nan
+    return x
+
+
+def round_half_even(x):
+    """RiscOp::Round is the C lane's rint: halves to even
+    (crates/chelis-backend-c/src/emit.rs:2434)."""
+    return np.rint(x)
+
+
+def cast_oracle(x):
+    return [O.cast("f64", "i32", round_half_even(x)), O.cast("f64", "f32", x), O.cast("f64", "bf16", x)]
+
+
+@pytest.mark.parametrize("path", ["dag", "device", "host"])
+def test_casts_bit_exact(path):
+    x = cast_inputs()
+    got = run_all("casts_f64_65536", [x])[path]
+    want = cast_oracle(x)
+    for g, (w, first, _) in zip(got, want):
+        assert first == -1
+        assert bits(g) == bits(w)
+
+
+def test_round_helper_matches_the_device_round():
+    """The test's round against the library's own round step, so the cast
+    check above is not resting on an assumption."""
+    x = cast_inputs()
+    out = C.empty(x.shape, np.float64)
+    C.fused_elementwise(C.fused_chain([("round", 0)]), [C.to_device(x)], out)
+    assert bits(out.numpy()) == bits(round_half_even(x))
+
+
+# ---------------------------------------------------------------- integer ops
+def integer_inputs(n=65536, zero_at=None):
+    rng = np.random.default_rng(62)
+    a = rng.integers(-(2 ** 62), 2 ** 62, n, dtype=np.int64)
+    b = rng.integers(-1000, 1000, n, dtype=np.int64)
+    b[b == 0] = 7
+    a[:6] = [7, 7, -7, -7, -(2 ** 62), 5]  # the fifth: a - floor_div(a, -1) is exactly i64's minimum
+    b[:6] = [2, -2, 2, -2, -1, 3]
+    if zero_at is not None:
+        b[zero_at] = 0
+    return a, b
+
+
+def integer_oracle(a, b):
+    steps = [("floor_div", "q", "a", "b"), ("mod", "r", "a", "b"), ("max_elem", "m", "q", "r"),
+             ("sub", "d", "a", "m"), ("trunc_div", "t", "a", "b")]
+    env = {"a": a, "b": b}
+    for op, dst, x, y in steps:
+        env[dst], first, _ = O.int_binary(op, "i64", env[x], env[y])
+        assert first == -1, (op, first)
+    return [env["q"], env["r"], env["d"], env["t"]]
+
+
+@pytest.mark.parametrize("path", ["dag", "device", "host"])
+def test_integer_ops_bit_exact(path):
+    a, b = integer_inputs()
+    got = run_all("integer_ops_i64_65536", [a, b])[path]
+    for g, w in zip(got, integer_oracle(a, b)):
+        assert np.array_equal(g, w)
+
+
+def test_integer_trap_through_the_dag_run():
+    a, b = integer_inputs(zero_at=[40000, 777])
+    with pytest.raises(C.ChelisError, match="^numeric trap: division by zero in floor_div at i64$"):
+        run_dag("integer_ops_i64_65536", [a, b])
+    # the record was read and cleared: the next run is clean
+    a, b = integer_inputs()
+    run_dag("integer_ops_i64_65536", [a, b])
+
+
+# ---------------------------------------------------------------- gathers
+def gather_inputs(bad=False):
+    rng = np.random.default_rng(63)
+    table = rng.standard_normal((50000, 64)).astype(np.float32)
+    ids = rng.integers(0, 50000, 4096).astype(np.int64)
+    logits = rng.standard_normal((4096, 10)).astype(np.float32)
+    labels = rng.integers(0, 10, (4096, 1)).astype(np.int64)
+    if bad:
+        labels[100, 0] = 10
+    return table, ids, logits, labels
+
+
+@pytest.mark.parametrize("path", ["dag", "device", "host"])
+def test_gathers_bit_exact(path):
+    table, ids, logits, labels = gather_inputs()
+    got = run_all("gathers_50000x64_4096x10", [table, ids, logits, labels])[path]
+    assert bits(got[0]) == bits(O.gather(table, ids, 0)[0])
+    assert bits(got[1]) == bits(O.gather(logits, labels, 1, batch_rank=1)[0])
+    assert np.array_equal(got[0], table[ids]) and np.array_equal(got[1][:, 0], logits[np.arange(4096), labels[:, 0]])
+
+
+# ---------------------------------------------------------------- generated entries trap
+CHILD = r"""
+import sys, numpy as np
+sys.path.insert(0, sys.argv[1])
+import ctypes, chelis_amd as C
+lib = ctypes.CDLL(sys.argv[2])
+case = sys.argv[3]
+if case == "integer":
+    n = 65536
+    a = np.arange(n, dtype=np.int64) - 3
+    b = np.ones(n, np.int64)
+    b[[50000, 9]] = 0
+    C.host_entry(sys.argv[4], [a, b], 4, library=lib)
+elif case == "cast":
+    x = np.zeros(65536)
+    x[[3000, 70]] = [np.inf, 3e9]
+    C.host_entry(sys.argv[4], [x], 3, library=lib)
+elif case == "gather":
+    table = np.zeros((50000, 64), np.float32)
+    ids = np.zeros(4096, np.int64)
+    ids[17] = -1
+    logits = np.zeros((4096, 10), np.float32)
+    labels = np.zeros((4096, 1), np.int64)
+    outs = C.device_entry(sys.argv[4], [C.to_device(v) for v in (table, ids, logits, labels)], 2, library=lib)
+print("returned", flush=True)
+"""
+
+
+@pytest.mark.parametrize("name,case,text", [
+    ("integer_ops_i64_65536", "integer", "numeric trap: division by zero in floor_div at i64"),
+    ("casts_f64_65536", "cast", "numeric trap: overflow in cast at i32"),
+    ("gathers_50000x64_4096x10", "gather", "numeric trap: domain in gather at i64"),
+])
+def test_generated_entries_exit_with_the_trap_line(name, case, text):
+    g = generated(name)
+    r = subprocess.run([sys.executable, "-c", CHILD, os.path.dirname(HERE), g.path, case, g.name],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 1, (r.returncode, r.stdout[-1000:], r.stderr[-2000:])
+    assert text in r.stderr and "returned" not in r.stdout
