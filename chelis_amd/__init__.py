@@ -139,6 +139,7 @@ SIGNATURES = {
     "chelis_hip_compare": (c_int32, [c_int32, P, P, P]),
     "chelis_hip_logical": (c_int32, [c_int32, P, P, P]),
     "chelis_hip_where": (c_int32, [P, P, P, P]),
+    "chelis_hip_extrema_adjoint": (c_int32, [c_int32, c_int32, P, P, P, P]),
     "chelis_hip_cast": (c_int32, [P, P, POINTER(NumericFailure)]),
     "chelis_hip_integer_elementwise": (c_int32, [c_int32, P, P, P, POINTER(NumericFailure)]),
     "chelis_hip_gather": (c_int32, [P, P, c_int32, c_int32, P, POINTER(NumericFailure)]),
@@ -531,6 +532,14 @@ def logical(kind: str, a, b=None, out=None):
 def where(cond, a, b, out=None):
     out = out or empty(_bshape(cond, a, b), a.dtype)
     check(lib().chelis_hip_where(_p(cond), _p(a), _p(b), _p(out)), "where")
+    return out
+
+
+def extrema_adjoint(kind: str, operand: str, a, b, g, out=None):
+    """chelis_hip_extrema_adjoint: kind "max" / "min", operand "left" / "right"."""
+    out = out or empty(_bshape(a, b, g), g.dtype)
+    check(lib().chelis_hip_extrema_adjoint(("max", "min").index(kind), ("left", "right").index(operand), _p(a),
+                                           _p(b), _p(g), _p(out)), "extrema_adjoint")
     return out
 
 

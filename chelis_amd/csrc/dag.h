@@ -65,6 +65,8 @@ enum class Op : uint8_t {
     Relu, ReluAdjoint, Where, Compare, Dropout, DropoutReplay, Cast, Logical, Mod,
     // sparse selection along one axis
     Gather,
+    // the extrema cotangent; keyed draws and emission-time key derivations
+    ExtremaAdjoint, UniformLike, KeyFromSeed, SplitKey, FoldIn,
     // reductions over one axis
     Sum, MaxReduce, MinReduce, ProdReduce, Argmax, Argmin, Count, Softmax,
     // movement
@@ -126,6 +128,7 @@ struct Node {
     int64_t named_claims = 0;              // ExtentWitness: claims against other witnesses
     std::string compare;            // Compare / Logical kind (snake_case wire name)
     int64_t batch_rank = 0;         // Gather (its axis in `axis`)
+    int32_t code = 0;               // ExtremaAdjoint: min (bit 0), right operand (bit 1); Split: the branch
     Prim const_prec = Prim::Other;  // Const
     uint64_t const_bits = 0;        // float bits, or the integer / bool value
     std::vector<Step> steps;        // FusedElem
@@ -195,7 +198,10 @@ enum class RegionKind : uint8_t {
     LinregStep, MlpStep,
     // one node each: comparison, logical, where, checked cast, checked
     // integer arithmetic (code = the op), gather (axis, batch_rank)
-    Compare, Logical, Where, Cast, Integer, Gather
+    Compare, Logical, Where, Cast, Integer, Gather,
+    // the extrema cotangent (code: min bit 0, right operand bit 1), a keyed
+    // uniform draw
+    ExtremaAdjoint, Uniform
 };
 const char *region_kind_name(RegionKind k);
 
@@ -227,6 +233,11 @@ struct Region {
     // batch rank (its axis in `axis`)
     int32_t code = 0;
     int64_t batch_rank = 0;
+    // uniform_like: the bounds; uniform_like / dropout: a key derived while
+    // planning (host_key), else the key is the last value in `in`
+    double low = 0.0, high = 0.0;
+    bool host_key = false;
+    uint64_t key = 0;
     std::vector<int64_t> outputs() const {
         std::vector<int64_t> o{out};
         o.insert(o.end(), more_out.begin(), more_out.end());

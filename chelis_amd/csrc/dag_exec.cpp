@@ -348,7 +348,16 @@ int32_t run_plan(chelis_dag_program *prog, const chelis_gpu_tensor *const *input
             case RegionKind::Relu: s = chelis_hip_relu(in[0], out); break;
             case RegionKind::ReluAdjoint: s = chelis_hip_relu_adjoint(in[0], in[1], out); break;
             case RegionKind::Dropout:
-                s = dropout_device_key(static_cast<const uint64_t *>(in[1]->data), in[0], r.rate, out);
+                s = r.host_key ? (r.replay ? chelis_hip_dropout_replay(r.key, in[0], r.rate, out)
+                                           : chelis_hip_dropout(r.key, in[0], r.rate, out))
+                               : dropout_device_key(static_cast<const uint64_t *>(in[1]->data), in[0], r.rate, out);
+                break;
+            case RegionKind::Uniform:
+                s = uniform_like_run(r.key, r.host_key ? nullptr : static_cast<const uint64_t *>(in[0]->data), r.low,
+                                     r.high, out);
+                break;
+            case RegionKind::ExtremaAdjoint:
+                s = chelis_hip_extrema_adjoint(r.code & 1, (r.code >> 1) & 1, in[0], in[1], in[2], out);
                 break;
             case RegionKind::Matmul: {
                 const chelis_gpu_tensor *bias = r.has_bias ? in[2] : nullptr;

@@ -65,6 +65,8 @@ const char *region_kind_name(RegionKind k) {
         case RegionKind::Cast: return "cast";
         case RegionKind::Integer: return "integer";
         case RegionKind::Gather: return "gather";
+        case RegionKind::ExtremaAdjoint: return "extrema_adjoint";
+        case RegionKind::Uniform: return "uniform_like";
     }
     return "?";
 }
@@ -892,6 +894,47 @@ struct Planner {
             default: return -1;
         }
     }
+    // [05-RNG-1/2] on the host: splitmix64, derive(k, j) =
+    // splitmix64(k ^ rotl64(splitmix64(j), 29)) (dtype_semantics.rs:4039-4060)
+    static uint64_t splitmix(uint64_t x) {
+        x += 0x9e3779b97f4a7c15ull;
+        x = (x ^ (x >> 30)) * 0xbf58476d1ce4e5b9ull;
+        x = (x ^ (x >> 27)) * 0x94d049bb133111ebull;
+        return x ^ (x >> 31);
+    }
+    static uint64_t derive(uint64_t k, uint64_t j) {
+        const uint64_t e = splitmix(j);
+        return splitmix(k ^ ((e << 29) | (e >> 35)));
+    }
+    // The key a rank-0 key node holds when it is derived from literal seeds
+    // and indices alone, as the reference derives draw keys at emission
+    // (emit.rs:3594-3653): key_from_seed is the seed's bits, split a derive
+    // by the branch, fold_in derive(derive(k, 2), n).
+    bool derived_key(int64_t id, uint64_t *k) const {
+        const Node &n = N(id);
+        if (!n.dims.empty() || n.prec != Prim::Key) return false;
+        double v;
+        Prim p;
+        switch (n.op) {
+            case Op::KeyFromSeed:
+                if (n.inputs.size() != 1 || N(n.inputs[0]).op != Op::Const || N(n.inputs[0]).const_prec != Prim::Int64)
+                    return false;
+                *k = N(n.inputs[0]).const_bits;
+                return true;
+            case Op::SplitKey:
+                if (n.inputs.size() != 1 || !derived_key(n.inputs[0], k)) return false;
+                *k = derive(*k, (uint64_t)n.code);
+                return true;
+            case Op::FoldIn:
+                if (n.inputs.size() != 2 || !derived_key(n.inputs[0], k) || !const_of(n.inputs[1], &v, &p) ||
+                    p != Prim::Int64 || N(n.inputs[1]).op != Op::Const)
+                    return false;
+                *k = derive(derive(*k, 2), N(n.inputs[1]).const_bits);
+                return true;
+            default:
+                return false;
+        }
+    }
     static int compare_code(const std::string &k) {
         static const char *names[] = {"cmp_lt", "lt", "eq", "neq", "gt", "gte", "lte"};
         for (int i = 0; i < 7; ++i)
@@ -1055,12 +1098,58 @@ struct Planner {
                     r.kind = RegionKind::Dropout;
                     r.replay = n.op == Op::DropoutReplay;
                     r.rate = rate;
-                    r.in = {n.inputs[0], n.inputs[2]};
+                    r.host_key = derived_key(n.inputs[2], &r.key);
+                    r.in = r.host_key ? std::vector<int64_t>{n.inputs[0]} : std::vector<int64_t>{n.inputs[0], n.inputs[2]};
                     r.out = n.id;
                     r.covers = {n.id};
                     claim(r);
                     continue;
                 }
+                case Op::KeyFromSeed: case Op::SplitKey: case Op::FoldIn: {
+                    // derived here; every reader is a draw that takes the key
+                    // from the plan
+                    uint64_t k;
+                    if (!derived_key(n.id, &k))
+                        return fail("node " + std::to_string(n.id) + ": " + n.variant +
+                                    " of a run-time seed, index or key tensor is not derived by this build (the "
+                                    "reference derives draw keys at emission only, emit.rs:3594-3653)");
+                    for (int64_t u : users[n.id]) {
+                        const Op uo = N(u).op;
+                        if (uo != Op::SplitKey && uo != Op::FoldIn && uo != Op::UniformLike && uo != Op::Dropout &&
+                            uo != Op::DropoutReplay)
+                            return fail("node " + std::to_string(n.id) + ": a derived key read by " + N(u).variant);
+                    }
+                    if (std::find(g.roots.begin(), g.roots.end(), n.id) != g.roots.end())
+                        return fail("node " + std::to_string(n.id) + ": a derived key as a result");
+                    continue;
+                }
+                case Op::UniformLike: {
+                    // inputs [template, low, high, key] (dag.rs:995-1005);
+                    // literal bounds, a rank-0 key (emit.rs:3655-3700)
+                    double lo, hi;
+                    Prim lp, hp;
+                    if (n.inputs.size() != 4 || !const_of(n.inputs[1], &lo, &lp) || !const_of(n.inputs[2], &hi, &hp))
+                        return fail("node " + std::to_string(n.id) + ": uniform_like needs literal bounds and a key");
+                    if (n.owner_activation >= 0)
+                        return fail("node " + std::to_string(n.id) + ": a draw under an activation is not built");
+                    if (N(n.inputs[3]).prec != Prim::Key || !N(n.inputs[3]).dims.empty())
+                        return fail("node " + std::to_string(n.id) + ": uniform_like's key must be one rank-0 key");
+                    Region r;
+                    r.kind = RegionKind::Uniform;
+                    r.low = lo;
+                    r.high = hi;
+                    r.host_key = derived_key(n.inputs[3], &r.key);
+                    if (!r.host_key) r.in = {n.inputs[3]};
+                    r.out = n.id;
+                    r.covers = {n.id};
+                    claim(r);
+                    continue;
+                }
+                case Op::ExtremaAdjoint:
+                    if (n.inputs.size() != 3)
+                        return fail("node " + std::to_string(n.id) + ": ExtremaAdjoint needs left, right and cotangent");
+                    single(n, RegionKind::ExtremaAdjoint, n.code);
+                    continue;
                 default:
                     return fail("node " + std::to_string(n.id) + ": " + n.variant +
                                 " is outside the region kinds this build runs");

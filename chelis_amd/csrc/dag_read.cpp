@@ -43,6 +43,8 @@ const OpName kOps[] = {
     {"Copy", Op::Copy}, {"FusedElem", Op::FusedElem}, {"BlasMatmul", Op::BlasMatmul},
     {"Store", Op::Store}, {"ExtentWitness", Op::ExtentWitness}, {"NamedCast", Op::NamedCast},
     {"Logical", Op::Logical}, {"Mod", Op::Mod}, {"Gather", Op::Gather},
+    {"ExtremaAdjoint", Op::ExtremaAdjoint}, {"UniformLike", Op::UniformLike}, {"KeyFromSeed", Op::KeyFromSeed},
+    {"Split", Op::SplitKey}, {"FoldIn", Op::FoldIn},
 };
 
 struct PrimName {
@@ -288,6 +290,22 @@ bool read_op(const Json &op, Graph *g, Node *n, std::string *why) {
             if (!int_of(p.get("axis"), &n->axis) || !int_of(p.get("batch_rank"), &n->batch_rank))
                 return (*why = "Gather needs axis and batch_rank", false);
             return true;
+        case Op::ExtremaAdjoint: {
+            // ExtremaKind / ExtremaOperand (dag.rs:596-606)
+            const Json *kind = p.get("kind"), *operand = p.get("operand");
+            if (!kind || kind->kind != Json::String || !operand || operand->kind != Json::String ||
+                (kind->text != "Max" && kind->text != "Min") || (operand->text != "Left" && operand->text != "Right"))
+                return (*why = "ExtremaAdjoint needs kind Max|Min and operand Left|Right", false);
+            n->code = (kind->text == "Min" ? 1 : 0) | (operand->text == "Right" ? 2 : 0);
+            return true;
+        }
+        case Op::SplitKey: {
+            const Json *branch = p.get("branch");  // KeyBranch
+            if (!branch || branch->kind != Json::String || (branch->text != "Left" && branch->text != "Right"))
+                return (*why = "Split needs branch Left|Right", false);
+            n->code = branch->text == "Right" ? 1 : 0;
+            return true;
+        }
         case Op::Cast:
             if (!prim_of(p.get("new_precision"), &n->cast_to)) return (*why = "Cast needs new_precision", false);
             return true;

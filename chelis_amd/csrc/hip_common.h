@@ -100,6 +100,10 @@ bool row_view(const chelis_gpu_tensor *t, RowView *v);
 // [05-OP-37]'s drop test unit < rate at the dtype, as an integer cut-off:
 // an element is dropped exactly when its word >> 11 is below the result.
 uint64_t dropout_cut(double rate, chelis_dtype dt);
+// uniform_like with the key given on the host (key_dev null) or read on the
+// device from key_dev.
+int32_t uniform_like_run(uint64_t key, const uint64_t *key_dev, double low, double high,
+                         const chelis_gpu_tensor *out);
 int32_t dropout_device_key(const uint64_t *key_dev, const chelis_gpu_tensor *x, double rate,
                            const chelis_gpu_tensor *y);
 

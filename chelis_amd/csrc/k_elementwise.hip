@@ -811,12 +811,20 @@ extern "C" int32_t chelis_hip_dropout_replay(uint64_t key, const chelis_gpu_tens
     return unary_entry<Unary::Dropout>("dropout_replay", g, nullptr, dx, u);
 }
 
-extern "C" int32_t chelis_hip_uniform_like(uint64_t key, double low, double high, const chelis_gpu_tensor *out) {
+namespace chelis {
+// [05-OP-8]'s bounds at the draw's dtype: finite, ordered, a finite span.
+int32_t uniform_like_run(uint64_t key, const uint64_t *key_dev, double low, double high,
+                         const chelis_gpu_tensor *out) {
     if (!out || !is_float(out->dtype)) return set_error(CHELIS_HIP_EDOMAIN, "uniform_like: f32 or f64 result required");
     const bool f32 = out->dtype == CHELIS_DTYPE_F32;
     const double lo = f32 ? (double)(float)low : low, hi = f32 ? (double)(float)high : high;
     const double span = f32 ? (double)((float)hi - (float)lo) : hi - lo;
     if (!(std::isfinite(lo) && std::isfinite(hi) && lo <= hi && std::isfinite(span)))
         return set_error(CHELIS_HIP_EDOMAIN, "numeric trap: domain in uniform_like at %s", f32 ? "f32" : "f64");
-    return unary_entry<Unary::Uniform>("uniform_like", nullptr, nullptr, out, UnaryArgs{key, low, high, nullptr});
+    return unary_entry<Unary::Uniform>("uniform_like", nullptr, nullptr, out, UnaryArgs{key, low, high, key_dev});
+}
+}  // namespace chelis
+
+extern "C" int32_t chelis_hip_uniform_like(uint64_t key, double low, double high, const chelis_gpu_tensor *out) {
+    return chelis::uniform_like_run(key, nullptr, low, high, out);
 }

@@ -182,6 +182,27 @@ struct WhereOp {
     }
 };
 
+// [05-OP-40] extrema cotangent (kernels.rs:1030-1134): the cotangent where
+// `operand` was selected, +0 elsewhere. max selects the left operand when it
+// is NaN, or when the right one is not NaN and left >= right (min: <=), the
+// first-operand tie rule of max_elem / min_elem; bf16 / f16 compare decoded
+// values and pass the cotangent's stored bits.
+template <int DT>
+struct ExtremaAdjointOp {
+    static constexpr int N = 3;
+    static constexpr bool kTraps = false;
+    int32_t is_min, right;
+    typename Dt<DT>::S *out;
+    __device__ unsigned long long operator()(int64_t i, const Ops &o, const int64_t (&off)[3]) const {
+        using S = typename Dt<DT>::S;
+        const auto a = semantic<DT>(static_cast<const S *>(o.p[0])[off[0]]);
+        const auto b = semantic<DT>(static_cast<const S *>(o.p[1])[off[1]]);
+        const bool left = a != a || (b == b && (is_min ? a <= b : a >= b));
+        out[i] = left != (right != 0) ? static_cast<const S *>(o.p[2])[off[2]] : S{};
+        return 0ull;
+    }
+};
+
 // ---------------------------------------------------------------- checked cast
 // Round-half-even right shift of a magnitude.
 __device__ inline uint64_t rshift_even(uint64_t v, int s) {
@@ -689,6 +710,37 @@ extern "C" int32_t chelis_hip_where(const chelis_gpu_tensor *cond, const chelis_
         case 4: return launch_map(WhereOp<uint32_t>{static_cast<uint32_t *>(out->data)}, ins, 3, out, nullptr, "where");
         default:
             return launch_map(WhereOp<uint64_t>{static_cast<uint64_t *>(out->data)}, ins, 3, out, nullptr, "where");
+    }
+}
+
+extern "C" int32_t chelis_hip_extrema_adjoint(int32_t kind, int32_t operand, const chelis_gpu_tensor *a,
+                                              const chelis_gpu_tensor *b, const chelis_gpu_tensor *g,
+                                              const chelis_gpu_tensor *out) {
+    if (int32_t s = check_out(out, "extrema_adjoint")) return s;
+    if ((kind != CHELIS_EXTREMA_MAX && kind != CHELIS_EXTREMA_MIN) ||
+        (operand != CHELIS_EXTREMA_LEFT && operand != CHELIS_EXTREMA_RIGHT))
+        return set_error(CHELIS_HIP_EDOMAIN, "extrema_adjoint: unknown kind %d or operand %d", kind, operand);
+    if (int32_t s = check_broadcast(a, out, "extrema_adjoint", "a")) return s;
+    if (int32_t s = check_broadcast(b, out, "extrema_adjoint", "b")) return s;
+    if (int32_t s = check_broadcast(g, out, "extrema_adjoint", "g")) return s;
+    if (a->dtype != out->dtype || b->dtype != out->dtype || g->dtype != out->dtype)
+        return set_error(CHELIS_HIP_EDOMAIN, "extrema_adjoint: operand dtypes differ from the output");
+    const chelis_gpu_tensor *ins[3] = {a, b, g};
+    const int32_t mn = kind == CHELIS_EXTREMA_MIN, rt = operand == CHELIS_EXTREMA_RIGHT;
+    switch (out->dtype) {
+        case CHELIS_DTYPE_F32:
+            return launch_map(ExtremaAdjointOp<CHELIS_DTYPE_F32>{mn, rt, static_cast<float *>(out->data)}, ins, 3,
+                              out, nullptr, "extrema_adjoint");
+        case CHELIS_DTYPE_F64:
+            return launch_map(ExtremaAdjointOp<CHELIS_DTYPE_F64>{mn, rt, static_cast<double *>(out->data)}, ins, 3,
+                              out, nullptr, "extrema_adjoint");
+        case CHELIS_DTYPE_BF16:
+            return launch_map(ExtremaAdjointOp<CHELIS_DTYPE_BF16>{mn, rt, static_cast<uint16_t *>(out->data)}, ins,
+                              3, out, nullptr, "extrema_adjoint");
+        case CHELIS_DTYPE_F16:
+            return launch_map(ExtremaAdjointOp<CHELIS_DTYPE_F16>{mn, rt, static_cast<uint16_t *>(out->data)}, ins,
+                              3, out, nullptr, "extrema_adjoint");
+        default: return set_error(CHELIS_HIP_EUNSUPPORTED, "extrema_adjoint: f32, f64, bf16 or f16 only");
     }
 }
 

@@ -188,6 +188,18 @@ int32_t chelis_hip_logical(int32_t kind, const chelis_gpu_tensor *a, const cheli
 int32_t chelis_hip_where(const chelis_gpu_tensor *cond, const chelis_gpu_tensor *a, const chelis_gpu_tensor *b,
                          const chelis_gpu_tensor *out);
 
+/* ---- extrema cotangent ----
+ * kernels.rs:1030-1134 (RiscOp::ExtremaAdjoint{kind, operand}, [05-OP-40]):
+ * out = g where `operand` was selected by max_elem / min_elem of (a, b),
+ * +0 elsewhere. max selects a when a is NaN, or when b is not NaN and
+ * a >= b (min: a <= b). f32, f64, bf16, f16 (16-bit operands compare their
+ * decoded values; the cotangent keeps its stored bits). */
+enum { CHELIS_EXTREMA_MAX = 0, CHELIS_EXTREMA_MIN = 1 };
+enum { CHELIS_EXTREMA_LEFT = 0, CHELIS_EXTREMA_RIGHT = 1 };
+int32_t chelis_hip_extrema_adjoint(int32_t kind, int32_t operand, const chelis_gpu_tensor *a,
+                                   const chelis_gpu_tensor *b, const chelis_gpu_tensor *g,
+                                   const chelis_gpu_tensor *out);
+
 /* ---- checked casts, checked integer arithmetic, gather ----
  * Failures follow [04-NUM-9]: a failing element stores zero and the launch
  * reports the lowest-index failing element ([04-NUM-15]) with its kind and

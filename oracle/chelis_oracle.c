@@ -790,6 +790,23 @@ void orc_where(const uint8_t *cond, const void *a, const void *b, void *out, int
         memcpy((char *)out + i * width, (const char *)(cond[i] ? a : b) + i * width, (size_t)width);
 }
 
+/* [05-OP-40] extrema cotangent (RiscOp::ExtremaAdjoint, crates/chelis-backend-
+ * hip/src/kernels.rs:1030-1134): g where `right` (0: the left operand, 1:
+ * the right) was selected by max (is_min 0) or min of (a, b), +0 elsewhere;
+ * the left operand is selected when it is NaN, or when the right one is not
+ * NaN and left >= right (min: <=). Float dtypes (bf16 / f16 compare decoded
+ * values); the cotangent's stored bytes are copied. */
+void orc_extrema_adjoint(int is_min, int right, int dt, const void *a, const void *b, const void *g, void *out,
+                         int64_t n) {
+    const int w = odt_width(dt);
+    for (int64_t i = 0; i < n; ++i) {
+        const double x = odt_float_at(dt, a, i), y = odt_float_at(dt, b, i);
+        const int left = isnan(x) || (!isnan(y) && (is_min ? x <= y : x >= y));
+        if (left != right) memcpy((char *)out + i * w, (const char *)g + i * w, (size_t)w);
+        else memset((char *)out + i * w, 0, (size_t)w);
+    }
+}
+
 /* Round-half-even right shift of a magnitude (the C lane's
  * chelis_host_round_shift_even_u64, crates/chelis-backend-c/src/
  * host_emit.rs:1705-1713). */

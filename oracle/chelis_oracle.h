@@ -136,6 +136,8 @@ void orc_mlp_train_step_f32(const float *x, const float *onehot, float *w1, floa
 void orc_compare(int kind, int dt, const void *a, const void *b, uint8_t *out, int64_t n);
 void orc_logical(int kind, const uint8_t *a, const uint8_t *b, uint8_t *out, int64_t n);
 void orc_where(const uint8_t *cond, const void *a, const void *b, void *out, int64_t width, int64_t n);
+void orc_extrema_adjoint(int is_min, int right, int dt, const void *a, const void *b, const void *g, void *out,
+                         int64_t n);
 int64_t orc_cast(int src, int dst, const void *x, void *y, int64_t n, int32_t *kind);
 int64_t orc_int_binary(int op, int dt, const void *a, const void *b, void *y, int64_t n, int32_t *kind);
 int64_t orc_int_unary(int op, int dt, const void *x, void *y, int64_t n, int32_t *kind);

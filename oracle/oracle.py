@@ -98,6 +98,7 @@ def _declare(L):
         "orc_logical": (None, [ctypes.c_int, c_p, c_p, c_p, c_i64]),
         "orc_where": (None, [c_p, c_p, c_p, c_p, c_i64, c_i64]),
         "orc_cast": (c_i64, [ctypes.c_int, ctypes.c_int, c_p, c_p, c_i64, c_p]),
+        "orc_extrema_adjoint": (None, [ctypes.c_int, ctypes.c_int, ctypes.c_int, c_p, c_p, c_p, c_p, c_i64]),
         "orc_int_binary": (c_i64, [ctypes.c_int, ctypes.c_int, c_p, c_p, c_p, c_i64, c_p]),
         "orc_int_unary": (c_i64, [ctypes.c_int, ctypes.c_int, c_p, c_p, c_i64, c_p]),
         "orc_gather": (c_i64, [c_p, c_i64, c_i64, c_i64, c_i64, c_p, ctypes.c_int, c_i64, c_i64, c_p, c_p]),
@@ -424,6 +425,15 @@ def where(cond, a, b) -> np.ndarray:
     shape, (c, a, b) = _broadcast(_carrier("bool", cond), a, b.astype(a.dtype, copy=False))
     out = np.empty(shape, a.dtype)
     lib().orc_where(_ptr(c), _ptr(a), _ptr(b), _ptr(out), a.dtype.itemsize, out.size)
+    return out
+
+
+def extrema_adjoint(kind: str, operand: str, dt: str, a, b, g) -> np.ndarray:
+    """kind "max" / "min", operand "left" / "right"; operands broadcast."""
+    shape, (a, b, g) = _broadcast(_carrier(dt, a), _carrier(dt, b), _carrier(dt, g))
+    out = np.empty(shape, CARRIERS[dt])
+    lib().orc_extrema_adjoint(int(kind == "min"), int(operand == "right"), DTYPE_IDS[dt], _ptr(a), _ptr(b), _ptr(g),
+                              _ptr(out), out.size)
     return out
 
 

@@ -130,6 +130,26 @@ class Dag:
         """RiscOp::Logical(LogicalKind), snake_case kinds (dag.rs:553-559)."""
         return self.node({"Logical": kind}, [a] if b is None else [a, b], self.dims(a), "bool")
 
+    def extrema_adjoint(self, kind, operand, a, b, g):
+        """RiscOp::ExtremaAdjoint{kind: Max|Min, operand: Left|Right}
+        (dag.rs:949-952, 596-606)."""
+        return self.node({"ExtremaAdjoint": {"kind": kind, "operand": operand}}, [a, b, g], self.dims(g), self.prec(g))
+
+    # ---- keys and draws (dag.rs:995-1060) ----
+    def key_from_seed(self, seed: int):
+        return self.node("KeyFromSeed", [self.const(seed, [], "i64")], [], "key")
+
+    def split(self, key, branch):
+        return self.node({"Split": {"branch": branch}}, [key], [], "key")
+
+    def fold_in(self, key, n: int):
+        return self.node("FoldIn", [key, self.const(n, [], "i64")], [], "key")
+
+    def uniform_like(self, template, low, high, key):
+        p = self.prec(template)
+        return self.node("UniformLike", [template, self.const(low, [], p), self.const(high, [], p), key],
+                         self.dims(template), p)
+
     def cast(self, x, prec):
         return self.node({"Cast": {"new_precision": PREC[prec]}}, [x], self.dims(x), prec)
 
@@ -461,6 +481,28 @@ def gather_program(V, D, B, T):
     return g
 
 
+def draws_program(R, N, seed=1234):
+    """A uniform draw and a dropout whose keys the plan derives from a
+    literal seed (key_from_seed, split, fold_in)."""
+    g = Dag("draws")
+    x = g.load("x", [R, N], "f32")
+    k0 = g.key_from_seed(seed)
+    u = g.uniform_like(x, -1.0, 2.0, g.fold_in(g.split(k0, "Left"), 7))
+    d = g.dropout(x, g.const(0.1, [], "f32"), g.split(k0, "Right"))
+    g.roots = [u, d]
+    return g
+
+
+def extrema_adjoint_program(R, N):
+    g = Dag("extrema_adjoints")
+    a = g.load("a", [R, N], "f32")
+    b = g.load("b", [R, N], "f32")
+    c = g.load("g", [R, N], "f32")
+    g.roots = [g.extrema_adjoint("Max", "Left", a, b, c), g.extrema_adjoint("Max", "Right", a, b, c),
+               g.extrema_adjoint("Min", "Left", a, b, c)]
+    return g
+
+
 FIXTURES = {
     "softmax_f32_16384x1024": lambda: softmax_program(16384, 1024, "f32"),
     "softmax_f64_4096x4096": lambda: softmax_program(4096, 4096, "f64"),
@@ -479,6 +521,8 @@ FIXTURES = {
     "casts_f64_65536": lambda: cast_program(65536),
     "integer_ops_i64_65536": lambda: integer_program(65536),
     "gathers_50000x64_4096x10": lambda: gather_program(50000, 64, 4096, 10),
+    "draws_f32_1024x512": lambda: draws_program(1024, 512),
+    "extrema_adjoints_f32_4096x1024": lambda: extrema_adjoint_program(4096, 1024),
 }
 
 OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "dags")

@@ -593,3 +593,24 @@ def test_generated_entries_read_the_failure_record_only_when_a_launch_traps():
     assert "chelis_hip_take_numeric_failure" in src and "chelis_numeric_trap(chelis_failure.message)" in src
     src = C.CodegenResult(open(os.path.join(DAGS, "select_rows_f32_4096x1024.json")).read(), "f").c_source
     assert "chelis_hip_take_numeric_failure" not in src
+
+
+def test_draw_keys_derive_while_planning_or_are_refused():
+    """key_from_seed / split / fold_in of literals are derived while planning
+    and take no launch (emit.rs:3594-3653); a run-time seed, or a derived key
+    read as a value, is refused as the reference refuses it."""
+    p = C.DagProgram(open(os.path.join(DAGS, "draws_f32_1024x512.json")).read())
+    assert region_kinds(p) == ["uniform_like", "dropout"]
+    g = DB.Dag("runtime_seed")
+    s = g.load("s", [], "i64")
+    x = g.load("x", [8], "f32")
+    k = g.node("KeyFromSeed", [s], [], "key")
+    g.roots = [g.uniform_like(x, 0.0, 1.0, k)]
+    with pytest.raises(C.ChelisError, match="run-time seed"):
+        C.DagProgram(g.json())
+    g = DB.Dag("key_result")
+    g.roots = [g.key_from_seed(5)]
+    with pytest.raises(C.ChelisError, match="derived key as a result"):
+        C.DagProgram(g.json())
+    p = C.DagProgram(open(os.path.join(DAGS, "extrema_adjoints_f32_4096x1024.json")).read())
+    assert region_kinds(p) == ["extrema_adjoint"] * 3

@@ -223,3 +223,33 @@ def test_generated_entries_exit_with_the_trap_line(name, case, text):
                        capture_output=True, text=True, timeout=300)
     assert r.returncode == 1, (r.returncode, r.stdout[-1000:], r.stderr[-2000:])
     assert text in r.stderr and "returned" not in r.stdout
+
+
+# ---------------------------------------------------------------- keyed draws, extrema cotangent
+@pytest.mark.parametrize("path", ["dag", "device", "host"])
+def test_draws_with_plan_derived_keys_bit_exact(path):
+    """key_from_seed(1234), split, fold_in(7) derived while planning
+    ([05-OP-69..72]), then uniform_like(-1, 2) and dropout(0.1) on the
+    device: the oracle's draws from the same derived keys, bit for bit."""
+    x = np.random.default_rng(64).standard_normal((1024, 512)).astype(np.float32)
+    got = run_all("draws_f32_1024x512", [x])[path]
+    left, right = O.split(1234)
+    u = O.uniform_like(O.fold_in(left, 7), -1.0, 2.0, x.size, np.float32).reshape(x.shape)
+    assert bits(got[0]) == bits(u)
+    assert bits(got[1]) == bits(O.dropout(right, x, np.float32(0.1)))
+
+
+@pytest.mark.parametrize("path", ["dag", "device", "host"])
+def test_extrema_adjoints_bit_exact(path):
+    rng = np.random.default_rng(65)
+    a = rng.standard_normal((4096, 1024)).astype(np.float32)
+    b = a.copy()
+    b[::2] = rng.standard_normal((2048, 1024)).astype(np.float32)  # half the rows tie exactly
+    a[0, :4] = [np.nan, 0.0, -0.0, np.inf]
+    b[0, :4] = [1.0, -0.0, 0.0, np.nan]
+    g = rng.standard_normal((4096, 1024)).astype(np.float32)
+    got = run_all("extrema_adjoints_f32_4096x1024", [a, b, g])[path]
+    want = [O.extrema_adjoint("max", "left", "f32", a, b, g), O.extrema_adjoint("max", "right", "f32", a, b, g),
+            O.extrema_adjoint("min", "left", "f32", a, b, g)]
+    for x, y in zip(got, want):
+        assert bits(x) == bits(y)

@@ -254,3 +254,19 @@ def test_deferred_record_keeps_the_earliest_failing_launch():
     assert C.take_numeric_failure() is None
     C.cast(bad_late, np.int64, deferred=True)
     assert C.take_numeric_failure() == (5, 2, "numeric trap: domain in cast at i64")
+
+
+@pytest.mark.parametrize("dt", ["f32", "f64", "bf16", "f16"])
+def test_extrema_adjoint_every_kind_and_operand(dt):
+    rng = np.random.default_rng(50 + DTS.index(dt))
+    v = sample(dt, 60, rng)
+    a = np.repeat(v, len(v))
+    b = np.tile(v, len(v))
+    g = sample(dt, len(a), rng)[: len(a)]
+    da, db, dg = C.to_device(a), C.to_device(b), C.to_device(g)
+    for kind in (0, 1):
+        for operand in (0, 1):
+            k, side = ("max", "min")[kind], ("left", "right")[operand]
+            out = C.extrema_adjoint(k, side, da, db, dg)
+            want = O.extrema_adjoint(k, side, dt, oracle_carrier(dt, a), oracle_carrier(dt, b), oracle_carrier(dt, g))
+            assert bits(out.numpy()).tobytes() == bits(want).tobytes(), (dt, kind, operand)

@@ -423,3 +423,37 @@ def test_gather_out_of_range_is_a_domain_trap_at_the_first_index():
     # result [2, 4]: row 0 fails first at its position 1
     assert (first, O.trap_text(kind, "gather", "i64")) == (1, "numeric trap: domain in gather at i64")
     assert out[0, 1] == 0 and out[1, 0] == 6.0
+
+
+# ---------------------------------------------------------------- extrema cotangent
+@pytest.mark.parametrize("dt", ["f32", "f64", "bf16", "f16"])
+def test_extrema_adjoint_routes_the_cotangent_to_the_selected_operand(dt):
+    """[05-OP-40] in words (spec/05-risc-primitives.md:289-302): the first
+    NaN in operand order is selected; otherwise the numerical maximum
+    (minimum), the first operand on every equality (signed zeros equal);
+    the selected operand gets the whole cotangent, the other +0. The
+    selection is read off exact rational order."""
+    rng = np.random.default_rng(12)
+    v = _values(dt, rng)
+    a = np.repeat(v, len(v))
+    b = np.tile(v, len(v))
+    g = (np.arange(a.size) % 251 + 1).astype(np.float64)
+    if dt in ("bf16", "f16"):
+        g = O.narrow_encode(dt, g.astype(np.float32))
+    else:
+        g = g.astype(CAR[dt])
+    for kind in ("max", "min"):
+        left = O.extrema_adjoint(kind, "left", dt, a, b, g)
+        right = O.extrema_adjoint(kind, "right", dt, a, b, g)
+        for i in range(a.size):
+            na, x = _exact(dt, a[i])
+            nb, y = _exact(dt, b[i])
+            if na or nb:
+                pick_left = na
+            else:
+                pick_left = (x >= y) if kind == "max" else (x <= y)
+            gl, gr = (g[i], 0) if pick_left else (0, g[i])
+            assert left.view(np.uint8).reshape(a.size, -1)[i].tobytes() == np.array(
+                [gl], g.dtype).view(np.uint8).tobytes(), (kind, dt, a[i], b[i])
+            assert right.view(np.uint8).reshape(a.size, -1)[i].tobytes() == np.array(
+                [gr], g.dtype).view(np.uint8).tobytes(), (kind, dt, a[i], b[i])
