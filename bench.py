@@ -335,9 +335,9 @@ BW_SET = [
     ("layer_norm_f32_65536x1024", r"layer_norm_kernel<float", 2 * 65536 * 1024 * 4),
     ("relu_f32_16384x4096", r"unary_kernel<float", 2 * 16384 * 4096 * 4),
     ("fused_chain_sqdiff_f32_16384x4096", r"fused_flat_vec_kernel<float", 3 * 16384 * 4096 * 4),
-    ("reduce_sum_rows_f32_16384x4096", r"reduce_rows_vec_kernel<float, \(Rk\)0, \d+, false",
+    ("reduce_sum_rows_f32_16384x4096", r"reduce_rows_vec_kernel<float, \(.*Rk\)0, \d+, false",
      16384 * 4096 * 4 + 16384 * 4),
-    ("reduce_sum_sqdiff_rows_f32_16384x4096", r"reduce_rows_vec_kernel<float, \(Rk\)0, \d+, true",
+    ("reduce_sum_sqdiff_rows_f32_16384x4096", r"reduce_rows_vec_kernel<float, \(.*Rk\)0, \d+, true",
      2 * 16384 * 4096 * 4 + 16384 * 4),
     # two launches per column sum (the 128-leaf groups, then their join):
     # the traffic is their sum
@@ -364,8 +364,10 @@ VALU_SET = [
     ("softmax_f32_16384x1024", r"softmax_kernel<float,[^>]*, true, false>"),
     ("softmax_f64_4096x4096", r"softmax_kernel<double,[^>]*, true, true>"),
     ("softmax_f64_4096x4096_exact", r"softmax_kernel<double,[^>]*, true, false>"),
-    ("gelu_f32_16384x4096", r"unary_kernel<float, \(.*Unary\)0>"),
-    ("dropout_f32_16384x4096", r"unary_kernel<float, \(.*Unary\)3>"),
+    # the binary32 default GELU (Unary 5, GeluFast) and dropout on the
+    # resident streaming map
+    ("gelu_f32_16384x4096", r"unary_stream_kernel<float, \(.*Unary\)5>"),
+    ("dropout_f32_16384x4096", r"unary_stream_kernel<float, \(.*Unary\)3>"),
 ]
 SIMDS = 1024  # 256 CUs x 4 SIMDs
 PROFILE_LAUNCHES = 3

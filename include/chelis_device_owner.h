@@ -2,7 +2,7 @@
  * crates/chelis-backend-hip/runtime/chelis_device_owner.h:16-24, same names,
  * argument meaning and trap behaviour (every invalid input traps `domain`
  * or `overflow` in metadata_plan; a HIP failure aborts). Implemented in
- * chelis_amd/csrc/device_owner.cpp. Differences are internal only: clone
+ * chelis_amd/csrc/device_owner.hip. Differences are internal only: clone
  * and strided host copies run as one device gather on the library stream
  * instead of one hipMemcpy per element. */
 #ifndef CHELIS_DEVICE_OWNER_H
