@@ -415,3 +415,22 @@ def test_skinny_repeatable():
     c0 = C.matmul(da, db).numpy()
     for _ in range(3):
         assert bits_equal(C.matmul(da, db).numpy(), c0)
+
+
+@pytest.mark.parametrize("act", [None, "relu"])
+def test_batched_projection_shape_with_per_batch_bias(act):
+    """Three [4096 x 1024] x [1024 x 1024] f32 products with per-batch bias
+    (the transformer's Q/K/V shape: 768 128-tiles, a round and a half of the
+    resident workgroups): sampled rows of every batch against float64."""
+    rng = np.random.default_rng(46)
+    x = rand(rng, (3, 4096, 1024), np.float32)
+    w = rand(rng, (3, 1024, 1024), np.float32)
+    bias = rand(rng, (3, 1024), np.float32)
+    c = C.linear(C.to_device(x), C.to_device(w), C.to_device(bias), act).numpy()
+    rows = rng.choice(4096, 48, replace=False)
+    for j in range(3):
+        ref = x[j][rows].astype(np.float64) @ w[j].astype(np.float64) + bias[j]
+        if act == "relu":
+            ref = np.maximum(ref, 0.0)
+        got = c[j][rows].astype(np.float64)
+        assert np.abs(got - ref).max() / np.abs(ref).max() <= 1e-5, j
