@@ -209,14 +209,34 @@ def test_batched_broadcast_attention_form():
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
-def test_config_3ab_4096_cube_sampled_rows(dtype):
+def test_config_3ab_4096_cube_every_row(dtype):
+    """Configs 3a / 3b at full size: the canonical-tree product (the exact
+    flag) equals the oracle on sampled rows, and the default MFMA product is
+    within the normwise bar of it on every row, and elementwise on the
+    sampled rows. Over all 16.7M binary32 outputs the MFMA tiles' sequential
+    accumulation along K (error growing as sqrt(K / 4) roundings) leaves the
+    worst entry at about 1.2e-5 relative: measured here as at most 2e-5, with
+    at least 99.999 % of the entries >= rms within 1e-5."""
     seeds = (20, 21) if dtype == np.float32 else (22, 23)
     A = np.random.default_rng(seeds[0]).uniform(-1, 1, (4096, 4096)).astype(dtype)
     B = np.random.default_rng(seeds[1]).uniform(-1, 1, (4096, 4096)).astype(dtype)
-    c = C.matmul(C.to_device(A), C.to_device(B)).numpy()
+    dA, dB = C.to_device(A), C.to_device(B)
+    c = C.matmul(dA, dB).numpy()
     rows = np.random.default_rng(0).choice(4096, 48, replace=False)
     rows = np.concatenate([[0, 127, 128, 4095], rows])
-    check_close(c[rows], O.matmul(np.ascontiguousarray(A[rows]), B), dtype)
+    tree = C.matmul(dA, dB, exact=True).numpy()
+    # the canonical-tree kernels are the oracle's bits on the sampled rows
+    assert bits_equal(tree[rows], O.matmul(np.ascontiguousarray(A[rows]), B))
+    check_close(c[rows], tree[rows], dtype)
+    tol = TOL[dtype]
+    err = np.abs(c.astype(np.float64) - tree)
+    assert err.max() <= tol * np.abs(tree).max()
+    big = np.abs(tree) >= np.sqrt(np.mean(tree.astype(np.float64) ** 2))
+    rel = err[big] / np.abs(tree[big])
+    if dtype == np.float64:
+        assert rel.max() <= tol
+    else:
+        assert rel.max() <= 2 * tol and np.mean(rel > tol) <= 1e-5, (rel.max(), np.mean(rel > tol))
 
 
 @pytest.mark.parametrize("act", [None, "relu", "gelu"])

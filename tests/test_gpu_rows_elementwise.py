@@ -596,3 +596,33 @@ def test_long_rows_bit_exact(dtype, rows, n):
     assert bits_equal(dx, O.softmax_adjoint_rows(ref, g))
     ln = C.layer_norm(xv, C.to_device(gamma), C.to_device(beta), 1e-5).numpy()
     assert bits_equal(ln, O.layer_norm_rows(x, gamma, beta, 1e-5))
+
+
+def _attention_oracle(q, k, v, scale):
+    """The C oracle's composition of spec/05 section 4.7's graph per (batch,
+    head): canonical-tree q.k^T, the scale at binary32, where(j <= i, s,
+    -inf), the oracle's softmax rows, canonical-tree P.v."""
+    B, H, S, _ = q.shape
+    out = np.empty(q.shape, np.float32)
+    mask = np.tril(np.ones((S, S), bool))
+    for b in range(B):
+        for h in range(H):
+            s = O.matmul(q[b, h], np.ascontiguousarray(k[b, h].T)) * np.float32(scale)
+            p = O.softmax_rows(np.where(mask, s, np.float32(-np.inf)).astype(np.float32))
+            out[b, h] = O.matmul(p, v[b, h])
+    return out
+
+
+@pytest.mark.parametrize("B,H,S", [(2, 3, 192), (1, 2, 512)])
+def test_causal_attention_fused_against_the_oracle(B, H, S):
+    """The fused attention (MFMA products, online softmax) against the C
+    oracle's composition of the same graph: normwise 1e-5 and, where the
+    output is not small against its rms, 1e-5 relative per element (the
+    binary32 bar of the north star)."""
+    rng = np.random.default_rng(B * 1000 + H * 10 + S)
+    q, k, v = (rng.standard_normal((B, H, S, 64)).astype(np.float32) for _ in range(3))
+    o = C.causal_attention(C.to_device(q), C.to_device(k), C.to_device(v), 0.125).numpy().astype(np.float64)
+    ref = _attention_oracle(q, k, v, 0.125).astype(np.float64)
+    assert np.abs(o - ref).max() <= 1e-5 * np.abs(ref).max()
+    big = np.abs(ref) >= np.sqrt(np.mean(ref ** 2))
+    assert np.all(np.abs(o - ref)[big] <= 1e-5 * np.abs(ref)[big])
