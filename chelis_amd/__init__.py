@@ -144,6 +144,7 @@ SIGNATURES = {
     "chelis_hip_integer_elementwise": (c_int32, [c_int32, P, P, P, POINTER(NumericFailure)]),
     "chelis_hip_gather": (c_int32, [P, P, c_int32, c_int32, P, POINTER(NumericFailure)]),
     "chelis_hip_take_numeric_failure": (c_int32, [POINTER(NumericFailure)]),
+    "chelis_hip_allocation_counts": (None, [POINTER(c_int64), POINTER(c_int64)]),
     "chelis_hip_set_exact_matmul": (c_int32, [c_int32]),
     "chelis_hip_set_exact": (c_int32, [c_int32]),
     # chelis_dag.h
@@ -571,6 +572,13 @@ def gather(values, indices, axis: int, batch_rank: int = 0, out=None, deferred: 
     check(lib().chelis_hip_gather(_p(values), _p(indices), axis, batch_rank, _p(out),
                                   None if deferred else ctypes.byref(f)), "gather")
     return out, None if deferred else _failure(f)
+
+
+def allocation_counts():
+    """(scratch requests, device allocations) the library has made so far."""
+    a, b = c_int64(0), c_int64(0)
+    lib().chelis_hip_allocation_counts(ctypes.byref(a), ctypes.byref(b))
+    return a.value, b.value
 
 
 def take_numeric_failure():

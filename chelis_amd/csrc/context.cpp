@@ -66,8 +66,18 @@ int size_class(size_t bytes) {
 }
 }  // namespace
 
+namespace {
+std::atomic<int64_t> g_scratch_requests{0}, g_device_allocations{0};
+}  // namespace
+
+hipError_t device_malloc(void **p, size_t bytes) {
+    g_device_allocations.fetch_add(1, std::memory_order_relaxed);
+    return hipMalloc(p, bytes);
+}
+
 void *scratch_alloc(size_t bytes) {
     if (!bytes) return nullptr;
+    g_scratch_requests.fetch_add(1, std::memory_order_relaxed);
     int device = 0;
     if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) return nullptr;
     const int c = size_class(bytes);
@@ -82,7 +92,7 @@ void *scratch_alloc(size_t bytes) {
         }
     }
     void *p = nullptr;
-    if (hipMalloc(&p, size_t(1) << c) != hipSuccess) return nullptr;
+    if (device_malloc(&p, size_t(1) << c) != hipSuccess) return nullptr;
     return p;
 }
 
@@ -112,7 +122,7 @@ int32_t *status_words(int32_t **host) {
     std::lock_guard<std::mutex> lock(g_status_mutex);
     if (!g_status[device]) {
         int32_t *d = nullptr, *h = nullptr;
-        if (hipMalloc(&d, 256) != hipSuccess) return nullptr;
+        if (device_malloc(reinterpret_cast<void **>(&d), 256) != hipSuccess) return nullptr;
         if (hipMemset(d, 0, 256) != hipSuccess || hipDeviceSynchronize() != hipSuccess ||
             hipHostMalloc(&h, sizeof(int32_t), hipHostMallocDefault) != hipSuccess) {
             (void)hipFree(d);
@@ -260,3 +270,8 @@ const char *chelis_hip_build_info(void) {
 }
 
 }  // extern "C"
+
+extern "C" void chelis_hip_allocation_counts(int64_t *scratch_requests, int64_t *device_allocations) {
+    if (scratch_requests) *scratch_requests = chelis::g_scratch_requests.load(std::memory_order_relaxed);
+    if (device_allocations) *device_allocations = chelis::g_device_allocations.load(std::memory_order_relaxed);
+}

@@ -163,7 +163,7 @@ int32_t constant_pool(chelis_dag_program *prog, void **pool) {
             cells[k] = w >= 8 ? v : (v & ((uint64_t(1) << (8 * w)) - 1));  // little-endian: low bytes first
         }
         void *p = nullptr;
-        CHELIS_HIP_TRY(hipMalloc(&p, cells.size() * 8));
+        CHELIS_HIP_TRY(device_malloc(&p, cells.size() * 8));
         const hipError_t e = hipMemcpy(p, cells.data(), cells.size() * 8, hipMemcpyHostToDevice);
         if (e != hipSuccess) {
             (void)hipFree(p);

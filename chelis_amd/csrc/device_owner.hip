@@ -286,7 +286,7 @@ chelis_device_tensor_owner *allocate(chelis_metadata_plan *plan) {
     const int32_t device = device_now();
     void *storage = nullptr;
     if (bytes > 0) {
-        hip_must(hipMalloc(&storage, static_cast<size_t>(bytes)), "hipMalloc");
+        hip_must(chelis::device_malloc(&storage, static_cast<size_t>(bytes)), "hipMalloc");
         const hipStream_t st = library_stream();
         hip_must(hipMemsetAsync(storage, 0, static_cast<size_t>(bytes), st), "hipMemsetAsync");
         hip_must(hipStreamSynchronize(st), "hipStreamSynchronize");

@@ -51,6 +51,9 @@ int32_t *status_words(int32_t **host);
 // the hot path makes no allocation calls. scratch_free takes the size given
 // to scratch_alloc. Returns null when the device cannot allocate.
 void *scratch_alloc(size_t bytes);
+// hipMalloc, counted (chelis_hip_allocation_counts): every device allocation
+// the library makes goes through it.
+hipError_t device_malloc(void **p, size_t bytes);
 void scratch_free(void *p, size_t bytes);
 
 #define CHELIS_HIP_TRY(expr)                                                              \

@@ -149,6 +149,11 @@ int32_t chelis_hip_reduce(int32_t op, const chelis_fused_chain *chain, const che
  * another stream beside a direct call) race on it; calls enqueued on the
  * library stream run in order. */
 #define CHELIS_HIP_STATIC_SCRATCH_BYTES (8u * 1024u * 1024u)
+/* Allocation counters (no counterpart in the reference; for callers and
+ * tests that must know an entry allocates nothing): scratch requests
+ * served by the library's cache or by a new allocation, and device
+ * allocations, each counted since the process started. */
+void chelis_hip_allocation_counts(int64_t *scratch_requests, int64_t *device_allocations);
 int32_t chelis_hip_reduce_static(int32_t op, const chelis_fused_chain *chain, const chelis_gpu_tensor *const *inputs,
                                  int32_t n_inputs, int32_t axis, const chelis_gpu_tensor *out);
 /* kernels.rs:375-557 count: Bool8 -> i64 over one axis. A byte that is not

@@ -1,7 +1,9 @@
 """chelis_hip_reduce_static, the allocation-free reduce entry: its results
 against chelis_hip_reduce's (the entry it mirrors) bit for bit, on two calls
-in a row with the second input smaller, through the C ABI; and the clear
-refusal of a reduction whose partials exceed the fixed array."""
+in a row with the second input smaller, through the C ABI; no scratch
+request and no device allocation across its calls
+(chelis_hip_allocation_counts, which does see the allocating entry's); and
+the clear refusal of a reduction whose partials exceed the fixed array."""
 import numpy as np
 import pytest
 
@@ -37,8 +39,14 @@ def test_static_reduce_matches_the_allocating_entry(op, dtype, shape1, shape2, a
             x = np.round(x * 4) / 4  # ties, so the first-index rule is exercised
         d = C.to_device(x)
         ref = C.reduce(op, d, axis).numpy()
-        got = C.reduce(op, d, axis, static=True).numpy()
-        assert np.array_equal(bits(got), bits(ref)), (op, shape)
+        out = C.empty(ref.shape, ref.dtype)
+        C.synchronize()
+        before = C.allocation_counts()
+        got = C.reduce(op, d, axis, out=out, static=True)
+        C.synchronize()
+        # the entry's defining property: no scratch request, no allocation
+        assert C.allocation_counts() == before, (op, shape)
+        assert np.array_equal(bits(got.numpy()), bits(ref)), (op, shape)
 
 
 def test_static_reduce_chain_leaf_twice():
@@ -50,8 +58,26 @@ def test_static_reduce_chain_leaf_twice():
         dx, dm = C.to_device(x), C.to_device(m)
         mv = dm.view((rows, n), (1, 0))
         ref = C.reduce("sum", [dx, mv], 1, chain=ch).numpy()
-        got = C.reduce("sum", [dx, mv], 1, chain=ch, static=True).numpy()
-        assert np.array_equal(bits(got), bits(ref))
+        out = C.empty(ref.shape, ref.dtype)
+        C.synchronize()
+        before = C.allocation_counts()
+        got = C.reduce("sum", [dx, mv], 1, chain=ch, out=out, static=True)
+        C.synchronize()
+        assert C.allocation_counts() == before
+        assert np.array_equal(bits(got.numpy()), bits(ref))
+
+
+def test_the_counters_see_the_allocating_entry():
+    """A two-pass reduction through chelis_hip_reduce asks for scratch (a
+    cached block or a new one), so the counters the static test relies on
+    do move when an entry allocates."""
+    d = C.to_device(np.ones((64, 1 << 20), np.float32))
+    out = C.empty((64,), np.float32)
+    C.synchronize()
+    before = C.allocation_counts()
+    C.reduce("sum", d, 1, out=out)
+    C.synchronize()
+    assert C.allocation_counts()[0] > before[0]
 
 
 def test_static_reduce_refuses_partials_beyond_the_array():
