@@ -144,6 +144,7 @@ SIGNATURES = {
     "chelis_hip_integer_elementwise": (c_int32, [c_int32, P, P, P, POINTER(NumericFailure)]),
     "chelis_hip_gather": (c_int32, [P, P, c_int32, c_int32, P, POINTER(NumericFailure)]),
     "chelis_hip_take_numeric_failure": (c_int32, [POINTER(NumericFailure)]),
+    "chelis_hip_cumsum": (c_int32, [P, c_int32, c_int32, P, POINTER(NumericFailure)]),
     "chelis_hip_allocation_counts": (None, [POINTER(c_int64), POINTER(c_int64)]),
     "chelis_hip_set_exact_matmul": (c_int32, [c_int32]),
     "chelis_hip_set_exact": (c_int32, [c_int32]),
@@ -581,6 +582,17 @@ def allocation_counts():
     return a.value, b.value
 
 
+def cumsum(x, axis: int, reverse: bool = False, out=None, deferred: bool = False):
+    """chelis_hip_cumsum; returns (out, failure) as cast does. i8 / i16 scan
+    into i32."""
+    ax = axis % len(x.shape)
+    if out is None:
+        out = empty(x.shape, np.int32 if x.dtype in (np.int8, np.int16) else x.dtype)
+    f = NumericFailure()
+    check(lib().chelis_hip_cumsum(_p(x), ax, int(reverse), _p(out), None if deferred else ctypes.byref(f)), "cumsum")
+    return out, None if deferred else _failure(f)
+
+
 def take_numeric_failure():
     """chelis_hip_take_numeric_failure: the earliest deferred failure since
     the last read as (index, kind, trap line), or None; clears the record."""
@@ -704,7 +716,7 @@ class DagProgram:
         kinds = [line.split()[1] for line in self.describe().splitlines() if len(line.split()) > 1]
         self.has_count = "count" in kinds
         # launches that record into the deferred failure record
-        self.has_traps = any(k in ("cast", "integer", "gather") for k in kinds)
+        self.has_traps = any(k in ("cast", "integer", "gather", "cumsum") for k in kinds)
 
     def __del__(self):
         try:

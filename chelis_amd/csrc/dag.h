@@ -67,6 +67,8 @@ enum class Op : uint8_t {
     Gather,
     // the extrema cotangent; keyed draws and emission-time key derivations
     ExtremaAdjoint, UniformLike, KeyFromSeed, SplitKey, FoldIn,
+    // the ordered inclusive scan
+    Cumsum,
     // reductions over one axis
     Sum, MaxReduce, MinReduce, ProdReduce, Argmax, Argmin, Count, Softmax,
     // movement
@@ -128,7 +130,8 @@ struct Node {
     int64_t named_claims = 0;              // ExtentWitness: claims against other witnesses
     std::string compare;            // Compare / Logical kind (snake_case wire name)
     int64_t batch_rank = 0;         // Gather (its axis in `axis`)
-    int32_t code = 0;               // ExtremaAdjoint: min (bit 0), right operand (bit 1); Split: the branch
+    int32_t code = 0;               // ExtremaAdjoint: min (bit 0), right operand (bit 1); Split: the branch;
+                                    // Cumsum: 1 for the decreasing direction (its axis in `axis`)
     Prim const_prec = Prim::Other;  // Const
     uint64_t const_bits = 0;        // float bits, or the integer / bool value
     std::vector<Step> steps;        // FusedElem
@@ -201,7 +204,9 @@ enum class RegionKind : uint8_t {
     Compare, Logical, Where, Cast, Integer, Gather,
     // the extrema cotangent (code: min bit 0, right operand bit 1), a keyed
     // uniform draw
-    ExtremaAdjoint, Uniform
+    ExtremaAdjoint, Uniform,
+    // the ordered scan (axis, code: reverse)
+    Scan
 };
 const char *region_kind_name(RegionKind k);
 

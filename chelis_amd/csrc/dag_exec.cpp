@@ -356,6 +356,9 @@ int32_t run_plan(chelis_dag_program *prog, const chelis_gpu_tensor *const *input
                 s = uniform_like_run(r.key, r.host_key ? nullptr : static_cast<const uint64_t *>(in[0]->data), r.low,
                                      r.high, out);
                 break;
+            case RegionKind::Scan:
+                s = chelis_hip_cumsum(in[0], (int32_t)r.axis, r.code, out, nullptr);
+                break;
             case RegionKind::ExtremaAdjoint:
                 s = chelis_hip_extrema_adjoint(r.code & 1, (r.code >> 1) & 1, in[0], in[1], in[2], out);
                 break;

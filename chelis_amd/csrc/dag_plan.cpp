@@ -67,6 +67,7 @@ const char *region_kind_name(RegionKind k) {
         case RegionKind::Gather: return "gather";
         case RegionKind::ExtremaAdjoint: return "extrema_adjoint";
         case RegionKind::Uniform: return "uniform_like";
+        case RegionKind::Scan: return "cumsum";
     }
     return "?";
 }
@@ -1140,6 +1141,19 @@ struct Planner {
                     r.high = hi;
                     r.host_key = derived_key(n.inputs[3], &r.key);
                     if (!r.host_key) r.in = {n.inputs[3]};
+                    r.out = n.id;
+                    r.covers = {n.id};
+                    claim(r);
+                    continue;
+                }
+                case Op::Cumsum: {
+                    if (n.inputs.size() != 1)
+                        return fail("node " + std::to_string(n.id) + ": Cumsum reads one tensor");
+                    Region r;
+                    r.kind = RegionKind::Scan;
+                    r.axis = n.axis;
+                    r.code = n.code;
+                    r.in = n.inputs;
                     r.out = n.id;
                     r.covers = {n.id};
                     claim(r);

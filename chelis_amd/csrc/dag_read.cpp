@@ -44,7 +44,7 @@ const OpName kOps[] = {
     {"Store", Op::Store}, {"ExtentWitness", Op::ExtentWitness}, {"NamedCast", Op::NamedCast},
     {"Logical", Op::Logical}, {"Mod", Op::Mod}, {"Gather", Op::Gather},
     {"ExtremaAdjoint", Op::ExtremaAdjoint}, {"UniformLike", Op::UniformLike}, {"KeyFromSeed", Op::KeyFromSeed},
-    {"Split", Op::SplitKey}, {"FoldIn", Op::FoldIn},
+    {"Split", Op::SplitKey}, {"FoldIn", Op::FoldIn}, {"Cumsum", Op::Cumsum},
 };
 
 struct PrimName {
@@ -297,6 +297,14 @@ bool read_op(const Json &op, Graph *g, Node *n, std::string *why) {
                 (kind->text != "Max" && kind->text != "Min") || (operand->text != "Left" && operand->text != "Right"))
                 return (*why = "ExtremaAdjoint needs kind Max|Min and operand Left|Right", false);
             n->code = (kind->text == "Min" ? 1 : 0) | (operand->text == "Right" ? 2 : 0);
+            return true;
+        }
+        case Op::Cumsum: {
+            const Json *dir = p.get("direction");  // ScanDirection (dag.rs:819-822)
+            if (!int_of(p.get("axis"), &n->axis) || !dir || dir->kind != Json::String ||
+                (dir->text != "Increasing" && dir->text != "Decreasing"))
+                return (*why = "Cumsum needs axis and direction Increasing|Decreasing", false);
+            n->code = dir->text == "Decreasing" ? 1 : 0;
             return true;
         }
         case Op::SplitKey: {

@@ -440,6 +440,66 @@ __global__ __launch_bounds__(256) void gather_kernel(const U *__restrict__ value
     }
 }
 
+// ---------------------------------------------------------------- ordered scan
+// [05-OP-33] cumsum (kernels.rs:2793 ordered_scan, with the C lane's
+// accumulation, crates/chelis-runtime/src/lib.rs:7020-7105): one thread per
+// scan line of the [outer, n, inner] view - adjacent threads on adjacent
+// inner positions, so the loads of a step are coalesced when inner is wide -
+// walking its n leaves in order (from the end when reverse). The first leaf
+// is the first prefix; each later prefix adds the leaf at the accumulator
+// width (binary32 for bf16 / f16, i32 for i8 / i16); every prefix is stored
+// at the result dtype, NaN canonical. An integer prefix outside the
+// accumulator's range fails overflow, keyed by its place in the C lane's
+// evaluation order (line by line, then step): ((o * inner + j) * n + step);
+// the line then stores zeros.
+template <int DT> struct ScanTypes { using A = float; using R = typename Dt<DT>::S; };
+template <> struct ScanTypes<CHELIS_DTYPE_F64> { using A = double; using R = double; };
+template <> struct ScanTypes<CHELIS_DTYPE_I8> { using A = int32_t; using R = int32_t; };
+template <> struct ScanTypes<CHELIS_DTYPE_I16> { using A = int32_t; using R = int32_t; };
+template <> struct ScanTypes<CHELIS_DTYPE_I32> { using A = int32_t; using R = int32_t; };
+template <> struct ScanTypes<CHELIS_DTYPE_I64> { using A = int64_t; using R = int64_t; };
+
+template <int DT>
+__global__ __launch_bounds__(256) void cumsum_kernel(const typename Dt<DT>::S *__restrict__ x, View8 xv,
+                                                     typename ScanTypes<DT>::R *__restrict__ y, int64_t outer,
+                                                     int64_t n, int64_t inner, int reverse, uint64_t seq,
+                                                     unsigned long long *rec) {
+    using A = typename ScanTypes<DT>::A;
+    using R = typename ScanTypes<DT>::R;
+    const int64_t lines = outer * inner, stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t base = (int64_t)blockIdx.x * blockDim.x; base < lines; base += stride) {
+        const int64_t t = base + threadIdx.x;
+        unsigned long long k = 0ull;
+        if (t < lines) {
+            const int64_t o = t / inner, j = t % inner;
+            A acc = A(0);
+            bool failed = false;
+            for (int64_t step = 0; step < n; ++step) {
+                const int64_t pos = reverse ? n - 1 - step : step;
+                const int64_t f = (o * n + pos) * inner + j;
+                const typename Dt<DT>::S raw = x[logical_offset(xv, f)];
+                if constexpr (Dt<DT>::kFloat) {
+                    const A v = (A)semantic<DT>(raw);
+                    acc = canon(step == 0 ? v : acc + v);
+                    if constexpr (DT == CHELIS_DTYPE_BF16) y[f] = f32_to_bf16(acc);
+                    else if constexpr (DT == CHELIS_DTYPE_F16) y[f] = f32_to_f16(acc);
+                    else y[f] = acc;
+                } else {
+                    const A v = (A)raw;
+                    A r = v;
+                    if (!failed && step > 0 && __builtin_add_overflow(acc, v, &r)) {
+                        failed = true;
+                        k = fail_key(seq, t * n + step, kOverflow);
+                    }
+                    acc = failed ? A(0) : r;
+                    y[f] = (R)acc;
+                }
+            }
+        }
+        if constexpr (!Dt<DT>::kFloat) merge_failures(k, rec);
+    }
+}
+
 // ---------------------------------------------------------------- host: the failure channel
 // Per device: word [2..3] of the status words is the deferred record, [4..5]
 // the record of a call that waits for its own result. A deferred launch's
@@ -845,6 +905,54 @@ extern "C" int32_t chelis_hip_gather(const chelis_gpu_tensor *values, const chel
         case 2: st = launch_gather<uint16_t>(values, indices, out, g, sink); break;
         case 4: st = launch_gather<uint32_t>(values, indices, out, g, sink); break;
         default: st = launch_gather<uint64_t>(values, indices, out, g, sink); break;
+    }
+    if (st) return st;
+    return close_sink(sink, label, failure);
+}
+
+namespace {
+template <int DT>
+int32_t launch_cumsum(const chelis_gpu_tensor *x, const chelis_gpu_tensor *out, int64_t outer, int64_t n,
+                      int64_t inner, int32_t reverse, const Sink &s) {
+    hipStream_t st = stream();
+    if (!st) return set_error(CHELIS_HIP_EHIP, "no HIP device");
+    const int64_t lines = outer * inner;
+    if (!lines || !n) return CHELIS_HIP_OK;
+    cumsum_kernel<DT><<<dim3((unsigned)map_blocks(lines)), dim3(256), 0, st>>>(
+        static_cast<const typename Dt<DT>::S *>(x->data), view_of(x),
+        static_cast<typename ScanTypes<DT>::R *>(out->data), outer, n, inner, reverse, s.seq, s.rec);
+    CHELIS_LAUNCH_CHECK();
+    return CHELIS_HIP_OK;
+}
+}  // namespace
+
+extern "C" int32_t chelis_hip_cumsum(const chelis_gpu_tensor *x, int32_t axis, int32_t reverse,
+                                     const chelis_gpu_tensor *out, chelis_hip_numeric_failure *failure) {
+    if (int32_t s = check_tensor(x, "x")) return s;
+    if (int32_t s = check_out(out, "cumsum")) return s;
+    if (x->dtype == CHELIS_DTYPE_BOOL || !is_castable(x->dtype))
+        return set_error(CHELIS_HIP_EDOMAIN, "cumsum: a signed integer or float operand");
+    if (axis < 0 || axis >= x->rank) return set_error(CHELIS_HIP_EDOMAIN, "cumsum: axis %d outside the rank", axis);
+    const chelis_dtype rdt = (x->dtype == CHELIS_DTYPE_I8 || x->dtype == CHELIS_DTYPE_I16) ? CHELIS_DTYPE_I32 : x->dtype;
+    if (out->dtype != rdt) return set_error(CHELIS_HIP_EDOMAIN, "cumsum: the result dtype is %s", dtype_name(rdt));
+    if (!same_shape(x, out)) return set_error(CHELIS_HIP_EDOMAIN, "cumsum: the result has the operand's shape");
+    int64_t outer = 1, inner = 1;
+    for (int32_t a = 0; a < axis; ++a) outer *= x->shape[a];
+    for (int32_t a = axis + 1; a < x->rank; ++a) inner *= x->shape[a];
+    const int64_t n = x->shape[axis];
+    const std::string label = std::string("cumsum at ") + dtype_name(rdt);
+    Sink sink;
+    if (int32_t s = open_sink(failure != nullptr, label, &sink)) return s;
+    int32_t st;
+    switch (x->dtype) {
+        case CHELIS_DTYPE_F32: st = launch_cumsum<CHELIS_DTYPE_F32>(x, out, outer, n, inner, reverse, sink); break;
+        case CHELIS_DTYPE_F64: st = launch_cumsum<CHELIS_DTYPE_F64>(x, out, outer, n, inner, reverse, sink); break;
+        case CHELIS_DTYPE_BF16: st = launch_cumsum<CHELIS_DTYPE_BF16>(x, out, outer, n, inner, reverse, sink); break;
+        case CHELIS_DTYPE_F16: st = launch_cumsum<CHELIS_DTYPE_F16>(x, out, outer, n, inner, reverse, sink); break;
+        case CHELIS_DTYPE_I8: st = launch_cumsum<CHELIS_DTYPE_I8>(x, out, outer, n, inner, reverse, sink); break;
+        case CHELIS_DTYPE_I16: st = launch_cumsum<CHELIS_DTYPE_I16>(x, out, outer, n, inner, reverse, sink); break;
+        case CHELIS_DTYPE_I32: st = launch_cumsum<CHELIS_DTYPE_I32>(x, out, outer, n, inner, reverse, sink); break;
+        default: st = launch_cumsum<CHELIS_DTYPE_I64>(x, out, outer, n, inner, reverse, sink); break;
     }
     if (st) return st;
     return close_sink(sink, label, failure);

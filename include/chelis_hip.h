@@ -262,6 +262,19 @@ int32_t chelis_hip_integer_elementwise(int32_t op, const chelis_gpu_tensor *a, c
                                        const chelis_gpu_tensor *out, chelis_hip_numeric_failure *failure);
 int32_t chelis_hip_gather(const chelis_gpu_tensor *values, const chelis_gpu_tensor *indices, int32_t axis,
                           int32_t batch_rank, const chelis_gpu_tensor *out, chelis_hip_numeric_failure *failure);
+/* cumsum: RiscOp::Cumsum{axis, direction} ([05-OP-33]; the reference HIP
+ * lane's ordered_scan, kernels.rs:2793, with the C lane's accumulation,
+ * crates/chelis-runtime/src/lib.rs:7020-7105): an inclusive scan along
+ * `axis`, from the end when `reverse` (the decreasing direction). The first
+ * leaf is the first prefix; each later one adds the leaf at the accumulator
+ * width - binary32 for bf16 / f16, i32 for i8 / i16 (whose result is i32),
+ * the dtype otherwise - and each prefix is stored at the result dtype, NaN
+ * canonical. An integer prefix out of range fails `overflow`
+ * (`numeric trap: overflow in cumsum at <result dtype>`); the failure's
+ * index is then the prefix's place in the scan's evaluation order (line by
+ * line: ((o * inner + j) * n + step)), the order the C lane traps in. */
+int32_t chelis_hip_cumsum(const chelis_gpu_tensor *x, int32_t axis, int32_t reverse, const chelis_gpu_tensor *out,
+                          chelis_hip_numeric_failure *failure);
 /* Waits for the library stream, then reads and clears the current device's
  * deferred failure record (kind 0: none). */
 int32_t chelis_hip_take_numeric_failure(chelis_hip_numeric_failure *failure);

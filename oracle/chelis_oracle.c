@@ -1021,3 +1021,56 @@ int64_t orc_gather(const void *values, int64_t width, int64_t before, int64_t ax
     }
     return first;
 }
+
+/* [05-OP-33] ordered inclusive scan along the middle axis of a contiguous
+ * [outer, n, inner] tensor: the C lane's chelis_tensor_cumsum
+ * (crates/chelis-runtime/src/lib.rs:7020-7105). Per line, in the order
+ * outer, inner, step: the first leaf is the first prefix (NaN canonical),
+ * each later prefix is the previous one plus the leaf at the accumulator
+ * width - binary32 for bf16 / f16, i32 for i8 / i16, the dtype otherwise -
+ * and each prefix is stored at the result dtype (bf16 / f16 rounded from the
+ * binary32 prefix; i8 / i16 scan into i32). reverse scans each line from its
+ * end (the decreasing direction, crates/chelis-backend-c/src/emit.rs:
+ * 8000-8075). An integer prefix outside the accumulator's range fails
+ * overflow; the return is that prefix's position in the evaluation order
+ * ((o * inner + j) * n + step), or -1. */
+int64_t orc_cumsum(int dt, const void *x, void *y, int64_t outer, int64_t n, int64_t inner, int reverse,
+                   int32_t *kind) {
+    int64_t first = -1;
+    *kind = 0;
+    const int idt = (dt == ODT_I8 || dt == ODT_I16) ? ODT_I32 : dt;  /* result dtype */
+    int64_t lo, hi;
+    odt_limits(idt == ODT_I64 ? ODT_I64 : ODT_I32, &lo, &hi);
+    for (int64_t o = 0; o < outer; ++o)
+        for (int64_t j = 0; j < inner; ++j) {
+            double facc = 0.0;
+            float sacc = 0.0f;
+            int64_t iacc = 0;
+            for (int64_t step = 0; step < n; ++step) {
+                const int64_t pos = reverse ? n - 1 - step : step;
+                const int64_t f = (o * n + pos) * inner + j;
+                if (dt == ODT_F64) {
+                    const double v = ((const double *)x)[f];
+                    facc = nan64(step == 0 ? v : facc + v);
+                    ((double *)y)[f] = facc;
+                } else if (odt_is_float(dt)) {
+                    const float v = (float)odt_float_at(dt, x, f);
+                    sacc = nan32(step == 0 ? v : sacc + v);
+                    if (dt == ODT_F32) ((float *)y)[f] = sacc;
+                    else ((uint16_t *)y)[f] = orc_enc16(dt == ODT_BF16 ? 0 : 1, sacc);
+                } else {
+                    const int64_t v = odt_int_at(dt, x, f);
+                    int64_t r = v;
+                    int fail = 0;
+                    if (step > 0) fail = __builtin_add_overflow(iacc, v, &r) || r < lo || r > hi;
+                    if (fail && first < 0) {
+                        first = (o * inner + j) * n + step;
+                        *kind = OFAIL_OVERFLOW;
+                    }
+                    iacc = fail ? 0 : r;
+                    odt_int_store(idt, y, f, iacc);
+                }
+            }
+        }
+    return first;
+}

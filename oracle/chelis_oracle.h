@@ -141,6 +141,8 @@ void orc_extrema_adjoint(int is_min, int right, int dt, const void *a, const voi
 int64_t orc_cast(int src, int dst, const void *x, void *y, int64_t n, int32_t *kind);
 int64_t orc_int_binary(int op, int dt, const void *a, const void *b, void *y, int64_t n, int32_t *kind);
 int64_t orc_int_unary(int op, int dt, const void *x, void *y, int64_t n, int32_t *kind);
+int64_t orc_cumsum(int dt, const void *x, void *y, int64_t outer, int64_t n, int64_t inner, int reverse,
+                   int32_t *kind);
 int64_t orc_gather(const void *values, int64_t width, int64_t before, int64_t axis_size, int64_t after,
                    const void *idx, int idx_dt, int64_t index_count, int64_t batch_count, void *out, int32_t *kind);
 

@@ -101,6 +101,7 @@ def _declare(L):
         "orc_extrema_adjoint": (None, [ctypes.c_int, ctypes.c_int, ctypes.c_int, c_p, c_p, c_p, c_p, c_i64]),
         "orc_int_binary": (c_i64, [ctypes.c_int, ctypes.c_int, c_p, c_p, c_p, c_i64, c_p]),
         "orc_int_unary": (c_i64, [ctypes.c_int, ctypes.c_int, c_p, c_p, c_i64, c_p]),
+        "orc_cumsum": (c_i64, [ctypes.c_int, c_p, c_p, c_i64, c_i64, c_i64, ctypes.c_int, c_p]),
         "orc_gather": (c_i64, [c_p, c_i64, c_i64, c_i64, c_i64, c_p, ctypes.c_int, c_i64, c_i64, c_p, c_p]),
     })
     for name, (res, args) in sig.items():
@@ -487,3 +488,19 @@ def gather(values: np.ndarray, indices: np.ndarray, axis: int, batch_rank: int =
                              2 if indices.dtype == np.int32 else 4, index_count, batch, _ptr(out),
                              ctypes.byref(kind))
     return out, first, kind.value
+
+
+def cumsum(dt: str, x, axis: int, reverse: bool = False):
+    """(result, first failing position in the evaluation order or -1, kind):
+    [05-OP-33]'s ordered scan, the C lane's accumulation. i8 / i16 scan into
+    i32."""
+    x = _carrier(dt, x)
+    ax = axis % x.ndim
+    outer = int(np.prod(x.shape[:ax], dtype=np.int64))
+    inner = int(np.prod(x.shape[ax + 1:], dtype=np.int64))
+    rdt = "i32" if dt in ("i8", "i16") else dt
+    y = np.empty(x.shape, CARRIERS[rdt])
+    kind = ctypes.c_int32(0)
+    first = lib().orc_cumsum(DTYPE_IDS[dt], _ptr(x), _ptr(y), outer, x.shape[ax], inner, int(reverse),
+                             ctypes.byref(kind))
+    return y, first, kind.value

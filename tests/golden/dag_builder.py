@@ -135,6 +135,13 @@ class Dag:
         (dag.rs:949-952, 596-606)."""
         return self.node({"ExtremaAdjoint": {"kind": kind, "operand": operand}}, [a, b, g], self.dims(g), self.prec(g))
 
+    def cumsum(self, x, axis, direction="Increasing"):
+        """RiscOp::Cumsum{axis, direction} (dag.rs:1408-1411); i8 / i16 scan
+        into i32."""
+        p = self.prec(x)
+        return self.node({"Cumsum": {"axis": axis, "direction": direction}}, [x], self.dims(x),
+                         "i32" if p in ("i8", "i16") else p)
+
     # ---- keys and draws (dag.rs:995-1060) ----
     def key_from_seed(self, seed: int):
         return self.node("KeyFromSeed", [self.const(seed, [], "i64")], [], "key")
@@ -493,6 +500,16 @@ def draws_program(R, N, seed=1234):
     return g
 
 
+def scan_program(R, N):
+    """Ordered scans: running sums along rows and, from the end, along
+    columns (f32), and an i64 running total."""
+    g = Dag("scans")
+    x = g.load("x", [R, N], "f32")
+    c = g.load("c", [R], "i64")
+    g.roots = [g.cumsum(x, 1), g.cumsum(x, 0, "Decreasing"), g.cumsum(c, 0)]
+    return g
+
+
 def extrema_adjoint_program(R, N):
     g = Dag("extrema_adjoints")
     a = g.load("a", [R, N], "f32")
@@ -523,6 +540,7 @@ FIXTURES = {
     "gathers_50000x64_4096x10": lambda: gather_program(50000, 64, 4096, 10),
     "draws_f32_1024x512": lambda: draws_program(1024, 512),
     "extrema_adjoints_f32_4096x1024": lambda: extrema_adjoint_program(4096, 1024),
+    "scans_f32_512x1024": lambda: scan_program(512, 1024),
 }
 
 OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "dags")

@@ -614,3 +614,14 @@ def test_draw_keys_derive_while_planning_or_are_refused():
         C.DagProgram(g.json())
     p = C.DagProgram(open(os.path.join(DAGS, "extrema_adjoints_f32_4096x1024.json")).read())
     assert region_kinds(p) == ["extrema_adjoint"] * 3
+
+
+def test_cumsum_plans_as_a_scan_and_reads_back_verbatim():
+    p = C.DagProgram(open(os.path.join(DAGS, "scans_f32_512x1024.json")).read())
+    assert region_kinds(p) == ["cumsum"] * 3
+    g = DB.Dag("scan")
+    x = g.load("x", [3, 4], "i8")
+    g.roots = [g.cumsum(x, 0, "Decreasing")]
+    out = json.loads(C.dag_fuse(g.json()))
+    assert out["nodes"][1]["op"] == {"Cumsum": {"axis": 0, "direction": "Decreasing"}}
+    assert out["nodes"][1]["output_type"]["precision"] == "Int32"

@@ -253,3 +253,22 @@ def test_extrema_adjoints_bit_exact(path):
             O.extrema_adjoint("min", "left", "f32", a, b, g)]
     for x, y in zip(got, want):
         assert bits(x) == bits(y)
+
+
+@pytest.mark.parametrize("path", ["dag", "device", "host"])
+def test_scans_bit_exact(path):
+    rng = np.random.default_rng(66)
+    x = rng.standard_normal((512, 1024)).astype(np.float32)
+    c = rng.integers(-10 ** 12, 10 ** 12, 512).astype(np.int64)
+    got = run_all("scans_f32_512x1024", [x, c])[path]
+    want = [O.cumsum("f32", x, 1)[0], O.cumsum("f32", x, 0, reverse=True)[0], O.cumsum("i64", c, 0)[0]]
+    for g, w in zip(got, want):
+        assert bits(g) == bits(w)
+
+
+def test_scan_overflow_traps_through_the_dag_run():
+    x = np.zeros((512, 1024), np.float32)
+    c = np.zeros(512, np.int64)
+    c[[7, 8]] = np.iinfo(np.int64).max
+    with pytest.raises(C.ChelisError, match="^numeric trap: overflow in cumsum at i64$"):
+        run_dag("scans_f32_512x1024", [x, c])

@@ -270,3 +270,41 @@ def test_extrema_adjoint_every_kind_and_operand(dt):
             out = C.extrema_adjoint(k, side, da, db, dg)
             want = O.extrema_adjoint(k, side, dt, oracle_carrier(dt, a), oracle_carrier(dt, b), oracle_carrier(dt, g))
             assert bits(out.numpy()).tobytes() == bits(want).tobytes(), (dt, kind, operand)
+
+
+# ---------------------------------------------------------------- ordered scan
+@pytest.mark.parametrize("dt", ["f32", "f64", "bf16", "f16", "i8", "i16", "i32", "i64"])
+@pytest.mark.parametrize("reverse", [False, True])
+def test_cumsum_every_dtype_axis_and_direction(dt, reverse):
+    rng = np.random.default_rng(70 + DTS.index(dt))
+    if dt in ("f32", "f64"):
+        x = (rng.standard_normal((6, 333, 70)) * 10.0 ** rng.integers(-3, 4, (6, 333, 70))).astype(NP[dt])
+        x[0, 5, 3] = np.nan
+    elif dt in ("bf16", "f16"):
+        x = O.narrow_encode(dt, rng.standard_normal((6, 333, 70)).astype(np.float32))
+        x = x.view(np.float16) if dt == "f16" else x
+    else:
+        x = rng.integers(-100, 100, (6, 333, 70)).astype(NP[dt])
+    dx = C.to_device(x)
+    for axis in range(3):
+        want, first, _ = O.cumsum(dt, oracle_carrier(dt, x), axis, reverse)
+        out, failure = C.cumsum(dx, axis, reverse)
+        assert first == -1 and failure is None
+        assert bits(out.numpy()).tobytes() == bits(want).tobytes(), (dt, axis, reverse)
+
+
+def test_cumsum_overflow_in_the_lanes_order_and_a_strided_view():
+    big = np.iinfo(np.int64).max
+    x = np.zeros((4, 10, 3), np.int64)
+    x[2, 0, 1], x[2, 1, 1] = big, 1       # line (o=2, j=1) overflows at step 1
+    x[3, 0, 0], x[3, 4, 0] = big, 1       # a later line
+    want, first, kind = O.cumsum("i64", x, 1)
+    out, failure = C.cumsum(C.to_device(x), 1)
+    assert failure == (first, kind, "numeric trap: overflow in cumsum at i64") and first == (2 * 3 + 1) * 10 + 1
+    assert np.array_equal(out.numpy(), want)
+    rng = np.random.default_rng(71)
+    base = rng.standard_normal((64, 48)).astype(np.float32)
+    d = C.to_device(base)
+    v = d.view((48, 64), (1, 48))  # the transpose
+    out, failure = C.cumsum(v, 1)
+    assert failure is None and bits(out.numpy()).tobytes() == bits(O.cumsum("f32", np.ascontiguousarray(base.T), 1)[0]).tobytes()

@@ -457,3 +457,62 @@ def test_extrema_adjoint_routes_the_cotangent_to_the_selected_operand(dt):
                 [gl], g.dtype).view(np.uint8).tobytes(), (kind, dt, a[i], b[i])
             assert right.view(np.uint8).reshape(a.size, -1)[i].tobytes() == np.array(
                 [gr], g.dtype).view(np.uint8).tobytes(), (kind, dt, a[i], b[i])
+
+
+# ---------------------------------------------------------------- ordered scan
+def _bf16_rne(f32):
+    b = f32.view(np.uint32).astype(np.uint64)
+    up = (b + 0x7FFF + ((b >> 16) & 1)) >> 16
+    return up.astype(np.uint16)
+
+
+@pytest.mark.parametrize("dt", ["f32", "f64", "bf16", "f16"])
+@pytest.mark.parametrize("reverse", [False, True])
+def test_cumsum_floats_are_the_sequential_left_fold(dt, reverse):
+    """[05-OP-33]: numpy's add.accumulate (a sequential fold) at the
+    accumulator width - binary32 for the 16-bit dtypes, each prefix then
+    rounded to nearest even - along either direction; a -0 first leaf stays
+    -0 (no base is added)."""
+    rng = np.random.default_rng(13)
+    x = (rng.standard_normal((5, 300, 7)) * 10.0 ** rng.integers(-3, 4, (5, 300, 7)))
+    x[0, 0, 0] = -0.0
+    for axis in range(3):
+        if dt in ("f32", "f64"):
+            xv = x.astype(CAR[dt])
+            acc = np.flip(np.cumsum(np.flip(xv, axis), axis, dtype=CAR[dt]), axis) if reverse else np.cumsum(
+                xv, axis, dtype=CAR[dt])
+            got, first, _ = O.cumsum(dt, xv, axis, reverse)
+            want = acc
+        else:
+            bits = O.narrow_encode(dt, x.astype(np.float32))
+            f = O.narrow_decode(dt, bits)
+            acc = np.flip(np.cumsum(np.flip(f, axis), axis, dtype=np.float32), axis) if reverse else np.cumsum(
+                f, axis, dtype=np.float32)
+            want = acc.astype(np.float16).view(np.uint16) if dt == "f16" else _bf16_rne(acc)
+            got, first, _ = O.cumsum(dt, bits, axis, reverse)
+        assert first == -1
+        assert got.tobytes() == want.tobytes(), (dt, axis, reverse)
+    got, _, _ = O.cumsum("f32", np.array([-0.0, -0.0], np.float32), 0)
+    assert got.view(np.uint32).tolist() == [0x80000000, 0x80000000]
+    got, _, _ = O.cumsum("f32", np.array([1.0, np.nan, 2.0], np.float32), 0)
+    assert got.view(np.uint32).tolist()[1:] == [0x7FC00000, 0x7FC00000]
+
+
+@pytest.mark.parametrize("dt", ["i8", "i16", "i32", "i64"])
+def test_cumsum_integers_exact_with_the_overflow_trap(dt):
+    """Python's unbounded integers; i8 / i16 scan into i32; the first
+    overflowing prefix in the evaluation order (line by line)."""
+    rng = np.random.default_rng(14)
+    info = np.iinfo(CAR[dt])
+    x = rng.integers(info.min, info.max, (4, 50, 3), dtype=CAR[dt], endpoint=True)
+    if dt in ("i32", "i64"):
+        x = (x // 1000).astype(CAR[dt])
+    got, first, kind = O.cumsum(dt, x, 1)
+    want = np.cumsum(x.astype(object), 1)
+    assert first == -1 and got.tolist() == want.tolist()
+    assert got.dtype == (np.int32 if dt in ("i8", "i16", "i32") else np.int64)
+    if dt in ("i32", "i64"):
+        big = np.iinfo(CAR[dt]).max
+        y = np.array([[[1], [big], [5]], [[0], [0], [0]]], CAR[dt])  # [2, 3, 1]: line 0 overflows at step 1
+        _, first, kind = O.cumsum(dt, y, 1)
+        assert (first, O.trap_text(kind, "cumsum", dt)) == (1, f"numeric trap: overflow in cumsum at {dt}")
