@@ -145,6 +145,7 @@ SIGNATURES = {
     "chelis_hip_gather": (c_int32, [P, P, c_int32, c_int32, P, POINTER(NumericFailure)]),
     "chelis_hip_take_numeric_failure": (c_int32, [POINTER(NumericFailure)]),
     "chelis_hip_cumsum": (c_int32, [P, c_int32, c_int32, P, POINTER(NumericFailure)]),
+    "chelis_hip_pad": (c_int32, [P, POINTER(c_int64), ctypes.c_uint64, P]),
     "chelis_hip_allocation_counts": (None, [POINTER(c_int64), POINTER(c_int64)]),
     "chelis_hip_set_exact_matmul": (c_int32, [c_int32]),
     "chelis_hip_set_exact": (c_int32, [c_int32]),
@@ -504,7 +505,7 @@ def trap_status() -> int:
 COMPARE_KINDS = {"cmp_lt": 0, "lt": 1, "eq": 2, "neq": 3, "gt": 4, "gte": 5, "lte": 6}
 LOGICAL_KINDS = {"and": 0, "or": 1, "not": 2}
 INT_OPS = {"add": 0, "sub": 1, "mul": 2, "floor_div": 3, "trunc_div": 4, "mod": 5, "max_elem": 6, "min_elem": 7,
-           "neg": 8, "abs": 9}
+           "neg": 8, "abs": 9, "bitand": 10, "bitor": 11, "bitxor": 12, "shl": 13, "shr": 14}
 
 
 def _bshape(*ts):
@@ -591,6 +592,19 @@ def cumsum(x, axis: int, reverse: bool = False, out=None, deferred: bool = False
     f = NumericFailure()
     check(lib().chelis_hip_cumsum(_p(x), ax, int(reverse), _p(out), None if deferred else ctypes.byref(f)), "cumsum")
     return out, None if deferred else _failure(f)
+
+
+def pad(x, lo, hi, fill, out=None):
+    """chelis_hip_pad: lo / hi elements before / after each axis; `fill` a
+    value of x's dtype (bf16 as its 16-bit pattern)."""
+    lo, hi = [int(v) for v in lo], [int(v) for v in hi]
+    shape = tuple(int(e) + a + b for e, a, b in zip(x.shape, lo, hi))
+    out = out or empty(shape, x.dtype)
+    carrier = np.uint16 if x.dtype == np.uint16 else x.dtype
+    bits = np.array([fill], carrier).view(np.dtype("u%d" % np.dtype(carrier).itemsize))[0]
+    arr = (ctypes.c_int64 * max(1, len(lo)))(*lo)
+    check(lib().chelis_hip_pad(_p(x), arr, int(bits), _p(out)), "pad")
+    return out
 
 
 def take_numeric_failure():

@@ -69,6 +69,11 @@ enum class Op : uint8_t {
     ExtremaAdjoint, UniformLike, KeyFromSeed, SplitKey, FoldIn,
     // the ordered inclusive scan
     Cumsum,
+    // two's-complement bitwise ops and shifts (code: the kind)
+    Bitwise,
+    // movement with bounds: pad (a materialized copy), shrink and stride
+    // (views)
+    Pad, Shrink, Stride,
     // reductions over one axis
     Sum, MaxReduce, MinReduce, ProdReduce, Argmax, Argmin, Count, Softmax,
     // movement
@@ -96,6 +101,7 @@ struct Step {
 // from a node value, or the to-the-end sentinel); Node::extent_error says
 // which, and the planner refuses it.
 constexpr int64_t kUnboundExtent = -1;
+constexpr int64_t kToEnd = INT64_MIN;  // a shrink's to-the-end bound
 inline bool extent_is_symbol(int64_t e) { return e <= -2; }
 inline int64_t symbol_extent(int64_t symbol) { return -2 - symbol; }
 inline int64_t extent_symbol(int64_t e) { return -2 - e; }
@@ -131,7 +137,12 @@ struct Node {
     std::string compare;            // Compare / Logical kind (snake_case wire name)
     int64_t batch_rank = 0;         // Gather (its axis in `axis`)
     int32_t code = 0;               // ExtremaAdjoint: min (bit 0), right operand (bit 1); Split: the branch;
-                                    // Cumsum: 1 for the decreasing direction (its axis in `axis`)
+                                    // Cumsum: 1 for the decreasing direction (its axis in `axis`);
+                                    // Bitwise: 0 and, 1 or, 2 xor, 3 shift left, 4 shift right
+    // Pad: elements added before / after each axis (fill in const_*);
+    // Shrink: start / end per axis (end kToEnd: the axis' end); Stride: the
+    // step per axis. Extent codes as in dims.
+    std::vector<int64_t> lo, hi, step;
     Prim const_prec = Prim::Other;  // Const
     uint64_t const_bits = 0;        // float bits, or the integer / bool value
     std::vector<Step> steps;        // FusedElem
@@ -205,8 +216,8 @@ enum class RegionKind : uint8_t {
     // the extrema cotangent (code: min bit 0, right operand bit 1), a keyed
     // uniform draw
     ExtremaAdjoint, Uniform,
-    // the ordered scan (axis, code: reverse)
-    Scan
+    // the ordered scan (axis, code: reverse); a pad (lo, fill)
+    Scan, Pad
 };
 const char *region_kind_name(RegionKind k);
 
@@ -243,6 +254,9 @@ struct Region {
     double low = 0.0, high = 0.0;
     bool host_key = false;
     uint64_t key = 0;
+    // pad: elements before each axis and the fill's bits
+    std::vector<int64_t> lo;
+    uint64_t fill = 0;
     std::vector<int64_t> outputs() const {
         std::vector<int64_t> o{out};
         o.insert(o.end(), more_out.begin(), more_out.end());

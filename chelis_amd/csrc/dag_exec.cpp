@@ -306,6 +306,33 @@ int32_t run_plan(chelis_dag_program *prog, const chelis_gpu_tensor *const *input
                                              "dag: node %lld reshapes a view that is not one run of memory",
                                              (long long)n.id);
                         break;
+                    case Op::Shrink:
+                    case Op::Stride: {
+                        // element o of the view is element o * step + start of
+                        // its operand; the bounds are checked against the
+                        // operand's extents as they are at run time
+                        const bool shrink = n.op == Op::Shrink;
+                        int64_t offset = 0;
+                        p.strides = b.strides;
+                        for (size_t a = 0; a < dims.size(); ++a) {
+                            const int64_t start = shrink ? n.lo[a] : 0, step = shrink ? 1 : n.step[a];
+                            const int64_t end = shrink ? (n.hi[a] == kToEnd ? b.shape[a] : n.hi[a]) : 0;
+                            const bool ok = shrink ? (start <= end && end <= b.shape[a] && dims[a] == end - start)
+                                                   : (dims[a] == (b.shape[a] + step - 1) / step);
+                            if (!ok)
+                                return set_error(CHELIS_HIP_EDOMAIN,
+                                                 "dag: node %lld: %s bounds do not fit its operand's extent %lld on "
+                                                 "axis %zu",
+                                                 (long long)n.id, shrink ? "shrink" : "stride",
+                                                 (long long)b.shape[a], a);
+                            if (dims[a] > 0) offset += start * b.strides[a];
+                            p.strides[a] = b.strides[a] * step;
+                        }
+                        const int64_t bytes = offset * prim_width(n.prec);
+                        p.t.data = static_cast<char *>(b.t.data) + bytes;
+                        p.t.byte_capacity = b.t.byte_capacity - bytes;
+                        break;
+                    }
                     default:  // Realize / Copy / Store: the same bytes
                         p.strides = b.strides;
                         break;
@@ -356,6 +383,7 @@ int32_t run_plan(chelis_dag_program *prog, const chelis_gpu_tensor *const *input
                 s = uniform_like_run(r.key, r.host_key ? nullptr : static_cast<const uint64_t *>(in[0]->data), r.low,
                                      r.high, out);
                 break;
+            case RegionKind::Pad: s = chelis_hip_pad(in[0], r.lo.data(), r.fill, out); break;
             case RegionKind::Scan:
                 s = chelis_hip_cumsum(in[0], (int32_t)r.axis, r.code, out, nullptr);
                 break;

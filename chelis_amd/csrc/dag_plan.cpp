@@ -68,6 +68,7 @@ const char *region_kind_name(RegionKind k) {
         case RegionKind::ExtremaAdjoint: return "extrema_adjoint";
         case RegionKind::Uniform: return "uniform_like";
         case RegionKind::Scan: return "cumsum";
+        case RegionKind::Pad: return "pad";
     }
     return "?";
 }
@@ -356,6 +357,36 @@ struct Planner {
     bool fail(const std::string &what) {
         if (error.empty()) error = what;
         return false;
+    }
+    // A Pad, Shrink or Stride this build cannot run: bounds read from node
+    // values (RtDim::Node), a rank that differs from its operand's, or
+    // literal bounds that do not produce the node's literal extents
+    // (spec/05-risc-primitives.md section 2.4.1: a negative bound, a shrink
+    // past its operand, a step below one).
+    std::string window_error(const Node &n) const {
+        if (n.inputs.size() != 1) return n.variant + " with bounds read from node values (run-time bounds)";
+        const Node &src = N(n.inputs[0]);
+        const size_t rk = src.dims.size();
+        const std::vector<int64_t> &first = n.op == Op::Stride ? n.step : n.lo;
+        if (first.size() != rk || n.dims.size() != rk) return n.variant + " bounds do not match its operand's rank";
+        for (size_t a = 0; a < rk; ++a) {
+            const int64_t f = first[a], h = n.op == Op::Stride ? 0 : n.hi[a];
+            if (f < 0 || (h < 0 && !(n.op == Op::Shrink && h == kToEnd && f == 0)))
+                return n.variant + " with a bound that is not a literal";
+            if (n.op == Op::Stride && f < 1) return "Stride with a step below one";
+            const int64_t se = src.dims[a], oe = n.dims[a];
+            if (se < 0 || oe < 0) continue;  // run-time extents: checked when the program runs
+            int64_t want = 0;
+            if (n.op == Op::Pad) want = f + se + h;
+            else if (n.op == Op::Stride) want = (se + f - 1) / f;
+            else {
+                const int64_t end = h == kToEnd ? se : h;
+                if (end < f || end > se) return "Shrink bounds outside the operand on axis " + std::to_string(a);
+                want = end - f;
+            }
+            if (want != oe) return n.variant + " bounds do not give the node's extent on axis " + std::to_string(a);
+        }
+        return "";
     }
     // The value of a Const, or of an Expand chain over one.
     bool const_of(int64_t id, double *v, Prim *p) const {
@@ -994,6 +1025,13 @@ struct Planner {
                 case Op::Load: case Op::Const: case Op::Expand: case Op::Permute: case Op::Reshape:
                 case Op::Realize: case Op::Copy: case Op::Store:
                     continue;  // inputs, constants and views
+                case Op::Shrink: case Op::Stride: {
+                    // views of their operand (an offset, scaled strides),
+                    // as the reference HIP lane's stride is (emit.rs:4918-4931)
+                    const std::string why = window_error(n);
+                    if (!why.empty()) return fail("node " + std::to_string(n.id) + ": " + why);
+                    continue;
+                }
                 case Op::ExtentWitness:
                     // checked on the host before the launches (build_plan);
                     // its value itself is read by nothing this build runs
@@ -1159,6 +1197,26 @@ struct Planner {
                     claim(r);
                     continue;
                 }
+                case Op::Bitwise:
+                    if (!is_integer(n.prec) || n.inputs.size() != 2)
+                        return fail("node " + std::to_string(n.id) + ": Bitwise needs two integer operands");
+                    single(n, RegionKind::Integer, CHELIS_INT_BITAND + n.code);
+                    continue;
+                case Op::Pad: {
+                    const std::string why = window_error(n);
+                    if (!why.empty()) return fail("node " + std::to_string(n.id) + ": " + why);
+                    if (n.const_prec != n.prec)
+                        return fail("node " + std::to_string(n.id) + ": Pad's fill is not of the tensor's dtype");
+                    Region r;
+                    r.kind = RegionKind::Pad;
+                    r.lo = n.lo;
+                    r.fill = n.const_bits;
+                    r.in = {n.inputs[0]};
+                    r.out = n.id;
+                    r.covers = {n.id};
+                    claim(r);
+                    continue;
+                }
                 case Op::ExtremaAdjoint:
                     if (n.inputs.size() != 3)
                         return fail("node " + std::to_string(n.id) + ": ExtremaAdjoint needs left, right and cotangent");
@@ -1202,7 +1260,7 @@ struct Planner {
 
 bool is_view_op(Op op) {
     return op == Op::Expand || op == Op::Permute || op == Op::Reshape || op == Op::Realize || op == Op::Copy ||
-           op == Op::Store;
+           op == Op::Store || op == Op::Shrink || op == Op::Stride;
 }
 
 // The reference's output specs (emit.rs:5901-5933): Store nodes in node

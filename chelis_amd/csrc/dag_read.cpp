@@ -45,6 +45,7 @@ const OpName kOps[] = {
     {"Logical", Op::Logical}, {"Mod", Op::Mod}, {"Gather", Op::Gather},
     {"ExtremaAdjoint", Op::ExtremaAdjoint}, {"UniformLike", Op::UniformLike}, {"KeyFromSeed", Op::KeyFromSeed},
     {"Split", Op::SplitKey}, {"FoldIn", Op::FoldIn}, {"Cumsum", Op::Cumsum},
+    {"Bitwise", Op::Bitwise}, {"Pad", Op::Pad}, {"Shrink", Op::Shrink}, {"Stride", Op::Stride},
 };
 
 struct PrimName {
@@ -279,6 +280,47 @@ bool read_op(const Json &op, Graph *g, Node *n, std::string *why) {
                 int64_t e;
                 if (!extent_of(d, g, n, &e)) return (*why = "Reshape new_shape holds a non-extent", false);
                 n->new_shape.push_back(e);
+            }
+            return true;
+        }
+        case Op::Bitwise: {
+            // BitwiseKind, snake_case (crates/chelis-numeric-core/src/bitwise.rs:8-14)
+            static const char *kinds[] = {"and", "or", "xor", "shift_left", "shift_right"};
+            if (p.kind != Json::String) return (*why = "Bitwise needs its kind", false);
+            for (int k = 0; k < 5; ++k)
+                if (p.text == kinds[k]) {
+                    n->code = k;
+                    return true;
+                }
+            return (*why = "Bitwise kind `" + p.text + "` is unknown", false);
+        }
+        case Op::Pad: case Op::Shrink: {
+            // Vec<(RtDim, RtDim)> (dag.rs:1202-1208): [[before, after], ...] /
+            // [[start, end], ...]; a shrink end may be ToEnd
+            const Json *pairs = p.get(n->op == Op::Pad ? "padding" : "bounds");
+            if (!pairs || pairs->kind != Json::Array) return (*why = var + " needs its bounds", false);
+            for (const Json &pr : pairs->items) {
+                if (pr.kind != Json::Array || pr.items.size() != 2) return (*why = var + " bounds are pairs", false);
+                int64_t a = 0, b = 0;
+                if (!extent_of(pr.items[0], g, n, &a)) return (*why = var + " holds a bound that is not an extent", false);
+                if (n->op == Op::Shrink && pr.items[1].kind == Json::String && pr.items[1].text == "ToEnd") {
+                    b = kToEnd;
+                } else if (!extent_of(pr.items[1], g, n, &b)) {
+                    return (*why = var + " holds a bound that is not an extent", false);
+                }
+                n->lo.push_back(a);
+                n->hi.push_back(b);
+            }
+            if (n->op == Op::Pad && !scalar_of(p.get("fill"), n)) return (*why = "Pad with an unreadable fill", false);
+            return true;
+        }
+        case Op::Stride: {
+            const Json *st = p.get("strides");
+            if (!st || st->kind != Json::Array) return (*why = "Stride needs its steps", false);
+            for (const Json &d : st->items) {
+                int64_t e = 0;
+                if (!extent_of(d, g, n, &e)) return (*why = "Stride holds a step that is not an extent", false);
+                n->step.push_back(e);
             }
             return true;
         }

@@ -21,6 +21,7 @@
 #include <limits>
 #include <mutex>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "hip_common.h"
@@ -90,6 +91,10 @@ __device__ inline void offsets(const Ops &o, const Shape &sh, int64_t idx, int64
         off[k] = s;
     }
 }
+
+// A record key: ~(launch sequence << kSeqShift | element index << 2 | kind),
+// so the atomic maximum keeps the earliest launch's lowest failing element.
+constexpr int kSeqShift = 42;
 
 __device__ inline unsigned long long fail_key(uint64_t seq, int64_t i, int kind) {
     return ~(seq | ((uint64_t)i << 2) | (uint64_t)kind);
@@ -352,7 +357,30 @@ __device__ inline int int_binary(int op, T x, T z, T *r) {
             return 0;
         }
         case CHELIS_INT_MAX_ELEM: *r = x > z ? x : z; return 0;
-        default: *r = x < z ? x : z; return 0;
+        case CHELIS_INT_MIN_ELEM: *r = x < z ? x : z; return 0;
+        case CHELIS_INT_BITAND: *r = (T)(x & z); return 0;
+        case CHELIS_INT_BITOR: *r = (T)(x | z); return 0;
+        case CHELIS_INT_BITXOR: *r = (T)(x ^ z); return 0;
+        default: {
+            // [04-NUM-13]: the bits move as the unsigned w-bit pattern; a
+            // count of w or more empties it (shr: fills it with the sign)
+            using U = std::make_unsigned_t<T>;
+            constexpr int W = 8 * (int)sizeof(T);
+            if (z < 0) return kDomain;
+            const U u = (U)x;
+            if (op == CHELIS_INT_SHL) {
+                *r = z >= W ? (T)0 : (T)(U)(u << (int)z);
+            } else {
+                const bool neg = x < 0;
+                if (z >= W) *r = neg ? (T)-1 : (T)0;
+                else {
+                    U v = (U)(u >> (int)z);
+                    if (neg && z != 0) v = (U)(v | (U)~((U)~(U)0 >> (int)z));
+                    *r = (T)v;
+                }
+            }
+            return 0;
+        }
     }
 }
 
@@ -390,6 +418,21 @@ struct IntUnaryOp {
         return 0ull;
     }
 };
+
+// After a shift launch, in stream order: when the record names this
+// launch's failure, the count at the failing element goes to the detail word
+// (the C lane's message prints it). One thread; broadcast axes of the count
+// have extent 1 and contribute nothing.
+template <typename T>
+__global__ void shift_detail_kernel(const unsigned long long *rec, uint64_t seq, Ops o, Shape sh, long long *detail) {
+    if (threadIdx.x != 0) return;
+    const unsigned long long w = __hip_atomic_load(rec, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (!w || ((~w) >> kSeqShift) != (seq >> kSeqShift)) return;
+    const int64_t i = (int64_t)(((~w) >> 2) & ((1ull << (kSeqShift - 2)) - 1));
+    int64_t off[2];
+    offsets(o, sh, i, off);
+    *detail = (long long)static_cast<const T *>(o.p[1])[off[1]];
+}
 
 // ---------------------------------------------------------------- gather
 // A view's element at a row-major logical index (chelis_logical_offset).
@@ -500,21 +543,60 @@ __global__ __launch_bounds__(256) void cumsum_kernel(const typename Dt<DT>::S *_
     }
 }
 
+// ---------------------------------------------------------------- pad
+// kernels.rs:1587-1637 / the C lane's emit_pad: output element o reads the
+// source at o - lo on every axis when that lies inside the source, else it
+// is the fill. Both sides strided (rank <= 8); elements moved as raw bits.
+struct PadGeom {
+    int32_t rank;
+    int64_t out_shape[8], out_strides[8], lo[8], src_shape[8], src_strides[8];
+};
+template <typename U>
+__global__ __launch_bounds__(256) void pad_kernel(const U *__restrict__ x, U *__restrict__ y, PadGeom g,
+                                                  int64_t total, U fill) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+        int64_t r = i, so = 0, yo = 0;
+        bool inside = true;
+#pragma unroll
+        for (int a = 7; a >= 0; --a) {
+            if (a < g.rank) {
+                const int64_t c = r % g.out_shape[a];
+                r /= g.out_shape[a];
+                const int64_t sc = c - g.lo[a];
+                inside = inside && sc >= 0 && sc < g.src_shape[a];
+                so += sc * g.src_strides[a];
+                yo += c * g.out_strides[a];
+            }
+        }
+        U v = fill;
+        if (inside) v = x[so];
+        y[yo] = v;
+    }
+}
+
 // ---------------------------------------------------------------- host: the failure channel
 // Per device: word [2..3] of the status words is the deferred record, [4..5]
 // the record of a call that waits for its own result. A deferred launch's
 // sequence number indexes the label ("add at i64") its message names.
 constexpr int kMaxDevices = 64;
-constexpr int kSeqShift = 42;
 constexpr uint64_t kSeqMax = (1ull << (64 - kSeqShift)) - 1;
 std::mutex g_fail_mutex;
-std::vector<std::string> g_labels[kMaxDevices];
 
 struct Sink {
     unsigned long long *rec = nullptr;
+    long long *detail = nullptr;  // a failing shift's count
     uint64_t seq = 0;
     bool wait = false;
 };
+
+// A deferred launch's message: "numeric trap: <kind> in <text>", or for a
+// shift the C lane's count line.
+struct Label {
+    std::string text;
+    bool shift = false;
+};
+std::vector<Label> g_labels[kMaxDevices];
 
 const char *dtype_name(chelis_dtype d) {
     switch (d) {
@@ -537,36 +619,48 @@ const char *kind_text(int kind) {
 // The sink a trapping launch records into: its own word when the caller
 // waits for the result (failure != NULL), else the deferred word under the
 // next sequence number, labelled "<op> at <prim>".
-int32_t open_sink(bool wait, const std::string &label, Sink *s) {
+int32_t open_sink(bool wait, const std::string &label, Sink *s, bool shift = false) {
     int32_t *words = status_words(nullptr);
     if (!words) return set_error(CHELIS_HIP_EHIP, "no HIP device status words");
     s->wait = wait;
     if (wait) {
         s->rec = reinterpret_cast<unsigned long long *>(words + 4);
+        s->detail = reinterpret_cast<long long *>(words + 8);
         s->seq = 0;
         return CHELIS_HIP_OK;
     }
     int device = 0;
     CHELIS_HIP_TRY(hipGetDevice(&device));
     std::lock_guard<std::mutex> lock(g_fail_mutex);
-    std::vector<std::string> &labels = g_labels[device];
+    std::vector<Label> &labels = g_labels[device];
     const uint64_t seq = std::min<uint64_t>(labels.size(), kSeqMax);
-    if (labels.size() <= kSeqMax) labels.push_back(label);
+    if (labels.size() <= kSeqMax) labels.push_back(Label{label, shift});
     s->rec = reinterpret_cast<unsigned long long *>(words + 2);
+    s->detail = reinterpret_cast<long long *>(words + 6);
     s->seq = seq << kSeqShift;
     return CHELIS_HIP_OK;
 }
 
-void fill_failure(chelis_hip_numeric_failure *f, unsigned long long word, const std::string &label) {
+// The failure of a record word; a shift's message reads the count from the
+// detail word (the stream is idle).
+int32_t fill_failure(chelis_hip_numeric_failure *f, unsigned long long word, const Label &label,
+                     const long long *detail) {
     f->index = -1;
     f->kind = 0;
     f->reserved = 0;
     f->message[0] = 0;
-    if (!word) return;
+    if (!word) return CHELIS_HIP_OK;
     const uint64_t key = ~word;
     f->kind = (int32_t)(key & 3u);
     f->index = (int64_t)((key >> 2) & ((1ull << (kSeqShift - 2)) - 1));
-    snprintf(f->message, sizeof f->message, "numeric trap: %s in %s", kind_text(f->kind), label.c_str());
+    if (label.shift) {
+        long long count = 0;
+        CHELIS_HIP_TRY(hipMemcpy(&count, detail, sizeof count, hipMemcpyDeviceToHost));
+        snprintf(f->message, sizeof f->message, "shift amount must be non-negative, got %lld", count);
+    } else {
+        snprintf(f->message, sizeof f->message, "numeric trap: %s in %s", kind_text(f->kind), label.text.c_str());
+    }
+    return CHELIS_HIP_OK;
 }
 
 // Reads and clears a record word (the stream is idle).
@@ -580,13 +674,12 @@ int32_t take_word(unsigned long long *rec, unsigned long long *word) {
 }
 
 // After the launch of a waiting call: its record, read and cleared.
-int32_t close_sink(const Sink &s, const std::string &label, chelis_hip_numeric_failure *f) {
+int32_t close_sink(const Sink &s, const std::string &label, chelis_hip_numeric_failure *f, bool shift = false) {
     if (!s.wait) return CHELIS_HIP_OK;
     CHELIS_HIP_TRY(hipStreamSynchronize(stream()));
     unsigned long long word = 0ull;
     if (int32_t st = take_word(s.rec, &word)) return st;
-    fill_failure(f, word, label);
-    return CHELIS_HIP_OK;
+    return fill_failure(f, word, Label{label, shift}, s.detail);
 }
 
 // ---------------------------------------------------------------- host: checks and launches
@@ -604,6 +697,21 @@ int32_t check_out(const chelis_gpu_tensor *out, const char *what) {
     if (int32_t s = check_tensor(out, "out")) return s;
     if (!is_contiguous(out)) return set_error(CHELIS_HIP_EUNSUPPORTED, "%s: the output must be contiguous", what);
     return CHELIS_HIP_OK;
+}
+
+// A strided output no two of whose elements share an address: sorted by
+// stride, each axis steps past everything the smaller axes span.
+bool non_overlapping(const chelis_gpu_tensor *t) {
+    std::vector<std::pair<int64_t, int64_t>> ax;
+    for (int32_t a = 0; a < t->rank; ++a)
+        if (t->shape[a] > 1) ax.push_back({t->strides[a], t->shape[a]});
+    std::sort(ax.begin(), ax.end());
+    int64_t span = 1;
+    for (const auto &p : ax) {
+        if (p.first < span) return false;
+        span = p.first * p.second;
+    }
+    return true;
 }
 
 int64_t map_blocks(int64_t count) { return std::max<int64_t>(1, std::min<int64_t>((count + 255) / 256, 65536)); }
@@ -672,13 +780,27 @@ int32_t launch_int(int32_t op, const chelis_gpu_tensor *a, const chelis_gpu_tens
         return launch_map(IntUnaryOp<T>{op, o, s.seq}, ins, 1, out, s.rec, "integer_elementwise");
     }
     const chelis_gpu_tensor *ins[2] = {a, b};
-    return launch_map(IntBinaryOp<T>{op, o, s.seq}, ins, 2, out, s.rec, "integer_elementwise");
+    if (int32_t st = launch_map(IntBinaryOp<T>{op, o, s.seq}, ins, 2, out, s.rec, "integer_elementwise")) return st;
+    if ((op == CHELIS_INT_SHL || op == CHELIS_INT_SHR) && out->count) {
+        Shape sh;
+        int64_t st2[CHELIS_FUSED_MAX_INPUTS][kMaxRank] = {};
+        collapse(out, ins, 2, &sh, st2);  // succeeded in launch_map
+        Ops ops{};
+        for (int k = 0; k < 2; ++k) {
+            ops.p[k] = ins[k]->data;
+            for (int ax = 0; ax < kMaxRank; ++ax) ops.st[k][ax] = st2[k][ax];
+        }
+        shift_detail_kernel<T><<<1, 64, 0, stream()>>>(s.rec, s.seq, ops, sh, s.detail);
+        CHELIS_LAUNCH_CHECK();
+    }
+    return CHELIS_HIP_OK;
 }
 
 const char *int_op_name(int32_t op) {
-    static const char *names[] = {"add", "sub", "mul", "floor_div", "trunc_div", "mod",
-                                  "max_elem", "min_elem", "neg", "abs"};
-    return op >= 0 && op <= CHELIS_INT_ABS ? names[op] : "?";
+    static const char *names[] = {"add",      "sub",      "mul", "floor_div", "trunc_div", "mod",    "max_elem",
+                                  "min_elem", "neg",      "abs", "bitand",    "bitor",     "bitxor", "shl",
+                                  "shr"};
+    return op >= 0 && op <= CHELIS_INT_SHR ? names[op] : "?";
 }
 
 View8 view_of(const chelis_gpu_tensor *t) {
@@ -832,8 +954,9 @@ extern "C" int32_t chelis_hip_cast(const chelis_gpu_tensor *x, const chelis_gpu_
 
 extern "C" int32_t chelis_hip_integer_elementwise(int32_t op, const chelis_gpu_tensor *a, const chelis_gpu_tensor *b,
                                                   const chelis_gpu_tensor *out, chelis_hip_numeric_failure *failure) {
-    if (op < CHELIS_INT_ADD || op > CHELIS_INT_ABS)
+    if (op < CHELIS_INT_ADD || op > CHELIS_INT_SHR)
         return set_error(CHELIS_HIP_EDOMAIN, "integer_elementwise: unknown op %d", op);
+    const bool shift = op == CHELIS_INT_SHL || op == CHELIS_INT_SHR;
     const bool unary = op == CHELIS_INT_NEG || op == CHELIS_INT_ABS;
     if (int32_t s = check_out(out, "integer_elementwise")) return s;
     if (int32_t s = check_broadcast(a, out, "integer_elementwise", "a")) return s;
@@ -846,7 +969,7 @@ extern "C" int32_t chelis_hip_integer_elementwise(int32_t op, const chelis_gpu_t
         return set_error(CHELIS_HIP_EDOMAIN, "integer_elementwise: i8, i16, i32 or i64 operands only");
     const std::string label = std::string(int_op_name(op)) + " at " + dtype_name(out->dtype);
     Sink sink;
-    if (int32_t s = open_sink(failure != nullptr, label, &sink)) return s;
+    if (int32_t s = open_sink(failure != nullptr, label, &sink, shift)) return s;
     int32_t st;
     switch (out->dtype) {
         case CHELIS_DTYPE_I8: st = launch_int<int8_t>(op, a, b, out, sink); break;
@@ -855,7 +978,7 @@ extern "C" int32_t chelis_hip_integer_elementwise(int32_t op, const chelis_gpu_t
         default: st = launch_int<int64_t>(op, a, b, out, sink); break;
     }
     if (st) return st;
-    return close_sink(sink, label, failure);
+    return close_sink(sink, label, failure, shift);
 }
 
 extern "C" int32_t chelis_hip_gather(const chelis_gpu_tensor *values, const chelis_gpu_tensor *indices, int32_t axis,
@@ -958,6 +1081,45 @@ extern "C" int32_t chelis_hip_cumsum(const chelis_gpu_tensor *x, int32_t axis, i
     return close_sink(sink, label, failure);
 }
 
+template <typename U>
+int32_t launch_pad(const chelis_gpu_tensor *x, const PadGeom &g, uint64_t fill, const chelis_gpu_tensor *out) {
+    pad_kernel<U><<<dim3((unsigned)map_blocks(out->count)), dim3(256), 0, stream()>>>(
+        static_cast<const U *>(x->data), static_cast<U *>(out->data), g, out->count, (U)fill);
+    CHELIS_LAUNCH_CHECK();
+    return CHELIS_HIP_OK;
+}
+
+extern "C" int32_t chelis_hip_pad(const chelis_gpu_tensor *x, const int64_t *lo, uint64_t fill_bits,
+                                  const chelis_gpu_tensor *out) {
+    if (int32_t s = check_tensor(x, "x")) return s;
+    if (int32_t s = check_tensor(out, "out")) return s;
+    if (!non_overlapping(out)) return set_error(CHELIS_HIP_EUNSUPPORTED, "pad: the output's elements overlap");
+    if (out->dtype != x->dtype) return set_error(CHELIS_HIP_EDOMAIN, "pad: output dtype differs from x");
+    if (x->rank != out->rank || x->rank > 8)
+        return set_error(CHELIS_HIP_EDOMAIN, "pad: x and the output need one rank, at most 8");
+    if (x->rank > 0 && !lo) return set_error(CHELIS_HIP_EDOMAIN, "pad: null lo");
+    PadGeom g{};
+    g.rank = x->rank;
+    for (int32_t a = 0; a < x->rank; ++a) {
+        if (lo[a] < 0 || x->shape[a] < 0 || lo[a] + x->shape[a] > out->shape[a])
+            return set_error(CHELIS_HIP_EDOMAIN, "pad: axis %d: %lld before %lld source elements exceed %lld", a,
+                             (long long)lo[a], (long long)x->shape[a], (long long)out->shape[a]);
+        g.out_shape[a] = out->shape[a];
+        g.out_strides[a] = out->strides[a];
+        g.lo[a] = lo[a];
+        g.src_shape[a] = x->shape[a];
+        g.src_strides[a] = x->strides[a];
+    }
+    if (!stream()) return set_error(CHELIS_HIP_EHIP, "no HIP device");
+    if (!out->count) return CHELIS_HIP_OK;
+    switch (dtype_width(out->dtype)) {
+        case 1: return launch_pad<uint8_t>(x, g, fill_bits, out);
+        case 2: return launch_pad<uint16_t>(x, g, fill_bits, out);
+        case 4: return launch_pad<uint32_t>(x, g, fill_bits, out);
+        default: return launch_pad<uint64_t>(x, g, fill_bits, out);
+    }
+}
+
 extern "C" int32_t chelis_hip_take_numeric_failure(chelis_hip_numeric_failure *failure) {
     if (!failure) return set_error(CHELIS_HIP_EDOMAIN, "take_numeric_failure: null record");
     int32_t *words = status_words(nullptr);
@@ -967,16 +1129,15 @@ extern "C" int32_t chelis_hip_take_numeric_failure(chelis_hip_numeric_failure *f
     if (int32_t s = take_word(reinterpret_cast<unsigned long long *>(words + 2), &word)) return s;
     int device = 0;
     CHELIS_HIP_TRY(hipGetDevice(&device));
-    std::string label;
+    Label label;
     {
         std::lock_guard<std::mutex> lock(g_fail_mutex);
-        std::vector<std::string> &labels = g_labels[device];
+        std::vector<Label> &labels = g_labels[device];
         const uint64_t seq = word ? (~word) >> kSeqShift : 0;
         if (word && seq < labels.size()) label = labels[seq];
         labels.clear();
     }
-    fill_failure(failure, word, label);
-    return CHELIS_HIP_OK;
+    return fill_failure(failure, word, label, reinterpret_cast<const long long *>(words + 6));
 }
 
 }  // namespace chelis

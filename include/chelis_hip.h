@@ -234,7 +234,13 @@ int32_t chelis_hip_extrema_adjoint(int32_t kind, int32_t operand, const chelis_g
  * reference HIP lane checks sub and abs only (kernels.rs:769-810, 1434) and
  * has no mod (emit.rs:2574); this build checks every op as the C lane does.
  * b is ignored for neg and abs. Trap line `numeric trap: <kind> in <op> at
- * <dtype>`.
+ * <dtype>`. The bitwise ops ([05-OP-47], RiscOp::Bitwise, the reference HIP
+ * lane's binary_bitwise_typed, kernels.rs:687-760): bitand / bitor / bitxor
+ * on the w-bit two's complement; shl and shr take b as the count - a count
+ * at or above w gives 0 (shr of a negative value: -1), shr extends the sign
+ * - and a negative count fails `domain` with the C lane's line
+ * `shift amount must be non-negative, got <count>` ([04-NUM-13],
+ * crates/chelis-runtime/include/chelis_runtime.h:297-330) as the message.
  *
  * gather: RiscOp::Gather{axis, batch_rank} (crates/chelis-dag-core/src/
  * dag.rs:1349-1356) with the reference's geometry (emit.rs:3807-3900,
@@ -256,7 +262,8 @@ int32_t chelis_hip_cast(const chelis_gpu_tensor *x, const chelis_gpu_tensor *out
 enum {
     CHELIS_INT_ADD = 0, CHELIS_INT_SUB = 1, CHELIS_INT_MUL = 2, CHELIS_INT_FLOOR_DIV = 3,
     CHELIS_INT_TRUNC_DIV = 4, CHELIS_INT_MOD = 5, CHELIS_INT_MAX_ELEM = 6, CHELIS_INT_MIN_ELEM = 7,
-    CHELIS_INT_NEG = 8, CHELIS_INT_ABS = 9
+    CHELIS_INT_NEG = 8, CHELIS_INT_ABS = 9, CHELIS_INT_BITAND = 10, CHELIS_INT_BITOR = 11,
+    CHELIS_INT_BITXOR = 12, CHELIS_INT_SHL = 13, CHELIS_INT_SHR = 14
 };
 int32_t chelis_hip_integer_elementwise(int32_t op, const chelis_gpu_tensor *a, const chelis_gpu_tensor *b,
                                        const chelis_gpu_tensor *out, chelis_hip_numeric_failure *failure);
@@ -275,6 +282,15 @@ int32_t chelis_hip_gather(const chelis_gpu_tensor *values, const chelis_gpu_tens
  * line: ((o * inner + j) * n + step)), the order the C lane traps in. */
 int32_t chelis_hip_cumsum(const chelis_gpu_tensor *x, int32_t axis, int32_t reverse, const chelis_gpu_tensor *out,
                           chelis_hip_numeric_failure *failure);
+/* pad: RiscOp::Pad{padding, fill} (crates/chelis-dag-core/src/dag.rs:1202;
+ * the reference HIP lane's pad_typed, kernels.rs:1587-1637). out has x's
+ * rank and dtype; lo[a] elements come before x on axis a, and out's extent
+ * leaves out->shape[a] - lo[a] - x->shape[a] >= 0 after it. Every element
+ * outside x is fill_bits' low dtype-width bytes (a float's stored bits, an
+ * integer's two's complement). Any strides on either side (the output's
+ * elements must not overlap); rank <= 8. */
+int32_t chelis_hip_pad(const chelis_gpu_tensor *x, const int64_t *lo, uint64_t fill_bits,
+                       const chelis_gpu_tensor *out);
 /* Waits for the library stream, then reads and clears the current device's
  * deferred failure record (kind 0: none). */
 int32_t chelis_hip_take_numeric_failure(chelis_hip_numeric_failure *failure);

@@ -936,7 +936,9 @@ int64_t orc_cast(int src, int dst, const void *x, void *y, int64_t n, int32_t *k
  * floor_div and trunc_div overflow on MIN / -1 (mod of -1 is 0); floor_div
  * rounds the truncated quotient down when the remainder's sign differs from
  * the divisor's; max_elem / min_elem never trap. op: 0 add, 1 sub, 2 mul,
- * 3 floor_div, 4 trunc_div, 5 mod, 6 max_elem, 7 min_elem. */
+ * 3 floor_div, 4 trunc_div, 5 mod, 6 max_elem, 7 min_elem; the bitwise ops
+ * of [05-OP-47] (crates/chelis-backend-c/src/emit.rs:2354-2362): 8 bitand,
+ * 9 bitor, 10 bitxor on the two's-complement bits, 11 shl, 12 shr. */
 int64_t orc_int_binary(int op, int dt, const void *a, const void *b, void *y, int64_t n, int32_t *kind) {
     int64_t first = -1, lo, hi;
     *kind = 0;
@@ -962,7 +964,37 @@ int64_t orc_int_binary(int op, int dt, const void *a, const void *b, void *y, in
                 }
                 break;
             case 6: r = x > z ? x : z; break;
-            default: r = x < z ? x : z; break;
+            case 7: r = x < z ? x : z; break;
+            case 8: r = x & z; break;
+            case 9: r = x | z; break;
+            case 10: r = x ^ z; break;
+            default: {
+                /* [04-NUM-13] shifts (crates/chelis-runtime/include/
+                 * chelis_runtime.h:297-330): the w-bit pattern moved as an
+                 * unsigned word, read back as two's complement; a count of w
+                 * or more gives 0 (shr of a negative value: -1); a negative
+                 * count fails (the C lane's "shift amount must be
+                 * non-negative" trap, here domain) */
+                const int w = odt_bits(dt);
+                const uint64_t mask = w == 64 ? ~0ull : ((1ull << w) - 1);
+                const uint64_t raw = (uint64_t)x & mask;
+                uint64_t v;
+                if (z < 0) {
+                    fail = OFAIL_DOMAIN;
+                    v = 0;
+                } else if (op == 11) {
+                    v = z >= w ? 0 : (raw << z) & mask;
+                } else {
+                    const int neg = (raw >> (w - 1)) & 1;
+                    if (z >= w) v = neg ? mask : 0;
+                    else {
+                        v = raw >> z;
+                        if (neg && z > 0) v |= mask & ~(mask >> z);
+                    }
+                }
+                r = (v >> (w - 1)) & 1 ? (int64_t)(v | ~mask) : (int64_t)v;
+                break;
+            }
         }
         odt_int_store(dt, y, i, fail ? 0 : r);
         if (fail && first < 0) {
@@ -1073,4 +1105,47 @@ int64_t orc_cumsum(int dt, const void *x, void *y, int64_t outer, int64_t n, int
             }
         }
     return first;
+}
+
+/* Movement with bounds over contiguous row-major arrays of `width`-byte
+ * elements (rank <= 8).
+ * Pad (RiscOp::Pad{padding, fill}): the C lane fills the result with the
+ * fill's bits, then copies source element i to the result at its
+ * coordinates plus `lo` (crates/chelis-backend-c/src/emit.rs:10880-10954).
+ * Shrink / Stride (emit.rs:10956-11042): result element o reads the source
+ * at o * step + start on every axis (shrink: step 1; stride: start 0). */
+static void orc_coords(int64_t i, int rank, const int64_t *shape, int64_t *c) {
+    for (int a = rank - 1; a >= 0; --a) {
+        c[a] = shape[a] ? i % shape[a] : 0;
+        i = shape[a] ? i / shape[a] : 0;
+    }
+}
+static int64_t orc_flat(int rank, const int64_t *shape, const int64_t *c) {
+    int64_t f = 0;
+    for (int a = 0; a < rank; ++a) f = f * shape[a] + c[a];
+    return f;
+}
+void orc_pad(int width, const void *x, int rank, const int64_t *src_shape, const int64_t *lo,
+             const int64_t *out_shape, uint64_t fill, void *y) {
+    int64_t n_out = 1, n_src = 1, c[8];
+    for (int a = 0; a < rank; ++a) {
+        n_out *= out_shape[a];
+        n_src *= src_shape[a];
+    }
+    for (int64_t i = 0; i < n_out; ++i) memcpy((char *)y + i * width, &fill, (size_t)width);
+    for (int64_t i = 0; i < n_src; ++i) {
+        orc_coords(i, rank, src_shape, c);
+        for (int a = 0; a < rank; ++a) c[a] += lo[a];
+        memcpy((char *)y + orc_flat(rank, out_shape, c) * width, (const char *)x + i * width, (size_t)width);
+    }
+}
+void orc_slice(int width, const void *x, int rank, const int64_t *src_shape, const int64_t *start,
+               const int64_t *step, const int64_t *out_shape, void *y) {
+    int64_t n_out = 1, c[8];
+    for (int a = 0; a < rank; ++a) n_out *= out_shape[a];
+    for (int64_t i = 0; i < n_out; ++i) {
+        orc_coords(i, rank, out_shape, c);
+        for (int a = 0; a < rank; ++a) c[a] = c[a] * step[a] + start[a];
+        memcpy((char *)y + i * width, (const char *)x + orc_flat(rank, src_shape, c) * width, (size_t)width);
+    }
 }

@@ -143,6 +143,10 @@ int64_t orc_int_binary(int op, int dt, const void *a, const void *b, void *y, in
 int64_t orc_int_unary(int op, int dt, const void *x, void *y, int64_t n, int32_t *kind);
 int64_t orc_cumsum(int dt, const void *x, void *y, int64_t outer, int64_t n, int64_t inner, int reverse,
                    int32_t *kind);
+void orc_pad(int width, const void *x, int rank, const int64_t *src_shape, const int64_t *lo,
+             const int64_t *out_shape, uint64_t fill, void *y);
+void orc_slice(int width, const void *x, int rank, const int64_t *src_shape, const int64_t *start,
+               const int64_t *step, const int64_t *out_shape, void *y);
 int64_t orc_gather(const void *values, int64_t width, int64_t before, int64_t axis_size, int64_t after,
                    const void *idx, int idx_dt, int64_t index_count, int64_t batch_count, void *out, int32_t *kind);
 

@@ -102,6 +102,8 @@ def _declare(L):
         "orc_int_binary": (c_i64, [ctypes.c_int, ctypes.c_int, c_p, c_p, c_p, c_i64, c_p]),
         "orc_int_unary": (c_i64, [ctypes.c_int, ctypes.c_int, c_p, c_p, c_i64, c_p]),
         "orc_cumsum": (c_i64, [ctypes.c_int, c_p, c_p, c_i64, c_i64, c_i64, ctypes.c_int, c_p]),
+        "orc_pad": (None, [ctypes.c_int, c_p, ctypes.c_int, c_p, c_p, c_p, ctypes.c_uint64, c_p]),
+        "orc_slice": (None, [ctypes.c_int, c_p, ctypes.c_int, c_p, c_p, c_p, c_p, c_p]),
         "orc_gather": (c_i64, [c_p, c_i64, c_i64, c_i64, c_i64, c_p, ctypes.c_int, c_i64, c_i64, c_p, c_p]),
     })
     for name, (res, args) in sig.items():
@@ -380,7 +382,8 @@ CARRIERS = {"f32": np.float32, "f64": np.float64, "i32": np.int32, "bool": np.ui
             "bf16": np.uint16, "f16": np.uint16, "i8": np.int8, "i16": np.int16}
 COMPARE_KINDS = {"cmp_lt": 0, "lt": 1, "eq": 2, "neq": 3, "gt": 4, "gte": 5, "lte": 6}
 LOGICAL_KINDS = {"and": 0, "or": 1, "not": 2}
-INT_BINARY = {"add": 0, "sub": 1, "mul": 2, "floor_div": 3, "trunc_div": 4, "mod": 5, "max_elem": 6, "min_elem": 7}
+INT_BINARY = {"add": 0, "sub": 1, "mul": 2, "floor_div": 3, "trunc_div": 4, "mod": 5, "max_elem": 6, "min_elem": 7,
+              "bitand": 8, "bitor": 9, "bitxor": 10, "shl": 11, "shr": 12}
 INT_UNARY = {"neg": 0, "abs": 1}
 FAILURE_KINDS = {1: "overflow", 2: "domain", 3: "division by zero"}
 
@@ -504,3 +507,31 @@ def cumsum(dt: str, x, axis: int, reverse: bool = False):
     first = lib().orc_cumsum(DTYPE_IDS[dt], _ptr(x), _ptr(y), outer, x.shape[ax], inner, int(reverse),
                              ctypes.byref(kind))
     return y, first, kind.value
+
+
+def _i64s(v):
+    return np.ascontiguousarray(np.asarray(v, np.int64).reshape(-1))
+
+
+def pad(x, lo, hi, fill):
+    """RiscOp::Pad over any dtype: `fill` a scalar of x's dtype (a 16-bit
+    float as its bits in x's carrier)."""
+    x = np.ascontiguousarray(x)
+    lo, hi = _i64s(lo), _i64s(hi)
+    out_shape = _i64s([e + a + b for e, a, b in zip(x.shape, lo, hi)])
+    y = np.empty(tuple(out_shape), x.dtype)
+    bits = int(np.array([fill], x.dtype).view(np.dtype("u%d" % x.itemsize))[0])
+    src = _i64s(x.shape)
+    lib().orc_pad(x.itemsize, _ptr(x), x.ndim, _ptr(src), _ptr(lo), _ptr(out_shape), bits, _ptr(y))
+    return y
+
+
+def slice_(x, start, step, out_shape):
+    """RiscOp::Shrink (step 1) / RiscOp::Stride (start 0): element o reads
+    x at o * step + start."""
+    x = np.ascontiguousarray(x)
+    start, step, out_shape = _i64s(start), _i64s(step), _i64s(out_shape)
+    y = np.empty(tuple(out_shape), x.dtype)
+    src = _i64s(x.shape)
+    lib().orc_slice(x.itemsize, _ptr(x), x.ndim, _ptr(src), _ptr(start), _ptr(step), _ptr(out_shape), _ptr(y))
+    return y

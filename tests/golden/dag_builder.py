@@ -167,6 +167,36 @@ class Dag:
         return self.node({"Gather": {"axis": axis, "batch_rank": batch_rank}}, [values, indices], dims,
                          self.prec(values))
 
+    def bitwise(self, kind, a, b):
+        """RiscOp::Bitwise(kind) (dag.rs:911): and, or, xor, shift_left,
+        shift_right."""
+        return self.node({"Bitwise": kind}, [a, b], self.dims(a), self.prec(a))
+
+    def pad(self, x, pads, fill):
+        """RiscOp::Pad{padding, fill} (dag.rs:1202-1205), literal bounds."""
+        p = self.prec(x)
+        if p == "f32":
+            v = {"dtype": "f32", "bits": _f32_bits(fill)}
+        elif p == "f64":
+            v = {"dtype": "f64", "bits": _f64_bits(fill)}
+        else:
+            v = {"dtype": INT_TAGS[p], "value": int(fill)}
+        dims = [d + a + b for d, (a, b) in zip(self.dims(x), pads)]
+        padding = [[{"Lit": a}, {"Lit": b}] for a, b in pads]
+        return self.node({"Pad": {"padding": padding, "fill": v}}, [x], dims, p)
+
+    def shrink(self, x, bounds):
+        """RiscOp::Shrink{bounds} (dag.rs:1206-1208): (start, end) per axis."""
+        dims = [b - a for a, b in bounds]
+        return self.node({"Shrink": {"bounds": [[{"Lit": a}, {"Lit": b}] for a, b in bounds]}}, [x], dims,
+                         self.prec(x))
+
+    def stride(self, x, steps):
+        """RiscOp::Stride{strides} (dag.rs:1209-1211): every step-th element
+        from the first."""
+        dims = [-(-d // k) for d, k in zip(self.dims(x), steps)]
+        return self.node({"Stride": {"strides": [{"Lit": k} for k in steps]}}, [x], dims, self.prec(x))
+
     def dropout(self, x, rate, key, replay=False):
         return self.node("DropoutReplay" if replay else "Dropout", [x, rate, key], self.dims(x), self.prec(x))
 
@@ -454,6 +484,30 @@ def select_program(R, N):
     return g
 
 
+def bitwise_program(n):
+    """[05-OP-47] over i32 vectors: and, xor and both shifts by a count
+    vector."""
+    g = Dag("bitwise")
+    a = g.load("a", [n], "i32")
+    b = g.load("b", [n], "i32")
+    c = g.load("c", [n], "i32")
+    g.roots = [g.bitwise("and", a, b), g.bitwise("xor", a, b), g.bitwise("or", a, b),
+               g.bitwise("shift_left", a, c), g.bitwise("shift_right", a, c)]
+    return g
+
+
+def movement_program():
+    """Shrink and stride as views read by a chain, a pad of the chain's
+    result, and a stride and a shrink as results."""
+    g = Dag("movement")
+    x = g.load("x", [512, 1000], "f32")
+    s = g.shrink(x, [(10, 490), (100, 1000)])
+    t = g.stride(s, [3, 2])
+    y = g.binary("Add", t, g.scalar_like(1.0, t))
+    g.roots = [g.pad(y, [(2, 1), (0, 5)], -1.5), g.stride(x, [2, 5]), g.shrink(x, [(500, 512), (0, 1000)])]
+    return g
+
+
 def cast_program(n):
     """Checked casts of an f64 vector: rounded to i32, and narrowed to f32
     and bf16."""
@@ -541,6 +595,8 @@ FIXTURES = {
     "draws_f32_1024x512": lambda: draws_program(1024, 512),
     "extrema_adjoints_f32_4096x1024": lambda: extrema_adjoint_program(4096, 1024),
     "scans_f32_512x1024": lambda: scan_program(512, 1024),
+    "bitwise_i32_65536": lambda: bitwise_program(65536),
+    "movement_f32_512x1000": movement_program,
 }
 
 OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "dags")

@@ -625,3 +625,35 @@ def test_cumsum_plans_as_a_scan_and_reads_back_verbatim():
     out = json.loads(C.dag_fuse(g.json()))
     assert out["nodes"][1]["op"] == {"Cumsum": {"axis": 0, "direction": "Decreasing"}}
     assert out["nodes"][1]["output_type"]["precision"] == "Int32"
+
+
+def test_bitwise_pad_shrink_stride_plan_and_read_back_verbatim():
+    p = C.DagProgram(open(os.path.join(DAGS, "bitwise_i32_65536.json")).read())
+    assert region_kinds(p) == ["integer"] * 5
+    p = C.DagProgram(open(os.path.join(DAGS, "movement_f32_512x1000.json")).read())
+    assert region_kinds(p) == ["chain", "pad", "copy", "copy"]
+    text = open(os.path.join(DAGS, "movement_f32_512x1000.json")).read()
+    assert json.loads(C.dag_fuse(text))["nodes"][1]["op"] == {
+        "Shrink": {"bounds": [[{"Lit": 10}, {"Lit": 490}], [{"Lit": 100}, {"Lit": 1000}]]}}
+
+
+def test_movement_bounds_this_build_refuses():
+    g = DB.Dag("bad")
+    x = g.load("x", [8, 6], "f32")
+    g.roots = [g.shrink(x, [(2, 9), (0, 6)])]  # past the operand
+    with pytest.raises(C.ChelisError, match="Shrink bounds outside the operand on axis 0"):
+        C.DagProgram(g.json())
+    g = DB.Dag("bad")
+    x = g.load("x", [8, 6], "f32")
+    n = g.stride(x, [3, 2])
+    g.nodes[n]["output_type"]["dims"][0] = {"Lit": 2}  # ceil(8 / 3) is 3
+    g.roots = [n]
+    with pytest.raises(C.ChelisError, match="bounds do not give the node's extent on axis 0"):
+        C.DagProgram(g.json())
+    g = DB.Dag("bad")
+    x = g.load("x", [8, 6], "f32")
+    k = g.const(2, [], "i64")
+    n = g.node({"Shrink": {"bounds": [[{"Node": 1}, {"Lit": 8}], [{"Lit": 0}, {"Lit": 6}]]}}, [x, k], [6, 6], "f32")
+    g.roots = [n]
+    with pytest.raises(C.ChelisError, match="run-time bounds"):
+        C.DagProgram(g.json())

@@ -201,6 +201,12 @@ elif case == "cast":
     x = np.zeros(65536)
     x[[3000, 70]] = [np.inf, 3e9]
     C.host_entry(sys.argv[4], [x], 3, library=lib)
+elif case == "shift":
+    n = 65536
+    a = np.arange(n, dtype=np.int32)
+    c = np.ones(n, np.int32)
+    c[[40000, 12]] = [-1, -4]
+    C.host_entry(sys.argv[4], [a, a, c], 5, library=lib)
 elif case == "gather":
     table = np.zeros((50000, 64), np.float32)
     ids = np.zeros(4096, np.int64)
@@ -216,6 +222,7 @@ print("returned", flush=True)
     ("integer_ops_i64_65536", "integer", "numeric trap: division by zero in floor_div at i64"),
     ("casts_f64_65536", "cast", "numeric trap: overflow in cast at i32"),
     ("gathers_50000x64_4096x10", "gather", "numeric trap: domain in gather at i64"),
+    ("bitwise_i32_65536", "shift", "shift amount must be non-negative, got -4"),
 ])
 def test_generated_entries_exit_with_the_trap_line(name, case, text):
     g = generated(name)
@@ -272,3 +279,47 @@ def test_scan_overflow_traps_through_the_dag_run():
     c[[7, 8]] = np.iinfo(np.int64).max
     with pytest.raises(C.ChelisError, match="^numeric trap: overflow in cumsum at i64$"):
         run_dag("scans_f32_512x1024", [x, c])
+
+
+# ---------------------------------------------------------------- bitwise, movement
+def bitwise_inputs(n=65536):
+    rng = np.random.default_rng(67)
+    a = rng.integers(-(2 ** 31), 2 ** 31, n, dtype=np.int64).astype(np.int32)
+    b = rng.integers(-(2 ** 31), 2 ** 31, n, dtype=np.int64).astype(np.int32)
+    c = rng.integers(0, 40, n).astype(np.int32)
+    c[:4] = [0, 31, 32, 1000]
+    a[:4] = [-1, -(2 ** 31), 5, -7]
+    return a, b, c
+
+
+@pytest.mark.parametrize("path", ["dag", "device", "host"])
+def test_bitwise_bit_exact(path):
+    a, b, c = bitwise_inputs()
+    got = run_all("bitwise_i32_65536", [a, b, c])[path]
+    want = [O.int_binary(op, "i32", a, y)[0] for op, y in
+            (("bitand", b), ("bitxor", b), ("bitor", b), ("shl", c), ("shr", c))]
+    for g, w in zip(got, want):
+        assert np.array_equal(g, w)
+
+
+def test_negative_shift_count_through_the_dag_run():
+    a, b, c = bitwise_inputs()
+    c[[900, 300]] = [-5, -2]
+    with pytest.raises(C.ChelisError, match="^shift amount must be non-negative, got -2$"):
+        run_dag("bitwise_i32_65536", [a, b, c])
+
+
+@pytest.mark.parametrize("path", ["dag", "device", "host"])
+def test_movement_views_and_pad_bit_exact(path):
+    """Shrink and stride as views (an offset, scaled strides) read by a
+    chain, a pad of the chain's result, and a stride and a shrink written
+    out by copies."""
+    x = np.random.default_rng(68).standard_normal((512, 1000)).astype(np.float32)
+    got = run_all("movement_f32_512x1000", [x])[path]
+    s = O.slice_(x, [10, 100], [1, 1], [480, 900])
+    t = O.slice_(s, [0, 0], [3, 2], [160, 450])
+    y = t + np.float32(1.0)
+    want = [O.pad(y, [2, 0], [1, 5], np.float32(-1.5)), O.slice_(x, [0, 0], [2, 5], [256, 200]),
+            O.slice_(x, [500, 0], [1, 1], [12, 1000])]
+    for g, w in zip(got, want):
+        assert g.shape == w.shape and bits(g) == bits(w)

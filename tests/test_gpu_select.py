@@ -171,8 +171,29 @@ def test_integer_binary_every_op(dt):
         assert np.array_equal(out.numpy(), want), (dt, op)
         if first < 0:
             assert failure is None
+        elif op in ("shl", "shr"):
+            text = f"shift amount must be non-negative, got {int(b[first])}"
+            assert failure == (first, kind, text), (dt, op, failure)
         else:
             assert failure == (first, kind, O.trap_text(kind, op, dt)), (dt, op, failure)
+
+
+def test_shift_counts_broadcast_and_the_deferred_count_line():
+    """A broadcast count row; through the deferred record the message
+    still names the count at the earliest failing launch's lowest element."""
+    x = np.arange(-40, 40, dtype=np.int16).reshape(8, 10)
+    c = np.array([[0, 1, 3, 15, 16, 17, 100, 2, 5, 9]], np.int16)
+    want, first, _ = O.int_binary("shr", "i16", x, np.broadcast_to(c, x.shape))
+    out, failure = C.integer_op("shr", C.to_device(x), C.to_device(c))
+    assert failure is None and np.array_equal(out.numpy(), want)
+    bad = c.copy()
+    bad[0, [6, 3]] = [-7, -2]
+    C.take_numeric_failure()
+    C.integer_op("add", C.to_device(x), C.to_device(x), deferred=True)
+    C.integer_op("shl", C.to_device(x), C.to_device(bad), deferred=True)
+    C.integer_op("shr", C.to_device(x), C.to_device(np.full((1, 10), -9, np.int16)), deferred=True)
+    assert C.take_numeric_failure() == (3, 2, "shift amount must be non-negative, got -2")
+    assert C.take_numeric_failure() is None
 
 
 @pytest.mark.parametrize("dt", ["i8", "i32", "i64"])
@@ -308,3 +329,26 @@ def test_cumsum_overflow_in_the_lanes_order_and_a_strided_view():
     v = d.view((48, 64), (1, 48))  # the transpose
     out, failure = C.cumsum(v, 1)
     assert failure is None and bits(out.numpy()).tobytes() == bits(O.cumsum("f32", np.ascontiguousarray(base.T), 1)[0]).tobytes()
+
+
+# ---------------------------------------------------------------- pad
+@pytest.mark.parametrize("dtype", [np.float32, np.float64, np.uint16, np.int8, np.int32, np.int64])
+def test_pad_matches_the_oracle(dtype):
+    rng = np.random.default_rng(72)
+    x = (rng.standard_normal((33, 1, 70)) * 40).astype(dtype)
+    fill = dtype(5) if dtype != np.float32 else np.float32(-0.0)
+    for lo, hi in (([0, 0, 0], [0, 0, 0]), ([2, 3, 1], [1, 0, 9]), ([0, 5, 64], [7, 2, 0])):
+        out = C.pad(C.to_device(x), lo, hi, fill)
+        assert bits(out.numpy()).tobytes() == bits(O.pad(x, lo, hi, fill)).tobytes(), (lo, hi)
+
+
+def test_pad_of_a_transposed_view_into_a_strided_output():
+    rng = np.random.default_rng(73)
+    base = rng.standard_normal((40, 24)).astype(np.float64)
+    v = C.to_device(base).view((24, 40), (1, 24))
+    holder = C.empty((30, 2, 46), np.float64)
+    out = holder.view((30, 46), (2 * 46, 1))  # every other [30, 46] plane row
+    C.pad(v, [4, 1], [2, 5], 2.5, out=out)
+    want = O.pad(np.ascontiguousarray(base.T), [4, 1], [2, 5], 2.5)
+    got = holder.numpy()[:, 0, :]
+    assert got.tobytes() == want.tobytes()

@@ -320,7 +320,22 @@ def test_cast_reports_the_lowest_index_offender():
 
 
 # ---------------------------------------------------------------- integer arithmetic
-def _py(op, x, y):
+def _wrap(v, bits):
+    half = 1 << (bits - 1)
+    return (v + half) % (1 << bits) - half
+
+
+def _py(op, x, y, bits=64):
+    if op in ("bitand", "bitor", "bitxor"):
+        # Python's integers behave as infinite two's complement
+        return x & y if op == "bitand" else x | y if op == "bitor" else x ^ y
+    if op in ("shl", "shr"):
+        # [05-OP-47] / [04-NUM-13], spec/05-risc-primitives.md:4062-4082
+        if y < 0:
+            return "domain"
+        if op == "shl":
+            return 0 if y >= bits else _wrap(x << y, bits)
+        return (-1 if x < 0 else 0) if y >= bits else x >> y
     if op == "add":
         return x + y
     if op == "sub":
@@ -353,7 +368,7 @@ def test_integer_binary_against_unbounded_integers(op, dt):
                         rng.integers(info.min, info.max, 100, dtype=CAR[dt], endpoint=True)]).astype(CAR[dt])
     for i in range(len(a)):
         y, first, kind = O.int_binary(op, dt, a[i:i + 1], b[i:i + 1])
-        want = _py(op, int(a[i]), int(b[i]))
+        want = _py(op, int(a[i]), int(b[i]), info.bits)
         if isinstance(want, str):
             assert first == 0 and O.FAILURE_KINDS[kind] == want
         elif want < info.min or want > info.max:
@@ -383,6 +398,17 @@ def test_integer_trap_texts_of_the_c_lane():
     assert first == 1 and O.trap_text(kind, "mul", "i8") == "numeric trap: overflow in mul at i8"
     _, first, kind = O.int_unary("neg", "i64", [5, -(2 ** 63)])
     assert first == 1 and O.trap_text(kind, "neg", "i64") == "numeric trap: overflow in neg at i64"
+
+
+def test_shift_known_answers():
+    """The spec's cases: counts at or above w give 0 (shr of a negative
+    value -1), shr extends the sign, shl drops the bits past w."""
+    assert O.int_binary("shl", "i8", [1, 1, -1, 3, 64], [7, 8, 1, 100, 1])[0].tolist() == [-128, 0, -2, 0, -128]
+    assert O.int_binary("shr", "i8", [-128, -128, -1, 127, -5], [7, 8, 100, 6, 1])[0].tolist() == [-1, -1, -1, 1, -3]
+    assert O.int_binary("shr", "i64", [-(2 ** 63), 2 ** 62], [63, 62])[0].tolist() == [-1, 1]
+    assert O.int_binary("bitxor", "i16", [-1, 0x5555], [0x00FF, -1])[0].tolist() == [-256, -0x5556]
+    y, first, kind = O.int_binary("shl", "i32", [1, 2, 3], [0, -3, -1])
+    assert (first, O.FAILURE_KINDS[kind]) == (1, "domain")
 
 
 @pytest.mark.parametrize("dt", ["i8", "i32", "i64"])
@@ -516,3 +542,26 @@ def test_cumsum_integers_exact_with_the_overflow_trap(dt):
         y = np.array([[[1], [big], [5]], [[0], [0], [0]]], CAR[dt])  # [2, 3, 1]: line 0 overflows at step 1
         _, first, kind = O.cumsum(dt, y, 1)
         assert (first, O.trap_text(kind, "cumsum", dt)) == (1, f"numeric trap: overflow in cumsum at {dt}")
+
+
+# ---------------------------------------------------------------- movement with bounds
+@pytest.mark.parametrize("dtype", [np.float32, np.float64, np.uint16, np.int8, np.int32, np.int64])
+def test_pad_is_numpy_constant_pad(dtype):
+    rng = np.random.default_rng(15)
+    for shape, pads in [((5, 7), [(1, 2), (0, 3)]), ((3, 1, 4), [(0, 0), (2, 2), (1, 0)]), ((6,), [(4, 0)]),
+                        ((2, 0, 3), [(1, 1), (2, 0), (0, 1)])]:
+        x = (rng.standard_normal(shape) * 50).astype(dtype)
+        fill = dtype(7) if dtype != np.float32 else np.float32(-0.0)
+        want = np.pad(x, pads, constant_values=fill)
+        got = O.pad(x, [p[0] for p in pads], [p[1] for p in pads], fill)
+        assert got.shape == want.shape and got.tobytes() == want.tobytes(), (shape, pads)
+
+
+def test_shrink_and_stride_are_numpy_slices():
+    x = np.arange(5 * 9 * 4, dtype=np.float64).reshape(5, 9, 4) * 1.5
+    assert O.slice_(x, [1, 2, 0], [1, 1, 1], [3, 6, 4]).tobytes() == x[1:4, 2:8, :].tobytes()
+    for steps in ([1, 2, 3], [2, 4, 1], [5, 9, 4], [7, 1, 2]):
+        out = [-(-e // s) for e, s in zip(x.shape, steps)]
+        want = x[::steps[0], ::steps[1], ::steps[2]]
+        assert O.slice_(x, [0, 0, 0], steps, out).tobytes() == np.ascontiguousarray(want).tobytes(), steps
+    assert O.slice_(x, [2, 3, 1], [1, 1, 1], [0, 6, 3]).size == 0
