@@ -146,6 +146,8 @@ SIGNATURES = {
     "chelis_hip_take_numeric_failure": (c_int32, [POINTER(NumericFailure)]),
     "chelis_hip_cumsum": (c_int32, [P, c_int32, c_int32, P, POINTER(NumericFailure)]),
     "chelis_hip_pad": (c_int32, [P, POINTER(c_int64), ctypes.c_uint64, P]),
+    "chelis_hip_scatter": (c_int32, [c_int32, P, P, P, c_int32, c_int32, P, POINTER(NumericFailure)]),
+    "chelis_hip_scatter_elements": (c_int32, [P, P, P, c_int32, P, POINTER(NumericFailure)]),
     "chelis_hip_allocation_counts": (None, [POINTER(c_int64), POINTER(c_int64)]),
     "chelis_hip_set_exact_matmul": (c_int32, [c_int32]),
     "chelis_hip_set_exact": (c_int32, [c_int32]),
@@ -607,6 +609,26 @@ def pad(x, lo, hi, fill, out=None):
     return out
 
 
+def scatter(target, indices, updates, axis: int, batch_rank: int = 0, add: bool = False, out=None,
+            deferred: bool = False):
+    """chelis_hip_scatter (ScatterAdd when `add`, else the replacing
+    Scatter); returns (out, failure) as cast does."""
+    out = out or empty(target.shape, target.dtype)
+    f = NumericFailure()
+    check(lib().chelis_hip_scatter(int(add), _p(target), _p(indices), _p(updates), axis, batch_rank, _p(out),
+                                   None if deferred else ctypes.byref(f)), "scatter")
+    return out, None if deferred else _failure(f)
+
+
+def scatter_elements(data, indices, updates, axis: int, out=None, deferred: bool = False):
+    """chelis_hip_scatter_elements; returns (out, failure) as cast does."""
+    out = out or empty(data.shape, data.dtype)
+    f = NumericFailure()
+    check(lib().chelis_hip_scatter_elements(_p(data), _p(indices), _p(updates), axis, _p(out),
+                                            None if deferred else ctypes.byref(f)), "scatter_elements")
+    return out, None if deferred else _failure(f)
+
+
 def take_numeric_failure():
     """chelis_hip_take_numeric_failure: the earliest deferred failure since
     the last read as (index, kind, trap line), or None; clears the record."""
@@ -730,7 +752,7 @@ class DagProgram:
         kinds = [line.split()[1] for line in self.describe().splitlines() if len(line.split()) > 1]
         self.has_count = "count" in kinds
         # launches that record into the deferred failure record
-        self.has_traps = any(k in ("cast", "integer", "gather", "cumsum") for k in kinds)
+        self.has_traps = any(k in ("cast", "integer", "gather", "cumsum", "scatter") for k in kinds)
 
     def __del__(self):
         try:

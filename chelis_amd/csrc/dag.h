@@ -74,6 +74,8 @@ enum class Op : uint8_t {
     // movement with bounds: pad (a materialized copy), shrink and stride
     // (views)
     Pad, Shrink, Stride,
+    // sparse writes: target, indices, updates (axis, batch_rank)
+    ScatterAdd, Scatter, ScatterElements,
     // reductions over one axis
     Sum, MaxReduce, MinReduce, ProdReduce, Argmax, Argmin, Count, Softmax,
     // movement
@@ -216,8 +218,9 @@ enum class RegionKind : uint8_t {
     // the extrema cotangent (code: min bit 0, right operand bit 1), a keyed
     // uniform draw
     ExtremaAdjoint, Uniform,
-    // the ordered scan (axis, code: reverse); a pad (lo, fill)
-    Scan, Pad
+    // the ordered scan (axis, code: reverse); a pad (lo, fill); a scatter
+    // (code: 0 replace, 1 add, 2 elements; axis, batch_rank)
+    Scan, Pad, Scatter
 };
 const char *region_kind_name(RegionKind k);
 

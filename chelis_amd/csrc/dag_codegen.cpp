@@ -281,7 +281,8 @@ std::string emit_source(const Plan &plan, const Graph &fused, const std::string 
         bool traps = false;
         for (const Region &r : plan.regions)
             traps = traps || r.kind == RegionKind::Cast || r.kind == RegionKind::Integer ||
-                    r.kind == RegionKind::Gather || r.kind == RegionKind::Scan;
+                    r.kind == RegionKind::Gather || r.kind == RegionKind::Scan ||
+                    r.kind == RegionKind::Scatter;
         if (traps) {
             // the earliest failing launch's lowest failing element
             // ([04-NUM-15]), read once after the run

@@ -384,6 +384,11 @@ int32_t run_plan(chelis_dag_program *prog, const chelis_gpu_tensor *const *input
                                      r.high, out);
                 break;
             case RegionKind::Pad: s = chelis_hip_pad(in[0], r.lo.data(), r.fill, out); break;
+            case RegionKind::Scatter:
+                s = r.code == 2 ? chelis_hip_scatter_elements(in[0], in[1], in[2], (int32_t)r.axis, out, nullptr)
+                                : chelis_hip_scatter(r.code, in[0], in[1], in[2], (int32_t)r.axis,
+                                                     (int32_t)r.batch_rank, out, nullptr);
+                break;
             case RegionKind::Scan:
                 s = chelis_hip_cumsum(in[0], (int32_t)r.axis, r.code, out, nullptr);
                 break;

@@ -69,6 +69,7 @@ const char *region_kind_name(RegionKind k) {
         case RegionKind::Uniform: return "uniform_like";
         case RegionKind::Scan: return "cumsum";
         case RegionKind::Pad: return "pad";
+        case RegionKind::Scatter: return "scatter";
     }
     return "?";
 }
@@ -1202,6 +1203,21 @@ struct Planner {
                         return fail("node " + std::to_string(n.id) + ": Bitwise needs two integer operands");
                     single(n, RegionKind::Integer, CHELIS_INT_BITAND + n.code);
                     continue;
+                case Op::ScatterAdd: case Op::Scatter: case Op::ScatterElements: {
+                    if (n.inputs.size() != 3)
+                        return fail("node " + std::to_string(n.id) + ": " + n.variant +
+                                    " reads target, indices and updates");
+                    Region r;
+                    r.kind = RegionKind::Scatter;
+                    r.code = n.op == Op::Scatter ? 0 : n.op == Op::ScatterAdd ? 1 : 2;
+                    r.axis = n.axis;
+                    r.batch_rank = n.batch_rank;
+                    r.in = n.inputs;
+                    r.out = n.id;
+                    r.covers = {n.id};
+                    claim(r);
+                    continue;
+                }
                 case Op::Pad: {
                     const std::string why = window_error(n);
                     if (!why.empty()) return fail("node " + std::to_string(n.id) + ": " + why);

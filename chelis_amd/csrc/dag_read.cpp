@@ -46,6 +46,7 @@ const OpName kOps[] = {
     {"ExtremaAdjoint", Op::ExtremaAdjoint}, {"UniformLike", Op::UniformLike}, {"KeyFromSeed", Op::KeyFromSeed},
     {"Split", Op::SplitKey}, {"FoldIn", Op::FoldIn}, {"Cumsum", Op::Cumsum},
     {"Bitwise", Op::Bitwise}, {"Pad", Op::Pad}, {"Shrink", Op::Shrink}, {"Stride", Op::Stride},
+    {"ScatterAdd", Op::ScatterAdd}, {"Scatter", Op::Scatter}, {"ScatterElements", Op::ScatterElements},
 };
 
 struct PrimName {
@@ -328,9 +329,12 @@ bool read_op(const Json &op, Graph *g, Node *n, std::string *why) {
             if (p.kind != Json::String) return (*why = var + " needs its kind", false);
             n->compare = p.text;
             return true;
-        case Op::Gather:
+        case Op::Gather: case Op::ScatterAdd: case Op::Scatter:
             if (!int_of(p.get("axis"), &n->axis) || !int_of(p.get("batch_rank"), &n->batch_rank))
-                return (*why = "Gather needs axis and batch_rank", false);
+                return (*why = var + " needs axis and batch_rank", false);
+            return true;
+        case Op::ScatterElements:
+            if (!int_of(p.get("axis"), &n->axis)) return (*why = "ScatterElements needs an axis", false);
             return true;
         case Op::ExtremaAdjoint: {
             // ExtremaKind / ExtremaOperand (dag.rs:596-606)

@@ -24,6 +24,8 @@
 #include <type_traits>
 #include <vector>
 
+#include <hipcub/hipcub.hpp>
+
 #include "hip_common.h"
 #include "narrow.h"
 #include "strided.h"
@@ -575,6 +577,152 @@ __global__ __launch_bounds__(256) void pad_kernel(const U *__restrict__ x, U *__
     }
 }
 
+// ---------------------------------------------------------------- scatter
+// ScatterAdd / Scatter / ScatterElements with the C lane's results
+// (crates/chelis-backend-c/src/emit.rs:7382-7470, 7772-7990): every update
+// gets its destination in the row-major target, then the (destination,
+// position) pairs are radix-sorted - a stable sort, so each destination's
+// updates lie together in ascending position. Scatter and ScatterElements
+// keep the last of each run (the highest position: the last write); the
+// add folds each run - the target's value, then the updates in order - by
+// the canonical pair tree. The reference HIP lane adds with atomics (an
+// order that varies run to run) and runs the replacing forms on one thread
+// (crates/chelis-backend-hip/src/kernels.rs:2599-2765).
+struct ScatterGeom {
+    int64_t axis_size, after, index_count, outer_per_batch, total;  // hyperplane form
+    int32_t elements, rank, axis;                                  // ScatterElements
+    int64_t idx_shape[8], target_shape[8];
+};
+
+// An update's destination (the sentinel, past every destination, when its
+// index is outside the axis: it fails domain at its position) and its
+// position.
+template <typename I, typename K>
+__global__ __launch_bounds__(256) void scatter_keys_kernel(const I *__restrict__ indices, View8 iv, ScatterGeom g,
+                                                           K sentinel, K *__restrict__ keys, K *__restrict__ pos,
+                                                           uint64_t seq, unsigned long long *rec) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t base = (int64_t)blockIdx.x * blockDim.x; base < g.total; base += stride) {
+        const int64_t i = base + threadIdx.x;
+        unsigned long long k = 0ull;
+        if (i < g.total) {
+            int64_t dst = 0;
+            bool ok;
+            if (g.elements) {
+                const int64_t sel = (int64_t)indices[logical_offset(iv, i)];
+                ok = sel >= 0 && sel < g.target_shape[g.axis];
+                int64_t r = i, scale = 1;
+                for (int a = g.rank - 1; a >= 0; --a) {
+                    const int64_t c = r % g.idx_shape[a];
+                    r /= g.idx_shape[a];
+                    dst += (a == g.axis ? sel : c) * scale;
+                    scale *= g.target_shape[a];
+                }
+            } else {
+                const int64_t d = i % g.after, t = i / g.after, j = t % g.index_count, b = t / g.index_count;
+                const int64_t sel = (int64_t)indices[logical_offset(iv, (b / g.outer_per_batch) * g.index_count + j)];
+                ok = sel >= 0 && sel < g.axis_size;
+                dst = (b * g.axis_size + sel) * g.after + d;
+            }
+            keys[i] = ok ? (K)dst : sentinel;
+            pos[i] = (K)i;
+            if (!ok) k = fail_key(seq, i, kDomain);
+        }
+        merge_failures(k, rec);
+    }
+}
+
+// The last update of each destination's run.
+template <typename U, typename K>
+__global__ __launch_bounds__(256) void scatter_last_kernel(const K *__restrict__ skeys, const K *__restrict__ spos,
+                                                           int64_t n, K sentinel, const U *__restrict__ upd, View8 uv,
+                                                           U *__restrict__ out) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < n; p += stride) {
+        const K d = skeys[p];
+        if (d != sentinel && (p + 1 == n || skeys[p + 1] != d)) out[d] = upd[logical_offset(uv, (int64_t)spos[p])];
+    }
+}
+
+// One node of the add's tree at the operand's arithmetic width: binary32 /
+// binary64 adds; bf16 / f16 in binary32, rounded to the format at every
+// node ([04-NUM-8]); integers checked against the width.
+template <int DT>
+struct AddNode {
+    using S = typename Dt<DT>::S;
+    using A = std::conditional_t<DT == CHELIS_DTYPE_F64, double,
+                                 std::conditional_t<Dt<DT>::kFloat, float, int64_t>>;
+    __device__ static A leaf(S v) {
+        if constexpr (DT == CHELIS_DTYPE_BF16) return bf16_to_f32(v);
+        else if constexpr (DT == CHELIS_DTYPE_F16) return f16_to_f32(v);
+        else return (A)v;
+    }
+    __device__ static bool add(A l, A r, A *o) {
+        if constexpr (DT == CHELIS_DTYPE_BF16) *o = bf16_to_f32(f32_to_bf16(l + r));
+        else if constexpr (DT == CHELIS_DTYPE_F16) *o = f16_to_f32(f32_to_f16(l + r));
+        else if constexpr (Dt<DT>::kFloat) *o = l + r;
+        else {
+            if (__builtin_add_overflow(l, r, o)) return false;
+            return *o >= (A)std::numeric_limits<S>::min() && *o <= (A)std::numeric_limits<S>::max();
+        }
+        return true;
+    }
+    __device__ static S store(A v) {
+        if constexpr (DT == CHELIS_DTYPE_BF16) return f32_to_bf16(v);
+        else if constexpr (DT == CHELIS_DTYPE_F16) return f32_to_f16(v);
+        else if constexpr (Dt<DT>::kFloat) return canon(v);
+        else return (S)v;
+    }
+};
+
+// A thread per run start folds [out[d], its updates...] leaf by leaf in a
+// carry stack: a complete pair subtree of 2^l leaves waits at level l until
+// its sibling arrives, and the partial subtrees left at the end join from
+// the lowest level up - the canonical adjacent-pair tree. An integer node
+// outside the width fails overflow, keyed past every update position (index
+// errors come first, as in the C lane's order).
+template <int DT, typename K>
+__global__ __launch_bounds__(256) void scatter_add_kernel(const K *__restrict__ skeys, const K *__restrict__ spos,
+                                                          int64_t n, K sentinel, const typename Dt<DT>::S *upd,
+                                                          View8 uv, typename Dt<DT>::S *out, uint64_t seq,
+                                                          unsigned long long *rec) {
+    using N = AddNode<DT>;
+    using A = typename N::A;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t base = (int64_t)blockIdx.x * blockDim.x; base < n; base += stride) {
+        const int64_t p = base + threadIdx.x;
+        unsigned long long k = 0ull;
+        if (p < n) {
+            const K d = skeys[p];
+            if (d != sentinel && (p == 0 || skeys[p - 1] != d)) {
+                A st[48];
+                uint64_t cnt = 0;
+                bool ok = true;
+                auto push = [&](A v) {
+                    int lv = 0;
+                    for (uint64_t c = cnt; (c & 1) && ok; c >>= 1, ++lv) ok = N::add(st[lv], v, &v);
+                    st[lv] = v;
+                    ++cnt;
+                };
+                push(N::leaf(out[d]));
+                for (int64_t q = p; q < n && skeys[q] == d && ok; ++q)
+                    push(N::leaf(upd[logical_offset(uv, (int64_t)spos[q])]));
+                A acc{};
+                bool have = false;
+                for (int lv = 0; ok && (cnt >> lv) != 0; ++lv)
+                    if ((cnt >> lv) & 1) {
+                        if (have) ok = N::add(st[lv], acc, &acc);
+                        else acc = st[lv];
+                        have = true;
+                    }
+                if (ok) out[d] = N::store(acc);
+                else k = fail_key(seq, n + (int64_t)d, kOverflow);
+            }
+        }
+        if constexpr (!Dt<DT>::kFloat) merge_failures(k, rec);
+    }
+}
+
 // ---------------------------------------------------------------- host: the failure channel
 // Per device: word [2..3] of the status words is the deferred record, [4..5]
 // the record of a call that waits for its own result. A deferred launch's
@@ -595,6 +743,7 @@ struct Sink {
 struct Label {
     std::string text;
     bool shift = false;
+    std::string overflow;  // when set, the text of an overflow (another prim)
 };
 std::vector<Label> g_labels[kMaxDevices];
 
@@ -619,7 +768,8 @@ const char *kind_text(int kind) {
 // The sink a trapping launch records into: its own word when the caller
 // waits for the result (failure != NULL), else the deferred word under the
 // next sequence number, labelled "<op> at <prim>".
-int32_t open_sink(bool wait, const std::string &label, Sink *s, bool shift = false) {
+int32_t open_sink(bool wait, const std::string &label, Sink *s, bool shift = false,
+                  const std::string &overflow = std::string()) {
     int32_t *words = status_words(nullptr);
     if (!words) return set_error(CHELIS_HIP_EHIP, "no HIP device status words");
     s->wait = wait;
@@ -634,7 +784,7 @@ int32_t open_sink(bool wait, const std::string &label, Sink *s, bool shift = fal
     std::lock_guard<std::mutex> lock(g_fail_mutex);
     std::vector<Label> &labels = g_labels[device];
     const uint64_t seq = std::min<uint64_t>(labels.size(), kSeqMax);
-    if (labels.size() <= kSeqMax) labels.push_back(Label{label, shift});
+    if (labels.size() <= kSeqMax) labels.push_back(Label{label, shift, overflow});
     s->rec = reinterpret_cast<unsigned long long *>(words + 2);
     s->detail = reinterpret_cast<long long *>(words + 6);
     s->seq = seq << kSeqShift;
@@ -658,7 +808,8 @@ int32_t fill_failure(chelis_hip_numeric_failure *f, unsigned long long word, con
         CHELIS_HIP_TRY(hipMemcpy(&count, detail, sizeof count, hipMemcpyDeviceToHost));
         snprintf(f->message, sizeof f->message, "shift amount must be non-negative, got %lld", count);
     } else {
-        snprintf(f->message, sizeof f->message, "numeric trap: %s in %s", kind_text(f->kind), label.text.c_str());
+        const std::string &t = f->kind == kOverflow && !label.overflow.empty() ? label.overflow : label.text;
+        snprintf(f->message, sizeof f->message, "numeric trap: %s in %s", kind_text(f->kind), t.c_str());
     }
     return CHELIS_HIP_OK;
 }
@@ -674,12 +825,13 @@ int32_t take_word(unsigned long long *rec, unsigned long long *word) {
 }
 
 // After the launch of a waiting call: its record, read and cleared.
-int32_t close_sink(const Sink &s, const std::string &label, chelis_hip_numeric_failure *f, bool shift = false) {
+int32_t close_sink(const Sink &s, const std::string &label, chelis_hip_numeric_failure *f, bool shift = false,
+                   const std::string &overflow = std::string()) {
     if (!s.wait) return CHELIS_HIP_OK;
     CHELIS_HIP_TRY(hipStreamSynchronize(stream()));
     unsigned long long word = 0ull;
     if (int32_t st = take_word(s.rec, &word)) return st;
-    return fill_failure(f, word, Label{label, shift}, s.detail);
+    return fill_failure(f, word, Label{label, shift, overflow}, s.detail);
 }
 
 // ---------------------------------------------------------------- host: checks and launches
@@ -1118,6 +1270,191 @@ extern "C" int32_t chelis_hip_pad(const chelis_gpu_tensor *x, const int64_t *lo,
         case 4: return launch_pad<uint32_t>(x, g, fill_bits, out);
         default: return launch_pad<uint64_t>(x, g, fill_bits, out);
     }
+}
+
+namespace {
+// The scatter's passes over keys of width K (destinations and positions):
+// the target copied into out, the keys, the stable sort, the runs applied.
+template <typename K>
+int32_t run_scatter(int32_t mode, const chelis_gpu_tensor *target, const chelis_gpu_tensor *indices,
+                    const chelis_gpu_tensor *updates, const chelis_gpu_tensor *out, const ScatterGeom &g,
+                    const Sink &s) {
+    hipStream_t st = stream();
+    const int64_t zeros[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (int32_t r = chelis_hip_pad(target, zeros, 0, out)) return r;
+    const int64_t n = g.total;
+    if (!n) return CHELIS_HIP_OK;
+    const K sentinel = (K)out->count;
+    int end_bit = 1;
+    while (end_bit < (int)(8 * sizeof(K)) && ((uint64_t)sentinel >> end_bit) != 0) ++end_bit;
+    size_t temp = 0;
+    K *none = nullptr;
+    // the item count hipcub takes is an int: a larger scatter is refused by the caller
+    CHELIS_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(nullptr, temp, none, none, none, none, (int)n, 0, end_bit, st));
+    const size_t pairs = (size_t)n * sizeof(K);
+    char *buf = static_cast<char *>(scratch_alloc(4 * pairs + temp));
+    if (!buf) return set_error(CHELIS_HIP_EHIP, "scatter: no device memory for %lld updates", (long long)n);
+    K *keys = reinterpret_cast<K *>(buf), *pos = keys + n, *skeys = pos + n, *spos = skeys + n;
+    void *tmp = buf + 4 * pairs;
+    int32_t rc = CHELIS_HIP_OK;
+    const View8 iv = view_of(indices), uv = view_of(updates);
+    const unsigned blocks = (unsigned)map_blocks(n);
+    if (indices->dtype == CHELIS_DTYPE_I32)
+        scatter_keys_kernel<int32_t, K><<<blocks, 256, 0, st>>>(static_cast<const int32_t *>(indices->data), iv, g,
+                                                               sentinel, keys, pos, s.seq, s.rec);
+    else
+        scatter_keys_kernel<int64_t, K><<<blocks, 256, 0, st>>>(static_cast<const int64_t *>(indices->data), iv, g,
+                                                               sentinel, keys, pos, s.seq, s.rec);
+    if (hipGetLastError() != hipSuccess) rc = set_error(CHELIS_HIP_EHIP, "scatter: key launch failed");
+    if (!rc && hipcub::DeviceRadixSort::SortPairs(tmp, temp, keys, skeys, pos, spos, (int)n, 0, end_bit, st) !=
+                   hipSuccess)
+        rc = set_error(CHELIS_HIP_EHIP, "scatter: the sort failed");
+    if (!rc) {
+        if (mode != 1) {
+            switch (dtype_width(out->dtype)) {
+                case 1:
+                    scatter_last_kernel<uint8_t, K><<<blocks, 256, 0, st>>>(
+                        skeys, spos, n, sentinel, static_cast<const uint8_t *>(updates->data), uv,
+                        static_cast<uint8_t *>(out->data));
+                    break;
+                case 2:
+                    scatter_last_kernel<uint16_t, K><<<blocks, 256, 0, st>>>(
+                        skeys, spos, n, sentinel, static_cast<const uint16_t *>(updates->data), uv,
+                        static_cast<uint16_t *>(out->data));
+                    break;
+                case 4:
+                    scatter_last_kernel<uint32_t, K><<<blocks, 256, 0, st>>>(
+                        skeys, spos, n, sentinel, static_cast<const uint32_t *>(updates->data), uv,
+                        static_cast<uint32_t *>(out->data));
+                    break;
+                default:
+                    scatter_last_kernel<uint64_t, K><<<blocks, 256, 0, st>>>(
+                        skeys, spos, n, sentinel, static_cast<const uint64_t *>(updates->data), uv,
+                        static_cast<uint64_t *>(out->data));
+            }
+        } else {
+#define CHELIS_SCATTER_ADD(DT)                                                                                    \
+    case DT:                                                                                                      \
+        scatter_add_kernel<DT, K><<<blocks, 256, 0, st>>>(                                                        \
+            skeys, spos, n, sentinel, static_cast<const typename Dt<DT>::S *>(updates->data), uv,                 \
+            static_cast<typename Dt<DT>::S *>(out->data), s.seq, s.rec);                                          \
+        break;
+            switch (out->dtype) {
+                CHELIS_SCATTER_ADD(CHELIS_DTYPE_F32)
+                CHELIS_SCATTER_ADD(CHELIS_DTYPE_F64)
+                CHELIS_SCATTER_ADD(CHELIS_DTYPE_BF16)
+                CHELIS_SCATTER_ADD(CHELIS_DTYPE_F16)
+                CHELIS_SCATTER_ADD(CHELIS_DTYPE_I8)
+                CHELIS_SCATTER_ADD(CHELIS_DTYPE_I16)
+                CHELIS_SCATTER_ADD(CHELIS_DTYPE_I32)
+                CHELIS_SCATTER_ADD(CHELIS_DTYPE_I64)
+                default: rc = set_error(CHELIS_HIP_EDOMAIN, "scatter: no add for this dtype");
+            }
+#undef CHELIS_SCATTER_ADD
+        }
+        if (!rc && hipGetLastError() != hipSuccess) rc = set_error(CHELIS_HIP_EHIP, "scatter: launch failed");
+    }
+    scratch_free(buf, 4 * pairs + temp);
+    return rc;
+}
+
+int32_t scatter_common(int32_t mode, const chelis_gpu_tensor *target, const chelis_gpu_tensor *indices,
+                       const chelis_gpu_tensor *updates, const chelis_gpu_tensor *out, ScatterGeom &g,
+                       chelis_hip_numeric_failure *failure) {
+    static const char *names[] = {"scatter_replace", "scatter", "scatter_elements"};
+    const std::string label = std::string(names[mode]) + " at i64";
+    const std::string overflow = mode == 1 ? std::string("scatter at ") + dtype_name(out->dtype) : std::string();
+    if (g.total > (int64_t)std::numeric_limits<int>::max())
+        return set_error(CHELIS_HIP_EUNSUPPORTED, "%s: more than 2^31 - 1 updates", names[mode]);
+    Sink sink;
+    if (int32_t r = open_sink(failure != nullptr, label, &sink, false, overflow)) return r;
+    const bool narrow = (uint64_t)out->count < 0xFFFFFFFFull && (uint64_t)g.total < 0xFFFFFFFFull;
+    const int32_t st = narrow ? run_scatter<uint32_t>(mode, target, indices, updates, out, g, sink)
+                              : run_scatter<uint64_t>(mode, target, indices, updates, out, g, sink);
+    if (st) return st;
+    return close_sink(sink, label, failure, false, overflow);
+}
+
+int32_t scatter_operands(const char *what, const chelis_gpu_tensor *target, const chelis_gpu_tensor *indices,
+                         const chelis_gpu_tensor *updates, const chelis_gpu_tensor *out) {
+    if (int32_t s = check_tensor(target, "target")) return s;
+    if (int32_t s = check_tensor(indices, "indices")) return s;
+    if (int32_t s = check_tensor(updates, "updates")) return s;
+    if (int32_t s = check_out(out, what)) return s;
+    if (indices->dtype != CHELIS_DTYPE_I32 && indices->dtype != CHELIS_DTYPE_I64)
+        return set_error(CHELIS_HIP_EDOMAIN, "%s: indices must be i32 or i64", what);
+    if (out->dtype != target->dtype || updates->dtype != target->dtype)
+        return set_error(CHELIS_HIP_EDOMAIN, "%s: target, updates and output need one dtype", what);
+    if (out->rank != target->rank || target->rank > 8)
+        return set_error(CHELIS_HIP_EDOMAIN, "%s: the output has the target's shape (rank <= 8)", what);
+    for (int32_t a = 0; a < target->rank; ++a)
+        if (out->shape[a] != target->shape[a])
+            return set_error(CHELIS_HIP_EDOMAIN, "%s: the output has the target's shape", what);
+    return CHELIS_HIP_OK;
+}
+}  // namespace
+
+extern "C" int32_t chelis_hip_scatter(int32_t add, const chelis_gpu_tensor *target, const chelis_gpu_tensor *indices,
+                                      const chelis_gpu_tensor *updates, int32_t axis, int32_t batch_rank,
+                                      const chelis_gpu_tensor *out, chelis_hip_numeric_failure *failure) {
+    const char *what = add ? "scatter" : "scatter_replace";
+    if (int32_t s = scatter_operands(what, target, indices, updates, out)) return s;
+    if (axis < 0 || axis >= target->rank || batch_rank < 0 || batch_rank > axis || batch_rank > indices->rank)
+        return set_error(CHELIS_HIP_EDOMAIN, "%s: axis %d / batch_rank %d outside the operands", what, axis,
+                         batch_rank);
+    // emit.rs:3993-4042: the updates have the gathered shape, paired batch
+    // extents agree; either failing is the domain trap
+    const std::string trap = std::string("numeric trap: domain in ") + what + " at i64";
+    bool shape_ok = updates->rank == target->rank - 1 + indices->rank - batch_rank;
+    for (int32_t a = 0, k = 0; shape_ok && a < target->rank; ++a) {
+        if (a == axis) {
+            for (int32_t q = batch_rank; q < indices->rank && shape_ok; ++q)
+                shape_ok = updates->shape[k++] == indices->shape[q];
+        } else {
+            shape_ok = updates->shape[k++] == target->shape[a];
+        }
+    }
+    int64_t batch = 1, before = 1, after = 1;
+    for (int32_t a = 0; a < batch_rank; ++a) {
+        shape_ok = shape_ok && target->shape[a] == indices->shape[a];
+        batch *= target->shape[a];
+    }
+    if (!shape_ok) return set_error(CHELIS_HIP_EDOMAIN, "%s", trap.c_str());
+    for (int32_t a = 0; a < axis; ++a) before *= target->shape[a];
+    for (int32_t a = axis + 1; a < target->rank; ++a) after *= target->shape[a];
+    ScatterGeom g{};
+    g.axis_size = target->shape[axis];
+    g.after = after;
+    g.index_count = batch == 0 ? 0 : indices->count / batch;
+    g.outer_per_batch = (batch == 0 || before == 0) ? 1 : before / batch;
+    g.total = updates->count;
+    if (g.total && (g.after == 0 || g.index_count == 0)) g.total = 0;
+    return scatter_common(add ? 1 : 0, target, indices, updates, out, g, failure);
+}
+
+extern "C" int32_t chelis_hip_scatter_elements(const chelis_gpu_tensor *data, const chelis_gpu_tensor *indices,
+                                               const chelis_gpu_tensor *updates, int32_t axis,
+                                               const chelis_gpu_tensor *out, chelis_hip_numeric_failure *failure) {
+    if (int32_t s = scatter_operands("scatter_elements", data, indices, updates, out)) return s;
+    if (axis < 0 || axis >= data->rank)
+        return set_error(CHELIS_HIP_EDOMAIN, "scatter_elements: axis %d outside the operands", axis);
+    // emit.rs:4160-4168: the updates have the indices' shape, every operand
+    // the data's rank (crates/chelis-abi/src/metadata.rs:831-846: off the axis no index
+    // extent passes the data's)
+    bool shape_ok = indices->rank == data->rank && updates->rank == data->rank;
+    for (int32_t a = 0; shape_ok && a < data->rank; ++a)
+        shape_ok = updates->shape[a] == indices->shape[a] && (a == axis || indices->shape[a] <= data->shape[a]);
+    if (!shape_ok) return set_error(CHELIS_HIP_EDOMAIN, "numeric trap: domain in scatter_elements at i64");
+    ScatterGeom g{};
+    g.elements = 1;
+    g.rank = data->rank;
+    g.axis = axis;
+    g.total = updates->count;
+    for (int32_t a = 0; a < data->rank; ++a) {
+        g.idx_shape[a] = indices->shape[a];
+        g.target_shape[a] = data->shape[a];
+    }
+    return scatter_common(2, data, indices, updates, out, g, failure);
 }
 
 extern "C" int32_t chelis_hip_take_numeric_failure(chelis_hip_numeric_failure *failure) {

@@ -291,6 +291,37 @@ int32_t chelis_hip_cumsum(const chelis_gpu_tensor *x, int32_t axis, int32_t reve
  * elements must not overlap); rank <= 8. */
 int32_t chelis_hip_pad(const chelis_gpu_tensor *x, const int64_t *lo, uint64_t fill_bits,
                        const chelis_gpu_tensor *out);
+/* scatter: RiscOp::ScatterAdd{axis, batch_rank} when `add`, else
+ * RiscOp::Scatter{axis, batch_rank} (crates/chelis-dag-core/src/dag.rs:
+ * 1360-1384), replacing the reference HIP lane's scatter_add (atomics) and
+ * single-thread scatter_replace (kernels.rs:2599-2716) with the C lane's
+ * results (crates/chelis-backend-c/src/emit.rs:7382-7470, 7842-7990). out
+ * has the target's shape; updates the gathered shape target[..axis] ++
+ * indices[batch_rank..] ++ target[axis+1..] (else CHELIS_HIP_EDOMAIN with
+ * `numeric trap: domain in scatter at i64`). Update u goes where the gather
+ * of the same geometry would read. Replace: each cell takes its last update
+ * in row-major position (the last write). Add: each targeted cell is the
+ * canonical pair tree over [its target value, its updates in ascending
+ * position] at the operand width (bf16 / f16 rounded at every node, the
+ * total NaN-canonical); any dtype but bool. An index outside the axis fails
+ * `domain` at the update's position (`numeric trap: domain in scatter at
+ * i64`, or `scatter_replace`); an integer node outside the width fails
+ * `overflow` (`numeric trap: overflow in scatter at <dtype>`), its index the
+ * update count plus the destination's row-major index. Operands may be
+ * strided; out contiguous. At most 2^31 - 1 updates.
+ *
+ * scatter_elements: RiscOp::ScatterElements{axis} (dag.rs:1386-1404;
+ * kernels.rs:2718-2765): indices and updates share a shape and every
+ * operand the data's rank, no index extent off the axis above the data's
+ * (crates/chelis-abi/src/metadata.rs:831-846); the update at coordinates c
+ * goes to c with c[axis] = indices[c], the last write winning. Failures as
+ * scatter's, named scatter_elements. */
+int32_t chelis_hip_scatter(int32_t add, const chelis_gpu_tensor *target, const chelis_gpu_tensor *indices,
+                           const chelis_gpu_tensor *updates, int32_t axis, int32_t batch_rank,
+                           const chelis_gpu_tensor *out, chelis_hip_numeric_failure *failure);
+int32_t chelis_hip_scatter_elements(const chelis_gpu_tensor *data, const chelis_gpu_tensor *indices,
+                                    const chelis_gpu_tensor *updates, int32_t axis, const chelis_gpu_tensor *out,
+                                    chelis_hip_numeric_failure *failure);
 /* Waits for the library stream, then reads and clears the current device's
  * deferred failure record (kind 0: none). */
 int32_t chelis_hip_take_numeric_failure(chelis_hip_numeric_failure *failure);

@@ -1149,3 +1149,143 @@ void orc_slice(int width, const void *x, int rank, const int64_t *src_shape, con
         memcpy((char *)y + i * width, (const char *)x + orc_flat(rank, src_shape, c) * width, (size_t)width);
     }
 }
+
+/* Sparse scatters (RiscOp::ScatterAdd / Scatter / ScatterElements,
+ * crates/chelis-dag-core/src/dag.rs:1360-1404) as the C lane runs them
+ * (crates/chelis-backend-c/src/emit.rs:7382-7470): the result starts as the
+ * target; the updates are visited in ascending row-major position, each
+ * index checked against the axis extent (the first outside it fails
+ * domain: its position is returned). `dest` holds each update's flat
+ * destination in the row-major target. Replace (add = 0) stores each update
+ * in turn, so the last write wins. Add records the destinations, orders
+ * them by a stable counting sort, and folds per destination - its target
+ * value, then its updates in ascending position - level by level, adjacent
+ * pairs left to right, an odd tail carried up (emit.rs:7772-7801,
+ * 7842-7990): floats add at the dtype (bf16 / f16 in binary32, rounded at
+ * every node), the total NaN-canonical; integers fail overflow at the first
+ * node outside the width (returned as n + the destination). */
+static int64_t orc_scatter_apply(int add, int dt, const int64_t *dest, int64_t n, const void *upd, void *out,
+                                 int64_t out_n, int32_t *kind) {
+    const int w = odt_width(dt);
+    if (!add) {
+        for (int64_t i = 0; i < n; ++i) memcpy((char *)out + dest[i] * w, (const char *)upd + i * w, (size_t)w);
+        return -1;
+    }
+    int64_t *end = (int64_t *)calloc((size_t)(out_n + 1), sizeof(int64_t));
+    int64_t *order = (int64_t *)malloc((size_t)(n + 1) * sizeof(int64_t));
+    double *lv = (double *)malloc((size_t)(n + 2) * sizeof(double));
+    int64_t *li = (int64_t *)malloc((size_t)(n + 2) * sizeof(int64_t));
+    int64_t first = -1, lo, hi;
+    odt_limits(dt, &lo, &hi);
+    for (int64_t i = 0; i < n; ++i) end[dest[i]] += 1;
+    for (int64_t d = 1; d < out_n; ++d) end[d] += end[d - 1];
+    for (int64_t i = n - 1; i >= 0; --i) order[--end[dest[i]]] = i;
+    for (int64_t d = 0; d < out_n && first < 0; ++d) {
+        const int64_t a = end[d], b = d + 1 < out_n ? end[d + 1] : n;
+        if (a == b) continue;
+        int64_t leaves = b - a + 1;
+        if (odt_is_float(dt)) {
+            lv[0] = odt_float_at(dt, out, d);
+            for (int64_t k = a; k < b; ++k) lv[k - a + 1] = odt_float_at(dt, upd, order[k]);
+        } else {
+            li[0] = odt_int_at(dt, out, d);
+            for (int64_t k = a; k < b; ++k) li[k - a + 1] = odt_int_at(dt, upd, order[k]);
+        }
+        while (leaves > 1 && first < 0) {
+            const int64_t next = leaves / 2 + leaves % 2;
+            for (int64_t q = 0; q < next; ++q) {
+                const int64_t l = 2 * q, r = l + 1;
+                if (r >= leaves) {
+                    lv[q] = lv[l];
+                    li[q] = li[l];
+                    continue;
+                }
+                switch (dt) {
+                    case ODT_F32: lv[q] = (double)((float)lv[l] + (float)lv[r]); break;
+                    case ODT_F64: lv[q] = lv[l] + lv[r]; break;
+                    case ODT_BF16: case ODT_F16: {
+                        const int k16 = dt == ODT_BF16 ? 0 : 1;
+                        lv[q] = (double)orc_dec16(k16, orc_enc16(k16, (float)lv[l] + (float)lv[r]));
+                        break;
+                    }
+                    default: {
+                        /* operands within the width: only i64 can leave int64 */
+                        int64_t t64 = 0;
+                        const int bad = __builtin_add_overflow(li[l], li[r], &t64);
+                        if (bad || t64 < lo || t64 > hi) {
+                            first = n + d;
+                            *kind = OFAIL_OVERFLOW;
+                        }
+                        li[q] = t64;
+                    }
+                }
+            }
+            leaves = next;
+        }
+        if (first >= 0) break;
+        switch (dt) {
+            case ODT_F32: ((float *)out)[d] = nan32((float)lv[0]); break;
+            case ODT_F64: ((double *)out)[d] = nan64(lv[0]); break;
+            case ODT_BF16: ((uint16_t *)out)[d] = orc_enc16(0, (float)lv[0]); break;
+            case ODT_F16: ((uint16_t *)out)[d] = orc_enc16(1, (float)lv[0]); break;
+            default: odt_int_store(dt, out, d, li[0]);
+        }
+    }
+    free(end);
+    free(order);
+    free(lv);
+    free(li);
+    return first;
+}
+/* Scatter / ScatterAdd (hyperplane form, the gather's geometry above):
+ * update (b, j, d) of [before, index_count, after] goes to the target at
+ * (b, idx[batch of b, j], d) of [before, axis_size, after]. */
+int64_t orc_scatter(int add, int dt, const void *target, const int64_t *idx, const void *upd, void *out,
+                    int64_t before, int64_t axis_size, int64_t after, int64_t index_count, int64_t outer_per_batch,
+                    int32_t *kind) {
+    const int w = odt_width(dt);
+    const int64_t out_n = before * axis_size * after, n = before * index_count * after;
+    *kind = 0;
+    memcpy(out, target, (size_t)(out_n * w));
+    int64_t *dest = (int64_t *)malloc((size_t)(n + 1) * sizeof(int64_t));
+    for (int64_t i = 0; i < n; ++i) {
+        const int64_t d = i % after, t = i / after, j = t % index_count, b = t / index_count;
+        const int64_t g = idx[(b / outer_per_batch) * index_count + j];
+        if (g < 0 || g >= axis_size) {
+            free(dest);
+            *kind = OFAIL_DOMAIN;
+            return i;
+        }
+        dest[i] = (b * axis_size + g) * after + d;
+    }
+    const int64_t r = orc_scatter_apply(add, dt, dest, n, upd, out, out_n, kind);
+    free(dest);
+    return r;
+}
+/* ScatterElements (dag.rs:1386-1404): the update at coordinates c of the
+ * indices' shape goes to the target at c with c[axis] = idx[c]. */
+int64_t orc_scatter_elements(int dt, const void *target, const int64_t *idx, const void *upd, void *out, int rank,
+                             const int64_t *idx_shape, const int64_t *target_shape, int axis, int32_t *kind) {
+    const int w = odt_width(dt);
+    int64_t out_n = 1, n = 1, c[8];
+    for (int a = 0; a < rank; ++a) {
+        out_n *= target_shape[a];
+        n *= idx_shape[a];
+    }
+    *kind = 0;
+    memcpy(out, target, (size_t)(out_n * w));
+    int64_t *dest = (int64_t *)malloc((size_t)(n + 1) * sizeof(int64_t));
+    for (int64_t i = 0; i < n; ++i) {
+        orc_coords(i, rank, idx_shape, c);
+        if (idx[i] < 0 || idx[i] >= target_shape[axis]) {
+            free(dest);
+            *kind = OFAIL_DOMAIN;
+            return i;
+        }
+        c[axis] = idx[i];
+        dest[i] = orc_flat(rank, target_shape, c);
+    }
+    const int64_t r = orc_scatter_apply(0, dt, dest, n, upd, out, out_n, kind);
+    free(dest);
+    return r;
+}

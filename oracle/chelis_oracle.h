@@ -147,6 +147,11 @@ void orc_pad(int width, const void *x, int rank, const int64_t *src_shape, const
              const int64_t *out_shape, uint64_t fill, void *y);
 void orc_slice(int width, const void *x, int rank, const int64_t *src_shape, const int64_t *start,
                const int64_t *step, const int64_t *out_shape, void *y);
+int64_t orc_scatter(int add, int dt, const void *target, const int64_t *idx, const void *upd, void *out,
+                    int64_t before, int64_t axis_size, int64_t after, int64_t index_count, int64_t outer_per_batch,
+                    int32_t *kind);
+int64_t orc_scatter_elements(int dt, const void *target, const int64_t *idx, const void *upd, void *out, int rank,
+                             const int64_t *idx_shape, const int64_t *target_shape, int axis, int32_t *kind);
 int64_t orc_gather(const void *values, int64_t width, int64_t before, int64_t axis_size, int64_t after,
                    const void *idx, int idx_dt, int64_t index_count, int64_t batch_count, void *out, int32_t *kind);
 

@@ -104,6 +104,10 @@ def _declare(L):
         "orc_cumsum": (c_i64, [ctypes.c_int, c_p, c_p, c_i64, c_i64, c_i64, ctypes.c_int, c_p]),
         "orc_pad": (None, [ctypes.c_int, c_p, ctypes.c_int, c_p, c_p, c_p, ctypes.c_uint64, c_p]),
         "orc_slice": (None, [ctypes.c_int, c_p, ctypes.c_int, c_p, c_p, c_p, c_p, c_p]),
+        "orc_scatter": (c_i64, [ctypes.c_int, ctypes.c_int, c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_i64,
+                                c_p]),
+        "orc_scatter_elements": (c_i64, [ctypes.c_int, c_p, c_p, c_p, c_p, ctypes.c_int, c_p, c_p, ctypes.c_int,
+                                         c_p]),
         "orc_gather": (c_i64, [c_p, c_i64, c_i64, c_i64, c_i64, c_p, ctypes.c_int, c_i64, c_i64, c_p, c_p]),
     })
     for name, (res, args) in sig.items():
@@ -535,3 +539,38 @@ def slice_(x, start, step, out_shape):
     src = _i64s(x.shape)
     lib().orc_slice(x.itemsize, _ptr(x), x.ndim, _ptr(src), _ptr(start), _ptr(step), _ptr(out_shape), _ptr(y))
     return y
+
+
+def scatter(dt: str, target, indices, updates, axis: int, batch_rank: int = 0, add: bool = False):
+    """RiscOp::ScatterAdd (add) / Scatter: (result, first failing position
+    or -1, kind); updates have the gathered shape target[..axis] ++
+    indices[batch_rank..] ++ target[axis+1..]. A domain failure's position
+    is the update's; an overflow's is the update count + the destination."""
+    target = _carrier(dt, target)
+    updates = _carrier(dt, updates)
+    idx = np.ascontiguousarray(indices, np.int64)
+    assert updates.shape == gather_shape(target.shape, idx.shape, axis, batch_rank), "updates shape"
+    batch = int(np.prod(target.shape[:batch_rank], dtype=np.int64))
+    before = int(np.prod(target.shape[:axis], dtype=np.int64))
+    after = int(np.prod(target.shape[axis + 1:], dtype=np.int64))
+    index_count = idx.size // batch if batch else 0
+    opb = before // batch if batch and before else 1
+    out = np.empty_like(target)
+    kind = ctypes.c_int32(0)
+    first = lib().orc_scatter(int(add), DTYPE_IDS[dt], _ptr(target), _ptr(idx), _ptr(updates), _ptr(out), before,
+                              target.shape[axis], after, index_count, opb, ctypes.byref(kind))
+    return out, first, kind.value
+
+
+def scatter_elements(dt: str, data, indices, updates, axis: int):
+    """RiscOp::ScatterElements: (result, first failing position or -1, kind)."""
+    data = _carrier(dt, data)
+    updates = _carrier(dt, updates)
+    idx = np.ascontiguousarray(indices, np.int64)
+    assert updates.shape == idx.shape and idx.ndim == data.ndim
+    out = np.empty_like(data)
+    kind = ctypes.c_int32(0)
+    ishape, dshape = _i64s(idx.shape), _i64s(data.shape)  # held for the call
+    first = lib().orc_scatter_elements(DTYPE_IDS[dt], _ptr(data), _ptr(idx), _ptr(updates), _ptr(out), data.ndim,
+                                       _ptr(ishape), _ptr(dshape), axis, ctypes.byref(kind))
+    return out, first, kind.value

@@ -197,6 +197,17 @@ class Dag:
         dims = [-(-d // k) for d, k in zip(self.dims(x), steps)]
         return self.node({"Stride": {"strides": [{"Lit": k} for k in steps]}}, [x], dims, self.prec(x))
 
+    def scatter(self, target, indices, updates, axis, batch_rank=0, add=False):
+        """RiscOp::ScatterAdd / Scatter{axis, batch_rank} (dag.rs:1360-1384)."""
+        op = "ScatterAdd" if add else "Scatter"
+        return self.node({op: {"axis": axis, "batch_rank": batch_rank}}, [target, indices, updates],
+                         self.dims(target), self.prec(target))
+
+    def scatter_elements(self, data, indices, updates, axis):
+        """RiscOp::ScatterElements{axis} (dag.rs:1386-1404)."""
+        return self.node({"ScatterElements": {"axis": axis}}, [data, indices, updates], self.dims(data),
+                         self.prec(data))
+
     def dropout(self, x, rate, key, replay=False):
         return self.node("DropoutReplay" if replay else "Dropout", [x, rate, key], self.dims(x), self.prec(x))
 
@@ -508,6 +519,22 @@ def movement_program():
     return g
 
 
+def scatter_program():
+    """The gather's adjoint into an embedding table (duplicate ids
+    accumulate by the canonical tree), a replacing scatter of rows, and an
+    element-wise scatter along the last axis."""
+    g = Dag("scatters")
+    table = g.load("table", [5000, 64], "f32")
+    ids = g.load("ids", [4096], "i64")
+    grads = g.load("grads", [4096, 64], "f32")
+    data = g.load("data", [512, 100], "f32")
+    cols = g.load("cols", [512, 30], "i32")
+    vals = g.load("vals", [512, 30], "f32")
+    g.roots = [g.scatter(table, ids, grads, 0, add=True), g.scatter(table, ids, grads, 0),
+               g.scatter_elements(data, cols, vals, 1)]
+    return g
+
+
 def cast_program(n):
     """Checked casts of an f64 vector: rounded to i32, and narrowed to f32
     and bf16."""
@@ -597,6 +624,7 @@ FIXTURES = {
     "scans_f32_512x1024": lambda: scan_program(512, 1024),
     "bitwise_i32_65536": lambda: bitwise_program(65536),
     "movement_f32_512x1000": movement_program,
+    "scatters_5000x64_4096": scatter_program,
 }
 
 OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "dags")

@@ -657,3 +657,11 @@ def test_movement_bounds_this_build_refuses():
     g.roots = [n]
     with pytest.raises(C.ChelisError, match="run-time bounds"):
         C.DagProgram(g.json())
+
+
+def test_scatters_plan_one_launch_each():
+    p = C.DagProgram(open(os.path.join(DAGS, "scatters_5000x64_4096.json")).read())
+    assert region_kinds(p) == ["scatter"] * 3
+    text = open(os.path.join(DAGS, "scatters_5000x64_4096.json")).read()
+    nodes = json.loads(C.dag_fuse(text))["nodes"]
+    assert [list(n["op"])[0] for n in nodes[6:]] == ["ScatterAdd", "Scatter", "ScatterElements"]

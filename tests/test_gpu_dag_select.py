@@ -207,6 +207,12 @@ elif case == "shift":
     c = np.ones(n, np.int32)
     c[[40000, 12]] = [-1, -4]
     C.host_entry(sys.argv[4], [a, a, c], 5, library=lib)
+elif case == "scatter":
+    table = np.zeros((5000, 64), np.float32)
+    ids = np.zeros(4096, np.int64)
+    ids[[3000, 40]] = [5000, -3]
+    C.host_entry(sys.argv[4], [table, ids, np.zeros((4096, 64), np.float32), np.zeros((512, 100), np.float32),
+                               np.zeros((512, 30), np.int32), np.zeros((512, 30), np.float32)], 3, library=lib)
 elif case == "gather":
     table = np.zeros((50000, 64), np.float32)
     ids = np.zeros(4096, np.int64)
@@ -223,6 +229,7 @@ print("returned", flush=True)
     ("casts_f64_65536", "cast", "numeric trap: overflow in cast at i32"),
     ("gathers_50000x64_4096x10", "gather", "numeric trap: domain in gather at i64"),
     ("bitwise_i32_65536", "shift", "shift amount must be non-negative, got -4"),
+    ("scatters_5000x64_4096", "scatter", "numeric trap: domain in scatter at i64"),
 ])
 def test_generated_entries_exit_with_the_trap_line(name, case, text):
     g = generated(name)
@@ -323,3 +330,32 @@ def test_movement_views_and_pad_bit_exact(path):
             O.slice_(x, [500, 0], [1, 1], [12, 1000])]
     for g, w in zip(got, want):
         assert g.shape == w.shape and bits(g) == bits(w)
+
+
+# ---------------------------------------------------------------- scatters
+def scatter_inputs(bad_col=False):
+    rng = np.random.default_rng(69)
+    table = rng.standard_normal((5000, 64)).astype(np.float32)
+    ids = rng.integers(0, 700, 4096).astype(np.int64)
+    grads = rng.standard_normal((4096, 64)).astype(np.float32)
+    data = rng.standard_normal((512, 100)).astype(np.float32)
+    cols = rng.integers(0, 100, (512, 30)).astype(np.int32)
+    if bad_col:
+        cols[9, 4] = 100
+    vals = rng.standard_normal((512, 30)).astype(np.float32)
+    return [table, ids, grads, data, cols, vals]
+
+
+@pytest.mark.parametrize("path", ["dag", "device", "host"])
+def test_scatters_bit_exact(path):
+    table, ids, grads, data, cols, vals = ins = scatter_inputs()
+    got = run_all("scatters_5000x64_4096", ins)[path]
+    want = [O.scatter("f32", table, ids, grads, 0, add=True)[0], O.scatter("f32", table, ids, grads, 0)[0],
+            O.scatter_elements("f32", data, cols, vals, 1)[0]]
+    for g, w in zip(got, want):
+        assert bits(g) == bits(w)
+
+
+def test_scatter_elements_trap_through_the_dag_run():
+    with pytest.raises(C.ChelisError, match="^numeric trap: domain in scatter_elements at i64$"):
+        run_dag("scatters_5000x64_4096", scatter_inputs(bad_col=True))

@@ -352,3 +352,101 @@ def test_pad_of_a_transposed_view_into_a_strided_output():
     want = O.pad(np.ascontiguousarray(base.T), [4, 1], [2, 5], 2.5)
     got = holder.numpy()[:, 0, :]
     assert got.tobytes() == want.tobytes()
+
+
+# ---------------------------------------------------------------- scatters
+def _values(dt, shape, rng):
+    """sample()'s values repeated to fill `shape`."""
+    n = int(np.prod(shape))
+    return np.resize(sample(dt, n, rng), n).reshape(shape)
+
+
+def _scatter_case(dt, rng, shape, axis, ishape, batch_rank=0, itype=np.int64):
+    target = _values(dt, shape, rng)
+    if dt in ("i8", "i16", "i32", "i64"):
+        target = np.clip(target, -20, 20).astype(NP[dt])
+    idx = rng.integers(0, shape[axis], ishape).astype(itype)
+    ushape = O.gather_shape(shape, ishape, axis, batch_rank)
+    upd = _values(dt, ushape, rng)
+    if dt in ("i8", "i16", "i32", "i64"):
+        upd = np.clip(upd, -5, 5).astype(NP[dt])
+    return target, idx, upd
+
+
+@pytest.mark.parametrize("dt", ["f32", "f64", "bf16", "f16", "i8", "i16", "i32", "i64"])
+@pytest.mark.parametrize("add", [False, True])
+def test_scatter_matches_the_oracle(dt, add):
+    rng = np.random.default_rng(80 + DTS.index(dt))
+    for shape, axis, ishape, br, itype in (((50, 16), 0, (300,), 0, np.int64), ((6, 40, 5), 1, (7, 9), 0, np.int32),
+                                           ((8, 30), 1, (8, 50), 1, np.int64), ((9,), 0, (400,), 0, np.int32)):
+        target, idx, upd = _scatter_case(dt, rng, shape, axis, ishape, br, itype)
+        want, first, _ = O.scatter(dt, oracle_carrier(dt, target), idx, oracle_carrier(dt, upd), axis, br, add=add)
+        out, failure = C.scatter(C.to_device(target), C.to_device(idx), C.to_device(upd), axis, br, add=add)
+        assert first == -1 and failure is None
+        assert bits(out.numpy()).tobytes() == bits(want).tobytes(), (dt, add, shape, axis)
+
+
+def test_scatter_add_long_runs_and_strided_updates():
+    """Runs of thousands of updates on a few cells, and the updates as a
+    transposed view: still the canonical tree in ascending position."""
+    rng = np.random.default_rng(88)
+    target = rng.standard_normal((4, 33)).astype(np.float32)
+    idx = rng.integers(0, 4, 20000)
+    base = (rng.standard_normal((33, 20000)) * 10.0 ** rng.integers(-4, 5, (33, 20000))).astype(np.float32)
+    upd = C.to_device(base).view((20000, 33), (1, 20000))
+    want, _, _ = O.scatter("f32", target, idx, np.ascontiguousarray(base.T), 0, add=True)
+    out, failure = C.scatter(C.to_device(target), C.to_device(idx), upd, 0, add=True)
+    assert failure is None and out.numpy().tobytes() == want.tobytes()
+
+
+def test_scatter_embedding_gradient_shape():
+    """The gather adjoint of the gathers fixture: 4096 ids into a
+    [50000, 64] table."""
+    rng = np.random.default_rng(89)
+    table = np.zeros((50000, 64), np.float32)
+    ids = rng.integers(0, 500, 4096)  # many repeats
+    g = rng.standard_normal((4096, 64)).astype(np.float32)
+    want, _, _ = O.scatter("f32", table, ids, g, 0, add=True)
+    out, failure = C.scatter(C.to_device(table), C.to_device(ids), C.to_device(g), 0, add=True)
+    assert failure is None and out.numpy().tobytes() == want.tobytes()
+
+
+def test_scatter_failures_and_their_lines():
+    t = C.to_device(np.zeros((10, 3), np.float32))
+    idx = np.arange(70) % 10
+    idx[[44, 5]] = [-1, 10]
+    u = C.to_device(np.ones((70, 3), np.float32))
+    _, f = C.scatter(t, C.to_device(idx), u, 0, add=True)
+    assert f == (5 * 3, 2, "numeric trap: domain in scatter at i64")
+    _, f = C.scatter(t, C.to_device(idx), u, 0)
+    assert f == (5 * 3, 2, "numeric trap: domain in scatter_replace at i64")
+    # an i16 tree that leaves the width at destination 3 (and later at 7)
+    ti = np.zeros(10, np.int16)
+    ii = np.array([3, 3, 7, 7, 1])
+    ui = np.array([30000, 30000, 30000, 30000, 5], np.int16)
+    want, first, kind = O.scatter("i16", ti, ii, ui, 0, add=True)
+    _, f = C.scatter(C.to_device(ti), C.to_device(ii), C.to_device(ui), 0, add=True)
+    assert f == (first, kind, "numeric trap: overflow in scatter at i16") and first == 5 + 3
+    with pytest.raises(C.ChelisError, match="numeric trap: domain in scatter at i64"):
+        C.scatter(t, C.to_device(np.zeros(4, np.int64)), C.to_device(np.ones((5, 3), np.float32)), 0, add=True)
+    C.take_numeric_failure()
+    C.scatter(t, C.to_device(idx), u, 0, add=True, deferred=True)
+    assert C.take_numeric_failure() == (15, 2, "numeric trap: domain in scatter at i64")
+
+
+@pytest.mark.parametrize("dt", ["f32", "i64", "bf16"])
+def test_scatter_elements_matches_the_oracle(dt):
+    rng = np.random.default_rng(90)
+    data = _values(dt, (6, 7, 5), rng)
+    for axis in range(3):
+        ishape = (4, 3, 5) if axis != 2 else (6, 7, 9)
+        idx = rng.integers(0, data.shape[axis], ishape)
+        upd = _values(dt, ishape, rng)
+        want, first, _ = O.scatter_elements(dt, oracle_carrier(dt, data), idx, oracle_carrier(dt, upd), axis)
+        out, failure = C.scatter_elements(C.to_device(data), C.to_device(idx), C.to_device(upd), axis)
+        assert first == -1 and failure is None
+        assert bits(out.numpy()).tobytes() == bits(want).tobytes(), axis
+    bad = np.zeros((6, 7, 5), np.int64)
+    bad[1, 2, 3] = 7
+    _, f = C.scatter_elements(C.to_device(data), C.to_device(bad), C.to_device(data), 2)
+    assert f == ((1 * 7 + 2) * 5 + 3, 2, "numeric trap: domain in scatter_elements at i64")

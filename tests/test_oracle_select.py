@@ -565,3 +565,115 @@ def test_shrink_and_stride_are_numpy_slices():
         want = x[::steps[0], ::steps[1], ::steps[2]]
         assert O.slice_(x, [0, 0, 0], steps, out).tobytes() == np.ascontiguousarray(want).tobytes(), steps
     assert O.slice_(x, [2, 3, 1], [1, 1, 1], [0, 6, 3]).size == 0
+
+
+# ---------------------------------------------------------------- scatters
+def _destinations(target_shape, idx, axis):
+    """Flat target destination of every update (hyperplane form, no batch
+    axes): numpy's own index arithmetic over the gathered shape."""
+    ushape = target_shape[:axis] + idx.shape + target_shape[axis + 1:]
+    coords = list(np.unravel_index(np.arange(int(np.prod(ushape))), ushape))
+    k = idx.ndim
+    sel = idx[tuple(coords[axis:axis + k])]
+    tcoords = coords[:axis] + [sel] + coords[axis + k:]
+    return np.ravel_multi_index(tuple(tcoords), target_shape)
+
+
+@pytest.mark.parametrize("dt", ["f32", "f64", "i16", "i64"])
+def test_scatter_replace_keeps_the_highest_position(dt):
+    """Last write wins: every targeted cell holds the update whose row-major
+    position is the largest among those aimed at it (np.maximum.at over the
+    positions), every other cell the target's value."""
+    rng = np.random.default_rng(16)
+    for shape, axis, ishape in (((6, 9, 4), 1, (5,)), ((7, 3), 0, (4, 2)), ((5, 8), 1, (20,))):
+        target = (rng.standard_normal(shape) * 100).astype(CAR[dt])
+        idx = rng.integers(0, shape[axis], ishape)
+        upd = (rng.standard_normal(O.gather_shape(shape, ishape, axis, 0)) * 100).astype(CAR[dt])
+        got, first, _ = O.scatter(dt, target, idx, upd, axis)
+        dest = _destinations(shape, idx, axis)
+        win = np.full(target.size, -1, np.int64)
+        np.maximum.at(win, dest, np.arange(dest.size))
+        want = target.reshape(-1).copy()
+        hit = win >= 0
+        want[hit] = upd.reshape(-1)[win[hit]]
+        assert first == -1 and got.reshape(-1).tobytes() == want.tobytes(), (shape, axis)
+
+
+@pytest.mark.parametrize("dt", ["f32", "f64"])
+def test_scatter_add_folds_each_destination_by_the_canonical_tree(dt):
+    """Each targeted cell is the canonical tree sum (O.tree_sum, pinned
+    with the reductions) of [its target value, its updates in ascending
+    position]; with integer-valued operands it is np.add.at exactly."""
+    rng = np.random.default_rng(17)
+    target = (rng.standard_normal((40, 6)) * 10.0 ** rng.integers(-3, 6, (40, 6))).astype(CAR[dt])
+    idx = rng.integers(0, 40, 300)
+    upd = (rng.standard_normal((300, 6)) * 10.0 ** rng.integers(-3, 6, (300, 6))).astype(CAR[dt])
+    got, first, _ = O.scatter(dt, target, idx, upd, 0, add=True)
+    assert first == -1
+    for r in range(40):
+        rows = np.nonzero(idx == r)[0]
+        for c in range(6):
+            want = target[r, c] if rows.size == 0 else O.tree_sum(np.concatenate([[target[r, c]], upd[rows, c]]).astype(CAR[dt]))
+            assert np.array([got[r, c]]).tobytes() == np.array([want], CAR[dt]).tobytes(), (r, c)
+    ti = rng.integers(-50, 50, (40, 6)).astype(CAR[dt])
+    ui = rng.integers(-50, 50, (300, 6)).astype(CAR[dt])
+    want = ti.copy()
+    np.add.at(want, idx, ui)
+    assert np.array_equal(O.scatter(dt, ti, idx, ui, 0, add=True)[0], want)
+
+
+def test_scatter_add_known_answers():
+    """bf16 rounds at every node: [256, 1, 1] gives (256 + 1 -> 256) + 1 ->
+    256 (each tie to even), where one rounding of the exact 258 keeps 258.
+    An i8 tree (100 + 27) + (1 + -1) stays in range where a left fold
+    (100 + 27 + 1) would not. A f32 tree [1e8, 4, 4, 4, 4] gives 100000016,
+    a left fold 1e8."""
+    b = lambda v: O.narrow_encode("bf16", np.array(v, np.float32))
+    got, _, _ = O.scatter("bf16", b([256.0, 0.0]), np.array([0, 0]), b([1.0, 1.0]), 0, add=True)
+    assert O.narrow_decode("bf16", got).tolist() == [256.0, 0.0]
+    got, first, _ = O.scatter("i8", np.array([100], np.int8), np.array([0, 0, 0]), np.array([27, 1, -1], np.int8),
+                              0, add=True)
+    assert first == -1 and got.tolist() == [127]
+    got, first, kind = O.scatter("i8", np.array([100, 0], np.int8), np.array([1, 0, 0]),
+                                 np.array([5, 27, 1], np.int8), 0, add=True)
+    assert (first, O.trap_text(kind, "scatter", "i8")) == (3 + 0, "numeric trap: overflow in scatter at i8")
+    got, _, _ = O.scatter("f32", np.array([1e8], np.float32), np.zeros(4, np.int64), np.full(4, 4.0, np.float32), 0,
+                          add=True)
+    assert got.tolist() == [100000016.0]
+
+
+def test_scatter_domain_failure_and_batch_axes():
+    target = np.zeros((3, 5), np.float32)
+    _, first, kind = O.scatter("f32", target, np.array([1, 4, 5, -1]), np.ones((3, 4), np.float32), 1)
+    assert (first, O.FAILURE_KINDS[kind]) == (2, "domain")
+    # one batch axis: row b of the target takes row b's own indices
+    idx = np.array([[0, 2], [4, 4], [1, 0]])
+    upd = np.arange(6, dtype=np.float32).reshape(3, 2) + 1
+    got, first, _ = O.scatter("f32", target, idx, upd, 1, batch_rank=1, add=True)
+    want = np.zeros((3, 5), np.float32)
+    for r in range(3):
+        for j in range(2):
+            want[r, idx[r, j]] += upd[r, j]
+    assert first == -1 and np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("dt", ["f32", "i32"])
+def test_scatter_elements_keeps_the_highest_position(dt):
+    rng = np.random.default_rng(18)
+    data = (rng.standard_normal((6, 7, 5)) * 100).astype(CAR[dt])
+    for axis in range(3):
+        ishape = (4, 3, 5) if axis != 2 else (6, 7, 9)
+        idx = rng.integers(0, data.shape[axis], ishape)
+        upd = (rng.standard_normal(ishape) * 100).astype(CAR[dt])
+        got, first, _ = O.scatter_elements(dt, data, idx, upd, axis)
+        coords = list(np.unravel_index(np.arange(idx.size), ishape))
+        coords[axis] = idx.reshape(-1)
+        dest = np.ravel_multi_index(tuple(coords), data.shape)
+        win = np.full(data.size, -1, np.int64)
+        np.maximum.at(win, dest, np.arange(dest.size))
+        want = data.reshape(-1).copy()
+        want[win >= 0] = upd.reshape(-1)[win[win >= 0]]
+        assert first == -1 and got.reshape(-1).tobytes() == want.tobytes(), axis
+    bad = np.zeros((6, 7, 5), np.int64)
+    bad[1, 2, 3] = 7
+    assert O.scatter_elements(dt, data, bad, np.zeros((6, 7, 5), CAR[dt]), 2)[1] == (1 * 7 + 2) * 5 + 3
