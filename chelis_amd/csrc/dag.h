@@ -76,6 +76,8 @@ enum class Op : uint8_t {
     Pad, Shrink, Stride,
     // sparse writes: target, indices, updates (axis, batch_rank)
     ScatterAdd, Scatter, ScatterElements,
+    // a literal tensor; the release of a value (no data moves)
+    ConstTensor, Drop,
     // reductions over one axis
     Sum, MaxReduce, MinReduce, ProdReduce, Argmax, Argmin, Count, Softmax,
     // movement
@@ -146,7 +148,8 @@ struct Node {
     // step per axis. Extent codes as in dims.
     std::vector<int64_t> lo, hi, step;
     Prim const_prec = Prim::Other;  // Const
-    uint64_t const_bits = 0;        // float bits, or the integer / bool value
+    uint64_t const_bits = 0;        // float bits, or the integer / bool value; ConstTensor: its element count
+    std::vector<uint64_t> tensor_cells;  // ConstTensor: its elements' bytes, row-major, packed in 8-byte cells
     std::vector<Step> steps;        // FusedElem
     Prim cast_to = Prim::Other;     // Cast
     std::string raw_op;             // the op as read (written back verbatim)
@@ -276,6 +279,7 @@ struct ValueInfo {
     int64_t slot = -1;                // Slot: workspace slot
     int64_t slot_offset = 0;          // Slot: bytes into the slot (a matmul group's later results)
     int64_t const_index = -1;         // Const: constant pool entry
+    bool const_dense = false;         // a ConstTensor: row-major from const_index on
     // physical order of a materialized value: perm[i] = the logical axis
     // stored i-th (outermost first); empty = row-major
     std::vector<int64_t> layout;

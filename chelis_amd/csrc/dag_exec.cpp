@@ -240,6 +240,14 @@ int32_t run_plan(chelis_dag_program *prog, const chelis_gpu_tensor *const *input
                 p.strides.assign(dims.size(), 0);
                 p.t.data = static_cast<char *>(pool) + 8 * v.const_index;
                 p.t.byte_capacity = 8;
+                if (v.const_dense) {  // a literal tensor, row-major
+                    int64_t acc = 1;
+                    for (size_t a = dims.size(); a-- > 0;) {
+                        p.strides[a] = acc;
+                        acc *= std::max<int64_t>(dims[a], 1);
+                    }
+                    p.t.byte_capacity = 8 * (int64_t)((acc * prim_width(n.prec) + 7) / 8);
+                }
                 p.t.dtype = prim_dtype(n.prec);
                 p.live = true;
                 p.seal();
@@ -460,8 +468,15 @@ int32_t run_plan(chelis_dag_program *prog, const chelis_gpu_tensor *const *input
                 s = chelis_hip_gather(in[0], in[1], (int32_t)r.axis, (int32_t)r.batch_rank, out, nullptr);
                 break;
             case RegionKind::Copy: {
+                // floats through the identity chain (its vector paths);
+                // other dtypes as raw elements (a pad with no padding)
                 const chelis_gpu_tensor *dst = outputs[r.axis];
-                s = chelis_hip_fused_elementwise(&identity_chain(), in.data(), 1, dst);
+                if (dst->dtype == CHELIS_DTYPE_F32 || dst->dtype == CHELIS_DTYPE_F64) {
+                    s = chelis_hip_fused_elementwise(&identity_chain(), in.data(), 1, dst);
+                } else {
+                    static const int64_t zeros[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+                    s = chelis_hip_pad(in[0], zeros, 0, dst);
+                }
                 break;
             }
             case RegionKind::MatmulGroup: {

@@ -1024,8 +1024,15 @@ struct Planner {
             }
             switch (n.op) {
                 case Op::Load: case Op::Const: case Op::Expand: case Op::Permute: case Op::Reshape:
-                case Op::Realize: case Op::Copy: case Op::Store:
-                    continue;  // inputs, constants and views
+                case Op::Realize: case Op::Copy: case Op::Store: case Op::Drop:
+                    continue;  // inputs, constants, views and releases
+                case Op::ConstTensor: {
+                    const int64_t c = n.count();
+                    if (c < 0 || (uint64_t)c != n.const_bits || n.const_prec != n.prec)
+                        return fail("node " + std::to_string(n.id) +
+                                    ": ConstTensor data does not fill the node's literal extents at its dtype");
+                    continue;
+                }
                 case Op::Shrink: case Op::Stride: {
                     // views of their operand (an offset, scaled strides),
                     // as the reference HIP lane's stride is (emit.rs:4918-4931)
@@ -1486,6 +1493,15 @@ bool build_plan(const Graph &input, Plan *plan, std::string *error) {
             v.const_index = (int64_t)plan->const_bits.size();
             plan->const_bits.push_back(nd.const_bits);
             plan->const_prec.push_back(nd.const_prec);
+        } else if (nd.op == Op::ConstTensor) {
+            // the literal's bytes in the pool, whole 8-byte cells (unmasked)
+            v.storage = Storage::Const;
+            v.const_dense = true;
+            v.const_index = (int64_t)plan->const_bits.size();
+            for (uint64_t cell : nd.tensor_cells) {
+                plan->const_bits.push_back(cell);
+                plan->const_prec.push_back(Prim::Int64);
+            }
         } else if (produced[nd.id]) {
             v.storage = Storage::Slot;
         } else if (is_view_op(nd.op) && P.claimed[nd.id] < 0) {

@@ -47,6 +47,7 @@ const OpName kOps[] = {
     {"Split", Op::SplitKey}, {"FoldIn", Op::FoldIn}, {"Cumsum", Op::Cumsum},
     {"Bitwise", Op::Bitwise}, {"Pad", Op::Pad}, {"Shrink", Op::Shrink}, {"Stride", Op::Stride},
     {"ScatterAdd", Op::ScatterAdd}, {"Scatter", Op::Scatter}, {"ScatterElements", Op::ScatterElements},
+    {"ConstTensor", Op::ConstTensor}, {"Drop", Op::Drop},
 };
 
 struct PrimName {
@@ -256,6 +257,46 @@ bool read_op(const Json &op, Graph *g, Node *n, std::string *why) {
         case Op::Const:
             if (!scalar_of(p.get("value"), n)) return (*why = "Const with an unreadable scalar", false);
             return true;
+        case Op::ConstTensor: {
+            // TensorStorage (dtype_semantics/wire_codec.rs:472-482): {"dtype":
+            // tag, "bits": [hex...]} for floats, {"dtype": tag, "values":
+            // [...]} for integers and bools
+            const Json *d = p.get("data");
+            const Json *dt = d ? d->get("dtype") : nullptr;
+            if (!dt || dt->kind != Json::String) return (*why = "ConstTensor with unreadable data", false);
+            const PrimName *q = nullptr;
+            for (const PrimName &c : kPrims)
+                if (dt->text == c.scalar) q = &c;
+            if (!q || q->prim == Prim::Key) return (*why = "ConstTensor of dtype `" + dt->text + "`", false);
+            n->const_prec = q->prim;
+            const int64_t w = prim_width(q->prim);
+            const Json *items = d->get(prim_is_float(q->prim) ? "bits" : "values");
+            if (!items || items->kind != Json::Array) return (*why = "ConstTensor with unreadable data", false);
+            const size_t count = items->items.size();
+            n->tensor_cells.assign((count * (size_t)w + 7) / 8, 0);
+            for (size_t k = 0; k < count; ++k) {
+                const Json &e = items->items[k];
+                uint64_t v = 0;
+                bool ok = true;
+                if (prim_is_float(q->prim)) {
+                    ok = e.kind == Json::String;
+                    if (ok) v = hex_bits(e.text, &ok);
+                } else if (e.kind == Json::Bool) {
+                    v = e.boolean ? 1 : 0;
+                } else {
+                    int64_t iv = 0;
+                    ok = int_of(&e, &iv);
+                    v = (uint64_t)iv;
+                }
+                if (!ok) return (*why = "ConstTensor element " + std::to_string(k) + " is unreadable", false);
+                for (int64_t b = 0; b < w; ++b) {
+                    const size_t byte = k * (size_t)w + (size_t)b;
+                    n->tensor_cells[byte / 8] |= ((v >> (8 * b)) & 0xffu) << (8 * (byte % 8));
+                }
+            }
+            n->const_bits = count;  // the element count, checked against the node's extents
+            return true;
+        }
         case Op::Sum:
             if (!int_of(p.get("axis"), &n->axis) || !prim_of(p.get("accumulator"), &n->accumulator))
                 return (*why = "Sum needs axis and accumulator", false);

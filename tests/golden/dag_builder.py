@@ -34,6 +34,8 @@ import json
 import os
 import struct
 
+import numpy as np
+
 PREC = {"f32": "F32", "f64": "F64", "bool": "Bool", "i64": "Int64", "key": "Key", "i32": "Int32", "i16": "Int16",
         "i8": "Int8", "bf16": "Bf16", "f16": "F16"}
 INT_TAGS = {"i64": "int64", "i32": "int32", "i16": "int16", "i8": "int8"}
@@ -97,6 +99,24 @@ class Dag:
         else:
             raise ValueError(prec)
         return self.node({"Const": {"value": v}}, [], dims, prec, shape_deps=shape_deps)
+
+    def const_tensor(self, values, dims, prec):
+        """RiscOp::ConstTensor{data} (dag.rs:1291-1293): TensorStorage's wire
+        form, floats as hex bits, integers and bools as values."""
+        flat = np.asarray(values).reshape(-1)
+        if prec == "f32":
+            data = {"dtype": "f32", "bits": [_f32_bits(float(v)) for v in flat]}
+        elif prec == "f64":
+            data = {"dtype": "f64", "bits": [_f64_bits(float(v)) for v in flat]}
+        elif prec == "bool":
+            data = {"dtype": "bool", "values": [bool(v) for v in flat]}
+        else:
+            data = {"dtype": INT_TAGS[prec], "values": [int(v) for v in flat]}
+        return self.node({"ConstTensor": {"data": data}}, [], dims, prec)
+
+    def drop(self, x):
+        """RiscOp::Drop (dag.rs:1303-1304): a live-range close, no data moves."""
+        return self.node("Drop", [x], self.dims(x), self.prec(x))
 
     # ---- elementwise ----
     def binary(self, op, a, b, prec=None):
@@ -535,6 +555,21 @@ def scatter_program():
     return g
 
 
+def literal_program():
+    """A literal row added to every row of x (a ConstTensor read through an
+    Expand), a literal i32 tensor as a result, and a Drop of an input."""
+    g = Dag("literals")
+    x = g.load("x", [256, 1000], "f32")
+    y = g.load("y", [3, 4], "i32")
+    row = g.const_tensor(np.float32(np.arange(1000)) * np.float32(0.37) - np.float32(100.5), [1000], "f32")
+    grid = g.const_tensor(np.arange(12).reshape(3, 4) * 7 - 40, [3, 4], "i32")
+    out = g.binary("Add", x, g.expand(row, 0, 256))
+    total = g.bitwise("xor", y, grid)
+    g.drop(y)
+    g.roots = [out, grid, total]
+    return g
+
+
 def cast_program(n):
     """Checked casts of an f64 vector: rounded to i32, and narrowed to f32
     and bf16."""
@@ -625,6 +660,7 @@ FIXTURES = {
     "bitwise_i32_65536": lambda: bitwise_program(65536),
     "movement_f32_512x1000": movement_program,
     "scatters_5000x64_4096": scatter_program,
+    "literals_f32_256x1000": literal_program,
 }
 
 OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "dags")

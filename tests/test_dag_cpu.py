@@ -665,3 +665,14 @@ def test_scatters_plan_one_launch_each():
     text = open(os.path.join(DAGS, "scatters_5000x64_4096.json")).read()
     nodes = json.loads(C.dag_fuse(text))["nodes"]
     assert [list(n["op"])[0] for n in nodes[6:]] == ["ScatterAdd", "Scatter", "ScatterElements"]
+
+
+def test_literal_tensors_sit_in_the_constant_pool():
+    text = open(os.path.join(DAGS, "literals_f32_256x1000.json")).read()
+    p = C.DagProgram(text)
+    assert region_kinds(p) == ["chain", "integer", "copy"]
+    assert C.dag_fuse(text).count('"ConstTensor"') == 2
+    g = DB.Dag("bad")
+    g.roots = [g.const_tensor([1.0, 2.0, 3.0], [4], "f32")]  # three values for four elements
+    with pytest.raises(C.ChelisError, match="ConstTensor data does not fill"):
+        C.DagProgram(g.json())

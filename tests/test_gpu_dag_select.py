@@ -359,3 +359,19 @@ def test_scatters_bit_exact(path):
 def test_scatter_elements_trap_through_the_dag_run():
     with pytest.raises(C.ChelisError, match="^numeric trap: domain in scatter_elements at i64$"):
         run_dag("scatters_5000x64_4096", scatter_inputs(bad_col=True))
+
+
+@pytest.mark.parametrize("path", ["dag", "device", "host"])
+def test_literal_tensors_bit_exact(path):
+    """ConstTensor literals in the constant pool: a row read through an
+    Expand by a chain, an i32 tensor as a result and as an operand; a Drop
+    moves nothing."""
+    rng = np.random.default_rng(70)
+    x = rng.standard_normal((256, 1000)).astype(np.float32)
+    y = rng.integers(-1000, 1000, (3, 4)).astype(np.int32)
+    got = run_all("literals_f32_256x1000", [x, y])[path]
+    row = np.float32(np.arange(1000)) * np.float32(0.37) - np.float32(100.5)
+    grid = (np.arange(12).reshape(3, 4) * 7 - 40).astype(np.int32)
+    assert bits(got[0]) == bits(x + row[None, :])
+    assert np.array_equal(got[1], grid)
+    assert np.array_equal(got[2], O.int_binary("bitxor", "i32", y, grid)[0])
