@@ -402,6 +402,73 @@ __global__ __launch_bounds__(THREADS, kMinWavesPerEu<T>) void gemm_mfma_kernel(G
         return;
     }
     T *C = static_cast<T *>(p.c) + z0 * p.sc0 + z1 * p.sc1;
+    if constexpr (!GELU && sizeof(T) == 4) {
+        // The tile through LDS in quarters of BM/4 rows, then each thread
+        // finishes V consecutive columns of a row per step - its bias
+        // elements read once, residual, output (and the loads) as 16-byte
+        // vectors where the layout allows. Straight from the accumulators,
+        // each lane would write 64-byte pieces of four rows per store and
+        // read the bias and residual an element at a time (measured on
+        // 4096 x 4096 x 1024 with a bias: 288 -> 278 us; the transformer
+        // block 974 -> 959 us).
+        constexpr int V = 16 / (int)sizeof(T);
+        using VT = typename Vec16<T>::type;
+        constexpr int QR = BM / 4, LDT = BN + V, CG = BN / V, RS = THREADS / CG;
+        static_assert(QR * LDT <= 2 * BM * LD, "quarter tile fits in As");
+        T *tile = &As[0][0];
+        const int cg = threadIdx.x % CG, r0 = threadIdx.x / CG;
+        const int64_t n = n0 + V * cg;
+        const T *bias = static_cast<const T *>(p.nbz ? p.biasz[z0 * p.nb1 + z1] : p.bias);
+        const T *resid = static_cast<const T *>(p.resid);
+        const int64_t boff = p.nbz ? 0 : z0 * p.sbias0 + z1 * p.sbias1;
+        const T *rbase = resid ? resid + z0 * p.sr0 + z1 * p.sr1 : nullptr;
+        const bool vec = p.scn == 1 && p.scm % V == 0 && (reinterpret_cast<uintptr_t>(C) & 15) == 0 &&
+                         p.N % V == 0 &&
+                         (!resid || (p.srn == 1 && p.srm % V == 0 && (reinterpret_cast<uintptr_t>(rbase) & 15) == 0));
+        T b[V];
+#pragma unroll
+        for (int u = 0; u < V; ++u) b[u] = bias && n + u < p.N ? bias[boff + (n + u) * p.sbias] : T(0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            __syncthreads();  // As: the main loop's (or the last quarter's) reads are done
+            if (wm == q / 2) {
+#pragma unroll
+                for (int ii = 0; ii < TM / 2; ++ii)
+#pragma unroll
+                    for (int j = 0; j < TM; ++j)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            tile[(ii * 16 + M::row(fq, r)) * LDT + wn * WT + j * 16 + fr] =
+                                acc[(q % 2) * (TM / 2) + ii][j][r];
+            }
+            __syncthreads();
+#pragma unroll
+            for (int row = r0; row < QR; row += RS) {
+                const int64_t m = m0 + q * QR + row;
+                if (m >= p.M) continue;
+                const VT t = *reinterpret_cast<const VT *>(&tile[row * LDT + V * cg]);
+                const T *tv = reinterpret_cast<const T *>(&t);
+                if (vec && n < p.N) {
+                    VT rv{};
+                    if (resid) rv = *reinterpret_cast<const VT *>(rbase + m * p.srm + n);
+                    const T *rr = reinterpret_cast<const T *>(&rv);
+                    VT o;
+                    T *oo = reinterpret_cast<T *>(&o);
+#pragma unroll
+                    for (int u = 0; u < V; ++u) oo[u] = epilogue_values<T, false>(tv[u], p, bias != nullptr, b[u], rr[u]);
+                    *reinterpret_cast<VT *>(C + m * p.scm + n) = o;
+                } else {
+#pragma unroll
+                    for (int u = 0; u < V; ++u)
+                        if (n + u < p.N) {
+                            const T r = resid ? rbase[m * p.srm + (n + u) * p.srn] : T(0);
+                            C[m * p.scm + (n + u) * p.scn] = epilogue_values<T, false>(tv[u], p, bias != nullptr, b[u], r);
+                        }
+                }
+            }
+        }
+        return;
+    }
     if constexpr (GELU && sizeof(T) == 4) {
         // The GELU graph once, not once per held output: the tile goes
         // through LDS in quarters of BM/4 rows; the two waves owning a
