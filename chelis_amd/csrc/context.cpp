@@ -184,6 +184,8 @@ int32_t check_tensor(const chelis_gpu_tensor *t, const char *name) {
 }
 
 bool is_contiguous(const chelis_gpu_tensor *t) {
+    for (int32_t a = 0; a < t->rank; ++a)
+        if (t->shape[a] == 0) return true;  // no element: any strides hold it
     int64_t expect = 1;
     for (int32_t a = t->rank; a-- > 0;) {
         if (t->shape[a] != 1 && t->strides[a] != expect) return false;

@@ -508,7 +508,9 @@ __global__ __launch_bounds__(THREADS, kMinWavesPerEu<T>) void gemm_mfma_kernel(G
             const bool nin = n < p.N, hb = bias != nullptr;
             const T b = hb && nin ? bias[(p.nbz ? 0 : z0 * p.sbias0 + z1 * p.sbias1) + n * p.sbias] : T(0);
             const T *resid = static_cast<const T *>(p.resid);
-#pragma unroll 1
+            // four rows in flight per thread (4096 x 4096 x 1024 with the
+            // GELU epilogue: 304.4 us rolled, 304.8 unrolled by 2, 300.9 by 4)
+#pragma unroll 4
             for (int row = threadIdx.x / BN; row < QR; row += THREADS / BN) {
                 const int64_t m = m0 + q * QR + row;
                 if (m < p.M && nin) {

@@ -16,6 +16,9 @@ import pytest
 import chelis_amd as C
 from oracle import oracle as O
 
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+import dag_builder as DB  # noqa: E402
+
 pytestmark = pytest.mark.gpu
 HERE = os.path.dirname(os.path.abspath(__file__))
 DAGS = os.path.join(HERE, "golden", "dags")
@@ -375,3 +378,20 @@ def test_literal_tensors_bit_exact(path):
     assert bits(got[0]) == bits(x + row[None, :])
     assert np.array_equal(got[1], grid)
     assert np.array_equal(got[2], O.int_binary("bitxor", "i32", y, grid)[0])
+
+
+def test_shrink_over_a_run_time_axis_at_two_sizes():
+    """A shrink whose row bound runs to the end of a run-time extent
+    ((0, ToEnd), spec/05 section 2.4.1) and whose column bounds are
+    literal, read by a chain: one plan runs at two row counts."""
+    g = DB.Dag("shrink_rt")
+    x = g.load("x", ["rows", 1000], "f32")
+    n = g.node({"Shrink": {"bounds": [[{"Lit": 0}, "ToEnd"], [{"Lit": 100}, {"Lit": 900}]]}}, [x], ["rows", 800],
+               "f32")
+    g.roots = [g.binary("Mul", n, g.scalar_like(2.0, n))]
+    prog = C.DagProgram(g.json())
+    for rows in (64, 300):
+        xs = np.random.default_rng(rows).standard_normal((rows, 1000)).astype(np.float32)
+        got = prog.run([C.to_device(xs)])[0].numpy()
+        want = O.slice_(xs, [0, 100], [1, 1], [rows, 800]) * np.float32(2.0)
+        assert got.shape == (rows, 800) and bits(got) == bits(want)

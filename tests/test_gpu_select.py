@@ -450,3 +450,47 @@ def test_scatter_elements_matches_the_oracle(dt):
     bad[1, 2, 3] = 7
     _, f = C.scatter_elements(C.to_device(data), C.to_device(bad), C.to_device(data), 2)
     assert f == ((1 * 7 + 2) * 5 + 3, 2, "numeric trap: domain in scatter_elements at i64")
+
+
+# ---------------------------------------------------------------- empty and strided edges
+def test_empty_operands_launch_nothing_and_keep_the_target():
+    t = np.arange(12, dtype=np.float32).reshape(4, 3)
+    out, f = C.scatter(C.to_device(t), C.to_device(np.zeros(0, np.int64)), C.to_device(np.zeros((0, 3), np.float32)),
+                       0, add=True)
+    assert f is None and np.array_equal(out.numpy(), t)
+    out, f = C.scatter(C.to_device(t), C.to_device(np.zeros(0, np.int64)), C.to_device(np.zeros((0, 3), np.float32)),
+                       0)
+    assert f is None and np.array_equal(out.numpy(), t)
+    out = C.pad(C.to_device(np.zeros((0, 5), np.float32)), [2, 1], [1, 0], 3.0)
+    assert out.numpy().shape == (3, 6) and np.all(out.numpy() == 3.0)
+    out, f = C.cumsum(C.to_device(np.zeros((3, 0, 2), np.int64)), 1)
+    assert f is None and out.numpy().shape == (3, 0, 2)
+    out, f = C.integer_op("shl", C.to_device(np.zeros(0, np.int32)), C.to_device(np.zeros(0, np.int32)))
+    assert f is None and out.numpy().shape == (0,)
+
+
+def test_scatter_from_strided_target_and_indices():
+    rng = np.random.default_rng(91)
+    base = rng.standard_normal((6, 40)).astype(np.float32)
+    target = C.to_device(base).view((40, 6), (1, 40))  # the transpose
+    idx_base = rng.integers(0, 40, (2, 30)).astype(np.int32)
+    idx = C.to_device(idx_base).view((30,), (1,), 30)  # row 1 of the index array
+    upd = rng.standard_normal((30, 6)).astype(np.float32)
+    for add in (False, True):
+        want, _, _ = O.scatter("f32", np.ascontiguousarray(base.T), idx_base[1], upd, 0, add=add)
+        out, f = C.scatter(target, idx, C.to_device(upd), 0, add=add)
+        assert f is None and out.numpy().tobytes() == want.tobytes()
+
+
+def test_scatter_add_i8_tree_stays_in_range_where_a_left_fold_would_not():
+    t = np.array([100, 0], np.int8)
+    out, f = C.scatter(C.to_device(t), C.to_device(np.array([0, 0, 0])), C.to_device(np.array([27, 1, -1], np.int8)),
+                       0, add=True)
+    assert f is None and out.numpy().tolist() == [127, 0]
+
+
+def test_cumsum_of_a_broadcast_view():
+    row = np.array([1.5, -2.0, 0.25], np.float32)
+    v = C.to_device(row).view((5, 3), (0, 1))
+    out, f = C.cumsum(v, 0)
+    assert f is None and out.numpy().tobytes() == O.cumsum("f32", np.broadcast_to(row, (5, 3)).copy(), 0)[0].tobytes()
