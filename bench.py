@@ -800,6 +800,8 @@ def main(argv=None) -> int:
         # bf16 (np.uint16 bit patterns) with the binary32 accumulator
         r, _ = bench_gemm(C, H, 4096, 4096, 4096, "bf16", (28, 29), gs, gw)
         kernels["gemm_bf16_4096^3"] = gemm_line(r, "bf16", "mfma")
+        kernels["gemm_bf16_4096^3"]["path"] = ("hipBLASLt (a plain 16-bit product; epilogues, batches and the exact "
+                                               "flag stay on this library's MFMA tiles)")
         progs, lin, tr, mlp = bench_programs(C, H, max(5, args.steps // 2), args.warmup)
         kernels.update(progs)
         dag_path = bench_dag_path(C, H, max(5, args.steps // 2), args.warmup, kernels, lin, tr, mlp, x, x64)

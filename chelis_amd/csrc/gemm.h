@@ -78,6 +78,9 @@ __device__ inline T gemm_epilogue(T acc, const GemmProblem &p, int64_t z0, int64
 }
 
 int32_t gemm_mfma(chelis_dtype dt, const GemmProblem &p, hipStream_t st);
+// A plain 16-bit product on hipBLASLt when it takes the shape and layout
+// (gemm_lt.cpp); false leaves it to the MFMA tiles.
+bool gemm16_lt(chelis_dtype dt, const GemmProblem &p, hipStream_t st);
 // The MFMA tiles' raw sums as K slices, part[slice][z][m][n] (no epilogue,
 // no combine; one slice when the product is not split), and their count.
 int64_t gemm_mfma_slice_count(chelis_dtype dt, const GemmProblem &p);

@@ -158,6 +158,7 @@ int32_t dispatch(chelis_dtype dt, const GemmProblem &p, int32_t flags) {
     if (exact_mode()) flags |= CHELIS_MATMUL_EXACT;
     if (is_narrow16(dt)) {
         if ((flags & CHELIS_MATMUL_EXACT) || p.K == 0) return dispatch_narrow_exact(dt, p, st);
+        if (gemm16_lt(dt, p, st)) return CHELIS_HIP_OK;
         return gemm_mfma16(dt, p, st);
     }
     const bool f64 = dt == CHELIS_DTYPE_F64;
