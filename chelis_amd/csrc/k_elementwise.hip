@@ -290,7 +290,9 @@ __device__ inline T unary_one(T x, T g, int64_t i, const UnaryArgs &u, const Tab
         // element is x / (1 - rate) (binary32: through the binary64
         // reciprocal of the divisor, quot_f32, which rounds to the IEEE
         // quotient).
-        const bool drop = (random_word(u.key, (uint64_t)i) >> 11) < u.cut;
+        // (word >> 11) < cut, as word < cut * 2^11 (no shift per element;
+        // cut = 2^53, which drops every element, does not fit the product)
+        const bool drop = (u.cut >> 53) != 0 || random_word(u.key, (uint64_t)i) < (u.cut << 11);
         if constexpr (sizeof(T) == 4) return drop ? T(0) : canon(quot_f32(x, u.inv_keep));
         else return drop ? T(0) : canon(x / (T(1) - (T)u.p0));
     } else {
@@ -356,7 +358,9 @@ template <> struct NtVec<double> { using type = f64x2_t; };
 // vectors per buffer: each thread evaluates one buffer of kStreamBatch
 // vectors while the other buffer's loads are in flight (a ping-pong, so no
 // register moves); fewer for the register-heavy exact GELU
-template <Unary OP> constexpr int kStreamBatch = OP == Unary::Gelu ? 1 : 3;
+// (dropout, [16384,4096] f32 at settled clocks: 1 vector 106-110 us, 2
+// vectors 107-110, 3 vectors 111-113, 4 vectors 109-111, 6 vectors 119)
+template <Unary OP> constexpr int kStreamBatch = OP == Unary::Gelu ? 1 : OP == Unary::Dropout ? 2 : 3;
 
 template <typename T, Unary OP>
 __global__ __launch_bounds__(256) void unary_stream_kernel(const T *__restrict__ x, T *__restrict__ y, int64_t n,
