@@ -104,6 +104,50 @@ void scratch_free(void *p, size_t bytes) {
     g_free[device][size_class(bytes)].push_back(p);
 }
 
+// ---- owner storage ---------------------------------------------------------
+// chelis_device_tensor_alloc's blocks come from the same per-device size
+// classes, up to kOwnerCacheMax bytes (larger ones are allocated and freed
+// directly), so an entry that allocates its outputs on every call reuses
+// the blocks earlier calls released instead of paying hipMalloc and hipFree
+// (hipFree waits for the whole device). A released block waits for the
+// device before it returns to the cache, as hipFree would, so no queued use
+// on any stream outlives it.
+namespace {
+constexpr size_t kOwnerCacheMax = size_t(1) << 28;
+}  // namespace
+
+void *owner_block_alloc(size_t bytes) {
+    if (!bytes) return nullptr;
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) return nullptr;
+    void *p = nullptr;
+    if (bytes > kOwnerCacheMax) return device_malloc(&p, bytes) == hipSuccess ? p : nullptr;
+    const int c = size_class(bytes);
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mutex);
+        std::vector<void *> &fl = g_free[device][c];
+        if (!fl.empty()) {
+            p = fl.back();
+            fl.pop_back();
+            return p;
+        }
+    }
+    return device_malloc(&p, size_t(1) << c) == hipSuccess ? p : nullptr;
+}
+
+hipError_t owner_block_free(void *p, size_t bytes) {
+    if (!p) return hipSuccess;
+    if (bytes > kOwnerCacheMax) return hipFree(p);
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return e;
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    g_free[device][size_class(bytes)].push_back(p);
+    return hipSuccess;
+}
+
 // ---- status words ---------------------------------------------------------
 // Two int32 words per device, allocated and cleared once, kept until the
 // process ends: word 0 carries the error code of a launcher that returns it

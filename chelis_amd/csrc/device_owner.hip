@@ -177,10 +177,10 @@ chelis_device_tensor_owner *make_owner(chelis_metadata_plan *plan, void *storage
 
 void destroy_owner(chelis_device_tensor_owner *o) {
     if (o->owns_storage && o->storage) {
-        // hipFree waits for the device, so no queued use outlives the block
+        // the free waits for the device, so no queued use outlives the block
         const int32_t here = device_now();
         if (here != o->device) hip_must(hipSetDevice(o->device), "hipSetDevice");
-        hip_must(hipFree(o->storage), "hipFree");
+        hip_must(chelis::owner_block_free(o->storage, static_cast<size_t>(o->packet.byte_capacity)), "hipFree");
         if (here != o->device) hip_must(hipSetDevice(here), "hipSetDevice");
     }
     chelis_metadata_plan_release(o->plan);
@@ -286,7 +286,8 @@ chelis_device_tensor_owner *allocate(chelis_metadata_plan *plan) {
     const int32_t device = device_now();
     void *storage = nullptr;
     if (bytes > 0) {
-        hip_must(chelis::device_malloc(&storage, static_cast<size_t>(bytes)), "hipMalloc");
+        storage = chelis::owner_block_alloc(static_cast<size_t>(bytes));
+        if (!storage) hip_must(hipErrorOutOfMemory, "hipMalloc");
         const hipStream_t st = library_stream();
         hip_must(hipMemsetAsync(storage, 0, static_cast<size_t>(bytes), st), "hipMemsetAsync");
         hip_must(hipStreamSynchronize(st), "hipStreamSynchronize");

@@ -55,6 +55,10 @@ void *scratch_alloc(size_t bytes);
 // the library makes goes through it.
 hipError_t device_malloc(void **p, size_t bytes);
 void scratch_free(void *p, size_t bytes);
+// Storage of owned device tensors (chelis_device_tensor_alloc): cached
+// blocks for sizes up to 256 MiB; the free waits for the device first.
+void *owner_block_alloc(size_t bytes);
+hipError_t owner_block_free(void *p, size_t bytes);
 
 #define CHELIS_HIP_TRY(expr)                                                              \
     do {                                                                                  \
