@@ -310,8 +310,7 @@ def bench_bandwidth(C, H, steps, warmup):
     line("relu_adjoint_f32_16384x4096", lambda i: C.relu_adjoint(X[i % 3], G[i % 3], Y[i % 3]), 3 * nb)
     line("dropout_f32_16384x4096", lambda i: C.dropout(44, X[i % 3], 0.1, Y[i % 3]), 2 * nb,
          "VALU (splitmix64 64-bit multiplies per element)")
-    line("gelu_f32_16384x4096", lambda i: C.gelu(X[i % 3], Y[i % 3]), 2 * nb,
-         "VALU (binary32 x Phi(x): an erfcx polynomial times exp2 of a binary64 argument)")
+    line("gelu_f32_16384x4096", lambda i: C.gelu(X[i % 3], Y[i % 3]), 2 * nb)
     sq = C.fused_chain([("sub", 0, 1), ("mul", ("s", 0), ("s", 0))])
     line("fused_chain_sqdiff_f32_16384x4096", lambda i: C.fused_elementwise(sq, [X[i % 3], G[i % 3]], Y[i % 3]),
          3 * nb)

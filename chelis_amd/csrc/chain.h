@@ -201,13 +201,15 @@ __device__ inline float gelu_fast_f32(float x, bool &slow) {
 }
 
 // A workgroup's copy of the binary32 erfc and exp tables in LDS; every
-// thread calls it, and the caller's next barrier publishes the copy.
+// thread of the NT-thread workgroup calls it, and the caller's next barrier
+// publishes the copy.
 struct ErfcLdsStore {
     double bt[37][10];
     double et[64];
+    template <int NT>
     __device__ void fill() {
-        for (int i = threadIdx.x; i < 37 * 10; i += blockDim.x) bt[i / 10][i % 10] = chelis_erfcx_b[i / 10][i % 10];
-        for (int i = threadIdx.x; i < 64; i += blockDim.x) et[i] = chelis_exp2_64_tab[i][0];
+        for (int i = threadIdx.x; i < 37 * 10; i += NT) bt[i / 10][i % 10] = chelis_erfcx_b[i / 10][i % 10];
+        for (int i = threadIdx.x; i < 64; i += NT) et[i] = chelis_exp2_64_tab[i][0];
     }
     __device__ ErfcTablesLds tabs() const { return ErfcTablesLds{bt, et}; }
 };

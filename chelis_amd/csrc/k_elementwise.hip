@@ -10,12 +10,21 @@
 // arithmetic, and only genuinely strided views (row/column broadcast,
 // permuted axes) pay for coordinates. A broadcast operand (stride 0) is
 // re-read through L2/MALL, not materialized.
+#include <type_traits>
+
 #include "chain.h"
 #include "narrow.h"
 #include "strided.h"
 
 namespace chelis {
 namespace {
+
+// Every kernel in this file runs 256 threads per workgroup (the launches
+// below pass that count). Index arithmetic uses the constant: blockDim.x is
+// read from the dispatch packet with a vector memory load at the start of
+// each wave, a full memory round trip before a one-vector-per-thread wave
+// can form its first address.
+constexpr int kMapThreads = 256;
 
 struct Operand {
     const void *p;
@@ -39,8 +48,8 @@ __global__ __launch_bounds__(256) void fused_chain_kernel(ChainDev ch, Operands 
                                                           int64_t count) {
     __shared__ T slots[256 * kSlotStride];
     T *slot = slots + threadIdx.x * kSlotStride;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < count; idx += stride) {
+    const int64_t stride = (int64_t)gridDim.x * kMapThreads;
+    for (int64_t idx = (int64_t)blockIdx.x * kMapThreads + threadIdx.x; idx < count; idx += stride) {
         int64_t coord[kMaxRank];
         int64_t rem = idx;
 #pragma unroll
@@ -96,8 +105,8 @@ __global__ __launch_bounds__(256) void narrow_chain_kernel(ChainDev ch, Operands
                                                            uint16_t *__restrict__ out, int64_t count) {
     __shared__ uint16_t slots[256 * kSlotStride];
     uint16_t *slot = slots + threadIdx.x * kSlotStride;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < count; idx += stride) {
+    const int64_t stride = (int64_t)gridDim.x * kMapThreads;
+    for (int64_t idx = (int64_t)blockIdx.x * kMapThreads + threadIdx.x; idx < count; idx += stride) {
         int64_t coord[kMaxRank];
         int64_t rem = idx;
 #pragma unroll
@@ -133,8 +142,8 @@ __global__ __launch_bounds__(256) void narrow_relu_kernel(const uint16_t *__rest
                                                           const uint16_t *__restrict__ g, uint16_t *__restrict__ y,
                                                           int64_t n) {
     const int64_t nv = n / 8;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; v < nv; v += stride) {
+    const int64_t stride = (int64_t)gridDim.x * kMapThreads;
+    for (int64_t v = (int64_t)blockIdx.x * kMapThreads + threadIdx.x; v < nv; v += stride) {
         uint4 xv = reinterpret_cast<const uint4 *>(x)[v], gv{}, yv;
         if constexpr (ADJ) gv = reinterpret_cast<const uint4 *>(g)[v];
         const uint16_t *xe = reinterpret_cast<const uint16_t *>(&xv);
@@ -144,7 +153,7 @@ __global__ __launch_bounds__(256) void narrow_relu_kernel(const uint16_t *__rest
         for (int i = 0; i < 8; ++i) ye[i] = ADJ ? narrow_relu_adjoint<K>(xe[i], ge[i]) : narrow_relu<K>(xe[i]);
         reinterpret_cast<uint4 *>(y)[v] = yv;
     }
-    const int64_t t = nv * 8 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t t = nv * 8 + (int64_t)blockIdx.x * kMapThreads + threadIdx.x;
     if (t < n) y[t] = ADJ ? narrow_relu_adjoint<K>(x[t], g[t]) : narrow_relu<K>(x[t]);
 }
 
@@ -302,6 +311,22 @@ __device__ inline T unary_one(T x, T g, int64_t i, const UnaryArgs &u, const Tab
     }
 }
 
+// 16-byte vectors as clang vector types: the nontemporal load and store
+// builtins take those (not HIP's float4 / double2 structs).
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef double f64x2_t __attribute__((ext_vector_type(2)));
+template <typename T> struct NtVec;
+template <> struct NtVec<float> { using type = f32x4_t; };
+template <> struct NtVec<double> { using type = f64x2_t; };
+
+// One 16-byte vector per thread (grid-stride past 2^16 workgroups), loads
+// and stores nontemporal: every element is read once and written once. The
+// binary32 default-mode GELU evaluates a vector's four elements side by
+// side and branches once to the graph for those gelu_fast_f32 does not
+// serve. ([16384,4096] f32 at settled clocks: GELU 83 us here against
+// 99-103 us as a resident grid streaming several vectors per thread, whose
+// copy form alone took 85-124 us; a plain copy in this form 82.5 us with
+// nontemporal accesses, 88.4 without.)
 template <typename T, Unary OP>
 __global__ __launch_bounds__(256) void unary_kernel(const T *__restrict__ x, const T *__restrict__ g,
                                                     T *__restrict__ y, int64_t n, UnaryArgs u) {
@@ -310,22 +335,33 @@ __global__ __launch_bounds__(256) void unary_kernel(const T *__restrict__ x, con
     if constexpr (OP == Unary::Dropout) u.inv_keep = 1.0 / (double)(T(1) - (T)u.p0);
     // binary32 GELU reads its erfc and exp tables from LDS
     auto run = [&](const auto &tb) {
-        using V = Vec16<T>;
-        const int64_t nv = n / V::V;
-        const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-        for (int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; v < nv; v += stride) {
-            typename V::type xv{}, gv{}, yv;
-            if constexpr (OP != Unary::Uniform) xv = reinterpret_cast<const typename V::type *>(x)[v];
-            if constexpr (OP == Unary::ReluAdjoint) gv = reinterpret_cast<const typename V::type *>(g)[v];
-            const T *xe = reinterpret_cast<const T *>(&xv);
-            const T *ge = reinterpret_cast<const T *>(&gv);
-            T *ye = reinterpret_cast<T *>(&yv);
+        using NV = typename NtVec<T>::type;
+        constexpr int V = Vec16<T>::V;
+        const int64_t nv = n / V;
+        const int64_t stride = (int64_t)gridDim.x * kMapThreads;
+        for (int64_t v = (int64_t)blockIdx.x * kMapThreads + threadIdx.x; v < nv; v += stride) {
+            NV xv{}, gv{}, yv;
+            if constexpr (OP != Unary::Uniform) xv = __builtin_nontemporal_load(reinterpret_cast<const NV *>(x) + v);
+            if constexpr (OP == Unary::ReluAdjoint) gv = __builtin_nontemporal_load(reinterpret_cast<const NV *>(g) + v);
+            if constexpr (OP == Unary::GeluFast && sizeof(T) == 4) {
+                bool sl[V], any = false;
 #pragma unroll
-            for (int i = 0; i < V::V; ++i) ye[i] = unary_one<T, OP>(xe[i], ge[i], v * V::V + i, u, tb);
-            reinterpret_cast<typename V::type *>(y)[v] = yv;
+                for (int i = 0; i < V; ++i) {
+                    yv[i] = gelu_fast_f32(xv[i], sl[i]);
+                    any = any || sl[i];
+                }
+                if (any)
+#pragma unroll
+                    for (int i = 0; i < V; ++i)
+                        if (sl[i]) yv[i] = gelu_one_t<T>(xv[i], ErfcTablesConst{});
+            } else {
+#pragma unroll
+                for (int i = 0; i < V; ++i) yv[i] = unary_one<T, OP>(xv[i], gv[i], v * V + i, u, tb);
+            }
+            __builtin_nontemporal_store(yv, reinterpret_cast<NV *>(y) + v);
         }
         // tail
-        const int64_t t = nv * V::V + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+        const int64_t t = nv * V + (int64_t)blockIdx.x * kMapThreads + threadIdx.x;
         if (t < n) {
             const T xe = (OP != Unary::Uniform) ? x[t] : T(0);
             const T ge = (OP == Unary::ReluAdjoint) ? g[t] : T(0);
@@ -334,7 +370,7 @@ __global__ __launch_bounds__(256) void unary_kernel(const T *__restrict__ x, con
     };
     if constexpr (OP == Unary::Gelu && sizeof(T) == 4) {
         __shared__ ErfcLdsStore gtab;
-        gtab.fill();
+        gtab.fill<kMapThreads>();
         __syncthreads();
         run(gtab.tabs());
     } else {
@@ -342,25 +378,21 @@ __global__ __launch_bounds__(256) void unary_kernel(const T *__restrict__ x, con
     }
 }
 
-// The VALU-heavy maps (GELU in both modes, keyed dropout, uniform_like): a
+// The exact-mode GELU, keyed dropout and uniform_like (VALU-heavy): a
 // resident grid whose threads walk the vectors with a stride, the next
-// vector's load issued before the current one is evaluated, so each wave's
-// memory traffic overlaps its own arithmetic (with one vector per thread
-// the waves of a SIMD loaded together, waited together and computed
-// together, leaving the VALU or the memory idle in turn). Loads and stores
-// are nontemporal: every element is read once and written once.
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef double f64x2_t __attribute__((ext_vector_type(2)));
-template <typename T> struct NtVec;
-template <> struct NtVec<float> { using type = f32x4_t; };
-template <> struct NtVec<double> { using type = f64x2_t; };
-
+// vectors' loads issued before the current ones are evaluated, so each
+// wave's memory traffic overlaps its own arithmetic. Loads and stores are
+// nontemporal.
 // vectors per buffer: each thread evaluates one buffer of kStreamBatch
 // vectors while the other buffer's loads are in flight (a ping-pong, so no
 // register moves); fewer for the register-heavy exact GELU
 // (dropout, [16384,4096] f32 at settled clocks: 1 vector 106-110 us, 2
 // vectors 107-110, 3 vectors 111-113, 4 vectors 109-111, 6 vectors 119)
 template <Unary OP> constexpr int kStreamBatch = OP == Unary::Gelu ? 1 : OP == Unary::Dropout ? 2 : 3;
+
+// the maps that take the resident streaming grid; the others run one vector
+// per thread (unary_kernel)
+template <Unary OP> constexpr bool kStreamed = OP == Unary::Gelu || OP == Unary::Dropout || OP == Unary::Uniform;
 
 template <typename T, Unary OP>
 __global__ __launch_bounds__(256) void unary_stream_kernel(const T *__restrict__ x, T *__restrict__ y, int64_t n,
@@ -373,58 +405,59 @@ __global__ __launch_bounds__(256) void unary_stream_kernel(const T *__restrict__
         using NV = typename NtVec<T>::type;
         constexpr int V = Vec16<T>::V;
         const int64_t nv = n / V;
-        const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+        const int64_t stride = (int64_t)gridDim.x * kMapThreads;
         const NV *xv = reinterpret_cast<const NV *>(x);
         NV *yv = reinterpret_cast<NV *>(y);
         constexpr int B = kStreamBatch<OP>;
-        const int64_t v0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+        const int64_t v0 = (int64_t)blockIdx.x * kMapThreads + threadIdx.x;
+        // every load is issued (an index past the end reads the last vector,
+        // which is not stored), so the wait counts are exact on every path
         auto load = [&](NV (&buf)[B], int64_t base) {
-#pragma unroll
-            for (int j = 0; j < B; ++j)
-                if (reads && base + j * stride < nv) buf[j] = __builtin_nontemporal_load(xv + base + j * stride);
-        };
-        auto eval_store = [&](const NV (&buf)[B], int64_t base) {
 #pragma unroll
             for (int j = 0; j < B; ++j) {
                 const int64_t v = base + j * stride;
-                if (v >= nv) break;
+                if (reads) buf[j] = __builtin_nontemporal_load(xv + (v < nv ? v : nv - 1));
+            }
+        };
+        auto eval_store = [&](const NV (&buf)[B], int64_t base, auto checked) {
+#pragma unroll
+            for (int j = 0; j < B; ++j) {
+                const int64_t v = base + j * stride;
+                if (decltype(checked)::value && v >= nv) break;
                 const NV cur = buf[j];
                 NV out;
-                if constexpr (OP == Unary::GeluFast && sizeof(T) == 4) {
-                    // the vector's evaluations side by side, then one branch to
-                    // the graph for the inputs the direct evaluation does not serve
-                    bool sl[V], any = false;
 #pragma unroll
-                    for (int i = 0; i < V; ++i) {
-                        out[i] = gelu_fast_f32(cur[i], sl[i]);
-                        any = any || sl[i];
-                    }
-                    if (any)
-#pragma unroll
-                        for (int i = 0; i < V; ++i)
-                            if (sl[i]) out[i] = gelu_one_t<T>(cur[i], ErfcTablesConst{});
-                } else {
-#pragma unroll
-                    for (int i = 0; i < V; ++i) out[i] = unary_one<T, OP>(cur[i], T(0), v * V + i, u, tb);
-                }
+                for (int i = 0; i < V; ++i) out[i] = unary_one<T, OP>(cur[i], T(0), v * V + i, u, tb);
                 __builtin_nontemporal_store(out, yv + v);
             }
         };
         NV ba[B] = {}, bb[B] = {};
-        load(ba, v0);
-        for (int64_t base = v0; base < nv; base += 2 * B * stride) {
+        if (nv > 0) {
+            // whole rounds (every thread's 2 B vectors below nv): no bounds
+            // branches, and the barriers keep the next buffer's loads ahead of
+            // this buffer's arithmetic; then one checked round
+            const int64_t full = nv / (2 * B * stride);
+            int64_t base = v0;
+            load(ba, base);
+            for (int64_t r = 0; r < full; ++r, base += 2 * B * stride) {
+                load(bb, base + B * stride);
+                __builtin_amdgcn_sched_barrier(0);
+                eval_store(ba, base, std::false_type{});
+                load(ba, base + 2 * B * stride);
+                __builtin_amdgcn_sched_barrier(0);
+                eval_store(bb, base + B * stride, std::false_type{});
+            }
             load(bb, base + B * stride);
-            eval_store(ba, base);
-            load(ba, base + 2 * B * stride);
-            eval_store(bb, base + B * stride);
+            eval_store(ba, base, std::true_type{});
+            eval_store(bb, base + B * stride, std::true_type{});
         }
         // tail: the last n % V elements
-        const int64_t t = nv * V + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-        if (t < n) y[t] = unary_one<T, OP == Unary::GeluFast ? Unary::Gelu : OP>(reads ? x[t] : T(0), T(0), t, u, tb);
+        const int64_t t = nv * V + (int64_t)blockIdx.x * kMapThreads + threadIdx.x;
+        if (t < n) y[t] = unary_one<T, OP>(reads ? x[t] : T(0), T(0), t, u, tb);
     };
     if constexpr (OP == Unary::Gelu && sizeof(T) == 4) {
         __shared__ ErfcLdsStore gtab;
-        gtab.fill();
+        gtab.fill<kMapThreads>();
         __syncthreads();
         run(gtab.tabs());
     } else {
@@ -453,10 +486,7 @@ int32_t launch_unary(const chelis_gpu_tensor *x, const chelis_gpu_tensor *g, con
     if (!n) return CHELIS_HIP_OK;
     constexpr int V = Vec16<T>::V;
     const int64_t nv = n / V;
-    // one 16-byte vector per thread up to 2^16 blocks (16 Mi vectors):
-    // enough waves that one's loads overlap another's arithmetic (the RNG
-    // maps are VALU-heavy), grid-stride beyond
-    if constexpr (OP != Unary::Relu && OP != Unary::ReluAdjoint) {
+    if constexpr (kStreamed<OP>) {
         // exactly the workgroups that are resident at once (a second round
         // of a few would leave most of the chip idle at the end)
         static const int per_cu = [] {
@@ -473,6 +503,8 @@ int32_t launch_unary(const chelis_gpu_tensor *x, const chelis_gpu_tensor *g, con
         CHELIS_LAUNCH_CHECK();
         return CHELIS_HIP_OK;
     } else {
+        // one 16-byte vector per thread up to 2^16 blocks (16 Mi vectors),
+        // grid-stride beyond
         int64_t blocks = (nv + 255) / 256;
         if (blocks > 65536) blocks = 65536;
         if (blocks < 1) blocks = 1;

@@ -483,7 +483,7 @@ __global__ __launch_bounds__(THREADS, kMinWavesPerEu<T>) void gemm_mfma_kernel(G
         // the erfc and exp tables in LDS for the epilogue's GELU (published
         // by the first quarter's barrier)
         __shared__ ErfcLdsStore gtab;
-        gtab.fill();
+        gtab.fill<THREADS>();
         const ErfcTablesLds tb = gtab.tabs();
 #pragma unroll
         for (int q = 0; q < 4; ++q) {

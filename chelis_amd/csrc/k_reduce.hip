@@ -36,6 +36,11 @@
 namespace chelis {
 namespace {
 
+// Every kernel in this file runs 256 threads per workgroup; grid-stride
+// index arithmetic uses the constant, not blockDim.x (a vector load from
+// the dispatch packet at the start of each wave).
+constexpr int kReduceThreads = 256;
+
 enum class Rk : int { Sum, Max, Min, ArgMax, ArgMin };
 
 template <typename T, Rk K>
@@ -321,8 +326,8 @@ __global__ __launch_bounds__(256) void reduce_cols_kernel(ChainDev ch, LeafSrc s
     __shared__ T slots[CHAIN ? 256 * kSlotStride : 1];
     T *slot = slots + (CHAIN ? threadIdx.x * kSlotStride : 0);
     const int64_t total = outer * groups * inner;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += stride) {
+    const int64_t stride = (int64_t)gridDim.x * kReduceThreads;
+    for (int64_t t = (int64_t)blockIdx.x * kReduceThreads + threadIdx.x; t < total; t += stride) {
         const int64_t j = t % inner;
         const int64_t og = t / inner;
         const int64_t g = og % groups, o = og / groups;
@@ -398,7 +403,7 @@ __global__ __launch_bounds__(256) void reduce_cols4_kernel(ChainDev ch, LeafSrc 
 
 template <typename T>
 __global__ void fill_kernel(T *p, int64_t n, T v) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t i = (int64_t)blockIdx.x * kReduceThreads + threadIdx.x;
     if (i < n) p[i] = v;
 }
 
@@ -415,8 +420,8 @@ __global__ __launch_bounds__(256) void prod_fold_kernel(const T *__restrict__ x,
                                                         int64_t inner, int64_t so, int64_t sn, int64_t si,
                                                         T *__restrict__ out) {
     const int64_t total = outer * inner;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += stride) {
+    const int64_t stride = (int64_t)gridDim.x * kReduceThreads;
+    for (int64_t t = (int64_t)blockIdx.x * kReduceThreads + threadIdx.x; t < total; t += stride) {
         const int64_t o = t / inner, j = t % inner;
         const T *p = x + o * so + j * si;
         T acc = T(1);
