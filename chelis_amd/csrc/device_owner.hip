@@ -206,11 +206,16 @@ struct Strided {
     int64_t stride[kCopyRank];
 };
 
+// The kernels below that index by thread run 256 threads per workgroup
+// (their launches pass that count): the constant, not blockDim.x, which
+// is a vector load from the dispatch packet at the start of each wave.
+constexpr int kCopyThreads = 256;
+
 template <typename W>
 __global__ __launch_bounds__(256) void strided_to_dense_kernel(const W *__restrict__ src, W *__restrict__ dst,
                                                                Strided v, int64_t count) {
-    const int64_t step = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += step) {
+    const int64_t step = (int64_t)gridDim.x * kCopyThreads;
+    for (int64_t i = (int64_t)blockIdx.x * kCopyThreads + threadIdx.x; i < count; i += step) {
         int64_t rem = i, off = 0;
         for (int a = v.rank - 1; a >= 0; --a) {
             const int64_t e = v.extent[a];

@@ -419,14 +419,19 @@ int32_t gemm16_kind(const GemmProblem &p, hipStream_t st) {
     return CHELIS_HIP_OK;
 }
 
+// The kernels below that index by thread run 256 threads per workgroup
+// (their launches pass that count): the constant, not blockDim.x, which
+// is a vector load from the dispatch packet at the start of each wave.
+constexpr int kConvThreads = 256;
+
 // dst[z][r][c] = src[z0 * s0 + z1 * s1 + r * sr + c * sc] widened to binary32
 // (z = z0 * nz1 + z1; dst contiguous).
 template <Narrow KIND>
 __global__ __launch_bounds__(256) void widen_kernel(const uint16_t *__restrict__ src, float *__restrict__ dst,
                                                     int64_t nz1, int64_t rows, int64_t cols, int64_t s0, int64_t s1,
                                                     int64_t sr, int64_t sc, int64_t count) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+    const int64_t stride = (int64_t)gridDim.x * kConvThreads;
+    for (int64_t i = (int64_t)blockIdx.x * kConvThreads + threadIdx.x; i < count; i += stride) {
         const int64_t c = i % cols, r = (i / cols) % rows, z = i / (cols * rows);
         dst[i] = narrow_to_f32<KIND>(src[(z / nz1) * s0 + (z % nz1) * s1 + r * sr + c * sc]);
     }
@@ -437,8 +442,8 @@ template <Narrow KIND>
 __global__ __launch_bounds__(256) void narrow_kernel(const float *__restrict__ src, uint16_t *__restrict__ dst,
                                                      int64_t nz1, int64_t rows, int64_t cols, int64_t s0, int64_t s1,
                                                      int64_t sr, int64_t sc, int64_t count) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+    const int64_t stride = (int64_t)gridDim.x * kConvThreads;
+    for (int64_t i = (int64_t)blockIdx.x * kConvThreads + threadIdx.x; i < count; i += stride) {
         const int64_t c = i % cols, r = (i / cols) % rows, z = i / (cols * rows);
         dst[(z / nz1) * s0 + (z % nz1) * s1 + r * sr + c * sc] = f32_to_narrow<KIND>(src[i]);
     }

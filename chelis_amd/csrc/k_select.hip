@@ -115,13 +115,18 @@ __device__ inline void merge_failures(unsigned long long k, unsigned long long *
     if ((threadIdx.x & 63) == 0) atomicMax(rec, k);
 }
 
+// The kernels below that index by thread run 256 threads per workgroup
+// (their launches pass that count): the constant, not blockDim.x, which
+// is a vector load from the dispatch packet at the start of each wave.
+constexpr int kSelectThreads = 256;
+
 // One element per lane per step; the block's steps start at a uniform base
 // so a wave's lanes are always in the same step (lanes past the end take no
 // element and report no failure).
 template <class F>
 __global__ __launch_bounds__(256) void map_kernel(F f, Ops o, Shape sh, int64_t count, unsigned long long *rec) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t base = (int64_t)blockIdx.x * blockDim.x; base < count; base += stride) {
+    const int64_t stride = (int64_t)gridDim.x * kSelectThreads;
+    for (int64_t base = (int64_t)blockIdx.x * kSelectThreads; base < count; base += stride) {
         const int64_t i = base + threadIdx.x;
         unsigned long long k = 0ull;
         if (i < count) {
@@ -465,8 +470,8 @@ template <typename U, typename I>
 __global__ __launch_bounds__(256) void gather_kernel(const U *__restrict__ values, View8 vv,
                                                      const I *__restrict__ idx, View8 iv, U *__restrict__ out,
                                                      GatherGeom g, uint64_t seq, unsigned long long *rec) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t base = (int64_t)blockIdx.x * blockDim.x; base < g.total; base += stride) {
+    const int64_t stride = (int64_t)gridDim.x * kSelectThreads;
+    for (int64_t base = (int64_t)blockIdx.x * kSelectThreads; base < g.total; base += stride) {
         const int64_t i = base + threadIdx.x;
         unsigned long long k = 0ull;
         if (i < g.total) {
@@ -511,8 +516,8 @@ __global__ __launch_bounds__(256) void cumsum_kernel(const typename Dt<DT>::S *_
                                                      unsigned long long *rec) {
     using A = typename ScanTypes<DT>::A;
     using R = typename ScanTypes<DT>::R;
-    const int64_t lines = outer * inner, stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t base = (int64_t)blockIdx.x * blockDim.x; base < lines; base += stride) {
+    const int64_t lines = outer * inner, stride = (int64_t)gridDim.x * kSelectThreads;
+    for (int64_t base = (int64_t)blockIdx.x * kSelectThreads; base < lines; base += stride) {
         const int64_t t = base + threadIdx.x;
         unsigned long long k = 0ull;
         if (t < lines) {
@@ -556,8 +561,8 @@ struct PadGeom {
 template <typename U>
 __global__ __launch_bounds__(256) void pad_kernel(const U *__restrict__ x, U *__restrict__ y, PadGeom g,
                                                   int64_t total, U fill) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t stride = (int64_t)gridDim.x * kSelectThreads;
+    for (int64_t i = (int64_t)blockIdx.x * kSelectThreads + threadIdx.x; i < total; i += stride) {
         int64_t r = i, so = 0, yo = 0;
         bool inside = true;
 #pragma unroll
@@ -601,8 +606,8 @@ template <typename I, typename K>
 __global__ __launch_bounds__(256) void scatter_keys_kernel(const I *__restrict__ indices, View8 iv, ScatterGeom g,
                                                            K sentinel, K *__restrict__ keys, K *__restrict__ pos,
                                                            uint64_t seq, unsigned long long *rec) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t base = (int64_t)blockIdx.x * blockDim.x; base < g.total; base += stride) {
+    const int64_t stride = (int64_t)gridDim.x * kSelectThreads;
+    for (int64_t base = (int64_t)blockIdx.x * kSelectThreads; base < g.total; base += stride) {
         const int64_t i = base + threadIdx.x;
         unsigned long long k = 0ull;
         if (i < g.total) {
@@ -637,8 +642,8 @@ template <typename U, typename K>
 __global__ __launch_bounds__(256) void scatter_last_kernel(const K *__restrict__ skeys, const K *__restrict__ spos,
                                                            int64_t n, K sentinel, const U *__restrict__ upd, View8 uv,
                                                            U *__restrict__ out) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < n; p += stride) {
+    const int64_t stride = (int64_t)gridDim.x * kSelectThreads;
+    for (int64_t p = (int64_t)blockIdx.x * kSelectThreads + threadIdx.x; p < n; p += stride) {
         const K d = skeys[p];
         if (d != sentinel && (p + 1 == n || skeys[p + 1] != d)) out[d] = upd[logical_offset(uv, (int64_t)spos[p])];
     }
@@ -688,8 +693,8 @@ __global__ __launch_bounds__(256) void scatter_add_kernel(const K *__restrict__ 
                                                           unsigned long long *rec) {
     using N = AddNode<DT>;
     using A = typename N::A;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t base = (int64_t)blockIdx.x * blockDim.x; base < n; base += stride) {
+    const int64_t stride = (int64_t)gridDim.x * kSelectThreads;
+    for (int64_t base = (int64_t)blockIdx.x * kSelectThreads; base < n; base += stride) {
         const int64_t p = base + threadIdx.x;
         unsigned long long k = 0ull;
         if (p < n) {
