@@ -386,9 +386,9 @@ VALU_SET = [
     ("softmax_f32_16384x1024", r"softmax_kernel<float,[^>]*, true, false>"),
     ("softmax_f64_4096x4096", r"softmax_kernel<double,[^>]*, true, true>"),
     ("softmax_f64_4096x4096_exact", r"softmax_kernel<double,[^>]*, true, false>"),
-    # the binary32 default GELU (Unary 5, GeluFast) and dropout on the
-    # resident streaming map
-    ("gelu_f32_16384x4096", r"unary_stream_kernel<float, \(.*Unary\)5>"),
+    # the binary32 default GELU (Unary 5, GeluFast; one vector per thread)
+    # and dropout (the resident streaming map)
+    ("gelu_f32_16384x4096", r"unary_kernel<float, \(.*Unary\)5>"),
     ("dropout_f32_16384x4096", r"unary_stream_kernel<float, \(.*Unary\)3>"),
 ]
 SIMDS = 1024  # 256 CUs x 4 SIMDs
