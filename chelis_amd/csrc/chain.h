@@ -297,6 +297,25 @@ struct Vec16F<double> {
     using type = double2;
 };
 
+// 16-byte nontemporal load and store of a Vec16F value (the builtins take
+// clang vector types, not HIP's float4 / double2): for operands read once
+// or written once, which then do not displace reused lines in the caches.
+template <typename T>
+__device__ inline typename Vec16F<T>::type load_nt16(const T *p) {
+    typedef T E __attribute__((ext_vector_type(16 / sizeof(T))));
+    const E e = __builtin_nontemporal_load(reinterpret_cast<const E *>(p));
+    typename Vec16F<T>::type q;
+    __builtin_memcpy(&q, &e, 16);
+    return q;
+}
+template <typename T>
+__device__ inline void store_nt16(T *p, const typename Vec16F<T>::type &q) {
+    typedef T E __attribute__((ext_vector_type(16 / sizeof(T))));
+    E e;
+    __builtin_memcpy(&e, &q, 16);
+    __builtin_nontemporal_store(e, reinterpret_cast<E *>(p));
+}
+
 template <typename T, int V>
 __device__ inline void apply_step_vec(uint8_t op, const T (&x)[V], const T (&y)[V], double imm, T (&r)[V]) {
     switch (op) {

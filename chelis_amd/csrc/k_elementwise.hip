@@ -231,7 +231,7 @@ __global__ __launch_bounds__(256) void fused_flat_vec_kernel(ChainDev ch, FlatGr
 #pragma unroll
                 for (int j = 0; j < V; ++j) e[j] = b;
             } else if (full) {
-                in[k] = *reinterpret_cast<const Q *>(p + i0);
+                in[k] = load_nt16(p + i0);
             } else {
 #pragma unroll
                 for (int j = 0; j < V; ++j) e[j] = i0 + j < G.count ? p[i0 + j] : T(0);
@@ -248,7 +248,7 @@ __global__ __launch_bounds__(256) void fused_flat_vec_kernel(ChainDev ch, FlatGr
         Q rq;
 #pragma unroll
         for (int j = 0; j < V; ++j) reinterpret_cast<T *>(&rq)[j] = r[j];
-        *reinterpret_cast<Q *>(out + i0) = rq;
+        store_nt16(out + i0, rq);
     } else {
 #pragma unroll
         for (int j = 0; j < V; ++j)

@@ -85,7 +85,8 @@ struct LeafSrc {
 template <typename T, bool CHAIN>
 __device__ inline T leaf(const ChainDev &ch, const LeafSrc &src, T *slot, int64_t o, int64_t i, int64_t j) {
     if constexpr (!CHAIN) {
-        return static_cast<const T *>(src.p[0])[o * src.so[0] + i * src.sn[0] + j * src.si[0]];
+        // nontemporal: each leaf is read once ([16384,4096] column sum 54 -> 49 us)
+        return __builtin_nontemporal_load(static_cast<const T *>(src.p[0]) + (o * src.so[0] + i * src.sn[0] + j * src.si[0]));
     } else {
         T in[CHELIS_FUSED_MAX_INPUTS];
 #pragma unroll
@@ -214,7 +215,7 @@ __global__ __launch_bounds__(256) void reduce_rows_vec_kernel(ChainDev ch, LeafS
                 if (NIN > 0 || k < src.n_in) {
                     const T *p = static_cast<const T *>(src.p[k]) + o * src.so[k];
                     if (i0 + V <= n) {
-                        in[s][k] = *reinterpret_cast<const Q *>(p + i0);
+                        in[s][k] = load_nt16(p + i0);
                     } else {
 #pragma unroll
                         for (int e = 0; e < V; ++e)
@@ -231,7 +232,7 @@ __global__ __launch_bounds__(256) void reduce_rows_vec_kernel(ChainDev ch, LeafS
         for (int s = 0; s < S; ++s) {
             const int64_t i0 = g * G + (int64_t)s * 64 * V + (int64_t)lane * V;
             if (i0 + V <= n) {
-                const Q q = *reinterpret_cast<const Q *>(row + i0);
+                const Q q = load_nt16(row + i0);
                 const T *qe = reinterpret_cast<const T *>(&q);
 #pragma unroll
                 for (int e = 0; e < V; ++e) v[s][e] = qe[e];
