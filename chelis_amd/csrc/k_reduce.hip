@@ -478,7 +478,8 @@ __global__ __launch_bounds__(256) void count_rows_vec_kernel(const uint8_t *__re
     uint32_t bad = 0;
 #pragma unroll 4
     for (int64_t v = lane; v < nv; v += 64) {
-        const uint4 w = reinterpret_cast<const uint4 *>(r)[v];
+        typedef uint32_t U4 __attribute__((ext_vector_type(4)));
+        const U4 w = __builtin_nontemporal_load(reinterpret_cast<const U4 *>(r) + v);  // read once
         bad |= (w.x | w.y | w.z | w.w) & 0xFEFEFEFEu;
         c += __popc(w.x & 0x01010101u) + __popc(w.y & 0x01010101u) + __popc(w.z & 0x01010101u) +
              __popc(w.w & 0x01010101u);
