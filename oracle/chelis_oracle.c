@@ -492,6 +492,9 @@ void orc_dropout_f64(uint64_t key, const double *x, double rate, double *y, int6
     for (int64_t i = 0; i < n; ++i)
         y[i] = orc_unit(key, (uint64_t)i) < rate ? 0.0 : nan64(x[i] / (1.0 - rate));
 }
+void orc_dropout_replay_f64(uint64_t key, const double *g, double rate, double *dx, int64_t n) {
+    orc_dropout_f64(key, g, rate, dx, n);
+}
 
 /* ------------------------------------------------------------------ */
 /* Canonical-tree matmul: spec/05 section 4.1 (insert, mul, sum over k with

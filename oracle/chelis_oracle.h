@@ -97,6 +97,7 @@ void orc_relu_adjoint_f32(const float *x, const float *g, float *y, int64_t n);
 void orc_dropout_f32(uint64_t key, const float *x, float rate, float *y, int64_t n);
 void orc_dropout_replay_f32(uint64_t key, const float *g, float rate, float *dx, int64_t n);
 void orc_dropout_f64(uint64_t key, const double *x, double rate, double *y, int64_t n);
+void orc_dropout_replay_f64(uint64_t key, const double *g, double rate, double *dx, int64_t n);
 
 /* ---- bfloat16 / binary16 storage (kind 0 = bf16, 1 = f16) ----
  * [04-NUM-8]: stored as 16 bits, computed at binary32, finalized once per

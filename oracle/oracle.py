@@ -78,6 +78,7 @@ def _declare(L):
         "orc_dropout_f32": (None, [c_u64, c_p, c_f32, c_p, c_i64]),
         "orc_dropout_replay_f32": (None, [c_u64, c_p, c_f32, c_p, c_i64]),
         "orc_dropout_f64": (None, [c_u64, c_p, c_f64, c_p, c_i64]),
+        "orc_dropout_replay_f64": (None, [c_u64, c_p, c_f64, c_p, c_i64]),
         "orc_matmul_f32": (None, [c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_i64]),
         "orc_matmul_f64": (None, [c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_i64]),
         "orc_linreg_step_f64": (None, [c_p, c_p, c_p, c_p, c_p, c_i64, c_i64]),
@@ -262,9 +263,11 @@ def dropout(key: int, x: np.ndarray, rate) -> np.ndarray:
 
 
 def dropout_replay(key: int, g: np.ndarray, rate) -> np.ndarray:
-    g = np.ascontiguousarray(g, np.float32)
+    """The forward mask on the cotangent, kept values divided by (1 - rate),
+    at g's dtype (binary32 unless g is binary64)."""
+    g = np.ascontiguousarray(g, np.float64 if np.asarray(g).dtype == np.float64 else np.float32)
     y = np.empty_like(g)
-    lib().orc_dropout_replay_f32(key & (2**64 - 1), _ptr(g), rate, _ptr(y), g.size)
+    getattr(lib(), f"orc_dropout_replay_{_f(g.dtype)}")(key & (2**64 - 1), _ptr(g), rate, _ptr(y), g.size)
     return y
 
 

@@ -271,6 +271,23 @@ def test_uniform_like_bit_exact(dtype):
     assert bits_equal(out.numpy(), O.uniform_like(12345, dtype(-1.0), dtype(1.0), 100003, dtype))
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_streamed_maps_over_whole_rounds_bit_exact(dtype):
+    """Dropout, its replay and uniform_like run a resident grid that walks
+    whole rounds of vectors unchecked and then one checked round: at
+    3 * 2^23 + 5 elements every thread takes several whole rounds (the
+    smaller sizes above take only the checked one), the checked round holds
+    a partial vector count and the scalar tail one element."""
+    n = 3 * (1 << 23) + 5
+    key = O.fold_in(44, 9)
+    x = np.random.default_rng(21).standard_normal(n).astype(dtype)
+    assert bits_equal(C.dropout(key, C.to_device(x), 0.1).numpy(), O.dropout(key, x, dtype(0.1)))
+    assert bits_equal(C.dropout_replay(key, C.to_device(x), 0.3).numpy(), O.dropout_replay(key, x, dtype(0.3)))
+    out = C.empty((n,), dtype)
+    C.uniform_like(777, -2.0, 3.0, out)
+    assert bits_equal(out.numpy(), O.uniform_like(777, dtype(-2.0), dtype(3.0), n, dtype))
+
+
 def gelu_f32_close(y, ref, x):
     """The binary32 default-mode GELU bar: within 1e-6 relative of the Phi
     graph (ten times inside the north star's 1e-5), with an absolute floor

@@ -67,6 +67,9 @@ def test_dropout_fixed_stream():
     assert O.dropout(right, x, np.float32(g["rate"])).tolist() == g["forward_right_key"]
     # grad of sum(dropout(left, x)) wrt x is the replay of ones
     assert O.dropout_replay(left, np.ones(4, np.float32), np.float32(g["rate"])).tolist() == g["grad_left_key"]
+    # at binary64 the same stream: the unit at 53 bits against the rate
+    assert O.dropout_replay(left, np.ones(4, np.float64), g["rate"]).tolist() == g["grad_left_key"]
+    assert O.dropout(right, x.astype(np.float64), g["rate"]).tolist() == g["forward_right_key"]
 
 
 def test_dropout_rate_zero_is_identity_and_mask_matches_units():
