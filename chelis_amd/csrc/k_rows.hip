@@ -540,8 +540,13 @@ __global__ __launch_bounds__(64 * W * R) void layer_norm_kernel(const T *__restr
     __shared__ T lds[R * W * S];
     RowCoord<W, R> c;
     if (c.row >= rows) return;
-    T v[S][V], q[S][V];
+    T v[S][V], q[S][V], gm[S][V], bt[S][V];
     load_row<T, V, S, W>(x + c.row * ldx, n, vec_ok, c.tid_in_row, T(-0.0), v);
+    // gamma/beta are [n] vectors shared by every row: their loads go out with
+    // the row's, ahead of the reductions' barriers (after them each row waited
+    // out two more cache round trips: [65536,1024] 90.8 -> 88.5 us)
+    load_row<T, V, S, W, false>(gamma, n, vec_ok, c.tid_in_row, T(0), gm);
+    load_row<T, V, S, W, false>(beta, n, vec_ok, c.tid_in_row, T(0), bt);
     const T extent = (T)n;
     const T mean = canon(canon(row_tree_sum<T, V, S, W, R>(v, lds, c)) / extent);
     constexpr int SEG = 64 * W * V;
@@ -555,17 +560,14 @@ __global__ __launch_bounds__(64 * W * R) void layer_norm_kernel(const T *__restr
         }
     const T var = canon(canon(row_tree_sum<T, V, S, W, R>(q, lds, c)) / extent);
     const T denom = canon_bits(sqrt(canon(var + eps)));
-    // gamma/beta are [n] vectors shared by every row
-    load_row<T, V, S, W, false>(gamma, n, vec_ok, c.tid_in_row, T(0), q);
 #pragma unroll
     for (int s = 0; s < S; ++s)
 #pragma unroll
-        for (int i = 0; i < V; ++i) v[s][i] = canon(canon(v[s][i] / denom) * q[s][i]);
-    load_row<T, V, S, W, false>(beta, n, vec_ok, c.tid_in_row, T(0), q);
+        for (int i = 0; i < V; ++i) v[s][i] = canon(canon(v[s][i] / denom) * gm[s][i]);
 #pragma unroll
     for (int s = 0; s < S; ++s)
 #pragma unroll
-        for (int i = 0; i < V; ++i) v[s][i] = canon(v[s][i] + q[s][i]);
+        for (int i = 0; i < V; ++i) v[s][i] = canon(v[s][i] + bt[s][i]);
     store_row<T, V, S, W>(y + c.row * ldy, n, vec_ok, c.tid_in_row, v);
 }
 
